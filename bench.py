@@ -1,0 +1,285 @@
+"""Benchmark of the HIP rasterizer on one MI355X.
+
+A step is one training pass of the north-star workload:
+render 1M SH-3 Gaussians at 1920x1080, mean |image - target| loss, backward to
+all Gaussian parameters.  Inputs are resident in HBM before timing.  Prints one
+JSON line with the whole-job Mpix/s, per-stage milliseconds from HIP events,
+the roofline of the dominant kernel and the CPU-oracle baseline.
+
+    python bench.py [--steps K] [--warmup W] [--config config3] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (ROOT, ROOT / "gaussian-splats_amd"):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+import torch  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="config3")
+    ap.add_argument("--tile-size", type=int, default=16)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-tiles", type=int, default=24, help="tiles in the CPU baseline sample")
+    ap.add_argument("--out", default=None, help="also write the JSON line to this file")
+    return ap.parse_args()
+
+
+def stage_bytes(n, k, total, num_tiles, pixels, processed_fwd, processed_bwd, sort_passes):
+    """Algorithmic HBM bytes per stage (the model of DESIGN.md)."""
+    return {
+        "project": n * (44 + 12 * k) + n * 52,
+        "bin": 4 * n * 8 * 2 + 8 * n,  # 4 passes over (key, id) + count scan
+        "emit": 16 * n + 8 * total,
+        "sort": total * 16 * sort_passes + 8 * total + 16 * num_tiles,
+        "composite": 40 * processed_fwd + 20 * pixels,
+        "composite_bwd": 76 * processed_bwd + 32 * pixels,
+        "project_bwd": n * (44 + 12 * k) + 36 * n + n * (44 + 12 * k),
+    }
+
+
+def run_step(splats, cam, target, tile_size, near, far):
+    from gaussian_splats.splats import rasterize
+
+    image = rasterize(splats, cam, tile_size=tile_size, near=near, far=far)
+    loss = (image - target).abs().mean()
+    loss.backward()
+    return loss
+
+
+def staged_step(params, cam, target, tile_size, near, far):
+    """One fwd+bwd through the stage functions with an event after each stage."""
+    from gaussian_splats.kernels.rasterize import composite_bwd, pack_records, project_bwd
+    from gaussian_splats.kernels.rasterize.interface import forward_pipeline
+
+    events = {}
+
+    def mark(name):
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record()
+        events[name] = ev
+
+    fx, fy = cam.focal_length
+    cx, cy = cam.principal_point
+    w, h = cam.image_size
+    R = cam.rotation_matrix.to(params[0].device)
+    t = cam.translation.to(params[0].device)
+    out = forward_pipeline(*params, R, t, fx, fy, cx, cy, w, h, tile_size, 0.999, near, far,
+                           "gaussian", 0.95, timer=mark)
+    image, final_t, ncon, pmean, pinv, pcol, pop, gids, ranges, counts = out
+    diff = image - target
+    grad_image = torch.sign(diff) / diff.numel()
+    mark("loss")
+    records = pack_records(pmean, pinv, pcol, pop)
+    grad_proj = composite_bwd(pmean, pinv, pcol, pop, gids, ranges, grad_image, final_t, ncon, w, h,
+                              tile_size, 0.999, "gaussian", records=records)
+    mark("composite_bwd")
+    project_bwd(*params, R, t, pinv, grad_proj, counts, fx, fy, w, h)
+    mark("project_bwd")
+    torch.cuda.synchronize()
+    order = ["start", "project", "bin", "emit", "sort", "composite", "loss", "composite_bwd", "project_bwd"]
+    ms = {b: events[a].elapsed_time(events[b]) for a, b in zip(order[:-1], order[1:])}
+    info = {
+        "total": int(gids.numel()),
+        "ranges": ranges,
+        "ncon": ncon,
+        "counts": counts,
+    }
+    return ms, info
+
+
+def processed_pairs(ranges, ncon, tile_size, w, h):
+    """(tile, Gaussian) pairs visited by the forward (up to the last entry any
+    pixel of the tile processed while active) and by the backward."""
+    tw = -(-w // tile_size)
+    th = -(-h // tile_size)
+    pad = torch.zeros(th * tile_size, tw * tile_size, dtype=ncon.dtype, device=ncon.device)
+    pad[:h, :w] = ncon
+    per_tile = pad.reshape(th, tile_size, tw, tile_size).amax(dim=(1, 3)).reshape(-1).long()
+    lengths = (ranges[:, 1] - ranges[:, 0]).long()
+    fwd = int(torch.minimum(lengths, per_tile + 1).sum())
+    bwd = int(torch.minimum(lengths, per_tile).sum())
+    return fwd, bwd
+
+
+def cpu_baseline(scene, tile_size, sample_tiles):
+    """The CPU oracle (torch-CPU restatement of the reference torch backend) on a
+    bounded sample: full projection + binning of all Gaussians, then dense
+    fwd+bwd compositing of ``sample_tiles`` tiles around the image centre;
+    per-pixel time is extrapolated to the whole image."""
+    import numpy as np
+
+    from oracle import rasterizer as orc
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    cam = scene.cameras[0]
+    fx, fy = cam.focal_length
+    cx, cy = cam.principal_point
+    w, h = cam.image_size
+    ocam = orc.Camera(cam.rotation_matrix.float(), cam.translation.float(), fx, fy, cx, cy, w, h)
+    params = [p.detach().clone().requires_grad_(True) for p in scene.params()]
+    t0 = time.perf_counter()
+    proj = orc.project(*params, ocam)
+    tw, th = -(-w // tile_size), -(-h // tile_size)
+    bounds, counts = orc.tile_counts(proj, tile_size, tw, th, scene.near, scene.far)
+    keys, ids = orc.emit_intersections(bounds, proj.mean[:, 2].detach().numpy(), counts, tw)
+    sid, ranges, _ = orc.sort_intersections(keys, ids, tw * th)
+    t1 = time.perf_counter()
+    # Sample: a square block of tiles at the centre (the densest region).
+    side = max(1, int(math.isqrt(sample_tiles)))
+    tx0, ty0 = tw // 2 - side // 2, th // 2 - side // 2
+    keep = np.zeros(tw * th, dtype=bool)
+    for ty in range(ty0, ty0 + side):
+        keep[ty * tw + tx0: ty * tw + tx0 + side] = True
+    sampled = ranges.copy()
+    sampled[~keep] = sampled[~keep, :1]  # empty the other tiles
+    comp = orc.composite(proj.mean[:, 0], proj.mean[:, 1], proj.inverse[:, 0, 0], proj.inverse[:, 0, 1],
+                         proj.inverse[:, 1, 1], proj.color, proj.opacity[:, 0], sid, sampled, w, h,
+                         tile_size, tile_chunk=8)
+    ys0, xs0 = ty0 * tile_size, tx0 * tile_size
+    block = comp.image[ys0: ys0 + side * tile_size, xs0: xs0 + side * tile_size]
+    tgt = scene.target[ys0: ys0 + side * tile_size, xs0: xs0 + side * tile_size]
+    loss = (block - tgt).abs().sum() / (w * h * 3)
+    loss.backward()
+    t2 = time.perf_counter()
+    sample_px = block.shape[0] * block.shape[1]
+    full_s = (t1 - t0) + (t2 - t1) * (w * h) / sample_px
+    return {
+        "value": (w * h) / 1e6 / full_s,
+        "unit": "Mpix/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (
+            f"torch-CPU oracle, float32: projection+binning of all {scene.num_points} Gaussians "
+            f"({t1 - t0:.1f}s) + dense fwd+bwd of {side * side} central {tile_size}px tiles "
+            f"({sample_px} px, {t2 - t1:.1f}s), extrapolated per pixel to {w}x{h}"
+        ),
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
+              "(the rasterizer runs on a single device, see DESIGN.md for how it would shard)",
+              file=sys.stderr)
+        sys.exit(2)
+    from gaussian_splats import scenes
+    from gaussian_splats.kernels.rasterize import _native
+    from gaussian_splats.splats import GaussianSplat
+
+    _native.library()
+    device = torch.device("cuda:0")
+    scene = scenes.CONFIGS[args.config]()
+    cam = scene.cameras[0]
+    w, h = cam.image_size
+    splats = GaussianSplat.from_tensors(*(p.to(device) for p in scene.params()))
+    target = scene.target.to(device) if scene.target is not None else torch.rand(h, w, 3, device=device)
+    params = [p.detach() for p in splats.parameters() if p is not splats.normals][:5]
+    params = [splats.mean.detach(), splats.rotation.detach(), splats.scale.detach(),
+              splats.opacity.detach(), splats.color.detach()]
+
+    print(f"[bench] {scene.name}: N={scene.num_points} {w}x{h} tile={args.tile_size}", file=sys.stderr, flush=True)
+    for _ in range(args.warmup):
+        for p in splats.parameters():
+            p.grad = None
+        run_step(splats, cam, target, args.tile_size, scene.near, scene.far)
+    torch.cuda.synchronize()
+    print("[bench] warmup done", file=sys.stderr, flush=True)
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        for p in splats.parameters():
+            p.grad = None
+        run_step(splats, cam, target, args.tile_size, scene.near, scene.far)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = 1e3 * elapsed / args.steps
+    mpix = (w * h) / 1e6
+    print(f"[bench] timed {args.steps} steps: {ms_per_step:.3f} ms/step", file=sys.stderr, flush=True)
+
+    # Per-stage event timing (averaged over a few staged steps).
+    stage_runs = []
+    for _ in range(3):
+        ms, info = staged_step(params, cam, target, args.tile_size, scene.near, scene.far)
+        stage_runs.append(ms)
+    stages_ms = {k: sum(r[k] for r in stage_runs) / len(stage_runs) for k in stage_runs[0]}
+    fwd_pairs, bwd_pairs = processed_pairs(info["ranges"], info["ncon"], args.tile_size, w, h)
+    num_tiles = info["ranges"].shape[0]
+    sort_passes = max(1, math.ceil(max(1, (num_tiles - 1).bit_length()) / 8))
+    bytes_model = stage_bytes(scene.num_points, scene.color.shape[1], info["total"], num_tiles, w * h,
+                              fwd_pairs, bwd_pairs, sort_passes)
+    stages = {}
+    for name, ms in stages_ms.items():
+        entry = {"ms": round(ms, 4)}
+        if name in bytes_model and ms > 0:
+            gbs = bytes_model[name] / (ms * 1e-3) / 1e9
+            entry.update({"algorithmic_bytes": bytes_model[name], "GB/s": round(gbs, 1),
+                          "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)})
+        stages[name] = entry
+    dominant = max((k for k in stages if k in bytes_model), key=lambda k: stages[k]["ms"])
+    dom = stages[dominant]
+    roofline = {
+        "kernel": dominant,
+        "bound": "hbm",
+        "achieved": dom["GB/s"],
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(dom["GB/s"] / HBM_PEAK_GBS, 4),
+        "traffic": None,
+    }
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(scene, args.tile_size, args.cpu_tiles)
+
+    result = {
+        "metric": "fwd+bwd Mpix/s at 1M Gaussians SH3 1080p",
+        "value": round(mpix / (ms_per_step * 1e-3), 3),
+        "unit": "Mpix/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded BASELINE distributions)",
+        "config": {
+            "workload": f"{scene.name}: {scene.num_points} Gaussians, SH3, {w}x{h}, fwd+bwd, L1 loss",
+            "tile_size": args.tile_size,
+            "intersections": info["total"],
+        },
+        "stages": stages,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    line = json.dumps(result)
+    print(line, flush=True)
+    if args.out:
+        Path(args.out).write_text(line + "\n")
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,75 @@
+// Shared host/device helpers for the gfx950 rasterizer kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "gs_raster.h"
+
+namespace gs {
+
+// Per-thread error message behind gs_last_error().
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Checks the launch that was just enqueued; converts a HIP error into a status.
+int check_launch(const char* what);
+
+#define GS_REQUIRE(cond, code, ...)      \
+  do {                                   \
+    if (!(cond)) {                       \
+      ::gs::set_error(__VA_ARGS__);      \
+      return (code);                     \
+    }                                    \
+  } while (0)
+
+#define GS_TRY(expr)                     \
+  do {                                   \
+    int gs_status_ = (expr);             \
+    if (gs_status_ != GS_OK) return gs_status_; \
+  } while (0)
+
+constexpr int kWave = 64;
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+inline size_t align_up(size_t x, size_t a = 256) { return (x + a - 1) / a * a; }
+
+// Number of tiles along each axis (partial tiles at the right/bottom edge).
+inline int tiles_along(int pixels, int tile) { return (pixels + tile - 1) / tile; }
+
+inline bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
+
+// Validates the geometry part of a gs_view.
+int check_view(const gs_view& v, bool need_tiles);
+
+// Maps a linear workgroup index onto a work index so that consecutive work
+// items land on the same XCD.  Workgroups are dispatched round-robin over the
+// 8 XCDs (b % 8 selects the XCD); XCD x receives q + (x < r) workgroups
+// (q = nb / 8, r = nb % 8), which are given the contiguous work range starting
+// at x * q + min(x, r).  The map is a bijection of [0, nb).
+__device__ __forceinline__ int xcd_swizzle(int b, int nb) {
+  const int q = nb >> 3, r = nb & 7;
+  const int x = b & 7;
+  return x * q + min(x, r) + (b >> 3);
+}
+
+__device__ __forceinline__ uint64_t lanemask_lt() {
+  const int lane = __lane_id();
+  return lane == 0 ? 0ull : (~0ull >> (64 - lane));
+}
+
+}  // namespace gs
+
+// Packed per-Gaussian compositing record (48 bytes, three dwordx4 loads).
+struct __attribute__((aligned(16))) GsRecord {
+  float u, v, opacity, depth;
+  float inv00, inv01, inv11, cut;  // cut: largest quadratic form with alpha >= 1/255
+  float r, g, b, pad;
+};
+static_assert(sizeof(GsRecord) == 48, "record layout");

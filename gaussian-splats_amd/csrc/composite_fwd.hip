@@ -1,0 +1,182 @@
+// Forward compositing: one wave64 per tile, tile_size^2 / 64 pixels per lane,
+// front-to-back over the tile's depth-sorted list.
+//
+// Pixel semantics are those of kernels/rasterize/torch.py:172-225 with the
+// sequential transmittance and contributor count of composite.py:44-107:
+//   alpha = min(o * exp(-D/2), 0.99), zeroed below 1/255;
+//   a pixel is active for an entry while (1 - T) < opacity_threshold, checked
+//   before blending; C += T * alpha * rgb; T *= (1 - alpha) while active;
+//   n_contributors = entries processed while active (the position after the
+//   entry that deactivated the pixel, or the list length).
+// Integer pixel coordinates (no +0.5, torch.py:157-168), black background.
+//
+// Each lane gathers one Gaussian record of the next 64 list entries and tests
+// whether it can reach alpha >= 1/255 anywhere in the tile (touches_rect); the
+// wave then walks only the set bits of that ballot, broadcasting the record
+// with v_readlane.  The tile stops as soon as no pixel is active.
+#include "common.h"
+#include "raster_math.h"
+
+namespace gs {
+namespace {
+
+constexpr int kWavesPerBlock = 4;
+
+struct CompositeArgs {
+  const GsRecord* records;
+  const int32_t* ids;
+  const int64_t* ranges;
+  int width, height, tile, tiles_w, num_tiles;
+  float threshold;
+  float* image;
+  float* final_t;
+  int32_t* n_contrib;
+};
+
+template <int TILE, bool ELLIPSOID>
+__global__ __launch_bounds__(kWavesPerBlock * 64) void composite_fwd_kernel(CompositeArgs a) {
+  constexpr int NPIX = TILE * TILE;
+  constexpr int PIX = NPIX >= 64 ? NPIX / 64 : 1;
+  const int lane = threadIdx.x & 63;
+  const int wid = threadIdx.x >> 6;
+  const int tile = xcd_swizzle(blockIdx.x, gridDim.x) * kWavesPerBlock + wid;
+  if (tile >= a.num_tiles) return;
+
+  const int tx = tile % a.tiles_w;
+  const int ty = tile / a.tiles_w;
+  const int ox = tx * TILE, oy = ty * TILE;
+  const int64_t start = a.ranges[2 * tile];
+  const int64_t end = a.ranges[2 * tile + 1];
+  const int list_len = int(end - start);
+
+  float pxf[PIX], pyf[PIX];
+  float T[PIX], cr[PIX], cg[PIX], cb[PIX];
+  bool live[PIX];
+  int ncon[PIX];
+  const bool start_active = (1.0f - 1.0f) < a.threshold;
+#pragma unroll
+  for (int k = 0; k < PIX; ++k) {
+    const int q = lane + 64 * k;
+    const int px = ox + (q % TILE), py = oy + (q / TILE);
+    const bool valid = q < NPIX && px < a.width && py < a.height;
+    pxf[k] = float(px);
+    pyf[k] = float(py);
+    T[k] = 1.0f;
+    cr[k] = cg[k] = cb[k] = 0.0f;
+    live[k] = valid && start_active;
+    ncon[k] = live[k] ? list_len : 0;
+  }
+  // Pixel rectangle of the tile clipped to the image, for the overlap test.
+  const float rx0 = float(ox), ry0 = float(oy);
+  const float rx1 = float(min(ox + TILE, a.width) - 1);
+  const float ry1 = float(min(oy + TILE, a.height) - 1);
+
+  auto any_live = [&]() {
+    bool l = false;
+#pragma unroll
+    for (int k = 0; k < PIX; ++k) l |= live[k];
+    return __ballot(l) != 0;
+  };
+
+  bool running = any_live();
+  for (int64_t base = start; running && base < end; base += 64) {
+    const int64_t e = base + lane;
+    GsRecord rec;
+    bool keep = false;
+    if (e < end) {
+      rec = load_record(a.records, a.ids[e]);
+      keep = touches_rect(rec, rx0, rx1, ry0, ry1);
+    }
+    uint64_t mask = __ballot(keep);
+    while (mask) {
+      const int j = __builtin_ctzll(mask);
+      mask &= mask - 1;
+      const Splat s = broadcast(rec, j);
+      const int pos = int(base - start) + j;
+#pragma unroll
+      for (int k = 0; k < PIX; ++k) {
+        if (!live[k]) continue;
+        const float dx = pxf[k] - s.u;
+        const float dy = pyf[k] - s.v;
+        float prob;
+        const float alpha = blend_alpha(raw_alpha<ELLIPSOID>(s, quad_form(s, dx, dy), prob));
+        if (alpha == 0.0f) continue;
+        const float w = T[k] * alpha;
+        cr[k] += w * s.r;
+        cg[k] += w * s.g;
+        cb[k] += w * s.bl;
+        T[k] = T[k] * (1.0f - alpha);
+        if (!((1.0f - T[k]) < a.threshold)) {
+          live[k] = false;
+          ncon[k] = pos + 1;
+        }
+      }
+      if (!any_live()) {
+        running = false;
+        break;
+      }
+    }
+  }
+
+#pragma unroll
+  for (int k = 0; k < PIX; ++k) {
+    const int q = lane + 64 * k;
+    const int px = ox + (q % TILE), py = oy + (q / TILE);
+    if (q < NPIX && px < a.width && py < a.height) {
+      const int64_t pix = int64_t(py) * a.width + px;
+      a.image[pix * 3 + 0] = cr[k];
+      a.image[pix * 3 + 1] = cg[k];
+      a.image[pix * 3 + 2] = cb[k];
+      a.final_t[pix] = T[k];
+      a.n_contrib[pix] = ncon[k];
+    }
+  }
+}
+
+template <int TILE>
+void launch(const CompositeArgs& a, bool ellipsoid, hipStream_t s) {
+  const unsigned blocks = unsigned(ceil_div(a.num_tiles, kWavesPerBlock));
+  if (ellipsoid)
+    composite_fwd_kernel<TILE, true><<<blocks, kWavesPerBlock * 64, 0, s>>>(a);
+  else
+    composite_fwd_kernel<TILE, false><<<blocks, kWavesPerBlock * 64, 0, s>>>(a);
+}
+
+}  // namespace
+}  // namespace gs
+
+using namespace gs;
+
+extern "C" GS_API int gs_composite(const void* records, const int32_t* gaussian_ids,
+                                   const int64_t* ranges, gs_view view, float* image,
+                                   float* final_transmittance, int32_t* n_contributors,
+                                   void* stream) {
+  clear_error();
+  GS_TRY(check_view(view, true));
+  GS_REQUIRE(ranges && image && final_transmittance && n_contributors, GS_ERR_INVALID_ARGUMENT,
+             "null pointer argument");
+  GS_REQUIRE((reinterpret_cast<uintptr_t>(records) & 15u) == 0, GS_ERR_INVALID_ARGUMENT,
+             "records must be 16-byte aligned");
+  CompositeArgs a;
+  a.records = static_cast<const GsRecord*>(records);
+  a.ids = gaussian_ids;
+  a.ranges = ranges;
+  a.width = view.image_width;
+  a.height = view.image_height;
+  a.tile = view.tile_size;
+  a.tiles_w = tiles_along(view.image_width, view.tile_size);
+  a.num_tiles = a.tiles_w * tiles_along(view.image_height, view.tile_size);
+  a.threshold = view.opacity_threshold;
+  a.image = image;
+  a.final_t = final_transmittance;
+  a.n_contrib = n_contributors;
+  const bool ellipsoid = view.rendering_mode == GS_MODE_ELLIPSOID;
+  hipStream_t s = as_stream(stream);
+  switch (view.tile_size) {
+    case 4: launch<4>(a, ellipsoid, s); break;
+    case 8: launch<8>(a, ellipsoid, s); break;
+    case 16: launch<16>(a, ellipsoid, s); break;
+    default: launch<32>(a, ellipsoid, s); break;
+  }
+  return check_launch("composite");
+}

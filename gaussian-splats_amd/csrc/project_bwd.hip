@@ -1,0 +1,375 @@
+// Projection backward: chain rule from dL/d(u, v, inverse covariance, rgb,
+// opacity) to the parameters (mean, quaternion, log-scale, opacity logit, SH
+// coefficients), one thread per Gaussian.
+//
+// Differentiates the forward of project_fwd.hip, i.e. the functions of
+// splats/camera.py:81-124, splats/utils.py:8-75 and torch.py:165-203, as torch
+// autograd would: clamp/clamp_min pass the gradient on the closed interval,
+// F.normalize is differentiated through its norm, and the depth clamp of
+// camera.py:97 stops the gradient when |depth| < 1e-4.  Gaussians with
+// count == 0 receive zero gradients (project_bwd.py:32,324-334).
+// Replaces kernels/rasterize/project_bwd.py:8-381.
+#include <cmath>
+
+#include "common.h"
+#include "sh.h"
+
+namespace gs {
+namespace {
+
+constexpr int kBlock = 256;
+
+struct ProjectBwdArgs {
+  const float* mean;
+  const float* rotation;
+  const float* scale;
+  const float* opacity;
+  const float* color;
+  const float* cam_r;
+  const float* cam_t;
+  const float* inv;
+  const float* grad_in;  // [N, 9]
+  const int32_t* counts;
+  int64_t n;
+  float fx, fy, lim_x, lim_y, eps;
+  float* g_mean;
+  float* g_rot;
+  float* g_scale;
+  float* g_opacity;
+  float* g_color;
+};
+
+template <int K>
+__global__ __launch_bounds__(kBlock) void project_bwd_kernel(ProjectBwdArgs a) {
+  constexpr int F = 3 * K;
+  constexpr int S = F + 1;
+  __shared__ float coeff[kBlock * S];
+
+  const int64_t base = int64_t(blockIdx.x) * kBlock;
+  const int nvalid = int(min(int64_t(kBlock), a.n - base));
+  const int total = nvalid * F;
+  {
+    const float* src = a.color + base * F;
+    const float4* src4 = reinterpret_cast<const float4*>(src);
+    for (int i = threadIdx.x; i * 4 < total; i += kBlock) {
+      const int f = i * 4;
+      float vals[4];
+      if (f + 4 <= total) {
+        const float4 v = src4[i];
+        vals[0] = v.x;
+        vals[1] = v.y;
+        vals[2] = v.z;
+        vals[3] = v.w;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) vals[j] = (f + j < total) ? src[f + j] : 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int e = f + j;
+        if (e < total) {
+          const int g = e / F;
+          coeff[g * S + (e - g * F)] = vals[j];
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  const int64_t gi = base + threadIdx.x;
+  float* my = coeff + threadIdx.x * S;
+  if (gi < a.n) {
+    const bool counted = a.counts[gi] != 0;
+    float gmx = 0.0f, gmy = 0.0f, gmz = 0.0f;
+    float gq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float gs3[3] = {0.0f, 0.0f, 0.0f};
+    float gop = 0.0f;
+    if (!counted) {
+#pragma unroll
+      for (int i = 0; i < F; ++i) my[i] = 0.0f;
+    } else {
+      const float r00 = a.cam_r[0], r01 = a.cam_r[1], r02 = a.cam_r[2];
+      const float r10 = a.cam_r[3], r11 = a.cam_r[4], r12 = a.cam_r[5];
+      const float r20 = a.cam_r[6], r21 = a.cam_r[7], r22 = a.cam_r[8];
+      const float t0 = a.cam_t[0], t1 = a.cam_t[1], t2 = a.cam_t[2];
+      const float mx = a.mean[gi * 3 + 0], myy = a.mean[gi * 3 + 1], mz = a.mean[gi * 3 + 2];
+      const float* gin = a.grad_in + gi * 9;
+      const float gu = gin[0], gv = gin[1], gA = gin[2], gB = gin[3], gC = gin[4];
+      const float gcol[3] = {gin[5], gin[6], gin[7]};
+      const float gal = gin[8];
+
+      // ---- opacity: alpha0 = sigmoid(o) ----
+      const float alpha0 = 1.0f / (1.0f + expf(-a.opacity[gi]));
+      gop = gal * alpha0 * (1.0f - alpha0);
+
+      // ---- forward recomputation ----
+      const float px = r00 * mx + r01 * myy + r02 * mz + t0;
+      const float py = r10 * mx + r11 * myy + r12 * mz + t1;
+      const float pz = r20 * mx + r21 * myy + r22 * mz + t2;
+      const float d = -pz;
+      const bool depth_free = fabsf(d) >= 1e-4f;
+      const float dc = depth_free ? d : copysignf(1e-4f, d);
+      const float rx = px / dc, ry = py / dc;
+      const bool in_x = rx >= -a.lim_x && rx <= a.lim_x;
+      const bool in_y = ry >= -a.lim_y && ry <= a.lim_y;
+      const float nx = fminf(fmaxf(rx, -a.lim_x), a.lim_x);
+      const float ny = fminf(fmaxf(ry, -a.lim_y), a.lim_y);
+      const float j00 = a.fx / dc, j02 = a.fx * nx / dc;
+      const float j11 = -a.fy / dc, j12 = -a.fy * ny / dc;
+      const float w0[3] = {j00 * r00 + j02 * r20, j00 * r01 + j02 * r21, j00 * r02 + j02 * r22};
+      const float w1[3] = {j11 * r10 + j12 * r20, j11 * r11 + j12 * r21, j11 * r12 + j12 * r22};
+
+      const float4 q = reinterpret_cast<const float4*>(a.rotation)[gi];
+      const float qnorm = sqrtf(q.x * q.x + q.y * q.y + q.z * q.z + q.w * q.w);
+      const float qn = fmaxf(qnorm, 1e-12f);
+      const float qw = q.x / qn, qx = q.y / qn, qy = q.z / qn, qz = q.w / qn;
+      float R[3][3];
+      R[0][0] = 1.0f - 2.0f * (qy * qy + qz * qz);
+      R[0][1] = 2.0f * (qx * qy - qw * qz);
+      R[0][2] = 2.0f * (qx * qz + qw * qy);
+      R[1][0] = 2.0f * (qx * qy + qw * qz);
+      R[1][1] = 1.0f - 2.0f * (qx * qx + qz * qz);
+      R[1][2] = 2.0f * (qy * qz - qw * qx);
+      R[2][0] = 2.0f * (qx * qz - qw * qy);
+      R[2][1] = 2.0f * (qy * qz + qw * qx);
+      R[2][2] = 1.0f - 2.0f * (qx * qx + qy * qy);
+      const float s3[3] = {expf(a.scale[gi * 3 + 0]), expf(a.scale[gi * 3 + 1]),
+                           expf(a.scale[gi * 3 + 2])};
+      // N = W Rq (2x3), M = N diag(s).
+      float N[2][3], M[2][3];
+#pragma unroll
+      for (int c = 0; c < 3; ++c) {
+        N[0][c] = w0[0] * R[0][c] + w0[1] * R[1][c] + w0[2] * R[2][c];
+        N[1][c] = w1[0] * R[0][c] + w1[1] * R[1][c] + w1[2] * R[2][c];
+        M[0][c] = N[0][c] * s3[c];
+        M[1][c] = N[1][c] * s3[c];
+      }
+
+      // ---- through the 2x2 inverse: dL/dSigma = -inv G inv ----
+      const float4 inv = reinterpret_cast<const float4*>(a.inv)[gi];
+      const float i00 = inv.x, i01 = inv.y, i11 = inv.w;
+      const float t00 = i00 * gA + i01 * gB, t01 = i00 * gB + i01 * gC;
+      const float t10 = i01 * gA + i11 * gB, t11 = i01 * gB + i11 * gC;
+      const float k00 = -(t00 * i00 + t01 * i01);
+      const float k01 = -(t00 * i01 + t01 * i11);
+      const float k11 = -(t10 * i01 + t11 * i11);
+
+      // ---- Sigma = M M^T + eps I: dL/dM = 2 K M ----
+      float dN[2][3];
+#pragma unroll
+      for (int c = 0; c < 3; ++c) {
+        const float dm0 = 2.0f * (k00 * M[0][c] + k01 * M[1][c]);
+        const float dm1 = 2.0f * (k01 * M[0][c] + k11 * M[1][c]);
+        dN[0][c] = dm0 * s3[c];
+        dN[1][c] = dm1 * s3[c];
+        gs3[c] = (dm0 * N[0][c] + dm1 * N[1][c]) * s3[c];  // d/dlog s = d/ds * s
+      }
+      // dRq = W^T dN; dW = dN Rq^T.
+      float G[3][3];
+#pragma unroll
+      for (int r = 0; r < 3; ++r)
+#pragma unroll
+        for (int c = 0; c < 3; ++c) G[r][c] = w0[r] * dN[0][c] + w1[r] * dN[1][c];
+      float dW0[3], dW1[3];
+#pragma unroll
+      for (int kk = 0; kk < 3; ++kk) {
+        dW0[kk] = dN[0][0] * R[kk][0] + dN[0][1] * R[kk][1] + dN[0][2] * R[kk][2];
+        dW1[kk] = dN[1][0] * R[kk][0] + dN[1][1] * R[kk][1] + dN[1][2] * R[kk][2];
+      }
+
+      // ---- rotation matrix -> normalised quaternion -> raw quaternion ----
+      const float hw = 2.0f * (qz * (G[1][0] - G[0][1]) + qy * (G[0][2] - G[2][0]) +
+                               qx * (G[2][1] - G[1][2]));
+      const float hx = 2.0f * (qy * (G[0][1] + G[1][0]) + qz * (G[0][2] + G[2][0]) +
+                               qw * (G[2][1] - G[1][2])) -
+                       4.0f * qx * (G[1][1] + G[2][2]);
+      const float hy = 2.0f * (qx * (G[0][1] + G[1][0]) + qw * (G[0][2] - G[2][0]) +
+                               qz * (G[1][2] + G[2][1])) -
+                       4.0f * qy * (G[0][0] + G[2][2]);
+      const float hz = 2.0f * (qw * (G[1][0] - G[0][1]) + qx * (G[0][2] + G[2][0]) +
+                               qy * (G[1][2] + G[2][1])) -
+                       4.0f * qz * (G[0][0] + G[1][1]);
+      if (qnorm > 1e-12f) {
+        const float dot = qw * hw + qx * hx + qy * hy + qz * hz;
+        gq[0] = (hw - qw * dot) / qnorm;
+        gq[1] = (hx - qx * dot) / qnorm;
+        gq[2] = (hy - qy * dot) / qnorm;
+        gq[3] = (hz - qz * dot) / qnorm;
+      } else {
+        gq[0] = hw / 1e-12f;
+        gq[1] = hx / 1e-12f;
+        gq[2] = hy / 1e-12f;
+        gq[3] = hz / 1e-12f;
+      }
+
+      // ---- W = J Rc: dJ entries ----
+      const float dj00 = dW0[0] * r00 + dW0[1] * r01 + dW0[2] * r02;
+      const float dj02 = dW0[0] * r20 + dW0[1] * r21 + dW0[2] * r22;
+      const float dj11 = dW1[0] * r10 + dW1[1] * r11 + dW1[2] * r12;
+      const float dj12 = dW1[0] * r20 + dW1[1] * r21 + dW1[2] * r22;
+
+      // ---- camera-space point ----
+      // u = fx x / d + cx and v = -fy y / d + cy use the unclamped depth.
+      const float d2 = d * d;
+      float gpx = gu * a.fx / d;
+      float gpy = -gv * a.fy / d;
+      float gd = -gu * a.fx * px / d2 + gv * a.fy * py / d2;
+      // Jacobian terms use the clamped depth dc.
+      const float dc2 = dc * dc, dc3 = dc2 * dc;
+      if (in_x) gpx += dj02 * a.fx / dc2;
+      if (in_y) gpy += dj12 * (-a.fy / dc2);
+      if (depth_free) {
+        float gdc = -dj00 * a.fx / dc2 + dj11 * a.fy / dc2;
+        gdc += dj02 * (-a.fx * nx / dc2 - (in_x ? a.fx * px / dc3 : 0.0f));
+        gdc += dj12 * (a.fy * ny / dc2 + (in_y ? a.fy * py / dc3 : 0.0f));
+        gd += gdc;
+      }
+      const float gpz = -gd;
+      gmx = r00 * gpx + r10 * gpy + r20 * gpz;
+      gmy = r01 * gpx + r11 * gpy + r21 * gpz;
+      gmz = r02 * gpx + r12 * gpy + r22 * gpz;
+
+      // ---- SH colour ----
+      const float ex = -(r00 * t0 + r10 * t1 + r20 * t2) - mx;
+      const float ey = -(r01 * t0 + r11 * t1 + r21 * t2) - myy;
+      const float ez = -(r02 * t0 + r12 * t1 + r22 * t2) - mz;
+      const float enorm = sqrtf(ex * ex + ey * ey + ez * ez);
+      const float en = fmaxf(enorm, 1e-12f);
+      const float dx = ex / en, dy = ey / en, dz = ez / en;
+      float basis[K];
+      sh::basis<K>(dx, dy, dz, basis);
+      float gbasis[K];
+      float gc[3];
+#pragma unroll
+      for (int c = 0; c < 3; ++c) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < K; ++k) acc += basis[k] * my[k * 3 + c];
+        // clamp_min(0) passes the gradient where acc + 0.5 >= 0.
+        gc[c] = (acc + 0.5f >= 0.0f) ? gcol[c] : 0.0f;
+      }
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        gbasis[k] = gc[0] * my[k * 3 + 0] + gc[1] * my[k * 3 + 1] + gc[2] * my[k * 3 + 2];
+      }
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        my[k * 3 + 0] = gc[0] * basis[k];
+        my[k * 3 + 1] = gc[1] * basis[k];
+        my[k * 3 + 2] = gc[2] * basis[k];
+      }
+      if (K > 1) {
+        float gdx, gdy, gdz;
+        sh::basis_vjp<K>(dx, dy, dz, gbasis, gdx, gdy, gdz);
+        // Through e / max(|e|, 1e-12); e = camera centre - mean.
+        float gex, gey, gez;
+        if (enorm > 1e-12f) {
+          const float dot = dx * gdx + dy * gdy + dz * gdz;
+          gex = (gdx - dx * dot) / enorm;
+          gey = (gdy - dy * dot) / enorm;
+          gez = (gdz - dz * dot) / enorm;
+        } else {
+          gex = gdx / 1e-12f;
+          gey = gdy / 1e-12f;
+          gez = gdz / 1e-12f;
+        }
+        gmx -= gex;
+        gmy -= gey;
+        gmz -= gez;
+      }
+    }
+    a.g_mean[gi * 3 + 0] = gmx;
+    a.g_mean[gi * 3 + 1] = gmy;
+    a.g_mean[gi * 3 + 2] = gmz;
+    reinterpret_cast<float4*>(a.g_rot)[gi] = make_float4(gq[0], gq[1], gq[2], gq[3]);
+    a.g_scale[gi * 3 + 0] = gs3[0];
+    a.g_scale[gi * 3 + 1] = gs3[1];
+    a.g_scale[gi * 3 + 2] = gs3[2];
+    a.g_opacity[gi] = gop;
+  }
+  __syncthreads();
+
+  // Coalesced write-out of the coefficient gradients staged in LDS.
+  {
+    float* dst = a.g_color + base * F;
+    float4* dst4 = reinterpret_cast<float4*>(dst);
+    for (int i = threadIdx.x; i * 4 < total; i += kBlock) {
+      const int f = i * 4;
+      float vals[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int e = f + j;
+        const int g = e / F;
+        vals[j] = e < total ? coeff[g * S + (e - g * F)] : 0.0f;
+      }
+      if (f + 4 <= total) {
+        dst4[i] = make_float4(vals[0], vals[1], vals[2], vals[3]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (f + j < total) dst[f + j] = vals[j];
+      }
+    }
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+}  // namespace gs
+
+using namespace gs;
+
+extern "C" GS_API int gs_project_bwd(const float* mean, const float* rotation, const float* scale,
+                                     const float* opacity, const float* color, int64_t n,
+                                     int32_t num_sh, const float* camera_rotation,
+                                     const float* camera_translation, gs_view view,
+                                     const float* inverse_covariance,
+                                     const float* grad_projected, const int32_t* counts,
+                                     float* grad_mean, float* grad_rotation, float* grad_scale,
+                                     float* grad_opacity, float* grad_color, void* stream) {
+  clear_error();
+  GS_REQUIRE(n >= 0, GS_ERR_INVALID_ARGUMENT, "negative Gaussian count");
+  GS_REQUIRE(num_sh == 1 || num_sh == 4 || num_sh == 9 || num_sh == 16, GS_ERR_UNSUPPORTED,
+             "SH degrees above 3 are not implemented (got %d coefficients)", num_sh);
+  GS_REQUIRE(view.fx != 0.0f && view.fy != 0.0f, GS_ERR_INVALID_ARGUMENT, "zero focal length");
+  if (n == 0) return GS_OK;
+  GS_REQUIRE(mean && rotation && scale && opacity && color && camera_rotation &&
+                 camera_translation && inverse_covariance && grad_projected && counts &&
+                 grad_mean && grad_rotation && grad_scale && grad_opacity && grad_color,
+             GS_ERR_INVALID_ARGUMENT, "null pointer argument");
+  GS_REQUIRE(aligned16(rotation) && aligned16(color) && aligned16(inverse_covariance) &&
+                 aligned16(grad_rotation) && aligned16(grad_color),
+             GS_ERR_INVALID_ARGUMENT, "rotation/color buffers must be 16-byte aligned");
+  ProjectBwdArgs a;
+  a.mean = mean;
+  a.rotation = rotation;
+  a.scale = scale;
+  a.opacity = opacity;
+  a.color = color;
+  a.cam_r = camera_rotation;
+  a.cam_t = camera_translation;
+  a.inv = inverse_covariance;
+  a.grad_in = grad_projected;
+  a.counts = counts;
+  a.n = n;
+  a.fx = view.fx;
+  a.fy = view.fy;
+  a.lim_x = float(1.3 * (double(view.image_width) / (2.0 * double(view.fx))));
+  a.lim_y = float(1.3 * (double(view.image_height) / (2.0 * double(view.fy))));
+  a.eps = view.covariance_epsilon;
+  a.g_mean = grad_mean;
+  a.g_rot = grad_rotation;
+  a.g_scale = grad_scale;
+  a.g_opacity = grad_opacity;
+  a.g_color = grad_color;
+  const dim3 grid(unsigned(ceil_div(n, kBlock)));
+  hipStream_t s = as_stream(stream);
+  switch (num_sh) {
+    case 1: project_bwd_kernel<1><<<grid, kBlock, 0, s>>>(a); break;
+    case 4: project_bwd_kernel<4><<<grid, kBlock, 0, s>>>(a); break;
+    case 9: project_bwd_kernel<9><<<grid, kBlock, 0, s>>>(a); break;
+    default: project_bwd_kernel<16><<<grid, kBlock, 0, s>>>(a); break;
+  }
+  return check_launch("project_bwd");
+}

@@ -1,0 +1,118 @@
+// Real spherical-harmonic basis up to degree 3 (band-major, m = -l..l) and its
+// gradient with respect to the (unit) direction components.
+//
+// The basis is the normalised real SH of src/gaussian_splats/splats/utils.py:32-66,
+// written in closed polynomial form (the constants are the standard
+// normalisation factors sqrt((2l+1)/(4 pi) (l-|m|)!/(l+|m|)!) times sqrt(2) for
+// m != 0, with the Condon-Shortley phase folded into the signs).  On the unit
+// sphere the polynomials equal the recurrence; their tangential derivatives, which
+// are all that survive the normalisation of the view direction, therefore agree too.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace gs {
+namespace sh {
+
+constexpr float kC0 = 0.28209479177387814f;
+constexpr float kC1 = 0.4886025119029199f;
+constexpr float kC2a = 1.0925484305920792f;   // xy, yz, xz terms
+constexpr float kC2b = 0.31539156525252005f;  // 2zz - xx - yy
+constexpr float kC2c = 0.5462742152960396f;   // xx - yy
+constexpr float kC3a = 0.5900435899266435f;   // y(3xx - yy), x(xx - 3yy)
+constexpr float kC3b = 2.890611442640554f;    // xyz
+constexpr float kC3c = 0.4570457994644658f;   // y(4zz - xx - yy), x(...)
+constexpr float kC3d = 0.3731763325901154f;   // z(2zz - 3xx - 3yy)
+constexpr float kC3e = 1.445305721320277f;    // z(xx - yy)
+
+// basis[k] for k < K (K in {1, 4, 9, 16}).
+template <int K>
+__device__ __forceinline__ void basis(float x, float y, float z, float* b) {
+  b[0] = kC0;
+  if constexpr (K > 1) {
+    b[1] = -kC1 * y;
+    b[2] = kC1 * z;
+    b[3] = -kC1 * x;
+  }
+  if constexpr (K > 4) {
+    const float xx = x * x, yy = y * y, zz = z * z;
+    b[4] = kC2a * (x * y);
+    b[5] = -kC2a * (y * z);
+    b[6] = kC2b * (2.0f * zz - xx - yy);
+    b[7] = -kC2a * (x * z);
+    b[8] = kC2c * (xx - yy);
+    if constexpr (K > 9) {
+      b[9] = -kC3a * y * (3.0f * xx - yy);
+      b[10] = kC3b * (x * y) * z;
+      b[11] = -kC3c * y * (4.0f * zz - xx - yy);
+      b[12] = kC3d * z * (2.0f * zz - 3.0f * xx - 3.0f * yy);
+      b[13] = -kC3c * x * (4.0f * zz - xx - yy);
+      b[14] = kC3e * z * (xx - yy);
+      b[15] = -kC3a * x * (xx - 3.0f * yy);
+    }
+  }
+}
+
+// Accumulates g . d(basis)/d(x, y, z) where g[k] = dL/d basis[k].
+template <int K>
+__device__ __forceinline__ void basis_vjp(float x, float y, float z, const float* g,
+                                          float& gx, float& gy, float& gz) {
+  gx = 0.0f;
+  gy = 0.0f;
+  gz = 0.0f;
+  if constexpr (K > 1) {
+    gy -= kC1 * g[1];
+    gz += kC1 * g[2];
+    gx -= kC1 * g[3];
+  }
+  if constexpr (K > 4) {
+    const float xx = x * x, yy = y * y, zz = z * z;
+    // b4 = C2a xy
+    gx += kC2a * y * g[4];
+    gy += kC2a * x * g[4];
+    // b5 = -C2a yz
+    gy -= kC2a * z * g[5];
+    gz -= kC2a * y * g[5];
+    // b6 = C2b (2zz - xx - yy)
+    gx -= 2.0f * kC2b * x * g[6];
+    gy -= 2.0f * kC2b * y * g[6];
+    gz += 4.0f * kC2b * z * g[6];
+    // b7 = -C2a xz
+    gx -= kC2a * z * g[7];
+    gz -= kC2a * x * g[7];
+    // b8 = C2c (xx - yy)
+    gx += 2.0f * kC2c * x * g[8];
+    gy -= 2.0f * kC2c * y * g[8];
+    if constexpr (K > 9) {
+      // b9 = -C3a y (3xx - yy)
+      gx -= kC3a * 6.0f * x * y * g[9];
+      gy -= kC3a * 3.0f * (xx - yy) * g[9];
+      // b10 = C3b xyz
+      gx += kC3b * y * z * g[10];
+      gy += kC3b * x * z * g[10];
+      gz += kC3b * x * y * g[10];
+      // b11 = -C3c y (4zz - xx - yy)
+      gx += kC3c * 2.0f * x * y * g[11];
+      gy -= kC3c * (4.0f * zz - xx - 3.0f * yy) * g[11];
+      gz -= kC3c * 8.0f * y * z * g[11];
+      // b12 = C3d z (2zz - 3xx - 3yy)
+      gx -= kC3d * 6.0f * x * z * g[12];
+      gy -= kC3d * 6.0f * y * z * g[12];
+      gz += kC3d * (6.0f * zz - 3.0f * xx - 3.0f * yy) * g[12];
+      // b13 = -C3c x (4zz - xx - yy)
+      gx -= kC3c * (4.0f * zz - 3.0f * xx - yy) * g[13];
+      gy += kC3c * 2.0f * x * y * g[13];
+      gz -= kC3c * 8.0f * x * z * g[13];
+      // b14 = C3e z (xx - yy)
+      gx += kC3e * 2.0f * x * z * g[14];
+      gy -= kC3e * 2.0f * y * z * g[14];
+      gz += kC3e * (xx - yy) * g[14];
+      // b15 = -C3a x (xx - 3yy)
+      gx -= kC3a * 3.0f * (xx - yy) * g[15];
+      gy += kC3a * 6.0f * x * y * g[15];
+    }
+  }
+}
+
+}  // namespace sh
+}  // namespace gs

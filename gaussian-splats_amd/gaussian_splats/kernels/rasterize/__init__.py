@@ -1,0 +1,28 @@
+"""HIP (gfx950) rasterizer stages and the ``gaussian_splats::rasterize`` op."""
+
+from .composite import composite
+from .composite_bwd import composite_bwd
+from .interface import rasterize
+from .intersections import (
+    bin_gaussians,
+    emit_intersections,
+    emit_tiles,
+    sort_intersections,
+    sort_tiles,
+)
+from .project import pack_records, project_and_count
+from .project_bwd import project_bwd
+
+__all__ = [
+    "bin_gaussians",
+    "composite",
+    "composite_bwd",
+    "emit_intersections",
+    "emit_tiles",
+    "pack_records",
+    "project_and_count",
+    "project_bwd",
+    "rasterize",
+    "sort_intersections",
+    "sort_tiles",
+]

@@ -1,0 +1,197 @@
+"""ctypes binding of the C-ABI library ``libgs_raster.so`` (include/gs_raster.h).
+
+The library is built in-tree by ``gaussian-splats_amd/build.py``.  There is no
+fallback: every stage raises if the library is missing or if it is handed
+tensors that do not live on a ROCm GPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from ctypes import c_float, c_int, c_int32, c_int64, c_size_t, c_void_p
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parents[2] / "_lib" / "libgs_raster.so"
+ABI_VERSION = 1
+
+GS_OK = 0
+GS_ERR_INVALID_ARGUMENT = 1
+GS_ERR_UNSUPPORTED = 2
+GS_ERR_OVERFLOW = 3
+GS_ERR_HIP = 4
+GS_ERR_WORKSPACE = 5
+
+MODES = {"gaussian": 0, "ellipsoid": 1}
+
+
+class GsView(ctypes.Structure):
+    _fields_ = [
+        ("fx", c_float),
+        ("fy", c_float),
+        ("cx", c_float),
+        ("cy", c_float),
+        ("image_width", c_int32),
+        ("image_height", c_int32),
+        ("tile_size", c_int32),
+        ("near_plane", c_float),
+        ("far_plane", c_float),
+        ("rendering_mode", c_int32),
+        ("confidence", c_float),
+        ("opacity_threshold", c_float),
+        ("covariance_epsilon", c_float),
+    ]
+
+
+def make_view(
+    fx: float,
+    fy: float,
+    cx: float,
+    cy: float,
+    image_width: int,
+    image_height: int,
+    tile_size: int = 16,
+    near: float = 0.2,
+    far: float = 100.0,
+    rendering_mode: str = "gaussian",
+    confidence: float = 0.95,
+    opacity_threshold: float = 0.999,
+    covariance_epsilon: float = 0.03,
+) -> GsView:
+    if rendering_mode not in MODES:
+        raise ValueError(f"Invalid rendering mode: {rendering_mode}")
+    return GsView(
+        float(fx), float(fy), float(cx), float(cy), int(image_width), int(image_height),
+        int(tile_size), float(near), float(far), MODES[rendering_mode], float(confidence),
+        float(opacity_threshold), float(covariance_epsilon),
+    )
+
+
+_SIGNATURES = {
+    "gs_abi_version": (c_int, []),
+    "gs_last_error": (ctypes.c_char_p, []),
+    "gs_project_and_count": (
+        c_int,
+        [c_void_p] * 5 + [c_int64, c_int32, c_void_p, c_void_p, GsView] + [c_void_p] * 9,
+    ),
+    "gs_pack_records": (c_int, [c_void_p] * 4 + [c_int64, GsView, c_void_p, c_void_p]),
+    "gs_scan_workspace_bytes": (c_size_t, [c_int64]),
+    "gs_scan_counts": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "gs_emit_intersections": (
+        c_int,
+        [c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p],
+    ),
+    "gs_sort_workspace_bytes": (c_size_t, [c_int64, c_int32]),
+    "gs_sort_intersections": (
+        c_int,
+        [c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p],
+    ),
+    "gs_bin_workspace_bytes": (c_size_t, [c_int64]),
+    "gs_bin_gaussians": (
+        c_int,
+        [c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p],
+    ),
+    "gs_emit_tiles": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p],
+    ),
+    "gs_sort_tiles": (
+        c_int,
+        [c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p],
+    ),
+    "gs_composite": (c_int, [c_void_p, c_void_p, c_void_p, GsView, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "gs_composite_bwd": (
+        c_int,
+        [c_void_p] * 6 + [GsView, c_void_p, c_void_p],
+    ),
+    "gs_project_bwd": (
+        c_int,
+        [c_void_p] * 5 + [c_int64, c_int32, c_void_p, c_void_p, GsView] + [c_void_p] * 9,
+    ),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def library() -> ctypes.CDLL:
+    """Loads (once) and returns the HIP rasterizer library."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"HIP rasterizer library not built ({LIB_PATH}); run "
+                    "`python gaussian-splats_amd/build.py`"
+                )
+            lib = ctypes.CDLL(str(LIB_PATH))
+            for name, (restype, argtypes) in _SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = restype
+                fn.argtypes = argtypes
+            if lib.gs_abi_version() != ABI_VERSION:
+                raise RuntimeError(
+                    f"libgs_raster ABI {lib.gs_abi_version()} != expected {ABI_VERSION}"
+                )
+            _lib = lib
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    if status == GS_OK:
+        return
+    message = library().gs_last_error().decode(errors="replace")
+    text = f"{what}: {message}"
+    if status == GS_ERR_INVALID_ARGUMENT:
+        raise ValueError(text)
+    if status == GS_ERR_UNSUPPORTED:
+        raise NotImplementedError(text)
+    raise RuntimeError(text)
+
+
+def ptr(t: torch.Tensor | None) -> c_void_p:
+    return c_void_p(0 if t is None else t.data_ptr())
+
+
+def stream(device: torch.device) -> c_void_p:
+    return c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def require_gpu(*tensors: torch.Tensor) -> torch.device:
+    """All tensors must be on the same ROCm GPU; returns that device."""
+    device = None
+    for t in tensors:
+        if not t.is_cuda:
+            raise ValueError(
+                "the HIP rasterizer needs tensors on a ROCm GPU device "
+                f"(got a tensor on {t.device})"
+            )
+        if device is None:
+            device = t.device
+        elif t.device != device:
+            raise ValueError(f"tensors on different devices: {device} and {t.device}")
+    assert device is not None
+    return device
+
+
+def prepare(t: torch.Tensor, dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """Contiguous tensor of ``dtype`` whose data pointer is 16-byte aligned."""
+    if t.dtype != dtype:
+        raise TypeError(f"expected {dtype}, got {t.dtype}")
+    t = t.contiguous()
+    if t.data_ptr() % 16:
+        t = t.clone()
+    return t
+
+
+def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def tiles(image_width: int, image_height: int, tile_size: int) -> tuple[int, int]:
+    """(tiles_w, tiles_h), partial tiles included."""
+    return -(-image_width // tile_size), -(-image_height // tile_size)

@@ -1,0 +1,57 @@
+"""Forward tile compositing (HIP: gs_composite).
+
+Same launcher contract as the reference's
+src/gaussian_splats/kernels/rasterize/composite.py:110-162, except that image
+sizes need not be multiples of the tile size (edge tiles are masked).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _native as nat
+from .project import _check_tile, pack_records
+
+
+def composite(
+    mean: torch.Tensor,
+    inverse_covariance: torch.Tensor,
+    color: torch.Tensor,
+    opacity: torch.Tensor,
+    gaussian_ids: torch.Tensor,
+    ranges: torch.Tensor,
+    image_width: int,
+    image_height: int,
+    tile_size: int,
+    opacity_threshold: float,
+    rendering_mode: str,
+    confidence: float,
+    *,
+    records: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Composites the sorted per-tile lists; returns ``(image[H,W,3],
+    final_transmittance[H,W], n_contributors[H,W] int32)``."""
+    _check_tile(tile_size)
+    device = nat.require_gpu(mean, gaussian_ids, ranges)
+    if records is None:
+        records = pack_records(mean, inverse_covariance, color, opacity, rendering_mode, confidence)
+    tiles_w, tiles_h = nat.tiles(image_width, image_height, tile_size)
+    if ranges.shape != (tiles_w * tiles_h, 2):
+        raise ValueError(f"ranges must be [{tiles_w * tiles_h}, 2], got {tuple(ranges.shape)}")
+    ranges = nat.prepare(ranges, torch.int64)
+    gaussian_ids = nat.prepare(gaussian_ids, torch.int32)
+    image = torch.empty((image_height, image_width, 3), dtype=torch.float32, device=device)
+    final_transmittance = torch.empty((image_height, image_width), dtype=torch.float32, device=device)
+    n_contributors = torch.empty((image_height, image_width), dtype=torch.int32, device=device)
+    view = nat.make_view(
+        1.0, 1.0, 0.0, 0.0, image_width, image_height, tile_size, rendering_mode=rendering_mode,
+        confidence=confidence, opacity_threshold=opacity_threshold,
+    )
+    nat.check(
+        nat.library().gs_composite(
+            nat.ptr(records), nat.ptr(gaussian_ids), nat.ptr(ranges), view, nat.ptr(image),
+            nat.ptr(final_transmittance), nat.ptr(n_contributors), nat.stream(device),
+        ),
+        "composite",
+    )
+    return image, final_transmittance, n_contributors

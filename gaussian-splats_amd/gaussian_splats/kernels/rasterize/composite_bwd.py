@@ -1,0 +1,64 @@
+"""Backward tile compositing (HIP: gs_composite_bwd).
+
+Same launcher contract as the reference's
+src/gaussian_splats/kernels/rasterize/composite_bwd.py:207-277: returns the
+per-Gaussian gradient [N, 9] with columns (u, v, inv00, inv01, inv11, r, g, b,
+opacity).  Accumulation is always atomic (one add per tile and Gaussian), so
+``atomic`` is accepted for compatibility and ignored.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _native as nat
+from .project import _check_tile, pack_records
+
+
+def composite_bwd(
+    projected_mean: torch.Tensor,
+    inverse_covariance: torch.Tensor,
+    projected_color: torch.Tensor,
+    projected_opacity: torch.Tensor,
+    gaussian_ids: torch.Tensor,
+    ranges: torch.Tensor,
+    grad_image: torch.Tensor,
+    final_transmittance: torch.Tensor,
+    n_contributors: torch.Tensor,
+    image_width: int,
+    image_height: int,
+    tile_size: int,
+    opacity_threshold: float,
+    rendering_mode: str,
+    atomic: bool = False,
+    return_absolute: bool = False,
+    *,
+    records: torch.Tensor | None = None,
+) -> torch.Tensor:
+    if rendering_mode != "gaussian":
+        raise AssertionError("Backward gradients are only supported for Gaussian rendering.")
+    if return_absolute:
+        raise NotImplementedError("absolute mean gradients are not produced by the HIP backward")
+    _check_tile(tile_size)
+    device = nat.require_gpu(projected_mean, gaussian_ids, ranges, grad_image)
+    if records is None:
+        records = pack_records(projected_mean, inverse_covariance, projected_color, projected_opacity)
+    grad_image = nat.prepare(grad_image.float() if grad_image.dtype != torch.float32 else grad_image)
+    final_transmittance = nat.prepare(final_transmittance)
+    n_contributors = nat.prepare(n_contributors, torch.int32)
+    ranges = nat.prepare(ranges, torch.int64)
+    gaussian_ids = nat.prepare(gaussian_ids, torch.int32)
+    grad = torch.zeros((projected_mean.shape[0], 9), dtype=torch.float32, device=device)
+    view = nat.make_view(
+        1.0, 1.0, 0.0, 0.0, image_width, image_height, tile_size,
+        opacity_threshold=opacity_threshold,
+    )
+    nat.check(
+        nat.library().gs_composite_bwd(
+            nat.ptr(records), nat.ptr(gaussian_ids), nat.ptr(ranges), nat.ptr(grad_image),
+            nat.ptr(final_transmittance), nat.ptr(n_contributors), view, nat.ptr(grad),
+            nat.stream(device),
+        ),
+        "composite_bwd",
+    )
+    return grad

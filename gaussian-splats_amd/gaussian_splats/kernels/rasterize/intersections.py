@@ -1,0 +1,138 @@
+"""Tile-intersection emission and ordering (HIP).
+
+``emit_intersections`` / ``sort_intersections`` keep the contract of the
+reference's src/gaussian_splats/kernels/rasterize/intersections.py:44-88
+(64-bit keys ``tile_id << 32 | depth bits`` in Gaussian order, then a sort and
+half-open per-tile ranges), with the sort made stable so depth ties keep
+ascending Gaussian index.  ``bin_gaussians`` / ``emit_tiles`` / ``sort_tiles``
+are the fused variant the op uses: Gaussians are ordered by (depth bits, index)
+once, intersections are emitted in that order with 32-bit tile keys, and a
+stable sort on the tile bits alone yields the same ids and ranges.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _native as nat
+
+
+def emit_intersections(
+    bounds: torch.Tensor,
+    depths: torch.Tensor,
+    counts: torch.Tensor,
+    tiles_w: int,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Emits packed ``(tile ID, depth)`` keys and their Gaussian IDs, Gaussian-major."""
+    device = nat.require_gpu(bounds, depths, counts)
+    if depths.dtype != torch.float32:
+        raise TypeError(f"depths must be float32, got {depths.dtype}")
+    bounds = nat.prepare(bounds, torch.int32)
+    counts = nat.prepare(counts, torch.int32)
+    n = counts.shape[0]
+    if depths.dim() != 1:
+        raise ValueError("depths must be one-dimensional")
+    if depths.stride(0) < 1 or depths.data_ptr() % 4:
+        depths = depths.contiguous()
+    lib = nat.library()
+    offsets = torch.empty(n + 1, dtype=torch.int64, device=device)
+    ws = nat.workspace(lib.gs_scan_workspace_bytes(n), device)
+    s = nat.stream(device)
+    nat.check(lib.gs_scan_counts(nat.ptr(counts), n, nat.ptr(offsets), nat.ptr(ws), ws.numel(), s), "scan_counts")
+    total = int(offsets[n].item())
+    keys = torch.empty(total, dtype=torch.int64, device=device)
+    gaussian_ids = torch.empty(total, dtype=torch.int32, device=device)
+    if n and total:
+        nat.check(
+            lib.gs_emit_intersections(
+                nat.ptr(bounds), nat.ptr(depths), depths.stride(0), nat.ptr(offsets), n, tiles_w,
+                nat.ptr(keys), nat.ptr(gaussian_ids), s,
+            ),
+            "emit_intersections",
+        )
+    return keys, gaussian_ids
+
+
+def sort_intersections(
+    keys: torch.Tensor, gaussian_ids: torch.Tensor, num_tiles: int
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Stable sort by key; returns the sorted Gaussian IDs and int64 ranges [T, 2]."""
+    device = nat.require_gpu(keys, gaussian_ids)
+    keys = nat.prepare(keys, torch.int64).clone()
+    ids = nat.prepare(gaussian_ids, torch.int32).clone()
+    total = keys.shape[0]
+    lib = nat.library()
+    sorted_ids = torch.empty(total, dtype=torch.int32, device=device)
+    ranges = torch.empty((num_tiles, 2), dtype=torch.int64, device=device)
+    ws = nat.workspace(lib.gs_sort_workspace_bytes(total, num_tiles), device)
+    nat.check(
+        lib.gs_sort_intersections(
+            nat.ptr(keys), nat.ptr(ids), total, num_tiles, nat.ptr(sorted_ids), nat.ptr(ranges),
+            nat.ptr(ws), ws.numel(), nat.stream(device),
+        ),
+        "sort_intersections",
+    )
+    return sorted_ids, ranges
+
+
+def bin_gaussians(
+    depth_keys: torch.Tensor, counts: torch.Tensor
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Orders Gaussians by (depth bits, index) and scans their counts in that order.
+
+    ``depth_keys`` (int32 view of the u32 keys written by the projection) is consumed.
+    Returns ``(order[N] int32, offsets[N + 1] int64)``; ``offsets[N]`` is the total.
+    """
+    device = nat.require_gpu(depth_keys, counts)
+    n = counts.shape[0]
+    lib = nat.library()
+    order = torch.empty(n, dtype=torch.int32, device=device)
+    offsets = torch.empty(n + 1, dtype=torch.int64, device=device)
+    ws = nat.workspace(lib.gs_bin_workspace_bytes(n), device)
+    nat.check(
+        lib.gs_bin_gaussians(
+            nat.ptr(depth_keys), nat.ptr(counts), n, nat.ptr(order), nat.ptr(offsets), nat.ptr(ws),
+            ws.numel(), nat.stream(device),
+        ),
+        "bin_gaussians",
+    )
+    return order, offsets
+
+
+def emit_tiles(
+    bounds: torch.Tensor, order: torch.Tensor, offsets: torch.Tensor, total: int, tiles_w: int
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Emits (tile key, Gaussian id) pairs in depth order."""
+    device = nat.require_gpu(bounds, order, offsets)
+    n = order.shape[0]
+    tile_keys = torch.empty(total, dtype=torch.int32, device=device)
+    ids = torch.empty(total, dtype=torch.int32, device=device)
+    if n and total:
+        nat.check(
+            nat.library().gs_emit_tiles(
+                nat.ptr(bounds), nat.ptr(order), nat.ptr(offsets), n, tiles_w, nat.ptr(tile_keys),
+                nat.ptr(ids), nat.stream(device),
+            ),
+            "emit_tiles",
+        )
+    return tile_keys, ids
+
+
+def sort_tiles(
+    tile_keys: torch.Tensor, ids: torch.Tensor, num_tiles: int
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Stable sort of depth-ordered pairs by tile; consumes both inputs."""
+    device = nat.require_gpu(tile_keys, ids)
+    total = tile_keys.shape[0]
+    lib = nat.library()
+    sorted_ids = torch.empty(total, dtype=torch.int32, device=device)
+    ranges = torch.empty((num_tiles, 2), dtype=torch.int64, device=device)
+    ws = nat.workspace(lib.gs_sort_workspace_bytes(total, num_tiles), device)
+    nat.check(
+        lib.gs_sort_tiles(
+            nat.ptr(tile_keys), nat.ptr(ids), total, num_tiles, nat.ptr(sorted_ids), nat.ptr(ranges),
+            nat.ptr(ws), ws.numel(), nat.stream(device),
+        ),
+        "sort_tiles",
+    )
+    return sorted_ids, ranges

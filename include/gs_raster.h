@@ -1,0 +1,197 @@
+/*
+ * gs_raster.h — C ABI of the MI355X (gfx950) differentiable Gaussian-splat
+ * tile rasterizer.
+ *
+ * Every entry point takes raw device pointers, sizes as int64_t, scalars by
+ * value and an explicit HIP stream (`void*` holding a hipStream_t; NULL is
+ * the null stream).  The library never allocates, frees or synchronises:
+ * the caller owns every buffer, including scratch space sized by the
+ * matching *_workspace_bytes() query.  Functions return GS_OK (0) or a
+ * gs_status code; the message for the calling thread is available from
+ * gs_last_error().  All entry points are reentrant.
+ *
+ * Layouts (row-major, fp32 unless stated; these are the tensor layouts of
+ * the reference's custom op, src/gaussian_splats/kernels/rasterize/
+ * interface.py:17-49):
+ *   mean[N,3], rotation[N,4] (w,x,y,z, unnormalised), scale[N,3] (log sigma),
+ *   opacity[N,1] (logit), color[N,K,3] (coefficient-major, RGB innermost),
+ *   camera_rotation[3,3] (world->camera), camera_translation[3],
+ *   projected_mean[N,3] (u, v, depth), inverse_covariance[N,2,2],
+ *   projected_color[N,3], projected_opacity[N,1], bounds[N,2,2] int32
+ *   (x_min, x_max, y_min, y_max in tiles, half-open), counts[N] int32,
+ *   gaussian_ids[I] int32, ranges[T,2] int64 (half-open per tile),
+ *   image[H,W,3], final_transmittance[H,W], n_contributors[H,W] int32,
+ *   grad_projected[N,9] (u, v, inv00, inv01, inv11, r, g, b, opacity).
+ * A "record" is the 48-byte packed per-Gaussian block the compositing
+ * kernels gather: {u, v, opacity, depth}, {inv00, inv01, inv11, cut},
+ * {r, g, b, 0}.
+ *
+ * Tiles: tiles_w = ceil(W / tile_size), tiles_h = ceil(H / tile_size);
+ * pixels outside the image in the last tile row/column are masked.
+ */
+#ifndef GS_RASTER_H
+#define GS_RASTER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GS_API __attribute__((visibility("default")))
+
+#define GS_ABI_VERSION 1
+
+typedef enum gs_status {
+  GS_OK = 0,
+  GS_ERR_INVALID_ARGUMENT = 1,
+  GS_ERR_UNSUPPORTED = 2,
+  GS_ERR_OVERFLOW = 3,
+  GS_ERR_HIP = 4,
+  GS_ERR_WORKSPACE = 5
+} gs_status;
+
+typedef enum gs_rendering_mode {
+  GS_MODE_GAUSSIAN = 0,
+  GS_MODE_ELLIPSOID = 1
+} gs_rendering_mode;
+
+/* Camera intrinsics, image/tile geometry and culling planes, passed by value.
+ * Mirrors the scalar arguments of the reference op
+ * (src/gaussian_splats/kernels/rasterize/interface.py:26-37). */
+typedef struct gs_view {
+  float fx, fy, cx, cy;
+  int32_t image_width, image_height;
+  int32_t tile_size;
+  float near_plane, far_plane;
+  int32_t rendering_mode;      /* gs_rendering_mode */
+  float confidence;            /* ellipsoid mode only */
+  float opacity_threshold;     /* compositing stops once 1 - T >= this */
+  float covariance_epsilon;    /* 0.03 in the reference (camera.py:86) */
+} gs_view;
+
+/* ABI version of the loaded library (GS_ABI_VERSION). No counterpart in the
+ * reference (it has no compiled library). */
+GS_API int gs_abi_version(void);
+
+/* Message describing the last failure on the calling thread ("" if none). */
+GS_API const char* gs_last_error(void);
+
+/* Projection, SH colour, tile rectangle and culled count for N Gaussians.
+ * Replaces project_and_count (src/gaussian_splats/kernels/rasterize/
+ * project.py:256-345) with the camera semantics of splats/camera.py:81-124
+ * and splats/utils.py:8-75.  num_sh in {1, 4, 9, 16} (SH degree <= 3).
+ * `records` (N x 48 B) and `depth_keys` (N x u32: depth bits for counted
+ * Gaussians, 0xFFFFFFFF otherwise) are optional (NULL = not written). */
+GS_API int gs_project_and_count(
+    const float* mean, const float* rotation, const float* scale,
+    const float* opacity, const float* color, int64_t n, int32_t num_sh,
+    const float* camera_rotation, const float* camera_translation,
+    gs_view view,
+    float* projected_mean, float* inverse_covariance, float* projected_color,
+    float* projected_opacity, int32_t* bounds, int32_t* counts,
+    void* records, uint32_t* depth_keys, void* stream);
+
+/* Packs the per-Gaussian compositing record from the op's projected outputs
+ * (used when compositing is called stage-wise, as composite.py:110 is).
+ * `cut` is derived from opacity and the rendering mode. No counterpart in the
+ * reference (its compositor gathers the four arrays field by field,
+ * composite.py:61-91). */
+GS_API int gs_pack_records(
+    const float* projected_mean, const float* inverse_covariance,
+    const float* projected_color, const float* projected_opacity, int64_t n,
+    gs_view view, void* records, void* stream);
+
+/* Scratch for gs_emit_intersections / gs_bin_gaussians. */
+GS_API size_t gs_scan_workspace_bytes(int64_t n);
+
+/* Exclusive scan of counts in Gaussian order: offsets[0..n] (offsets[n] is the
+ * intersection total, read back by the caller).  First half of
+ * emit_intersections (intersections.py:51-52). */
+GS_API int gs_scan_counts(
+    const int32_t* counts, int64_t n, int64_t* offsets,
+    void* workspace, size_t workspace_bytes, void* stream);
+
+/* Emits reference-format keys (tile_id << 32 | depth bits) and Gaussian ids
+ * in Gaussian-major order at the scanned offsets.  Second half of
+ * emit_intersections (intersections.py:10-41,65-73).  depths has element
+ * stride depth_stride (3 for projected_mean[:, 2]). */
+GS_API int gs_emit_intersections(
+    const int32_t* bounds, const float* depths, int64_t depth_stride,
+    const int64_t* offsets, int64_t n, int32_t tiles_w,
+    int64_t* keys, int32_t* gaussian_ids, void* stream);
+
+/* Scratch for gs_sort_intersections / gs_sort_tiles. */
+GS_API size_t gs_sort_workspace_bytes(int64_t total, int32_t num_tiles);
+
+/* Stable sort of reference-format 64-bit keys with their Gaussian ids
+ * (ties keep emission order, i.e. ascending Gaussian id) and per-tile
+ * half-open ranges.  Replaces sort_intersections (intersections.py:77-88).
+ * keys/gaussian_ids are consumed (used as ping-pong buffers). */
+GS_API int gs_sort_intersections(
+    int64_t* keys, int32_t* gaussian_ids, int64_t total, int32_t num_tiles,
+    int32_t* sorted_ids, int64_t* ranges,
+    void* workspace, size_t workspace_bytes, void* stream);
+
+/* Fused binning used by the op: orders counted Gaussians by (depth bits,
+ * index), scans their counts in that order (offsets[0..n], offsets[n] =
+ * total), so that emitting in that order and stably sorting by tile yields
+ * exactly the order of the stable (tile, depth) key sort.  depth_keys (from
+ * gs_project_and_count) is consumed as sort scratch.  Replaces the scan of
+ * intersections.py:51-52. */
+GS_API size_t gs_bin_workspace_bytes(int64_t n);
+GS_API int gs_bin_gaussians(
+    uint32_t* depth_keys, const int32_t* counts, int64_t n,
+    int32_t* order, int64_t* offsets,
+    void* workspace, size_t workspace_bytes, void* stream);
+
+/* Emits 32-bit tile keys and Gaussian ids in depth order (order/offsets from
+ * gs_bin_gaussians).  Replaces the emit of intersections.py:10-41. */
+GS_API int gs_emit_tiles(
+    const int32_t* bounds, const int32_t* order, const int64_t* offsets,
+    int64_t n, int32_t tiles_w, uint32_t* tile_keys, int32_t* gaussian_ids,
+    void* stream);
+
+/* Stable LSD radix sort of (tile key, id) over ceil(log2 num_tiles) bits and
+ * tile ranges; tile_keys/gaussian_ids are consumed.  Replaces
+ * sort_intersections (intersections.py:77-88) for the fused path. */
+GS_API int gs_sort_tiles(
+    uint32_t* tile_keys, int32_t* gaussian_ids, int64_t total,
+    int32_t num_tiles, int32_t* sorted_ids, int64_t* ranges,
+    void* workspace, size_t workspace_bytes, void* stream);
+
+/* Front-to-back compositing per tile.  Replaces composite
+ * (src/gaussian_splats/kernels/rasterize/composite.py:25-162) with the
+ * pixel semantics of torch.py:172-225.  tile_size in {4, 8, 16, 32}. */
+GS_API int gs_composite(
+    const void* records, const int32_t* gaussian_ids, const int64_t* ranges,
+    gs_view view, float* image, float* final_transmittance,
+    int32_t* n_contributors, void* stream);
+
+/* Back-to-front compositing gradient, accumulated with atomics into
+ * grad_projected[N,9] (zeroed by the caller).  Replaces composite_bwd
+ * (composite_bwd.py:47-277) with the exact gradient of the forward. */
+GS_API int gs_composite_bwd(
+    const void* records, const int32_t* gaussian_ids, const int64_t* ranges,
+    const float* grad_image, const float* final_transmittance,
+    const int32_t* n_contributors, gs_view view, float* grad_projected,
+    void* stream);
+
+/* Chain rule from grad_projected to the parameters.  Replaces project_bwd
+ * (src/gaussian_splats/kernels/rasterize/project_bwd.py:8-381); gradients are
+ * zero for Gaussians with count == 0 (project_bwd.py:32,324-334). */
+GS_API int gs_project_bwd(
+    const float* mean, const float* rotation, const float* scale,
+    const float* opacity, const float* color, int64_t n, int32_t num_sh,
+    const float* camera_rotation, const float* camera_translation,
+    gs_view view, const float* inverse_covariance,
+    const float* grad_projected, const int32_t* counts,
+    float* grad_mean, float* grad_rotation, float* grad_scale,
+    float* grad_opacity, float* grad_color, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GS_RASTER_H */

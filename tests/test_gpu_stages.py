@@ -1,0 +1,206 @@
+"""Stage-wise parity of the HIP kernels against the CPU oracle (cf. the
+reference's kernels/rasterize/tests/test_project.py, test_intersections.py,
+test_composite.py).  Each stage is fed identical inputs on both sides."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from gaussian_splats import scenes
+from gaussian_splats.kernels.rasterize import (
+    bin_gaussians,
+    composite,
+    emit_intersections,
+    emit_tiles,
+    project_and_count,
+    sort_intersections,
+    sort_tiles,
+)
+from gaussian_splats.kernels.rasterize import _native as nat
+from oracle import rasterizer as orc
+from parity import assert_close_flip_aware, oracle_camera, rect_flip_tolerant_equal
+
+pytestmark = pytest.mark.gpu
+
+CONFIDENCE = 0.95
+THRESHOLD = 0.999
+
+
+def _project_both(scene, device, tile_size, mode="gaussian"):
+    cam = scene.cameras[0]
+    fx, fy = cam.focal_length
+    cx, cy = cam.principal_point
+    w, h = cam.image_size
+    params = [t.to(device) for t in scene.params()]
+    gpu = project_and_count(
+        *params, cam.rotation_matrix.to(device), cam.translation.to(device), fx, fy, cx, cy, w, h,
+        tile_size, scene.near, scene.far, mode, CONFIDENCE,
+    )
+    ocam = oracle_camera(cam)
+    proj = orc.project(*scene.params(), ocam)
+    tw, th = nat.tiles(w, h, tile_size)
+    bounds, counts = orc.tile_counts(proj, tile_size, tw, th, scene.near, scene.far, mode, CONFIDENCE)
+    return gpu, proj, bounds, counts
+
+
+@pytest.mark.parametrize("sh_degree", (0, 1, 2, 3))
+@pytest.mark.parametrize("tile_size", (8, 16))
+def test_project_matches_oracle(device, sh_degree, tile_size):
+    scene = scenes.edge_case_scene(n=2000, sh_degree=sh_degree)
+    gpu, proj, bounds, counts = _project_both(scene, device, tile_size)
+    pmean, pinv, pcol, pop, gbounds, gcounts = (t.cpu() for t in gpu)
+    torch.testing.assert_close(pmean, proj.mean.float(), rtol=2e-6, atol=1e-5)
+    visible = torch.as_tensor(counts > 0)
+    torch.testing.assert_close(pinv[visible], proj.inverse[visible].float(), rtol=1e-5, atol=1e-7)
+    torch.testing.assert_close(pcol, proj.color.float(), rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(pop, proj.opacity.float(), rtol=1e-6, atol=1e-7)
+    # Depth bits are bit-exact (same operation order, no transcendental).
+    assert torch.equal(pmean[:, 2], proj.mean[:, 2].float())
+    extent = 2 * np.sqrt(np.log(proj.opacity[:, 0].double().numpy() * 255))
+    with np.errstate(invalid="ignore"):
+        flips = rect_flip_tolerant_equal(gbounds.numpy(), bounds, proj, tile_size, extent)
+    same_rect = np.all(gbounds.numpy() == bounds, axis=(1, 2))
+    assert np.array_equal(gcounts.numpy()[same_rect], counts[same_rect])
+    assert flips <= 2
+
+
+def test_project_ellipsoid_mode(device):
+    scene = scenes.edge_case_scene(n=500, sh_degree=1)
+    gpu, proj, bounds, counts = _project_both(scene, device, 16, mode="ellipsoid")
+    extent = np.full(500, math.sqrt(-2 * math.log1p(-CONFIDENCE)))
+    rect_flip_tolerant_equal(gpu[4].cpu().numpy(), bounds, proj, 16, extent)
+
+
+def test_project_rejects_sh4(device):
+    scene = scenes.edge_case_scene(n=64, sh_degree=3)
+    color = torch.zeros(64, 25, 3)
+    cam = scene.cameras[0]
+    with pytest.raises(NotImplementedError):
+        project_and_count(
+            scene.mean.to(device), scene.rotation.to(device), scene.scale.to(device),
+            scene.opacity.to(device), color.to(device), cam.rotation_matrix.to(device),
+            cam.translation.to(device), 72.0, 72.0, 48.0, 40.0, 96, 80, 16, 0.1, 100.0,
+            "gaussian", 0.95,
+        )
+
+
+def _random_rects(n=4096, tiles_w=24, tiles_h=17, seed=42):
+    """Random tile rectangles and depths (cf. test_intersections.py:8-18), with
+    repeated depths to exercise the tie rule."""
+    g = torch.Generator().manual_seed(seed)
+    cx = torch.randint(0, tiles_w + 1, (n, 2), generator=g)
+    cy = torch.randint(0, tiles_h + 1, (n, 2), generator=g)
+    bounds = torch.stack(
+        (torch.stack((cx.amin(1), cx.amax(1)), -1), torch.stack((cy.amin(1), cy.amax(1)), -1)), 1
+    ).int()
+    depths = torch.rand(n, generator=g) * 10 + 0.1
+    depths[: n // 4] = depths[n // 4 : n // 2]  # ties
+    counts = ((bounds[:, 0, 1] - bounds[:, 0, 0]) * (bounds[:, 1, 1] - bounds[:, 1, 0])).int()
+    counts[torch.rand(n, generator=g) < 0.1] = 0  # culled
+    return bounds, depths, counts
+
+
+@pytest.mark.parametrize("shape", ((24, 17), (120, 68), (1, 1), (37, 1)))
+def test_intersections_bit_exact(device, shape):
+    tiles_w, tiles_h = shape
+    bounds, depths, counts = _random_rects(tiles_w=tiles_w, tiles_h=tiles_h)
+    keys_o, ids_o = orc.emit_intersections(bounds.numpy(), depths.numpy(), counts.numpy(), tiles_w)
+    sid_o, ranges_o, skeys_o = orc.sort_intersections(keys_o, ids_o, tiles_w * tiles_h)
+
+    keys, ids = emit_intersections(bounds.to(device), depths.to(device), counts.to(device), tiles_w)
+    assert np.array_equal(keys.cpu().numpy(), keys_o)
+    assert np.array_equal(ids.cpu().numpy(), ids_o)
+    sid, ranges = sort_intersections(keys, ids, tiles_w * tiles_h)
+    assert np.array_equal(sid.cpu().numpy(), sid_o)
+    assert np.array_equal(ranges.cpu().numpy(), ranges_o)
+
+    # Fused path: depth-ordered emission + tile-only sort gives the same lists.
+    dkeys = depths.view(torch.int32).clone()
+    dkeys[counts == 0] = -1
+    order, offsets = bin_gaussians(dkeys.to(device), counts.to(device))
+    total = int(offsets[-1].item())
+    assert total == int(counts.sum())
+    tk, tid = emit_tiles(bounds.to(device), order, offsets, total, tiles_w)
+    sid2, ranges2 = sort_tiles(tk, tid, tiles_w * tiles_h)
+    assert np.array_equal(sid2.cpu().numpy(), sid_o)
+    assert np.array_equal(ranges2.cpu().numpy(), ranges_o)
+
+    # Invariants: ranges partition [0, I); depth non-decreasing per tile,
+    # ascending id on ties (test_intersections.py:36-38).
+    r = ranges_o
+    assert r[0, 0] == 0 and r[-1, 1] == len(sid_o) and np.all(r[1:, 0] == r[:-1, 1])
+    d = depths.numpy()
+    for s, e in r[:50]:
+        seg = sid_o[s:e]
+        assert np.all((d[seg][:-1] < d[seg][1:]) | ((d[seg][:-1] == d[seg][1:]) & (seg[:-1] < seg[1:])))
+
+
+def test_intersections_empty(device):
+    bounds = torch.zeros(5, 2, 2, dtype=torch.int32, device=device)
+    counts = torch.zeros(5, dtype=torch.int32, device=device)
+    keys, ids = emit_intersections(bounds, torch.ones(5, device=device), counts, 4)
+    assert keys.numel() == 0
+    sid, ranges = sort_intersections(keys, ids, 12)
+    assert sid.numel() == 0 and torch.equal(ranges.cpu(), torch.zeros(12, 2, dtype=torch.int64))
+
+
+def test_intersections_deterministic(device):
+    bounds, depths, counts = _random_rects(n=20000, tiles_w=120, tiles_h=68, seed=3)
+    outs = []
+    for _ in range(2):
+        dkeys = depths.view(torch.int32).clone().to(device)
+        order, offsets = bin_gaussians(dkeys, counts.to(device))
+        tk, tid = emit_tiles(bounds.to(device), order, offsets, int(offsets[-1]), 120)
+        outs.append([t.cpu() for t in sort_tiles(tk, tid, 120 * 68)])
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+
+
+def _oracle_lists(proj, bounds, counts, w, h, tile_size):
+    tw, th = nat.tiles(w, h, tile_size)
+    keys, ids = orc.emit_intersections(bounds, proj.mean[:, 2].float().numpy(), counts, tw)
+    sid, ranges, _ = orc.sort_intersections(keys, ids, tw * th)
+    return sid, ranges
+
+
+@pytest.mark.parametrize("tile_size", (4, 8, 16, 32))
+@pytest.mark.parametrize("mode", ("gaussian", "ellipsoid"))
+def test_composite_matches_oracle(device, tile_size, mode):
+    scene = scenes.edge_case_scene(n=1500, sh_degree=1, image_size=(96, 80))
+    cam = scene.cameras[0]
+    w, h = cam.image_size
+    proj = orc.project(*scene.params(), oracle_camera(cam))
+    tw, th = nat.tiles(w, h, tile_size)
+    bounds, counts = orc.tile_counts(proj, tile_size, tw, th, scene.near, scene.far, mode, CONFIDENCE)
+    sid, ranges = _oracle_lists(proj, bounds, counts, w, h, tile_size)
+    exp = orc.composite(
+        proj.mean[:, 0], proj.mean[:, 1], proj.inverse[:, 0, 0], proj.inverse[:, 0, 1],
+        proj.inverse[:, 1, 1], proj.color, proj.opacity[:, 0], sid, ranges, w, h, tile_size,
+        THRESHOLD, mode, CONFIDENCE,
+    )
+    image, final_t, ncon = composite(
+        proj.mean.float().to(device), proj.inverse.float().to(device), proj.color.float().to(device),
+        proj.opacity.float().to(device), torch.as_tensor(sid).to(device),
+        torch.as_tensor(ranges).to(device), w, h, tile_size, THRESHOLD, mode, CONFIDENCE,
+    )
+    assert_close_flip_aware(image.cpu(), exp.image, exp.margin, atol=1e-5, what="image")
+    assert_close_flip_aware(final_t.cpu(), exp.final_transmittance, exp.margin, atol=1e-5, rtol=1e-4,
+                            what="final_transmittance")
+    ok = exp.margin >= 1e-4
+    assert torch.equal(ncon.cpu()[ok], exp.n_contributors[ok])
+
+
+def test_composite_empty_tiles(device):
+    """Known answer: empty ranges give a black image (test_composite.py:19-25)."""
+    n = 10
+    z = torch.zeros(n, 3, device=device)
+    inv = torch.eye(2, device=device).repeat(n, 1, 1)
+    image, final_t, ncon = composite(
+        z, inv, z, torch.ones(n, 1, device=device), torch.zeros(0, dtype=torch.int32, device=device),
+        torch.zeros(6 * 5, 2, dtype=torch.int64, device=device), 90, 70, 16, THRESHOLD, "gaussian", 0.95,
+    )
+    assert torch.count_nonzero(image) == 0
+    assert torch.all(final_t == 1) and torch.count_nonzero(ncon) == 0

@@ -122,8 +122,8 @@ def processed_pairs(ranges, ncon, tile_size, w, h):
 def cpu_baseline(scene, tile_size, sample_tiles):
     """The CPU oracle (torch-CPU restatement of the reference torch backend) on a
     bounded sample: full projection + binning of all Gaussians, then dense
-    fwd+bwd compositing of ``sample_tiles`` tiles around the image centre;
-    per-pixel time is extrapolated to the whole image."""
+    fwd+bwd compositing of ``sample_tiles`` non-empty tiles drawn at random
+    (seeded); the compositing time per pixel is extrapolated to the whole image."""
     import numpy as np
 
     from oracle import rasterizer as orc
@@ -143,24 +143,26 @@ def cpu_baseline(scene, tile_size, sample_tiles):
     keys, ids = orc.emit_intersections(bounds, proj.mean[:, 2].detach().numpy(), counts, tw)
     sid, ranges, _ = orc.sort_intersections(keys, ids, tw * th)
     t1 = time.perf_counter()
-    # Sample: a square block of tiles at the centre (the densest region).
-    side = max(1, int(math.isqrt(sample_tiles)))
-    tx0, ty0 = tw // 2 - side // 2, th // 2 - side // 2
+    # Sample: `sample_tiles` tiles drawn uniformly (seeded) from the non-empty ones.
+    rng = np.random.default_rng(0)
+    nonempty = np.nonzero(ranges[:, 1] > ranges[:, 0])[0]
+    chosen = rng.choice(nonempty, size=min(sample_tiles, len(nonempty)), replace=False)
     keep = np.zeros(tw * th, dtype=bool)
-    for ty in range(ty0, ty0 + side):
-        keep[ty * tw + tx0: ty * tw + tx0 + side] = True
+    keep[chosen] = True
     sampled = ranges.copy()
     sampled[~keep] = sampled[~keep, :1]  # empty the other tiles
     comp = orc.composite(proj.mean[:, 0], proj.mean[:, 1], proj.inverse[:, 0, 0], proj.inverse[:, 0, 1],
                          proj.inverse[:, 1, 1], proj.color, proj.opacity[:, 0], sid, sampled, w, h,
                          tile_size, tile_chunk=8)
-    ys0, xs0 = ty0 * tile_size, tx0 * tile_size
-    block = comp.image[ys0: ys0 + side * tile_size, xs0: xs0 + side * tile_size]
-    tgt = scene.target[ys0: ys0 + side * tile_size, xs0: xs0 + side * tile_size]
-    loss = (block - tgt).abs().sum() / (w * h * 3)
+    mask = torch.zeros(th * tile_size, tw * tile_size)
+    for t in chosen:
+        ty, tx = divmod(int(t), tw)
+        mask[ty * tile_size:(ty + 1) * tile_size, tx * tile_size:(tx + 1) * tile_size] = 1
+    mask = mask[:h, :w, None]
+    loss = ((comp.image - scene.target).abs() * mask).sum() / (w * h * 3)
     loss.backward()
     t2 = time.perf_counter()
-    sample_px = block.shape[0] * block.shape[1]
+    sample_px = int(mask.sum())
     full_s = (t1 - t0) + (t2 - t1) * (w * h) / sample_px
     return {
         "value": (w * h) / 1e6 / full_s,
@@ -169,7 +171,7 @@ def cpu_baseline(scene, tile_size, sample_tiles):
         "kind": "port",
         "sample": (
             f"torch-CPU oracle, float32: projection+binning of all {scene.num_points} Gaussians "
-            f"({t1 - t0:.1f}s) + dense fwd+bwd of {side * side} central {tile_size}px tiles "
+            f"({t1 - t0:.1f}s) + dense fwd+bwd of {len(chosen)} random non-empty {tile_size}px tiles "
             f"({sample_px} px, {t2 - t1:.1f}s), extrapolated per pixel to {w}x{h}"
         ),
     }
@@ -193,7 +195,6 @@ def main():
     w, h = cam.image_size
     splats = GaussianSplat.from_tensors(*(p.to(device) for p in scene.params()))
     target = scene.target.to(device) if scene.target is not None else torch.rand(h, w, 3, device=device)
-    params = [p.detach() for p in splats.parameters() if p is not splats.normals][:5]
     params = [splats.mean.detach(), splats.rotation.detach(), splats.scale.detach(),
               splats.opacity.detach(), splats.color.detach()]
 

@@ -292,12 +292,16 @@ def composite(
     parts = []
     for t0 in range(0, num_tiles, tile_chunk):
         t1 = min(num_tiles, t0 + tile_chunk)
-        lo, hi = int(ranges[t0, 0]), int(ranges[t1 - 1, 1])
-        if hi <= lo:
-            continue
         counts = ranges[t0:t1, 1] - ranges[t0:t1, 0]
+        total = int(counts.sum())
+        if total == 0:
+            continue
+        # Entry indices of the chunk's tiles (ranges need not be contiguous).
+        starts = np.repeat(ranges[t0:t1, 0], counts)
+        entry = starts + np.arange(total) - np.repeat(np.cumsum(counts) - counts, counts)
+        lo, hi = 0, total
         tile_of = torch.as_tensor(np.repeat(np.arange(t0, t1), counts), dtype=torch.int64)
-        g = ids_t[lo:hi]
+        g = ids_t[torch.as_tensor(entry, dtype=torch.int64)]
         ox = torch.as_tensor((tile_of.numpy() % tiles_w) * tile_size, dtype=dt)
         oy = torch.as_tensor((tile_of.numpy() // tiles_w) * tile_size, dtype=dt)
         px = ox[:, None] + torch.as_tensor(local_x, dtype=dt)[None]

@@ -19,6 +19,17 @@ from parity import assert_close_flip_aware, oracle_camera
 pytestmark = pytest.mark.gpu
 
 THRESHOLD = 0.999
+GRAD_MARGIN = 1e-5
+
+
+def assert_grad_close(actual, expected, scale, what):
+    err = (actual - expected).abs()
+    bound = 1e-4 * expected.abs() + 1e-6 * scale
+    bad = err > bound
+    assert not bool(bad.any()), (
+        f"{what}: {int(bad.sum())} of {bad.numel()} gradients off; worst excess "
+        f"{float((err / bound).max()):.2f}x, max abs err {float(err.max()):.3e}, scale {scale:.3e}"
+    )
 
 
 def _op_inputs(scene, device, tile_size):
@@ -115,14 +126,15 @@ def test_composite_backward_matches_autograd(device):
         torch.as_tensor(sid).to(device), torch.as_tensor(ranges).to(device),
         grad_image.to(device), final_t, ncon, w, h, ts, THRESHOLD, "gaussian",
     ).cpu()
-    good = exp.gaussian_margin >= 1e-4
-    assert float(good.double().mean()) > 0.95
-    scale = expected.abs().amax(0)
-    err = (grad.double() - expected).abs()
-    rel = err / (expected.abs() + 1e-6 * scale)
-    worst = rel[good].amax(0)
-    print("per-column worst relative error", worst)
-    torch.testing.assert_close(grad.double()[good], expected[good], rtol=1e-4, atol=1e-6 * float(scale.max()))
+    # Tolerance: 1e-4 relative, 1e-6 absolute in units of the column's largest
+    # gradient.  Gaussians one of whose discrete decisions lies within 1e-5 of
+    # its threshold are excluded: there any float32 evaluation (the reference's
+    # own included) may decide differently from float64.
+    good = exp.gaussian_margin >= GRAD_MARGIN
+    assert float(good.double().mean()) > 0.85, float(good.double().mean())
+    for col in range(9):
+        scale = float(expected[:, col].abs().max())
+        assert_grad_close(grad.double()[good, col], expected[good, col], scale, f"column {col}")
 
 
 @pytest.mark.parametrize("loss", ("sum", "mean_l1"))
@@ -153,14 +165,12 @@ def test_backward_matches_autograd(device, loss):
     out_loss.backward()
     actual = [splats.mean.grad, splats.rotation.grad, splats.scale.grad, splats.opacity.grad,
               splats.color.grad]
-    good = ref.composite.gaussian_margin >= 1e-4
-    if loss == "mean_l1":
-        # |x| has a kink at 0: drop Gaussians reaching pixels where image == target.
-        pass
-    assert float(good.double().mean()) > 0.9
+    # Tolerance: 1e-4 relative, 1e-6 absolute in units of the parameter's
+    # largest gradient, over the Gaussians whose decisions are well conditioned.
+    good = ref.composite.gaussian_margin >= GRAD_MARGIN
+    assert float(good.double().mean()) > 0.85, float(good.double().mean())
     names = ("mean", "rotation", "scale", "opacity", "color")
     for name, a, e in zip(names, actual, expected):
         a = a.detach().cpu().double()[good]
         e = e.detach()[good]
-        scale = float(e.abs().max())
-        torch.testing.assert_close(a, e, rtol=1e-4, atol=max(1e-6 * scale, 1e-12), msg=name)
+        assert_grad_close(a, e, float(e.abs().max()), name)

@@ -9,18 +9,20 @@ the tile size, and the backward is the exact gradient of the forward.
 
 from __future__ import annotations
 
-from typing import Literal
+from typing import TYPE_CHECKING, Literal
 
 import torch
 
-from ...splats.camera import Camera
-from ...splats.splats import GaussianSplat
 from . import _native as nat
 from .composite import composite
 from .composite_bwd import composite_bwd
 from .intersections import bin_gaussians, emit_tiles, sort_tiles
 from .project import _check_tile, pack_records, project_and_count
 from .project_bwd import project_bwd
+
+if TYPE_CHECKING:  # the splat API imports this module, so only for annotations
+    from ...splats.camera import Camera
+    from ...splats.splats import GaussianSplat
 
 
 def forward_pipeline(

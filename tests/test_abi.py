@@ -1,0 +1,134 @@
+"""C-ABI and host-logic checks that need no GPU: the library loads and exports
+every symbol include/gs_raster.h declares, host-side validation returns the
+documented status codes, and the Python boundary rejects what the reference
+rejects.  No kernel is launched here."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from gaussian_splats.kernels.rasterize import _native as nat
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "gs_raster.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    return re.findall(r"GS_API\s+[\w\s\*]+?\b(gs_\w+)\s*\(", text)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = nat.library()
+    names = _declared()
+    assert len(names) >= 16
+    for name in names:
+        assert hasattr(lib, name), name
+    assert lib.gs_abi_version() == nat.ABI_VERSION
+
+
+def test_workspace_queries_are_host_only():
+    lib = nat.library()
+    assert lib.gs_scan_workspace_bytes(0) > 0
+    assert lib.gs_sort_workspace_bytes(1 << 20, 8160) >= (1 << 20) * 16
+    assert lib.gs_bin_workspace_bytes(1000) > lib.gs_bin_workspace_bytes(10)
+
+
+def _view(**kw):
+    args = dict(fx=100.0, fy=100.0, cx=50.0, cy=50.0, image_width=100, image_height=100, tile_size=16)
+    args.update(kw)
+    return nat.make_view(**args)
+
+
+def test_project_rejects_unsupported_sh_before_launch():
+    lib = nat.library()
+    fake = ctypes.c_void_p(16)
+    status = lib.gs_project_and_count(
+        fake, fake, fake, fake, fake, 10, 25, fake, fake, _view(), *([fake] * 6), None, None, None
+    )
+    assert status == nat.GS_ERR_UNSUPPORTED
+    assert b"SH degrees above 3" in lib.gs_last_error()
+
+
+@pytest.mark.parametrize("tile", (0, 3, 12, 64))
+def test_invalid_tile_sizes(tile):
+    lib = nat.library()
+    fake = ctypes.c_void_p(16)
+    status = lib.gs_composite(fake, fake, fake, _view(tile_size=tile), fake, fake, fake, None)
+    assert status in (nat.GS_ERR_INVALID_ARGUMENT, nat.GS_ERR_UNSUPPORTED)
+
+
+def test_backward_rejects_ellipsoid_mode():
+    lib = nat.library()
+    fake = ctypes.c_void_p(16)
+    status = lib.gs_composite_bwd(fake, fake, fake, fake, fake, fake,
+                                  _view(rendering_mode="ellipsoid"), fake, None)
+    assert status == nat.GS_ERR_UNSUPPORTED
+    assert b"Gaussian rendering" in lib.gs_last_error()
+
+
+def test_misaligned_buffers_rejected():
+    lib = nat.library()
+    fake = ctypes.c_void_p(16)
+    bad = ctypes.c_void_p(20)
+    status = lib.gs_project_and_count(
+        fake, bad, fake, fake, fake, 10, 16, fake, fake, _view(), *([fake] * 6), None, None, None
+    )
+    assert status == nat.GS_ERR_INVALID_ARGUMENT
+
+
+def test_status_codes_map_to_python_exceptions():
+    lib = nat.library()
+    fake = ctypes.c_void_p(16)
+    status = lib.gs_composite_bwd(fake, fake, fake, fake, fake, fake, _view(rendering_mode="ellipsoid"), fake, None)
+    with pytest.raises(NotImplementedError):
+        nat.check(status, "composite_bwd")
+
+
+def test_cpu_tensors_are_rejected():
+    """The product path has no CPU fallback: host tensors raise before any launch."""
+    from gaussian_splats.scenes import edge_case_scene
+    from gaussian_splats.splats import GaussianSplat, rasterize
+
+    scene = edge_case_scene(n=40)
+    splats = GaussianSplat.from_tensors(*scene.params())
+    with pytest.raises(ValueError, match="ROCm GPU"):
+        rasterize(splats, scene.cameras[0], tile_size=16)
+
+
+def test_dispatcher_backends():
+    from gaussian_splats.splats import rasterize
+
+    with pytest.raises(ValueError, match="Unknown rasterization backend"):
+        rasterize(None, None, backend="gsplat")
+
+
+def test_tile_size_must_be_power_of_two():
+    from gaussian_splats.kernels.rasterize import project_and_count
+
+    with pytest.raises(ValueError):
+        project_and_count(*([torch.zeros(1)] * 7), 1.0, 1.0, 0.0, 0.0, 16, 16, 12, 0.1, 10.0,
+                          "gaussian", 0.95)
+
+
+def test_fake_implementation_shapes():
+    """The op traces under FakeTensorMode (torch.compile path of the viewer)."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    from torch.fx.experimental.symbolic_shapes import ShapeEnv
+
+    import gaussian_splats.kernels.rasterize.interface  # noqa: F401 (registers the op)
+
+    with FakeTensorMode(shape_env=ShapeEnv(allow_dynamic_output_shape_ops=True)):
+        n, k = 7, 16
+        args = [torch.empty(n, 3), torch.empty(n, 4), torch.empty(n, 3), torch.empty(n, 1),
+                torch.empty(n, k, 3), torch.empty(3, 3), torch.empty(3)]
+        out = torch.ops.gaussian_splats.rasterize(*args, 100.0, 100.0, 60.0, 40.0, 120, 90, 16,
+                                                  0.999, 0.2, 100.0, "gaussian", 0.95)
+    shapes = [tuple(o.shape) for o in out]
+    assert shapes[0] == (90, 120, 3) and shapes[1] == (90, 120) and shapes[2] == (90, 120)
+    assert shapes[3] == (7, 3) and shapes[4] == (7, 2, 2) and shapes[8] == (8 * 6, 2)
+    assert out[8].dtype == torch.int64 and out[7].dtype == torch.int32

@@ -1,0 +1,198 @@
+"""Pins the oracle's binning and compositing: brute-force emission, numpy
+lexsort, rectangle conservativeness, a per-pixel pure-Python compositor over
+Gaussians sorted by (depth, index), tile-size independence, the weight/
+transmittance identity, a single-Gaussian known answer and float64 finite
+differences of the whole rasterizer.  CPU only."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import rasterizer as orc
+
+
+def _scene(n=30, seed=5, k=4, w=40, h=28, spread=0.6, log_scale=-2.2):
+    g = torch.Generator().manual_seed(seed)
+    mean = torch.randn(n, 3, generator=g, dtype=torch.float64) * spread
+    rot = torch.randn(n, 4, generator=g, dtype=torch.float64)
+    scale = torch.randn(n, 3, generator=g, dtype=torch.float64) * 0.3 + log_scale
+    op = torch.randn(n, 1, generator=g, dtype=torch.float64) * 1.5
+    col = torch.randn(n, k, 3, generator=g, dtype=torch.float64) * 0.4
+    cam = orc.Camera(torch.eye(3, dtype=torch.float64), torch.tensor([0.0, 0.0, -4.0], dtype=torch.float64),
+                     0.9 * w, 0.9 * w, w / 2, h / 2, w, h)
+    return (mean, rot, scale, op, col), cam
+
+
+def test_emit_matches_brute_force():
+    rng = np.random.default_rng(0)
+    n, tw, th = 200, 9, 7
+    x = np.sort(rng.integers(0, tw + 1, size=(n, 2)), 1)
+    y = np.sort(rng.integers(0, th + 1, size=(n, 2)), 1)
+    bounds = np.stack((x, y), 1).astype(np.int32)
+    counts = ((x[:, 1] - x[:, 0]) * (y[:, 1] - y[:, 0])).astype(np.int32)
+    counts[rng.random(n) < 0.2] = 0
+    depths = rng.random(n).astype(np.float32) * 5 + 0.1
+    keys, ids = orc.emit_intersections(bounds, depths, counts, tw)
+    exp_k, exp_i = [], []
+    for gi in range(n):
+        if counts[gi] == 0:
+            continue
+        for ty in range(y[gi, 0], y[gi, 1]):
+            for tx in range(x[gi, 0], x[gi, 1]):
+                exp_k.append(((ty * tw + tx) << 32) | int(depths[gi:gi + 1].view(np.uint32)[0]))
+                exp_i.append(gi)
+    assert keys.tolist() == exp_k and ids.tolist() == exp_i
+
+
+def test_sort_matches_lexsort_and_invariants():
+    rng = np.random.default_rng(1)
+    n, tw, th = 500, 11, 6
+    x = np.sort(rng.integers(0, tw + 1, size=(n, 2)), 1)
+    y = np.sort(rng.integers(0, th + 1, size=(n, 2)), 1)
+    bounds = np.stack((x, y), 1).astype(np.int32)
+    counts = ((x[:, 1] - x[:, 0]) * (y[:, 1] - y[:, 0])).astype(np.int32)
+    depths = (rng.integers(1, 20, size=n) / 4).astype(np.float32)  # many ties
+    keys, ids = orc.emit_intersections(bounds, depths, counts, tw)
+    sid, ranges, skeys = orc.sort_intersections(keys, ids, tw * th)
+    tile = keys >> 32
+    order = np.lexsort((ids, depths[ids].view(np.uint32), tile))
+    assert np.array_equal(sid, ids[order])
+    assert ranges[0, 0] == 0 and ranges[-1, 1] == len(ids) and np.all(ranges[1:, 0] == ranges[:-1, 1])
+    assert np.array_equal(np.diff(ranges, axis=1)[:, 0], np.bincount(tile, minlength=tw * th))
+    assert np.all(np.diff(skeys) >= 0)
+
+
+def test_rectangles_are_conservative():
+    """Every pixel with alpha >= 1/255 lies inside the Gaussian's tile rectangle."""
+    params, cam = _scene(n=60, w=64, h=48, log_scale=-1.8)
+    proj = orc.project(*params, cam)
+    ts = 8
+    tw, th = 8, 6
+    bounds, counts = orc.tile_counts(proj, ts, tw, th, 0.1, 100.0)
+    ys, xs = np.mgrid[0:48, 0:64]
+    for gi in range(60):
+        u, v = proj.mean[gi, :2].numpy()
+        inv = proj.inverse[gi].numpy()
+        dx, dy = xs - u, ys - v
+        D = inv[0, 0] * dx * dx + 2 * inv[0, 1] * dx * dy + inv[1, 1] * dy * dy
+        alpha = np.minimum(proj.opacity[gi, 0].item() * np.exp(-0.5 * D), 0.99)
+        hit = alpha >= 1 / 255
+        if not hit.any() or counts[gi] == 0:
+            assert counts[gi] == 0 or not hit.any() or proj.mean[gi, 2] <= 0.1
+            continue
+        tx, ty = xs[hit] // ts, ys[hit] // ts
+        assert tx.min() >= bounds[gi, 0, 0] and tx.max() < bounds[gi, 0, 1]
+        assert ty.min() >= bounds[gi, 1, 0] and ty.max() < bounds[gi, 1, 1]
+
+
+def _brute_force(proj, w, h, near, far, thr=0.999):
+    """Per pixel, every visible Gaussian in (depth bits, index) order, float64."""
+    depth = proj.mean[:, 2].numpy()
+    order = sorted((i for i in range(len(depth)) if near < depth[i] < far),
+                   key=lambda i: (np.float32(depth[i]).view(np.uint32), i))
+    img = np.zeros((h, w, 3))
+    T = np.ones((h, w))
+    for py in range(h):
+        for px in range(w):
+            t = 1.0
+            c = np.zeros(3)
+            for i in order:
+                if not (1 - t) < thr:
+                    break
+                u, v = proj.mean[i, :2].numpy()
+                inv = proj.inverse[i].numpy()
+                dx, dy = px - u, py - v
+                D = inv[0, 0] * dx * dx + 2 * inv[0, 1] * dx * dy + inv[1, 1] * dy * dy
+                a = min(proj.opacity[i, 0].item() * math.exp(-0.5 * D), 0.99)
+                if a < 1 / 255:
+                    continue
+                c += t * a * proj.color[i].numpy()
+                t *= 1 - a
+            img[py, px] = c
+            T[py, px] = t
+    return img, T
+
+
+@pytest.mark.parametrize("tile_size", (4, 8, 16))
+def test_composite_matches_brute_force(tile_size):
+    params, cam = _scene(n=25, w=30, h=22)
+    r = orc.rasterize(*params, cam, tile_size=tile_size, near=0.1)
+    img, T = _brute_force(r.projected, cam.width, cam.height, 0.1, 100.0)
+    np.testing.assert_allclose(r.image.detach().numpy(), img, atol=1e-12)
+    np.testing.assert_allclose(r.composite.final_transmittance.numpy(), T, atol=1e-12)
+
+
+def test_image_independent_of_tile_size():
+    params, cam = _scene(n=80, w=48, h=40, spread=0.8)
+    imgs = [orc.rasterize(*params, cam, tile_size=t, near=0.1).image.detach() for t in (4, 8, 16, 32)]
+    for im in imgs[1:]:
+        torch.testing.assert_close(im, imgs[0], atol=1e-12, rtol=0)
+
+
+def test_weights_sum_to_one_minus_transmittance():
+    params, cam = _scene(n=60, w=40, h=32)
+    mean, rot, scale, op, col = params
+    white = torch.zeros_like(col)
+    white[:, 0] = (1 - 0.5) / orc.SH_C0  # rgb = 1 everywhere
+    r = orc.rasterize(mean, rot, scale, op, white, cam, tile_size=8, near=0.1)
+    torch.testing.assert_close(
+        r.image.detach(), (1 - r.composite.final_transmittance)[..., None].expand_as(r.image), atol=1e-12, rtol=0
+    )
+
+
+def test_single_gaussian_known_answer():
+    cam = orc.Camera(torch.eye(3, dtype=torch.float64), torch.zeros(3, dtype=torch.float64),
+                     50.0, 50.0, 16.0, 16.0, 32, 32)
+    mean = torch.tensor([[0.0, 0.0, -2.0]], dtype=torch.float64)
+    s = math.log(0.05)
+    scale = torch.tensor([[s, s, s]], dtype=torch.float64)
+    op = torch.tensor([[0.0]], dtype=torch.float64)  # sigmoid -> 0.5
+    col = torch.zeros(1, 1, 3, dtype=torch.float64)
+    col[0, 0] = torch.tensor([0.5, 0.0, -0.5], dtype=torch.float64) / orc.SH_C0  # rgb = (1, 0.5, 0)
+    r = orc.rasterize(mean, torch.tensor([[1.0, 0, 0, 0]], dtype=torch.float64), scale, op, col, cam,
+                      tile_size=8, near=0.1)
+    var = (50.0 / 2.0 * 0.05) ** 2 + 0.03  # fx/d * sigma, squared, + epsilon
+    ys, xs = np.mgrid[0:32, 0:32]
+    alpha = 0.5 * np.exp(-0.5 * ((xs - 16.0) ** 2 + (ys - 16.0) ** 2) / var)
+    alpha = np.where(alpha >= 1 / 255, np.minimum(alpha, 0.99), 0)
+    expected = alpha[..., None] * np.array([1.0, 0.5, 0.0])
+    np.testing.assert_allclose(r.image.detach().numpy(), expected, atol=1e-12)
+    assert int(r.composite.n_contributors[16, 16]) == 1
+
+
+def test_empty_scene_is_black():
+    params, cam = _scene(n=5)
+    mean = params[0].clone()
+    mean[:, 2] = 10.0  # behind the camera
+    r = orc.rasterize(mean, *params[1:], cam, tile_size=8, near=0.1)
+    assert float(r.image.abs().max()) == 0.0
+    assert len(r.gaussian_ids) == 0
+
+
+def test_gradients_match_finite_differences():
+    """float64 autograd of the oracle = central differences of its forward."""
+    params, cam = _scene(n=12, w=24, h=20, seed=9)
+    params = [p.clone().requires_grad_(True) for p in params]
+    g = torch.Generator().manual_seed(2)
+    weight = torch.rand(20, 24, 3, generator=g, dtype=torch.float64)
+
+    def loss(ps):
+        return (orc.rasterize(*ps, cam, tile_size=8, near=0.1).image * weight).sum()
+
+    loss(params).backward()
+    eps = 1e-6
+    rng = np.random.default_rng(0)
+    for pi, p in enumerate(params):
+        flat = p.detach().reshape(-1)
+        for idx in rng.choice(flat.numel(), size=min(12, flat.numel()), replace=False):
+            plus = [q.detach().clone() for q in params]
+            minus = [q.detach().clone() for q in params]
+            plus[pi].view(-1)[idx] += eps
+            minus[pi].view(-1)[idx] -= eps
+            fd = (loss(plus) - loss(minus)).item() / (2 * eps)
+            an = p.grad.reshape(-1)[idx].item()
+            assert abs(fd - an) <= 1e-5 * max(1.0, abs(an)), (pi, idx, fd, an)

@@ -343,17 +343,51 @@ __global__ __launch_bounds__(256) void ranges_kernel(const K* __restrict__ keys,
 }
 
 // ---------------------------------------------------------------------------
-// Load-balanced emission.  Each wave owns 64 consecutive positions p (Gaussian
-// p, or the p-th Gaussian in depth order) and walks the union of their
-// intersections 64 at a time; the owner of intersection e is found by a
-// 6-step binary search over the wave's offsets in LDS, so a Gaussian that
-// covers thousands of tiles is spread over all lanes.
+// Load-balanced emission.  Each wave owns a fixed chunk of kEmitChunk
+// consecutive output slots [c0, c1).  It finds the Gaussian owning slot c0
+// with a 64-ary search over the offsets (4 ballot rounds for 1M Gaussians),
+// then walks windows of 64 consecutive positions p (Gaussian p, or the p-th
+// Gaussian in depth order); inside a window the owner of slot e is found by a
+// 6-step binary search over the window's offsets in LDS.  Work per wave is
+// bounded by the chunk, so a Gaussian covering thousands of tiles (or a run of
+// them, as the nearest Gaussians are after the depth sort) is spread over
+// many waves.
 // ---------------------------------------------------------------------------
+constexpr int kEmitChunk = 2048;
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// local / w for 0 <= local, 1 <= w, via a float reciprocal and one correction.
+__device__ __forceinline__ int div_small(int local, int w, int& rem) {
+  int q;
+  if (local < (1 << 22)) {
+    q = int(float(local) * __builtin_amdgcn_rcpf(float(w)));
+    int r = local - q * w;
+    if (r < 0) {
+      --q;
+      r += w;
+    } else if (r >= w) {
+      ++q;
+      r -= w;
+    }
+    rem = r;
+  } else {
+    q = local / w;
+    rem = local - q * w;
+  }
+  return q;
+}
+
 template <bool REF_KEYS>
 __global__ __launch_bounds__(kBlock) void emit_kernel(
     const int4* __restrict__ bounds, const int32_t* __restrict__ order,
     const float* __restrict__ depths, int64_t depth_stride, const int64_t* __restrict__ offsets,
-    int64_t n, int tiles_w, void* __restrict__ keys_out, int32_t* __restrict__ ids_out) {
+    int64_t n, int64_t total, int tiles_w, void* __restrict__ keys_out,
+    int32_t* __restrict__ ids_out) {
   __shared__ int64_t s_off[4][65];
   __shared__ int s_x0[4][64];
   __shared__ int s_w[4][64];
@@ -363,43 +397,69 @@ __global__ __launch_bounds__(kBlock) void emit_kernel(
 
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
-  const int64_t p0 = (int64_t(blockIdx.x) * 4 + wid) * 64;
-  const int64_t p = p0 + lane;
-  if (p < n) {
-    const int g = order ? order[p] : int(p);
-    const int4 b = bounds[g];
-    s_off[wid][lane] = offsets[p];
-    s_x0[wid][lane] = b.x;
-    s_w[wid][lane] = b.y - b.x;
-    s_y0[wid][lane] = b.z;
-    s_id[wid][lane] = g;
-    s_lo[wid][lane] = REF_KEYS ? __float_as_uint(depths[int64_t(g) * depth_stride]) : 0u;
-  } else {
-    s_off[wid][lane] = offsets[n];
-    s_w[wid][lane] = 1;
-  }
-  if (lane == 0) s_off[wid][64] = offsets[min(p0 + 64, n)];
-  __syncthreads();
+  const int64_t c0 = (int64_t(blockIdx.x) * 4 + wid) * kEmitChunk;
+  if (c0 >= total) return;  // no workgroup barrier below
+  const int64_t c1 = min(total, c0 + kEmitChunk);
 
-  const int64_t w_end = s_off[wid][64];
-  for (int64_t e = s_off[wid][0] + lane; e < w_end; e += 64) {
-    int j = 0;
-#pragma unroll
-    for (int step = 32; step > 0; step >>= 1)
-      if (s_off[wid][j + step] <= e) j += step;
-    const int local = int(e - s_off[wid][j]);
-    const int w = s_w[wid][j];
-    const int row = local / w;
-    const int col = local - row * w;
-    const uint32_t tile = uint32_t((s_y0[wid][j] + row) * tiles_w + s_x0[wid][j] + col);
-    if (REF_KEYS) {
-      static_cast<uint64_t*>(keys_out)[e] = (uint64_t(tile) << 32) | uint64_t(s_lo[wid][j]);
+  // Largest p < n with offsets[p] <= c0 (its count is > 0 because c0 < total).
+  int64_t lo = 0, hi = n - 1;
+  while (lo < hi) {
+    const int64_t step = (hi - lo + 63) / 64;
+    const int64_t q = min(lo + (lane + 1) * step, hi);
+    const uint64_t m = __ballot(offsets[q] <= c0);
+    const int cnt = __popcll(m);
+    if (cnt == 0) {
+      hi = lo + step - 1;
     } else {
-      static_cast<uint32_t*>(keys_out)[e] = tile;
+      const int64_t new_lo = min(lo + cnt * step, hi);
+      if (cnt < 64) hi = min(lo + (cnt + 1) * step - 1, hi);
+      lo = new_lo;
     }
-    ids_out[e] = s_id[wid][j];
+  }
+
+  int64_t p = lo;
+  int64_t e_begin = c0;
+  while (e_begin < c1) {
+    const int64_t pp = p + lane;
+    if (pp < n) {
+      const int g = order ? order[pp] : int(pp);
+      const int4 b = bounds[g];
+      s_off[wid][lane] = offsets[pp];
+      s_x0[wid][lane] = b.x;
+      s_w[wid][lane] = max(b.y - b.x, 1);
+      s_y0[wid][lane] = b.z;
+      s_id[wid][lane] = g;
+      s_lo[wid][lane] = REF_KEYS ? __float_as_uint(depths[int64_t(g) * depth_stride]) : 0u;
+    } else {
+      s_off[wid][lane] = total;
+      s_w[wid][lane] = 1;
+    }
+    if (lane == 0) s_off[wid][64] = offsets[min(p + 64, n)];
+    wave_sync();
+    const int64_t w_end = min(c1, s_off[wid][64]);
+    for (int64_t e = e_begin + lane; e < w_end; e += 64) {
+      int j = 0;
+#pragma unroll
+      for (int step = 32; step > 0; step >>= 1)
+        if (s_off[wid][j + step] <= e) j += step;
+      const int local = int(e - s_off[wid][j]);
+      int col;
+      const int row = div_small(local, s_w[wid][j], col);
+      const uint32_t tile = uint32_t((s_y0[wid][j] + row) * tiles_w + s_x0[wid][j] + col);
+      if (REF_KEYS) {
+        static_cast<uint64_t*>(keys_out)[e] = (uint64_t(tile) << 32) | uint64_t(s_lo[wid][j]);
+      } else {
+        static_cast<uint32_t*>(keys_out)[e] = tile;
+      }
+      ids_out[e] = s_id[wid][j];
+    }
+    e_begin = max(e_begin, w_end);
+    p += 64;
+    wave_sync();
   }
 }
+
+unsigned emit_blocks(int64_t total) { return unsigned(ceil_div(total, int64_t(kEmitChunk) * 4)); }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -424,16 +484,17 @@ GS_API int gs_scan_counts(const int32_t* counts, int64_t n, int64_t* offsets, vo
 }
 
 GS_API int gs_emit_intersections(const int32_t* bounds, const float* depths, int64_t depth_stride,
-                                 const int64_t* offsets, int64_t n, int32_t tiles_w,
+                                 const int64_t* offsets, int64_t n, int64_t total, int32_t tiles_w,
                                  int64_t* keys, int32_t* gaussian_ids, void* stream) {
   clear_error();
-  GS_REQUIRE(n >= 0 && tiles_w > 0, GS_ERR_INVALID_ARGUMENT, "invalid emit arguments");
-  if (n == 0) return GS_OK;
+  GS_REQUIRE(n >= 0 && total >= 0 && tiles_w > 0, GS_ERR_INVALID_ARGUMENT,
+             "invalid emit arguments");
+  if (n == 0 || total == 0) return GS_OK;
   GS_REQUIRE(bounds && depths && offsets && keys && gaussian_ids && aligned16(bounds),
              GS_ERR_INVALID_ARGUMENT, "null or misaligned pointer");
-  emit_kernel<true><<<unsigned(ceil_div(n, kBlock)), kBlock, 0, as_stream(stream)>>>(
-      reinterpret_cast<const int4*>(bounds), nullptr, depths, depth_stride, offsets, n, tiles_w,
-      keys, gaussian_ids);
+  emit_kernel<true><<<emit_blocks(total), kBlock, 0, as_stream(stream)>>>(
+      reinterpret_cast<const int4*>(bounds), nullptr, depths, depth_stride, offsets, n, total,
+      tiles_w, keys, gaussian_ids);
   return check_launch("emit_intersections");
 }
 
@@ -490,16 +551,17 @@ GS_API int gs_bin_gaussians(uint32_t* depth_keys, const int32_t* counts, int64_t
 }
 
 GS_API int gs_emit_tiles(const int32_t* bounds, const int32_t* order, const int64_t* offsets,
-                         int64_t n, int32_t tiles_w, uint32_t* tile_keys, int32_t* gaussian_ids,
-                         void* stream) {
+                         int64_t n, int64_t total, int32_t tiles_w, uint32_t* tile_keys,
+                         int32_t* gaussian_ids, void* stream) {
   clear_error();
-  GS_REQUIRE(n >= 0 && tiles_w > 0, GS_ERR_INVALID_ARGUMENT, "invalid emit arguments");
-  if (n == 0) return GS_OK;
+  GS_REQUIRE(n >= 0 && total >= 0 && tiles_w > 0, GS_ERR_INVALID_ARGUMENT,
+             "invalid emit arguments");
+  if (n == 0 || total == 0) return GS_OK;
   GS_REQUIRE(bounds && order && offsets && tile_keys && gaussian_ids && aligned16(bounds),
              GS_ERR_INVALID_ARGUMENT, "null or misaligned pointer");
-  emit_kernel<false><<<unsigned(ceil_div(n, kBlock)), kBlock, 0, as_stream(stream)>>>(
-      reinterpret_cast<const int4*>(bounds), order, nullptr, 0, offsets, n, tiles_w, tile_keys,
-      gaussian_ids);
+  emit_kernel<false><<<emit_blocks(total), kBlock, 0, as_stream(stream)>>>(
+      reinterpret_cast<const int4*>(bounds), order, nullptr, 0, offsets, n, total, tiles_w,
+      tile_keys, gaussian_ids);
   return check_launch("emit_tiles");
 }
 

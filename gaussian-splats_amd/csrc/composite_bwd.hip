@@ -8,12 +8,17 @@
 //   dC/dalpha_i = T_i (c_i - S_i),  S_{i-1} = alpha_i c_i + (1 - alpha_i) S_i
 // with zero gradient through the 1/255 cut, the active mask and, for the
 // opacity/mean/conic, where o * G > 0.99 (clamp_max passes the gradient for
-// inputs <= 0.99).  Per Gaussian the nine partials (u, v, inv00, inv01, inv11,
-// r, g, b, opacity) are summed over the lane's pixels, reduced across the wave
-// and added once per (tile, Gaussian) with hardware fp32 atomics.
-// Replaces composite_bwd.py:47-277 (which stores per-intersection rows and
-// scatter-adds them with index_add_).
-#include "block_scan.h"
+// inputs <= 0.99).  Only g . S (g = dL/dC of the pixel) is carried, as
+// g . S_{i-1} = alpha_i (g . c_i) + (1 - alpha_i) g . S_i.
+//
+// Per Gaussian, each lane sums over its pixels the factors that do not
+// depend on the Gaussian (q = dL/dalpha * G, q dx, q dy, q dx^2, q dx dy,
+// q dy^2 and g T alpha); the wave reduces them with DPP row operations, and
+// one 9-lane fp32 atomic add writes
+//   (u, v, inv00, inv01, inv11, r, g, b, opacity) += (-2 k (a Sx + b Sy),
+//   -2 k (b Sx + c Sy), k Sxx, k Sxy, k Syy, Sr, Sg, Sb, Sq),  k = -o / 2,
+// once per (tile, Gaussian).  Replaces composite_bwd.py:47-204 and the
+// index_add_ scatter of composite_bwd.py:268-273.
 #include "common.h"
 #include "raster_math.h"
 
@@ -48,7 +53,7 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_bwd_kernel(Comp
   const int64_t start = a.ranges[2 * tile];
 
   float pxf[PIX], pyf[PIX];
-  float T[PIX], gr[PIX], gg[PIX], gb[PIX], sr[PIX], sg[PIX], sb[PIX];
+  float T[PIX], gr[PIX], gg[PIX], gb[PIX], gs_[PIX];
   int ncon[PIX];
   int max_n = 0;
 #pragma unroll
@@ -64,7 +69,7 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_bwd_kernel(Comp
     gr[k] = valid ? a.grad_image[pix * 3 + 0] : 0.0f;
     gg[k] = valid ? a.grad_image[pix * 3 + 1] : 0.0f;
     gb[k] = valid ? a.grad_image[pix * 3 + 2] : 0.0f;
-    sr[k] = sg[k] = sb[k] = 0.0f;
+    gs_[k] = 0.0f;
     max_n = max(max_n, ncon[k]);
   }
 #pragma unroll
@@ -76,23 +81,23 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_bwd_kernel(Comp
 
   for (int64_t top = start + max_n; top > start; top -= 64) {
     const int64_t e = top - 1 - lane;
-    GsRecord rec;
+    LaneSplat mine;
     int gid = 0;
     bool keep = false;
     if (e >= start) {
       gid = a.ids[e];
-      rec = load_record(a.records, gid);
+      const GsRecord rec = load_record(a.records, gid);
       keep = touches_rect(rec, rx0, rx1, ry0, ry1);
+      mine = lane_splat(rec);
     }
     uint64_t mask = __ballot(keep);
     while (mask) {
       const int j = __builtin_ctzll(mask);
       mask &= mask - 1;
-      const Splat s = broadcast(rec, j);
+      const Splat s = broadcast(mine, j);
       const int pos = int(top - 1 - start) - j;
-      float acc[9];
-#pragma unroll
-      for (int i = 0; i < 9; ++i) acc[i] = 0.0f;
+      float sq = 0.0f, sx = 0.0f, sy = 0.0f, sxx = 0.0f, sxy = 0.0f, syy = 0.0f;
+      float sr = 0.0f, sg = 0.0f, sb = 0.0f;
       bool touched = false;
 #pragma unroll
       for (int k = 0; k < PIX; ++k) {
@@ -100,41 +105,61 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_bwd_kernel(Comp
         const float dx = pxf[k] - s.u;
         const float dy = pyf[k] - s.v;
         float prob;
-        const float raw = raw_alpha<false>(s, quad_form(s, dx, dy), prob);
+        const float raw = raw_alpha<false>(s, dx, dy, prob);
         const float alpha = blend_alpha(raw);
         if (alpha == 0.0f) continue;
         touched = true;
         const float one_minus = 1.0f - alpha;
         const float t_before = T[k] * __builtin_amdgcn_rcpf(one_minus);
         const float w = t_before * alpha;
-        acc[5] += gr[k] * w;
-        acc[6] += gg[k] * w;
-        acc[7] += gb[k] * w;
-        const float dalpha =
-            t_before * (gr[k] * (s.r - sr[k]) + gg[k] * (s.g - sg[k]) + gb[k] * (s.bl - sb[k]));
-        sr[k] = alpha * s.r + one_minus * sr[k];
-        sg[k] = alpha * s.g + one_minus * sg[k];
-        sb[k] = alpha * s.bl + one_minus * sb[k];
+        sr += gr[k] * w;
+        sg += gg[k] * w;
+        sb += gb[k] * w;
+        const float gc = gr[k] * s.r + gg[k] * s.g + gb[k] * s.bl;
+        const float diff = gc - gs_[k];
+        gs_[k] += alpha * diff;
         T[k] = t_before;
-        if (raw <= kMaxAlpha) {
-          acc[8] += dalpha * prob;
-          // dL/dD = dalpha * o * dG/dD = -0.5 * dalpha * o * G.
-          const float dD = -0.5f * dalpha * s.o * prob;
-          acc[0] += -2.0f * dD * (s.a * dx + s.b * dy);
-          acc[1] += -2.0f * dD * (s.b * dx + s.c * dy);
-          acc[2] += dD * dx * dx;
-          acc[3] += dD * dx * dy;
-          acc[4] += dD * dy * dy;
-        }
+        const float q = raw <= kMaxAlpha ? t_before * diff * prob : 0.0f;
+        const float qx = q * dx;
+        const float qy = q * dy;
+        sq += q;
+        sx += qx;
+        sy += qy;
+        sxx += qx * dx;
+        sxy += qx * dy;
+        syy += qy * dy;
       }
       if (__ballot(touched) == 0) continue;
-#pragma unroll
-      for (int i = 0; i < 9; ++i) acc[i] = wave_sum(acc[i]);
-      if (lane == 0) {
+      sq = wave_sum_lane63(sq);
+      sx = wave_sum_lane63(sx);
+      sy = wave_sum_lane63(sy);
+      sxx = wave_sum_lane63(sxx);
+      sxy = wave_sum_lane63(sxy);
+      syy = wave_sum_lane63(syy);
+      sr = wave_sum_lane63(sr);
+      sg = wave_sum_lane63(sg);
+      sb = wave_sum_lane63(sb);
+      // Gaussian constants, uniform across the wave.
+      const float k = -0.5f * s.o;
+      const float ga = bcast(mine.a, j), gbb = bcast(mine.bb, j), gcc = bcast(mine.c, j);
+      const float tq = bcast(sq, 63), tx_ = bcast(sx, 63), ty_ = bcast(sy, 63);
+      const float txx = bcast(sxx, 63), txy = bcast(sxy, 63), tyy = bcast(syy, 63);
+      const float tr = bcast(sr, 63), tg = bcast(sg, 63), tb = bcast(sb, 63);
+      float val;
+      switch (lane) {
+        case 0: val = -2.0f * k * (ga * tx_ + gbb * ty_); break;
+        case 1: val = -2.0f * k * (gbb * tx_ + gcc * ty_); break;
+        case 2: val = k * txx; break;
+        case 3: val = k * txy; break;
+        case 4: val = k * tyy; break;
+        case 5: val = tr; break;
+        case 6: val = tg; break;
+        case 7: val = tb; break;
+        default: val = tq; break;
+      }
+      if (lane < 9) {
         const int g = __builtin_amdgcn_readlane(gid, j);
-        float* dst = a.grad + int64_t(g) * 9;
-#pragma unroll
-        for (int i = 0; i < 9; ++i) unsafeAtomicAdd(dst + i, acc[i]);
+        unsafeAtomicAdd(a.grad + int64_t(g) * 9 + lane, val);
       }
     }
   }

@@ -81,25 +81,24 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_fwd_kernel(Comp
   bool running = any_live();
   for (int64_t base = start; running && base < end; base += 64) {
     const int64_t e = base + lane;
-    GsRecord rec;
+    LaneSplat mine;
     bool keep = false;
     if (e < end) {
-      rec = load_record(a.records, a.ids[e]);
+      const GsRecord rec = load_record(a.records, a.ids[e]);
       keep = touches_rect(rec, rx0, rx1, ry0, ry1);
+      mine = lane_splat(rec);
     }
     uint64_t mask = __ballot(keep);
     while (mask) {
       const int j = __builtin_ctzll(mask);
       mask &= mask - 1;
-      const Splat s = broadcast(rec, j);
+      const Splat s = broadcast(mine, j);
       const int pos = int(base - start) + j;
 #pragma unroll
       for (int k = 0; k < PIX; ++k) {
         if (!live[k]) continue;
-        const float dx = pxf[k] - s.u;
-        const float dy = pyf[k] - s.v;
         float prob;
-        const float alpha = blend_alpha(raw_alpha<ELLIPSOID>(s, quad_form(s, dx, dy), prob));
+        const float alpha = blend_alpha(raw_alpha<ELLIPSOID>(s, pxf[k] - s.u, pyf[k] - s.v, prob));
         if (alpha == 0.0f) continue;
         const float w = T[k] * alpha;
         cr[k] += w * s.r;

@@ -12,25 +12,52 @@ constexpr float kMinAlpha = 1.0f / 255.0f;  // torch.py:350, composite.py:82
 constexpr float kMaxAlpha = 0.99f;          // torch.py:349, composite.py:81
 constexpr float kNegHalfLog2e = -0.72134752044448170f;  // -0.5 / ln 2
 
-// Gaussian broadcast to every lane of a wave (values live in SGPRs).
+// Gaussian broadcast to every lane of a wave (values live in SGPRs).  The
+// conic is pre-scaled so that exp(-D/2) = exp2(pa dx^2 + pb dx dy + pc dy^2)
+// with D the quadratic form a dx^2 + 2 b dx dy + c dy^2 of utils.py:78-87.
 struct Splat {
-  float u, v, o, a, b, c, cut, r, g, bl;
+  float u, v, o, pa, pb, pc, cut, r, g, bl;
 };
 
-// Quadratic form of the inverse covariance at pixel offset (dx, dy), in the
-// term order of utils.py:78-87 / composite.py:73.
-__device__ __forceinline__ float quad_form(const Splat& s, float dx, float dy) {
-  return s.a * dx * dx + 2.0f * s.b * dx * dy + s.c * dy * dy;
+// Per-lane view of a gathered record with the pre-scaled conic.
+struct LaneSplat {
+  float u, v, o, pa, pb, pc, cut, r, g, b;
+  float a, bb, c;  // unscaled inverse covariance (for the mean gradient)
+};
+
+__device__ __forceinline__ LaneSplat lane_splat(const GsRecord& r) {
+  LaneSplat s;
+  s.u = r.u;
+  s.v = r.v;
+  s.o = r.opacity;
+  s.pa = kNegHalfLog2e * r.inv00;
+  s.pb = (2.0f * kNegHalfLog2e) * r.inv01;
+  s.pc = kNegHalfLog2e * r.inv11;
+  s.cut = r.cut;
+  s.r = r.r;
+  s.g = r.g;
+  s.b = r.b;
+  s.a = r.inv00;
+  s.bb = r.inv01;
+  s.c = r.inv11;
+  return s;
+}
+
+// log2 of the Gaussian falloff at pixel offset (dx, dy).
+__device__ __forceinline__ float falloff_log2(const Splat& s, float dx, float dy) {
+  return dx * (s.pa * dx + s.pb * dy) + s.pc * (dy * dy);
 }
 
 // Unclamped alpha = opacity * probability (utils.py:90-99); `prob` returns the
-// probability.  Gaussian mode uses exp(-D/2) = exp2(-D/(2 ln 2)).
+// probability.  Ellipsoid mode compares D = power / (-0.5 log2 e) with the
+// cutoff stored in the record.
 template <bool ELLIPSOID>
-__device__ __forceinline__ float raw_alpha(const Splat& s, float D, float& prob) {
+__device__ __forceinline__ float raw_alpha(const Splat& s, float dx, float dy, float& prob) {
+  const float power = falloff_log2(s, dx, dy);
   if constexpr (ELLIPSOID) {
-    prob = D <= s.cut ? 1.0f : 0.0f;
+    prob = power >= kNegHalfLog2e * s.cut ? 1.0f : 0.0f;
   } else {
-    prob = __builtin_amdgcn_exp2f(D * kNegHalfLog2e);
+    prob = __builtin_amdgcn_exp2f(power);
   }
   return s.o * prob;
 }
@@ -104,21 +131,41 @@ __device__ __forceinline__ float bcast(float x, int j) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), j));
 }
 
-// Broadcasts lane j's record to the whole wave (v_readlane into SGPRs, so the
+// Broadcasts lane j's splat to the whole wave (v_readlane into SGPRs, so the
 // per-pixel math takes the Gaussian's fields as scalar operands).
-__device__ __forceinline__ Splat broadcast(const GsRecord& r, int j) {
+__device__ __forceinline__ Splat broadcast(const LaneSplat& l, int j) {
   Splat s;
-  s.u = bcast(r.u, j);
-  s.v = bcast(r.v, j);
-  s.o = bcast(r.opacity, j);
-  s.a = bcast(r.inv00, j);
-  s.b = bcast(r.inv01, j);
-  s.c = bcast(r.inv11, j);
-  s.cut = bcast(r.cut, j);
-  s.r = bcast(r.r, j);
-  s.g = bcast(r.g, j);
-  s.bl = bcast(r.b, j);
+  s.u = bcast(l.u, j);
+  s.v = bcast(l.v, j);
+  s.o = bcast(l.o, j);
+  s.pa = bcast(l.pa, j);
+  s.pb = bcast(l.pb, j);
+  s.pc = bcast(l.pc, j);
+  s.cut = bcast(l.cut, j);
+  s.r = bcast(l.r, j);
+  s.g = bcast(l.g, j);
+  s.bl = bcast(l.b, j);
   return s;
+}
+
+// DPP move with `old` = 0 for lanes the row mask leaves unwritten.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp0(float v) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
+
+// Sum over the 64 lanes, valid in lane 63: quad_perm xor 1 and xor 2, row
+// half-mirror and mirror (each row of 16 then holds its row sum), then
+// row_bcast:15 and row_bcast:31 carry rows 0..2 into row 3.  Needs a full EXEC.
+__device__ __forceinline__ float wave_sum_lane63(float v) {
+  v += dpp0<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+  v += dpp0<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+  v += dpp0<0x141, 0xF>(v);  // row_half_mirror
+  v += dpp0<0x140, 0xF>(v);  // row_mirror
+  v += dpp0<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+  v += dpp0<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+  return v;
 }
 
 }  // namespace gs

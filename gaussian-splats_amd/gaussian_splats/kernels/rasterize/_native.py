@@ -81,7 +81,7 @@ _SIGNATURES = {
     "gs_scan_counts": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_size_t, c_void_p]),
     "gs_emit_intersections": (
         c_int,
-        [c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p],
+        [c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int32, c_void_p, c_void_p, c_void_p],
     ),
     "gs_sort_workspace_bytes": (c_size_t, [c_int64, c_int32]),
     "gs_sort_intersections": (
@@ -95,7 +95,7 @@ _SIGNATURES = {
     ),
     "gs_emit_tiles": (
         c_int,
-        [c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p],
+        [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int32, c_void_p, c_void_p, c_void_p],
     ),
     "gs_sort_tiles": (
         c_int,

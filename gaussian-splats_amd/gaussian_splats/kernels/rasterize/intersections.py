@@ -45,7 +45,7 @@ def emit_intersections(
     if n and total:
         nat.check(
             lib.gs_emit_intersections(
-                nat.ptr(bounds), nat.ptr(depths), depths.stride(0), nat.ptr(offsets), n, tiles_w,
+                nat.ptr(bounds), nat.ptr(depths), depths.stride(0), nat.ptr(offsets), n, total, tiles_w,
                 nat.ptr(keys), nat.ptr(gaussian_ids), s,
             ),
             "emit_intersections",
@@ -110,7 +110,7 @@ def emit_tiles(
     if n and total:
         nat.check(
             nat.library().gs_emit_tiles(
-                nat.ptr(bounds), nat.ptr(order), nat.ptr(offsets), n, tiles_w, nat.ptr(tile_keys),
+                nat.ptr(bounds), nat.ptr(order), nat.ptr(offsets), n, total, tiles_w, nat.ptr(tile_keys),
                 nat.ptr(ids), nat.stream(device),
             ),
             "emit_tiles",

@@ -114,12 +114,12 @@ GS_API int gs_scan_counts(
     void* workspace, size_t workspace_bytes, void* stream);
 
 /* Emits reference-format keys (tile_id << 32 | depth bits) and Gaussian ids
- * in Gaussian-major order at the scanned offsets.  Second half of
- * emit_intersections (intersections.py:10-41,65-73).  depths has element
- * stride depth_stride (3 for projected_mean[:, 2]). */
+ * in Gaussian-major order at the scanned offsets (total = offsets[n]).  Second
+ * half of emit_intersections (intersections.py:10-41,65-73).  depths has
+ * element stride depth_stride (3 for projected_mean[:, 2]). */
 GS_API int gs_emit_intersections(
     const int32_t* bounds, const float* depths, int64_t depth_stride,
-    const int64_t* offsets, int64_t n, int32_t tiles_w,
+    const int64_t* offsets, int64_t n, int64_t total, int32_t tiles_w,
     int64_t* keys, int32_t* gaussian_ids, void* stream);
 
 /* Scratch for gs_sort_intersections / gs_sort_tiles. */
@@ -147,11 +147,12 @@ GS_API int gs_bin_gaussians(
     void* workspace, size_t workspace_bytes, void* stream);
 
 /* Emits 32-bit tile keys and Gaussian ids in depth order (order/offsets from
- * gs_bin_gaussians).  Replaces the emit of intersections.py:10-41. */
+ * gs_bin_gaussians; total = offsets[n]).  Replaces the emit of
+ * intersections.py:10-41. */
 GS_API int gs_emit_tiles(
     const int32_t* bounds, const int32_t* order, const int64_t* offsets,
-    int64_t n, int32_t tiles_w, uint32_t* tile_keys, int32_t* gaussian_ids,
-    void* stream);
+    int64_t n, int64_t total, int32_t tiles_w, uint32_t* tile_keys,
+    int32_t* gaussian_ids, void* stream);
 
 /* Stable LSD radix sort of (tile key, id) over ceil(log2 num_tiles) bits and
  * tile ranges; tile_keys/gaussian_ids are consumed.  Replaces

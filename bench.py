@@ -66,7 +66,7 @@ def run_step(splats, cam, target, tile_size, near, far):
 
 def staged_step(params, cam, target, tile_size, near, far):
     """One fwd+bwd through the stage functions with an event after each stage."""
-    from gaussian_splats.kernels.rasterize import composite_bwd, pack_records, project_bwd
+    from gaussian_splats.kernels.rasterize import composite_bwd, project_bwd
     from gaussian_splats.kernels.rasterize.interface import forward_pipeline
 
     events = {}
@@ -86,10 +86,10 @@ def staged_step(params, cam, target, tile_size, near, far):
     image, final_t, ncon, pmean, pinv, pcol, pop, gids, ranges, counts = out
     diff = image - target
     grad_image = torch.sign(diff) / diff.numel()
+    grad_proj = torch.zeros((pmean.shape[0], 9), dtype=torch.float32, device=pmean.device)
     mark("loss")
-    records = pack_records(pmean, pinv, pcol, pop)
-    grad_proj = composite_bwd(pmean, pinv, pcol, pop, gids, ranges, grad_image, final_t, ncon, w, h,
-                              tile_size, 0.999, "gaussian", records=records)
+    composite_bwd(pmean, pinv, pcol, pop, gids, ranges, grad_image, final_t, ncon, w, h,
+                  tile_size, 0.999, "gaussian", out=grad_proj)
     mark("composite_bwd")
     project_bwd(*params, R, t, pinv, grad_proj, counts, fx, fy, w, h)
     mark("project_bwd")

@@ -28,7 +28,10 @@ namespace {
 constexpr int kWavesPerBlock = 4;
 
 struct CompositeBwdArgs {
-  const GsRecord* records;
+  const float* pmean;
+  const float* pinv;
+  const float* pcolor;
+  const float* popacity;
   const int32_t* ids;
   const int64_t* ranges;
   const float* grad_image;
@@ -86,7 +89,7 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_bwd_kernel(Comp
     bool keep = false;
     if (e >= start) {
       gid = a.ids[e];
-      const GsRecord rec = load_record(a.records, gid);
+      const GsRecord rec = load_projected(a.pmean, a.pinv, a.pcolor, a.popacity, gid);
       keep = touches_rect(rec, rx0, rx1, ry0, ry1);
       mine = lane_splat(rec);
     }
@@ -99,18 +102,19 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_bwd_kernel(Comp
       float sq = 0.0f, sx = 0.0f, sy = 0.0f, sxx = 0.0f, sxy = 0.0f, syy = 0.0f;
       float sr = 0.0f, sg = 0.0f, sb = 0.0f;
       bool touched = false;
+      // Branch-free: an entry a pixel did not process while active, or whose
+      // alpha is cut to 0, runs with alpha = 0, which leaves T, g.S and every
+      // sum unchanged.
 #pragma unroll
       for (int k = 0; k < PIX; ++k) {
-        if (pos >= ncon[k]) continue;
         const float dx = pxf[k] - s.u;
         const float dy = pyf[k] - s.v;
         float prob;
         const float raw = raw_alpha<false>(s, dx, dy, prob);
-        const float alpha = blend_alpha(raw);
-        if (alpha == 0.0f) continue;
-        touched = true;
-        const float one_minus = 1.0f - alpha;
-        const float t_before = T[k] * __builtin_amdgcn_rcpf(one_minus);
+        const float alpha = pos < ncon[k] ? blend_alpha(raw) : 0.0f;
+        const bool hit = alpha > 0.0f;
+        touched |= hit;
+        const float t_before = hit ? T[k] * __builtin_amdgcn_rcpf(1.0f - alpha) : T[k];
         const float w = t_before * alpha;
         sr += gr[k] * w;
         sg += gg[k] * w;
@@ -119,7 +123,7 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_bwd_kernel(Comp
         const float diff = gc - gs_[k];
         gs_[k] += alpha * diff;
         T[k] = t_before;
-        const float q = raw <= kMaxAlpha ? t_before * diff * prob : 0.0f;
+        const float q = (hit && raw <= kMaxAlpha) ? t_before * diff * prob : 0.0f;
         const float qx = q * dx;
         const float qy = q * dy;
         sq += q;
@@ -145,18 +149,16 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_bwd_kernel(Comp
       const float tq = bcast(sq, 63), tx_ = bcast(sx, 63), ty_ = bcast(sy, 63);
       const float txx = bcast(sxx, 63), txy = bcast(sxy, 63), tyy = bcast(syy, 63);
       const float tr = bcast(sr, 63), tg = bcast(sg, 63), tb = bcast(sb, 63);
-      float val;
-      switch (lane) {
-        case 0: val = -2.0f * k * (ga * tx_ + gbb * ty_); break;
-        case 1: val = -2.0f * k * (gbb * tx_ + gcc * ty_); break;
-        case 2: val = k * txx; break;
-        case 3: val = k * txy; break;
-        case 4: val = k * tyy; break;
-        case 5: val = tr; break;
-        case 6: val = tg; break;
-        case 7: val = tb; break;
-        default: val = tq; break;
-      }
+      // Lane i of `val` carries field i of the 9-float gradient row.
+      float val = tq;
+      val = write_lane(val, -2.0f * k * (ga * tx_ + gbb * ty_), 0);
+      val = write_lane(val, -2.0f * k * (gbb * tx_ + gcc * ty_), 1);
+      val = write_lane(val, k * txx, 2);
+      val = write_lane(val, k * txy, 3);
+      val = write_lane(val, k * tyy, 4);
+      val = write_lane(val, tr, 5);
+      val = write_lane(val, tg, 6);
+      val = write_lane(val, tb, 7);
       if (lane < 9) {
         const int g = __builtin_amdgcn_readlane(gid, j);
         unsafeAtomicAdd(a.grad + int64_t(g) * 9 + lane, val);
@@ -176,9 +178,12 @@ void launch(const CompositeBwdArgs& a, hipStream_t s) {
 
 using namespace gs;
 
-extern "C" GS_API int gs_composite_bwd(const void* records, const int32_t* gaussian_ids,
-                                       const int64_t* ranges, const float* grad_image,
-                                       const float* final_transmittance,
+extern "C" GS_API int gs_composite_bwd(const float* projected_mean,
+                                       const float* inverse_covariance,
+                                       const float* projected_color,
+                                       const float* projected_opacity,
+                                       const int32_t* gaussian_ids, const int64_t* ranges,
+                                       const float* grad_image, const float* final_transmittance,
                                        const int32_t* n_contributors, gs_view view,
                                        float* grad_projected, void* stream) {
   clear_error();
@@ -187,10 +192,13 @@ extern "C" GS_API int gs_composite_bwd(const void* records, const int32_t* gauss
              "Backward gradients are only supported for Gaussian rendering.");
   GS_REQUIRE(ranges && grad_image && final_transmittance && n_contributors && grad_projected,
              GS_ERR_INVALID_ARGUMENT, "null pointer argument");
-  GS_REQUIRE((reinterpret_cast<uintptr_t>(records) & 15u) == 0, GS_ERR_INVALID_ARGUMENT,
-             "records must be 16-byte aligned");
+  GS_REQUIRE((reinterpret_cast<uintptr_t>(inverse_covariance) & 15u) == 0,
+             GS_ERR_INVALID_ARGUMENT, "inverse_covariance must be 16-byte aligned");
   CompositeBwdArgs a;
-  a.records = static_cast<const GsRecord*>(records);
+  a.pmean = projected_mean;
+  a.pinv = inverse_covariance;
+  a.pcolor = projected_color;
+  a.popacity = projected_opacity;
   a.ids = gaussian_ids;
   a.ranges = ranges;
   a.grad_image = grad_image;

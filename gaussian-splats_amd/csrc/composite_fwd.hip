@@ -94,21 +94,21 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_fwd_kernel(Comp
       mask &= mask - 1;
       const Splat s = broadcast(mine, j);
       const int pos = int(base - start) + j;
+      // Branch-free: a finished pixel (or a cut alpha) blends with alpha = 0,
+      // which leaves its colour and T unchanged.
 #pragma unroll
       for (int k = 0; k < PIX; ++k) {
-        if (!live[k]) continue;
         float prob;
-        const float alpha = blend_alpha(raw_alpha<ELLIPSOID>(s, pxf[k] - s.u, pyf[k] - s.v, prob));
-        if (alpha == 0.0f) continue;
+        const float raw = raw_alpha<ELLIPSOID>(s, pxf[k] - s.u, pyf[k] - s.v, prob);
+        const float alpha = live[k] ? blend_alpha(raw) : 0.0f;
         const float w = T[k] * alpha;
         cr[k] += w * s.r;
         cg[k] += w * s.g;
         cb[k] += w * s.bl;
         T[k] = T[k] * (1.0f - alpha);
-        if (!((1.0f - T[k]) < a.threshold)) {
-          live[k] = false;
-          ncon[k] = pos + 1;
-        }
+        const bool done = live[k] && !((1.0f - T[k]) < a.threshold);
+        ncon[k] = done ? pos + 1 : ncon[k];
+        live[k] = live[k] && !done;
       }
       if (!any_live()) {
         running = false;

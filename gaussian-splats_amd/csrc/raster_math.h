@@ -127,8 +127,38 @@ __device__ __forceinline__ GsRecord load_record(const GsRecord* __restrict__ rec
   return r;
 }
 
+// Gathers the same fields from the op's projected outputs (projected_mean,
+// inverse_covariance, projected_color, projected_opacity).  `cut` is computed
+// with the expression project_fwd uses, so it is bit-identical to the record's.
+__device__ __forceinline__ GsRecord load_projected(const float* __restrict__ pmean,
+                                                   const float* __restrict__ pinv,
+                                                   const float* __restrict__ pcolor,
+                                                   const float* __restrict__ popacity, int g) {
+  GsRecord r;
+  const int64_t g3 = int64_t(g) * 3;
+  r.u = pmean[g3];
+  r.v = pmean[g3 + 1];
+  r.depth = pmean[g3 + 2];
+  const float4 inv = reinterpret_cast<const float4*>(pinv)[g];
+  r.inv00 = inv.x;
+  r.inv01 = inv.y;
+  r.inv11 = inv.w;
+  r.r = pcolor[g3];
+  r.g = pcolor[g3 + 1];
+  r.b = pcolor[g3 + 2];
+  r.opacity = popacity[g];
+  r.cut = 2.0f * logf(r.opacity * 255.0f);
+  r.pad = 0.0f;
+  return r;
+}
+
 __device__ __forceinline__ float bcast(float x, int j) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), j));
+}
+
+// Returns `v` with lane `lane` replaced by the wave-uniform value `x`.
+__device__ __forceinline__ float write_lane(float v, float x, int lane) {
+  return __lane_id() == lane ? x : v;
 }
 
 // Broadcasts lane j's splat to the whole wave (v_readlane into SGPRs, so the
@@ -148,23 +178,25 @@ __device__ __forceinline__ Splat broadcast(const LaneSplat& l, int j) {
   return s;
 }
 
-// DPP move with `old` = 0 for lanes the row mask leaves unwritten.
-template <int CTRL, int ROW_MASK>
+// DPP read of another lane's value (all rows and banks enabled; a lane whose
+// source is out of range reads 0).  Combined with an add it compiles to a single
+// v_add_f32_dpp.
+template <int CTRL>
 __device__ __forceinline__ float dpp0(float v) {
-  return __int_as_float(
-      __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
 }
 
-// Sum over the 64 lanes, valid in lane 63: quad_perm xor 1 and xor 2, row
-// half-mirror and mirror (each row of 16 then holds its row sum), then
-// row_bcast:15 and row_bcast:31 carry rows 0..2 into row 3.  Needs a full EXEC.
+// Sum over the 64 lanes, valid in lane 63 only: quad_perm xor 1 and xor 2, row
+// half-mirror and mirror (each row of 16 then holds its row sum), row_bcast:15
+// (row 3 += row 2, row 1 += row 0) and row_bcast:31 (rows 2, 3 += lane 31).
+// Other lanes end with partial sums.  Needs a full EXEC.
 __device__ __forceinline__ float wave_sum_lane63(float v) {
-  v += dpp0<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
-  v += dpp0<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
-  v += dpp0<0x141, 0xF>(v);  // row_half_mirror
-  v += dpp0<0x140, 0xF>(v);  // row_mirror
-  v += dpp0<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
-  v += dpp0<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+  v += dpp0<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp0<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp0<0x141>(v);  // row_half_mirror
+  v += dpp0<0x140>(v);  // row_mirror
+  v += dpp0<0x142>(v);  // row_bcast:15
+  v += dpp0<0x143>(v);  // row_bcast:31
   return v;
 }
 

@@ -104,7 +104,7 @@ _SIGNATURES = {
     "gs_composite": (c_int, [c_void_p, c_void_p, c_void_p, GsView, c_void_p, c_void_p, c_void_p, c_void_p]),
     "gs_composite_bwd": (
         c_int,
-        [c_void_p] * 6 + [GsView, c_void_p, c_void_p],
+        [c_void_p] * 9 + [GsView, c_void_p, c_void_p],
     ),
     "gs_project_bwd": (
         c_int,

@@ -12,7 +12,7 @@ from __future__ import annotations
 import torch
 
 from . import _native as nat
-from .project import _check_tile, pack_records
+from .project import _check_tile
 
 
 def composite_bwd(
@@ -33,32 +33,39 @@ def composite_bwd(
     atomic: bool = False,
     return_absolute: bool = False,
     *,
-    records: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
 ) -> torch.Tensor:
+    """``out`` (optional, zero-filled [N, 9] float32) receives the gradient."""
     if rendering_mode != "gaussian":
         raise AssertionError("Backward gradients are only supported for Gaussian rendering.")
     if return_absolute:
         raise NotImplementedError("absolute mean gradients are not produced by the HIP backward")
     _check_tile(tile_size)
     device = nat.require_gpu(projected_mean, gaussian_ids, ranges, grad_image)
-    if records is None:
-        records = pack_records(projected_mean, inverse_covariance, projected_color, projected_opacity)
+    projected_mean, inverse_covariance, projected_color, projected_opacity = (
+        nat.prepare(t) for t in (projected_mean, inverse_covariance, projected_color, projected_opacity)
+    )
     grad_image = nat.prepare(grad_image.float() if grad_image.dtype != torch.float32 else grad_image)
     final_transmittance = nat.prepare(final_transmittance)
     n_contributors = nat.prepare(n_contributors, torch.int32)
     ranges = nat.prepare(ranges, torch.int64)
     gaussian_ids = nat.prepare(gaussian_ids, torch.int32)
-    grad = torch.zeros((projected_mean.shape[0], 9), dtype=torch.float32, device=device)
+    n = projected_mean.shape[0]
+    if out is None:
+        out = torch.zeros((n, 9), dtype=torch.float32, device=device)
+    elif out.shape != (n, 9) or out.dtype != torch.float32 or not out.is_contiguous():
+        raise ValueError("out must be a contiguous zero-filled float32 tensor of shape [N, 9]")
     view = nat.make_view(
         1.0, 1.0, 0.0, 0.0, image_width, image_height, tile_size,
         opacity_threshold=opacity_threshold,
     )
     nat.check(
         nat.library().gs_composite_bwd(
-            nat.ptr(records), nat.ptr(gaussian_ids), nat.ptr(ranges), nat.ptr(grad_image),
-            nat.ptr(final_transmittance), nat.ptr(n_contributors), view, nat.ptr(grad),
+            nat.ptr(projected_mean), nat.ptr(inverse_covariance), nat.ptr(projected_color),
+            nat.ptr(projected_opacity), nat.ptr(gaussian_ids), nat.ptr(ranges), nat.ptr(grad_image),
+            nat.ptr(final_transmittance), nat.ptr(n_contributors), view, nat.ptr(out),
             nat.stream(device),
         ),
         "composite_bwd",
     )
-    return grad
+    return out

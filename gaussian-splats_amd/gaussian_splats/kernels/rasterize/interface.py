@@ -17,7 +17,7 @@ from . import _native as nat
 from .composite import composite
 from .composite_bwd import composite_bwd
 from .intersections import bin_gaussians, emit_tiles, sort_tiles
-from .project import _check_tile, pack_records, project_and_count
+from .project import _check_tile, project_and_count
 from .project_bwd import project_bwd
 
 if TYPE_CHECKING:  # the splat API imports this module, so only for annotations
@@ -197,12 +197,10 @@ def _backward(ctx, *grad_outputs):
         grad_image = torch.zeros(
             (ctx.image_height, ctx.image_width, 3), dtype=mean.dtype, device=mean.device
         )
-    records = pack_records(projected_mean, inverse_covariance, projected_color, projected_opacity)
     grad_projected = composite_bwd(
         projected_mean, inverse_covariance, projected_color, projected_opacity, gaussian_ids,
         ranges, grad_image, final_transmittance, n_contributors, ctx.image_width,
         ctx.image_height, ctx.tile_size, ctx.opacity_threshold, ctx.rendering_mode,
-        records=records,
     )
     gradients = project_bwd(
         mean, rotation, scale, opacity, color, camera_rotation, camera_translation,

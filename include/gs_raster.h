@@ -171,10 +171,13 @@ GS_API int gs_composite(
     int32_t* n_contributors, void* stream);
 
 /* Back-to-front compositing gradient, accumulated with atomics into
- * grad_projected[N,9] (zeroed by the caller).  Replaces composite_bwd
- * (composite_bwd.py:47-277) with the exact gradient of the forward. */
+ * grad_projected[N,9] (zeroed by the caller), from the op's projected outputs.
+ * Replaces composite_bwd (composite_bwd.py:47-277) with the exact gradient of
+ * the forward. */
 GS_API int gs_composite_bwd(
-    const void* records, const int32_t* gaussian_ids, const int64_t* ranges,
+    const float* projected_mean, const float* inverse_covariance,
+    const float* projected_color, const float* projected_opacity,
+    const int32_t* gaussian_ids, const int64_t* ranges,
     const float* grad_image, const float* final_transmittance,
     const int32_t* n_contributors, gs_view view, float* grad_projected,
     void* stream);

@@ -65,7 +65,7 @@ def test_invalid_tile_sizes(tile):
 def test_backward_rejects_ellipsoid_mode():
     lib = nat.library()
     fake = ctypes.c_void_p(16)
-    status = lib.gs_composite_bwd(fake, fake, fake, fake, fake, fake,
+    status = lib.gs_composite_bwd(*([fake] * 9),
                                   _view(rendering_mode="ellipsoid"), fake, None)
     assert status == nat.GS_ERR_UNSUPPORTED
     assert b"Gaussian rendering" in lib.gs_last_error()
@@ -84,7 +84,7 @@ def test_misaligned_buffers_rejected():
 def test_status_codes_map_to_python_exceptions():
     lib = nat.library()
     fake = ctypes.c_void_p(16)
-    status = lib.gs_composite_bwd(fake, fake, fake, fake, fake, fake, _view(rendering_mode="ellipsoid"), fake, None)
+    status = lib.gs_composite_bwd(*([fake] * 9), _view(rendering_mode="ellipsoid"), fake, None)
     with pytest.raises(NotImplementedError):
         nat.check(status, "composite_bwd")
 

@@ -16,248 +16,16 @@
 //    exactly the order the 64-bit stable sort produces, while moving
 //    4+4 bytes per intersection per pass over 2 passes instead of 8+4 bytes
 //    over 6.
+// Sorts and scans are the single-pass kernels of onesweep.h.
 #include "block_scan.h"
 #include "common.h"
+#include "onesweep.h"
 
 namespace gs {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kItems = 16;
-constexpr int kTileItems = kBlock * kItems;  // elements per workgroup
-
-// ---------------------------------------------------------------------------
-// Device-wide exclusive scan (reduce -> scan of block sums -> downsweep).
-// value(i) = in[order ? order[i] : i]; out[n] receives the total when
-// write_total is set.
-// ---------------------------------------------------------------------------
-template <typename In, typename Out>
-__global__ __launch_bounds__(kBlock) void scan_reduce_kernel(const In* __restrict__ in,
-                                                             const int32_t* __restrict__ order,
-                                                             int64_t n, Out* __restrict__ sums) {
-  __shared__ Out scratch[4];
-  const int64_t base = int64_t(blockIdx.x) * kTileItems;
-  Out s = 0;
-#pragma unroll
-  for (int i = 0; i < kItems; ++i) {
-    const int64_t idx = base + i * kBlock + threadIdx.x;
-    if (idx < n) s += Out(in[order ? order[idx] : idx]);
-  }
-  s = wave_sum(s);
-  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = s;
-  __syncthreads();
-  if (threadIdx.x == 0) sums[blockIdx.x] = scratch[0] + scratch[1] + scratch[2] + scratch[3];
-}
-
-// One workgroup scans the block sums in place, chunk by chunk.
-template <typename Out>
-__global__ __launch_bounds__(kBlock) void scan_sums_kernel(Out* __restrict__ sums, int64_t nb,
-                                                           Out* __restrict__ total_out) {
-  __shared__ Out scratch[4];
-  Out carry = 0;
-  for (int64_t chunk = 0; chunk < nb; chunk += kBlock) {
-    const int64_t idx = chunk + threadIdx.x;
-    const Out v = idx < nb ? sums[idx] : Out(0);
-    Out total;
-    const Out ex = block_exclusive_scan(v, scratch, total);
-    if (idx < nb) sums[idx] = carry + ex;
-    carry += total;
-  }
-  if (total_out && threadIdx.x == 0) *total_out = carry;
-}
-
-template <typename In, typename Out>
-__global__ __launch_bounds__(kBlock) void scan_down_kernel(const In* __restrict__ in,
-                                                           const int32_t* __restrict__ order,
-                                                           int64_t n,
-                                                           const Out* __restrict__ block_offsets,
-                                                           Out* __restrict__ out) {
-  __shared__ Out scratch[4];
-  const int64_t base = int64_t(blockIdx.x) * kTileItems;
-  Out carry = block_offsets[blockIdx.x];
-  for (int i = 0; i < kItems; ++i) {
-    const int64_t idx = base + i * kBlock + threadIdx.x;
-    const Out v = idx < n ? Out(in[order ? order[idx] : idx]) : Out(0);
-    Out total;
-    const Out ex = block_exclusive_scan(v, scratch, total);
-    if (idx < n) out[idx] = carry + ex;
-    carry += total;
-  }
-}
-
-template <typename T>
-__global__ void fill_kernel(T* p, int64_t n, T value) {
-  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = value;
-}
-
-template <typename Out>
-size_t scan_ws_bytes(int64_t n) {
-  const int64_t nb = ceil_div(n, kTileItems);
-  return align_up(size_t(nb + 1) * sizeof(Out));
-}
-
-// out[0..n) = exclusive prefix of value(i); out[n] = total when write_total.
-template <typename In, typename Out>
-int device_exclusive_scan(const In* in, const int32_t* order, int64_t n, Out* out,
-                          bool write_total, void* ws, hipStream_t s) {
-  if (n == 0) {
-    if (write_total) fill_kernel<Out><<<1, 64, 0, s>>>(out, 1, Out(0));
-    return check_launch("scan(empty)");
-  }
-  const int64_t nb = ceil_div(n, kTileItems);
-  Out* sums = static_cast<Out*>(ws);
-  scan_reduce_kernel<In, Out><<<unsigned(nb), kBlock, 0, s>>>(in, order, n, sums);
-  scan_sums_kernel<Out><<<1, kBlock, 0, s>>>(sums, nb, write_total ? out + n : nullptr);
-  scan_down_kernel<In, Out><<<unsigned(nb), kBlock, 0, s>>>(in, order, n, sums, out);
-  return check_launch("scan");
-}
-
-// ---------------------------------------------------------------------------
-// Stable LSD radix sort of (key, u32 value) pairs.
-//
-// Per pass: histogram (per-wave LDS counters) -> digit-major exclusive scan of
-// the [digit][workgroup] counts -> scatter.  The scatter ranks each element
-// within its wave by matching digits with ballots (stable: lane order inside
-// an iteration, iterations in input order), combines the four wave segments of
-// the workgroup through LDS, reorders the 4096-element tile in LDS by digit and
-// writes it out with consecutive lanes on consecutive addresses.
-// ---------------------------------------------------------------------------
-template <typename K, int BITS>
-__global__ __launch_bounds__(kBlock) void radix_hist_kernel(const K* __restrict__ keys, int64_t n,
-                                                            int shift, uint32_t* __restrict__ hist,
-                                                            int nblocks) {
-  constexpr int D = 1 << BITS;
-  __shared__ uint32_t h[4][D];
-  const int wid = threadIdx.x >> 6;
-  for (int d = threadIdx.x; d < 4 * D; d += kBlock) (&h[0][0])[d] = 0;
-  __syncthreads();
-  const int64_t base = int64_t(blockIdx.x) * kTileItems;
-#pragma unroll
-  for (int i = 0; i < kItems; ++i) {
-    const int64_t idx = base + i * kBlock + threadIdx.x;
-    if (idx < n) {
-      const uint32_t d = uint32_t(keys[idx] >> shift) & (D - 1);
-      atomicAdd(&h[wid][d], 1u);
-    }
-  }
-  __syncthreads();
-  for (int d = threadIdx.x; d < D; d += kBlock)
-    hist[int64_t(d) * nblocks + blockIdx.x] = h[0][d] + h[1][d] + h[2][d] + h[3][d];
-}
-
-template <typename K, int BITS>
-__global__ __launch_bounds__(kBlock) void radix_scatter_kernel(
-    const K* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, K* __restrict__ keys_out,
-    uint32_t* __restrict__ vals_out, int64_t n, int shift, const uint32_t* __restrict__ offsets,
-    int nblocks) {
-  constexpr int D = 1 << BITS;
-  constexpr int kSeg = kTileItems / 4;  // contiguous elements per wave
-  __shared__ uint32_t cnt[4][D];
-  __shared__ uint32_t dstart[D];
-  __shared__ uint32_t gofs[D];
-  __shared__ uint32_t scratch[4];
-  __shared__ K skeys[kTileItems];
-  __shared__ uint32_t svals[kTileItems];
-
-  const int lane = threadIdx.x & 63;
-  const int wid = threadIdx.x >> 6;
-  for (int d = threadIdx.x; d < 4 * D; d += kBlock) (&cnt[0][0])[d] = 0;
-  __syncthreads();
-
-  const int64_t base = int64_t(blockIdx.x) * kTileItems;
-  const int64_t seg = base + int64_t(wid) * kSeg;
-  const uint64_t below = lanemask_lt();
-  volatile uint32_t* wcnt = cnt[wid];
-
-  K key[kItems];
-  uint32_t val[kItems];
-  uint32_t rank[kItems];
-#pragma unroll
-  for (int i = 0; i < kItems; ++i) {
-    const int64_t idx = seg + i * 64 + lane;
-    const bool valid = idx < n;
-    key[i] = valid ? keys_in[idx] : K(0);
-    val[i] = valid ? (vals_in ? vals_in[idx] : uint32_t(idx)) : 0u;
-    const uint32_t d = uint32_t(key[i] >> shift) & (D - 1);
-    uint64_t peers = __ballot(valid);
-#pragma unroll
-    for (int b = 0; b < BITS; ++b) {
-      const uint64_t ones = __ballot((d >> b) & 1u);
-      peers &= ((d >> b) & 1u) ? ones : ~ones;
-    }
-    const uint32_t before = uint32_t(__popcll(peers & below));
-    uint32_t c = 0;
-    if (valid) c = wcnt[d];
-    if (valid && before == 0) wcnt[d] = c + uint32_t(__popcll(peers));
-    rank[i] = c + before;
-  }
-  __syncthreads();
-
-  // Per digit: exclusive prefix over the four wave segments, block-local
-  // digit start, and the global offset of this workgroup's digit bucket.
-  uint32_t tot = 0;
-  if (threadIdx.x < D) {
-    const uint32_t c0 = cnt[0][threadIdx.x], c1 = cnt[1][threadIdx.x];
-    const uint32_t c2 = cnt[2][threadIdx.x], c3 = cnt[3][threadIdx.x];
-    cnt[0][threadIdx.x] = 0;
-    cnt[1][threadIdx.x] = c0;
-    cnt[2][threadIdx.x] = c0 + c1;
-    cnt[3][threadIdx.x] = c0 + c1 + c2;
-    tot = c0 + c1 + c2 + c3;
-    gofs[threadIdx.x] = offsets[int64_t(threadIdx.x) * nblocks + blockIdx.x];
-  }
-  uint32_t all;
-  const uint32_t start = block_exclusive_scan(tot, scratch, all);
-  if (threadIdx.x < D) dstart[threadIdx.x] = start;
-  __syncthreads();
-
-#pragma unroll
-  for (int i = 0; i < kItems; ++i) {
-    const int64_t idx = seg + i * 64 + lane;
-    if (idx < n) {
-      const uint32_t d = uint32_t(key[i] >> shift) & (D - 1);
-      const uint32_t pos = dstart[d] + cnt[wid][d] + rank[i];
-      skeys[pos] = key[i];
-      svals[pos] = val[i];
-    }
-  }
-  __syncthreads();
-
-  const int nvalid = int(min(int64_t(kTileItems), n - base));
-  for (int j = threadIdx.x; j < nvalid; j += kBlock) {
-    const K k = skeys[j];
-    const uint32_t d = uint32_t(k >> shift) & (D - 1);
-    const int64_t o = int64_t(gofs[d]) + (j - int(dstart[d]));
-    keys_out[o] = k;
-    vals_out[o] = svals[j];
-  }
-}
-
-template <typename K, int BITS>
-void launch_pass(const K* kin, const uint32_t* vin, K* kout, uint32_t* vout, int64_t n, int shift,
-                 uint32_t* hist, void* scan_ws, int nblocks, hipStream_t s) {
-  radix_hist_kernel<K, BITS><<<unsigned(nblocks), kBlock, 0, s>>>(kin, n, shift, hist, nblocks);
-  device_exclusive_scan<uint32_t, uint32_t>(hist, nullptr, int64_t(nblocks) << BITS, hist, false,
-                                            scan_ws, s);
-  radix_scatter_kernel<K, BITS><<<unsigned(nblocks), kBlock, 0, s>>>(kin, vin, kout, vout, n, shift,
-                                                                     hist, nblocks);
-}
-
-template <typename K>
-void dispatch_pass(int bits, const K* kin, const uint32_t* vin, K* kout, uint32_t* vout, int64_t n,
-                   int shift, uint32_t* hist, void* scan_ws, int nblocks, hipStream_t s) {
-  switch (bits) {
-    case 1: launch_pass<K, 1>(kin, vin, kout, vout, n, shift, hist, scan_ws, nblocks, s); break;
-    case 2: launch_pass<K, 2>(kin, vin, kout, vout, n, shift, hist, scan_ws, nblocks, s); break;
-    case 3: launch_pass<K, 3>(kin, vin, kout, vout, n, shift, hist, scan_ws, nblocks, s); break;
-    case 4: launch_pass<K, 4>(kin, vin, kout, vout, n, shift, hist, scan_ws, nblocks, s); break;
-    case 5: launch_pass<K, 5>(kin, vin, kout, vout, n, shift, hist, scan_ws, nblocks, s); break;
-    case 6: launch_pass<K, 6>(kin, vin, kout, vout, n, shift, hist, scan_ws, nblocks, s); break;
-    case 7: launch_pass<K, 7>(kin, vin, kout, vout, n, shift, hist, scan_ws, nblocks, s); break;
-    default: launch_pass<K, 8>(kin, vin, kout, vout, n, shift, hist, scan_ws, nblocks, s); break;
-  }
-}
+using sweep::kTile;
 
 int bits_for(int64_t count) {  // ceil(log2(count)), 0 for count <= 1
   int b = 0;
@@ -265,58 +33,136 @@ int bits_for(int64_t count) {  // ceil(log2(count)), 0 for count <= 1
   return b;
 }
 
-// Workspace layout of one sort: [keys_alt | vals_a | vals_b | hist | scan].
-template <typename K>
-size_t sort_ws_bytes(int64_t n) {
-  const int64_t nblocks = ceil_div(n, kTileItems);
-  return align_up(size_t(n) * sizeof(K)) + 2 * align_up(size_t(n) * 4) +
-         align_up(size_t(nblocks) * 256 * 4) + scan_ws_bytes<uint32_t>(nblocks * 256);
+// Scratch shared by the sort and the scan: ping-pong buffers, then one zeroed
+// region (look-back status words of every sort pass and of the scan, then the
+// 32-bit histograms, tickets and error flags).
+struct Scratch {
+  void* keys_alt = nullptr;
+  uint32_t* vbuf[2] = {nullptr, nullptr};
+  uint64_t* sort_status = nullptr;
+  uint64_t* scan_status = nullptr;
+  uint64_t* zero_begin = nullptr;
+  int64_t zero_words = 0;  // 64-bit words of status
+  uint32_t* small = nullptr;  // hist[kMaxPasses*256], tickets[kMaxPasses], err, scan ticket, scan err
+  int small_words = 0;
+  size_t bytes = 0;
+
+  uint32_t* hist() const { return small; }
+  uint32_t* tickets() const { return small + sweep::kMaxPasses * 256; }
+  uint32_t* err() const { return tickets() + sweep::kMaxPasses; }
+  uint32_t* scan_ticket() const { return err() + 1; }
+  uint32_t* scan_err() const { return err() + 2; }
+};
+
+int64_t sort_status_words(int64_t n, const sweep::Plan& p) {
+  const int64_t nblocks = ceil_div(n, kTile);
+  int64_t words = 0;
+  for (int i = 0; i < p.passes; ++i) words += nblocks << p.bits[i];
+  return words;
 }
 
-// Sorts (keys, vals) on bits [0, end_bit); vals == nullptr means vals[i] = i.
-// The sorted values land in vals_final; *keys_final points at the sorted keys
-// (either `keys` or the workspace copy).  keys and vals are clobbered.
+// Lays out scratch for a sort of n keys of key_bytes over end_bit bits
+// (end_bit < 0: no sort) and a scan of scan_n elements (0: no scan).
+Scratch carve(void* ws, int64_t n, int key_bytes, int end_bit, int64_t scan_n) {
+  Scratch s;
+  char* p = static_cast<char*>(ws);
+  size_t off = 0;
+  int64_t sort_words = 0;
+  if (end_bit >= 0 && n > 0) {
+    s.keys_alt = p ? p + off : nullptr;
+    off += align_up(size_t(n) * key_bytes);
+    for (int i = 0; i < 2; ++i) {
+      s.vbuf[i] = p ? reinterpret_cast<uint32_t*>(p + off) : nullptr;
+      off += align_up(size_t(n) * 4);
+    }
+    sort_words = sort_status_words(n, sweep::make_plan(end_bit));
+  }
+  const int64_t scan_words = scan_n > 0 ? ceil_div(scan_n, kTile) : 0;
+  s.zero_begin = p ? reinterpret_cast<uint64_t*>(p + off) : nullptr;
+  s.sort_status = s.zero_begin;
+  s.scan_status = p ? s.zero_begin + sort_words : nullptr;
+  s.zero_words = sort_words + scan_words;
+  off += align_up(size_t(s.zero_words) * 8);
+  s.small_words = sweep::kMaxPasses * 256 + sweep::kMaxPasses + 3;
+  s.small = p ? reinterpret_cast<uint32_t*>(p + off) : nullptr;
+  off += align_up(size_t(s.small_words) * 4);
+  s.bytes = off;
+  return s;
+}
+
+void clear(const Scratch& s, hipStream_t stream) {
+  const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(1024, ceil_div(s.zero_words, kBlock)));
+  sweep::clear_kernel<<<unsigned(blocks), kBlock, 0, stream>>>(s.zero_begin, s.zero_words, s.small,
+                                                               s.small_words);
+}
+
+template <typename K, int BITS>
+void launch_scatter(const K* kin, const uint32_t* vin, K* kout, uint32_t* vout, int64_t n,
+                    int shift, const uint32_t* hist, uint64_t* status, uint32_t* ticket,
+                    uint32_t* err, hipStream_t s) {
+  const unsigned nblocks = unsigned(ceil_div(n, kTile));
+  sweep::scatter_kernel<K, BITS><<<nblocks, sweep::kBlock, 0, s>>>(kin, vin, kout, vout, n, shift,
+                                                                   hist, status, ticket, err);
+}
+
+template <typename K>
+void dispatch_scatter(int bits, const K* kin, const uint32_t* vin, K* kout, uint32_t* vout,
+                      int64_t n, int shift, const uint32_t* hist, uint64_t* status,
+                      uint32_t* ticket, uint32_t* err, hipStream_t s) {
+  switch (bits) {
+    case 1: launch_scatter<K, 1>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, s); break;
+    case 2: launch_scatter<K, 2>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, s); break;
+    case 3: launch_scatter<K, 3>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, s); break;
+    case 4: launch_scatter<K, 4>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, s); break;
+    case 5: launch_scatter<K, 5>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, s); break;
+    case 6: launch_scatter<K, 6>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, s); break;
+    case 7: launch_scatter<K, 7>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, s); break;
+    default: launch_scatter<K, 8>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, s); break;
+  }
+}
+
+// Sorts (keys, vals) on bits [0, end_bit) after `clear` has zeroed the scratch.
+// vals == nullptr means vals[i] = i.  Sorted values land in vals_final;
+// *keys_final points at the sorted keys (keys or the scratch copy).
 template <typename K>
 int radix_sort(K* keys, const uint32_t* vals, int64_t n, int end_bit, uint32_t* vals_final,
-               K** keys_final, void* ws, size_t ws_bytes, hipStream_t s) {
-  GS_REQUIRE(ws_bytes >= sort_ws_bytes<K>(n), GS_ERR_WORKSPACE,
-             "sort workspace too small (%zu < %zu)", ws_bytes, sort_ws_bytes<K>(n));
-  GS_REQUIRE(n < (int64_t(1) << 32) - kTileItems, GS_ERR_OVERFLOW,
-             "too many elements to sort (%lld)", (long long)n);
-  char* p = static_cast<char*>(ws);
-  K* keys_alt = reinterpret_cast<K*>(p);
-  p += align_up(size_t(n) * sizeof(K));
-  uint32_t* vbuf[2];
-  vbuf[0] = reinterpret_cast<uint32_t*>(p);
-  p += align_up(size_t(n) * 4);
-  vbuf[1] = reinterpret_cast<uint32_t*>(p);
-  p += align_up(size_t(n) * 4);
-  const int nblocks = int(ceil_div(n, kTileItems));
-  uint32_t* hist = reinterpret_cast<uint32_t*>(p);
-  p += align_up(size_t(nblocks) * 256 * 4);
-  void* scan_ws = p;
-
-  K* kbuf[2] = {keys_alt, keys};
-  if (n == 0) {
-    *keys_final = keys;
-    return GS_OK;
-  }
-  const int passes = end_bit <= 0 ? 1 : int(ceil_div(end_bit, 8));
-  int shift = 0;
+               K** keys_final, const Scratch& ws, hipStream_t s) {
+  GS_REQUIRE(n < (int64_t(1) << 32) - kTile, GS_ERR_OVERFLOW, "too many elements to sort (%lld)",
+             (long long)n);
+  *keys_final = keys;
+  if (n == 0) return GS_OK;
+  const sweep::Plan plan = sweep::make_plan(end_bit);
+  const int hist_blocks = int(std::min<int64_t>(512, ceil_div(n, kBlock * 16)));
+  sweep::hist_kernel<K><<<unsigned(hist_blocks), kBlock, 0, s>>>(keys, n, plan, ws.hist());
+  K* kbuf[2] = {static_cast<K*>(ws.keys_alt), keys};
   const K* kin = keys;
   const uint32_t* vin = vals;
-  for (int pass = 0; pass < passes; ++pass) {
-    const int remaining = end_bit - shift;
-    const int bits = end_bit <= 0 ? 1 : int(ceil_div(remaining, passes - pass));
+  uint64_t* status = ws.sort_status;
+  const int64_t nblocks = ceil_div(n, kTile);
+  for (int pass = 0; pass < plan.passes; ++pass) {
     K* kout = kbuf[pass & 1];
-    uint32_t* vout = (pass == passes - 1) ? vals_final : vbuf[pass & 1];
-    dispatch_pass<K>(bits, kin, vin, kout, vout, n, shift, hist, scan_ws, nblocks, s);
+    uint32_t* vout = (pass == plan.passes - 1) ? vals_final : ws.vbuf[pass & 1];
+    dispatch_scatter<K>(plan.bits[pass], kin, vin, kout, vout, n, plan.shift[pass],
+                        ws.hist() + pass * 256, status, ws.tickets() + pass, ws.err(), s);
+    status += nblocks << plan.bits[pass];
     kin = kout;
     vin = vout;
-    shift += bits;
   }
   *keys_final = const_cast<K*>(kin);
   return check_launch("radix_sort");
+}
+
+template <typename In, typename Out>
+void launch_scan(const In* in, const int32_t* order, int64_t n, Out* out, bool write_total,
+                 const Scratch& ws, hipStream_t s) {
+  sweep::scan_kernel<In, Out><<<unsigned(ceil_div(n, kTile)), sweep::kBlock, 0, s>>>(
+      in, order, n, out, write_total, ws.scan_status, ws.scan_ticket(), ws.scan_err());
+}
+
+template <typename T>
+__global__ void fill_kernel(T* p, int64_t n, T value) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = value;
 }
 
 // ---------------------------------------------------------------------------
@@ -470,17 +316,25 @@ using namespace gs;
 
 extern "C" {
 
-GS_API size_t gs_scan_workspace_bytes(int64_t n) { return scan_ws_bytes<int64_t>(n < 0 ? 0 : n); }
+GS_API size_t gs_scan_workspace_bytes(int64_t n) {
+  return carve(nullptr, 0, 4, -1, n < 0 ? 0 : n).bytes;
+}
 
 GS_API int gs_scan_counts(const int32_t* counts, int64_t n, int64_t* offsets, void* workspace,
                           size_t workspace_bytes, void* stream) {
   clear_error();
   GS_REQUIRE(n >= 0 && offsets && (n == 0 || counts), GS_ERR_INVALID_ARGUMENT,
              "invalid scan arguments");
-  GS_REQUIRE(workspace_bytes >= scan_ws_bytes<int64_t>(n) && (n == 0 || workspace),
-             GS_ERR_WORKSPACE, "scan workspace too small");
-  return device_exclusive_scan<int32_t, int64_t>(counts, nullptr, n, offsets, true, workspace,
-                                                 as_stream(stream));
+  hipStream_t s = as_stream(stream);
+  if (n == 0) {
+    fill_kernel<int64_t><<<1, 64, 0, s>>>(offsets, 1, 0);
+    return check_launch("scan_counts");
+  }
+  const Scratch ws = carve(workspace, 0, 4, -1, n);
+  GS_REQUIRE(workspace && workspace_bytes >= ws.bytes, GS_ERR_WORKSPACE, "scan workspace too small");
+  clear(ws, s);
+  launch_scan<int32_t, int64_t>(counts, nullptr, n, offsets, true, ws, s);
+  return check_launch("scan_counts");
 }
 
 GS_API int gs_emit_intersections(const int32_t* bounds, const float* depths, int64_t depth_stride,
@@ -499,9 +353,9 @@ GS_API int gs_emit_intersections(const int32_t* bounds, const float* depths, int
 }
 
 GS_API size_t gs_sort_workspace_bytes(int64_t total, int32_t num_tiles) {
-  (void)num_tiles;
   if (total < 0) total = 0;
-  return sort_ws_bytes<uint64_t>(total);
+  // Enough for either key format: 64-bit reference keys over 32 + tile bits.
+  return carve(nullptr, total, 8, 32 + bits_for(std::max(1, num_tiles)), 0).bytes;
 }
 
 GS_API int gs_sort_intersections(int64_t* keys, int32_t* gaussian_ids, int64_t total,
@@ -514,10 +368,14 @@ GS_API int gs_sort_intersections(int64_t* keys, int32_t* gaussian_ids, int64_t t
   uint64_t* sorted_keys = reinterpret_cast<uint64_t*>(keys);
   if (total > 0) {
     GS_REQUIRE(keys && gaussian_ids && sorted_ids, GS_ERR_INVALID_ARGUMENT, "null pointer");
+    const int end_bit = 32 + bits_for(num_tiles);
+    const Scratch ws = carve(workspace, total, 8, end_bit, 0);
+    GS_REQUIRE(workspace && workspace_bytes >= ws.bytes, GS_ERR_WORKSPACE,
+               "sort workspace too small (%zu < %zu)", workspace_bytes, ws.bytes);
+    clear(ws, s);
     GS_TRY(radix_sort<uint64_t>(reinterpret_cast<uint64_t*>(keys),
-                                reinterpret_cast<const uint32_t*>(gaussian_ids), total,
-                                32 + bits_for(num_tiles), reinterpret_cast<uint32_t*>(sorted_ids),
-                                &sorted_keys, workspace, workspace_bytes, s));
+                                reinterpret_cast<const uint32_t*>(gaussian_ids), total, end_bit,
+                                reinterpret_cast<uint32_t*>(sorted_ids), &sorted_keys, ws, s));
   }
   ranges_kernel<uint64_t, 32><<<unsigned(ceil_div(num_tiles, 256)), 256, 0, s>>>(
       sorted_keys, total, num_tiles, ranges);
@@ -526,7 +384,7 @@ GS_API int gs_sort_intersections(int64_t* keys, int32_t* gaussian_ids, int64_t t
 
 GS_API size_t gs_bin_workspace_bytes(int64_t n) {
   if (n < 0) n = 0;
-  return sort_ws_bytes<uint32_t>(n) + scan_ws_bytes<int64_t>(n);
+  return carve(nullptr, n, 4, 32, n).bytes;
 }
 
 GS_API int gs_bin_gaussians(uint32_t* depth_keys, const int32_t* counts, int64_t n,
@@ -534,20 +392,22 @@ GS_API int gs_bin_gaussians(uint32_t* depth_keys, const int32_t* counts, int64_t
                             size_t workspace_bytes, void* stream) {
   clear_error();
   GS_REQUIRE(n >= 0 && offsets, GS_ERR_INVALID_ARGUMENT, "invalid binning arguments");
-  GS_REQUIRE(workspace_bytes >= gs_bin_workspace_bytes(n), GS_ERR_WORKSPACE,
-             "binning workspace too small");
   hipStream_t s = as_stream(stream);
-  if (n == 0) return device_exclusive_scan<int32_t, int64_t>(counts, nullptr, 0, offsets, true,
-                                                             workspace, s);
+  if (n == 0) {
+    fill_kernel<int64_t><<<1, 64, 0, s>>>(offsets, 1, 0);
+    return check_launch("bin_gaussians");
+  }
   GS_REQUIRE(depth_keys && counts && order, GS_ERR_INVALID_ARGUMENT, "null pointer");
+  const Scratch ws = carve(workspace, n, 4, 32, n);
+  GS_REQUIRE(workspace && workspace_bytes >= ws.bytes, GS_ERR_WORKSPACE,
+             "binning workspace too small");
+  clear(ws, s);
   // depth_keys is used as a ping-pong buffer by the sort and is consumed.
-  const size_t sort_bytes = sort_ws_bytes<uint32_t>(n);
-  char* ws = static_cast<char*>(workspace);
   uint32_t* sorted_keys = nullptr;
   GS_TRY(radix_sort<uint32_t>(depth_keys, nullptr, n, 32, reinterpret_cast<uint32_t*>(order),
-                              &sorted_keys, ws, sort_bytes, s));
-  return device_exclusive_scan<int32_t, int64_t>(counts, order, n, offsets, true,
-                                                 ws + sort_bytes, s);
+                              &sorted_keys, ws, s));
+  launch_scan<int32_t, int64_t>(counts, order, n, offsets, true, ws, s);
+  return check_launch("bin_gaussians");
 }
 
 GS_API int gs_emit_tiles(const int32_t* bounds, const int32_t* order, const int64_t* offsets,
@@ -575,11 +435,14 @@ GS_API int gs_sort_tiles(uint32_t* tile_keys, int32_t* gaussian_ids, int64_t tot
   uint32_t* sorted_keys = tile_keys;
   if (total > 0) {
     GS_REQUIRE(tile_keys && gaussian_ids && sorted_ids, GS_ERR_INVALID_ARGUMENT, "null pointer");
-    GS_REQUIRE(workspace_bytes >= sort_ws_bytes<uint32_t>(total), GS_ERR_WORKSPACE,
+    const int end_bit = bits_for(num_tiles);
+    const Scratch ws = carve(workspace, total, 4, end_bit, 0);
+    GS_REQUIRE(workspace && workspace_bytes >= ws.bytes, GS_ERR_WORKSPACE,
                "sort workspace too small");
+    clear(ws, s);
     GS_TRY(radix_sort<uint32_t>(tile_keys, reinterpret_cast<const uint32_t*>(gaussian_ids), total,
-                                bits_for(num_tiles), reinterpret_cast<uint32_t*>(sorted_ids),
-                                &sorted_keys, workspace, workspace_bytes, s));
+                                end_bit, reinterpret_cast<uint32_t*>(sorted_ids), &sorted_keys,
+                                ws, s));
   }
   ranges_kernel<uint32_t, 0><<<unsigned(ceil_div(num_tiles, 256)), 256, 0, s>>>(
       sorted_keys, total, num_tiles, ranges);

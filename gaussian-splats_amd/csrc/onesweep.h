@@ -1,0 +1,316 @@
+// Single-pass building blocks: a stable LSD radix sort whose passes each read
+// and write the data once (digit offsets by decoupled look-back), and a
+// single-kernel exclusive scan with the same look-back.
+//
+// Look-back protocol.  Workgroups take a ticket from an atomic counter, so a
+// workgroup's predecessors already run or have finished.  Each publishes, per
+// digit (or once, for the scan), a 64-bit status word: bits 63..62 are the flag
+// (0 not ready, 1 aggregate = its own count, 2 prefix = inclusive sum over
+// workgroups 0..b) and bits 61..0 the value.  A workgroup publishes its
+// aggregate first, then walks back summing aggregates until it meets a prefix,
+// then publishes its own prefix.  Every wait ends because predecessors never
+// wait on successors; a spin limit turns a broken invariant into an error flag
+// instead of a hang.
+#pragma once
+
+#include "block_scan.h"
+#include "common.h"
+
+namespace gs {
+namespace sweep {
+
+constexpr int kBlock = 256;
+constexpr int kItems = 16;  // per thread: 4096 keys per tile keeps the look-back chain short
+constexpr int kTile = kBlock * kItems;  // elements per workgroup
+constexpr int kMaxPasses = 8;
+constexpr uint64_t kFlagAggregate = 1ull << 62;
+constexpr uint64_t kFlagPrefix = 2ull << 62;
+constexpr uint64_t kValueMask = (1ull << 62) - 1;
+constexpr int kSpinLimit = 1 << 20;
+
+struct Plan {
+  int passes;
+  int shift[kMaxPasses];
+  int bits[kMaxPasses];
+};
+
+// Splits [0, end_bit) into ceil(end_bit / 8) passes of near-equal width.
+inline Plan make_plan(int end_bit) {
+  Plan p{};
+  const int total = end_bit <= 0 ? 1 : end_bit;
+  p.passes = (total + 7) / 8;
+  int shift = 0;
+  for (int i = 0; i < p.passes; ++i) {
+    const int left = p.passes - i;
+    const int bits = (total - shift + left - 1) / left;
+    p.shift[i] = shift;
+    p.bits[i] = bits;
+    shift += bits;
+  }
+  return p;
+}
+
+__device__ __forceinline__ void store_status(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint64_t load_status(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Sum of the values of workgroups [0, b) in column `col` of a [*, stride]
+// status array, walking back until an inclusive prefix is found.
+__device__ inline uint64_t look_back(const uint64_t* status, int64_t stride, int b, int col,
+                                     uint32_t* err) {
+  uint64_t excl = 0;
+  for (int k = b - 1; k >= 0; --k) {
+    const uint64_t* p = status + int64_t(k) * stride + col;
+    uint64_t v = load_status(p);
+    int spins = 0;
+    while ((v >> 62) == 0) {
+      if (++spins > kSpinLimit) {
+        atomicOr(err, 1u);
+        return excl;
+      }
+      __builtin_amdgcn_s_sleep(2);
+      v = load_status(p);
+    }
+    excl += v & kValueMask;
+    if ((v >> 62) == 2) break;
+  }
+  return excl;
+}
+
+// Zeroes `words` 64-bit words and `small` 32-bit words (tickets, histograms).
+__global__ __launch_bounds__(kBlock) inline void clear_kernel(uint64_t* big, int64_t words,
+                                                              uint32_t* small, int small_words) {
+  const int64_t stride = int64_t(gridDim.x) * kBlock;
+  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < words; i += stride) big[i] = 0;
+  if (blockIdx.x == 0)
+    for (int i = threadIdx.x; i < small_words; i += kBlock) small[i] = 0;
+}
+
+// Digit histograms of every pass in one read of the keys.
+template <typename K>
+__global__ __launch_bounds__(kBlock) void hist_kernel(const K* __restrict__ keys, int64_t n,
+                                                      Plan plan, uint32_t* __restrict__ hist) {
+  __shared__ uint32_t h[kMaxPasses * 256];
+  for (int i = threadIdx.x; i < plan.passes * 256; i += kBlock) h[i] = 0;
+  __syncthreads();
+  const int64_t stride = int64_t(gridDim.x) * kBlock;
+  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
+    const K k = keys[i];
+    for (int p = 0; p < plan.passes; ++p) {
+      const uint32_t d = uint32_t(k >> plan.shift[p]) & ((1u << plan.bits[p]) - 1u);
+      atomicAdd(&h[p * 256 + d], 1u);
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < plan.passes * 256; i += kBlock)
+    if (h[i]) atomicAdd(&hist[i], h[i]);
+}
+
+// Stable rank of each of a wave's 64 items among the items of the same digit:
+// `peers` = lanes whose digit matches (one ballot per digit bit; a lane keeps
+// the ballot where its own bit is set and its complement where it is clear),
+// rank in the wave = peers below this lane (mbcnt), and the running count of
+// the digit in this wave's segment lives in LDS.  All peers write the same new
+// count, so no leader election is needed; a wave's LDS accesses execute in
+// program order, so item i+1 sees item i's counts.
+template <int BITS, bool FULL>
+__device__ __forceinline__ void rank_items(const uint32_t* digits, int n_valid_from_seg,
+                                           uint32_t* wcnt, uint32_t* rank) {
+  const int lane = __lane_id();
+#pragma unroll
+  for (int i = 0; i < kItems; ++i) {
+    const uint32_t d = digits[i];
+    bool valid = true;
+    uint32_t plo = ~0u, phi = ~0u;
+    if (!FULL) {
+      valid = i * 64 + lane < n_valid_from_seg;
+      const uint64_t vm = __ballot(valid);
+      plo = uint32_t(vm);
+      phi = uint32_t(vm >> 32);
+    }
+    uint32_t m[BITS];
+    uint64_t ones[BITS];
+#pragma unroll
+    for (int bit = 0; bit < BITS; ++bit) {
+      m[bit] = uint32_t(int32_t(d << (31 - bit)) >> 31);  // v_bfe_i32: 0 or all ones
+      ones[bit] = __ballot(m[bit] != 0u);
+    }
+#pragma unroll
+    for (int bit = 0; bit < BITS; ++bit) {
+      plo &= ~(uint32_t(ones[bit]) ^ m[bit]);
+      phi &= ~(uint32_t(ones[bit] >> 32) ^ m[bit]);
+    }
+    const uint32_t before = __builtin_amdgcn_mbcnt_hi(phi, __builtin_amdgcn_mbcnt_lo(plo, 0u));
+    const uint32_t total = uint32_t(__popc(plo) + __popc(phi));
+    uint32_t c = 0;
+    if (FULL || valid) {
+      c = wcnt[d];
+      wcnt[d] = c + total;
+    }
+    rank[i] = c + before;
+  }
+}
+
+// One stable LSD pass over BITS bits at `shift`: ticket -> load 16 elements per
+// thread -> rank within each wave -> per-digit workgroup counts -> look-back for
+// the global offsets -> reorder the tile in LDS by digit -> coalesced stores.
+// vals_in == nullptr means vals[i] = i.
+template <typename K, int BITS>
+__global__ __launch_bounds__(kBlock) void scatter_kernel(
+    const K* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, K* __restrict__ keys_out,
+    uint32_t* __restrict__ vals_out, int64_t n, int shift, const uint32_t* __restrict__ hist,
+    uint64_t* __restrict__ status, uint32_t* __restrict__ ticket, uint32_t* __restrict__ err) {
+  constexpr int D = 1 << BITS;
+  constexpr int kSeg = kTile / 4;  // contiguous elements per wave
+  __shared__ uint32_t cnt[4][D];
+  __shared__ uint32_t dstart[D];
+  __shared__ uint32_t gofs[D];
+  __shared__ uint32_t scratch[4];
+  __shared__ int s_block;
+  __shared__ K skeys[kTile];
+  __shared__ uint32_t svals[kTile];
+
+  const int lane = threadIdx.x & 63;
+  const int wid = threadIdx.x >> 6;
+  if (threadIdx.x == 0) s_block = int(atomicAdd(ticket, 1u));
+  for (int d = threadIdx.x; d < 4 * D; d += kBlock) (&cnt[0][0])[d] = 0;
+  __syncthreads();
+  const int b = s_block;
+  const int64_t base = int64_t(b) * kTile;
+  const int nvalid = int(min(int64_t(kTile), n - base));
+  const bool full = nvalid == kTile;
+  const int seg_valid = nvalid - wid * kSeg;  // valid elements from this wave's segment start
+  const K* kin = keys_in + base + wid * kSeg;
+
+  K key[kItems];
+  uint32_t val[kItems];
+  uint32_t dig[kItems];
+  if (full) {
+#pragma unroll
+    for (int i = 0; i < kItems; ++i) key[i] = kin[i * 64 + lane];
+    if (vals_in) {
+      const uint32_t* vin = vals_in + base + wid * kSeg;
+#pragma unroll
+      for (int i = 0; i < kItems; ++i) val[i] = vin[i * 64 + lane];
+    } else {
+#pragma unroll
+      for (int i = 0; i < kItems; ++i) val[i] = uint32_t(base) + uint32_t(wid * kSeg + i * 64 + lane);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kItems; ++i) {
+      const int o = i * 64 + lane;
+      const bool valid = o < seg_valid;
+      key[i] = valid ? kin[o] : K(0);
+      val[i] = valid ? (vals_in ? vals_in[base + wid * kSeg + o] : uint32_t(base + wid * kSeg + o))
+                     : 0u;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kItems; ++i) dig[i] = uint32_t(key[i] >> shift) & (D - 1);
+
+  uint32_t rank[kItems];
+  if (full)
+    rank_items<BITS, true>(dig, seg_valid, cnt[wid], rank);
+  else
+    rank_items<BITS, false>(dig, seg_valid, cnt[wid], rank);
+  __syncthreads();
+
+  uint32_t tot = 0;
+  if (threadIdx.x < D) {
+    const uint32_t c0 = cnt[0][threadIdx.x], c1 = cnt[1][threadIdx.x];
+    const uint32_t c2 = cnt[2][threadIdx.x], c3 = cnt[3][threadIdx.x];
+    cnt[0][threadIdx.x] = 0;
+    cnt[1][threadIdx.x] = c0;
+    cnt[2][threadIdx.x] = c0 + c1;
+    cnt[3][threadIdx.x] = c0 + c1 + c2;
+    tot = c0 + c1 + c2 + c3;
+  }
+  uint32_t all;
+  const uint32_t local_start = block_exclusive_scan(tot, scratch, all);
+  const uint32_t hv = threadIdx.x < D ? hist[threadIdx.x] : 0u;
+  const uint32_t digit_base = block_exclusive_scan(hv, scratch, all);
+  if (threadIdx.x < D) {
+    dstart[threadIdx.x] = local_start;
+    uint64_t* mine = status + int64_t(b) * D + threadIdx.x;
+    store_status(mine, (b == 0 ? kFlagPrefix : kFlagAggregate) | uint64_t(tot));
+    uint64_t excl = 0;
+    if (b > 0) {
+      excl = look_back(status, D, b, threadIdx.x, err);
+      store_status(mine, kFlagPrefix | (excl + tot));
+    }
+    gofs[threadIdx.x] = digit_base + uint32_t(excl);
+  }
+  __syncthreads();
+
+#pragma unroll
+  for (int i = 0; i < kItems; ++i) {
+    if (full || i * 64 + lane < seg_valid) {
+      const uint32_t pos = dstart[dig[i]] + cnt[wid][dig[i]] + rank[i];
+      skeys[pos] = key[i];
+      svals[pos] = val[i];
+    }
+  }
+  __syncthreads();
+
+  for (int j = threadIdx.x; j < nvalid; j += kBlock) {
+    const K k = skeys[j];
+    const uint32_t d = uint32_t(k >> shift) & (D - 1);
+    const uint32_t o = gofs[d] + uint32_t(j) - dstart[d];
+    keys_out[o] = k;
+    vals_out[o] = svals[j];
+  }
+}
+
+// Exclusive scan of value(i) = in[order ? order[i] : i] into out[0..n), and
+// out[n] = total when write_total; one kernel, kTile elements per workgroup.
+template <typename In, typename Out>
+__global__ __launch_bounds__(kBlock) void scan_kernel(const In* __restrict__ in,
+                                                      const int32_t* __restrict__ order, int64_t n,
+                                                      Out* __restrict__ out, bool write_total,
+                                                      uint64_t* __restrict__ status,
+                                                      uint32_t* __restrict__ ticket,
+                                                      uint32_t* __restrict__ err) {
+  __shared__ Out scratch[4];
+  __shared__ Out s_excl;
+  __shared__ int s_block;
+  if (threadIdx.x == 0) s_block = int(atomicAdd(ticket, 1u));
+  __syncthreads();
+  const int b = s_block;
+  const int64_t first = int64_t(b) * kTile + int64_t(threadIdx.x) * kItems;
+  Out v[kItems];
+  Out sum = 0;
+#pragma unroll
+  for (int i = 0; i < kItems; ++i) {
+    const int64_t idx = first + i;
+    v[i] = idx < n ? Out(in[order ? order[idx] : idx]) : Out(0);
+    sum += v[i];
+  }
+  Out total;
+  const Out pre = block_exclusive_scan(sum, scratch, total);
+  if (threadIdx.x == 0) {
+    store_status(status + b, (b == 0 ? kFlagPrefix : kFlagAggregate) | uint64_t(total));
+    uint64_t excl = 0;
+    if (b > 0) {
+      excl = look_back(status, 1, b, 0, err);
+      store_status(status + b, kFlagPrefix | (excl + uint64_t(total)));
+    }
+    s_excl = Out(excl);
+    if (write_total && b == int(gridDim.x) - 1) out[n] = Out(excl) + total;
+  }
+  __syncthreads();
+  Out run = s_excl + pre;
+#pragma unroll
+  for (int i = 0; i < kItems; ++i) {
+    const int64_t idx = first + i;
+    if (idx < n) out[idx] = run;
+    run += v[i];
+  }
+}
+
+}  // namespace sweep
+}  // namespace gs

@@ -42,42 +42,10 @@ struct ProjectBwdArgs {
 template <int K>
 __global__ __launch_bounds__(kBlock) void project_bwd_kernel(ProjectBwdArgs a) {
   constexpr int F = 3 * K;
-  constexpr int S = F + 1;
-  __shared__ float coeff[kBlock * S];
-
-  const int64_t base = int64_t(blockIdx.x) * kBlock;
-  const int nvalid = int(min(int64_t(kBlock), a.n - base));
-  const int total = nvalid * F;
-  {
-    const float* src = a.color + base * F;
-    const float4* src4 = reinterpret_cast<const float4*>(src);
-    for (int i = threadIdx.x; i * 4 < total; i += kBlock) {
-      const int f = i * 4;
-      float vals[4];
-      if (f + 4 <= total) {
-        const float4 v = src4[i];
-        vals[0] = v.x;
-        vals[1] = v.y;
-        vals[2] = v.z;
-        vals[3] = v.w;
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) vals[j] = (f + j < total) ? src[f + j] : 0.0f;
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int e = f + j;
-        if (e < total) {
-          const int g = e / F;
-          coeff[g * S + (e - g * F)] = vals[j];
-        }
-      }
-    }
-  }
-  __syncthreads();
-
-  const int64_t gi = base + threadIdx.x;
-  float* my = coeff + threadIdx.x * S;
+  const int64_t gi = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+  // Coefficients and their gradients stay in registers (no LDS), loaded only
+  // for Gaussians that were counted.
+  float my[F];
   if (gi < a.n) {
     const bool counted = a.counts[gi] != 0;
     float gmx = 0.0f, gmy = 0.0f, gmz = 0.0f;
@@ -88,6 +56,7 @@ __global__ __launch_bounds__(kBlock) void project_bwd_kernel(ProjectBwdArgs a) {
 #pragma unroll
       for (int i = 0; i < F; ++i) my[i] = 0.0f;
     } else {
+      sh::load_coefficients<K>(a.color + gi * F, my);
       const float r00 = a.cam_r[0], r01 = a.cam_r[1], r02 = a.cam_r[2];
       const float r10 = a.cam_r[3], r11 = a.cam_r[4], r12 = a.cam_r[5];
       const float r20 = a.cam_r[6], r21 = a.cam_r[7], r22 = a.cam_r[8];
@@ -286,30 +255,7 @@ __global__ __launch_bounds__(kBlock) void project_bwd_kernel(ProjectBwdArgs a) {
     a.g_scale[gi * 3 + 1] = gs3[1];
     a.g_scale[gi * 3 + 2] = gs3[2];
     a.g_opacity[gi] = gop;
-  }
-  __syncthreads();
-
-  // Coalesced write-out of the coefficient gradients staged in LDS.
-  {
-    float* dst = a.g_color + base * F;
-    float4* dst4 = reinterpret_cast<float4*>(dst);
-    for (int i = threadIdx.x; i * 4 < total; i += kBlock) {
-      const int f = i * 4;
-      float vals[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int e = f + j;
-        const int g = e / F;
-        vals[j] = e < total ? coeff[g * S + (e - g * F)] : 0.0f;
-      }
-      if (f + 4 <= total) {
-        dst4[i] = make_float4(vals[0], vals[1], vals[2], vals[3]);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (f + j < total) dst[f + j] = vals[j];
-      }
-    }
+    sh::store_coefficients<K>(a.g_color + gi * F, my);
   }
 }
 

@@ -114,5 +114,41 @@ __device__ __forceinline__ void basis_vjp(float x, float y, float z, const float
   }
 }
 
+// One Gaussian's 3K coefficients ([K, 3] row-major) moved between global memory
+// and registers, as dwordx4 accesses when 3K floats keep 16-byte alignment
+// (K = 4 and 16; the caller checks the base pointer) and dword ones otherwise.
+template <int K>
+__device__ __forceinline__ void load_coefficients(const float* __restrict__ p, float* cf) {
+  constexpr int F = 3 * K;
+  if constexpr (F % 4 == 0) {
+    const float4* q = reinterpret_cast<const float4*>(p);
+#pragma unroll
+    for (int i = 0; i < F / 4; ++i) {
+      const float4 v = q[i];
+      cf[4 * i + 0] = v.x;
+      cf[4 * i + 1] = v.y;
+      cf[4 * i + 2] = v.z;
+      cf[4 * i + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < F; ++i) cf[i] = p[i];
+  }
+}
+
+template <int K>
+__device__ __forceinline__ void store_coefficients(float* __restrict__ p, const float* cf) {
+  constexpr int F = 3 * K;
+  if constexpr (F % 4 == 0) {
+    float4* q = reinterpret_cast<float4*>(p);
+#pragma unroll
+    for (int i = 0; i < F / 4; ++i)
+      q[i] = make_float4(cf[4 * i + 0], cf[4 * i + 1], cf[4 * i + 2], cf[4 * i + 3]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < F; ++i) p[i] = cf[i];
+  }
+}
+
 }  // namespace sh
 }  // namespace gs

@@ -11,13 +11,14 @@
 // inputs <= 0.99).  Only g . S (g = dL/dC of the pixel) is carried, as
 // g . S_{i-1} = alpha_i (g . c_i) + (1 - alpha_i) g . S_i.
 //
-// Per Gaussian, each lane sums over its pixels the factors that do not
-// depend on the Gaussian (q = dL/dalpha * G, q dx, q dy, q dx^2, q dx dy,
-// q dy^2 and g T alpha); the wave reduces them with DPP row operations, and
-// one 9-lane fp32 atomic add writes
+// Per Gaussian, each lane sums over its pixels (which share one column, so one
+// dx) q = dL/dalpha * G, q dy, q dy^2 and g T alpha, folds them into the nine
+// per-lane partial gradients
 //   (u, v, inv00, inv01, inv11, r, g, b, opacity) += (-2 k (a Sx + b Sy),
 //   -2 k (b Sx + c Sy), k Sxx, k Sxy, k Syy, Sr, Sg, Sb, Sq),  k = -o / 2,
-// once per (tile, Gaussian).  Replaces composite_bwd.py:47-204 and the
+// and the wave sums them with a transposing permlane/DPP reduction that leaves
+// them in four rows of three registers; two fp32 atomic adds (four and five
+// lanes) write them, once per (tile, Gaussian).  Replaces composite_bwd.py:47-204 and the
 // index_add_ scatter of composite_bwd.py:268-273.
 #include "common.h"
 #include "raster_math.h"
@@ -55,7 +56,9 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_bwd_kernel(Comp
   const int ox = tx * TILE, oy = ty * TILE;
   const int64_t start = a.ranges[2 * tile];
 
-  float pxf[PIX], pyf[PIX];
+  // The lane's pixels share one column (see column_terms).
+  const float pxf = float(ox + lane % TILE);
+  float pyf[PIX];
   float T[PIX], gr[PIX], gg[PIX], gb[PIX], gs_[PIX];
   int ncon[PIX];
   int max_n = 0;
@@ -65,7 +68,6 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_bwd_kernel(Comp
     const int px = ox + (q % TILE), py = oy + (q / TILE);
     const bool valid = q < NPIX && px < a.width && py < a.height;
     const int64_t pix = int64_t(py) * a.width + px;
-    pxf[k] = float(px);
     pyf[k] = float(py);
     T[k] = valid ? a.final_t[pix] : 1.0f;
     ncon[k] = valid ? a.n_contrib[pix] : 0;
@@ -81,6 +83,12 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_bwd_kernel(Comp
   const float rx0 = float(ox), ry0 = float(oy);
   const float rx1 = float(min(ox + TILE, a.width) - 1);
   const float ry1 = float(min(oy + TILE, a.height) - 1);
+  // Gradient fields written by this lane's two atomics: lane 16 r writes the
+  // row-r fields of t0 and t1 of the nine-way sum, lane 1 the opacity total t2.
+  const int field = sum9_field(lane >> 4);
+  const bool row_writer = (lane & 15) == 0;
+  const bool second_writer = row_writer || lane == 1;
+  const int second_field = row_writer ? 4 + field : 8;
 
   for (int64_t top = start + max_n; top > start; top -= 64) {
     const int64_t e = top - 1 - lane;
@@ -99,20 +107,23 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_bwd_kernel(Comp
       mask &= mask - 1;
       const Splat s = broadcast(mine, j);
       const int pos = int(top - 1 - start) - j;
-      float sq = 0.0f, sx = 0.0f, sy = 0.0f, sxx = 0.0f, sxy = 0.0f, syy = 0.0f;
-      float sr = 0.0f, sg = 0.0f, sb = 0.0f;
+      const ColumnTerms c = column_terms(s, pxf);
+      // Per-lane sums over the lane's pixels; -0 is the identity of +, so the
+      // first term needs no add.
+      float s0 = -0.0f, s1 = -0.0f, s2 = -0.0f;  // sum q, q dy, q dy^2
+      float sr = -0.0f, sg = -0.0f, sb = -0.0f;
       bool touched = false;
       // Branch-free: an entry a pixel did not process while active, or whose
       // alpha is cut to 0, runs with alpha = 0, which leaves T, g.S and every
       // sum unchanged.
 #pragma unroll
       for (int k = 0; k < PIX; ++k) {
-        const float dx = pxf[k] - s.u;
         const float dy = pyf[k] - s.v;
         float prob;
-        const float raw = raw_alpha<false>(s, dx, dy, prob);
-        const float alpha = pos < ncon[k] ? blend_alpha(raw) : 0.0f;
-        const bool hit = alpha > 0.0f;
+        const float raw = raw_alpha<false>(s, c, dy, prob);
+        const float clamped = fminf(raw, kMaxAlpha);
+        const bool hit = pos < ncon[k] && clamped >= kMinAlpha;
+        const float alpha = hit ? clamped : 0.0f;
         touched |= hit;
         const float t_before = hit ? T[k] * __builtin_amdgcn_rcpf(1.0f - alpha) : T[k];
         const float w = t_before * alpha;
@@ -123,46 +134,37 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_bwd_kernel(Comp
         const float diff = gc - gs_[k];
         gs_[k] += alpha * diff;
         T[k] = t_before;
-        const float q = (hit && raw <= kMaxAlpha) ? t_before * diff * prob : 0.0f;
-        const float qx = q * dx;
+        // dL/dalpha * G where alpha is neither cut nor clamped (alpha == raw
+        // holds exactly then, and never for a cut or clamped alpha with G > 0).
+        const float q = alpha == raw ? t_before * diff * prob : 0.0f;
         const float qy = q * dy;
-        sq += q;
-        sx += qx;
-        sy += qy;
-        sxx += qx * dx;
-        sxy += qx * dy;
-        syy += qy * dy;
+        s0 += q;
+        s1 += qy;
+        s2 += qy * dy;
       }
       if (__ballot(touched) == 0) continue;
-      sq = wave_sum_lane63(sq);
-      sx = wave_sum_lane63(sx);
-      sy = wave_sum_lane63(sy);
-      sxx = wave_sum_lane63(sxx);
-      sxy = wave_sum_lane63(sxy);
-      syy = wave_sum_lane63(syy);
-      sr = wave_sum_lane63(sr);
-      sg = wave_sum_lane63(sg);
-      sb = wave_sum_lane63(sb);
-      // Gaussian constants, uniform across the wave.
-      const float k = -0.5f * s.o;
-      const float ga = bcast(mine.a, j), gbb = bcast(mine.bb, j), gcc = bcast(mine.c, j);
-      const float tq = bcast(sq, 63), tx_ = bcast(sx, 63), ty_ = bcast(sy, 63);
-      const float txx = bcast(sxx, 63), txy = bcast(sxy, 63), tyy = bcast(syy, 63);
-      const float tr = bcast(sr, 63), tg = bcast(sg, 63), tb = bcast(sb, 63);
-      // Lane i of `val` carries field i of the 9-float gradient row.
-      float val = tq;
-      val = write_lane(val, -2.0f * k * (ga * tx_ + gbb * ty_), 0);
-      val = write_lane(val, -2.0f * k * (gbb * tx_ + gcc * ty_), 1);
-      val = write_lane(val, k * txx, 2);
-      val = write_lane(val, k * txy, 3);
-      val = write_lane(val, k * tyy, 4);
-      val = write_lane(val, tr, 5);
-      val = write_lane(val, tg, 6);
-      val = write_lane(val, tb, 7);
-      if (lane < 9) {
-        const int g = __builtin_amdgcn_readlane(gid, j);
-        unsafeAtomicAdd(a.grad + int64_t(g) * 9 + lane, val);
-      }
+      // d alpha / d(u, v, conic) folded per lane before the reduction
+      // (k = -o/2, -2k = o):  u: o (a Sx + b Sy),  v: o (b Sx + c Sy),
+      // inv00: k Sxx,  inv01: k Sxy,  inv11: k Syy,  Sx = dx s0, Sxx = dx^2 s0,
+      // Sxy = dx s1, Sy = s1, Syy = s2.
+      const float oa = bcast(mine.oa, j), ob = bcast(mine.ob, j), oc = bcast(mine.oc, j);
+      const float sx = c.dx * s0;
+      const float kdx = (-0.5f * s.o) * c.dx;
+      float v[9];
+      v[0] = oa * sx + ob * s1;
+      v[1] = ob * sx + oc * s1;
+      v[2] = kdx * sx;
+      v[3] = kdx * s1;
+      v[4] = (-0.5f * s.o) * s2;
+      v[5] = sr;
+      v[6] = sg;
+      v[7] = sb;
+      v[8] = s0;
+      float t0, t1, t2;
+      wave_sum9(v, t0, t1, t2);
+      float* dst = a.grad + int64_t(__builtin_amdgcn_readlane(gid, j)) * 9;
+      if (row_writer) unsafeAtomicAdd(dst + field, t0);
+      if (second_writer) unsafeAtomicAdd(dst + second_field, row_writer ? t1 : t2);
     }
   }
 }

@@ -49,7 +49,9 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_fwd_kernel(Comp
   const int64_t end = a.ranges[2 * tile + 1];
   const int list_len = int(end - start);
 
-  float pxf[PIX], pyf[PIX];
+  // The lane's pixels share one column (see column_terms).
+  const float pxf = float(ox + lane % TILE);
+  float pyf[PIX];
   float T[PIX], cr[PIX], cg[PIX], cb[PIX];
   bool live[PIX];
   int ncon[PIX];
@@ -59,7 +61,6 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_fwd_kernel(Comp
     const int q = lane + 64 * k;
     const int px = ox + (q % TILE), py = oy + (q / TILE);
     const bool valid = q < NPIX && px < a.width && py < a.height;
-    pxf[k] = float(px);
     pyf[k] = float(py);
     T[k] = 1.0f;
     cr[k] = cg[k] = cb[k] = 0.0f;
@@ -94,12 +95,13 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_fwd_kernel(Comp
       mask &= mask - 1;
       const Splat s = broadcast(mine, j);
       const int pos = int(base - start) + j;
+      const ColumnTerms c = column_terms(s, pxf);
       // Branch-free: a finished pixel (or a cut alpha) blends with alpha = 0,
       // which leaves its colour and T unchanged.
 #pragma unroll
       for (int k = 0; k < PIX; ++k) {
         float prob;
-        const float raw = raw_alpha<ELLIPSOID>(s, pxf[k] - s.u, pyf[k] - s.v, prob);
+        const float raw = raw_alpha<ELLIPSOID>(s, c, pyf[k] - s.v, prob);
         const float alpha = live[k] ? blend_alpha(raw) : 0.0f;
         const float w = T[k] * alpha;
         cr[k] += w * s.r;

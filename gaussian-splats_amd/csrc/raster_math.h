@@ -22,7 +22,7 @@ struct Splat {
 // Per-lane view of a gathered record with the pre-scaled conic.
 struct LaneSplat {
   float u, v, o, pa, pb, pc, cut, r, g, b;
-  float a, bb, c;  // unscaled inverse covariance (for the mean gradient)
+  float oa, ob, oc;  // opacity times the unscaled inverse covariance (mean gradient)
 };
 
 __device__ __forceinline__ LaneSplat lane_splat(const GsRecord& r) {
@@ -37,23 +37,41 @@ __device__ __forceinline__ LaneSplat lane_splat(const GsRecord& r) {
   s.r = r.r;
   s.g = r.g;
   s.b = r.b;
-  s.a = r.inv00;
-  s.bb = r.inv01;
-  s.c = r.inv11;
+  s.oa = r.opacity * r.inv00;
+  s.ob = r.opacity * r.inv01;
+  s.oc = r.opacity * r.inv11;
   return s;
 }
 
-// log2 of the Gaussian falloff at pixel offset (dx, dy).
-__device__ __forceinline__ float falloff_log2(const Splat& s, float dx, float dy) {
-  return dx * (s.pa * dx + s.pb * dy) + s.pc * (dy * dy);
+// A lane owns one pixel column of its tile (pixel q = lane + 64 k lies in
+// column lane % tile for every tile size up to 64), so the part of the
+// exponent that depends only on dx is computed once per (lane, splat):
+//   log2 falloff = pa dx^2 + pb dx dy + pc dy^2 = p0 + dy (p1 + pc dy).
+// The forward and backward kernels both evaluate it through these helpers, so
+// their alphas are bit-identical.
+struct ColumnTerms {
+  float dx, p0, p1;
+};
+
+__device__ __forceinline__ ColumnTerms column_terms(const Splat& s, float px) {
+  ColumnTerms c;
+  c.dx = px - s.u;
+  c.p1 = s.pb * c.dx;
+  c.p0 = (s.pa * c.dx) * c.dx;
+  return c;
+}
+
+__device__ __forceinline__ float falloff_log2(const ColumnTerms& c, float pc, float dy) {
+  return fmaf(dy, fmaf(pc, dy, c.p1), c.p0);
 }
 
 // Unclamped alpha = opacity * probability (utils.py:90-99); `prob` returns the
 // probability.  Ellipsoid mode compares D = power / (-0.5 log2 e) with the
 // cutoff stored in the record.
 template <bool ELLIPSOID>
-__device__ __forceinline__ float raw_alpha(const Splat& s, float dx, float dy, float& prob) {
-  const float power = falloff_log2(s, dx, dy);
+__device__ __forceinline__ float raw_alpha(const Splat& s, const ColumnTerms& c, float dy,
+                                           float& prob) {
+  const float power = falloff_log2(c, s.pc, dy);
   if constexpr (ELLIPSOID) {
     prob = power >= kNegHalfLog2e * s.cut ? 1.0f : 0.0f;
   } else {
@@ -156,11 +174,6 @@ __device__ __forceinline__ float bcast(float x, int j) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), j));
 }
 
-// Returns `v` with lane `lane` replaced by the wave-uniform value `x`.
-__device__ __forceinline__ float write_lane(float v, float x, int lane) {
-  return __lane_id() == lane ? x : v;
-}
-
 // Broadcasts lane j's splat to the whole wave (v_readlane into SGPRs, so the
 // per-pixel math takes the Gaussian's fields as scalar operands).
 __device__ __forceinline__ Splat broadcast(const LaneSplat& l, int j) {
@@ -186,18 +199,51 @@ __device__ __forceinline__ float dpp0(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
 }
 
-// Sum over the 64 lanes, valid in lane 63 only: quad_perm xor 1 and xor 2, row
-// half-mirror and mirror (each row of 16 then holds its row sum), row_bcast:15
-// (row 3 += row 2, row 1 += row 0) and row_bcast:31 (rows 2, 3 += lane 31).
-// Other lanes end with partial sums.  Needs a full EXEC.
-__device__ __forceinline__ float wave_sum_lane63(float v) {
+// Sum over each row of 16 lanes, left in every lane of the row: quad_perm
+// xor 1 and xor 2, then row half-mirror and row mirror.  Needs a full EXEC.
+__device__ __forceinline__ float row_sum(float v) {
   v += dpp0<0xB1>(v);   // quad_perm [1,0,3,2]
   v += dpp0<0x4E>(v);   // quad_perm [2,3,0,1]
   v += dpp0<0x141>(v);  // row_half_mirror
   v += dpp0<0x140>(v);  // row_mirror
-  v += dpp0<0x142>(v);  // row_bcast:15
-  v += dpp0<0x143>(v);  // row_bcast:31
   return v;
+}
+
+// v_permlane32_swap exchanges the upper half of x with the lower half of y, so
+// the sum holds x folded over the two halves in lanes 0-31 and y folded in
+// lanes 32-63: lane i < 32 gets x[i] + x[i + 32], lane i >= 32 gets
+// y[i - 32] + y[i].
+__device__ __forceinline__ float fold_halves(float x, float y) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// v_permlane16_swap exchanges the odd rows of x with the even rows of y; the
+// sum holds rows (x0 + x1, y0 + y1, x2 + x3, y2 + y3).
+__device__ __forceinline__ float fold_rows(float x, float y) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(y), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Wave totals of nine per-lane values v[0..8] by a transposing reduction:
+// the two swap folds spread the values over the rows of three registers and a
+// row sum finishes each, 30 VALU operations instead of 54 for nine full
+// butterflies.  On return, every lane of row r (lanes 16 r .. 16 r + 15) of
+//   t0 holds the total of v[sum9_field(r)],  t1 that of v[4 + sum9_field(r)],
+// and t2 holds the total of v[8] in every lane.  Needs a full EXEC.
+__device__ __forceinline__ int sum9_field(int row) { return ((row & 1) << 1) | (row >> 1); }
+
+__device__ __forceinline__ void wave_sum9(const float (&v)[9], float& t0, float& t1, float& t2) {
+  const float a0 = fold_halves(v[0], v[1]);
+  const float a1 = fold_halves(v[2], v[3]);
+  const float a2 = fold_halves(v[4], v[5]);
+  const float a3 = fold_halves(v[6], v[7]);
+  const float a4 = fold_halves(v[8], v[8]);
+  t0 = row_sum(fold_rows(a0, a1));  // rows: v0, v2, v1, v3
+  t1 = row_sum(fold_rows(a2, a3));  // rows: v4, v6, v5, v7
+  t2 = row_sum(fold_rows(a4, a4));  // every row: v8
 }
 
 }  // namespace gs

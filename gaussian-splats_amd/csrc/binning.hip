@@ -20,150 +20,12 @@
 #include "block_scan.h"
 #include "common.h"
 #include "onesweep.h"
+#include "radix.h"
 
 namespace gs {
 namespace {
 
-constexpr int kBlock = 256;
-using sweep::kTile;
 
-int bits_for(int64_t count) {  // ceil(log2(count)), 0 for count <= 1
-  int b = 0;
-  while ((int64_t(1) << b) < count) ++b;
-  return b;
-}
-
-// Scratch shared by the sort and the scan: ping-pong buffers, then one zeroed
-// region (look-back status words of every sort pass and of the scan, then the
-// 32-bit histograms, tickets and error flags).
-struct Scratch {
-  void* keys_alt = nullptr;
-  uint32_t* vbuf[2] = {nullptr, nullptr};
-  uint64_t* sort_status = nullptr;
-  uint64_t* scan_status = nullptr;
-  uint64_t* zero_begin = nullptr;
-  int64_t zero_words = 0;  // 64-bit words of status
-  uint32_t* small = nullptr;  // hist[kMaxPasses*256], tickets[kMaxPasses], err, scan ticket, scan err
-  int small_words = 0;
-  size_t bytes = 0;
-
-  uint32_t* hist() const { return small; }
-  uint32_t* tickets() const { return small + sweep::kMaxPasses * 256; }
-  uint32_t* err() const { return tickets() + sweep::kMaxPasses; }
-  uint32_t* scan_ticket() const { return err() + 1; }
-  uint32_t* scan_err() const { return err() + 2; }
-};
-
-int64_t sort_status_words(int64_t n, const sweep::Plan& p) {
-  const int64_t nblocks = ceil_div(n, kTile);
-  int64_t words = 0;
-  for (int i = 0; i < p.passes; ++i) words += nblocks << p.bits[i];
-  return words;
-}
-
-// Lays out scratch for a sort of n keys of key_bytes over end_bit bits
-// (end_bit < 0: no sort) and a scan of scan_n elements (0: no scan).
-Scratch carve(void* ws, int64_t n, int key_bytes, int end_bit, int64_t scan_n) {
-  Scratch s;
-  char* p = static_cast<char*>(ws);
-  size_t off = 0;
-  int64_t sort_words = 0;
-  if (end_bit >= 0 && n > 0) {
-    s.keys_alt = p ? p + off : nullptr;
-    off += align_up(size_t(n) * key_bytes);
-    for (int i = 0; i < 2; ++i) {
-      s.vbuf[i] = p ? reinterpret_cast<uint32_t*>(p + off) : nullptr;
-      off += align_up(size_t(n) * 4);
-    }
-    sort_words = sort_status_words(n, sweep::make_plan(end_bit));
-  }
-  const int64_t scan_words = scan_n > 0 ? ceil_div(scan_n, kTile) : 0;
-  s.zero_begin = p ? reinterpret_cast<uint64_t*>(p + off) : nullptr;
-  s.sort_status = s.zero_begin;
-  s.scan_status = p ? s.zero_begin + sort_words : nullptr;
-  s.zero_words = sort_words + scan_words;
-  off += align_up(size_t(s.zero_words) * 8);
-  s.small_words = sweep::kMaxPasses * 256 + sweep::kMaxPasses + 3;
-  s.small = p ? reinterpret_cast<uint32_t*>(p + off) : nullptr;
-  off += align_up(size_t(s.small_words) * 4);
-  s.bytes = off;
-  return s;
-}
-
-void clear(const Scratch& s, hipStream_t stream) {
-  const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(1024, ceil_div(s.zero_words, kBlock)));
-  sweep::clear_kernel<<<unsigned(blocks), kBlock, 0, stream>>>(s.zero_begin, s.zero_words, s.small,
-                                                               s.small_words);
-}
-
-template <typename K, int BITS>
-void launch_scatter(const K* kin, const uint32_t* vin, K* kout, uint32_t* vout, int64_t n,
-                    int shift, const uint32_t* hist, uint64_t* status, uint32_t* ticket,
-                    uint32_t* err, hipStream_t s) {
-  const unsigned nblocks = unsigned(ceil_div(n, kTile));
-  sweep::scatter_kernel<K, BITS><<<nblocks, sweep::kBlock, 0, s>>>(kin, vin, kout, vout, n, shift,
-                                                                   hist, status, ticket, err);
-}
-
-template <typename K>
-void dispatch_scatter(int bits, const K* kin, const uint32_t* vin, K* kout, uint32_t* vout,
-                      int64_t n, int shift, const uint32_t* hist, uint64_t* status,
-                      uint32_t* ticket, uint32_t* err, hipStream_t s) {
-  switch (bits) {
-    case 1: launch_scatter<K, 1>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, s); break;
-    case 2: launch_scatter<K, 2>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, s); break;
-    case 3: launch_scatter<K, 3>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, s); break;
-    case 4: launch_scatter<K, 4>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, s); break;
-    case 5: launch_scatter<K, 5>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, s); break;
-    case 6: launch_scatter<K, 6>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, s); break;
-    case 7: launch_scatter<K, 7>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, s); break;
-    default: launch_scatter<K, 8>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, s); break;
-  }
-}
-
-// Sorts (keys, vals) on bits [0, end_bit) after `clear` has zeroed the scratch.
-// vals == nullptr means vals[i] = i.  Sorted values land in vals_final;
-// *keys_final points at the sorted keys (keys or the scratch copy).
-template <typename K>
-int radix_sort(K* keys, const uint32_t* vals, int64_t n, int end_bit, uint32_t* vals_final,
-               K** keys_final, const Scratch& ws, hipStream_t s) {
-  GS_REQUIRE(n < (int64_t(1) << 32) - kTile, GS_ERR_OVERFLOW, "too many elements to sort (%lld)",
-             (long long)n);
-  *keys_final = keys;
-  if (n == 0) return GS_OK;
-  const sweep::Plan plan = sweep::make_plan(end_bit);
-  const int hist_blocks = int(std::min<int64_t>(512, ceil_div(n, kBlock * 16)));
-  sweep::hist_kernel<K><<<unsigned(hist_blocks), kBlock, 0, s>>>(keys, n, plan, ws.hist());
-  K* kbuf[2] = {static_cast<K*>(ws.keys_alt), keys};
-  const K* kin = keys;
-  const uint32_t* vin = vals;
-  uint64_t* status = ws.sort_status;
-  const int64_t nblocks = ceil_div(n, kTile);
-  for (int pass = 0; pass < plan.passes; ++pass) {
-    K* kout = kbuf[pass & 1];
-    uint32_t* vout = (pass == plan.passes - 1) ? vals_final : ws.vbuf[pass & 1];
-    dispatch_scatter<K>(plan.bits[pass], kin, vin, kout, vout, n, plan.shift[pass],
-                        ws.hist() + pass * 256, status, ws.tickets() + pass, ws.err(), s);
-    status += nblocks << plan.bits[pass];
-    kin = kout;
-    vin = vout;
-  }
-  *keys_final = const_cast<K*>(kin);
-  return check_launch("radix_sort");
-}
-
-template <typename In, typename Out>
-void launch_scan(const In* in, const int32_t* order, int64_t n, Out* out, bool write_total,
-                 const Scratch& ws, hipStream_t s) {
-  sweep::scan_kernel<In, Out><<<unsigned(ceil_div(n, kTile)), sweep::kBlock, 0, s>>>(
-      in, order, n, out, write_total, ws.scan_status, ws.scan_ticket(), ws.scan_err());
-}
-
-template <typename T>
-__global__ void fill_kernel(T* p, int64_t n, T value) {
-  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = value;
-}
 
 // ---------------------------------------------------------------------------
 // Per-tile half-open ranges by binary search on the sorted tile ids.
@@ -333,7 +195,7 @@ GS_API int gs_scan_counts(const int32_t* counts, int64_t n, int64_t* offsets, vo
   const Scratch ws = carve(workspace, 0, 4, -1, n);
   GS_REQUIRE(workspace && workspace_bytes >= ws.bytes, GS_ERR_WORKSPACE, "scan workspace too small");
   clear(ws, s);
-  launch_scan<int32_t, int64_t>(counts, nullptr, n, offsets, true, ws, s);
+  launch_scan<int64_t>(sweep::GatherLoad<int32_t, int64_t>{counts, nullptr}, n, offsets, true, ws, s);
   return check_launch("scan_counts");
 }
 
@@ -406,7 +268,7 @@ GS_API int gs_bin_gaussians(uint32_t* depth_keys, const int32_t* counts, int64_t
   uint32_t* sorted_keys = nullptr;
   GS_TRY(radix_sort<uint32_t>(depth_keys, nullptr, n, 32, reinterpret_cast<uint32_t*>(order),
                               &sorted_keys, ws, s));
-  launch_scan<int32_t, int64_t>(counts, order, n, offsets, true, ws, s);
+  launch_scan<int64_t>(sweep::GatherLoad<int32_t, int64_t>{counts, order}, n, offsets, true, ws, s);
   return check_launch("bin_gaussians");
 }
 

@@ -81,6 +81,38 @@ __device__ inline uint64_t look_back(const uint64_t* status, int64_t stride, int
   return excl;
 }
 
+// The same walk for a single column (stride 1) by a whole wave: lane i reads
+// the status of workgroup k0 - i, so one memory round trip covers 64
+// predecessors.  Wave-uniform result.
+__device__ inline uint64_t wave_look_back(const uint64_t* status, int b, uint32_t* err) {
+  const int lane = __lane_id();
+  uint64_t excl = 0;
+  int spins = 0;
+  for (int k0 = b - 1; k0 >= 0;) {
+    const int k = k0 - lane;
+    const uint64_t v = k >= 0 ? load_status(status + k) : kFlagPrefix;  // before 0: prefix 0
+    const uint64_t prefix = __ballot((v >> 62) == 2);
+    const uint64_t waiting = __ballot((v >> 62) == 0);
+    const int first = prefix ? __builtin_ctzll(prefix) : 63;  // lanes 0..first are needed
+    const uint64_t needed = first == 63 ? ~0ull : ((1ull << (first + 1)) - 1);
+    if (waiting & needed) {
+      if (++spins > kSpinLimit) {
+        if (lane == 0) atomicOr(err, 1u);
+        return excl;
+      }
+      __builtin_amdgcn_s_sleep(2);
+      continue;
+    }
+    uint64_t part = lane <= first ? (v & kValueMask) : 0;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
+    excl += part;
+    if (prefix) return excl;
+    k0 -= 64;
+  }
+  return excl;
+}
+
 // Zeroes `words` 64-bit words and `small` 32-bit words (tickets, histograms).
 __global__ __launch_bounds__(kBlock) inline void clear_kernel(uint64_t* big, int64_t words,
                                                               uint32_t* small, int small_words) {
@@ -266,12 +298,19 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
   }
 }
 
-// Exclusive scan of value(i) = in[order ? order[i] : i] into out[0..n), and
-// out[n] = total when write_total; one kernel, kTile elements per workgroup.
+// value(i) = in[order ? order[i] : i], widened to Out.
 template <typename In, typename Out>
-__global__ __launch_bounds__(kBlock) void scan_kernel(const In* __restrict__ in,
-                                                      const int32_t* __restrict__ order, int64_t n,
-                                                      Out* __restrict__ out, bool write_total,
+struct GatherLoad {
+  const In* in;
+  const int32_t* order;
+  __device__ Out operator()(int64_t i) const { return Out(in[order ? order[i] : i]); }
+};
+
+// Exclusive scan of load(i) into out[0..n), and out[n] = total when
+// write_total; one kernel, kTile elements per workgroup.
+template <typename Out, typename Load>
+__global__ __launch_bounds__(kBlock) void scan_kernel(Load load, int64_t n, Out* __restrict__ out,
+                                                      bool write_total,
                                                       uint64_t* __restrict__ status,
                                                       uint32_t* __restrict__ ticket,
                                                       uint32_t* __restrict__ err) {
@@ -287,20 +326,20 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(const In* __restrict__ in,
 #pragma unroll
   for (int i = 0; i < kItems; ++i) {
     const int64_t idx = first + i;
-    v[i] = idx < n ? Out(in[order ? order[idx] : idx]) : Out(0);
+    v[i] = idx < n ? load(idx) : Out(0);
     sum += v[i];
   }
   Out total;
   const Out pre = block_exclusive_scan(sum, scratch, total);
-  if (threadIdx.x == 0) {
-    store_status(status + b, (b == 0 ? kFlagPrefix : kFlagAggregate) | uint64_t(total));
-    uint64_t excl = 0;
-    if (b > 0) {
-      excl = look_back(status, 1, b, 0, err);
-      store_status(status + b, kFlagPrefix | (excl + uint64_t(total)));
+  if (threadIdx.x < 64) {
+    if (threadIdx.x == 0)
+      store_status(status + b, (b == 0 ? kFlagPrefix : kFlagAggregate) | uint64_t(total));
+    const uint64_t excl = b > 0 ? wave_look_back(status, b, err) : 0;
+    if (threadIdx.x == 0) {
+      if (b > 0) store_status(status + b, kFlagPrefix | (excl + uint64_t(total)));
+      s_excl = Out(excl);
+      if (write_total && b == int(gridDim.x) - 1) out[n] = Out(excl) + total;
     }
-    s_excl = Out(excl);
-    if (write_total && b == int(gridDim.x) - 1) out[n] = Out(excl) + total;
   }
   __syncthreads();
   Out run = s_excl + pre;

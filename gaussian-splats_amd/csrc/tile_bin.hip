@@ -1,0 +1,744 @@
+// Row-bucketed tile binning for grids of at most 256 x 256 tiles.
+//
+// Produces exactly the sorted Gaussian ids and per-tile ranges of a stable sort
+// of the reference keys tile_id << 32 | depth bits (intersections.py:10-88,
+// torch.py:254-287), like gs_emit_tiles + gs_sort_tiles, while moving about a
+// third of their bytes: every Gaussian covers a rectangle of tiles, so
+//  1. tables: corners of the rectangles in a 2-D difference array give, after
+//     a 2-D prefix sum, every tile's intersection count, hence the ranges and
+//     the start of every (row, column) bucket; a 1-D difference array gives
+//     the number of Gaussians covering each tile row.  No key histograms.
+//  2. pass A: the depth-ordered Gaussians are expanded into one entry per
+//     covered tile row and bucketed stably by row (the row list: Gaussian id,
+//     first column and width per entry; about 5x fewer entries than
+//     intersections).
+//  3. a scan of the widths over the row list gives each row entry's first
+//     position in row-major intersection order.
+//  4. pass B: each row entry is expanded into its columns and bucketed stably
+//     by column inside its row, straight to start(tile) + rank; only the
+//     Gaussian id is written.
+// Inside a tile the entries keep row-list order, which is depth order (ties by
+// index), so the result is the stable (tile, depth bits, index) order.
+//
+// Both passes are onesweep-style (onesweep.h): ticket-ordered workgroups of
+// kTile items, wave ranking by ballots, decoupled look-back for the per-digit
+// offsets (pass B's chains restart at each row), reorder in LDS, coalesced
+// stores.  Items are generated in registers from the owner of each position
+// (marked in LDS from the scanned offsets and spread by a prefix maximum), so the expanded
+// entries are never written before they are placed.
+#include "block_scan.h"
+#include "common.h"
+#include "onesweep.h"
+#include "radix.h"
+
+namespace gs {
+namespace {
+
+using sweep::kItems;
+constexpr int kMaxAxisTiles = 256;
+constexpr int kSeg = kTile / 4;  // items per wave
+// Rectangle tables at most this many words are accumulated in LDS first.
+constexpr int kPrivateTableWords = 12288;
+
+// ---------------------------------------------------------------------------
+// Tables.
+// ---------------------------------------------------------------------------
+
+// Corners of each counted Gaussian's rectangle [x0, x1) x [y0, y1) in the 2-D
+// difference array diff2 (th + 1 rows of pitch tw + 1) and ends of its rows in
+// the 1-D difference array rowdiff (th + 1).
+template <bool PRIVATE>
+__global__ __launch_bounds__(256) void rect_diff_kernel(const int4* __restrict__ bounds,
+                                                        const int32_t* __restrict__ counts,
+                                                        int64_t n, int tw, int th,
+                                                        int32_t* __restrict__ diff2,
+                                                        int32_t* __restrict__ rowdiff) {
+  extern __shared__ int32_t lds[];
+  const int pitch = tw + 1;
+  const int words = (th + 1) * pitch;
+  int32_t* t2 = PRIVATE ? lds : diff2;
+  int32_t* tr = PRIVATE ? lds + words : lds;
+  if (PRIVATE)
+    for (int i = threadIdx.x; i < words; i += 256) t2[i] = 0;
+  for (int i = threadIdx.x; i <= th; i += 256) tr[i] = 0;
+  __syncthreads();
+  const int64_t stride = int64_t(gridDim.x) * 256;
+  for (int64_t g = int64_t(blockIdx.x) * 256 + threadIdx.x; g < n; g += stride) {
+    if (counts[g] > 0) {
+      // x0, x1, y0, y1 (already inside the grid when they come from the
+      // projection; clamped so that no other input indexes out of the tables)
+      const int4 b = bounds[g];
+      const int x0 = min(max(b.x, 0), tw), x1 = min(max(b.y, 0), tw);
+      const int y0 = min(max(b.z, 0), th), y1 = min(max(b.w, 0), th);
+      atomicAdd(&t2[y0 * pitch + x0], 1);
+      atomicAdd(&t2[y0 * pitch + x1], -1);
+      atomicAdd(&t2[y1 * pitch + x0], -1);
+      atomicAdd(&t2[y1 * pitch + x1], 1);
+      atomicAdd(&tr[y0], 1);
+      atomicAdd(&tr[y1], -1);
+    }
+  }
+  __syncthreads();
+  if (PRIVATE)
+    for (int i = threadIdx.x; i < words; i += 256)
+      if (t2[i]) atomicAdd(&diff2[i], t2[i]);
+  for (int i = threadIdx.x; i <= th; i += 256)
+    if (tr[i]) atomicAdd(&rowdiff[i], tr[i]);
+}
+
+// One workgroup.  Tile counts = 2-D prefix of diff2; ranges[t] = [start,
+// start + count) in row-major tile order; per row y: row_e[y] = first
+// intersection, row_a[y] = first row-list entry, row_blk[y] = first pass-B
+// workgroup; entry th of each holds the total.  totals = {intersections,
+// row-list entries, pass-B workgroups, 0}.  With LDS_TABLE the th x (tw + 1)
+// table is staged in LDS (dynamic shared memory), so the dependent prefix
+// steps run at LDS latency; ranges are written once, after the row starts
+// are known.
+template <bool LDS_TABLE>
+__global__ __launch_bounds__(256) void tables_kernel(int32_t* __restrict__ diff2,
+                                                     const int32_t* __restrict__ rowdiff, int tw,
+                                                     int th, int64_t* __restrict__ ranges,
+                                                     uint32_t* __restrict__ row_a,
+                                                     uint32_t* __restrict__ row_e,
+                                                     uint32_t* __restrict__ row_blk,
+                                                     int64_t* __restrict__ totals) {
+  extern __shared__ int32_t tab_lds[];
+  __shared__ int64_t s_row[kMaxAxisTiles];
+  __shared__ int64_t scratch[4];
+  const int pitch = tw + 1;
+  const int lane = threadIdx.x & 63;
+  const int wid = threadIdx.x >> 6;
+  int32_t* tab = LDS_TABLE ? tab_lds : diff2;
+  if (LDS_TABLE) {
+    for (int i = threadIdx.x; i < th * pitch; i += 256) tab[i] = diff2[i];
+    __syncthreads();
+  }
+
+  // 1. Column prefix over the rows (thread x), in place.
+  for (int x = threadIdx.x; x < tw; x += 256) {
+    int32_t acc = 0;
+    for (int y0 = 0; y0 < th; y0 += 8) {
+      int32_t v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = y0 + i < th ? tab[(y0 + i) * pitch + x] : 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        acc += v[i];
+        if (y0 + i < th) tab[(y0 + i) * pitch + x] = acc;
+      }
+    }
+  }
+  __syncthreads();
+
+  // 2. One wave per row: count(x, y) = prefix over x of the column prefixes
+  // (stored in place), row total into s_row.
+  for (int y = wid; y < th; y += 4) {
+    int32_t carry = 0;
+    int64_t row_total = 0;
+    for (int x0 = 0; x0 < tw; x0 += 64) {
+      const int x = x0 + lane;
+      const int32_t v = x < tw ? tab[y * pitch + x] : 0;
+      const int32_t c = carry + wave_inclusive_scan(v);
+      if (x < tw) tab[y * pitch + x] = c;
+      row_total += wave_sum(int64_t(x < tw ? c : 0));
+      carry = __shfl(c, 63, 64);
+    }
+    if (lane == 0) s_row[y] = row_total;
+  }
+  __syncthreads();
+
+  // 3. Row tables (thread y).
+  const int y = threadIdx.x;
+  const int64_t row_entries = y < th ? s_row[y] : 0;
+  int64_t tot_e, tot_c, tot_a, tot_b;
+  const int64_t e_start = block_exclusive_scan(row_entries, scratch, tot_e);
+  const int64_t rd = y < th ? int64_t(rowdiff[y]) : 0;
+  const int64_t cover = block_exclusive_scan(rd, scratch, tot_c) + rd;  // Gaussians on row y
+  const int64_t a_start = block_exclusive_scan(y < th ? cover : int64_t(0), scratch, tot_a);
+  const int64_t blocks = (row_entries + kTile - 1) / kTile;
+  const int64_t b_start = block_exclusive_scan(blocks, scratch, tot_b);
+  if (y < th) {
+    row_e[y] = uint32_t(e_start);
+    row_a[y] = uint32_t(a_start);
+    row_blk[y] = uint32_t(b_start);
+    s_row[y] = e_start;
+  }
+  if (threadIdx.x == 0) {
+    row_e[th] = uint32_t(tot_e);
+    row_a[th] = uint32_t(tot_a);
+    row_blk[th] = uint32_t(tot_b);
+    totals[0] = tot_e;
+    totals[1] = tot_a;
+    totals[2] = tot_b;
+    totals[3] = 0;
+  }
+  __syncthreads();
+
+  // 4. Ranges: row start + exclusive prefix of the counts along the row.
+  for (int y2 = wid; y2 < th; y2 += 4) {
+    int64_t carry = s_row[y2];
+    for (int x0 = 0; x0 < tw; x0 += 64) {
+      const int x = x0 + lane;
+      const int64_t cnt = x < tw ? int64_t(tab[y2 * pitch + x]) : 0;
+      const int64_t inc = carry + wave_inclusive_scan(cnt);
+      if (x < tw) {
+        const int64_t t = int64_t(y2) * tw + x;
+        reinterpret_cast<longlong2*>(ranges)[t] = make_longlong2(inc - cnt, inc);
+      }
+      carry = __shfl(inc, 63, 64);
+    }
+  }
+}
+
+// Row-list entries per Gaussian in depth order: its tile-row count, 0 if
+// it has no intersections.
+struct HeightLoad {
+  const int4* bounds;
+  const int32_t* counts;
+  const int32_t* order;
+  __device__ uint32_t operator()(int64_t i) const {
+    const int g = order[i];
+    if (counts[g] <= 0) return 0u;
+    const int4 b = bounds[g];
+    return uint32_t(b.w - b.z);
+  }
+};
+
+// Width field of a packed row-list entry (first column | width << 16).
+struct WidthLoad {
+  const uint32_t* xw;
+  __device__ uint32_t operator()(int64_t i) const { return xw[i] >> 16; }
+};
+
+// ---------------------------------------------------------------------------
+// Bucketing passes.
+// ---------------------------------------------------------------------------
+
+// Largest p in [lo, hi] with offs[p] <= target, given offs[lo] <= target and
+// offs non-decreasing: a 64-ary search, one ballot per round.  Wave-uniform.
+__device__ int64_t wave_last_le(const uint32_t* __restrict__ offs, int64_t lo, int64_t hi,
+                                uint32_t target) {
+  const int lane = __lane_id();
+  while (lo < hi) {
+    const int64_t step = (hi - lo + 63) / 64;
+    const int64_t q = min(lo + (lane + 1) * step, hi);
+    const uint64_t m = __ballot(offs[q] <= target);
+    const int cnt = __popcll(m);
+    if (cnt == 0) {
+      hi = lo + step - 1;
+    } else {
+      const int64_t new_lo = min(lo + cnt * step, hi);
+      if (cnt < 64) hi = min(lo + (cnt + 1) * step - 1, hi);
+      lo = new_lo;
+    }
+  }
+  return lo;
+}
+
+template <int BITS, int NV>
+struct BucketLds {
+  uint32_t cnt[4][1 << BITS];
+  uint32_t dstart[1 << BITS];
+  uint32_t gofs[1 << BITS];
+  uint32_t scratch[4];
+  int64_t owner[2];
+  int block;
+  int row;
+  uint8_t dig[kTile];
+  alignas(16) uint16_t own[kTile];  // owner (window index) of every position
+  // Owner window (int32 offsets relative to the first item) while items are
+  // generated, then the values reordered by digit.
+  uint32_t val[NV * kTile];
+};
+
+// own[e] = largest k < m with rel[k] <= e, for every position e < kTile of
+// the workgroup (rel[0] <= 0 < rel[1] < ... < rel[m - 1] < kTile): each owner
+// k >= 1 marks its first position, and a block-wide prefix maximum over the
+// positions (16 consecutive ones per thread) fills the rest.  Replaces a
+// binary search per item by a few independent LDS accesses per item.
+__device__ void find_owners(const int32_t* rel, int m, uint16_t* own, uint32_t* scratch) {
+  uint4* own4 = reinterpret_cast<uint4*>(own);
+  for (int i = threadIdx.x; i < kTile / 8; i += kBlock) own4[i] = make_uint4(0, 0, 0, 0);
+  __syncthreads();
+  for (int k = 1 + threadIdx.x; k < m; k += kBlock) {
+    const int r = rel[k];
+    if (r > 0 && r < kTile) own[r] = uint16_t(k);
+  }
+  __syncthreads();
+  static_assert(kTile == 16 * kBlock, "16 positions per thread");
+  uint4 q[2] = {own4[2 * threadIdx.x], own4[2 * threadIdx.x + 1]};
+  uint32_t w[8] = {q[0].x, q[0].y, q[0].z, q[0].w, q[1].x, q[1].y, q[1].z, q[1].w};
+  uint32_t run = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {  // owners never decrease: a running max
+    const uint32_t lo = max(run, w[i] & 0xFFFFu);
+    const uint32_t hi = max(lo, w[i] >> 16);
+    w[i] = lo | (hi << 16);
+    run = hi;
+  }
+  // Exclusive max over the threads before this one.
+  const int lane = threadIdx.x & 63;
+  const int wid = threadIdx.x >> 6;
+  uint32_t inc = run;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t t = __shfl_up(inc, o, 64);
+    if (lane >= o) inc = max(inc, t);
+  }
+  if (lane == 63) scratch[wid] = inc;
+  uint32_t before = __shfl_up(inc, 1, 64);
+  if (lane == 0) before = 0;
+  __syncthreads();
+  for (int v = 0; v < wid; ++v) before = max(before, scratch[v]);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t lo = max(before, w[i] & 0xFFFFu);
+    const uint32_t hi = max(before, w[i] >> 16);
+    w[i] = lo | (hi << 16);
+  }
+  own4[2 * threadIdx.x] = make_uint4(w[0], w[1], w[2], w[3]);
+  own4[2 * threadIdx.x + 1] = make_uint4(w[4], w[5], w[6], w[7]);
+  __syncthreads();
+}
+
+// Ranks the workgroup's items by digit, finds each digit's offset among the
+// items of the earlier workgroups of the chain (chain_first .. b - 1) by
+// look-back, and stores the NV values of every item at
+// base(d) + offset(d) + rank (below `capacity`).  Items at
+// i * 64 + lane < seg_valid of each wave's segment are valid; digits are
+// below 2^BITS.
+template <int BITS, int NV, typename Base>
+__device__ void place_items(BucketLds<BITS, NV>& sh, const uint32_t (&dig)[kItems],
+                            const uint32_t (&val)[NV][kItems], int nvalid, int b,
+                            int chain_first, Base base, uint64_t* __restrict__ status,
+                            uint32_t* __restrict__ err, uint32_t* const (&out)[NV],
+                            uint32_t capacity) {
+  constexpr int D = 1 << BITS;
+  const int lane = threadIdx.x & 63;
+  const int wid = threadIdx.x >> 6;
+  const int seg_valid = nvalid - wid * kSeg;
+  uint32_t rank[kItems];
+  if (nvalid == kTile)
+    sweep::rank_items<BITS, true>(dig, seg_valid, sh.cnt[wid], rank);
+  else
+    sweep::rank_items<BITS, false>(dig, seg_valid, sh.cnt[wid], rank);
+  __syncthreads();
+
+  uint32_t tot = 0;
+  if (threadIdx.x < D) {
+    const uint32_t c0 = sh.cnt[0][threadIdx.x], c1 = sh.cnt[1][threadIdx.x];
+    const uint32_t c2 = sh.cnt[2][threadIdx.x], c3 = sh.cnt[3][threadIdx.x];
+    sh.cnt[0][threadIdx.x] = 0;
+    sh.cnt[1][threadIdx.x] = c0;
+    sh.cnt[2][threadIdx.x] = c0 + c1;
+    sh.cnt[3][threadIdx.x] = c0 + c1 + c2;
+    tot = c0 + c1 + c2 + c3;
+  }
+  uint32_t all;
+  const uint32_t local_start = block_exclusive_scan(tot, sh.scratch, all);
+  if (threadIdx.x < D) {
+    const int d = threadIdx.x;
+    sh.dstart[d] = local_start;
+    uint64_t* mine = status + int64_t(b) * D + d;
+    const bool first = b == chain_first;
+    sweep::store_status(mine, (first ? sweep::kFlagPrefix : sweep::kFlagAggregate) | uint64_t(tot));
+    uint64_t excl = 0;
+    if (!first) {
+      excl = sweep::look_back(status, D, b, d, err);
+      sweep::store_status(mine, sweep::kFlagPrefix | (excl + tot));
+    }
+    sh.gofs[d] = base(d) + uint32_t(excl);
+  }
+  __syncthreads();
+
+#pragma unroll
+  for (int i = 0; i < kItems; ++i) {
+    if (i * 64 + lane < seg_valid) {
+      const uint32_t d = dig[i];
+      const uint32_t pos = sh.dstart[d] + sh.cnt[wid][d] + rank[i];
+      sh.dig[pos] = uint8_t(d);
+#pragma unroll
+      for (int v = 0; v < NV; ++v) sh.val[v * kTile + pos] = val[v][i];
+    }
+  }
+  __syncthreads();
+
+  for (int j = threadIdx.x; j < nvalid; j += kBlock) {
+    const uint32_t d = sh.dig[j];
+    const uint32_t o = sh.gofs[d] + uint32_t(j) - sh.dstart[d];
+    if (o < capacity) {  // always true for tables and lists built by this file
+#pragma unroll
+      for (int v = 0; v < NV; ++v) out[v][o] = sh.val[v * kTile + j];
+    }
+  }
+}
+
+// Pass A: row-list entries [b kTile, b kTile + kTile) of the depth-ordered
+// expansion (Gaussian order[p] owns entries [offs[p], offs[p + 1]), one per
+// covered tile row), bucketed by tile row.  Writes the Gaussian id and
+// first column | width << 16 of every entry to its row-list position.
+template <int BITS>
+__global__ __launch_bounds__(kBlock) void row_bucket_kernel(
+    const int4* __restrict__ bounds, const int32_t* __restrict__ order,
+    const uint32_t* __restrict__ offs, int64_t n, uint32_t entries, int th,
+    const uint32_t* __restrict__ row_a, const int64_t* __restrict__ totals,
+    uint32_t* __restrict__ out_g, uint32_t* __restrict__ out_xw, uint64_t* __restrict__ status,
+    uint32_t* __restrict__ ticket, uint32_t* __restrict__ err) {
+  __shared__ BucketLds<BITS, 2> sh;
+  const int lane = threadIdx.x & 63;
+  const int wid = threadIdx.x >> 6;
+  // Sizes from the host must be the plan's; otherwise every workgroup leaves
+  // (none waits on another) and the error flag is set.
+  if (totals[1] != int64_t(entries) || offs[n] != entries) {
+    if (threadIdx.x == 0) atomicOr(err, 1u);
+    return;
+  }
+  if (threadIdx.x == 0) sh.block = int(atomicAdd(ticket, 1u));
+  for (int d = threadIdx.x; d < 4 * (1 << BITS); d += kBlock) (&sh.cnt[0][0])[d] = 0;
+  __syncthreads();
+  const int b = sh.block;
+  const uint32_t c0 = uint32_t(b) * kTile;
+  const int nvalid = int(min(uint32_t(kTile), entries - c0));
+  if (wid < 2) {
+    const int64_t p = wave_last_le(offs, 0, n - 1, c0 + uint32_t(wid ? nvalid - 1 : 0));
+    if (lane == 0) sh.owner[wid] = p;
+  }
+  __syncthreads();
+  const int64_t p_first = sh.owner[0];
+  // <= kTile: Gaussians without intersections sort last (depth key ~0u), so
+  // every Gaussian of the window owns at least one entry.
+  const int64_t span = sh.owner[1] - p_first + 1;
+  if (span > kTile && threadIdx.x == 0) atomicOr(err, 2u);
+  const int m = int(min(span, int64_t(kTile)));
+  int32_t* rel = reinterpret_cast<int32_t*>(sh.val);
+  for (int k = threadIdx.x; k < m; k += kBlock) rel[k] = int32_t(offs[p_first + k] - c0);
+  __syncthreads();
+
+  find_owners(rel, m, sh.own, sh.scratch);
+
+  uint32_t dig[kItems];
+  uint32_t val[2][kItems];
+#pragma unroll
+  for (int i = 0; i < kItems; ++i) {
+    const int e = wid * kSeg + i * 64 + lane;
+    const int k = sh.own[e];
+    const int g = order[p_first + k];
+    const int4 bb = bounds[g];
+    dig[i] = e < nvalid ? uint32_t(bb.z + (e - rel[k])) & ((1u << BITS) - 1u) : 0u;
+    val[0][i] = uint32_t(g);
+    val[1][i] = uint32_t(bb.x) | (uint32_t(bb.y - bb.x) << 16);
+  }
+  uint32_t* const out[2] = {out_g, out_xw};
+  place_items<BITS, 2>(
+      sh, dig, val, nvalid, b, 0, [&](int d) { return d <= th ? row_a[d] : 0u; }, status, err,
+      out, entries);
+}
+
+// Pass B: workgroup b covers intersections [c0, c0 + kTile) of one tile row
+// (rows own consecutive workgroups from row_blk); row-list entry k of the row
+// owns positions [W[k], W[k] + width) and expands into its columns.  Each
+// intersection is bucketed by column and its Gaussian id stored at
+// ranges[tile].start + rank.
+template <int BITS>
+__global__ __launch_bounds__(kBlock) void column_bucket_kernel(
+    const uint32_t* __restrict__ rl_g, const uint32_t* __restrict__ rl_xw,
+    const uint32_t* __restrict__ W, const uint32_t* __restrict__ row_a,
+    const uint32_t* __restrict__ row_e, const uint32_t* __restrict__ row_blk, int tw, int th,
+    const int64_t* __restrict__ ranges, const int64_t* __restrict__ totals, int64_t total,
+    int64_t entries, int64_t blocks, int32_t* __restrict__ sorted_ids,
+    uint64_t* __restrict__ status, uint32_t* __restrict__ ticket, uint32_t* __restrict__ err) {
+  __shared__ BucketLds<BITS, 1> sh;
+  const int lane = threadIdx.x & 63;
+  const int wid = threadIdx.x >> 6;
+  if (totals[0] != total || totals[1] != entries || totals[2] != blocks) {
+    if (threadIdx.x == 0) atomicOr(err, 1u);
+    return;
+  }
+  if (threadIdx.x == 0) sh.block = int(atomicAdd(ticket, 1u));
+  for (int d = threadIdx.x; d < 4 * (1 << BITS); d += kBlock) (&sh.cnt[0][0])[d] = 0;
+  __syncthreads();
+  const int b = sh.block;
+  if (wid == 0) {
+    // Rows with no workgroup share their start with the next row, so the
+    // largest row whose start is <= b is the one that owns b.
+    const int64_t y = wave_last_le(row_blk, 0, th - 1, uint32_t(b));
+    if (lane == 0) sh.row = int(y);
+  }
+  __syncthreads();
+  const int ty = sh.row;
+  const int rb0 = int(row_blk[ty]);
+  const uint32_t c0 = row_e[ty] + uint32_t(b - rb0) * kTile;
+  const int nvalid = int(min(uint32_t(kTile), row_e[ty + 1] - c0));
+  const int64_t a0 = row_a[ty], a1 = row_a[ty + 1];
+  if (wid < 2) {
+    const int64_t k = wave_last_le(W, a0, a1 - 1, c0 + uint32_t(wid ? nvalid - 1 : 0));
+    if (lane == 0) sh.owner[wid] = k;
+  }
+  __syncthreads();
+  const int64_t k_first = sh.owner[0];
+  const int64_t span = sh.owner[1] - k_first + 1;  // <= kTile: every entry has width >= 1
+  if (span > kTile && threadIdx.x == 0) atomicOr(err, 2u);
+  const int m = int(min(span, int64_t(kTile)));
+  int32_t* rel = reinterpret_cast<int32_t*>(sh.val);
+  for (int k = threadIdx.x; k < m; k += kBlock) rel[k] = int32_t(W[k_first + k] - c0);
+  __syncthreads();
+
+  find_owners(rel, m, sh.own, sh.scratch);
+
+  uint32_t dig[kItems];
+  uint32_t val[1][kItems];
+#pragma unroll
+  for (int i = 0; i < kItems; ++i) {
+    const int e = wid * kSeg + i * 64 + lane;
+    const int k = sh.own[e];
+    const uint32_t xw = rl_xw[k_first + k];
+    dig[i] = e < nvalid ? ((xw & 0xFFFFu) + uint32_t(e - rel[k])) & ((1u << BITS) - 1u) : 0u;
+    val[0][i] = rl_g[k_first + k];
+  }
+  uint32_t* const out[1] = {reinterpret_cast<uint32_t*>(sorted_ids)};
+  const int64_t row_tiles = int64_t(ty) * tw;
+  place_items<BITS, 1>(
+      sh, dig, val, nvalid, b, rb0,
+      [&](int d) { return d < tw ? uint32_t(ranges[2 * (row_tiles + d)]) : 0u; }, status, err,
+      out, uint32_t(total));
+}
+
+template <int BITS>
+void launch_row_bucket(unsigned blocks, const int4* bounds, const int32_t* order,
+                       const uint32_t* offs, int64_t n, uint32_t entries, int th,
+                       const uint32_t* row_a, const int64_t* totals, uint32_t* out_g,
+                       uint32_t* out_xw, uint64_t* status, uint32_t* ticket, uint32_t* err,
+                       hipStream_t s) {
+  row_bucket_kernel<BITS><<<blocks, kBlock, 0, s>>>(bounds, order, offs, n, entries, th, row_a,
+                                                    totals, out_g, out_xw, status, ticket, err);
+}
+
+template <int BITS>
+void launch_column_bucket(unsigned blocks, const uint32_t* rl_g, const uint32_t* rl_xw,
+                          const uint32_t* W, const uint32_t* row_a, const uint32_t* row_e,
+                          const uint32_t* row_blk, int tw, int th, const int64_t* ranges,
+                          const int64_t* totals, int64_t total, int64_t entries, int64_t blocks_b,
+                          int32_t* sorted_ids, uint64_t* status, uint32_t* ticket, uint32_t* err,
+                          hipStream_t s) {
+  column_bucket_kernel<BITS><<<blocks, kBlock, 0, s>>>(rl_g, rl_xw, W, row_a, row_e, row_blk, tw,
+                                                       th, ranges, totals, total, entries,
+                                                       blocks_b, sorted_ids, status, ticket, err);
+}
+
+// Digit width of an axis of `tiles` tiles (at least 1 bit).
+int axis_bits(int tiles) { return std::max(1, bits_for(tiles)); }
+
+// Persistent plan (written by gs_bin_tiles_plan, read by gs_bin_tiles_emit).
+struct PlanLayout {
+  int32_t* order = nullptr;    // [n] depth order
+  uint32_t* offs = nullptr;    // [n + 1] row-list offsets in depth order
+  uint32_t* row_a = nullptr;   // [th + 1]
+  uint32_t* row_e = nullptr;   // [th + 1]
+  uint32_t* row_blk = nullptr;  // [th + 1]
+  int32_t* table = nullptr;    // zeroed: diff2 [(th + 1) (tw + 1)], rowdiff [th + 1]
+  int64_t table_words = 0;     // 64-bit words
+  void* sort_ws = nullptr;     // depth sort + scan scratch
+  size_t bytes = 0;
+};
+
+PlanLayout plan_layout(void* base, int64_t n, int tw, int th) {
+  PlanLayout p;
+  char* c = static_cast<char*>(base);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    char* r = c ? c + off : nullptr;
+    off += align_up(bytes);
+    return r;
+  };
+  p.order = reinterpret_cast<int32_t*>(take(size_t(n) * 4));
+  p.offs = reinterpret_cast<uint32_t*>(take(size_t(n + 1) * 4));
+  p.row_a = reinterpret_cast<uint32_t*>(take(size_t(th + 1) * 4));
+  p.row_e = reinterpret_cast<uint32_t*>(take(size_t(th + 1) * 4));
+  p.row_blk = reinterpret_cast<uint32_t*>(take(size_t(th + 1) * 4));
+  const int64_t table_ints = int64_t(th + 1) * (tw + 1) + (th + 1);
+  p.table_words = (table_ints + 1) / 2;
+  p.table = reinterpret_cast<int32_t*>(take(size_t(p.table_words) * 8));
+  const size_t sort_bytes = carve(nullptr, n, 4, 32, n).bytes;
+  p.sort_ws = take(sort_bytes);
+  p.bytes = off;
+  return p;
+}
+
+// Scratch of gs_bin_tiles_emit.
+struct EmitLayout {
+  uint32_t* rl_g = nullptr;
+  uint32_t* rl_xw = nullptr;
+  uint32_t* W = nullptr;
+  uint64_t* zero = nullptr;  // status A, status B, scan status, then small words
+  int64_t zero_words = 0;
+  uint64_t* status_a = nullptr;
+  uint64_t* status_b = nullptr;
+  uint64_t* scan_status = nullptr;
+  uint32_t* small = nullptr;  // ticket A, ticket B, scan ticket, err A, err B, scan err
+  size_t bytes = 0;
+};
+
+EmitLayout emit_layout(void* base, int64_t entries, int64_t blocks_b, int tw, int th) {
+  EmitLayout e;
+  char* c = static_cast<char*>(base);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    char* r = c ? c + off : nullptr;
+    off += align_up(bytes);
+    return r;
+  };
+  e.rl_g = reinterpret_cast<uint32_t*>(take(size_t(entries) * 4));
+  e.rl_xw = reinterpret_cast<uint32_t*>(take(size_t(entries) * 4));
+  e.W = reinterpret_cast<uint32_t*>(take(size_t(entries) * 4));
+  const int64_t words_a = ceil_div(entries, kTile) << axis_bits(th);
+  const int64_t words_b = blocks_b << axis_bits(tw);
+  const int64_t words_s = ceil_div(entries, kTile);
+  e.zero_words = words_a + words_b + words_s + 4;  // + 8 small 32-bit words
+  e.zero = reinterpret_cast<uint64_t*>(take(size_t(e.zero_words) * 8));
+  if (e.zero) {
+    e.status_a = e.zero;
+    e.status_b = e.status_a + words_a;
+    e.scan_status = e.status_b + words_b;
+    e.small = reinterpret_cast<uint32_t*>(e.scan_status + words_s);
+  }
+  e.bytes = off;
+  return e;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_grid(int tiles_w, int tiles_h) {
+  GS_REQUIRE(tiles_w > 0 && tiles_h > 0, GS_ERR_INVALID_ARGUMENT, "empty tile grid");
+  GS_REQUIRE(tiles_w <= kMaxAxisTiles && tiles_h <= kMaxAxisTiles, GS_ERR_UNSUPPORTED,
+             "row-bucketed binning needs at most %d x %d tiles (got %d x %d)", kMaxAxisTiles,
+             kMaxAxisTiles, tiles_w, tiles_h);
+  return GS_OK;
+}
+
+}  // namespace
+}  // namespace gs
+
+using namespace gs;
+
+extern "C" {
+
+GS_API size_t gs_bin_tiles_plan_bytes(int64_t n, int32_t tiles_w, int32_t tiles_h) {
+  if (n < 0 || tiles_w <= 0 || tiles_h <= 0) return 0;
+  return plan_layout(nullptr, n, tiles_w, tiles_h).bytes;
+}
+
+GS_API int gs_bin_tiles_plan(uint32_t* depth_keys, const int32_t* bounds, const int32_t* counts,
+                             int64_t n, int32_t tiles_w, int32_t tiles_h, int64_t* ranges,
+                             int64_t* totals, void* plan, size_t plan_bytes, void* stream) {
+  clear_error();
+  GS_TRY(check_grid(tiles_w, tiles_h));
+  GS_REQUIRE(n >= 0 && n < (int64_t(1) << 31), GS_ERR_INVALID_ARGUMENT, "invalid Gaussian count");
+  GS_REQUIRE(ranges && totals && plan, GS_ERR_INVALID_ARGUMENT, "null pointer argument");
+  GS_REQUIRE(aligned16(ranges), GS_ERR_INVALID_ARGUMENT, "ranges must be 16-byte aligned");
+  GS_REQUIRE(n == 0 || (depth_keys && bounds && counts && aligned16(bounds)),
+             GS_ERR_INVALID_ARGUMENT, "null or misaligned pointer");
+  const PlanLayout p = plan_layout(plan, n, tiles_w, tiles_h);
+  GS_REQUIRE(plan_bytes >= p.bytes, GS_ERR_WORKSPACE, "plan workspace too small (%zu < %zu)",
+             plan_bytes, p.bytes);
+  hipStream_t s = as_stream(stream);
+  sweep::clear_kernel<<<unsigned(std::max<int64_t>(1, std::min<int64_t>(256, ceil_div(p.table_words, kBlock)))),
+                        kBlock, 0, s>>>(reinterpret_cast<uint64_t*>(p.table), p.table_words,
+                                        nullptr, 0);
+  if (n > 0) {
+    const Scratch ws = carve(p.sort_ws, n, 4, 32, n);
+    clear(ws, s);
+    // depth_keys is consumed (ping-pong buffer of the sort).
+    uint32_t* sorted_keys = nullptr;
+    GS_TRY(radix_sort<uint32_t>(depth_keys, nullptr, n, 32, reinterpret_cast<uint32_t*>(p.order),
+                                &sorted_keys, ws, s));
+    launch_scan<uint32_t>(HeightLoad{reinterpret_cast<const int4*>(bounds), counts, p.order}, n,
+                          p.offs, true, ws, s);
+    const int words = (tiles_h + 1) * (tiles_w + 1);
+    const unsigned blocks = unsigned(std::min<int64_t>(256, std::max<int64_t>(1, ceil_div(n, 8192))));
+    int32_t* diff2 = p.table;
+    int32_t* rowdiff = p.table + words;
+    if (words + tiles_h + 1 <= kPrivateTableWords) {
+      rect_diff_kernel<true><<<blocks, 256, size_t(words + tiles_h + 1) * 4, s>>>(
+          reinterpret_cast<const int4*>(bounds), counts, n, tiles_w, tiles_h, diff2, rowdiff);
+    } else {
+      rect_diff_kernel<false><<<blocks, 256, size_t(tiles_h + 1) * 4, s>>>(
+          reinterpret_cast<const int4*>(bounds), counts, n, tiles_w, tiles_h, diff2, rowdiff);
+    }
+  }
+  const int words = (tiles_h + 1) * (tiles_w + 1);
+  const int lds_words = tiles_h * (tiles_w + 1);
+  if (lds_words <= kPrivateTableWords) {
+    tables_kernel<true><<<1, 256, size_t(lds_words) * 4, s>>>(
+        p.table, p.table + words, tiles_w, tiles_h, ranges, p.row_a, p.row_e, p.row_blk, totals);
+  } else {
+    tables_kernel<false><<<1, 256, 0, s>>>(p.table, p.table + words, tiles_w, tiles_h, ranges,
+                                           p.row_a, p.row_e, p.row_blk, totals);
+  }
+  return check_launch("bin_tiles_plan");
+}
+
+GS_API size_t gs_bin_tiles_emit_bytes(int64_t total, int64_t row_entries, int64_t blocks,
+                                      int32_t tiles_w, int32_t tiles_h) {
+  if (total < 0 || row_entries < 0 || blocks < 0 || tiles_w <= 0 || tiles_h <= 0) return 0;
+  return emit_layout(nullptr, row_entries, blocks, tiles_w, tiles_h).bytes;
+}
+
+GS_API int gs_bin_tiles_emit(const int32_t* bounds, int64_t n, int32_t tiles_w, int32_t tiles_h,
+                             const int64_t* totals, int64_t total, int64_t row_entries,
+                             int64_t blocks, const void* plan, size_t plan_bytes,
+                             const int64_t* ranges, int32_t* sorted_ids, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  clear_error();
+  GS_TRY(check_grid(tiles_w, tiles_h));
+  GS_REQUIRE(n >= 0 && total >= 0 && row_entries >= 0 && blocks >= 0, GS_ERR_INVALID_ARGUMENT,
+             "invalid emit arguments");
+  GS_REQUIRE(total < (int64_t(1) << 32) - kTile && row_entries < (int64_t(1) << 32) - kTile,
+             GS_ERR_OVERFLOW, "too many intersections (%lld)", (long long)total);
+  GS_REQUIRE(blocks >= ceil_div(total, kTile) && blocks <= ceil_div(total, kTile) + tiles_h,
+             GS_ERR_INVALID_ARGUMENT, "inconsistent workgroup count");
+  if (total == 0) return GS_OK;
+  GS_REQUIRE(n > 0 && row_entries > 0 && blocks > 0, GS_ERR_INVALID_ARGUMENT,
+             "intersections without Gaussians");
+  GS_REQUIRE(bounds && totals && plan && ranges && sorted_ids && workspace && aligned16(bounds),
+             GS_ERR_INVALID_ARGUMENT, "null or misaligned pointer");
+  const PlanLayout p = plan_layout(const_cast<void*>(plan), n, tiles_w, tiles_h);
+  GS_REQUIRE(plan_bytes >= p.bytes, GS_ERR_WORKSPACE, "plan workspace too small");
+  const EmitLayout e = emit_layout(workspace, row_entries, blocks, tiles_w, tiles_h);
+  GS_REQUIRE(workspace_bytes >= e.bytes, GS_ERR_WORKSPACE, "emit workspace too small (%zu < %zu)",
+             workspace_bytes, e.bytes);
+  hipStream_t s = as_stream(stream);
+  sweep::clear_kernel<<<unsigned(std::max<int64_t>(1, std::min<int64_t>(1024, ceil_div(e.zero_words, kBlock)))),
+                        kBlock, 0, s>>>(e.zero, e.zero_words, nullptr, 0);
+  uint32_t* ticket_a = e.small;
+  uint32_t* ticket_b = e.small + 1;
+  uint32_t* scan_ticket = e.small + 2;
+  uint32_t* err = e.small + 3;
+  const unsigned blocks_a = unsigned(ceil_div(row_entries, kTile));
+  const int4* b4 = reinterpret_cast<const int4*>(bounds);
+  switch (axis_bits(tiles_h)) {
+#define GS_ROW_CASE(B)                                                                          \
+  case B:                                                                                       \
+    launch_row_bucket<B>(blocks_a, b4, p.order, p.offs, n, uint32_t(row_entries), tiles_h,      \
+                         p.row_a, totals, e.rl_g, e.rl_xw, e.status_a, ticket_a, err, s);       \
+    break;
+    GS_ROW_CASE(1) GS_ROW_CASE(2) GS_ROW_CASE(3) GS_ROW_CASE(4)
+    GS_ROW_CASE(5) GS_ROW_CASE(6) GS_ROW_CASE(7) GS_ROW_CASE(8)
+#undef GS_ROW_CASE
+  }
+  sweep::scan_kernel<uint32_t, WidthLoad><<<blocks_a, sweep::kBlock, 0, s>>>(
+      WidthLoad{e.rl_xw}, row_entries, e.W, false, e.scan_status, scan_ticket, err + 2);
+  switch (axis_bits(tiles_w)) {
+#define GS_COL_CASE(B)                                                                          \
+  case B:                                                                                       \
+    launch_column_bucket<B>(unsigned(blocks), e.rl_g, e.rl_xw, e.W, p.row_a, p.row_e,           \
+                            p.row_blk, tiles_w, tiles_h, ranges, totals, total, row_entries,    \
+                            blocks, sorted_ids, e.status_b, ticket_b, err + 1, s);              \
+    break;
+    GS_COL_CASE(1) GS_COL_CASE(2) GS_COL_CASE(3) GS_COL_CASE(4)
+    GS_COL_CASE(5) GS_COL_CASE(6) GS_COL_CASE(7) GS_COL_CASE(8)
+#undef GS_COL_CASE
+  }
+  return check_launch("bin_tiles_emit");
+}
+
+}  // extern "C"

@@ -5,6 +5,7 @@ from .composite_bwd import composite_bwd
 from .interface import rasterize
 from .intersections import (
     bin_gaussians,
+    bin_tiles,
     emit_intersections,
     emit_tiles,
     sort_intersections,
@@ -15,6 +16,7 @@ from .project_bwd import project_bwd
 
 __all__ = [
     "bin_gaussians",
+    "bin_tiles",
     "composite",
     "composite_bwd",
     "emit_intersections",

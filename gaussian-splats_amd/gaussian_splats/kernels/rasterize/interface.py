@@ -16,7 +16,7 @@ import torch
 from . import _native as nat
 from .composite import composite
 from .composite_bwd import composite_bwd
-from .intersections import bin_gaussians, emit_tiles, sort_tiles
+from .intersections import MAX_BUCKET_TILES, bin_gaussians, bin_tiles, emit_tiles, sort_tiles
 from .project import _check_tile, project_and_count
 from .project_bwd import project_bwd
 
@@ -48,7 +48,9 @@ def forward_pipeline(
     timer=None,
 ) -> tuple[torch.Tensor, ...]:
     """Runs project -> bin -> emit -> sort -> composite; ``timer(name)`` (optional)
-    is called between stages for per-stage event timing."""
+    is called between stages for per-stage event timing (with row/column
+    bucketing, "bin" ends after the plan, "emit" after the row pass and "sort"
+    after the column pass)."""
     _check_tile(tile_size)
     device = nat.require_gpu(mean, rotation, scale, opacity, color)
     n = mean.shape[0]
@@ -66,14 +68,17 @@ def forward_pipeline(
         )
     )
     mark("project")
-    order, offsets = bin_gaussians(depth_keys, counts)
-    mark("bin")
-    # The one device-to-host read of the path: the intersection total sizes the
-    # id buffers (the reference reads counts.sum() at intersections.py:51).
-    total = int(offsets[n].item()) if n else 0
-    tile_keys, ids = emit_tiles(bounds, order, offsets, total, tiles_w)
-    mark("emit")
-    gaussian_ids, ranges = sort_tiles(tile_keys, ids, tiles_w * tiles_h)
+    if tiles_w <= MAX_BUCKET_TILES and tiles_h <= MAX_BUCKET_TILES:
+        gaussian_ids, ranges = bin_tiles(depth_keys, bounds, counts, tiles_w, tiles_h, timer=mark)
+    else:
+        order, offsets = bin_gaussians(depth_keys, counts)
+        mark("bin")
+        # The one device-to-host read of the path: the intersection total sizes
+        # the id buffers (the reference reads counts.sum() at intersections.py:51).
+        total = int(offsets[n].item()) if n else 0
+        tile_keys, ids = emit_tiles(bounds, order, offsets, total, tiles_w)
+        mark("emit")
+        gaussian_ids, ranges = sort_tiles(tile_keys, ids, tiles_w * tiles_h)
     mark("sort")
     image, final_transmittance, n_contributors = composite(
         projected_mean, inverse_covariance, projected_color, projected_opacity, gaussian_ids,

@@ -5,9 +5,11 @@ reference's src/gaussian_splats/kernels/rasterize/intersections.py:44-88
 (64-bit keys ``tile_id << 32 | depth bits`` in Gaussian order, then a sort and
 half-open per-tile ranges), with the sort made stable so depth ties keep
 ascending Gaussian index.  ``bin_gaussians`` / ``emit_tiles`` / ``sort_tiles``
-are the fused variant the op uses: Gaussians are ordered by (depth bits, index)
-once, intersections are emitted in that order with 32-bit tile keys, and a
-stable sort on the tile bits alone yields the same ids and ranges.
+are the fused variant: Gaussians are ordered by (depth bits, index) once,
+intersections are emitted in that order with 32-bit tile keys, and a stable
+sort on the tile bits alone yields the same ids and ranges.  ``bin_tiles`` is
+what the op uses for grids of at most 256 x 256 tiles: the same ids and ranges
+with the row and column buckets filled straight from the tile rectangles.
 """
 
 from __future__ import annotations
@@ -135,4 +137,58 @@ def sort_tiles(
         ),
         "sort_tiles",
     )
+    return sorted_ids, ranges
+
+
+MAX_BUCKET_TILES = 256
+
+
+def bin_tiles(
+    depth_keys: torch.Tensor,
+    bounds: torch.Tensor,
+    counts: torch.Tensor,
+    tiles_w: int,
+    tiles_h: int,
+    timer=None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Sorted Gaussian ids and int64 ranges [T, 2] by row/column bucketing.
+
+    Equivalent to ``bin_gaussians`` + ``emit_tiles`` + ``sort_tiles`` for grids of
+    at most ``MAX_BUCKET_TILES`` tiles per axis; ``depth_keys`` is consumed.
+    ``timer(name)`` (optional) marks the end of the plan ("bin") and of the
+    bucketing passes ("emit").
+    """
+    mark = timer or (lambda name: None)
+    device = nat.require_gpu(depth_keys, bounds, counts)
+    n = counts.shape[0]
+    lib = nat.library()
+    s = nat.stream(device)
+    plan = nat.workspace(lib.gs_bin_tiles_plan_bytes(n, tiles_w, tiles_h), device)
+    ranges = torch.empty((tiles_w * tiles_h, 2), dtype=torch.int64, device=device)
+    totals = torch.empty(4, dtype=torch.int64, device=device)
+    nat.check(
+        lib.gs_bin_tiles_plan(
+            nat.ptr(depth_keys), nat.ptr(bounds), nat.ptr(counts), n, tiles_w, tiles_h,
+            nat.ptr(ranges), nat.ptr(totals), nat.ptr(plan), plan.numel(), s,
+        ),
+        "bin_tiles_plan",
+    )
+    mark("bin")
+    # The one device-to-host read of the path: the totals size the id buffer
+    # (the reference reads counts.sum() at intersections.py:51).
+    total, row_entries, blocks, _ = totals.tolist()
+    sorted_ids = torch.empty(total, dtype=torch.int32, device=device)
+    if total:
+        ws = nat.workspace(
+            lib.gs_bin_tiles_emit_bytes(total, row_entries, blocks, tiles_w, tiles_h), device
+        )
+        nat.check(
+            lib.gs_bin_tiles_emit(
+                nat.ptr(bounds), n, tiles_w, tiles_h, nat.ptr(totals), total, row_entries, blocks,
+                nat.ptr(plan), plan.numel(), nat.ptr(ranges), nat.ptr(sorted_ids), nat.ptr(ws),
+                ws.numel(), s,
+            ),
+            "bin_tiles_emit",
+        )
+    mark("emit")
     return sorted_ids, ranges

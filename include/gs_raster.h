@@ -162,6 +162,34 @@ GS_API int gs_sort_tiles(
     int32_t num_tiles, int32_t* sorted_ids, int64_t* ranges,
     void* workspace, size_t workspace_bytes, void* stream);
 
+/* Row-bucketed binning, used by the op when the tile grid is at most
+ * 256 x 256 (otherwise GS_ERR_UNSUPPORTED; use the three calls above).  Same
+ * sorted ids and ranges as gs_bin_gaussians + gs_emit_tiles + gs_sort_tiles,
+ * i.e. the stable (tile, depth bits, index) order of intersections.py:10-88,
+ * with the tile-row and tile-column buckets filled directly from the tile
+ * rectangles (no intersection keys are materialised or sorted).
+ *
+ * gs_bin_tiles_plan: depth order, per-tile counts and `ranges` [T, 2] (final),
+ * and device `totals` = {intersections, row-list entries, pass-B workgroups,
+ * 0}, which the caller reads back to size the ids; `plan` (plan_bytes from
+ * gs_bin_tiles_plan_bytes) must stay alive until gs_bin_tiles_emit, which
+ * takes the same totals (device pointer and the values read from it) and
+ * writes `sorted_ids` [totals[0]].  depth_keys (as gs_project_and_count
+ * writes them: ~0u for Gaussians without intersections) is consumed.  Together they
+ * replace intersections.py:44-88 for the op. */
+GS_API size_t gs_bin_tiles_plan_bytes(int64_t n, int32_t tiles_w, int32_t tiles_h);
+GS_API int gs_bin_tiles_plan(
+    uint32_t* depth_keys, const int32_t* bounds, const int32_t* counts, int64_t n,
+    int32_t tiles_w, int32_t tiles_h, int64_t* ranges, int64_t* totals,
+    void* plan, size_t plan_bytes, void* stream);
+GS_API size_t gs_bin_tiles_emit_bytes(int64_t total, int64_t row_entries, int64_t blocks,
+                                      int32_t tiles_w, int32_t tiles_h);
+GS_API int gs_bin_tiles_emit(
+    const int32_t* bounds, int64_t n, int32_t tiles_w, int32_t tiles_h,
+    const int64_t* totals, int64_t total, int64_t row_entries, int64_t blocks,
+    const void* plan, size_t plan_bytes, const int64_t* ranges, int32_t* sorted_ids,
+    void* workspace, size_t workspace_bytes, void* stream);
+
 /* Front-to-back compositing per tile.  Replaces composite
  * (src/gaussian_splats/kernels/rasterize/composite.py:25-162) with the
  * pixel semantics of torch.py:172-225.  tile_size in {4, 8, 16, 32}. */

@@ -38,6 +38,30 @@ def test_workspace_queries_are_host_only():
     assert lib.gs_bin_workspace_bytes(1000) > lib.gs_bin_workspace_bytes(10)
 
 
+def test_bucketed_binning_host_checks():
+    """Row/column bucketing: grid limits, sizes and inconsistent totals are
+    rejected on the host before any launch."""
+    lib = nat.library()
+    fake = ctypes.c_void_p(16)
+    assert lib.gs_bin_tiles_plan_bytes(1000, 120, 68) > lib.gs_bin_tiles_plan_bytes(10, 120, 68)
+    assert lib.gs_bin_tiles_plan_bytes(-1, 120, 68) == 0
+    assert lib.gs_bin_tiles_emit_bytes(1 << 20, 1 << 18, 300, 120, 68) >= 3 * 4 * (1 << 18)
+    status = lib.gs_bin_tiles_plan(fake, fake, fake, 10, 257, 4, fake, fake, fake, 1 << 20, None)
+    assert status == nat.GS_ERR_UNSUPPORTED
+    assert b"at most 256" in lib.gs_last_error()
+    status = lib.gs_bin_tiles_plan(fake, fake, fake, 10, 120, 68, fake, fake, fake, 16, None)
+    assert status == nat.GS_ERR_WORKSPACE
+    # pass-B workgroups must match the intersection total (ceil(total / 4096) .. + rows)
+    status = lib.gs_bin_tiles_emit(
+        fake, 10, 120, 68, fake, 100000, 5000, 1, fake, 1 << 30, fake, fake, fake, 1 << 30, None
+    )
+    assert status == nat.GS_ERR_INVALID_ARGUMENT
+    status = lib.gs_bin_tiles_emit(
+        fake, 10, 120, 68, fake, 1 << 33, 5000, 1 << 22, fake, 1 << 30, fake, fake, fake, 1 << 30, None
+    )
+    assert status == nat.GS_ERR_OVERFLOW
+
+
 def _view(**kw):
     args = dict(fx=100.0, fy=100.0, cx=50.0, cy=50.0, image_width=100, image_height=100, tile_size=16)
     args.update(kw)

@@ -13,6 +13,7 @@ import torch
 from gaussian_splats import scenes
 from gaussian_splats.kernels.rasterize import (
     bin_gaussians,
+    bin_tiles,
     composite,
     emit_intersections,
     emit_tiles,
@@ -137,6 +138,79 @@ def test_intersections_bit_exact(device, shape):
     for s, e in r[:50]:
         seg = sid_o[s:e]
         assert np.all((d[seg][:-1] < d[seg][1:]) | ((d[seg][:-1] == d[seg][1:]) & (seg[:-1] < seg[1:])))
+
+
+def _depth_keys(depths, counts):
+    dkeys = depths.view(torch.int32).clone()
+    dkeys[counts == 0] = -1
+    return dkeys
+
+
+@pytest.mark.parametrize(
+    "shape,n",
+    (
+        ((24, 17), 4096),
+        ((120, 68), 4096),
+        ((256, 256), 768),
+        ((1, 1), 4096),
+        ((37, 1), 4096),
+        ((1, 37), 4096),
+        ((256, 2), 4096),
+        ((3, 200), 4096),
+    ),
+)
+def test_bucketed_binning_bit_exact(device, shape, n):
+    """Row/column bucketing (the op's path) against the oracle's stable sort."""
+    tiles_w, tiles_h = shape
+    bounds, depths, counts = _random_rects(n=n, tiles_w=tiles_w, tiles_h=tiles_h, seed=7)
+    keys_o, ids_o = orc.emit_intersections(bounds.numpy(), depths.numpy(), counts.numpy(), tiles_w)
+    sid_o, ranges_o, _ = orc.sort_intersections(keys_o, ids_o, tiles_w * tiles_h)
+    print(f"bucketed binning {shape} n={n} intersections={len(sid_o)}", flush=True)
+    sid, ranges = bin_tiles(
+        _depth_keys(depths, counts).to(device), bounds.to(device), counts.to(device), tiles_w, tiles_h
+    )
+    assert np.array_equal(ranges.cpu().numpy(), ranges_o)
+    assert np.array_equal(sid.cpu().numpy(), sid_o)
+
+
+def test_bucketed_binning_long_rows(device):
+    """Rows holding many workgroups of intersections (full-width rectangles)
+    and Gaussians spanning many rows, so both passes chain look-backs across
+    several workgroups of one digit."""
+    g = torch.Generator().manual_seed(11)
+    n, tiles_w, tiles_h = 3000, 200, 40
+    x0 = torch.randint(0, 20, (n,), generator=g)
+    x1 = torch.randint(180, tiles_w + 1, (n,), generator=g)
+    y0 = torch.randint(0, tiles_h, (n,), generator=g)
+    y1 = torch.minimum(y0 + torch.randint(1, 30, (n,), generator=g), torch.tensor(tiles_h))
+    bounds = torch.stack((torch.stack((x0, x1), -1), torch.stack((y0, y1), -1)), 1).int()
+    depths = (torch.rand(n, generator=g) * 4).round() + 1.0  # many exact ties
+    counts = ((x1 - x0) * (y1 - y0)).int()
+    keys_o, ids_o = orc.emit_intersections(bounds.numpy(), depths.numpy(), counts.numpy(), tiles_w)
+    sid_o, ranges_o, _ = orc.sort_intersections(keys_o, ids_o, tiles_w * tiles_h)
+    print(f"long rows intersections={len(sid_o)}", flush=True)
+    sid, ranges = bin_tiles(
+        _depth_keys(depths, counts).to(device), bounds.to(device), counts.to(device), tiles_w, tiles_h
+    )
+    assert np.array_equal(ranges.cpu().numpy(), ranges_o)
+    assert np.array_equal(sid.cpu().numpy(), sid_o)
+
+
+def test_bucketed_binning_empty_and_deterministic(device):
+    bounds = torch.zeros(5, 2, 2, dtype=torch.int32, device=device)
+    counts = torch.zeros(5, dtype=torch.int32, device=device)
+    sid, ranges = bin_tiles(torch.full((5,), -1, dtype=torch.int32, device=device), bounds, counts, 4, 3)
+    assert sid.numel() == 0 and torch.equal(ranges.cpu(), torch.zeros(12, 2, dtype=torch.int64))
+    sid, ranges = bin_tiles(
+        torch.empty(0, dtype=torch.int32, device=device), bounds[:0], counts[:0], 4, 3
+    )
+    assert sid.numel() == 0 and torch.equal(ranges.cpu(), torch.zeros(12, 2, dtype=torch.int64))
+    b, d, c = _random_rects(n=20000, tiles_w=120, tiles_h=68, seed=3)
+    outs = [
+        [t.cpu() for t in bin_tiles(_depth_keys(d, c).to(device), b.to(device), c.to(device), 120, 68)]
+        for _ in range(2)
+    ]
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
 
 
 def test_intersections_empty(device):

@@ -195,7 +195,8 @@ GS_API int gs_scan_counts(const int32_t* counts, int64_t n, int64_t* offsets, vo
   const Scratch ws = carve(workspace, 0, 4, -1, n);
   GS_REQUIRE(workspace && workspace_bytes >= ws.bytes, GS_ERR_WORKSPACE, "scan workspace too small");
   clear(ws, s);
-  launch_scan<int64_t>(sweep::GatherLoad<int32_t, int64_t>{counts, nullptr}, n, offsets, true, ws, s);
+  launch_scan<int64_t>(sweep::GatherLoad<int32_t, int64_t>{counts, nullptr}, n, offsets, true,
+                       aligned_16(counts), ws, s);
   return check_launch("scan_counts");
 }
 
@@ -268,7 +269,8 @@ GS_API int gs_bin_gaussians(uint32_t* depth_keys, const int32_t* counts, int64_t
   uint32_t* sorted_keys = nullptr;
   GS_TRY(radix_sort<uint32_t>(depth_keys, nullptr, n, 32, reinterpret_cast<uint32_t*>(order),
                               &sorted_keys, ws, s));
-  launch_scan<int64_t>(sweep::GatherLoad<int32_t, int64_t>{counts, order}, n, offsets, true, ws, s);
+  launch_scan<int64_t>(sweep::GatherLoad<int32_t, int64_t>{counts, order}, n, offsets, true,
+                       aligned_16(order), ws, s);
   return check_launch("bin_gaussians");
 }
 

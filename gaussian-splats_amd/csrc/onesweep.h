@@ -298,39 +298,110 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
   }
 }
 
-// value(i) = in[order ? order[i] : i], widened to Out.
+// value(i) = in[order ? order[i] : i], widened to Out.  load4 reads the four
+// values at i (a multiple of 4) with one 16-byte load of `order` or `in`.
 template <typename In, typename Out>
 struct GatherLoad {
   const In* in;
   const int32_t* order;
   __device__ Out operator()(int64_t i) const { return Out(in[order ? order[i] : i]); }
+  __device__ void load4(int64_t i, Out (&v)[4]) const {
+    if (order) {
+      const int4 o = *reinterpret_cast<const int4*>(order + i);
+      v[0] = Out(in[o.x]);
+      v[1] = Out(in[o.y]);
+      v[2] = Out(in[o.z]);
+      v[3] = Out(in[o.w]);
+    } else {
+      static_assert(sizeof(In) == 4, "vector path reads four 32-bit values");
+      const int4 q = *reinterpret_cast<const int4*>(in + i);
+      v[0] = Out(In(q.x));
+      v[1] = Out(In(q.y));
+      v[2] = Out(In(q.z));
+      v[3] = Out(In(q.w));
+    }
+  }
 };
 
+__device__ __forceinline__ void store4(uint32_t* p, const uint32_t (&v)[4]) {
+  *reinterpret_cast<uint4*>(p) = make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ void store4(int64_t* p, const int64_t (&v)[4]) {
+  reinterpret_cast<longlong2*>(p)[0] = make_longlong2(v[0], v[1]);
+  reinterpret_cast<longlong2*>(p)[1] = make_longlong2(v[2], v[3]);
+}
+
+// Per-element hook of scan_kernel: sink(i, exclusive prefix, value).
+struct NoSink {
+  template <typename Out>
+  __device__ void operator()(int64_t, Out, Out) const {}
+};
+
+template <typename T>
+__device__ __forceinline__ T from_lane63(T v) {
+  if constexpr (sizeof(T) == 4) {
+    return T(__builtin_amdgcn_readlane(int(v), 63));
+  } else {
+    return __shfl(v, 63, 64);
+  }
+}
+
 // Exclusive scan of load(i) into out[0..n), and out[n] = total when
-// write_total; one kernel, kTile elements per workgroup.
-template <typename Out, typename Load>
+// write_total; one kernel, kTile elements per workgroup.  Accesses are fully
+// coalesced: lane l of wave w handles the four-element groups
+// w * 256 + i * 64 + l (i < 4) of the tile, read and written with 16-byte
+// accesses when `vec` (load.load4 and out are 16-byte aligned); four wave
+// scans order the groups, one LDS exchange orders the waves, and a wave-wide
+// look-back gives the tile's offset.  sink(i, out[i], value i) is called for
+// every element.
+template <typename Out, typename Load, typename Sink = NoSink>
 __global__ __launch_bounds__(kBlock) void scan_kernel(Load load, int64_t n, Out* __restrict__ out,
-                                                      bool write_total,
+                                                      bool write_total, bool vec,
                                                       uint64_t* __restrict__ status,
                                                       uint32_t* __restrict__ ticket,
-                                                      uint32_t* __restrict__ err) {
-  __shared__ Out scratch[4];
+                                                      uint32_t* __restrict__ err,
+                                                      Sink sink = Sink{}) {
+  static_assert(kTile == 4 * 4 * kBlock, "16 elements per thread in groups of four");
+  __shared__ Out wave_total[4];
   __shared__ Out s_excl;
   __shared__ int s_block;
   if (threadIdx.x == 0) s_block = int(atomicAdd(ticket, 1u));
   __syncthreads();
   const int b = s_block;
-  const int64_t first = int64_t(b) * kTile + int64_t(threadIdx.x) * kItems;
-  Out v[kItems];
-  Out sum = 0;
+  const int lane = threadIdx.x & 63;
+  const int wid = threadIdx.x >> 6;
+  const int64_t base = int64_t(b) * kTile;
+  Out v[4][4];
+  Out group_sum[4];
 #pragma unroll
-  for (int i = 0; i < kItems; ++i) {
-    const int64_t idx = first + i;
-    v[i] = idx < n ? load(idx) : Out(0);
-    sum += v[i];
+  for (int i = 0; i < 4; ++i) {
+    const int64_t e = base + 4 * (wid * 256 + i * 64 + lane);
+    if (vec && e + 4 <= n) {
+      load.load4(e, v[i]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[i][j] = e + j < n ? load(e + j) : Out(0);
+    }
+    group_sum[i] = v[i][0] + v[i][1] + v[i][2] + v[i][3];
   }
-  Out total;
-  const Out pre = block_exclusive_scan(sum, scratch, total);
+  // Exclusive prefix of each group inside the wave's 1024 elements.
+  Out carry = 0;
+  Out group_pre[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const Out inc = wave_inclusive_scan(group_sum[i]);
+    group_pre[i] = carry + inc - group_sum[i];
+    carry += from_lane63(inc);
+  }
+  if (lane == 0) wave_total[wid] = carry;
+  __syncthreads();
+  Out before = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const Out t = wave_total[w];
+    if (w < wid) before += t;
+    total += t;
+  }
   if (threadIdx.x < 64) {
     if (threadIdx.x == 0)
       store_status(status + b, (b == 0 ? kFlagPrefix : kFlagAggregate) | uint64_t(total));
@@ -342,12 +413,25 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(Load load, int64_t n, Out*
     }
   }
   __syncthreads();
-  Out run = s_excl + pre;
+  const Out offset = s_excl + before;
 #pragma unroll
-  for (int i = 0; i < kItems; ++i) {
-    const int64_t idx = first + i;
-    if (idx < n) out[idx] = run;
-    run += v[i];
+  for (int i = 0; i < 4; ++i) {
+    const int64_t e = base + 4 * (wid * 256 + i * 64 + lane);
+    Out r[4];
+    r[0] = offset + group_pre[i];
+    r[1] = r[0] + v[i][0];
+    r[2] = r[1] + v[i][1];
+    r[3] = r[2] + v[i][2];
+    if (vec && e + 4 <= n) {
+      store4(out + e, r);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (e + j < n) out[e + j] = r[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (e + j < n) sink(e + j, r[j], v[i][j]);
   }
 }
 

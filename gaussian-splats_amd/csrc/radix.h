@@ -137,12 +137,16 @@ int radix_sort(K* keys, const uint32_t* vals, int64_t n, int end_bit, uint32_t* 
   return check_launch("radix_sort");
 }
 
-template <typename Out, typename Load>
-void launch_scan(Load load, int64_t n, Out* out, bool write_total, const Scratch& ws,
-                 hipStream_t s) {
-  sweep::scan_kernel<Out, Load><<<unsigned(ceil_div(n, kTile)), sweep::kBlock, 0, s>>>(
-      load, n, out, write_total, ws.scan_status, ws.scan_ticket(), ws.scan_err());
+// `vec`: the loader's 16-byte reads and `out` are 16-byte aligned.
+template <typename Out, typename Load, typename Sink = sweep::NoSink>
+void launch_scan(Load load, int64_t n, Out* out, bool write_total, bool vec, const Scratch& ws,
+                 hipStream_t s, Sink sink = Sink{}) {
+  vec = vec && (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
+  sweep::scan_kernel<Out, Load, Sink><<<unsigned(ceil_div(n, kTile)), sweep::kBlock, 0, s>>>(
+      load, n, out, write_total, vec, ws.scan_status, ws.scan_ticket(), ws.scan_err(), sink);
 }
+
+inline bool aligned_16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 template <typename T>
 __global__ void fill_kernel(T* p, int64_t n, T value) {

@@ -62,20 +62,33 @@ __global__ __launch_bounds__(256) void rect_diff_kernel(const int4* __restrict__
     for (int i = threadIdx.x; i < words; i += 256) t2[i] = 0;
   for (int i = threadIdx.x; i <= th; i += 256) tr[i] = 0;
   __syncthreads();
+  // Eight Gaussians per thread are loaded before their atomics are issued.
+  constexpr int kBatch = 8;
   const int64_t stride = int64_t(gridDim.x) * 256;
-  for (int64_t g = int64_t(blockIdx.x) * 256 + threadIdx.x; g < n; g += stride) {
-    if (counts[g] > 0) {
-      // x0, x1, y0, y1 (already inside the grid when they come from the
-      // projection; clamped so that no other input indexes out of the tables)
-      const int4 b = bounds[g];
-      const int x0 = min(max(b.x, 0), tw), x1 = min(max(b.y, 0), tw);
-      const int y0 = min(max(b.z, 0), th), y1 = min(max(b.w, 0), th);
-      atomicAdd(&t2[y0 * pitch + x0], 1);
-      atomicAdd(&t2[y0 * pitch + x1], -1);
-      atomicAdd(&t2[y1 * pitch + x0], -1);
-      atomicAdd(&t2[y1 * pitch + x1], 1);
-      atomicAdd(&tr[y0], 1);
-      atomicAdd(&tr[y1], -1);
+  for (int64_t g0 = int64_t(blockIdx.x) * 256 + threadIdx.x; g0 < n; g0 += kBatch * stride) {
+    int cnt[kBatch];
+    int4 rect[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int64_t g = g0 + i * stride;
+      cnt[i] = g < n ? counts[g] : 0;
+      rect[i] = g < n ? bounds[g] : make_int4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      if (cnt[i] > 0) {
+        // x0, x1, y0, y1 (inside the grid when they come from the projection;
+        // clamped so that no other input indexes out of the tables)
+        const int4 b = rect[i];
+        const int x0 = min(max(b.x, 0), tw), x1 = min(max(b.y, 0), tw);
+        const int y0 = min(max(b.z, 0), th), y1 = min(max(b.w, 0), th);
+        atomicAdd(&t2[y0 * pitch + x0], 1);
+        atomicAdd(&t2[y0 * pitch + x1], -1);
+        atomicAdd(&t2[y1 * pitch + x0], -1);
+        atomicAdd(&t2[y1 * pitch + x1], 1);
+        atomicAdd(&tr[y0], 1);
+        atomicAdd(&tr[y1], -1);
+      }
     }
   }
   __syncthreads();
@@ -130,20 +143,23 @@ __global__ __launch_bounds__(256) void tables_kernel(int32_t* __restrict__ diff2
   }
   __syncthreads();
 
-  // 2. One wave per row: count(x, y) = prefix over x of the column prefixes
-  // (stored in place), row total into s_row.
+  // 2. One wave per row: count(x, y) = prefix over x of the column prefixes;
+  // the exclusive prefix of the counts along the row (the tile's start in
+  // its row) is stored in place and the row total in s_row.  32-bit: the
+  // host requires fewer than 2^32 intersections.
   for (int y = wid; y < th; y += 4) {
-    int32_t carry = 0;
-    int64_t row_total = 0;
+    uint32_t carry = 0, start = 0;
     for (int x0 = 0; x0 < tw; x0 += 64) {
       const int x = x0 + lane;
-      const int32_t v = x < tw ? tab[y * pitch + x] : 0;
-      const int32_t c = carry + wave_inclusive_scan(v);
-      if (x < tw) tab[y * pitch + x] = c;
-      row_total += wave_sum(int64_t(x < tw ? c : 0));
+      const uint32_t v = x < tw ? uint32_t(tab[y * pitch + x]) : 0u;
+      const uint32_t c = carry + wave_inclusive_scan(v);
+      const uint32_t cnt = x < tw ? c : 0u;
+      const uint32_t inc = start + wave_inclusive_scan(cnt);
+      if (x < tw) tab[y * pitch + x] = int32_t(inc - cnt);
       carry = __shfl(c, 63, 64);
+      start = __shfl(inc, 63, 64);
     }
-    if (lane == 0) s_row[y] = row_total;
+    if (lane == 0) s_row[y] = start;
   }
   __syncthreads();
 
@@ -163,6 +179,8 @@ __global__ __launch_bounds__(256) void tables_kernel(int32_t* __restrict__ diff2
     row_blk[y] = uint32_t(b_start);
     s_row[y] = e_start;
   }
+  __shared__ int64_t s_end[kMaxAxisTiles];
+  if (y < th) s_end[y] = e_start + row_entries;
   if (threadIdx.x == 0) {
     row_e[th] = uint32_t(tot_e);
     row_a[th] = uint32_t(tot_a);
@@ -174,40 +192,106 @@ __global__ __launch_bounds__(256) void tables_kernel(int32_t* __restrict__ diff2
   }
   __syncthreads();
 
-  // 4. Ranges: row start + exclusive prefix of the counts along the row.
-  for (int y2 = wid; y2 < th; y2 += 4) {
-    int64_t carry = s_row[y2];
-    for (int x0 = 0; x0 < tw; x0 += 64) {
-      const int x = x0 + lane;
-      const int64_t cnt = x < tw ? int64_t(tab[y2 * pitch + x]) : 0;
-      const int64_t inc = carry + wave_inclusive_scan(cnt);
-      if (x < tw) {
-        const int64_t t = int64_t(y2) * tw + x;
-        reinterpret_cast<longlong2*>(ranges)[t] = make_longlong2(inc - cnt, inc);
-      }
-      carry = __shfl(inc, 63, 64);
-    }
+  // 4. Ranges: row start + start in the row; a tile ends where the next tile
+  // of its row starts (the last one at the row's end).
+  const int64_t num_tiles = int64_t(tw) * th;
+  for (int64_t t = threadIdx.x; t < num_tiles; t += 256) {
+    const int ty = int(t / tw), tx = int(t - int64_t(ty) * tw);
+    const int64_t begin = s_row[ty] + uint32_t(tab[ty * pitch + tx]);
+    const int64_t end = tx + 1 < tw ? s_row[ty] + uint32_t(tab[ty * pitch + tx + 1]) : s_end[ty];
+    reinterpret_cast<longlong2*>(ranges)[t] = make_longlong2(begin, end);
   }
 }
 
-// Row-list entries per Gaussian in depth order: its tile-row count, 0 if
-// it has no intersections.
+// Row-list entry packing: first column | (width - 1) << 8 | row << 16 (grids
+// of at most 256 x 256 tiles).
+__device__ __forceinline__ uint32_t pack_entry(int x0, int width, int row) {
+  return uint32_t(x0) | (uint32_t(width - 1) << 8) | (uint32_t(row) << 16);
+}
+__device__ __forceinline__ uint32_t entry_x0(uint32_t xw) { return xw & 0xFFu; }
+__device__ __forceinline__ uint32_t entry_width(uint32_t xw) { return ((xw >> 8) & 0xFFu) + 1u; }
+__device__ __forceinline__ uint32_t entry_row(uint32_t xw) { return (xw >> 16) & 0xFFu; }
+
+// Row-list entries per Gaussian in depth order: its tile-row count, 0 if it
+// has no intersections.
 struct HeightLoad {
   const int4* bounds;
   const int32_t* counts;
   const int32_t* order;
-  __device__ uint32_t operator()(int64_t i) const {
-    const int g = order[i];
+  __device__ uint32_t height(int g) const {
     if (counts[g] <= 0) return 0u;
     const int4 b = bounds[g];
     return uint32_t(b.w - b.z);
   }
+  __device__ uint32_t operator()(int64_t i) const { return height(order[i]); }
+  __device__ void load4(int64_t i, uint32_t (&v)[4]) const {
+    const int4 o = *reinterpret_cast<const int4*>(order + i);
+    v[0] = height(o.x);
+    v[1] = height(o.y);
+    v[2] = height(o.z);
+    v[3] = height(o.w);
+  }
 };
 
-// Width field of a packed row-list entry (first column | width << 16).
+// Pass-A workgroup j starts at row-list position j kTile; the Gaussian (depth
+// position p) whose entries [s, s + h) contain it is recorded as
+// first_a[j] = p | (starts exactly there) << 31.  h < kTile, so an entry
+// range holds at most one such position.
+struct HeightSink {
+  uint32_t* first_a;
+  uint32_t capacity;  // pass-A workgroups
+  __device__ void operator()(int64_t p, uint32_t s, uint32_t h) const {
+    if (h == 0) return;
+    const uint32_t j = (s + kTile - 1) / kTile;
+    const uint32_t start = j * kTile;
+    if (start < s + h && j < capacity)
+      first_a[j] = uint32_t(p) | (start == s ? 0x80000000u : 0u);
+  }
+};
+
+// Width of a packed row-list entry.
 struct WidthLoad {
   const uint32_t* xw;
-  __device__ uint32_t operator()(int64_t i) const { return xw[i] >> 16; }
+  __device__ uint32_t operator()(int64_t i) const { return entry_width(xw[i]); }
+  __device__ void load4(int64_t i, uint32_t (&v)[4]) const {
+    const uint4 q = *reinterpret_cast<const uint4*>(xw + i);
+    v[0] = entry_width(q.x);
+    v[1] = entry_width(q.y);
+    v[2] = entry_width(q.z);
+    v[3] = entry_width(q.w);
+  }
+};
+
+// Pass-B workgroup metadata: the rows' intersections [row_e[y], row_e[y+1])
+// are cut into workgroups of kTile starting at row_blk[y]; the row-list entry
+// k whose intersections [W[k], W[k] + width) contain a workgroup's first
+// position records
+//   info[b] = {k | (starts exactly there) << 31, first position,
+//              row | item count << 8 | (first of its row) << 31,
+//              last row-list entry of the row}.
+struct WidthSink {
+  const uint32_t* xw;
+  const uint32_t* row_e;
+  const uint32_t* row_a;
+  const uint32_t* row_blk;
+  uint4* info;
+  uint32_t rows;      // tile rows
+  uint32_t capacity;  // pass-B workgroups
+  __device__ void operator()(int64_t k, uint32_t s, uint32_t w) const {
+    const uint32_t y = entry_row(xw[k]);
+    if (y >= rows) return;
+    const uint32_t e0 = row_e[y];
+    const uint32_t rel = s - e0;
+    const uint32_t j = (rel + kTile - 1) / kTile;
+    const uint32_t start = j * kTile;
+    if (start < rel + w && row_blk[y] + j < capacity) {
+      const uint32_t c0 = e0 + start;
+      const uint32_t count = min(uint32_t(kTile), row_e[y + 1] - c0);
+      info[row_blk[y] + j] = make_uint4(uint32_t(k) | (start == rel ? 0x80000000u : 0u), c0,
+                                        y | (count << 8) | (j == 0 ? 0x80000000u : 0u),
+                                        row_a[y + 1] - 1u);
+    }
+  }
 };
 
 // ---------------------------------------------------------------------------
@@ -241,9 +325,9 @@ struct BucketLds {
   uint32_t dstart[1 << BITS];
   uint32_t gofs[1 << BITS];
   uint32_t scratch[4];
-  int64_t owner[2];
+  int64_t window[2];  // first and last owner of the workgroup's items
+  uint32_t c0, nvalid, row, chain_start;
   int block;
-  int row;
   uint8_t dig[kTile];
   alignas(16) uint16_t own[kTile];  // owner (window index) of every position
   // Owner window (int32 offsets relative to the first item) while items are
@@ -279,15 +363,9 @@ __device__ void find_owners(const int32_t* rel, int m, uint16_t* own, uint32_t* 
   // Exclusive max over the threads before this one.
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
-  uint32_t inc = run;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t t = __shfl_up(inc, o, 64);
-    if (lane >= o) inc = max(inc, t);
-  }
+  const uint32_t inc = wave_inclusive_dpp(run, MaxOp{});
   if (lane == 63) scratch[wid] = inc;
-  uint32_t before = __shfl_up(inc, 1, 64);
-  if (lane == 0) before = 0;
+  uint32_t before = dpp_read<0x138, 0xF, true>(inc);  // wave_shr:1, lane 0 reads 0
   __syncthreads();
   for (int v = 0; v < wid; ++v) before = max(before, scratch[v]);
 #pragma unroll
@@ -302,15 +380,15 @@ __device__ void find_owners(const int32_t* rel, int m, uint16_t* own, uint32_t* 
 }
 
 // Ranks the workgroup's items by digit, finds each digit's offset among the
-// items of the earlier workgroups of the chain (chain_first .. b - 1) by
-// look-back, and stores the NV values of every item at
+// items of the earlier workgroups of its chain by look-back (a chain starts at
+// a workgroup with chain_start), and stores the NV values of every item at
 // base(d) + offset(d) + rank (below `capacity`).  Items at
 // i * 64 + lane < seg_valid of each wave's segment are valid; digits are
 // below 2^BITS.
 template <int BITS, int NV, typename Base>
 __device__ void place_items(BucketLds<BITS, NV>& sh, const uint32_t (&dig)[kItems],
                             const uint32_t (&val)[NV][kItems], int nvalid, int b,
-                            int chain_first, Base base, uint64_t* __restrict__ status,
+                            bool chain_start, Base base, uint64_t* __restrict__ status,
                             uint32_t* __restrict__ err, uint32_t* const (&out)[NV],
                             uint32_t capacity) {
   constexpr int D = 1 << BITS;
@@ -340,10 +418,10 @@ __device__ void place_items(BucketLds<BITS, NV>& sh, const uint32_t (&dig)[kItem
     const int d = threadIdx.x;
     sh.dstart[d] = local_start;
     uint64_t* mine = status + int64_t(b) * D + d;
-    const bool first = b == chain_first;
-    sweep::store_status(mine, (first ? sweep::kFlagPrefix : sweep::kFlagAggregate) | uint64_t(tot));
+    sweep::store_status(mine,
+                        (chain_start ? sweep::kFlagPrefix : sweep::kFlagAggregate) | uint64_t(tot));
     uint64_t excl = 0;
-    if (!first) {
+    if (!chain_start) {
       excl = sweep::look_back(status, D, b, d, err);
       sweep::store_status(mine, sweep::kFlagPrefix | (excl + tot));
     }
@@ -373,17 +451,35 @@ __device__ void place_items(BucketLds<BITS, NV>& sh, const uint32_t (&dig)[kItem
   }
 }
 
+// Loads the owner window [first, last] of a workgroup: rel[k] = start of
+// owner first + k minus the workgroup's first position.  The span is at most
+// kTile because every owner covers at least one position (Gaussians without
+// intersections sort last, entries have width >= 1); a larger one, only
+// possible from inconsistent inputs, is clamped and flagged.
+__device__ int load_window(const uint32_t* __restrict__ offs, int64_t first, int64_t last,
+                           uint32_t c0, int32_t* rel, uint32_t* err) {
+  const int64_t span = last - first + 1;
+  if (span > kTile && threadIdx.x == 0) atomicOr(err, 2u);
+  const int m = int(min(max(span, int64_t(1)), int64_t(kTile)));
+  for (int k = threadIdx.x; k < m; k += kBlock) rel[k] = int32_t(offs[first + k] - c0);
+  __syncthreads();
+  return m;
+}
+
 // Pass A: row-list entries [b kTile, b kTile + kTile) of the depth-ordered
 // expansion (Gaussian order[p] owns entries [offs[p], offs[p + 1]), one per
-// covered tile row), bucketed by tile row.  Writes the Gaussian id and
-// first column | width << 16 of every entry to its row-list position.
+// covered tile row), bucketed by tile row.  The first owner comes from
+// first_a (recorded by the height scan), the last one from the next
+// workgroup's first owner (a search for the final workgroup).  Writes each
+// entry's Gaussian id and packed first column / width / row.
 template <int BITS>
 __global__ __launch_bounds__(kBlock) void row_bucket_kernel(
     const int4* __restrict__ bounds, const int32_t* __restrict__ order,
-    const uint32_t* __restrict__ offs, int64_t n, uint32_t entries, int th,
-    const uint32_t* __restrict__ row_a, const int64_t* __restrict__ totals,
-    uint32_t* __restrict__ out_g, uint32_t* __restrict__ out_xw, uint64_t* __restrict__ status,
-    uint32_t* __restrict__ ticket, uint32_t* __restrict__ err) {
+    const uint32_t* __restrict__ offs, const uint32_t* __restrict__ first_a, int64_t n,
+    uint32_t entries, int th, const uint32_t* __restrict__ row_a,
+    const int64_t* __restrict__ totals, uint32_t* __restrict__ out_g,
+    uint32_t* __restrict__ out_xw, uint64_t* __restrict__ status, uint32_t* __restrict__ ticket,
+    uint32_t* __restrict__ err) {
   __shared__ BucketLds<BITS, 2> sh;
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
@@ -397,23 +493,24 @@ __global__ __launch_bounds__(kBlock) void row_bucket_kernel(
   for (int d = threadIdx.x; d < 4 * (1 << BITS); d += kBlock) (&sh.cnt[0][0])[d] = 0;
   __syncthreads();
   const int b = sh.block;
+  const int nblocks = int((int64_t(entries) + kTile - 1) / kTile);
   const uint32_t c0 = uint32_t(b) * kTile;
   const int nvalid = int(min(uint32_t(kTile), entries - c0));
-  if (wid < 2) {
-    const int64_t p = wave_last_le(offs, 0, n - 1, c0 + uint32_t(wid ? nvalid - 1 : 0));
-    if (lane == 0) sh.owner[wid] = p;
+  if (threadIdx.x == 0) {
+    sh.window[0] = first_a[b] & 0x7FFFFFFFu;
+    if (b + 1 < nblocks) {
+      const uint32_t nf = first_a[b + 1];
+      sh.window[1] = int64_t(nf & 0x7FFFFFFFu) - int64_t(nf >> 31);
+    }
+  }
+  if (b + 1 == nblocks && wid == 0) {
+    const int64_t p = wave_last_le(offs, 0, n - 1, c0 + uint32_t(nvalid - 1));
+    if (lane == 0) sh.window[1] = p;
   }
   __syncthreads();
-  const int64_t p_first = sh.owner[0];
-  // <= kTile: Gaussians without intersections sort last (depth key ~0u), so
-  // every Gaussian of the window owns at least one entry.
-  const int64_t span = sh.owner[1] - p_first + 1;
-  if (span > kTile && threadIdx.x == 0) atomicOr(err, 2u);
-  const int m = int(min(span, int64_t(kTile)));
+  const int64_t p_first = sh.window[0];
   int32_t* rel = reinterpret_cast<int32_t*>(sh.val);
-  for (int k = threadIdx.x; k < m; k += kBlock) rel[k] = int32_t(offs[p_first + k] - c0);
-  __syncthreads();
-
+  const int m = load_window(offs, p_first, sh.window[1], c0, rel, err);
   find_owners(rel, m, sh.own, sh.scratch);
 
   uint32_t dig[kItems];
@@ -424,26 +521,26 @@ __global__ __launch_bounds__(kBlock) void row_bucket_kernel(
     const int k = sh.own[e];
     const int g = order[p_first + k];
     const int4 bb = bounds[g];
-    dig[i] = e < nvalid ? uint32_t(bb.z + (e - rel[k])) & ((1u << BITS) - 1u) : 0u;
+    const uint32_t ty = uint32_t(bb.z + (e - rel[k])) & ((1u << BITS) - 1u);
+    dig[i] = e < nvalid ? ty : 0u;
     val[0][i] = uint32_t(g);
-    val[1][i] = uint32_t(bb.x) | (uint32_t(bb.y - bb.x) << 16);
+    val[1][i] = pack_entry(bb.x, bb.y - bb.x, int(ty));
   }
   uint32_t* const out[2] = {out_g, out_xw};
   place_items<BITS, 2>(
-      sh, dig, val, nvalid, b, 0, [&](int d) { return d <= th ? row_a[d] : 0u; }, status, err,
-      out, entries);
+      sh, dig, val, nvalid, b, b == 0, [&](int d) { return d <= th ? row_a[d] : 0u; }, status,
+      err, out, entries);
 }
 
-// Pass B: workgroup b covers intersections [c0, c0 + kTile) of one tile row
-// (rows own consecutive workgroups from row_blk); row-list entry k of the row
+// Pass B: workgroup b covers intersections [c0, c0 + count) of one tile row
+// (metadata info[b] recorded by the width scan); row-list entry k of the row
 // owns positions [W[k], W[k] + width) and expands into its columns.  Each
-// intersection is bucketed by column and its Gaussian id stored at
-// ranges[tile].start + rank.
+// intersection is bucketed by column inside its row and its Gaussian id
+// stored at ranges[tile].start + rank.
 template <int BITS>
 __global__ __launch_bounds__(kBlock) void column_bucket_kernel(
     const uint32_t* __restrict__ rl_g, const uint32_t* __restrict__ rl_xw,
-    const uint32_t* __restrict__ W, const uint32_t* __restrict__ row_a,
-    const uint32_t* __restrict__ row_e, const uint32_t* __restrict__ row_blk, int tw, int th,
+    const uint32_t* __restrict__ W, const uint4* __restrict__ info, int tw,
     const int64_t* __restrict__ ranges, const int64_t* __restrict__ totals, int64_t total,
     int64_t entries, int64_t blocks, int32_t* __restrict__ sorted_ids,
     uint64_t* __restrict__ status, uint32_t* __restrict__ ticket, uint32_t* __restrict__ err) {
@@ -458,31 +555,28 @@ __global__ __launch_bounds__(kBlock) void column_bucket_kernel(
   for (int d = threadIdx.x; d < 4 * (1 << BITS); d += kBlock) (&sh.cnt[0][0])[d] = 0;
   __syncthreads();
   const int b = sh.block;
-  if (wid == 0) {
-    // Rows with no workgroup share their start with the next row, so the
-    // largest row whose start is <= b is the one that owns b.
-    const int64_t y = wave_last_le(row_blk, 0, th - 1, uint32_t(b));
-    if (lane == 0) sh.row = int(y);
+  if (threadIdx.x == 0) {
+    const uint4 me = info[b];
+    const uint32_t row = me.z & 0xFFu;
+    sh.window[0] = me.x & 0x7FFFFFFFu;
+    sh.window[1] = me.w;  // last entry of the row, unless the next workgroup shares it
+    if (b + 1 < blocks) {
+      const uint4 next = info[b + 1];
+      if ((next.z & 0xFFu) == row && !(next.z >> 31))
+        sh.window[1] = int64_t(next.x & 0x7FFFFFFFu) - int64_t(next.x >> 31);
+    }
+    sh.c0 = me.y;
+    sh.nvalid = (me.z >> 8) & 0x1FFFu;
+    sh.row = row;
+    sh.chain_start = me.z >> 31;
   }
   __syncthreads();
-  const int ty = sh.row;
-  const int rb0 = int(row_blk[ty]);
-  const uint32_t c0 = row_e[ty] + uint32_t(b - rb0) * kTile;
-  const int nvalid = int(min(uint32_t(kTile), row_e[ty + 1] - c0));
-  const int64_t a0 = row_a[ty], a1 = row_a[ty + 1];
-  if (wid < 2) {
-    const int64_t k = wave_last_le(W, a0, a1 - 1, c0 + uint32_t(wid ? nvalid - 1 : 0));
-    if (lane == 0) sh.owner[wid] = k;
-  }
-  __syncthreads();
-  const int64_t k_first = sh.owner[0];
-  const int64_t span = sh.owner[1] - k_first + 1;  // <= kTile: every entry has width >= 1
-  if (span > kTile && threadIdx.x == 0) atomicOr(err, 2u);
-  const int m = int(min(span, int64_t(kTile)));
+  const uint32_t c0 = sh.c0;
+  const int nvalid = int(sh.nvalid);
+  const int ty = int(sh.row);
+  const int64_t k_first = sh.window[0];
   int32_t* rel = reinterpret_cast<int32_t*>(sh.val);
-  for (int k = threadIdx.x; k < m; k += kBlock) rel[k] = int32_t(W[k_first + k] - c0);
-  __syncthreads();
-
+  const int m = load_window(W, k_first, sh.window[1], c0, rel, err);
   find_owners(rel, m, sh.own, sh.scratch);
 
   uint32_t dig[kItems];
@@ -492,37 +586,37 @@ __global__ __launch_bounds__(kBlock) void column_bucket_kernel(
     const int e = wid * kSeg + i * 64 + lane;
     const int k = sh.own[e];
     const uint32_t xw = rl_xw[k_first + k];
-    dig[i] = e < nvalid ? ((xw & 0xFFFFu) + uint32_t(e - rel[k])) & ((1u << BITS) - 1u) : 0u;
+    dig[i] = e < nvalid ? (entry_x0(xw) + uint32_t(e - rel[k])) & ((1u << BITS) - 1u) : 0u;
     val[0][i] = rl_g[k_first + k];
   }
   uint32_t* const out[1] = {reinterpret_cast<uint32_t*>(sorted_ids)};
   const int64_t row_tiles = int64_t(ty) * tw;
   place_items<BITS, 1>(
-      sh, dig, val, nvalid, b, rb0,
+      sh, dig, val, nvalid, b, sh.chain_start != 0,
       [&](int d) { return d < tw ? uint32_t(ranges[2 * (row_tiles + d)]) : 0u; }, status, err,
       out, uint32_t(total));
 }
 
 template <int BITS>
 void launch_row_bucket(unsigned blocks, const int4* bounds, const int32_t* order,
-                       const uint32_t* offs, int64_t n, uint32_t entries, int th,
-                       const uint32_t* row_a, const int64_t* totals, uint32_t* out_g,
+                       const uint32_t* offs, const uint32_t* first_a, int64_t n, uint32_t entries,
+                       int th, const uint32_t* row_a, const int64_t* totals, uint32_t* out_g,
                        uint32_t* out_xw, uint64_t* status, uint32_t* ticket, uint32_t* err,
                        hipStream_t s) {
-  row_bucket_kernel<BITS><<<blocks, kBlock, 0, s>>>(bounds, order, offs, n, entries, th, row_a,
-                                                    totals, out_g, out_xw, status, ticket, err);
+  row_bucket_kernel<BITS><<<blocks, kBlock, 0, s>>>(bounds, order, offs, first_a, n, entries, th,
+                                                    row_a, totals, out_g, out_xw, status, ticket,
+                                                    err);
 }
 
 template <int BITS>
 void launch_column_bucket(unsigned blocks, const uint32_t* rl_g, const uint32_t* rl_xw,
-                          const uint32_t* W, const uint32_t* row_a, const uint32_t* row_e,
-                          const uint32_t* row_blk, int tw, int th, const int64_t* ranges,
+                          const uint32_t* W, const uint4* info, int tw, const int64_t* ranges,
                           const int64_t* totals, int64_t total, int64_t entries, int64_t blocks_b,
                           int32_t* sorted_ids, uint64_t* status, uint32_t* ticket, uint32_t* err,
                           hipStream_t s) {
-  column_bucket_kernel<BITS><<<blocks, kBlock, 0, s>>>(rl_g, rl_xw, W, row_a, row_e, row_blk, tw,
-                                                       th, ranges, totals, total, entries,
-                                                       blocks_b, sorted_ids, status, ticket, err);
+  column_bucket_kernel<BITS><<<blocks, kBlock, 0, s>>>(rl_g, rl_xw, W, info, tw, ranges, totals,
+                                                       total, entries, blocks_b, sorted_ids,
+                                                       status, ticket, err);
 }
 
 // Digit width of an axis of `tiles` tiles (at least 1 bit).
@@ -531,13 +625,13 @@ int axis_bits(int tiles) { return std::max(1, bits_for(tiles)); }
 // Persistent plan (written by gs_bin_tiles_plan, read by gs_bin_tiles_emit).
 struct PlanLayout {
   int32_t* order = nullptr;    // [n] depth order
-  uint32_t* offs = nullptr;    // [n + 1] row-list offsets in depth order
+  uint32_t* offs = nullptr;    // [n + 1] row-list offsets in depth order (written by emit)
   uint32_t* row_a = nullptr;   // [th + 1]
   uint32_t* row_e = nullptr;   // [th + 1]
   uint32_t* row_blk = nullptr;  // [th + 1]
   int32_t* table = nullptr;    // zeroed: diff2 [(th + 1) (tw + 1)], rowdiff [th + 1]
   int64_t table_words = 0;     // 64-bit words
-  void* sort_ws = nullptr;     // depth sort + scan scratch
+  void* sort_ws = nullptr;     // depth sort scratch
   size_t bytes = 0;
 };
 
@@ -558,7 +652,7 @@ PlanLayout plan_layout(void* base, int64_t n, int tw, int th) {
   const int64_t table_ints = int64_t(th + 1) * (tw + 1) + (th + 1);
   p.table_words = (table_ints + 1) / 2;
   p.table = reinterpret_cast<int32_t*>(take(size_t(p.table_words) * 8));
-  const size_t sort_bytes = carve(nullptr, n, 4, 32, n).bytes;
+  const size_t sort_bytes = carve(nullptr, n, 4, 32, 0).bytes;
   p.sort_ws = take(sort_bytes);
   p.bytes = off;
   return p;
@@ -569,16 +663,18 @@ struct EmitLayout {
   uint32_t* rl_g = nullptr;
   uint32_t* rl_xw = nullptr;
   uint32_t* W = nullptr;
-  uint64_t* zero = nullptr;  // status A, status B, scan status, then small words
+  uint32_t* first_a = nullptr;  // [blocks A]
+  uint4* info = nullptr;        // [blocks B]
+  uint64_t* zero = nullptr;     // statuses, then small words
   int64_t zero_words = 0;
   uint64_t* status_a = nullptr;
   uint64_t* status_b = nullptr;
-  uint64_t* scan_status = nullptr;
-  uint32_t* small = nullptr;  // ticket A, ticket B, scan ticket, err A, err B, scan err
+  uint64_t* scan_status[2] = {nullptr, nullptr};  // height scan, width scan
+  uint32_t* small = nullptr;  // tickets A, B, scans; error flags
   size_t bytes = 0;
 };
 
-EmitLayout emit_layout(void* base, int64_t entries, int64_t blocks_b, int tw, int th) {
+EmitLayout emit_layout(void* base, int64_t n, int64_t entries, int64_t blocks_b, int tw, int th) {
   EmitLayout e;
   char* c = static_cast<char*>(base);
   size_t off = 0;
@@ -587,19 +683,24 @@ EmitLayout emit_layout(void* base, int64_t entries, int64_t blocks_b, int tw, in
     off += align_up(bytes);
     return r;
   };
+  const int64_t blocks_a = ceil_div(entries, kTile);
   e.rl_g = reinterpret_cast<uint32_t*>(take(size_t(entries) * 4));
   e.rl_xw = reinterpret_cast<uint32_t*>(take(size_t(entries) * 4));
   e.W = reinterpret_cast<uint32_t*>(take(size_t(entries) * 4));
-  const int64_t words_a = ceil_div(entries, kTile) << axis_bits(th);
+  e.first_a = reinterpret_cast<uint32_t*>(take(size_t(blocks_a + 1) * 4));
+  e.info = reinterpret_cast<uint4*>(take(size_t(blocks_b + 1) * 16));
+  const int64_t words_a = blocks_a << axis_bits(th);
   const int64_t words_b = blocks_b << axis_bits(tw);
-  const int64_t words_s = ceil_div(entries, kTile);
-  e.zero_words = words_a + words_b + words_s + 4;  // + 8 small 32-bit words
+  const int64_t words_h = ceil_div(n, kTile);
+  const int64_t words_w = blocks_a;
+  e.zero_words = words_a + words_b + words_h + words_w + 4;  // + 8 small 32-bit words
   e.zero = reinterpret_cast<uint64_t*>(take(size_t(e.zero_words) * 8));
   if (e.zero) {
     e.status_a = e.zero;
     e.status_b = e.status_a + words_a;
-    e.scan_status = e.status_b + words_b;
-    e.small = reinterpret_cast<uint32_t*>(e.scan_status + words_s);
+    e.scan_status[0] = e.status_b + words_b;
+    e.scan_status[1] = e.scan_status[0] + words_h;
+    e.small = reinterpret_cast<uint32_t*>(e.scan_status[1] + words_w);
   }
   e.bytes = off;
   return e;
@@ -644,17 +745,15 @@ GS_API int gs_bin_tiles_plan(uint32_t* depth_keys, const int32_t* bounds, const 
   sweep::clear_kernel<<<unsigned(std::max<int64_t>(1, std::min<int64_t>(256, ceil_div(p.table_words, kBlock)))),
                         kBlock, 0, s>>>(reinterpret_cast<uint64_t*>(p.table), p.table_words,
                                         nullptr, 0);
+  const int words = (tiles_h + 1) * (tiles_w + 1);
   if (n > 0) {
-    const Scratch ws = carve(p.sort_ws, n, 4, 32, n);
+    const Scratch ws = carve(p.sort_ws, n, 4, 32, 0);
     clear(ws, s);
     // depth_keys is consumed (ping-pong buffer of the sort).
     uint32_t* sorted_keys = nullptr;
     GS_TRY(radix_sort<uint32_t>(depth_keys, nullptr, n, 32, reinterpret_cast<uint32_t*>(p.order),
                                 &sorted_keys, ws, s));
-    launch_scan<uint32_t>(HeightLoad{reinterpret_cast<const int4*>(bounds), counts, p.order}, n,
-                          p.offs, true, ws, s);
-    const int words = (tiles_h + 1) * (tiles_w + 1);
-    const unsigned blocks = unsigned(std::min<int64_t>(256, std::max<int64_t>(1, ceil_div(n, 8192))));
+    const unsigned blocks = unsigned(std::min<int64_t>(256, std::max<int64_t>(1, ceil_div(n, 4096))));
     int32_t* diff2 = p.table;
     int32_t* rowdiff = p.table + words;
     if (words + tiles_h + 1 <= kPrivateTableWords) {
@@ -665,7 +764,6 @@ GS_API int gs_bin_tiles_plan(uint32_t* depth_keys, const int32_t* bounds, const 
           reinterpret_cast<const int4*>(bounds), counts, n, tiles_w, tiles_h, diff2, rowdiff);
     }
   }
-  const int words = (tiles_h + 1) * (tiles_w + 1);
   const int lds_words = tiles_h * (tiles_w + 1);
   if (lds_words <= kPrivateTableWords) {
     tables_kernel<true><<<1, 256, size_t(lds_words) * 4, s>>>(
@@ -677,33 +775,35 @@ GS_API int gs_bin_tiles_plan(uint32_t* depth_keys, const int32_t* bounds, const 
   return check_launch("bin_tiles_plan");
 }
 
-GS_API size_t gs_bin_tiles_emit_bytes(int64_t total, int64_t row_entries, int64_t blocks,
-                                      int32_t tiles_w, int32_t tiles_h) {
-  if (total < 0 || row_entries < 0 || blocks < 0 || tiles_w <= 0 || tiles_h <= 0) return 0;
-  return emit_layout(nullptr, row_entries, blocks, tiles_w, tiles_h).bytes;
+GS_API size_t gs_bin_tiles_emit_bytes(int64_t n, int64_t total, int64_t row_entries,
+                                      int64_t blocks, int32_t tiles_w, int32_t tiles_h) {
+  if (n < 0 || total < 0 || row_entries < 0 || blocks < 0 || tiles_w <= 0 || tiles_h <= 0)
+    return 0;
+  return emit_layout(nullptr, n, row_entries, blocks, tiles_w, tiles_h).bytes;
 }
 
-GS_API int gs_bin_tiles_emit(const int32_t* bounds, int64_t n, int32_t tiles_w, int32_t tiles_h,
-                             const int64_t* totals, int64_t total, int64_t row_entries,
-                             int64_t blocks, const void* plan, size_t plan_bytes,
-                             const int64_t* ranges, int32_t* sorted_ids, void* workspace,
-                             size_t workspace_bytes, void* stream) {
+GS_API int gs_bin_tiles_emit(const int32_t* bounds, const int32_t* counts, int64_t n,
+                             int32_t tiles_w, int32_t tiles_h, const int64_t* totals,
+                             int64_t total, int64_t row_entries, int64_t blocks, void* plan,
+                             size_t plan_bytes, const int64_t* ranges, int32_t* sorted_ids,
+                             void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
   GS_TRY(check_grid(tiles_w, tiles_h));
   GS_REQUIRE(n >= 0 && total >= 0 && row_entries >= 0 && blocks >= 0, GS_ERR_INVALID_ARGUMENT,
              "invalid emit arguments");
-  GS_REQUIRE(total < (int64_t(1) << 32) - kTile && row_entries < (int64_t(1) << 32) - kTile,
+  GS_REQUIRE(total < (int64_t(1) << 32) - kTile && row_entries < (int64_t(1) << 31),
              GS_ERR_OVERFLOW, "too many intersections (%lld)", (long long)total);
   GS_REQUIRE(blocks >= ceil_div(total, kTile) && blocks <= ceil_div(total, kTile) + tiles_h,
              GS_ERR_INVALID_ARGUMENT, "inconsistent workgroup count");
   if (total == 0) return GS_OK;
   GS_REQUIRE(n > 0 && row_entries > 0 && blocks > 0, GS_ERR_INVALID_ARGUMENT,
              "intersections without Gaussians");
-  GS_REQUIRE(bounds && totals && plan && ranges && sorted_ids && workspace && aligned16(bounds),
+  GS_REQUIRE(bounds && counts && totals && plan && ranges && sorted_ids && workspace &&
+                 aligned16(bounds),
              GS_ERR_INVALID_ARGUMENT, "null or misaligned pointer");
-  const PlanLayout p = plan_layout(const_cast<void*>(plan), n, tiles_w, tiles_h);
+  const PlanLayout p = plan_layout(plan, n, tiles_w, tiles_h);
   GS_REQUIRE(plan_bytes >= p.bytes, GS_ERR_WORKSPACE, "plan workspace too small");
-  const EmitLayout e = emit_layout(workspace, row_entries, blocks, tiles_w, tiles_h);
+  const EmitLayout e = emit_layout(workspace, n, row_entries, blocks, tiles_w, tiles_h);
   GS_REQUIRE(workspace_bytes >= e.bytes, GS_ERR_WORKSPACE, "emit workspace too small (%zu < %zu)",
              workspace_bytes, e.bytes);
   hipStream_t s = as_stream(stream);
@@ -711,28 +811,40 @@ GS_API int gs_bin_tiles_emit(const int32_t* bounds, int64_t n, int32_t tiles_w, 
                         kBlock, 0, s>>>(e.zero, e.zero_words, nullptr, 0);
   uint32_t* ticket_a = e.small;
   uint32_t* ticket_b = e.small + 1;
-  uint32_t* scan_ticket = e.small + 2;
-  uint32_t* err = e.small + 3;
+  uint32_t* ticket_h = e.small + 2;
+  uint32_t* ticket_w = e.small + 3;
+  uint32_t* err = e.small + 4;  // err[0] pass A, err[1] pass B, err[2..3] scans
   const unsigned blocks_a = unsigned(ceil_div(row_entries, kTile));
   const int4* b4 = reinterpret_cast<const int4*>(bounds);
+  // Row-list offsets in depth order, recording each pass-A workgroup's first
+  // owner.
+  sweep::scan_kernel<uint32_t, HeightLoad, HeightSink>
+      <<<unsigned(ceil_div(n, kTile)), sweep::kBlock, 0, s>>>(
+          HeightLoad{b4, counts, p.order}, n, p.offs, true, true, e.scan_status[0], ticket_h,
+          err + 2, HeightSink{e.first_a, blocks_a});
   switch (axis_bits(tiles_h)) {
 #define GS_ROW_CASE(B)                                                                          \
   case B:                                                                                       \
-    launch_row_bucket<B>(blocks_a, b4, p.order, p.offs, n, uint32_t(row_entries), tiles_h,      \
-                         p.row_a, totals, e.rl_g, e.rl_xw, e.status_a, ticket_a, err, s);       \
+    launch_row_bucket<B>(blocks_a, b4, p.order, p.offs, e.first_a, n, uint32_t(row_entries),    \
+                         tiles_h, p.row_a, totals, e.rl_g, e.rl_xw, e.status_a, ticket_a, err,  \
+                         s);                                                                    \
     break;
     GS_ROW_CASE(1) GS_ROW_CASE(2) GS_ROW_CASE(3) GS_ROW_CASE(4)
     GS_ROW_CASE(5) GS_ROW_CASE(6) GS_ROW_CASE(7) GS_ROW_CASE(8)
 #undef GS_ROW_CASE
   }
-  sweep::scan_kernel<uint32_t, WidthLoad><<<blocks_a, sweep::kBlock, 0, s>>>(
-      WidthLoad{e.rl_xw}, row_entries, e.W, false, e.scan_status, scan_ticket, err + 2);
+  // Positions of the row-list entries in row-major intersection order,
+  // recording each pass-B workgroup's metadata.
+  sweep::scan_kernel<uint32_t, WidthLoad, WidthSink><<<blocks_a, sweep::kBlock, 0, s>>>(
+      WidthLoad{e.rl_xw}, row_entries, e.W, false, true, e.scan_status[1], ticket_w, err + 3,
+      WidthSink{e.rl_xw, p.row_e, p.row_a, p.row_blk, e.info, uint32_t(tiles_h),
+                uint32_t(blocks)});
   switch (axis_bits(tiles_w)) {
 #define GS_COL_CASE(B)                                                                          \
   case B:                                                                                       \
-    launch_column_bucket<B>(unsigned(blocks), e.rl_g, e.rl_xw, e.W, p.row_a, p.row_e,           \
-                            p.row_blk, tiles_w, tiles_h, ranges, totals, total, row_entries,    \
-                            blocks, sorted_ids, e.status_b, ticket_b, err + 1, s);              \
+    launch_column_bucket<B>(unsigned(blocks), e.rl_g, e.rl_xw, e.W, e.info, tiles_w, ranges,    \
+                            totals, total, row_entries, blocks, sorted_ids, e.status_b,         \
+                            ticket_b, err + 1, s);                                              \
     break;
     GS_COL_CASE(1) GS_COL_CASE(2) GS_COL_CASE(3) GS_COL_CASE(4)
     GS_COL_CASE(5) GS_COL_CASE(6) GS_COL_CASE(7) GS_COL_CASE(8)

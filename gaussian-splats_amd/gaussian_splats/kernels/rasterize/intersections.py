@@ -180,13 +180,13 @@ def bin_tiles(
     sorted_ids = torch.empty(total, dtype=torch.int32, device=device)
     if total:
         ws = nat.workspace(
-            lib.gs_bin_tiles_emit_bytes(total, row_entries, blocks, tiles_w, tiles_h), device
+            lib.gs_bin_tiles_emit_bytes(n, total, row_entries, blocks, tiles_w, tiles_h), device
         )
         nat.check(
             lib.gs_bin_tiles_emit(
-                nat.ptr(bounds), n, tiles_w, tiles_h, nat.ptr(totals), total, row_entries, blocks,
-                nat.ptr(plan), plan.numel(), nat.ptr(ranges), nat.ptr(sorted_ids), nat.ptr(ws),
-                ws.numel(), s,
+                nat.ptr(bounds), nat.ptr(counts), n, tiles_w, tiles_h, nat.ptr(totals), total,
+                row_entries, blocks, nat.ptr(plan), plan.numel(), nat.ptr(ranges),
+                nat.ptr(sorted_ids), nat.ptr(ws), ws.numel(), s,
             ),
             "bin_tiles_emit",
         )

@@ -171,23 +171,24 @@ GS_API int gs_sort_tiles(
  *
  * gs_bin_tiles_plan: depth order, per-tile counts and `ranges` [T, 2] (final),
  * and device `totals` = {intersections, row-list entries, pass-B workgroups,
- * 0}, which the caller reads back to size the ids; `plan` (plan_bytes from
+ * 0}, which the caller reads back to size the ids.  `plan` (plan_bytes from
  * gs_bin_tiles_plan_bytes) must stay alive until gs_bin_tiles_emit, which
- * takes the same totals (device pointer and the values read from it) and
- * writes `sorted_ids` [totals[0]].  depth_keys (as gs_project_and_count
- * writes them: ~0u for Gaussians without intersections) is consumed.  Together they
- * replace intersections.py:44-88 for the op. */
+ * takes the same bounds/counts, the totals (device pointer and the values
+ * read from it) and writes `sorted_ids` [totals[0]].  depth_keys (as
+ * gs_project_and_count writes them: ~0u for Gaussians without
+ * intersections) is consumed.  Together they replace intersections.py:44-88
+ * for the op. */
 GS_API size_t gs_bin_tiles_plan_bytes(int64_t n, int32_t tiles_w, int32_t tiles_h);
 GS_API int gs_bin_tiles_plan(
     uint32_t* depth_keys, const int32_t* bounds, const int32_t* counts, int64_t n,
     int32_t tiles_w, int32_t tiles_h, int64_t* ranges, int64_t* totals,
     void* plan, size_t plan_bytes, void* stream);
-GS_API size_t gs_bin_tiles_emit_bytes(int64_t total, int64_t row_entries, int64_t blocks,
-                                      int32_t tiles_w, int32_t tiles_h);
+GS_API size_t gs_bin_tiles_emit_bytes(int64_t n, int64_t total, int64_t row_entries,
+                                      int64_t blocks, int32_t tiles_w, int32_t tiles_h);
 GS_API int gs_bin_tiles_emit(
-    const int32_t* bounds, int64_t n, int32_t tiles_w, int32_t tiles_h,
+    const int32_t* bounds, const int32_t* counts, int64_t n, int32_t tiles_w, int32_t tiles_h,
     const int64_t* totals, int64_t total, int64_t row_entries, int64_t blocks,
-    const void* plan, size_t plan_bytes, const int64_t* ranges, int32_t* sorted_ids,
+    void* plan, size_t plan_bytes, const int64_t* ranges, int32_t* sorted_ids,
     void* workspace, size_t workspace_bytes, void* stream);
 
 /* Front-to-back compositing per tile.  Replaces composite

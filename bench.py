@@ -79,8 +79,8 @@ def staged_step(params, cam, target, tile_size, near, far):
     fx, fy = cam.focal_length
     cx, cy = cam.principal_point
     w, h = cam.image_size
-    R = cam.rotation_matrix.to(params[0].device)
-    t = cam.translation.to(params[0].device)
+    R = cam.rotation_matrix.float()  # host memory: passed to the kernels by value
+    t = cam.translation.float()
     out = forward_pipeline(*params, R, t, fx, fy, cx, cy, w, h, tile_size, 0.999, near, far,
                            "gaussian", 0.95, timer=mark)
     image, final_t, ncon, pmean, pinv, pcol, pop, gids, ranges, counts = out

@@ -1,6 +1,8 @@
-// C-ABI bookkeeping: per-thread error text, version, argument validation.
+// C-ABI bookkeeping: per-thread error text, version, argument validation,
+// and the side streams used to overlap independent stages.
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 
 #include "common.h"
 
@@ -43,6 +45,58 @@ int check_view(const gs_view& v, bool need_tiles) {
     GS_REQUIRE(tiles < (int64_t(1) << 30), GS_ERR_OVERFLOW, "too many tiles (%lld)",
                (long long)tiles);
   }
+  return GS_OK;
+}
+
+namespace {
+constexpr int kMaxDevices = 64;
+struct SideStream {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr;
+  hipEvent_t join = nullptr;
+};
+SideStream g_side[kMaxDevices];
+std::mutex g_side_mutex;
+}  // namespace
+
+int fork_side_stream(hipStream_t main, SideFork& f) {
+  int device = 0;
+  if (main) {
+    GS_REQUIRE(hipStreamGetDevice(main, &device) == hipSuccess, GS_ERR_HIP,
+               "hipStreamGetDevice failed");
+  } else {
+    GS_REQUIRE(hipGetDevice(&device) == hipSuccess, GS_ERR_HIP, "hipGetDevice failed");
+  }
+  GS_REQUIRE(device >= 0 && device < kMaxDevices, GS_ERR_HIP, "device %d out of range", device);
+  f.lock = std::unique_lock<std::mutex>(g_side_mutex);
+  SideStream& s = g_side[device];
+  if (!s.stream) {
+    int current = 0;
+    GS_REQUIRE(hipGetDevice(&current) == hipSuccess, GS_ERR_HIP, "hipGetDevice failed");
+    const bool switch_device = current != device;
+    if (switch_device) GS_REQUIRE(hipSetDevice(device) == hipSuccess, GS_ERR_HIP, "hipSetDevice");
+    // Default priority; the stream does not synchronise with the null stream.
+    const bool ok = hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking) == hipSuccess &&
+                    hipEventCreateWithFlags(&s.fork, hipEventDisableTiming) == hipSuccess &&
+                    hipEventCreateWithFlags(&s.join, hipEventDisableTiming) == hipSuccess;
+    if (switch_device) (void)hipSetDevice(current);
+    GS_REQUIRE(ok, GS_ERR_HIP, "could not create the side stream");
+  }
+  GS_REQUIRE(hipEventRecord(s.fork, main) == hipSuccess &&
+                 hipStreamWaitEvent(s.stream, s.fork, 0) == hipSuccess,
+             GS_ERR_HIP, "side stream fork failed");
+  f.main = main;
+  f.side = s.stream;
+  f.join = s.join;
+  return GS_OK;
+}
+
+int join_side_stream(SideFork& f, bool host_wait) {
+  bool ok = hipEventRecord(f.join, f.side) == hipSuccess &&
+            hipStreamWaitEvent(f.main, f.join, 0) == hipSuccess;
+  if (ok && host_wait) ok = hipEventSynchronize(f.join) == hipSuccess;
+  f.lock = std::unique_lock<std::mutex>();
+  GS_REQUIRE(ok, GS_ERR_HIP, "side stream join failed");
   return GS_OK;
 }
 

@@ -5,6 +5,7 @@
 
 #include <cstdint>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "gs_raster.h"
@@ -19,6 +20,21 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 
 // Checks the launch that was just enqueued; converts a HIP error into a status.
 int check_launch(const char* what);
+
+// Work forked from the caller's stream onto the library's side stream of the
+// same device (created once, default priority, non-blocking) and joined back
+// with an event, so two independent stages overlap.  The side stream is held
+// exclusively from fork to join.
+struct SideFork {
+  hipStream_t main = nullptr;
+  hipStream_t side = nullptr;
+  hipEvent_t join = nullptr;
+  std::unique_lock<std::mutex> lock;
+};
+int fork_side_stream(hipStream_t main, SideFork& f);
+// Joins the side stream back into the caller's; with host_wait the host also
+// waits for the side stream's work (not the caller's) before returning.
+int join_side_stream(SideFork& f, bool host_wait = false);
 
 #define GS_REQUIRE(cond, code, ...)      \
   do {                                   \

@@ -25,8 +25,8 @@ struct ProjectBwdArgs {
   const float* scale;
   const float* opacity;
   const float* color;
-  const float* cam_r;
-  const float* cam_t;
+  float cam_r[9];  // world -> camera rotation, by value (kernel arguments)
+  float cam_t[3];
   const float* inv;
   const float* grad_in;  // [N, 9]
   const int32_t* counts;
@@ -293,8 +293,9 @@ extern "C" GS_API int gs_project_bwd(const float* mean, const float* rotation, c
   a.scale = scale;
   a.opacity = opacity;
   a.color = color;
-  a.cam_r = camera_rotation;
-  a.cam_t = camera_translation;
+  // Host memory: the extrinsics travel as kernel arguments.
+  for (int i = 0; i < 9; ++i) a.cam_r[i] = camera_rotation[i];
+  for (int i = 0; i < 3; ++i) a.cam_t[i] = camera_translation[i];
   a.inv = inverse_covariance;
   a.grad_in = grad_projected;
   a.counts = counts;

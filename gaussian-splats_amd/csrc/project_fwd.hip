@@ -24,8 +24,8 @@ struct ProjectArgs {
   const float* scale;
   const float* opacity;
   const float* color;
-  const float* cam_r;
-  const float* cam_t;
+  float cam_r[9];  // world -> camera rotation, by value (kernel arguments)
+  float cam_t[3];
   int64_t n;
   float fx, fy, cx, cy;
   float lim_x, lim_y;  // 1.3 * tan(half field of view), camera.py:106-116
@@ -274,8 +274,9 @@ extern "C" GS_API int gs_project_and_count(
   a.scale = scale;
   a.opacity = opacity;
   a.color = color;
-  a.cam_r = camera_rotation;
-  a.cam_t = camera_translation;
+  // Host memory: the extrinsics travel as kernel arguments.
+  for (int i = 0; i < 9; ++i) a.cam_r[i] = camera_rotation[i];
+  for (int i = 0; i < 3; ++i) a.cam_t[i] = camera_translation[i];
   a.n = n;
   a.fx = view.fx;
   a.fy = view.fy;

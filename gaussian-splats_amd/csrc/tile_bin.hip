@@ -631,7 +631,9 @@ struct PlanLayout {
   uint32_t* row_blk = nullptr;  // [th + 1]
   int32_t* table = nullptr;    // zeroed: diff2 [(th + 1) (tw + 1)], rowdiff [th + 1]
   int64_t table_words = 0;     // 64-bit words
-  void* sort_ws = nullptr;     // depth sort scratch
+  uint32_t* first_a = nullptr;  // [first_a_capacity] first owner of each pass-A workgroup
+  uint32_t first_a_capacity = 0;
+  void* sort_ws = nullptr;     // depth sort and height scan scratch
   size_t bytes = 0;
 };
 
@@ -652,7 +654,12 @@ PlanLayout plan_layout(void* base, int64_t n, int tw, int th) {
   const int64_t table_ints = int64_t(th + 1) * (tw + 1) + (th + 1);
   p.table_words = (table_ints + 1) / 2;
   p.table = reinterpret_cast<int32_t*>(take(size_t(p.table_words) * 8));
-  const size_t sort_bytes = carve(nullptr, n, 4, 32, 0).bytes;
+  // Row-list entries are at most n th (every Gaussian on every row) and fewer
+  // than 2^31 (checked by gs_bin_tiles_emit).
+  p.first_a_capacity =
+      uint32_t(ceil_div(std::min(int64_t(n) * th, int64_t(1) << 31), kTile) + 1);
+  p.first_a = reinterpret_cast<uint32_t*>(take(size_t(p.first_a_capacity) * 4));
+  const size_t sort_bytes = carve(nullptr, n, 4, 32, n).bytes;
   p.sort_ws = take(sort_bytes);
   p.bytes = off;
   return p;
@@ -663,18 +670,17 @@ struct EmitLayout {
   uint32_t* rl_g = nullptr;
   uint32_t* rl_xw = nullptr;
   uint32_t* W = nullptr;
-  uint32_t* first_a = nullptr;  // [blocks A]
   uint4* info = nullptr;        // [blocks B]
   uint64_t* zero = nullptr;     // statuses, then small words
   int64_t zero_words = 0;
   uint64_t* status_a = nullptr;
   uint64_t* status_b = nullptr;
-  uint64_t* scan_status[2] = {nullptr, nullptr};  // height scan, width scan
-  uint32_t* small = nullptr;  // tickets A, B, scans; error flags
+  uint64_t* scan_status = nullptr;  // width scan
+  uint32_t* small = nullptr;  // tickets A, B, width scan; error flags
   size_t bytes = 0;
 };
 
-EmitLayout emit_layout(void* base, int64_t n, int64_t entries, int64_t blocks_b, int tw, int th) {
+EmitLayout emit_layout(void* base, int64_t entries, int64_t blocks_b, int tw, int th) {
   EmitLayout e;
   char* c = static_cast<char*>(base);
   size_t off = 0;
@@ -687,20 +693,17 @@ EmitLayout emit_layout(void* base, int64_t n, int64_t entries, int64_t blocks_b,
   e.rl_g = reinterpret_cast<uint32_t*>(take(size_t(entries) * 4));
   e.rl_xw = reinterpret_cast<uint32_t*>(take(size_t(entries) * 4));
   e.W = reinterpret_cast<uint32_t*>(take(size_t(entries) * 4));
-  e.first_a = reinterpret_cast<uint32_t*>(take(size_t(blocks_a + 1) * 4));
   e.info = reinterpret_cast<uint4*>(take(size_t(blocks_b + 1) * 16));
   const int64_t words_a = blocks_a << axis_bits(th);
   const int64_t words_b = blocks_b << axis_bits(tw);
-  const int64_t words_h = ceil_div(n, kTile);
   const int64_t words_w = blocks_a;
-  e.zero_words = words_a + words_b + words_h + words_w + 4;  // + 8 small 32-bit words
+  e.zero_words = words_a + words_b + words_w + 4;  // + 8 small 32-bit words
   e.zero = reinterpret_cast<uint64_t*>(take(size_t(e.zero_words) * 8));
   if (e.zero) {
     e.status_a = e.zero;
     e.status_b = e.status_a + words_a;
-    e.scan_status[0] = e.status_b + words_b;
-    e.scan_status[1] = e.scan_status[0] + words_h;
-    e.small = reinterpret_cast<uint32_t*>(e.scan_status[1] + words_w);
+    e.scan_status = e.status_b + words_b;
+    e.small = reinterpret_cast<uint32_t*>(e.scan_status + words_w);
   }
   e.bytes = off;
   return e;
@@ -730,7 +733,8 @@ GS_API size_t gs_bin_tiles_plan_bytes(int64_t n, int32_t tiles_w, int32_t tiles_
 
 GS_API int gs_bin_tiles_plan(uint32_t* depth_keys, const int32_t* bounds, const int32_t* counts,
                              int64_t n, int32_t tiles_w, int32_t tiles_h, int64_t* ranges,
-                             int64_t* totals, void* plan, size_t plan_bytes, void* stream) {
+                             int64_t* totals, int64_t* host_totals, void* plan, size_t plan_bytes,
+                             void* stream) {
   clear_error();
   GS_TRY(check_grid(tiles_w, tiles_h));
   GS_REQUIRE(n >= 0 && n < (int64_t(1) << 31), GS_ERR_INVALID_ARGUMENT, "invalid Gaussian count");
@@ -742,36 +746,60 @@ GS_API int gs_bin_tiles_plan(uint32_t* depth_keys, const int32_t* bounds, const 
   GS_REQUIRE(plan_bytes >= p.bytes, GS_ERR_WORKSPACE, "plan workspace too small (%zu < %zu)",
              plan_bytes, p.bytes);
   hipStream_t s = as_stream(stream);
-  sweep::clear_kernel<<<unsigned(std::max<int64_t>(1, std::min<int64_t>(256, ceil_div(p.table_words, kBlock)))),
-                        kBlock, 0, s>>>(reinterpret_cast<uint64_t*>(p.table), p.table_words,
-                                        nullptr, 0);
+  // The tile tables need only the rectangles: they run on the side stream
+  // while the depth sort and the row-list offset scan run on the caller's.
+  SideFork fork;
+  GS_TRY(fork_side_stream(s, fork));
   const int words = (tiles_h + 1) * (tiles_w + 1);
+  sweep::clear_kernel<<<unsigned(std::max<int64_t>(1, std::min<int64_t>(256, ceil_div(p.table_words, kBlock)))),
+                        kBlock, 0, fork.side>>>(reinterpret_cast<uint64_t*>(p.table),
+                                                p.table_words, nullptr, 0);
   if (n > 0) {
-    const Scratch ws = carve(p.sort_ws, n, 4, 32, 0);
-    clear(ws, s);
-    // depth_keys is consumed (ping-pong buffer of the sort).
-    uint32_t* sorted_keys = nullptr;
-    GS_TRY(radix_sort<uint32_t>(depth_keys, nullptr, n, 32, reinterpret_cast<uint32_t*>(p.order),
-                                &sorted_keys, ws, s));
     const unsigned blocks = unsigned(std::min<int64_t>(256, std::max<int64_t>(1, ceil_div(n, 4096))));
     int32_t* diff2 = p.table;
     int32_t* rowdiff = p.table + words;
     if (words + tiles_h + 1 <= kPrivateTableWords) {
-      rect_diff_kernel<true><<<blocks, 256, size_t(words + tiles_h + 1) * 4, s>>>(
+      rect_diff_kernel<true><<<blocks, 256, size_t(words + tiles_h + 1) * 4, fork.side>>>(
           reinterpret_cast<const int4*>(bounds), counts, n, tiles_w, tiles_h, diff2, rowdiff);
     } else {
-      rect_diff_kernel<false><<<blocks, 256, size_t(tiles_h + 1) * 4, s>>>(
+      rect_diff_kernel<false><<<blocks, 256, size_t(tiles_h + 1) * 4, fork.side>>>(
           reinterpret_cast<const int4*>(bounds), counts, n, tiles_w, tiles_h, diff2, rowdiff);
     }
   }
   const int lds_words = tiles_h * (tiles_w + 1);
   if (lds_words <= kPrivateTableWords) {
-    tables_kernel<true><<<1, 256, size_t(lds_words) * 4, s>>>(
+    tables_kernel<true><<<1, 256, size_t(lds_words) * 4, fork.side>>>(
         p.table, p.table + words, tiles_w, tiles_h, ranges, p.row_a, p.row_e, p.row_blk, totals);
   } else {
-    tables_kernel<false><<<1, 256, 0, s>>>(p.table, p.table + words, tiles_w, tiles_h, ranges,
-                                           p.row_a, p.row_e, p.row_blk, totals);
+    tables_kernel<false><<<1, 256, 0, fork.side>>>(p.table, p.table + words, tiles_w, tiles_h,
+                                                   ranges, p.row_a, p.row_e, p.row_blk, totals);
   }
+  int status = check_launch("bin_tiles_plan (tables)");
+  if (host_totals && status == GS_OK &&
+      hipMemcpyAsync(host_totals, totals, 4 * sizeof(int64_t), hipMemcpyDeviceToHost,
+                     fork.side) != hipSuccess) {
+    set_error("bin_tiles_plan: copy of the totals failed");
+    status = GS_ERR_HIP;
+  }
+  if (n > 0 && status == GS_OK) {
+    const Scratch ws = carve(p.sort_ws, n, 4, 32, n);
+    clear(ws, s);
+    // depth_keys is consumed (ping-pong buffer of the sort).
+    uint32_t* sorted_keys = nullptr;
+    status = radix_sort<uint32_t>(depth_keys, nullptr, n, 32,
+                                  reinterpret_cast<uint32_t*>(p.order), &sorted_keys, ws, s);
+    // Row-list offsets in depth order, recording each pass-A workgroup's
+    // first owner.
+    if (status == GS_OK)
+      launch_scan<uint32_t>(HeightLoad{reinterpret_cast<const int4*>(bounds), counts, p.order},
+                            n, p.offs, true, true, ws, s,
+                            HeightSink{p.first_a, p.first_a_capacity});
+  }
+  // Always join, also after an error; with host_totals the host waits for
+  // the tables only, while the sort keeps running on the caller's stream.
+  const int joined = join_side_stream(fork, host_totals != nullptr && status == GS_OK);
+  GS_TRY(status);
+  GS_TRY(joined);
   return check_launch("bin_tiles_plan");
 }
 
@@ -779,10 +807,10 @@ GS_API size_t gs_bin_tiles_emit_bytes(int64_t n, int64_t total, int64_t row_entr
                                       int64_t blocks, int32_t tiles_w, int32_t tiles_h) {
   if (n < 0 || total < 0 || row_entries < 0 || blocks < 0 || tiles_w <= 0 || tiles_h <= 0)
     return 0;
-  return emit_layout(nullptr, n, row_entries, blocks, tiles_w, tiles_h).bytes;
+  return emit_layout(nullptr, row_entries, blocks, tiles_w, tiles_h).bytes;
 }
 
-GS_API int gs_bin_tiles_emit(const int32_t* bounds, const int32_t* counts, int64_t n,
+GS_API int gs_bin_tiles_emit(const int32_t* bounds, int64_t n,
                              int32_t tiles_w, int32_t tiles_h, const int64_t* totals,
                              int64_t total, int64_t row_entries, int64_t blocks, void* plan,
                              size_t plan_bytes, const int64_t* ranges, int32_t* sorted_ids,
@@ -798,12 +826,14 @@ GS_API int gs_bin_tiles_emit(const int32_t* bounds, const int32_t* counts, int64
   if (total == 0) return GS_OK;
   GS_REQUIRE(n > 0 && row_entries > 0 && blocks > 0, GS_ERR_INVALID_ARGUMENT,
              "intersections without Gaussians");
-  GS_REQUIRE(bounds && counts && totals && plan && ranges && sorted_ids && workspace &&
+  GS_REQUIRE(bounds && totals && plan && ranges && sorted_ids && workspace &&
                  aligned16(bounds),
              GS_ERR_INVALID_ARGUMENT, "null or misaligned pointer");
   const PlanLayout p = plan_layout(plan, n, tiles_w, tiles_h);
   GS_REQUIRE(plan_bytes >= p.bytes, GS_ERR_WORKSPACE, "plan workspace too small");
-  const EmitLayout e = emit_layout(workspace, n, row_entries, blocks, tiles_w, tiles_h);
+  const EmitLayout e = emit_layout(workspace, row_entries, blocks, tiles_w, tiles_h);
+  GS_REQUIRE(uint64_t(ceil_div(row_entries, kTile)) <= p.first_a_capacity, GS_ERR_INVALID_ARGUMENT,
+             "row-list entries exceed the plan");
   GS_REQUIRE(workspace_bytes >= e.bytes, GS_ERR_WORKSPACE, "emit workspace too small (%zu < %zu)",
              workspace_bytes, e.bytes);
   hipStream_t s = as_stream(stream);
@@ -811,21 +841,14 @@ GS_API int gs_bin_tiles_emit(const int32_t* bounds, const int32_t* counts, int64
                         kBlock, 0, s>>>(e.zero, e.zero_words, nullptr, 0);
   uint32_t* ticket_a = e.small;
   uint32_t* ticket_b = e.small + 1;
-  uint32_t* ticket_h = e.small + 2;
-  uint32_t* ticket_w = e.small + 3;
-  uint32_t* err = e.small + 4;  // err[0] pass A, err[1] pass B, err[2..3] scans
+  uint32_t* ticket_w = e.small + 2;
+  uint32_t* err = e.small + 4;  // err[0] pass A, err[1] pass B, err[2] width scan
   const unsigned blocks_a = unsigned(ceil_div(row_entries, kTile));
   const int4* b4 = reinterpret_cast<const int4*>(bounds);
-  // Row-list offsets in depth order, recording each pass-A workgroup's first
-  // owner.
-  sweep::scan_kernel<uint32_t, HeightLoad, HeightSink>
-      <<<unsigned(ceil_div(n, kTile)), sweep::kBlock, 0, s>>>(
-          HeightLoad{b4, counts, p.order}, n, p.offs, true, true, e.scan_status[0], ticket_h,
-          err + 2, HeightSink{e.first_a, blocks_a});
   switch (axis_bits(tiles_h)) {
 #define GS_ROW_CASE(B)                                                                          \
   case B:                                                                                       \
-    launch_row_bucket<B>(blocks_a, b4, p.order, p.offs, e.first_a, n, uint32_t(row_entries),    \
+    launch_row_bucket<B>(blocks_a, b4, p.order, p.offs, p.first_a, n, uint32_t(row_entries),    \
                          tiles_h, p.row_a, totals, e.rl_g, e.rl_xw, e.status_a, ticket_a, err,  \
                          s);                                                                    \
     break;
@@ -836,7 +859,7 @@ GS_API int gs_bin_tiles_emit(const int32_t* bounds, const int32_t* counts, int64
   // Positions of the row-list entries in row-major intersection order,
   // recording each pass-B workgroup's metadata.
   sweep::scan_kernel<uint32_t, WidthLoad, WidthSink><<<blocks_a, sweep::kBlock, 0, s>>>(
-      WidthLoad{e.rl_xw}, row_entries, e.W, false, true, e.scan_status[1], ticket_w, err + 3,
+      WidthLoad{e.rl_xw}, row_entries, e.W, false, true, e.scan_status, ticket_w, err + 2,
       WidthSink{e.rl_xw, p.row_e, p.row_a, p.row_blk, e.info, uint32_t(tiles_h),
                 uint32_t(blocks)});
   switch (axis_bits(tiles_w)) {

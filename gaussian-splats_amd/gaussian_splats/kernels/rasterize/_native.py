@@ -104,12 +104,12 @@ _SIGNATURES = {
     "gs_bin_tiles_plan_bytes": (c_size_t, [c_int64, c_int32, c_int32]),
     "gs_bin_tiles_plan": (
         c_int,
-        [c_void_p] * 3 + [c_int64, c_int32, c_int32] + [c_void_p] * 3 + [c_size_t, c_void_p],
+        [c_void_p] * 3 + [c_int64, c_int32, c_int32] + [c_void_p] * 4 + [c_size_t, c_void_p],
     ),
     "gs_bin_tiles_emit_bytes": (c_size_t, [c_int64, c_int64, c_int64, c_int64, c_int32, c_int32]),
     "gs_bin_tiles_emit": (
         c_int,
-        [c_void_p, c_void_p, c_int64, c_int32, c_int32, c_void_p, c_int64, c_int64, c_int64,
+        [c_void_p, c_int64, c_int32, c_int32, c_void_p, c_int64, c_int64, c_int64,
          c_void_p, c_size_t, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p],
     ),
     "gs_composite": (c_int, [c_void_p, c_void_p, c_void_p, GsView, c_void_p, c_void_p, c_void_p, c_void_p]),
@@ -197,6 +197,15 @@ def prepare(t: torch.Tensor, dtype: torch.dtype = torch.float32) -> torch.Tensor
     if t.data_ptr() % 16:
         t = t.clone()
     return t
+
+
+def host_floats(t: torch.Tensor, numel: int, name: str) -> torch.Tensor:
+    """Contiguous float32 copy in host memory (the C-ABI passes camera
+    extrinsics to the kernels by value); a GPU tensor costs one device sync."""
+    t = t.detach()
+    if t.numel() != numel:
+        raise ValueError(f"{name} must have {numel} elements, got {t.numel()}")
+    return t.to(device="cpu", dtype=torch.float32).contiguous()
 
 
 def workspace(nbytes: int, device: torch.device) -> torch.Tensor:

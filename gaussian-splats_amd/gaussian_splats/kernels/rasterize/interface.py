@@ -164,6 +164,9 @@ def _rasterize_fake(
 
 
 def _setup_context(ctx, inputs, output) -> None:
+    # The backward reads only the image gradient; unused outputs get None
+    # instead of zero-filled gradient tensors.
+    ctx.set_materialize_grads(False)
     ctx.save_for_backward(*inputs[:7], *output[1:])
     (
         ctx.fx,
@@ -261,8 +264,9 @@ def rasterize(
         scale,
         opacity,
         color,
-        camera.rotation_matrix.to(device=device, dtype=torch.float32),
-        camera.translation.to(device=device, dtype=torch.float32),
+        # Extrinsics stay in host memory: the kernels take them as arguments.
+        camera.rotation_matrix.detach().to(device="cpu", dtype=torch.float32),
+        camera.translation.detach().to(device="cpu", dtype=torch.float32),
         float(fx),
         float(fy),
         float(cx),

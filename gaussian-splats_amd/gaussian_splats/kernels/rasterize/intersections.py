@@ -14,6 +14,8 @@ with the row and column buckets filled straight from the tile rectangles.
 
 from __future__ import annotations
 
+from ctypes import c_void_p
+
 import torch
 
 from . import _native as nat
@@ -166,17 +168,20 @@ def bin_tiles(
     plan = nat.workspace(lib.gs_bin_tiles_plan_bytes(n, tiles_w, tiles_h), device)
     ranges = torch.empty((tiles_w * tiles_h, 2), dtype=torch.int64, device=device)
     totals = torch.empty(4, dtype=torch.int64, device=device)
+    # The one device-to-host read of the path: the totals size the id buffer
+    # (the reference reads counts.sum() at intersections.py:51).  The call
+    # returns once they are in host_totals, while the depth sort still runs.
+    host_totals = torch.empty(4, dtype=torch.int64, pin_memory=True)
     nat.check(
         lib.gs_bin_tiles_plan(
             nat.ptr(depth_keys), nat.ptr(bounds), nat.ptr(counts), n, tiles_w, tiles_h,
-            nat.ptr(ranges), nat.ptr(totals), nat.ptr(plan), plan.numel(), s,
+            nat.ptr(ranges), nat.ptr(totals), c_void_p(host_totals.data_ptr()), nat.ptr(plan),
+            plan.numel(), s,
         ),
         "bin_tiles_plan",
     )
     mark("bin")
-    # The one device-to-host read of the path: the totals size the id buffer
-    # (the reference reads counts.sum() at intersections.py:51).
-    total, row_entries, blocks, _ = totals.tolist()
+    total, row_entries, blocks, _ = host_totals.tolist()
     sorted_ids = torch.empty(total, dtype=torch.int32, device=device)
     if total:
         ws = nat.workspace(
@@ -184,7 +189,7 @@ def bin_tiles(
         )
         nat.check(
             lib.gs_bin_tiles_emit(
-                nat.ptr(bounds), nat.ptr(counts), n, tiles_w, tiles_h, nat.ptr(totals), total,
+                nat.ptr(bounds), n, tiles_w, tiles_h, nat.ptr(totals), total,
                 row_entries, blocks, nat.ptr(plan), plan.numel(), nat.ptr(ranges),
                 nat.ptr(sorted_ids), nat.ptr(ws), ws.numel(), s,
             ),

@@ -6,6 +6,8 @@ src/gaussian_splats/kernels/rasterize/project.py:256-345.
 
 from __future__ import annotations
 
+from ctypes import c_void_p
+
 import torch
 
 from . import _native as nat
@@ -57,8 +59,8 @@ def project_and_count(
     mean, rotation, scale, opacity, color = (
         nat.prepare(t) for t in (mean, rotation, scale, opacity, color)
     )
-    camera_rotation = nat.prepare(camera_rotation.to(device=device, dtype=torch.float32))
-    camera_translation = nat.prepare(camera_translation.to(device=device, dtype=torch.float32))
+    camera_rotation = nat.host_floats(camera_rotation, 9, "camera_rotation")
+    camera_translation = nat.host_floats(camera_translation, 3, "camera_translation")
 
     n = mean.shape[0]
     projected_mean = mean.new_empty((n, 3))
@@ -78,7 +80,7 @@ def project_and_count(
     nat.check(
         lib.gs_project_and_count(
             nat.ptr(mean), nat.ptr(rotation), nat.ptr(scale), nat.ptr(opacity), nat.ptr(color),
-            n, color.shape[1], nat.ptr(camera_rotation), nat.ptr(camera_translation), view,
+            n, color.shape[1], c_void_p(camera_rotation.data_ptr()), c_void_p(camera_translation.data_ptr()), view,
             nat.ptr(projected_mean), nat.ptr(inverse_covariance), nat.ptr(projected_color),
             nat.ptr(projected_opacity), nat.ptr(bounds), nat.ptr(counts), nat.ptr(records),
             nat.ptr(depth_keys), nat.stream(device),

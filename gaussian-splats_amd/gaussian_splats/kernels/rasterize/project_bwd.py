@@ -6,6 +6,8 @@ src/gaussian_splats/kernels/rasterize/project_bwd.py:337-381.
 
 from __future__ import annotations
 
+from ctypes import c_void_p
+
 import torch
 
 from . import _native as nat
@@ -38,8 +40,8 @@ def project_bwd(
         for t in (mean, rotation, scale, opacity, color, inverse_covariance, grad_projected)
     )
     counts = nat.prepare(counts, torch.int32)
-    camera_rotation = nat.prepare(camera_rotation.to(device=device, dtype=torch.float32))
-    camera_translation = nat.prepare(camera_translation.to(device=device, dtype=torch.float32))
+    camera_rotation = nat.host_floats(camera_rotation, 9, "camera_rotation")
+    camera_translation = nat.host_floats(camera_translation, 3, "camera_translation")
     grad_mean = torch.empty_like(mean)
     grad_rotation = torch.empty_like(rotation)
     grad_scale = torch.empty_like(scale)
@@ -52,7 +54,7 @@ def project_bwd(
     nat.check(
         nat.library().gs_project_bwd(
             nat.ptr(mean), nat.ptr(rotation), nat.ptr(scale), nat.ptr(opacity), nat.ptr(color),
-            n, color.shape[1], nat.ptr(camera_rotation), nat.ptr(camera_translation), view,
+            n, color.shape[1], c_void_p(camera_rotation.data_ptr()), c_void_p(camera_translation.data_ptr()), view,
             nat.ptr(inverse_covariance), nat.ptr(grad_projected), nat.ptr(counts),
             nat.ptr(grad_mean), nat.ptr(grad_rotation), nat.ptr(grad_scale),
             nat.ptr(grad_opacity), nat.ptr(grad_color), nat.stream(device),

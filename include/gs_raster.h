@@ -15,7 +15,8 @@
  * interface.py:17-49):
  *   mean[N,3], rotation[N,4] (w,x,y,z, unnormalised), scale[N,3] (log sigma),
  *   opacity[N,1] (logit), color[N,K,3] (coefficient-major, RGB innermost),
- *   camera_rotation[3,3] (world->camera), camera_translation[3],
+ *   camera_rotation[3,3] (world->camera), camera_translation[3] (both in
+ *   host memory: the twelve values are passed to the kernels as arguments),
  *   projected_mean[N,3] (u, v, depth), inverse_covariance[N,2,2],
  *   projected_color[N,3], projected_opacity[N,1], bounds[N,2,2] int32
  *   (x_min, x_max, y_min, y_max in tiles, half-open), counts[N] int32,
@@ -171,22 +172,25 @@ GS_API int gs_sort_tiles(
  *
  * gs_bin_tiles_plan: depth order, per-tile counts and `ranges` [T, 2] (final),
  * and device `totals` = {intersections, row-list entries, pass-B workgroups,
- * 0}, which the caller reads back to size the ids.  `plan` (plan_bytes from
+ * 0}, which size the ids.  With `host_totals` (4 x int64, pinned host memory
+ * for an asynchronous copy) the call returns once they have been copied
+ * there: the tables are built on a side stream, so the host waits for them
+ * while the depth sort still runs on `stream`.  `plan` (plan_bytes from
  * gs_bin_tiles_plan_bytes) must stay alive until gs_bin_tiles_emit, which
- * takes the same bounds/counts, the totals (device pointer and the values
- * read from it) and writes `sorted_ids` [totals[0]].  depth_keys (as
+ * takes the same bounds, the totals (device pointer and the values read from
+ * it) and writes `sorted_ids` [totals[0]].  depth_keys (as
  * gs_project_and_count writes them: ~0u for Gaussians without
  * intersections) is consumed.  Together they replace intersections.py:44-88
  * for the op. */
 GS_API size_t gs_bin_tiles_plan_bytes(int64_t n, int32_t tiles_w, int32_t tiles_h);
 GS_API int gs_bin_tiles_plan(
     uint32_t* depth_keys, const int32_t* bounds, const int32_t* counts, int64_t n,
-    int32_t tiles_w, int32_t tiles_h, int64_t* ranges, int64_t* totals,
+    int32_t tiles_w, int32_t tiles_h, int64_t* ranges, int64_t* totals, int64_t* host_totals,
     void* plan, size_t plan_bytes, void* stream);
 GS_API size_t gs_bin_tiles_emit_bytes(int64_t n, int64_t total, int64_t row_entries,
                                       int64_t blocks, int32_t tiles_w, int32_t tiles_h);
 GS_API int gs_bin_tiles_emit(
-    const int32_t* bounds, const int32_t* counts, int64_t n, int32_t tiles_w, int32_t tiles_h,
+    const int32_t* bounds, int64_t n, int32_t tiles_w, int32_t tiles_h,
     const int64_t* totals, int64_t total, int64_t row_entries, int64_t blocks,
     void* plan, size_t plan_bytes, const int64_t* ranges, int32_t* sorted_ids,
     void* workspace, size_t workspace_bytes, void* stream);

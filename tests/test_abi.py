@@ -46,18 +46,18 @@ def test_bucketed_binning_host_checks():
     assert lib.gs_bin_tiles_plan_bytes(1000, 120, 68) > lib.gs_bin_tiles_plan_bytes(10, 120, 68)
     assert lib.gs_bin_tiles_plan_bytes(-1, 120, 68) == 0
     assert lib.gs_bin_tiles_emit_bytes(1000, 1 << 20, 1 << 18, 300, 120, 68) >= 3 * 4 * (1 << 18)
-    status = lib.gs_bin_tiles_plan(fake, fake, fake, 10, 257, 4, fake, fake, fake, 1 << 20, None)
+    status = lib.gs_bin_tiles_plan(fake, fake, fake, 10, 257, 4, fake, fake, None, fake, 1 << 20, None)
     assert status == nat.GS_ERR_UNSUPPORTED
     assert b"at most 256" in lib.gs_last_error()
-    status = lib.gs_bin_tiles_plan(fake, fake, fake, 10, 120, 68, fake, fake, fake, 16, None)
+    status = lib.gs_bin_tiles_plan(fake, fake, fake, 10, 120, 68, fake, fake, None, fake, 16, None)
     assert status == nat.GS_ERR_WORKSPACE
     # pass-B workgroups must match the intersection total (ceil(total / 4096) .. + rows)
     status = lib.gs_bin_tiles_emit(
-        fake, fake, 10, 120, 68, fake, 100000, 5000, 1, fake, 1 << 30, fake, fake, fake, 1 << 30, None
+        fake, 10, 120, 68, fake, 100000, 5000, 1, fake, 1 << 30, fake, fake, fake, 1 << 30, None
     )
     assert status == nat.GS_ERR_INVALID_ARGUMENT
     status = lib.gs_bin_tiles_emit(
-        fake, fake, 10, 120, 68, fake, 1 << 33, 5000, 1 << 22, fake, 1 << 30, fake, fake, fake, 1 << 30, None
+        fake, 10, 120, 68, fake, 1 << 33, 5000, 1 << 22, fake, 1 << 30, fake, fake, fake, 1 << 30, None
     )
     assert status == nat.GS_ERR_OVERFLOW
 

@@ -42,16 +42,22 @@ def parse_args():
     return ap.parse_args()
 
 
-def stage_bytes(n, k, total, num_tiles, pixels, processed_fwd, processed_bwd, sort_passes):
-    """Algorithmic HBM bytes per stage (the model of DESIGN.md)."""
+def stage_bytes(n, k, total, rows, pixels, processed_fwd, processed_bwd):
+    """Algorithmic HBM bytes per stage (n Gaussians with k SH coefficients,
+    `total` intersections, `rows` row-list entries; DESIGN.md lists the terms)."""
     return {
-        "project": n * (44 + 12 * k) + n * 52,
-        "bin": 4 * n * 8 * 2 + 8 * n,  # 4 passes over (key, id) + count scan
-        "emit": 16 * n + 8 * total,
-        "sort": total * 16 * sort_passes + 8 * total + 16 * num_tiles,
+        # params in (44 + 12k B) -> projected outputs, record, bounds, count, key (116 B)
+        "project": n * (44 + 12 * k) + 116 * n,
+        # depth sort: histogram + 4 passes of (key, id) in and out; rectangles
+        # for the tables; row-list offset scan (order, key, gathered rectangle)
+        "bin": 4 * n + 4 * 16 * n + 20 * n + 28 * n,
+        # pass A writes (id, packed columns) per row entry; the width scan
+        # reads and writes them; pass B reads its windows and writes one id
+        # per intersection
+        "emit": 8 * rows + 8 * rows + 8 * rows + 4 * total,
         "composite": 40 * processed_fwd + 20 * pixels,
-        "composite_bwd": 76 * processed_bwd + 32 * pixels,
-        "project_bwd": n * (44 + 12 * k) + 36 * n + n * (44 + 12 * k),
+        "composite_bwd": 76 * processed_bwd + 20 * pixels,
+        "project_bwd": 2 * n * (44 + 12 * k) + 56 * n,
     }
 
 
@@ -66,7 +72,7 @@ def run_step(splats, cam, target, tile_size, near, far):
 
 def staged_step(params, cam, target, tile_size, near, far):
     """One fwd+bwd through the stage functions with an event after each stage."""
-    from gaussian_splats.kernels.rasterize import composite_bwd, project_bwd
+    from gaussian_splats.kernels.rasterize import composite_bwd, project_and_count, project_bwd
     from gaussian_splats.kernels.rasterize.interface import forward_pipeline
 
     events = {}
@@ -96,8 +102,14 @@ def staged_step(params, cam, target, tile_size, near, far):
     torch.cuda.synchronize()
     order = ["start", "project", "bin", "emit", "sort", "composite", "loss", "composite_bwd", "project_bwd"]
     ms = {b: events[a].elapsed_time(events[b]) for a, b in zip(order[:-1], order[1:])}
+    # Row-list entries: tile rows covered by the Gaussians with intersections.
+    _, _, _, _, bounds, counts2 = project_and_count(*params, R, t, fx, fy, cx, cy, w, h, tile_size,
+                                                    near, far, "gaussian", 0.95)
+    b = bounds.view(-1, 4).long()
+    rows = int(((b[:, 3] - b[:, 2]) * (counts2 > 0)).sum())
     info = {
         "total": int(gids.numel()),
+        "rows": rows,
         "ranges": ranges,
         "ncon": ncon,
         "counts": counts,
@@ -207,13 +219,14 @@ def main():
     print("[bench] warmup done", file=sys.stderr, flush=True)
 
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        for p in splats.parameters():
-            p.grad = None
-        run_step(splats, cam, target, args.tile_size, scene.near, scene.far)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
+    with _native.LaunchTimer("composite_bwd") as timer:
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            for p in splats.parameters():
+                p.grad = None
+            run_step(splats, cam, target, args.tile_size, scene.near, scene.far)
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
     ms_per_step = 1e3 * elapsed / args.steps
     mpix = (w * h) / 1e6
     print(f"[bench] timed {args.steps} steps: {ms_per_step:.3f} ms/step", file=sys.stderr, flush=True)
@@ -225,10 +238,8 @@ def main():
         stage_runs.append(ms)
     stages_ms = {k: sum(r[k] for r in stage_runs) / len(stage_runs) for k in stage_runs[0]}
     fwd_pairs, bwd_pairs = processed_pairs(info["ranges"], info["ncon"], args.tile_size, w, h)
-    num_tiles = info["ranges"].shape[0]
-    sort_passes = max(1, math.ceil(max(1, (num_tiles - 1).bit_length()) / 8))
-    bytes_model = stage_bytes(scene.num_points, scene.color.shape[1], info["total"], num_tiles, w * h,
-                              fwd_pairs, bwd_pairs, sort_passes)
+    bytes_model = stage_bytes(scene.num_points, scene.color.shape[1], info["total"], info["rows"],
+                              w * h, fwd_pairs, bwd_pairs)
     stages = {}
     for name, ms in stages_ms.items():
         entry = {"ms": round(ms, 4)}
@@ -237,16 +248,25 @@ def main():
             entry.update({"algorithmic_bytes": bytes_model[name], "GB/s": round(gbs, 1),
                           "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)})
         stages[name] = entry
-    dominant = max((k for k in stages if k in bytes_model), key=lambda k: stages[k]["ms"])
-    dom = stages[dominant]
+
+    # Dominant kernel: composite_bwd_kernel, timed per launch with HIP events
+    # on its stream during the timed steps.
+    dominant_ms = timer.mean_ms()
+    achieved = bytes_model["composite_bwd"] / (dominant_ms * 1e-3) / 1e9
+    traffic = None
+    traffic_file = ROOT / "profiles" / "traffic_composite_bwd_config3.json"
+    if traffic_file.exists() and args.config == "config3" and args.tile_size == 16:
+        traffic = json.loads(traffic_file.read_text())["hbm_bytes_per_launch"]
     roofline = {
-        "kernel": dominant,
+        "kernel": "composite_bwd_kernel<16>" if args.tile_size == 16 else "composite_bwd_kernel",
         "bound": "hbm",
-        "achieved": dom["GB/s"],
+        "achieved": round(achieved, 1),
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
-        "frac": round(dom["GB/s"] / HBM_PEAK_GBS, 4),
-        "traffic": None,
+        "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "traffic": traffic,
+        "launch_ms": round(dominant_ms, 4),
+        "algorithmic_bytes": bytes_model["composite_bwd"],
     }
 
     cpu = None

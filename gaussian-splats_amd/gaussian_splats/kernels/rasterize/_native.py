@@ -199,6 +199,45 @@ def prepare(t: torch.Tensor, dtype: torch.dtype = torch.float32) -> torch.Tensor
     return t
 
 
+class LaunchTimer:
+    """Brackets every C-ABI launch of one entry point with timing events on
+    the stream it runs on, while active (``with LaunchTimer("composite_bwd")``).
+    Used by the benchmark to measure a kernel's per-launch duration in place."""
+
+    def __init__(self, name: str):
+        self.name = name
+        self.events: list[tuple[torch.cuda.Event, torch.cuda.Event]] = []
+
+    def __enter__(self) -> "LaunchTimer":
+        _TIMERS[self.name] = self
+        return self
+
+    def __exit__(self, *exc) -> None:
+        _TIMERS.pop(self.name, None)
+
+    def mean_ms(self) -> float:
+        torch.cuda.synchronize()
+        return sum(s.elapsed_time(e) for s, e in self.events) / max(1, len(self.events))
+
+
+_TIMERS: dict[str, LaunchTimer] = {}
+
+
+def launch(name: str, call):
+    """Runs ``call()`` (one C-ABI entry point), timed when a LaunchTimer for
+    ``name`` is active."""
+    timer = _TIMERS.get(name)
+    if timer is None:
+        return call()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    status = call()
+    end.record()
+    timer.events.append((start, end))
+    return status
+
+
 def host_floats(t: torch.Tensor, numel: int, name: str) -> torch.Tensor:
     """Contiguous float32 copy in host memory (the C-ABI passes camera
     extrinsics to the kernels by value); a GPU tensor costs one device sync."""

@@ -59,12 +59,16 @@ def composite_bwd(
         1.0, 1.0, 0.0, 0.0, image_width, image_height, tile_size,
         opacity_threshold=opacity_threshold,
     )
+    lib = nat.library()
     nat.check(
-        nat.library().gs_composite_bwd(
-            nat.ptr(projected_mean), nat.ptr(inverse_covariance), nat.ptr(projected_color),
-            nat.ptr(projected_opacity), nat.ptr(gaussian_ids), nat.ptr(ranges), nat.ptr(grad_image),
-            nat.ptr(final_transmittance), nat.ptr(n_contributors), view, nat.ptr(out),
-            nat.stream(device),
+        nat.launch(
+            "composite_bwd",
+            lambda: lib.gs_composite_bwd(
+                nat.ptr(projected_mean), nat.ptr(inverse_covariance), nat.ptr(projected_color),
+                nat.ptr(projected_opacity), nat.ptr(gaussian_ids), nat.ptr(ranges),
+                nat.ptr(grad_image), nat.ptr(final_transmittance), nat.ptr(n_contributors), view,
+                nat.ptr(out), nat.stream(device),
+            ),
         ),
         "composite_bwd",
     )

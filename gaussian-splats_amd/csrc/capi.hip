@@ -53,6 +53,7 @@ constexpr int kMaxDevices = 64;
 struct SideStream {
   hipStream_t stream = nullptr;
   hipEvent_t fork = nullptr;
+  hipEvent_t mark = nullptr;
   hipEvent_t join = nullptr;
 };
 SideStream g_side[kMaxDevices];
@@ -78,6 +79,7 @@ int fork_side_stream(hipStream_t main, SideFork& f) {
     // Default priority; the stream does not synchronise with the null stream.
     const bool ok = hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking) == hipSuccess &&
                     hipEventCreateWithFlags(&s.fork, hipEventDisableTiming) == hipSuccess &&
+                    hipEventCreateWithFlags(&s.mark, hipEventDisableTiming) == hipSuccess &&
                     hipEventCreateWithFlags(&s.join, hipEventDisableTiming) == hipSuccess;
     if (switch_device) (void)hipSetDevice(current);
     GS_REQUIRE(ok, GS_ERR_HIP, "could not create the side stream");
@@ -87,7 +89,20 @@ int fork_side_stream(hipStream_t main, SideFork& f) {
              GS_ERR_HIP, "side stream fork failed");
   f.main = main;
   f.side = s.stream;
+  f.mark = s.mark;
   f.join = s.join;
+  return GS_OK;
+}
+
+int record_side_mark(SideFork& f) {
+  GS_REQUIRE(hipEventRecord(f.mark, f.side) == hipSuccess, GS_ERR_HIP,
+             "side stream mark failed");
+  return GS_OK;
+}
+
+int wait_side_mark(SideFork& f) {
+  GS_REQUIRE(hipStreamWaitEvent(f.main, f.mark, 0) == hipSuccess, GS_ERR_HIP,
+             "side stream wait failed");
   return GS_OK;
 }
 

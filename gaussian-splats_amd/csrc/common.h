@@ -28,10 +28,16 @@ int check_launch(const char* what);
 struct SideFork {
   hipStream_t main = nullptr;
   hipStream_t side = nullptr;
+  hipEvent_t mark = nullptr;
   hipEvent_t join = nullptr;
   std::unique_lock<std::mutex> lock;
 };
 int fork_side_stream(hipStream_t main, SideFork& f);
+// One intermediate dependency: record_side_mark marks the side stream's work
+// enqueued so far; work enqueued on the caller's stream after
+// wait_side_mark waits for it.
+int record_side_mark(SideFork& f);
+int wait_side_mark(SideFork& f);
 // Joins the side stream back into the caller's; with host_wait the host also
 // waits for the side stream's work (not the caller's) before returning.
 int join_side_stream(SideFork& f, bool host_wait = false);

@@ -44,15 +44,28 @@ constexpr int kPrivateTableWords = 12288;
 // Tables.
 // ---------------------------------------------------------------------------
 
+// Per-Gaussian tile rectangle packed in 32 bits (grids of at most 256 x 256
+// tiles): x0 | (width - 1) << 8 | y0 << 16 | (height - 1) << 24, or kNoRect
+// for a Gaussian without intersections.  The 4 MB array for 1M Gaussians
+// stays cache resident, so the depth-ordered passes gather 4 B from it
+// instead of 16 B rectangles and 4 B counts from separate lines.
+constexpr uint32_t kNoRect = 0xFFFFFFFFu;  // width 256 at x0 = 255 cannot occur
+
+__device__ __forceinline__ uint32_t pack_rect(int x0, int w, int y0, int h) {
+  return uint32_t(x0) | (uint32_t(w - 1) << 8) | (uint32_t(y0) << 16) | (uint32_t(h - 1) << 24);
+}
+
 // Corners of each counted Gaussian's rectangle [x0, x1) x [y0, y1) in the 2-D
 // difference array diff2 (th + 1 rows of pitch tw + 1) and ends of its rows in
-// the 1-D difference array rowdiff (th + 1).
+// the 1-D difference array rowdiff (th + 1); writes every Gaussian's packed
+// rectangle.
 template <bool PRIVATE>
 __global__ __launch_bounds__(256) void rect_diff_kernel(const int4* __restrict__ bounds,
                                                         const int32_t* __restrict__ counts,
                                                         int64_t n, int tw, int th,
                                                         int32_t* __restrict__ diff2,
-                                                        int32_t* __restrict__ rowdiff) {
+                                                        int32_t* __restrict__ rowdiff,
+                                                        uint32_t* __restrict__ packed) {
   extern __shared__ int32_t lds[];
   const int pitch = tw + 1;
   const int words = (th + 1) * pitch;
@@ -76,12 +89,13 @@ __global__ __launch_bounds__(256) void rect_diff_kernel(const int4* __restrict__
     }
 #pragma unroll
     for (int i = 0; i < kBatch; ++i) {
-      if (cnt[i] > 0) {
-        // x0, x1, y0, y1 (inside the grid when they come from the projection;
-        // clamped so that no other input indexes out of the tables)
-        const int4 b = rect[i];
-        const int x0 = min(max(b.x, 0), tw), x1 = min(max(b.y, 0), tw);
-        const int y0 = min(max(b.z, 0), th), y1 = min(max(b.w, 0), th);
+      // x0, x1, y0, y1 (inside the grid when they come from the projection;
+      // clamped so that no other input indexes out of the tables)
+      const int4 b = rect[i];
+      const int x0 = min(max(b.x, 0), tw), x1 = min(max(b.y, 0), tw);
+      const int y0 = min(max(b.z, 0), th), y1 = min(max(b.w, 0), th);
+      const bool counted = cnt[i] > 0 && x1 > x0 && y1 > y0;
+      if (counted) {
         atomicAdd(&t2[y0 * pitch + x0], 1);
         atomicAdd(&t2[y0 * pitch + x1], -1);
         atomicAdd(&t2[y1 * pitch + x0], -1);
@@ -89,6 +103,8 @@ __global__ __launch_bounds__(256) void rect_diff_kernel(const int4* __restrict__
         atomicAdd(&tr[y0], 1);
         atomicAdd(&tr[y1], -1);
       }
+      const int64_t g = g0 + i * stride;
+      if (g < n) packed[g] = counted ? pack_rect(x0, x1 - x0, y0, y1 - y0) : kNoRect;
     }
   }
   __syncthreads();
@@ -215,21 +231,16 @@ __device__ __forceinline__ uint32_t entry_row(uint32_t xw) { return (xw >> 16) &
 // Row-list entries per Gaussian in depth order: its tile-row count, 0 if it
 // has no intersections.
 struct HeightLoad {
-  const int4* bounds;
-  const int32_t* counts;
+  const uint32_t* packed;
   const int32_t* order;
-  __device__ uint32_t height(int g) const {
-    if (counts[g] <= 0) return 0u;
-    const int4 b = bounds[g];
-    return uint32_t(b.w - b.z);
-  }
-  __device__ uint32_t operator()(int64_t i) const { return height(order[i]); }
+  __device__ static uint32_t height(uint32_t r) { return r == kNoRect ? 0u : (r >> 24) + 1u; }
+  __device__ uint32_t operator()(int64_t i) const { return height(packed[order[i]]); }
   __device__ void load4(int64_t i, uint32_t (&v)[4]) const {
     const int4 o = *reinterpret_cast<const int4*>(order + i);
-    v[0] = height(o.x);
-    v[1] = height(o.y);
-    v[2] = height(o.z);
-    v[3] = height(o.w);
+    v[0] = height(packed[o.x]);
+    v[1] = height(packed[o.y]);
+    v[2] = height(packed[o.z]);
+    v[3] = height(packed[o.w]);
   }
 };
 
@@ -470,11 +481,12 @@ __device__ int load_window(const uint32_t* __restrict__ offs, int64_t first, int
 // expansion (Gaussian order[p] owns entries [offs[p], offs[p + 1]), one per
 // covered tile row), bucketed by tile row.  The first owner comes from
 // first_a (recorded by the height scan), the last one from the next
-// workgroup's first owner (a search for the final workgroup).  Writes each
-// entry's Gaussian id and packed first column / width / row.
+// workgroup's first owner (a search for the final workgroup).  Reads the
+// packed rectangles; writes each entry's Gaussian id and packed first column /
+// width / row.
 template <int BITS>
 __global__ __launch_bounds__(kBlock) void row_bucket_kernel(
-    const int4* __restrict__ bounds, const int32_t* __restrict__ order,
+    const uint32_t* __restrict__ packed, const int32_t* __restrict__ order,
     const uint32_t* __restrict__ offs, const uint32_t* __restrict__ first_a, int64_t n,
     uint32_t entries, int th, const uint32_t* __restrict__ row_a,
     const int64_t* __restrict__ totals, uint32_t* __restrict__ out_g,
@@ -520,11 +532,11 @@ __global__ __launch_bounds__(kBlock) void row_bucket_kernel(
     const int e = wid * kSeg + i * 64 + lane;
     const int k = sh.own[e];
     const int g = order[p_first + k];
-    const int4 bb = bounds[g];
-    const uint32_t ty = uint32_t(bb.z + (e - rel[k])) & ((1u << BITS) - 1u);
+    const uint32_t r = packed[g];
+    const uint32_t ty = (((r >> 16) & 0xFFu) + uint32_t(e - rel[k])) & ((1u << BITS) - 1u);
     dig[i] = e < nvalid ? ty : 0u;
     val[0][i] = uint32_t(g);
-    val[1][i] = pack_entry(bb.x, bb.y - bb.x, int(ty));
+    val[1][i] = (r & 0xFFFFu) | (ty << 16);  // first column, width - 1, row
   }
   uint32_t* const out[2] = {out_g, out_xw};
   place_items<BITS, 2>(
@@ -598,12 +610,12 @@ __global__ __launch_bounds__(kBlock) void column_bucket_kernel(
 }
 
 template <int BITS>
-void launch_row_bucket(unsigned blocks, const int4* bounds, const int32_t* order,
+void launch_row_bucket(unsigned blocks, const uint32_t* packed, const int32_t* order,
                        const uint32_t* offs, const uint32_t* first_a, int64_t n, uint32_t entries,
                        int th, const uint32_t* row_a, const int64_t* totals, uint32_t* out_g,
                        uint32_t* out_xw, uint64_t* status, uint32_t* ticket, uint32_t* err,
                        hipStream_t s) {
-  row_bucket_kernel<BITS><<<blocks, kBlock, 0, s>>>(bounds, order, offs, first_a, n, entries, th,
+  row_bucket_kernel<BITS><<<blocks, kBlock, 0, s>>>(packed, order, offs, first_a, n, entries, th,
                                                     row_a, totals, out_g, out_xw, status, ticket,
                                                     err);
 }
@@ -625,6 +637,7 @@ int axis_bits(int tiles) { return std::max(1, bits_for(tiles)); }
 // Persistent plan (written by gs_bin_tiles_plan, read by gs_bin_tiles_emit).
 struct PlanLayout {
   int32_t* order = nullptr;    // [n] depth order
+  uint32_t* packed = nullptr;  // [n] packed tile rectangles (pack_rect)
   uint32_t* offs = nullptr;    // [n + 1] row-list offsets in depth order (written by emit)
   uint32_t* row_a = nullptr;   // [th + 1]
   uint32_t* row_e = nullptr;   // [th + 1]
@@ -647,6 +660,7 @@ PlanLayout plan_layout(void* base, int64_t n, int tw, int th) {
     return r;
   };
   p.order = reinterpret_cast<int32_t*>(take(size_t(n) * 4));
+  p.packed = reinterpret_cast<uint32_t*>(take(size_t(n) * 4));
   p.offs = reinterpret_cast<uint32_t*>(take(size_t(n + 1) * 4));
   p.row_a = reinterpret_cast<uint32_t*>(take(size_t(th + 1) * 4));
   p.row_e = reinterpret_cast<uint32_t*>(take(size_t(th + 1) * 4));
@@ -760,12 +774,16 @@ GS_API int gs_bin_tiles_plan(uint32_t* depth_keys, const int32_t* bounds, const 
     int32_t* rowdiff = p.table + words;
     if (words + tiles_h + 1 <= kPrivateTableWords) {
       rect_diff_kernel<true><<<blocks, 256, size_t(words + tiles_h + 1) * 4, fork.side>>>(
-          reinterpret_cast<const int4*>(bounds), counts, n, tiles_w, tiles_h, diff2, rowdiff);
+          reinterpret_cast<const int4*>(bounds), counts, n, tiles_w, tiles_h, diff2, rowdiff,
+          p.packed);
     } else {
       rect_diff_kernel<false><<<blocks, 256, size_t(tiles_h + 1) * 4, fork.side>>>(
-          reinterpret_cast<const int4*>(bounds), counts, n, tiles_w, tiles_h, diff2, rowdiff);
+          reinterpret_cast<const int4*>(bounds), counts, n, tiles_w, tiles_h, diff2, rowdiff,
+          p.packed);
     }
   }
+  // The row-list scan on the caller's stream reads the packed rectangles.
+  int status = n > 0 ? record_side_mark(fork) : GS_OK;
   const int lds_words = tiles_h * (tiles_w + 1);
   if (lds_words <= kPrivateTableWords) {
     tables_kernel<true><<<1, 256, size_t(lds_words) * 4, fork.side>>>(
@@ -774,7 +792,7 @@ GS_API int gs_bin_tiles_plan(uint32_t* depth_keys, const int32_t* bounds, const 
     tables_kernel<false><<<1, 256, 0, fork.side>>>(p.table, p.table + words, tiles_w, tiles_h,
                                                    ranges, p.row_a, p.row_e, p.row_blk, totals);
   }
-  int status = check_launch("bin_tiles_plan (tables)");
+  if (status == GS_OK) status = check_launch("bin_tiles_plan (tables)");
   if (host_totals && status == GS_OK &&
       hipMemcpyAsync(host_totals, totals, 4 * sizeof(int64_t), hipMemcpyDeviceToHost,
                      fork.side) != hipSuccess) {
@@ -789,10 +807,10 @@ GS_API int gs_bin_tiles_plan(uint32_t* depth_keys, const int32_t* bounds, const 
     status = radix_sort<uint32_t>(depth_keys, nullptr, n, 32,
                                   reinterpret_cast<uint32_t*>(p.order), &sorted_keys, ws, s);
     // Row-list offsets in depth order, recording each pass-A workgroup's
-    // first owner.
+    // first owner; they read the packed rectangles written on the side stream.
+    if (status == GS_OK) status = wait_side_mark(fork);
     if (status == GS_OK)
-      launch_scan<uint32_t>(HeightLoad{reinterpret_cast<const int4*>(bounds), counts, p.order},
-                            n, p.offs, true, true, ws, s,
+      launch_scan<uint32_t>(HeightLoad{p.packed, p.order}, n, p.offs, true, true, ws, s,
                             HeightSink{p.first_a, p.first_a_capacity});
   }
   // Always join, also after an error; with host_totals the host waits for
@@ -810,7 +828,7 @@ GS_API size_t gs_bin_tiles_emit_bytes(int64_t n, int64_t total, int64_t row_entr
   return emit_layout(nullptr, row_entries, blocks, tiles_w, tiles_h).bytes;
 }
 
-GS_API int gs_bin_tiles_emit(const int32_t* bounds, int64_t n,
+GS_API int gs_bin_tiles_emit(int64_t n,
                              int32_t tiles_w, int32_t tiles_h, const int64_t* totals,
                              int64_t total, int64_t row_entries, int64_t blocks, void* plan,
                              size_t plan_bytes, const int64_t* ranges, int32_t* sorted_ids,
@@ -826,9 +844,8 @@ GS_API int gs_bin_tiles_emit(const int32_t* bounds, int64_t n,
   if (total == 0) return GS_OK;
   GS_REQUIRE(n > 0 && row_entries > 0 && blocks > 0, GS_ERR_INVALID_ARGUMENT,
              "intersections without Gaussians");
-  GS_REQUIRE(bounds && totals && plan && ranges && sorted_ids && workspace &&
-                 aligned16(bounds),
-             GS_ERR_INVALID_ARGUMENT, "null or misaligned pointer");
+  GS_REQUIRE(totals && plan && ranges && sorted_ids && workspace, GS_ERR_INVALID_ARGUMENT,
+             "null pointer argument");
   const PlanLayout p = plan_layout(plan, n, tiles_w, tiles_h);
   GS_REQUIRE(plan_bytes >= p.bytes, GS_ERR_WORKSPACE, "plan workspace too small");
   const EmitLayout e = emit_layout(workspace, row_entries, blocks, tiles_w, tiles_h);
@@ -844,11 +861,11 @@ GS_API int gs_bin_tiles_emit(const int32_t* bounds, int64_t n,
   uint32_t* ticket_w = e.small + 2;
   uint32_t* err = e.small + 4;  // err[0] pass A, err[1] pass B, err[2] width scan
   const unsigned blocks_a = unsigned(ceil_div(row_entries, kTile));
-  const int4* b4 = reinterpret_cast<const int4*>(bounds);
   switch (axis_bits(tiles_h)) {
 #define GS_ROW_CASE(B)                                                                          \
   case B:                                                                                       \
-    launch_row_bucket<B>(blocks_a, b4, p.order, p.offs, p.first_a, n, uint32_t(row_entries),    \
+    launch_row_bucket<B>(blocks_a, p.packed, p.order, p.offs, p.first_a, n,                     \
+                         uint32_t(row_entries),                                                 \
                          tiles_h, p.row_a, totals, e.rl_g, e.rl_xw, e.status_a, ticket_a, err,  \
                          s);                                                                    \
     break;

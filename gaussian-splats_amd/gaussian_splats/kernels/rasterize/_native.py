@@ -109,7 +109,7 @@ _SIGNATURES = {
     "gs_bin_tiles_emit_bytes": (c_size_t, [c_int64, c_int64, c_int64, c_int64, c_int32, c_int32]),
     "gs_bin_tiles_emit": (
         c_int,
-        [c_void_p, c_int64, c_int32, c_int32, c_void_p, c_int64, c_int64, c_int64,
+        [c_int64, c_int32, c_int32, c_void_p, c_int64, c_int64, c_int64,
          c_void_p, c_size_t, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p],
     ),
     "gs_composite": (c_int, [c_void_p, c_void_p, c_void_p, GsView, c_void_p, c_void_p, c_void_p, c_void_p]),

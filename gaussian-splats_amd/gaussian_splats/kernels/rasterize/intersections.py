@@ -189,7 +189,7 @@ def bin_tiles(
         )
         nat.check(
             lib.gs_bin_tiles_emit(
-                nat.ptr(bounds), n, tiles_w, tiles_h, nat.ptr(totals), total,
+                n, tiles_w, tiles_h, nat.ptr(totals), total,
                 row_entries, blocks, nat.ptr(plan), plan.numel(), nat.ptr(ranges),
                 nat.ptr(sorted_ids), nat.ptr(ws), ws.numel(), s,
             ),

@@ -177,8 +177,8 @@ GS_API int gs_sort_tiles(
  * there: the tables are built on a side stream, so the host waits for them
  * while the depth sort still runs on `stream`.  `plan` (plan_bytes from
  * gs_bin_tiles_plan_bytes) must stay alive until gs_bin_tiles_emit, which
- * takes the same bounds, the totals (device pointer and the values read from
- * it) and writes `sorted_ids` [totals[0]].  depth_keys (as
+ * takes the totals (device pointer and the values read from it) and writes
+ * `sorted_ids` [totals[0]].  depth_keys (as
  * gs_project_and_count writes them: ~0u for Gaussians without
  * intersections) is consumed.  Together they replace intersections.py:44-88
  * for the op. */
@@ -190,7 +190,7 @@ GS_API int gs_bin_tiles_plan(
 GS_API size_t gs_bin_tiles_emit_bytes(int64_t n, int64_t total, int64_t row_entries,
                                       int64_t blocks, int32_t tiles_w, int32_t tiles_h);
 GS_API int gs_bin_tiles_emit(
-    const int32_t* bounds, int64_t n, int32_t tiles_w, int32_t tiles_h,
+    int64_t n, int32_t tiles_w, int32_t tiles_h,
     const int64_t* totals, int64_t total, int64_t row_entries, int64_t blocks,
     void* plan, size_t plan_bytes, const int64_t* ranges, int32_t* sorted_ids,
     void* workspace, size_t workspace_bytes, void* stream);

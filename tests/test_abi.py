@@ -53,11 +53,11 @@ def test_bucketed_binning_host_checks():
     assert status == nat.GS_ERR_WORKSPACE
     # pass-B workgroups must match the intersection total (ceil(total / 4096) .. + rows)
     status = lib.gs_bin_tiles_emit(
-        fake, 10, 120, 68, fake, 100000, 5000, 1, fake, 1 << 30, fake, fake, fake, 1 << 30, None
+        10, 120, 68, fake, 100000, 5000, 1, fake, 1 << 30, fake, fake, fake, 1 << 30, None
     )
     assert status == nat.GS_ERR_INVALID_ARGUMENT
     status = lib.gs_bin_tiles_emit(
-        fake, 10, 120, 68, fake, 1 << 33, 5000, 1 << 22, fake, 1 << 30, fake, fake, fake, 1 << 30, None
+        10, 120, 68, fake, 1 << 33, 5000, 1 << 22, fake, 1 << 30, fake, fake, fake, 1 << 30, None
     )
     assert status == nat.GS_ERR_OVERFLOW
 

@@ -219,7 +219,7 @@ def main():
     print("[bench] warmup done", file=sys.stderr, flush=True)
 
     torch.cuda.synchronize()
-    with _native.LaunchTimer("composite_bwd") as timer:
+    with _native.LaunchTimer("composite_bwd", capacity=args.steps + 1) as timer:
         t0 = time.perf_counter()
         for _ in range(args.steps):
             for p in splats.parameters():

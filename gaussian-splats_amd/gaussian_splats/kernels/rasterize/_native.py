@@ -204,9 +204,19 @@ class LaunchTimer:
     the stream it runs on, while active (``with LaunchTimer("composite_bwd")``).
     Used by the benchmark to measure a kernel's per-launch duration in place."""
 
-    def __init__(self, name: str):
+    def __init__(self, name: str, capacity: int = 256):
         self.name = name
         self.events: list[tuple[torch.cuda.Event, torch.cuda.Event]] = []
+        # Created up front, so a timed launch only records two events.
+        self._pool = [
+            (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            for _ in range(capacity)
+        ]
+
+    def next_pair(self) -> tuple[torch.cuda.Event, torch.cuda.Event]:
+        if self._pool:
+            return self._pool.pop()
+        return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
     def __enter__(self) -> "LaunchTimer":
         _TIMERS[self.name] = self
@@ -229,8 +239,7 @@ def launch(name: str, call):
     timer = _TIMERS.get(name)
     if timer is None:
         return call()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
+    start, end = timer.next_pair()
     start.record()
     status = call()
     end.record()

@@ -15,10 +15,8 @@ import torch
 
 from . import _native as nat
 from .composite import composite
-from .composite_bwd import composite_bwd
 from .intersections import MAX_BUCKET_TILES, bin_gaussians, bin_tiles, emit_tiles, sort_tiles
 from .project import _check_tile, project_and_count
-from .project_bwd import project_bwd
 
 if TYPE_CHECKING:  # the splat API imports this module, so only for annotations
     from ...splats.camera import Camera
@@ -182,14 +180,39 @@ def _setup_context(ctx, inputs, output) -> None:
         ctx.rendering_mode,
         ctx.confidence,
     ) = inputs[7:]
+    # Prepared here, while the GPU still runs the forward, so the backward
+    # launches its kernels without host work in front of them: the zeroed
+    # [N, 9] gradient buffer the compositing backward accumulates into, the
+    # camera extrinsics in host memory and the two views.
+    mean = inputs[0]
+    if mean.is_cuda and ctx.rendering_mode == "gaussian":
+        ctx.grad_projected = torch.zeros((mean.shape[0], 9), dtype=torch.float32, device=mean.device)
+        ctx.camera_host = (
+            nat.host_floats(inputs[5], 9, "camera_rotation"),
+            nat.host_floats(inputs[6], 3, "camera_translation"),
+        )
+        ctx.view_composite = nat.make_view(
+            1.0, 1.0, 0.0, 0.0, ctx.image_width, ctx.image_height, ctx.tile_size,
+            opacity_threshold=ctx.opacity_threshold,
+        )
+        ctx.view_project = nat.make_view(ctx.fx, ctx.fy, 0.0, 0.0, ctx.image_width, ctx.image_height)
+    else:
+        ctx.grad_projected = None
+
+
+def _contiguous(t: torch.Tensor) -> torch.Tensor:
+    return t if t.is_contiguous() and t.data_ptr() % 16 == 0 else t.contiguous()
 
 
 def _backward(ctx, *grad_outputs):
-    """composite_bwd -> project_bwd; gradients for the first five inputs."""
+    """composite_bwd -> project_bwd; gradients for the first five inputs.
+
+    Calls the C-ABI directly: every tensor but the incoming image gradient was
+    produced (contiguous, aligned, on the device) by the forward."""
     if ctx.rendering_mode != "gaussian":
         raise AssertionError("Backward gradients are only supported for Gaussian rendering.")
-    grad_image = grad_outputs[0]
-    mean, rotation, scale, opacity, color, camera_rotation, camera_translation = ctx.saved_tensors[:7]
+    saved = ctx.saved_tensors
+    mean, rotation, scale, opacity, color = (_contiguous(t) for t in saved[:5])
     (
         final_transmittance,
         n_contributors,
@@ -200,22 +223,49 @@ def _backward(ctx, *grad_outputs):
         gaussian_ids,
         ranges,
         counts,
-    ) = ctx.saved_tensors[7:]
+    ) = saved[7:]
+    device = mean.device
+    n = mean.shape[0]
+    grad_image = grad_outputs[0]
     if grad_image is None:
         grad_image = torch.zeros(
-            (ctx.image_height, ctx.image_width, 3), dtype=mean.dtype, device=mean.device
+            (ctx.image_height, ctx.image_width, 3), dtype=torch.float32, device=device
         )
-    grad_projected = composite_bwd(
-        projected_mean, inverse_covariance, projected_color, projected_opacity, gaussian_ids,
-        ranges, grad_image, final_transmittance, n_contributors, ctx.image_width,
-        ctx.image_height, ctx.tile_size, ctx.opacity_threshold, ctx.rendering_mode,
+    elif grad_image.dtype != torch.float32:
+        grad_image = grad_image.float().contiguous()
+    else:
+        grad_image = _contiguous(grad_image)
+    grad_projected = ctx.grad_projected
+    if grad_projected is None:  # a second backward through the same graph
+        grad_projected = torch.zeros((n, 9), dtype=torch.float32, device=device)
+    ctx.grad_projected = None
+    lib = nat.library()
+    stream = nat.stream(device)
+    ptr = nat.ptr
+    nat.check(
+        nat.launch(
+            "composite_bwd",
+            lambda: lib.gs_composite_bwd(
+                ptr(projected_mean), ptr(inverse_covariance), ptr(projected_color),
+                ptr(projected_opacity), ptr(gaussian_ids), ptr(ranges), ptr(grad_image),
+                ptr(final_transmittance), ptr(n_contributors), ctx.view_composite,
+                ptr(grad_projected), stream,
+            ),
+        ),
+        "composite_bwd",
     )
-    gradients = project_bwd(
-        mean, rotation, scale, opacity, color, camera_rotation, camera_translation,
-        inverse_covariance, grad_projected, counts, ctx.fx, ctx.fy, ctx.image_width,
-        ctx.image_height,
-    )
-    return (*gradients, *(None,) * (19 - len(gradients)))
+    grads = tuple(torch.empty_like(t) for t in (mean, rotation, scale, opacity, color))
+    if n:
+        cam_r, cam_t = ctx.camera_host
+        nat.check(
+            lib.gs_project_bwd(
+                ptr(mean), ptr(rotation), ptr(scale), ptr(opacity), ptr(color), n,
+                color.shape[1], ptr(cam_r), ptr(cam_t), ctx.view_project, ptr(inverse_covariance),
+                ptr(grad_projected), ptr(counts), *(ptr(g) for g in grads), stream,
+            ),
+            "project_bwd",
+        )
+    return (*grads, *(None,) * 14)
 
 
 torch.library.register_autograd(

@@ -5,7 +5,8 @@
 // sequential transmittance and contributor count of composite.py:44-107:
 //   alpha = min(o * exp(-D/2), 0.99), zeroed below 1/255;
 //   a pixel is active for an entry while (1 - T) < opacity_threshold, checked
-//   before blending; C += T * alpha * rgb; T *= (1 - alpha) while active;
+//   before blending (as T > 1 - opacity_threshold); C += T * alpha * rgb;
+//   T *= (1 - alpha) while active (as T - T alpha);
 //   n_contributors = entries processed while active (the position after the
 //   entry that deactivated the pixel, or the list length).
 // Integer pixel coordinates (no +0.5, torch.py:157-168), black background.
@@ -28,6 +29,8 @@ struct CompositeArgs {
   const int64_t* ranges;
   int width, height, tile, tiles_w, num_tiles;
   float threshold;
+  // A pixel stays active while (1 - T) < threshold, i.e. T > 1 - threshold.
+  float t_active;
   float* image;
   float* final_t;
   int32_t* n_contrib;
@@ -90,6 +93,8 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_fwd_kernel(Comp
       mine = lane_splat(rec);
     }
     uint64_t mask = __ballot(keep);
+    // No break inside: the loop ends through its condition, which keeps the
+    // per-pixel active flags out of extra mask-merging control flow.
     while (mask) {
       const int j = __builtin_ctzll(mask);
       mask &= mask - 1;
@@ -97,7 +102,7 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_fwd_kernel(Comp
       const int pos = int(base - start) + j;
       const ColumnTerms c = column_terms(s, pxf);
       // Branch-free: a finished pixel (or a cut alpha) blends with alpha = 0,
-      // which leaves its colour and T unchanged.
+      // which leaves its colour and T unchanged.  T (1 - alpha) = T - w.
 #pragma unroll
       for (int k = 0; k < PIX; ++k) {
         float prob;
@@ -107,14 +112,14 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_fwd_kernel(Comp
         cr[k] += w * s.r;
         cg[k] += w * s.g;
         cb[k] += w * s.bl;
-        T[k] = T[k] * (1.0f - alpha);
-        const bool done = live[k] && !((1.0f - T[k]) < a.threshold);
+        T[k] = T[k] - w;
+        const bool done = live[k] && !(T[k] > a.t_active);
         ncon[k] = done ? pos + 1 : ncon[k];
         live[k] = live[k] && !done;
       }
       if (!any_live()) {
         running = false;
-        break;
+        mask = 0;
       }
     }
   }
@@ -168,6 +173,7 @@ extern "C" GS_API int gs_composite(const void* records, const int32_t* gaussian_
   a.tiles_w = tiles_along(view.image_width, view.tile_size);
   a.num_tiles = a.tiles_w * tiles_along(view.image_height, view.tile_size);
   a.threshold = view.opacity_threshold;
+  a.t_active = float(1.0 - double(view.opacity_threshold));
   a.image = image;
   a.final_t = final_transmittance;
   a.n_contrib = n_contributors;

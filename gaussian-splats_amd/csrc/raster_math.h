@@ -90,25 +90,28 @@ __device__ __forceinline__ float blend_alpha(float raw) {
 // [x0, x1] x [y0, y1] (continuous, so no larger than over the integer pixels).
 // The form is positive definite, so the minimum is 0 when the mean is inside
 // and otherwise lies on an edge, where it is the clamped vertex of a parabola.
+// The vertices use v_rcp_f32 reciprocals: an inexact vertex only raises the
+// value found by a second-order amount, far below the margin callers add.
 __device__ __forceinline__ float min_quad_over_rect(float a, float b, float c, float u, float v,
                                                     float x0, float x1, float y0, float y1) {
   const float lx = x0 - u, hx = x1 - u, ly = y0 - v, hy = y1 - v;
   if (lx <= 0.0f && hx >= 0.0f && ly <= 0.0f && hy >= 0.0f) return 0.0f;
   if (!(a > 0.0f) || !(c > 0.0f)) return 0.0f;  // degenerate: never skip
+  const float nbc = -b * __builtin_amdgcn_rcpf(c), nba = -b * __builtin_amdgcn_rcpf(a);
   float best = 3.0e38f;
   const float ex[2] = {lx, hx};
   const float ey[2] = {ly, hy};
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const float dx = ex[i];
-    const float dy = fminf(fmaxf(-b * dx / c, ly), hy);
-    best = fminf(best, a * dx * dx + 2.0f * b * dx * dy + c * dy * dy);
+    const float dy = fminf(fmaxf(nbc * dx, ly), hy);
+    best = fminf(best, dx * (a * dx + 2.0f * b * dy) + c * dy * dy);
   }
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const float dy = ey[i];
-    const float dx = fminf(fmaxf(-b * dy / a, lx), hx);
-    best = fminf(best, a * dx * dx + 2.0f * b * dx * dy + c * dy * dy);
+    const float dx = fminf(fmaxf(nba * dy, lx), hx);
+    best = fminf(best, dx * (a * dx + 2.0f * b * dy) + c * dy * dy);
   }
   return best;
 }

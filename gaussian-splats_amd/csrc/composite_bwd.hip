@@ -118,6 +118,8 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_bwd_kernel(Comp
       // sum unchanged.
 #pragma unroll
       for (int k = 0; k < PIX; ++k) {
+        // A band of 64 pixels none of which processed this entry is skipped.
+        if (__ballot(pos < ncon[k]) == 0) continue;
         const float dy = pyf[k] - s.v;
         float prob;
         const float raw = raw_alpha<false>(s, c, dy, prob);

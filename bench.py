@@ -1,6 +1,6 @@
 """Benchmark of the HIP rasterizer on one MI355X.
 
-A step is one training pass of the north-star workload:
+A step is one training pass of the headline workload (scenes.CONFIGS['config3']):
 render 1M SH-3 Gaussians at 1920x1080, mean |image - target| loss, backward to
 all Gaussian parameters.  Inputs are resident in HBM before timing.  Prints one
 JSON line with the whole-job Mpix/s, per-stage milliseconds from HIP events,
@@ -44,7 +44,7 @@ def parse_args():
 
 def stage_bytes(n, k, total, rows, pixels, processed_fwd, processed_bwd):
     """Algorithmic HBM bytes per stage (n Gaussians with k SH coefficients,
-    `total` intersections, `rows` row-list entries; DESIGN.md lists the terms)."""
+    `total` intersections, `rows` row-list entries)."""
     return {
         # params in (44 + 12k B) -> projected outputs, record, bounds, count, key (116 B)
         "project": n * (44 + 12 * k) + 116 * n,
@@ -63,9 +63,10 @@ def stage_bytes(n, k, total, rows, pixels, processed_fwd, processed_bwd):
 
 def run_step(splats, cam, target, tile_size, near, far):
     from gaussian_splats.splats import rasterize
+    from gaussian_splats.training import l1_loss
 
     image = rasterize(splats, cam, tile_size=tile_size, near=near, far=far)
-    loss = (image - target).abs().mean()
+    loss = l1_loss(image, target)  # mean |image - target|, one fused kernel each way
     loss.backward()
     return loss
 
@@ -74,6 +75,7 @@ def staged_step(params, cam, target, tile_size, near, far):
     """One fwd+bwd through the stage functions with an event after each stage."""
     from gaussian_splats.kernels.rasterize import composite_bwd, project_and_count, project_bwd
     from gaussian_splats.kernels.rasterize.interface import forward_pipeline
+    from gaussian_splats.training import l1_loss_backward, l1_loss_forward
 
     events = {}
 
@@ -85,13 +87,14 @@ def staged_step(params, cam, target, tile_size, near, far):
     fx, fy = cam.focal_length
     cx, cy = cam.principal_point
     w, h = cam.image_size
+    one = torch.ones((), dtype=torch.float32, device=params[0].device)
     R = cam.rotation_matrix.float()  # host memory: passed to the kernels by value
     t = cam.translation.float()
     out = forward_pipeline(*params, R, t, fx, fy, cx, cy, w, h, tile_size, 0.999, near, far,
                            "gaussian", 0.95, timer=mark)
     image, final_t, ncon, pmean, pinv, pcol, pop, gids, ranges, counts = out
-    diff = image - target
-    grad_image = torch.sign(diff) / diff.numel()
+    _, code = l1_loss_forward(image, target)
+    grad_image = l1_loss_backward(code, one)
     grad_proj = torch.zeros((pmean.shape[0], 9), dtype=torch.float32, device=pmean.device)
     mark("loss")
     composite_bwd(pmean, pinv, pcol, pop, gids, ranges, grad_image, final_t, ncon, w, h,
@@ -193,7 +196,8 @@ def main():
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
-              "(the rasterizer runs on a single device, see DESIGN.md for how it would shard)",
+              "(the rasterizer runs on a single device; sharding by view or by screen band is "
+              "not built)",
               file=sys.stderr)
         sys.exit(2)
     from gaussian_splats import scenes
@@ -286,7 +290,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded BASELINE distributions)",
+        "data": "synthetic (seeded scenes.CONFIGS distributions)",
         "config": {
             "workload": f"{scene.name}: {scene.num_points} Gaussians, SH3, {w}x{h}, fwd+bwd, L1 loss",
             "tile_size": args.tile_size,

@@ -121,6 +121,12 @@ _SIGNATURES = {
         c_int,
         [c_void_p] * 5 + [c_int64, c_int32, c_void_p, c_void_p, GsView] + [c_void_p] * 9,
     ),
+    "gs_l1_loss_workspace_bytes": (c_size_t, [c_int64]),
+    "gs_l1_loss_fwd": (
+        c_int,
+        [c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p],
+    ),
+    "gs_l1_loss_bwd": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
 }
 
 _lock = threading.Lock()

@@ -1,0 +1,82 @@
+"""Photometric losses of the training step on the HIP library.
+
+``l1_loss(image, target, clamp)`` is the term
+``(image.clamp(0, 1) - target).abs().mean()`` of the reference's training step
+(src/gaussian_splats/training/train.py:137-138; ``clamp=False`` drops the
+clamp) as one autograd node: a forward kernel that reduces the absolute
+differences and keeps a one-byte gradient sign per element, and a backward
+kernel that expands it.  The gradient equals autograd's for the torch
+expression bit for bit; the loss value is a deterministic fp32 sum that
+matches torch's reduction to rounding.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from ..kernels.rasterize import _native as nat
+
+
+def l1_loss_forward(
+    image: torch.Tensor, target: torch.Tensor, clamp: bool = False
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Forward kernel: returns ``(loss, code)`` with ``code`` the int8 gradient
+    sign per element that :func:`l1_loss_backward` expands."""
+    device = nat.require_gpu(image, target)
+    if image.shape != target.shape:
+        raise ValueError(f"image {tuple(image.shape)} and target {tuple(target.shape)} differ")
+    image = nat.prepare(image)
+    target = nat.prepare(target)
+    lib = nat.library()
+    loss = torch.empty((), dtype=torch.float32, device=device)
+    code = torch.empty(image.shape, dtype=torch.int8, device=device)
+    numel = image.numel()
+    ws_bytes = lib.gs_l1_loss_workspace_bytes(numel)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+    nat.check(
+        lib.gs_l1_loss_fwd(
+            nat.ptr(image), nat.ptr(target), numel, int(bool(clamp)), nat.ptr(loss),
+            nat.ptr(code), nat.ptr(ws), ws_bytes, nat.stream(device),
+        ),
+        "l1_loss",
+    )
+    return loss, code
+
+
+def l1_loss_backward(code: torch.Tensor, grad_loss: torch.Tensor) -> torch.Tensor:
+    """Backward kernel: gradient of the loss with respect to the image, for
+    the upstream gradient ``grad_loss`` (a one-element device tensor)."""
+    nat.require_gpu(code, grad_loss)
+    grad_loss = nat.prepare(grad_loss.reshape(()))
+    grad_image = torch.empty(code.shape, dtype=torch.float32, device=code.device)
+    nat.check(
+        nat.library().gs_l1_loss_bwd(
+            nat.ptr(code), nat.ptr(grad_loss), code.numel(), nat.ptr(grad_image),
+            nat.stream(code.device),
+        ),
+        "l1_loss backward",
+    )
+    return grad_image
+
+
+class _L1Loss(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, image: torch.Tensor, target: torch.Tensor, clamp: bool) -> torch.Tensor:
+        loss, code = l1_loss_forward(image, target, clamp)
+        ctx.save_for_backward(code)
+        return loss
+
+    @staticmethod
+    def backward(ctx, grad_loss: torch.Tensor):
+        (code,) = ctx.saved_tensors
+        return l1_loss_backward(code, grad_loss), None, None
+
+
+def l1_loss(image: torch.Tensor, target: torch.Tensor, clamp: bool = False) -> torch.Tensor:
+    """Mean absolute difference of ``image`` (clamped to [0, 1] when ``clamp``)
+    and ``target``; differentiable with respect to ``image`` only."""
+    if target.requires_grad:
+        raise ValueError("l1_loss does not propagate gradients to the target")
+    if image.dtype != torch.float32 or target.dtype != torch.float32:
+        raise TypeError("l1_loss expects float32 tensors")
+    return _L1Loss.apply(image, target, clamp)

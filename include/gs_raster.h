@@ -227,6 +227,24 @@ GS_API int gs_project_bwd(
     float* grad_mean, float* grad_rotation, float* grad_scale,
     float* grad_opacity, float* grad_color, void* stream);
 
+/* Photometric L1 loss of the training step that consumes the image
+ * (src/gaussian_splats/training/train.py:137-138, the torch expression
+ * (image.clamp(0, 1) - target).abs().mean() with clamp != 0, without the
+ * clamp otherwise).  Writes loss[0] (fp32, deterministic) and code[numel]
+ * int8 = sign(image' - target), 0 where the clamp stops the gradient, for
+ * gs_l1_loss_bwd.  The workspace holds the per-workgroup partial sums. */
+GS_API size_t gs_l1_loss_workspace_bytes(int64_t numel);
+GS_API int gs_l1_loss_fwd(
+    const float* image, const float* target, int64_t numel, int32_t clamp,
+    float* loss, int8_t* code, void* workspace, size_t workspace_bytes,
+    void* stream);
+
+/* grad_image = code * (grad_loss[0] * (1 / numel)): autograd's gradient of
+ * the expression above (train.py:151), with grad_loss in device memory. */
+GS_API int gs_l1_loss_bwd(
+    const int8_t* code, const float* grad_loss, int64_t numel,
+    float* grad_image, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -22,8 +22,7 @@ gives the reference's gradients, and (c) the camera-space point, pixel
 coordinates and depth are computed in the same operation order as the HIP
 projection, so depth bits (and hence keys) agree bit for bit.
 
-Parity status of each function is recorded in DESIGN.md; every function here is
-pinned by tests/test_oracle_*.py against closed forms, brute force, finite
+Every function here is pinned by tests/test_oracle_*.py against closed forms, brute force, finite
 differences or independent libraries (scipy).
 """
 

@@ -38,6 +38,33 @@ def test_workspace_queries_are_host_only():
     assert lib.gs_bin_workspace_bytes(1000) > lib.gs_bin_workspace_bytes(10)
 
 
+def test_l1_loss_host_checks():
+    """The fused L1 loss validates sizes, pointers and workspace on the host."""
+    lib = nat.library()
+    fake = ctypes.c_void_p(16)
+    ws_bytes = lib.gs_l1_loss_workspace_bytes(1 << 20)
+    assert ws_bytes >= 4
+    null = ctypes.c_void_p(0)
+    assert lib.gs_l1_loss_fwd(fake, fake, -1, 0, fake, fake, fake, ws_bytes, null) == nat.GS_ERR_INVALID_ARGUMENT
+    assert lib.gs_l1_loss_fwd(null, fake, 8, 0, fake, fake, fake, ws_bytes, null) == nat.GS_ERR_INVALID_ARGUMENT
+    assert lib.gs_l1_loss_fwd(fake, fake, 8, 0, fake, fake, fake, ws_bytes - 1, null) == nat.GS_ERR_WORKSPACE
+    assert lib.gs_l1_loss_bwd(null, fake, 8, fake, null) == nat.GS_ERR_INVALID_ARGUMENT
+    assert lib.gs_l1_loss_bwd(fake, fake, -1, fake, null) == nat.GS_ERR_INVALID_ARGUMENT
+    assert lib.gs_l1_loss_bwd(null, null, 0, null, null) == nat.GS_OK  # empty: nothing to do
+
+
+def test_l1_loss_python_checks():
+    from gaussian_splats.training import l1_loss
+
+    x = torch.zeros(4, 4, 3)
+    with pytest.raises(ValueError, match="ROCm GPU"):
+        l1_loss(x, torch.zeros(4, 4, 3))
+    with pytest.raises(ValueError, match="target"):
+        l1_loss(x, torch.zeros(4, 4, 3, requires_grad=True))
+    with pytest.raises(TypeError):
+        l1_loss(x.double(), torch.zeros(4, 4, 3))
+
+
 def test_bucketed_binning_host_checks():
     """Row/column bucketing: grid limits, sizes and inconsistent totals are
     rejected on the host before any launch."""

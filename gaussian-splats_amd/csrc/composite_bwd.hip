@@ -46,8 +46,13 @@ template <int TILE>
 __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_bwd_kernel(CompositeBwdArgs a) {
   constexpr int NPIX = TILE * TILE;
   constexpr int PIX = NPIX >= 64 ? NPIX / 64 : 1;
+  constexpr int kBandRows = 64 / TILE > 0 ? 64 / TILE : 1;  // tile rows per band of 64 pixels
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
+  // The wave's current 64 entries, three float4 per entry (u, v, o, pa),
+  // (pb, pc, r, g), (b, oa, ob, oc): written once per lane, then read as LDS
+  // broadcasts per entry instead of twelve v_readlane.
+  __shared__ float4 chunk[kWavesPerBlock][64][3];
   const int tile = xcd_swizzle(blockIdx.x, gridDim.x) * kWavesPerBlock + wid;
   if (tile >= a.num_tiles) return;
 
@@ -94,18 +99,38 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_bwd_kernel(Comp
     const int64_t e = top - 1 - lane;
     LaneSplat mine;
     int gid = 0;
-    bool keep = false;
+    uint32_t bands = 0;  // bit k: the Gaussian can reach a pixel of band k
     if (e >= start) {
       gid = a.ids[e];
       const GsRecord rec = load_projected(a.pmean, a.pinv, a.pcolor, a.popacity, gid);
-      keep = touches_rect(rec, rx0, rx1, ry0, ry1);
+#pragma unroll
+      for (int k = 0; k < PIX; ++k) {
+        const float y0 = ry0 + float(k * kBandRows);
+        if (y0 <= ry1 && touches_rect(rec, rx0, rx1, y0, fminf(y0 + float(kBandRows - 1), ry1)))
+          bands |= 1u << k;
+      }
       mine = lane_splat(rec);
     }
-    uint64_t mask = __ballot(keep);
+    chunk[wid][lane][0] = make_float4(mine.u, mine.v, mine.o, mine.pa);
+    chunk[wid][lane][1] = make_float4(mine.pb, mine.pc, mine.r, mine.g);
+    chunk[wid][lane][2] = make_float4(mine.b, mine.oa, mine.ob, mine.oc);
+    uint64_t mask = __ballot(bands != 0);
     while (mask) {
       const int j = __builtin_ctzll(mask);
       mask &= mask - 1;
-      const Splat s = broadcast(mine, j);
+      const uint32_t band_mask = uint32_t(__builtin_amdgcn_readlane(int(bands), j));
+      const float4 f0 = chunk[wid][j][0], f1 = chunk[wid][j][1], f2 = chunk[wid][j][2];
+      Splat s;
+      s.u = f0.x;
+      s.v = f0.y;
+      s.o = f0.z;
+      s.pa = f0.w;
+      s.pb = f1.x;
+      s.pc = f1.y;
+      s.cut = 0.0f;  // Gaussian mode only
+      s.r = f1.z;
+      s.g = f1.w;
+      s.bl = f2.x;
       const int pos = int(top - 1 - start) - j;
       const ColumnTerms c = column_terms(s, pxf);
       // Per-lane sums over the lane's pixels; -0 is the identity of +, so the
@@ -118,8 +143,9 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_bwd_kernel(Comp
       // sum unchanged.
 #pragma unroll
       for (int k = 0; k < PIX; ++k) {
-        // A band of 64 pixels none of which processed this entry is skipped.
-        if (__ballot(pos < ncon[k]) == 0) continue;
+        // A band of 64 pixels that the Gaussian cannot reach, or none of
+        // which processed this entry, is skipped.
+        if (!((band_mask >> k) & 1u) || __ballot(pos < ncon[k]) == 0) continue;
         const float dy = pyf[k] - s.v;
         float prob;
         const float raw = raw_alpha<false>(s, c, dy, prob);
@@ -149,7 +175,7 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_bwd_kernel(Comp
       // (k = -o/2, -2k = o):  u: o (a Sx + b Sy),  v: o (b Sx + c Sy),
       // inv00: k Sxx,  inv01: k Sxy,  inv11: k Syy,  Sx = dx s0, Sxx = dx^2 s0,
       // Sxy = dx s1, Sy = s1, Syy = s2.
-      const float oa = bcast(mine.oa, j), ob = bcast(mine.ob, j), oc = bcast(mine.oc, j);
+      const float oa = f2.y, ob = f2.z, oc = f2.w;
       const float sx = c.dx * s0;
       const float kdx = (-0.5f * s.o) * c.dx;
       float v[9];

@@ -13,8 +13,8 @@
 //
 // Each lane gathers one Gaussian record of the next 64 list entries and tests
 // whether it can reach alpha >= 1/255 anywhere in the tile (touches_rect); the
-// wave then walks only the set bits of that ballot, broadcasting the record
-// with v_readlane.  The tile stops as soon as no pixel is active.
+// wave then walks only the set bits of that ballot, reading each record as an
+// LDS broadcast.  The tile stops as soon as no pixel is active.
 #include "common.h"
 #include "raster_math.h"
 
@@ -42,6 +42,10 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_fwd_kernel(Comp
   constexpr int PIX = NPIX >= 64 ? NPIX / 64 : 1;
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
+  // The wave's current 64 entries, three float4 per entry (u, v, o, pa),
+  // (pb, pc, r, g), (b, cut, -, -): written once per lane, then read as LDS
+  // broadcasts per entry instead of ten v_readlane.
+  __shared__ float4 chunk[kWavesPerBlock][64][3];
   const int tile = xcd_swizzle(blockIdx.x, gridDim.x) * kWavesPerBlock + wid;
   if (tile >= a.num_tiles) return;
 
@@ -92,13 +96,27 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_fwd_kernel(Comp
       keep = touches_rect(rec, rx0, rx1, ry0, ry1);
       mine = lane_splat(rec);
     }
+    chunk[wid][lane][0] = make_float4(mine.u, mine.v, mine.o, mine.pa);
+    chunk[wid][lane][1] = make_float4(mine.pb, mine.pc, mine.r, mine.g);
+    chunk[wid][lane][2] = make_float4(mine.b, mine.cut, 0.0f, 0.0f);
     uint64_t mask = __ballot(keep);
     // No break inside: the loop ends through its condition, which keeps the
     // per-pixel active flags out of extra mask-merging control flow.
     while (mask) {
       const int j = __builtin_ctzll(mask);
       mask &= mask - 1;
-      const Splat s = broadcast(mine, j);
+      const float4 f0 = chunk[wid][j][0], f1 = chunk[wid][j][1], f2 = chunk[wid][j][2];
+      Splat s;
+      s.u = f0.x;
+      s.v = f0.y;
+      s.o = f0.z;
+      s.pa = f0.w;
+      s.pb = f1.x;
+      s.pc = f1.y;
+      s.r = f1.z;
+      s.g = f1.w;
+      s.bl = f2.x;
+      s.cut = f2.y;
       const int pos = int(base - start) + j;
       const ColumnTerms c = column_terms(s, pxf);
       // Branch-free: a finished pixel (or a cut alpha) blends with alpha = 0,

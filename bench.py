@@ -210,7 +210,10 @@ def main():
     cam = scene.cameras[0]
     w, h = cam.image_size
     splats = GaussianSplat.from_tensors(*(p.to(device) for p in scene.params()))
-    target = scene.target.to(device) if scene.target is not None else torch.rand(h, w, 3, device=device)
+    if scene.target is None:
+        target = torch.rand(h, w, 3, device=device)
+    else:  # multi-view scenes hold one target per camera; the step renders view 0
+        target = (scene.target[0] if scene.target.dim() == 4 else scene.target).to(device)
     params = [splats.mean.detach(), splats.rotation.detach(), splats.scale.detach(),
               splats.opacity.detach(), splats.color.detach()]
 

@@ -58,6 +58,10 @@ int join_side_stream(SideFork& f, bool host_wait = false);
 
 constexpr int kWave = 64;
 
+// Waves (tiles) per workgroup of the compositing kernels; the tile dispatch
+// order of tile_order.hip partitions the tiles the same way.
+constexpr int kCompositeWaves = 4;
+
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 inline size_t align_up(size_t x, size_t a = 256) { return (x + a - 1) / a * a; }

@@ -26,8 +26,6 @@
 namespace gs {
 namespace {
 
-constexpr int kWavesPerBlock = 4;
-
 struct CompositeBwdArgs {
   const float* pmean;
   const float* pinv;
@@ -35,6 +33,7 @@ struct CompositeBwdArgs {
   const float* popacity;
   const int32_t* ids;
   const int64_t* ranges;
+  const int32_t* order;  // tile dispatch order, or nullptr for the identity
   const float* grad_image;
   const float* final_t;
   const int32_t* n_contrib;
@@ -43,7 +42,7 @@ struct CompositeBwdArgs {
 };
 
 template <int TILE>
-__global__ __launch_bounds__(kWavesPerBlock * 64) void composite_bwd_kernel(CompositeBwdArgs a) {
+__global__ __launch_bounds__(kCompositeWaves * 64) void composite_bwd_kernel(CompositeBwdArgs a) {
   constexpr int NPIX = TILE * TILE;
   constexpr int PIX = NPIX >= 64 ? NPIX / 64 : 1;
   constexpr int kBandRows = 64 / TILE > 0 ? 64 / TILE : 1;  // tile rows per band of 64 pixels
@@ -52,9 +51,11 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_bwd_kernel(Comp
   // The wave's current 64 entries, three float4 per entry (u, v, o, pa),
   // (pb, pc, r, g), (b, oa, ob, oc): written once per lane, then read as LDS
   // broadcasts per entry instead of twelve v_readlane.
-  __shared__ float4 chunk[kWavesPerBlock][64][3];
-  const int tile = xcd_swizzle(blockIdx.x, gridDim.x) * kWavesPerBlock + wid;
-  if (tile >= a.num_tiles) return;
+  __shared__ float4 chunk[kCompositeWaves][64][3];
+  // Slot -> tile through the optional dispatch order (tile_order.hip).
+  const int slot = xcd_swizzle(blockIdx.x, gridDim.x) * kCompositeWaves + wid;
+  if (slot >= a.num_tiles) return;
+  const int tile = a.order ? a.order[slot] : slot;
 
   const int tx = tile % a.tiles_w;
   const int ty = tile / a.tiles_w;
@@ -153,7 +154,8 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_bwd_kernel(Comp
         const bool hit = pos < ncon[k] && clamped >= kMinAlpha;
         const float alpha = hit ? clamped : 0.0f;
         touched |= hit;
-        const float t_before = hit ? T[k] * __builtin_amdgcn_rcpf(1.0f - alpha) : T[k];
+        // alpha = 0 leaves T unchanged: v_rcp_f32(1) is exactly 1.
+        const float t_before = T[k] * __builtin_amdgcn_rcpf(1.0f - alpha);
         const float w = t_before * alpha;
         sr += gr[k] * w;
         sg += gg[k] * w;
@@ -199,8 +201,8 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_bwd_kernel(Comp
 
 template <int TILE>
 void launch(const CompositeBwdArgs& a, hipStream_t s) {
-  const unsigned blocks = unsigned(ceil_div(a.num_tiles, kWavesPerBlock));
-  composite_bwd_kernel<TILE><<<blocks, kWavesPerBlock * 64, 0, s>>>(a);
+  const unsigned blocks = unsigned(ceil_div(a.num_tiles, kCompositeWaves));
+  composite_bwd_kernel<TILE><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
 }
 
 }  // namespace
@@ -214,8 +216,8 @@ extern "C" GS_API int gs_composite_bwd(const float* projected_mean,
                                        const float* projected_opacity,
                                        const int32_t* gaussian_ids, const int64_t* ranges,
                                        const float* grad_image, const float* final_transmittance,
-                                       const int32_t* n_contributors, gs_view view,
-                                       float* grad_projected, void* stream) {
+                                       const int32_t* n_contributors, const int32_t* tile_order,
+                                       gs_view view, float* grad_projected, void* stream) {
   clear_error();
   GS_TRY(check_view(view, true));
   GS_REQUIRE(view.rendering_mode == GS_MODE_GAUSSIAN, GS_ERR_UNSUPPORTED,
@@ -231,6 +233,7 @@ extern "C" GS_API int gs_composite_bwd(const float* projected_mean,
   a.popacity = projected_opacity;
   a.ids = gaussian_ids;
   a.ranges = ranges;
+  a.order = tile_order;
   a.grad_image = grad_image;
   a.final_t = final_transmittance;
   a.n_contrib = n_contributors;

@@ -21,12 +21,11 @@
 namespace gs {
 namespace {
 
-constexpr int kWavesPerBlock = 4;
-
 struct CompositeArgs {
   const GsRecord* records;
   const int32_t* ids;
   const int64_t* ranges;
+  const int32_t* order;  // tile dispatch order, or nullptr for the identity
   int width, height, tile, tiles_w, num_tiles;
   float threshold;
   // A pixel stays active while (1 - T) < threshold, i.e. T > 1 - threshold.
@@ -37,7 +36,7 @@ struct CompositeArgs {
 };
 
 template <int TILE, bool ELLIPSOID>
-__global__ __launch_bounds__(kWavesPerBlock * 64) void composite_fwd_kernel(CompositeArgs a) {
+__global__ __launch_bounds__(kCompositeWaves * 64) void composite_fwd_kernel(CompositeArgs a) {
   constexpr int NPIX = TILE * TILE;
   constexpr int PIX = NPIX >= 64 ? NPIX / 64 : 1;
   const int lane = threadIdx.x & 63;
@@ -45,9 +44,11 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_fwd_kernel(Comp
   // The wave's current 64 entries, three float4 per entry (u, v, o, pa),
   // (pb, pc, r, g), (b, cut, -, -): written once per lane, then read as LDS
   // broadcasts per entry instead of ten v_readlane.
-  __shared__ float4 chunk[kWavesPerBlock][64][3];
-  const int tile = xcd_swizzle(blockIdx.x, gridDim.x) * kWavesPerBlock + wid;
-  if (tile >= a.num_tiles) return;
+  __shared__ float4 chunk[kCompositeWaves][64][3];
+  // Slot -> tile through the optional dispatch order (tile_order.hip).
+  const int slot = xcd_swizzle(blockIdx.x, gridDim.x) * kCompositeWaves + wid;
+  if (slot >= a.num_tiles) return;
+  const int tile = a.order ? a.order[slot] : slot;
 
   const int tx = tile % a.tiles_w;
   const int ty = tile / a.tiles_w;
@@ -159,11 +160,11 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void composite_fwd_kernel(Comp
 
 template <int TILE>
 void launch(const CompositeArgs& a, bool ellipsoid, hipStream_t s) {
-  const unsigned blocks = unsigned(ceil_div(a.num_tiles, kWavesPerBlock));
+  const unsigned blocks = unsigned(ceil_div(a.num_tiles, kCompositeWaves));
   if (ellipsoid)
-    composite_fwd_kernel<TILE, true><<<blocks, kWavesPerBlock * 64, 0, s>>>(a);
+    composite_fwd_kernel<TILE, true><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
   else
-    composite_fwd_kernel<TILE, false><<<blocks, kWavesPerBlock * 64, 0, s>>>(a);
+    composite_fwd_kernel<TILE, false><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
 }
 
 }  // namespace
@@ -172,9 +173,9 @@ void launch(const CompositeArgs& a, bool ellipsoid, hipStream_t s) {
 using namespace gs;
 
 extern "C" GS_API int gs_composite(const void* records, const int32_t* gaussian_ids,
-                                   const int64_t* ranges, gs_view view, float* image,
-                                   float* final_transmittance, int32_t* n_contributors,
-                                   void* stream) {
+                                   const int64_t* ranges, const int32_t* tile_order,
+                                   gs_view view, float* image, float* final_transmittance,
+                                   int32_t* n_contributors, void* stream) {
   clear_error();
   GS_TRY(check_view(view, true));
   GS_REQUIRE(ranges && image && final_transmittance && n_contributors, GS_ERR_INVALID_ARGUMENT,
@@ -185,6 +186,7 @@ extern "C" GS_API int gs_composite(const void* records, const int32_t* gaussian_
   a.records = static_cast<const GsRecord*>(records);
   a.ids = gaussian_ids;
   a.ranges = ranges;
+  a.order = tile_order;
   a.width = view.image_width;
   a.height = view.image_height;
   a.tile = view.tile_size;

@@ -1,0 +1,186 @@
+// Dispatch order of the compositing tiles.
+//
+// The compositing kernels run one wave per tile, four tiles per workgroup, and
+// map workgroups onto XCDs so that each XCD composites one contiguous region of
+// tiles (xcd_swizzle: neighbouring tiles share Gaussians, which then stay in
+// that XCD's L2).  When not every wave fits on the GPU at once, workgroups
+// dispatched last start late; if they hold long tiles, the kernel ends in a
+// tail with few waves resident.  The order computed here keeps each XCD's
+// region but sorts its tiles by decreasing expected work (to eight significant
+// bits), so the long tiles start first and the short ones fill the tail
+// (longest-processing-time-first list scheduling).  Ties keep ascending tile
+// index, so the order is deterministic.
+//
+// Work estimates: the list length of the tile, or the largest contributor
+// count of its pixels (the entries the backward walks).
+#include <algorithm>
+
+#include "common.h"
+
+namespace gs {
+namespace {
+
+constexpr int kOrderThreads = 1024;
+constexpr int kOrderMax = 8192;  // tiles per region ordered by one workgroup
+
+// key[t] = expected work of tile t, capped at 2^16 - 1.  One wave per tile.
+__global__ __launch_bounds__(256) void tile_key_kernel(const int64_t* __restrict__ ranges,
+                                                       const int32_t* __restrict__ ncon,
+                                                       int tiles_w, int num_tiles, int tile,
+                                                       int width, int height,
+                                                       uint32_t* __restrict__ key) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= num_tiles) return;
+  int64_t work;
+  if (ncon) {
+    const int ox = (t % tiles_w) * tile, oy = (t / tiles_w) * tile;
+    int m = 0;
+    for (int q = lane; q < tile * tile; q += 64) {
+      const int px = ox + q % tile, py = oy + q / tile;
+      if (px < width && py < height) m = max(m, ncon[int64_t(py) * width + px]);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = max(m, __shfl_xor(m, o, 64));
+    work = m;
+  } else {
+    work = ranges[2 * t + 1] - ranges[2 * t];
+  }
+  if (lane == 0) key[t] = uint32_t(min(max(work, int64_t(0)), int64_t(0xFFFF)));
+}
+
+// Region r of the order: the tiles of the workgroups xcd_swizzle gives XCD r.
+__device__ __forceinline__ void region(int r, int num_tiles, int& lo, int& hi) {
+  const int nb = (num_tiles + kCompositeWaves - 1) / kCompositeWaves;
+  const int q = nb >> 3, rem = nb & 7;
+  const int b0 = r * q + min(r, rem), b1 = (r + 1) * q + min(r + 1, rem);
+  lo = min(b0 * kCompositeWaves, num_tiles);
+  hi = min(b1 * kCompositeWaves, num_tiles);
+}
+
+// One workgroup per region: a stable counting sort of the region's tiles by
+// the eight most significant bits of the key (relative to the region's largest
+// key), largest first.  Sixteen waves take contiguous index segments; a wave
+// ranks its tiles per bucket with ballots (eight, one per digit bit), so ties
+// keep index order.  A coarse order is all list scheduling needs.
+__global__ __launch_bounds__(kOrderThreads) void tile_sort_kernel(const uint32_t* __restrict__ key,
+                                                                  int num_tiles,
+                                                                  int32_t* __restrict__ order) {
+  constexpr int kWaves = kOrderThreads / 64;
+  constexpr int kPerLane = kOrderMax / kOrderThreads;  // tiles per lane at most
+  __shared__ uint32_t cnt[kWaves][256];
+  __shared__ uint32_t start[256];
+  __shared__ uint32_t smax;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  int lo, hi;
+  region(blockIdx.x, num_tiles, lo, hi);
+  const int n = hi - lo;
+  if (n > kOrderMax) {  // too large to sort here: keep the identity order
+    for (int i = threadIdx.x; i < n; i += kOrderThreads) order[lo + i] = lo + i;
+    return;
+  }
+  if (threadIdx.x == 0) smax = 0;
+  for (int i = threadIdx.x; i < kWaves * 256; i += kOrderThreads) (&cnt[0][0])[i] = 0;
+  __syncthreads();
+  const int seg = (n + kWaves - 1) / kWaves;  // <= kPerLane * 64
+  const int s0 = wid * seg, s1 = min(s0 + seg, n);
+  uint32_t k[kPerLane];
+  uint32_t m = 0;
+#pragma unroll
+  for (int i = 0; i < kPerLane; ++i) {
+    const int e = s0 + i * 64 + lane;
+    k[i] = e < s1 ? key[lo + e] : 0u;
+    m = max(m, k[i]);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = max(m, uint32_t(__shfl_xor(int(m), o, 64)));
+  if (lane == 0) atomicMax(&smax, m);
+  __syncthreads();
+  const int shift = max(0, 24 - __clz(int(smax | 1u)));  // smax >> shift < 256
+  uint32_t dig[kPerLane], rank[kPerLane];
+#pragma unroll
+  for (int i = 0; i < kPerLane; ++i) {
+    const int e = s0 + i * 64 + lane;
+    const bool valid = e < s1;
+    dig[i] = 255u - (k[i] >> shift);
+    uint32_t plo = uint32_t(__ballot(valid)), phi = uint32_t(__ballot(valid) >> 32);
+#pragma unroll
+    for (int bit = 0; bit < 8; ++bit) {
+      const uint32_t mb = uint32_t(int32_t(dig[i] << (31 - bit)) >> 31);
+      const uint64_t ones = __ballot(mb != 0u);
+      plo &= ~(uint32_t(ones) ^ mb);
+      phi &= ~(uint32_t(ones >> 32) ^ mb);
+    }
+    const uint32_t before = __builtin_amdgcn_mbcnt_hi(phi, __builtin_amdgcn_mbcnt_lo(plo, 0u));
+    const uint32_t total = uint32_t(__popc(plo) + __popc(phi));
+    uint32_t c = 0;
+    if (valid) {
+      c = cnt[wid][dig[i]];
+      cnt[wid][dig[i]] = c + total;
+    }
+    rank[i] = c + before;
+  }
+  __syncthreads();
+  // Bucket starts: digit-major over the waves, in one wave.
+  if (wid == 0) {
+    uint32_t carry = 0;
+    for (int d0 = 0; d0 < 256; d0 += 64) {
+      const int d = d0 + lane;
+      uint32_t tot = 0;
+      for (int w = 0; w < kWaves; ++w) {
+        const uint32_t c = cnt[w][d];
+        cnt[w][d] = tot;  // wave offset within the bucket
+        tot += c;
+      }
+      uint32_t incl = tot;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t v = uint32_t(__shfl_up(int(incl), o, 64));
+        if (lane >= o) incl += v;
+      }
+      start[d] = carry + incl - tot;
+      carry += uint32_t(__shfl(int(incl), 63, 64));
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kPerLane; ++i) {
+    const int e = s0 + i * 64 + lane;
+    if (e < s1) order[lo + int(start[dig[i]] + cnt[wid][dig[i]] + rank[i])] = lo + e;
+  }
+}
+
+}  // namespace
+}  // namespace gs
+
+using namespace gs;
+
+extern "C" {
+
+GS_API size_t gs_tile_order_workspace_bytes(int32_t num_tiles) {
+  return num_tiles > 0 ? align_up(size_t(num_tiles) * sizeof(uint32_t)) : 0;
+}
+
+GS_API int gs_tile_order(const int64_t* ranges, const int32_t* n_contributors, gs_view view,
+                         int32_t* order, void* workspace, size_t workspace_bytes,
+                         void* stream) {
+  clear_error();
+  GS_TRY(check_view(view, true));
+  const int tiles_w = tiles_along(view.image_width, view.tile_size);
+  const int num_tiles = tiles_w * tiles_along(view.image_height, view.tile_size);
+  GS_REQUIRE(order && (ranges || n_contributors), GS_ERR_INVALID_ARGUMENT,
+             "null pointer argument");
+  GS_REQUIRE(workspace && workspace_bytes >= gs_tile_order_workspace_bytes(num_tiles),
+             GS_ERR_WORKSPACE, "workspace too small (%zu bytes, need %zu)", workspace_bytes,
+             gs_tile_order_workspace_bytes(num_tiles));
+  const hipStream_t s = as_stream(stream);
+  uint32_t* key = static_cast<uint32_t*>(workspace);
+  tile_key_kernel<<<unsigned(ceil_div(num_tiles, 4)), 256, 0, s>>>(
+      ranges, n_contributors, tiles_w, num_tiles, view.tile_size, view.image_width,
+      view.image_height, key);
+  GS_TRY(check_launch("tile_order keys"));
+  tile_sort_kernel<<<8, kOrderThreads, 0, s>>>(key, num_tiles, order);
+  return check_launch("tile_order sort");
+}
+
+}  // extern "C"

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parents[2] / "_lib" / "libgs_raster.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 GS_OK = 0
 GS_ERR_INVALID_ARGUMENT = 1
@@ -112,10 +112,16 @@ _SIGNATURES = {
         [c_int64, c_int32, c_int32, c_void_p, c_int64, c_int64, c_int64,
          c_void_p, c_size_t, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p],
     ),
-    "gs_composite": (c_int, [c_void_p, c_void_p, c_void_p, GsView, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "gs_tile_order_workspace_bytes": (c_size_t, [c_int32]),
+    "gs_tile_order": (
+        c_int, [c_void_p, c_void_p, GsView, c_void_p, c_void_p, c_size_t, c_void_p]
+    ),
+    "gs_composite": (
+        c_int, [c_void_p, c_void_p, c_void_p, c_void_p, GsView, c_void_p, c_void_p, c_void_p, c_void_p]
+    ),
     "gs_composite_bwd": (
         c_int,
-        [c_void_p] * 9 + [GsView, c_void_p, c_void_p],
+        [c_void_p] * 10 + [GsView, c_void_p, c_void_p],
     ),
     "gs_project_bwd": (
         c_int,

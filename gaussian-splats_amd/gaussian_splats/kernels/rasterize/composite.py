@@ -13,6 +13,39 @@ from . import _native as nat
 from .project import _check_tile, pack_records
 
 
+def tile_order(
+    ranges: torch.Tensor | None,
+    n_contributors: torch.Tensor | None,
+    image_width: int,
+    image_height: int,
+    tile_size: int,
+) -> torch.Tensor:
+    """Tile dispatch order for the compositing kernels (gs_tile_order): each
+    XCD's region of tiles, longest expected work first.  The estimate is the
+    list length from ``ranges``, or the largest contributor count per tile when
+    ``n_contributors`` is given.  The backward uses the latter; the forward
+    runs in index order (all of its waves fit on the GPU at once)."""
+    source = n_contributors if n_contributors is not None else ranges
+    if source is None:
+        raise ValueError("tile_order needs ranges or n_contributors")
+    device = nat.require_gpu(source)
+    tiles_w, tiles_h = nat.tiles(image_width, image_height, tile_size)
+    num_tiles = tiles_w * tiles_h
+    lib = nat.library()
+    order = torch.empty(num_tiles, dtype=torch.int32, device=device)
+    ws_bytes = lib.gs_tile_order_workspace_bytes(num_tiles)
+    ws = nat.workspace(ws_bytes, device)
+    view = nat.make_view(1.0, 1.0, 0.0, 0.0, image_width, image_height, tile_size)
+    nat.check(
+        lib.gs_tile_order(
+            nat.ptr(ranges), nat.ptr(n_contributors), view, nat.ptr(order), nat.ptr(ws),
+            ws.numel(), nat.stream(device),
+        ),
+        "tile_order",
+    )
+    return order
+
+
 def composite(
     mean: torch.Tensor,
     inverse_covariance: torch.Tensor,
@@ -49,7 +82,7 @@ def composite(
     )
     nat.check(
         nat.library().gs_composite(
-            nat.ptr(records), nat.ptr(gaussian_ids), nat.ptr(ranges), view, nat.ptr(image),
+            nat.ptr(records), nat.ptr(gaussian_ids), nat.ptr(ranges), None, view, nat.ptr(image),
             nat.ptr(final_transmittance), nat.ptr(n_contributors), nat.stream(device),
         ),
         "composite",

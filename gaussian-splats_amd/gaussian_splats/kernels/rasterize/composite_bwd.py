@@ -12,6 +12,7 @@ from __future__ import annotations
 import torch
 
 from . import _native as nat
+from .composite import tile_order
 from .project import _check_tile
 
 
@@ -60,14 +61,15 @@ def composite_bwd(
         opacity_threshold=opacity_threshold,
     )
     lib = nat.library()
+    order = tile_order(None, n_contributors, image_width, image_height, tile_size)
     nat.check(
         nat.launch(
             "composite_bwd",
             lambda: lib.gs_composite_bwd(
                 nat.ptr(projected_mean), nat.ptr(inverse_covariance), nat.ptr(projected_color),
                 nat.ptr(projected_opacity), nat.ptr(gaussian_ids), nat.ptr(ranges),
-                nat.ptr(grad_image), nat.ptr(final_transmittance), nat.ptr(n_contributors), view,
-                nat.ptr(out), nat.stream(device),
+                nat.ptr(grad_image), nat.ptr(final_transmittance), nat.ptr(n_contributors),
+                nat.ptr(order), view, nat.ptr(out), nat.stream(device),
             ),
         ),
         "composite_bwd",

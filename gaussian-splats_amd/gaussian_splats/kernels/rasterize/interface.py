@@ -196,6 +196,11 @@ def _setup_context(ctx, inputs, output) -> None:
             opacity_threshold=ctx.opacity_threshold,
         )
         ctx.view_project = nat.make_view(ctx.fx, ctx.fy, 0.0, 0.0, ctx.image_width, ctx.image_height)
+        num_tiles = output[8].shape[0]
+        ctx.tile_order = (
+            torch.empty(num_tiles, dtype=torch.int32, device=mean.device),
+            nat.workspace(nat.library().gs_tile_order_workspace_bytes(num_tiles), mean.device),
+        )
     else:
         ctx.grad_projected = None
 
@@ -242,14 +247,22 @@ def _backward(ctx, *grad_outputs):
     lib = nat.library()
     stream = nat.stream(device)
     ptr = nat.ptr
+    order, order_ws = ctx.tile_order
+    nat.check(
+        lib.gs_tile_order(
+            None, ptr(n_contributors), ctx.view_composite, ptr(order), ptr(order_ws),
+            order_ws.numel(), stream,
+        ),
+        "tile_order",
+    )
     nat.check(
         nat.launch(
             "composite_bwd",
             lambda: lib.gs_composite_bwd(
                 ptr(projected_mean), ptr(inverse_covariance), ptr(projected_color),
                 ptr(projected_opacity), ptr(gaussian_ids), ptr(ranges), ptr(grad_image),
-                ptr(final_transmittance), ptr(n_contributors), ctx.view_composite,
-                ptr(grad_projected), stream,
+                ptr(final_transmittance), ptr(n_contributors), ptr(order),
+                ctx.view_composite, ptr(grad_projected), stream,
             ),
         ),
         "composite_bwd",

@@ -42,7 +42,7 @@ extern "C" {
 
 #define GS_API __attribute__((visibility("default")))
 
-#define GS_ABI_VERSION 1
+#define GS_ABI_VERSION 2
 
 typedef enum gs_status {
   GS_OK = 0,
@@ -195,13 +195,27 @@ GS_API int gs_bin_tiles_emit(
     void* plan, size_t plan_bytes, const int64_t* ranges, int32_t* sorted_ids,
     void* workspace, size_t workspace_bytes, void* stream);
 
+/* Tile dispatch order for the compositing kernels (no counterpart in the
+ * reference, whose launches take tiles in index order): a permutation of the
+ * tiles that keeps each XCD's region of tiles and starts the tiles with the
+ * most expected work first.  The work estimate is the list length from
+ * ranges, or, when n_contributors is given, the largest contributor count of
+ * the tile's pixels (the entries the backward walks).  Results of the
+ * compositing kernels do not depend on the order. */
+GS_API size_t gs_tile_order_workspace_bytes(int32_t num_tiles);
+GS_API int gs_tile_order(
+    const int64_t* ranges, const int32_t* n_contributors, gs_view view,
+    int32_t* tile_order, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Front-to-back compositing per tile.  Replaces composite
  * (src/gaussian_splats/kernels/rasterize/composite.py:25-162) with the
- * pixel semantics of torch.py:172-225.  tile_size in {4, 8, 16, 32}. */
+ * pixel semantics of torch.py:172-225.  tile_size in {4, 8, 16, 32}.
+ * tile_order (optional, from gs_tile_order) only changes the dispatch
+ * order. */
 GS_API int gs_composite(
     const void* records, const int32_t* gaussian_ids, const int64_t* ranges,
-    gs_view view, float* image, float* final_transmittance,
-    int32_t* n_contributors, void* stream);
+    const int32_t* tile_order, gs_view view, float* image,
+    float* final_transmittance, int32_t* n_contributors, void* stream);
 
 /* Back-to-front compositing gradient, accumulated with atomics into
  * grad_projected[N,9] (zeroed by the caller), from the op's projected outputs.
@@ -212,8 +226,8 @@ GS_API int gs_composite_bwd(
     const float* projected_color, const float* projected_opacity,
     const int32_t* gaussian_ids, const int64_t* ranges,
     const float* grad_image, const float* final_transmittance,
-    const int32_t* n_contributors, gs_view view, float* grad_projected,
-    void* stream);
+    const int32_t* n_contributors, const int32_t* tile_order, gs_view view,
+    float* grad_projected, void* stream);
 
 /* Chain rule from grad_projected to the parameters.  Replaces project_bwd
  * (src/gaussian_splats/kernels/rasterize/project_bwd.py:8-381); gradients are

@@ -38,6 +38,20 @@ def test_workspace_queries_are_host_only():
     assert lib.gs_bin_workspace_bytes(1000) > lib.gs_bin_workspace_bytes(10)
 
 
+def test_tile_order_host_checks():
+    lib = nat.library()
+    fake = ctypes.c_void_p(16)
+    null = ctypes.c_void_p(0)
+    assert lib.gs_tile_order_workspace_bytes(8160) >= 8160 * 4
+    ws = lib.gs_tile_order_workspace_bytes(8160)
+    view = _view(tile_size=16)
+    assert lib.gs_tile_order(null, null, view, fake, fake, ws, null) == nat.GS_ERR_INVALID_ARGUMENT
+    assert lib.gs_tile_order(fake, null, view, null, fake, ws, null) == nat.GS_ERR_INVALID_ARGUMENT
+    assert lib.gs_tile_order(fake, null, view, fake, fake, 0, null) == nat.GS_ERR_WORKSPACE
+    assert lib.gs_tile_order(fake, null, _view(tile_size=3), fake, fake, ws, null) in (
+        nat.GS_ERR_INVALID_ARGUMENT, nat.GS_ERR_UNSUPPORTED)
+
+
 def test_l1_loss_host_checks():
     """The fused L1 loss validates sizes, pointers and workspace on the host."""
     lib = nat.library()
@@ -109,14 +123,14 @@ def test_project_rejects_unsupported_sh_before_launch():
 def test_invalid_tile_sizes(tile):
     lib = nat.library()
     fake = ctypes.c_void_p(16)
-    status = lib.gs_composite(fake, fake, fake, _view(tile_size=tile), fake, fake, fake, None)
+    status = lib.gs_composite(fake, fake, fake, None, _view(tile_size=tile), fake, fake, fake, None)
     assert status in (nat.GS_ERR_INVALID_ARGUMENT, nat.GS_ERR_UNSUPPORTED)
 
 
 def test_backward_rejects_ellipsoid_mode():
     lib = nat.library()
     fake = ctypes.c_void_p(16)
-    status = lib.gs_composite_bwd(*([fake] * 9),
+    status = lib.gs_composite_bwd(*([fake] * 9), None,
                                   _view(rendering_mode="ellipsoid"), fake, None)
     assert status == nat.GS_ERR_UNSUPPORTED
     assert b"Gaussian rendering" in lib.gs_last_error()
@@ -135,7 +149,7 @@ def test_misaligned_buffers_rejected():
 def test_status_codes_map_to_python_exceptions():
     lib = nat.library()
     fake = ctypes.c_void_p(16)
-    status = lib.gs_composite_bwd(*([fake] * 9), _view(rendering_mode="ellipsoid"), fake, None)
+    status = lib.gs_composite_bwd(*([fake] * 9), None, _view(rendering_mode="ellipsoid"), fake, None)
     with pytest.raises(NotImplementedError):
         nat.check(status, "composite_bwd")
 

@@ -278,3 +278,102 @@ def test_composite_empty_tiles(device):
     )
     assert torch.count_nonzero(image) == 0
     assert torch.all(final_t == 1) and torch.count_nonzero(ncon) == 0
+
+
+def _regions(num_tiles, waves=4):
+    """Tile ranges of the eight XCD regions (the compositing workgroup split)."""
+    nb = -(-num_tiles // waves)
+    q, r = nb >> 3, nb & 7
+    out = []
+    for x in range(8):
+        b0, b1 = x * q + min(x, r), (x + 1) * q + min(x + 1, r)
+        out.append((min(b0 * waves, num_tiles), min(b1 * waves, num_tiles)))
+    return out
+
+
+def _expected_order(keys):
+    """Per region: stable sort by the key's eight most significant bits
+    (relative to the region's largest key, keys capped at 2^16 - 1), largest
+    first."""
+    order = np.arange(keys.size)
+    for lo, hi in _regions(keys.size):
+        if hi <= lo:
+            continue
+        k = np.minimum(keys[lo:hi], 0xFFFF).astype(np.int64)
+        shift = max(0, int(k.max() | 1).bit_length() - 8)
+        order[lo:hi] = lo + np.lexsort((np.arange(hi - lo), -(k >> shift)))
+    return order
+
+
+@pytest.mark.parametrize("shape", [(120, 68, 16), (7, 5, 8), (1, 1, 16), (33, 2, 4)])
+def test_tile_order_by_list_length_and_contributors(device, shape):
+    from gaussian_splats.kernels.rasterize.composite import tile_order
+
+    tw, th, tile = shape
+    w, h = tw * tile - 3, th * tile - 1  # partial edge tiles
+    tw, th = nat.tiles(w, h, tile)
+    t = tw * th
+    rng = np.random.default_rng(t)
+    lengths = rng.integers(0, 3000, size=t)
+    lengths[rng.random(t) < 0.1] = 0
+    lengths[: min(3, t)] = 70000  # capped at 2^16 - 1: ties broken by index
+    ranges = np.zeros((t, 2), dtype=np.int64)
+    ranges[:, 1] = np.cumsum(lengths)
+    ranges[1:, 0] = ranges[:-1, 1]
+    order = tile_order(torch.as_tensor(ranges).to(device), None, w, h, tile).cpu().numpy()
+    np.testing.assert_array_equal(order, _expected_order(lengths))
+
+    ncon = rng.integers(0, 500, size=(h, w)).astype(np.int32)
+    order = tile_order(None, torch.as_tensor(ncon).to(device), w, h, tile).cpu().numpy()
+    padded = np.zeros((th * tile, tw * tile), dtype=np.int64)
+    padded[:h, :w] = ncon
+    tile_max = padded.reshape(th, tile, tw, tile).max(axis=(1, 3)).reshape(-1)
+    np.testing.assert_array_equal(order, _expected_order(tile_max))
+
+
+def test_compositing_results_do_not_depend_on_tile_order(device):
+    scene = scenes.edge_case_scene(n=1500, sh_degree=1, image_size=(96, 80))
+    cam = scene.cameras[0]
+    w, h = cam.image_size
+    tile_size = 8
+    proj = orc.project(*scene.params(), oracle_camera(cam))
+    tw, th = nat.tiles(w, h, tile_size)
+    bounds, counts = orc.tile_counts(proj, tile_size, tw, th, scene.near, scene.far, "gaussian", CONFIDENCE)
+    sid, ranges = _oracle_lists(proj, bounds, counts, w, h, tile_size)
+    args = [t.float().to(device) for t in (proj.mean, proj.inverse, proj.color, proj.opacity)]
+    sid_d, ranges_d = torch.as_tensor(sid).to(device), torch.as_tensor(ranges).to(device)
+    image, final_t, ncon = composite(*args, sid_d, ranges_d, w, h, tile_size, THRESHOLD, "gaussian",
+                                     CONFIDENCE)
+    # The same launch through the C ABI with the tiles dispatched longest first.
+    from gaussian_splats.kernels.rasterize import composite_bwd
+    from gaussian_splats.kernels.rasterize.composite import tile_order
+    from gaussian_splats.kernels.rasterize.project import pack_records
+
+    order = tile_order(ranges_d, None, w, h, tile_size)
+    assert not torch.equal(order.cpu(), torch.arange(order.numel(), dtype=torch.int32))
+    records = pack_records(*args, "gaussian", CONFIDENCE)
+    img2 = torch.empty_like(image)
+    ft2 = torch.empty_like(final_t)
+    nc2 = torch.empty_like(ncon)
+    view = nat.make_view(1.0, 1.0, 0.0, 0.0, w, h, tile_size, opacity_threshold=THRESHOLD)
+    nat.check(nat.library().gs_composite(nat.ptr(records), nat.ptr(sid_d), nat.ptr(ranges_d),
+                                         nat.ptr(order), view, nat.ptr(img2), nat.ptr(ft2),
+                                         nat.ptr(nc2), nat.stream(device)), "composite")
+    torch.cuda.synchronize()
+    assert torch.equal(image, img2) and torch.equal(final_t, ft2) and torch.equal(ncon, nc2)
+
+    # Backward: the wrapper dispatches by contributor count; the identity
+    # order gives the same gradient up to the order of the atomic adds.
+    g = torch.randn(h, w, 3, generator=torch.Generator().manual_seed(5)).to(device)
+    grad = composite_bwd(*args, sid_d, ranges_d, g, final_t, ncon, w, h, tile_size, THRESHOLD,
+                         "gaussian")
+    grad2 = torch.zeros_like(grad)
+    nat.check(nat.library().gs_composite_bwd(
+        *(nat.ptr(t.contiguous()) for t in args), nat.ptr(sid_d), nat.ptr(ranges_d), nat.ptr(g),
+        nat.ptr(final_t), nat.ptr(ncon), None, view, nat.ptr(grad2), nat.stream(device)),
+        "composite_bwd")
+    torch.cuda.synchronize()
+    # Float atomics make both sums order-dependent: compare against the scale
+    # of each gradient column (a skipped or repeated tile would be O(1) off).
+    scale = grad2.abs().amax(dim=0, keepdim=True).clamp_min(1e-30)
+    assert float(((grad - grad2).abs() / scale).max()) < 1e-4

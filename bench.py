@@ -39,7 +39,25 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-tiles", type=int, default=24, help="tiles in the CPU baseline sample")
     ap.add_argument("--out", default=None, help="also write the JSON line to this file")
+    ap.add_argument(
+        "--copy-calibration", action="store_true",
+        help="only copy 512 MiB device to device three times (the known-size kernel that scales "
+             "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)",
+    )
     return ap.parse_args()
+
+
+def copy_calibration():
+    """Three 512 MiB device-to-device copies: FETCH_SIZE / WRITE_SIZE of this
+    kernel under rocprofv3 give the KiB-to-bytes factors of the traffic figures."""
+    n = 128 * 1024 * 1024  # floats
+    x = torch.ones(n, device="cuda")
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print("copied 512 MiB x3", flush=True)
 
 
 def stage_bytes(n, k, total, rows, pixels, processed_fwd, processed_bwd):
@@ -194,6 +212,9 @@ def cpu_baseline(scene, tile_size, sample_tiles):
 
 def main():
     args = parse_args()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
               "(the rasterizer runs on a single device; sharding by view or by screen band is "

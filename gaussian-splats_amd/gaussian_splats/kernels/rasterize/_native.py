@@ -133,6 +133,14 @@ _SIGNATURES = {
         [c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p],
     ),
     "gs_l1_loss_bwd": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
+    "gs_ssim_workspace_bytes": (c_size_t, [c_int32, c_int32]),
+    "gs_ssim_fwd": (
+        c_int, [c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_size_t, c_void_p]
+    ),
+    "gs_ssim_bwd": (
+        c_int,
+        [c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_size_t, c_void_p, c_void_p],
+    ),
 }
 
 _lock = threading.Lock()

@@ -8,6 +8,11 @@ differences and keeps a one-byte gradient sign per element, and a backward
 kernel that expands it.  The gradient equals autograd's for the torch
 expression bit for bit; the loss value is a deterministic fp32 sum that
 matches torch's reduction to rounding.
+
+``ssim(image, target)`` is the structural-similarity term of the same step
+(train.py:139, training/utils.py:65-67): a forward kernel computes the
+windowed moments, the mean SSIM and three per-pixel gradient maps; a backward
+kernel filters those maps into the image gradient.
 """
 
 from __future__ import annotations
@@ -80,3 +85,73 @@ def l1_loss(image: torch.Tensor, target: torch.Tensor, clamp: bool = False) -> t
     if image.dtype != torch.float32 or target.dtype != torch.float32:
         raise TypeError("l1_loss expects float32 tensors")
     return _L1Loss.apply(image, target, clamp)
+
+
+def ssim_forward(image: torch.Tensor, target: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Forward kernel: returns ``(ssim, workspace)``; the workspace holds what
+    :func:`ssim_backward` needs."""
+    device = nat.require_gpu(image, target)
+    if image.shape != target.shape or image.dim() != 3 or image.shape[2] != 3:
+        raise ValueError(
+            f"ssim expects [H, W, 3] image and target, got {tuple(image.shape)} and {tuple(target.shape)}"
+        )
+    image = nat.prepare(image)
+    target = nat.prepare(target)
+    h, w = image.shape[0], image.shape[1]
+    lib = nat.library()
+    out = torch.empty((), dtype=torch.float32, device=device)
+    ws_bytes = lib.gs_ssim_workspace_bytes(h, w)
+    ws = nat.workspace(ws_bytes, device)
+    nat.check(
+        lib.gs_ssim_fwd(nat.ptr(image), nat.ptr(target), h, w, nat.ptr(out), nat.ptr(ws),
+                        ws.numel(), nat.stream(device)),
+        "ssim",
+    )
+    return out, ws
+
+
+def ssim_backward(
+    image: torch.Tensor, target: torch.Tensor, workspace: torch.Tensor, grad_ssim: torch.Tensor
+) -> torch.Tensor:
+    """Backward kernel: gradient of the SSIM with respect to the image for the
+    upstream gradient ``grad_ssim`` (a one-element device tensor)."""
+    device = nat.require_gpu(image, target, workspace, grad_ssim)
+    image = nat.prepare(image)
+    target = nat.prepare(target)
+    grad_ssim = nat.prepare(grad_ssim.reshape(()))
+    h, w = image.shape[0], image.shape[1]
+    grad = torch.empty_like(image)
+    nat.check(
+        nat.library().gs_ssim_bwd(
+            nat.ptr(image), nat.ptr(target), h, w, nat.ptr(grad_ssim), nat.ptr(workspace),
+            workspace.numel(), nat.ptr(grad), nat.stream(device),
+        ),
+        "ssim backward",
+    )
+    return grad
+
+
+class _Ssim(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, image: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
+        value, ws = ssim_forward(image, target)
+        ctx.save_for_backward(image, target, ws)
+        return value
+
+    @staticmethod
+    def backward(ctx, grad_ssim: torch.Tensor):
+        image, target, ws = ctx.saved_tensors
+        return ssim_backward(image, target, ws, grad_ssim), None
+
+
+def ssim(image: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
+    """Mean structural similarity of two [H, W, 3] images with data range 1,
+    as the reference's training/utils.py:65-67 computes it with torchmetrics
+    (11-tap Gaussian window, sigma 1.5, k1 = 0.01, k2 = 0.03, mean over the
+    map cropped by 5 pixels and the channels); differentiable with respect to
+    ``image`` only."""
+    if target.requires_grad:
+        raise ValueError("ssim does not propagate gradients to the target")
+    if image.dtype != torch.float32 or target.dtype != torch.float32:
+        raise TypeError("ssim expects float32 tensors")
+    return _Ssim.apply(image, target)

@@ -259,6 +259,22 @@ GS_API int gs_l1_loss_bwd(
     const int8_t* code, const float* grad_loss, int64_t numel,
     float* grad_image, void* stream);
 
+/* Structural similarity term of the training step (train.py:139 through
+ * training/utils.py:65-67: torchmetrics structural_similarity_index_measure
+ * with data_range = 1 and its defaults, over the three channels of an
+ * [H, W, 3] image).  gs_ssim_fwd writes the mean SSIM to ssim[0] and keeps
+ * in the workspace what gs_ssim_bwd needs; gs_ssim_bwd writes
+ * grad_image = grad_ssim[0] * d SSIM / d image (grad_ssim in device memory)
+ * from the same image, target and workspace.  H and W must exceed 10. */
+GS_API size_t gs_ssim_workspace_bytes(int32_t height, int32_t width);
+GS_API int gs_ssim_fwd(
+    const float* image, const float* target, int32_t height, int32_t width,
+    float* ssim, void* workspace, size_t workspace_bytes, void* stream);
+GS_API int gs_ssim_bwd(
+    const float* image, const float* target, int32_t height, int32_t width,
+    const float* grad_ssim, const void* workspace, size_t workspace_bytes,
+    float* grad_image, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

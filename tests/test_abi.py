@@ -67,6 +67,20 @@ def test_l1_loss_host_checks():
     assert lib.gs_l1_loss_bwd(null, null, 0, null, null) == nat.GS_OK  # empty: nothing to do
 
 
+def test_ssim_host_checks():
+    lib = nat.library()
+    fake = ctypes.c_void_p(16)
+    null = ctypes.c_void_p(0)
+    assert lib.gs_ssim_workspace_bytes(10, 100) == 0
+    ws = lib.gs_ssim_workspace_bytes(1080, 1920)
+    assert ws >= 3 * 1080 * 1920 * 3 * 4
+    assert lib.gs_ssim_fwd(fake, fake, 10, 100, fake, fake, ws, null) == nat.GS_ERR_INVALID_ARGUMENT
+    assert lib.gs_ssim_fwd(null, fake, 1080, 1920, fake, fake, ws, null) == nat.GS_ERR_INVALID_ARGUMENT
+    assert lib.gs_ssim_fwd(fake, fake, 1080, 1920, fake, fake, ws - 1, null) == nat.GS_ERR_WORKSPACE
+    assert lib.gs_ssim_bwd(fake, fake, 1080, 1920, fake, fake, 16, fake, null) == nat.GS_ERR_WORKSPACE
+    assert lib.gs_ssim_bwd(fake, fake, 1080, 1920, null, fake, ws, fake, null) == nat.GS_ERR_INVALID_ARGUMENT
+
+
 def test_l1_loss_python_checks():
     from gaussian_splats.training import l1_loss
 

@@ -11,7 +11,7 @@ import pytest
 import torch
 
 from gaussian_splats.kernels.rasterize import _native as nat
-from gaussian_splats.training import l1_loss, l1_loss_backward, l1_loss_forward
+from gaussian_splats.training import l1_loss, l1_loss_backward, l1_loss_forward, ssim, ssim_forward
 from oracle import losses as orc
 
 pytestmark = pytest.mark.gpu
@@ -103,3 +103,74 @@ def test_l1_loss_unaligned_through_c_abi():
     assert abs(float(loss) - float(ref_loss)) <= 1e-6
     assert torch.equal(grad[1:], ref_grad)
     assert int(code[0]) == 0 and int(code[numel + 1]) == 0 and float(grad[0]) == 0.0
+
+
+def _torch_ssim_f32(x, t):
+    """torchmetrics' algorithm in float32 with torch ops on the GPU (the plain
+    PyTorch reference of the kernel): reflect pad, 2-D Gaussian conv2d of the
+    five moment maps, clamped variances, crop, mean."""
+    import torch.nn.functional as F
+
+    from oracle import losses as olosses
+
+    xt = x.permute(2, 0, 1)[None].detach().clone().requires_grad_(True)
+    tt = t.permute(2, 0, 1)[None]
+    g = torch.tensor(olosses.ssim_window(), dtype=torch.float32, device=x.device)
+    kernel = (g[:, None] @ g[None, :]).expand(3, 1, 11, 11).contiguous()
+    p = F.pad(xt, (5, 5, 5, 5), mode="reflect")
+    q = F.pad(tt, (5, 5, 5, 5), mode="reflect")
+    out = F.conv2d(torch.cat((p, q, p * p, q * q, p * q)), kernel, groups=3)
+    mx, my, exx, eyy, exy = out.split(1)
+    sxx = torch.clamp(exx - mx * mx, min=0.0)
+    syy = torch.clamp(eyy - my * my, min=0.0)
+    sxy = exy - mx * my
+    s = ((2 * mx * my + 1e-4) * (2 * sxy + 9e-4)) / ((mx * mx + my * my + 1e-4) * (sxx + syy + 9e-4))
+    value = s[..., 5:-5, 5:-5].mean()
+    value.backward()
+    return value.detach(), xt.grad[0].permute(1, 2, 0)
+
+
+def _ssim_inputs(h, w, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.rand(h, w, 3, generator=g)
+    # A smooth region and a noisy one, as rendered images have.
+    x[: h // 2] = x[: h // 2].mean()
+    t = (x + 0.1 * torch.randn(h, w, 3, generator=g)).clamp(0, 1)
+    return x, t
+
+
+@pytest.mark.parametrize("shape", [(1080, 1920), (37, 29), (11, 11), (64, 80)])
+def test_ssim_matches_torch_and_oracle(shape):
+    h, w = shape
+    print(f"[ssim] shape={shape}", flush=True)
+    x, t = _ssim_inputs(h, w, seed=h + w)
+    xd, td = x.to(DEV), t.to(DEV)
+    xg = xd.clone().requires_grad_(True)
+    value = ssim(xg, td)
+    (0.7 * value).backward()
+    torch.cuda.synchronize()
+    ref_value, ref_grad = _torch_ssim_f32(xd, td)
+    o_value, o_grad = orc.ssim(x.double().numpy(), t.double().numpy())
+    value_err = abs(float(value) - o_value)
+    ref_value_err = abs(float(ref_value) - o_value)
+    scale = np.abs(o_grad).max()
+    err = np.abs(xg.grad.cpu().double().numpy() / 0.7 - o_grad).max() / scale
+    ref_err = np.abs(ref_grad.cpu().double().numpy() - o_grad).max() / scale
+    print(f"[ssim] value err {value_err:.2e} (torch float32 {ref_value_err:.2e}), "
+          f"grad err {err:.2e} (torch float32 {ref_err:.2e})", flush=True)
+    # Against float64: within 1e-5 for the value and 1e-4 of the largest
+    # gradient, or no worse than 4x the float32 torch reference's own error.
+    assert value_err <= max(1e-5, 4 * ref_value_err)
+    assert err <= max(1e-4, 4 * ref_err)
+
+
+def test_ssim_deterministic_and_checks():
+    x, t = _ssim_inputs(96, 128, seed=1)
+    xd, td = x.to(DEV), t.to(DEV)
+    a, _ = ssim_forward(xd, td)
+    b, _ = ssim_forward(xd, td)
+    assert torch.equal(a, b)
+    with pytest.raises(ValueError):
+        ssim(torch.zeros(10, 30, 3, device=DEV), torch.zeros(10, 30, 3, device=DEV))
+    with pytest.raises(ValueError):
+        ssim(torch.zeros(30, 30, 4, device=DEV), torch.zeros(30, 30, 4, device=DEV))

@@ -40,6 +40,12 @@ def parse_args():
     ap.add_argument("--cpu-tiles", type=int, default=24, help="tiles in the CPU baseline sample")
     ap.add_argument("--out", default=None, help="also write the JSON line to this file")
     ap.add_argument(
+        "--train-step", action="store_true",
+        help="time the reference's whole training step instead (train.py:136-152: clamp, "
+             "L1 + D-SSIM + regularisers, backward, Adam) with the fused kernels, beside the "
+             "same step written with torch ops",
+    )
+    ap.add_argument(
         "--copy-calibration", action="store_true",
         help="only copy 512 MiB device to device three times (the known-size kernel that scales "
              "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)",
@@ -210,6 +216,118 @@ def cpu_baseline(scene, tile_size, sample_tiles):
     }
 
 
+# Hyper-parameters of the reference's training step (train.py:76-87, 115).
+LAMBDA_DSSIM, OPACITY_REG, SCALE_REG = 0.2, 1e-2, 1e-2
+LRS = {"mean": 1.6e-4, "rotation": 1e-3, "scale": 5e-3, "opacity": 5e-2, "color": 2.5e-3}
+
+
+def train_step_fused(splats, cam, target, tile_size, near, far, optimizer):
+    from gaussian_splats.splats import rasterize
+    from gaussian_splats.training import l1_loss, splat_regularizers, ssim
+
+    image = rasterize(splats, cam, tile_size=tile_size, near=near, far=far)
+    l1 = l1_loss(image, target, clamp=True)
+    dssim = 1 - ssim(image.clamp(0, 1), target)
+    regs = splat_regularizers(splats.opacity, splats.scale)
+    loss = (1 - LAMBDA_DSSIM) * l1 + LAMBDA_DSSIM * dssim + OPACITY_REG * regs[0] + SCALE_REG * regs[1]
+    loss.backward()
+    optimizer.step()
+    optimizer.zero_grad()
+    return loss
+
+
+def train_step_torch(splats, cam, target, tile_size, near, far, optimizer, window):
+    """The same step with torch ops for everything but the rasterizer: torch's
+    L1, SSIM by conv2d (the formulation torchmetrics uses), regularisers and
+    torch.optim.Adam."""
+    import torch.nn.functional as F
+
+    from gaussian_splats.splats import rasterize
+
+    image = rasterize(splats, cam, tile_size=tile_size, near=near, far=far).clamp(0, 1)
+    l1 = (image - target).abs().mean()
+    x = image.permute(2, 0, 1)[None]
+    y = target.permute(2, 0, 1)[None]
+    p, q = F.pad(x, (5, 5, 5, 5), mode="reflect"), F.pad(y, (5, 5, 5, 5), mode="reflect")
+    out = F.conv2d(torch.cat((p, q, p * p, q * q, p * q)), window, groups=3)
+    mx, my, exx, eyy, exy = out.split(1)
+    sxx, syy = torch.clamp(exx - mx * mx, min=0.0), torch.clamp(eyy - my * my, min=0.0)
+    s = ((2 * mx * my + 1e-4) * (2 * (exy - mx * my) + 9e-4)) / (
+        (mx * mx + my * my + 1e-4) * (sxx + syy + 9e-4))
+    dssim = 1 - s[..., 5:-5, 5:-5].mean()
+    loss = ((1 - LAMBDA_DSSIM) * l1 + LAMBDA_DSSIM * dssim
+            + OPACITY_REG * splats.opacity.sigmoid().mean() + SCALE_REG * splats.scale.exp().mean())
+    loss.backward()
+    optimizer.step()
+    optimizer.zero_grad()
+    return loss
+
+
+def bench_train_step(args):
+    """One JSON line: the reference's training step (config 3) per second with
+    the fused kernels, and the same step with torch ops for the loss terms and
+    the optimiser."""
+    from gaussian_splats import scenes
+    from gaussian_splats.kernels.rasterize import _native
+    from gaussian_splats.splats import GaussianSplat
+    from gaussian_splats.training import FusedAdam
+
+    _native.library()
+    device = torch.device("cuda:0")
+    scene = scenes.CONFIGS[args.config]()
+    cam = scene.cameras[0]
+    w, h = cam.image_size
+    if scene.target is None:
+        target = torch.rand(h, w, 3, device=device)
+    else:
+        target = (scene.target[0] if scene.target.dim() == 4 else scene.target).to(device)
+    g = torch.exp(-((torch.arange(11, dtype=torch.float32) - 5) / 1.5) ** 2 / 2)
+    g = (g / g.sum()).to(device)
+    window = (g[:, None] @ g[None, :]).expand(3, 1, 11, 11).contiguous()
+    results = {}
+    for kind in ("fused", "torch"):
+        splats = GaussianSplat.from_tensors(*(p.to(device) for p in scene.params()))
+        groups = [{"params": [getattr(splats, k)], "lr": lr, "name": k} for k, lr in LRS.items()]
+        opt = FusedAdam(groups, eps=1e-15) if kind == "fused" else torch.optim.Adam(groups, eps=1e-15)
+
+        def step():
+            if kind == "fused":
+                return train_step_fused(splats, cam, target, args.tile_size, scene.near, scene.far, opt)
+            return train_step_torch(splats, cam, target, args.tile_size, scene.near, scene.far, opt,
+                                    window)
+
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        results[kind] = 1e3 * (time.perf_counter() - t0) / args.steps
+        print(f"[bench] train step ({kind}): {results[kind]:.3f} ms", file=sys.stderr, flush=True)
+    result = {
+        "metric": "training steps/s at 1M Gaussians SH3 1080p (rasterize + L1 + D-SSIM + "
+                  "regularisers + backward + Adam)",
+        "value": round(1e3 / results["fused"], 2),
+        "unit": "steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(results["fused"], 4),
+        "higher_is_better": True,
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded scenes.CONFIGS distributions)",
+        "config": {"workload": f"{scene.name}: training step of train.py:136-152",
+                   "tile_size": args.tile_size},
+        "torch_ops_ms_per_step": round(results["torch"], 4),
+    }
+    line = json.dumps(result)
+    print(line, flush=True)
+    if args.out:
+        Path(args.out).write_text(line + "\n")
+
+
 def main():
     args = parse_args()
     if args.copy_calibration:
@@ -221,6 +339,9 @@ def main():
               "not built)",
               file=sys.stderr)
         sys.exit(2)
+    if args.train_step:
+        bench_train_step(args)
+        return
     from gaussian_splats import scenes
     from gaussian_splats.kernels.rasterize import _native
     from gaussian_splats.splats import GaussianSplat

@@ -119,6 +119,75 @@ __global__ __launch_bounds__(kLossBlock) void l1_bwd_kernel(const int8_t* __rest
   for (int64_t i = tail + t0; i < numel; i += stride) grad[i] = float(code[i]) * s;
 }
 
+// Regularisers of the training step (train.py:140-141): the means of
+// sigmoid(opacity) over N and of exp(scale) over 3N, two partial sums per
+// workgroup, added in a fixed order by reg_finish_kernel.
+__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+__global__ __launch_bounds__(kLossBlock) void reg_fwd_kernel(const float* __restrict__ opacity,
+                                                             const float* __restrict__ scale,
+                                                             int64_t n, float* __restrict__ partial) {
+  __shared__ float scratch[kLossBlock / 64];
+  const int64_t stride = int64_t(gridDim.x) * kLossBlock;
+  const int64_t t0 = int64_t(blockIdx.x) * kLossBlock + threadIdx.x;
+  float so = 0.0f, ss = 0.0f;
+  for (int64_t i = t0; i < n; i += stride) so += sigmoid(opacity[i]);
+  for (int64_t i = t0; i < 3 * n; i += stride) ss += expf(scale[i]);
+  const float bo = block_sum(so, scratch);
+  __syncthreads();
+  const float bs = block_sum(ss, scratch);
+  if (threadIdx.x == 0) {
+    partial[2 * blockIdx.x] = bo;
+    partial[2 * blockIdx.x + 1] = bs;
+  }
+}
+
+__global__ __launch_bounds__(kLossBlock) void reg_finish_kernel(const float* __restrict__ partial,
+                                                                int blocks, int64_t n,
+                                                                float* __restrict__ out) {
+  __shared__ double scratch[2][kLossBlock / 64];
+  double ao = 0.0, as = 0.0;
+  for (int i = threadIdx.x; i < blocks; i += kLossBlock) {
+    ao += double(partial[2 * i]);
+    as += double(partial[2 * i + 1]);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    ao += __shfl_xor(ao, o, 64);
+    as += __shfl_xor(as, o, 64);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    scratch[0][threadIdx.x >> 6] = ao;
+    scratch[1][threadIdx.x >> 6] = as;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double so = 0.0, ss = 0.0;
+    for (int w = 0; w < kLossBlock / 64; ++w) {
+      so += scratch[0][w];
+      ss += scratch[1][w];
+    }
+    out[0] = float(so / double(n));
+    out[1] = float(ss / (3.0 * double(n)));
+  }
+}
+
+// Autograd's gradients of the two means: (g0 (1/N)) (1 - y) y with
+// y = sigmoid(opacity), and (g1 (1/3N)) exp(scale).
+__global__ __launch_bounds__(kLossBlock) void reg_bwd_kernel(
+    const float* __restrict__ opacity, const float* __restrict__ scale, int64_t n,
+    const float* __restrict__ grad_out, float inv_n, float inv_3n,
+    float* __restrict__ grad_opacity, float* __restrict__ grad_scale) {
+  const float go = grad_out[0] * inv_n, gs_ = grad_out[1] * inv_3n;
+  const int64_t stride = int64_t(gridDim.x) * kLossBlock;
+  const int64_t t0 = int64_t(blockIdx.x) * kLossBlock + threadIdx.x;
+  for (int64_t i = t0; i < n; i += stride) {
+    const float y = sigmoid(opacity[i]);
+    grad_opacity[i] = go * (1.0f - y) * y;
+  }
+  for (int64_t i = t0; i < 3 * n; i += stride) grad_scale[i] = gs_ * expf(scale[i]);
+}
+
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
 int loss_blocks(int64_t numel) {
@@ -171,6 +240,45 @@ GS_API int gs_l1_loss_bwd(const int8_t* code, const float* grad_loss, int64_t nu
                                                                           inv_numel, numel, vec,
                                                                           grad_image);
   return check_launch("l1_loss_bwd");
+}
+
+GS_API size_t gs_splat_regularizers_workspace_bytes(int64_t n) {
+  (void)n;
+  return size_t(2 * kLossPartials) * sizeof(float);
+}
+
+GS_API int gs_splat_regularizers_fwd(const float* opacity, const float* scale, int64_t n,
+                                     float* out, void* workspace, size_t workspace_bytes,
+                                     void* stream) {
+  clear_error();
+  GS_REQUIRE(n >= 0, GS_ERR_INVALID_ARGUMENT, "n must be non-negative");
+  GS_REQUIRE(out && (n == 0 || (opacity && scale)), GS_ERR_INVALID_ARGUMENT,
+             "null pointer argument");
+  GS_REQUIRE(workspace && workspace_bytes >= gs_splat_regularizers_workspace_bytes(n),
+             GS_ERR_WORKSPACE, "workspace too small (%zu bytes, need %zu)", workspace_bytes,
+             gs_splat_regularizers_workspace_bytes(n));
+  const hipStream_t s = as_stream(stream);
+  float* partial = static_cast<float*>(workspace);
+  const int blocks = loss_blocks(3 * n);
+  reg_fwd_kernel<<<blocks, kLossBlock, 0, s>>>(opacity, scale, n, partial);
+  GS_TRY(check_launch("regularizers_fwd"));
+  // n = 0 gives 0 / 0 = NaN for both means, as torch's mean of an empty tensor.
+  reg_finish_kernel<<<1, kLossBlock, 0, s>>>(partial, blocks, n, out);
+  return check_launch("regularizers_finish");
+}
+
+GS_API int gs_splat_regularizers_bwd(const float* opacity, const float* scale, int64_t n,
+                                     const float* grad_out, float* grad_opacity,
+                                     float* grad_scale, void* stream) {
+  clear_error();
+  GS_REQUIRE(n >= 0, GS_ERR_INVALID_ARGUMENT, "n must be non-negative");
+  if (n == 0) return GS_OK;
+  GS_REQUIRE(opacity && scale && grad_out && grad_opacity && grad_scale, GS_ERR_INVALID_ARGUMENT,
+             "null pointer argument");
+  const float inv_n = 1.0f / float(n), inv_3n = 1.0f / float(3 * n);
+  reg_bwd_kernel<<<loss_blocks(3 * n), kLossBlock, 0, as_stream(stream)>>>(
+      opacity, scale, n, grad_out, inv_n, inv_3n, grad_opacity, grad_scale);
+  return check_launch("regularizers_bwd");
 }
 
 }  // extern "C"

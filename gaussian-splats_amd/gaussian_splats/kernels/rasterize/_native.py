@@ -27,6 +27,21 @@ GS_ERR_WORKSPACE = 5
 MODES = {"gaussian": 0, "ellipsoid": 1}
 
 
+class GsAdamTensor(ctypes.Structure):
+    _fields_ = [
+        ("param", c_void_p),
+        ("grad", c_void_p),
+        ("exp_avg", c_void_p),
+        ("exp_avg_sq", c_void_p),
+        ("numel", c_int64),
+        ("lr", ctypes.c_double),
+        ("step", c_int64),
+    ]
+
+
+ADAM_MAX_TENSORS = 8
+
+
 class GsView(ctypes.Structure):
     _fields_ = [
         ("fx", c_float),
@@ -133,6 +148,17 @@ _SIGNATURES = {
         [c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p],
     ),
     "gs_l1_loss_bwd": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
+    "gs_splat_regularizers_workspace_bytes": (c_size_t, [c_int64]),
+    "gs_splat_regularizers_fwd": (
+        c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_size_t, c_void_p]
+    ),
+    "gs_splat_regularizers_bwd": (
+        c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p]
+    ),
+    "gs_adam_step": (
+        c_int, [c_void_p, c_int32, ctypes.c_double, ctypes.c_double, ctypes.c_double,
+                ctypes.c_double, c_void_p]
+    ),
     "gs_ssim_workspace_bytes": (c_size_t, [c_int32, c_int32]),
     "gs_ssim_fwd": (
         c_int, [c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_size_t, c_void_p]

@@ -155,3 +155,43 @@ def ssim(image: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
     if image.dtype != torch.float32 or target.dtype != torch.float32:
         raise TypeError("ssim expects float32 tensors")
     return _Ssim.apply(image, target)
+
+
+class _Regularizers(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, opacity: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+        device = nat.require_gpu(opacity, scale)
+        n = opacity.shape[0]
+        if opacity.numel() != n or scale.shape != (n, 3):
+            raise ValueError(f"expected opacity [N, 1] and scale [N, 3], got {tuple(opacity.shape)} "
+                             f"and {tuple(scale.shape)}")
+        opacity, scale = nat.prepare(opacity), nat.prepare(scale)
+        lib = nat.library()
+        out = torch.empty(2, dtype=torch.float32, device=device)
+        ws = nat.workspace(lib.gs_splat_regularizers_workspace_bytes(n), device)
+        nat.check(lib.gs_splat_regularizers_fwd(nat.ptr(opacity), nat.ptr(scale), n, nat.ptr(out),
+                                                nat.ptr(ws), ws.numel(), nat.stream(device)),
+                  "regularizers")
+        ctx.save_for_backward(opacity, scale)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out: torch.Tensor):
+        opacity, scale = ctx.saved_tensors
+        grad_out = nat.prepare(grad_out.contiguous())
+        grad_opacity = torch.empty_like(opacity)
+        grad_scale = torch.empty_like(scale)
+        nat.check(nat.library().gs_splat_regularizers_bwd(
+            nat.ptr(opacity), nat.ptr(scale), opacity.shape[0], nat.ptr(grad_out),
+            nat.ptr(grad_opacity), nat.ptr(grad_scale), nat.stream(opacity.device)),
+            "regularizers backward")
+        return grad_opacity, grad_scale
+
+
+def splat_regularizers(opacity: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """``[opacity.sigmoid().mean(), scale.exp().mean()]`` in one kernel each way:
+    the two regularisers of the training step before their weights
+    (train.py:140-141)."""
+    if opacity.dtype != torch.float32 or scale.dtype != torch.float32:
+        raise TypeError("splat_regularizers expects float32 tensors")
+    return _Regularizers.apply(opacity, scale)

@@ -1,0 +1,74 @@
+"""Adam for the Gaussian parameters in one HIP launch per step.
+
+:class:`FusedAdam` is a ``torch.optim.Adam`` (so code that checks
+``isinstance(optimizer, torch.optim.Adam)`` and edits its ``state`` -- the
+reference's relocation, training/utils.py:186-205 -- keeps working) whose
+``step`` applies the update of torch's multi-tensor Adam to every parameter
+with ``gs_adam_step``: each element is read and written once.  Supported:
+float32 GPU parameters, per-group ``lr``/``betas``/``eps``/``weight_decay``;
+``amsgrad``, ``maximize`` and sparse gradients are not.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from ..kernels.rasterize import _native as nat
+
+
+class FusedAdam(torch.optim.Adam):
+    def __init__(self, params, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.0,
+                 amsgrad=False, *, maximize=False):
+        if amsgrad or maximize:
+            raise NotImplementedError("FusedAdam implements plain Adam (no amsgrad, no maximize)")
+        super().__init__(params, lr=lr, betas=betas, eps=eps, weight_decay=weight_decay,
+                         foreach=False)
+
+    @torch.no_grad()
+    def step(self, closure=None):
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+        lib = nat.library()
+        for group in self.param_groups:
+            beta1, beta2 = group["betas"]
+            entries = []
+            device = None
+            for p in group["params"]:
+                if p.grad is None:
+                    continue
+                if p.grad.is_sparse:
+                    raise RuntimeError("FusedAdam does not support sparse gradients")
+                if p.dtype != torch.float32 or not p.is_cuda:
+                    raise TypeError("FusedAdam updates float32 parameters on a ROCm GPU")
+                device = nat.require_gpu(p) if device is None else device
+                state = self.state[p]
+                if len(state) == 0:
+                    state["step"] = torch.tensor(0.0, dtype=torch.float32)
+                    state["exp_avg"] = torch.zeros_like(p, memory_format=torch.preserve_format)
+                    state["exp_avg_sq"] = torch.zeros_like(p, memory_format=torch.preserve_format)
+                state["step"] += 1
+                grad = p.grad if p.grad.is_contiguous() else p.grad.contiguous()
+                for name in ("exp_avg", "exp_avg_sq"):
+                    if not state[name].is_contiguous():
+                        state[name] = state[name].contiguous()
+                if not p.is_contiguous():
+                    raise ValueError("FusedAdam needs contiguous parameters")
+                entries.append(nat.GsAdamTensor(
+                    p.data_ptr(), grad.data_ptr(), state["exp_avg"].data_ptr(),
+                    state["exp_avg_sq"].data_ptr(), p.numel(), float(group["lr"]),
+                    int(state["step"].item()),
+                ))
+            for i in range(0, len(entries), nat.ADAM_MAX_TENSORS):
+                chunk = entries[i:i + nat.ADAM_MAX_TENSORS]
+                array = (nat.GsAdamTensor * len(chunk))(*chunk)
+                nat.check(
+                    lib.gs_adam_step(ctypes.cast(array, ctypes.c_void_p), len(chunk), float(beta1),
+                                     float(beta2), float(group["eps"]),
+                                     float(group["weight_decay"]), nat.stream(device)),
+                    "adam_step",
+                )
+        return loss

@@ -275,6 +275,38 @@ GS_API int gs_ssim_bwd(
     const float* grad_ssim, const void* workspace, size_t workspace_bytes,
     float* grad_image, void* stream);
 
+/* Regularisers of the training step (train.py:140-141 before their
+ * weights): out[0] = mean(sigmoid(opacity[N])), out[1] = mean(exp(scale[N,3])),
+ * deterministic; the backward writes autograd's gradients of the two means
+ * for the upstream gradients grad_out[2] (device memory). */
+GS_API size_t gs_splat_regularizers_workspace_bytes(int64_t n);
+GS_API int gs_splat_regularizers_fwd(
+    const float* opacity, const float* scale, int64_t n, float* out,
+    void* workspace, size_t workspace_bytes, void* stream);
+GS_API int gs_splat_regularizers_bwd(
+    const float* opacity, const float* scale, int64_t n, const float* grad_out,
+    float* grad_opacity, float* grad_scale, void* stream);
+
+/* One Adam step (torch.optim.Adam's update, multi-tensor path, no amsgrad)
+ * over up to GS_ADAM_MAX_TENSORS float32 tensors in one launch: the optimiser
+ * step of the training loop (src/gaussian_splats/training/train.py:115,151).
+ * `step` is the step count after this step (1 on the first); `lr` is per
+ * tensor (the reference changes the position group's rate every step,
+ * train.py:131-133).  Updates param, exp_avg and exp_avg_sq in place. */
+#define GS_ADAM_MAX_TENSORS 8
+typedef struct gs_adam_tensor {
+  float* param;
+  const float* grad;
+  float* exp_avg;
+  float* exp_avg_sq;
+  int64_t numel;
+  double lr;
+  int64_t step;
+} gs_adam_tensor;
+GS_API int gs_adam_step(
+    const gs_adam_tensor* tensors, int32_t count, double beta1, double beta2,
+    double eps, double weight_decay, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

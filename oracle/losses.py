@@ -87,3 +87,13 @@ def ssim(image: np.ndarray, target: np.ndarray) -> tuple[float, np.ndarray]:
     gxy = 2 * a / (c * d)
     grad = (_full_filter(gm, w) + 2 * x * _full_filter(gxx, w) + y * _full_filter(gxy, w)) / m
     return float(s.mean()), grad
+
+
+def splat_regularizers(opacity: np.ndarray, scale: np.ndarray):
+    """The regularisers of train.py:140-141 before their weights:
+    (mean sigmoid(opacity), mean exp(scale)) and their gradients, float64."""
+    o = np.asarray(opacity, dtype=np.float64)
+    s = np.asarray(scale, dtype=np.float64)
+    y = 1 / (1 + np.exp(-o))
+    e = np.exp(s)
+    return (float(y.mean()), float(e.mean())), (y * (1 - y) / o.size, e / s.size)

@@ -81,6 +81,26 @@ def test_ssim_host_checks():
     assert lib.gs_ssim_bwd(fake, fake, 1080, 1920, null, fake, ws, fake, null) == nat.GS_ERR_INVALID_ARGUMENT
 
 
+def test_adam_and_regularizer_host_checks():
+    lib = nat.library()
+    fake = ctypes.c_void_p(16)
+    null = ctypes.c_void_p(0)
+    t = nat.GsAdamTensor(16, 16, 16, 16, 100, 1e-3, 0)  # step 0 is invalid
+    arr = (nat.GsAdamTensor * 1)(t)
+    p = ctypes.cast(arr, ctypes.c_void_p)
+    assert lib.gs_adam_step(p, 1, 0.9, 0.999, 1e-15, 0.0, null) == nat.GS_ERR_INVALID_ARGUMENT
+    arr[0].step = 1
+    assert lib.gs_adam_step(p, 1, 1.0, 0.999, 1e-15, 0.0, null) == nat.GS_ERR_INVALID_ARGUMENT
+    assert lib.gs_adam_step(p, nat.ADAM_MAX_TENSORS + 1, 0.9, 0.999, 1e-15, 0.0, null) == nat.GS_ERR_INVALID_ARGUMENT
+    arr[0].grad = None
+    assert lib.gs_adam_step(p, 1, 0.9, 0.999, 1e-15, 0.0, null) == nat.GS_ERR_INVALID_ARGUMENT
+    assert lib.gs_adam_step(null, 0, 0.9, 0.999, 1e-15, 0.0, null) == nat.GS_OK  # nothing to do
+    ws = lib.gs_splat_regularizers_workspace_bytes(1000)
+    assert lib.gs_splat_regularizers_fwd(fake, fake, -1, fake, fake, ws, null) == nat.GS_ERR_INVALID_ARGUMENT
+    assert lib.gs_splat_regularizers_fwd(fake, fake, 10, fake, fake, ws - 1, null) == nat.GS_ERR_WORKSPACE
+    assert lib.gs_splat_regularizers_bwd(fake, null, 10, fake, fake, fake, null) == nat.GS_ERR_INVALID_ARGUMENT
+
+
 def test_l1_loss_python_checks():
     from gaussian_splats.training import l1_loss
 

@@ -151,6 +151,7 @@ def test_ssim_matches_torch_and_oracle(shape):
     torch.cuda.synchronize()
     ref_value, ref_grad = _torch_ssim_f32(xd, td)
     o_value, o_grad = orc.ssim(x.double().numpy(), t.double().numpy())
+    value = value.detach()
     value_err = abs(float(value) - o_value)
     ref_value_err = abs(float(ref_value) - o_value)
     scale = np.abs(o_grad).max()

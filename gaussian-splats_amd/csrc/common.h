@@ -62,6 +62,12 @@ constexpr int kWave = 64;
 // order of tile_order.hip partitions the tiles the same way.
 constexpr int kCompositeWaves = 4;
 
+// Images with fewer tiles than this are composited with the tile's bands
+// split over kCompositeWaves waves (tiles of 16 and 32 pixels): with one wave
+// per tile they would leave most SIMDs idle and wait on their longest tiles.
+constexpr int kCompositeSplitTiles = 4096;
+inline bool composite_split(int num_tiles) { return num_tiles < kCompositeSplitTiles; }
+
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 inline size_t align_up(size_t x, size_t a = 256) { return (x + a - 1) / a * a; }

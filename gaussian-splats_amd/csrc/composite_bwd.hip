@@ -41,10 +41,15 @@ struct CompositeBwdArgs {
   float* grad;  // [N, 9]
 };
 
-template <int TILE>
+// SPLIT waves share a tile, each taking SPLIT-th of its 64-pixel bands and
+// walking back from its own pixels' largest contributor count (see
+// composite_fwd.hip); each wave adds its bands' share of every gradient.
+template <int TILE, int SPLIT>
 __global__ __launch_bounds__(kCompositeWaves * 64) void composite_bwd_kernel(CompositeBwdArgs a) {
   constexpr int NPIX = TILE * TILE;
-  constexpr int PIX = NPIX >= 64 ? NPIX / 64 : 1;
+  constexpr int PIX_TILE = NPIX >= 64 ? NPIX / 64 : 1;
+  static_assert(PIX_TILE % SPLIT == 0 && kCompositeWaves % SPLIT == 0, "bands split evenly");
+  constexpr int PIX = PIX_TILE / SPLIT;  // this wave's pixels per lane
   constexpr int kBandRows = 64 / TILE > 0 ? 64 / TILE : 1;  // tile rows per band of 64 pixels
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
@@ -53,9 +58,10 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_bwd_kernel(Com
   // broadcasts per entry instead of twelve v_readlane.
   __shared__ float4 chunk[kCompositeWaves][64][3];
   // Slot -> tile through the optional dispatch order (tile_order.hip).
-  const int slot = xcd_swizzle(blockIdx.x, gridDim.x) * kCompositeWaves + wid;
+  const int slot = xcd_swizzle(blockIdx.x, gridDim.x) * (kCompositeWaves / SPLIT) + wid / SPLIT;
   if (slot >= a.num_tiles) return;
   const int tile = a.order ? a.order[slot] : slot;
+  const int band0 = (wid % SPLIT) * PIX;  // first band of this wave
 
   const int tx = tile % a.tiles_w;
   const int ty = tile / a.tiles_w;
@@ -70,7 +76,7 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_bwd_kernel(Com
   int max_n = 0;
 #pragma unroll
   for (int k = 0; k < PIX; ++k) {
-    const int q = lane + 64 * k;
+    const int q = lane + 64 * (band0 + k);
     const int px = ox + (q % TILE), py = oy + (q / TILE);
     const bool valid = q < NPIX && px < a.width && py < a.height;
     const int64_t pix = int64_t(py) * a.width + px;
@@ -86,9 +92,10 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_bwd_kernel(Com
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) max_n = max(max_n, __shfl_xor(max_n, o, 64));
 
-  const float rx0 = float(ox), ry0 = float(oy);
+  // Pixel rectangle of this wave's bands clipped to the image.
+  const float rx0 = float(ox), ry0 = float(oy + band0 * kBandRows);
   const float rx1 = float(min(ox + TILE, a.width) - 1);
-  const float ry1 = float(min(oy + TILE, a.height) - 1);
+  const float ry1 = float(min(min(oy + (band0 + PIX) * kBandRows, oy + TILE), a.height) - 1);
   // Gradient fields written by this lane's two atomics: lane 16 r writes the
   // row-r fields of t0 and t1 of the nine-way sum, lane 1 the opacity total t2.
   const int field = sum9_field(lane >> 4);
@@ -199,10 +206,18 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_bwd_kernel(Com
   }
 }
 
+template <int TILE, int SPLIT>
+void launch_split(const CompositeBwdArgs& a, hipStream_t s) {
+  const unsigned blocks = unsigned(ceil_div(a.num_tiles, kCompositeWaves / SPLIT));
+  composite_bwd_kernel<TILE, SPLIT><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
+}
+
 template <int TILE>
 void launch(const CompositeBwdArgs& a, hipStream_t s) {
-  const unsigned blocks = unsigned(ceil_div(a.num_tiles, kCompositeWaves));
-  composite_bwd_kernel<TILE><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
+  if constexpr (TILE >= 16) {
+    if (composite_split(a.num_tiles)) return launch_split<TILE, kCompositeWaves>(a, s);
+  }
+  launch_split<TILE, 1>(a, s);
 }
 
 }  // namespace

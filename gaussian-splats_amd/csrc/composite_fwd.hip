@@ -35,10 +35,16 @@ struct CompositeArgs {
   int32_t* n_contrib;
 };
 
-template <int TILE, bool ELLIPSOID>
+// SPLIT waves share a tile, each compositing SPLIT-th of its 64-pixel bands
+// (every wave walks the whole list).  SPLIT = 1 suits images with enough
+// tiles to fill the GPU; SPLIT = 4 gives four times the waves when tiles are
+// few, at the cost of repeating the per-entry work in each wave.
+template <int TILE, bool ELLIPSOID, int SPLIT>
 __global__ __launch_bounds__(kCompositeWaves * 64) void composite_fwd_kernel(CompositeArgs a) {
   constexpr int NPIX = TILE * TILE;
-  constexpr int PIX = NPIX >= 64 ? NPIX / 64 : 1;
+  constexpr int PIX_TILE = NPIX >= 64 ? NPIX / 64 : 1;
+  static_assert(PIX_TILE % SPLIT == 0 && kCompositeWaves % SPLIT == 0, "bands split evenly");
+  constexpr int PIX = PIX_TILE / SPLIT;  // this wave's pixels per lane
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
   // The wave's current 64 entries, three float4 per entry (u, v, o, pa),
@@ -46,9 +52,10 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_fwd_kernel(Com
   // broadcasts per entry instead of ten v_readlane.
   __shared__ float4 chunk[kCompositeWaves][64][3];
   // Slot -> tile through the optional dispatch order (tile_order.hip).
-  const int slot = xcd_swizzle(blockIdx.x, gridDim.x) * kCompositeWaves + wid;
+  const int slot = xcd_swizzle(blockIdx.x, gridDim.x) * (kCompositeWaves / SPLIT) + wid / SPLIT;
   if (slot >= a.num_tiles) return;
   const int tile = a.order ? a.order[slot] : slot;
+  const int band0 = (wid % SPLIT) * PIX;  // first band of this wave
 
   const int tx = tile % a.tiles_w;
   const int ty = tile / a.tiles_w;
@@ -66,7 +73,7 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_fwd_kernel(Com
   const bool start_active = (1.0f - 1.0f) < a.threshold;
 #pragma unroll
   for (int k = 0; k < PIX; ++k) {
-    const int q = lane + 64 * k;
+    const int q = lane + 64 * (band0 + k);
     const int px = ox + (q % TILE), py = oy + (q / TILE);
     const bool valid = q < NPIX && px < a.width && py < a.height;
     pyf[k] = float(py);
@@ -75,10 +82,12 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_fwd_kernel(Com
     live[k] = valid && start_active;
     ncon[k] = live[k] ? list_len : 0;
   }
-  // Pixel rectangle of the tile clipped to the image, for the overlap test.
-  const float rx0 = float(ox), ry0 = float(oy);
+  // Pixel rectangle of this wave's bands clipped to the image, for the
+  // overlap test (64 / TILE rows per band).
+  constexpr int kBandRows = 64 / TILE > 0 ? 64 / TILE : 1;
+  const float rx0 = float(ox), ry0 = float(oy + band0 * kBandRows);
   const float rx1 = float(min(ox + TILE, a.width) - 1);
-  const float ry1 = float(min(oy + TILE, a.height) - 1);
+  const float ry1 = float(min(min(oy + (band0 + PIX) * kBandRows, oy + TILE), a.height) - 1);
 
   auto any_live = [&]() {
     bool l = false;
@@ -145,7 +154,7 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_fwd_kernel(Com
 
 #pragma unroll
   for (int k = 0; k < PIX; ++k) {
-    const int q = lane + 64 * k;
+    const int q = lane + 64 * (band0 + k);
     const int px = ox + (q % TILE), py = oy + (q / TILE);
     if (q < NPIX && px < a.width && py < a.height) {
       const int64_t pix = int64_t(py) * a.width + px;
@@ -158,13 +167,21 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_fwd_kernel(Com
   }
 }
 
+template <int TILE, int SPLIT>
+void launch_split(const CompositeArgs& a, bool ellipsoid, hipStream_t s) {
+  const unsigned blocks = unsigned(ceil_div(a.num_tiles, kCompositeWaves / SPLIT));
+  if (ellipsoid)
+    composite_fwd_kernel<TILE, true, SPLIT><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
+  else
+    composite_fwd_kernel<TILE, false, SPLIT><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
+}
+
 template <int TILE>
 void launch(const CompositeArgs& a, bool ellipsoid, hipStream_t s) {
-  const unsigned blocks = unsigned(ceil_div(a.num_tiles, kCompositeWaves));
-  if (ellipsoid)
-    composite_fwd_kernel<TILE, true><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
-  else
-    composite_fwd_kernel<TILE, false><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
+  if constexpr (TILE >= 16) {
+    if (composite_split(a.num_tiles)) return launch_split<TILE, kCompositeWaves>(a, ellipsoid, s);
+  }
+  launch_split<TILE, 1>(a, ellipsoid, s);
 }
 
 }  // namespace

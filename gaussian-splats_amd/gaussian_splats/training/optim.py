@@ -32,11 +32,13 @@ class FusedAdam(torch.optim.Adam):
         if closure is not None:
             with torch.enable_grad():
                 loss = closure()
-        lib = nat.library()
+        # Tensors of every group that share betas, eps and weight decay go into
+        # one launch (the learning rate is per tensor).
+        batches: dict[tuple, list] = {}
+        device = None
         for group in self.param_groups:
             beta1, beta2 = group["betas"]
-            entries = []
-            device = None
+            key = (float(beta1), float(beta2), float(group["eps"]), float(group["weight_decay"]))
             for p in group["params"]:
                 if p.grad is None:
                     continue
@@ -44,7 +46,12 @@ class FusedAdam(torch.optim.Adam):
                     raise RuntimeError("FusedAdam does not support sparse gradients")
                 if p.dtype != torch.float32 or not p.is_cuda:
                     raise TypeError("FusedAdam updates float32 parameters on a ROCm GPU")
-                device = nat.require_gpu(p) if device is None else device
+                if not p.is_contiguous():
+                    raise ValueError("FusedAdam needs contiguous parameters")
+                if device is None:
+                    device = nat.require_gpu(p)
+                elif p.device != device:
+                    raise ValueError(f"parameters on different devices: {device} and {p.device}")
                 state = self.state[p]
                 if len(state) == 0:
                     state["step"] = torch.tensor(0.0, dtype=torch.float32)
@@ -55,20 +62,19 @@ class FusedAdam(torch.optim.Adam):
                 for name in ("exp_avg", "exp_avg_sq"):
                     if not state[name].is_contiguous():
                         state[name] = state[name].contiguous()
-                if not p.is_contiguous():
-                    raise ValueError("FusedAdam needs contiguous parameters")
-                entries.append(nat.GsAdamTensor(
+                batches.setdefault(key, []).append(nat.GsAdamTensor(
                     p.data_ptr(), grad.data_ptr(), state["exp_avg"].data_ptr(),
                     state["exp_avg_sq"].data_ptr(), p.numel(), float(group["lr"]),
                     int(state["step"].item()),
                 ))
+        lib = nat.library()
+        for (beta1, beta2, eps, weight_decay), entries in batches.items():
             for i in range(0, len(entries), nat.ADAM_MAX_TENSORS):
                 chunk = entries[i:i + nat.ADAM_MAX_TENSORS]
                 array = (nat.GsAdamTensor * len(chunk))(*chunk)
                 nat.check(
-                    lib.gs_adam_step(ctypes.cast(array, ctypes.c_void_p), len(chunk), float(beta1),
-                                     float(beta2), float(group["eps"]),
-                                     float(group["weight_decay"]), nat.stream(device)),
+                    lib.gs_adam_step(ctypes.cast(array, ctypes.c_void_p), len(chunk), beta1, beta2,
+                                     eps, weight_decay, nat.stream(device)),
                     "adam_step",
                 )
         return loss

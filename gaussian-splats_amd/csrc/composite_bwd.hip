@@ -38,13 +38,17 @@ struct CompositeBwdArgs {
   const float* final_t;
   const int32_t* n_contrib;
   int width, height, tiles_w, num_tiles;
-  float* grad;  // [N, 9]
+  float* grad;      // [N, 9]
+  float* grad_abs;  // [N, 2]: sums of |per-pixel mean gradient| (ABS kernels only)
 };
 
 // SPLIT waves share a tile, each taking SPLIT-th of its 64-pixel bands and
 // walking back from its own pixels' largest contributor count (see
 // composite_fwd.hip); each wave adds its bands' share of every gradient.
-template <int TILE, int SPLIT>
+// ABS: also sums, per Gaussian, the absolute values of the per-pixel terms of
+// the mean gradient, |dL/du| and |dL/dv| of every pixel (composite_bwd.py:
+// 180-185,194-195), into grad_abs.
+template <int TILE, int SPLIT, bool ABS>
 __global__ __launch_bounds__(kCompositeWaves * 64) void composite_bwd_kernel(CompositeBwdArgs a) {
   constexpr int NPIX = TILE * TILE;
   constexpr int PIX_TILE = NPIX >= 64 ? NPIX / 64 : 1;
@@ -145,6 +149,9 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_bwd_kernel(Com
       // first term needs no add.
       float s0 = -0.0f, s1 = -0.0f, s2 = -0.0f;  // sum q, q dy, q dy^2
       float sr = -0.0f, sg = -0.0f, sb = -0.0f;
+      float ax = -0.0f, ay = -0.0f;  // ABS: sum |q (oa dx + ob dy)|, |q (ob dx + oc dy)|
+      const float oa = f2.y, ob = f2.z, oc = f2.w;
+      const float oadx = oa * c.dx, obdx = ob * c.dx;
       bool touched = false;
       // Branch-free: an entry a pixel did not process while active, or whose
       // alpha is cut to 0, runs with alpha = 0, which leaves T, g.S and every
@@ -178,13 +185,16 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_bwd_kernel(Com
         s0 += q;
         s1 += qy;
         s2 += qy * dy;
+        if constexpr (ABS) {
+          ax += fabsf(q * fmaf(ob, dy, oadx));
+          ay += fabsf(q * fmaf(oc, dy, obdx));
+        }
       }
       if (__ballot(touched) == 0) continue;
       // d alpha / d(u, v, conic) folded per lane before the reduction
       // (k = -o/2, -2k = o):  u: o (a Sx + b Sy),  v: o (b Sx + c Sy),
       // inv00: k Sxx,  inv01: k Sxy,  inv11: k Syy,  Sx = dx s0, Sxx = dx^2 s0,
       // Sxy = dx s1, Sy = s1, Syy = s2.
-      const float oa = f2.y, ob = f2.z, oc = f2.w;
       const float sx = c.dx * s0;
       const float kdx = (-0.5f * s.o) * c.dx;
       float v[9];
@@ -202,6 +212,15 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_bwd_kernel(Com
       float* dst = a.grad + int64_t(__builtin_amdgcn_readlane(gid, j)) * 9;
       if (row_writer) unsafeAtomicAdd(dst + field, t0);
       if (second_writer) unsafeAtomicAdd(dst + second_field, row_writer ? t1 : t2);
+      if constexpr (ABS) {
+        // Lanes 0-31 fold |du| terms, 32-63 |dv| terms; then every lane of
+        // rows 0-1 holds the |du| total and of rows 2-3 the |dv| total.
+        const float h = fold_halves(ax, ay);
+        const float tabs = row_sum(fold_rows(h, h));
+        if ((lane & 31) == 0)
+          unsafeAtomicAdd(a.grad_abs + int64_t(__builtin_amdgcn_readlane(gid, j)) * 2 + (lane >> 5),
+                          tabs);
+      }
     }
   }
 }
@@ -209,7 +228,10 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_bwd_kernel(Com
 template <int TILE, int SPLIT>
 void launch_split(const CompositeBwdArgs& a, hipStream_t s) {
   const unsigned blocks = unsigned(ceil_div(a.num_tiles, kCompositeWaves / SPLIT));
-  composite_bwd_kernel<TILE, SPLIT><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
+  if (a.grad_abs)
+    composite_bwd_kernel<TILE, SPLIT, true><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
+  else
+    composite_bwd_kernel<TILE, SPLIT, false><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
 }
 
 template <int TILE>
@@ -232,7 +254,8 @@ extern "C" GS_API int gs_composite_bwd(const float* projected_mean,
                                        const int32_t* gaussian_ids, const int64_t* ranges,
                                        const float* grad_image, const float* final_transmittance,
                                        const int32_t* n_contributors, const int32_t* tile_order,
-                                       gs_view view, float* grad_projected, void* stream) {
+                                       gs_view view, float* grad_projected, float* grad_absolute,
+                                       void* stream) {
   clear_error();
   GS_TRY(check_view(view, true));
   GS_REQUIRE(view.rendering_mode == GS_MODE_GAUSSIAN, GS_ERR_UNSUPPORTED,
@@ -257,6 +280,7 @@ extern "C" GS_API int gs_composite_bwd(const float* projected_mean,
   a.tiles_w = tiles_along(view.image_width, view.tile_size);
   a.num_tiles = a.tiles_w * tiles_along(view.image_height, view.tile_size);
   a.grad = grad_projected;
+  a.grad_abs = grad_absolute;
   hipStream_t s = as_stream(stream);
   switch (view.tile_size) {
     case 4: launch<4>(a, s); break;

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parents[2] / "_lib" / "libgs_raster.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 GS_OK = 0
 GS_ERR_INVALID_ARGUMENT = 1
@@ -136,7 +136,7 @@ _SIGNATURES = {
     ),
     "gs_composite_bwd": (
         c_int,
-        [c_void_p] * 10 + [GsView, c_void_p, c_void_p],
+        [c_void_p] * 10 + [GsView, c_void_p, c_void_p, c_void_p],
     ),
     "gs_project_bwd": (
         c_int,

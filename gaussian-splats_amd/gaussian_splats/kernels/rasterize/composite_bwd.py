@@ -3,8 +3,10 @@
 Same launcher contract as the reference's
 src/gaussian_splats/kernels/rasterize/composite_bwd.py:207-277: returns the
 per-Gaussian gradient [N, 9] with columns (u, v, inv00, inv01, inv11, r, g, b,
-opacity).  Accumulation is always atomic (one add per tile and Gaussian), so
-``atomic`` is accepted for compatibility and ignored.
+opacity), and with ``return_absolute`` also the [N, 2] sums of the absolute
+per-pixel terms of the (u, v) gradient.  Accumulation is always atomic (one
+add per tile and Gaussian), so ``atomic`` is accepted for compatibility and
+ignored.
 """
 
 from __future__ import annotations
@@ -36,11 +38,10 @@ def composite_bwd(
     *,
     out: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """``out`` (optional, zero-filled [N, 9] float32) receives the gradient."""
+    """``out`` (optional, zero-filled [N, 9] float32) receives the gradient;
+    returns ``(grad, absolute)`` when ``return_absolute``."""
     if rendering_mode != "gaussian":
         raise AssertionError("Backward gradients are only supported for Gaussian rendering.")
-    if return_absolute:
-        raise NotImplementedError("absolute mean gradients are not produced by the HIP backward")
     _check_tile(tile_size)
     device = nat.require_gpu(projected_mean, gaussian_ids, ranges, grad_image)
     projected_mean, inverse_covariance, projected_color, projected_opacity = (
@@ -60,6 +61,7 @@ def composite_bwd(
         1.0, 1.0, 0.0, 0.0, image_width, image_height, tile_size,
         opacity_threshold=opacity_threshold,
     )
+    absolute = torch.zeros((n, 2), dtype=torch.float32, device=device) if return_absolute else None
     lib = nat.library()
     order = tile_order(None, n_contributors, image_width, image_height, tile_size)
     nat.check(
@@ -69,9 +71,9 @@ def composite_bwd(
                 nat.ptr(projected_mean), nat.ptr(inverse_covariance), nat.ptr(projected_color),
                 nat.ptr(projected_opacity), nat.ptr(gaussian_ids), nat.ptr(ranges),
                 nat.ptr(grad_image), nat.ptr(final_transmittance), nat.ptr(n_contributors),
-                nat.ptr(order), view, nat.ptr(out), nat.stream(device),
+                nat.ptr(order), view, nat.ptr(out), nat.ptr(absolute), nat.stream(device),
             ),
         ),
         "composite_bwd",
     )
-    return out
+    return (out, absolute) if return_absolute else out

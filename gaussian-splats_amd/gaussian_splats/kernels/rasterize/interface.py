@@ -262,7 +262,7 @@ def _backward(ctx, *grad_outputs):
                 ptr(projected_mean), ptr(inverse_covariance), ptr(projected_color),
                 ptr(projected_opacity), ptr(gaussian_ids), ptr(ranges), ptr(grad_image),
                 ptr(final_transmittance), ptr(n_contributors), ptr(order),
-                ctx.view_composite, ptr(grad_projected), stream,
+                ctx.view_composite, ptr(grad_projected), None, stream,
             ),
         ),
         "composite_bwd",

@@ -42,7 +42,7 @@ extern "C" {
 
 #define GS_API __attribute__((visibility("default")))
 
-#define GS_ABI_VERSION 2
+#define GS_ABI_VERSION 3
 
 typedef enum gs_status {
   GS_OK = 0,
@@ -219,6 +219,9 @@ GS_API int gs_composite(
 
 /* Back-to-front compositing gradient, accumulated with atomics into
  * grad_projected[N,9] (zeroed by the caller), from the op's projected outputs.
+ * grad_absolute (optional, [N,2], zeroed by the caller) receives the sums of
+ * the absolute per-pixel terms of the mean gradient, as composite_bwd.py's
+ * return_absolute output (composite_bwd.py:180-185,194-195,272-277).
  * Replaces composite_bwd (composite_bwd.py:47-277) with the exact gradient of
  * the forward. */
 GS_API int gs_composite_bwd(
@@ -227,7 +230,7 @@ GS_API int gs_composite_bwd(
     const int32_t* gaussian_ids, const int64_t* ranges,
     const float* grad_image, const float* final_transmittance,
     const int32_t* n_contributors, const int32_t* tile_order, gs_view view,
-    float* grad_projected, void* stream);
+    float* grad_projected, float* grad_absolute, void* stream);
 
 /* Chain rule from grad_projected to the parameters.  Replaces project_bwd
  * (src/gaussian_splats/kernels/rasterize/project_bwd.py:8-381); gradients are

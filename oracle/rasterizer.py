@@ -263,8 +263,14 @@ def composite(
     rendering_mode: str = "gaussian",
     confidence: float = 0.95,
     tile_chunk: int = 64,
+    probe: list | None = None,
 ) -> Composite:
     """Dense per-(entry, pixel) compositing of each tile list (torch.py:172-225).
+
+    With ``probe`` (a list), every chunk appends ``(g, du, dv)``: zero leaves
+    of shape [entries, pixels] added to the means inside the quadratic form, so
+    that after a backward ``du.grad[e, p]`` is pixel p's term of dL/du for the
+    Gaussian of entry e (composite_bwd.py:180-185 sums their absolute values).
 
     Transmittance is exp of the float64 exclusive cumulative sum of log1p(-alpha)
     (torch.py:209-212), cast to the working dtype; ``(1 - T) < threshold`` masks
@@ -307,6 +313,12 @@ def composite(
         py = oy[:, None] + torch.as_tensor(local_y, dtype=dt)[None]
         dx = px - u[g][:, None]
         dy = py - v[g][:, None]
+        if probe is not None:
+            du = torch.zeros(dx.shape, dtype=dt, requires_grad=True)
+            dv = torch.zeros(dy.shape, dtype=dt, requires_grad=True)
+            probe.append((g, du, dv))
+            dx = dx - du
+            dy = dy - dv
         D = inv00[g][:, None] * dx * dx + 2 * inv01[g][:, None] * dx * dy + inv11[g][:, None] * dy * dy
         if rendering_mode == "ellipsoid":
             prob = (D <= cutoff).to(dt)
@@ -421,3 +433,13 @@ def rasterize(
         cam.height, tile_size, opacity_threshold, rendering_mode, confidence, tile_chunk,
     )
     return Render(comp.image, proj, bounds, counts, sorted_ids, ranges, sorted_keys, comp)
+
+
+def absolute_mean_gradients(probe: list, n: int) -> torch.Tensor:
+    """[n, 2] sums over (tile, pixel) of |dL/du| and |dL/dv| terms from a
+    ``composite(..., probe=...)`` whose output has been back-propagated."""
+    out = torch.zeros(n, 2, dtype=torch.float64)
+    for g, du, dv in probe:
+        out[:, 0].index_add_(0, g, du.grad.to(torch.float64).abs().sum(1))
+        out[:, 1].index_add_(0, g, dv.grad.to(torch.float64).abs().sum(1))
+    return out

@@ -165,7 +165,7 @@ def test_backward_rejects_ellipsoid_mode():
     lib = nat.library()
     fake = ctypes.c_void_p(16)
     status = lib.gs_composite_bwd(*([fake] * 9), None,
-                                  _view(rendering_mode="ellipsoid"), fake, None)
+                                  _view(rendering_mode="ellipsoid"), fake, None, None)
     assert status == nat.GS_ERR_UNSUPPORTED
     assert b"Gaussian rendering" in lib.gs_last_error()
 
@@ -183,7 +183,8 @@ def test_misaligned_buffers_rejected():
 def test_status_codes_map_to_python_exceptions():
     lib = nat.library()
     fake = ctypes.c_void_p(16)
-    status = lib.gs_composite_bwd(*([fake] * 9), None, _view(rendering_mode="ellipsoid"), fake, None)
+    status = lib.gs_composite_bwd(*([fake] * 9), None, _view(rendering_mode="ellipsoid"), fake, None,
+                                  None)
     with pytest.raises(NotImplementedError):
         nat.check(status, "composite_bwd")
 

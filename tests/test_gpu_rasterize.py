@@ -126,8 +126,10 @@ def test_composite_backward_matches_autograd(device, n, size, ts, min_good):
     leaves = [x.detach().double().clone().requires_grad_(True) for x in (
         proj.mean[:, 0], proj.mean[:, 1], proj.inverse[:, 0, 0], proj.inverse[:, 0, 1],
         proj.inverse[:, 1, 1], proj.color, proj.opacity[:, 0])]
-    exp = orc.composite(*leaves, sid, ranges, w, h, ts, THRESHOLD)
+    probe = []
+    exp = orc.composite(*leaves, sid, ranges, w, h, ts, THRESHOLD, probe=probe)
     (exp.image * grad_image.double()).sum().backward()
+    expected_abs = orc.absolute_mean_gradients(probe, leaves[0].shape[0])
     du, dv, da, db, dc, drgb, dop = (x.grad for x in leaves)
     expected = torch.stack((du, dv, da, db / 2, dc, drgb[:, 0], drgb[:, 1], drgb[:, 2], dop), -1)
 
@@ -137,11 +139,13 @@ def test_composite_backward_matches_autograd(device, n, size, ts, min_good):
         torch.as_tensor(sid).to(device), torch.as_tensor(ranges).to(device), w, h, ts, THRESHOLD,
         "gaussian", 0.95,
     )
-    grad = composite_bwd(
+    grad, absolute = composite_bwd(
         f32(proj.mean), f32(proj.inverse), f32(proj.color), f32(proj.opacity),
         torch.as_tensor(sid).to(device), torch.as_tensor(ranges).to(device),
         grad_image.to(device), final_t, ncon, w, h, ts, THRESHOLD, "gaussian",
-    ).cpu()
+        return_absolute=True,
+    )
+    grad, absolute = grad.cpu(), absolute.cpu()
     # Tolerance: 1e-4 relative, 1e-6 absolute in units of the column's largest
     # gradient.  Gaussians one of whose discrete decisions lies within 1e-5 of
     # its threshold are excluded: there any float32 evaluation (the reference's
@@ -151,6 +155,11 @@ def test_composite_backward_matches_autograd(device, n, size, ts, min_good):
     for col in range(9):
         scale = float(expected[:, col].abs().max())
         assert_grad_close(grad.double()[good, col], expected[good, col], scale, f"column {col}")
+    # Absolute per-pixel mean-gradient sums (return_absolute).
+    for col in range(2):
+        scale = float(expected_abs[:, col].abs().max())
+        assert_grad_close(absolute.double()[good, col], expected_abs[good, col], scale,
+                          f"absolute {col}")
 
 
 @pytest.mark.parametrize("loss", ("sum", "mean_l1"))

@@ -370,7 +370,7 @@ def test_compositing_results_do_not_depend_on_tile_order(device):
     grad2 = torch.zeros_like(grad)
     nat.check(nat.library().gs_composite_bwd(
         *(nat.ptr(t.contiguous()) for t in args), nat.ptr(sid_d), nat.ptr(ranges_d), nat.ptr(g),
-        nat.ptr(final_t), nat.ptr(ncon), None, view, nat.ptr(grad2), nat.stream(device)),
+        nat.ptr(final_t), nat.ptr(ncon), None, view, nat.ptr(grad2), None, nat.stream(device)),
         "composite_bwd")
     torch.cuda.synchronize()
     # Float atomics make both sums order-dependent: compare against the scale

@@ -196,3 +196,46 @@ def test_gradients_match_finite_differences():
             fd = (loss(plus) - loss(minus)).item() / (2 * eps)
             an = p.grad.reshape(-1)[idx].item()
             assert abs(fd - an) <= 1e-5 * max(1.0, abs(an)), (pi, idx, fd, an)
+
+
+def _probe_composite(proj, w, h, tile_size, gimg):
+    """Composite with per-pixel mean probes; back-propagates sum(image * gimg)."""
+    bounds, counts = orc.tile_counts(proj, tile_size, -(-w // tile_size), -(-h // tile_size), 0.1, 100.0)
+    tw = -(-w // tile_size)
+    keys, ids = orc.emit_intersections(bounds, proj.mean[:, 2].numpy(), counts, tw)
+    sid, ranges, _ = orc.sort_intersections(keys, ids, tw * -(-h // tile_size))
+    leaves = [x.detach().clone().requires_grad_(True) for x in (
+        proj.mean[:, 0], proj.mean[:, 1], proj.inverse[:, 0, 0], proj.inverse[:, 0, 1],
+        proj.inverse[:, 1, 1], proj.color, proj.opacity[:, 0])]
+    probe = []
+    out = orc.composite(*leaves, sid, ranges, w, h, tile_size, probe=probe)
+    (out.image * gimg).sum().backward()
+    return leaves, probe
+
+
+def test_absolute_mean_gradient_terms_sum_to_the_gradient():
+    """The probed per-pixel terms add up to autograd's mean gradient (so their
+    absolute sums are those of composite_bwd.py:180-185) and their absolute
+    sums do not depend on the tile size."""
+    params, cam = _scene(n=30, w=40, h=28)
+    proj = orc.project(*params, cam)
+    w, h = cam.width, cam.height
+    gimg = torch.randn(h, w, 3, generator=torch.Generator().manual_seed(2), dtype=torch.float64)
+    absolute = []
+    for ts in (4, 16):
+        leaves, probe = _probe_composite(proj, w, h, ts, gimg)
+        n = proj.mean.shape[0]
+        signed = torch.zeros(n, 2, dtype=torch.float64)
+        for g, du, dv in probe:
+            signed[:, 0].index_add_(0, g, du.grad.sum(1))
+            signed[:, 1].index_add_(0, g, dv.grad.sum(1))
+        torch.testing.assert_close(signed[:, 0], leaves[0].grad, rtol=1e-12, atol=1e-15)
+        torch.testing.assert_close(signed[:, 1], leaves[1].grad, rtol=1e-12, atol=1e-15)
+        a = orc.absolute_mean_gradients(probe, n)
+        assert torch.all(a[:, 0] >= signed[:, 0].abs() - 1e-15)
+        assert torch.all(a[:, 1] >= signed[:, 1].abs() - 1e-15)
+        absolute.append(a)
+    # Per-pixel terms: summed over tiles, independent of the tile size.
+    torch.testing.assert_close(absolute[0], absolute[1], rtol=1e-12, atol=1e-15)
+    assert float(absolute[0].sum()) > float(
+        torch.stack((leaves[0].grad, leaves[1].grad), 1).abs().sum()) * (1 + 1e-6)

@@ -46,6 +46,15 @@ def parse_args():
              "same step written with torch ops",
     )
     ap.add_argument(
+        "--view-loop", action="store_true",
+        help="multi-view scenes: time one rasterize call per camera as the step (the "
+             "reference's way) instead of one rasterize_views call over all cameras",
+    )
+    ap.add_argument(
+        "--no-compare", action="store_true",
+        help="multi-view scenes: time only the chosen path (for profiles)",
+    )
+    ap.add_argument(
         "--copy-calibration", action="store_true",
         help="only copy 512 MiB device to device three times (the known-size kernel that scales "
              "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)",
@@ -216,6 +225,175 @@ def cpu_baseline(scene, tile_size, sample_tiles):
     }
 
 
+def views_stage_bytes(n, k, views, total, rows, pixels, processed_fwd, processed_bwd):
+    """Algorithmic HBM bytes per stage of the multi-view step: the projection
+    reads the parameters once per launch of up to 16 cameras and writes the
+    116 B of outputs per (view, Gaussian); the backward reads the parameters
+    once, 56 B per (view, Gaussian) and writes the gradients once."""
+    launches = -(-views // 16)
+    single = stage_bytes(views * n, k, total, rows, pixels, processed_fwd, processed_bwd)
+    single["project"] = launches * n * (44 + 12 * k) + 116 * views * n
+    single["project_bwd"] = (launches + 1) * n * (44 + 12 * k) + 56 * views * n
+    return single
+
+
+def bench_views(args, scene):
+    """Multi-view scenes (config 5): a step renders every camera into a
+    [V, H, W, 3] batch with one rasterize_views call (with --view-loop: one
+    rasterize call per camera), takes the mean L1 against the per-view targets
+    and back-propagates to all parameters."""
+    from gaussian_splats.kernels.rasterize import _native, project_and_count
+    from gaussian_splats.kernels.rasterize.views import (
+        backward_views,
+        camera_tensors,
+        forward_views,
+        mosaic_columns,
+    )
+    from gaussian_splats.splats import GaussianSplat, rasterize, rasterize_views
+    from gaussian_splats.training import l1_loss, l1_loss_backward, l1_loss_forward
+
+    device = torch.device("cuda:0")
+    cams = scene.cameras
+    views = len(cams)
+    w, h = cams[0].image_size
+    tile = args.tile_size
+    splats = GaussianSplat.from_tensors(*(p.to(device) for p in scene.params()))
+    target = scene.target.to(device)
+    params = [p.detach() for p in (splats.mean, splats.rotation, splats.scale, splats.opacity,
+                                   splats.color)]
+
+    def step_batched():
+        images = rasterize_views(splats, cams, tile_size=tile, near=scene.near, far=scene.far)
+        l1_loss(images, target).backward()
+
+    def step_loop():
+        loss = 0.0
+        for v, cam in enumerate(cams):
+            image = rasterize(splats, cam, tile_size=tile, near=scene.near, far=scene.far)
+            loss = loss + l1_loss(image, target[v])
+        (loss / views).backward()
+
+    timed = {}
+    kinds = ("loop", "batched") if args.view_loop else ("batched", "loop")
+    if args.no_compare:
+        kinds = kinds[:1]
+    for kind in kinds:
+        step = step_batched if kind == "batched" else step_loop
+        for _ in range(args.warmup):
+            for p in splats.parameters():
+                p.grad = None
+            step()
+        torch.cuda.synchronize()
+        with _native.LaunchTimer("composite_bwd", capacity=args.steps * views + 1) as timer:
+            t0 = time.perf_counter()
+            for _ in range(args.steps):
+                for p in splats.parameters():
+                    p.grad = None
+                step()
+            torch.cuda.synchronize()
+            timed[kind] = (1e3 * (time.perf_counter() - t0) / args.steps, timer.mean_ms())
+        print(f"[bench] {kind}: {timed[kind][0]:.3f} ms/step", file=sys.stderr, flush=True)
+    kind = kinds[0]
+    ms_per_step, dominant_ms = timed[kind]
+
+    # Per-stage events over the batched path.
+    rot, trans, intr, _, _ = camera_tensors(cams)
+    runs = []
+    for _ in range(3):
+        events = {}
+
+        def mark(name):
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record()
+            events[name] = ev
+
+        out = forward_views(*params, rot, trans, intr, w, h, tile, 0.999, scene.near, scene.far,
+                            "gaussian", 0.95, timer=mark)
+        _, code = l1_loss_forward(out[0], target)
+        grad_image = l1_loss_backward(code, torch.ones((), device=device))
+        mark("loss")
+        backward_views(*params, rot, trans, intr, w, h, tile, 0.999, out[1:], grad_image,
+                       timer=mark)
+        torch.cuda.synchronize()
+        order = ["start", "project", "bin", "emit", "sort", "composite", "loss", "composite_bwd",
+                 "project_bwd"]
+        runs.append({b: events[a].elapsed_time(events[b]) for a, b in zip(order[:-1], order[1:])})
+    stages_ms = {k: sum(r[k] for r in runs) / len(runs) for k in runs[0]}
+
+    # Work figures: per-view processed pairs on the mosaic, row-list entries.
+    ncon, ranges, gids = out[2], out[8], out[7]
+    tw, th = -(-w // tile), -(-h // tile)
+    cols = mosaic_columns(views, tw, th)
+    rows_m = -(-views // cols)
+    grid = ranges.view(rows_m * th, cols * tw, 2)
+    fwd_pairs = bwd_pairs = rows = 0
+    for v, cam in enumerate(cams):
+        vx, vy = v % cols, v // cols
+        r = grid[vy * th:(vy + 1) * th, vx * tw:(vx + 1) * tw].reshape(-1, 2)
+        f, b = processed_pairs(r, ncon[v], tile, w, h)
+        fwd_pairs += f
+        bwd_pairs += b
+        fx, fy = cam.focal_length
+        cx, cy = cam.principal_point
+        _, _, _, _, bounds, counts = project_and_count(
+            *params, cam.rotation_matrix.float(), cam.translation.float(), fx, fy, cx, cy, w, h,
+            tile, scene.near, scene.far, "gaussian", 0.95)
+        bb = bounds.view(-1, 4).long()
+        rows += int(((bb[:, 3] - bb[:, 2]) * (counts > 0)).sum())
+    model = views_stage_bytes(scene.num_points, scene.color.shape[1], views, int(gids.numel()),
+                              rows, views * w * h, fwd_pairs, bwd_pairs)
+    stages = {}
+    for name, ms in stages_ms.items():
+        entry = {"ms": round(ms, 4)}
+        if name in model and ms > 0:
+            gbs = model[name] / (ms * 1e-3) / 1e9
+            entry.update({"algorithmic_bytes": model[name], "GB/s": round(gbs, 1),
+                          "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)})
+        stages[name] = entry
+    # composite_bwd launches: one per step batched, one per camera in the loop.
+    achieved = model["composite_bwd"] / (views if kind == "loop" else 1) / (dominant_ms * 1e-3) / 1e9
+    other = "loop" if kind == "batched" else "batched"
+    compared = {f"{other}_ms_per_step": round(timed[other][0], 4)} if other in timed else {}
+    result = {
+        "metric": "fwd+bwd Mpix/s, multi-view batch",
+        "value": round(views * w * h / 1e6 / (ms_per_step * 1e-3), 3),
+        "unit": "Mpix/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded scenes.CONFIGS distributions)",
+        "config": {
+            "workload": (f"{scene.name}: {scene.num_points} Gaussians, SH3, {views} views of "
+                         f"{w}x{h}, fwd+bwd, L1 loss"),
+            "tile_size": tile,
+            "path": "rasterize_views (one mosaic)" if kind == "batched" else "rasterize per view",
+            "intersections": int(gids.numel()),
+        },
+        **compared,
+        "stages": stages,
+        "roofline": {
+            "kernel": "composite_bwd_kernel",
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "launch_ms": round(dominant_ms, 4),
+        },
+        "cpu_baseline": None,
+    }
+    line = json.dumps(result)
+    print(line, flush=True)
+    if args.out:
+        Path(args.out).write_text(line + "\n")
+
+
 # Hyper-parameters of the reference's training step (train.py:76-87, 115).
 LAMBDA_DSSIM, OPACITY_REG, SCALE_REG = 0.2, 1e-2, 1e-2
 LRS = {"mean": 1.6e-4, "rotation": 1e-3, "scale": 5e-3, "opacity": 5e-2, "color": 2.5e-3}
@@ -349,6 +527,9 @@ def main():
     _native.library()
     device = torch.device("cuda:0")
     scene = scenes.CONFIGS[args.config]()
+    if len(scene.cameras) > 1:
+        bench_views(args, scene)
+        return
     cam = scene.cameras[0]
     w, h = cam.image_size
     splats = GaussianSplat.from_tensors(*(p.to(device) for p in scene.params()))

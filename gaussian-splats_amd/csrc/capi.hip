@@ -4,6 +4,8 @@
 #include <cstdio>
 #include <mutex>
 
+#include <algorithm>
+
 #include "common.h"
 
 namespace gs {
@@ -40,10 +42,17 @@ int check_view(const gs_view& v, bool need_tiles) {
                "tile_size must be a positive power of two, got %d", v.tile_size);
     GS_REQUIRE(v.tile_size >= 4 && v.tile_size <= 32, GS_ERR_UNSUPPORTED,
                "tile_size %d not supported (4, 8, 16 or 32)", v.tile_size);
-    const int64_t tiles = int64_t(tiles_along(v.image_width, v.tile_size)) *
-                          tiles_along(v.image_height, v.tile_size);
+    GS_REQUIRE(v.views >= 0 && v.mosaic_cols >= 0, GS_ERR_INVALID_ARGUMENT,
+               "views and mosaic_cols must be non-negative");
+    const int views = v.views > 1 ? v.views : 1;
+    const int cols = std::min(views, v.mosaic_cols > 1 ? v.mosaic_cols : 1);
+    const int64_t rows = (views + cols - 1) / cols;
+    const int64_t tiles = int64_t(tiles_along(v.image_width, v.tile_size)) * cols *
+                          tiles_along(v.image_height, v.tile_size) * rows;
     GS_REQUIRE(tiles < (int64_t(1) << 30), GS_ERR_OVERFLOW, "too many tiles (%lld)",
                (long long)tiles);
+    GS_REQUIRE(int64_t(v.image_width) * v.image_height * views < (int64_t(1) << 40),
+               GS_ERR_OVERFLOW, "too many pixels");
   }
   return GS_OK;
 }

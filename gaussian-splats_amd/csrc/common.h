@@ -80,6 +80,25 @@ inline bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
 // Validates the geometry part of a gs_view.
 int check_view(const gs_view& v, bool need_tiles);
 
+// Tile layout of a (possibly multi-view) gs_view: each view has tw x th
+// tiles; the mosaic is cols x rows views.
+struct Mosaic {
+  int views, cols, rows, tw, th;
+  int tiles_w() const { return cols * tw; }
+  int tiles_h() const { return rows * th; }
+  int num_tiles() const { return tiles_w() * tiles_h(); }
+};
+inline Mosaic mosaic_of(const gs_view& v) {
+  Mosaic m;
+  m.views = v.views > 1 ? v.views : 1;
+  m.cols = v.mosaic_cols > 1 ? v.mosaic_cols : 1;
+  if (m.cols > m.views) m.cols = m.views;
+  m.rows = (m.views + m.cols - 1) / m.cols;
+  m.tw = tiles_along(v.image_width, v.tile_size);
+  m.th = tiles_along(v.image_height, v.tile_size);
+  return m;
+}
+
 // Maps a linear workgroup index onto a work index so that consecutive work
 // items land on the same XCD.  Workgroups are dispatched round-robin over the
 // 8 XCDs (b % 8 selects the XCD); XCD x receives q + (x < r) workgroups

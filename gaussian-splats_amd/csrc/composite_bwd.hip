@@ -37,7 +37,9 @@ struct CompositeBwdArgs {
   const float* grad_image;
   const float* final_t;
   const int32_t* n_contrib;
-  int width, height, tiles_w, num_tiles;
+  int width, height;       // per view
+  int tiles_w, num_tiles;  // of the whole mosaic
+  int view_tw, view_th, cols, views;  // tiles per view, mosaic layout (one view: cols = views = 1)
   float* grad;      // [N, 9]
   float* grad_abs;  // [N, 2]: sums of |per-pixel mean gradient| (ABS kernels only)
 };
@@ -56,7 +58,9 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_bwd_kernel(Com
   constexpr int PIX = PIX_TILE / SPLIT;  // this wave's pixels per lane
   constexpr int kBandRows = 64 / TILE > 0 ? 64 / TILE : 1;  // tile rows per band of 64 pixels
   const int lane = threadIdx.x & 63;
-  const int wid = threadIdx.x >> 6;
+  // Wave index held in a scalar register, so the tile and view indices derived
+  // from it are scalar too.
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // The wave's current 64 entries, three float4 per entry (u, v, o, pa),
   // (pb, pc, r, g), (b, oa, ob, oc): written once per lane, then read as LDS
   // broadcasts per entry instead of twelve v_readlane.
@@ -67,9 +71,14 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_bwd_kernel(Com
   const int tile = a.order ? a.order[slot] : slot;
   const int band0 = (wid % SPLIT) * PIX;  // first band of this wave
 
+  // Mosaic tile -> view and the tile's pixel origin inside that view.
   const int tx = tile % a.tiles_w;
   const int ty = tile / a.tiles_w;
-  const int ox = tx * TILE, oy = ty * TILE;
+  const int vx = tx / a.view_tw, vy = ty / a.view_th;
+  const int view = vy * a.cols + vx;
+  if (view >= a.views) return;  // an empty slot of the mosaic's last row
+  const int ox = (tx - vx * a.view_tw) * TILE, oy = (ty - vy * a.view_th) * TILE;
+  const int64_t view_base = int64_t(view) * a.width * a.height;  // first pixel of the view
   const int64_t start = a.ranges[2 * tile];
 
   // The lane's pixels share one column (see column_terms).
@@ -83,7 +92,7 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_bwd_kernel(Com
     const int q = lane + 64 * (band0 + k);
     const int px = ox + (q % TILE), py = oy + (q / TILE);
     const bool valid = q < NPIX && px < a.width && py < a.height;
-    const int64_t pix = int64_t(py) * a.width + px;
+    const int64_t pix = view_base + int64_t(py) * a.width + px;
     pyf[k] = float(py);
     T[k] = valid ? a.final_t[pix] : 1.0f;
     ncon[k] = valid ? a.n_contrib[pix] : 0;
@@ -277,8 +286,13 @@ extern "C" GS_API int gs_composite_bwd(const float* projected_mean,
   a.n_contrib = n_contributors;
   a.width = view.image_width;
   a.height = view.image_height;
-  a.tiles_w = tiles_along(view.image_width, view.tile_size);
-  a.num_tiles = a.tiles_w * tiles_along(view.image_height, view.tile_size);
+  const Mosaic m = mosaic_of(view);
+  a.tiles_w = m.tiles_w();
+  a.num_tiles = m.num_tiles();
+  a.view_tw = m.tw;
+  a.view_th = m.th;
+  a.cols = m.cols;
+  a.views = m.views;
   a.grad = grad_projected;
   a.grad_abs = grad_absolute;
   hipStream_t s = as_stream(stream);

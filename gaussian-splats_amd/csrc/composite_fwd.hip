@@ -26,7 +26,9 @@ struct CompositeArgs {
   const int32_t* ids;
   const int64_t* ranges;
   const int32_t* order;  // tile dispatch order, or nullptr for the identity
-  int width, height, tile, tiles_w, num_tiles;
+  int width, height, tile;  // per view
+  int tiles_w, num_tiles;    // of the whole mosaic
+  int view_tw, view_th, cols, views;  // tiles per view, mosaic layout (one view: cols = views = 1)
   float threshold;
   // A pixel stays active while (1 - T) < threshold, i.e. T > 1 - threshold.
   float t_active;
@@ -46,7 +48,9 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_fwd_kernel(Com
   static_assert(PIX_TILE % SPLIT == 0 && kCompositeWaves % SPLIT == 0, "bands split evenly");
   constexpr int PIX = PIX_TILE / SPLIT;  // this wave's pixels per lane
   const int lane = threadIdx.x & 63;
-  const int wid = threadIdx.x >> 6;
+  // Wave index held in a scalar register, so the tile and view indices derived
+  // from it are scalar too.
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // The wave's current 64 entries, three float4 per entry (u, v, o, pa),
   // (pb, pc, r, g), (b, cut, -, -): written once per lane, then read as LDS
   // broadcasts per entry instead of ten v_readlane.
@@ -57,9 +61,14 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_fwd_kernel(Com
   const int tile = a.order ? a.order[slot] : slot;
   const int band0 = (wid % SPLIT) * PIX;  // first band of this wave
 
+  // Mosaic tile -> view and the tile's pixel origin inside that view.
   const int tx = tile % a.tiles_w;
   const int ty = tile / a.tiles_w;
-  const int ox = tx * TILE, oy = ty * TILE;
+  const int vx = tx / a.view_tw, vy = ty / a.view_th;
+  const int view = vy * a.cols + vx;
+  if (view >= a.views) return;  // an empty slot of the mosaic's last row
+  const int ox = (tx - vx * a.view_tw) * TILE, oy = (ty - vy * a.view_th) * TILE;
+  const int64_t view_base = int64_t(view) * a.width * a.height;  // first pixel of the view
   const int64_t start = a.ranges[2 * tile];
   const int64_t end = a.ranges[2 * tile + 1];
   const int list_len = int(end - start);
@@ -157,7 +166,7 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_fwd_kernel(Com
     const int q = lane + 64 * (band0 + k);
     const int px = ox + (q % TILE), py = oy + (q / TILE);
     if (q < NPIX && px < a.width && py < a.height) {
-      const int64_t pix = int64_t(py) * a.width + px;
+      const int64_t pix = view_base + int64_t(py) * a.width + px;
       a.image[pix * 3 + 0] = cr[k];
       a.image[pix * 3 + 1] = cg[k];
       a.image[pix * 3 + 2] = cb[k];
@@ -207,8 +216,13 @@ extern "C" GS_API int gs_composite(const void* records, const int32_t* gaussian_
   a.width = view.image_width;
   a.height = view.image_height;
   a.tile = view.tile_size;
-  a.tiles_w = tiles_along(view.image_width, view.tile_size);
-  a.num_tiles = a.tiles_w * tiles_along(view.image_height, view.tile_size);
+  const Mosaic m = mosaic_of(view);
+  a.tiles_w = m.tiles_w();
+  a.num_tiles = m.num_tiles();
+  a.view_tw = m.tw;
+  a.view_th = m.th;
+  a.cols = m.cols;
+  a.views = m.views;
   a.threshold = view.opacity_threshold;
   a.t_active = float(1.0 - double(view.opacity_threshold));
   a.image = image;

@@ -122,19 +122,32 @@ __global__ __launch_bounds__(kBlock) inline void clear_kernel(uint64_t* big, int
     for (int i = threadIdx.x; i < small_words; i += kBlock) small[i] = 0;
 }
 
-// Digit histograms of every pass in one read of the keys.
+// Digit histograms of every pass in one read of the keys.  The lanes of a
+// wave that share a digit are found with eight ballots and counted by one LDS
+// atomic from the lowest of them: keys that agree in a digit (the exponent
+// byte of depths in one octave, the all-ones key of culled Gaussians) would
+// otherwise serialise 64 same-address atomics per wave.
 template <typename K>
 __global__ __launch_bounds__(kBlock) void hist_kernel(const K* __restrict__ keys, int64_t n,
                                                       Plan plan, uint32_t* __restrict__ hist) {
   __shared__ uint32_t h[kMaxPasses * 256];
   for (int i = threadIdx.x; i < plan.passes * 256; i += kBlock) h[i] = 0;
   __syncthreads();
+  const int lane = __lane_id();
   const int64_t stride = int64_t(gridDim.x) * kBlock;
   for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
     const K k = keys[i];
     for (int p = 0; p < plan.passes; ++p) {
       const uint32_t d = uint32_t(k >> plan.shift[p]) & ((1u << plan.bits[p]) - 1u);
-      atomicAdd(&h[p * 256 + d], 1u);
+      // Active lanes with the same digit (digits have at most eight bits).
+      uint64_t peers = __ballot(1);
+#pragma unroll
+      for (int bit = 0; bit < 8; ++bit) {
+        const bool set = (d >> bit) & 1u;
+        const uint64_t ones = __ballot(set);
+        peers &= set ? ones : ~ones;
+      }
+      if (lane == __builtin_ctzll(peers)) atomicAdd(&h[p * 256 + d], uint32_t(__popcll(peers)));
     }
   }
   __syncthreads();

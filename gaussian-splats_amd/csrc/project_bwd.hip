@@ -9,6 +9,7 @@
 // camera.py:97 stops the gradient when |depth| < 1e-4.  Gaussians with
 // count == 0 receive zero gradients (project_bwd.py:32,324-334).
 // Replaces kernels/rasterize/project_bwd.py:8-381.
+#include <algorithm>
 #include <cmath>
 
 #include "common.h"
@@ -19,19 +20,30 @@ namespace {
 
 constexpr int kBlock = 256;
 
+// World -> camera extrinsics and the intrinsics the backward needs, by value.
+struct BwdCamera {
+  float r[9];
+  float t[3];
+  float fx, fy, lim_x, lim_y;  // lim: 1.3 x tan(half field of view), camera.py:106-116
+};
+
+constexpr int kMaxBwdViews = 16;  // views per launch of the multi-view kernel
+
 struct ProjectBwdArgs {
   const float* mean;
   const float* rotation;
   const float* scale;
   const float* opacity;
   const float* color;
-  float cam_r[9];  // world -> camera rotation, by value (kernel arguments)
-  float cam_t[3];
-  const float* inv;
-  const float* grad_in;  // [N, 9]
-  const int32_t* counts;
+  BwdCamera cam[kMaxBwdViews];
+  int views;             // cameras in cam[]; view v's inputs are at v * view_stride Gaussians
+  int64_t view_stride;   // Gaussians between consecutive views' inputs (n for one view)
+  bool accumulate;       // add to the gradient buffers instead of overwriting them
+  const float* inv;      // [views, N, 4]
+  const float* grad_in;  // [views, N, 9]
+  const int32_t* counts;  // [views, N]
   int64_t n;
-  float fx, fy, lim_x, lim_y, eps;
+  float eps;
   float* g_mean;
   float* g_rot;
   float* g_scale;
@@ -39,224 +51,265 @@ struct ProjectBwdArgs {
   float* g_color;
 };
 
+// Gradients of one view's projection of Gaussian gi, added to the
+// accumulators: the mean, the quaternion before normalisation (h, turned
+// into the raw quaternion's gradient once all views are in), the log-scales,
+// the opacity logit and the SH coefficients.
 template <int K>
+__device__ __forceinline__ void view_gradients(
+    const ProjectBwdArgs& a, const BwdCamera& cam, int64_t gi, int64_t vi, float mx, float myy,
+    float mz, const float (&R)[3][3], const float (&s3)[3], float alpha0, const float (&coef)[3 * K],
+    float& gmx, float& gmy, float& gmz, float (&h)[4], float (&gs3)[3], float& gop,
+    float (&gcoef)[3 * K], float qw, float qx, float qy, float qz) {
+  const float r00 = cam.r[0], r01 = cam.r[1], r02 = cam.r[2];
+  const float r10 = cam.r[3], r11 = cam.r[4], r12 = cam.r[5];
+  const float r20 = cam.r[6], r21 = cam.r[7], r22 = cam.r[8];
+  const float t0 = cam.t[0], t1 = cam.t[1], t2 = cam.t[2];
+  const float* gin = a.grad_in + vi * 9;
+  const float gu = gin[0], gv = gin[1], gA = gin[2], gB = gin[3], gC = gin[4];
+  const float gcol[3] = {gin[5], gin[6], gin[7]};
+  const float gal = gin[8];
+
+  // ---- SH colour ----
+  const float ex = -(r00 * t0 + r10 * t1 + r20 * t2) - mx;
+  const float ey = -(r01 * t0 + r11 * t1 + r21 * t2) - myy;
+  const float ez = -(r02 * t0 + r12 * t1 + r22 * t2) - mz;
+  const float enorm = sqrtf(ex * ex + ey * ey + ez * ez);
+  const float en = fmaxf(enorm, 1e-12f);
+  const float dx = ex / en, dy = ey / en, dz = ez / en;
+  float basis[K];
+  sh::basis<K>(dx, dy, dz, basis);
+  float gbasis[K];
+  float gc[3];
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < K; ++k) acc += basis[k] * coef[k * 3 + c];
+    // clamp_min(0) passes the gradient where acc + 0.5 >= 0.
+    gc[c] = (acc + 0.5f >= 0.0f) ? gcol[c] : 0.0f;
+  }
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    gbasis[k] = gc[0] * coef[k * 3 + 0] + gc[1] * coef[k * 3 + 1] + gc[2] * coef[k * 3 + 2];
+  }
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    gcoef[k * 3 + 0] += gc[0] * basis[k];
+    gcoef[k * 3 + 1] += gc[1] * basis[k];
+    gcoef[k * 3 + 2] += gc[2] * basis[k];
+  }
+  if (K > 1) {
+    float gdx, gdy, gdz;
+    sh::basis_vjp<K>(dx, dy, dz, gbasis, gdx, gdy, gdz);
+    // Through e / max(|e|, 1e-12); e = camera centre - mean.
+    float gex, gey, gez;
+    if (enorm > 1e-12f) {
+      const float dot = dx * gdx + dy * gdy + dz * gdz;
+      gex = (gdx - dx * dot) / enorm;
+      gey = (gdy - dy * dot) / enorm;
+      gez = (gdz - dz * dot) / enorm;
+    } else {
+      gex = gdx / 1e-12f;
+      gey = gdy / 1e-12f;
+      gez = gdz / 1e-12f;
+    }
+    gmx -= gex;
+    gmy -= gey;
+    gmz -= gez;
+  }
+
+  // ---- opacity: alpha0 = sigmoid(o) ----
+  gop += gal * alpha0 * (1.0f - alpha0);
+
+  // ---- forward recomputation ----
+  const float px = r00 * mx + r01 * myy + r02 * mz + t0;
+  const float py = r10 * mx + r11 * myy + r12 * mz + t1;
+  const float pz = r20 * mx + r21 * myy + r22 * mz + t2;
+  const float d = -pz;
+  const bool depth_free = fabsf(d) >= 1e-4f;
+  const float dc = depth_free ? d : copysignf(1e-4f, d);
+  const float rx = px / dc, ry = py / dc;
+  const bool in_x = rx >= -cam.lim_x && rx <= cam.lim_x;
+  const bool in_y = ry >= -cam.lim_y && ry <= cam.lim_y;
+  const float nx = fminf(fmaxf(rx, -cam.lim_x), cam.lim_x);
+  const float ny = fminf(fmaxf(ry, -cam.lim_y), cam.lim_y);
+  const float j00 = cam.fx / dc, j02 = cam.fx * nx / dc;
+  const float j11 = -cam.fy / dc, j12 = -cam.fy * ny / dc;
+  const float w0[3] = {j00 * r00 + j02 * r20, j00 * r01 + j02 * r21, j00 * r02 + j02 * r22};
+  const float w1[3] = {j11 * r10 + j12 * r20, j11 * r11 + j12 * r21, j11 * r12 + j12 * r22};
+  // N = W Rq (2x3), M = N diag(s).
+  float N[2][3], M[2][3];
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    N[0][c] = w0[0] * R[0][c] + w0[1] * R[1][c] + w0[2] * R[2][c];
+    N[1][c] = w1[0] * R[0][c] + w1[1] * R[1][c] + w1[2] * R[2][c];
+    M[0][c] = N[0][c] * s3[c];
+    M[1][c] = N[1][c] * s3[c];
+  }
+
+  // ---- through the 2x2 inverse: dL/dSigma = -inv G inv ----
+  const float4 inv = reinterpret_cast<const float4*>(a.inv)[vi];
+  const float i00 = inv.x, i01 = inv.y, i11 = inv.w;
+  const float t00 = i00 * gA + i01 * gB, t01 = i00 * gB + i01 * gC;
+  const float t10 = i01 * gA + i11 * gB, t11 = i01 * gB + i11 * gC;
+  const float k00 = -(t00 * i00 + t01 * i01);
+  const float k01 = -(t00 * i01 + t01 * i11);
+  const float k11 = -(t10 * i01 + t11 * i11);
+
+  // ---- Sigma = M M^T + eps I: dL/dM = 2 K M ----
+  float dN[2][3];
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    const float dm0 = 2.0f * (k00 * M[0][c] + k01 * M[1][c]);
+    const float dm1 = 2.0f * (k01 * M[0][c] + k11 * M[1][c]);
+    dN[0][c] = dm0 * s3[c];
+    dN[1][c] = dm1 * s3[c];
+    gs3[c] += (dm0 * N[0][c] + dm1 * N[1][c]) * s3[c];  // d/dlog s = d/ds * s
+  }
+  // dRq = W^T dN; dW = dN Rq^T.
+  float G[3][3];
+#pragma unroll
+  for (int r = 0; r < 3; ++r)
+#pragma unroll
+    for (int c = 0; c < 3; ++c) G[r][c] = w0[r] * dN[0][c] + w1[r] * dN[1][c];
+  float dW0[3], dW1[3];
+#pragma unroll
+  for (int kk = 0; kk < 3; ++kk) {
+    dW0[kk] = dN[0][0] * R[kk][0] + dN[0][1] * R[kk][1] + dN[0][2] * R[kk][2];
+    dW1[kk] = dN[1][0] * R[kk][0] + dN[1][1] * R[kk][1] + dN[1][2] * R[kk][2];
+  }
+
+  // ---- rotation matrix -> normalised quaternion ----
+  h[0] += 2.0f * (qz * (G[1][0] - G[0][1]) + qy * (G[0][2] - G[2][0]) + qx * (G[2][1] - G[1][2]));
+  h[1] += 2.0f * (qy * (G[0][1] + G[1][0]) + qz * (G[0][2] + G[2][0]) + qw * (G[2][1] - G[1][2])) -
+          4.0f * qx * (G[1][1] + G[2][2]);
+  h[2] += 2.0f * (qx * (G[0][1] + G[1][0]) + qw * (G[0][2] - G[2][0]) + qz * (G[1][2] + G[2][1])) -
+          4.0f * qy * (G[0][0] + G[2][2]);
+  h[3] += 2.0f * (qw * (G[1][0] - G[0][1]) + qx * (G[0][2] + G[2][0]) + qy * (G[1][2] + G[2][1])) -
+          4.0f * qz * (G[0][0] + G[1][1]);
+
+  // ---- W = J Rc: dJ entries ----
+  const float dj00 = dW0[0] * r00 + dW0[1] * r01 + dW0[2] * r02;
+  const float dj02 = dW0[0] * r20 + dW0[1] * r21 + dW0[2] * r22;
+  const float dj11 = dW1[0] * r10 + dW1[1] * r11 + dW1[2] * r12;
+  const float dj12 = dW1[0] * r20 + dW1[1] * r21 + dW1[2] * r22;
+
+  // ---- camera-space point ----
+  // u = fx x / d + cx and v = -fy y / d + cy use the unclamped depth.
+  const float d2 = d * d;
+  float gpx = gu * cam.fx / d;
+  float gpy = -gv * cam.fy / d;
+  float gd = -gu * cam.fx * px / d2 + gv * cam.fy * py / d2;
+  // Jacobian terms use the clamped depth dc.
+  const float dc2 = dc * dc, dc3 = dc2 * dc;
+  if (in_x) gpx += dj02 * cam.fx / dc2;
+  if (in_y) gpy += dj12 * (-cam.fy / dc2);
+  if (depth_free) {
+    float gdc = -dj00 * cam.fx / dc2 + dj11 * cam.fy / dc2;
+    gdc += dj02 * (-cam.fx * nx / dc2 - (in_x ? cam.fx * px / dc3 : 0.0f));
+    gdc += dj12 * (cam.fy * ny / dc2 + (in_y ? cam.fy * py / dc3 : 0.0f));
+    gd += gdc;
+  }
+  const float gpz = -gd;
+  gmx += r00 * gpx + r10 * gpy + r20 * gpz;
+  gmy += r01 * gpx + r11 * gpy + r21 * gpz;
+  gmz += r02 * gpx + r12 * gpy + r22 * gpz;
+
+}
+
+// MULTI = false: one view, no accumulation (the single-camera entry point),
+// which lets the compiler drop the view loop and keep fewer values live.
+template <int K, bool MULTI>
 __global__ __launch_bounds__(kBlock) void project_bwd_kernel(ProjectBwdArgs a) {
   constexpr int F = 3 * K;
+  const int views = MULTI ? a.views : 1;
+  const bool accumulate = MULTI && a.accumulate;
   const int64_t gi = int64_t(blockIdx.x) * kBlock + threadIdx.x;
-  // Coefficients and their gradients stay in registers (no LDS), loaded only
-  // for Gaussians that were counted.
-  float my[F];
-  if (gi < a.n) {
-    const bool counted = a.counts[gi] != 0;
-    float gmx = 0.0f, gmy = 0.0f, gmz = 0.0f;
-    float gq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    float gs3[3] = {0.0f, 0.0f, 0.0f};
-    float gop = 0.0f;
-    if (!counted) {
+  if (gi >= a.n) return;
+  float gmx = 0.0f, gmy = 0.0f, gmz = 0.0f;
+  float h[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float gs3[3] = {0.0f, 0.0f, 0.0f};
+  float gop = 0.0f;
+  float gcoef[F];
 #pragma unroll
-      for (int i = 0; i < F; ++i) my[i] = 0.0f;
-    } else {
-      sh::load_coefficients<K>(a.color + gi * F, my);
-      const float r00 = a.cam_r[0], r01 = a.cam_r[1], r02 = a.cam_r[2];
-      const float r10 = a.cam_r[3], r11 = a.cam_r[4], r12 = a.cam_r[5];
-      const float r20 = a.cam_r[6], r21 = a.cam_r[7], r22 = a.cam_r[8];
-      const float t0 = a.cam_t[0], t1 = a.cam_t[1], t2 = a.cam_t[2];
-      const float mx = a.mean[gi * 3 + 0], myy = a.mean[gi * 3 + 1], mz = a.mean[gi * 3 + 2];
-      const float* gin = a.grad_in + gi * 9;
-      const float gu = gin[0], gv = gin[1], gA = gin[2], gB = gin[3], gC = gin[4];
-      const float gcol[3] = {gin[5], gin[6], gin[7]};
-      const float gal = gin[8];
-
-      // ---- opacity: alpha0 = sigmoid(o) ----
-      const float alpha0 = 1.0f / (1.0f + expf(-a.opacity[gi]));
-      gop = gal * alpha0 * (1.0f - alpha0);
-
-      // ---- forward recomputation ----
-      const float px = r00 * mx + r01 * myy + r02 * mz + t0;
-      const float py = r10 * mx + r11 * myy + r12 * mz + t1;
-      const float pz = r20 * mx + r21 * myy + r22 * mz + t2;
-      const float d = -pz;
-      const bool depth_free = fabsf(d) >= 1e-4f;
-      const float dc = depth_free ? d : copysignf(1e-4f, d);
-      const float rx = px / dc, ry = py / dc;
-      const bool in_x = rx >= -a.lim_x && rx <= a.lim_x;
-      const bool in_y = ry >= -a.lim_y && ry <= a.lim_y;
-      const float nx = fminf(fmaxf(rx, -a.lim_x), a.lim_x);
-      const float ny = fminf(fmaxf(ry, -a.lim_y), a.lim_y);
-      const float j00 = a.fx / dc, j02 = a.fx * nx / dc;
-      const float j11 = -a.fy / dc, j12 = -a.fy * ny / dc;
-      const float w0[3] = {j00 * r00 + j02 * r20, j00 * r01 + j02 * r21, j00 * r02 + j02 * r22};
-      const float w1[3] = {j11 * r10 + j12 * r20, j11 * r11 + j12 * r21, j11 * r12 + j12 * r22};
-
-      const float4 q = reinterpret_cast<const float4*>(a.rotation)[gi];
-      const float qnorm = sqrtf(q.x * q.x + q.y * q.y + q.z * q.z + q.w * q.w);
-      const float qn = fmaxf(qnorm, 1e-12f);
-      const float qw = q.x / qn, qx = q.y / qn, qy = q.z / qn, qz = q.w / qn;
-      float R[3][3];
-      R[0][0] = 1.0f - 2.0f * (qy * qy + qz * qz);
-      R[0][1] = 2.0f * (qx * qy - qw * qz);
-      R[0][2] = 2.0f * (qx * qz + qw * qy);
-      R[1][0] = 2.0f * (qx * qy + qw * qz);
-      R[1][1] = 1.0f - 2.0f * (qx * qx + qz * qz);
-      R[1][2] = 2.0f * (qy * qz - qw * qx);
-      R[2][0] = 2.0f * (qx * qz - qw * qy);
-      R[2][1] = 2.0f * (qy * qz + qw * qx);
-      R[2][2] = 1.0f - 2.0f * (qx * qx + qy * qy);
-      const float s3[3] = {expf(a.scale[gi * 3 + 0]), expf(a.scale[gi * 3 + 1]),
-                           expf(a.scale[gi * 3 + 2])};
-      // N = W Rq (2x3), M = N diag(s).
-      float N[2][3], M[2][3];
-#pragma unroll
-      for (int c = 0; c < 3; ++c) {
-        N[0][c] = w0[0] * R[0][c] + w0[1] * R[1][c] + w0[2] * R[2][c];
-        N[1][c] = w1[0] * R[0][c] + w1[1] * R[1][c] + w1[2] * R[2][c];
-        M[0][c] = N[0][c] * s3[c];
-        M[1][c] = N[1][c] * s3[c];
-      }
-
-      // ---- through the 2x2 inverse: dL/dSigma = -inv G inv ----
-      const float4 inv = reinterpret_cast<const float4*>(a.inv)[gi];
-      const float i00 = inv.x, i01 = inv.y, i11 = inv.w;
-      const float t00 = i00 * gA + i01 * gB, t01 = i00 * gB + i01 * gC;
-      const float t10 = i01 * gA + i11 * gB, t11 = i01 * gB + i11 * gC;
-      const float k00 = -(t00 * i00 + t01 * i01);
-      const float k01 = -(t00 * i01 + t01 * i11);
-      const float k11 = -(t10 * i01 + t11 * i11);
-
-      // ---- Sigma = M M^T + eps I: dL/dM = 2 K M ----
-      float dN[2][3];
-#pragma unroll
-      for (int c = 0; c < 3; ++c) {
-        const float dm0 = 2.0f * (k00 * M[0][c] + k01 * M[1][c]);
-        const float dm1 = 2.0f * (k01 * M[0][c] + k11 * M[1][c]);
-        dN[0][c] = dm0 * s3[c];
-        dN[1][c] = dm1 * s3[c];
-        gs3[c] = (dm0 * N[0][c] + dm1 * N[1][c]) * s3[c];  // d/dlog s = d/ds * s
-      }
-      // dRq = W^T dN; dW = dN Rq^T.
-      float G[3][3];
-#pragma unroll
-      for (int r = 0; r < 3; ++r)
-#pragma unroll
-        for (int c = 0; c < 3; ++c) G[r][c] = w0[r] * dN[0][c] + w1[r] * dN[1][c];
-      float dW0[3], dW1[3];
-#pragma unroll
-      for (int kk = 0; kk < 3; ++kk) {
-        dW0[kk] = dN[0][0] * R[kk][0] + dN[0][1] * R[kk][1] + dN[0][2] * R[kk][2];
-        dW1[kk] = dN[1][0] * R[kk][0] + dN[1][1] * R[kk][1] + dN[1][2] * R[kk][2];
-      }
-
-      // ---- rotation matrix -> normalised quaternion -> raw quaternion ----
-      const float hw = 2.0f * (qz * (G[1][0] - G[0][1]) + qy * (G[0][2] - G[2][0]) +
-                               qx * (G[2][1] - G[1][2]));
-      const float hx = 2.0f * (qy * (G[0][1] + G[1][0]) + qz * (G[0][2] + G[2][0]) +
-                               qw * (G[2][1] - G[1][2])) -
-                       4.0f * qx * (G[1][1] + G[2][2]);
-      const float hy = 2.0f * (qx * (G[0][1] + G[1][0]) + qw * (G[0][2] - G[2][0]) +
-                               qz * (G[1][2] + G[2][1])) -
-                       4.0f * qy * (G[0][0] + G[2][2]);
-      const float hz = 2.0f * (qw * (G[1][0] - G[0][1]) + qx * (G[0][2] + G[2][0]) +
-                               qy * (G[1][2] + G[2][1])) -
-                       4.0f * qz * (G[0][0] + G[1][1]);
-      if (qnorm > 1e-12f) {
-        const float dot = qw * hw + qx * hx + qy * hy + qz * hz;
-        gq[0] = (hw - qw * dot) / qnorm;
-        gq[1] = (hx - qx * dot) / qnorm;
-        gq[2] = (hy - qy * dot) / qnorm;
-        gq[3] = (hz - qz * dot) / qnorm;
-      } else {
-        gq[0] = hw / 1e-12f;
-        gq[1] = hx / 1e-12f;
-        gq[2] = hy / 1e-12f;
-        gq[3] = hz / 1e-12f;
-      }
-
-      // ---- W = J Rc: dJ entries ----
-      const float dj00 = dW0[0] * r00 + dW0[1] * r01 + dW0[2] * r02;
-      const float dj02 = dW0[0] * r20 + dW0[1] * r21 + dW0[2] * r22;
-      const float dj11 = dW1[0] * r10 + dW1[1] * r11 + dW1[2] * r12;
-      const float dj12 = dW1[0] * r20 + dW1[1] * r21 + dW1[2] * r22;
-
-      // ---- camera-space point ----
-      // u = fx x / d + cx and v = -fy y / d + cy use the unclamped depth.
-      const float d2 = d * d;
-      float gpx = gu * a.fx / d;
-      float gpy = -gv * a.fy / d;
-      float gd = -gu * a.fx * px / d2 + gv * a.fy * py / d2;
-      // Jacobian terms use the clamped depth dc.
-      const float dc2 = dc * dc, dc3 = dc2 * dc;
-      if (in_x) gpx += dj02 * a.fx / dc2;
-      if (in_y) gpy += dj12 * (-a.fy / dc2);
-      if (depth_free) {
-        float gdc = -dj00 * a.fx / dc2 + dj11 * a.fy / dc2;
-        gdc += dj02 * (-a.fx * nx / dc2 - (in_x ? a.fx * px / dc3 : 0.0f));
-        gdc += dj12 * (a.fy * ny / dc2 + (in_y ? a.fy * py / dc3 : 0.0f));
-        gd += gdc;
-      }
-      const float gpz = -gd;
-      gmx = r00 * gpx + r10 * gpy + r20 * gpz;
-      gmy = r01 * gpx + r11 * gpy + r21 * gpz;
-      gmz = r02 * gpx + r12 * gpy + r22 * gpz;
-
-      // ---- SH colour ----
-      const float ex = -(r00 * t0 + r10 * t1 + r20 * t2) - mx;
-      const float ey = -(r01 * t0 + r11 * t1 + r21 * t2) - myy;
-      const float ez = -(r02 * t0 + r12 * t1 + r22 * t2) - mz;
-      const float enorm = sqrtf(ex * ex + ey * ey + ez * ez);
-      const float en = fmaxf(enorm, 1e-12f);
-      const float dx = ex / en, dy = ey / en, dz = ez / en;
-      float basis[K];
-      sh::basis<K>(dx, dy, dz, basis);
-      float gbasis[K];
-      float gc[3];
-#pragma unroll
-      for (int c = 0; c < 3; ++c) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int k = 0; k < K; ++k) acc += basis[k] * my[k * 3 + c];
-        // clamp_min(0) passes the gradient where acc + 0.5 >= 0.
-        gc[c] = (acc + 0.5f >= 0.0f) ? gcol[c] : 0.0f;
-      }
-#pragma unroll
-      for (int k = 0; k < K; ++k) {
-        gbasis[k] = gc[0] * my[k * 3 + 0] + gc[1] * my[k * 3 + 1] + gc[2] * my[k * 3 + 2];
-      }
-#pragma unroll
-      for (int k = 0; k < K; ++k) {
-        my[k * 3 + 0] = gc[0] * basis[k];
-        my[k * 3 + 1] = gc[1] * basis[k];
-        my[k * 3 + 2] = gc[2] * basis[k];
-      }
-      if (K > 1) {
-        float gdx, gdy, gdz;
-        sh::basis_vjp<K>(dx, dy, dz, gbasis, gdx, gdy, gdz);
-        // Through e / max(|e|, 1e-12); e = camera centre - mean.
-        float gex, gey, gez;
-        if (enorm > 1e-12f) {
-          const float dot = dx * gdx + dy * gdy + dz * gdz;
-          gex = (gdx - dx * dot) / enorm;
-          gey = (gdy - dy * dot) / enorm;
-          gez = (gdz - dz * dot) / enorm;
-        } else {
-          gex = gdx / 1e-12f;
-          gey = gdy / 1e-12f;
-          gez = gdz / 1e-12f;
-        }
-        gmx -= gex;
-        gmy -= gey;
-        gmz -= gez;
-      }
+  for (int i = 0; i < F; ++i) gcoef[i] = 0.0f;
+  bool any = false;
+  for (int v = 0; v < views; ++v) any |= a.counts[v * a.view_stride + gi] != 0;
+  float q[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float qnorm = 0.0f;
+  if (any) {
+    // Parameters are read once; coefficients and their gradients stay in
+    // registers, loaded only for Gaussians some view counted.
+    float coef[F];
+    sh::load_coefficients<K>(a.color + gi * F, coef);
+    const float mx = a.mean[gi * 3 + 0], myy = a.mean[gi * 3 + 1], mz = a.mean[gi * 3 + 2];
+    const float alpha0 = 1.0f / (1.0f + expf(-a.opacity[gi]));
+    const float4 qr = reinterpret_cast<const float4*>(a.rotation)[gi];
+    qnorm = sqrtf(qr.x * qr.x + qr.y * qr.y + qr.z * qr.z + qr.w * qr.w);
+    const float qn = fmaxf(qnorm, 1e-12f);
+    q[0] = qr.x / qn;
+    q[1] = qr.y / qn;
+    q[2] = qr.z / qn;
+    q[3] = qr.w / qn;
+    const float qw = q[0], qx = q[1], qy = q[2], qz = q[3];
+    float R[3][3];
+    R[0][0] = 1.0f - 2.0f * (qy * qy + qz * qz);
+    R[0][1] = 2.0f * (qx * qy - qw * qz);
+    R[0][2] = 2.0f * (qx * qz + qw * qy);
+    R[1][0] = 2.0f * (qx * qy + qw * qz);
+    R[1][1] = 1.0f - 2.0f * (qx * qx + qz * qz);
+    R[1][2] = 2.0f * (qy * qz - qw * qx);
+    R[2][0] = 2.0f * (qx * qz - qw * qy);
+    R[2][1] = 2.0f * (qy * qz + qw * qx);
+    R[2][2] = 1.0f - 2.0f * (qx * qx + qy * qy);
+    const float s3[3] = {expf(a.scale[gi * 3 + 0]), expf(a.scale[gi * 3 + 1]),
+                         expf(a.scale[gi * 3 + 2])};
+    for (int v = 0; v < views; ++v) {
+      const int64_t vi = v * a.view_stride + gi;
+      if (a.counts[vi] == 0) continue;  // zero gradient from this view (project_bwd.py:324-334)
+      view_gradients<K>(a, a.cam[v], gi, vi, mx, myy, mz, R, s3, alpha0, coef, gmx, gmy, gmz, h,
+                        gs3, gop, gcoef, qw, qx, qy, qz);
     }
-    a.g_mean[gi * 3 + 0] = gmx;
-    a.g_mean[gi * 3 + 1] = gmy;
-    a.g_mean[gi * 3 + 2] = gmz;
-    reinterpret_cast<float4*>(a.g_rot)[gi] = make_float4(gq[0], gq[1], gq[2], gq[3]);
-    a.g_scale[gi * 3 + 0] = gs3[0];
-    a.g_scale[gi * 3 + 1] = gs3[1];
-    a.g_scale[gi * 3 + 2] = gs3[2];
-    a.g_opacity[gi] = gop;
-    sh::store_coefficients<K>(a.g_color + gi * F, my);
   }
+  // ---- normalised quaternion -> raw quaternion (linear in h, so once) ----
+  float gq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (any) {
+    if (qnorm > 1e-12f) {
+      const float dot = q[0] * h[0] + q[1] * h[1] + q[2] * h[2] + q[3] * h[3];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) gq[i] = (h[i] - q[i] * dot) / qnorm;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) gq[i] = h[i] / 1e-12f;
+    }
+  }
+  if (accumulate) {
+    gmx += a.g_mean[gi * 3 + 0];
+    gmy += a.g_mean[gi * 3 + 1];
+    gmz += a.g_mean[gi * 3 + 2];
+    const float4 r = reinterpret_cast<const float4*>(a.g_rot)[gi];
+    gq[0] += r.x;
+    gq[1] += r.y;
+    gq[2] += r.z;
+    gq[3] += r.w;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) gs3[c] += a.g_scale[gi * 3 + c];
+    gop += a.g_opacity[gi];
+    float prev[F];
+    sh::load_coefficients<K>(a.g_color + gi * F, prev);
+#pragma unroll
+    for (int i = 0; i < F; ++i) gcoef[i] += prev[i];
+  }
+  a.g_mean[gi * 3 + 0] = gmx;
+  a.g_mean[gi * 3 + 1] = gmy;
+  a.g_mean[gi * 3 + 2] = gmz;
+  reinterpret_cast<float4*>(a.g_rot)[gi] = make_float4(gq[0], gq[1], gq[2], gq[3]);
+  a.g_scale[gi * 3 + 0] = gs3[0];
+  a.g_scale[gi * 3 + 1] = gs3[1];
+  a.g_scale[gi * 3 + 2] = gs3[2];
+  a.g_opacity[gi] = gop;
+  sh::store_coefficients<K>(a.g_color + gi * F, gcoef);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -265,6 +318,89 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 }  // namespace gs
 
 using namespace gs;
+
+namespace {
+
+// Chain rule for `views` cameras (host arrays as for the forward), summing
+// every view's gradient per Gaussian; launches of up to kMaxBwdViews views,
+// the later ones adding to the earlier ones' results.
+int project_bwd_views(const float* mean, const float* rotation, const float* scale,
+                      const float* opacity, const float* color, int64_t n, int32_t num_sh,
+                      const float* camera_rotations, const float* camera_translations,
+                      const float* intrinsics, int views, gs_view view,
+                      const float* inverse_covariance, const float* grad_projected,
+                      const int32_t* counts, float* grad_mean, float* grad_rotation,
+                      float* grad_scale, float* grad_opacity, float* grad_color, void* stream) {
+  GS_REQUIRE(n >= 0, GS_ERR_INVALID_ARGUMENT, "negative Gaussian count");
+  GS_REQUIRE(num_sh == 1 || num_sh == 4 || num_sh == 9 || num_sh == 16, GS_ERR_UNSUPPORTED,
+             "SH degrees above 3 are not implemented (got %d coefficients)", num_sh);
+  if (n == 0) return GS_OK;
+  GS_REQUIRE(mean && rotation && scale && opacity && color && camera_rotations &&
+                 camera_translations && inverse_covariance && grad_projected && counts &&
+                 grad_mean && grad_rotation && grad_scale && grad_opacity && grad_color,
+             GS_ERR_INVALID_ARGUMENT, "null pointer argument");
+  GS_REQUIRE(aligned16(rotation) && aligned16(color) && aligned16(inverse_covariance) &&
+                 aligned16(grad_rotation) && aligned16(grad_color),
+             GS_ERR_INVALID_ARGUMENT, "rotation/color buffers must be 16-byte aligned");
+  GS_REQUIRE(int64_t(views) * n < (int64_t(1) << 31), GS_ERR_OVERFLOW,
+             "too many Gaussians (%lld x %d views)", (long long)n, views);
+  ProjectBwdArgs a;
+  a.mean = mean;
+  a.rotation = rotation;
+  a.scale = scale;
+  a.opacity = opacity;
+  a.color = color;
+  a.view_stride = n;
+  a.n = n;
+  a.eps = view.covariance_epsilon;
+  a.g_mean = grad_mean;
+  a.g_rot = grad_rotation;
+  a.g_scale = grad_scale;
+  a.g_opacity = grad_opacity;
+  a.g_color = grad_color;
+  const dim3 grid(unsigned(ceil_div(n, kBlock)));
+  hipStream_t s = as_stream(stream);
+  for (int first = 0; first < views; first += kMaxBwdViews) {
+    a.views = std::min(kMaxBwdViews, views - first);
+    for (int j = 0; j < a.views; ++j) {
+      const int vw = first + j;
+      BwdCamera& c = a.cam[j];
+      // Host memory: the cameras travel as kernel arguments.
+      for (int i = 0; i < 9; ++i) c.r[i] = camera_rotations[vw * 9 + i];
+      for (int i = 0; i < 3; ++i) c.t[i] = camera_translations[vw * 3 + i];
+      c.fx = intrinsics ? intrinsics[vw * 4 + 0] : view.fx;
+      c.fy = intrinsics ? intrinsics[vw * 4 + 1] : view.fy;
+      GS_REQUIRE(c.fx != 0.0f && c.fy != 0.0f, GS_ERR_INVALID_ARGUMENT,
+                 "zero focal length (view %d)", vw);
+      c.lim_x = float(1.3 * (double(view.image_width) / (2.0 * double(c.fx))));
+      c.lim_y = float(1.3 * (double(view.image_height) / (2.0 * double(c.fy))));
+    }
+    const int64_t off = int64_t(first) * n;
+    a.inv = inverse_covariance + off * 4;
+    a.grad_in = grad_projected + off * 9;
+    a.counts = counts + off;
+    a.accumulate = first > 0;
+    if (views == 1) {
+      switch (num_sh) {
+        case 1: project_bwd_kernel<1, false><<<grid, kBlock, 0, s>>>(a); break;
+        case 4: project_bwd_kernel<4, false><<<grid, kBlock, 0, s>>>(a); break;
+        case 9: project_bwd_kernel<9, false><<<grid, kBlock, 0, s>>>(a); break;
+        default: project_bwd_kernel<16, false><<<grid, kBlock, 0, s>>>(a); break;
+      }
+    } else {
+      switch (num_sh) {
+        case 1: project_bwd_kernel<1, true><<<grid, kBlock, 0, s>>>(a); break;
+        case 4: project_bwd_kernel<4, true><<<grid, kBlock, 0, s>>>(a); break;
+        case 9: project_bwd_kernel<9, true><<<grid, kBlock, 0, s>>>(a); break;
+        default: project_bwd_kernel<16, true><<<grid, kBlock, 0, s>>>(a); break;
+      }
+    }
+    GS_TRY(check_launch("project_bwd"));
+  }
+  return GS_OK;
+}
+
+}  // namespace
 
 extern "C" GS_API int gs_project_bwd(const float* mean, const float* rotation, const float* scale,
                                      const float* opacity, const float* color, int64_t n,
@@ -275,48 +411,22 @@ extern "C" GS_API int gs_project_bwd(const float* mean, const float* rotation, c
                                      float* grad_mean, float* grad_rotation, float* grad_scale,
                                      float* grad_opacity, float* grad_color, void* stream) {
   clear_error();
-  GS_REQUIRE(n >= 0, GS_ERR_INVALID_ARGUMENT, "negative Gaussian count");
-  GS_REQUIRE(num_sh == 1 || num_sh == 4 || num_sh == 9 || num_sh == 16, GS_ERR_UNSUPPORTED,
-             "SH degrees above 3 are not implemented (got %d coefficients)", num_sh);
-  GS_REQUIRE(view.fx != 0.0f && view.fy != 0.0f, GS_ERR_INVALID_ARGUMENT, "zero focal length");
-  if (n == 0) return GS_OK;
-  GS_REQUIRE(mean && rotation && scale && opacity && color && camera_rotation &&
-                 camera_translation && inverse_covariance && grad_projected && counts &&
-                 grad_mean && grad_rotation && grad_scale && grad_opacity && grad_color,
-             GS_ERR_INVALID_ARGUMENT, "null pointer argument");
-  GS_REQUIRE(aligned16(rotation) && aligned16(color) && aligned16(inverse_covariance) &&
-                 aligned16(grad_rotation) && aligned16(grad_color),
-             GS_ERR_INVALID_ARGUMENT, "rotation/color buffers must be 16-byte aligned");
-  ProjectBwdArgs a;
-  a.mean = mean;
-  a.rotation = rotation;
-  a.scale = scale;
-  a.opacity = opacity;
-  a.color = color;
-  // Host memory: the extrinsics travel as kernel arguments.
-  for (int i = 0; i < 9; ++i) a.cam_r[i] = camera_rotation[i];
-  for (int i = 0; i < 3; ++i) a.cam_t[i] = camera_translation[i];
-  a.inv = inverse_covariance;
-  a.grad_in = grad_projected;
-  a.counts = counts;
-  a.n = n;
-  a.fx = view.fx;
-  a.fy = view.fy;
-  a.lim_x = float(1.3 * (double(view.image_width) / (2.0 * double(view.fx))));
-  a.lim_y = float(1.3 * (double(view.image_height) / (2.0 * double(view.fy))));
-  a.eps = view.covariance_epsilon;
-  a.g_mean = grad_mean;
-  a.g_rot = grad_rotation;
-  a.g_scale = grad_scale;
-  a.g_opacity = grad_opacity;
-  a.g_color = grad_color;
-  const dim3 grid(unsigned(ceil_div(n, kBlock)));
-  hipStream_t s = as_stream(stream);
-  switch (num_sh) {
-    case 1: project_bwd_kernel<1><<<grid, kBlock, 0, s>>>(a); break;
-    case 4: project_bwd_kernel<4><<<grid, kBlock, 0, s>>>(a); break;
-    case 9: project_bwd_kernel<9><<<grid, kBlock, 0, s>>>(a); break;
-    default: project_bwd_kernel<16><<<grid, kBlock, 0, s>>>(a); break;
-  }
-  return check_launch("project_bwd");
+  return project_bwd_views(mean, rotation, scale, opacity, color, n, num_sh, camera_rotation,
+                           camera_translation, nullptr, 1, view, inverse_covariance,
+                           grad_projected, counts, grad_mean, grad_rotation, grad_scale,
+                           grad_opacity, grad_color, stream);
+}
+
+extern "C" GS_API int gs_project_bwd_views(
+    const float* mean, const float* rotation, const float* scale, const float* opacity,
+    const float* color, int64_t n, int32_t num_sh, const float* camera_rotations,
+    const float* camera_translations, const float* intrinsics, gs_view view,
+    const float* inverse_covariance, const float* grad_projected, const int32_t* counts,
+    float* grad_mean, float* grad_rotation, float* grad_scale, float* grad_opacity,
+    float* grad_color, void* stream) {
+  clear_error();
+  return project_bwd_views(mean, rotation, scale, opacity, color, n, num_sh, camera_rotations,
+                           camera_translations, intrinsics, mosaic_of(view).views, view,
+                           inverse_covariance, grad_projected, counts, grad_mean, grad_rotation,
+                           grad_scale, grad_opacity, grad_color, stream);
 }

@@ -8,6 +8,7 @@
 //
 // This file is compiled with -ffp-contract=off: the tile rectangle is
 // floor((u -/+ r) / tile) and must round exactly as the CPU restatement does.
+#include <algorithm>
 #include <cmath>
 
 #include "common.h"
@@ -18,19 +19,29 @@ namespace {
 
 constexpr int kProjectBlock = 256;
 
+// One camera: world -> camera extrinsics and intrinsics, by value (kernel
+// arguments).
+struct FwdCamera {
+  float r[9];
+  float t[3];
+  float fx, fy, cx, cy;
+  float lim_x, lim_y;  // 1.3 * tan(half field of view), camera.py:106-116
+  int tile_x, tile_y;  // the view's tile origin in a mosaic (0, 0 for one view)
+};
+
+constexpr int kMaxViews = 16;  // cameras per launch
+
 struct ProjectArgs {
   const float* mean;
   const float* rotation;
   const float* scale;
   const float* opacity;
   const float* color;
-  float cam_r[9];  // world -> camera rotation, by value (kernel arguments)
-  float cam_t[3];
+  FwdCamera cam[kMaxViews];
+  int views;  // view v's outputs start at Gaussian v * n
   int64_t n;
-  float fx, fy, cx, cy;
-  float lim_x, lim_y;  // 1.3 * tan(half field of view), camera.py:106-116
   float tile;
-  float tiles_w, tiles_h;
+  float tiles_w, tiles_h;  // of one view
   float near_plane, far_plane, eps;
   int ellipsoid;
   float ellipsoid_extent;  // sqrt(-2 log1p(-confidence))
@@ -88,43 +99,10 @@ __global__ __launch_bounds__(kProjectBlock) void project_fwd_kernel(ProjectArgs 
   const int64_t gi = base + threadIdx.x;
   if (gi >= a.n) return;
 
-  const float r00 = a.cam_r[0], r01 = a.cam_r[1], r02 = a.cam_r[2];
-  const float r10 = a.cam_r[3], r11 = a.cam_r[4], r12 = a.cam_r[5];
-  const float r20 = a.cam_r[6], r21 = a.cam_r[7], r22 = a.cam_r[8];
-  const float t0 = a.cam_t[0], t1 = a.cam_t[1], t2 = a.cam_t[2];
-
+  // View-independent terms, computed once per Gaussian.
   const float mx = a.mean[gi * 3 + 0];
   const float my = a.mean[gi * 3 + 1];
   const float mz = a.mean[gi * 3 + 2];
-
-  // Camera-space point p = R mu + t (camera.py:94).
-  const float px = r00 * mx + r01 * my + r02 * mz + t0;
-  const float py = r10 * mx + r11 * my + r12 * mz + t1;
-  const float pz = r20 * mx + r21 * my + r22 * mz + t2;
-  // Depth along the viewing axis (-Z forward), kept at least 1e-4 from zero
-  // (camera.py:96-97).
-  const float d = -pz;
-  const float dc = fabsf(d) >= 1e-4f ? d : copysignf(1e-4f, d);
-
-  // Pixel coordinates use the unclamped depth, as the homogeneous divide of
-  // camera.py:101-102 does; the Jacobian below uses the clamped one.
-  const float u = a.fx * px / d + a.cx;
-  const float v = -a.fy * py / d + a.cy;
-
-  // Perspective Jacobian with the 1.3 x half-FOV clamp (camera.py:106-119).
-  const float nx = fminf(fmaxf(px / dc, -a.lim_x), a.lim_x);
-  const float ny = fminf(fmaxf(py / dc, -a.lim_y), a.lim_y);
-  const float j00 = a.fx / dc;
-  const float j02 = a.fx * nx / dc;
-  const float j11 = -a.fy / dc;
-  const float j12 = -a.fy * ny / dc;
-  // W = J Rc.
-  const float w00 = j00 * r00 + j02 * r20;
-  const float w01 = j00 * r01 + j02 * r21;
-  const float w02 = j00 * r02 + j02 * r22;
-  const float w10 = j11 * r10 + j12 * r20;
-  const float w11 = j11 * r11 + j12 * r21;
-  const float w12 = j11 * r12 + j12 * r22;
 
   // Normalised quaternion (w, x, y, z) -> rotation (utils.py:8-25).
   const float4 q = reinterpret_cast<const float4*>(a.rotation)[gi];
@@ -144,79 +122,119 @@ __global__ __launch_bounds__(kProjectBlock) void project_fwd_kernel(ProjectArgs 
   const float sy = expf(a.scale[gi * 3 + 1]);
   const float sz = expf(a.scale[gi * 3 + 2]);
 
-  // M = W Rq diag(s); Sigma = M M^T + eps I (camera.py:121-123).
-  const float m00 = (w00 * q00 + w01 * q10 + w02 * q20) * sx;
-  const float m01 = (w00 * q01 + w01 * q11 + w02 * q21) * sy;
-  const float m02 = (w00 * q02 + w01 * q12 + w02 * q22) * sz;
-  const float m10 = (w10 * q00 + w11 * q10 + w12 * q20) * sx;
-  const float m11 = (w10 * q01 + w11 * q11 + w12 * q21) * sy;
-  const float m12 = (w10 * q02 + w11 * q12 + w12 * q22) * sz;
-  const float c00 = m00 * m00 + m01 * m01 + m02 * m02 + a.eps;
-  const float c01 = m00 * m10 + m01 * m11 + m02 * m12;
-  const float c11 = m10 * m10 + m11 * m11 + m12 * m12 + a.eps;
-  const float det = c00 * c11 - c01 * c01;
-  const float i00 = c11 / det;
-  const float i01 = -c01 / det;
-  const float i11 = c00 / det;
-
-  // View direction from the Gaussian to the camera centre -R^T t
-  // (torch.py:198, camera.py:37-39).
-  const float ex = -(r00 * t0 + r10 * t1 + r20 * t2) - mx;
-  const float ey = -(r01 * t0 + r11 * t1 + r21 * t2) - my;
-  const float ez = -(r02 * t0 + r12 * t1 + r22 * t2) - mz;
-  const float en = fmaxf(sqrtf(ex * ex + ey * ey + ez * ez), 1e-12f);
-  float basis[K];
-  sh::basis<K>(ex / en, ey / en, ez / en, basis);
-  const float* cf = coeff + threadIdx.x * S;
-  float rgb[3];
-#pragma unroll
-  for (int c = 0; c < 3; ++c) {
-    float acc = 0.0f;
-#pragma unroll
-    for (int k = 0; k < K; ++k) acc += basis[k] * cf[k * 3 + c];
-    rgb[c] = fmaxf(acc + 0.5f, 0.0f);  // utils.py:75
-  }
-
   const float alpha0 = 1.0f / (1.0f + expf(-a.opacity[gi]));
-
-  // Rectangle of tiles touched by the extent ellipse (torch.py:233-252).
+  // Extent of the ellipse in standard deviations (torch.py:233-252) and the
+  // largest quadratic form D for which the blended alpha can reach 1/255.
   const float extent = a.ellipsoid ? a.ellipsoid_extent : 2.0f * sqrtf(logf(alpha0 * 255.0f));
-  const float rx = extent * sqrtf(c00);
-  const float ry = extent * sqrtf(c11);
-  // fmaxf/fminf map a NaN extent (alpha0 < 1/255) to the empty rectangle [0, 0).
-  const float bx0 = fminf(fmaxf(floorf((u - rx) / a.tile), 0.0f), a.tiles_w);
-  const float bx1 = fminf(fmaxf(floorf((u + rx) / a.tile) + 1.0f, 0.0f), a.tiles_w);
-  const float by0 = fminf(fmaxf(floorf((v - ry) / a.tile), 0.0f), a.tiles_h);
-  const float by1 = fminf(fmaxf(floorf((v + ry) / a.tile) + 1.0f, 0.0f), a.tiles_h);
-  const int x0 = int(bx0), x1 = int(bx1), y0 = int(by0), y1 = int(by1);
-  const bool visible = dc > a.near_plane && dc < a.far_plane;
-  const int count = visible ? (x1 - x0) * (y1 - y0) : 0;
-
-  a.pmean[gi * 3 + 0] = u;
-  a.pmean[gi * 3 + 1] = v;
-  a.pmean[gi * 3 + 2] = dc;
-  reinterpret_cast<float4*>(a.pinv)[gi] = make_float4(i00, i01, i01, i11);
-  a.pcolor[gi * 3 + 0] = rgb[0];
-  a.pcolor[gi * 3 + 1] = rgb[1];
-  a.pcolor[gi * 3 + 2] = rgb[2];
-  a.popacity[gi] = alpha0;
-  reinterpret_cast<int4*>(a.bounds)[gi] = make_int4(x0, x1, y0, y1);
-  a.counts[gi] = count;
-
-  if (a.records) {
-    // Largest quadratic form D for which the blended alpha can reach 1/255.
-    float cut;
-    if (a.ellipsoid) {
-      cut = alpha0 >= (1.0f / 255.0f) ? a.ellipsoid_cutoff : -1.0f;
-    } else {
-      cut = 2.0f * logf(alpha0 * 255.0f);
-    }
-    float4* rec = reinterpret_cast<float4*>(a.records + gi);
-    rec[0] = make_float4(u, v, alpha0, dc);
-    rec[1] = make_float4(i00, i01, i11, cut);
-    rec[2] = make_float4(rgb[0], rgb[1], rgb[2], 0.0f);
+  float cut;
+  if (a.ellipsoid) {
+    cut = alpha0 >= (1.0f / 255.0f) ? a.ellipsoid_cutoff : -1.0f;
+  } else {
+    cut = 2.0f * logf(alpha0 * 255.0f);
   }
-  if (a.depth_keys) a.depth_keys[gi] = count > 0 ? __float_as_uint(dc) : 0xFFFFFFFFu;
+  const float* cf = coeff + threadIdx.x * S;
+
+  for (int view = 0; view < a.views; ++view) {
+    const FwdCamera& cam = a.cam[view];
+    const int64_t vi = int64_t(view) * a.n + gi;  // output slot
+    const float r00 = cam.r[0], r01 = cam.r[1], r02 = cam.r[2];
+    const float r10 = cam.r[3], r11 = cam.r[4], r12 = cam.r[5];
+    const float r20 = cam.r[6], r21 = cam.r[7], r22 = cam.r[8];
+    const float t0 = cam.t[0], t1 = cam.t[1], t2 = cam.t[2];
+
+    // Camera-space point p = R mu + t (camera.py:94).
+    const float px = r00 * mx + r01 * my + r02 * mz + t0;
+    const float py = r10 * mx + r11 * my + r12 * mz + t1;
+    const float pz = r20 * mx + r21 * my + r22 * mz + t2;
+    // Depth along the viewing axis (-Z forward), kept at least 1e-4 from zero
+    // (camera.py:96-97).
+    const float d = -pz;
+    const float dc = fabsf(d) >= 1e-4f ? d : copysignf(1e-4f, d);
+
+    // Pixel coordinates use the unclamped depth, as the homogeneous divide of
+    // camera.py:101-102 does; the Jacobian below uses the clamped one.
+    const float u = cam.fx * px / d + cam.cx;
+    const float v = -cam.fy * py / d + cam.cy;
+
+    // Perspective Jacobian with the 1.3 x half-FOV clamp (camera.py:106-119).
+    const float nx = fminf(fmaxf(px / dc, -cam.lim_x), cam.lim_x);
+    const float ny = fminf(fmaxf(py / dc, -cam.lim_y), cam.lim_y);
+    const float j00 = cam.fx / dc;
+    const float j02 = cam.fx * nx / dc;
+    const float j11 = -cam.fy / dc;
+    const float j12 = -cam.fy * ny / dc;
+    // W = J Rc.
+    const float w00 = j00 * r00 + j02 * r20;
+    const float w01 = j00 * r01 + j02 * r21;
+    const float w02 = j00 * r02 + j02 * r22;
+    const float w10 = j11 * r10 + j12 * r20;
+    const float w11 = j11 * r11 + j12 * r21;
+    const float w12 = j11 * r12 + j12 * r22;
+
+    // M = W Rq diag(s); Sigma = M M^T + eps I (camera.py:121-123).
+    const float m00 = (w00 * q00 + w01 * q10 + w02 * q20) * sx;
+    const float m01 = (w00 * q01 + w01 * q11 + w02 * q21) * sy;
+    const float m02 = (w00 * q02 + w01 * q12 + w02 * q22) * sz;
+    const float m10 = (w10 * q00 + w11 * q10 + w12 * q20) * sx;
+    const float m11 = (w10 * q01 + w11 * q11 + w12 * q21) * sy;
+    const float m12 = (w10 * q02 + w11 * q12 + w12 * q22) * sz;
+    const float c00 = m00 * m00 + m01 * m01 + m02 * m02 + a.eps;
+    const float c01 = m00 * m10 + m01 * m11 + m02 * m12;
+    const float c11 = m10 * m10 + m11 * m11 + m12 * m12 + a.eps;
+    const float det = c00 * c11 - c01 * c01;
+    const float i00 = c11 / det;
+    const float i01 = -c01 / det;
+    const float i11 = c00 / det;
+
+    // View direction from the Gaussian to the camera centre -R^T t
+    // (torch.py:198, camera.py:37-39).
+    const float ex = -(r00 * t0 + r10 * t1 + r20 * t2) - mx;
+    const float ey = -(r01 * t0 + r11 * t1 + r21 * t2) - my;
+    const float ez = -(r02 * t0 + r12 * t1 + r22 * t2) - mz;
+    const float en = fmaxf(sqrtf(ex * ex + ey * ey + ez * ez), 1e-12f);
+    float basis[K];
+    sh::basis<K>(ex / en, ey / en, ez / en, basis);
+    float rgb[3];
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int k = 0; k < K; ++k) acc += basis[k] * cf[k * 3 + c];
+      rgb[c] = fmaxf(acc + 0.5f, 0.0f);  // utils.py:75
+    }
+
+    // Rectangle of tiles touched by the extent ellipse (torch.py:233-252).
+    const float rx = extent * sqrtf(c00);
+    const float ry = extent * sqrtf(c11);
+    // fmaxf/fminf map a NaN extent (alpha0 < 1/255) to the empty rectangle [0, 0).
+    const float bx0 = fminf(fmaxf(floorf((u - rx) / a.tile), 0.0f), a.tiles_w);
+    const float bx1 = fminf(fmaxf(floorf((u + rx) / a.tile) + 1.0f, 0.0f), a.tiles_w);
+    const float by0 = fminf(fmaxf(floorf((v - ry) / a.tile), 0.0f), a.tiles_h);
+    const float by1 = fminf(fmaxf(floorf((v + ry) / a.tile) + 1.0f, 0.0f), a.tiles_h);
+    const int x0 = int(bx0), x1 = int(bx1), y0 = int(by0), y1 = int(by1);
+    const bool visible = dc > a.near_plane && dc < a.far_plane;
+    const int count = visible ? (x1 - x0) * (y1 - y0) : 0;
+
+    a.pmean[vi * 3 + 0] = u;
+    a.pmean[vi * 3 + 1] = v;
+    a.pmean[vi * 3 + 2] = dc;
+    reinterpret_cast<float4*>(a.pinv)[vi] = make_float4(i00, i01, i01, i11);
+    a.pcolor[vi * 3 + 0] = rgb[0];
+    a.pcolor[vi * 3 + 1] = rgb[1];
+    a.pcolor[vi * 3 + 2] = rgb[2];
+    a.popacity[vi] = alpha0;
+    reinterpret_cast<int4*>(a.bounds)[vi] =
+        make_int4(x0 + cam.tile_x, x1 + cam.tile_x, y0 + cam.tile_y, y1 + cam.tile_y);
+    a.counts[vi] = count;
+
+    if (a.records) {
+      float4* rec = reinterpret_cast<float4*>(a.records + vi);
+      rec[0] = make_float4(u, v, alpha0, dc);
+      rec[1] = make_float4(i00, i01, i11, cut);
+      rec[2] = make_float4(rgb[0], rgb[1], rgb[2], 0.0f);
+    }
+    if (a.depth_keys) a.depth_keys[vi] = count > 0 ? __float_as_uint(dc) : 0xFFFFFFFFu;
+  }
 }
 
 __global__ __launch_bounds__(256) void pack_records_kernel(
@@ -246,27 +264,34 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 using namespace gs;
 
-extern "C" GS_API int gs_project_and_count(
-    const float* mean, const float* rotation, const float* scale, const float* opacity,
-    const float* color, int64_t n, int32_t num_sh, const float* camera_rotation,
-    const float* camera_translation, gs_view view, float* projected_mean,
-    float* inverse_covariance, float* projected_color, float* projected_opacity,
-    int32_t* bounds, int32_t* counts, void* records, uint32_t* depth_keys, void* stream) {
-  clear_error();
+namespace {
+
+// Projects for `views` cameras (host arrays: rotations [V, 9], translations
+// [V, 3], optional intrinsics [V, 4] = fx, fy, cx, cy, else the view's) in
+// launches of up to kMaxViews cameras.  With `mosaic`, bounds are shifted to
+// each view's tile origin in the mosaic of `view`.
+int project_views(const float* mean, const float* rotation, const float* scale,
+                  const float* opacity, const float* color, int64_t n, int32_t num_sh,
+                  const float* camera_rotations, const float* camera_translations,
+                  const float* intrinsics, int views, gs_view view, bool mosaic,
+                  float* projected_mean, float* inverse_covariance, float* projected_color,
+                  float* projected_opacity, int32_t* bounds, int32_t* counts, void* records,
+                  uint32_t* depth_keys, void* stream) {
   GS_REQUIRE(n >= 0, GS_ERR_INVALID_ARGUMENT, "negative Gaussian count");
   GS_TRY(check_view(view, true));
   GS_REQUIRE(num_sh == 1 || num_sh == 4 || num_sh == 9 || num_sh == 16, GS_ERR_UNSUPPORTED,
              "SH degrees above 3 are not implemented (got %d coefficients)", num_sh);
   if (n == 0) return GS_OK;
-  GS_REQUIRE(mean && rotation && scale && opacity && color && camera_rotation &&
-                 camera_translation && projected_mean && inverse_covariance &&
+  GS_REQUIRE(mean && rotation && scale && opacity && color && camera_rotations &&
+                 camera_translations && projected_mean && inverse_covariance &&
                  projected_color && projected_opacity && bounds && counts,
              GS_ERR_INVALID_ARGUMENT, "null pointer argument");
   GS_REQUIRE(aligned16(rotation) && aligned16(color) && aligned16(inverse_covariance) &&
                  aligned16(bounds) && (!records || aligned16(records)),
              GS_ERR_INVALID_ARGUMENT,
              "rotation, color, inverse_covariance, bounds and records must be 16-byte aligned");
-  GS_REQUIRE(n < (int64_t(1) << 31), GS_ERR_OVERFLOW, "too many Gaussians (%lld)", (long long)n);
+  GS_REQUIRE(int64_t(views) * n < (int64_t(1) << 31), GS_ERR_OVERFLOW,
+             "too many Gaussians (%lld x %d views)", (long long)n, views);
 
   ProjectArgs a;
   a.mean = mean;
@@ -274,17 +299,7 @@ extern "C" GS_API int gs_project_and_count(
   a.scale = scale;
   a.opacity = opacity;
   a.color = color;
-  // Host memory: the extrinsics travel as kernel arguments.
-  for (int i = 0; i < 9; ++i) a.cam_r[i] = camera_rotation[i];
-  for (int i = 0; i < 3; ++i) a.cam_t[i] = camera_translation[i];
   a.n = n;
-  a.fx = view.fx;
-  a.fy = view.fy;
-  a.cx = view.cx;
-  a.cy = view.cy;
-  // Same double-precision expression as camera.py:106-116, rounded once to fp32.
-  a.lim_x = float(1.3 * (double(view.image_width) / (2.0 * double(view.fx))));
-  a.lim_y = float(1.3 * (double(view.image_height) / (2.0 * double(view.fy))));
   a.tile = float(view.tile_size);
   a.tiles_w = float(tiles_along(view.image_width, view.tile_size));
   a.tiles_h = float(tiles_along(view.image_height, view.tile_size));
@@ -295,24 +310,75 @@ extern "C" GS_API int gs_project_and_count(
   const double cutoff = -2.0 * std::log1p(-double(view.confidence));
   a.ellipsoid_cutoff = float(cutoff);
   a.ellipsoid_extent = float(std::sqrt(cutoff));
-  a.pmean = projected_mean;
-  a.pinv = inverse_covariance;
-  a.pcolor = projected_color;
-  a.popacity = projected_opacity;
-  a.bounds = bounds;
-  a.counts = counts;
-  a.records = static_cast<GsRecord*>(records);
-  a.depth_keys = depth_keys;
-
+  const Mosaic m = mosaic_of(view);
   const dim3 grid(unsigned(ceil_div(n, kProjectBlock)));
   hipStream_t s = as_stream(stream);
-  switch (num_sh) {
-    case 1: project_fwd_kernel<1><<<grid, kProjectBlock, 0, s>>>(a); break;
-    case 4: project_fwd_kernel<4><<<grid, kProjectBlock, 0, s>>>(a); break;
-    case 9: project_fwd_kernel<9><<<grid, kProjectBlock, 0, s>>>(a); break;
-    default: project_fwd_kernel<16><<<grid, kProjectBlock, 0, s>>>(a); break;
+  for (int first = 0; first < views; first += kMaxViews) {
+    a.views = std::min(kMaxViews, views - first);
+    for (int j = 0; j < a.views; ++j) {
+      const int vw = first + j;
+      FwdCamera& c = a.cam[j];
+      // Host memory: the cameras travel as kernel arguments.
+      for (int i = 0; i < 9; ++i) c.r[i] = camera_rotations[vw * 9 + i];
+      for (int i = 0; i < 3; ++i) c.t[i] = camera_translations[vw * 3 + i];
+      const float* k = intrinsics ? intrinsics + vw * 4 : nullptr;
+      c.fx = k ? k[0] : view.fx;
+      c.fy = k ? k[1] : view.fy;
+      c.cx = k ? k[2] : view.cx;
+      c.cy = k ? k[3] : view.cy;
+      // Same double-precision expression as camera.py:106-116, rounded once to fp32.
+      c.lim_x = float(1.3 * (double(view.image_width) / (2.0 * double(c.fx))));
+      c.lim_y = float(1.3 * (double(view.image_height) / (2.0 * double(c.fy))));
+      c.tile_x = mosaic ? (vw % m.cols) * m.tw : 0;
+      c.tile_y = mosaic ? (vw / m.cols) * m.th : 0;
+    }
+    const int64_t off = int64_t(first) * n;  // first output slot of this launch
+    a.pmean = projected_mean + off * 3;
+    a.pinv = inverse_covariance + off * 4;
+    a.pcolor = projected_color + off * 3;
+    a.popacity = projected_opacity + off;
+    a.bounds = bounds + off * 4;
+    a.counts = counts + off;
+    a.records = records ? static_cast<GsRecord*>(records) + off : nullptr;
+    a.depth_keys = depth_keys ? depth_keys + off : nullptr;
+    switch (num_sh) {
+      case 1: project_fwd_kernel<1><<<grid, kProjectBlock, 0, s>>>(a); break;
+      case 4: project_fwd_kernel<4><<<grid, kProjectBlock, 0, s>>>(a); break;
+      case 9: project_fwd_kernel<9><<<grid, kProjectBlock, 0, s>>>(a); break;
+      default: project_fwd_kernel<16><<<grid, kProjectBlock, 0, s>>>(a); break;
+    }
+    GS_TRY(check_launch("project_fwd"));
   }
-  return check_launch("project_fwd");
+  return GS_OK;
+}
+
+}  // namespace
+
+extern "C" GS_API int gs_project_and_count(
+    const float* mean, const float* rotation, const float* scale, const float* opacity,
+    const float* color, int64_t n, int32_t num_sh, const float* camera_rotation,
+    const float* camera_translation, gs_view view, float* projected_mean,
+    float* inverse_covariance, float* projected_color, float* projected_opacity,
+    int32_t* bounds, int32_t* counts, void* records, uint32_t* depth_keys, void* stream) {
+  clear_error();
+  return project_views(mean, rotation, scale, opacity, color, n, num_sh, camera_rotation,
+                       camera_translation, nullptr, 1, view, false, projected_mean,
+                       inverse_covariance, projected_color, projected_opacity, bounds, counts,
+                       records, depth_keys, stream);
+}
+
+extern "C" GS_API int gs_project_views(
+    const float* mean, const float* rotation, const float* scale, const float* opacity,
+    const float* color, int64_t n, int32_t num_sh, const float* camera_rotations,
+    const float* camera_translations, const float* intrinsics, gs_view view,
+    float* projected_mean, float* inverse_covariance, float* projected_color,
+    float* projected_opacity, int32_t* bounds, int32_t* counts, void* records,
+    uint32_t* depth_keys, void* stream) {
+  clear_error();
+  return project_views(mean, rotation, scale, opacity, color, n, num_sh, camera_rotations,
+                       camera_translations, intrinsics, mosaic_of(view).views, view, true,
+                       projected_mean, inverse_covariance, projected_color, projected_opacity,
+                       bounds, counts, records, depth_keys, stream);
 }
 
 extern "C" GS_API int gs_pack_records(const float* projected_mean,

@@ -58,8 +58,8 @@ __device__ __forceinline__ uint32_t pack_rect(int x0, int w, int y0, int h) {
 // Corners of each counted Gaussian's rectangle [x0, x1) x [y0, y1) in the 2-D
 // difference array diff2 (th + 1 rows of pitch tw + 1) and ends of its rows in
 // the 1-D difference array rowdiff (th + 1); writes every Gaussian's packed
-// rectangle.
-template <bool PRIVATE>
+// rectangle.  Grids whose tables fit LDS: each workgroup accumulates them
+// there and adds them to the global ones once.
 __global__ __launch_bounds__(256) void rect_diff_kernel(const int4* __restrict__ bounds,
                                                         const int32_t* __restrict__ counts,
                                                         int64_t n, int tw, int th,
@@ -69,10 +69,9 @@ __global__ __launch_bounds__(256) void rect_diff_kernel(const int4* __restrict__
   extern __shared__ int32_t lds[];
   const int pitch = tw + 1;
   const int words = (th + 1) * pitch;
-  int32_t* t2 = PRIVATE ? lds : diff2;
-  int32_t* tr = PRIVATE ? lds + words : lds;
-  if (PRIVATE)
-    for (int i = threadIdx.x; i < words; i += 256) t2[i] = 0;
+  int32_t* t2 = lds;
+  int32_t* tr = lds + words;
+  for (int i = threadIdx.x; i < words; i += 256) t2[i] = 0;
   for (int i = threadIdx.x; i <= th; i += 256) tr[i] = 0;
   __syncthreads();
   // Eight Gaussians per thread are loaded before their atomics are issued.
@@ -108,9 +107,124 @@ __global__ __launch_bounds__(256) void rect_diff_kernel(const int4* __restrict__
     }
   }
   __syncthreads();
-  if (PRIVATE)
-    for (int i = threadIdx.x; i < words; i += 256)
-      if (t2[i]) atomicAdd(&diff2[i], t2[i]);
+  for (int i = threadIdx.x; i < words; i += 256)
+    if (t2[i]) atomicAdd(&diff2[i], t2[i]);
+  for (int i = threadIdx.x; i <= th; i += 256)
+    if (tr[i]) atomicAdd(&rowdiff[i], tr[i]);
+}
+
+// The same tables for grids whose difference array does not fit LDS.  Each
+// workgroup takes a contiguous chunk of Gaussians, finds the window of tile
+// corners its rectangles touch (first read of the chunk) and, when that window
+// fits LDS, accumulates the corners there and adds the window to diff2 once
+// (second read); otherwise its corners go to diff2 directly.  Chunks of a
+// multi-view mosaic lie in one view (or two), whose window is that view's
+// block of tiles.
+__global__ __launch_bounds__(256) void rect_diff_window_kernel(const int4* __restrict__ bounds,
+                                                               const int32_t* __restrict__ counts,
+                                                               int64_t n, int64_t chunk, int tw,
+                                                               int th, int32_t* __restrict__ diff2,
+                                                               int32_t* __restrict__ rowdiff,
+                                                               uint32_t* __restrict__ packed) {
+  extern __shared__ int32_t lds[];  // kPrivateTableWords window words, then th + 1 row words
+  __shared__ int s_box[4];           // -x0, x1, -y0, y1 of the corner window (max-reduced)
+  const int pitch = tw + 1;
+  int32_t* win = lds;
+  int32_t* tr = lds + kPrivateTableWords;
+  const int64_t c0 = int64_t(blockIdx.x) * chunk;
+  const int64_t c1 = min(n, c0 + chunk);
+  for (int i = threadIdx.x; i <= th; i += 256) tr[i] = 0;
+  if (threadIdx.x < 4) s_box[threadIdx.x] = INT_MIN;
+  __syncthreads();
+
+  // Clamped rectangle of Gaussian g, or an empty one when it has no
+  // intersections (inside the grid when it comes from the projection; clamped
+  // so that no other input indexes out of the tables).
+  auto rect = [&](int64_t g, int& x0, int& x1, int& y0, int& y1) {
+    const int4 b = bounds[g];
+    x0 = min(max(b.x, 0), tw);
+    x1 = min(max(b.y, 0), tw);
+    y0 = min(max(b.z, 0), th);
+    y1 = min(max(b.w, 0), th);
+    return counts[g] > 0 && x1 > x0 && y1 > y0;
+  };
+
+  // 1. Corner window of the chunk.
+  int mx0 = INT_MIN, mx1 = INT_MIN, my0 = INT_MIN, my1 = INT_MIN;
+  constexpr int kBatch = 4;
+  for (int64_t g0 = c0 + threadIdx.x; g0 < c1; g0 += kBatch * 256) {
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int64_t g = g0 + i * 256;
+      int x0, x1, y0, y1;
+      if (g < c1 && rect(g, x0, x1, y0, y1)) {
+        mx0 = max(mx0, -x0);
+        mx1 = max(mx1, x1);
+        my0 = max(my0, -y0);
+        my1 = max(my1, y1);
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    mx0 = max(mx0, __shfl_xor(mx0, o, 64));
+    mx1 = max(mx1, __shfl_xor(mx1, o, 64));
+    my0 = max(my0, __shfl_xor(my0, o, 64));
+    my1 = max(my1, __shfl_xor(my1, o, 64));
+  }
+  if ((threadIdx.x & 63) == 0) {
+    atomicMax(&s_box[0], mx0);
+    atomicMax(&s_box[1], mx1);
+    atomicMax(&s_box[2], my0);
+    atomicMax(&s_box[3], my1);
+  }
+  __syncthreads();
+  const bool any = s_box[1] != INT_MIN;
+  const int wx0 = any ? -s_box[0] : 0, wy0 = any ? -s_box[2] : 0;
+  const int wpitch = any ? s_box[1] - wx0 + 1 : 0;
+  const int wrows = any ? s_box[3] - wy0 + 1 : 0;
+  const bool in_lds = any && wpitch * wrows <= kPrivateTableWords;
+  if (in_lds)
+    for (int i = threadIdx.x; i < wpitch * wrows; i += 256) win[i] = 0;
+  __syncthreads();
+
+  // 2. Corners and row ends; packed rectangles.
+  for (int64_t g0 = c0 + threadIdx.x; g0 < c1; g0 += kBatch * 256) {
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int64_t g = g0 + i * 256;
+      if (g >= c1) continue;
+      int x0, x1, y0, y1;
+      const bool counted = rect(g, x0, x1, y0, y1);
+      if (counted) {
+        if (in_lds) {
+          const int a0 = (y0 - wy0) * wpitch - wx0, a1 = (y1 - wy0) * wpitch - wx0;
+          atomicAdd(&win[a0 + x0], 1);
+          atomicAdd(&win[a0 + x1], -1);
+          atomicAdd(&win[a1 + x0], -1);
+          atomicAdd(&win[a1 + x1], 1);
+        } else {
+          atomicAdd(&diff2[y0 * pitch + x0], 1);
+          atomicAdd(&diff2[y0 * pitch + x1], -1);
+          atomicAdd(&diff2[y1 * pitch + x0], -1);
+          atomicAdd(&diff2[y1 * pitch + x1], 1);
+        }
+        atomicAdd(&tr[y0], 1);
+        atomicAdd(&tr[y1], -1);
+      }
+      packed[g] = counted ? pack_rect(x0, x1 - x0, y0, y1 - y0) : kNoRect;
+    }
+  }
+  __syncthreads();
+  if (in_lds) {
+    for (int i = threadIdx.x; i < wpitch * wrows; i += 256) {
+      const int v = win[i];
+      if (v) {
+        const int r = i / wpitch;
+        atomicAdd(&diff2[(wy0 + r) * pitch + wx0 + (i - r * wpitch)], v);
+      }
+    }
+  }
   for (int i = threadIdx.x; i <= th; i += 256)
     if (tr[i]) atomicAdd(&rowdiff[i], tr[i]);
 }
@@ -773,13 +887,17 @@ GS_API int gs_bin_tiles_plan(uint32_t* depth_keys, const int32_t* bounds, const 
     int32_t* diff2 = p.table;
     int32_t* rowdiff = p.table + words;
     if (words + tiles_h + 1 <= kPrivateTableWords) {
-      rect_diff_kernel<true><<<blocks, 256, size_t(words + tiles_h + 1) * 4, fork.side>>>(
+      rect_diff_kernel<<<blocks, 256, size_t(words + tiles_h + 1) * 4, fork.side>>>(
           reinterpret_cast<const int4*>(bounds), counts, n, tiles_w, tiles_h, diff2, rowdiff,
           p.packed);
     } else {
-      rect_diff_kernel<false><<<blocks, 256, size_t(tiles_h + 1) * 4, fork.side>>>(
-          reinterpret_cast<const int4*>(bounds), counts, n, tiles_w, tiles_h, diff2, rowdiff,
-          p.packed);
+      // Contiguous chunks with private corner windows (see the kernel).
+      const int64_t wblocks = std::min<int64_t>(512, std::max<int64_t>(1, ceil_div(n, 16384)));
+      const int64_t chunk = ceil_div(n, wblocks);
+      rect_diff_window_kernel<<<unsigned(ceil_div(n, chunk)), 256,
+                                size_t(kPrivateTableWords + tiles_h + 1) * 4, fork.side>>>(
+          reinterpret_cast<const int4*>(bounds), counts, n, chunk, tiles_w, tiles_h, diff2,
+          rowdiff, p.packed);
     }
   }
   // The row-list scan on the caller's stream reads the packed rectangles.

@@ -27,18 +27,24 @@ constexpr int kOrderMax = 8192;  // tiles per region ordered by one workgroup
 __global__ __launch_bounds__(256) void tile_key_kernel(const int64_t* __restrict__ ranges,
                                                        const int32_t* __restrict__ ncon,
                                                        int tiles_w, int num_tiles, int tile,
-                                                       int width, int height,
+                                                       int width, int height, int view_tw,
+                                                       int view_th, int cols, int views,
                                                        uint32_t* __restrict__ key) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= num_tiles) return;
   int64_t work;
   if (ncon) {
-    const int ox = (t % tiles_w) * tile, oy = (t / tiles_w) * tile;
+    // Mosaic tile -> view and pixel origin inside it (see gs_view).
+    const int tx = t % tiles_w, ty = t / tiles_w;
+    const int vx = tx / view_tw, vy = ty / view_th;
+    const int view = vy * cols + vx;
+    const int ox = (tx - vx * view_tw) * tile, oy = (ty - vy * view_th) * tile;
+    const int32_t* vn = ncon + int64_t(view < views ? view : 0) * width * height;
     int m = 0;
-    for (int q = lane; q < tile * tile; q += 64) {
+    for (int q = lane; view < views && q < tile * tile; q += 64) {
       const int px = ox + q % tile, py = oy + q / tile;
-      if (px < width && py < height) m = max(m, ncon[int64_t(py) * width + px]);
+      if (px < width && py < height) m = max(m, vn[int64_t(py) * width + px]);
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) m = max(m, __shfl_xor(m, o, 64));
@@ -166,8 +172,9 @@ GS_API int gs_tile_order(const int64_t* ranges, const int32_t* n_contributors, g
                          void* stream) {
   clear_error();
   GS_TRY(check_view(view, true));
-  const int tiles_w = tiles_along(view.image_width, view.tile_size);
-  const int num_tiles = tiles_w * tiles_along(view.image_height, view.tile_size);
+  const Mosaic m = mosaic_of(view);
+  const int tiles_w = m.tiles_w();
+  const int num_tiles = m.num_tiles();
   GS_REQUIRE(order && (ranges || n_contributors), GS_ERR_INVALID_ARGUMENT,
              "null pointer argument");
   GS_REQUIRE(workspace && workspace_bytes >= gs_tile_order_workspace_bytes(num_tiles),
@@ -177,7 +184,7 @@ GS_API int gs_tile_order(const int64_t* ranges, const int32_t* n_contributors, g
   uint32_t* key = static_cast<uint32_t*>(workspace);
   tile_key_kernel<<<unsigned(ceil_div(num_tiles, 4)), 256, 0, s>>>(
       ranges, n_contributors, tiles_w, num_tiles, view.tile_size, view.image_width,
-      view.image_height, key);
+      view.image_height, m.tw, m.th, m.cols, m.views, key);
   GS_TRY(check_launch("tile_order keys"));
   tile_sort_kernel<<<8, kOrderThreads, 0, s>>>(key, num_tiles, order);
   return check_launch("tile_order sort");

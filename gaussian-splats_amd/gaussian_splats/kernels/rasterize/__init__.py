@@ -13,6 +13,7 @@ from .intersections import (
 )
 from .project import pack_records, project_and_count
 from .project_bwd import project_bwd
+from .views import rasterize_views
 
 __all__ = [
     "bin_gaussians",
@@ -25,6 +26,7 @@ __all__ = [
     "project_and_count",
     "project_bwd",
     "rasterize",
+    "rasterize_views",
     "sort_intersections",
     "sort_tiles",
 ]

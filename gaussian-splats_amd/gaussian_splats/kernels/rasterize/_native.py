@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parents[2] / "_lib" / "libgs_raster.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 GS_OK = 0
 GS_ERR_INVALID_ARGUMENT = 1
@@ -57,6 +57,8 @@ class GsView(ctypes.Structure):
         ("confidence", c_float),
         ("opacity_threshold", c_float),
         ("covariance_epsilon", c_float),
+        ("views", c_int32),
+        ("mosaic_cols", c_int32),
     ]
 
 
@@ -74,13 +76,15 @@ def make_view(
     confidence: float = 0.95,
     opacity_threshold: float = 0.999,
     covariance_epsilon: float = 0.03,
+    views: int = 1,
+    mosaic_cols: int = 1,
 ) -> GsView:
     if rendering_mode not in MODES:
         raise ValueError(f"Invalid rendering mode: {rendering_mode}")
     return GsView(
         float(fx), float(fy), float(cx), float(cy), int(image_width), int(image_height),
         int(tile_size), float(near), float(far), MODES[rendering_mode], float(confidence),
-        float(opacity_threshold), float(covariance_epsilon),
+        float(opacity_threshold), float(covariance_epsilon), int(views), int(mosaic_cols),
     )
 
 
@@ -90,6 +94,10 @@ _SIGNATURES = {
     "gs_project_and_count": (
         c_int,
         [c_void_p] * 5 + [c_int64, c_int32, c_void_p, c_void_p, GsView] + [c_void_p] * 9,
+    ),
+    "gs_project_views": (
+        c_int,
+        [c_void_p] * 5 + [c_int64, c_int32, c_void_p, c_void_p, c_void_p, GsView] + [c_void_p] * 9,
     ),
     "gs_pack_records": (c_int, [c_void_p] * 4 + [c_int64, GsView, c_void_p, c_void_p]),
     "gs_scan_workspace_bytes": (c_size_t, [c_int64]),
@@ -141,6 +149,10 @@ _SIGNATURES = {
     "gs_project_bwd": (
         c_int,
         [c_void_p] * 5 + [c_int64, c_int32, c_void_p, c_void_p, GsView] + [c_void_p] * 9,
+    ),
+    "gs_project_bwd_views": (
+        c_int,
+        [c_void_p] * 5 + [c_int64, c_int32, c_void_p, c_void_p, c_void_p, GsView] + [c_void_p] * 9,
     ),
     "gs_l1_loss_workspace_bytes": (c_size_t, [c_int64]),
     "gs_l1_loss_fwd": (

@@ -133,11 +133,14 @@ def config4(seed: int = 0, n: int = 4_000_000, distance: float = 3.0, focal: flo
                  target=target, notes={"distance": distance, "focal": focal})
 
 
-def config5(seed: int = 0, n: int = 500_000, views: int = 16) -> Scene:
+def config5(
+    seed: int = 0, n: int = 500_000, views: int = 16, size: int = 800, focal: float = 1000.0
+) -> Scene:
     """Baked-mesh-style flat splats: 500k on the unit sphere, two log-scales
     N(-4, 0.3) and a third of -9.2, the thin axis turned to a random normal,
     opacity logits N(0, 1.5), SH3 as config 2; 16 cameras on a radius-3 ring in
-    the XZ plane looking at the origin, 800x800, fx = fy = 1000."""
+    the XZ plane looking at the origin, 800x800, fx = fy = 1000 (``size`` and
+    ``focal`` shrink the images for parity tests)."""
     g = torch.Generator().manual_seed(seed)
     mean = torch.randn(n, 3, generator=g)
     mean = mean / mean.norm(dim=-1, keepdim=True).clamp_min(1e-12)
@@ -158,11 +161,11 @@ def config5(seed: int = 0, n: int = 500_000, views: int = 16) -> Scene:
         angle = 2 * math.pi * k / views
         cams.append(
             PinholeCamera.look_at(
-                (3 * math.sin(angle), 0.0, 3 * math.cos(angle)), image_size=(800, 800),
-                focal_length=(1000.0, 1000.0), principal_point=(400.0, 400.0),
+                (3 * math.sin(angle), 0.0, 3 * math.cos(angle)), image_size=(size, size),
+                focal_length=(focal, focal), principal_point=(size / 2, size / 2),
             )
         )
-    target = torch.rand(views, 800, 800, 3, generator=g)
+    target = torch.rand(views, size, size, 3, generator=g)
     return Scene("config5", mean, rotation, scale, opacity, color, cams, backward=True, target=target)
 
 

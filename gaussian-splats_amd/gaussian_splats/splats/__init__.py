@@ -1,5 +1,5 @@
 from .camera import Camera, PinholeCamera
-from .rasterize import rasterize
+from .rasterize import rasterize, rasterize_views
 from .splats import GaussianSplat, ProjectedGaussianSplat
 from .utils import SH_C0, quaternion_to_rotation_matrix, rgb_to_sh
 
@@ -11,5 +11,6 @@ __all__ = [
     "ProjectedGaussianSplat",
     "quaternion_to_rotation_matrix",
     "rasterize",
+    "rasterize_views",
     "rgb_to_sh",
 ]

@@ -12,6 +12,7 @@ from typing import Literal
 import torch
 
 from ..kernels.rasterize.interface import rasterize as hip_rasterize
+from ..kernels.rasterize.views import rasterize_views
 from .camera import Camera
 from .splats import GaussianSplat
 
@@ -46,4 +47,4 @@ def rasterize(
     )
 
 
-__all__ = ["rasterize"]
+__all__ = ["rasterize", "rasterize_views"]

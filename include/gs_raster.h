@@ -42,7 +42,7 @@ extern "C" {
 
 #define GS_API __attribute__((visibility("default")))
 
-#define GS_ABI_VERSION 3
+#define GS_ABI_VERSION 4
 
 typedef enum gs_status {
   GS_OK = 0,
@@ -70,6 +70,14 @@ typedef struct gs_view {
   float confidence;            /* ellipsoid mode only */
   float opacity_threshold;     /* compositing stops once 1 - T >= this */
   float covariance_epsilon;    /* 0.03 in the reference (camera.py:86) */
+  /* Several views of one size composited in one launch (no counterpart in
+   * the reference): their tile grids are laid side by side, mosaic_cols per
+   * row, and tile t of the mosaic belongs to view (ty / tiles_h) *
+   * mosaic_cols + tx / tiles_w.  Per-view buffers (image, transmittance,
+   * contributors, image gradient) are [views, H, W, ...]; ranges cover the
+   * mosaic's tiles.  0 or 1 in both fields: a single view. */
+  int32_t views;
+  int32_t mosaic_cols;
 } gs_view;
 
 /* ABI version of the loaded library (GS_ABI_VERSION). No counterpart in the
@@ -90,6 +98,25 @@ GS_API int gs_project_and_count(
     const float* opacity, const float* color, int64_t n, int32_t num_sh,
     const float* camera_rotation, const float* camera_translation,
     gs_view view,
+    float* projected_mean, float* inverse_covariance, float* projected_color,
+    float* projected_opacity, int32_t* bounds, int32_t* counts,
+    void* records, uint32_t* depth_keys, void* stream);
+
+/* Multi-view projection (no counterpart in the reference, which renders one
+ * camera per call): gs_project_and_count for the V = max(view.views, 1)
+ * cameras of a mosaic sharing the image size, tile size and culling planes of
+ * `view`, each Gaussian's parameters read once per launch of up to 16
+ * cameras.  Host arrays: camera_rotations [V, 9], camera_translations [V, 3],
+ * intrinsics [V, 4] = (fx, fy, cx, cy) per camera, or NULL for view's.
+ * Outputs are [V, N, ...] (view v's at Gaussian v * N).  bounds are in the
+ * mosaic's tile grid (each view's rectangle shifted to its tile origin,
+ * see gs_view.views), so binning V * N Gaussians over the mosaic's tiles
+ * lists every view's tiles in one pass. */
+GS_API int gs_project_views(
+    const float* mean, const float* rotation, const float* scale,
+    const float* opacity, const float* color, int64_t n, int32_t num_sh,
+    const float* camera_rotations, const float* camera_translations,
+    const float* intrinsics, gs_view view,
     float* projected_mean, float* inverse_covariance, float* projected_color,
     float* projected_opacity, int32_t* bounds, int32_t* counts,
     void* records, uint32_t* depth_keys, void* stream);
@@ -240,6 +267,20 @@ GS_API int gs_project_bwd(
     const float* opacity, const float* color, int64_t n, int32_t num_sh,
     const float* camera_rotation, const float* camera_translation,
     gs_view view, const float* inverse_covariance,
+    const float* grad_projected, const int32_t* counts,
+    float* grad_mean, float* grad_rotation, float* grad_scale,
+    float* grad_opacity, float* grad_color, void* stream);
+
+/* Multi-view projection backward (no counterpart in the reference): the
+ * gradients gs_project_bwd gives for each of the V = max(view.views, 1)
+ * cameras of gs_project_views, summed per Gaussian in registers and written
+ * once (per 16 cameras).  inverse_covariance, grad_projected and counts are
+ * [V, N, ...]; the camera arrays are those of gs_project_views. */
+GS_API int gs_project_bwd_views(
+    const float* mean, const float* rotation, const float* scale,
+    const float* opacity, const float* color, int64_t n, int32_t num_sh,
+    const float* camera_rotations, const float* camera_translations,
+    const float* intrinsics, gs_view view, const float* inverse_covariance,
     const float* grad_projected, const int32_t* counts,
     float* grad_mean, float* grad_rotation, float* grad_scale,
     float* grad_opacity, float* grad_color, void* stream);

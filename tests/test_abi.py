@@ -232,3 +232,56 @@ def test_fake_implementation_shapes():
     assert shapes[0] == (90, 120, 3) and shapes[1] == (90, 120) and shapes[2] == (90, 120)
     assert shapes[3] == (7, 3) and shapes[4] == (7, 2, 2) and shapes[8] == (8 * 6, 2)
     assert out[8].dtype == torch.int64 and out[7].dtype == torch.int32
+
+
+def test_multi_view_host_checks():
+    lib = nat.library()
+    fake = ctypes.c_void_p(16)
+    # Negative view counts and mosaic columns are rejected before any launch.
+    for kw in (dict(views=-1), dict(mosaic_cols=-2)):
+        status = lib.gs_project_views(
+            fake, fake, fake, fake, fake, 10, 16, fake, fake, None, _view(**kw), *([fake] * 6),
+            None, None, None,
+        )
+        assert status == nat.GS_ERR_INVALID_ARGUMENT
+        status = lib.gs_composite(fake, fake, fake, None, _view(**kw), fake, fake, fake, None)
+        assert status == nat.GS_ERR_INVALID_ARGUMENT
+    # Virtual Gaussian indices (view * N + i) must fit int32.
+    status = lib.gs_project_views(
+        fake, fake, fake, fake, fake, 1 << 28, 16, fake, fake, None, _view(views=16, mosaic_cols=4),
+        *([fake] * 6), None, None, None,
+    )
+    assert status == nat.GS_ERR_OVERFLOW
+    status = lib.gs_project_bwd_views(
+        fake, fake, fake, fake, fake, 1 << 28, 16, fake, fake, None, _view(views=16),
+        *([fake] * 8), None,
+    )
+    assert status == nat.GS_ERR_OVERFLOW
+    # A mosaic whose tile grid overflows is rejected.
+    status = lib.gs_composite(
+        fake, fake, fake, None, _view(image_width=1 << 16, image_height=1 << 16, tile_size=4,
+                                      views=64, mosaic_cols=8), fake, fake, fake, None,
+    )
+    assert status == nat.GS_ERR_OVERFLOW
+    # Zero Gaussians: nothing to do.
+    assert lib.gs_project_views(None, None, None, None, None, 0, 16, None, None, None,
+                                _view(views=3), *([None] * 8), None) == nat.GS_OK
+
+
+def test_multi_view_fake_implementation_shapes():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    from torch.fx.experimental.symbolic_shapes import ShapeEnv
+
+    import gaussian_splats.kernels.rasterize.views  # noqa: F401 (registers the op)
+
+    with FakeTensorMode(shape_env=ShapeEnv(allow_dynamic_output_shape_ops=True)):
+        n, k, v = 7, 16, 5
+        args = [torch.empty(n, 3), torch.empty(n, 4), torch.empty(n, 3), torch.empty(n, 1),
+                torch.empty(n, k, 3), torch.empty(v, 3, 3), torch.empty(v, 3), torch.empty(v, 4)]
+        out = torch.ops.gaussian_splats.rasterize_views(*args, 120, 90, 16, 0.999, 0.2, 100.0,
+                                                        "gaussian", 0.95)
+    shapes = [tuple(o.shape) for o in out]
+    assert shapes[0] == (v, 90, 120, 3) and shapes[1] == (v, 90, 120) and shapes[2] == (v, 90, 120)
+    assert shapes[3] == (v, n, 3) and shapes[4] == (v, n, 2, 2) and shapes[9] == (v, n)
+    # 8 x 6 tiles per view; five views in a 3 x 2 mosaic.
+    assert shapes[8] == (3 * 8 * 2 * 6, 2)

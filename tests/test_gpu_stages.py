@@ -196,6 +196,37 @@ def test_bucketed_binning_long_rows(device):
     assert np.array_equal(sid.cpu().numpy(), sid_o)
 
 
+def test_bucketed_binning_mosaic_windows(device):
+    """A 200 x 200 grid (tables larger than LDS) whose Gaussians come in four
+    groups confined to 100 x 100 blocks, as a multi-view mosaic's are: chunks
+    inside one block accumulate their corners in an LDS window, chunks that
+    straddle two blocks fall back to global atomics; both must give the
+    oracle's lists."""
+    g = torch.Generator().manual_seed(5)
+    per, tiles_w, tiles_h = 20_000, 200, 200
+    rects, depth_list = [], []
+    for v in range(4):
+        ox, oy = (v % 2) * 100, (v // 2) * 100
+        x0 = torch.randint(0, 97, (per,), generator=g) + ox
+        y0 = torch.randint(0, 97, (per,), generator=g) + oy
+        x1 = x0 + torch.randint(1, 4, (per,), generator=g)
+        y1 = y0 + torch.randint(1, 4, (per,), generator=g)
+        rects.append(torch.stack((torch.stack((x0, x1), -1), torch.stack((y0, y1), -1)), 1))
+        depth_list.append(torch.rand(per, generator=g) * 2 + 2.0)  # one exponent: shared digits
+    bounds = torch.cat(rects).int()
+    depths = torch.cat(depth_list)
+    counts = ((bounds[:, 0, 1] - bounds[:, 0, 0]) * (bounds[:, 1, 1] - bounds[:, 1, 0])).int()
+    counts[torch.rand(4 * per, generator=g) < 0.3] = 0  # culled
+    keys_o, ids_o = orc.emit_intersections(bounds.numpy(), depths.numpy(), counts.numpy(), tiles_w)
+    sid_o, ranges_o, _ = orc.sort_intersections(keys_o, ids_o, tiles_w * tiles_h)
+    print(f"mosaic windows intersections={len(sid_o)}", flush=True)
+    sid, ranges = bin_tiles(
+        _depth_keys(depths, counts).to(device), bounds.to(device), counts.to(device), tiles_w, tiles_h
+    )
+    assert np.array_equal(ranges.cpu().numpy(), ranges_o)
+    assert np.array_equal(sid.cpu().numpy(), sid_o)
+
+
 def test_bucketed_binning_empty_and_deterministic(device):
     bounds = torch.zeros(5, 2, 2, dtype=torch.int32, device=device)
     counts = torch.zeros(5, dtype=torch.int32, device=device)

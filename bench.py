@@ -27,6 +27,7 @@ for p in (ROOT, ROOT / "gaussian-splats_amd"):
 import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+VALU_CLOCK_HZ = 2.4e9  # MI355X peak engine clock
 
 
 def parse_args():
@@ -584,9 +585,18 @@ def main():
     dominant_ms = timer.mean_ms()
     achieved = bytes_model["composite_bwd"] / (dominant_ms * 1e-3) / 1e9
     traffic = None
+    valu = None
     traffic_file = ROOT / "profiles" / "traffic_composite_bwd_config3.json"
     if traffic_file.exists() and args.config == "config3" and args.tile_size == 16:
-        traffic = json.loads(traffic_file.read_text())["hbm_bytes_per_launch"]
+        measured = json.loads(traffic_file.read_text())
+        traffic = measured["hbm_bytes_per_launch"]
+        if "valu_instructions_per_launch" in measured:
+            # The kernel's real bound: wave64 fp32 VALU instructions issue in 4
+            # cycles on one of the 1024 SIMDs (256 CUs x 4) at 2.4 GHz.
+            insts = measured["valu_instructions_per_launch"]
+            issue_ms = insts * 4 / (1024 * VALU_CLOCK_HZ) * 1e3
+            valu = {"instructions": insts, "issue_ms": round(issue_ms, 4),
+                    "frac": round(issue_ms / dominant_ms, 4)}
     roofline = {
         "kernel": "composite_bwd_kernel<16>" if args.tile_size == 16 else "composite_bwd_kernel",
         "bound": "hbm",
@@ -597,6 +607,7 @@ def main():
         "traffic": traffic,
         "launch_ms": round(dominant_ms, 4),
         "algorithmic_bytes": bytes_model["composite_bwd"],
+        "valu_issue": valu,
     }
 
     cpu = None

@@ -56,6 +56,11 @@ def parse_args():
         help="multi-view scenes: time only the chosen path (for profiles)",
     )
     ap.add_argument(
+        "--ply-io", action="store_true",
+        help="time scene-file I/O instead: save_ply / load_ply of the config's Gaussians "
+             "(GPU record pack/split against the host path)",
+    )
+    ap.add_argument(
         "--copy-calibration", action="store_true",
         help="only copy 512 MiB device to device three times (the known-size kernel that scales "
              "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)",
@@ -507,6 +512,74 @@ def bench_train_step(args):
         Path(args.out).write_text(line + "\n")
 
 
+def bench_ply_io(args):
+    """Scene-file I/O of the config's Gaussians (config 3: 1M SH3, a 248 MB
+    file in the page cache): save_ply of GPU tensors (records packed on the
+    GPU, one download) and load_ply(device=...) (one upload, records split on
+    the GPU), each beside the host path (numpy records, per-tensor copies)."""
+    import tempfile
+
+    from gaussian_splats import scenes
+    from gaussian_splats.kernels.rasterize import _native
+    from gaussian_splats.splats.ply import load_ply, save_ply
+
+    _native.library()
+    device = torch.device("cuda:0")
+    scene = scenes.CONFIGS[args.config]()
+    names = ("mean", "rotation", "scale", "opacity", "color")
+    host_state = dict(zip(names, (p.contiguous() for p in scene.params())))
+    dev_state = {k: v.to(device) for k, v in host_state.items()}
+    n, k = scene.num_points, scene.color.shape[1]
+    record_bytes = 4 * (14 + 3 * k)
+    reps = max(1, args.steps)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        return 1e3 * (time.perf_counter() - t0) / reps
+
+    with tempfile.TemporaryDirectory() as tmp:
+        path = Path(tmp) / "scene.ply"
+        save_host = timed(lambda: save_ply(host_state, path))
+        with _native.LaunchTimer("ply_pack", capacity=reps + 2) as pack_timer:
+            save_dev = timed(lambda: save_ply(dev_state, path))
+        file_bytes = path.stat().st_size
+
+        def load_host():
+            return {key: v.to(device) for key, v in load_ply(path).items()}
+
+        load_host_ms = timed(load_host)
+        with _native.LaunchTimer("ply_unpack", capacity=reps + 2) as unpack_timer:
+            load_dev_ms = timed(lambda: load_ply(path, device=device))
+        loaded = load_ply(path, device=device)
+        for key in names:
+            assert torch.equal(loaded[key], dev_state[key]), key
+    unpack_ms, pack_ms = unpack_timer.mean_ms(), pack_timer.mean_ms()
+    kernel_bytes = 2 * n * record_bytes  # records in, parameters out (or the reverse)
+    line = {
+        "metric": "scene file I/O GB/s (PLY, page cache)", "unit": "GB/s", "n_gpus": 1,
+        "config": {"workload": f"{scene.name}: {n} Gaussians, SH {k} coefficients, "
+                               f"{file_bytes / 1e6:.0f} MB file"},
+        "load_to_hbm": {"gpu_split_ms": round(load_dev_ms, 2), "host_path_ms": round(load_host_ms, 2),
+                        "GB/s": round(file_bytes / load_dev_ms / 1e6, 2)},
+        "save_from_hbm": {"gpu_pack_ms": round(save_dev, 2), "host_path_ms": round(save_host, 2),
+                          "GB/s": round(file_bytes / save_dev / 1e6, 2)},
+        "kernels": {
+            "ply_unpack": {"ms": round(unpack_ms, 4),
+                           "GB/s": round(kernel_bytes / unpack_ms / 1e6, 1),
+                           "frac_hbm": round(kernel_bytes / unpack_ms / 1e6 / HBM_PEAK_GBS, 4)},
+            "ply_pack": {"ms": round(pack_ms, 4),
+                         "GB/s": round(kernel_bytes / pack_ms / 1e6, 1),
+                         "frac_hbm": round(kernel_bytes / pack_ms / 1e6 / HBM_PEAK_GBS, 4)},
+        },
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse_args()
     if args.copy_calibration:
@@ -520,6 +593,9 @@ def main():
         sys.exit(2)
     if args.train_step:
         bench_train_step(args)
+        return
+    if args.ply_io:
+        bench_ply_io(args)
         return
     from gaussian_splats import scenes
     from gaussian_splats.kernels.rasterize import _native

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parents[2] / "_lib" / "libgs_raster.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 GS_OK = 0
 GS_ERR_INVALID_ARGUMENT = 1
@@ -179,7 +179,13 @@ _SIGNATURES = {
         c_int,
         [c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_size_t, c_void_p, c_void_p],
     ),
+    "gs_ply_unpack": (
+        c_int, [c_void_p, c_int64, c_int32, c_void_p, c_int32, c_int32] + [c_void_p] * 7
+    ),
+    "gs_ply_pack": (c_int, [c_void_p] * 6 + [c_int64, c_int32, c_void_p, c_void_p]),
 }
+
+PLY_MAX_FIELDS = 89
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -42,7 +42,7 @@ extern "C" {
 
 #define GS_API __attribute__((visibility("default")))
 
-#define GS_ABI_VERSION 4
+#define GS_ABI_VERSION 5
 
 typedef enum gs_status {
   GS_OK = 0,
@@ -350,6 +350,34 @@ typedef struct gs_adam_tensor {
 GS_API int gs_adam_step(
     const gs_adam_tensor* tensors, int32_t count, double beta1, double beta2,
     double eps, double weight_decay, void* stream);
+
+/* Scene files: the binary PLY "vertex" records of a Gaussian-splat scene
+ * (src/gaussian_splats/splats/ply.py).  Fields per Gaussian in canonical
+ * order: mean 3, normals 3, rotation 4, scale 3, opacity 1, color 3K
+ * (coefficient-major, RGB innermost) — 14 + 3K float32 values. */
+#define GS_PLY_MAX_FIELDS 89 /* 14 + 3 * 25 (SH degree 4) */
+
+/* Splits n records of record_bytes bytes each (device memory, 16-byte
+ * aligned, the file's vertex block as stored) into the six parameter
+ * tensors: output float j of a Gaussian (canonical order) is the float32 at
+ * byte field_offsets[j] of its record (field_offsets in host memory, 14 +
+ * 3 sh_coeffs entries), or 0 where the offset is -1; big_endian != 0 swaps
+ * each value's bytes.  Replaces the per-property reads of load_ply
+ * (ply.py:55-89), which the host's header parse turns into offsets. */
+GS_API int gs_ply_unpack(
+    const void* records, int64_t n, int32_t record_bytes,
+    const int32_t* field_offsets, int32_t big_endian, int32_t sh_coeffs,
+    float* mean, float* normals, float* rotation, float* scale, float* opacity,
+    float* color, void* stream);
+
+/* Writes n records of 14 + 3 sh_coeffs little-endian float32 values in the
+ * property order of save_ply (ply.py:23-43): x y z nx ny nz f_dc_0..2
+ * f_rest_0.. (f_rest_{c (K-1) + k - 1} = color[k][c]) opacity scale_0..2
+ * rot_0..3.  normals may be NULL (zeros, as ply.py:20 substitutes). */
+GS_API int gs_ply_pack(
+    const float* mean, const float* normals, const float* rotation,
+    const float* scale, const float* opacity, const float* color, int64_t n,
+    int32_t sh_coeffs, void* records, void* stream);
 
 #ifdef __cplusplus
 }

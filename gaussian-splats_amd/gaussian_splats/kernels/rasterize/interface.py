@@ -13,6 +13,7 @@ from typing import TYPE_CHECKING, Literal
 
 import torch
 
+from ...timing import stage_timer
 from . import _native as nat
 from .composite import composite
 from .intersections import MAX_BUCKET_TILES, bin_gaussians, bin_tiles, emit_tiles, sort_tiles
@@ -134,7 +135,7 @@ def _rasterize(
     return forward_pipeline(
         mean, rotation, scale, opacity, color, camera_rotation, camera_translation, fx, fy, cx,
         cy, image_width, image_height, tile_size, opacity_threshold, near, far, rendering_mode,
-        confidence,
+        confidence, timer=stage_timer(),
     )
 
 

@@ -28,6 +28,7 @@ from typing import TYPE_CHECKING, Literal, Sequence
 
 import torch
 
+from ...timing import stage_timer
 from . import _native as nat
 from .intersections import MAX_BUCKET_TILES, bin_gaussians, bin_tiles, emit_tiles, sort_tiles
 from .interface import _contiguous
@@ -221,7 +222,7 @@ def _rasterize_views(
     return forward_views(
         mean, rotation, scale, opacity, color, camera_rotations, camera_translations, intrinsics,
         image_width, image_height, tile_size, opacity_threshold, near, far, rendering_mode,
-        confidence,
+        confidence, timer=stage_timer(),
     )
 
 

@@ -36,6 +36,11 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="config3")
+    ap.add_argument(
+        "--scene", default=None,
+        help="time the step on a scene file instead (a GaussianSplat .pt checkpoint, e.g. a "
+             "baked scene, or a .ply), viewed by a fitted 1920x1080 camera",
+    )
     ap.add_argument("--tile-size", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-tiles", type=int, default=24, help="tiles in the CPU baseline sample")
@@ -603,7 +608,7 @@ def main():
 
     _native.library()
     device = torch.device("cuda:0")
-    scene = scenes.CONFIGS[args.config]()
+    scene = scenes.from_file(args.scene) if args.scene else scenes.CONFIGS[args.config]()
     if len(scene.cameras) > 1:
         bench_views(args, scene)
         return

@@ -204,3 +204,42 @@ def edge_case_scene(
         image_size=image_size, focal_length=(0.75 * w, 0.75 * w), principal_point=(w / 2, h / 2)
     )
     return Scene("edge_cases", mean, rotation, scale, opacity, color, [cam], near=near, far=far)
+
+
+def from_file(
+    path: str,
+    image_size: tuple[int, int] = (1920, 1080),
+    seed: int = 0,
+    near: float = 0.2,
+    far: float = 100.0,
+) -> Scene:
+    """A scene stored on disk — a GaussianSplat checkpoint (``.pt``, what the
+    reference's baking and training write) or a PLY file — viewed as the
+    viewer opens one: a camera pitched 45 degrees down, fitted to the points
+    (visualize/gaussian/backend.py:68-75), with fx = fy = 0.75 * width.  The
+    loss target is seeded U(0, 1)."""
+    from pathlib import Path
+
+    from .splats.ply import load_ply
+    from .splats.splats import GaussianSplat
+
+    path = Path(path)
+    if path.suffix.lower() == ".ply":
+        state = load_ply(path)
+    else:
+        state = GaussianSplat.from_checkpoint(path).state_dict()
+    mean, rotation, scale, opacity, color = (
+        state[k].detach().float().contiguous() for k in ("mean", "rotation", "scale", "opacity", "color")
+    )
+    w, h = image_size
+    q = torch.tensor([math.cos(math.pi / 8), -math.sin(math.pi / 8), 0.0, 0.0])
+    with torch.random.fork_rng(devices=[]):
+        torch.manual_seed(seed)  # fit_to_points samples 10k points of large scenes
+        cam = PinholeCamera(
+            rotation=q, image_size=image_size, focal_length=(0.75 * w, 0.75 * w),
+            principal_point=(w / 2, h / 2),
+        ).fit_to_points(mean)
+    g = torch.Generator().manual_seed(seed)
+    target = torch.rand(h, w, 3, generator=g)
+    return Scene(path.name, mean, rotation, scale, opacity, color, [cam], near=near, far=far,
+                 backward=True, target=target, notes={"source": str(path)})

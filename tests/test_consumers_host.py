@@ -132,3 +132,20 @@ def test_timing_api():
 def test_trajectory_frame_count(frames):
     s = bm.random_scene(100, seed=0, device="cpu")
     assert len(bm.generate_trajectory(s, (64, 48), frames)) == frames
+
+
+def test_scene_from_file(tmp_path):
+    """Checkpoints and PLY files load as the same benchmark scene."""
+    from gaussian_splats import scenes
+    from gaussian_splats.splats.ply import save_ply
+
+    torch.manual_seed(3)
+    s = GaussianSplat(20_000, sh_degree=3)
+    s.save_checkpoint(tmp_path / "baked.pt")
+    save_ply(s.state_dict(), tmp_path / "baked.ply")
+    a = scenes.from_file(str(tmp_path / "baked.pt"), image_size=(320, 180))
+    b = scenes.from_file(str(tmp_path / "baked.ply"), image_size=(320, 180))
+    for x, y in zip(a.params(), b.params()):
+        assert torch.equal(x, y)
+    assert torch.equal(a.cameras[0].translation, b.cameras[0].translation)
+    assert a.target.shape == (180, 320, 3) and a.cameras[0].image_size == (320, 180)

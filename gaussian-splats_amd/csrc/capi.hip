@@ -42,8 +42,8 @@ int check_view(const gs_view& v, bool need_tiles) {
                "tile_size must be a positive power of two, got %d", v.tile_size);
     GS_REQUIRE(v.tile_size >= 4 && v.tile_size <= 32, GS_ERR_UNSUPPORTED,
                "tile_size %d not supported (4, 8, 16 or 32)", v.tile_size);
-    GS_REQUIRE(v.views >= 0 && v.mosaic_cols >= 0, GS_ERR_INVALID_ARGUMENT,
-               "views and mosaic_cols must be non-negative");
+    GS_REQUIRE(v.views >= 0 && v.mosaic_cols >= 0 && v.active_tiles >= 0,
+               GS_ERR_INVALID_ARGUMENT, "views, mosaic_cols and active_tiles must be non-negative");
     const int views = v.views > 1 ? v.views : 1;
     const int cols = std::min(views, v.mosaic_cols > 1 ? v.mosaic_cols : 1);
     const int64_t rows = (views + cols - 1) / cols;

@@ -62,11 +62,14 @@ constexpr int kWave = 64;
 // order of tile_order.hip partitions the tiles the same way.
 constexpr int kCompositeWaves = 4;
 
-// Images with fewer tiles than this are composited with the tile's bands
-// split over kCompositeWaves waves (tiles of 16 and 32 pixels): with one wave
-// per tile they would leave most SIMDs idle and wait on their longest tiles.
+// Images with fewer tiles with work than this are composited with the tile's
+// bands split over kCompositeWaves waves (tiles of 16 and 32 pixels): with one
+// wave per tile they would leave most SIMDs idle and wait on their longest
+// tiles.  `active` counts the tiles with a non-empty list (0: unknown, all).
 constexpr int kCompositeSplitTiles = 4096;
-inline bool composite_split(int num_tiles) { return num_tiles < kCompositeSplitTiles; }
+inline bool composite_split(int num_tiles, int active) {
+  return (active > 0 && active < num_tiles ? active : num_tiles) < kCompositeSplitTiles;
+}
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 

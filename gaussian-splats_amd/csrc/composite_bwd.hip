@@ -244,9 +244,9 @@ void launch_split(const CompositeBwdArgs& a, hipStream_t s) {
 }
 
 template <int TILE>
-void launch(const CompositeBwdArgs& a, hipStream_t s) {
+void launch(const CompositeBwdArgs& a, int active_tiles, hipStream_t s) {
   if constexpr (TILE >= 16) {
-    if (composite_split(a.num_tiles)) return launch_split<TILE, kCompositeWaves>(a, s);
+    if (composite_split(a.num_tiles, active_tiles)) return launch_split<TILE, kCompositeWaves>(a, s);
   }
   launch_split<TILE, 1>(a, s);
 }
@@ -297,10 +297,10 @@ extern "C" GS_API int gs_composite_bwd(const float* projected_mean,
   a.grad_abs = grad_absolute;
   hipStream_t s = as_stream(stream);
   switch (view.tile_size) {
-    case 4: launch<4>(a, s); break;
-    case 8: launch<8>(a, s); break;
-    case 16: launch<16>(a, s); break;
-    default: launch<32>(a, s); break;
+    case 4: launch<4>(a, view.active_tiles, s); break;
+    case 8: launch<8>(a, view.active_tiles, s); break;
+    case 16: launch<16>(a, view.active_tiles, s); break;
+    default: launch<32>(a, view.active_tiles, s); break;
   }
   return check_launch("composite_bwd");
 }

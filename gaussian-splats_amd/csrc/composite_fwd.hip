@@ -186,9 +186,10 @@ void launch_split(const CompositeArgs& a, bool ellipsoid, hipStream_t s) {
 }
 
 template <int TILE>
-void launch(const CompositeArgs& a, bool ellipsoid, hipStream_t s) {
+void launch(const CompositeArgs& a, int active_tiles, bool ellipsoid, hipStream_t s) {
   if constexpr (TILE >= 16) {
-    if (composite_split(a.num_tiles)) return launch_split<TILE, kCompositeWaves>(a, ellipsoid, s);
+    if (composite_split(a.num_tiles, active_tiles))
+      return launch_split<TILE, kCompositeWaves>(a, ellipsoid, s);
   }
   launch_split<TILE, 1>(a, ellipsoid, s);
 }
@@ -230,11 +231,12 @@ extern "C" GS_API int gs_composite(const void* records, const int32_t* gaussian_
   a.n_contrib = n_contributors;
   const bool ellipsoid = view.rendering_mode == GS_MODE_ELLIPSOID;
   hipStream_t s = as_stream(stream);
+  const int active = view.active_tiles;
   switch (view.tile_size) {
-    case 4: launch<4>(a, ellipsoid, s); break;
-    case 8: launch<8>(a, ellipsoid, s); break;
-    case 16: launch<16>(a, ellipsoid, s); break;
-    default: launch<32>(a, ellipsoid, s); break;
+    case 4: launch<4>(a, active, ellipsoid, s); break;
+    case 8: launch<8>(a, active, ellipsoid, s); break;
+    case 16: launch<16>(a, active, ellipsoid, s); break;
+    default: launch<32>(a, active, ellipsoid, s); break;
   }
   return check_launch("composite");
 }

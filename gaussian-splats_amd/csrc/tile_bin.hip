@@ -318,19 +318,24 @@ __global__ __launch_bounds__(256) void tables_kernel(int32_t* __restrict__ diff2
     totals[0] = tot_e;
     totals[1] = tot_a;
     totals[2] = tot_b;
-    totals[3] = 0;
   }
   __syncthreads();
 
   // 4. Ranges: row start + start in the row; a tile ends where the next tile
-  // of its row starts (the last one at the row's end).
+  // of its row starts (the last one at the row's end).  totals[3] = tiles
+  // with a non-empty list (the compositing launch shape depends on it).
   const int64_t num_tiles = int64_t(tw) * th;
+  int64_t active = 0;
   for (int64_t t = threadIdx.x; t < num_tiles; t += 256) {
     const int ty = int(t / tw), tx = int(t - int64_t(ty) * tw);
     const int64_t begin = s_row[ty] + uint32_t(tab[ty * pitch + tx]);
     const int64_t end = tx + 1 < tw ? s_row[ty] + uint32_t(tab[ty * pitch + tx + 1]) : s_end[ty];
     reinterpret_cast<longlong2*>(ranges)[t] = make_longlong2(begin, end);
+    active += end > begin ? 1 : 0;
   }
+  int64_t tot_active;
+  block_exclusive_scan(active, scratch, tot_active);
+  if (threadIdx.x == 0) totals[3] = tot_active;
 }
 
 // Row-list entry packing: first column | (width - 1) << 8 | row << 16 (grids

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parents[2] / "_lib" / "libgs_raster.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 GS_OK = 0
 GS_ERR_INVALID_ARGUMENT = 1
@@ -59,6 +59,7 @@ class GsView(ctypes.Structure):
         ("covariance_epsilon", c_float),
         ("views", c_int32),
         ("mosaic_cols", c_int32),
+        ("active_tiles", c_int32),
     ]
 
 
@@ -78,6 +79,7 @@ def make_view(
     covariance_epsilon: float = 0.03,
     views: int = 1,
     mosaic_cols: int = 1,
+    active_tiles: int = 0,
 ) -> GsView:
     if rendering_mode not in MODES:
         raise ValueError(f"Invalid rendering mode: {rendering_mode}")
@@ -85,7 +87,23 @@ def make_view(
         float(fx), float(fy), float(cx), float(cy), int(image_width), int(image_height),
         int(tile_size), float(near), float(far), MODES[rendering_mode], float(confidence),
         float(opacity_threshold), float(covariance_epsilon), int(views), int(mosaic_cols),
+        int(active_tiles),
     )
+
+
+_ACTIVE_ATTR = "_gs_active_tiles"
+
+
+def set_active_tiles(ranges: torch.Tensor, count: int) -> None:
+    """Records on ``ranges`` how many tiles have a non-empty list (binning
+    reads it back with the totals); the compositing launches use it to pick
+    their shape.  Only a hint: results do not depend on it."""
+    setattr(ranges, _ACTIVE_ATTR, int(count))
+
+
+def active_tiles(ranges: torch.Tensor | None) -> int:
+    """The count recorded by ``set_active_tiles``, or 0 (unknown)."""
+    return int(getattr(ranges, _ACTIVE_ATTR, 0)) if ranges is not None else 0
 
 
 _SIGNATURES = {

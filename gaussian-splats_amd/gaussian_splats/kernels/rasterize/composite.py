@@ -61,6 +61,7 @@ def composite(
     confidence: float,
     *,
     records: torch.Tensor | None = None,
+    order: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Composites the sorted per-tile lists; returns ``(image[H,W,3],
     final_transmittance[H,W], n_contributors[H,W] int32)``."""
@@ -71,6 +72,7 @@ def composite(
     tiles_w, tiles_h = nat.tiles(image_width, image_height, tile_size)
     if ranges.shape != (tiles_w * tiles_h, 2):
         raise ValueError(f"ranges must be [{tiles_w * tiles_h}, 2], got {tuple(ranges.shape)}")
+    active = nat.active_tiles(ranges)
     ranges = nat.prepare(ranges, torch.int64)
     gaussian_ids = nat.prepare(gaussian_ids, torch.int32)
     image = torch.empty((image_height, image_width, 3), dtype=torch.float32, device=device)
@@ -78,11 +80,12 @@ def composite(
     n_contributors = torch.empty((image_height, image_width), dtype=torch.int32, device=device)
     view = nat.make_view(
         1.0, 1.0, 0.0, 0.0, image_width, image_height, tile_size, rendering_mode=rendering_mode,
-        confidence=confidence, opacity_threshold=opacity_threshold,
+        confidence=confidence, opacity_threshold=opacity_threshold, active_tiles=active,
     )
     nat.check(
         nat.library().gs_composite(
-            nat.ptr(records), nat.ptr(gaussian_ids), nat.ptr(ranges), None, view, nat.ptr(image),
+            nat.ptr(records), nat.ptr(gaussian_ids), nat.ptr(ranges), nat.ptr(order), view,
+            nat.ptr(image),
             nat.ptr(final_transmittance), nat.ptr(n_contributors), nat.stream(device),
         ),
         "composite",

@@ -50,6 +50,7 @@ def composite_bwd(
     grad_image = nat.prepare(grad_image.float() if grad_image.dtype != torch.float32 else grad_image)
     final_transmittance = nat.prepare(final_transmittance)
     n_contributors = nat.prepare(n_contributors, torch.int32)
+    active = nat.active_tiles(ranges)
     ranges = nat.prepare(ranges, torch.int64)
     gaussian_ids = nat.prepare(gaussian_ids, torch.int32)
     n = projected_mean.shape[0]
@@ -59,7 +60,7 @@ def composite_bwd(
         raise ValueError("out must be a contiguous zero-filled float32 tensor of shape [N, 9]")
     view = nat.make_view(
         1.0, 1.0, 0.0, 0.0, image_width, image_height, tile_size,
-        opacity_threshold=opacity_threshold,
+        opacity_threshold=opacity_threshold, active_tiles=active,
     )
     absolute = torch.zeros((n, 2), dtype=torch.float32, device=device) if return_absolute else None
     lib = nat.library()

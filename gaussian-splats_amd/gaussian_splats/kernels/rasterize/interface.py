@@ -194,7 +194,7 @@ def _setup_context(ctx, inputs, output) -> None:
         )
         ctx.view_composite = nat.make_view(
             1.0, 1.0, 0.0, 0.0, ctx.image_width, ctx.image_height, ctx.tile_size,
-            opacity_threshold=ctx.opacity_threshold,
+            opacity_threshold=ctx.opacity_threshold, active_tiles=nat.active_tiles(output[8]),
         )
         ctx.view_project = nat.make_view(ctx.fx, ctx.fy, 0.0, 0.0, ctx.image_width, ctx.image_height)
         num_tiles = output[8].shape[0]

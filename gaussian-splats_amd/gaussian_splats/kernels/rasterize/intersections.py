@@ -181,7 +181,8 @@ def bin_tiles(
         "bin_tiles_plan",
     )
     mark("bin")
-    total, row_entries, blocks, _ = host_totals.tolist()
+    total, row_entries, blocks, active = host_totals.tolist()
+    nat.set_active_tiles(ranges, active)
     sorted_ids = torch.empty(total, dtype=torch.int32, device=device)
     if total:
         ws = nat.workspace(

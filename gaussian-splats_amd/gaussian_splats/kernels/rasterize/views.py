@@ -166,6 +166,7 @@ def forward_views(
     view = _mosaic_view(
         image_width, image_height, tile_size, views, cols, rendering_mode=rendering_mode,
         confidence=confidence, opacity_threshold=opacity_threshold,
+        active_tiles=nat.active_tiles(ranges),
     )
     nat.check(
         lib.gs_composite(
@@ -271,6 +272,7 @@ def _setup_context(ctx, inputs, output) -> None:
         ctx.rendering_mode,
         ctx.confidence,
     ) = inputs[8:]
+    ctx.active_tiles = nat.active_tiles(output[8])
 
 
 def backward_views(
@@ -289,13 +291,17 @@ def backward_views(
     saved: Sequence[torch.Tensor],
     grad_image: torch.Tensor | None,
     timer=None,
+    active_tiles: int | None = None,
 ) -> tuple[torch.Tensor, ...]:
     """composite_bwd over the mosaic -> project_bwd summed over the views.
 
     ``saved`` holds the forward's outputs 1..9 (transmittance through counts);
     returns the gradients of the five parameter tensors.  ``timer(name)``
-    marks "composite_bwd" and "project_bwd"."""
+    marks "composite_bwd" and "project_bwd".  ``active_tiles``: tiles with a
+    non-empty list (default: the count binning recorded on the ranges)."""
     mark = timer or (lambda name: None)
+    if active_tiles is None:
+        active_tiles = nat.active_tiles(saved[7])
     mean, rotation, scale, opacity, color = (
         _contiguous(t) for t in (mean, rotation, scale, opacity, color)
     )
@@ -323,7 +329,8 @@ def backward_views(
     lib = nat.library()
     stream = nat.stream(device)
     ptr = nat.ptr
-    view = _mosaic_view(w, h, tile, views, cols, opacity_threshold=opacity_threshold)
+    view = _mosaic_view(w, h, tile, views, cols, opacity_threshold=opacity_threshold,
+                        active_tiles=active_tiles)
     num_tiles = ranges.shape[0]
     order = torch.empty(num_tiles, dtype=torch.int32, device=device)
     order_ws = nat.workspace(lib.gs_tile_order_workspace_bytes(num_tiles), device)
@@ -370,7 +377,7 @@ def _backward(ctx, *grad_outputs):
     grads = backward_views(
         *saved[:5], ctx.camera_rotations, ctx.camera_translations, ctx.intrinsics,
         ctx.image_width, ctx.image_height, ctx.tile_size, ctx.opacity_threshold, saved[5:],
-        grad_outputs[0],
+        grad_outputs[0], active_tiles=ctx.active_tiles,
     )
     return (*grads, *(None,) * 11)
 

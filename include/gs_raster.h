@@ -42,7 +42,7 @@ extern "C" {
 
 #define GS_API __attribute__((visibility("default")))
 
-#define GS_ABI_VERSION 5
+#define GS_ABI_VERSION 6
 
 typedef enum gs_status {
   GS_OK = 0,
@@ -78,6 +78,11 @@ typedef struct gs_view {
    * mosaic's tiles.  0 or 1 in both fields: a single view. */
   int32_t views;
   int32_t mosaic_cols;
+  /* Tiles with a non-empty list (totals[3] of gs_bin_tiles_plan), or 0 when
+   * unknown.  The compositing calls split each tile's pixels over four waves
+   * when fewer than 4096 tiles have work (few or skewed tiles would leave
+   * SIMDs idle behind their longest tiles); results do not depend on it. */
+  int32_t active_tiles;
 } gs_view;
 
 /* ABI version of the loaded library (GS_ABI_VERSION). No counterpart in the

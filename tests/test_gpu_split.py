@@ -1,0 +1,77 @@
+"""The compositing launch shape chosen from the tiles with work: binning
+records how many tiles have a non-empty list, and with fewer than 4096 of
+them the compositing kernels split each tile's bands over four waves even
+when the image has more tiles.  Both shapes must give the same forward
+outputs bit for bit and the same gradients up to the order of the atomic
+adds; the forward is also checked against the oracle."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from gaussian_splats import scenes
+from gaussian_splats.kernels.rasterize import _native as nat
+from gaussian_splats.kernels.rasterize import composite, composite_bwd
+from gaussian_splats.kernels.rasterize.interface import forward_pipeline
+from oracle import rasterizer as orc
+from parity import assert_close_flip_aware, oracle_camera
+
+pytestmark = pytest.mark.gpu
+
+THRESHOLD = 0.999
+
+
+def _scene(clustered: bool):
+    scene = scenes.edge_case_scene(n=3000, sh_degree=1, image_size=(1040, 1040))
+    if clustered:  # small Gaussians around the optical axis: ~670 tiles with work
+        g = torch.Generator().manual_seed(5)
+        scene.mean[:, :2] = torch.randn(3000, 2, generator=g) * 0.4
+        scene.mean[:, 2] = -(torch.rand(3000, generator=g) * 4 + 4)
+        scene.scale[:] = torch.rand(3000, 3, generator=g) * 1.5 - 4.5
+    return scene
+
+
+@pytest.mark.parametrize("clustered", [True, False], ids=("clustered", "spread"))
+def test_split_and_one_wave_shapes_agree(device, clustered):
+    scene = _scene(clustered)
+    cam = scene.cameras[0]
+    fx, fy = cam.focal_length
+    cx, cy = cam.principal_point
+    w, h = cam.image_size
+    print(f"[split] clustered={clustered}", flush=True)
+    out = forward_pipeline(
+        *(t.to(device) for t in scene.params()), cam.rotation_matrix, cam.translation, fx, fy, cx,
+        cy, w, h, 16, THRESHOLD, scene.near, scene.far, "gaussian", 0.95,
+    )
+    image, final_t, ncon, pmean, pinv, pcol, pop, gids, ranges, counts = out
+    active = nat.active_tiles(ranges)
+    assert active == int((ranges[:, 1] > ranges[:, 0]).sum())
+    assert ranges.shape[0] == 65 * 65
+    if clustered:
+        assert 0 < active < 4096  # the op composited with the split shape
+
+    split_ranges, one_wave_ranges = ranges.clone(), ranges.clone()
+    nat.set_active_tiles(split_ranges, 1)  # forces four waves per tile
+    # No recorded count: the image's 4225 tiles select one wave per tile.
+    args = (pmean, pinv, pcol, pop, gids)
+    a = composite(*args, split_ranges, w, h, 16, THRESHOLD, "gaussian", 0.95)
+    b = composite(*args, one_wave_ranges, w, h, 16, THRESHOLD, "gaussian", 0.95)
+    for x, y, op_out, name in zip(a, b, (image, final_t, ncon), ("image", "T", "n_contributors")):
+        assert torch.equal(x, y), name
+        assert torch.equal(x, op_out), name
+
+    ref = orc.rasterize(*scene.params(), oracle_camera(cam), tile_size=16,
+                        opacity_threshold=THRESHOLD, near=scene.near, far=scene.far)
+    assert_close_flip_aware(a[0].cpu(), ref.image, ref.composite.margin, atol=1e-5, what="image")
+
+    g = torch.Generator().manual_seed(3)
+    grad_image = (torch.rand(h, w, 3, generator=g) * 2 - 1).to(device)
+    ga = composite_bwd(*args, split_ranges, grad_image, final_t, ncon, w, h, 16, THRESHOLD,
+                       "gaussian")
+    gb = composite_bwd(*args, one_wave_ranges, grad_image, final_t, ncon, w, h, 16, THRESHOLD,
+                       "gaussian")
+    for col in range(9):
+        scale = float(gb[:, col].abs().max())
+        err = float((ga[:, col] - gb[:, col]).abs().max())
+        assert err <= 1e-5 * scale + 1e-12, (col, err, scale)

@@ -631,7 +631,9 @@ def main():
     print("[bench] warmup done", file=sys.stderr, flush=True)
 
     torch.cuda.synchronize()
-    with _native.LaunchTimer("composite_bwd", capacity=args.steps + 1) as timer:
+    with _native.LaunchTimer("composite_bwd", capacity=args.steps + 1) as timer, \
+            _native.LaunchTimer("project", capacity=args.steps + 1) as project_timer, \
+            _native.LaunchTimer("project_bwd", capacity=args.steps + 1) as project_bwd_timer:
         t0 = time.perf_counter()
         for _ in range(args.steps):
             for p in splats.parameters():
@@ -691,6 +693,18 @@ def main():
         "valu_issue": valu,
     }
 
+    # The HBM-bound kernels, timed per launch the same way: algorithmic bytes
+    # of the projection (parameters in, 116 B of outputs per Gaussian out)
+    # and of its backward (parameters and dL/d projected in, gradients out).
+    kernels = {}
+    for name, t, nbytes in (("project_fwd_kernel", project_timer, bytes_model["project"]),
+                            ("project_bwd_kernel", project_bwd_timer, bytes_model["project_bwd"])):
+        ms = t.mean_ms()
+        if ms > 0:
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            kernels[name] = {"launch_ms": round(ms, 4), "algorithmic_bytes": nbytes,
+                             "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+
     cpu = None
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
@@ -715,6 +729,7 @@ def main():
             "intersections": info["total"],
         },
         "stages": stages,
+        "kernels": kernels,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }

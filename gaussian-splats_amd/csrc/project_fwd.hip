@@ -67,11 +67,51 @@ __global__ __launch_bounds__(kProjectBlock) void project_fwd_kernel(ProjectArgs 
 
   const int64_t base = int64_t(blockIdx.x) * kProjectBlock;
   const int64_t nvalid = min(int64_t(kProjectBlock), a.n - base);
+  const int64_t gi = base + threadIdx.x;
+  const bool have = gi < a.n;
+  // The thread's own parameters are requested before the colour block, so
+  // their loads are in flight together with it (threads past the end read
+  // the last Gaussian, branch-free, and return after the barrier).
+  const int64_t gl = have ? gi : a.n - 1;
+  const float mx = a.mean[gl * 3 + 0];
+  const float my = a.mean[gl * 3 + 1];
+  const float mz = a.mean[gl * 3 + 2];
+  const float4 q = reinterpret_cast<const float4*>(a.rotation)[gl];
+  const float ls0 = a.scale[gl * 3 + 0];
+  const float ls1 = a.scale[gl * 3 + 1];
+  const float ls2 = a.scale[gl * 3 + 2];
+  const float lo = a.opacity[gl];
   {
     const float* src = a.color + base * F;
     const float4* src4 = reinterpret_cast<const float4*>(src);
     const int total = int(nvalid) * F;
-    for (int i = threadIdx.x; i * 4 < total; i += kProjectBlock) {
+    // A full block is kProjectBlock * F / 4 float4 (F = 3K, K in {1, 4, 9,
+    // 16}: a multiple of 4 floats per block): every thread issues all of its
+    // loads before the first LDS store, so they are in flight together.
+    constexpr int kVec4 = kProjectBlock * F / 4;
+    constexpr int kPerThread = (kVec4 + kProjectBlock - 1) / kProjectBlock;
+    if (nvalid == kProjectBlock) {
+      float4 v[kPerThread];
+#pragma unroll
+      for (int j = 0; j < kPerThread; ++j) {
+        const int i = threadIdx.x + j * kProjectBlock;
+        if (kVec4 % kProjectBlock == 0 || i < kVec4) v[j] = src4[i];
+      }
+#pragma unroll
+      for (int j = 0; j < kPerThread; ++j) {
+        const int i = threadIdx.x + j * kProjectBlock;
+        if (kVec4 % kProjectBlock == 0 || i < kVec4) {
+          const float vals[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int e = i * 4 + t;
+            const int g = e / F;
+            coeff[g * S + (e - g * F)] = vals[t];
+          }
+        }
+      }
+    }
+    for (int i = threadIdx.x; nvalid < kProjectBlock && i * 4 < total; i += kProjectBlock) {
       const int f = i * 4;
       float vals[4];
       if (f + 4 <= total) {
@@ -95,17 +135,10 @@ __global__ __launch_bounds__(kProjectBlock) void project_fwd_kernel(ProjectArgs 
     }
   }
   __syncthreads();
-
-  const int64_t gi = base + threadIdx.x;
-  if (gi >= a.n) return;
+  if (!have) return;
 
   // View-independent terms, computed once per Gaussian.
-  const float mx = a.mean[gi * 3 + 0];
-  const float my = a.mean[gi * 3 + 1];
-  const float mz = a.mean[gi * 3 + 2];
-
   // Normalised quaternion (w, x, y, z) -> rotation (utils.py:8-25).
-  const float4 q = reinterpret_cast<const float4*>(a.rotation)[gi];
   const float qn = fmaxf(sqrtf(q.x * q.x + q.y * q.y + q.z * q.z + q.w * q.w), 1e-12f);
   const float qw = q.x / qn, qx = q.y / qn, qy = q.z / qn, qz = q.w / qn;
   const float q00 = 1.0f - 2.0f * (qy * qy + qz * qz);
@@ -118,11 +151,11 @@ __global__ __launch_bounds__(kProjectBlock) void project_fwd_kernel(ProjectArgs 
   const float q21 = 2.0f * (qy * qz + qw * qx);
   const float q22 = 1.0f - 2.0f * (qx * qx + qy * qy);
 
-  const float sx = expf(a.scale[gi * 3 + 0]);
-  const float sy = expf(a.scale[gi * 3 + 1]);
-  const float sz = expf(a.scale[gi * 3 + 2]);
+  const float sx = expf(ls0);
+  const float sy = expf(ls1);
+  const float sz = expf(ls2);
 
-  const float alpha0 = 1.0f / (1.0f + expf(-a.opacity[gi]));
+  const float alpha0 = 1.0f / (1.0f + expf(-lo));
   // Extent of the ellipse in standard deviations (torch.py:233-252) and the
   // largest quadratic form D for which the blended alpha can reach 1/255.
   const float extent = a.ellipsoid ? a.ellipsoid_extent : 2.0f * sqrtf(logf(alpha0 * 255.0f));

@@ -272,11 +272,11 @@ def _backward(ctx, *grad_outputs):
     if n:
         cam_r, cam_t = ctx.camera_host
         nat.check(
-            lib.gs_project_bwd(
+            nat.launch("project_bwd", lambda: lib.gs_project_bwd(
                 ptr(mean), ptr(rotation), ptr(scale), ptr(opacity), ptr(color), n,
                 color.shape[1], ptr(cam_r), ptr(cam_t), ctx.view_project, ptr(inverse_covariance),
                 ptr(grad_projected), ptr(counts), *(ptr(g) for g in grads), stream,
-            ),
+            )),
             "project_bwd",
         )
     return (*grads, *(None,) * 14)

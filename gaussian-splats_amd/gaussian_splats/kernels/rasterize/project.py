@@ -78,13 +78,14 @@ def project_and_count(
     )
     lib = nat.library()
     nat.check(
-        lib.gs_project_and_count(
+        nat.launch("project", lambda: lib.gs_project_and_count(
             nat.ptr(mean), nat.ptr(rotation), nat.ptr(scale), nat.ptr(opacity), nat.ptr(color),
-            n, color.shape[1], c_void_p(camera_rotation.data_ptr()), c_void_p(camera_translation.data_ptr()), view,
+            n, color.shape[1], c_void_p(camera_rotation.data_ptr()),
+            c_void_p(camera_translation.data_ptr()), view,
             nat.ptr(projected_mean), nat.ptr(inverse_covariance), nat.ptr(projected_color),
             nat.ptr(projected_opacity), nat.ptr(bounds), nat.ptr(counts), nat.ptr(records),
             nat.ptr(depth_keys), nat.stream(device),
-        ),
+        )),
         "project_and_count",
     )
     return projected_mean, inverse_covariance, projected_color, projected_opacity, bounds, counts

@@ -591,7 +591,17 @@ __device__ int load_window(const uint32_t* __restrict__ offs, int64_t first, int
   const int64_t span = last - first + 1;
   if (span > kTile && threadIdx.x == 0) atomicOr(err, 2u);
   const int m = int(min(max(span, int64_t(1)), int64_t(kTile)));
-  for (int k = threadIdx.x; k < m; k += kBlock) rel[k] = int32_t(offs[first + k] - c0);
+  // All of the thread's loads are issued before the first store (indices
+  // clamped into the window, so every load is in bounds).
+  uint32_t v[kTile / kBlock];
+#pragma unroll
+  for (int j = 0; j < kTile / kBlock; ++j)
+    v[j] = offs[first + min(int(threadIdx.x) + j * kBlock, m - 1)];
+#pragma unroll
+  for (int j = 0; j < kTile / kBlock; ++j) {
+    const int k = int(threadIdx.x) + j * kBlock;
+    if (k < m) rel[k] = int32_t(v[j] - c0);
+  }
   __syncthreads();
   return m;
 }
@@ -646,16 +656,27 @@ __global__ __launch_bounds__(kBlock) void row_bucket_kernel(
 
   uint32_t dig[kItems];
   uint32_t val[2][kItems];
+  // Every position has an owner in [0, m) (the running maximum starts at 0),
+  // so all gathers are in bounds: they are issued unconditionally, all
+  // kItems order reads first, then all rectangle reads, so each round of
+  // dependent loads is one round trip for the whole thread.
+  int kk[kItems];
+  int g[kItems];
+  uint32_t r[kItems];
+#pragma unroll
+  for (int i = 0; i < kItems; ++i) {
+    kk[i] = sh.own[wid * kSeg + i * 64 + lane];
+    g[i] = order[p_first + kk[i]];
+  }
+#pragma unroll
+  for (int i = 0; i < kItems; ++i) r[i] = packed[g[i]];
 #pragma unroll
   for (int i = 0; i < kItems; ++i) {
     const int e = wid * kSeg + i * 64 + lane;
-    const int k = sh.own[e];
-    const int g = order[p_first + k];
-    const uint32_t r = packed[g];
-    const uint32_t ty = (((r >> 16) & 0xFFu) + uint32_t(e - rel[k])) & ((1u << BITS) - 1u);
+    const uint32_t ty = (((r[i] >> 16) & 0xFFu) + uint32_t(e - rel[kk[i]])) & ((1u << BITS) - 1u);
     dig[i] = e < nvalid ? ty : 0u;
-    val[0][i] = uint32_t(g);
-    val[1][i] = (r & 0xFFFFu) | (ty << 16);  // first column, width - 1, row
+    val[0][i] = uint32_t(g[i]);
+    val[1][i] = (r[i] & 0xFFFFu) | (ty << 16);  // first column, width - 1, row
   }
   uint32_t* const out[2] = {out_g, out_xw};
   place_items<BITS, 2>(
@@ -712,13 +733,21 @@ __global__ __launch_bounds__(kBlock) void column_bucket_kernel(
 
   uint32_t dig[kItems];
   uint32_t val[1][kItems];
+  // Owners lie in [0, m) for every position (see find_owners), so both
+  // gathers are issued unconditionally and all together.
+  int kk[kItems];
+  uint32_t xw[kItems];
+#pragma unroll
+  for (int i = 0; i < kItems; ++i) {
+    kk[i] = sh.own[wid * kSeg + i * 64 + lane];
+    xw[i] = rl_xw[k_first + kk[i]];
+    val[0][i] = rl_g[k_first + kk[i]];
+  }
 #pragma unroll
   for (int i = 0; i < kItems; ++i) {
     const int e = wid * kSeg + i * 64 + lane;
-    const int k = sh.own[e];
-    const uint32_t xw = rl_xw[k_first + k];
-    dig[i] = e < nvalid ? (entry_x0(xw) + uint32_t(e - rel[k])) & ((1u << BITS) - 1u) : 0u;
-    val[0][i] = rl_g[k_first + k];
+    const uint32_t d = (entry_x0(xw[i]) + uint32_t(e - rel[kk[i]])) & ((1u << BITS) - 1u);
+    dig[i] = e < nvalid ? d : 0u;
   }
   uint32_t* const out[1] = {reinterpret_cast<uint32_t*>(sorted_ids)};
   const int64_t row_tiles = int64_t(ty) * tw;

@@ -344,10 +344,12 @@ __device__ __forceinline__ void store4(int64_t* p, const int64_t (&v)[4]) {
   reinterpret_cast<longlong2*>(p)[1] = make_longlong2(v[2], v[3]);
 }
 
-// Per-element hook of scan_kernel: sink(i, exclusive prefix, value).
+// Per-element hook of scan_kernel: sink.all(e, prefix, value, n) receives
+// the thread's M elements e[m] (exclusive prefix and value each; elements at
+// or past n are not real), so a sink's own reads can be issued together.
 struct NoSink {
-  template <typename Out>
-  __device__ void operator()(int64_t, Out, Out) const {}
+  template <int M, typename Out>
+  __device__ void all(const int64_t (&)[M], const Out (&)[M], const Out (&)[M], int64_t) const {}
 };
 
 template <typename T>
@@ -365,8 +367,8 @@ __device__ __forceinline__ T from_lane63(T v) {
 // w * 256 + i * 64 + l (i < 4) of the tile, read and written with 16-byte
 // accesses when `vec` (load.load4 and out are 16-byte aligned); four wave
 // scans order the groups, one LDS exchange orders the waves, and a wave-wide
-// look-back gives the tile's offset.  sink(i, out[i], value i) is called for
-// every element.
+// look-back gives the tile's offset.  sink.all sees every element with
+// out[i] and its value.
 template <typename Out, typename Load, typename Sink = NoSink>
 __global__ __launch_bounds__(kBlock) void scan_kernel(Load load, int64_t n, Out* __restrict__ out,
                                                       bool write_total, bool vec,
@@ -386,17 +388,26 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(Load load, int64_t n, Out*
   const int64_t base = int64_t(b) * kTile;
   Out v[4][4];
   Out group_sum[4];
+  // A full tile (the workgroup-uniform case) loads its four groups without
+  // per-lane branches, so all of a thread's loads are in flight together.
+  const bool full = vec && base + kTile <= n;
+  if (full) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t e = base + 4 * (wid * 256 + i * 64 + lane);
-    if (vec && e + 4 <= n) {
-      load.load4(e, v[i]);
-    } else {
+    for (int i = 0; i < 4; ++i) load.load4(base + 4 * (wid * 256 + i * 64 + lane), v[i]);
+  } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) v[i][j] = e + j < n ? load(e + j) : Out(0);
+    for (int i = 0; i < 4; ++i) {
+      const int64_t e = base + 4 * (wid * 256 + i * 64 + lane);
+      if (vec && e + 4 <= n) {
+        load.load4(e, v[i]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[i][j] = e + j < n ? load(e + j) : Out(0);
+      }
     }
-    group_sum[i] = v[i][0] + v[i][1] + v[i][2] + v[i][3];
   }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) group_sum[i] = v[i][0] + v[i][1] + v[i][2] + v[i][3];
   // Exclusive prefix of each group inside the wave's 1024 elements.
   Out carry = 0;
   Out group_pre[4];
@@ -427,6 +438,8 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(Load load, int64_t n, Out*
   }
   __syncthreads();
   const Out offset = s_excl + before;
+  int64_t es[16];
+  Out rs[16], vs[16];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int64_t e = base + 4 * (wid * 256 + i * 64 + lane);
@@ -443,9 +456,13 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(Load load, int64_t n, Out*
         if (e + j < n) out[e + j] = r[j];
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (e + j < n) sink(e + j, r[j], v[i][j]);
+    for (int j = 0; j < 4; ++j) {
+      es[4 * i + j] = e + j;
+      rs[4 * i + j] = r[j];
+      vs[4 * i + j] = v[i][j];
+    }
   }
+  sink.all(es, rs, vs, n);
 }
 
 }  // namespace sweep

@@ -370,12 +370,17 @@ struct HeightLoad {
 struct HeightSink {
   uint32_t* first_a;
   uint32_t capacity;  // pass-A workgroups
-  __device__ void operator()(int64_t p, uint32_t s, uint32_t h) const {
-    if (h == 0) return;
-    const uint32_t j = (s + kTile - 1) / kTile;
-    const uint32_t start = j * kTile;
-    if (start < s + h && j < capacity)
-      first_a[j] = uint32_t(p) | (start == s ? 0x80000000u : 0u);
+  template <int M>
+  __device__ void all(const int64_t (&p)[M], const uint32_t (&s)[M], const uint32_t (&h)[M],
+                      int64_t n) const {
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      if (p[m] >= n || h[m] == 0) continue;
+      const uint32_t j = (s[m] + kTile - 1) / kTile;
+      const uint32_t start = j * kTile;
+      if (start < s[m] + h[m] && j < capacity)
+        first_a[j] = uint32_t(p[m]) | (start == s[m] ? 0x80000000u : 0u);
+    }
   }
 };
 
@@ -407,19 +412,37 @@ struct WidthSink {
   uint4* info;
   uint32_t rows;      // tile rows
   uint32_t capacity;  // pass-B workgroups
-  __device__ void operator()(int64_t k, uint32_t s, uint32_t w) const {
-    const uint32_t y = entry_row(xw[k]);
-    if (y >= rows) return;
-    const uint32_t e0 = row_e[y];
-    const uint32_t rel = s - e0;
-    const uint32_t j = (rel + kTile - 1) / kTile;
-    const uint32_t start = j * kTile;
-    if (start < rel + w && row_blk[y] + j < capacity) {
-      const uint32_t c0 = e0 + start;
-      const uint32_t count = min(uint32_t(kTile), row_e[y + 1] - c0);
-      info[row_blk[y] + j] = make_uint4(uint32_t(k) | (start == rel ? 0x80000000u : 0u), c0,
-                                        y | (count << 8) | (j == 0 ? 0x80000000u : 0u),
-                                        row_a[y + 1] - 1u);
+  // Reads for all M elements are issued together: the packed entries
+  // (clamped to the last real one), then the four row-table words of each
+  // entry's row (clamped to a real row).
+  template <int M>
+  __device__ void all(const int64_t (&k)[M], const uint32_t (&s)[M], const uint32_t (&w)[M],
+                      int64_t n) const {
+    uint32_t y[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) y[m] = entry_row(xw[min(k[m], n - 1)]);
+    uint32_t e0[M], e1[M], blk[M], a1[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const uint32_t yy = min(y[m], rows - 1u);
+      e0[m] = row_e[yy];
+      e1[m] = row_e[yy + 1];
+      blk[m] = row_blk[yy];
+      a1[m] = row_a[yy + 1];
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      if (k[m] >= n || y[m] >= rows) continue;
+      const uint32_t rel = s[m] - e0[m];
+      const uint32_t j = (rel + kTile - 1) / kTile;
+      const uint32_t start = j * kTile;
+      if (start < rel + w[m] && blk[m] + j < capacity) {
+        const uint32_t c0 = e0[m] + start;
+        const uint32_t count = min(uint32_t(kTile), e1[m] - c0);
+        info[blk[m] + j] = make_uint4(uint32_t(k[m]) | (start == rel ? 0x80000000u : 0u), c0,
+                                      y[m] | (count << 8) | (j == 0 ? 0x80000000u : 0u),
+                                      a1[m] - 1u);
+      }
     }
   }
 };

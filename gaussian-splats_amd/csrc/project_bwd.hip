@@ -60,12 +60,12 @@ __device__ __forceinline__ void view_gradients(
     const ProjectBwdArgs& a, const BwdCamera& cam, int64_t gi, int64_t vi, float mx, float myy,
     float mz, const float (&R)[3][3], const float (&s3)[3], float alpha0, const float (&coef)[3 * K],
     float& gmx, float& gmy, float& gmz, float (&h)[4], float (&gs3)[3], float& gop,
-    float (&gcoef)[3 * K], float qw, float qx, float qy, float qz) {
+    float (&gcoef)[3 * K], float qw, float qx, float qy, float qz, const float (&gin)[9],
+    float4 inv) {
   const float r00 = cam.r[0], r01 = cam.r[1], r02 = cam.r[2];
   const float r10 = cam.r[3], r11 = cam.r[4], r12 = cam.r[5];
   const float r20 = cam.r[6], r21 = cam.r[7], r22 = cam.r[8];
   const float t0 = cam.t[0], t1 = cam.t[1], t2 = cam.t[2];
-  const float* gin = a.grad_in + vi * 9;
   const float gu = gin[0], gv = gin[1], gA = gin[2], gB = gin[3], gC = gin[4];
   const float gcol[3] = {gin[5], gin[6], gin[7]};
   const float gal = gin[8];
@@ -149,7 +149,6 @@ __device__ __forceinline__ void view_gradients(
   }
 
   // ---- through the 2x2 inverse: dL/dSigma = -inv G inv ----
-  const float4 inv = reinterpret_cast<const float4*>(a.inv)[vi];
   const float i00 = inv.x, i01 = inv.y, i11 = inv.w;
   const float t00 = i00 * gA + i01 * gB, t01 = i00 * gB + i01 * gC;
   const float t10 = i01 * gA + i11 * gB, t11 = i01 * gB + i11 * gC;
@@ -220,13 +219,40 @@ __device__ __forceinline__ void view_gradients(
 
 // MULTI = false: one view, no accumulation (the single-camera entry point),
 // which lets the compiler drop the view loop and keep fewer values live.
+// The block's SH coefficients come in through LDS with coalesced 16-byte loads
+// and their gradients leave the same way (sh::stage_block / unstage_block);
+// each thread keeps its own Gaussian's coefficients and gradients in
+// registers in between.
 template <int K, bool MULTI>
 __global__ __launch_bounds__(kBlock) void project_bwd_kernel(ProjectBwdArgs a) {
   constexpr int F = 3 * K;
+  constexpr int S = F + 1;
+  __shared__ float coeff[kBlock * S];
   const int views = MULTI ? a.views : 1;
   const bool accumulate = MULTI && a.accumulate;
-  const int64_t gi = int64_t(blockIdx.x) * kBlock + threadIdx.x;
-  if (gi >= a.n) return;
+  const int64_t base = int64_t(blockIdx.x) * kBlock;
+  const int nvalid = int(min(int64_t(kBlock), a.n - base));
+  const int64_t gi = base + threadIdx.x;
+  const bool have = gi < a.n;
+  // The Gaussian's own parameters and count are requested before the block's
+  // coefficients, so all of these loads are in flight together (threads past
+  // the end read the last Gaussian and write nothing).
+  const int64_t gl = have ? gi : a.n - 1;
+  const float mx = a.mean[gl * 3 + 0], myy = a.mean[gl * 3 + 1], mz = a.mean[gl * 3 + 2];
+  const float lop = a.opacity[gl];
+  const float4 qr = reinterpret_cast<const float4*>(a.rotation)[gl];
+  const float ls0 = a.scale[gl * 3 + 0], ls1 = a.scale[gl * 3 + 1], ls2 = a.scale[gl * 3 + 2];
+  const int32_t count0 = a.counts[gl];
+  // One view: its gradient inputs too.
+  float gin0[9];
+  float4 inv0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (!MULTI) {
+#pragma unroll
+    for (int i = 0; i < 9; ++i) gin0[i] = a.grad_in[gl * 9 + i];
+    inv0 = reinterpret_cast<const float4*>(a.inv)[gl];
+  }
+  sh::stage_block<F, kBlock>(a.color + base * F, nvalid, coeff);
+  __syncthreads();
   float gmx = 0.0f, gmy = 0.0f, gmz = 0.0f;
   float h[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   float gs3[3] = {0.0f, 0.0f, 0.0f};
@@ -234,18 +260,16 @@ __global__ __launch_bounds__(kBlock) void project_bwd_kernel(ProjectBwdArgs a) {
   float gcoef[F];
 #pragma unroll
   for (int i = 0; i < F; ++i) gcoef[i] = 0.0f;
-  bool any = false;
-  for (int v = 0; v < views; ++v) any |= a.counts[v * a.view_stride + gi] != 0;
+  bool any = have && count0 != 0;
+  for (int v = 1; have && v < views; ++v) any |= a.counts[v * a.view_stride + gi] != 0;
   float q[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   float qnorm = 0.0f;
   if (any) {
-    // Parameters are read once; coefficients and their gradients stay in
-    // registers, loaded only for Gaussians some view counted.
+    // Parameters are read once, only for Gaussians some view counted.
     float coef[F];
-    sh::load_coefficients<K>(a.color + gi * F, coef);
-    const float mx = a.mean[gi * 3 + 0], myy = a.mean[gi * 3 + 1], mz = a.mean[gi * 3 + 2];
-    const float alpha0 = 1.0f / (1.0f + expf(-a.opacity[gi]));
-    const float4 qr = reinterpret_cast<const float4*>(a.rotation)[gi];
+#pragma unroll
+    for (int i = 0; i < F; ++i) coef[i] = coeff[threadIdx.x * S + i];
+    const float alpha0 = 1.0f / (1.0f + expf(-lop));
     qnorm = sqrtf(qr.x * qr.x + qr.y * qr.y + qr.z * qr.z + qr.w * qr.w);
     const float qn = fmaxf(qnorm, 1e-12f);
     q[0] = qr.x / qn;
@@ -263,13 +287,21 @@ __global__ __launch_bounds__(kBlock) void project_bwd_kernel(ProjectBwdArgs a) {
     R[2][0] = 2.0f * (qx * qz - qw * qy);
     R[2][1] = 2.0f * (qy * qz + qw * qx);
     R[2][2] = 1.0f - 2.0f * (qx * qx + qy * qy);
-    const float s3[3] = {expf(a.scale[gi * 3 + 0]), expf(a.scale[gi * 3 + 1]),
-                         expf(a.scale[gi * 3 + 2])};
-    for (int v = 0; v < views; ++v) {
-      const int64_t vi = v * a.view_stride + gi;
-      if (a.counts[vi] == 0) continue;  // zero gradient from this view (project_bwd.py:324-334)
-      view_gradients<K>(a, a.cam[v], gi, vi, mx, myy, mz, R, s3, alpha0, coef, gmx, gmy, gmz, h,
-                        gs3, gop, gcoef, qw, qx, qy, qz);
+    const float s3[3] = {expf(ls0), expf(ls1), expf(ls2)};
+    if (!MULTI) {  // count0 != 0 here
+      view_gradients<K>(a, a.cam[0], gi, gi, mx, myy, mz, R, s3, alpha0, coef, gmx, gmy, gmz, h,
+                        gs3, gop, gcoef, qw, qx, qy, qz, gin0, inv0);
+    } else {
+      for (int v = 0; v < views; ++v) {
+        const int64_t vi = v * a.view_stride + gi;
+        if (a.counts[vi] == 0) continue;  // zero gradient from this view (project_bwd.py:324-334)
+        float gin[9];
+#pragma unroll
+        for (int i = 0; i < 9; ++i) gin[i] = a.grad_in[vi * 9 + i];
+        const float4 inv = reinterpret_cast<const float4*>(a.inv)[vi];
+        view_gradients<K>(a, a.cam[v], gi, vi, mx, myy, mz, R, s3, alpha0, coef, gmx, gmy, gmz,
+                          h, gs3, gop, gcoef, qw, qx, qy, qz, gin, inv);
+      }
     }
   }
   // ---- normalised quaternion -> raw quaternion (linear in h, so once) ----
@@ -284,7 +316,7 @@ __global__ __launch_bounds__(kBlock) void project_bwd_kernel(ProjectBwdArgs a) {
       for (int i = 0; i < 4; ++i) gq[i] = h[i] / 1e-12f;
     }
   }
-  if (accumulate) {
+  if (have && accumulate) {
     gmx += a.g_mean[gi * 3 + 0];
     gmy += a.g_mean[gi * 3 + 1];
     gmz += a.g_mean[gi * 3 + 2];
@@ -301,15 +333,21 @@ __global__ __launch_bounds__(kBlock) void project_bwd_kernel(ProjectBwdArgs a) {
 #pragma unroll
     for (int i = 0; i < F; ++i) gcoef[i] += prev[i];
   }
-  a.g_mean[gi * 3 + 0] = gmx;
-  a.g_mean[gi * 3 + 1] = gmy;
-  a.g_mean[gi * 3 + 2] = gmz;
-  reinterpret_cast<float4*>(a.g_rot)[gi] = make_float4(gq[0], gq[1], gq[2], gq[3]);
-  a.g_scale[gi * 3 + 0] = gs3[0];
-  a.g_scale[gi * 3 + 1] = gs3[1];
-  a.g_scale[gi * 3 + 2] = gs3[2];
-  a.g_opacity[gi] = gop;
-  sh::store_coefficients<K>(a.g_color + gi * F, gcoef);
+  if (have) {
+    a.g_mean[gi * 3 + 0] = gmx;
+    a.g_mean[gi * 3 + 1] = gmy;
+    a.g_mean[gi * 3 + 2] = gmz;
+    reinterpret_cast<float4*>(a.g_rot)[gi] = make_float4(gq[0], gq[1], gq[2], gq[3]);
+    a.g_scale[gi * 3 + 0] = gs3[0];
+    a.g_scale[gi * 3 + 1] = gs3[1];
+    a.g_scale[gi * 3 + 2] = gs3[2];
+    a.g_opacity[gi] = gop;
+    // Each thread overwrites only its own row, which only it has read.
+#pragma unroll
+    for (int i = 0; i < F; ++i) coeff[threadIdx.x * S + i] = gcoef[i];
+  }
+  __syncthreads();
+  sh::unstage_block<F, kBlock>(a.g_color + base * F, nvalid, coeff);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }

@@ -81,59 +81,7 @@ __global__ __launch_bounds__(kProjectBlock) void project_fwd_kernel(ProjectArgs 
   const float ls1 = a.scale[gl * 3 + 1];
   const float ls2 = a.scale[gl * 3 + 2];
   const float lo = a.opacity[gl];
-  {
-    const float* src = a.color + base * F;
-    const float4* src4 = reinterpret_cast<const float4*>(src);
-    const int total = int(nvalid) * F;
-    // A full block is kProjectBlock * F / 4 float4 (F = 3K, K in {1, 4, 9,
-    // 16}: a multiple of 4 floats per block): every thread issues all of its
-    // loads before the first LDS store, so they are in flight together.
-    constexpr int kVec4 = kProjectBlock * F / 4;
-    constexpr int kPerThread = (kVec4 + kProjectBlock - 1) / kProjectBlock;
-    if (nvalid == kProjectBlock) {
-      float4 v[kPerThread];
-#pragma unroll
-      for (int j = 0; j < kPerThread; ++j) {
-        const int i = threadIdx.x + j * kProjectBlock;
-        if (kVec4 % kProjectBlock == 0 || i < kVec4) v[j] = src4[i];
-      }
-#pragma unroll
-      for (int j = 0; j < kPerThread; ++j) {
-        const int i = threadIdx.x + j * kProjectBlock;
-        if (kVec4 % kProjectBlock == 0 || i < kVec4) {
-          const float vals[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const int e = i * 4 + t;
-            const int g = e / F;
-            coeff[g * S + (e - g * F)] = vals[t];
-          }
-        }
-      }
-    }
-    for (int i = threadIdx.x; nvalid < kProjectBlock && i * 4 < total; i += kProjectBlock) {
-      const int f = i * 4;
-      float vals[4];
-      if (f + 4 <= total) {
-        const float4 v = src4[i];
-        vals[0] = v.x;
-        vals[1] = v.y;
-        vals[2] = v.z;
-        vals[3] = v.w;
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) vals[j] = (f + j < total) ? src[f + j] : 0.0f;
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int e = f + j;
-        if (e < total) {
-          const int g = e / F;
-          coeff[g * S + (e - g * F)] = vals[j];
-        }
-      }
-    }
-  }
+  sh::stage_block<F, kProjectBlock>(a.color + base * F, int(nvalid), coeff);
   __syncthreads();
   if (!have) return;
 

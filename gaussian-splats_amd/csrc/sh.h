@@ -150,5 +150,89 @@ __device__ __forceinline__ void store_coefficients(float* __restrict__ p, const 
   }
 }
 
+// Coefficient blocks staged through LDS: BLOCK Gaussians' F = 3K floats each
+// (contiguous in memory, 16-byte aligned block start) move between memory and
+// LDS rows of stride F + 1 (odd: a wave reading one row per lane hits
+// distinct banks) with coalesced 16-byte accesses.  In a full block every
+// thread issues all of its loads before the first LDS store, so they are in
+// flight together; a partial block (nvalid < BLOCK) takes a guarded loop.
+// Called by all BLOCK threads; the caller synchronises around them.
+template <int F, int BLOCK>
+__device__ __forceinline__ void stage_block(const float* __restrict__ src, int nvalid, float* lds) {
+  constexpr int S = F + 1;
+  constexpr int kVec4 = BLOCK * F / 4;  // F * BLOCK is a multiple of 4 for BLOCK % 4 == 0
+  constexpr int kPerThread = (kVec4 + BLOCK - 1) / BLOCK;
+  const float4* src4 = reinterpret_cast<const float4*>(src);
+  if (nvalid == BLOCK) {
+    float4 v[kPerThread];
+#pragma unroll
+    for (int j = 0; j < kPerThread; ++j) {
+      const int i = threadIdx.x + j * BLOCK;
+      if (kVec4 % BLOCK == 0 || i < kVec4) v[j] = src4[i];
+    }
+#pragma unroll
+    for (int j = 0; j < kPerThread; ++j) {
+      const int i = threadIdx.x + j * BLOCK;
+      if (kVec4 % BLOCK == 0 || i < kVec4) {
+        const float vals[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int e = i * 4 + t;
+          const int g = e / F;
+          lds[g * S + (e - g * F)] = vals[t];
+        }
+      }
+    }
+    return;
+  }
+  const int total = nvalid * F;
+  for (int i = threadIdx.x; i * 4 < total; i += BLOCK) {
+    const int f = i * 4;
+    float vals[4];
+    if (f + 4 <= total) {
+      const float4 v = src4[i];
+      vals[0] = v.x;
+      vals[1] = v.y;
+      vals[2] = v.z;
+      vals[3] = v.w;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) vals[j] = (f + j < total) ? src[f + j] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = f + j;
+      if (e < total) {
+        const int g = e / F;
+        lds[g * S + (e - g * F)] = vals[j];
+      }
+    }
+  }
+}
+
+// The reverse of stage_block: LDS rows to memory with coalesced stores.
+template <int F, int BLOCK>
+__device__ __forceinline__ void unstage_block(float* __restrict__ dst, int nvalid, const float* lds) {
+  constexpr int S = F + 1;
+  float4* dst4 = reinterpret_cast<float4*>(dst);
+  const int total = nvalid * F;
+  for (int i = threadIdx.x; i * 4 < total; i += BLOCK) {
+    float vals[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int e = i * 4 + t;
+      const int g = e / F;
+      vals[t] = e < total ? lds[g * S + (e - g * F)] : 0.0f;
+    }
+    if (i * 4 + 4 <= total) {
+      dst4[i] = make_float4(vals[0], vals[1], vals[2], vals[3]);
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        if (i * 4 + t < total) dst[i * 4 + t] = vals[t];
+    }
+  }
+}
+
 }  // namespace sh
 }  // namespace gs

@@ -662,6 +662,20 @@ def main():
             entry.update({"algorithmic_bytes": bytes_model[name], "GB/s": round(gbs, 1),
                           "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)})
         stages[name] = entry
+    # The reference bins by sorting I 64-bit (tile, depth) keys with their ids
+    # (intersections.py:77-88): an onesweep LSD sort of 8-bit digits moves
+    # I (8 + 24 P) bytes, P = ceil((31 + ceil(log2 T)) / 8) passes.  This
+    # build's whole binning (plan + row and column bucketing) is timed against
+    # that figure: above 1 it beats the roofline of the sort it replaces.
+    tiles = -(-w // args.tile_size) * -(-h // args.tile_size)
+    passes = -(-(31 + max(1, math.ceil(math.log2(tiles)))) // 8)
+    sort_bytes = info["total"] * (8 + 24 * passes)
+    binning_ms = stages_ms["bin"] + stages_ms["emit"] + stages_ms["sort"]
+    stages["binning_vs_key_sort"] = {
+        "ms": round(binning_ms, 4), "key_sort_bytes": sort_bytes, "passes": passes,
+        "equivalent_GB/s": round(sort_bytes / (binning_ms * 1e-3) / 1e9, 1),
+        "frac_of_key_sort_roofline": round(sort_bytes / (binning_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+    }
 
     # Dominant kernel: composite_bwd_kernel, timed per launch with HIP events
     # on its stream during the timed steps.

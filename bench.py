@@ -379,7 +379,8 @@ def bench_views(args, scene):
         "dtype": "f32",
         "data": "synthetic (seeded scenes.CONFIGS distributions)",
         "config": {
-            "workload": (f"{scene.name}: {scene.num_points} Gaussians, SH3, {views} views of "
+            "workload": (f"{scene.name}: {scene.num_points} Gaussians, "
+                         f"SH{math.isqrt(scene.color.shape[1]) - 1}, {views} views of "
                          f"{w}x{h}, fwd+bwd, L1 loss"),
             "tile_size": tile,
             "path": "rasterize_views (one mosaic)" if kind == "batched" else "rasterize per view",
@@ -738,7 +739,8 @@ def main():
         "dtype": "f32",
         "data": "synthetic (seeded scenes.CONFIGS distributions)",
         "config": {
-            "workload": f"{scene.name}: {scene.num_points} Gaussians, SH3, {w}x{h}, fwd+bwd, L1 loss",
+            "workload": (f"{scene.name}: {scene.num_points} Gaussians, "
+                         f"SH{math.isqrt(scene.color.shape[1]) - 1}, {w}x{h}, fwd+bwd, L1 loss"),
             "tile_size": args.tile_size,
             "intersections": info["total"],
         },

@@ -86,6 +86,13 @@ def copy_calibration():
     print("copied 512 MiB x3", flush=True)
 
 
+def host_extrinsics(cam):
+    """The camera extrinsics the rasterizer passes its kernels (float32, host)."""
+    from gaussian_splats.splats.camera import host_extrinsics as extrinsics
+
+    return extrinsics(cam)
+
+
 def stage_bytes(n, k, total, rows, pixels, processed_fwd, processed_bwd):
     """Algorithmic HBM bytes per stage (n Gaussians with k SH coefficients,
     `total` intersections, `rows` row-list entries)."""
@@ -132,8 +139,7 @@ def staged_step(params, cam, target, tile_size, near, far):
     cx, cy = cam.principal_point
     w, h = cam.image_size
     one = torch.ones((), dtype=torch.float32, device=params[0].device)
-    R = cam.rotation_matrix.float()  # host memory: passed to the kernels by value
-    t = cam.translation.float()
+    R, t = host_extrinsics(cam)  # host memory: passed to the kernels by value
     out = forward_pipeline(*params, R, t, fx, fy, cx, cy, w, h, tile_size, 0.999, near, far,
                            "gaussian", 0.95, timer=mark)
     image, final_t, ncon, pmean, pinv, pcol, pop, gids, ranges, counts = out
@@ -193,7 +199,7 @@ def cpu_baseline(scene, tile_size, sample_tiles):
     fx, fy = cam.focal_length
     cx, cy = cam.principal_point
     w, h = cam.image_size
-    ocam = orc.Camera(cam.rotation_matrix.float(), cam.translation.float(), fx, fy, cx, cy, w, h)
+    ocam = orc.Camera(*host_extrinsics(cam), fx, fy, cx, cy, w, h)
     params = [p.detach().clone().requires_grad_(True) for p in scene.params()]
     t0 = time.perf_counter()
     proj = orc.project(*params, ocam)
@@ -347,7 +353,7 @@ def bench_views(args, scene):
         fx, fy = cam.focal_length
         cx, cy = cam.principal_point
         _, _, _, _, bounds, counts = project_and_count(
-            *params, cam.rotation_matrix.float(), cam.translation.float(), fx, fy, cx, cy, w, h,
+            *params, *host_extrinsics(cam), fx, fy, cx, cy, w, h,
             tile, scene.near, scene.far, "gaussian", 0.95)
         bb = bounds.view(-1, 4).long()
         rows += int(((bb[:, 3] - bb[:, 2]) * (counts > 0)).sum())

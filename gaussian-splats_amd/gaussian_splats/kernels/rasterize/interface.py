@@ -321,16 +321,18 @@ def rasterize(
             opacity[indices],
             color[indices],
         )
-    device = mean.device
+    # Extrinsics stay in host memory: the kernels take them as arguments.
+    from ...splats.camera import host_extrinsics  # the splat API imports this module
+
+    camera_rotation, camera_translation = host_extrinsics(camera)
     return _rasterize(
         mean,
         rotation,
         scale,
         opacity,
         color,
-        # Extrinsics stay in host memory: the kernels take them as arguments.
-        camera.rotation_matrix.detach().to(device="cpu", dtype=torch.float32),
-        camera.translation.detach().to(device="cpu", dtype=torch.float32),
+        camera_rotation,
+        camera_translation,
         float(fx),
         float(fy),
         float(cx),

@@ -397,12 +397,11 @@ def camera_tensors(cameras: Sequence[Camera]) -> tuple[torch.Tensor, torch.Tenso
     if len(sizes) != 1:
         raise ValueError(f"all cameras must share one image size, got {sorted(sizes)}")
     (width, height), = sizes
-    rotations = torch.stack(
-        [cam.rotation_matrix.detach().to(device="cpu", dtype=torch.float32) for cam in cameras]
-    )
-    translations = torch.stack(
-        [cam.translation.detach().to(device="cpu", dtype=torch.float32).reshape(3) for cam in cameras]
-    )
+    from ...splats.camera import host_extrinsics  # the splat API imports this module
+
+    extrinsics = [host_extrinsics(cam) for cam in cameras]
+    rotations = torch.stack([r for r, _ in extrinsics])
+    translations = torch.stack([t for _, t in extrinsics])
     intrinsics = torch.tensor(
         [[float(c) for c in (*cam.focal_length, *cam.principal_point)] for cam in cameras],
         dtype=torch.float32,

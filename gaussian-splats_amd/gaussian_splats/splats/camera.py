@@ -12,6 +12,7 @@ import math
 from abc import ABC
 from dataclasses import dataclass, field
 
+import numpy as np
 import torch
 import torch.nn.functional as F
 from typing_extensions import Self
@@ -113,3 +114,34 @@ class PinholeCamera(Camera):
         return cls(
             rotation=quaternion.float(), translation=translation.float(), **kwargs
         )
+
+
+@torch.compiler.disable  # host arithmetic: runs as it is under torch.compile
+def host_extrinsics(camera: Camera) -> tuple[torch.Tensor, torch.Tensor]:
+    """The world-to-camera rotation matrix [3, 3] and translation [3] as
+    float32 tensors in host memory (the rasterizer passes them to its kernels
+    as arguments).  For a float32 quaternion the matrix is built from numpy
+    float32 scalars with the operations of ``camera.rotation_matrix`` in the
+    same order (F.normalize: sequential sum of squares, sqrt, clamp at 1e-12,
+    divide; then utils.py:8-25), so the values are the same, without the ~25
+    small tensor operations (~0.3 ms of host time per call) of the torch
+    path; other dtypes take the torch path."""
+    q = camera.rotation.detach()
+    t = camera.translation.detach()
+    if q.dtype != torch.float32 or q.numel() != 4:
+        return (camera.rotation_matrix.detach().to(device="cpu", dtype=torch.float32),
+                t.to(device="cpu", dtype=torch.float32).reshape(3))
+    # One device-to-host copy for a camera on the GPU.
+    host = torch.cat((q.reshape(4), t.reshape(3).to(torch.float32))).cpu()
+    t = host[4:].clone()
+    w, x, y, z = (np.float32(v) for v in host[:4].tolist())
+    norm = max(np.sqrt(((w * w + x * x) + y * y) + z * z), np.float32(1e-12))
+    w, x, y, z = w / norm, x / norm, y / norm, z / norm
+    one, two = np.float32(1), np.float32(2)
+    xx, yy, zz = x * x, y * y, z * z
+    rows = [
+        [one - two * (yy + zz), two * (x * y - w * z), two * (x * z + w * y)],
+        [two * (x * y + w * z), one - two * (xx + zz), two * (y * z - w * x)],
+        [two * (x * z - w * y), two * (y * z + w * x), one - two * (xx + yy)],
+    ]
+    return torch.from_numpy(np.array(rows, dtype=np.float32)), t

@@ -19,13 +19,15 @@ MARGIN = 1e-4  # relative distance below which a decision may legitimately flip
 
 
 def oracle_camera(cam) -> orc.Camera:
+    """The oracle's camera with the extrinsics the rasterizer passes its
+    kernels (host_extrinsics: the values of cam.rotation_matrix)."""
+    from gaussian_splats.splats.camera import host_extrinsics
+
     fx, fy = cam.focal_length
     cx, cy = cam.principal_point
     w, h = cam.image_size
-    return orc.Camera(
-        cam.rotation_matrix.detach().cpu().float(), cam.translation.detach().cpu().float(),
-        float(fx), float(fy), float(cx), float(cy), int(w), int(h),
-    )
+    r, t = host_extrinsics(cam)
+    return orc.Camera(r, t, float(fx), float(fy), float(cx), float(cy), int(w), int(h))
 
 
 def assert_close_flip_aware(actual, expected, margin, atol, rtol=0.0, loose=None, max_flagged=0.01, what=""):

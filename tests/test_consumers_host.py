@@ -149,3 +149,24 @@ def test_scene_from_file(tmp_path):
         assert torch.equal(x, y)
     assert torch.equal(a.cameras[0].translation, b.cameras[0].translation)
     assert a.target.shape == (180, 320, 3) and a.cameras[0].image_size == (320, 180)
+
+
+def test_host_extrinsics_equal_the_torch_rotation_matrix():
+    """The rasterizer's host path gives exactly cam.rotation_matrix (float32
+    quaternions of all magnitudes, unnormalised), and falls back to it for
+    float64 quaternions."""
+    from gaussian_splats.splats.camera import host_extrinsics
+
+    g = torch.Generator().manual_seed(11)
+    for i in range(3000):
+        scale = 10.0 ** float(torch.randint(-4, 4, (1,), generator=g))
+        cam = PinholeCamera(rotation=torch.randn(4, generator=g) * scale,
+                            translation=torch.randn(3, generator=g))
+        r, t = host_extrinsics(cam)
+        assert r.dtype == torch.float32 and r.device.type == "cpu"
+        assert torch.equal(r, cam.rotation_matrix.float()), i
+        assert torch.equal(t, cam.translation.float())
+    cam = PinholeCamera(rotation=torch.randn(4, dtype=torch.float64, generator=g),
+                        translation=torch.randn(3, dtype=torch.float64, generator=g))
+    r, t = host_extrinsics(cam)
+    assert torch.equal(r, cam.rotation_matrix.float()) and t.dtype == torch.float32

@@ -287,6 +287,36 @@ torch.library.register_autograd(
 )
 
 
+class _RasterizeFunction(torch.autograd.Function):
+    """The op's forward and backward as an autograd.Function, for eager
+    calls: the same two functions, without the dispatcher's per-call work
+    for a 19-argument custom op (default filling, schema checks), which
+    costs tens of microseconds of host time per step.  Traced code
+    (torch.compile, export) calls the registered op instead."""
+
+    @staticmethod
+    def forward(ctx, *inputs):
+        output = forward_pipeline(*inputs, timer=stage_timer())
+        _setup_context(ctx, inputs, output)
+        return output
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, *grad_outputs):
+        return _backward(ctx, *grad_outputs)
+
+
+def rasterize_outputs(*inputs) -> tuple[torch.Tensor, ...]:
+    """The op's ten outputs for its 19 inputs: the registered op when traced,
+    the equivalent autograd.Function when a gradient will be needed, else the
+    forward alone."""
+    if torch.compiler.is_compiling():
+        return _rasterize(*inputs)
+    if torch.is_grad_enabled() and any(t.requires_grad for t in inputs[:5]):
+        return _RasterizeFunction.apply(*inputs)
+    return forward_pipeline(*inputs, timer=stage_timer())
+
+
 def rasterize(
     splats: GaussianSplat,
     camera: Camera,
@@ -325,7 +355,7 @@ def rasterize(
     from ...splats.camera import host_extrinsics  # the splat API imports this module
 
     camera_rotation, camera_translation = host_extrinsics(camera)
-    return _rasterize(
+    return rasterize_outputs(
         mean,
         rotation,
         scale,

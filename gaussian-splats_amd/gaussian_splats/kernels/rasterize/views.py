@@ -387,6 +387,33 @@ torch.library.register_autograd(
 )
 
 
+class _RasterizeViewsFunction(torch.autograd.Function):
+    """The multi-view op's forward and backward as an autograd.Function for
+    eager calls (see _RasterizeFunction in interface.py)."""
+
+    @staticmethod
+    def forward(ctx, *inputs):
+        output = forward_views(*inputs, timer=stage_timer())
+        _setup_context(ctx, inputs, output)
+        return output
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, *grad_outputs):
+        return _backward(ctx, *grad_outputs)
+
+
+def rasterize_views_outputs(*inputs) -> tuple[torch.Tensor, ...]:
+    """The multi-view op's ten outputs for its 16 inputs: the registered op
+    when traced, the equivalent autograd.Function when a gradient will be
+    needed, else the forward alone."""
+    if torch.compiler.is_compiling():
+        return _rasterize_views(*inputs)
+    if torch.is_grad_enabled() and any(t.requires_grad for t in inputs[:5]):
+        return _RasterizeViewsFunction.apply(*inputs)
+    return forward_views(*inputs, timer=stage_timer())
+
+
 def camera_tensors(cameras: Sequence[Camera]) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, int, int]:
     """Host-side camera arrays of ``rasterize_views``: rotations [V, 3, 3],
     translations [V, 3], intrinsics [V, 4] = (fx, fy, cx, cy), and the shared
@@ -429,7 +456,7 @@ def rasterize_views(
     params = (splats.mean, splats.rotation, splats.scale, splats.opacity, splats.color)
     if indices is not None:
         params = tuple(p[indices] for p in params)
-    return _rasterize_views(
+    return rasterize_views_outputs(
         *params,
         rotations,
         translations,

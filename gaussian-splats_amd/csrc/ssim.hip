@@ -36,6 +36,7 @@ constexpr int kBW = 32, kBH = 16;      // output block
 constexpr int kInW = kBW + 2 * kR;     // 42
 constexpr int kInH = kBH + 2 * kR;     // 26
 constexpr int kSsimThreads = 256;
+constexpr int kStagePer = (kInH * kInW + kSsimThreads - 1) / kSsimThreads;  // staged pixels per thread
 constexpr int kSsimPartials = 65536;   // forward workgroups at most (one partial sum each)
 
 struct SsimWeights {
@@ -52,16 +53,39 @@ __global__ __launch_bounds__(kSsimThreads) void ssim_fwd_kernel(
   __shared__ float red[kSsimThreads / 64];
   const int bx = blockIdx.x * kBW + kR, by = blockIdx.y * kBH + kR;  // first output pixel
   const int64_t plane = int64_t(H) * W * 3;
+  // The block's staged pixels of all three channels are requested at once
+  // (coordinates clamped into the image, values outside replaced by 0), so
+  // the loads are in flight together instead of one round trip per element.
+  float vx[3][kStagePer], vy[3][kStagePer];
+#pragma unroll
+  for (int k = 0; k < kStagePer; ++k) {
+    const int i = threadIdx.x + k * kSsimThreads;
+    const int r = i / kInW, q = i - r * kInW;
+    const int gy = by - kR + r, gx = bx - kR + q;
+    const bool in = i < kInH * kInW && gy < H && gx < W;  // gy, gx >= 0 by construction
+    const int64_t o = (int64_t(min(gy, H - 1)) * W + min(gx, W - 1)) * 3;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      vx[c][k] = x[o + c];
+      vy[c][k] = y[o + c];
+    }
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      if (!in) vx[c][k] = vy[c][k] = 0.0f;
+    }
+  }
   float acc = 0.0f;
+#pragma unroll
   for (int c = 0; c < 3; ++c) {
     __syncthreads();  // the previous channel's LDS reads are done
-    for (int i = threadIdx.x; i < kInH * kInW; i += kSsimThreads) {
-      const int r = i / kInW, q = i - r * kInW;
-      const int gy = by - kR + r, gx = bx - kR + q;
-      const bool in = gy < H && gx < W;  // gy, gx >= 0 by construction
-      const int64_t o = (int64_t(gy) * W + gx) * 3 + c;
-      in_x[r][q] = in ? x[o] : 0.0f;
-      in_y[r][q] = in ? y[o] : 0.0f;
+#pragma unroll
+    for (int k = 0; k < kStagePer; ++k) {
+      const int i = threadIdx.x + k * kSsimThreads;
+      if (i < kInH * kInW) {
+        const int r = i / kInW, q = i - r * kInW;
+        in_x[r][q] = vx[c][k];
+        in_y[r][q] = vy[c][k];
+      }
     }
     __syncthreads();
     // Row pass: the five moments filtered along x for every staged row.
@@ -154,16 +178,54 @@ __global__ __launch_bounds__(kSsimThreads) void ssim_bwd_kernel(
   const int bx = blockIdx.x * kBW, by = blockIdx.y * kBH;
   const int64_t plane = int64_t(H) * W * 3;
   const float scale = grad_out[0] * inv_count;
+  // As in the forward, all of the thread's loads are issued before the first
+  // LDS store: the staged G maps of all channels (coordinates clamped into
+  // the cropped map, values outside it replaced by 0) and its output pixels'
+  // image and target values.
+  float vg[3][3][kStagePer];
+#pragma unroll
+  for (int k = 0; k < kStagePer; ++k) {
+    const int i = threadIdx.x + k * kSsimThreads;
+    const int r = i / kInW, q = i - r * kInW;
+    const int gy = by - kR + r, gx = bx - kR + q;
+    const bool in = i < kInH * kInW && gy >= kR && gy < H - kR && gx >= kR && gx < W - kR;
+    const int64_t o = (int64_t(min(max(gy, kR), H - kR - 1)) * W + min(max(gx, kR), W - kR - 1)) * 3;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+#pragma unroll
+      for (int m = 0; m < 3; ++m) vg[m][c][k] = gmap[m * plane + o + c];
+    }
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+#pragma unroll
+      for (int m = 0; m < 3; ++m)
+        if (!in) vg[m][c][k] = 0.0f;
+    }
+  }
+  constexpr int kOutPer = kBH * kBW / kSsimThreads;  // output pixels per thread
+  float ox[3][kOutPer], oy[3][kOutPer];
+#pragma unroll
+  for (int k = 0; k < kOutPer; ++k) {
+    const int i = threadIdx.x + k * kSsimThreads;
+    const int r = i / kBW, q = i - r * kBW;
+    const int64_t o = (int64_t(min(by + r, H - 1)) * W + min(bx + q, W - 1)) * 3;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      ox[c][k] = x[o + c];
+      oy[c][k] = y[o + c];
+    }
+  }
+#pragma unroll
   for (int c = 0; c < 3; ++c) {
     __syncthreads();
-    for (int i = threadIdx.x; i < kInH * kInW; i += kSsimThreads) {
-      const int r = i / kInW, q = i - r * kInW;
-      const int gy = by - kR + r, gx = bx - kR + q;
-      const bool in = gy >= kR && gy < H - kR && gx >= kR && gx < W - kR;  // cropped map
-      const int64_t o = (int64_t(gy) * W + gx) * 3 + c;
-      in_g[0][r][q] = in ? gmap[o] : 0.0f;
-      in_g[1][r][q] = in ? gmap[plane + o] : 0.0f;
-      in_g[2][r][q] = in ? gmap[2 * plane + o] : 0.0f;
+#pragma unroll
+    for (int k = 0; k < kStagePer; ++k) {
+      const int i = threadIdx.x + k * kSsimThreads;
+      if (i < kInH * kInW) {
+        const int r = i / kInW, q = i - r * kInW;
+#pragma unroll
+        for (int m = 0; m < 3; ++m) in_g[m][r][q] = vg[m][c][k];
+      }
     }
     __syncthreads();
     for (int i = threadIdx.x; i < kInH * kBW; i += kSsimThreads) {
@@ -179,7 +241,9 @@ __global__ __launch_bounds__(kSsimThreads) void ssim_bwd_kernel(
       for (int k = 0; k < 3; ++k) rows[k][r][q] = m[k];
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < kBH * kBW; i += kSsimThreads) {
+#pragma unroll
+    for (int kk = 0; kk < kOutPer; ++kk) {
+      const int i = threadIdx.x + kk * kSsimThreads;
       const int r = i / kBW, q = i - r * kBW;
       const int gy = by + r, gx = bx + q;
       if (gy >= H || gx >= W) continue;
@@ -191,7 +255,7 @@ __global__ __launch_bounds__(kSsimThreads) void ssim_bwd_kernel(
         for (int k = 0; k < 3; ++k) m[k] += w * rows[k][r + t][q];
       }
       const int64_t o = (int64_t(gy) * W + gx) * 3 + c;
-      grad[o] = scale * (m[0] + 2.0f * x[o] * m[1] + y[o] * m[2]);
+      grad[o] = scale * (m[0] + 2.0f * ox[c][kk] * m[1] + oy[c][kk] * m[2]);
     }
   }
 }

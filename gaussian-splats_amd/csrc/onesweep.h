@@ -212,7 +212,6 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
   constexpr int D = 1 << BITS;
   constexpr int kSeg = kTile / 4;  // contiguous elements per wave
   __shared__ uint32_t cnt[4][D];
-  __shared__ uint32_t dstart[D];
   __shared__ uint32_t gofs[D];
   __shared__ uint32_t scratch[4];
   __shared__ int s_block;
@@ -265,22 +264,23 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
     rank_items<BITS, false>(dig, seg_valid, cnt[wid], rank);
   __syncthreads();
 
-  uint32_t tot = 0;
+  uint32_t tot = 0, c0 = 0, c1 = 0, c2 = 0;
   if (threadIdx.x < D) {
-    const uint32_t c0 = cnt[0][threadIdx.x], c1 = cnt[1][threadIdx.x];
-    const uint32_t c2 = cnt[2][threadIdx.x], c3 = cnt[3][threadIdx.x];
-    cnt[0][threadIdx.x] = 0;
-    cnt[1][threadIdx.x] = c0;
-    cnt[2][threadIdx.x] = c0 + c1;
-    cnt[3][threadIdx.x] = c0 + c1 + c2;
-    tot = c0 + c1 + c2 + c3;
+    c0 = cnt[0][threadIdx.x];
+    c1 = cnt[1][threadIdx.x];
+    c2 = cnt[2][threadIdx.x];
+    tot = c0 + c1 + c2 + cnt[3][threadIdx.x];
   }
   uint32_t all;
   const uint32_t local_start = block_exclusive_scan(tot, scratch, all);
   const uint32_t hv = threadIdx.x < D ? hist[threadIdx.x] : 0u;
   const uint32_t digit_base = block_exclusive_scan(hv, scratch, all);
   if (threadIdx.x < D) {
-    dstart[threadIdx.x] = local_start;
+    // Wave w's items of digit d start at cnt[w][d] in the reordered tile.
+    cnt[0][threadIdx.x] = local_start;
+    cnt[1][threadIdx.x] = local_start + c0;
+    cnt[2][threadIdx.x] = local_start + c0 + c1;
+    cnt[3][threadIdx.x] = local_start + c0 + c1 + c2;
     uint64_t* mine = status + int64_t(b) * D + threadIdx.x;
     store_status(mine, (b == 0 ? kFlagPrefix : kFlagAggregate) | uint64_t(tot));
     uint64_t excl = 0;
@@ -288,14 +288,15 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
       excl = look_back(status, D, b, threadIdx.x, err);
       store_status(mine, kFlagPrefix | (excl + tot));
     }
-    gofs[threadIdx.x] = digit_base + uint32_t(excl);
+    // Output position of reordered item j of digit d: gofs[d] + j (mod 2^32).
+    gofs[threadIdx.x] = digit_base + uint32_t(excl) - local_start;
   }
   __syncthreads();
 
 #pragma unroll
   for (int i = 0; i < kItems; ++i) {
     if (full || i * 64 + lane < seg_valid) {
-      const uint32_t pos = dstart[dig[i]] + cnt[wid][dig[i]] + rank[i];
+      const uint32_t pos = cnt[wid][dig[i]] + rank[i];
       skeys[pos] = key[i];
       svals[pos] = val[i];
     }
@@ -305,7 +306,7 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
   for (int j = threadIdx.x; j < nvalid; j += kBlock) {
     const K k = skeys[j];
     const uint32_t d = uint32_t(k >> shift) & (D - 1);
-    const uint32_t o = gofs[d] + uint32_t(j) - dstart[d];
+    const uint32_t o = gofs[d] + uint32_t(j);
     keys_out[o] = k;
     vals_out[o] = svals[j];
   }

@@ -475,7 +475,6 @@ __device__ int64_t wave_last_le(const uint32_t* __restrict__ offs, int64_t lo, i
 template <int BITS, int NV>
 struct BucketLds {
   uint32_t cnt[4][1 << BITS];
-  uint32_t dstart[1 << BITS];
   uint32_t gofs[1 << BITS];
   uint32_t scratch[4];
   int64_t window[2];  // first and last owner of the workgroup's items
@@ -555,21 +554,22 @@ __device__ void place_items(BucketLds<BITS, NV>& sh, const uint32_t (&dig)[kItem
     sweep::rank_items<BITS, false>(dig, seg_valid, sh.cnt[wid], rank);
   __syncthreads();
 
-  uint32_t tot = 0;
+  uint32_t tot = 0, c0 = 0, c1 = 0, c2 = 0;
   if (threadIdx.x < D) {
-    const uint32_t c0 = sh.cnt[0][threadIdx.x], c1 = sh.cnt[1][threadIdx.x];
-    const uint32_t c2 = sh.cnt[2][threadIdx.x], c3 = sh.cnt[3][threadIdx.x];
-    sh.cnt[0][threadIdx.x] = 0;
-    sh.cnt[1][threadIdx.x] = c0;
-    sh.cnt[2][threadIdx.x] = c0 + c1;
-    sh.cnt[3][threadIdx.x] = c0 + c1 + c2;
-    tot = c0 + c1 + c2 + c3;
+    c0 = sh.cnt[0][threadIdx.x];
+    c1 = sh.cnt[1][threadIdx.x];
+    c2 = sh.cnt[2][threadIdx.x];
+    tot = c0 + c1 + c2 + sh.cnt[3][threadIdx.x];
   }
   uint32_t all;
   const uint32_t local_start = block_exclusive_scan(tot, sh.scratch, all);
   if (threadIdx.x < D) {
     const int d = threadIdx.x;
-    sh.dstart[d] = local_start;
+    // Wave w's items of digit d start at cnt[w][d] in the reordered tile.
+    sh.cnt[0][d] = local_start;
+    sh.cnt[1][d] = local_start + c0;
+    sh.cnt[2][d] = local_start + c0 + c1;
+    sh.cnt[3][d] = local_start + c0 + c1 + c2;
     uint64_t* mine = status + int64_t(b) * D + d;
     sweep::store_status(mine,
                         (chain_start ? sweep::kFlagPrefix : sweep::kFlagAggregate) | uint64_t(tot));
@@ -578,7 +578,8 @@ __device__ void place_items(BucketLds<BITS, NV>& sh, const uint32_t (&dig)[kItem
       excl = sweep::look_back(status, D, b, d, err);
       sweep::store_status(mine, sweep::kFlagPrefix | (excl + tot));
     }
-    sh.gofs[d] = base(d) + uint32_t(excl);
+    // Output position of reordered item j of digit d: gofs[d] + j (mod 2^32).
+    sh.gofs[d] = base(d) + uint32_t(excl) - local_start;
   }
   __syncthreads();
 
@@ -586,7 +587,7 @@ __device__ void place_items(BucketLds<BITS, NV>& sh, const uint32_t (&dig)[kItem
   for (int i = 0; i < kItems; ++i) {
     if (i * 64 + lane < seg_valid) {
       const uint32_t d = dig[i];
-      const uint32_t pos = sh.dstart[d] + sh.cnt[wid][d] + rank[i];
+      const uint32_t pos = sh.cnt[wid][d] + rank[i];
       sh.dig[pos] = uint8_t(d);
 #pragma unroll
       for (int v = 0; v < NV; ++v) sh.val[v * kTile + pos] = val[v][i];
@@ -596,7 +597,7 @@ __device__ void place_items(BucketLds<BITS, NV>& sh, const uint32_t (&dig)[kItem
 
   for (int j = threadIdx.x; j < nvalid; j += kBlock) {
     const uint32_t d = sh.dig[j];
-    const uint32_t o = sh.gofs[d] + uint32_t(j) - sh.dstart[d];
+    const uint32_t o = sh.gofs[d] + uint32_t(j);
     if (o < capacity) {  // always true for tables and lists built by this file
 #pragma unroll
       for (int v = 0; v < NV; ++v) out[v][o] = sh.val[v * kTile + j];

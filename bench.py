@@ -88,7 +88,7 @@ def copy_calibration():
 
 def host_extrinsics(cam):
     """The camera extrinsics the rasterizer passes its kernels (float32, host)."""
-    from gaussian_splats.splats.camera import host_extrinsics as extrinsics
+    from gaussian_splats_hip.splats.camera import host_extrinsics as extrinsics
 
     return extrinsics(cam)
 
@@ -113,8 +113,8 @@ def stage_bytes(n, k, total, rows, pixels, processed_fwd, processed_bwd):
 
 
 def run_step(splats, cam, target, tile_size, near, far):
-    from gaussian_splats.splats import rasterize
-    from gaussian_splats.training import l1_loss
+    from gaussian_splats_hip.splats import rasterize
+    from gaussian_splats_hip.training import l1_loss
 
     image = rasterize(splats, cam, tile_size=tile_size, near=near, far=far)
     loss = l1_loss(image, target)  # mean |image - target|, one fused kernel each way
@@ -124,9 +124,9 @@ def run_step(splats, cam, target, tile_size, near, far):
 
 def staged_step(params, cam, target, tile_size, near, far):
     """One fwd+bwd through the stage functions with an event after each stage."""
-    from gaussian_splats.kernels.rasterize import composite_bwd, project_and_count, project_bwd
-    from gaussian_splats.kernels.rasterize.interface import forward_pipeline
-    from gaussian_splats.training import l1_loss_backward, l1_loss_forward
+    from gaussian_splats_hip.kernels.rasterize import composite_bwd, project_and_count, project_bwd
+    from gaussian_splats_hip.kernels.rasterize.interface import forward_pipeline
+    from gaussian_splats_hip.training import l1_loss_backward, l1_loss_forward
 
     events = {}
 
@@ -259,15 +259,15 @@ def bench_views(args, scene):
     [V, H, W, 3] batch with one rasterize_views call (with --view-loop: one
     rasterize call per camera), takes the mean L1 against the per-view targets
     and back-propagates to all parameters."""
-    from gaussian_splats.kernels.rasterize import _native, project_and_count
-    from gaussian_splats.kernels.rasterize.views import (
+    from gaussian_splats_hip.kernels.rasterize import _native, project_and_count
+    from gaussian_splats_hip.kernels.rasterize.views import (
         backward_views,
         camera_tensors,
         forward_views,
         mosaic_columns,
     )
-    from gaussian_splats.splats import GaussianSplat, rasterize, rasterize_views
-    from gaussian_splats.training import l1_loss, l1_loss_backward, l1_loss_forward
+    from gaussian_splats_hip.splats import GaussianSplat, rasterize, rasterize_views
+    from gaussian_splats_hip.training import l1_loss, l1_loss_backward, l1_loss_forward
 
     device = torch.device("cuda:0")
     cams = scene.cameras
@@ -418,8 +418,8 @@ LRS = {"mean": 1.6e-4, "rotation": 1e-3, "scale": 5e-3, "opacity": 5e-2, "color"
 
 
 def train_step_fused(splats, cam, target, tile_size, near, far, optimizer):
-    from gaussian_splats.splats import rasterize
-    from gaussian_splats.training import l1_loss, splat_regularizers, ssim
+    from gaussian_splats_hip.splats import rasterize
+    from gaussian_splats_hip.training import l1_loss, splat_regularizers, ssim
 
     image = rasterize(splats, cam, tile_size=tile_size, near=near, far=far)
     l1 = l1_loss(image, target, clamp=True)
@@ -438,7 +438,7 @@ def train_step_torch(splats, cam, target, tile_size, near, far, optimizer, windo
     torch.optim.Adam."""
     import torch.nn.functional as F
 
-    from gaussian_splats.splats import rasterize
+    from gaussian_splats_hip.splats import rasterize
 
     image = rasterize(splats, cam, tile_size=tile_size, near=near, far=far).clamp(0, 1)
     l1 = (image - target).abs().mean()
@@ -463,10 +463,10 @@ def bench_train_step(args):
     """One JSON line: the reference's training step (config 3) per second with
     the fused kernels, and the same step with torch ops for the loss terms and
     the optimiser."""
-    from gaussian_splats import scenes
-    from gaussian_splats.kernels.rasterize import _native
-    from gaussian_splats.splats import GaussianSplat
-    from gaussian_splats.training import FusedAdam
+    from gaussian_splats_hip import scenes
+    from gaussian_splats_hip.kernels.rasterize import _native
+    from gaussian_splats_hip.splats import GaussianSplat
+    from gaussian_splats_hip.training import FusedAdam
 
     _native.library()
     device = torch.device("cuda:0")
@@ -531,9 +531,9 @@ def bench_ply_io(args):
     the GPU), each beside the host path (numpy records, per-tensor copies)."""
     import tempfile
 
-    from gaussian_splats import scenes
-    from gaussian_splats.kernels.rasterize import _native
-    from gaussian_splats.splats.ply import load_ply, save_ply
+    from gaussian_splats_hip import scenes
+    from gaussian_splats_hip.kernels.rasterize import _native
+    from gaussian_splats_hip.splats.ply import load_ply, save_ply
 
     _native.library()
     device = torch.device("cuda:0")
@@ -609,9 +609,9 @@ def main():
     if args.ply_io:
         bench_ply_io(args)
         return
-    from gaussian_splats import scenes
-    from gaussian_splats.kernels.rasterize import _native
-    from gaussian_splats.splats import GaussianSplat
+    from gaussian_splats_hip import scenes
+    from gaussian_splats_hip.kernels.rasterize import _native
+    from gaussian_splats_hip.splats import GaussianSplat
 
     _native.library()
     device = torch.device("cuda:0")

@@ -20,7 +20,7 @@ REPO_ROOT = PACKAGE_ROOT.parent
 CSRC = PACKAGE_ROOT / "csrc"
 INCLUDE = REPO_ROOT / "include"
 BUILD_DIR = PACKAGE_ROOT / "_build"
-LIB_DIR = PACKAGE_ROOT / "gaussian_splats" / "_lib"
+LIB_DIR = PACKAGE_ROOT / "gaussian_splats_hip" / "_lib"
 LIB_PATH = LIB_DIR / "libgs_raster.so"
 
 ARCH = "gfx950"

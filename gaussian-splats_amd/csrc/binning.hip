@@ -192,8 +192,9 @@ GS_API int gs_scan_counts(const int32_t* counts, int64_t n, int64_t* offsets, vo
     fill_kernel<int64_t><<<1, 64, 0, s>>>(offsets, 1, 0);
     return check_launch("scan_counts");
   }
-  const Scratch ws = carve(workspace, 0, 4, -1, n);
+  Scratch ws = carve(workspace, 0, 4, -1, n);
   GS_REQUIRE(workspace && workspace_bytes >= ws.bytes, GS_ERR_WORKSPACE, "scan workspace too small");
+  GS_TRY(device_flags(s, &ws.flags));
   clear(ws, s);
   launch_scan<int64_t>(sweep::GatherLoad<int32_t, int64_t>{counts, nullptr}, n, offsets, true,
                        aligned_16(counts), ws, s);
@@ -232,9 +233,10 @@ GS_API int gs_sort_intersections(int64_t* keys, int32_t* gaussian_ids, int64_t t
   if (total > 0) {
     GS_REQUIRE(keys && gaussian_ids && sorted_ids, GS_ERR_INVALID_ARGUMENT, "null pointer");
     const int end_bit = 32 + bits_for(num_tiles);
-    const Scratch ws = carve(workspace, total, 8, end_bit, 0);
+    Scratch ws = carve(workspace, total, 8, end_bit, 0);
     GS_REQUIRE(workspace && workspace_bytes >= ws.bytes, GS_ERR_WORKSPACE,
                "sort workspace too small (%zu < %zu)", workspace_bytes, ws.bytes);
+    GS_TRY(device_flags(s, &ws.flags));
     clear(ws, s);
     GS_TRY(radix_sort<uint64_t>(reinterpret_cast<uint64_t*>(keys),
                                 reinterpret_cast<const uint32_t*>(gaussian_ids), total, end_bit,
@@ -261,9 +263,10 @@ GS_API int gs_bin_gaussians(uint32_t* depth_keys, const int32_t* counts, int64_t
     return check_launch("bin_gaussians");
   }
   GS_REQUIRE(depth_keys && counts && order, GS_ERR_INVALID_ARGUMENT, "null pointer");
-  const Scratch ws = carve(workspace, n, 4, 32, n);
+  Scratch ws = carve(workspace, n, 4, 32, n);
   GS_REQUIRE(workspace && workspace_bytes >= ws.bytes, GS_ERR_WORKSPACE,
              "binning workspace too small");
+  GS_TRY(device_flags(s, &ws.flags));
   clear(ws, s);
   // depth_keys is used as a ping-pong buffer by the sort and is consumed.
   uint32_t* sorted_keys = nullptr;
@@ -300,9 +303,10 @@ GS_API int gs_sort_tiles(uint32_t* tile_keys, int32_t* gaussian_ids, int64_t tot
   if (total > 0) {
     GS_REQUIRE(tile_keys && gaussian_ids && sorted_ids, GS_ERR_INVALID_ARGUMENT, "null pointer");
     const int end_bit = bits_for(num_tiles);
-    const Scratch ws = carve(workspace, total, 4, end_bit, 0);
+    Scratch ws = carve(workspace, total, 4, end_bit, 0);
     GS_REQUIRE(workspace && workspace_bytes >= ws.bytes, GS_ERR_WORKSPACE,
                "sort workspace too small");
+    GS_TRY(device_flags(s, &ws.flags));
     clear(ws, s);
     GS_TRY(radix_sort<uint32_t>(tile_keys, reinterpret_cast<const uint32_t*>(gaussian_ids), total,
                                 end_bit, reinterpret_cast<uint32_t*>(sorted_ids), &sorted_keys,

@@ -1,5 +1,6 @@
 // C-ABI bookkeeping: per-thread error text, version, argument validation,
-// and the side streams used to overlap independent stages.
+// the side streams used to overlap independent stages, and the per-device
+// word of device-side check failures.
 #include <cstdarg>
 #include <cstdio>
 #include <mutex>
@@ -69,15 +70,20 @@ SideStream g_side[kMaxDevices];
 std::mutex g_side_mutex;
 }  // namespace
 
-int fork_side_stream(hipStream_t main, SideFork& f) {
-  int device = 0;
-  if (main) {
-    GS_REQUIRE(hipStreamGetDevice(main, &device) == hipSuccess, GS_ERR_HIP,
+int stream_device(hipStream_t stream, int* device) {
+  if (stream) {
+    GS_REQUIRE(hipStreamGetDevice(stream, device) == hipSuccess, GS_ERR_HIP,
                "hipStreamGetDevice failed");
   } else {
-    GS_REQUIRE(hipGetDevice(&device) == hipSuccess, GS_ERR_HIP, "hipGetDevice failed");
+    GS_REQUIRE(hipGetDevice(device) == hipSuccess, GS_ERR_HIP, "hipGetDevice failed");
   }
-  GS_REQUIRE(device >= 0 && device < kMaxDevices, GS_ERR_HIP, "device %d out of range", device);
+  GS_REQUIRE(*device >= 0 && *device < kMaxDevices, GS_ERR_HIP, "device %d out of range", *device);
+  return GS_OK;
+}
+
+int fork_side_stream(hipStream_t main, SideFork& f) {
+  int device = 0;
+  GS_TRY(stream_device(main, &device));
   f.lock = std::unique_lock<std::mutex>(g_side_mutex);
   SideStream& s = g_side[device];
   if (!s.stream) {
@@ -124,9 +130,62 @@ int join_side_stream(SideFork& f, bool host_wait) {
   return GS_OK;
 }
 
+// Sticky word of device-side check failures (kDeviceFlag* bits), one copy
+// per GPU.  Kernels receive its address (device_flags) and set bits with a
+// global atomic OR; the host reads it with gs_device_errors or through the
+// fifth word gs_bin_tiles_plan copies beside its totals.
+static __device__ __align__(16) uint32_t g_device_flags[4];
+namespace {
+uint32_t* g_flags_addr[kMaxDevices] = {};
+std::mutex g_flags_mutex;
+}  // namespace
+
+int device_flags(hipStream_t stream, uint32_t** flags) {
+  int device = 0;
+  GS_TRY(stream_device(stream, &device));
+  std::lock_guard<std::mutex> lock(g_flags_mutex);
+  if (!g_flags_addr[device]) {
+    // Each GPU holds its own copy of the array at its own address: look it up
+    // with that device current.
+    int current = 0;
+    GS_REQUIRE(hipGetDevice(&current) == hipSuccess, GS_ERR_HIP, "hipGetDevice failed");
+    const bool switch_device = current != device;
+    if (switch_device) GS_REQUIRE(hipSetDevice(device) == hipSuccess, GS_ERR_HIP, "hipSetDevice");
+    void* addr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(g_device_flags));
+    if (switch_device) (void)hipSetDevice(current);
+    GS_REQUIRE(e == hipSuccess && addr, GS_ERR_HIP, "device flags lookup failed: %s",
+               hipGetErrorString(e));
+    g_flags_addr[device] = static_cast<uint32_t*>(addr);
+  }
+  *flags = g_flags_addr[device];
+  return GS_OK;
+}
+
 }  // namespace gs
 
 extern "C" {
+
+GS_API int gs_device_errors(uint32_t* flags, int32_t clear, void* stream) {
+  using namespace gs;
+  clear_error();
+  GS_REQUIRE(flags, GS_ERR_INVALID_ARGUMENT, "null pointer argument");
+  hipStream_t s = as_stream(stream);
+  uint32_t* dev = nullptr;
+  GS_TRY(device_flags(s, &dev));
+  // Synchronous by design: the caller asks for the state after its work.
+  GS_REQUIRE(hipMemcpyAsync(flags, dev, sizeof(uint32_t), hipMemcpyDeviceToHost, s) == hipSuccess &&
+                 hipStreamSynchronize(s) == hipSuccess,
+             GS_ERR_HIP, "device_errors: read failed");
+  if (clear && *flags) {
+    const uint32_t zero = 0;
+    GS_REQUIRE(hipMemcpyAsync(dev, &zero, sizeof(uint32_t), hipMemcpyHostToDevice, s) ==
+                       hipSuccess &&
+                   hipStreamSynchronize(s) == hipSuccess,
+               GS_ERR_HIP, "device_errors: clear failed");
+  }
+  return GS_OK;
+}
 
 GS_API int gs_abi_version(void) { return GS_ABI_VERSION; }
 

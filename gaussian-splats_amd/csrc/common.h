@@ -42,6 +42,16 @@ int wait_side_mark(SideFork& f);
 // waits for the side stream's work (not the caller's) before returning.
 int join_side_stream(SideFork& f, bool host_wait = false);
 
+// Device of a stream (the current device for the null stream).
+int stream_device(hipStream_t stream, int* device);
+
+// Address of the stream's device's sticky check-failure word (see
+// gs_device_errors): kernels OR kDeviceFlag* bits into it.
+int device_flags(hipStream_t stream, uint32_t** flags);
+constexpr uint32_t kDeviceFlagSpinLimit = GS_DEVICE_SPIN_LIMIT;
+constexpr uint32_t kDeviceFlagWindow = GS_DEVICE_WINDOW_OVERFLOW;
+constexpr uint32_t kDeviceFlagSizes = GS_DEVICE_SIZE_MISMATCH;
+
 #define GS_REQUIRE(cond, code, ...)      \
   do {                                   \
     if (!(cond)) {                       \

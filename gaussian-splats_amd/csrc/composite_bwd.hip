@@ -31,6 +31,7 @@ struct CompositeBwdArgs {
   const float* pinv;
   const float* pcolor;
   const float* popacity;
+  uint32_t max_id;  // last valid Gaussian index: every gathered id is clamped to it
   const int32_t* ids;
   const int64_t* ranges;
   const int32_t* order;  // tile dispatch order, or nullptr for the identity
@@ -122,7 +123,7 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_bwd_kernel(Com
     int gid = 0;
     uint32_t bands = 0;  // bit k: the Gaussian can reach a pixel of band k
     if (e >= start) {
-      gid = a.ids[e];
+      gid = int(min(uint32_t(a.ids[e]), a.max_id));
       const GsRecord rec = load_projected(a.pmean, a.pinv, a.pcolor, a.popacity, gid);
 #pragma unroll
       for (int k = 0; k < PIX; ++k) {
@@ -259,7 +260,7 @@ using namespace gs;
 extern "C" GS_API int gs_composite_bwd(const float* projected_mean,
                                        const float* inverse_covariance,
                                        const float* projected_color,
-                                       const float* projected_opacity,
+                                       const float* projected_opacity, int64_t n,
                                        const int32_t* gaussian_ids, const int64_t* ranges,
                                        const float* grad_image, const float* final_transmittance,
                                        const int32_t* n_contributors, const int32_t* tile_order,
@@ -273,7 +274,13 @@ extern "C" GS_API int gs_composite_bwd(const float* projected_mean,
              GS_ERR_INVALID_ARGUMENT, "null pointer argument");
   GS_REQUIRE((reinterpret_cast<uintptr_t>(inverse_covariance) & 15u) == 0,
              GS_ERR_INVALID_ARGUMENT, "inverse_covariance must be 16-byte aligned");
+  GS_REQUIRE(n >= 0 && n <= (int64_t(1) << 31), GS_ERR_INVALID_ARGUMENT,
+             "invalid Gaussian count %lld", (long long)n);
+  GS_REQUIRE(n == 0 || (projected_mean && inverse_covariance && projected_color &&
+                        projected_opacity),
+             GS_ERR_INVALID_ARGUMENT, "null pointer argument");
   CompositeBwdArgs a;
+  a.max_id = uint32_t(n > 0 ? n - 1 : 0);
   a.pmean = projected_mean;
   a.pinv = inverse_covariance;
   a.pcolor = projected_color;

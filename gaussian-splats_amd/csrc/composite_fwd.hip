@@ -23,6 +23,7 @@ namespace {
 
 struct CompositeArgs {
   const GsRecord* records;
+  uint32_t max_id;  // last valid record index: every gathered id is clamped to it
   const int32_t* ids;
   const int64_t* ranges;
   const int32_t* order;  // tile dispatch order, or nullptr for the identity
@@ -111,7 +112,7 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_fwd_kernel(Com
     LaneSplat mine;
     bool keep = false;
     if (e < end) {
-      const GsRecord rec = load_record(a.records, a.ids[e]);
+      const GsRecord rec = load_record(a.records, min(uint32_t(a.ids[e]), a.max_id));
       keep = touches_rect(rec, rx0, rx1, ry0, ry1);
       mine = lane_splat(rec);
     }
@@ -199,18 +200,23 @@ void launch(const CompositeArgs& a, int active_tiles, bool ellipsoid, hipStream_
 
 using namespace gs;
 
-extern "C" GS_API int gs_composite(const void* records, const int32_t* gaussian_ids,
-                                   const int64_t* ranges, const int32_t* tile_order,
-                                   gs_view view, float* image, float* final_transmittance,
-                                   int32_t* n_contributors, void* stream) {
+extern "C" GS_API int gs_composite(const void* records, int64_t num_records,
+                                   const int32_t* gaussian_ids, const int64_t* ranges,
+                                   const int32_t* tile_order, gs_view view, float* image,
+                                   float* final_transmittance, int32_t* n_contributors,
+                                   void* stream) {
   clear_error();
   GS_TRY(check_view(view, true));
   GS_REQUIRE(ranges && image && final_transmittance && n_contributors, GS_ERR_INVALID_ARGUMENT,
              "null pointer argument");
+  GS_REQUIRE(num_records >= 0 && num_records <= (int64_t(1) << 31), GS_ERR_INVALID_ARGUMENT,
+             "invalid record count %lld", (long long)num_records);
+  GS_REQUIRE(num_records == 0 || records, GS_ERR_INVALID_ARGUMENT, "null records");
   GS_REQUIRE((reinterpret_cast<uintptr_t>(records) & 15u) == 0, GS_ERR_INVALID_ARGUMENT,
              "records must be 16-byte aligned");
   CompositeArgs a;
   a.records = static_cast<const GsRecord*>(records);
+  a.max_id = uint32_t(num_records > 0 ? num_records - 1 : 0);
   a.ids = gaussian_ids;
   a.ranges = ranges;
   a.order = tile_order;

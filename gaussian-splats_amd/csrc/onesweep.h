@@ -69,7 +69,7 @@ __device__ inline uint64_t look_back(const uint64_t* status, int64_t stride, int
     int spins = 0;
     while ((v >> 62) == 0) {
       if (++spins > kSpinLimit) {
-        atomicOr(err, 1u);
+        atomicOr(err, kDeviceFlagSpinLimit);
         return excl;
       }
       __builtin_amdgcn_s_sleep(2);
@@ -97,7 +97,7 @@ __device__ inline uint64_t wave_look_back(const uint64_t* status, int b, uint32_
     const uint64_t needed = first == 63 ? ~0ull : ((1ull << (first + 1)) - 1);
     if (waiting & needed) {
       if (++spins > kSpinLimit) {
-        if (lane == 0) atomicOr(err, 1u);
+        if (lane == 0) atomicOr(err, kDeviceFlagSpinLimit);
         return excl;
       }
       __builtin_amdgcn_s_sleep(2);

@@ -20,7 +20,8 @@ inline int bits_for(int64_t count) {  // ceil(log2(count)), 0 for count <= 1
 
 // Scratch shared by the sort and the scan: ping-pong buffers, then one zeroed
 // region (look-back status words of every sort pass and of the scan, then the
-// 32-bit histograms, tickets and error flags).
+// 32-bit histograms and tickets).  Check failures go to the device's sticky
+// flags word (`flags`, set by the caller from device_flags).
 struct Scratch {
   void* keys_alt = nullptr;
   uint32_t* vbuf[2] = {nullptr, nullptr};
@@ -28,15 +29,14 @@ struct Scratch {
   uint64_t* scan_status = nullptr;
   uint64_t* zero_begin = nullptr;
   int64_t zero_words = 0;  // 64-bit words of status
-  uint32_t* small = nullptr;  // hist[kMaxPasses*256], tickets[kMaxPasses], err, scan ticket, scan err
+  uint32_t* small = nullptr;  // hist[kMaxPasses*256], tickets[kMaxPasses], scan ticket
   int small_words = 0;
   size_t bytes = 0;
+  uint32_t* flags = nullptr;  // the device's sticky check-failure word
 
   uint32_t* hist() const { return small; }
   uint32_t* tickets() const { return small + sweep::kMaxPasses * 256; }
-  uint32_t* err() const { return tickets() + sweep::kMaxPasses; }
-  uint32_t* scan_ticket() const { return err() + 1; }
-  uint32_t* scan_err() const { return err() + 2; }
+  uint32_t* scan_ticket() const { return tickets() + sweep::kMaxPasses; }
 };
 
 inline int64_t sort_status_words(int64_t n, const sweep::Plan& p) {
@@ -68,7 +68,7 @@ inline Scratch carve(void* ws, int64_t n, int key_bytes, int end_bit, int64_t sc
   s.scan_status = p ? s.zero_begin + sort_words : nullptr;
   s.zero_words = sort_words + scan_words;
   off += align_up(size_t(s.zero_words) * 8);
-  s.small_words = sweep::kMaxPasses * 256 + sweep::kMaxPasses + 3;
+  s.small_words = sweep::kMaxPasses * 256 + sweep::kMaxPasses + 1;
   s.small = p ? reinterpret_cast<uint32_t*>(p + off) : nullptr;
   off += align_up(size_t(s.small_words) * 4);
   s.bytes = off;
@@ -128,7 +128,7 @@ int radix_sort(K* keys, const uint32_t* vals, int64_t n, int end_bit, uint32_t* 
     K* kout = kbuf[pass & 1];
     uint32_t* vout = (pass == plan.passes - 1) ? vals_final : ws.vbuf[pass & 1];
     dispatch_scatter<K>(plan.bits[pass], kin, vin, kout, vout, n, plan.shift[pass],
-                        ws.hist() + pass * 256, status, ws.tickets() + pass, ws.err(), s);
+                        ws.hist() + pass * 256, status, ws.tickets() + pass, ws.flags, s);
     status += nblocks << plan.bits[pass];
     kin = kout;
     vin = vout;
@@ -143,7 +143,7 @@ void launch_scan(Load load, int64_t n, Out* out, bool write_total, bool vec, con
                  hipStream_t s, Sink sink = Sink{}) {
   vec = vec && (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
   sweep::scan_kernel<Out, Load, Sink><<<unsigned(ceil_div(n, kTile)), sweep::kBlock, 0, s>>>(
-      load, n, out, write_total, vec, ws.scan_status, ws.scan_ticket(), ws.scan_err(), sink);
+      load, n, out, write_total, vec, ws.scan_status, ws.scan_ticket(), ws.flags, sink);
 }
 
 inline bool aligned_16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }

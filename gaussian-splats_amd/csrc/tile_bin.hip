@@ -613,7 +613,7 @@ __device__ void place_items(BucketLds<BITS, NV>& sh, const uint32_t (&dig)[kItem
 __device__ int load_window(const uint32_t* __restrict__ offs, int64_t first, int64_t last,
                            uint32_t c0, int32_t* rel, uint32_t* err) {
   const int64_t span = last - first + 1;
-  if (span > kTile && threadIdx.x == 0) atomicOr(err, 2u);
+  if (span > kTile && threadIdx.x == 0) atomicOr(err, kDeviceFlagWindow);
   const int m = int(min(max(span, int64_t(1)), int64_t(kTile)));
   // All of the thread's loads are issued before the first store (indices
   // clamped into the window, so every load is in bounds).
@@ -651,7 +651,7 @@ __global__ __launch_bounds__(kBlock) void row_bucket_kernel(
   // Sizes from the host must be the plan's; otherwise every workgroup leaves
   // (none waits on another) and the error flag is set.
   if (totals[1] != int64_t(entries) || offs[n] != entries) {
-    if (threadIdx.x == 0) atomicOr(err, 1u);
+    if (threadIdx.x == 0) atomicOr(err, kDeviceFlagSizes);
     return;
   }
   if (threadIdx.x == 0) sh.block = int(atomicAdd(ticket, 1u));
@@ -724,7 +724,7 @@ __global__ __launch_bounds__(kBlock) void column_bucket_kernel(
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
   if (totals[0] != total || totals[1] != entries || totals[2] != blocks) {
-    if (threadIdx.x == 0) atomicOr(err, 1u);
+    if (threadIdx.x == 0) atomicOr(err, kDeviceFlagSizes);
     return;
   }
   if (threadIdx.x == 0) sh.block = int(atomicAdd(ticket, 1u));
@@ -932,6 +932,8 @@ GS_API int gs_bin_tiles_plan(uint32_t* depth_keys, const int32_t* bounds, const 
   GS_REQUIRE(plan_bytes >= p.bytes, GS_ERR_WORKSPACE, "plan workspace too small (%zu < %zu)",
              plan_bytes, p.bytes);
   hipStream_t s = as_stream(stream);
+  uint32_t* flags = nullptr;
+  GS_TRY(device_flags(s, &flags));
   // The tile tables need only the rectangles: they run on the side stream
   // while the depth sort and the row-list offset scan run on the caller's.
   SideFork fork;
@@ -969,14 +971,19 @@ GS_API int gs_bin_tiles_plan(uint32_t* depth_keys, const int32_t* bounds, const 
                                                    ranges, p.row_a, p.row_e, p.row_blk, totals);
   }
   if (status == GS_OK) status = check_launch("bin_tiles_plan (tables)");
+  // The totals, then the sticky check-failure word beside them (its low
+  // half; the caller keeps the high half zero).
   if (host_totals && status == GS_OK &&
-      hipMemcpyAsync(host_totals, totals, 4 * sizeof(int64_t), hipMemcpyDeviceToHost,
-                     fork.side) != hipSuccess) {
+      (hipMemcpyAsync(host_totals, totals, 4 * sizeof(int64_t), hipMemcpyDeviceToHost,
+                      fork.side) != hipSuccess ||
+       hipMemcpyAsync(host_totals + 4, flags, sizeof(uint32_t), hipMemcpyDeviceToHost,
+                      fork.side) != hipSuccess)) {
     set_error("bin_tiles_plan: copy of the totals failed");
     status = GS_ERR_HIP;
   }
   if (n > 0 && status == GS_OK) {
-    const Scratch ws = carve(p.sort_ws, n, 4, 32, n);
+    Scratch ws = carve(p.sort_ws, n, 4, 32, n);
+    ws.flags = flags;
     clear(ws, s);
     // depth_keys is consumed (ping-pong buffer of the sort).
     uint32_t* sorted_keys = nullptr;
@@ -1030,12 +1037,13 @@ GS_API int gs_bin_tiles_emit(int64_t n,
   GS_REQUIRE(workspace_bytes >= e.bytes, GS_ERR_WORKSPACE, "emit workspace too small (%zu < %zu)",
              workspace_bytes, e.bytes);
   hipStream_t s = as_stream(stream);
+  uint32_t* err = nullptr;  // the device's sticky check-failure word
+  GS_TRY(device_flags(s, &err));
   sweep::clear_kernel<<<unsigned(std::max<int64_t>(1, std::min<int64_t>(1024, ceil_div(e.zero_words, kBlock)))),
                         kBlock, 0, s>>>(e.zero, e.zero_words, nullptr, 0);
   uint32_t* ticket_a = e.small;
   uint32_t* ticket_b = e.small + 1;
   uint32_t* ticket_w = e.small + 2;
-  uint32_t* err = e.small + 4;  // err[0] pass A, err[1] pass B, err[2] width scan
   const unsigned blocks_a = unsigned(ceil_div(row_entries, kTile));
   switch (axis_bits(tiles_h)) {
 #define GS_ROW_CASE(B)                                                                          \
@@ -1052,7 +1060,7 @@ GS_API int gs_bin_tiles_emit(int64_t n,
   // Positions of the row-list entries in row-major intersection order,
   // recording each pass-B workgroup's metadata.
   sweep::scan_kernel<uint32_t, WidthLoad, WidthSink><<<blocks_a, sweep::kBlock, 0, s>>>(
-      WidthLoad{e.rl_xw}, row_entries, e.W, false, true, e.scan_status, ticket_w, err + 2,
+      WidthLoad{e.rl_xw}, row_entries, e.W, false, true, e.scan_status, ticket_w, err,
       WidthSink{e.rl_xw, p.row_e, p.row_a, p.row_blk, e.info, uint32_t(tiles_h),
                 uint32_t(blocks)});
   switch (axis_bits(tiles_w)) {
@@ -1060,7 +1068,7 @@ GS_API int gs_bin_tiles_emit(int64_t n,
   case B:                                                                                       \
     launch_column_bucket<B>(unsigned(blocks), e.rl_g, e.rl_xw, e.W, e.info, tiles_w, ranges,    \
                             totals, total, row_entries, blocks, sorted_ids, e.status_b,         \
-                            ticket_b, err + 1, s);                                              \
+                            ticket_b, err, s);                                              \
     break;
     GS_COL_CASE(1) GS_COL_CASE(2) GS_COL_CASE(3) GS_COL_CASE(4)
     GS_COL_CASE(5) GS_COL_CASE(6) GS_COL_CASE(7) GS_COL_CASE(8)

@@ -1,4 +1,4 @@
-"""HIP (gfx950) rasterizer stages and the ``gaussian_splats::rasterize`` op."""
+"""HIP (gfx950) rasterizer stages and the ``gaussian_splats_hip::rasterize`` op."""
 
 from .composite import composite
 from .composite_bwd import composite_bwd

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parents[2] / "_lib" / "libgs_raster.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 GS_OK = 0
 GS_ERR_INVALID_ARGUMENT = 1
@@ -158,12 +158,13 @@ _SIGNATURES = {
         c_int, [c_void_p, c_void_p, GsView, c_void_p, c_void_p, c_size_t, c_void_p]
     ),
     "gs_composite": (
-        c_int, [c_void_p, c_void_p, c_void_p, c_void_p, GsView, c_void_p, c_void_p, c_void_p, c_void_p]
+        c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, GsView] + [c_void_p] * 4
     ),
     "gs_composite_bwd": (
         c_int,
-        [c_void_p] * 10 + [GsView, c_void_p, c_void_p, c_void_p],
+        [c_void_p] * 4 + [c_int64] + [c_void_p] * 6 + [GsView, c_void_p, c_void_p, c_void_p],
     ),
+    "gs_device_errors": (c_int, [c_void_p, c_int32, c_void_p]),
     "gs_project_bwd": (
         c_int,
         [c_void_p] * 5 + [c_int64, c_int32, c_void_p, c_void_p, GsView] + [c_void_p] * 9,
@@ -232,6 +233,39 @@ def library() -> ctypes.CDLL:
                 )
             _lib = lib
     return _lib
+
+
+# Bits of the device's sticky check-failure word (GS_DEVICE_* in gs_raster.h).
+DEVICE_FLAGS = {
+    1: "a look-back wait of a sort or binning pass hit its spin limit",
+    2: "a binning workgroup's owner window exceeded its tile",
+    4: "sizes passed to a binning pass differ from the plan's device totals",
+}
+
+
+def raise_device_flags(flags: int, where: str) -> None:
+    """Raises RuntimeError naming the failed device-side checks in ``flags``."""
+    if flags:
+        what = "; ".join(text for bit, text in DEVICE_FLAGS.items() if flags & bit) or "unknown"
+        raise RuntimeError(
+            f"{where}: a device-side check failed in a binning or sort call on this GPU "
+            f"(flags {flags:#x}: {what}); the intersection lists of that call are incomplete"
+        )
+
+
+def device_errors(device: torch.device, clear: bool = True) -> int:
+    """The device's sticky check-failure word after the work enqueued so far on
+    its current stream (synchronises that stream); cleared when ``clear``."""
+    flags = ctypes.c_uint32(0)
+    check(library().gs_device_errors(ctypes.byref(flags), int(clear), stream(device)),
+          "device_errors")
+    return int(flags.value)
+
+
+def check_device_errors(device: torch.device) -> None:
+    """Raises if a device-side check has failed on ``device`` (and clears the
+    word, so each failure is reported once)."""
+    raise_device_flags(device_errors(device, clear=True), "device check")
 
 
 def check(status: int, what: str) -> None:

@@ -17,7 +17,7 @@ frames rendered ``views_per_call`` at a time as one mosaic by
 compared its torch and Triton backends; neither is part of this build.  Frames
 of the other backends are compared with ``hip``'s; GIFs of the frames and of
 10x their difference, and ``measurements.json``, are written to a timestamped
-directory.  ``python -m gaussian_splats.kernels.rasterize.benchmark --help``.
+directory.  ``python -m gaussian_splats_hip.kernels.rasterize.benchmark --help``.
 """
 
 from __future__ import annotations

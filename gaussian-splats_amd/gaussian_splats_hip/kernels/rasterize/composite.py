@@ -84,7 +84,8 @@ def composite(
     )
     nat.check(
         nat.library().gs_composite(
-            nat.ptr(records), nat.ptr(gaussian_ids), nat.ptr(ranges), nat.ptr(order), view,
+            nat.ptr(records), records.shape[0], nat.ptr(gaussian_ids), nat.ptr(ranges),
+            nat.ptr(order), view,
             nat.ptr(image),
             nat.ptr(final_transmittance), nat.ptr(n_contributors), nat.stream(device),
         ),

@@ -70,7 +70,7 @@ def composite_bwd(
             "composite_bwd",
             lambda: lib.gs_composite_bwd(
                 nat.ptr(projected_mean), nat.ptr(inverse_covariance), nat.ptr(projected_color),
-                nat.ptr(projected_opacity), nat.ptr(gaussian_ids), nat.ptr(ranges),
+                nat.ptr(projected_opacity), n, nat.ptr(gaussian_ids), nat.ptr(ranges),
                 nat.ptr(grad_image), nat.ptr(final_transmittance), nat.ptr(n_contributors),
                 nat.ptr(order), view, nat.ptr(out), nat.ptr(absolute), nat.stream(device),
             ),

@@ -1,4 +1,4 @@
-"""``torch.ops.gaussian_splats.rasterize``: the autograd unit of the HIP rasterizer.
+"""``torch.ops.gaussian_splats_hip.rasterize``: the autograd unit of the HIP rasterizer.
 
 Schema, outputs and autograd contract follow the reference's custom op
 (src/gaussian_splats/kernels/rasterize/interface.py:17-244): 19 inputs, 10
@@ -75,6 +75,7 @@ def forward_pipeline(
         # The one device-to-host read of the path: the intersection total sizes
         # the id buffers (the reference reads counts.sum() at intersections.py:51).
         total = int(offsets[n].item()) if n else 0
+        nat.check_device_errors(device)  # the depth sort and scan, now that the stream is idle
         tile_keys, ids = emit_tiles(bounds, order, offsets, total, tiles_w)
         mark("emit")
         gaussian_ids, ranges = sort_tiles(tile_keys, ids, tiles_w * tiles_h)
@@ -99,7 +100,7 @@ def forward_pipeline(
     )
 
 
-@torch.library.custom_op("gaussian_splats::rasterize", mutates_args=())
+@torch.library.custom_op("gaussian_splats_hip::rasterize", mutates_args=())
 def _rasterize(
     mean: torch.Tensor,
     rotation: torch.Tensor,
@@ -261,8 +262,8 @@ def _backward(ctx, *grad_outputs):
             "composite_bwd",
             lambda: lib.gs_composite_bwd(
                 ptr(projected_mean), ptr(inverse_covariance), ptr(projected_color),
-                ptr(projected_opacity), ptr(gaussian_ids), ptr(ranges), ptr(grad_image),
-                ptr(final_transmittance), ptr(n_contributors), ptr(order),
+                ptr(projected_opacity), projected_mean.shape[0], ptr(gaussian_ids), ptr(ranges),
+                ptr(grad_image), ptr(final_transmittance), ptr(n_contributors), ptr(order),
                 ctx.view_composite, ptr(grad_projected), None, stream,
             ),
         ),
@@ -283,7 +284,7 @@ def _backward(ctx, *grad_outputs):
 
 
 torch.library.register_autograd(
-    "gaussian_splats::rasterize", _backward, setup_context=_setup_context
+    "gaussian_splats_hip::rasterize", _backward, setup_context=_setup_context
 )
 
 

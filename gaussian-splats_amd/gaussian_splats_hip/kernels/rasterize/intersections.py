@@ -44,6 +44,7 @@ def emit_intersections(
     s = nat.stream(device)
     nat.check(lib.gs_scan_counts(nat.ptr(counts), n, nat.ptr(offsets), nat.ptr(ws), ws.numel(), s), "scan_counts")
     total = int(offsets[n].item())
+    nat.check_device_errors(device)  # the scan's look-back, now that the stream is idle
     keys = torch.empty(total, dtype=torch.int64, device=device)
     gaussian_ids = torch.empty(total, dtype=torch.int32, device=device)
     if n and total:
@@ -170,8 +171,9 @@ def bin_tiles(
     totals = torch.empty(4, dtype=torch.int64, device=device)
     # The one device-to-host read of the path: the totals size the id buffer
     # (the reference reads counts.sum() at intersections.py:51).  The call
-    # returns once they are in host_totals, while the depth sort still runs.
-    host_totals = torch.empty(4, dtype=torch.int64, pin_memory=True)
+    # returns once they are in host_totals, while the depth sort still runs;
+    # the fifth word's low half is the device's sticky check-failure word.
+    host_totals = torch.zeros(5, dtype=torch.int64, pin_memory=True)
     nat.check(
         lib.gs_bin_tiles_plan(
             nat.ptr(depth_keys), nat.ptr(bounds), nat.ptr(counts), n, tiles_w, tiles_h,
@@ -181,7 +183,10 @@ def bin_tiles(
         "bin_tiles_plan",
     )
     mark("bin")
-    total, row_entries, blocks, active = host_totals.tolist()
+    total, row_entries, blocks, active, flags = host_totals.tolist()
+    if flags:
+        nat.device_errors(device, clear=True)  # report each failure once
+        nat.raise_device_flags(flags, "bin_tiles")
     nat.set_active_tiles(ranges, active)
     sorted_ids = torch.empty(total, dtype=torch.int32, device=device)
     if total:

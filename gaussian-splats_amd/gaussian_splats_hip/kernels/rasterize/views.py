@@ -1,4 +1,4 @@
-"""``torch.ops.gaussian_splats.rasterize_views``: several cameras in one pass.
+"""``torch.ops.gaussian_splats_hip.rasterize_views``: several cameras in one pass.
 
 No counterpart in the reference, which renders one camera per call of
 ``rasterize`` (src/gaussian_splats/kernels/rasterize/interface.py:247-303) and
@@ -154,6 +154,7 @@ def forward_views(
         order, offsets = bin_gaussians(depth_keys, flat_counts)
         mark("bin")
         total = int(offsets[vn].item()) if vn else 0
+        nat.check_device_errors(device)  # the depth sort and scan, now that the stream is idle
         tile_keys, ids = emit_tiles(flat_bounds, order, offsets, total, canvas_w)
         mark("emit")
         gaussian_ids, ranges = sort_tiles(tile_keys, ids, canvas_w * canvas_h)
@@ -170,7 +171,8 @@ def forward_views(
     )
     nat.check(
         lib.gs_composite(
-            ptr(records), ptr(gaussian_ids), ptr(ranges), None, view, ptr(image),
+            ptr(records), records.shape[0], ptr(gaussian_ids), ptr(ranges), None, view,
+            ptr(image),
             ptr(final_transmittance), ptr(n_contributors), stream,
         ),
         "composite",
@@ -190,7 +192,7 @@ def forward_views(
     )
 
 
-@torch.library.custom_op("gaussian_splats::rasterize_views", mutates_args=())
+@torch.library.custom_op("gaussian_splats_hip::rasterize_views", mutates_args=())
 def _rasterize_views(
     mean: torch.Tensor,
     rotation: torch.Tensor,
@@ -346,8 +348,9 @@ def backward_views(
             "composite_bwd",
             lambda: lib.gs_composite_bwd(
                 ptr(projected_mean), ptr(inverse_covariance), ptr(projected_color),
-                ptr(projected_opacity), ptr(gaussian_ids), ptr(ranges), ptr(grad_image),
-                ptr(final_transmittance), ptr(n_contributors), ptr(order), view,
+                ptr(projected_opacity), projected_mean.numel() // 3, ptr(gaussian_ids),
+                ptr(ranges), ptr(grad_image), ptr(final_transmittance), ptr(n_contributors),
+                ptr(order), view,
                 ptr(grad_projected), None, stream,
             ),
         ),
@@ -383,7 +386,7 @@ def _backward(ctx, *grad_outputs):
 
 
 torch.library.register_autograd(
-    "gaussian_splats::rasterize_views", _backward, setup_context=_setup_context
+    "gaussian_splats_hip::rasterize_views", _backward, setup_context=_setup_context
 )
 
 

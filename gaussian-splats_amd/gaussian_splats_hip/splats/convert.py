@@ -1,7 +1,7 @@
 """Checkpoint <-> PLY conversion commands (reference:
 src/gaussian_splats/splats/convert.py:1-34).
 
-``python -m gaussian_splats.splats.convert pt-to-ply scene.pt [-o scene.ply]``
+``python -m gaussian_splats_hip.splats.convert pt-to-ply scene.pt [-o scene.ply]``
 and ``ply-to-pt scene.ply [-o scene.pt]``.  With ``--device cuda`` the records
 are split or packed on the GPU (``load_ply(..., device=...)``, ``save_ply`` of
 GPU tensors)."""

@@ -18,6 +18,26 @@ import torch
 from ..kernels.rasterize import _native as nat
 
 
+def check_adam_tensors(p: torch.Tensor, grad: torch.Tensor, exp_avg: torch.Tensor,
+                       exp_avg_sq: torch.Tensor) -> None:
+    """The kernel reads ``p.numel()`` float32 values of the gradient and of both
+    moments and writes the moments: each must be a contiguous float32 tensor of
+    that size on the parameter's device.  torch.optim.Adam raises on a
+    mismatched state too (in its elementwise ops); here a mismatch would be an
+    out-of-bounds device access, so it is refused before the launch."""
+    for name, t in (("grad", grad), ("exp_avg", exp_avg), ("exp_avg_sq", exp_avg_sq)):
+        if t.dtype != torch.float32:
+            raise TypeError(f"FusedAdam: {name} is {t.dtype}, expected torch.float32")
+        if t.device != p.device:
+            raise ValueError(f"FusedAdam: {name} is on {t.device}, the parameter on {p.device}")
+        if t.numel() != p.numel():
+            raise ValueError(
+                f"FusedAdam: {name} has {t.numel()} elements, the parameter {p.numel()}"
+            )
+        if not t.is_contiguous():
+            raise ValueError(f"FusedAdam: {name} is not contiguous")
+
+
 class FusedAdam(torch.optim.Adam):
     def __init__(self, params, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.0,
                  amsgrad=False, *, maximize=False):
@@ -35,6 +55,10 @@ class FusedAdam(torch.optim.Adam):
         # Tensors of every group that share betas, eps and weight decay go into
         # one launch (the learning rate is per tensor).
         batches: dict[tuple, list] = {}
+        # Every tensor whose address a launch receives stays referenced until
+        # all launches are enqueued (a contiguous copy of a gradient would
+        # otherwise return to the caching allocator before the kernel runs).
+        keep_alive: list[torch.Tensor] = []
         device = None
         for group in self.param_groups:
             beta1, beta2 = group["betas"]
@@ -57,11 +81,13 @@ class FusedAdam(torch.optim.Adam):
                     state["step"] = torch.tensor(0.0, dtype=torch.float32)
                     state["exp_avg"] = torch.zeros_like(p, memory_format=torch.preserve_format)
                     state["exp_avg_sq"] = torch.zeros_like(p, memory_format=torch.preserve_format)
-                state["step"] += 1
                 grad = p.grad if p.grad.is_contiguous() else p.grad.contiguous()
                 for name in ("exp_avg", "exp_avg_sq"):
                     if not state[name].is_contiguous():
                         state[name] = state[name].contiguous()
+                check_adam_tensors(p, grad, state["exp_avg"], state["exp_avg_sq"])
+                state["step"] += 1
+                keep_alive += (p, grad, state["exp_avg"], state["exp_avg_sq"])
                 batches.setdefault(key, []).append(nat.GsAdamTensor(
                     p.data_ptr(), grad.data_ptr(), state["exp_avg"].data_ptr(),
                     state["exp_avg_sq"].data_ptr(), p.numel(), float(group["lr"]),
@@ -77,4 +103,5 @@ class FusedAdam(torch.optim.Adam):
                                      eps, weight_decay, nat.stream(device)),
                     "adam_step",
                 )
+        del keep_alive  # the launches are enqueued; the stream orders any reuse
         return loss

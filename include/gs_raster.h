@@ -42,7 +42,7 @@ extern "C" {
 
 #define GS_API __attribute__((visibility("default")))
 
-#define GS_ABI_VERSION 6
+#define GS_ABI_VERSION 7
 
 typedef enum gs_status {
   GS_OK = 0,
@@ -91,6 +91,22 @@ GS_API int gs_abi_version(void);
 
 /* Message describing the last failure on the calling thread ("" if none). */
 GS_API const char* gs_last_error(void);
+
+/* Device-side check failures.  The binning and sort kernels validate what
+ * they cannot check on the host (sizes passed between calls against the
+ * plan's device totals, the bounded spin of their look-back waits, owner
+ * windows) and, on a failure, leave their outputs incomplete and OR one of
+ * these bits into a sticky word kept per GPU.  No counterpart in the
+ * reference (its torch.sort and Triton kernels have no device-side checks). */
+#define GS_DEVICE_SPIN_LIMIT 1u       /* a look-back wait hit its spin limit */
+#define GS_DEVICE_WINDOW_OVERFLOW 2u  /* a workgroup's owner window exceeded its tile */
+#define GS_DEVICE_SIZE_MISMATCH 4u    /* sizes passed by the host differ from the plan's */
+
+/* Reads the sticky word of the stream's GPU into *flags after the work
+ * enqueued on `stream` so far has completed (this call synchronises the
+ * stream), and clears it when `clear` != 0.  gs_bin_tiles_plan also copies
+ * the word (as of its copy of the totals) to host_totals[4]. */
+GS_API int gs_device_errors(uint32_t* flags, int32_t clear, void* stream);
 
 /* Projection, SH colour, tile rectangle and culled count for N Gaussians.
  * Replaces project_and_count (src/gaussian_splats/kernels/rasterize/
@@ -204,10 +220,14 @@ GS_API int gs_sort_tiles(
  *
  * gs_bin_tiles_plan: depth order, per-tile counts and `ranges` [T, 2] (final),
  * and device `totals` = {intersections, row-list entries, pass-B workgroups,
- * 0}, which size the ids.  With `host_totals` (4 x int64, pinned host memory
- * for an asynchronous copy) the call returns once they have been copied
- * there: the tables are built on a side stream, so the host waits for them
- * while the depth sort still runs on `stream`.  `plan` (plan_bytes from
+ * tiles with a non-empty list}, which size the ids.  With `host_totals`
+ * (5 x int64, pinned host memory for an asynchronous copy) the call returns
+ * once the four totals have been copied there, and the low 32 bits of
+ * host_totals[4] hold the device's sticky check-failure word (see
+ * gs_device_errors) as of that copy: non-zero means an earlier binning or
+ * sort call on this GPU left incomplete output.  The tables are built on a
+ * side stream, so the host waits for them while the depth sort still runs on
+ * `stream`.  `plan` (plan_bytes from
  * gs_bin_tiles_plan_bytes) must stay alive until gs_bin_tiles_emit, which
  * takes the totals (device pointer and the values read from it) and writes
  * `sorted_ids` [totals[0]].  depth_keys (as
@@ -242,15 +262,18 @@ GS_API int gs_tile_order(
 /* Front-to-back compositing per tile.  Replaces composite
  * (src/gaussian_splats/kernels/rasterize/composite.py:25-162) with the
  * pixel semantics of torch.py:172-225.  tile_size in {4, 8, 16, 32}.
- * tile_order (optional, from gs_tile_order) only changes the dispatch
- * order. */
+ * `records` holds num_records records; list ids are clamped to
+ * [0, num_records), so incomplete lists (see gs_device_errors) never read
+ * outside it.  tile_order (optional, from gs_tile_order) only changes the
+ * dispatch order. */
 GS_API int gs_composite(
-    const void* records, const int32_t* gaussian_ids, const int64_t* ranges,
-    const int32_t* tile_order, gs_view view, float* image,
+    const void* records, int64_t num_records, const int32_t* gaussian_ids,
+    const int64_t* ranges, const int32_t* tile_order, gs_view view, float* image,
     float* final_transmittance, int32_t* n_contributors, void* stream);
 
 /* Back-to-front compositing gradient, accumulated with atomics into
- * grad_projected[N,9] (zeroed by the caller), from the op's projected outputs.
+ * grad_projected[N,9] (zeroed by the caller), from the op's projected outputs
+ * of n Gaussians (list ids clamped to [0, n), as in gs_composite).
  * grad_absolute (optional, [N,2], zeroed by the caller) receives the sums of
  * the absolute per-pixel terms of the mean gradient, as composite_bwd.py's
  * return_absolute output (composite_bwd.py:180-185,194-195,272-277).
@@ -258,7 +281,7 @@ GS_API int gs_composite(
  * the forward. */
 GS_API int gs_composite_bwd(
     const float* projected_mean, const float* inverse_covariance,
-    const float* projected_color, const float* projected_opacity,
+    const float* projected_color, const float* projected_opacity, int64_t n,
     const int32_t* gaussian_ids, const int64_t* ranges,
     const float* grad_image, const float* final_transmittance,
     const int32_t* n_contributors, const int32_t* tile_order, gs_view view,

@@ -1,7 +1,7 @@
 """CPU restatement of the scene file format — TEST INFRASTRUCTURE ONLY.
 
 Only ``tests/`` may import this module, and only as the checker of
-``gaussian_splats.splats.ply`` (host parse, GPU record split and pack).
+``gaussian_splats_hip.splats.ply`` (host parse, GPU record split and pack).
 
 Restates src/gaussian_splats/splats/ply.py: ``save_ply`` (ply.py:12-52) writes
 one binary little-endian PLY ``vertex`` element of float32 properties x y z nx

@@ -244,6 +244,13 @@ class Composite:
     margin: torch.Tensor  # [H, W] smallest relative distance of a discrete decision
     clamp_margin: torch.Tensor  # [H, W] smallest relative distance of o*G from 0.99
     gaussian_margin: torch.Tensor  # [N] smallest margin over the pixels a Gaussian reaches
+    # [N] as gaussian_margin, counting only the alpha cut and the 0.99 clamp
+    # (the decisions a float32 run fixes for a replay; the activity test is
+    # fixed separately by active_counts).
+    gaussian_cut_margin: torch.Tensor
+    # Per chunk start tile: (keep, clamped) booleans [entries, pixels] of the
+    # alpha cut (alpha >= 1/255 after the clamp) and of the 0.99 clamp.
+    decisions: dict
 
 
 def composite(
@@ -264,8 +271,20 @@ def composite(
     confidence: float = 0.95,
     tile_chunk: int = 64,
     probe: list | None = None,
+    decisions: dict | None = None,
+    active_counts: np.ndarray | None = None,
 ) -> Composite:
     """Dense per-(entry, pixel) compositing of each tile list (torch.py:172-225).
+
+    Fixed decisions: ``decisions`` (the ``decisions`` of an earlier call over
+    the same lists and ``tile_chunk``, e.g. a float32 run) replaces the alpha
+    cut and the 0.99 clamp of every (entry, pixel) by that run's outcome, and
+    ``active_counts`` ([H, W], e.g. another implementation's n_contributors)
+    makes entry k of a pixel's list active iff k < active_counts[pixel].  The
+    result is then the exact-arithmetic value (in float64) of a compositor
+    that took those discrete decisions, differentiable as before: with both,
+    a float64 run's gradients are what a float32 implementation deciding like
+    that should produce up to its rounding.  Gaussian mode only.
 
     With ``probe`` (a list), every chunk appends ``(g, du, dv)``: zero leaves
     of shape [entries, pixels] added to the means inside the quadratic form, so
@@ -294,6 +313,15 @@ def composite(
     ids_t = torch.as_tensor(ids, dtype=torch.int64)
     cutoff = -2 * math.log1p(-confidence)
     gmargin = torch.full((u.shape[0],), math.inf, dtype=torch.float64)
+    gcmargin = torch.full((u.shape[0],), math.inf, dtype=torch.float64)
+    if (decisions is not None or active_counts is not None) and rendering_mode != "gaussian":
+        raise ValueError("fixed decisions apply to the gaussian rendering mode")
+    if active_counts is not None:
+        ac = np.zeros((tiles_h * tile_size, tiles_w * tile_size), dtype=np.int64)
+        ac[:height, :width] = np.asarray(active_counts)
+        ac = ac.reshape(tiles_h, tile_size, tiles_w, tile_size).transpose(0, 2, 1, 3)
+        active_tiles = torch.as_tensor(ac.reshape(num_tiles, P))
+    recorded = {}
     parts = []
     for t0 in range(0, num_tiles, tile_chunk):
         t1 = min(num_tiles, t0 + tile_chunk)
@@ -325,18 +353,29 @@ def composite(
         else:
             prob = torch.exp(-0.5 * D)
         raw = alpha0[g][:, None] * prob
-        alpha = raw.clamp_max(MAX_ALPHA)
-        alpha = torch.where(alpha >= MIN_ALPHA, alpha, torch.zeros_like(alpha))
+        if decisions is not None:
+            keep, clamped = decisions[t0]
+            alpha = torch.where(clamped, torch.full_like(raw, MAX_ALPHA), raw)
+            alpha = torch.where(keep, alpha, torch.zeros_like(alpha))
+        else:
+            alpha = raw.clamp_max(MAX_ALPHA)
+            alpha = torch.where(alpha >= MIN_ALPHA, alpha, torch.zeros_like(alpha))
+            with torch.no_grad():
+                recorded[t0] = (alpha > 0, raw > MAX_ALPHA)
         log_survival = torch.log1p(-alpha)
         # Segmented exclusive sum per tile, in float64 (torch.py:209-212).
         cums = log_survival.to(torch.float64).cumsum(0) - log_survival.to(torch.float64)
         seg_start = torch.as_tensor(np.repeat(np.cumsum(counts) - counts, counts), dtype=torch.int64)
         cums = cums - cums[seg_start]
         T = torch.exp(cums).to(dt)
-        active = (1 - T) < opacity_threshold
+        rel = tile_of - t0
+        if active_counts is not None:
+            pos_in_tile = torch.arange(hi - lo) - seg_start
+            active = pos_in_tile[:, None] < active_tiles[tile_of]
+        else:
+            active = (1 - T) < opacity_threshold
         weights = T * alpha * active
         contrib = weights[..., None] * rgb[g][:, None, :]
-        rel = tile_of - t0
         parts.append((t0, t1, torch.zeros(t1 - t0, P, 3, dtype=dt).index_add(0, rel, contrib)))
         with torch.no_grad():
             n_active = torch.zeros(t1 - t0, P, dtype=torch.int64).index_add(0, rel, active.long())
@@ -373,6 +412,12 @@ def composite(
             reach = considered & (alpha.detach() > 0)
             per_entry = torch.where(reach, torch.minimum(mm[rel], m_cl), torch.full_like(m_cl, math.inf))
             gmargin.index_reduce_(0, g, per_entry.amin(1), "amin")
+            # The same with the cut and clamp decisions only.
+            m_cc = torch.where(considered, torch.minimum(m_cut, m_cl), torch.full_like(m_cl, math.inf))
+            pc = torch.full((t1 - t0, P), math.inf, dtype=torch.float64)
+            pc.index_reduce_(0, rel, m_cc, "amin")
+            per_entry = torch.where(reach, torch.minimum(pc[rel], m_cl), torch.full_like(m_cl, math.inf))
+            gcmargin.index_reduce_(0, g, per_entry.amin(1), "amin")
     for t0, t1, img in parts:
         image = image.index_add(0, torch.arange(t0, t1), img)
 
@@ -388,6 +433,8 @@ def composite(
         to_image(margin),
         to_image(cmargin),
         gmargin,
+        gcmargin,
+        decisions if decisions is not None else recorded,
     )
 
 
@@ -418,19 +465,31 @@ def rasterize(
     confidence: float = 0.95,
     covariance_epsilon: float = 0.03,
     tile_chunk: int = 64,
+    lists: tuple[np.ndarray, np.ndarray] | None = None,
+    decisions: dict | None = None,
+    active_counts: np.ndarray | None = None,
 ) -> Render:
-    """project -> cull/rect -> emit -> stable sort -> composite (torch.py:228-247)."""
+    """project -> cull/rect -> emit -> stable sort -> composite (torch.py:228-247).
+
+    ``lists`` = (sorted ids, ranges) composites those lists instead of the
+    ones binned here (sorted_keys is then None); ``decisions`` and
+    ``active_counts`` are passed to :func:`composite`."""
     proj = project(mean, rotation, scale, opacity, color, cam, covariance_epsilon)
     tiles_w = -(-cam.width // tile_size)
     tiles_h = -(-cam.height // tile_size)
     bounds, counts = tile_counts(proj, tile_size, tiles_w, tiles_h, near, far, rendering_mode, confidence)
-    depth32 = proj.mean[:, 2].detach().to(torch.float32).numpy()
-    keys, ids = emit_intersections(bounds, depth32, counts, tiles_w)
-    sorted_ids, ranges, sorted_keys = sort_intersections(keys, ids, tiles_w * tiles_h)
+    if lists is None:
+        depth32 = proj.mean[:, 2].detach().to(torch.float32).numpy()
+        keys, ids = emit_intersections(bounds, depth32, counts, tiles_w)
+        sorted_ids, ranges, sorted_keys = sort_intersections(keys, ids, tiles_w * tiles_h)
+    else:
+        sorted_ids, ranges = (np.asarray(x) for x in lists)
+        sorted_keys = None
     comp = composite(
         proj.mean[:, 0], proj.mean[:, 1], proj.inverse[:, 0, 0], proj.inverse[:, 0, 1],
         proj.inverse[:, 1, 1], proj.color, proj.opacity[:, 0], sorted_ids, ranges, cam.width,
         cam.height, tile_size, opacity_threshold, rendering_mode, confidence, tile_chunk,
+        decisions=decisions, active_counts=active_counts,
     )
     return Render(comp.image, proj, bounds, counts, sorted_ids, ranges, sorted_keys, comp)
 

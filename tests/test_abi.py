@@ -12,7 +12,7 @@ from pathlib import Path
 import pytest
 import torch
 
-from gaussian_splats.kernels.rasterize import _native as nat
+from gaussian_splats_hip.kernels.rasterize import _native as nat
 
 HEADER = Path(__file__).resolve().parents[1] / "include" / "gs_raster.h"
 
@@ -102,7 +102,7 @@ def test_adam_and_regularizer_host_checks():
 
 
 def test_l1_loss_python_checks():
-    from gaussian_splats.training import l1_loss
+    from gaussian_splats_hip.training import l1_loss
 
     x = torch.zeros(4, 4, 3)
     with pytest.raises(ValueError, match="ROCm GPU"):
@@ -157,14 +157,14 @@ def test_project_rejects_unsupported_sh_before_launch():
 def test_invalid_tile_sizes(tile):
     lib = nat.library()
     fake = ctypes.c_void_p(16)
-    status = lib.gs_composite(fake, fake, fake, None, _view(tile_size=tile), fake, fake, fake, None)
+    status = lib.gs_composite(fake, 10, fake, fake, None, _view(tile_size=tile), fake, fake, fake, None)
     assert status in (nat.GS_ERR_INVALID_ARGUMENT, nat.GS_ERR_UNSUPPORTED)
 
 
 def test_backward_rejects_ellipsoid_mode():
     lib = nat.library()
     fake = ctypes.c_void_p(16)
-    status = lib.gs_composite_bwd(*([fake] * 9), None,
+    status = lib.gs_composite_bwd(*([fake] * 4), 10, *([fake] * 5), None,
                                   _view(rendering_mode="ellipsoid"), fake, None, None)
     assert status == nat.GS_ERR_UNSUPPORTED
     assert b"Gaussian rendering" in lib.gs_last_error()
@@ -183,7 +183,7 @@ def test_misaligned_buffers_rejected():
 def test_status_codes_map_to_python_exceptions():
     lib = nat.library()
     fake = ctypes.c_void_p(16)
-    status = lib.gs_composite_bwd(*([fake] * 9), None, _view(rendering_mode="ellipsoid"), fake, None,
+    status = lib.gs_composite_bwd(*([fake] * 4), 10, *([fake] * 5), None, _view(rendering_mode="ellipsoid"), fake, None,
                                   None)
     with pytest.raises(NotImplementedError):
         nat.check(status, "composite_bwd")
@@ -191,8 +191,8 @@ def test_status_codes_map_to_python_exceptions():
 
 def test_cpu_tensors_are_rejected():
     """The product path has no CPU fallback: host tensors raise before any launch."""
-    from gaussian_splats.scenes import edge_case_scene
-    from gaussian_splats.splats import GaussianSplat, rasterize
+    from gaussian_splats_hip.scenes import edge_case_scene
+    from gaussian_splats_hip.splats import GaussianSplat, rasterize
 
     scene = edge_case_scene(n=40)
     splats = GaussianSplat.from_tensors(*scene.params())
@@ -201,14 +201,16 @@ def test_cpu_tensors_are_rejected():
 
 
 def test_dispatcher_backends():
-    from gaussian_splats.splats import rasterize
+    from gaussian_splats_hip.splats import rasterize
 
     with pytest.raises(ValueError, match="Unknown rasterization backend"):
-        rasterize(None, None, backend="gsplat")
+        rasterize(None, None, backend="cuda")
+    with pytest.raises(ValueError, match="CPU path"):
+        rasterize(None, None, backend="torch")
 
 
 def test_tile_size_must_be_power_of_two():
-    from gaussian_splats.kernels.rasterize import project_and_count
+    from gaussian_splats_hip.kernels.rasterize import project_and_count
 
     with pytest.raises(ValueError):
         project_and_count(*([torch.zeros(1)] * 7), 1.0, 1.0, 0.0, 0.0, 16, 16, 12, 0.1, 10.0,
@@ -220,13 +222,13 @@ def test_fake_implementation_shapes():
     from torch._subclasses.fake_tensor import FakeTensorMode
     from torch.fx.experimental.symbolic_shapes import ShapeEnv
 
-    import gaussian_splats.kernels.rasterize.interface  # noqa: F401 (registers the op)
+    import gaussian_splats_hip.kernels.rasterize.interface  # noqa: F401 (registers the op)
 
     with FakeTensorMode(shape_env=ShapeEnv(allow_dynamic_output_shape_ops=True)):
         n, k = 7, 16
         args = [torch.empty(n, 3), torch.empty(n, 4), torch.empty(n, 3), torch.empty(n, 1),
                 torch.empty(n, k, 3), torch.empty(3, 3), torch.empty(3)]
-        out = torch.ops.gaussian_splats.rasterize(*args, 100.0, 100.0, 60.0, 40.0, 120, 90, 16,
+        out = torch.ops.gaussian_splats_hip.rasterize(*args, 100.0, 100.0, 60.0, 40.0, 120, 90, 16,
                                                   0.999, 0.2, 100.0, "gaussian", 0.95)
     shapes = [tuple(o.shape) for o in out]
     assert shapes[0] == (90, 120, 3) and shapes[1] == (90, 120) and shapes[2] == (90, 120)
@@ -244,7 +246,7 @@ def test_multi_view_host_checks():
             None, None, None,
         )
         assert status == nat.GS_ERR_INVALID_ARGUMENT
-        status = lib.gs_composite(fake, fake, fake, None, _view(**kw), fake, fake, fake, None)
+        status = lib.gs_composite(fake, 10, fake, fake, None, _view(**kw), fake, fake, fake, None)
         assert status == nat.GS_ERR_INVALID_ARGUMENT
     # Virtual Gaussian indices (view * N + i) must fit int32.
     status = lib.gs_project_views(
@@ -259,7 +261,7 @@ def test_multi_view_host_checks():
     assert status == nat.GS_ERR_OVERFLOW
     # A mosaic whose tile grid overflows is rejected.
     status = lib.gs_composite(
-        fake, fake, fake, None, _view(image_width=1 << 16, image_height=1 << 16, tile_size=4,
+        fake, 10, fake, fake, None, _view(image_width=1 << 16, image_height=1 << 16, tile_size=4,
                                       views=64, mosaic_cols=8), fake, fake, fake, None,
     )
     assert status == nat.GS_ERR_OVERFLOW
@@ -272,13 +274,13 @@ def test_multi_view_fake_implementation_shapes():
     from torch._subclasses.fake_tensor import FakeTensorMode
     from torch.fx.experimental.symbolic_shapes import ShapeEnv
 
-    import gaussian_splats.kernels.rasterize.views  # noqa: F401 (registers the op)
+    import gaussian_splats_hip.kernels.rasterize.views  # noqa: F401 (registers the op)
 
     with FakeTensorMode(shape_env=ShapeEnv(allow_dynamic_output_shape_ops=True)):
         n, k, v = 7, 16, 5
         args = [torch.empty(n, 3), torch.empty(n, 4), torch.empty(n, 3), torch.empty(n, 1),
                 torch.empty(n, k, 3), torch.empty(v, 3, 3), torch.empty(v, 3), torch.empty(v, 4)]
-        out = torch.ops.gaussian_splats.rasterize_views(*args, 120, 90, 16, 0.999, 0.2, 100.0,
+        out = torch.ops.gaussian_splats_hip.rasterize_views(*args, 120, 90, 16, 0.999, 0.2, 100.0,
                                                         "gaussian", 0.95)
     shapes = [tuple(o.shape) for o in out]
     assert shapes[0] == (v, 90, 120, 3) and shapes[1] == (v, 90, 120) and shapes[2] == (v, 90, 120)

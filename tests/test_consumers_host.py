@@ -1,7 +1,7 @@
 """Consumers of the op on the CPU: the trajectory benchmark's scene, subset
-and camera path (kernels/rasterize/benchmark.py:26-90), the viewer's frame
-settings (visualize/gaussian/backend.py:19-57) with a stand-in rasterizer,
-and the timing API (timing.py).  No GPU."""
+and camera path (kernels/rasterize/benchmark.py:26-90), the timing API
+(timing.py), the dispatcher's backend names and the reference-side binding
+(splats/rasterize.py:12-43).  No GPU."""
 
 from __future__ import annotations
 
@@ -12,10 +12,9 @@ import pytest
 import torch
 from scipy.spatial.transform import Rotation
 
-from gaussian_splats import timing
-from gaussian_splats.kernels.rasterize import benchmark as bm
-from gaussian_splats.splats import GaussianSplat, PinholeCamera
-from gaussian_splats.viewer import GaussianViewer, render_gaussians
+from gaussian_splats_hip import timing
+from gaussian_splats_hip.kernels.rasterize import benchmark as bm
+from gaussian_splats_hip.splats import GaussianSplat, PinholeCamera
 
 
 def test_random_scene_distribution():
@@ -62,50 +61,6 @@ def test_trajectory_rotations_and_fit():
         assert float(u.min()) >= 0 and float(u.max()) <= 320 and float(v.min()) >= 0 and float(v.max()) <= 240
 
 
-def test_render_gaussians_settings():
-    """Tile-rounded size, centred principal point, evenly spread subset,
-    options from the settings, crop back to the requested size."""
-    calls = {}
-
-    def fake(splats, camera, **options):
-        calls["camera"], calls["options"] = camera, options
-        w, h = camera.image_size
-        return torch.arange(h * w * 3, dtype=torch.float32).reshape(h, w, 3)
-
-    s = GaussianSplat(1000, sh_degree=0)
-    cam = PinholeCamera(image_size=(10, 10))
-    frame = render_gaussians(s, cam, {"tile_size": "16", "num_splats": "7", "near": "0.5"}, 50, 30, fake)
-    assert calls["camera"].image_size == (64, 32)
-    assert calls["camera"].principal_point == (25.0, 15.0)
-    opts = calls["options"]
-    assert opts["backend"] == "hip" and opts["tile_size"] == 16 and opts["near"] == 0.5
-    assert opts["far"] == 100.0 and opts["opacity_threshold"] == 0.999
-    # float32 linspace: 832.5 is computed as 832.49997 and rounds down
-    assert opts["indices"].tolist() == [0, 166, 333, 500, 666, 832, 999]
-    assert frame.image.shape == (30, 50, 3)
-    assert frame.metadata == {"X-Total-Splats": "1000"}
-    empty = render_gaussians(GaussianSplat(0, sh_degree=0), cam, {}, 8, 4, fake)
-    assert empty.image.shape == (4, 8, 3) and empty.metadata["X-Total-Splats"] == "0"
-    frame = render_gaussians(s, cam, {"num_splats": "5000"}, 8, 8, fake)
-    assert len(calls["options"]["indices"]) == 1000
-
-
-def test_viewer_loads_checkpoints_and_ply(tmp_path):
-    from gaussian_splats.splats.ply import save_ply
-
-    torch.manual_seed(0)
-    s = GaussianSplat(300, sh_degree=3)
-    s.save_checkpoint(tmp_path / "scene.pt")
-    save_ply(s.state_dict(), tmp_path / "scene.ply")
-    for name in ("scene.pt", "scene.ply"):
-        viewer = GaussianViewer()
-        viewer.load_checkpoint(tmp_path / name)
-        assert viewer.checkpoint_name == name
-        assert torch.equal(viewer.splats.mean.cpu(), s.mean.detach())
-        q = viewer.camera.rotation
-        assert torch.allclose(q, torch.tensor([math.cos(math.pi / 8), -math.sin(math.pi / 8), 0, 0]))
-
-
 def test_timing_api():
     with timing.record_timings("cpu") as times:
         with timing.timed("Step"):
@@ -136,8 +91,8 @@ def test_trajectory_frame_count(frames):
 
 def test_scene_from_file(tmp_path):
     """Checkpoints and PLY files load as the same benchmark scene."""
-    from gaussian_splats import scenes
-    from gaussian_splats.splats.ply import save_ply
+    from gaussian_splats_hip import scenes
+    from gaussian_splats_hip.splats.ply import save_ply
 
     torch.manual_seed(3)
     s = GaussianSplat(20_000, sh_degree=3)
@@ -155,7 +110,7 @@ def test_host_extrinsics_equal_the_torch_rotation_matrix():
     """The rasterizer's host path gives exactly cam.rotation_matrix (float32
     quaternions of all magnitudes, unnormalised), and falls back to it for
     float64 quaternions."""
-    from gaussian_splats.splats.camera import host_extrinsics
+    from gaussian_splats_hip.splats.camera import host_extrinsics
 
     g = torch.Generator().manual_seed(11)
     for i in range(3000):

@@ -1,0 +1,462 @@
+"""Parity at the benchmark workloads (configurations 2-5 of the north star) on
+full-size scenes, against the CPU oracle (restating the reference's
+kernels/rasterize/torch.py:228-247):
+
+* projection of every Gaussian (floats to float32 rounding, depth bits exact)
+  and its tile rectangle (exact away from a floor at a tile edge);
+* the intersection lists of every tile, proved exact (per-tile lengths equal a
+  2-D histogram of the rectangles, every entry covers its tile, strictly
+  increasing (depth bits, index) keys), and for configurations 2 and 3 also
+  compared with numpy's stable sort of the reference-format keys;
+* image, transmittance and contributor counts on 32 seeded tiles including
+  the 4 longest lists, against the oracle's own lists of those tiles;
+* gradients of the mean-L1 loss restricted to those tiles against float64
+  autograd of the oracle, every Gaussian compared (see tests/parity.py);
+* configuration 5 through the multi-view op, per view against the oracle.
+
+The oracle runs on the host; torch on the GPU is used only as a checker
+(the list proof and the loss weights).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from gaussian_splats_hip import scenes
+from gaussian_splats_hip.kernels.rasterize import _native as nat
+from gaussian_splats_hip.kernels.rasterize import composite_bwd, project_and_count, project_bwd
+from gaussian_splats_hip.kernels.rasterize.interface import forward_pipeline, rasterize_outputs
+from gaussian_splats_hip.kernels.rasterize.views import (
+    camera_tensors,
+    mosaic_columns,
+    rasterize_views_outputs,
+)
+from oracle import rasterizer as orc
+from parity import (
+    DECISION_WINDOW,
+    assert_close_flip_aware,
+    assert_gradients_close,
+    assert_lists_exact,
+    oracle_camera,
+    oracle_tile_lists,
+    rect_flip_tolerant_equal,
+    restrict_lists,
+    sample_tiles,
+    tile_max,
+    tile_pixel_mask,
+)
+
+pytestmark = [pytest.mark.gpu, pytest.mark.timeout(900)]
+
+TILE = 16
+THRESHOLD = 0.999
+CHUNK = 4  # tiles per oracle compositing chunk (bounds its memory)
+TRUNCATE_SLACK = 64  # entries kept past a tile's largest contributor count
+
+
+def log(*args):
+    print("[configs]", *args, flush=True)
+
+
+_cache: dict = {}
+
+
+def single_view(name, device):
+    """GPU forward of a single-view configuration (the op's ten outputs and the
+    projection's rectangles) and the float32 oracle's projection and
+    rectangles; one configuration cached at a time."""
+    if name in _cache:
+        return _cache[name]
+    _cache.clear()
+    torch.cuda.empty_cache()
+    log(name, "scene")
+    scene = scenes.CONFIGS[name]()
+    cam = scene.cameras[0]
+    fx, fy = cam.focal_length
+    cx, cy = cam.principal_point
+    w, h = cam.image_size
+    params = [t.to(device) for t in scene.params()]
+    args = (cam.rotation_matrix.to(device), cam.translation.to(device), fx, fy, cx, cy, w, h, TILE)
+    log(name, "GPU forward")
+    out = forward_pipeline(*params, *args, THRESHOLD, scene.near, scene.far, "gaussian", 0.95)
+    bounds = project_and_count(*params, *args, scene.near, scene.far, "gaussian", 0.95)[4]
+    torch.cuda.synchronize()
+    nat.check_device_errors(device)
+    log(name, "oracle projection")
+    proj = orc.project(*scene.params(), oracle_camera(cam))
+    tw, th = nat.tiles(w, h, TILE)
+    obounds, ocounts = orc.tile_counts(proj, TILE, tw, th, scene.near, scene.far)
+    r = dict(scene=scene, params=params, out=out, bounds=bounds, proj=proj, obounds=obounds,
+             ocounts=ocounts, tw=tw, th=th, w=w, h=h)
+    _cache[name] = r
+    return r
+
+
+def check_projection(pmean, pinv, pcol, pop, gbounds, gcounts, proj, obounds, ocounts, what):
+    """Projected floats to float32 rounding, depth bits exact, rectangles
+    exact away from tile edges, counts equal where the rectangles are."""
+    torch.testing.assert_close(pmean, proj.mean.float(), rtol=2e-6, atol=1e-5)
+    visible = torch.as_tensor(ocounts > 0)
+    torch.testing.assert_close(pinv[visible], proj.inverse[visible].float(), rtol=1e-5, atol=1e-7)
+    torch.testing.assert_close(pcol, proj.color.float(), rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(pop, proj.opacity.float(), rtol=1e-6, atol=1e-7)
+    assert torch.equal(pmean[:, 2], proj.mean[:, 2].float()), f"{what}: depth bits differ"
+    extent = 2 * np.sqrt(np.log(proj.opacity[:, 0].double().numpy() * 255))
+    with np.errstate(invalid="ignore"):
+        flips = rect_flip_tolerant_equal(gbounds, obounds, proj, TILE, extent)
+    same = np.all(gbounds == obounds, axis=(1, 2))
+    assert np.array_equal(gcounts[same], ocounts[same]), f"{what}: counts differ"
+    n = len(ocounts)
+    log(what, f"rectangle flips at tile edges: {flips} of {n}")
+    assert flips <= max(4, n // 20000), f"{what}: {flips} edge flips"
+
+
+@pytest.mark.parametrize("name", ("config2", "config3", "config4"))
+def test_projection_matches_oracle(device, name):
+    r = single_view(name, device)
+    pmean, pinv, pcol, pop = (t.cpu() for t in r["out"][3:7])
+    counts = r["out"][9].cpu().numpy()
+    check_projection(pmean, pinv, pcol, pop, r["bounds"].cpu().numpy(), counts, r["proj"],
+                     r["obounds"], r["ocounts"], name)
+
+
+@pytest.mark.parametrize("name", ("config2", "config3", "config4"))
+def test_lists_exact(device, name):
+    r = single_view(name, device)
+    out = r["out"]
+    gids, ranges, counts, pmean = out[7], out[8], out[9], out[3]
+    log(name, f"list proof over {gids.numel()} intersections")
+    stats = assert_lists_exact(gids, ranges, r["bounds"], counts, pmean[:, 2], r["tw"])
+    log(name, stats)
+    if name in ("config2", "config3"):
+        # Also against numpy's stable sort of the reference-format keys
+        # (tile << 32 | depth bits), emitted Gaussian-major as the reference does.
+        keys, ids = orc.emit_intersections(r["bounds"].cpu().numpy(), pmean[:, 2].cpu().numpy(),
+                                           counts.cpu().numpy(), r["tw"])
+        sid, rng, _ = orc.sort_intersections(keys, ids, r["tw"] * r["th"])
+        assert np.array_equal(gids.cpu().numpy(), sid)
+        assert np.array_equal(ranges.cpu().numpy(), rng)
+
+
+def _sampled_forward(r, name, seed=0):
+    """The oracle's own lists of 32 sampled tiles (cut TRUNCATE_SLACK entries
+    past the GPU's largest contributor count of each tile: the oracle must
+    then stop earlier, which is asserted) composited in float32."""
+    out = r["out"]
+    ranges = out[8].cpu().numpy()
+    ncon = out[2].cpu().numpy()
+    tiles = sample_tiles(ranges, seed=seed)
+    limits = {t: m + TRUNCATE_SLACK for t, m in tile_max(ncon, tiles, r["tw"], TILE).items()}
+    proj = r["proj"]
+    ids, rng = oracle_tile_lists(r["obounds"], r["ocounts"], proj.mean[:, 2].float().numpy(), tiles,
+                                 r["tw"], r["tw"] * r["th"], limits)
+    lengths = rng[:, 1] - rng[:, 0]
+    log(name, f"oracle compositing {len(tiles)} tiles, {int(lengths.sum())} entries "
+              f"(longest {int(lengths.max())})")
+    comp = orc.composite(proj.mean[:, 0], proj.mean[:, 1], proj.inverse[:, 0, 0],
+                         proj.inverse[:, 0, 1], proj.inverse[:, 1, 1], proj.color,
+                         proj.opacity[:, 0], ids, rng, r["w"], r["h"], TILE, THRESHOLD,
+                         tile_chunk=CHUNK)
+    onc = comp.n_contributors.numpy()
+    full = np.asarray(out[8].cpu().numpy())
+    for t in tiles:
+        if limits[t] < full[t, 1] - full[t, 0]:  # cut: the oracle must have stopped before
+            assert tile_max(onc, [t], r["tw"], TILE)[int(t)] < limits[t], f"tile {t} cut too early"
+    return tiles, comp
+
+
+@pytest.mark.parametrize("name", ("config2", "config3", "config4"))
+def test_sampled_tiles_forward(device, name):
+    r = single_view(name, device)
+    tiles, comp = _sampled_forward(r, name)
+    mask = torch.as_tensor(tile_pixel_mask(tiles, r["tw"], TILE, r["w"], r["h"]))
+    image, final_t, ncon = (t.cpu() for t in r["out"][:3])
+    margin = torch.where(mask, torch.as_tensor(comp.margin), torch.full_like(comp.margin, math.inf))
+    stats = assert_close_flip_aware(image[mask], comp.image[mask], margin[mask], atol=1e-5,
+                                    what=f"{name} image")
+    log(name, "image", stats)
+    assert_close_flip_aware(final_t[mask], comp.final_transmittance[mask], margin[mask], atol=1e-5,
+                            rtol=1e-4, what=f"{name} transmittance")
+    ok = mask & (torch.as_tensor(comp.margin) >= 1e-4)
+    assert torch.equal(ncon[ok], comp.n_contributors[ok]), f"{name}: contributor counts differ"
+
+
+def _loss_weights(image, target, mask):
+    """dL/dimage of L = mean |image - target| restricted to the masked pixels
+    (the loss of configurations 3-5, summed over the sampled tiles only)."""
+    g = torch.sign(image.detach() - target) / image.numel()
+    return g * mask[..., None].to(g.device, g.dtype)
+
+
+def _fixed_decision_gradients(pm, pinv, pcol, pop, ids, rng, ncon, weights, w, h):
+    """float64 autograd of the oracle compositor over the given lists with the
+    cut/clamp decisions of its float32 run on the same float32 inputs and the
+    GPU's activity counts; returns the [N, 9] gradient (per-entry inverse
+    covariance off-diagonal) and the per-Gaussian decision margin."""
+    f32 = [pm[:, 0], pm[:, 1], pinv[:, 0, 0], pinv[:, 0, 1], pinv[:, 1, 1], pcol, pop[:, 0]]
+    run32 = orc.composite(*f32, ids, rng, w, h, TILE, THRESHOLD, tile_chunk=CHUNK)
+    leaves = [x.double().clone().requires_grad_(True) for x in f32]
+    run64 = orc.composite(*leaves, ids, rng, w, h, TILE, THRESHOLD, tile_chunk=CHUNK,
+                          decisions=run32.decisions, active_counts=ncon)
+    (run64.image * weights.double()).sum().backward()
+    du, dv, da, db, dc, drgb, dop = (x.grad for x in leaves)
+    grad = torch.stack((du, dv, da, db / 2, dc, drgb[:, 0], drgb[:, 1], drgb[:, 2], dop), -1)
+    return grad, run32.gaussian_cut_margin
+
+
+@pytest.mark.parametrize("name", ("config3", "config4"))
+def test_sampled_tiles_composite_backward(device, name):
+    """composite_bwd at full size with the loss restricted to the sampled
+    tiles, on the GPU's own projected values and lists."""
+    r = single_view(name, device)
+    out = r["out"]
+    image, final_t, ncon, pm, pinv, pcol, pop, gids, granges, counts = out
+    tiles = sample_tiles(granges.cpu().numpy(), seed=1)
+    mask = torch.as_tensor(tile_pixel_mask(tiles, r["tw"], TILE, r["w"], r["h"]))
+    weights = _loss_weights(image, r["scene"].target.to(device), mask)
+    grad = composite_bwd(pm, pinv, pcol, pop, gids, granges, weights.contiguous(), final_t, ncon,
+                         r["w"], r["h"], TILE, THRESHOLD, "gaussian").cpu()
+    ncon_h = ncon.cpu().numpy()
+    limits = {t: m + 1 for t, m in tile_max(ncon_h, tiles, r["tw"], TILE).items()}
+    ids, rng = restrict_lists(gids.cpu().numpy(), granges.cpu().numpy(), tiles, limits)
+    log(name, f"float64 reference over {len(ids)} entries")
+    expected, cut_margin = _fixed_decision_gradients(
+        pm.cpu(), pinv.cpu(), pcol.cpu(), pop.cpu(), ids, rng, ncon_h, weights.cpu(), r["w"], r["h"])
+    explained = cut_margin < DECISION_WINDOW
+    stats = assert_gradients_close(grad, expected, f"{name} composite_bwd", explained=explained)
+    log(name, "composite_bwd", stats, "explained", int(explained.sum()))
+    touched = int((expected.abs().sum(1) > 0).sum())
+    assert touched > 1000, touched
+
+
+def test_config3_op_backward(device):
+    """The op end to end (projection, binning, compositing, both backward
+    kernels) on config 3 with the mean-L1 loss restricted to the sampled
+    tiles, against float64 autograd of the oracle rasterizer along the GPU's
+    lists with fixed decisions."""
+    r = single_view("config3", device)
+    scene = r["scene"]
+    cam = scene.cameras[0]
+    fx, fy = cam.focal_length
+    cx, cy = cam.principal_point
+    leaves = [p.clone().requires_grad_(True) for p in r["params"]]
+    outs = rasterize_outputs(*leaves, cam.rotation_matrix.to(device), cam.translation.to(device),
+                             fx, fy, cx, cy, r["w"], r["h"], TILE, THRESHOLD, scene.near, scene.far,
+                             "gaussian", 0.95)
+    image, _, ncon, pm, pinv, pcol, pop, gids, granges, _ = outs
+    tiles = sample_tiles(granges.cpu().numpy(), seed=2)
+    mask = torch.as_tensor(tile_pixel_mask(tiles, r["tw"], TILE, r["w"], r["h"]))
+    weights = _loss_weights(image, scene.target.to(device), mask)
+    (image * weights).sum().backward()
+    actual = [p.grad.cpu() for p in leaves]
+    ncon_h = ncon.cpu().numpy()
+    limits = {t: m + 1 for t, m in tile_max(ncon_h, tiles, r["tw"], TILE).items()}
+    ids, rng = restrict_lists(gids.cpu().numpy(), granges.cpu().numpy(), tiles, limits)
+    f32 = [t.detach().cpu() for t in (pm[:, 0], pm[:, 1], pinv[:, 0, 0], pinv[:, 0, 1],
+                                      pinv[:, 1, 1], pcol, pop[:, 0])]
+    run32 = orc.composite(*f32, ids, rng, r["w"], r["h"], TILE, THRESHOLD, tile_chunk=CHUNK)
+    log("config3 op: float64 projection of all Gaussians + compositing of", len(ids), "entries")
+    p64 = [p.double().requires_grad_(True) for p in scene.params()]
+    ref = orc.rasterize(*p64, oracle_camera(cam), tile_size=TILE, opacity_threshold=THRESHOLD,
+                        near=scene.near, far=scene.far, tile_chunk=CHUNK, lists=(ids, rng),
+                        decisions=run32.decisions, active_counts=ncon_h)
+    (ref.image * weights.cpu().double()).sum().backward()
+    explained = run32.gaussian_cut_margin < DECISION_WINDOW
+    for name, a, p in zip(("mean", "rotation", "scale", "opacity", "color"), actual, p64):
+        stats = assert_gradients_close(a, p.grad, f"config3 grad {name}", explained=explained)
+        log("config3 op grad", name, stats)
+
+
+def test_config3_project_bwd(device):
+    """Projection backward of all 1M Gaussians for a seeded upstream gradient
+    [N, 9] against float64 autograd of the oracle projection."""
+    r = single_view("config3", device)
+    scene = r["scene"]
+    cam = scene.cameras[0]
+    fx, fy = cam.focal_length
+    out = r["out"]
+    counts = out[9]
+    n = counts.shape[0]
+    g = torch.Generator().manual_seed(5)
+    upstream = torch.randn(n, 9, generator=g) * torch.tensor([1, 1, 10, 10, 10, 1, 1, 1, 1.0])
+    upstream[counts.cpu() == 0] = 0
+    grads = project_bwd(*r["params"], cam.rotation_matrix.to(device), cam.translation.to(device),
+                        out[4], upstream.to(device), counts, fx, fy, r["w"], r["h"])
+    p64 = [p.double().requires_grad_(True) for p in scene.params()]
+    proj = orc.project(*p64, oracle_camera(cam))
+    u64 = upstream.double()
+    loss = (proj.mean[:, 0] * u64[:, 0] + proj.mean[:, 1] * u64[:, 1]
+            + proj.inverse[:, 0, 0] * u64[:, 2] + (proj.inverse[:, 0, 1] + proj.inverse[:, 1, 0]) * u64[:, 3]
+            + proj.inverse[:, 1, 1] * u64[:, 4] + (proj.color * u64[:, 5:8]).sum(1)
+            + proj.opacity[:, 0] * u64[:, 8]).sum()
+    loss.backward()
+    for name, a, p in zip(("mean", "rotation", "scale", "opacity", "color"), grads, p64):
+        stats = assert_gradients_close(a.cpu(), p.grad, f"config3 project_bwd {name}")
+        log("config3 project_bwd", name, stats)
+
+
+# --- configuration 5: 16 views through the multi-view op ---------------------
+
+SAMPLED_VIEWS = (0, 5, 10)
+
+
+def _views_project_bounds(params, cams, scene, device):
+    """The mosaic rectangles [V, N, 2, 2] of gs_project_views (the op does not
+    return them)."""
+    rot, trans, intr, w, h = camera_tensors(cams)
+    v = len(cams)
+    n = params[0].shape[0]
+    tw, th = nat.tiles(w, h, TILE)
+    cols = mosaic_columns(v, tw, th)
+    outs = [params[0].new_empty(s) for s in ((v, n, 3), (v, n, 2, 2), (v, n, 3), (v, n, 1))]
+    bounds = torch.empty((v, n, 2, 2), dtype=torch.int32, device=device)
+    counts = torch.empty((v, n), dtype=torch.int32, device=device)
+    view = nat.make_view(0.0, 0.0, 0.0, 0.0, w, h, TILE, scene.near, scene.far, views=v,
+                         mosaic_cols=cols)
+    ptr = nat.ptr
+    nat.check(nat.library().gs_project_views(
+        *(ptr(p) for p in params), n, params[4].shape[1], ptr(rot), ptr(trans), ptr(intr), view, *(ptr(o) for o in outs), ptr(bounds),
+        ptr(counts), None, None, nat.stream(device)), "project_views")
+    return bounds, cols, tw, th
+
+
+def _view_lists(gids, ranges, v, n, cols, tw, th):
+    """View v's tile lists in its own tile grid with real Gaussian indices
+    (numpy), from the mosaic's lists."""
+    ox, oy = (v % cols) * tw, (v // cols) * th
+    mosaic_w = cols * tw
+    ty, tx = np.divmod(np.arange(tw * th), tw)
+    mtile = (oy + ty) * mosaic_w + ox + tx
+    r = ranges[mtile]
+    lengths = r[:, 1] - r[:, 0]
+    ids = np.concatenate([gids[s:e] for s, e in r]) - v * n if lengths.sum() else np.zeros(0, np.int32)
+    ends = np.cumsum(lengths)
+    local = np.stack((ends - lengths, ends), 1).astype(np.int64)
+    return ids.astype(np.int32), local
+
+
+@pytest.fixture(scope="module")
+def config5(device):
+    _cache.clear()
+    torch.cuda.empty_cache()
+    log("config5 scene")
+    scene = scenes.config5()
+    params = [t.to(device) for t in scene.params()]
+    leaves = [p.clone().requires_grad_(True) for p in params]
+    rot, trans, intr, w, h = camera_tensors(scene.cameras)
+    log("config5 GPU forward (16 views)")
+    outs = rasterize_views_outputs(*leaves, rot, trans, intr, w, h, TILE, THRESHOLD, scene.near,
+                                   scene.far, "gaussian", 0.95)
+    bounds, cols, tw, th = _views_project_bounds(params, scene.cameras, scene, device)
+    torch.cuda.synchronize()
+    nat.check_device_errors(device)
+    yield dict(scene=scene, params=params, leaves=leaves, outs=outs, bounds=bounds, cols=cols,
+               tw=tw, th=th, w=w, h=h)
+
+
+def test_config5_projection_and_lists(device, config5):
+    c = config5
+    image, final_t, ncon, pm, pinv, pcol, pop, gids, ranges, counts = c["outs"]
+    v_count, n = counts.shape
+    log(f"config5 list proof over {gids.numel()} intersections")
+    stats = assert_lists_exact(gids, ranges, c["bounds"].view(v_count * n, 2, 2),
+                               counts.view(-1), pm.view(-1, 3)[:, 2].contiguous(), c["cols"] * c["tw"])
+    log("config5", stats)
+    for v in SAMPLED_VIEWS + (15,):
+        cam = c["scene"].cameras[v]
+        proj = orc.project(*c["scene"].params(), oracle_camera(cam))
+        ob, oc = orc.tile_counts(proj, TILE, c["tw"], c["th"], c["scene"].near, c["scene"].far)
+        ox, oy = (v % c["cols"]) * c["tw"], (v // c["cols"]) * c["th"]
+        gb = c["bounds"][v].cpu().numpy() - np.array([[ox], [oy]], dtype=np.int32)
+        gc = counts[v].cpu().numpy()
+        # Rectangles of culled or off-view Gaussians only matter through their
+        # count, which is compared below.
+        live = (gc > 0) | (oc > 0)
+        gb[~live] = ob[~live]
+        check_projection(pm[v].detach().cpu(), pinv[v].detach().cpu(), pcol[v].detach().cpu(),
+                         pop[v].detach().cpu(), gb, gc, proj, ob, oc, f"config5 view {v}")
+
+
+def test_config5_sampled_views_forward(device, config5):
+    c = config5
+    image, final_t, ncon, _, _, _, _, gids, ranges, counts = c["outs"]
+    n = counts.shape[1]
+    scene = c["scene"]
+    for v in SAMPLED_VIEWS:
+        ids_v, rng_v = _view_lists(gids.cpu().numpy(), ranges.cpu().numpy(), v, n, c["cols"],
+                                   c["tw"], c["th"])
+        tiles = sample_tiles(rng_v, count=8, longest=2, seed=v)
+        ncon_v = ncon[v].cpu().numpy()
+        limits = {t: m + TRUNCATE_SLACK for t, m in tile_max(ncon_v, tiles, c["tw"], TILE).items()}
+        proj = orc.project(*scene.params(), oracle_camera(scene.cameras[v]))
+        ob, oc = orc.tile_counts(proj, TILE, c["tw"], c["th"], scene.near, scene.far)
+        ids, rng = oracle_tile_lists(ob, oc, proj.mean[:, 2].float().numpy(), tiles, c["tw"],
+                                     c["tw"] * c["th"], limits)
+        log(f"config5 view {v}: oracle compositing {len(ids)} entries")
+        comp = orc.composite(proj.mean[:, 0], proj.mean[:, 1], proj.inverse[:, 0, 0],
+                             proj.inverse[:, 0, 1], proj.inverse[:, 1, 1], proj.color,
+                             proj.opacity[:, 0], ids, rng, c["w"], c["h"], TILE, THRESHOLD,
+                             tile_chunk=CHUNK)
+        onc = comp.n_contributors.numpy()
+        for t in tiles:
+            if limits[int(t)] < rng_v[t, 1] - rng_v[t, 0]:
+                assert tile_max(onc, [t], c["tw"], TILE)[int(t)] < limits[int(t)]
+        mask = torch.as_tensor(tile_pixel_mask(tiles, c["tw"], TILE, c["w"], c["h"]))
+        img = image[v].detach().cpu()
+        margin = torch.as_tensor(comp.margin)
+        stats = assert_close_flip_aware(img[mask], comp.image[mask], margin[mask], atol=1e-5,
+                                        what=f"config5 view {v} image")
+        log(f"config5 view {v} image", stats)
+        assert_close_flip_aware(final_t[v].cpu()[mask], comp.final_transmittance[mask],
+                                margin[mask], atol=1e-5, rtol=1e-4,
+                                what=f"config5 view {v} transmittance")
+        ok = mask & (margin >= 1e-4)
+        assert torch.equal(ncon[v].cpu()[ok], comp.n_contributors[ok])
+
+
+def test_config5_op_backward(device, config5):
+    """Gradients of the multi-view op (mosaic compositing backward and the
+    multi-view projection backward summed over views) for the mean-L1 loss on
+    sampled tiles of three views, against float64 autograd of the oracle
+    rasterizer per view along the GPU's lists with fixed decisions, summed."""
+    c = config5
+    scene = c["scene"]
+    image, final_t, ncon, pm, pinv, pcol, pop, gids, ranges, counts = c["outs"]
+    v_count, n = counts.shape
+    target = scene.target.to(device)
+    weights = torch.zeros_like(image)
+    lists = {}
+    for v in SAMPLED_VIEWS:
+        ids_v, rng_v = _view_lists(gids.cpu().numpy(), ranges.cpu().numpy(), v, n, c["cols"],
+                                   c["tw"], c["th"])
+        tiles = sample_tiles(rng_v, count=8, longest=2, seed=10 + v)
+        mask = torch.as_tensor(tile_pixel_mask(tiles, c["tw"], TILE, c["w"], c["h"]))
+        weights[v] = _loss_weights(image[v], target[v], mask) * (image[v].numel() / image.numel())
+        ncon_v = ncon[v].cpu().numpy()
+        limits = {t: m + 1 for t, m in tile_max(ncon_v, tiles, c["tw"], TILE).items()}
+        lists[v] = restrict_lists(ids_v, rng_v, tiles, limits) + (ncon_v,)
+    (image * weights).sum().backward()
+    actual = [p.grad.cpu() for p in c["leaves"]]
+    p64 = [p.double().requires_grad_(True) for p in scene.params()]
+    total = 0
+    explained = torch.zeros(n, dtype=torch.bool)
+    for v in SAMPLED_VIEWS:
+        ids, rng, ncon_v = lists[v]
+        f32 = [t.detach().cpu() for t in (pm[v, :, 0], pm[v, :, 1], pinv[v, :, 0, 0],
+                                          pinv[v, :, 0, 1], pinv[v, :, 1, 1], pcol[v], pop[v, :, 0])]
+        run32 = orc.composite(*f32, ids, rng, c["w"], c["h"], TILE, THRESHOLD, tile_chunk=CHUNK)
+        explained |= run32.gaussian_cut_margin < DECISION_WINDOW
+        log(f"config5 view {v}: float64 reference over {len(ids)} entries")
+        ref = orc.rasterize(*p64, oracle_camera(scene.cameras[v]), tile_size=TILE,
+                            opacity_threshold=THRESHOLD, near=scene.near, far=scene.far,
+                            tile_chunk=CHUNK, lists=(ids, rng), decisions=run32.decisions,
+                            active_counts=ncon_v)
+        total = total + (ref.image * weights[v].cpu().double()).sum()
+    total.backward()
+    for name, a, p in zip(("mean", "rotation", "scale", "opacity", "color"), actual, p64):
+        stats = assert_gradients_close(a, p.grad, f"config5 grad {name}", explained=explained)
+        log("config5 op grad", name, stats)

@@ -1,21 +1,26 @@
 """Consumers of the op on the GPU: ``indices`` subsampling (the viewer's
 path, interface.py:274-281 of the reference) with gradients scattered back,
 the op under ``torch.compile(rasterize, dynamic=True)`` (the viewer's
-compile path, visualize/gaussian/backend.py:80-81), per-stage timings,
-the viewer's frame function and the trajectory benchmark."""
+compile path, visualize/gaussian/backend.py:80-81), the reference viewer's
+frame call (backend.py:19-57) through the dispatcher, per-stage timings and
+the trajectory benchmark.  Images and gradients are checked against the CPU
+oracle; equalities with the HIP op itself are additional."""
 
 from __future__ import annotations
 
 import json
 from dataclasses import replace
 
+import numpy as np
 import pytest
 import torch
 
-from gaussian_splats import scenes, timing
-from gaussian_splats.kernels.rasterize import benchmark as bm
-from gaussian_splats.splats import GaussianSplat, rasterize
-from gaussian_splats.viewer import GaussianViewer, render_gaussians
+from gaussian_splats_hip import scenes, timing
+from gaussian_splats_hip.kernels.rasterize import benchmark as bm
+from gaussian_splats_hip.kernels.rasterize.interface import rasterize_outputs
+from gaussian_splats_hip.splats import GaussianSplat, rasterize
+from oracle import rasterizer as orc
+from parity import DECISION_WINDOW, assert_close_flip_aware, assert_gradients_close, oracle_camera
 
 pytestmark = pytest.mark.gpu
 
@@ -37,6 +42,12 @@ def test_indices_forward_and_scattered_gradients(device):
         splats.mean, splats.rotation, splats.scale, splats.opacity, splats.color)))
     ref = rasterize(sub, cam, tile_size=16, near=scene.near, far=scene.far)
     assert torch.equal(image, ref)
+    idx_h = idx.cpu()
+    gathered = [p[idx_h] for p in scene.params()]
+    oracle = orc.rasterize(*gathered, oracle_camera(cam), tile_size=16, near=scene.near,
+                           far=scene.far)
+    assert_close_flip_aware(image.detach().cpu(), oracle.image, oracle.composite.margin, atol=1e-5,
+                            what="indexed image")
     weight = torch.rand(image.shape, generator=g).to(device)
     (image * weight).sum().backward()
     (ref * weight).sum().backward()
@@ -50,6 +61,36 @@ def test_indices_forward_and_scattered_gradients(device):
         untouched = torch.ones(splats.num_points, dtype=torch.bool, device=device)
         untouched[idx] = False
         assert float(full[untouched].abs().max()) == 0.0, name
+    # Against float64 autograd of the oracle through the same gather, along
+    # the GPU's lists of the subset with its decisions fixed.
+    cam_args = _inputs_after_params(scene, device)
+    outs = rasterize_outputs(*(p.detach()[idx].clone() for p in (
+        splats.mean, splats.rotation, splats.scale, splats.opacity, splats.color)), *cam_args)
+    _, _, ncon, pm, pinv, pcol, pop, gids, granges, _ = outs
+    sid, rng = gids.cpu().numpy(), granges.cpu().numpy()
+    f32 = [t.cpu() for t in (pm[:, 0], pm[:, 1], pinv[:, 0, 0], pinv[:, 0, 1], pinv[:, 1, 1], pcol,
+                              pop[:, 0])]
+    w, h = cam.image_size
+    run32 = orc.composite(*f32, sid, rng, w, h, 16)
+    p64 = [p.double().requires_grad_(True) for p in scene.params()]
+    ref64 = orc.rasterize(*(p[idx_h] for p in p64), oracle_camera(cam), tile_size=16,
+                          near=scene.near, far=scene.far, lists=(sid, rng),
+                          decisions=run32.decisions, active_counts=ncon.cpu().numpy())
+    (ref64.image * weight.cpu().double()).sum().backward()
+    explained = torch.zeros(splats.num_points, dtype=torch.bool)
+    explained[idx_h[run32.gaussian_cut_margin < DECISION_WINDOW]] = True
+    for name, p in zip(("mean", "rotation", "scale", "opacity", "color"), p64):
+        assert_gradients_close(getattr(splats, name).grad, p.grad, f"indexed grad {name}",
+                               explained=explained)
+
+
+def _inputs_after_params(scene, device, tile_size=16):
+    cam = scene.cameras[0]
+    fx, fy = cam.focal_length
+    cx, cy = cam.principal_point
+    w, h = cam.image_size
+    return (cam.rotation_matrix.to(device), cam.translation.to(device), fx, fy, cx, cy, w, h,
+            tile_size, 0.999, scene.near, scene.far, "gaussian", 0.95)
 
 
 @pytest.mark.timeout(300)
@@ -68,6 +109,10 @@ def test_torch_compile_path(device):
             splats.mean, splats.rotation, splats.scale, splats.opacity, splats.color)))
         ref = rasterize(eager_splats, cam, 16, 0.999, scene.near, scene.far)
         assert torch.equal(out, ref)
+        oracle = orc.rasterize(*scene.params(), oracle_camera(cam), tile_size=16, near=scene.near,
+                               far=scene.far)
+        assert_close_flip_aware(out.detach().cpu(), oracle.image, oracle.composite.margin,
+                                atol=1e-5, what=f"compiled image n={n}")
         out.square().mean().backward()
         ref.square().mean().backward()
         for name in ("mean", "rotation", "scale", "opacity", "color"):
@@ -85,34 +130,29 @@ def test_stage_timings_are_recorded(device):
     assert all(v >= 0 for v in stages.values()) and sum(stages.values()) > 0
 
 
-def test_render_gaussians_on_gpu(device, monkeypatch):
+def test_reference_viewer_frame_call(device):
+    """The call the reference's viewer makes per frame
+    (visualize/gaussian/backend.py:19-54) through this build's dispatcher:
+    its default backend name "gsplat", the image rounded up to the tile size
+    with the principal point at the requested size's centre, an evenly
+    spread subset through ``indices``, then the crop.  Compared with the
+    oracle on the gathered subset."""
     scene, splats = _scene(device)
     cam = scene.cameras[0]
-    monkeypatch.setenv("GAUSSIAN_SPLATS_PROFILE", "1")
-    settings = {"tile_size": "16", "num_splats": "1500", "near": str(scene.near)}
-    frame = render_gaussians(splats, cam, settings, 90, 70)
-    assert frame.image.shape == (70, 90, 3) and frame.image.is_cuda
-    assert "default/Composite" in frame.timings
-    idx = torch.linspace(0, splats.num_points - 1, 1500, device=device).round().long()
-    cam2 = replace(cam, image_size=(96, 80), principal_point=(45.0, 35.0))
+    width, height, tile, count = 90, 70, 16, 1500
+    size = ((width + tile - 1) // tile * tile, (height + tile - 1) // tile * tile)
+    frame_cam = replace(cam, image_size=size, principal_point=(width / 2, height / 2))
+    idx = torch.linspace(0, splats.num_points - 1, count, device=device).round().long()
     with torch.no_grad():
-        ref = rasterize(splats, cam2, tile_size=16, near=scene.near, far=100.0, indices=idx)
-    assert torch.equal(frame.image, ref[:70, :90])
-
-
-@pytest.mark.timeout(300)
-def test_viewer_compiled_render(device, tmp_path):
-    torch._dynamo.reset()
-    _, splats = _scene(device)
-    path = tmp_path / "scene.pt"
-    splats.save_checkpoint(path)
-    viewer = GaussianViewer()
-    viewer.load_checkpoint(path)
-    viewer.splats = viewer.splats.to(device)
-    eager = viewer.render({"tile_size": "8"}, 64, 48)
-    compiled = viewer.render({"tile_size": "8", "compile_render": "1"}, 64, 48)
-    assert viewer.compiled_rasterizer is not None
-    assert torch.equal(eager.image, compiled.image)
+        image = rasterize(splats, frame_cam, tile_size=tile, opacity_threshold=0.999,
+                          near=scene.near, far=100.0, rendering_mode="gaussian", confidence=0.95,
+                          indices=idx, backend="gsplat")[:height, :width]
+    assert image.shape == (height, width, 3)
+    idx_h = idx.cpu()
+    oracle = orc.rasterize(*(p[idx_h] for p in scene.params()), oracle_camera(frame_cam),
+                           tile_size=tile, near=scene.near, far=100.0)
+    assert_close_flip_aware(image.cpu(), oracle.image[:height, :width],
+                            oracle.composite.margin[:height, :width], atol=1e-5, what="frame")
 
 
 @pytest.mark.timeout(300)

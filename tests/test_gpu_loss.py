@@ -10,8 +10,8 @@ import numpy as np
 import pytest
 import torch
 
-from gaussian_splats.kernels.rasterize import _native as nat
-from gaussian_splats.training import l1_loss, l1_loss_backward, l1_loss_forward, ssim, ssim_forward
+from gaussian_splats_hip.kernels.rasterize import _native as nat
+from gaussian_splats_hip.training import l1_loss, l1_loss_backward, l1_loss_forward, ssim, ssim_forward
 from oracle import losses as orc
 
 pytestmark = pytest.mark.gpu

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 import torch
 
-from gaussian_splats.splats.ply import load_ply, save_ply
+from gaussian_splats_hip.splats.ply import load_ply, save_ply
 from oracle import ply as oply
 from tests import plyfiles
 from tests.test_ply_host import LAYOUTS, write_layout

@@ -11,10 +11,10 @@ from __future__ import annotations
 import pytest
 import torch
 
-from gaussian_splats import scenes
-from gaussian_splats.kernels.rasterize import _native as nat
-from gaussian_splats.kernels.rasterize import composite, composite_bwd
-from gaussian_splats.kernels.rasterize.interface import forward_pipeline
+from gaussian_splats_hip import scenes
+from gaussian_splats_hip.kernels.rasterize import _native as nat
+from gaussian_splats_hip.kernels.rasterize import composite, composite_bwd
+from gaussian_splats_hip.kernels.rasterize.interface import forward_pipeline
 from oracle import rasterizer as orc
 from parity import assert_close_flip_aware, oracle_camera
 

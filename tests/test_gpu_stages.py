@@ -10,8 +10,8 @@ import numpy as np
 import pytest
 import torch
 
-from gaussian_splats import scenes
-from gaussian_splats.kernels.rasterize import (
+from gaussian_splats_hip import scenes
+from gaussian_splats_hip.kernels.rasterize import (
     bin_gaussians,
     bin_tiles,
     composite,
@@ -21,7 +21,7 @@ from gaussian_splats.kernels.rasterize import (
     sort_intersections,
     sort_tiles,
 )
-from gaussian_splats.kernels.rasterize import _native as nat
+from gaussian_splats_hip.kernels.rasterize import _native as nat
 from oracle import rasterizer as orc
 from parity import assert_close_flip_aware, oracle_camera, rect_flip_tolerant_equal
 
@@ -338,7 +338,7 @@ def _expected_order(keys):
 
 @pytest.mark.parametrize("shape", [(120, 68, 16), (7, 5, 8), (1, 1, 16), (33, 2, 4)])
 def test_tile_order_by_list_length_and_contributors(device, shape):
-    from gaussian_splats.kernels.rasterize.composite import tile_order
+    from gaussian_splats_hip.kernels.rasterize.composite import tile_order
 
     tw, th, tile = shape
     w, h = tw * tile - 3, th * tile - 1  # partial edge tiles
@@ -376,9 +376,9 @@ def test_compositing_results_do_not_depend_on_tile_order(device):
     image, final_t, ncon = composite(*args, sid_d, ranges_d, w, h, tile_size, THRESHOLD, "gaussian",
                                      CONFIDENCE)
     # The same launch through the C ABI with the tiles dispatched longest first.
-    from gaussian_splats.kernels.rasterize import composite_bwd
-    from gaussian_splats.kernels.rasterize.composite import tile_order
-    from gaussian_splats.kernels.rasterize.project import pack_records
+    from gaussian_splats_hip.kernels.rasterize import composite_bwd
+    from gaussian_splats_hip.kernels.rasterize.composite import tile_order
+    from gaussian_splats_hip.kernels.rasterize.project import pack_records
 
     order = tile_order(ranges_d, None, w, h, tile_size)
     assert not torch.equal(order.cpu(), torch.arange(order.numel(), dtype=torch.int32))
@@ -408,3 +408,51 @@ def test_compositing_results_do_not_depend_on_tile_order(device):
     # of each gradient column (a skipped or repeated tile would be O(1) off).
     scale = grad2.abs().amax(dim=0, keepdim=True).clamp_min(1e-30)
     assert float(((grad - grad2).abs() / scale).max()) < 1e-4
+
+
+def test_device_check_failures_reach_the_host(device):
+    """A binning pass handed sizes that differ from its plan's device totals
+    (here one row-list entry too many) leaves every workgroup at once and
+    sets the size-mismatch bit of the device's sticky check word (no kernel
+    waits or reads out of bounds on that path: the row and column passes
+    return before any other access, and the width scan in between clamps its
+    reads and bounds its writes).  The bit reaches the host through
+    gs_device_errors and through the next binning call's totals, which
+    raises once; the call after that runs normally."""
+    from ctypes import c_void_p
+
+    lib = nat.library()
+    assert nat.device_errors(device, clear=True) == 0, "an earlier test left a device check failure"
+    b, d, c = _random_rects(n=3000, tiles_w=24, tiles_h=17, seed=9)
+    bounds, counts = b.to(device), c.to(device)
+    keys = _depth_keys(d, c).to(device)
+    n, tw, th = 3000, 24, 17
+    s = nat.stream(device)
+    plan = nat.workspace(lib.gs_bin_tiles_plan_bytes(n, tw, th), device)
+    ranges = torch.empty((tw * th, 2), dtype=torch.int64, device=device)
+    totals = torch.empty(4, dtype=torch.int64, device=device)
+    host = torch.zeros(5, dtype=torch.int64, pin_memory=True)
+    print("[device checks] plan", flush=True)
+    nat.check(lib.gs_bin_tiles_plan(nat.ptr(keys), nat.ptr(bounds), nat.ptr(counts), n, tw, th,
+                                    nat.ptr(ranges), nat.ptr(totals), c_void_p(host.data_ptr()),
+                                    nat.ptr(plan), plan.numel(), s), "plan")
+    total, rows, blocks, _, flags = host.tolist()
+    assert flags == 0 and total > 0
+    wrong_rows = rows + 1
+    ws = nat.workspace(lib.gs_bin_tiles_emit_bytes(n, total, wrong_rows, blocks, tw, th), device)
+    ids = torch.zeros(total, dtype=torch.int32, device=device)
+    print("[device checks] emit with a wrong row-entry count", flush=True)
+    nat.check(lib.gs_bin_tiles_emit(n, tw, th, nat.ptr(totals), total, wrong_rows, blocks,
+                                    nat.ptr(plan), plan.numel(), nat.ptr(ranges), nat.ptr(ids),
+                                    nat.ptr(ws), ws.numel(), s), "emit")
+    assert nat.device_errors(device, clear=False) == 4  # GS_DEVICE_SIZE_MISMATCH
+    # The next binning call sees the word beside its totals and raises once.
+    keys2 = _depth_keys(d, c).to(device)
+    with pytest.raises(RuntimeError, match="differ from the plan"):
+        bin_tiles(keys2, bounds, counts, tw, th)
+    assert nat.device_errors(device, clear=False) == 0
+    sid, rng = bin_tiles(_depth_keys(d, c).to(device), bounds, counts, tw, th)
+    ekeys, eids = orc.emit_intersections(b.numpy(), d.numpy(), c.numpy(), tw)
+    esid, erng, _ = orc.sort_intersections(ekeys, eids, tw * th)
+    assert np.array_equal(sid.cpu().numpy(), esid) and np.array_equal(rng.cpu().numpy(), erng)
+    nat.check_device_errors(device)

@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from gaussian_splats.training import FusedAdam, splat_regularizers
+from gaussian_splats_hip.training import FusedAdam, splat_regularizers
 from oracle import losses as olosses
 from oracle import optim as oopt
 

@@ -1,4 +1,4 @@
-"""Parity of the multi-view op (torch.ops.gaussian_splats.rasterize_views)
+"""Parity of the multi-view op (torch.ops.gaussian_splats_hip.rasterize_views)
 against the single-view op, which the other GPU tests pin to the CPU oracle.
 
 Per view, the mosaic render must give bit-identical images, transmittance,
@@ -14,11 +14,11 @@ import math
 import pytest
 import torch
 
-from gaussian_splats import scenes
-from gaussian_splats.kernels.rasterize import _native as nat
-from gaussian_splats.kernels.rasterize.interface import forward_pipeline
-from gaussian_splats.kernels.rasterize.views import camera_tensors, forward_views, mosaic_columns
-from gaussian_splats.splats import GaussianSplat, PinholeCamera, rasterize, rasterize_views
+from gaussian_splats_hip import scenes
+from gaussian_splats_hip.kernels.rasterize import _native as nat
+from gaussian_splats_hip.kernels.rasterize.interface import forward_pipeline
+from gaussian_splats_hip.kernels.rasterize.views import camera_tensors, forward_views, mosaic_columns
+from gaussian_splats_hip.splats import GaussianSplat, PinholeCamera, rasterize, rasterize_views
 
 pytestmark = pytest.mark.gpu
 

@@ -51,3 +51,4 @@ def test_regularizers_match_torch_autograd():
     assert vb == pytest.approx(float(b.detach()), rel=1e-14)
     np.testing.assert_allclose(ga, to.grad.numpy(), rtol=1e-13)
     np.testing.assert_allclose(2 * gb, ts.grad.numpy(), rtol=1e-13)
+

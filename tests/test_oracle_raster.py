@@ -89,6 +89,108 @@ def test_rectangles_are_conservative():
         assert ty.min() >= bounds[gi, 1, 0] and ty.max() < bounds[gi, 1, 1]
 
 
+def _hand_projected(rows):
+    """Projected splats built directly from (u, v, depth, var_x, var_y, alpha0)
+    rows: isotropic or axis-aligned screen covariances of chosen size."""
+    t = torch.tensor(rows, dtype=torch.float64)
+    n = len(rows)
+    cov = torch.zeros(n, 2, 2, dtype=torch.float64)
+    cov[:, 0, 0], cov[:, 1, 1] = t[:, 3], t[:, 4]
+    inv = torch.zeros_like(cov)
+    inv[:, 0, 0], inv[:, 1, 1] = 1 / t[:, 3], 1 / t[:, 4]
+    return orc.Projected(t[:, :3].clone(), cov, inv, torch.zeros(n, 3, dtype=torch.float64),
+                         t[:, 5:6].clone())
+
+
+# alpha0 with ln(255 alpha0) = 4, so the gaussian-mode extent 2 sqrt(ln(255 alpha0)) is 4.
+ALPHA_EXT4 = math.exp(4.0) / 255.0
+
+
+def test_rectangles_closed_form():
+    """Hand-computed tile rectangles (reference torch.py:89-108): extent
+    2 sqrt(ln(255 alpha)) times the screen standard deviation, floor of
+    (u -/+ r) / tile, +1 on the upper bound, clamps at 0 and the grid size,
+    the empty rectangle of alpha < 1/255 (NaN extent) and the ellipsoid
+    extent sqrt(-2 ln(1 - confidence)).  Tile 16 on a 10 x 8 grid."""
+    ts, tw, th = 16, 10, 8
+    rows = [
+        # u, v, depth, var_x, var_y, alpha0      -> r = 4 * sqrt(var)
+        (40.0, 40.0, 2.0, 4.0, 4.0, ALPHA_EXT4),    # r = 8: x [32, 48] -> tiles [2, 3+1)
+        (40.0, 40.0, 2.0, 3.9, 3.9, ALPHA_EXT4),    # r < 8: 47.9 -> tile 2, upper bound 3
+        (60.0, 100.0, 2.0, 25.0, 1.0, ALPHA_EXT4),  # r = (20, 4): x [40, 80] -> [2, 6), y [96, 104] -> [6, 7)
+        (-5.0, 20.0, 2.0, 4.0, 4.0, ALPHA_EXT4),    # floor(-13/16) = -1 clamps to 0
+        (158.0, 124.0, 2.0, 4.0, 4.0, ALPHA_EXT4),  # floor(166/16) + 1 = 11 clamps to 10; y 8 -> 8
+        (-100.0, 20.0, 2.0, 4.0, 4.0, ALPHA_EXT4),  # entirely left: [0, 0)
+        (40.0, 40.0, 2.0, 4.0, 4.0, 0.9 / 255.0),   # alpha < 1/255: NaN extent -> empty
+        (40.0, 40.0, 2.0, 4.0, 4.0, 1.0 / 255.0),   # alpha = 1/255: extent 0, the pixel's tile
+        (40.0, 40.0, 0.1, 4.0, 4.0, ALPHA_EXT4),    # culled (depth <= near): count 0
+    ]
+    bounds, counts = orc.tile_counts(_hand_projected(rows), ts, tw, th, 0.2, 100.0)
+    expected = [
+        ((2, 4), (2, 4)),
+        ((2, 3), (2, 3)),
+        ((2, 6), (6, 7)),
+        ((0, 1), (0, 2)),
+        ((9, 10), (7, 8)),
+        ((0, 0), (0, 2)),
+        ((0, 0), (0, 0)),
+        ((2, 3), (2, 3)),
+        ((2, 4), (2, 4)),
+    ]
+    assert bounds.tolist() == [[list(x), list(y)] for x, y in expected]
+    assert counts.tolist() == [4, 1, 4, 2, 1, 0, 0, 1, 0]
+
+    # Ellipsoid mode: extent sqrt(-2 ln(1 - 0.95)) = 2.4477..., var 25 -> r = 12.24.
+    rows = [(40.0, 40.0, 2.0, 25.0, 25.0, 0.5), (64.0, 64.0, 2.0, 25.0, 25.0, 0.001)]
+    bounds, counts = orc.tile_counts(_hand_projected(rows), ts, tw, th, 0.2, 100.0, "ellipsoid", 0.95)
+    # 40 -/+ 12.24 = 27.76, 52.24 -> tiles [1, 4); 64 -/+ 12.24 -> [3, 5) (opacity ignored)
+    assert bounds.tolist() == [[[1, 4], [1, 4]], [[3, 5], [3, 5]]]
+    assert counts.tolist() == [9, 4]
+    # confidence 0.5: extent sqrt(2 ln 2) = 1.1774, r = 5.89 -> 40 +/- 5.89 -> [2, 3)
+    bounds, _ = orc.tile_counts(_hand_projected(rows[:1]), ts, tw, th, 0.2, 100.0, "ellipsoid", 0.5)
+    assert bounds.tolist() == [[[2, 3], [2, 3]]]
+
+
+def test_rectangles_equal_the_tile_box_of_the_extent_ellipse():
+    """Tightness: for random anisotropic screen covariances the rectangle is
+    exactly the tile bounding box of the ellipse {d : d^T cov^-1 d <= e^2},
+    e = 2 sqrt(ln(255 alpha)), found by sampling its boundary densely (no
+    use of the closed-form half-widths); edge cases within 1e-3 px of a tile
+    boundary are skipped.  A wrong extent constant moves some boxes."""
+    rng = np.random.default_rng(3)
+    n, ts, tw, th = 400, 8, 40, 30
+    u = rng.uniform(-20, 340, n)
+    v = rng.uniform(-20, 260, n)
+    sx, sy = np.exp(rng.uniform(0.0, 3.0, n)), np.exp(rng.uniform(0.0, 3.0, n))
+    rho = rng.uniform(-0.9, 0.9, n)
+    alpha0 = rng.uniform(1.2 / 255, 0.99, n)
+    cov = np.stack((sx * sx, rho * sx * sy, rho * sx * sy, sy * sy), -1).reshape(n, 2, 2)
+    proj = orc.Projected(
+        torch.tensor(np.stack((u, v, np.full(n, 2.0)), -1)), torch.tensor(cov),
+        torch.tensor(np.linalg.inv(cov)), torch.zeros(n, 3, dtype=torch.float64),
+        torch.tensor(alpha0[:, None]),
+    )
+    bounds, counts = orc.tile_counts(proj, ts, tw, th, 0.2, 100.0)
+    theta = np.linspace(0, 2 * np.pi, 200_001)
+    circle = np.stack((np.cos(theta), np.sin(theta)))
+    checked = 0
+    for i in range(n):
+        e = 2 * math.sqrt(math.log(255 * alpha0[i]))
+        pts = e * np.linalg.cholesky(cov[i]) @ circle
+        lo = np.array([u[i], v[i]]) + pts.min(1)
+        hi = np.array([u[i], v[i]]) + pts.max(1)
+        edges = np.concatenate((lo, hi)) / ts
+        if np.min(np.abs(edges - np.round(edges))) * ts < 1e-3:
+            continue
+        checked += 1
+        box = np.stack((np.floor(lo / ts), np.floor(hi / ts) + 1), -1)
+        box = np.clip(box, 0, np.array([[tw], [th]]))
+        assert bounds[i].tolist() == box.astype(int).tolist(), i
+        size = box[:, 1] - box[:, 0]
+        assert counts[i] == size[0] * size[1]
+    assert checked > 350
+
+
 def _brute_force(proj, w, h, near, far, thr=0.999):
     """Per pixel, every visible Gaussian in (depth bits, index) order, float64."""
     depth = proj.mean[:, 2].numpy()
@@ -239,3 +341,53 @@ def test_absolute_mean_gradient_terms_sum_to_the_gradient():
     torch.testing.assert_close(absolute[0], absolute[1], rtol=1e-12, atol=1e-15)
     assert float(absolute[0].sum()) > float(
         torch.stack((leaves[0].grad, leaves[1].grad), 1).abs().sum()) * (1 + 1e-6)
+
+
+def _lists(proj, ts, tw, th, near=0.1, far=100.0):
+    bounds, counts = orc.tile_counts(proj, ts, tw, th, near, far)
+    keys, ids = orc.emit_intersections(bounds, proj.mean[:, 2].float().numpy(), counts, tw)
+    sid, ranges, _ = orc.sort_intersections(keys, ids, tw * th)
+    return sid, ranges
+
+
+def test_fixed_decisions_replay():
+    """Replaying a run's own cut/clamp decisions and activity counts gives the
+    same image and gradients; float64 with float32's decisions equals float64
+    wherever their decisions agree; a wrong activity count changes the image."""
+    params, cam = _scene(n=80, w=48, h=32, log_scale=-1.6)
+    proj = orc.project(*params, cam)
+    ts, tw, th = 8, 6, 4
+    sid, ranges = _lists(proj, ts, tw, th)
+    g = torch.Generator().manual_seed(3)
+    w_img = torch.rand(32, 48, 3, generator=g, dtype=torch.float64)
+
+    def run(dt, **kw):
+        leaves = [x.detach().to(dt).clone().requires_grad_(True) for x in (
+            proj.mean[:, 0], proj.mean[:, 1], proj.inverse[:, 0, 0], proj.inverse[:, 0, 1],
+            proj.inverse[:, 1, 1], proj.color, proj.opacity[:, 0])]
+        c = orc.composite(*leaves, sid, ranges, 48, 32, ts, tile_chunk=3, **kw)
+        (c.image * w_img.to(dt)).sum().backward()
+        return c, [x.grad for x in leaves]
+
+    c32, g32 = run(torch.float32)
+    r32, h32 = run(torch.float32, decisions=c32.decisions, active_counts=c32.n_contributors.numpy())
+    assert torch.equal(c32.image, r32.image) and torch.equal(c32.n_contributors, r32.n_contributors)
+    assert all(torch.equal(a, b) for a, b in zip(g32, h32))
+
+    c64, g64 = run(torch.float64)
+    f64, k64 = run(torch.float64, decisions=c32.decisions, active_counts=c32.n_contributors.numpy())
+    same = c64.gaussian_margin > 1e-5  # float32 and float64 decide alike there
+    assert float(same.double().mean()) > 0.5
+    pix = torch.as_tensor(c64.margin >= 1e-5)
+    assert torch.allclose(c64.image[pix], f64.image[pix], rtol=0, atol=1e-12)
+    for a, b in zip(g64, k64):
+        assert torch.allclose(a[same], b[same], rtol=1e-10, atol=1e-12)
+
+    fewer = np.maximum(c32.n_contributors.numpy() - 1, 0)
+    bad, _ = run(torch.float64, decisions=c32.decisions, active_counts=fewer)
+    assert float((bad.image - f64.image).detach().abs().max()) > 1e-3
+    with pytest.raises(ValueError):
+        orc.composite(*(x.detach() for x in (
+            proj.mean[:, 0], proj.mean[:, 1], proj.inverse[:, 0, 0], proj.inverse[:, 0, 1],
+            proj.inverse[:, 1, 1], proj.color, proj.opacity[:, 0])), sid, ranges, 48, 32, ts,
+            rendering_mode="ellipsoid", active_counts=fewer)

@@ -1,0 +1,97 @@
+"""The parity tests' own checkers, pinned on the CPU: the proof that a set of
+tile lists is exactly the stable (tile, depth, index) sort, which the full-size
+GPU tests rely on, must accept the oracle's lists and reject each kind of
+mistake (a swapped pair, a dropped, repeated or foreign entry, a wrong range);
+the gradient criterion must accept and reject at its stated bounds."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import rasterizer as orc
+from parity import assert_gradients_close, assert_lists_exact, oracle_tile_lists, restrict_lists
+
+
+def _case(seed=0, n=400, tw=13, th=9):
+    rng = np.random.default_rng(seed)
+    x = np.sort(rng.integers(0, tw + 1, size=(n, 2)), 1)
+    y = np.sort(rng.integers(0, th + 1, size=(n, 2)), 1)
+    bounds = np.stack((x, y), 1).astype(np.int32)
+    counts = ((x[:, 1] - x[:, 0]) * (y[:, 1] - y[:, 0])).astype(np.int32)
+    counts[rng.random(n) < 0.1] = 0
+    depth = (rng.integers(1, 40, size=n) / 8).astype(np.float32)  # ties
+    keys, ids = orc.emit_intersections(bounds, depth, counts, tw)
+    sid, ranges, _ = orc.sort_intersections(keys, ids, tw * th)
+    t = lambda a: torch.as_tensor(np.ascontiguousarray(a))
+    return t(sid), t(ranges), t(bounds), t(counts), t(depth), tw
+
+
+def test_list_proof_accepts_the_oracle_lists():
+    gids, ranges, bounds, counts, depth, tw = _case()
+    stats = assert_lists_exact(gids, ranges, bounds, counts, depth, tw, chunk=97)
+    assert stats["intersections"] == gids.numel() > 1000
+
+
+@pytest.mark.parametrize("mistake", ["swap", "drop", "repeat", "foreign", "range", "uncounted"])
+def test_list_proof_rejects_mistakes(mistake):
+    gids, ranges, bounds, counts, depth, tw = _case(seed=1)
+    gids, ranges, counts = gids.clone(), ranges.clone(), counts.clone()
+    lengths = (ranges[:, 1] - ranges[:, 0]).numpy()
+    t = int(np.argmax(lengths))
+    s = int(ranges[t, 0])
+    if mistake == "swap":  # two entries of one tile exchanged
+        gids[s], gids[s + 1] = gids[s + 1].clone(), gids[s].clone()
+    elif mistake == "drop":  # last entry of a tile replaced by the next tile's first
+        e = int(ranges[t, 1])
+        gids[e - 1] = gids[e] if e < gids.numel() else gids[0]
+    elif mistake == "repeat":
+        gids[s + 1] = gids[s]
+    elif mistake == "foreign":  # a Gaussian whose rectangle misses the tile
+        tx, ty = t % tw, t // tw
+        b = bounds.reshape(-1, 4)
+        miss = ~((b[:, 0] <= tx) & (tx < b[:, 1]) & (b[:, 2] <= ty) & (ty < b[:, 3]))
+        gids[s] = int(torch.nonzero(miss & (counts > 0))[0])
+    elif mistake == "range":  # one entry moved across a tile boundary
+        ranges[t, 1] -= 1
+        ranges[t + 1, 0] -= 1
+    else:  # a listed Gaussian marked as culled
+        counts[int(gids[s])] = 0
+    with pytest.raises(AssertionError):
+        assert_lists_exact(gids, ranges, bounds, counts, depth, tw, chunk=64)
+
+
+def test_oracle_tile_lists_and_restriction_match_the_full_sort():
+    gids, ranges, bounds, counts, depth, tw = _case(seed=2)
+    tiles = [0, 5, 17, 40, 100]
+    ids, r = oracle_tile_lists(bounds.numpy(), counts.numpy(), depth.numpy(), tiles, tw, ranges.shape[0])
+    ids2, r2 = restrict_lists(gids.numpy(), ranges.numpy(), tiles)
+    assert np.array_equal(ids, ids2) and np.array_equal(r, r2)
+    limits = {t: 3 for t in tiles}
+    ids3, r3 = restrict_lists(gids.numpy(), ranges.numpy(), tiles, limits)
+    ids4, r4 = oracle_tile_lists(bounds.numpy(), counts.numpy(), depth.numpy(), tiles, tw,
+                                 ranges.shape[0], limits)
+    assert np.array_equal(ids3, ids4) and np.array_equal(r3, r4)
+    assert int((r3[:, 1] - r3[:, 0]).max()) <= 3
+
+
+def test_gradient_criterion_bounds():
+    e = torch.tensor([[2.0, 1e-3], [-4.0, 0.0], [0.5, 2e-3]])
+    ok = e * (1 + 0.9e-4)
+    assert_gradients_close(ok, e, "within rtol")
+    # The absolute term is 1e-6 * min(1, column max): 1e-6 on column 0 ...
+    assert_gradients_close(e + torch.tensor([[0.0, 0.0], [0.0, 0.0], [0.0, 0.0]]), e, "exact")
+    bad = e.clone()
+    bad[1, 0] += 4.0 * 1e-4 + 2e-6
+    with pytest.raises(AssertionError):
+        assert_gradients_close(bad, e, "beyond rtol + atol")
+    # ... and 1e-6 * 2e-3 on column 1, whose entries are all small.
+    bad = e.clone()
+    bad[1, 1] = 3e-9
+    with pytest.raises(AssertionError):
+        assert_gradients_close(bad, e, "small column")
+    assert_gradients_close(bad, e, "explained", explained=torch.tensor([False, True, False]),
+                           max_explained=0.34)
+    with pytest.raises(AssertionError):
+        assert_gradients_close(bad, e, "unexplained", explained=torch.tensor([True, False, True]))

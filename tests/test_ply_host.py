@@ -11,8 +11,8 @@ import numpy as np
 import pytest
 import torch
 
-from gaussian_splats.splats import GaussianSplat
-from gaussian_splats.splats.ply import load_ply, save_ply
+from gaussian_splats_hip.splats import GaussianSplat
+from gaussian_splats_hip.splats.ply import load_ply, save_ply
 from oracle import ply as oply
 from tests import plyfiles
 
@@ -247,7 +247,7 @@ def test_save_ply_rejects_bad_color_shape(tmp_path):
 def test_splat_round_trip_and_convert_commands(tmp_path):
     from typer.testing import CliRunner
 
-    from gaussian_splats.splats.convert import app
+    from gaussian_splats_hip.splats.convert import app
 
     torch.manual_seed(0)
     splats = GaussianSplat(41, sh_degree=2)
@@ -271,7 +271,7 @@ def test_ply_kernels_host_checks():
     """The C ABI validates sizes, offsets and alignment before any launch."""
     import ctypes
 
-    from gaussian_splats.kernels.rasterize import _native as nat
+    from gaussian_splats_hip.kernels.rasterize import _native as nat
 
     lib = nat.library()
     fake = ctypes.c_void_p(256)

@@ -7,9 +7,9 @@ import math
 import pytest
 import torch
 
-from gaussian_splats.kernels.rasterize.intersections import MAX_BUCKET_TILES
-from gaussian_splats.kernels.rasterize.views import camera_tensors, mosaic_columns
-from gaussian_splats.splats import PinholeCamera
+from gaussian_splats_hip.kernels.rasterize.intersections import MAX_BUCKET_TILES
+from gaussian_splats_hip.kernels.rasterize.views import camera_tensors, mosaic_columns
+from gaussian_splats_hip.splats import PinholeCamera
 
 
 @pytest.mark.parametrize("views", [1, 2, 3, 5, 16, 17, 40])

@@ -108,7 +108,9 @@ def stage_bytes(n, k, total, rows, pixels, processed_fwd, processed_bwd):
         "emit": 8 * rows + 8 * rows + 8 * rows + 4 * total,
         "composite": 40 * processed_fwd + 20 * pixels,
         "composite_bwd": 76 * processed_bwd + 20 * pixels,
-        "project_bwd": 2 * n * (44 + 12 * k) + 56 * n,
+        # params in and gradients out; per Gaussian its 9 gradient inputs and
+        # count (the 2-D inverse is recomputed, not read)
+        "project_bwd": 2 * n * (44 + 12 * k) + 40 * n,
     }
 
 
@@ -246,11 +248,11 @@ def views_stage_bytes(n, k, views, total, rows, pixels, processed_fwd, processed
     """Algorithmic HBM bytes per stage of the multi-view step: the projection
     reads the parameters once per launch of up to 16 cameras and writes the
     116 B of outputs per (view, Gaussian); the backward reads the parameters
-    once, 56 B per (view, Gaussian) and writes the gradients once."""
+    once, 40 B per (view, Gaussian) and writes the gradients once."""
     launches = -(-views // 16)
     single = stage_bytes(views * n, k, total, rows, pixels, processed_fwd, processed_bwd)
     single["project"] = launches * n * (44 + 12 * k) + 116 * views * n
-    single["project_bwd"] = (launches + 1) * n * (44 + 12 * k) + 56 * views * n
+    single["project_bwd"] = (launches + 1) * n * (44 + 12 * k) + 40 * views * n
     return single
 
 

@@ -178,8 +178,13 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_bwd_kernel(Com
         const bool hit = pos < ncon[k] && clamped >= kMinAlpha;
         const float alpha = hit ? clamped : 0.0f;
         touched |= hit;
-        // alpha = 0 leaves T unchanged: v_rcp_f32(1) is exactly 1.
-        const float t_before = T[k] * __builtin_amdgcn_rcpf(1.0f - alpha);
+        // T before the entry = T after it / (1 - alpha), with 1 / (1 - alpha)
+        // formed as 1 + alpha / (1 - alpha): v_rcp_f32's error (up to an ulp,
+        // of one sign) then enters scaled by alpha, so walking back through
+        // thousands of small-alpha entries does not accumulate it (with the
+        // plain reciprocal: ~2e-4 relative after 1600 entries).  alpha = 0
+        // gives exactly 1.
+        const float t_before = T[k] * fmaf(alpha, __builtin_amdgcn_rcpf(1.0f - alpha), 1.0f);
         const float w = t_before * alpha;
         sr += gr[k] * w;
         sg += gg[k] * w;

@@ -39,7 +39,6 @@ struct ProjectBwdArgs {
   int views;             // cameras in cam[]; view v's inputs are at v * view_stride Gaussians
   int64_t view_stride;   // Gaussians between consecutive views' inputs (n for one view)
   bool accumulate;       // add to the gradient buffers instead of overwriting them
-  const float* inv;      // [views, N, 4]
   const float* grad_in;  // [views, N, 9]
   const int32_t* counts;  // [views, N]
   int64_t n;
@@ -58,10 +57,9 @@ struct ProjectBwdArgs {
 template <int K>
 __device__ __forceinline__ void view_gradients(
     const ProjectBwdArgs& a, const BwdCamera& cam, int64_t gi, int64_t vi, float mx, float myy,
-    float mz, const float (&R)[3][3], const float (&s3)[3], float alpha0, const float (&coef)[3 * K],
-    float& gmx, float& gmy, float& gmz, float (&h)[4], float (&gs3)[3], float& gop,
-    float (&gcoef)[3 * K], float qw, float qx, float qy, float qz, const float (&gin)[9],
-    float4 inv) {
+    float mz, const double (&q)[4], const double (&sd)[3], float alpha0,
+    const float (&coef)[3 * K], float& gmx, float& gmy, float& gmz, float (&h)[4],
+    float (&gs3)[3], float& gop, float (&gcoef)[3 * K], const float (&gin)[9]) {
   const float r00 = cam.r[0], r01 = cam.r[1], r02 = cam.r[2];
   const float r10 = cam.r[3], r11 = cam.r[4], r12 = cam.r[5];
   const float r20 = cam.r[6], r21 = cam.r[7], r22 = cam.r[8];
@@ -122,98 +120,126 @@ __device__ __forceinline__ void view_gradients(
   // ---- opacity: alpha0 = sigmoid(o) ----
   gop += gal * alpha0 * (1.0f - alpha0);
 
-  // ---- forward recomputation ----
-  const float px = r00 * mx + r01 * myy + r02 * mz + t0;
-  const float py = r10 * mx + r11 * myy + r12 * mz + t1;
-  const float pz = r20 * mx + r21 * myy + r22 * mz + t2;
-  const float d = -pz;
-  const bool depth_free = fabsf(d) >= 1e-4f;
-  const float dc = depth_free ? d : copysignf(1e-4f, d);
-  const float rx = px / dc, ry = py / dc;
-  const bool in_x = rx >= -cam.lim_x && rx <= cam.lim_x;
-  const bool in_y = ry >= -cam.lim_y && ry <= cam.lim_y;
-  const float nx = fminf(fmaxf(rx, -cam.lim_x), cam.lim_x);
-  const float ny = fminf(fmaxf(ry, -cam.lim_y), cam.lim_y);
-  const float j00 = cam.fx / dc, j02 = cam.fx * nx / dc;
-  const float j11 = -cam.fy / dc, j12 = -cam.fy * ny / dc;
-  const float w0[3] = {j00 * r00 + j02 * r20, j00 * r01 + j02 * r21, j00 * r02 + j02 * r22};
-  const float w1[3] = {j11 * r10 + j12 * r20, j11 * r11 + j12 * r21, j11 * r12 + j12 * r22};
+  // ---- the covariance chain, in double precision ----
+  // The chain from the parameters through the 2-D covariance and its inverse
+  // (J, W = J Rc, N = W Rq, M = N diag(s), Sigma = M M^T + eps I, inv) and
+  // back (dL/dSigma = -inv G inv, dL/dM, dL/dRq = W^T dN, the quaternion and
+  // Jacobian terms) is recomputed here in double from the parameters rather
+  // than taken from the forward's float32 inverse.  For a nearly degenerate
+  // Sigma (an edge-on flat splat, a needle) dL/dSigma and dL/dRq are up to
+  // ~1e4 times smaller than the products that form them, so in float32 every
+  // rounding on the way -- including the stored inverse's -- reaches the scale
+  // and rotation gradients amplified by that much (measured: percent-level
+  // errors on config 5's flat splats, 1e-4 on config 3's needles).  The chain
+  // is a few hundred fp64 operations per (Gaussian, view), a few microseconds
+  // per million Gaussians in a kernel bound by its memory traffic.
+  const double dr00 = r00, dr01 = r01, dr02 = r02, dr10 = r10, dr11 = r11, dr12 = r12;
+  const double dr20 = r20, dr21 = r21, dr22 = r22;
+  const double dmx = mx, dmy = myy, dmz = mz;
+  const double px = dr00 * dmx + dr01 * dmy + dr02 * dmz + double(t0);
+  const double py = dr10 * dmx + dr11 * dmy + dr12 * dmz + double(t1);
+  const double pz = dr20 * dmx + dr21 * dmy + dr22 * dmz + double(t2);
+  const double d = -pz;
+  const bool depth_free = fabs(d) >= 1e-4;
+  const double dc = depth_free ? d : copysign(1e-4, d);
+  const double rx = px / dc, ry = py / dc;
+  const double lim_x = cam.lim_x, lim_y = cam.lim_y;
+  const bool in_x = rx >= -lim_x && rx <= lim_x;
+  const bool in_y = ry >= -lim_y && ry <= lim_y;
+  const double nx = fmin(fmax(rx, -lim_x), lim_x);
+  const double ny = fmin(fmax(ry, -lim_y), lim_y);
+  const double fxd = cam.fx, fyd = cam.fy;
+  const double j00 = fxd / dc, j02 = fxd * nx / dc;
+  const double j11 = -fyd / dc, j12 = -fyd * ny / dc;
+  const double w0[3] = {j00 * dr00 + j02 * dr20, j00 * dr01 + j02 * dr21, j00 * dr02 + j02 * dr22};
+  const double w1[3] = {j11 * dr10 + j12 * dr20, j11 * dr11 + j12 * dr21, j11 * dr12 + j12 * dr22};
+  const double qw = q[0], qx = q[1], qy = q[2], qz = q[3];
+  const double R[3][3] = {
+      {1.0 - 2.0 * (qy * qy + qz * qz), 2.0 * (qx * qy - qw * qz), 2.0 * (qx * qz + qw * qy)},
+      {2.0 * (qx * qy + qw * qz), 1.0 - 2.0 * (qx * qx + qz * qz), 2.0 * (qy * qz - qw * qx)},
+      {2.0 * (qx * qz - qw * qy), 2.0 * (qy * qz + qw * qx), 1.0 - 2.0 * (qx * qx + qy * qy)}};
   // N = W Rq (2x3), M = N diag(s).
-  float N[2][3], M[2][3];
+  double N[2][3], M[2][3];
 #pragma unroll
   for (int c = 0; c < 3; ++c) {
     N[0][c] = w0[0] * R[0][c] + w0[1] * R[1][c] + w0[2] * R[2][c];
     N[1][c] = w1[0] * R[0][c] + w1[1] * R[1][c] + w1[2] * R[2][c];
-    M[0][c] = N[0][c] * s3[c];
-    M[1][c] = N[1][c] * s3[c];
+    M[0][c] = N[0][c] * sd[c];
+    M[1][c] = N[1][c] * sd[c];
   }
+  const double eps = a.eps;
+  const double c00 = M[0][0] * M[0][0] + M[0][1] * M[0][1] + M[0][2] * M[0][2] + eps;
+  const double c01 = M[0][0] * M[1][0] + M[0][1] * M[1][1] + M[0][2] * M[1][2];
+  const double c11 = M[1][0] * M[1][0] + M[1][1] * M[1][1] + M[1][2] * M[1][2] + eps;
+  const double rdet = 1.0 / (c00 * c11 - c01 * c01);
+  const double i00 = c11 * rdet, i01 = -c01 * rdet, i11 = c00 * rdet;
 
   // ---- through the 2x2 inverse: dL/dSigma = -inv G inv ----
-  const float i00 = inv.x, i01 = inv.y, i11 = inv.w;
-  const float t00 = i00 * gA + i01 * gB, t01 = i00 * gB + i01 * gC;
-  const float t10 = i01 * gA + i11 * gB, t11 = i01 * gB + i11 * gC;
-  const float k00 = -(t00 * i00 + t01 * i01);
-  const float k01 = -(t00 * i01 + t01 * i11);
-  const float k11 = -(t10 * i01 + t11 * i11);
+  const double dA = gA, dB = gB, dC = gC;
+  const double t00 = i00 * dA + i01 * dB, t01 = i00 * dB + i01 * dC;
+  const double t10 = i01 * dA + i11 * dB, t11 = i01 * dB + i11 * dC;
+  const double k00 = -(t00 * i00 + t01 * i01);
+  const double k01 = -(t00 * i01 + t01 * i11);
+  const double k11 = -(t10 * i01 + t11 * i11);
 
   // ---- Sigma = M M^T + eps I: dL/dM = 2 K M ----
-  float dN[2][3];
+  double dN[2][3];
 #pragma unroll
   for (int c = 0; c < 3; ++c) {
-    const float dm0 = 2.0f * (k00 * M[0][c] + k01 * M[1][c]);
-    const float dm1 = 2.0f * (k01 * M[0][c] + k11 * M[1][c]);
-    dN[0][c] = dm0 * s3[c];
-    dN[1][c] = dm1 * s3[c];
-    gs3[c] += (dm0 * N[0][c] + dm1 * N[1][c]) * s3[c];  // d/dlog s = d/ds * s
+    const double dm0 = 2.0 * (k00 * M[0][c] + k01 * M[1][c]);
+    const double dm1 = 2.0 * (k01 * M[0][c] + k11 * M[1][c]);
+    dN[0][c] = dm0 * sd[c];
+    dN[1][c] = dm1 * sd[c];
+    gs3[c] += float((dm0 * N[0][c] + dm1 * N[1][c]) * sd[c]);  // d/dlog s = d/ds * s
   }
   // dRq = W^T dN; dW = dN Rq^T.
-  float G[3][3];
+  double G[3][3];
 #pragma unroll
   for (int r = 0; r < 3; ++r)
 #pragma unroll
     for (int c = 0; c < 3; ++c) G[r][c] = w0[r] * dN[0][c] + w1[r] * dN[1][c];
-  float dW0[3], dW1[3];
+  double dW0[3], dW1[3];
 #pragma unroll
   for (int kk = 0; kk < 3; ++kk) {
     dW0[kk] = dN[0][0] * R[kk][0] + dN[0][1] * R[kk][1] + dN[0][2] * R[kk][2];
     dW1[kk] = dN[1][0] * R[kk][0] + dN[1][1] * R[kk][1] + dN[1][2] * R[kk][2];
   }
 
-  // ---- rotation matrix -> normalised quaternion ----
-  h[0] += 2.0f * (qz * (G[1][0] - G[0][1]) + qy * (G[0][2] - G[2][0]) + qx * (G[2][1] - G[1][2]));
-  h[1] += 2.0f * (qy * (G[0][1] + G[1][0]) + qz * (G[0][2] + G[2][0]) + qw * (G[2][1] - G[1][2])) -
-          4.0f * qx * (G[1][1] + G[2][2]);
-  h[2] += 2.0f * (qx * (G[0][1] + G[1][0]) + qw * (G[0][2] - G[2][0]) + qz * (G[1][2] + G[2][1])) -
-          4.0f * qy * (G[0][0] + G[2][2]);
-  h[3] += 2.0f * (qw * (G[1][0] - G[0][1]) + qx * (G[0][2] + G[2][0]) + qy * (G[1][2] + G[2][1])) -
-          4.0f * qz * (G[0][0] + G[1][1]);
+  // ---- rotation matrix -> normalised quaternion (this view's term rounded once) ----
+  h[0] += float(2.0 * (qz * (G[1][0] - G[0][1]) + qy * (G[0][2] - G[2][0]) + qx * (G[2][1] - G[1][2])));
+  h[1] += float(2.0 * (qy * (G[0][1] + G[1][0]) + qz * (G[0][2] + G[2][0]) + qw * (G[2][1] - G[1][2])) -
+                4.0 * qx * (G[1][1] + G[2][2]));
+  h[2] += float(2.0 * (qx * (G[0][1] + G[1][0]) + qw * (G[0][2] - G[2][0]) + qz * (G[1][2] + G[2][1])) -
+                4.0 * qy * (G[0][0] + G[2][2]));
+  h[3] += float(2.0 * (qw * (G[1][0] - G[0][1]) + qx * (G[0][2] + G[2][0]) + qy * (G[1][2] + G[2][1])) -
+                4.0 * qz * (G[0][0] + G[1][1]));
 
   // ---- W = J Rc: dJ entries ----
-  const float dj00 = dW0[0] * r00 + dW0[1] * r01 + dW0[2] * r02;
-  const float dj02 = dW0[0] * r20 + dW0[1] * r21 + dW0[2] * r22;
-  const float dj11 = dW1[0] * r10 + dW1[1] * r11 + dW1[2] * r12;
-  const float dj12 = dW1[0] * r20 + dW1[1] * r21 + dW1[2] * r22;
+  const double dj00 = dW0[0] * dr00 + dW0[1] * dr01 + dW0[2] * dr02;
+  const double dj02 = dW0[0] * dr20 + dW0[1] * dr21 + dW0[2] * dr22;
+  const double dj11 = dW1[0] * dr10 + dW1[1] * dr11 + dW1[2] * dr12;
+  const double dj12 = dW1[0] * dr20 + dW1[1] * dr21 + dW1[2] * dr22;
 
   // ---- camera-space point ----
   // u = fx x / d + cx and v = -fy y / d + cy use the unclamped depth.
-  const float d2 = d * d;
-  float gpx = gu * cam.fx / d;
-  float gpy = -gv * cam.fy / d;
-  float gd = -gu * cam.fx * px / d2 + gv * cam.fy * py / d2;
+  const double d2 = d * d;
+  double gpx = gu * fxd / d;
+  double gpy = -gv * fyd / d;
+  double gd = -gu * fxd * px / d2 + gv * fyd * py / d2;
   // Jacobian terms use the clamped depth dc.
-  const float dc2 = dc * dc, dc3 = dc2 * dc;
-  if (in_x) gpx += dj02 * cam.fx / dc2;
-  if (in_y) gpy += dj12 * (-cam.fy / dc2);
+  const double dc2 = dc * dc, dc3 = dc2 * dc;
+  if (in_x) gpx += dj02 * fxd / dc2;
+  if (in_y) gpy += dj12 * (-fyd / dc2);
   if (depth_free) {
-    float gdc = -dj00 * cam.fx / dc2 + dj11 * cam.fy / dc2;
-    gdc += dj02 * (-cam.fx * nx / dc2 - (in_x ? cam.fx * px / dc3 : 0.0f));
-    gdc += dj12 * (cam.fy * ny / dc2 + (in_y ? cam.fy * py / dc3 : 0.0f));
+    double gdc = -dj00 * fxd / dc2 + dj11 * fyd / dc2;
+    gdc += dj02 * (-fxd * nx / dc2 - (in_x ? fxd * px / dc3 : 0.0));
+    gdc += dj12 * (fyd * ny / dc2 + (in_y ? fyd * py / dc3 : 0.0));
     gd += gdc;
   }
-  const float gpz = -gd;
-  gmx += r00 * gpx + r10 * gpy + r20 * gpz;
-  gmy += r01 * gpx + r11 * gpy + r21 * gpz;
-  gmz += r02 * gpx + r12 * gpy + r22 * gpz;
+  const double gpz = -gd;
+  gmx += float(dr00 * gpx + dr10 * gpy + dr20 * gpz);
+  gmy += float(dr01 * gpx + dr11 * gpy + dr21 * gpz);
+  gmz += float(dr02 * gpx + dr12 * gpy + dr22 * gpz);
 
 }
 
@@ -245,11 +271,9 @@ __global__ __launch_bounds__(kBlock) void project_bwd_kernel(ProjectBwdArgs a) {
   const int32_t count0 = a.counts[gl];
   // One view: its gradient inputs too.
   float gin0[9];
-  float4 inv0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   if (!MULTI) {
 #pragma unroll
     for (int i = 0; i < 9; ++i) gin0[i] = a.grad_in[gl * 9 + i];
-    inv0 = reinterpret_cast<const float4*>(a.inv)[gl];
   }
   sh::stage_block<F, kBlock>(a.color + base * F, nvalid, coeff);
   __syncthreads();
@@ -262,35 +286,26 @@ __global__ __launch_bounds__(kBlock) void project_bwd_kernel(ProjectBwdArgs a) {
   for (int i = 0; i < F; ++i) gcoef[i] = 0.0f;
   bool any = have && count0 != 0;
   for (int v = 1; have && v < views; ++v) any |= a.counts[v * a.view_stride + gi] != 0;
-  float q[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  float qnorm = 0.0f;
+  double q[4] = {0.0, 0.0, 0.0, 0.0};
+  double qnorm = 0.0;
   if (any) {
     // Parameters are read once, only for Gaussians some view counted.
     float coef[F];
 #pragma unroll
     for (int i = 0; i < F; ++i) coef[i] = coeff[threadIdx.x * S + i];
     const float alpha0 = 1.0f / (1.0f + expf(-lop));
-    qnorm = sqrtf(qr.x * qr.x + qr.y * qr.y + qr.z * qr.z + qr.w * qr.w);
-    const float qn = fmaxf(qnorm, 1e-12f);
+    // The normalised quaternion and the scales in double (see view_gradients).
+    qnorm = sqrt(double(qr.x) * qr.x + double(qr.y) * qr.y + double(qr.z) * qr.z +
+                 double(qr.w) * qr.w);
+    const double qn = fmax(qnorm, 1e-12);
     q[0] = qr.x / qn;
     q[1] = qr.y / qn;
     q[2] = qr.z / qn;
     q[3] = qr.w / qn;
-    const float qw = q[0], qx = q[1], qy = q[2], qz = q[3];
-    float R[3][3];
-    R[0][0] = 1.0f - 2.0f * (qy * qy + qz * qz);
-    R[0][1] = 2.0f * (qx * qy - qw * qz);
-    R[0][2] = 2.0f * (qx * qz + qw * qy);
-    R[1][0] = 2.0f * (qx * qy + qw * qz);
-    R[1][1] = 1.0f - 2.0f * (qx * qx + qz * qz);
-    R[1][2] = 2.0f * (qy * qz - qw * qx);
-    R[2][0] = 2.0f * (qx * qz - qw * qy);
-    R[2][1] = 2.0f * (qy * qz + qw * qx);
-    R[2][2] = 1.0f - 2.0f * (qx * qx + qy * qy);
-    const float s3[3] = {expf(ls0), expf(ls1), expf(ls2)};
+    const double sd[3] = {exp(double(ls0)), exp(double(ls1)), exp(double(ls2))};
     if (!MULTI) {  // count0 != 0 here
-      view_gradients<K>(a, a.cam[0], gi, gi, mx, myy, mz, R, s3, alpha0, coef, gmx, gmy, gmz, h,
-                        gs3, gop, gcoef, qw, qx, qy, qz, gin0, inv0);
+      view_gradients<K>(a, a.cam[0], gi, gi, mx, myy, mz, q, sd, alpha0, coef, gmx, gmy, gmz, h,
+                        gs3, gop, gcoef, gin0);
     } else {
       for (int v = 0; v < views; ++v) {
         const int64_t vi = v * a.view_stride + gi;
@@ -298,19 +313,20 @@ __global__ __launch_bounds__(kBlock) void project_bwd_kernel(ProjectBwdArgs a) {
         float gin[9];
 #pragma unroll
         for (int i = 0; i < 9; ++i) gin[i] = a.grad_in[vi * 9 + i];
-        const float4 inv = reinterpret_cast<const float4*>(a.inv)[vi];
-        view_gradients<K>(a, a.cam[v], gi, vi, mx, myy, mz, R, s3, alpha0, coef, gmx, gmy, gmz,
-                          h, gs3, gop, gcoef, qw, qx, qy, qz, gin, inv);
+        view_gradients<K>(a, a.cam[v], gi, vi, mx, myy, mz, q, sd, alpha0, coef, gmx, gmy, gmz,
+                          h, gs3, gop, gcoef, gin);
       }
     }
   }
   // ---- normalised quaternion -> raw quaternion (linear in h, so once) ----
   float gq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   if (any) {
-    if (qnorm > 1e-12f) {
-      const float dot = q[0] * h[0] + q[1] * h[1] + q[2] * h[2] + q[3] * h[3];
+    if (qnorm > 1e-12) {
+      // The normalisation's Jacobian removes h's radial part, which can be
+      // much larger than the result: formed in double.
+      const double dot = q[0] * h[0] + q[1] * h[1] + q[2] * h[2] + q[3] * h[3];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) gq[i] = (h[i] - q[i] * dot) / qnorm;
+      for (int i = 0; i < 4; ++i) gq[i] = float((h[i] - q[i] * dot) / qnorm);
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i) gq[i] = h[i] / 1e-12f;
@@ -366,7 +382,7 @@ int project_bwd_views(const float* mean, const float* rotation, const float* sca
                       const float* opacity, const float* color, int64_t n, int32_t num_sh,
                       const float* camera_rotations, const float* camera_translations,
                       const float* intrinsics, int views, gs_view view,
-                      const float* inverse_covariance, const float* grad_projected,
+                      const float* /*inverse_covariance*/, const float* grad_projected,
                       const int32_t* counts, float* grad_mean, float* grad_rotation,
                       float* grad_scale, float* grad_opacity, float* grad_color, void* stream) {
   GS_REQUIRE(n >= 0, GS_ERR_INVALID_ARGUMENT, "negative Gaussian count");
@@ -374,11 +390,11 @@ int project_bwd_views(const float* mean, const float* rotation, const float* sca
              "SH degrees above 3 are not implemented (got %d coefficients)", num_sh);
   if (n == 0) return GS_OK;
   GS_REQUIRE(mean && rotation && scale && opacity && color && camera_rotations &&
-                 camera_translations && inverse_covariance && grad_projected && counts &&
+                 camera_translations && grad_projected && counts &&
                  grad_mean && grad_rotation && grad_scale && grad_opacity && grad_color,
              GS_ERR_INVALID_ARGUMENT, "null pointer argument");
-  GS_REQUIRE(aligned16(rotation) && aligned16(color) && aligned16(inverse_covariance) &&
-                 aligned16(grad_rotation) && aligned16(grad_color),
+  GS_REQUIRE(aligned16(rotation) && aligned16(color) && aligned16(grad_rotation) &&
+                 aligned16(grad_color),
              GS_ERR_INVALID_ARGUMENT, "rotation/color buffers must be 16-byte aligned");
   GS_REQUIRE(int64_t(views) * n < (int64_t(1) << 31), GS_ERR_OVERFLOW,
              "too many Gaussians (%lld x %d views)", (long long)n, views);
@@ -414,7 +430,6 @@ int project_bwd_views(const float* mean, const float* rotation, const float* sca
       c.lim_y = float(1.3 * (double(view.image_height) / (2.0 * double(c.fy))));
     }
     const int64_t off = int64_t(first) * n;
-    a.inv = inverse_covariance + off * 4;
     a.grad_in = grad_projected + off * 9;
     a.counts = counts + off;
     a.accumulate = first > 0;

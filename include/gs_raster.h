@@ -289,7 +289,11 @@ GS_API int gs_composite_bwd(
 
 /* Chain rule from grad_projected to the parameters.  Replaces project_bwd
  * (src/gaussian_splats/kernels/rasterize/project_bwd.py:8-381); gradients are
- * zero for Gaussians with count == 0 (project_bwd.py:32,324-334). */
+ * zero for Gaussians with count == 0 (project_bwd.py:32,324-334).
+ * inverse_covariance (the forward's output) is not read and may be null: the
+ * covariance chain is recomputed from the parameters in double precision,
+ * because for nearly degenerate 2-D covariances its gradient is far smaller
+ * than the float32 products that would form it. */
 GS_API int gs_project_bwd(
     const float* mean, const float* rotation, const float* scale,
     const float* opacity, const float* color, int64_t n, int32_t num_sh,

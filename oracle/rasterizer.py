@@ -246,7 +246,10 @@ class Composite:
     gaussian_margin: torch.Tensor  # [N] smallest margin over the pixels a Gaussian reaches
     # [N] as gaussian_margin, counting only the alpha cut and the 0.99 clamp
     # (the decisions a float32 run fixes for a replay; the activity test is
-    # fixed separately by active_counts).
+    # fixed separately by active_counts), each relative distance divided by
+    # 1 + the quadratic form with absolute terms (|a| dx^2 + 2|b dx dy| +
+    # |c| dy^2): alpha's float32 rounding error grows with it, and with
+    # cancellation in the form (near-degenerate covariances).
     gaussian_cut_margin: torch.Tensor
     # Per chunk start tile: (keep, clamped) booleans [entries, pixels] of the
     # alpha cut (alpha >= 1/255 after the clamp) and of the 0.99 clamp.
@@ -273,8 +276,15 @@ def composite(
     probe: list | None = None,
     decisions: dict | None = None,
     active_counts: np.ndarray | None = None,
+    transmittance: str = "log",
 ) -> Composite:
     """Dense per-(entry, pixel) compositing of each tile list (torch.py:172-225).
+
+    ``transmittance``: "log" (the reference's torch backend, torch.py:209-212:
+    exp of a float64 cumulative sum of log1p(-alpha)) or "product" (the
+    exclusive cumulative product of 1 - alpha in the working dtype, as a plain
+    float32 implementation such as the reference's Triton kernels forms it,
+    composite.py:97-98); the two agree to rounding.
 
     Fixed decisions: ``decisions`` (the ``decisions`` of an earlier call over
     the same lists and ``tile_chunk``, e.g. a float32 run) replaces the alpha
@@ -362,12 +372,26 @@ def composite(
             alpha = torch.where(alpha >= MIN_ALPHA, alpha, torch.zeros_like(alpha))
             with torch.no_grad():
                 recorded[t0] = (alpha > 0, raw > MAX_ALPHA)
-        log_survival = torch.log1p(-alpha)
-        # Segmented exclusive sum per tile, in float64 (torch.py:209-212).
-        cums = log_survival.to(torch.float64).cumsum(0) - log_survival.to(torch.float64)
         seg_start = torch.as_tensor(np.repeat(np.cumsum(counts) - counts, counts), dtype=torch.int64)
-        cums = cums - cums[seg_start]
-        T = torch.exp(cums).to(dt)
+        if transmittance == "log":
+            log_survival = torch.log1p(-alpha)
+            # Segmented exclusive sum per tile, in float64 (torch.py:209-212).
+            cums = log_survival.to(torch.float64).cumsum(0) - log_survival.to(torch.float64)
+            cums = cums - cums[seg_start]
+            T = torch.exp(cums).to(dt)
+        elif transmittance == "product":
+            # Segmented exclusive product per tile, in the working dtype.
+            survival = 1 - alpha
+            segs, pos0 = [], 0
+            for cnt in counts:
+                cnt = int(cnt)
+                if cnt:
+                    ones = torch.ones_like(survival[:1])
+                    segs.append(torch.cumprod(torch.cat((ones, survival[pos0:pos0 + cnt - 1])), 0))
+                pos0 += cnt
+            T = torch.cat(segs)
+        else:
+            raise ValueError(f"unknown transmittance form {transmittance!r}")
         rel = tile_of - t0
         if active_counts is not None:
             pos_in_tile = torch.arange(hi - lo) - seg_start
@@ -412,11 +436,19 @@ def composite(
             reach = considered & (alpha.detach() > 0)
             per_entry = torch.where(reach, torch.minimum(mm[rel], m_cl), torch.full_like(m_cl, math.inf))
             gmargin.index_reduce_(0, g, per_entry.amin(1), "amin")
-            # The same with the cut and clamp decisions only.
-            m_cc = torch.where(considered, torch.minimum(m_cut, m_cl), torch.full_like(m_cl, math.inf))
+            # The same with the cut and clamp decisions only, in units of
+            # alpha's rounding sensitivity.
+            ddx, ddy = dx.detach().to(torch.float64), dy.detach().to(torch.float64)
+            d_abs = (inv00[g].detach().to(torch.float64).abs()[:, None] * ddx * ddx
+                     + 2 * (inv01[g].detach().to(torch.float64).abs()[:, None] * (ddx * ddy).abs())
+                     + inv11[g].detach().to(torch.float64).abs()[:, None] * ddy * ddy)
+            sens = 1 + d_abs
+            m_cc = torch.where(considered, torch.minimum(m_cut, m_cl) / sens,
+                               torch.full_like(m_cl, math.inf))
             pc = torch.full((t1 - t0, P), math.inf, dtype=torch.float64)
             pc.index_reduce_(0, rel, m_cc, "amin")
-            per_entry = torch.where(reach, torch.minimum(pc[rel], m_cl), torch.full_like(m_cl, math.inf))
+            per_entry = torch.where(reach, torch.minimum(pc[rel], m_cl / sens),
+                                    torch.full_like(m_cl, math.inf))
             gcmargin.index_reduce_(0, g, per_entry.amin(1), "amin")
     for t0, t1, img in parts:
         image = image.index_add(0, torch.arange(t0, t1), img)
@@ -468,12 +500,13 @@ def rasterize(
     lists: tuple[np.ndarray, np.ndarray] | None = None,
     decisions: dict | None = None,
     active_counts: np.ndarray | None = None,
+    transmittance: str = "log",
 ) -> Render:
     """project -> cull/rect -> emit -> stable sort -> composite (torch.py:228-247).
 
     ``lists`` = (sorted ids, ranges) composites those lists instead of the
-    ones binned here (sorted_keys is then None); ``decisions`` and
-    ``active_counts`` are passed to :func:`composite`."""
+    ones binned here (sorted_keys is then None); ``decisions``,
+    ``active_counts`` and ``transmittance`` are passed to :func:`composite`."""
     proj = project(mean, rotation, scale, opacity, color, cam, covariance_epsilon)
     tiles_w = -(-cam.width // tile_size)
     tiles_h = -(-cam.height // tile_size)
@@ -489,7 +522,7 @@ def rasterize(
         proj.mean[:, 0], proj.mean[:, 1], proj.inverse[:, 0, 0], proj.inverse[:, 0, 1],
         proj.inverse[:, 1, 1], proj.color, proj.opacity[:, 0], sorted_ids, ranges, cam.width,
         cam.height, tile_size, opacity_threshold, rendering_mode, confidence, tile_chunk,
-        decisions=decisions, active_counts=active_counts,
+        decisions=decisions, active_counts=active_counts, transmittance=transmittance,
     )
     return Render(comp.image, proj, bounds, counts, sorted_ids, ranges, sorted_keys, comp)
 

@@ -38,8 +38,12 @@ from gaussian_splats_hip.kernels.rasterize.views import (
 from oracle import rasterizer as orc
 from parity import (
     DECISION_WINDOW,
+    FLOAT32_SAMPLES,
     assert_close_flip_aware,
+    assert_close_to_truth,
     assert_gradients_close,
+    fixed_decision_composite_grads,
+    fixed_decision_rasterize_grads,
     assert_lists_exact,
     oracle_camera,
     oracle_tile_lists,
@@ -48,6 +52,7 @@ from parity import (
     sample_tiles,
     tile_max,
     tile_pixel_mask,
+    ulp_perturbed,
 )
 
 pytestmark = [pytest.mark.gpu, pytest.mark.timeout(900)]
@@ -91,19 +96,37 @@ def single_view(name, device):
     tw, th = nat.tiles(w, h, TILE)
     obounds, ocounts = orc.tile_counts(proj, TILE, tw, th, scene.near, scene.far)
     r = dict(scene=scene, params=params, out=out, bounds=bounds, proj=proj, obounds=obounds,
-             ocounts=ocounts, tw=tw, th=th, w=w, h=h)
+             ocounts=ocounts, tw=tw, th=th, w=w, h=h, cam=cam)
     _cache[name] = r
     return r
 
 
-def check_projection(pmean, pinv, pcol, pop, gbounds, gcounts, proj, obounds, ocounts, what):
-    """Projected floats to float32 rounding, depth bits exact, rectangles
-    exact away from tile edges, counts equal where the rectangles are."""
-    torch.testing.assert_close(pmean, proj.mean.float(), rtol=2e-6, atol=1e-5)
+def check_projection(pmean, pinv, pcol, pop, gbounds, gcounts, proj, obounds, ocounts, what,
+                     params, cam):
+    """Projected floats against the float64 oracle (2e-6 / 1e-5 relative, or
+    within the float32 oracle's error scale on the Gaussian, see
+    assert_close_to_truth: the 2x2 inversion loses the condition number's
+    worth of digits in any float32 evaluation), depth bits exact against the
+    float32 oracle (same operation order), rectangles exact away from tile
+    edges, counts equal where the rectangles are."""
+    n = pmean.shape[0]
+    ocam = oracle_camera(cam)
+    proj64 = orc.project(*(p.double() for p in params), ocam)
+    samples = [proj] + [orc.project(*ulp_perturbed(params, k), ocam)
+                        for k in range(1, FLOAT32_SAMPLES)]
     visible = torch.as_tensor(ocounts > 0)
-    torch.testing.assert_close(pinv[visible], proj.inverse[visible].float(), rtol=1e-5, atol=1e-7)
-    torch.testing.assert_close(pcol, proj.color.float(), rtol=1e-5, atol=1e-6)
-    torch.testing.assert_close(pop, proj.opacity.float(), rtol=1e-6, atol=1e-7)
+    stats = {}
+    stats["uv"] = assert_close_to_truth(pmean[:, :2], proj64.mean[:, :2],
+                                        [q.mean[:, :2] for q in samples], 2e-6, 1e-5,
+                                        f"{what} pixel means")
+    stats["inverse"] = assert_close_to_truth(pinv.reshape(n, 4), proj64.inverse.reshape(n, 4),
+                                             [q.inverse.reshape(n, 4) for q in samples], 1e-5,
+                                             1e-7, f"{what} inverse covariance", rows=visible)
+    stats["color"] = assert_close_to_truth(pcol, proj64.color, [q.color for q in samples], 1e-5,
+                                           1e-6, f"{what} colour")
+    stats["opacity"] = assert_close_to_truth(pop, proj64.opacity, [q.opacity for q in samples],
+                                             1e-6, 1e-7, f"{what} opacity")
+    log(what, "projection", stats)
     assert torch.equal(pmean[:, 2], proj.mean[:, 2].float()), f"{what}: depth bits differ"
     extent = 2 * np.sqrt(np.log(proj.opacity[:, 0].double().numpy() * 255))
     with np.errstate(invalid="ignore"):
@@ -121,7 +144,7 @@ def test_projection_matches_oracle(device, name):
     pmean, pinv, pcol, pop = (t.cpu() for t in r["out"][3:7])
     counts = r["out"][9].cpu().numpy()
     check_projection(pmean, pinv, pcol, pop, r["bounds"].cpu().numpy(), counts, r["proj"],
-                     r["obounds"], r["ocounts"], name)
+                     r["obounds"], r["ocounts"], name, r["scene"].params(), r["cam"])
 
 
 @pytest.mark.parametrize("name", ("config2", "config3", "config4"))
@@ -192,22 +215,6 @@ def _loss_weights(image, target, mask):
     return g * mask[..., None].to(g.device, g.dtype)
 
 
-def _fixed_decision_gradients(pm, pinv, pcol, pop, ids, rng, ncon, weights, w, h):
-    """float64 autograd of the oracle compositor over the given lists with the
-    cut/clamp decisions of its float32 run on the same float32 inputs and the
-    GPU's activity counts; returns the [N, 9] gradient (per-entry inverse
-    covariance off-diagonal) and the per-Gaussian decision margin."""
-    f32 = [pm[:, 0], pm[:, 1], pinv[:, 0, 0], pinv[:, 0, 1], pinv[:, 1, 1], pcol, pop[:, 0]]
-    run32 = orc.composite(*f32, ids, rng, w, h, TILE, THRESHOLD, tile_chunk=CHUNK)
-    leaves = [x.double().clone().requires_grad_(True) for x in f32]
-    run64 = orc.composite(*leaves, ids, rng, w, h, TILE, THRESHOLD, tile_chunk=CHUNK,
-                          decisions=run32.decisions, active_counts=ncon)
-    (run64.image * weights.double()).sum().backward()
-    du, dv, da, db, dc, drgb, dop = (x.grad for x in leaves)
-    grad = torch.stack((du, dv, da, db / 2, dc, drgb[:, 0], drgb[:, 1], drgb[:, 2], dop), -1)
-    return grad, run32.gaussian_cut_margin
-
-
 @pytest.mark.parametrize("name", ("config3", "config4"))
 def test_sampled_tiles_composite_backward(device, name):
     """composite_bwd at full size with the loss restricted to the sampled
@@ -224,10 +231,13 @@ def test_sampled_tiles_composite_backward(device, name):
     limits = {t: m + 1 for t, m in tile_max(ncon_h, tiles, r["tw"], TILE).items()}
     ids, rng = restrict_lists(gids.cpu().numpy(), granges.cpu().numpy(), tiles, limits)
     log(name, f"float64 reference over {len(ids)} entries")
-    expected, cut_margin = _fixed_decision_gradients(
-        pm.cpu(), pinv.cpu(), pcol.cpu(), pop.cpu(), ids, rng, ncon_h, weights.cpu(), r["w"], r["h"])
+    pm, pinv, pcol, pop = (t.cpu() for t in (pm, pinv, pcol, pop))
+    cols32 = (pm[:, 0], pm[:, 1], pinv[:, 0, 0], pinv[:, 0, 1], pinv[:, 1, 1], pcol, pop[:, 0])
+    expected, expected32, cut_margin, _ = fixed_decision_composite_grads(
+        cols32, ids, rng, r["w"], r["h"], TILE, ncon_h, weights.cpu(), tile_chunk=CHUNK)
     explained = cut_margin < DECISION_WINDOW
-    stats = assert_gradients_close(grad, expected, f"{name} composite_bwd", explained=explained)
+    stats = assert_gradients_close(grad, expected, f"{name} composite_bwd", explained=explained,
+                                   reference32=expected32)
     log(name, "composite_bwd", stats, "explained", int(explained.sum()))
     touched = int((expected.abs().sum(1) > 0).sum())
     assert touched > 1000, touched
@@ -256,18 +266,15 @@ def test_config3_op_backward(device):
     ncon_h = ncon.cpu().numpy()
     limits = {t: m + 1 for t, m in tile_max(ncon_h, tiles, r["tw"], TILE).items()}
     ids, rng = restrict_lists(gids.cpu().numpy(), granges.cpu().numpy(), tiles, limits)
-    f32 = [t.detach().cpu() for t in (pm[:, 0], pm[:, 1], pinv[:, 0, 0], pinv[:, 0, 1],
-                                      pinv[:, 1, 1], pcol, pop[:, 0])]
-    run32 = orc.composite(*f32, ids, rng, r["w"], r["h"], TILE, THRESHOLD, tile_chunk=CHUNK)
-    log("config3 op: float64 projection of all Gaussians + compositing of", len(ids), "entries")
-    p64 = [p.double().requires_grad_(True) for p in scene.params()]
-    ref = orc.rasterize(*p64, oracle_camera(cam), tile_size=TILE, opacity_threshold=THRESHOLD,
-                        near=scene.near, far=scene.far, tile_chunk=CHUNK, lists=(ids, rng),
-                        decisions=run32.decisions, active_counts=ncon_h)
-    (ref.image * weights.cpu().double()).sum().backward()
-    explained = run32.gaussian_cut_margin < DECISION_WINDOW
-    for name, a, p in zip(("mean", "rotation", "scale", "opacity", "color"), actual, p64):
-        stats = assert_gradients_close(a, p.grad, f"config3 grad {name}", explained=explained)
+    log("config3 op: oracle projection of all Gaussians + compositing of", len(ids), "entries")
+    cols32 = (pm[:, 0], pm[:, 1], pinv[:, 0, 0], pinv[:, 0, 1], pinv[:, 1, 1], pcol, pop[:, 0])
+    g64, g32, margin = fixed_decision_rasterize_grads(
+        scene.params(), oracle_camera(cam), TILE, scene.near, scene.far, (ids, rng), cols32, ncon_h,
+        weights.cpu(), tile_chunk=CHUNK)
+    explained = margin < DECISION_WINDOW
+    for name, a, e, e32 in zip(("mean", "rotation", "scale", "opacity", "color"), actual, g64, g32):
+        stats = assert_gradients_close(a, e, f"config3 grad {name}", explained=explained,
+                                       reference32=e32)
         log("config3 op grad", name, stats)
 
 
@@ -286,16 +293,24 @@ def test_config3_project_bwd(device):
     upstream[counts.cpu() == 0] = 0
     grads = project_bwd(*r["params"], cam.rotation_matrix.to(device), cam.translation.to(device),
                         out[4], upstream.to(device), counts, fx, fy, r["w"], r["h"])
-    p64 = [p.double().requires_grad_(True) for p in scene.params()]
-    proj = orc.project(*p64, oracle_camera(cam))
-    u64 = upstream.double()
-    loss = (proj.mean[:, 0] * u64[:, 0] + proj.mean[:, 1] * u64[:, 1]
-            + proj.inverse[:, 0, 0] * u64[:, 2] + (proj.inverse[:, 0, 1] + proj.inverse[:, 1, 0]) * u64[:, 3]
-            + proj.inverse[:, 1, 1] * u64[:, 4] + (proj.color * u64[:, 5:8]).sum(1)
-            + proj.opacity[:, 0] * u64[:, 8]).sum()
-    loss.backward()
-    for name, a, p in zip(("mean", "rotation", "scale", "opacity", "color"), grads, p64):
-        stats = assert_gradients_close(a.cpu(), p.grad, f"config3 project_bwd {name}")
+    def oracle_grads(params, dt):
+        p = [x.to(dt).clone().requires_grad_(True) for x in params]
+        proj = orc.project(*p, oracle_camera(cam))
+        u = upstream.to(dt)
+        loss = (proj.mean[:, 0] * u[:, 0] + proj.mean[:, 1] * u[:, 1]
+                + proj.inverse[:, 0, 0] * u[:, 2]
+                + (proj.inverse[:, 0, 1] + proj.inverse[:, 1, 0]) * u[:, 3]
+                + proj.inverse[:, 1, 1] * u[:, 4] + (proj.color * u[:, 5:8]).sum(1)
+                + proj.opacity[:, 0] * u[:, 8]).sum()
+        loss.backward()
+        return [x.grad for x in p]
+
+    g64 = oracle_grads(scene.params(), torch.float64)
+    runs = [oracle_grads(ulp_perturbed(scene.params(), k), torch.float32)
+            for k in range(FLOAT32_SAMPLES)]
+    names = ("mean", "rotation", "scale", "opacity", "color")
+    for name, a, e, e32 in zip(names, grads, g64, [list(x) for x in zip(*runs)]):
+        stats = assert_gradients_close(a.cpu(), e, f"config3 project_bwd {name}", reference32=e32)
         log("config3 project_bwd", name, stats)
 
 
@@ -378,7 +393,8 @@ def test_config5_projection_and_lists(device, config5):
         live = (gc > 0) | (oc > 0)
         gb[~live] = ob[~live]
         check_projection(pm[v].detach().cpu(), pinv[v].detach().cpu(), pcol[v].detach().cpu(),
-                         pop[v].detach().cpu(), gb, gc, proj, ob, oc, f"config5 view {v}")
+                         pop[v].detach().cpu(), gb, gc, proj, ob, oc, f"config5 view {v}",
+                         c["scene"].params(), cam)
 
 
 def test_config5_sampled_views_forward(device, config5):
@@ -408,11 +424,13 @@ def test_config5_sampled_views_forward(device, config5):
         mask = torch.as_tensor(tile_pixel_mask(tiles, c["tw"], TILE, c["w"], c["h"]))
         img = image[v].detach().cpu()
         margin = torch.as_tensor(comp.margin)
+        # Flat splats put more pixels within 1e-4 of a decision (their alpha
+        # falls from the peak to the cut within a pixel): up to 3% flagged.
         stats = assert_close_flip_aware(img[mask], comp.image[mask], margin[mask], atol=1e-5,
-                                        what=f"config5 view {v} image")
+                                        what=f"config5 view {v} image", max_flagged=0.03)
         log(f"config5 view {v} image", stats)
         assert_close_flip_aware(final_t[v].cpu()[mask], comp.final_transmittance[mask],
-                                margin[mask], atol=1e-5, rtol=1e-4,
+                                margin[mask], atol=1e-5, rtol=1e-4, max_flagged=0.03,
                                 what=f"config5 view {v} transmittance")
         ok = mask & (margin >= 1e-4)
         assert torch.equal(ncon[v].cpu()[ok], comp.n_contributors[ok])
@@ -441,22 +459,21 @@ def test_config5_op_backward(device, config5):
         lists[v] = restrict_lists(ids_v, rng_v, tiles, limits) + (ncon_v,)
     (image * weights).sum().backward()
     actual = [p.grad.cpu() for p in c["leaves"]]
-    p64 = [p.double().requires_grad_(True) for p in scene.params()]
-    total = 0
+    g64 = g32 = None
     explained = torch.zeros(n, dtype=torch.bool)
     for v in SAMPLED_VIEWS:
         ids, rng, ncon_v = lists[v]
-        f32 = [t.detach().cpu() for t in (pm[v, :, 0], pm[v, :, 1], pinv[v, :, 0, 0],
-                                          pinv[v, :, 0, 1], pinv[v, :, 1, 1], pcol[v], pop[v, :, 0])]
-        run32 = orc.composite(*f32, ids, rng, c["w"], c["h"], TILE, THRESHOLD, tile_chunk=CHUNK)
-        explained |= run32.gaussian_cut_margin < DECISION_WINDOW
-        log(f"config5 view {v}: float64 reference over {len(ids)} entries")
-        ref = orc.rasterize(*p64, oracle_camera(scene.cameras[v]), tile_size=TILE,
-                            opacity_threshold=THRESHOLD, near=scene.near, far=scene.far,
-                            tile_chunk=CHUNK, lists=(ids, rng), decisions=run32.decisions,
-                            active_counts=ncon_v)
-        total = total + (ref.image * weights[v].cpu().double()).sum()
-    total.backward()
-    for name, a, p in zip(("mean", "rotation", "scale", "opacity", "color"), actual, p64):
-        stats = assert_gradients_close(a, p.grad, f"config5 grad {name}", explained=explained)
+        log(f"config5 view {v}: oracle reference over {len(ids)} entries")
+        cols32 = (pm[v, :, 0], pm[v, :, 1], pinv[v, :, 0, 0], pinv[v, :, 0, 1], pinv[v, :, 1, 1],
+                  pcol[v], pop[v, :, 0])
+        e64, e32, margin = fixed_decision_rasterize_grads(
+            scene.params(), oracle_camera(scene.cameras[v]), TILE, scene.near, scene.far, (ids, rng),
+            cols32, ncon_v, weights[v].cpu(), tile_chunk=CHUNK)
+        g64 = e64 if g64 is None else [x + y for x, y in zip(g64, e64)]
+        # Per parameter, the float32 samples of each view summed sample-wise.
+        g32 = e32 if g32 is None else [[x + y for x, y in zip(xs, ys)] for xs, ys in zip(g32, e32)]
+        explained |= margin < DECISION_WINDOW
+    for name, a, e, e32 in zip(("mean", "rotation", "scale", "opacity", "color"), actual, g64, g32):
+        stats = assert_gradients_close(a, e, f"config5 grad {name}", explained=explained,
+                                       reference32=e32)
         log("config5 op grad", name, stats)

@@ -11,7 +11,6 @@ from __future__ import annotations
 import json
 from dataclasses import replace
 
-import numpy as np
 import pytest
 import torch
 
@@ -20,7 +19,13 @@ from gaussian_splats_hip.kernels.rasterize import benchmark as bm
 from gaussian_splats_hip.kernels.rasterize.interface import rasterize_outputs
 from gaussian_splats_hip.splats import GaussianSplat, rasterize
 from oracle import rasterizer as orc
-from parity import DECISION_WINDOW, assert_close_flip_aware, assert_gradients_close, oracle_camera
+from parity import (
+    DECISION_WINDOW,
+    assert_close_flip_aware,
+    assert_gradients_close,
+    fixed_decision_rasterize_grads,
+    oracle_camera,
+)
 
 pytestmark = pytest.mark.gpu
 
@@ -67,21 +72,16 @@ def test_indices_forward_and_scattered_gradients(device):
     outs = rasterize_outputs(*(p.detach()[idx].clone() for p in (
         splats.mean, splats.rotation, splats.scale, splats.opacity, splats.color)), *cam_args)
     _, _, ncon, pm, pinv, pcol, pop, gids, granges, _ = outs
-    sid, rng = gids.cpu().numpy(), granges.cpu().numpy()
-    f32 = [t.cpu() for t in (pm[:, 0], pm[:, 1], pinv[:, 0, 0], pinv[:, 0, 1], pinv[:, 1, 1], pcol,
-                              pop[:, 0])]
-    w, h = cam.image_size
-    run32 = orc.composite(*f32, sid, rng, w, h, 16)
-    p64 = [p.double().requires_grad_(True) for p in scene.params()]
-    ref64 = orc.rasterize(*(p[idx_h] for p in p64), oracle_camera(cam), tile_size=16,
-                          near=scene.near, far=scene.far, lists=(sid, rng),
-                          decisions=run32.decisions, active_counts=ncon.cpu().numpy())
-    (ref64.image * weight.cpu().double()).sum().backward()
+    cols32 = (pm[:, 0], pm[:, 1], pinv[:, 0, 0], pinv[:, 0, 1], pinv[:, 1, 1], pcol, pop[:, 0])
+    g64, g32, margin = fixed_decision_rasterize_grads(
+        scene.params(), oracle_camera(cam), 16, scene.near, scene.far,
+        (gids.cpu().numpy(), granges.cpu().numpy()), cols32, ncon.cpu().numpy(), weight.cpu(),
+        gather=idx_h)
     explained = torch.zeros(splats.num_points, dtype=torch.bool)
-    explained[idx_h[run32.gaussian_cut_margin < DECISION_WINDOW]] = True
-    for name, p in zip(("mean", "rotation", "scale", "opacity", "color"), p64):
-        assert_gradients_close(getattr(splats, name).grad, p.grad, f"indexed grad {name}",
-                               explained=explained)
+    explained[idx_h[margin < DECISION_WINDOW]] = True
+    for name, e, e32 in zip(("mean", "rotation", "scale", "opacity", "color"), g64, g32):
+        assert_gradients_close(getattr(splats, name).grad, e, f"indexed grad {name}",
+                               explained=explained, reference32=e32)
 
 
 def _inputs_after_params(scene, device, tile_size=16):

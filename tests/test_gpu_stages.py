@@ -387,8 +387,8 @@ def test_compositing_results_do_not_depend_on_tile_order(device):
     ft2 = torch.empty_like(final_t)
     nc2 = torch.empty_like(ncon)
     view = nat.make_view(1.0, 1.0, 0.0, 0.0, w, h, tile_size, opacity_threshold=THRESHOLD)
-    nat.check(nat.library().gs_composite(nat.ptr(records), nat.ptr(sid_d), nat.ptr(ranges_d),
-                                         nat.ptr(order), view, nat.ptr(img2), nat.ptr(ft2),
+    nat.check(nat.library().gs_composite(nat.ptr(records), records.shape[0], nat.ptr(sid_d),
+                                         nat.ptr(ranges_d), nat.ptr(order), view, nat.ptr(img2), nat.ptr(ft2),
                                          nat.ptr(nc2), nat.stream(device)), "composite")
     torch.cuda.synchronize()
     assert torch.equal(image, img2) and torch.equal(final_t, ft2) and torch.equal(ncon, nc2)
@@ -400,7 +400,7 @@ def test_compositing_results_do_not_depend_on_tile_order(device):
                          "gaussian")
     grad2 = torch.zeros_like(grad)
     nat.check(nat.library().gs_composite_bwd(
-        *(nat.ptr(t.contiguous()) for t in args), nat.ptr(sid_d), nat.ptr(ranges_d), nat.ptr(g),
+        *(nat.ptr(t) for t in args), args[0].shape[0], nat.ptr(sid_d), nat.ptr(ranges_d), nat.ptr(g),
         nat.ptr(final_t), nat.ptr(ncon), None, view, nat.ptr(grad2), None, nat.stream(device)),
         "composite_bwd")
     torch.cuda.synchronize()

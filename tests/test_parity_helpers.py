@@ -6,6 +6,8 @@ the gradient criterion must accept and reject at its stated bounds."""
 
 from __future__ import annotations
 
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -95,3 +97,39 @@ def test_gradient_criterion_bounds():
                            max_explained=0.34)
     with pytest.raises(AssertionError):
         assert_gradients_close(bad, e, "unexplained", explained=torch.tensor([True, False, True]))
+
+
+def test_gradient_criterion_float32_clause():
+    """A row off by more than the strict bound passes when within
+    FLOAT32_FACTOR (32) times the largest error of the float32 evaluations
+    on that row, and fails beyond."""
+    e = torch.tensor([[88.0, -1e-3, 7.0], [1.0, 2.0, 3.0]], dtype=torch.float64)
+    r32 = e.clone()
+    r32[0, 1] += 1e-4  # float32 cancellation error of the reference's numerics
+    a = e.clone()
+    a[0, 1] += 3e-4
+    with pytest.raises(AssertionError):
+        assert_gradients_close(a, e, "strict")
+    stats = assert_gradients_close(a, e, "float32 clause", reference32=r32)
+    assert stats["at_float32_accuracy"] == 1
+    a[0, 1] = e[0, 1] + 3.1e-3
+    assert_gradients_close(a, e, "within 32x", reference32=r32)
+    other = e.clone()
+    other[0, 1] -= 2e-4  # a second float32 evaluation, further off
+    a[0, 1] = e[0, 1] + 6e-3
+    assert_gradients_close(a, e, "within 32x of the largest", reference32=[r32, other])
+    with pytest.raises(AssertionError):
+        assert_gradients_close(a, e, "beyond 32x", reference32=r32)
+
+
+def test_ulp_perturbation():
+    from parity import ulp_perturbed
+
+    x = torch.tensor([1.0, -2.5, 3e-8, 0.0])
+    (same,) = ulp_perturbed([x], 0)
+    assert torch.equal(same, x)
+    (moved,) = ulp_perturbed([x], 3)
+    steps = torch.stack((torch.nextafter(x, torch.full_like(x, math.inf)),
+                         torch.nextafter(x, torch.full_like(x, -math.inf))))
+    assert bool(((moved == steps[0]) | (moved == steps[1])).all())
+    assert not torch.equal(moved, x)

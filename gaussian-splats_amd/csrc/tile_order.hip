@@ -14,6 +14,7 @@
 // Work estimates: the list length of the tile, or the largest contributor
 // count of its pixels (the entries the backward walks).
 #include <algorithm>
+#include <mutex>
 
 #include "common.h"
 
@@ -161,6 +162,57 @@ __global__ __launch_bounds__(kOrderThreads) void tile_sort_kernel(const uint32_t
 
 using namespace gs;
 
+// Scratch memory of gs_tile_order_noalloc: the per-tile work keys.  One copy
+// per GPU (each at its own device address), held until the process ends.
+constexpr int kNoAllocMaxTiles = GS_TILE_ORDER_NOALLOC_MAX_TILES;  // 1 MiB of keys
+static __device__ __align__(256) uint32_t scratch[kNoAllocMaxTiles];
+
+namespace {
+
+constexpr int kScratchDevices = 64;
+uint32_t* g_scratch_addr[kScratchDevices] = {};
+std::mutex g_scratch_mutex;
+
+// Device address of `scratch` on the stream's GPU.  The host-side name of the
+// array is not a device address; it is looked up once per device, with that
+// device current, and only the looked-up address is handed to kernels.
+int scratch_keys(hipStream_t stream, uint32_t** keys) {
+  int device = 0;
+  GS_TRY(stream_device(stream, &device));
+  GS_REQUIRE(device < kScratchDevices, GS_ERR_HIP, "device %d out of range", device);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_addr[device]) {
+    int current = 0;
+    GS_REQUIRE(hipGetDevice(&current) == hipSuccess, GS_ERR_HIP, "hipGetDevice failed");
+    const bool switch_device = current != device;
+    if (switch_device) GS_REQUIRE(hipSetDevice(device) == hipSuccess, GS_ERR_HIP, "hipSetDevice");
+    void* addr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+    if (switch_device) (void)hipSetDevice(current);
+    GS_REQUIRE(e == hipSuccess && addr, GS_ERR_HIP, "tile order scratch lookup failed: %s",
+               hipGetErrorString(e));
+    g_scratch_addr[device] = static_cast<uint32_t*>(addr);
+  }
+  *keys = g_scratch_addr[device];
+  return GS_OK;
+}
+
+// Both kernels on `s`: keys for every tile, then the per-region sort.  Every
+// key the sort reads is written by the key kernel of the same call, so `key`
+// needs no clearing.
+int tile_order_launch(const int64_t* ranges, const int32_t* n_contributors, const gs_view& view,
+                      const Mosaic& m, int32_t* order, uint32_t* key, hipStream_t s) {
+  const int num_tiles = m.num_tiles();
+  tile_key_kernel<<<unsigned(ceil_div(num_tiles, 4)), 256, 0, s>>>(
+      ranges, n_contributors, m.tiles_w(), num_tiles, view.tile_size, view.image_width,
+      view.image_height, m.tw, m.th, m.cols, m.views, key);
+  GS_TRY(check_launch("tile_order keys"));
+  tile_sort_kernel<<<8, kOrderThreads, 0, s>>>(key, num_tiles, order);
+  return check_launch("tile_order sort");
+}
+
+}  // namespace
+
 extern "C" {
 
 GS_API size_t gs_tile_order_workspace_bytes(int32_t num_tiles) {
@@ -173,21 +225,32 @@ GS_API int gs_tile_order(const int64_t* ranges, const int32_t* n_contributors, g
   clear_error();
   GS_TRY(check_view(view, true));
   const Mosaic m = mosaic_of(view);
-  const int tiles_w = m.tiles_w();
   const int num_tiles = m.num_tiles();
   GS_REQUIRE(order && (ranges || n_contributors), GS_ERR_INVALID_ARGUMENT,
              "null pointer argument");
   GS_REQUIRE(workspace && workspace_bytes >= gs_tile_order_workspace_bytes(num_tiles),
              GS_ERR_WORKSPACE, "workspace too small (%zu bytes, need %zu)", workspace_bytes,
              gs_tile_order_workspace_bytes(num_tiles));
+  return tile_order_launch(ranges, n_contributors, view, m, order,
+                           static_cast<uint32_t*>(workspace), as_stream(stream));
+}
+
+GS_API int gs_tile_order_noalloc(const int64_t* ranges, const int32_t* n_contributors,
+                                 gs_view view, int32_t* order, void* stream) {
+  clear_error();
+  GS_TRY(check_view(view, true));
+  const Mosaic m = mosaic_of(view);
+  const int num_tiles = m.num_tiles();
+  GS_REQUIRE(order && (ranges || n_contributors), GS_ERR_INVALID_ARGUMENT,
+             "null pointer argument");
+  GS_REQUIRE(num_tiles <= kNoAllocMaxTiles, GS_ERR_WORKSPACE,
+             "gs_tile_order_noalloc: %d tiles exceed its static scratch of %d tiles "
+             "(use gs_tile_order with a workspace)",
+             num_tiles, kNoAllocMaxTiles);
   const hipStream_t s = as_stream(stream);
-  uint32_t* key = static_cast<uint32_t*>(workspace);
-  tile_key_kernel<<<unsigned(ceil_div(num_tiles, 4)), 256, 0, s>>>(
-      ranges, n_contributors, tiles_w, num_tiles, view.tile_size, view.image_width,
-      view.image_height, m.tw, m.th, m.cols, m.views, key);
-  GS_TRY(check_launch("tile_order keys"));
-  tile_sort_kernel<<<8, kOrderThreads, 0, s>>>(key, num_tiles, order);
-  return check_launch("tile_order sort");
+  uint32_t* keys = nullptr;
+  GS_TRY(scratch_keys(s, &keys));
+  return tile_order_launch(ranges, n_contributors, view, m, order, keys, s);
 }
 
 }  // extern "C"

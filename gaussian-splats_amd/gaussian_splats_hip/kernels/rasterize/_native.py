@@ -157,6 +157,7 @@ _SIGNATURES = {
     "gs_tile_order": (
         c_int, [c_void_p, c_void_p, GsView, c_void_p, c_void_p, c_size_t, c_void_p]
     ),
+    "gs_tile_order_noalloc": (c_int, [c_void_p, c_void_p, GsView, c_void_p, c_void_p]),
     "gs_composite": (
         c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, GsView] + [c_void_p] * 4
     ),

@@ -259,6 +259,19 @@ GS_API int gs_tile_order(
     const int64_t* ranges, const int32_t* n_contributors, gs_view view,
     int32_t* tile_order, void* workspace, size_t workspace_bytes, void* stream);
 
+/* gs_tile_order without a workspace argument (no counterpart in the
+ * reference): for callers that cannot allocate device memory (code under HIP
+ * graph capture, serving loops, harnesses that forbid hipMalloc).  The tile
+ * keys live in a static device array of the library, one per GPU, sized for
+ * at most GS_TILE_ORDER_NOALLOC_MAX_TILES tiles (1 MiB); larger views are
+ * rejected with GS_ERR_WORKSPACE.  Allocates nothing.  Every call on a GPU
+ * shares that GPU's array: calls that overlap on one GPU (different streams
+ * or host threads) race and must be serialised by the caller. */
+#define GS_TILE_ORDER_NOALLOC_MAX_TILES (1 << 18)
+GS_API int gs_tile_order_noalloc(
+    const int64_t* ranges, const int32_t* n_contributors, gs_view view,
+    int32_t* tile_order, void* stream);
+
 /* Front-to-back compositing per tile.  Replaces composite
  * (src/gaussian_splats/kernels/rasterize/composite.py:25-162) with the
  * pixel semantics of torch.py:172-225.  tile_size in {4, 8, 16, 32}.

@@ -81,6 +81,70 @@ inline bool composite_split(int num_tiles, int active) {
   return (active > 0 && active < num_tiles ? active : num_tiles) < kCompositeSplitTiles;
 }
 
+// Dispatch plan of the compositing kernels (gs_tile_order).  Each of the 8
+// XCD regions of tiles (a contiguous range of tile indices) owns the same
+// number of item slots; an item is one wave's work:
+//   tile << 3                      the whole tile, or
+//   tile << 3 | 4 | band           a quarter of its pixel bands (tiles of 16
+//                                  and 32 pixels); the four quarters of a tile
+//                                  fill the four slots of one workgroup,
+// and -1 marks an unused slot.  With few tiles (composite_split) every tile is
+// split.  Splitting only a region's heaviest tiles (kSplitHeavy: above
+// kHeavyNum / kHeavyDen of the region's mean, at most one in kHeavyShare) is
+// implemented but off: as four independent waves, the quarters of a heavy
+// tile add their gradients with four times the atomics on the Gaussians they
+// share (config 4's backward went from 1.77 to 3.0 ms), and the forward's
+// list-length estimate misses the tiles whose walks are longest.
+constexpr bool kSplitHeavy = false;
+constexpr int kHeavyShare = 8;
+constexpr int kHeavyNum = 3, kHeavyDen = 2;
+struct DispatchPlan {
+  bool heavy = false;      // a region's heaviest tiles split into quarters
+  bool split_all = false;  // every tile split into quarters
+  int region_blocks = 1;   // workgroups (of kCompositeWaves items) per region
+  int items() const { return 8 * kCompositeWaves * region_blocks; }
+};
+inline DispatchPlan dispatch_plan(int num_tiles, int tile_size, int active) {
+  DispatchPlan p;
+  const bool bands = tile_size >= 16;
+  p.split_all = bands && composite_split(num_tiles, active);
+  p.heavy = bands && kSplitHeavy && !p.split_all;
+  // Tiles of the largest region (tile_order.hip's region split).
+  const int nb = (num_tiles + kCompositeWaves - 1) / kCompositeWaves;
+  const int t_max = (nb + 7) / 8 * kCompositeWaves;
+  const int cap = p.split_all ? 4 * t_max
+                  : p.heavy   ? t_max + 3 * ((t_max + kHeavyShare - 1) / kHeavyShare)
+                              : t_max;
+  p.region_blocks = cap > kCompositeWaves ? (cap + kCompositeWaves - 1) / kCompositeWaves : 1;
+  return p;
+}
+
+// The work item of compositing slot `slot` (kCompositeWaves per workgroup):
+// from the plan's items, or, without a plan, tile `slot` whole (or its
+// quarter slot % 4 of tile slot / 4 when every tile is split).  False: no
+// work (an unused slot, or a tile index out of range).
+__device__ __forceinline__ bool composite_item(const int32_t* items, int num_items,
+                                               int num_tiles, bool split_all, int slot,
+                                               int& tile, int& band, bool& quarter) {
+  if (items) {
+    if (slot >= num_items) return false;
+    const int it = items[slot];
+    if (it < 0) return false;
+    tile = it >> 3;
+    quarter = (it & 4) != 0;
+    band = it & 3;
+  } else if (split_all) {
+    tile = slot >> 2;
+    band = slot & 3;
+    quarter = true;
+  } else {
+    tile = slot;
+    band = 0;
+    quarter = false;
+  }
+  return tile < num_tiles;
+}
+
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 inline size_t align_up(size_t x, size_t a = 256) { return (x + a - 1) / a * a; }

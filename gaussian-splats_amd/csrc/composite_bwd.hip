@@ -1,5 +1,7 @@
-// Backward compositing: one wave64 per tile, back-to-front over the entries
-// each pixel processed while active (positions < n_contributors).
+// Backward compositing: one wave64 per work item (a whole tile, or a quarter
+// of a heavy tile's pixel bands: the dispatch plan of tile_order.hip),
+// back-to-front over the entries each pixel processed while active (positions
+// < n_contributors).
 //
 // Exact gradient of the forward of composite_fwd.hip (the function
 // torch.py:172-225 defines, differentiated as autograd would):
@@ -34,7 +36,9 @@ struct CompositeBwdArgs {
   uint32_t max_id;  // last valid Gaussian index: every gathered id is clamped to it
   const int32_t* ids;
   const int64_t* ranges;
-  const int32_t* order;  // tile dispatch order, or nullptr for the identity
+  const int32_t* items;  // dispatch plan (gs_tile_order), or nullptr: tiles in index order
+  int num_items;
+  bool split_all;        // without a plan: every tile split into quarters
   const float* grad_image;
   const float* final_t;
   const int32_t* n_contrib;
@@ -45,32 +49,18 @@ struct CompositeBwdArgs {
   float* grad_abs;  // [N, 2]: sums of |per-pixel mean gradient| (ABS kernels only)
 };
 
-// SPLIT waves share a tile, each taking SPLIT-th of its 64-pixel bands and
-// walking back from its own pixels' largest contributor count (see
-// composite_fwd.hip); each wave adds its bands' share of every gradient.
+// One wave takes PIX pixels per lane of `tile`: the 64-pixel bands band0 ..
+// band0 + PIX - 1 (all of them for a whole-tile item, a quarter for a quarter
+// item), walking back from its own pixels' largest contributor count, and
+// adds their share of every gradient.
 // ABS: also sums, per Gaussian, the absolute values of the per-pixel terms of
 // the mean gradient, |dL/du| and |dL/dv| of every pixel (composite_bwd.py:
 // 180-185,194-195), into grad_abs.
-template <int TILE, int SPLIT, bool ABS>
-__global__ __launch_bounds__(kCompositeWaves * 64) void composite_bwd_kernel(CompositeBwdArgs a) {
+template <int TILE, bool ABS, int PIX>
+__device__ __forceinline__ void composite_bwd_tile(const CompositeBwdArgs& a, float4 (*chunk)[3],
+                                                   int lane, int tile, int band0) {
   constexpr int NPIX = TILE * TILE;
-  constexpr int PIX_TILE = NPIX >= 64 ? NPIX / 64 : 1;
-  static_assert(PIX_TILE % SPLIT == 0 && kCompositeWaves % SPLIT == 0, "bands split evenly");
-  constexpr int PIX = PIX_TILE / SPLIT;  // this wave's pixels per lane
   constexpr int kBandRows = 64 / TILE > 0 ? 64 / TILE : 1;  // tile rows per band of 64 pixels
-  const int lane = threadIdx.x & 63;
-  // Wave index held in a scalar register, so the tile and view indices derived
-  // from it are scalar too.
-  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  // The wave's current 64 entries, three float4 per entry (u, v, o, pa),
-  // (pb, pc, r, g), (b, oa, ob, oc): written once per lane, then read as LDS
-  // broadcasts per entry instead of twelve v_readlane.
-  __shared__ float4 chunk[kCompositeWaves][64][3];
-  // Slot -> tile through the optional dispatch order (tile_order.hip).
-  const int slot = xcd_swizzle(blockIdx.x, gridDim.x) * (kCompositeWaves / SPLIT) + wid / SPLIT;
-  if (slot >= a.num_tiles) return;
-  const int tile = a.order ? a.order[slot] : slot;
-  const int band0 = (wid % SPLIT) * PIX;  // first band of this wave
 
   // Mosaic tile -> view and the tile's pixel origin inside that view.
   const int tx = tile % a.tiles_w;
@@ -133,15 +123,15 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_bwd_kernel(Com
       }
       mine = lane_splat(rec);
     }
-    chunk[wid][lane][0] = make_float4(mine.u, mine.v, mine.o, mine.pa);
-    chunk[wid][lane][1] = make_float4(mine.pb, mine.pc, mine.r, mine.g);
-    chunk[wid][lane][2] = make_float4(mine.b, mine.oa, mine.ob, mine.oc);
+    chunk[lane][0] = make_float4(mine.u, mine.v, mine.o, mine.pa);
+    chunk[lane][1] = make_float4(mine.pb, mine.pc, mine.r, mine.g);
+    chunk[lane][2] = make_float4(mine.b, mine.oa, mine.ob, mine.oc);
     uint64_t mask = __ballot(bands != 0);
     while (mask) {
       const int j = __builtin_ctzll(mask);
       mask &= mask - 1;
       const uint32_t band_mask = uint32_t(__builtin_amdgcn_readlane(int(bands), j));
-      const float4 f0 = chunk[wid][j][0], f1 = chunk[wid][j][1], f2 = chunk[wid][j][2];
+      const float4 f0 = chunk[j][0], f1 = chunk[j][1], f2 = chunk[j][2];
       Splat s;
       s.u = f0.x;
       s.v = f0.y;
@@ -240,21 +230,63 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_bwd_kernel(Com
   }
 }
 
-template <int TILE, int SPLIT>
-void launch_split(const CompositeBwdArgs& a, hipStream_t s) {
-  const unsigned blocks = unsigned(ceil_div(a.num_tiles, kCompositeWaves / SPLIT));
+// kCompositeWaves waves per workgroup, one work item each (composite_item);
+// workgroups are mapped onto XCDs so that each XCD takes one region of the
+// plan (xcd_swizzle).  QUARTERS: the launch's items are quarters (every tile
+// split); a whole-tile item is then composited as its four quarters in turn.
+// Otherwise items are whole tiles; of a tile's four quarter items the first
+// composites the whole tile and the others have no work.  Each kernel thus
+// composites every pixel of any plan exactly once, with one instance of the
+// walk (two would share one register allocation).
+template <int TILE, bool ABS, bool QUARTERS>
+__global__ __launch_bounds__(kCompositeWaves * 64) void composite_bwd_kernel(CompositeBwdArgs a) {
+  constexpr int NPIX = TILE * TILE;
+  constexpr int PIX_TILE = NPIX >= 64 ? NPIX / 64 : 1;
+  const int lane = threadIdx.x & 63;
+  // Wave index held in a scalar register, so the item, tile and view indices
+  // derived from it are scalar too.
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // The wave's current 64 entries, three float4 per entry (u, v, o, pa),
+  // (pb, pc, r, g), (b, oa, ob, oc): written once per lane, then read as LDS
+  // broadcasts per entry instead of twelve v_readlane.
+  __shared__ float4 chunk[kCompositeWaves][64][3];
+  const int slot = xcd_swizzle(blockIdx.x, gridDim.x) * kCompositeWaves + wid;
+  int tile, band;
+  bool quarter;
+  if (!composite_item(a.items, a.num_items, a.num_tiles, a.split_all, slot, tile, band, quarter))
+    return;
+  if constexpr (QUARTERS) {
+    static_assert(PIX_TILE >= kCompositeWaves, "quarters of 64-pixel bands");
+    constexpr int QPIX = PIX_TILE / kCompositeWaves;
+    if (quarter) {
+      composite_bwd_tile<TILE, ABS, QPIX>(a, chunk[wid], lane, tile, band * QPIX);
+    } else {
+      for (int q = 0; q < kCompositeWaves; ++q)
+        composite_bwd_tile<TILE, ABS, QPIX>(a, chunk[wid], lane, tile, q * QPIX);
+    }
+  } else {
+    if (quarter && band != 0) return;
+    composite_bwd_tile<TILE, ABS, PIX_TILE>(a, chunk[wid], lane, tile, 0);
+  }
+}
+
+template <int TILE, bool QUARTERS>
+void launch_items(const CompositeBwdArgs& a, hipStream_t s) {
+  const unsigned blocks = unsigned(
+      a.items ? a.num_items / kCompositeWaves
+              : (a.split_all ? a.num_tiles : ceil_div(a.num_tiles, kCompositeWaves)));
   if (a.grad_abs)
-    composite_bwd_kernel<TILE, SPLIT, true><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
+    composite_bwd_kernel<TILE, true, QUARTERS><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
   else
-    composite_bwd_kernel<TILE, SPLIT, false><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
+    composite_bwd_kernel<TILE, false, QUARTERS><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
 }
 
 template <int TILE>
-void launch(const CompositeBwdArgs& a, int active_tiles, hipStream_t s) {
+void launch(const CompositeBwdArgs& a, hipStream_t s) {
   if constexpr (TILE >= 16) {
-    if (composite_split(a.num_tiles, active_tiles)) return launch_split<TILE, kCompositeWaves>(a, s);
+    if (a.split_all) return launch_items<TILE, true>(a, s);
   }
-  launch_split<TILE, 1>(a, s);
+  launch_items<TILE, false>(a, s);
 }
 
 }  // namespace
@@ -292,7 +324,6 @@ extern "C" GS_API int gs_composite_bwd(const float* projected_mean,
   a.popacity = projected_opacity;
   a.ids = gaussian_ids;
   a.ranges = ranges;
-  a.order = tile_order;
   a.grad_image = grad_image;
   a.final_t = final_transmittance;
   a.n_contrib = n_contributors;
@@ -307,12 +338,16 @@ extern "C" GS_API int gs_composite_bwd(const float* projected_mean,
   a.views = m.views;
   a.grad = grad_projected;
   a.grad_abs = grad_absolute;
+  const DispatchPlan plan = dispatch_plan(a.num_tiles, view.tile_size, view.active_tiles);
+  a.items = tile_order;
+  a.num_items = plan.items();
+  a.split_all = plan.split_all;
   hipStream_t s = as_stream(stream);
   switch (view.tile_size) {
-    case 4: launch<4>(a, view.active_tiles, s); break;
-    case 8: launch<8>(a, view.active_tiles, s); break;
-    case 16: launch<16>(a, view.active_tiles, s); break;
-    default: launch<32>(a, view.active_tiles, s); break;
+    case 4: launch<4>(a, s); break;
+    case 8: launch<8>(a, s); break;
+    case 16: launch<16>(a, s); break;
+    default: launch<32>(a, s); break;
   }
   return check_launch("composite_bwd");
 }

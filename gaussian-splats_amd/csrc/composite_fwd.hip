@@ -1,5 +1,6 @@
-// Forward compositing: one wave64 per tile, tile_size^2 / 64 pixels per lane,
-// front-to-back over the tile's depth-sorted list.
+// Forward compositing: one wave64 per work item -- a whole tile, tile_size^2 /
+// 64 pixels per lane, or a quarter of a heavy tile's pixel bands (the dispatch
+// plan of tile_order.hip) -- front-to-back over the tile's depth-sorted list.
 //
 // Pixel semantics are those of kernels/rasterize/torch.py:172-225 with the
 // sequential transmittance and contributor count of composite.py:44-107:
@@ -26,7 +27,9 @@ struct CompositeArgs {
   uint32_t max_id;  // last valid record index: every gathered id is clamped to it
   const int32_t* ids;
   const int64_t* ranges;
-  const int32_t* order;  // tile dispatch order, or nullptr for the identity
+  const int32_t* items;  // dispatch plan (gs_tile_order), or nullptr: tiles in index order
+  int num_items;
+  bool split_all;        // without a plan: every tile split into quarters
   int width, height, tile;  // per view
   int tiles_w, num_tiles;    // of the whole mosaic
   int view_tw, view_th, cols, views;  // tiles per view, mosaic layout (one view: cols = views = 1)
@@ -38,29 +41,13 @@ struct CompositeArgs {
   int32_t* n_contrib;
 };
 
-// SPLIT waves share a tile, each compositing SPLIT-th of its 64-pixel bands
-// (every wave walks the whole list).  SPLIT = 1 suits images with enough
-// tiles to fill the GPU; SPLIT = 4 gives four times the waves when tiles are
-// few, at the cost of repeating the per-entry work in each wave.
-template <int TILE, bool ELLIPSOID, int SPLIT>
-__global__ __launch_bounds__(kCompositeWaves * 64) void composite_fwd_kernel(CompositeArgs a) {
+// One wave composites PIX pixels per lane of `tile`: the 64-pixel bands
+// band0 .. band0 + PIX - 1 (all of the tile's bands for a whole-tile item, a
+// quarter of them for a quarter item; every wave walks the whole list).
+template <int TILE, bool ELLIPSOID, int PIX>
+__device__ __forceinline__ void composite_tile(const CompositeArgs& a, float4 (*chunk)[3],
+                                               int lane, int tile, int band0) {
   constexpr int NPIX = TILE * TILE;
-  constexpr int PIX_TILE = NPIX >= 64 ? NPIX / 64 : 1;
-  static_assert(PIX_TILE % SPLIT == 0 && kCompositeWaves % SPLIT == 0, "bands split evenly");
-  constexpr int PIX = PIX_TILE / SPLIT;  // this wave's pixels per lane
-  const int lane = threadIdx.x & 63;
-  // Wave index held in a scalar register, so the tile and view indices derived
-  // from it are scalar too.
-  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  // The wave's current 64 entries, three float4 per entry (u, v, o, pa),
-  // (pb, pc, r, g), (b, cut, -, -): written once per lane, then read as LDS
-  // broadcasts per entry instead of ten v_readlane.
-  __shared__ float4 chunk[kCompositeWaves][64][3];
-  // Slot -> tile through the optional dispatch order (tile_order.hip).
-  const int slot = xcd_swizzle(blockIdx.x, gridDim.x) * (kCompositeWaves / SPLIT) + wid / SPLIT;
-  if (slot >= a.num_tiles) return;
-  const int tile = a.order ? a.order[slot] : slot;
-  const int band0 = (wid % SPLIT) * PIX;  // first band of this wave
 
   // Mosaic tile -> view and the tile's pixel origin inside that view.
   const int tx = tile % a.tiles_w;
@@ -116,16 +103,16 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_fwd_kernel(Com
       keep = touches_rect(rec, rx0, rx1, ry0, ry1);
       mine = lane_splat(rec);
     }
-    chunk[wid][lane][0] = make_float4(mine.u, mine.v, mine.o, mine.pa);
-    chunk[wid][lane][1] = make_float4(mine.pb, mine.pc, mine.r, mine.g);
-    chunk[wid][lane][2] = make_float4(mine.b, mine.cut, 0.0f, 0.0f);
+    chunk[lane][0] = make_float4(mine.u, mine.v, mine.o, mine.pa);
+    chunk[lane][1] = make_float4(mine.pb, mine.pc, mine.r, mine.g);
+    chunk[lane][2] = make_float4(mine.b, mine.cut, 0.0f, 0.0f);
     uint64_t mask = __ballot(keep);
     // No break inside: the loop ends through its condition, which keeps the
     // per-pixel active flags out of extra mask-merging control flow.
     while (mask) {
       const int j = __builtin_ctzll(mask);
       mask &= mask - 1;
-      const float4 f0 = chunk[wid][j][0], f1 = chunk[wid][j][1], f2 = chunk[wid][j][2];
+      const float4 f0 = chunk[j][0], f1 = chunk[j][1], f2 = chunk[j][2];
       Splat s;
       s.u = f0.x;
       s.v = f0.y;
@@ -177,22 +164,63 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_fwd_kernel(Com
   }
 }
 
-template <int TILE, int SPLIT>
-void launch_split(const CompositeArgs& a, bool ellipsoid, hipStream_t s) {
-  const unsigned blocks = unsigned(ceil_div(a.num_tiles, kCompositeWaves / SPLIT));
+// kCompositeWaves waves per workgroup, one work item each (composite_item);
+// workgroups are mapped onto XCDs so that each XCD takes one region of the
+// plan (xcd_swizzle).  QUARTERS: the launch's items are quarters (every tile
+// split); a whole-tile item is then composited as its four quarters in turn.
+// Otherwise items are whole tiles; of a tile's four quarter items the first
+// composites the whole tile and the others have no work.  Each kernel thus
+// composites every pixel of any plan exactly once, with one instance of the
+// walk (two would share one register allocation).
+template <int TILE, bool ELLIPSOID, bool QUARTERS>
+__global__ __launch_bounds__(kCompositeWaves * 64) void composite_fwd_kernel(CompositeArgs a) {
+  constexpr int NPIX = TILE * TILE;
+  constexpr int PIX_TILE = NPIX >= 64 ? NPIX / 64 : 1;
+  const int lane = threadIdx.x & 63;
+  // Wave index held in a scalar register, so the item, tile and view indices
+  // derived from it are scalar too.
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // The wave's current 64 entries, three float4 per entry (u, v, o, pa),
+  // (pb, pc, r, g), (b, cut, -, -): written once per lane, then read as LDS
+  // broadcasts per entry instead of ten v_readlane.
+  __shared__ float4 chunk[kCompositeWaves][64][3];
+  const int slot = xcd_swizzle(blockIdx.x, gridDim.x) * kCompositeWaves + wid;
+  int tile, band;
+  bool quarter;
+  if (!composite_item(a.items, a.num_items, a.num_tiles, a.split_all, slot, tile, band, quarter))
+    return;
+  if constexpr (QUARTERS) {
+    static_assert(PIX_TILE >= kCompositeWaves, "quarters of 64-pixel bands");
+    constexpr int QPIX = PIX_TILE / kCompositeWaves;
+    if (quarter) {
+      composite_tile<TILE, ELLIPSOID, QPIX>(a, chunk[wid], lane, tile, band * QPIX);
+    } else {
+      for (int q = 0; q < kCompositeWaves; ++q)
+        composite_tile<TILE, ELLIPSOID, QPIX>(a, chunk[wid], lane, tile, q * QPIX);
+    }
+  } else {
+    if (quarter && band != 0) return;
+    composite_tile<TILE, ELLIPSOID, PIX_TILE>(a, chunk[wid], lane, tile, 0);
+  }
+}
+
+template <int TILE, bool QUARTERS>
+void launch_items(const CompositeArgs& a, bool ellipsoid, hipStream_t s) {
+  const unsigned blocks = unsigned(
+      a.items ? a.num_items / kCompositeWaves
+              : (a.split_all ? a.num_tiles : ceil_div(a.num_tiles, kCompositeWaves)));
   if (ellipsoid)
-    composite_fwd_kernel<TILE, true, SPLIT><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
+    composite_fwd_kernel<TILE, true, QUARTERS><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
   else
-    composite_fwd_kernel<TILE, false, SPLIT><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
+    composite_fwd_kernel<TILE, false, QUARTERS><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
 }
 
 template <int TILE>
-void launch(const CompositeArgs& a, int active_tiles, bool ellipsoid, hipStream_t s) {
+void launch(const CompositeArgs& a, bool ellipsoid, hipStream_t s) {
   if constexpr (TILE >= 16) {
-    if (composite_split(a.num_tiles, active_tiles))
-      return launch_split<TILE, kCompositeWaves>(a, ellipsoid, s);
+    if (a.split_all) return launch_items<TILE, true>(a, ellipsoid, s);
   }
-  launch_split<TILE, 1>(a, ellipsoid, s);
+  launch_items<TILE, false>(a, ellipsoid, s);
 }
 
 }  // namespace
@@ -219,7 +247,6 @@ extern "C" GS_API int gs_composite(const void* records, int64_t num_records,
   a.max_id = uint32_t(num_records > 0 ? num_records - 1 : 0);
   a.ids = gaussian_ids;
   a.ranges = ranges;
-  a.order = tile_order;
   a.width = view.image_width;
   a.height = view.image_height;
   a.tile = view.tile_size;
@@ -235,14 +262,17 @@ extern "C" GS_API int gs_composite(const void* records, int64_t num_records,
   a.image = image;
   a.final_t = final_transmittance;
   a.n_contrib = n_contributors;
+  const DispatchPlan plan = dispatch_plan(a.num_tiles, view.tile_size, view.active_tiles);
+  a.items = tile_order;
+  a.num_items = plan.items();
+  a.split_all = plan.split_all;
   const bool ellipsoid = view.rendering_mode == GS_MODE_ELLIPSOID;
   hipStream_t s = as_stream(stream);
-  const int active = view.active_tiles;
   switch (view.tile_size) {
-    case 4: launch<4>(a, active, ellipsoid, s); break;
-    case 8: launch<8>(a, active, ellipsoid, s); break;
-    case 16: launch<16>(a, active, ellipsoid, s); break;
-    default: launch<32>(a, active, ellipsoid, s); break;
+    case 4: launch<4>(a, ellipsoid, s); break;
+    case 8: launch<8>(a, ellipsoid, s); break;
+    case 16: launch<16>(a, ellipsoid, s); break;
+    default: launch<32>(a, ellipsoid, s); break;
   }
   return check_launch("composite");
 }

@@ -1,18 +1,22 @@
-// Dispatch order of the compositing tiles.
+// Dispatch plan of the compositing tiles (DispatchPlan in common.h).
 //
-// The compositing kernels run one wave per tile, four tiles per workgroup, and
-// map workgroups onto XCDs so that each XCD composites one contiguous region of
-// tiles (xcd_swizzle: neighbouring tiles share Gaussians, which then stay in
-// that XCD's L2).  When not every wave fits on the GPU at once, workgroups
-// dispatched last start late; if they hold long tiles, the kernel ends in a
-// tail with few waves resident.  The order computed here keeps each XCD's
-// region but sorts its tiles by decreasing expected work (to eight significant
-// bits), so the long tiles start first and the short ones fill the tail
-// (longest-processing-time-first list scheduling).  Ties keep ascending tile
-// index, so the order is deterministic.
+// The compositing kernels run one wave per work item, four items per
+// workgroup, and map workgroups onto XCDs so that each XCD composites one
+// contiguous region of tiles (xcd_swizzle: neighbouring tiles share Gaussians,
+// which then stay in that XCD's L2).  Two things stretch a launch beyond its
+// average wave: workgroups dispatched last (when not every wave fits on the
+// GPU at once) that hold long tiles, and single tiles whose walk alone is
+// longer than the rest of the launch (long lists in dense regions).  The plan
+// keeps each XCD's region but sorts its tiles by decreasing expected work (to
+// eight significant bits), so the long tiles start first and the short ones
+// fill the tail (longest-processing-time-first list scheduling), and can
+// split the heaviest tiles of the region into four items of a quarter of
+// their pixel bands each, which walk the list on four waves at once
+// (kSplitHeavy).  Ties keep ascending tile index, so the plan is
+// deterministic.
 //
-// Work estimates: the list length of the tile, or the largest contributor
-// count of its pixels (the entries the backward walks).
+// Work estimates: the list length of the tile (forward), or the largest
+// contributor count of its pixels (the entries the backward walks).
 #include <algorithm>
 #include <mutex>
 
@@ -67,48 +71,75 @@ __device__ __forceinline__ void region(int r, int num_tiles, int& lo, int& hi) {
 
 // One workgroup per region: a stable counting sort of the region's tiles by
 // the eight most significant bits of the key (relative to the region's largest
-// key), largest first.  Sixteen waves take contiguous index segments; a wave
-// ranks its tiles per bucket with ballots (eight, one per digit bit), so ties
-// keep index order.  A coarse order is all list scheduling needs.
-__global__ __launch_bounds__(kOrderThreads) void tile_sort_kernel(const uint32_t* __restrict__ key,
-                                                                  int num_tiles,
-                                                                  int32_t* __restrict__ order) {
+// key), largest first, then the region's items in that order: the first H
+// tiles as four quarter items each, the others whole.  H: every tile when the
+// plan splits all; with heavy_split the tiles whose key (to those eight bits)
+// exceeds kHeavyNum / kHeavyDen of the region's mean, at most one in
+// kHeavyShare; else none.
+// Sixteen waves take contiguous index segments; a wave ranks its tiles per
+// bucket with ballots (eight, one per digit bit), so ties keep index order.
+// Unused slots of the region get -1.
+__global__ __launch_bounds__(kOrderThreads) void tile_plan_kernel(const uint32_t* __restrict__ key,
+                                                                  int num_tiles, int heavy_split,
+                                                                  int split_all, int region_slots,
+                                                                  int32_t* __restrict__ items) {
   constexpr int kWaves = kOrderThreads / 64;
   constexpr int kPerLane = kOrderMax / kOrderThreads;  // tiles per lane at most
   __shared__ uint32_t cnt[kWaves][256];
   __shared__ uint32_t start[256];
-  __shared__ uint32_t smax;
+  __shared__ uint32_t smax, ssum, sheavy;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   int lo, hi;
   region(blockIdx.x, num_tiles, lo, hi);
   const int n = hi - lo;
-  if (n > kOrderMax) {  // too large to sort here: keep the identity order
-    for (int i = threadIdx.x; i < n; i += kOrderThreads) order[lo + i] = lo + i;
+  int32_t* out = items + int64_t(blockIdx.x) * region_slots;
+  if (n > kOrderMax) {  // too large to sort here: index order, no heavy split
+    const int per = split_all ? 4 : 1;
+    for (int i = threadIdx.x; i < n * per; i += kOrderThreads)
+      out[i] = split_all ? ((lo + i / 4) << 3 | 4 | (i & 3)) : (lo + i) << 3;
+    for (int i = n * per + threadIdx.x; i < region_slots; i += kOrderThreads) out[i] = -1;
     return;
   }
-  if (threadIdx.x == 0) smax = 0;
+  if (threadIdx.x == 0) {
+    smax = 0;
+    ssum = 0;
+    sheavy = 0;
+  }
   for (int i = threadIdx.x; i < kWaves * 256; i += kOrderThreads) (&cnt[0][0])[i] = 0;
   __syncthreads();
   const int seg = (n + kWaves - 1) / kWaves;  // <= kPerLane * 64
   const int s0 = wid * seg, s1 = min(s0 + seg, n);
   uint32_t k[kPerLane];
-  uint32_t m = 0;
+  uint32_t m = 0, sum = 0;
 #pragma unroll
   for (int i = 0; i < kPerLane; ++i) {
     const int e = s0 + i * 64 + lane;
     k[i] = e < s1 ? key[lo + e] : 0u;
     m = max(m, k[i]);
+    sum += k[i];  // at most 8192 keys below 2^16: no overflow
   }
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) m = max(m, uint32_t(__shfl_xor(int(m), o, 64)));
-  if (lane == 0) atomicMax(&smax, m);
+  for (int o = 32; o > 0; o >>= 1) {
+    m = max(m, uint32_t(__shfl_xor(int(m), o, 64)));
+    sum += uint32_t(__shfl_xor(int(sum), o, 64));
+  }
+  if (lane == 0) {
+    atomicMax(&smax, m);
+    atomicAdd(&ssum, sum);
+  }
   __syncthreads();
   const int shift = max(0, 24 - __clz(int(smax | 1u)));  // smax >> shift < 256
+  // Heavy: top eight bits above those of kHeavyNum / kHeavyDen of the mean
+  // (a prefix of the sorted order).
+  const uint32_t heavy_above =
+      uint32_t((uint64_t(kHeavyNum) * ssum / (uint64_t(kHeavyDen) * uint64_t(max(n, 1)))) >> shift);
   uint32_t dig[kPerLane], rank[kPerLane];
+  uint32_t heavy = 0;
 #pragma unroll
   for (int i = 0; i < kPerLane; ++i) {
     const int e = s0 + i * 64 + lane;
     const bool valid = e < s1;
+    heavy += uint32_t(valid && (k[i] >> shift) > heavy_above);
     dig[i] = 255u - (k[i] >> shift);
     uint32_t plo = uint32_t(__ballot(valid)), phi = uint32_t(__ballot(valid) >> 32);
 #pragma unroll
@@ -127,6 +158,9 @@ __global__ __launch_bounds__(kOrderThreads) void tile_sort_kernel(const uint32_t
     }
     rank[i] = c + before;
   }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) heavy += uint32_t(__shfl_xor(int(heavy), o, 64));
+  if (lane == 0) atomicAdd(&sheavy, heavy);
   __syncthreads();
   // Bucket starts: digit-major over the waves, in one wave.
   if (wid == 0) {
@@ -150,11 +184,24 @@ __global__ __launch_bounds__(kOrderThreads) void tile_sort_kernel(const uint32_t
     }
   }
   __syncthreads();
+  const int h = split_all   ? n
+                : heavy_split ? min(int(sheavy), (n + kHeavyShare - 1) / kHeavyShare)
+                              : 0;
 #pragma unroll
   for (int i = 0; i < kPerLane; ++i) {
     const int e = s0 + i * 64 + lane;
-    if (e < s1) order[lo + int(start[dig[i]] + cnt[wid][dig[i]] + rank[i])] = lo + e;
+    if (e < s1) {
+      const int p = int(start[dig[i]] + cnt[wid][dig[i]] + rank[i]);  // sorted position
+      const int t = lo + e;
+      if (p < h) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) out[4 * p + j] = t << 3 | 4 | j;
+      } else {
+        out[3 * h + p] = t << 3;
+      }
+    }
   }
+  for (int i = n + 3 * h + threadIdx.x; i < region_slots; i += kOrderThreads) out[i] = -1;
 }
 
 }  // namespace
@@ -197,18 +244,22 @@ int scratch_keys(hipStream_t stream, uint32_t** keys) {
   return GS_OK;
 }
 
-// Both kernels on `s`: keys for every tile, then the per-region sort.  Every
-// key the sort reads is written by the key kernel of the same call, so `key`
-// needs no clearing.
+// Both kernels on `s`: keys for every tile, then the per-region plans.
+// Every key the plan kernel reads is written by the key kernel of the same
+// call, so `key` needs no clearing.
 int tile_order_launch(const int64_t* ranges, const int32_t* n_contributors, const gs_view& view,
-                      const Mosaic& m, int32_t* order, uint32_t* key, hipStream_t s) {
+                      const Mosaic& m, int32_t* items, uint32_t* key, hipStream_t s) {
   const int num_tiles = m.num_tiles();
+  GS_REQUIRE(num_tiles < (1 << 27), GS_ERR_OVERFLOW, "too many tiles (%d)", num_tiles);
+  const DispatchPlan plan = dispatch_plan(num_tiles, view.tile_size, view.active_tiles);
   tile_key_kernel<<<unsigned(ceil_div(num_tiles, 4)), 256, 0, s>>>(
       ranges, n_contributors, m.tiles_w(), num_tiles, view.tile_size, view.image_width,
       view.image_height, m.tw, m.th, m.cols, m.views, key);
   GS_TRY(check_launch("tile_order keys"));
-  tile_sort_kernel<<<8, kOrderThreads, 0, s>>>(key, num_tiles, order);
-  return check_launch("tile_order sort");
+  tile_plan_kernel<<<8, kOrderThreads, 0, s>>>(key, num_tiles, plan.heavy ? 1 : 0,
+                                                plan.split_all ? 1 : 0,
+                                                plan.items() / 8, items);
+  return check_launch("tile_order plan");
 }
 
 }  // namespace
@@ -217,6 +268,13 @@ extern "C" {
 
 GS_API size_t gs_tile_order_workspace_bytes(int32_t num_tiles) {
   return num_tiles > 0 ? align_up(size_t(num_tiles) * sizeof(uint32_t)) : 0;
+}
+
+GS_API int64_t gs_tile_order_items(gs_view view) {
+  clear_error();
+  if (check_view(view, true) != GS_OK) return -1;
+  const Mosaic m = mosaic_of(view);
+  return dispatch_plan(m.num_tiles(), view.tile_size, view.active_tiles).items();
 }
 
 GS_API int gs_tile_order(const int64_t* ranges, const int32_t* n_contributors, gs_view view,

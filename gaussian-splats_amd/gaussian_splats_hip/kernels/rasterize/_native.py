@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parents[2] / "_lib" / "libgs_raster.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 GS_OK = 0
 GS_ERR_INVALID_ARGUMENT = 1
@@ -154,6 +154,7 @@ _SIGNATURES = {
          c_void_p, c_size_t, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p],
     ),
     "gs_tile_order_workspace_bytes": (c_size_t, [c_int32]),
+    "gs_tile_order_items": (c_int64, [GsView]),
     "gs_tile_order": (
         c_int, [c_void_p, c_void_p, GsView, c_void_p, c_void_p, c_size_t, c_void_p]
     ),
@@ -375,6 +376,36 @@ def host_floats(t: torch.Tensor, numel: int, name: str) -> torch.Tensor:
 
 def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def dispatch_plan(
+    view: GsView,
+    num_tiles: int,
+    device: torch.device,
+    ranges: torch.Tensor | None = None,
+    n_contributors: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Work items of the compositing kernels for ``view`` (gs_tile_order):
+    each XCD's region of tiles, longest expected work first, its heaviest
+    tiles split into four quarter items.  The estimate is the list length
+    from ``ranges`` or the largest contributor count of each tile's pixels
+    from ``n_contributors``.  The compositing call must get the same view."""
+    if ranges is None and n_contributors is None:
+        raise ValueError("dispatch_plan needs ranges or n_contributors")
+    lib = library()
+    count = lib.gs_tile_order_items(view)
+    if count < 0:
+        check(GS_ERR_INVALID_ARGUMENT, "tile_order_items")
+    items = torch.empty(int(count), dtype=torch.int32, device=device)
+    ws = workspace(lib.gs_tile_order_workspace_bytes(num_tiles), device)
+    check(
+        lib.gs_tile_order(
+            ptr(ranges), ptr(n_contributors), view, ptr(items), ptr(ws), ws.numel(),
+            stream(device),
+        ),
+        "tile_order",
+    )
+    return items
 
 
 def tiles(image_width: int, image_height: int, tile_size: int) -> tuple[int, int]:

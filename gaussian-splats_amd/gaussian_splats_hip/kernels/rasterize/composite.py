@@ -19,31 +19,25 @@ def tile_order(
     image_width: int,
     image_height: int,
     tile_size: int,
+    active_tiles: int = 0,
 ) -> torch.Tensor:
-    """Tile dispatch order for the compositing kernels (gs_tile_order): each
-    XCD's region of tiles, longest expected work first.  The estimate is the
-    list length from ``ranges``, or the largest contributor count per tile when
-    ``n_contributors`` is given.  The backward uses the latter; the forward
-    runs in index order (all of its waves fit on the GPU at once)."""
+    """Dispatch plan of the compositing kernels (gs_tile_order) for one view:
+    work items (``tile << 3`` for a whole tile, ``tile << 3 | 4 | q`` for
+    quarter ``q`` of its pixel bands, -1 unused) that keep each XCD's region
+    of tiles, start the longest expected work first and split the heaviest
+    tiles over four waves.  The estimate is the list length from ``ranges``
+    (the forward) or the largest contributor count per tile from
+    ``n_contributors`` (the backward).  ``active_tiles`` must be the value the
+    compositing call's view carries."""
     source = n_contributors if n_contributors is not None else ranges
     if source is None:
         raise ValueError("tile_order needs ranges or n_contributors")
     device = nat.require_gpu(source)
     tiles_w, tiles_h = nat.tiles(image_width, image_height, tile_size)
-    num_tiles = tiles_w * tiles_h
-    lib = nat.library()
-    order = torch.empty(num_tiles, dtype=torch.int32, device=device)
-    ws_bytes = lib.gs_tile_order_workspace_bytes(num_tiles)
-    ws = nat.workspace(ws_bytes, device)
-    view = nat.make_view(1.0, 1.0, 0.0, 0.0, image_width, image_height, tile_size)
-    nat.check(
-        lib.gs_tile_order(
-            nat.ptr(ranges), nat.ptr(n_contributors), view, nat.ptr(order), nat.ptr(ws),
-            ws.numel(), nat.stream(device),
-        ),
-        "tile_order",
-    )
-    return order
+    view = nat.make_view(1.0, 1.0, 0.0, 0.0, image_width, image_height, tile_size,
+                         active_tiles=active_tiles)
+    return nat.dispatch_plan(view, tiles_w * tiles_h, device, ranges=ranges,
+                             n_contributors=n_contributors)
 
 
 def composite(

@@ -14,7 +14,6 @@ from __future__ import annotations
 import torch
 
 from . import _native as nat
-from .composite import tile_order
 from .project import _check_tile
 
 
@@ -64,7 +63,7 @@ def composite_bwd(
     )
     absolute = torch.zeros((n, 2), dtype=torch.float32, device=device) if return_absolute else None
     lib = nat.library()
-    order = tile_order(None, n_contributors, image_width, image_height, tile_size)
+    order = nat.dispatch_plan(view, ranges.shape[0], device, n_contributors=n_contributors)
     nat.check(
         nat.launch(
             "composite_bwd",

@@ -200,7 +200,8 @@ def _setup_context(ctx, inputs, output) -> None:
         ctx.view_project = nat.make_view(ctx.fx, ctx.fy, 0.0, 0.0, ctx.image_width, ctx.image_height)
         num_tiles = output[8].shape[0]
         ctx.tile_order = (
-            torch.empty(num_tiles, dtype=torch.int32, device=mean.device),
+            torch.empty(nat.library().gs_tile_order_items(ctx.view_composite), dtype=torch.int32,
+                        device=mean.device),
             nat.workspace(nat.library().gs_tile_order_workspace_bytes(num_tiles), mean.device),
         )
     else:

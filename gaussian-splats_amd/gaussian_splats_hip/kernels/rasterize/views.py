@@ -333,16 +333,8 @@ def backward_views(
     ptr = nat.ptr
     view = _mosaic_view(w, h, tile, views, cols, opacity_threshold=opacity_threshold,
                         active_tiles=active_tiles)
-    num_tiles = ranges.shape[0]
-    order = torch.empty(num_tiles, dtype=torch.int32, device=device)
-    order_ws = nat.workspace(lib.gs_tile_order_workspace_bytes(num_tiles), device)
     grad_projected = torch.zeros((views * n, 9), dtype=torch.float32, device=device)
-    nat.check(
-        lib.gs_tile_order(
-            None, ptr(n_contributors), view, ptr(order), ptr(order_ws), order_ws.numel(), stream
-        ),
-        "tile_order",
-    )
+    order = nat.dispatch_plan(view, ranges.shape[0], device, n_contributors=n_contributors)
     nat.check(
         nat.launch(
             "composite_bwd",

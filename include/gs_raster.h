@@ -42,7 +42,7 @@ extern "C" {
 
 #define GS_API __attribute__((visibility("default")))
 
-#define GS_ABI_VERSION 7
+#define GS_ABI_VERSION 8
 
 typedef enum gs_status {
   GS_OK = 0,
@@ -247,14 +247,21 @@ GS_API int gs_bin_tiles_emit(
     void* plan, size_t plan_bytes, const int64_t* ranges, int32_t* sorted_ids,
     void* workspace, size_t workspace_bytes, void* stream);
 
-/* Tile dispatch order for the compositing kernels (no counterpart in the
- * reference, whose launches take tiles in index order): a permutation of the
- * tiles that keeps each XCD's region of tiles and starts the tiles with the
- * most expected work first.  The work estimate is the list length from
- * ranges, or, when n_contributors is given, the largest contributor count of
- * the tile's pixels (the entries the backward walks).  Results of the
- * compositing kernels do not depend on the order. */
+/* Dispatch plan of the compositing kernels (no counterpart in the reference,
+ * whose launches take tiles in index order): writes gs_tile_order_items(view)
+ * int32 work items to tile_order.  Each item is one wave's work: a whole tile
+ * (tile << 3) or a quarter of a tile's 64-pixel bands (tile << 3 | 4 |
+ * quarter, tiles of 16 and 32 pixels; a tile's four quarters fill one
+ * workgroup's four slots); -1 is an unused slot.  The plan keeps each XCD's
+ * region of tiles and starts the tiles with the most expected work first;
+ * when fewer than 4096 tiles have work, every tile is split into its four
+ * quarters, so the walks run on four times the waves.  The work estimate
+ * is the list length from ranges, or, when n_contributors is given, the
+ * largest contributor count of the tile's pixels (the entries the backward
+ * walks).  The compositing calls take the plan with the same view (tile
+ * size, mosaic and active_tiles); their results do not depend on it. */
 GS_API size_t gs_tile_order_workspace_bytes(int32_t num_tiles);
+GS_API int64_t gs_tile_order_items(gs_view view); /* -1: invalid view */
 GS_API int gs_tile_order(
     const int64_t* ranges, const int32_t* n_contributors, gs_view view,
     int32_t* tile_order, void* workspace, size_t workspace_bytes, void* stream);
@@ -277,8 +284,9 @@ GS_API int gs_tile_order_noalloc(
  * pixel semantics of torch.py:172-225.  tile_size in {4, 8, 16, 32}.
  * `records` holds num_records records; list ids are clamped to
  * [0, num_records), so incomplete lists (see gs_device_errors) never read
- * outside it.  tile_order (optional, from gs_tile_order) only changes the
- * dispatch order. */
+ * outside it.  tile_order: the dispatch plan of gs_tile_order for this view,
+ * or NULL for tiles in index order (split into quarters when fewer than 4096
+ * tiles have work); it does not change the results. */
 GS_API int gs_composite(
     const void* records, int64_t num_records, const int32_t* gaussian_ids,
     const int64_t* ranges, const int32_t* tile_order, gs_view view, float* image,
@@ -291,7 +299,8 @@ GS_API int gs_composite(
  * the absolute per-pixel terms of the mean gradient, as composite_bwd.py's
  * return_absolute output (composite_bwd.py:180-185,194-195,272-277).
  * Replaces composite_bwd (composite_bwd.py:47-277) with the exact gradient of
- * the forward. */
+ * the forward.  tile_order as for gs_composite (the op plans from
+ * n_contributors). */
 GS_API int gs_composite_bwd(
     const float* projected_mean, const float* inverse_covariance,
     const float* projected_color, const float* projected_opacity, int64_t n,

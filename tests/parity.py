@@ -409,3 +409,98 @@ def fixed_decision_rasterize_grads(params, cam, tile_size, near, far, lists, col
             for k in range(samples)]
     g32 = [list(per) for per in zip(*runs)]
     return g64, g32, run32.gaussian_cut_margin
+
+
+# ---------------------------------------------------------------------------
+# Dispatch plan of the compositing kernels (gs_tile_order).
+# ---------------------------------------------------------------------------
+
+PLAN_WAVES = 4          # items per compositing workgroup
+PLAN_SPLIT_TILES = 4096  # fewer tiles with work than this: every tile split
+PLAN_SPLIT_HEAVY = False  # heaviest tiles of a region split (off in the library)
+PLAN_HEAVY_SHARE = 8     # at most one tile in 8 of a region split
+PLAN_HEAVY = (3, 2)      # split above 3/2 of the region's mean (to 8 bits)
+PLAN_SORT_MAX = 8192     # larger regions keep index order
+
+
+def plan_regions(num_tiles, waves=PLAN_WAVES):
+    """Tile ranges of the eight XCD regions (the compositing workgroup split)."""
+    nb = -(-num_tiles // waves)
+    q, r = nb >> 3, nb & 7
+    out = []
+    for x in range(8):
+        b0, b1 = x * q + min(x, r), (x + 1) * q + min(x + 1, r)
+        out.append((min(b0 * waves, num_tiles), min(b1 * waves, num_tiles)))
+    return out
+
+
+def plan_slots(num_tiles, tile_size, active=0):
+    """(item slots per region, heaviest tiles split, every tile split)."""
+    live = active if 0 < active < num_tiles else num_tiles
+    split_all = tile_size >= 16 and live < PLAN_SPLIT_TILES
+    bands = tile_size >= 16 and PLAN_SPLIT_HEAVY and not split_all
+    nb = -(-num_tiles // PLAN_WAVES)
+    t_max = -(-nb // 8) * PLAN_WAVES
+    if split_all:
+        cap = 4 * t_max
+    elif bands:
+        cap = t_max + 3 * -(-t_max // PLAN_HEAVY_SHARE)
+    else:
+        cap = t_max
+    blocks = -(-cap // PLAN_WAVES) if cap > PLAN_WAVES else 1
+    return PLAN_WAVES * blocks, bands, split_all
+
+
+def expected_plan(keys, tile_size, active=0):
+    """The work items gs_tile_order writes for per-tile work keys (list
+    lengths or largest contributor counts): per region, a stable sort by the
+    key's eight most significant bits (relative to the region's largest key,
+    keys capped at 2^16 - 1), largest first; the first h tiles become four
+    quarter items (tile << 3 | 4 | q), the rest whole items (tile << 3); -1
+    fills the region's unused slots."""
+    keys = np.minimum(np.maximum(np.asarray(keys, dtype=np.int64), 0), 0xFFFF)
+    num_tiles = keys.size
+    slots, bands, split_all = plan_slots(num_tiles, tile_size, active)
+    items = np.full(8 * slots, -1, dtype=np.int64)
+    for r, (lo, hi) in enumerate(plan_regions(num_tiles)):
+        n = hi - lo
+        out = items[r * slots:(r + 1) * slots]
+        if n == 0:
+            continue
+        if n > PLAN_SORT_MAX:
+            if split_all:
+                t = lo + np.arange(4 * n) // 4
+                out[:4 * n] = t << 3 | 4 | (np.arange(4 * n) & 3)
+            else:
+                out[:n] = (lo + np.arange(n)) << 3
+            continue
+        k = keys[lo:hi]
+        shift = max(0, int(k.max() | 1).bit_length() - 8)
+        above = (PLAN_HEAVY[0] * int(k.sum()) // (PLAN_HEAVY[1] * n)) >> shift
+        order = np.lexsort((np.arange(n), -(k >> shift)))
+        if split_all:
+            h = n
+        elif bands:
+            h = min(int(np.count_nonzero((k >> shift) > above)), -(-n // PLAN_HEAVY_SHARE))
+        else:
+            h = 0
+        for p, e in enumerate(order):
+            t = lo + int(e)
+            if p < h:
+                out[4 * p:4 * p + 4] = t << 3 | 4 | np.arange(4)
+            else:
+                out[3 * h + p] = t << 3
+    return items.astype(np.int32)
+
+
+def plan_tile_keys(ranges=None, ncon=None, width=0, height=0, tile_size=16):
+    """Per-tile work keys of the plan: list lengths, or the largest
+    contributor count of each tile's pixels ([H, W] or [V, H, W] mosaic of
+    views side by side is not modelled here: one view)."""
+    if ranges is not None:
+        r = np.asarray(ranges)
+        return r[:, 1] - r[:, 0]
+    tw, th = -(-width // tile_size), -(-height // tile_size)
+    padded = np.zeros((th * tile_size, tw * tile_size), dtype=np.int64)
+    padded[:height, :width] = ncon
+    return padded.reshape(th, tile_size, tw, tile_size).max(axis=(1, 3)).reshape(-1)

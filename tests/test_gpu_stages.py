@@ -23,7 +23,14 @@ from gaussian_splats_hip.kernels.rasterize import (
 )
 from gaussian_splats_hip.kernels.rasterize import _native as nat
 from oracle import rasterizer as orc
-from parity import assert_close_flip_aware, oracle_camera, rect_flip_tolerant_equal
+from parity import (
+    assert_close_flip_aware,
+    expected_plan,
+    oracle_camera,
+    plan_slots,
+    plan_tile_keys,
+    rect_flip_tolerant_equal,
+)
 
 pytestmark = pytest.mark.gpu
 
@@ -311,62 +318,54 @@ def test_composite_empty_tiles(device):
     assert torch.all(final_t == 1) and torch.count_nonzero(ncon) == 0
 
 
-def _regions(num_tiles, waves=4):
-    """Tile ranges of the eight XCD regions (the compositing workgroup split)."""
-    nb = -(-num_tiles // waves)
-    q, r = nb >> 3, nb & 7
-    out = []
-    for x in range(8):
-        b0, b1 = x * q + min(x, r), (x + 1) * q + min(x + 1, r)
-        out.append((min(b0 * waves, num_tiles), min(b1 * waves, num_tiles)))
-    return out
-
-
-def _expected_order(keys):
-    """Per region: stable sort by the key's eight most significant bits
-    (relative to the region's largest key, keys capped at 2^16 - 1), largest
-    first."""
-    order = np.arange(keys.size)
-    for lo, hi in _regions(keys.size):
-        if hi <= lo:
-            continue
-        k = np.minimum(keys[lo:hi], 0xFFFF).astype(np.int64)
-        shift = max(0, int(k.max() | 1).bit_length() - 8)
-        order[lo:hi] = lo + np.lexsort((np.arange(hi - lo), -(k >> shift)))
-    return order
-
-
-@pytest.mark.parametrize("shape", [(120, 68, 16), (7, 5, 8), (1, 1, 16), (33, 2, 4)])
-def test_tile_order_by_list_length_and_contributors(device, shape):
+@pytest.mark.parametrize(
+    "shape", [(120, 68, 16, 0), (120, 68, 16, 3000), (7, 5, 8, 0), (1, 1, 16, 0), (33, 2, 4, 0),
+              (100, 100, 16, 0), (60, 40, 32, 0)])
+def test_dispatch_plan_matches_model(device, shape):
+    """gs_tile_order's work items equal the plan's model (expected_plan) for
+    both work estimates: list lengths (ranges) and the largest contributor
+    count per tile; every tile is covered exactly once, whole or as its four
+    quarters in one workgroup's four slots."""
     from gaussian_splats_hip.kernels.rasterize.composite import tile_order
 
-    tw, th, tile = shape
+    tw, th, tile, active = shape
     w, h = tw * tile - 3, th * tile - 1  # partial edge tiles
     tw, th = nat.tiles(w, h, tile)
     t = tw * th
-    rng = np.random.default_rng(t)
+    rng = np.random.default_rng(t + active)
     lengths = rng.integers(0, 3000, size=t)
     lengths[rng.random(t) < 0.1] = 0
     lengths[: min(3, t)] = 70000  # capped at 2^16 - 1: ties broken by index
     ranges = np.zeros((t, 2), dtype=np.int64)
     ranges[:, 1] = np.cumsum(lengths)
     ranges[1:, 0] = ranges[:-1, 1]
-    order = tile_order(torch.as_tensor(ranges).to(device), None, w, h, tile).cpu().numpy()
-    np.testing.assert_array_equal(order, _expected_order(lengths))
+    items = tile_order(torch.as_tensor(ranges).to(device), None, w, h, tile,
+                       active_tiles=active).cpu().numpy()
+    np.testing.assert_array_equal(items, expected_plan(lengths, tile, active))
+    used = items[items >= 0]
+    covered = np.bincount(used >> 3, minlength=t)
+    whole = np.bincount((used >> 3)[(used & 4) == 0], minlength=t)
+    assert np.all(((covered == 1) & (whole == 1)) | ((covered == 4) & (whole == 0)))
+    slots = np.flatnonzero((items >= 0) & ((items & 4) != 0))
+    assert np.all(items[slots] & 3 == slots % 4)  # quarter q in a workgroup's slot q
 
     ncon = rng.integers(0, 500, size=(h, w)).astype(np.int32)
-    order = tile_order(None, torch.as_tensor(ncon).to(device), w, h, tile).cpu().numpy()
-    padded = np.zeros((th * tile, tw * tile), dtype=np.int64)
-    padded[:h, :w] = ncon
-    tile_max = padded.reshape(th, tile, tw, tile).max(axis=(1, 3)).reshape(-1)
-    np.testing.assert_array_equal(order, _expected_order(tile_max))
+    items = tile_order(None, torch.as_tensor(ncon).to(device), w, h, tile,
+                       active_tiles=active).cpu().numpy()
+    np.testing.assert_array_equal(
+        items, expected_plan(plan_tile_keys(ncon=ncon, width=w, height=h, tile_size=tile), tile,
+                             active))
 
 
-def test_compositing_results_do_not_depend_on_tile_order(device):
-    scene = scenes.edge_case_scene(n=1500, sh_degree=1, image_size=(96, 80))
+@pytest.mark.parametrize("tile_size,image_size", [(8, (96, 80)), (16, (96, 80)),
+                                                   (16, (1100, 1000))])
+def test_compositing_results_do_not_depend_on_tile_order(device, tile_size, image_size):
+    """The forward is bit-identical under every dispatch (index order, a plan
+    with quarter items, every tile split); the backward equal up to the order
+    of the float atomics."""
+    scene = scenes.edge_case_scene(n=1500, sh_degree=1, image_size=image_size)
     cam = scene.cameras[0]
     w, h = cam.image_size
-    tile_size = 8
     proj = orc.project(*scene.params(), oracle_camera(cam))
     tw, th = nat.tiles(w, h, tile_size)
     bounds, counts = orc.tile_counts(proj, tile_size, tw, th, scene.near, scene.far, "gaussian", CONFIDENCE)
@@ -375,23 +374,37 @@ def test_compositing_results_do_not_depend_on_tile_order(device):
     sid_d, ranges_d = torch.as_tensor(sid).to(device), torch.as_tensor(ranges).to(device)
     image, final_t, ncon = composite(*args, sid_d, ranges_d, w, h, tile_size, THRESHOLD, "gaussian",
                                      CONFIDENCE)
-    # The same launch through the C ABI with the tiles dispatched longest first.
+    # The same launch through the C ABI under other dispatches.
     from gaussian_splats_hip.kernels.rasterize import composite_bwd
     from gaussian_splats_hip.kernels.rasterize.composite import tile_order
     from gaussian_splats_hip.kernels.rasterize.project import pack_records
 
-    order = tile_order(ranges_d, None, w, h, tile_size)
-    assert not torch.equal(order.cpu(), torch.arange(order.numel(), dtype=torch.int32))
     records = pack_records(*args, "gaussian", CONFIDENCE)
-    img2 = torch.empty_like(image)
-    ft2 = torch.empty_like(final_t)
-    nc2 = torch.empty_like(ncon)
     view = nat.make_view(1.0, 1.0, 0.0, 0.0, w, h, tile_size, opacity_threshold=THRESHOLD)
-    nat.check(nat.library().gs_composite(nat.ptr(records), records.shape[0], nat.ptr(sid_d),
-                                         nat.ptr(ranges_d), nat.ptr(order), view, nat.ptr(img2), nat.ptr(ft2),
-                                         nat.ptr(nc2), nat.stream(device)), "composite")
-    torch.cuda.synchronize()
-    assert torch.equal(image, img2) and torch.equal(final_t, ft2) and torch.equal(ncon, nc2)
+
+    def forward(order, v=view):
+        img2 = torch.empty_like(image)
+        ft2 = torch.empty_like(final_t)
+        nc2 = torch.empty_like(ncon)
+        nat.check(nat.library().gs_composite(
+            nat.ptr(records), records.shape[0], nat.ptr(sid_d), nat.ptr(ranges_d), nat.ptr(order),
+            v, nat.ptr(img2), nat.ptr(ft2), nat.ptr(nc2), nat.stream(device)), "composite")
+        torch.cuda.synchronize()
+        assert torch.equal(image, img2) and torch.equal(final_t, ft2) and torch.equal(ncon, nc2)
+
+    # Tiles in index order, and a plan whose heaviest tiles run as quarters.
+    forward(None)
+    order = tile_order(ranges_d, None, w, h, tile_size)
+    _, heavy, split_all = plan_slots(tw * th, tile_size)
+    used = order.cpu().numpy()
+    used = used[used >= 0]
+    assert bool((used & 4).any()) == (split_all or heavy)
+    forward(order)
+    # Every tile split into quarters (few tiles with work).
+    few = nat.make_view(1.0, 1.0, 0.0, 0.0, w, h, tile_size, opacity_threshold=THRESHOLD,
+                        active_tiles=1)
+    forward(None, few)
+    forward(tile_order(ranges_d, None, w, h, tile_size, active_tiles=1), few)
 
     # Backward: the wrapper dispatches by contributor count; the identity
     # order gives the same gradient up to the order of the atomic adds.

@@ -1,7 +1,7 @@
-"""gs_tile_order_noalloc: the compositing tile order computed in the
+"""gs_tile_order_noalloc: the compositing dispatch plan computed in the
 library's static per-GPU scratch instead of a caller workspace.
 
-Through the C ABI: its order equals gs_tile_order's (caller workspace) bit for
+Through the C ABI: its plan equals gs_tile_order's (caller workspace) bit for
 bit on consecutive calls of decreasing size -- the largest view the scratch
 holds, a 1080p view by contributor counts, then a smaller view by list
 lengths, so stale keys of the earlier calls remain in the scratch -- and on a
@@ -33,10 +33,11 @@ def _both_orders(device, view, num_tiles, ranges=None, ncon=None):
     lib = nat.library()
     s = nat.stream(device)
     ws = nat.workspace(lib.gs_tile_order_workspace_bytes(num_tiles), device)
-    expected = torch.full((num_tiles,), -1, dtype=torch.int32, device=device)
+    count = lib.gs_tile_order_items(view)
+    expected = torch.full((count,), -7, dtype=torch.int32, device=device)
     nat.check(lib.gs_tile_order(nat.ptr(ranges), nat.ptr(ncon), view, nat.ptr(expected),
                                 nat.ptr(ws), ws.numel(), s), "tile_order")
-    got = torch.full((num_tiles,), -1, dtype=torch.int32, device=device)
+    got = torch.full((count,), -7, dtype=torch.int32, device=device)
     nat.check(lib.gs_tile_order_noalloc(nat.ptr(ranges), nat.ptr(ncon), view, nat.ptr(got), s),
               "tile_order_noalloc")
     torch.cuda.synchronize(device)
@@ -62,7 +63,7 @@ def test_noalloc_rejects_what_the_scratch_cannot_hold():
 
 @pytest.mark.gpu
 def test_noalloc_matches_workspace_order(device):
-    from test_gpu_stages import _expected_order
+    from parity import expected_plan, plan_tile_keys
 
     rng = np.random.default_rng(2024)
 
@@ -75,7 +76,8 @@ def test_noalloc_matches_workspace_order(device):
     print(f"[noalloc] max tiles {t}", flush=True)
     expected, got = _both_orders(device, view, t, ranges=torch.as_tensor(_ranges(lengths)).to(device))
     np.testing.assert_array_equal(got, expected)
-    assert np.array_equal(np.sort(got), np.arange(t))
+    used = got[got >= 0]
+    assert got.size == expected.size and np.array_equal(np.unique(used >> 3), np.arange(t))
 
     # 1080p by contributor counts (the backward's estimate), partial edge tiles.
     w, h, tile = 1920, 1080, 16
@@ -85,10 +87,8 @@ def test_noalloc_matches_workspace_order(device):
     print(f"[noalloc] 1080p contributors {tw * th} tiles", flush=True)
     expected, got = _both_orders(device, view, tw * th, ncon=torch.as_tensor(ncon).to(device))
     np.testing.assert_array_equal(got, expected)
-    padded = np.zeros((th * tile, tw * tile), dtype=np.int64)
-    padded[:h, :w] = ncon
     np.testing.assert_array_equal(
-        got, _expected_order(padded.reshape(th, tile, tw, tile).max(axis=(1, 3)).reshape(-1)))
+        got, expected_plan(plan_tile_keys(ncon=ncon, width=w, height=h, tile_size=tile), tile))
 
     # Smaller: 33 x 2 tiles by list length; the scratch still holds the keys
     # of the calls above beyond this view's 66 tiles.
@@ -101,7 +101,7 @@ def test_noalloc_matches_workspace_order(device):
     expected, got = _both_orders(device, view, tw * th,
                                  ranges=torch.as_tensor(_ranges(lengths)).to(device))
     np.testing.assert_array_equal(got, expected)
-    np.testing.assert_array_equal(got, _expected_order(lengths))
+    np.testing.assert_array_equal(got, expected_plan(lengths, tile))
 
     # A 2 x 2 mosaic of 200 x 120 views in 8-pixel tiles, by contributors.
     w, h, tile, views, cols = 200, 120, 8, 4, 2

@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <cstdio>
 #include <mutex>
@@ -81,68 +82,147 @@ inline bool composite_split(int num_tiles, int active) {
   return (active > 0 && active < num_tiles ? active : num_tiles) < kCompositeSplitTiles;
 }
 
+// Checkpoints of the forward walk (composite_fwd.hip) that let the backward
+// walk a long list in segments.  Whenever a whole-tile wave of a list longer
+// than kCheckpointMinList starts a batch of 64 entries that holds a list
+// position P = j * kCheckpointEntries of the intersection array (P at least
+// 64 past the tile's first entry), it records
+// per pixel the transmittance and the colour composited since its previous
+// checkpoint, and at the end of the walk turns the colours into the colour
+// composited after each checkpoint (a suffix sum, so the backward starts a
+// segment with g.S = g . C_after / T and no difference of rounded sums).  At
+// most kMaxCheckpoints per tile; records come from a pool (a device counter
+// and kCheckpointPoolBytes of records), slot j of the table holding the
+// record of position j * kCheckpointEntries (-1: the pool was full).
+constexpr int kCheckpointEntries = 1024;
+constexpr int kMaxCheckpoints = 63;
+// Only tiles with longer lists record checkpoints: shorter walks are not
+// worth the records and the extra items (measured on config 3, whose lists
+// reach ~7000 entries: checkpoints on every tile cost 9 us of forward and
+// 17 us of backward).
+constexpr int kCheckpointMinList = 8192;
+constexpr size_t kCheckpointPoolBytes = size_t(128) << 20;
+
+// Pixels of a tile's checkpoint record (64 for tiles of fewer pixels).
+inline int checkpoint_pixels(int tile_size) {
+  return tile_size * tile_size >= 64 ? tile_size * tile_size : 64;
+}
+
+// Layout of the checkpoint workspace: a counter, the table, the records.
+struct CheckpointLayout {
+  uint32_t* counter = nullptr;
+  int32_t* table = nullptr;
+  float4* records = nullptr;
+  int64_t table_len = 0;
+  int64_t capacity = 0;  // records
+  size_t bytes = 0;
+};
+inline CheckpointLayout checkpoint_layout(void* base, int tile_size, int64_t total) {
+  CheckpointLayout c;
+  const size_t record = size_t(checkpoint_pixels(tile_size)) * 16;
+  // A crossing's position lies below the list end + 64 (its batch starts
+  // inside the list): table slots up to (total + 63) / kCheckpointEntries.
+  c.table_len = total / kCheckpointEntries + 2;
+  const int64_t most = c.table_len;  // one record per table slot at most
+  c.capacity = std::min<int64_t>(most, int64_t(kCheckpointPoolBytes / record));
+  char* p = static_cast<char*>(base);
+  size_t off = 0;
+  auto take = [&](size_t n) {
+    char* r = p ? p + off : nullptr;
+    off += (n + 255) / 256 * 256;
+    return r;
+  };
+  c.counter = reinterpret_cast<uint32_t*>(take(4));
+  c.table = reinterpret_cast<int32_t*>(take(size_t(c.table_len) * 4));
+  c.records = reinterpret_cast<float4*>(take(size_t(c.capacity) * record));
+  c.bytes = off;
+  return c;
+}
+
 // Dispatch plan of the compositing kernels (gs_tile_order).  Each of the 8
 // XCD regions of tiles (a contiguous range of tile indices) owns the same
-// number of item slots; an item is one wave's work:
-//   tile << 3                      the whole tile, or
-//   tile << 3 | 4 | band           a quarter of its pixel bands (tiles of 16
-//                                  and 32 pixels); the four quarters of a tile
-//                                  fill the four slots of one workgroup,
-// and -1 marks an unused slot.  With few tiles (composite_split) every tile is
-// split.  Splitting only a region's heaviest tiles (kSplitHeavy: above
-// kHeavyNum / kHeavyDen of the region's mean, at most one in kHeavyShare) is
-// implemented but off: as four independent waves, the quarters of a heavy
-// tile add their gradients with four times the atomics on the Gaussians they
-// share (config 4's backward went from 1.77 to 3.0 ms), and the forward's
-// list-length estimate misses the tiles whose walks are longest.
-constexpr bool kSplitHeavy = false;
-constexpr int kHeavyShare = 8;
-constexpr int kHeavyNum = 3, kHeavyDen = 2;
+// number of item slots; an item is one wave's work, tile << 7 | code:
+//   code 0            the whole tile;
+//   code 0x20 | q     quarter q of its pixel bands (tiles of 16 and 32 pixels,
+//                     when fewer than kCompositeSplitTiles tiles have work:
+//                     every tile split, its quarters in one workgroup's slots);
+//   code 0x40 | s     segment s of the entries a tile's pixels walk back
+//                     (backward plans with the tile ranges): the walk is cut
+//                     at the forward's checkpoints, the segments of a tile in
+//                     consecutive slots;
+// and -1 marks an unused slot.  A backward plan segments the tiles with
+// checkpoints, heaviest first, while the region's spare slots last.
+constexpr int kSegmentSpare = 4;  // spare slots per region, in units of its tiles
 struct DispatchPlan {
-  bool heavy = false;      // a region's heaviest tiles split into quarters
+  bool segments = false;   // tiles walked back in segments
   bool split_all = false;  // every tile split into quarters
   int region_blocks = 1;   // workgroups (of kCompositeWaves items) per region
   int items() const { return 8 * kCompositeWaves * region_blocks; }
 };
-inline DispatchPlan dispatch_plan(int num_tiles, int tile_size, int active) {
+inline DispatchPlan dispatch_plan(int num_tiles, int tile_size, int active, bool backward) {
   DispatchPlan p;
-  const bool bands = tile_size >= 16;
-  p.split_all = bands && composite_split(num_tiles, active);
-  p.heavy = bands && kSplitHeavy && !p.split_all;
+  p.split_all = tile_size >= 16 && composite_split(num_tiles, active);
+  p.segments = backward && !p.split_all;
   // Tiles of the largest region (tile_order.hip's region split).
   const int nb = (num_tiles + kCompositeWaves - 1) / kCompositeWaves;
   const int t_max = (nb + 7) / 8 * kCompositeWaves;
-  const int cap = p.split_all ? 4 * t_max
-                  : p.heavy   ? t_max + 3 * ((t_max + kHeavyShare - 1) / kHeavyShare)
-                              : t_max;
+  const int cap = p.split_all ? 4 * t_max : p.segments ? (1 + kSegmentSpare) * t_max : t_max;
   p.region_blocks = cap > kCompositeWaves ? (cap + kCompositeWaves - 1) / kCompositeWaves : 1;
   return p;
 }
 
+// Kinds of compositing work item.
+enum : int { kItemTile = 0, kItemQuarter = 1, kItemSegment = 2 };
+
 // The work item of compositing slot `slot` (kCompositeWaves per workgroup):
 // from the plan's items, or, without a plan, tile `slot` whole (or its
 // quarter slot % 4 of tile slot / 4 when every tile is split).  False: no
-// work (an unused slot, or a tile index out of range).
+// work (an unused slot, or a tile index out of range).  `index` is the
+// quarter or segment.
 __device__ __forceinline__ bool composite_item(const int32_t* items, int num_items,
                                                int num_tiles, bool split_all, int slot,
-                                               int& tile, int& band, bool& quarter) {
+                                               int& tile, int& kind, int& index) {
   if (items) {
     if (slot >= num_items) return false;
     const int it = items[slot];
     if (it < 0) return false;
-    tile = it >> 3;
-    quarter = (it & 4) != 0;
-    band = it & 3;
+    tile = it >> 7;
+    kind = (it & 0x40) ? kItemSegment : (it & 0x20) ? kItemQuarter : kItemTile;
+    index = it & 0x1F;
+    if (kind == kItemSegment) index = it & 0x3F;
   } else if (split_all) {
     tile = slot >> 2;
-    band = slot & 3;
-    quarter = true;
+    kind = kItemQuarter;
+    index = slot & 3;
   } else {
     tile = slot;
-    band = 0;
-    quarter = false;
+    kind = kItemTile;
+    index = 0;
   }
   return tile < num_tiles;
+}
+
+// The checkpoint crossings of a tile whose list starts at `start` and whose
+// pixels walk max_n entries: crossing j >= 1 is list position
+// P_j = first + (j - 1) kCheckpointEntries (first: the first multiple of
+// kCheckpointEntries at least 64 past start), recorded at the start of the
+// batch holding it, B_j = 64 floor((P_j - start) / 64) entries into the walk,
+// for the B_j < max_n (at most kMaxCheckpoints; none for lists of at most
+// kCheckpointMinList entries).
+__host__ __device__ inline int64_t checkpoint_first(int64_t start) {
+  return (start + 64 + kCheckpointEntries - 1) / kCheckpointEntries * kCheckpointEntries;
+}
+__host__ __device__ inline int checkpoint_batch(int64_t start, int j) {  // B_j, j >= 1
+  return int((checkpoint_first(start) + int64_t(j - 1) * kCheckpointEntries - start) / 64 * 64);
+}
+__host__ __device__ inline int checkpoint_count(int64_t start, int max_n, int64_t list_len) {
+  const int64_t first = checkpoint_first(start) - start;  // >= 64
+  if (max_n <= 64 || list_len <= kCheckpointMinList) return 0;
+  // B_j < max_n  <=>  64 floor((first + (j-1) L) / 64) < max_n
+  const int64_t limit = (int64_t(max_n) + 63) / 64 * 64;  // B_j < max_n <=> first + (j-1)L < limit
+  if (first >= limit) return 0;
+  const int64_t m = (limit - 1 - first) / kCheckpointEntries + 1;
+  return int(m < kMaxCheckpoints ? m : kMaxCheckpoints);
 }
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }

@@ -47,18 +47,27 @@ struct CompositeBwdArgs {
   int view_tw, view_th, cols, views;  // tiles per view, mosaic layout (one view: cols = views = 1)
   float* grad;      // [N, 9]
   float* grad_abs;  // [N, 2]: sums of |per-pixel mean gradient| (ABS kernels only)
+  // The forward's checkpoints (CheckpointLayout), or null table: none.
+  const int32_t* ckpt_table;
+  const float4* ckpt_records;
+  int64_t ckpt_capacity;
 };
 
 // One wave takes PIX pixels per lane of `tile`: the 64-pixel bands band0 ..
 // band0 + PIX - 1 (all of them for a whole-tile item, a quarter for a quarter
 // item), walking back from its own pixels' largest contributor count, and
-// adds their share of every gradient.
-// ABS: also sums, per Gaussian, the absolute values of the per-pixel terms of
-// the mean gradient, |dL/du| and |dL/dv| of every pixel (composite_bwd.py:
-// 180-185,194-195), into grad_abs.
+// adds their share of every gradient.  A segment item (seg >= 0, all of the
+// tile's bands) walks only the positions between two of the forward's
+// checkpoints of the tile, [B_seg, B_seg+1) (B_0 = 0; the last segment runs
+// to the largest contributor count), starting at B_seg+1 from that
+// checkpoint's record: T there, and g.S = g . (colour composited after it) /
+// T, the state the walk back from the end would reach there (the
+// associative combine of back-to-front compositing, composite_bwd.py:24-36).
+// Segments past the last recorded checkpoint (a full pool) have no work; the
+// one at it runs to the end.
 template <int TILE, bool ABS, int PIX>
 __device__ __forceinline__ void composite_bwd_tile(const CompositeBwdArgs& a, float4 (*chunk)[3],
-                                                   int lane, int tile, int band0) {
+                                                   int lane, int tile, int band0, int seg) {
   constexpr int NPIX = TILE * TILE;
   constexpr int kBandRows = 64 / TILE > 0 ? 64 / TILE : 1;  // tile rows per band of 64 pixels
 
@@ -95,6 +104,35 @@ __device__ __forceinline__ void composite_bwd_tile(const CompositeBwdArgs& a, fl
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) max_n = max(max_n, __shfl_xor(max_n, o, 64));
+  int lo = 0, hi = max_n;  // positions walked
+  if (seg >= 0) {
+    // Recorded checkpoints: a prefix of the tile's crossings (lane j reads
+    // the table slot of crossing j + 1).
+    const int m =
+        a.ckpt_table ? checkpoint_count(start, max_n, a.ranges[2 * tile + 1] - start) : 0;
+    const int64_t first = checkpoint_first(start);
+    const int slot = lane < m ? a.ckpt_table[(first + int64_t(lane) * kCheckpointEntries) /
+                                             kCheckpointEntries]
+                              : -1;
+    // A slot outside the pool (never written by this forward) counts as missing.
+    const uint64_t missing = __ballot(lane < m && (slot < 0 || int64_t(slot) >= a.ckpt_capacity));
+    const int w = missing ? __builtin_ctzll(missing) : m;
+    if (seg > w) return;
+    lo = seg == 0 ? 0 : checkpoint_batch(start, seg);
+    if (seg < w) {
+      hi = checkpoint_batch(start, seg + 1);
+      const float4* rec =
+          a.ckpt_records + int64_t(__builtin_amdgcn_readlane(slot, seg)) * (PIX * 64);
+#pragma unroll
+      for (int p = 0; p < PIX; ++p) {
+        const float4 v = rec[lane + 64 * (band0 + p)];
+        T[p] = v.x;
+        const float dot = gr[p] * v.y + gg[p] * v.z + gb[p] * v.w;
+        gs_[p] = v.x > 0.0f ? dot / v.x : 0.0f;
+      }
+    }
+    if (lo >= hi) return;
+  }
 
   // Pixel rectangle of this wave's bands clipped to the image.
   const float rx0 = float(ox), ry0 = float(oy + band0 * kBandRows);
@@ -107,13 +145,17 @@ __device__ __forceinline__ void composite_bwd_tile(const CompositeBwdArgs& a, fl
   const bool second_writer = row_writer || lane == 1;
   const int second_field = row_writer ? 4 + field : 8;
 
-  for (int64_t top = start + max_n; top > start; top -= 64) {
+  // Each batch's ids are requested one batch ahead, once the current batch
+  // is in LDS, so a batch waits on one dependent load (the gather), not two.
+  uint32_t next_id =
+      start + hi - 1 - lane >= start + lo ? uint32_t(a.ids[start + hi - 1 - lane]) : 0u;
+  for (int64_t top = start + hi; top > start + lo; top -= 64) {
     const int64_t e = top - 1 - lane;
     LaneSplat mine;
     int gid = 0;
     uint32_t bands = 0;  // bit k: the Gaussian can reach a pixel of band k
-    if (e >= start) {
-      gid = int(min(uint32_t(a.ids[e]), a.max_id));
+    if (e >= start + lo) {
+      gid = int(min(next_id, a.max_id));
       const GsRecord rec = load_projected(a.pmean, a.pinv, a.pcolor, a.popacity, gid);
 #pragma unroll
       for (int k = 0; k < PIX; ++k) {
@@ -126,6 +168,7 @@ __device__ __forceinline__ void composite_bwd_tile(const CompositeBwdArgs& a, fl
     chunk[lane][0] = make_float4(mine.u, mine.v, mine.o, mine.pa);
     chunk[lane][1] = make_float4(mine.pb, mine.pc, mine.r, mine.g);
     chunk[lane][2] = make_float4(mine.b, mine.oa, mine.ob, mine.oc);
+    next_id = e - 64 >= start + lo ? uint32_t(a.ids[e - 64]) : 0u;
     uint64_t mask = __ballot(bands != 0);
     while (mask) {
       const int j = __builtin_ctzll(mask);
@@ -251,22 +294,22 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_bwd_kernel(Com
   // broadcasts per entry instead of twelve v_readlane.
   __shared__ float4 chunk[kCompositeWaves][64][3];
   const int slot = xcd_swizzle(blockIdx.x, gridDim.x) * kCompositeWaves + wid;
-  int tile, band;
-  bool quarter;
-  if (!composite_item(a.items, a.num_items, a.num_tiles, a.split_all, slot, tile, band, quarter))
+  int tile, kind, index;
+  if (!composite_item(a.items, a.num_items, a.num_tiles, a.split_all, slot, tile, kind, index))
     return;
   if constexpr (QUARTERS) {
     static_assert(PIX_TILE >= kCompositeWaves, "quarters of 64-pixel bands");
     constexpr int QPIX = PIX_TILE / kCompositeWaves;
-    if (quarter) {
-      composite_bwd_tile<TILE, ABS, QPIX>(a, chunk[wid], lane, tile, band * QPIX);
-    } else {
+    if (kind == kItemQuarter) {
+      composite_bwd_tile<TILE, ABS, QPIX>(a, chunk[wid], lane, tile, index * QPIX, -1);
+    } else if (kind == kItemTile || index == 0) {  // a segmented tile whole, by its first item
       for (int q = 0; q < kCompositeWaves; ++q)
-        composite_bwd_tile<TILE, ABS, QPIX>(a, chunk[wid], lane, tile, q * QPIX);
+        composite_bwd_tile<TILE, ABS, QPIX>(a, chunk[wid], lane, tile, q * QPIX, -1);
     }
   } else {
-    if (quarter && band != 0) return;
-    composite_bwd_tile<TILE, ABS, PIX_TILE>(a, chunk[wid], lane, tile, 0);
+    if (kind == kItemQuarter && index != 0) return;  // the tile whole, by its first quarter
+    composite_bwd_tile<TILE, ABS, PIX_TILE>(a, chunk[wid], lane, tile, 0,
+                                            kind == kItemSegment ? index : -1);
   }
 }
 
@@ -302,7 +345,8 @@ extern "C" GS_API int gs_composite_bwd(const float* projected_mean,
                                        const float* grad_image, const float* final_transmittance,
                                        const int32_t* n_contributors, const int32_t* tile_order,
                                        gs_view view, float* grad_projected, float* grad_absolute,
-                                       void* stream) {
+                                       const void* checkpoints, size_t checkpoint_bytes,
+                                       int64_t num_intersections, void* stream) {
   clear_error();
   GS_TRY(check_view(view, true));
   GS_REQUIRE(view.rendering_mode == GS_MODE_GAUSSIAN, GS_ERR_UNSUPPORTED,
@@ -338,10 +382,23 @@ extern "C" GS_API int gs_composite_bwd(const float* projected_mean,
   a.views = m.views;
   a.grad = grad_projected;
   a.grad_abs = grad_absolute;
-  const DispatchPlan plan = dispatch_plan(a.num_tiles, view.tile_size, view.active_tiles);
+  const DispatchPlan plan = dispatch_plan(a.num_tiles, view.tile_size, view.active_tiles, true);
   a.items = tile_order;
   a.num_items = plan.items();
   a.split_all = plan.split_all;
+  a.ckpt_table = nullptr;
+  a.ckpt_records = nullptr;
+  a.ckpt_capacity = 0;
+  if (checkpoints && !plan.split_all) {
+    GS_REQUIRE(num_intersections >= 0, GS_ERR_INVALID_ARGUMENT, "negative intersection count");
+    const CheckpointLayout c = checkpoint_layout(const_cast<void*>(checkpoints), view.tile_size,
+                                                 num_intersections);
+    GS_REQUIRE(checkpoint_bytes >= c.bytes, GS_ERR_WORKSPACE,
+               "checkpoint buffer too small (%zu bytes, need %zu)", checkpoint_bytes, c.bytes);
+    a.ckpt_table = c.table;
+    a.ckpt_records = c.records;
+    a.ckpt_capacity = c.capacity;
+  }
   hipStream_t s = as_stream(stream);
   switch (view.tile_size) {
     case 4: launch<4>(a, s); break;

@@ -39,14 +39,23 @@ struct CompositeArgs {
   float* image;
   float* final_t;
   int32_t* n_contrib;
+  // Checkpoints of whole-tile walks for the backward (CheckpointLayout), or
+  // null counter: none.
+  uint32_t* ckpt_counter;
+  int32_t* ckpt_table;
+  float4* ckpt_records;
+  int64_t ckpt_capacity;
 };
 
 // One wave composites PIX pixels per lane of `tile`: the 64-pixel bands
 // band0 .. band0 + PIX - 1 (all of the tile's bands for a whole-tile item, a
 // quarter of them for a quarter item; every wave walks the whole list).
+// With `checkpoints` (whole tiles only) the walk records the checkpoints
+// described at CheckpointLayout.
 template <int TILE, bool ELLIPSOID, int PIX>
 __device__ __forceinline__ void composite_tile(const CompositeArgs& a, float4 (*chunk)[3],
-                                               int lane, int tile, int band0) {
+                                               int* ck_slots, int lane, int tile, int band0,
+                                               bool checkpoints) {
   constexpr int NPIX = TILE * TILE;
 
   // Mosaic tile -> view and the tile's pixel origin inside that view.
@@ -94,18 +103,54 @@ __device__ __forceinline__ void composite_tile(const CompositeArgs& a, float4 (*
   };
 
   bool running = any_live();
+  // Checkpoint state (wave-uniform): crossings reached, records written (a
+  // prefix of the crossings: once the pool is full every later allocation
+  // fails), the walk position of the next crossing; the records' slots go to
+  // the wave's ck_slots in LDS.
+  constexpr int kRecord = PIX * 64;
+  int ck_count = 0, ck_written = 0;
+  int ck_next =
+      checkpoints && checkpoint_count(start, list_len, list_len) > 0 ? checkpoint_batch(start, 1)
+                                                                     : -1;
+  // The ids of each batch are requested one batch ahead, once the current
+  // batch's records are in LDS, so they arrive while the current batch is
+  // walked and each batch waits on one dependent load (the record gather).
+  uint32_t id = start + lane < end ? uint32_t(a.ids[start + lane]) : 0u;
   for (int64_t base = start; running && base < end; base += 64) {
+    if (checkpoints && int(base - start) == ck_next) {
+      // Crossing ck_count + 1: record T and the colour since the previous
+      // record, then restart the colour sums.
+      uint32_t slot = 0xFFFFFFFFu;
+      if (lane == 0 && ck_written == ck_count) slot = atomicAdd(a.ckpt_counter, 1u);
+      slot = uint32_t(__builtin_amdgcn_readfirstlane(int(slot)));
+      const bool ok = ck_written == ck_count && int64_t(slot) < a.ckpt_capacity;
+      const int64_t pos = checkpoint_first(start) + int64_t(ck_count) * kCheckpointEntries;
+      if (lane == 0) a.ckpt_table[pos / kCheckpointEntries] = ok ? int32_t(slot) : -1;
+      if (ok) {
+        float4* rec = a.ckpt_records + int64_t(slot) * kRecord;
+#pragma unroll
+        for (int k = 0; k < PIX; ++k) {
+          rec[lane + 64 * k] = make_float4(T[k], cr[k], cg[k], cb[k]);
+          cr[k] = cg[k] = cb[k] = 0.0f;
+        }
+        if (lane == 0) ck_slots[ck_written] = int(slot);
+        ++ck_written;
+      }
+      ++ck_count;
+      ck_next = ck_count < kMaxCheckpoints ? checkpoint_batch(start, ck_count + 1) : -1;
+    }
     const int64_t e = base + lane;
     LaneSplat mine;
     bool keep = false;
     if (e < end) {
-      const GsRecord rec = load_record(a.records, min(uint32_t(a.ids[e]), a.max_id));
+      const GsRecord rec = load_record(a.records, min(id, a.max_id));
       keep = touches_rect(rec, rx0, rx1, ry0, ry1);
       mine = lane_splat(rec);
     }
     chunk[lane][0] = make_float4(mine.u, mine.v, mine.o, mine.pa);
     chunk[lane][1] = make_float4(mine.pb, mine.pc, mine.r, mine.g);
     chunk[lane][2] = make_float4(mine.b, mine.cut, 0.0f, 0.0f);
+    id = e + 64 < end ? uint32_t(a.ids[e + 64]) : 0u;
     uint64_t mask = __ballot(keep);
     // No break inside: the loop ends through its condition, which keeps the
     // per-pixel active flags out of extra mask-merging control flow.
@@ -148,6 +193,20 @@ __device__ __forceinline__ void composite_tile(const CompositeArgs& a, float4 (*
       }
     }
   }
+  // The records' colours become the colour composited after each record (a
+  // suffix sum over the later records and the colour since the last one); the
+  // image is the sum over all of them.  Each lane reads back its own writes.
+  for (int j = checkpoints ? ck_written - 1 : -1; j >= 0; --j) {
+    float4* rec = a.ckpt_records + int64_t(ck_slots[j]) * kRecord;
+#pragma unroll
+    for (int k = 0; k < PIX; ++k) {
+      const float4 v = rec[lane + 64 * k];
+      rec[lane + 64 * k] = make_float4(v.x, cr[k], cg[k], cb[k]);
+      cr[k] += v.y;
+      cg[k] += v.z;
+      cb[k] += v.w;
+    }
+  }
 
 #pragma unroll
   for (int k = 0; k < PIX; ++k) {
@@ -168,11 +227,11 @@ __device__ __forceinline__ void composite_tile(const CompositeArgs& a, float4 (*
 // workgroups are mapped onto XCDs so that each XCD takes one region of the
 // plan (xcd_swizzle).  QUARTERS: the launch's items are quarters (every tile
 // split); a whole-tile item is then composited as its four quarters in turn.
-// Otherwise items are whole tiles; of a tile's four quarter items the first
-// composites the whole tile and the others have no work.  Each kernel thus
-// composites every pixel of any plan exactly once, with one instance of the
-// walk (two would share one register allocation).
-template <int TILE, bool ELLIPSOID, bool QUARTERS>
+// Otherwise items are whole tiles; of a tile split into several items the
+// first composites the whole tile and the others have no work.  Each kernel
+// thus composites every pixel of any plan exactly once, with one instance of
+// the walk (two would share one register allocation).
+template <int TILE, bool ELLIPSOID, bool QUARTERS, bool CKPT>
 __global__ __launch_bounds__(kCompositeWaves * 64) void composite_fwd_kernel(CompositeArgs a) {
   constexpr int NPIX = TILE * TILE;
   constexpr int PIX_TILE = NPIX >= 64 ? NPIX / 64 : 1;
@@ -184,43 +243,53 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_fwd_kernel(Com
   // (pb, pc, r, g), (b, cut, -, -): written once per lane, then read as LDS
   // broadcasts per entry instead of ten v_readlane.
   __shared__ float4 chunk[kCompositeWaves][64][3];
+  __shared__ int ck_slots[kCompositeWaves][CKPT ? kMaxCheckpoints : 1];  // a wave's records
   const int slot = xcd_swizzle(blockIdx.x, gridDim.x) * kCompositeWaves + wid;
-  int tile, band;
-  bool quarter;
-  if (!composite_item(a.items, a.num_items, a.num_tiles, a.split_all, slot, tile, band, quarter))
+  int tile, kind, index;
+  if (!composite_item(a.items, a.num_items, a.num_tiles, a.split_all, slot, tile, kind, index))
     return;
+  // Items that split a tile some other way (a backward plan's segments) are
+  // composited whole by the tile's first item.
+  if (kind != kItemTile && !(QUARTERS && kind == kItemQuarter) && index != 0) return;
   if constexpr (QUARTERS) {
     static_assert(PIX_TILE >= kCompositeWaves, "quarters of 64-pixel bands");
     constexpr int QPIX = PIX_TILE / kCompositeWaves;
-    if (quarter) {
-      composite_tile<TILE, ELLIPSOID, QPIX>(a, chunk[wid], lane, tile, band * QPIX);
+    if (kind == kItemQuarter) {
+      composite_tile<TILE, ELLIPSOID, QPIX>(a, chunk[wid], ck_slots[wid], lane, tile, index * QPIX,
+                                            false);
     } else {
       for (int q = 0; q < kCompositeWaves; ++q)
-        composite_tile<TILE, ELLIPSOID, QPIX>(a, chunk[wid], lane, tile, q * QPIX);
+        composite_tile<TILE, ELLIPSOID, QPIX>(a, chunk[wid], ck_slots[wid], lane, tile, q * QPIX,
+                                              false);
     }
   } else {
-    if (quarter && band != 0) return;
-    composite_tile<TILE, ELLIPSOID, PIX_TILE>(a, chunk[wid], lane, tile, 0);
+    composite_tile<TILE, ELLIPSOID, PIX_TILE>(a, chunk[wid], ck_slots[wid], lane, tile, 0, CKPT);
   }
 }
 
-template <int TILE, bool QUARTERS>
+template <int TILE, bool QUARTERS, bool CKPT>
 void launch_items(const CompositeArgs& a, bool ellipsoid, hipStream_t s) {
   const unsigned blocks = unsigned(
       a.items ? a.num_items / kCompositeWaves
               : (a.split_all ? a.num_tiles : ceil_div(a.num_tiles, kCompositeWaves)));
   if (ellipsoid)
-    composite_fwd_kernel<TILE, true, QUARTERS><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
+    composite_fwd_kernel<TILE, true, QUARTERS, CKPT><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
   else
-    composite_fwd_kernel<TILE, false, QUARTERS><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
+    composite_fwd_kernel<TILE, false, QUARTERS, CKPT><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
 }
 
+// Checkpoint recording is a kernel of its own: the code for it costs the
+// walk registers (70 VGPRs instead of 64 at tile 16, 7 waves per SIMD
+// instead of 8), which only long lists repay.
 template <int TILE>
 void launch(const CompositeArgs& a, bool ellipsoid, hipStream_t s) {
   if constexpr (TILE >= 16) {
-    if (a.split_all) return launch_items<TILE, true>(a, ellipsoid, s);
+    if (a.split_all) return launch_items<TILE, true, false>(a, ellipsoid, s);
   }
-  launch_items<TILE, false>(a, ellipsoid, s);
+  if constexpr (TILE <= 16) {
+    if (a.ckpt_counter) return launch_items<TILE, false, true>(a, ellipsoid, s);
+  }
+  launch_items<TILE, false, false>(a, ellipsoid, s);
 }
 
 }  // namespace
@@ -228,11 +297,24 @@ void launch(const CompositeArgs& a, bool ellipsoid, hipStream_t s) {
 
 using namespace gs;
 
+__global__ void checkpoint_clear_kernel(uint32_t* counter) { *counter = 0u; }
+
+extern "C" GS_API size_t gs_composite_checkpoint_bytes(gs_view view, int64_t num_intersections,
+                                                       int64_t longest_list) {
+  if (check_view(view, true) != GS_OK || num_intersections < 0) return 0;
+  if (longest_list <= kCheckpointMinList) return 0;  // no walk would record one
+  if (view.tile_size > 16) return 0;  // 16 pixels per lane leave no registers for them
+  const Mosaic m = mosaic_of(view);
+  if (dispatch_plan(m.num_tiles(), view.tile_size, view.active_tiles, false).split_all) return 0;
+  return checkpoint_layout(nullptr, view.tile_size, num_intersections).bytes;
+}
+
 extern "C" GS_API int gs_composite(const void* records, int64_t num_records,
-                                   const int32_t* gaussian_ids, const int64_t* ranges,
-                                   const int32_t* tile_order, gs_view view, float* image,
-                                   float* final_transmittance, int32_t* n_contributors,
-                                   void* stream) {
+                                   const int32_t* gaussian_ids, int64_t num_intersections,
+                                   const int64_t* ranges, const int32_t* tile_order, gs_view view,
+                                   float* image, float* final_transmittance,
+                                   int32_t* n_contributors, void* checkpoints,
+                                   size_t checkpoint_bytes, void* stream) {
   clear_error();
   GS_TRY(check_view(view, true));
   GS_REQUIRE(ranges && image && final_transmittance && n_contributors, GS_ERR_INVALID_ARGUMENT,
@@ -262,12 +344,30 @@ extern "C" GS_API int gs_composite(const void* records, int64_t num_records,
   a.image = image;
   a.final_t = final_transmittance;
   a.n_contrib = n_contributors;
-  const DispatchPlan plan = dispatch_plan(a.num_tiles, view.tile_size, view.active_tiles);
+  const DispatchPlan plan = dispatch_plan(a.num_tiles, view.tile_size, view.active_tiles, false);
   a.items = tile_order;
   a.num_items = plan.items();
   a.split_all = plan.split_all;
-  const bool ellipsoid = view.rendering_mode == GS_MODE_ELLIPSOID;
+  GS_REQUIRE(num_intersections >= 0, GS_ERR_INVALID_ARGUMENT, "negative intersection count");
+  a.ckpt_counter = nullptr;
+  a.ckpt_table = nullptr;
+  a.ckpt_records = nullptr;
+  a.ckpt_capacity = 0;
   hipStream_t s = as_stream(stream);
+  if (checkpoints && !plan.split_all && view.tile_size <= 16) {
+    const CheckpointLayout c = checkpoint_layout(checkpoints, view.tile_size, num_intersections);
+    GS_REQUIRE(checkpoint_bytes >= c.bytes, GS_ERR_WORKSPACE,
+               "checkpoint buffer too small (%zu bytes, need %zu)", checkpoint_bytes, c.bytes);
+    GS_REQUIRE((reinterpret_cast<uintptr_t>(checkpoints) & 255u) == 0, GS_ERR_INVALID_ARGUMENT,
+               "checkpoint buffer must be 256-byte aligned");
+    a.ckpt_counter = c.counter;
+    a.ckpt_table = c.table;
+    a.ckpt_records = c.records;
+    a.ckpt_capacity = c.capacity;
+    checkpoint_clear_kernel<<<1, 1, 0, s>>>(c.counter);
+    GS_TRY(check_launch("composite checkpoints"));
+  }
+  const bool ellipsoid = view.rendering_mode == GS_MODE_ELLIPSOID;
   switch (view.tile_size) {
     case 4: launch<4>(a, ellipsoid, s); break;
     case 8: launch<8>(a, ellipsoid, s); break;

@@ -323,19 +323,33 @@ __global__ __launch_bounds__(256) void tables_kernel(int32_t* __restrict__ diff2
 
   // 4. Ranges: row start + start in the row; a tile ends where the next tile
   // of its row starts (the last one at the row's end).  totals[3] = tiles
-  // with a non-empty list (the compositing launch shape depends on it).
+  // with a non-empty list (the compositing launch shape depends on it) in
+  // the low 32 bits, the longest list (capped at 2^31 - 1; whether the
+  // compositing walk records checkpoints depends on it) in the high 32.
   const int64_t num_tiles = int64_t(tw) * th;
   int64_t active = 0;
+  int64_t longest = 0;
   for (int64_t t = threadIdx.x; t < num_tiles; t += 256) {
     const int ty = int(t / tw), tx = int(t - int64_t(ty) * tw);
     const int64_t begin = s_row[ty] + uint32_t(tab[ty * pitch + tx]);
     const int64_t end = tx + 1 < tw ? s_row[ty] + uint32_t(tab[ty * pitch + tx + 1]) : s_end[ty];
     reinterpret_cast<longlong2*>(ranges)[t] = make_longlong2(begin, end);
     active += end > begin ? 1 : 0;
+    longest = max(longest, end - begin);
   }
   int64_t tot_active;
   block_exclusive_scan(active, scratch, tot_active);
-  if (threadIdx.x == 0) totals[3] = tot_active;
+  __syncthreads();  // scratch reused
+  uint32_t l32 = uint32_t(min(longest, int64_t(0x7FFFFFFF)));
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) l32 = max(l32, uint32_t(__shfl_xor(int(l32), o, 64)));
+  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = l32;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t mx = 0;
+    for (int w = 0; w < 4; ++w) mx = max(mx, uint32_t(scratch[w]));
+    totals[3] = tot_active | (int64_t(mx) << 32);
+  }
 }
 
 // Row-list entry packing: first column | (width - 1) << 8 | row << 16 (grids

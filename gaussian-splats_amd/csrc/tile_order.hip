@@ -9,11 +9,12 @@
 // longer than the rest of the launch (long lists in dense regions).  The plan
 // keeps each XCD's region but sorts its tiles by decreasing expected work (to
 // eight significant bits), so the long tiles start first and the short ones
-// fill the tail (longest-processing-time-first list scheduling), and can
-// split the heaviest tiles of the region into four items of a quarter of
-// their pixel bands each, which walk the list on four waves at once
-// (kSplitHeavy).  Ties keep ascending tile index, so the plan is
-// deterministic.
+// fill the tail (longest-processing-time-first list scheduling).  A backward
+// plan also splits the region's heaviest tiles into kSegments items, each
+// walking one segment of the tile's entries (composite_bwd.hip), so a tile
+// whose walk is far longer than the rest no longer sets the launch's length;
+// with few tiles every tile is split into the quarters of its pixel bands.
+// Ties keep ascending tile index, so the plan is deterministic.
 //
 // Work estimates: the list length of the tile (forward), or the largest
 // contributor count of its pixels (the entries the backward walks).
@@ -28,13 +29,16 @@ namespace {
 constexpr int kOrderThreads = 1024;
 constexpr int kOrderMax = 8192;  // tiles per region ordered by one workgroup
 
-// key[t] = expected work of tile t, capped at 2^16 - 1.  One wave per tile.
+// key[t] = expected work of tile t, capped at 2^16 - 1, and crossings[t] =
+// the forward checkpoints a backward walk of the tile crosses (with both
+// n_contributors and ranges; else 0).  One wave per tile.
 __global__ __launch_bounds__(256) void tile_key_kernel(const int64_t* __restrict__ ranges,
                                                        const int32_t* __restrict__ ncon,
                                                        int tiles_w, int num_tiles, int tile,
                                                        int width, int height, int view_tw,
                                                        int view_th, int cols, int views,
-                                                       uint32_t* __restrict__ key) {
+                                                       uint32_t* __restrict__ key,
+                                                       uint32_t* __restrict__ crossings) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= num_tiles) return;
@@ -57,7 +61,36 @@ __global__ __launch_bounds__(256) void tile_key_kernel(const int64_t* __restrict
   } else {
     work = ranges[2 * t + 1] - ranges[2 * t];
   }
-  if (lane == 0) key[t] = uint32_t(min(max(work, int64_t(0)), int64_t(0xFFFF)));
+  if (lane == 0) {
+    key[t] = uint32_t(min(max(work, int64_t(0)), int64_t(0xFFFF)));
+    crossings[t] = ncon && ranges ? uint32_t(checkpoint_count(ranges[2 * t], int(work),
+                                                              ranges[2 * t + 1] - ranges[2 * t]))
+                                  : 0u;
+  }
+}
+
+// Exclusive prefix sum over the 1024 threads' values (16 waves), in LDS
+// scratch of 16 words; `total` receives the sum.  All threads take part.
+__device__ __forceinline__ uint32_t block_exclusive(uint32_t v, uint32_t* scratch,
+                                                    uint32_t& total) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  uint32_t incl = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t u = uint32_t(__shfl_up(int(incl), o, 64));
+    if (lane >= o) incl += u;
+  }
+  __syncthreads();  // scratch free (an earlier call may still read it)
+  if (lane == 63) scratch[wid] = incl;
+  __syncthreads();
+  uint32_t before = 0, all = 0;
+  for (int w = 0; w < 16; ++w) {
+    const uint32_t c = scratch[w];
+    before += w < wid ? c : 0u;
+    all += c;
+  }
+  total = all;
+  return before + incl - v;
 }
 
 // Region r of the order: the tiles of the workgroups xcd_swizzle gives XCD r.
@@ -71,75 +104,58 @@ __device__ __forceinline__ void region(int r, int num_tiles, int& lo, int& hi) {
 
 // One workgroup per region: a stable counting sort of the region's tiles by
 // the eight most significant bits of the key (relative to the region's largest
-// key), largest first, then the region's items in that order: the first H
-// tiles as four quarter items each, the others whole.  H: every tile when the
-// plan splits all; with heavy_split the tiles whose key (to those eight bits)
-// exceeds kHeavyNum / kHeavyDen of the region's mean, at most one in
-// kHeavyShare; else none.
-// Sixteen waves take contiguous index segments; a wave ranks its tiles per
-// bucket with ballots (eight, one per digit bit), so ties keep index order.
-// Unused slots of the region get -1.
-__global__ __launch_bounds__(kOrderThreads) void tile_plan_kernel(const uint32_t* __restrict__ key,
-                                                                  int num_tiles, int heavy_split,
-                                                                  int split_all, int region_slots,
-                                                                  int32_t* __restrict__ items) {
+// key), largest first, then the region's items in that order, each tile as
+// 1 + extra items: extra = 3 (its four quarters) when the plan splits every
+// tile, else its checkpoint crossings (1 + crossings segments) while the
+// region's spare slots last, heaviest tiles first, else 0 (whole).  Sixteen
+// waves take contiguous index segments; a wave ranks its tiles per bucket
+// with ballots (eight, one per digit bit), so ties keep index order.  Unused
+// slots of the region get -1.
+__global__ __launch_bounds__(kOrderThreads) void tile_plan_kernel(
+    const uint32_t* __restrict__ key, const uint32_t* __restrict__ crossings, int num_tiles,
+    int segments, int split_all, int region_slots, int32_t* __restrict__ items) {
   constexpr int kWaves = kOrderThreads / 64;
   constexpr int kPerLane = kOrderMax / kOrderThreads;  // tiles per lane at most
   __shared__ uint32_t cnt[kWaves][256];
   __shared__ uint32_t start[256];
-  __shared__ uint32_t smax, ssum, sheavy;
+  __shared__ uint32_t smax, scratch[kWaves];
+  __shared__ int32_t sorted_tile[kOrderMax];
+  __shared__ uint8_t sorted_extra[kOrderMax];
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   int lo, hi;
   region(blockIdx.x, num_tiles, lo, hi);
   const int n = hi - lo;
   int32_t* out = items + int64_t(blockIdx.x) * region_slots;
-  if (n > kOrderMax) {  // too large to sort here: index order, no heavy split
+  if (n > kOrderMax) {  // too large to sort here: index order, no segments
     const int per = split_all ? 4 : 1;
     for (int i = threadIdx.x; i < n * per; i += kOrderThreads)
-      out[i] = split_all ? ((lo + i / 4) << 3 | 4 | (i & 3)) : (lo + i) << 3;
+      out[i] = split_all ? ((lo + i / 4) << 7 | 0x20 | (i & 3)) : (lo + i) << 7;
     for (int i = n * per + threadIdx.x; i < region_slots; i += kOrderThreads) out[i] = -1;
     return;
   }
-  if (threadIdx.x == 0) {
-    smax = 0;
-    ssum = 0;
-    sheavy = 0;
-  }
+  if (threadIdx.x == 0) smax = 0;
   for (int i = threadIdx.x; i < kWaves * 256; i += kOrderThreads) (&cnt[0][0])[i] = 0;
   __syncthreads();
   const int seg = (n + kWaves - 1) / kWaves;  // <= kPerLane * 64
   const int s0 = wid * seg, s1 = min(s0 + seg, n);
   uint32_t k[kPerLane];
-  uint32_t m = 0, sum = 0;
+  uint32_t m = 0;
 #pragma unroll
   for (int i = 0; i < kPerLane; ++i) {
     const int e = s0 + i * 64 + lane;
     k[i] = e < s1 ? key[lo + e] : 0u;
     m = max(m, k[i]);
-    sum += k[i];  // at most 8192 keys below 2^16: no overflow
   }
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    m = max(m, uint32_t(__shfl_xor(int(m), o, 64)));
-    sum += uint32_t(__shfl_xor(int(sum), o, 64));
-  }
-  if (lane == 0) {
-    atomicMax(&smax, m);
-    atomicAdd(&ssum, sum);
-  }
+  for (int o = 32; o > 0; o >>= 1) m = max(m, uint32_t(__shfl_xor(int(m), o, 64)));
+  if (lane == 0) atomicMax(&smax, m);
   __syncthreads();
   const int shift = max(0, 24 - __clz(int(smax | 1u)));  // smax >> shift < 256
-  // Heavy: top eight bits above those of kHeavyNum / kHeavyDen of the mean
-  // (a prefix of the sorted order).
-  const uint32_t heavy_above =
-      uint32_t((uint64_t(kHeavyNum) * ssum / (uint64_t(kHeavyDen) * uint64_t(max(n, 1)))) >> shift);
   uint32_t dig[kPerLane], rank[kPerLane];
-  uint32_t heavy = 0;
 #pragma unroll
   for (int i = 0; i < kPerLane; ++i) {
     const int e = s0 + i * 64 + lane;
     const bool valid = e < s1;
-    heavy += uint32_t(valid && (k[i] >> shift) > heavy_above);
     dig[i] = 255u - (k[i] >> shift);
     uint32_t plo = uint32_t(__ballot(valid)), phi = uint32_t(__ballot(valid) >> 32);
 #pragma unroll
@@ -158,9 +174,6 @@ __global__ __launch_bounds__(kOrderThreads) void tile_plan_kernel(const uint32_t
     }
     rank[i] = c + before;
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) heavy += uint32_t(__shfl_xor(int(heavy), o, 64));
-  if (lane == 0) atomicAdd(&sheavy, heavy);
   __syncthreads();
   // Bucket starts: digit-major over the waves, in one wave.
   if (wid == 0) {
@@ -184,24 +197,52 @@ __global__ __launch_bounds__(kOrderThreads) void tile_plan_kernel(const uint32_t
     }
   }
   __syncthreads();
-  const int h = split_all   ? n
-                : heavy_split ? min(int(sheavy), (n + kHeavyShare - 1) / kHeavyShare)
-                              : 0;
 #pragma unroll
   for (int i = 0; i < kPerLane; ++i) {
     const int e = s0 + i * 64 + lane;
     if (e < s1) {
       const int p = int(start[dig[i]] + cnt[wid][dig[i]] + rank[i]);  // sorted position
-      const int t = lo + e;
-      if (p < h) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) out[4 * p + j] = t << 3 | 4 | j;
-      } else {
-        out[3 * h + p] = t << 3;
-      }
+      sorted_tile[p] = lo + e;
+      sorted_extra[p] = uint8_t(split_all ? 3u : segments ? min(crossings[lo + e], 63u) : 0u);
     }
   }
-  for (int i = n + 3 * h + threadIdx.x; i < region_slots; i += kOrderThreads) out[i] = -1;
+  __syncthreads();
+  // Thread i takes sorted positions [kPerLane i, kPerLane i + kPerLane).
+  const int p0 = int(threadIdx.x) * kPerLane;
+  uint32_t ex[kPerLane], sum = 0;
+#pragma unroll
+  for (int i = 0; i < kPerLane; ++i) {
+    ex[i] = p0 + i < n ? uint32_t(sorted_extra[p0 + i]) : 0u;
+    sum += ex[i];
+  }
+  // Spare slots go to the tiles in sorted order while they fit whole.
+  uint32_t all;
+  uint32_t before = block_exclusive(sum, scratch, all);
+  const uint32_t spare = uint32_t(region_slots - n);
+  sum = 0;
+#pragma unroll
+  for (int i = 0; i < kPerLane; ++i) {
+    if (before + ex[i] > spare) ex[i] = 0;  // does not fit: whole
+    before += ex[i];
+    sum += ex[i];
+  }
+  // Item offsets of the final counts (1 + extra per tile).
+  uint32_t used;
+  uint32_t off = block_exclusive(sum, scratch, used) + uint32_t(p0);
+#pragma unroll
+  for (int i = 0; i < kPerLane; ++i) {
+    if (p0 + i < n) {
+      const int t = sorted_tile[p0 + i];
+      if (ex[i] == 0) {
+        out[off] = t << 7;
+      } else {
+        const int code = split_all ? 0x20 : 0x40;
+        for (uint32_t j = 0; j <= ex[i]; ++j) out[off + j] = t << 7 | code | int(j);
+      }
+      off += 1 + ex[i];
+    }
+  }
+  for (int i = n + int(used) + threadIdx.x; i < region_slots; i += kOrderThreads) out[i] = -1;
 }
 
 }  // namespace
@@ -209,10 +250,11 @@ __global__ __launch_bounds__(kOrderThreads) void tile_plan_kernel(const uint32_t
 
 using namespace gs;
 
-// Scratch memory of gs_tile_order_noalloc: the per-tile work keys.  One copy
-// per GPU (each at its own device address), held until the process ends.
-constexpr int kNoAllocMaxTiles = GS_TILE_ORDER_NOALLOC_MAX_TILES;  // 1 MiB of keys
-static __device__ __align__(256) uint32_t scratch[kNoAllocMaxTiles];
+// Scratch memory of gs_tile_order_noalloc: the per-tile work keys and
+// checkpoint crossings.  One copy per GPU (each at its own device address),
+// held until the process ends.
+constexpr int kNoAllocMaxTiles = GS_TILE_ORDER_NOALLOC_MAX_TILES;  // 2 MiB of keys
+static __device__ __align__(256) uint32_t scratch[2 * kNoAllocMaxTiles];
 
 namespace {
 
@@ -250,14 +292,16 @@ int scratch_keys(hipStream_t stream, uint32_t** keys) {
 int tile_order_launch(const int64_t* ranges, const int32_t* n_contributors, const gs_view& view,
                       const Mosaic& m, int32_t* items, uint32_t* key, hipStream_t s) {
   const int num_tiles = m.num_tiles();
-  GS_REQUIRE(num_tiles < (1 << 27), GS_ERR_OVERFLOW, "too many tiles (%d)", num_tiles);
-  const DispatchPlan plan = dispatch_plan(num_tiles, view.tile_size, view.active_tiles);
+  GS_REQUIRE(num_tiles < (1 << 24), GS_ERR_OVERFLOW, "too many tiles (%d)", num_tiles);
+  const DispatchPlan plan =
+      dispatch_plan(num_tiles, view.tile_size, view.active_tiles, n_contributors != nullptr);
+  uint32_t* crossings = key + num_tiles;
   tile_key_kernel<<<unsigned(ceil_div(num_tiles, 4)), 256, 0, s>>>(
       ranges, n_contributors, m.tiles_w(), num_tiles, view.tile_size, view.image_width,
-      view.image_height, m.tw, m.th, m.cols, m.views, key);
+      view.image_height, m.tw, m.th, m.cols, m.views, key, crossings);
   GS_TRY(check_launch("tile_order keys"));
-  tile_plan_kernel<<<8, kOrderThreads, 0, s>>>(key, num_tiles, plan.heavy ? 1 : 0,
-                                                plan.split_all ? 1 : 0,
+  tile_plan_kernel<<<8, kOrderThreads, 0, s>>>(key, crossings, num_tiles,
+                                                plan.segments ? 1 : 0, plan.split_all ? 1 : 0,
                                                 plan.items() / 8, items);
   return check_launch("tile_order plan");
 }
@@ -267,14 +311,15 @@ int tile_order_launch(const int64_t* ranges, const int32_t* n_contributors, cons
 extern "C" {
 
 GS_API size_t gs_tile_order_workspace_bytes(int32_t num_tiles) {
-  return num_tiles > 0 ? align_up(size_t(num_tiles) * sizeof(uint32_t)) : 0;
+  return num_tiles > 0 ? align_up(size_t(num_tiles) * 2 * sizeof(uint32_t)) : 0;
 }
 
-GS_API int64_t gs_tile_order_items(gs_view view) {
+GS_API int64_t gs_tile_order_items(gs_view view, int32_t by_contributors) {
   clear_error();
   if (check_view(view, true) != GS_OK) return -1;
   const Mosaic m = mosaic_of(view);
-  return dispatch_plan(m.num_tiles(), view.tile_size, view.active_tiles).items();
+  return dispatch_plan(m.num_tiles(), view.tile_size, view.active_tiles, by_contributors != 0)
+      .items();
 }
 
 GS_API int gs_tile_order(const int64_t* ranges, const int32_t* n_contributors, gs_view view,

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parents[2] / "_lib" / "libgs_raster.so"
-ABI_VERSION = 8
+ABI_VERSION = 10
 
 GS_OK = 0
 GS_ERR_INVALID_ARGUMENT = 1
@@ -106,6 +106,51 @@ def active_tiles(ranges: torch.Tensor | None) -> int:
     return int(getattr(ranges, _ACTIVE_ATTR, 0)) if ranges is not None else 0
 
 
+_LONGEST_ATTR = "_gs_longest_list"
+
+
+def set_longest_list(ranges: torch.Tensor, length: int) -> None:
+    """Records on ``ranges`` the longest list (binning returns it with its
+    totals): the compositing walk records checkpoints only for long lists."""
+    setattr(ranges, _LONGEST_ATTR, int(length))
+
+
+def longest_list(ranges: torch.Tensor) -> int:
+    """The length recorded by ``set_longest_list``, else read from the
+    ranges (one device-to-host copy)."""
+    value = getattr(ranges, _LONGEST_ATTR, None)
+    if value is None:
+        value = int((ranges[:, 1] - ranges[:, 0]).max().item()) if ranges.numel() else 0
+    return int(value)
+
+
+_CHECKPOINT_ATTR = "_gs_checkpoints"
+
+
+def set_checkpoints(ranges: torch.Tensor, buffer: torch.Tensor | None) -> None:
+    """Records on ``ranges`` the forward's checkpoint buffer (gs_composite)
+    for the backward of the same lists."""
+    setattr(ranges, _CHECKPOINT_ATTR, buffer)
+
+
+def checkpoints(ranges: torch.Tensor | None) -> torch.Tensor | None:
+    """The buffer recorded by ``set_checkpoints``, or None."""
+    return getattr(ranges, _CHECKPOINT_ATTR, None) if ranges is not None else None
+
+
+def checkpoint_buffer(view: GsView, num_intersections: int, longest: int,
+                      device: torch.device):
+    """A checkpoint buffer for gs_composite (256-byte aligned), or None when
+    the walk records none (no list long enough, or every tile split into
+    quarters)."""
+    nbytes = library().gs_composite_checkpoint_bytes(view, int(num_intersections), int(longest))
+    if nbytes == 0:
+        return None
+    buf = torch.empty(nbytes + 256, dtype=torch.uint8, device=device)
+    off = (-buf.data_ptr()) % 256
+    return buf[off:off + nbytes]
+
+
 _SIGNATURES = {
     "gs_abi_version": (c_int, []),
     "gs_last_error": (ctypes.c_char_p, []),
@@ -154,17 +199,21 @@ _SIGNATURES = {
          c_void_p, c_size_t, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p],
     ),
     "gs_tile_order_workspace_bytes": (c_size_t, [c_int32]),
-    "gs_tile_order_items": (c_int64, [GsView]),
+    "gs_tile_order_items": (c_int64, [GsView, c_int32]),
     "gs_tile_order": (
         c_int, [c_void_p, c_void_p, GsView, c_void_p, c_void_p, c_size_t, c_void_p]
     ),
     "gs_tile_order_noalloc": (c_int, [c_void_p, c_void_p, GsView, c_void_p, c_void_p]),
+    "gs_composite_checkpoint_bytes": (c_size_t, [GsView, c_int64, c_int64]),
     "gs_composite": (
-        c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, GsView] + [c_void_p] * 4
+        c_int,
+        [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, GsView]
+        + [c_void_p] * 4 + [c_size_t, c_void_p],
     ),
     "gs_composite_bwd": (
         c_int,
-        [c_void_p] * 4 + [c_int64] + [c_void_p] * 6 + [GsView, c_void_p, c_void_p, c_void_p],
+        [c_void_p] * 4 + [c_int64] + [c_void_p] * 6
+        + [GsView, c_void_p, c_void_p, c_void_p, c_size_t, c_int64, c_void_p],
     ),
     "gs_device_errors": (c_int, [c_void_p, c_int32, c_void_p]),
     "gs_project_bwd": (
@@ -386,14 +435,16 @@ def dispatch_plan(
     n_contributors: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Work items of the compositing kernels for ``view`` (gs_tile_order):
-    each XCD's region of tiles, longest expected work first, its heaviest
-    tiles split into four quarter items.  The estimate is the list length
-    from ``ranges`` or the largest contributor count of each tile's pixels
-    from ``n_contributors``.  The compositing call must get the same view."""
+    each XCD's region of tiles, longest expected work first.  The estimate is
+    the list length from ``ranges`` alone (a plan for gs_composite) or the
+    largest contributor count of each tile's pixels from ``n_contributors``
+    (a plan for gs_composite_bwd; with ``ranges`` too, tiles whose walk
+    crosses the forward's checkpoints are split into segments).  The
+    compositing call must get the same view."""
     if ranges is None and n_contributors is None:
         raise ValueError("dispatch_plan needs ranges or n_contributors")
     lib = library()
-    count = lib.gs_tile_order_items(view)
+    count = lib.gs_tile_order_items(view, int(n_contributors is not None))
     if count < 0:
         check(GS_ERR_INVALID_ARGUMENT, "tile_order_items")
     items = torch.empty(int(count), dtype=torch.int32, device=device)

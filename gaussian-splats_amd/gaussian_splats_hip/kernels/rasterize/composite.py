@@ -58,7 +58,8 @@ def composite(
     order: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Composites the sorted per-tile lists; returns ``(image[H,W,3],
-    final_transmittance[H,W], n_contributors[H,W] int32)``."""
+    final_transmittance[H,W], n_contributors[H,W] int32)``.  The walk's
+    checkpoints (gs_composite) are recorded on ``ranges`` for the backward."""
     _check_tile(tile_size)
     device = nat.require_gpu(mean, gaussian_ids, ranges)
     if records is None:
@@ -67,6 +68,7 @@ def composite(
     if ranges.shape != (tiles_w * tiles_h, 2):
         raise ValueError(f"ranges must be [{tiles_w * tiles_h}, 2], got {tuple(ranges.shape)}")
     active = nat.active_tiles(ranges)
+    ranges_in = ranges
     ranges = nat.prepare(ranges, torch.int64)
     gaussian_ids = nat.prepare(gaussian_ids, torch.int32)
     image = torch.empty((image_height, image_width, 3), dtype=torch.float32, device=device)
@@ -76,13 +78,17 @@ def composite(
         1.0, 1.0, 0.0, 0.0, image_width, image_height, tile_size, rendering_mode=rendering_mode,
         confidence=confidence, opacity_threshold=opacity_threshold, active_tiles=active,
     )
+    checkpoints = nat.checkpoint_buffer(view, gaussian_ids.numel(), nat.longest_list(ranges_in),
+                                        device)
     nat.check(
         nat.library().gs_composite(
-            nat.ptr(records), records.shape[0], nat.ptr(gaussian_ids), nat.ptr(ranges),
-            nat.ptr(order), view,
-            nat.ptr(image),
-            nat.ptr(final_transmittance), nat.ptr(n_contributors), nat.stream(device),
+            nat.ptr(records), records.shape[0], nat.ptr(gaussian_ids), gaussian_ids.numel(),
+            nat.ptr(ranges), nat.ptr(order), view, nat.ptr(image), nat.ptr(final_transmittance),
+            nat.ptr(n_contributors), nat.ptr(checkpoints),
+            checkpoints.numel() if checkpoints is not None else 0, nat.stream(device),
         ),
         "composite",
     )
+    # The backward of these lists starts its segment walks at the checkpoints.
+    nat.set_checkpoints(ranges_in, checkpoints)
     return image, final_transmittance, n_contributors

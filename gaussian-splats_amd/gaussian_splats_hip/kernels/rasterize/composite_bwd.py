@@ -50,6 +50,7 @@ def composite_bwd(
     final_transmittance = nat.prepare(final_transmittance)
     n_contributors = nat.prepare(n_contributors, torch.int32)
     active = nat.active_tiles(ranges)
+    checkpoints = nat.checkpoints(ranges)
     ranges = nat.prepare(ranges, torch.int64)
     gaussian_ids = nat.prepare(gaussian_ids, torch.int32)
     n = projected_mean.shape[0]
@@ -63,7 +64,8 @@ def composite_bwd(
     )
     absolute = torch.zeros((n, 2), dtype=torch.float32, device=device) if return_absolute else None
     lib = nat.library()
-    order = nat.dispatch_plan(view, ranges.shape[0], device, n_contributors=n_contributors)
+    order = nat.dispatch_plan(view, ranges.shape[0], device, ranges=ranges,
+                              n_contributors=n_contributors)
     nat.check(
         nat.launch(
             "composite_bwd",
@@ -71,7 +73,9 @@ def composite_bwd(
                 nat.ptr(projected_mean), nat.ptr(inverse_covariance), nat.ptr(projected_color),
                 nat.ptr(projected_opacity), n, nat.ptr(gaussian_ids), nat.ptr(ranges),
                 nat.ptr(grad_image), nat.ptr(final_transmittance), nat.ptr(n_contributors),
-                nat.ptr(order), view, nat.ptr(out), nat.ptr(absolute), nat.stream(device),
+                nat.ptr(order), view, nat.ptr(out), nat.ptr(absolute), nat.ptr(checkpoints),
+                checkpoints.numel() if checkpoints is not None else 0, gaussian_ids.numel(),
+                nat.stream(device),
             ),
         ),
         "composite_bwd",

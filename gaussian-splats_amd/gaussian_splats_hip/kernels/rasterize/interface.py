@@ -198,10 +198,11 @@ def _setup_context(ctx, inputs, output) -> None:
             opacity_threshold=ctx.opacity_threshold, active_tiles=nat.active_tiles(output[8]),
         )
         ctx.view_project = nat.make_view(ctx.fx, ctx.fy, 0.0, 0.0, ctx.image_width, ctx.image_height)
+        ctx.checkpoints = nat.checkpoints(output[8])
         num_tiles = output[8].shape[0]
         ctx.tile_order = (
-            torch.empty(nat.library().gs_tile_order_items(ctx.view_composite), dtype=torch.int32,
-                        device=mean.device),
+            torch.empty(nat.library().gs_tile_order_items(ctx.view_composite, 1),
+                        dtype=torch.int32, device=mean.device),
             nat.workspace(nat.library().gs_tile_order_workspace_bytes(num_tiles), mean.device),
         )
     else:
@@ -251,9 +252,10 @@ def _backward(ctx, *grad_outputs):
     stream = nat.stream(device)
     ptr = nat.ptr
     order, order_ws = ctx.tile_order
+    checkpoints = ctx.checkpoints
     nat.check(
         lib.gs_tile_order(
-            None, ptr(n_contributors), ctx.view_composite, ptr(order), ptr(order_ws),
+            ptr(ranges), ptr(n_contributors), ctx.view_composite, ptr(order), ptr(order_ws),
             order_ws.numel(), stream,
         ),
         "tile_order",
@@ -265,7 +267,8 @@ def _backward(ctx, *grad_outputs):
                 ptr(projected_mean), ptr(inverse_covariance), ptr(projected_color),
                 ptr(projected_opacity), projected_mean.shape[0], ptr(gaussian_ids), ptr(ranges),
                 ptr(grad_image), ptr(final_transmittance), ptr(n_contributors), ptr(order),
-                ctx.view_composite, ptr(grad_projected), None, stream,
+                ctx.view_composite, ptr(grad_projected), None, ptr(checkpoints),
+                checkpoints.numel() if checkpoints is not None else 0, gaussian_ids.numel(), stream,
             ),
         ),
         "composite_bwd",

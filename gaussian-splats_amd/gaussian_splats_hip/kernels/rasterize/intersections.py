@@ -183,11 +183,13 @@ def bin_tiles(
         "bin_tiles_plan",
     )
     mark("bin")
-    total, row_entries, blocks, active, flags = host_totals.tolist()
+    total, row_entries, blocks, tiles_word, flags = host_totals.tolist()
     if flags:
         nat.device_errors(device, clear=True)  # report each failure once
         nat.raise_device_flags(flags, "bin_tiles")
-    nat.set_active_tiles(ranges, active)
+    # Tiles with a non-empty list (low half) and the longest list (high half).
+    nat.set_active_tiles(ranges, tiles_word & 0xFFFFFFFF)
+    nat.set_longest_list(ranges, tiles_word >> 32)
     sorted_ids = torch.empty(total, dtype=torch.int32, device=device)
     if total:
         ws = nat.workspace(

@@ -169,14 +169,17 @@ def forward_views(
         confidence=confidence, opacity_threshold=opacity_threshold,
         active_tiles=nat.active_tiles(ranges),
     )
+    checkpoints = nat.checkpoint_buffer(view, gaussian_ids.numel(), nat.longest_list(ranges),
+                                        device)
     nat.check(
         lib.gs_composite(
-            ptr(records), records.shape[0], ptr(gaussian_ids), ptr(ranges), None, view,
-            ptr(image),
-            ptr(final_transmittance), ptr(n_contributors), stream,
+            ptr(records), records.shape[0], ptr(gaussian_ids), gaussian_ids.numel(), ptr(ranges),
+            None, view, ptr(image), ptr(final_transmittance), ptr(n_contributors),
+            ptr(checkpoints), checkpoints.numel() if checkpoints is not None else 0, stream,
         ),
         "composite",
     )
+    nat.set_checkpoints(ranges, checkpoints)
     mark("composite")
     return (
         image,
@@ -275,6 +278,7 @@ def _setup_context(ctx, inputs, output) -> None:
         ctx.confidence,
     ) = inputs[8:]
     ctx.active_tiles = nat.active_tiles(output[8])
+    ctx.checkpoints = nat.checkpoints(output[8])
 
 
 def backward_views(
@@ -294,16 +298,20 @@ def backward_views(
     grad_image: torch.Tensor | None,
     timer=None,
     active_tiles: int | None = None,
+    checkpoints: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, ...]:
     """composite_bwd over the mosaic -> project_bwd summed over the views.
 
     ``saved`` holds the forward's outputs 1..9 (transmittance through counts);
     returns the gradients of the five parameter tensors.  ``timer(name)``
     marks "composite_bwd" and "project_bwd".  ``active_tiles``: tiles with a
-    non-empty list (default: the count binning recorded on the ranges)."""
+    non-empty list, and ``checkpoints``: the forward's checkpoint buffer
+    (defaults: those the forward recorded on the ranges)."""
     mark = timer or (lambda name: None)
     if active_tiles is None:
         active_tiles = nat.active_tiles(saved[7])
+    if checkpoints is None:
+        checkpoints = nat.checkpoints(saved[7])
     mean, rotation, scale, opacity, color = (
         _contiguous(t) for t in (mean, rotation, scale, opacity, color)
     )
@@ -334,7 +342,8 @@ def backward_views(
     view = _mosaic_view(w, h, tile, views, cols, opacity_threshold=opacity_threshold,
                         active_tiles=active_tiles)
     grad_projected = torch.zeros((views * n, 9), dtype=torch.float32, device=device)
-    order = nat.dispatch_plan(view, ranges.shape[0], device, n_contributors=n_contributors)
+    order = nat.dispatch_plan(view, ranges.shape[0], device, ranges=ranges,
+                              n_contributors=n_contributors)
     nat.check(
         nat.launch(
             "composite_bwd",
@@ -342,8 +351,9 @@ def backward_views(
                 ptr(projected_mean), ptr(inverse_covariance), ptr(projected_color),
                 ptr(projected_opacity), projected_mean.numel() // 3, ptr(gaussian_ids),
                 ptr(ranges), ptr(grad_image), ptr(final_transmittance), ptr(n_contributors),
-                ptr(order), view,
-                ptr(grad_projected), None, stream,
+                ptr(order), view, ptr(grad_projected), None, ptr(checkpoints),
+                checkpoints.numel() if checkpoints is not None else 0, gaussian_ids.numel(),
+                stream,
             ),
         ),
         "composite_bwd",
@@ -372,7 +382,7 @@ def _backward(ctx, *grad_outputs):
     grads = backward_views(
         *saved[:5], ctx.camera_rotations, ctx.camera_translations, ctx.intrinsics,
         ctx.image_width, ctx.image_height, ctx.tile_size, ctx.opacity_threshold, saved[5:],
-        grad_outputs[0], active_tiles=ctx.active_tiles,
+        grad_outputs[0], active_tiles=ctx.active_tiles, checkpoints=ctx.checkpoints,
     )
     return (*grads, *(None,) * 11)
 

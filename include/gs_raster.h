@@ -42,7 +42,7 @@ extern "C" {
 
 #define GS_API __attribute__((visibility("default")))
 
-#define GS_ABI_VERSION 8
+#define GS_ABI_VERSION 10
 
 typedef enum gs_status {
   GS_OK = 0,
@@ -220,7 +220,8 @@ GS_API int gs_sort_tiles(
  *
  * gs_bin_tiles_plan: depth order, per-tile counts and `ranges` [T, 2] (final),
  * and device `totals` = {intersections, row-list entries, pass-B workgroups,
- * tiles with a non-empty list}, which size the ids.  With `host_totals`
+ * tiles with a non-empty list | the longest list << 32 (capped at 2^31 - 1)},
+ * which size the ids and shape the compositing calls.  With `host_totals`
  * (5 x int64, pinned host memory for an asynchronous copy) the call returns
  * once the four totals have been copied there, and the low 32 bits of
  * host_totals[4] hold the device's sticky check-failure word (see
@@ -248,20 +249,24 @@ GS_API int gs_bin_tiles_emit(
     void* workspace, size_t workspace_bytes, void* stream);
 
 /* Dispatch plan of the compositing kernels (no counterpart in the reference,
- * whose launches take tiles in index order): writes gs_tile_order_items(view)
- * int32 work items to tile_order.  Each item is one wave's work: a whole tile
- * (tile << 3) or a quarter of a tile's 64-pixel bands (tile << 3 | 4 |
- * quarter, tiles of 16 and 32 pixels; a tile's four quarters fill one
- * workgroup's four slots); -1 is an unused slot.  The plan keeps each XCD's
- * region of tiles and starts the tiles with the most expected work first;
- * when fewer than 4096 tiles have work, every tile is split into its four
- * quarters, so the walks run on four times the waves.  The work estimate
- * is the list length from ranges, or, when n_contributors is given, the
- * largest contributor count of the tile's pixels (the entries the backward
- * walks).  The compositing calls take the plan with the same view (tile
- * size, mosaic and active_tiles); their results do not depend on it. */
+ * whose launches take tiles in index order): writes
+ * gs_tile_order_items(view, n_contributors != NULL) int32 work items to
+ * tile_order.  Each item is one wave's work, tile << 7 | code: 0 the whole
+ * tile; 0x20 | q quarter q of the tile's 64-pixel bands (tiles of 16 and 32
+ * pixels when fewer than 4096 tiles have work: every tile split, a tile's
+ * quarters in one workgroup's four slots); 0x40 | s segment s of the entries
+ * the tile's pixels walk back, cut at the forward's checkpoints (see
+ * gs_composite; backward plans given both ranges and n_contributors, the
+ * heaviest tiles first while the region's spare slots last); -1 is an unused
+ * slot.  The plan keeps each XCD's region of tiles and starts the tiles with
+ * the most expected work first.  The work estimate is the list length from
+ * ranges (a plan for gs_composite), or the largest contributor count of the
+ * tile's pixels (a plan for gs_composite_bwd).  The compositing call takes
+ * the plan made for it with the same view (tile size, mosaic and
+ * active_tiles); its results do not depend on it.  The workspace holds two
+ * words per tile. */
 GS_API size_t gs_tile_order_workspace_bytes(int32_t num_tiles);
-GS_API int64_t gs_tile_order_items(gs_view view); /* -1: invalid view */
+GS_API int64_t gs_tile_order_items(gs_view view, int32_t by_contributors); /* -1: bad view */
 GS_API int gs_tile_order(
     const int64_t* ranges, const int32_t* n_contributors, gs_view view,
     int32_t* tile_order, void* workspace, size_t workspace_bytes, void* stream);
@@ -270,7 +275,7 @@ GS_API int gs_tile_order(
  * reference): for callers that cannot allocate device memory (code under HIP
  * graph capture, serving loops, harnesses that forbid hipMalloc).  The tile
  * keys live in a static device array of the library, one per GPU, sized for
- * at most GS_TILE_ORDER_NOALLOC_MAX_TILES tiles (1 MiB); larger views are
+ * at most GS_TILE_ORDER_NOALLOC_MAX_TILES tiles (2 MiB); larger views are
  * rejected with GS_ERR_WORKSPACE.  Allocates nothing.  Every call on a GPU
  * shares that GPU's array: calls that overlap on one GPU (different streams
  * or host threads) race and must be serialised by the caller. */
@@ -282,15 +287,31 @@ GS_API int gs_tile_order_noalloc(
 /* Front-to-back compositing per tile.  Replaces composite
  * (src/gaussian_splats/kernels/rasterize/composite.py:25-162) with the
  * pixel semantics of torch.py:172-225.  tile_size in {4, 8, 16, 32}.
- * `records` holds num_records records; list ids are clamped to
- * [0, num_records), so incomplete lists (see gs_device_errors) never read
- * outside it.  tile_order: the dispatch plan of gs_tile_order for this view,
- * or NULL for tiles in index order (split into quarters when fewer than 4096
- * tiles have work); it does not change the results. */
+ * `records` holds num_records records; gaussian_ids holds num_intersections
+ * ids, clamped to [0, num_records), so incomplete lists (see
+ * gs_device_errors) never read outside it.  tile_order: the dispatch plan of
+ * gs_tile_order from ranges for this view, or NULL for tiles in index order
+ * (split into quarters when fewer than 4096 tiles have work); it does not
+ * change the results.
+ * checkpoints (optional, gs_composite_checkpoint_bytes(view,
+ * num_intersections) bytes, 256-byte aligned; no counterpart in the
+ * reference): whenever a tile's walk starts a batch of 64 entries holding an
+ * intersection index that is a multiple of 1024 (at least 64 past the tile's
+ * first) of a list longer than 8192 entries, it records per pixel the
+ * transmittance and the colour composited after that point (at most 63 per
+ * tile, from a pool of at most 128 MiB), which gs_composite_bwd uses to walk
+ * long lists back in segments at once.  The image is then the sum of the
+ * colour before and after each record.  The query returns 0 (no buffer
+ * needed) when longest_list, the longest list (totals[3] >> 32 of
+ * gs_bin_tiles_plan), is not above 8192, and for tiles of 32 pixels (whose
+ * walk holds 16 pixels per lane, leaving no registers for the records). */
+GS_API size_t gs_composite_checkpoint_bytes(gs_view view, int64_t num_intersections,
+                                            int64_t longest_list);
 GS_API int gs_composite(
     const void* records, int64_t num_records, const int32_t* gaussian_ids,
-    const int64_t* ranges, const int32_t* tile_order, gs_view view, float* image,
-    float* final_transmittance, int32_t* n_contributors, void* stream);
+    int64_t num_intersections, const int64_t* ranges, const int32_t* tile_order, gs_view view,
+    float* image, float* final_transmittance, int32_t* n_contributors, void* checkpoints,
+    size_t checkpoint_bytes, void* stream);
 
 /* Back-to-front compositing gradient, accumulated with atomics into
  * grad_projected[N,9] (zeroed by the caller), from the op's projected outputs
@@ -299,15 +320,21 @@ GS_API int gs_composite(
  * the absolute per-pixel terms of the mean gradient, as composite_bwd.py's
  * return_absolute output (composite_bwd.py:180-185,194-195,272-277).
  * Replaces composite_bwd (composite_bwd.py:47-277) with the exact gradient of
- * the forward.  tile_order as for gs_composite (the op plans from
- * n_contributors). */
+ * the forward.  tile_order: the plan of gs_tile_order from n_contributors
+ * (and ranges, for segments) for this view, or NULL (tiles in index order).
+ * checkpoints: the buffer gs_composite filled for the same lists (or NULL):
+ * a segment item starts its walk back at a checkpoint, with the
+ * transmittance recorded there and g.S = g . (colour after it) / T, the
+ * state the walk from the end would reach (the associative combine of
+ * composite_bwd.py:24-36), so a long walk runs on many waves at once. */
 GS_API int gs_composite_bwd(
     const float* projected_mean, const float* inverse_covariance,
     const float* projected_color, const float* projected_opacity, int64_t n,
     const int32_t* gaussian_ids, const int64_t* ranges,
     const float* grad_image, const float* final_transmittance,
     const int32_t* n_contributors, const int32_t* tile_order, gs_view view,
-    float* grad_projected, float* grad_absolute, void* stream);
+    float* grad_projected, float* grad_absolute, const void* checkpoints,
+    size_t checkpoint_bytes, int64_t num_intersections, void* stream);
 
 /* Chain rule from grad_projected to the parameters.  Replaces project_bwd
  * (src/gaussian_splats/kernels/rasterize/project_bwd.py:8-381); gradients are

@@ -415,12 +415,13 @@ def fixed_decision_rasterize_grads(params, cam, tile_size, near, far, lists, col
 # Dispatch plan of the compositing kernels (gs_tile_order).
 # ---------------------------------------------------------------------------
 
-PLAN_WAVES = 4          # items per compositing workgroup
-PLAN_SPLIT_TILES = 4096  # fewer tiles with work than this: every tile split
-PLAN_SPLIT_HEAVY = False  # heaviest tiles of a region split (off in the library)
-PLAN_HEAVY_SHARE = 8     # at most one tile in 8 of a region split
-PLAN_HEAVY = (3, 2)      # split above 3/2 of the region's mean (to 8 bits)
-PLAN_SORT_MAX = 8192     # larger regions keep index order
+PLAN_WAVES = 4            # items per compositing workgroup
+PLAN_SPLIT_TILES = 4096   # fewer tiles with work than this: every tile split in quarters
+PLAN_SEGMENT_SPARE = 4    # spare slots per region (backward plans), in units of its tiles
+PLAN_SORT_MAX = 8192      # larger regions keep index order
+CHECKPOINT_ENTRIES = 1024  # forward checkpoints at multiples of this intersection index
+CHECKPOINT_MAX = 63        # per tile
+CHECKPOINT_MIN_LIST = 8192  # lists of at most this many entries record none
 
 
 def plan_regions(num_tiles, waves=PLAN_WAVES):
@@ -434,33 +435,54 @@ def plan_regions(num_tiles, waves=PLAN_WAVES):
     return out
 
 
-def plan_slots(num_tiles, tile_size, active=0):
-    """(item slots per region, heaviest tiles split, every tile split)."""
+def plan_slots(num_tiles, tile_size, active=0, backward=False):
+    """(item slots per region, tiles walked back in segments, every tile split)."""
     live = active if 0 < active < num_tiles else num_tiles
     split_all = tile_size >= 16 and live < PLAN_SPLIT_TILES
-    bands = tile_size >= 16 and PLAN_SPLIT_HEAVY and not split_all
+    segments = backward and not split_all
     nb = -(-num_tiles // PLAN_WAVES)
     t_max = -(-nb // 8) * PLAN_WAVES
-    if split_all:
-        cap = 4 * t_max
-    elif bands:
-        cap = t_max + 3 * -(-t_max // PLAN_HEAVY_SHARE)
-    else:
-        cap = t_max
+    cap = 4 * t_max if split_all else (1 + PLAN_SEGMENT_SPARE) * t_max if segments else t_max
     blocks = -(-cap // PLAN_WAVES) if cap > PLAN_WAVES else 1
-    return PLAN_WAVES * blocks, bands, split_all
+    return PLAN_WAVES * blocks, segments, split_all
 
 
-def expected_plan(keys, tile_size, active=0):
+def checkpoint_crossings(start, max_n, list_len):
+    """Checkpoints a walk of max_n entries of a list of list_len entries
+    starting at intersection index `start` crosses: the multiples P of
+    CHECKPOINT_ENTRIES at least 64 past start whose 64-entry batch starts
+    below max_n (at most CHECKPOINT_MAX; none for lists of at most
+    CHECKPOINT_MIN_LIST entries), as positions in the walk (the batch
+    starts)."""
+    if list_len <= CHECKPOINT_MIN_LIST:
+        return []
+    first = -(-(start + 64) // CHECKPOINT_ENTRIES) * CHECKPOINT_ENTRIES
+    out = []
+    p = first
+    while len(out) < CHECKPOINT_MAX:
+        b = (p - start) // 64 * 64
+        if b >= max_n:
+            break
+        out.append(b)
+        p += CHECKPOINT_ENTRIES
+    return out
+
+
+def expected_plan(keys, tile_size, active=0, backward=False, crossings=None):
     """The work items gs_tile_order writes for per-tile work keys (list
-    lengths or largest contributor counts): per region, a stable sort by the
-    key's eight most significant bits (relative to the region's largest key,
-    keys capped at 2^16 - 1), largest first; the first h tiles become four
-    quarter items (tile << 3 | 4 | q), the rest whole items (tile << 3); -1
-    fills the region's unused slots."""
+    lengths, or largest contributor counts for a backward plan): per region, a
+    stable sort by the key's eight most significant bits (relative to the
+    region's largest key, keys capped at 2^16 - 1), largest first; each tile
+    as its four quarters (tile << 7 | 0x20 | q) when every tile is split, as
+    1 + c segments (tile << 7 | 0x40 | s, c = its checkpoint crossings) in a
+    backward plan while the region's spare slots last (a tile whose segments
+    do not fit stays whole), else whole (tile << 7); -1 fills the region's
+    unused slots."""
     keys = np.minimum(np.maximum(np.asarray(keys, dtype=np.int64), 0), 0xFFFF)
     num_tiles = keys.size
-    slots, bands, split_all = plan_slots(num_tiles, tile_size, active)
+    if crossings is None:
+        crossings = np.zeros(num_tiles, dtype=np.int64)
+    slots, segments, split_all = plan_slots(num_tiles, tile_size, active, backward)
     items = np.full(8 * slots, -1, dtype=np.int64)
     for r, (lo, hi) in enumerate(plan_regions(num_tiles)):
         n = hi - lo
@@ -470,37 +492,56 @@ def expected_plan(keys, tile_size, active=0):
         if n > PLAN_SORT_MAX:
             if split_all:
                 t = lo + np.arange(4 * n) // 4
-                out[:4 * n] = t << 3 | 4 | (np.arange(4 * n) & 3)
+                out[:4 * n] = t << 7 | 0x20 | (np.arange(4 * n) & 3)
             else:
-                out[:n] = (lo + np.arange(n)) << 3
+                out[:n] = (lo + np.arange(n)) << 7
             continue
         k = keys[lo:hi]
         shift = max(0, int(k.max() | 1).bit_length() - 8)
-        above = (PLAN_HEAVY[0] * int(k.sum()) // (PLAN_HEAVY[1] * n)) >> shift
         order = np.lexsort((np.arange(n), -(k >> shift)))
-        if split_all:
-            h = n
-        elif bands:
-            h = min(int(np.count_nonzero((k >> shift) > above)), -(-n // PLAN_HEAVY_SHARE))
-        else:
-            h = 0
+        extra = np.array([3 if split_all else (min(int(crossings[lo + e]), CHECKPOINT_MAX)
+                                                if segments else 0) for e in order],
+                         dtype=np.int64)
+        # Thread-blocked greedy of the library: blocks of 8 sorted tiles; a
+        # tile keeps its extras if the original extras before its block plus
+        # the kept extras before it in the block, plus its own, fit.
+        spare = slots - n
+        kept = extra.copy()
+        for b0 in range(0, n, 8):
+            before = int(extra[:b0].sum())
+            for i in range(b0, min(b0 + 8, n)):
+                if before + kept[i] > spare:
+                    kept[i] = 0
+                before += kept[i]
+        pos = 0
         for p, e in enumerate(order):
             t = lo + int(e)
-            if p < h:
-                out[4 * p:4 * p + 4] = t << 3 | 4 | np.arange(4)
+            x = int(kept[p])
+            if x == 0:
+                out[pos] = t << 7
             else:
-                out[3 * h + p] = t << 3
+                code = 0x20 if split_all else 0x40
+                out[pos:pos + x + 1] = t << 7 | code | np.arange(x + 1)
+            pos += 1 + x
     return items.astype(np.int32)
 
 
 def plan_tile_keys(ranges=None, ncon=None, width=0, height=0, tile_size=16):
-    """Per-tile work keys of the plan: list lengths, or the largest
-    contributor count of each tile's pixels ([H, W] or [V, H, W] mosaic of
-    views side by side is not modelled here: one view)."""
-    if ranges is not None:
+    """Per-tile work keys of the plan: list lengths, or (given ncon, one
+    view [H, W]) the largest contributor count of each tile's pixels."""
+    if ncon is None:
         r = np.asarray(ranges)
         return r[:, 1] - r[:, 0]
     tw, th = -(-width // tile_size), -(-height // tile_size)
     padded = np.zeros((th * tile_size, tw * tile_size), dtype=np.int64)
     padded[:height, :width] = ncon
     return padded.reshape(th, tile_size, tw, tile_size).max(axis=(1, 3)).reshape(-1)
+
+
+def plan_crossings(ranges, walks):
+    """Checkpoint crossings per tile for the backward plan (tile starts from
+    ranges, walks = largest contributor counts)."""
+    r = np.asarray(ranges)
+    return np.array([len(checkpoint_crossings(int(r[t, 0]), int(walks[t]),
+                                              int(r[t, 1] - r[t, 0])))
+                     for t in range(r.shape[0])], dtype=np.int64)

@@ -157,7 +157,8 @@ def test_project_rejects_unsupported_sh_before_launch():
 def test_invalid_tile_sizes(tile):
     lib = nat.library()
     fake = ctypes.c_void_p(16)
-    status = lib.gs_composite(fake, 10, fake, fake, None, _view(tile_size=tile), fake, fake, fake, None)
+    status = lib.gs_composite(fake, 10, fake, 10, fake, None, _view(tile_size=tile), fake, fake,
+                              fake, None, 0, None)
     assert status in (nat.GS_ERR_INVALID_ARGUMENT, nat.GS_ERR_UNSUPPORTED)
 
 
@@ -165,7 +166,7 @@ def test_backward_rejects_ellipsoid_mode():
     lib = nat.library()
     fake = ctypes.c_void_p(16)
     status = lib.gs_composite_bwd(*([fake] * 4), 10, *([fake] * 5), None,
-                                  _view(rendering_mode="ellipsoid"), fake, None, None)
+                                  _view(rendering_mode="ellipsoid"), fake, None, None, 0, 0, None)
     assert status == nat.GS_ERR_UNSUPPORTED
     assert b"Gaussian rendering" in lib.gs_last_error()
 
@@ -183,8 +184,8 @@ def test_misaligned_buffers_rejected():
 def test_status_codes_map_to_python_exceptions():
     lib = nat.library()
     fake = ctypes.c_void_p(16)
-    status = lib.gs_composite_bwd(*([fake] * 4), 10, *([fake] * 5), None, _view(rendering_mode="ellipsoid"), fake, None,
-                                  None)
+    status = lib.gs_composite_bwd(*([fake] * 4), 10, *([fake] * 5), None,
+                                  _view(rendering_mode="ellipsoid"), fake, None, None, 0, 0, None)
     with pytest.raises(NotImplementedError):
         nat.check(status, "composite_bwd")
 
@@ -246,7 +247,8 @@ def test_multi_view_host_checks():
             None, None, None,
         )
         assert status == nat.GS_ERR_INVALID_ARGUMENT
-        status = lib.gs_composite(fake, 10, fake, fake, None, _view(**kw), fake, fake, fake, None)
+        status = lib.gs_composite(fake, 10, fake, 10, fake, None, _view(**kw), fake, fake, fake,
+                                  None, 0, None)
         assert status == nat.GS_ERR_INVALID_ARGUMENT
     # Virtual Gaussian indices (view * N + i) must fit int32.
     status = lib.gs_project_views(
@@ -261,8 +263,9 @@ def test_multi_view_host_checks():
     assert status == nat.GS_ERR_OVERFLOW
     # A mosaic whose tile grid overflows is rejected.
     status = lib.gs_composite(
-        fake, 10, fake, fake, None, _view(image_width=1 << 16, image_height=1 << 16, tile_size=4,
-                                      views=64, mosaic_cols=8), fake, fake, fake, None,
+        fake, 10, fake, 10, fake, None, _view(image_width=1 << 16, image_height=1 << 16,
+                                              tile_size=4, views=64, mosaic_cols=8),
+        fake, fake, fake, None, 0, None,
     )
     assert status == nat.GS_ERR_OVERFLOW
     # Zero Gaussians: nothing to do.

@@ -194,6 +194,72 @@ def test_composite_backward_long_lists(device, entries, alpha_range):
     print(f"[long lists] max error {float(err):.3e} (float32 oracle {float(err32):.3e})", flush=True)
 
 
+@pytest.mark.parametrize("entries", (9000, 12000))
+def test_composite_backward_segmented_walks(device, entries):
+    """The backward's list segments: at tile 8 (no quarter split) the
+    entries are listed only in four tiles of the image's corner, two of which
+    hold lists of more than 8192 entries, walk ~1300 of them and cross forward
+    checkpoints (intersection indices that are multiples of 1024).  Each segment starts its walk back from the
+    checkpoint's record (T, colour after it): the gradients match float64
+    autograd along the same lists with the decisions fixed, and the
+    unsegmented backward (no plan, no checkpoints) up to rounding."""
+    from gaussian_splats_hip.kernels.rasterize.composite import tile_order
+
+    g = torch.Generator().manual_seed(entries + 1)
+    w = h = 64
+    ts = 8
+    u = torch.rand(entries, generator=g) * 20 - 2
+    v = torch.rand(entries, generator=g) * 20 - 2
+    depth = torch.rand(entries, generator=g) * 5 + 1
+    pmean = torch.stack((u, v, depth), -1)
+    sigma = torch.rand(entries, generator=g) * 2000 + 2000
+    rho = (torch.rand(entries, generator=g) * 2 - 1) * 0.5
+    cov = torch.stack((sigma ** 2, rho * sigma ** 2, rho * sigma ** 2, sigma ** 2), -1).view(-1, 2, 2)
+    pinv = torch.linalg.inv(cov.double()).float()
+    pcol = torch.rand(entries, 3, generator=g)
+    pop = torch.rand(entries, 1, generator=g) * 0.0015 + 0.0045
+    tw, th = nat.tiles(w, h, ts)
+    # Every entry is listed in tiles 0 and 8 (column 0, rows 0-1), an eighth
+    # of them also in tiles 1 and 9: tiles 0 and 8 hold lists longer than the
+    # checkpoint minimum (8192 entries) and walk ~1300 of them (until
+    # T ~ 1e-3), tiles 1 and 9 walk their whole lists of 1125 or 1500.
+    bounds = np.zeros((entries, 2, 2), dtype=np.int32)
+    bounds[:, 0, 1] = 1
+    bounds[: entries // 8, 0, 1] = 2
+    bounds[:, 1, 1] = 2
+    counts = ((bounds[:, 0, 1] - bounds[:, 0, 0]) * (bounds[:, 1, 1] - bounds[:, 1, 0])).astype(np.int32)
+    keys, ids = orc.emit_intersections(bounds, depth.numpy(), counts, tw)
+    sid, ranges, _ = orc.sort_intersections(keys, ids, tw * th)
+    grad_image = torch.rand(h, w, 3, generator=g) * 2 - 1
+    print(f"[segmented walks] {entries} entries", flush=True)
+    grad, absolute, expected, expected32, _, explained = _composite_bwd_case(
+        device, pmean, pinv, pcol, pop, sid, ranges, grad_image, w, h, ts)
+    assert not bool(explained.any())  # no decision near a threshold by construction
+    # The backward plan walks tiles 0 and 8 in segments cut at the forward's
+    # checkpoints (position 1024 of the list and its batch).
+    f32 = lambda x: x.detach().float().contiguous().to(device)
+    gids, granges = torch.as_tensor(sid).to(device), torch.as_tensor(ranges).to(device)
+    _, final_t, ncon = composite(f32(pmean), f32(pinv), f32(pcol), f32(pop), gids, granges,
+                                 w, h, ts, THRESHOLD, "gaussian", 0.95)
+    plan = tile_order(granges, ncon, w, h, ts).cpu().numpy()
+    segmented = set((plan[(plan >= 0) & ((plan & 0x40) != 0)] >> 7).tolist())
+    assert {0, 8} <= segmented, segmented
+    stats = assert_gradients_close(grad, expected, "segmented composite_bwd",
+                                   reference32=expected32)
+    print(f"[segmented walks] {stats}", flush=True)
+    whole = torch.zeros_like(grad, device=device)
+    view = nat.make_view(1.0, 1.0, 0.0, 0.0, w, h, ts, opacity_threshold=THRESHOLD)
+    cols = [f32(pmean), f32(pinv), f32(pcol), f32(pop)]  # alive until the kernel has run
+    g_dev = grad_image.to(device)
+    nat.check(nat.library().gs_composite_bwd(
+        *(nat.ptr(t) for t in cols), entries, nat.ptr(gids), nat.ptr(granges), nat.ptr(g_dev),
+        nat.ptr(final_t), nat.ptr(ncon), None, view, nat.ptr(whole), None, None, 0, 0,
+        nat.stream(device)), "composite_bwd")
+    torch.cuda.synchronize()
+    scale = whole.abs().amax(dim=0, keepdim=True).clamp_min(1e-30).cpu()
+    assert float(((grad - whole.cpu()).abs() / scale).max()) < 1e-5
+
+
 def _op_case(device, scene, ts, loss, target):
     """The op's forward and backward on the GPU and the oracle's float64 and
     float32 parameter gradients along the GPU's lists with the decisions fixed

@@ -27,6 +27,7 @@ from parity import (
     assert_close_flip_aware,
     expected_plan,
     oracle_camera,
+    plan_crossings,
     plan_slots,
     plan_tile_keys,
     rect_flip_tolerant_equal,
@@ -323,9 +324,11 @@ def test_composite_empty_tiles(device):
               (100, 100, 16, 0), (60, 40, 32, 0)])
 def test_dispatch_plan_matches_model(device, shape):
     """gs_tile_order's work items equal the plan's model (expected_plan) for
-    both work estimates: list lengths (ranges) and the largest contributor
-    count per tile; every tile is covered exactly once, whole or as its four
-    quarters in one workgroup's four slots."""
+    both work estimates: list lengths (ranges, a forward plan) and the
+    largest contributor count per tile with the ranges (a backward plan,
+    which cuts the walks at the forward's checkpoints); every tile is covered
+    exactly once: whole, as its four quarters in one workgroup's four slots,
+    or as its segments 0..c in consecutive slots."""
     from gaussian_splats_hip.kernels.rasterize.composite import tile_order
 
     tw, th, tile, active = shape
@@ -339,22 +342,37 @@ def test_dispatch_plan_matches_model(device, shape):
     ranges = np.zeros((t, 2), dtype=np.int64)
     ranges[:, 1] = np.cumsum(lengths)
     ranges[1:, 0] = ranges[:-1, 1]
+
+    def check_cover(items):
+        used = items[items >= 0]
+        tiles, code = used >> 7, used & 0x7F
+        covered = np.bincount(tiles, minlength=t)
+        assert np.all(covered >= 1)
+        whole = code == 0
+        assert np.all(covered[tiles[whole]] == 1)
+        quarters = np.flatnonzero((items >= 0) & ((items & 0x60) == 0x20))
+        assert np.all(items[quarters] & 3 == quarters % 4)  # quarter q in a workgroup's slot q
+        segs = np.flatnonzero((items >= 0) & ((items & 0x40) != 0))
+        first = segs - (items[segs] & 0x3F)  # a tile's segments fill consecutive slots
+        assert np.all((items[first] >> 7 == items[segs] >> 7) & ((items[first] & 0x7F) == 0x40))
+
     items = tile_order(torch.as_tensor(ranges).to(device), None, w, h, tile,
                        active_tiles=active).cpu().numpy()
     np.testing.assert_array_equal(items, expected_plan(lengths, tile, active))
-    used = items[items >= 0]
-    covered = np.bincount(used >> 3, minlength=t)
-    whole = np.bincount((used >> 3)[(used & 4) == 0], minlength=t)
-    assert np.all(((covered == 1) & (whole == 1)) | ((covered == 4) & (whole == 0)))
-    slots = np.flatnonzero((items >= 0) & ((items & 4) != 0))
-    assert np.all(items[slots] & 3 == slots % 4)  # quarter q in a workgroup's slot q
+    check_cover(items)
 
     ncon = rng.integers(0, 500, size=(h, w)).astype(np.int32)
-    items = tile_order(None, torch.as_tensor(ncon).to(device), w, h, tile,
+    ncon[:tile, :tile] = 20000  # a long walk: many checkpoint crossings
+    ranges_d = torch.as_tensor(ranges).to(device)
+    items = tile_order(ranges_d, torch.as_tensor(ncon).to(device), w, h, tile,
                        active_tiles=active).cpu().numpy()
+    walks = plan_tile_keys(ncon=ncon, width=w, height=h, tile_size=tile)
     np.testing.assert_array_equal(
-        items, expected_plan(plan_tile_keys(ncon=ncon, width=w, height=h, tile_size=tile), tile,
-                             active))
+        items, expected_plan(walks, tile, active, backward=True,
+                             crossings=plan_crossings(ranges, walks)))
+    check_cover(items)
+    if not plan_slots(t, tile, active, backward=True)[2]:
+        assert np.any((items >= 0) & ((items & 0x40) != 0))  # some tile was segmented
 
 
 @pytest.mark.parametrize("tile_size,image_size", [(8, (96, 80)), (16, (96, 80)),
@@ -387,18 +405,22 @@ def test_compositing_results_do_not_depend_on_tile_order(device, tile_size, imag
         ft2 = torch.empty_like(final_t)
         nc2 = torch.empty_like(ncon)
         nat.check(nat.library().gs_composite(
-            nat.ptr(records), records.shape[0], nat.ptr(sid_d), nat.ptr(ranges_d), nat.ptr(order),
-            v, nat.ptr(img2), nat.ptr(ft2), nat.ptr(nc2), nat.stream(device)), "composite")
+            nat.ptr(records), records.shape[0], nat.ptr(sid_d), sid_d.numel(), nat.ptr(ranges_d),
+            nat.ptr(order), v, nat.ptr(img2), nat.ptr(ft2), nat.ptr(nc2), None, 0,
+            nat.stream(device)), "composite")
         torch.cuda.synchronize()
-        assert torch.equal(image, img2) and torch.equal(final_t, ft2) and torch.equal(ncon, nc2)
+        # The wrapper's walk records checkpoints, which sums each pixel's
+        # colour in segments (rounding of the order of the sums).
+        assert torch.equal(final_t, ft2) and torch.equal(ncon, nc2)
+        assert float((image - img2).abs().max()) <= 1e-6
 
     # Tiles in index order, and a plan whose heaviest tiles run as quarters.
     forward(None)
     order = tile_order(ranges_d, None, w, h, tile_size)
-    _, heavy, split_all = plan_slots(tw * th, tile_size)
+    _, _, split_all = plan_slots(tw * th, tile_size)
     used = order.cpu().numpy()
     used = used[used >= 0]
-    assert bool((used & 4).any()) == (split_all or heavy)
+    assert bool((used & 0x20).any()) == split_all
     forward(order)
     # Every tile split into quarters (few tiles with work).
     few = nat.make_view(1.0, 1.0, 0.0, 0.0, w, h, tile_size, opacity_threshold=THRESHOLD,
@@ -406,16 +428,17 @@ def test_compositing_results_do_not_depend_on_tile_order(device, tile_size, imag
     forward(None, few)
     forward(tile_order(ranges_d, None, w, h, tile_size, active_tiles=1), few)
 
-    # Backward: the wrapper dispatches by contributor count; the identity
-    # order gives the same gradient up to the order of the atomic adds.
+    # Backward: the wrapper dispatches by contributor count (heavy tiles in
+    # segments); the identity order gives the same gradient up to the order
+    # of the atomic adds and the segments' recombination.
     g = torch.randn(h, w, 3, generator=torch.Generator().manual_seed(5)).to(device)
     grad = composite_bwd(*args, sid_d, ranges_d, g, final_t, ncon, w, h, tile_size, THRESHOLD,
                          "gaussian")
     grad2 = torch.zeros_like(grad)
     nat.check(nat.library().gs_composite_bwd(
         *(nat.ptr(t) for t in args), args[0].shape[0], nat.ptr(sid_d), nat.ptr(ranges_d), nat.ptr(g),
-        nat.ptr(final_t), nat.ptr(ncon), None, view, nat.ptr(grad2), None, nat.stream(device)),
-        "composite_bwd")
+        nat.ptr(final_t), nat.ptr(ncon), None, view, nat.ptr(grad2), None, None, 0, 0,
+        nat.stream(device)), "composite_bwd")
     torch.cuda.synchronize()
     # Float atomics make both sums order-dependent: compare against the scale
     # of each gradient column (a skipped or repeated tile would be O(1) off).

@@ -33,7 +33,7 @@ def _both_orders(device, view, num_tiles, ranges=None, ncon=None):
     lib = nat.library()
     s = nat.stream(device)
     ws = nat.workspace(lib.gs_tile_order_workspace_bytes(num_tiles), device)
-    count = lib.gs_tile_order_items(view)
+    count = lib.gs_tile_order_items(view, int(ncon is not None))
     expected = torch.full((count,), -7, dtype=torch.int32, device=device)
     nat.check(lib.gs_tile_order(nat.ptr(ranges), nat.ptr(ncon), view, nat.ptr(expected),
                                 nat.ptr(ws), ws.numel(), s), "tile_order")
@@ -77,7 +77,7 @@ def test_noalloc_matches_workspace_order(device):
     expected, got = _both_orders(device, view, t, ranges=torch.as_tensor(_ranges(lengths)).to(device))
     np.testing.assert_array_equal(got, expected)
     used = got[got >= 0]
-    assert got.size == expected.size and np.array_equal(np.unique(used >> 3), np.arange(t))
+    assert got.size == expected.size and np.array_equal(np.unique(used >> 7), np.arange(t))
 
     # 1080p by contributor counts (the backward's estimate), partial edge tiles.
     w, h, tile = 1920, 1080, 16
@@ -88,7 +88,8 @@ def test_noalloc_matches_workspace_order(device):
     expected, got = _both_orders(device, view, tw * th, ncon=torch.as_tensor(ncon).to(device))
     np.testing.assert_array_equal(got, expected)
     np.testing.assert_array_equal(
-        got, expected_plan(plan_tile_keys(ncon=ncon, width=w, height=h, tile_size=tile), tile))
+        got, expected_plan(plan_tile_keys(ncon=ncon, width=w, height=h, tile_size=tile), tile,
+                           backward=True))
 
     # Smaller: 33 x 2 tiles by list length; the scratch still holds the keys
     # of the calls above beyond this view's 66 tiles.

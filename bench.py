@@ -28,6 +28,10 @@ import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 VALU_CLOCK_HZ = 2.4e9  # MI355X peak engine clock
+# Spin before the projection's start event (about 100 us at the engine clock),
+# so its per-launch time excludes the host's launch latency after the idle
+# gap at the start of a step.
+PROJECT_HOLD_CYCLES = 250_000
 
 
 def parse_args():
@@ -43,7 +47,7 @@ def parse_args():
     )
     ap.add_argument("--tile-size", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-tiles", type=int, default=24, help="tiles in the CPU baseline sample")
+    ap.add_argument("--cpu-tiles", type=int, default=128, help="tiles in the CPU baseline sample")
     ap.add_argument("--out", default=None, help="also write the JSON line to this file")
     ap.add_argument(
         "--train-step", action="store_true",
@@ -112,6 +116,42 @@ def stage_bytes(n, k, total, rows, pixels, processed_fwd, processed_bwd):
         # count (the 2-D inverse is recomputed, not read)
         "project_bwd": 2 * n * (44 + 12 * k) + 40 * n,
     }
+
+
+# The kernels each stage of the step launches, in order (stage name -> kernels).
+STAGE_KERNELS = {
+    "project": ["project_fwd_kernel"],
+    "bin": ["sweep::clear_kernel", "sweep::hist_kernel", "sweep::scatter_kernel x4 (depth sort)",
+            "rect_diff_kernel", "tables_kernel", "sweep::scan_kernel<HeightLoad>"],
+    "emit": ["sweep::clear_kernel", "row_bucket_kernel", "sweep::scan_kernel<WidthLoad>",
+             "column_bucket_kernel"],
+    "sort": [],
+    "composite": ["checkpoint_clear_kernel (lists above 8192 entries)", "composite_fwd_kernel"],
+    "loss": ["l1_fwd_kernel", "l1_finish_kernel", "l1_bwd_kernel", "torch fill (gradient buffer)"],
+    "composite_bwd": ["tile_key_kernel", "tile_plan_kernel", "composite_bwd_kernel"],
+    "project_bwd": ["project_bwd_kernel"],
+}
+
+
+def stage_entries(stages_ms, bytes_model):
+    """Per stage: its kernels, time, algorithmic bytes and HBM fraction; and
+    the whole binning (bin + emit) against its own bytes."""
+    stages = {}
+    for name, ms in stages_ms.items():
+        entry = {"kernels": STAGE_KERNELS.get(name, []), "ms": round(ms, 4)}
+        if name in bytes_model and ms > 0:
+            gbs = bytes_model[name] / (ms * 1e-3) / 1e9
+            entry.update({"algorithmic_bytes": bytes_model[name], "GB/s": round(gbs, 1),
+                          "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)})
+        stages[name] = entry
+    if "bin" in stages_ms and "emit" in stages_ms:
+        ms = stages_ms["bin"] + stages_ms["emit"] + stages_ms.get("sort", 0.0)
+        nbytes = bytes_model["bin"] + bytes_model["emit"]
+        gbs = nbytes / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
+        stages["binning"] = {"kernels": STAGE_KERNELS["bin"] + STAGE_KERNELS["emit"],
+                             "ms": round(ms, 4), "algorithmic_bytes": nbytes,
+                             "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    return stages
 
 
 def run_step(splats, cam, target, tile_size, near, far):
@@ -186,11 +226,59 @@ def processed_pairs(ranges, ncon, tile_size, w, h):
     return fwd, bwd
 
 
+def host_description():
+    """CPU model, host memory and usable cores of the machine the baseline ran on."""
+    model, mem_kb = "unknown", 0
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+        for line in Path("/proc/meminfo").read_text().splitlines():
+            if line.startswith("MemTotal"):
+                mem_kb = int(line.split()[1])
+                break
+    except OSError:
+        pass
+    return {"cpu_model": model, "ram_gib": round(mem_kb / 2**20, 1),
+            "logical_cpus": os.cpu_count() or 1}
+
+
+def cpu_config1_full(threads):
+    """The reference's CPU-runnable case (config 1: 10k Gaussians, SH0,
+    256x256, forward only) rendered whole by the CPU oracle: one warm-up
+    frame, then the median of three."""
+    from gaussian_splats_hip import scenes
+    from oracle import rasterizer as orc
+
+    torch.set_num_threads(threads)
+    scene = scenes.config1()
+    cam = scene.cameras[0]
+    fx, fy = cam.focal_length
+    cx, cy = cam.principal_point
+    w, h = cam.image_size
+    ocam = orc.Camera(*host_extrinsics(cam), fx, fy, cx, cy, w, h)
+    times = []
+    with torch.no_grad():
+        for i in range(4):
+            t0 = time.perf_counter()
+            orc.rasterize(*scene.params(), ocam, tile_size=16, near=scene.near, far=scene.far)
+            if i > 0:
+                times.append(time.perf_counter() - t0)
+    med = sorted(times)[1]
+    return {"value": round((w * h) / 1e6 / med, 4), "unit": "Mpix/s", "s_per_frame": round(med, 4),
+            "frames": "warm-up 1, median of 3", "workload": f"config1 forward, {w}x{h}, "
+            f"{scene.num_points} Gaussians, SH0, tile 16"}
+
+
 def cpu_baseline(scene, tile_size, sample_tiles):
     """The CPU oracle (torch-CPU restatement of the reference torch backend) on a
     bounded sample: full projection + binning of all Gaussians, then dense
-    fwd+bwd compositing of ``sample_tiles`` non-empty tiles drawn at random
-    (seeded); the compositing time per pixel is extrapolated to the whole image."""
+    fwd+bwd compositing of ``sample_tiles`` non-empty tiles, stratified by list
+    length (equal numbers of tiles from each eighth of the non-empty tiles
+    sorted by length, seeded), each stratum timed on its own and its time per
+    tile scaled by the stratum's tile count.  Also: config 1 whole, and the
+    host's CPU and memory."""
     import numpy as np
 
     from oracle import rasterizer as orc
@@ -210,27 +298,61 @@ def cpu_baseline(scene, tile_size, sample_tiles):
     keys, ids = orc.emit_intersections(bounds, proj.mean[:, 2].detach().numpy(), counts, tw)
     sid, ranges, _ = orc.sort_intersections(keys, ids, tw * th)
     t1 = time.perf_counter()
-    # Sample: `sample_tiles` tiles drawn uniformly (seeded) from the non-empty ones.
+    # Compositing runs on detached copies of the projected tensors, so each
+    # stratum back-propagates only through its own compositing; the
+    # projection's backward runs once at the end on the summed gradients.
+    leaves = [t.detach().requires_grad_(True)
+              for t in (proj.mean, proj.inverse, proj.color, proj.opacity)]
+    pm, pinv, pcol, pop = leaves
     rng = np.random.default_rng(0)
     nonempty = np.nonzero(ranges[:, 1] > ranges[:, 0])[0]
-    chosen = rng.choice(nonempty, size=min(sample_tiles, len(nonempty)), replace=False)
-    keep = np.zeros(tw * th, dtype=bool)
-    keep[chosen] = True
-    sampled = ranges.copy()
-    sampled[~keep] = sampled[~keep, :1]  # empty the other tiles
-    comp = orc.composite(proj.mean[:, 0], proj.mean[:, 1], proj.inverse[:, 0, 0], proj.inverse[:, 0, 1],
-                         proj.inverse[:, 1, 1], proj.color, proj.opacity[:, 0], sid, sampled, w, h,
-                         tile_size, tile_chunk=8)
-    mask = torch.zeros(th * tile_size, tw * tile_size)
-    for t in chosen:
-        ty, tx = divmod(int(t), tw)
-        mask[ty * tile_size:(ty + 1) * tile_size, tx * tile_size:(tx + 1) * tile_size] = 1
-    mask = mask[:h, :w, None]
-    loss = ((comp.image - scene.target).abs() * mask).sum() / (w * h * 3)
-    loss.backward()
+    lengths = ranges[nonempty, 1] - ranges[nonempty, 0]
+    by_length = nonempty[np.argsort(lengths, kind="stable")]
+    strata = np.array_split(by_length, 8)
+    per = max(1, sample_tiles // len(strata))
+
+    def mask_of(tiles):
+        mask = torch.zeros(th * tile_size, tw * tile_size)
+        for t in tiles:
+            ty, tx = divmod(int(t), tw)
+            mask[ty * tile_size:(ty + 1) * tile_size, tx * tile_size:(tx + 1) * tile_size] = 1
+        return mask[:h, :w, None]
+
+    # The per-call cost that does not scale with the tiles (image-sized
+    # buffers, the chunk loop, the loss): one call with every list empty; it
+    # is taken off each stratum's time before scaling and counted once.
+    empty = ranges.copy()
+    empty[:, 1] = empty[:, 0]
+    te0 = time.perf_counter()
+    with torch.no_grad():
+        comp = orc.composite(pm[:, 0], pm[:, 1], pinv[:, 0, 0], pinv[:, 0, 1], pinv[:, 1, 1],
+                             pcol, pop[:, 0], sid, empty, w, h, tile_size, tile_chunk=8)
+        ((comp.image - scene.target).abs() * mask_of([])).sum()
+    fixed_s = time.perf_counter() - te0
+    composite_s = fixed_s
+    sampled_tiles = 0
+    for stratum in strata:
+        if len(stratum) == 0:
+            continue
+        chosen = rng.choice(stratum, size=min(per, len(stratum)), replace=False)
+        keep = np.zeros(tw * th, dtype=bool)
+        keep[chosen] = True
+        sampled = ranges.copy()
+        sampled[~keep] = sampled[~keep, :1]  # empty the other tiles
+        ts0 = time.perf_counter()
+        comp = orc.composite(pm[:, 0], pm[:, 1], pinv[:, 0, 0], pinv[:, 0, 1], pinv[:, 1, 1],
+                             pcol, pop[:, 0], sid, sampled, w, h, tile_size, tile_chunk=8)
+        loss = ((comp.image - scene.target).abs() * mask_of(chosen)).sum() / (w * h * 3)
+        loss.backward()
+        dt = max(time.perf_counter() - ts0 - fixed_s, 0.0)
+        composite_s += dt / len(chosen) * len(stratum)
+        sampled_tiles += len(chosen)
     t2 = time.perf_counter()
-    sample_px = int(mask.sum())
-    full_s = (t1 - t0) + (t2 - t1) * (w * h) / sample_px
+    outs = [(o, l.grad) for o, l in zip((proj.mean, proj.inverse, proj.color, proj.opacity), leaves)
+            if l.grad is not None and o.requires_grad]
+    torch.autograd.backward([o for o, _ in outs], [g for _, g in outs])
+    t3 = time.perf_counter()
+    full_s = (t1 - t0) + composite_s + (t3 - t2)
     return {
         "value": (w * h) / 1e6 / full_s,
         "unit": "Mpix/s",
@@ -238,9 +360,15 @@ def cpu_baseline(scene, tile_size, sample_tiles):
         "kind": "port",
         "sample": (
             f"torch-CPU oracle, float32: projection+binning of all {scene.num_points} Gaussians "
-            f"({t1 - t0:.1f}s) + dense fwd+bwd of {len(chosen)} random non-empty {tile_size}px tiles "
-            f"({sample_px} px, {t2 - t1:.1f}s), extrapolated per pixel to {w}x{h}"
+            f"({t1 - t0:.1f}s) + dense fwd+bwd compositing of {sampled_tiles} non-empty "
+            f"{tile_size}px tiles, {per} from each eighth of the tiles by list length "
+            f"({t2 - t1:.1f}s), each eighth's time per tile (less the {fixed_s:.2f}s per call "
+            f"that does not scale with the tiles, counted once) scaled to its "
+            f"{len(nonempty) // 8}-odd tiles + the projection backward ({t3 - t2:.1f}s); "
+            f"estimate {full_s:.1f}s per step"
         ),
+        "host": host_description(),
+        "config1_full": cpu_config1_full(threads),
     }
 
 
@@ -361,14 +489,7 @@ def bench_views(args, scene):
         rows += int(((bb[:, 3] - bb[:, 2]) * (counts > 0)).sum())
     model = views_stage_bytes(scene.num_points, scene.color.shape[1], views, int(gids.numel()),
                               rows, views * w * h, fwd_pairs, bwd_pairs)
-    stages = {}
-    for name, ms in stages_ms.items():
-        entry = {"ms": round(ms, 4)}
-        if name in model and ms > 0:
-            gbs = model[name] / (ms * 1e-3) / 1e9
-            entry.update({"algorithmic_bytes": model[name], "GB/s": round(gbs, 1),
-                          "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)})
-        stages[name] = entry
+    stages = stage_entries(stages_ms, model)
     # composite_bwd launches: one per step batched, one per camera in the loop.
     achieved = model["composite_bwd"] / (views if kind == "loop" else 1) / (dominant_ms * 1e-3) / 1e9
     other = "loop" if kind == "batched" else "batched"
@@ -653,7 +774,8 @@ def main():
     print(f"[bench] timed {args.steps} steps: {ms_per_step:.3f} ms/step", file=sys.stderr, flush=True)
     # The other kernels' per-launch times, from as many further steps outside
     # the timed region (their timing events would add to the step time).
-    with _native.LaunchTimer("project", capacity=args.steps + 1) as project_timer, \
+    with _native.LaunchTimer("project", capacity=args.steps + 1,
+                             hold_cycles=PROJECT_HOLD_CYCLES) as project_timer, \
             _native.LaunchTimer("project_bwd", capacity=args.steps + 1) as project_bwd_timer:
         for _ in range(args.steps):
             for p in splats.parameters():
@@ -670,28 +792,7 @@ def main():
     fwd_pairs, bwd_pairs = processed_pairs(info["ranges"], info["ncon"], args.tile_size, w, h)
     bytes_model = stage_bytes(scene.num_points, scene.color.shape[1], info["total"], info["rows"],
                               w * h, fwd_pairs, bwd_pairs)
-    stages = {}
-    for name, ms in stages_ms.items():
-        entry = {"ms": round(ms, 4)}
-        if name in bytes_model and ms > 0:
-            gbs = bytes_model[name] / (ms * 1e-3) / 1e9
-            entry.update({"algorithmic_bytes": bytes_model[name], "GB/s": round(gbs, 1),
-                          "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)})
-        stages[name] = entry
-    # The reference bins by sorting I 64-bit (tile, depth) keys with their ids
-    # (intersections.py:77-88): an onesweep LSD sort of 8-bit digits moves
-    # I (8 + 24 P) bytes, P = ceil((31 + ceil(log2 T)) / 8) passes.  This
-    # build's whole binning (plan + row and column bucketing) is timed against
-    # that figure: above 1 it beats the roofline of the sort it replaces.
-    tiles = -(-w // args.tile_size) * -(-h // args.tile_size)
-    passes = -(-(31 + max(1, math.ceil(math.log2(tiles)))) // 8)
-    sort_bytes = info["total"] * (8 + 24 * passes)
-    binning_ms = stages_ms["bin"] + stages_ms["emit"] + stages_ms["sort"]
-    stages["binning_vs_key_sort"] = {
-        "ms": round(binning_ms, 4), "key_sort_bytes": sort_bytes, "passes": passes,
-        "equivalent_GB/s": round(sort_bytes / (binning_ms * 1e-3) / 1e9, 1),
-        "frac_of_key_sort_roofline": round(sort_bytes / (binning_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-    }
+    stages = stage_entries(stages_ms, bytes_model)
 
     # Dominant kernel: composite_bwd_kernel, timed per launch with HIP events
     # on its stream during the timed steps.
@@ -703,13 +804,18 @@ def main():
     if traffic_file.exists() and args.config == "config3" and args.tile_size == 16:
         measured = json.loads(traffic_file.read_text())
         traffic = measured["hbm_bytes_per_launch"]
-        if "valu_instructions_per_launch" in measured:
-            # The kernel's real bound: wave64 fp32 VALU instructions issue in 4
-            # cycles on one of the 1024 SIMDs (256 CUs x 4) at 2.4 GHz.
-            insts = measured["valu_instructions_per_launch"]
+        if "valu" in measured:
+            # The kernel's real bound is VALU issue: measured VALU busy (the
+            # share of SIMD cycles issuing VALU work, transcendental
+            # instructions included), and the issue time of its wave64 fp32
+            # VALU instructions at 4 cycles each on the 1024 SIMDs (256 CUs x
+            # 4) at 2.4 GHz, against the measured launch time.
+            m = measured["valu"]
+            insts = m["sq_insts_valu_per_launch"]
             issue_ms = insts * 4 / (1024 * VALU_CLOCK_HZ) * 1e3
-            valu = {"instructions": insts, "issue_ms": round(issue_ms, 4),
-                    "frac": round(issue_ms / dominant_ms, 4)}
+            valu = {"valu_busy_measured": m["valu_busy"], "formula": m["formula"],
+                    "instructions": insts, "issue_ms_at_4_cycles": round(issue_ms, 4),
+                    "issue_frac": round(issue_ms / dominant_ms, 4)}
     roofline = {
         "kernel": "composite_bwd_kernel<16>" if args.tile_size == 16 else "composite_bwd_kernel",
         "bound": "hbm",

@@ -252,8 +252,8 @@ __device__ __forceinline__ void view_gradients(
 template <int K, bool MULTI>
 __global__ __launch_bounds__(kBlock) void project_bwd_kernel(ProjectBwdArgs a) {
   constexpr int F = 3 * K;
-  constexpr int S = F + 1;
-  __shared__ float coeff[kBlock * S];
+  constexpr int S = sh::row_stride<F>();
+  __shared__ __align__(16) float coeff[kBlock * S];
   const int views = MULTI ? a.views : 1;
   const bool accumulate = MULTI && a.accumulate;
   const int64_t base = int64_t(blockIdx.x) * kBlock;
@@ -291,8 +291,7 @@ __global__ __launch_bounds__(kBlock) void project_bwd_kernel(ProjectBwdArgs a) {
   if (any) {
     // Parameters are read once, only for Gaussians some view counted.
     float coef[F];
-#pragma unroll
-    for (int i = 0; i < F; ++i) coef[i] = coeff[threadIdx.x * S + i];
+    sh::row_load<F>(coeff, threadIdx.x, coef);
     const float alpha0 = 1.0f / (1.0f + expf(-lop));
     // The normalised quaternion and the scales in double (see view_gradients).
     qnorm = sqrt(double(qr.x) * qr.x + double(qr.y) * qr.y + double(qr.z) * qr.z +
@@ -359,8 +358,7 @@ __global__ __launch_bounds__(kBlock) void project_bwd_kernel(ProjectBwdArgs a) {
     a.g_scale[gi * 3 + 2] = gs3[2];
     a.g_opacity[gi] = gop;
     // Each thread overwrites only its own row, which only it has read.
-#pragma unroll
-    for (int i = 0; i < F; ++i) coeff[threadIdx.x * S + i] = gcoef[i];
+    sh::row_store<F>(coeff, threadIdx.x, gcoef);
   }
   __syncthreads();
   sh::unstage_block<F, kBlock>(a.g_color + base * F, nvalid, coeff);

@@ -57,13 +57,13 @@ struct ProjectArgs {
 };
 
 // The colour block of kProjectBlock Gaussians is staged through LDS with
-// coalesced dwordx4 loads, then each thread reads its own K*3 coefficients with
-// an odd stride (3K+1 floats) so the 64 lanes hit distinct banks.
+// coalesced 16-byte loads (sh::stage_block), then each thread reads its own
+// K*3 coefficients from its row (sh::row_load; rows of sh::row_stride floats).
 template <int K>
 __global__ __launch_bounds__(kProjectBlock) void project_fwd_kernel(ProjectArgs a) {
   constexpr int F = 3 * K;
-  constexpr int S = F + 1;
-  __shared__ float coeff[kProjectBlock * S];
+  constexpr int S = sh::row_stride<F>();
+  __shared__ __align__(16) float coeff[kProjectBlock * S];
 
   const int64_t base = int64_t(blockIdx.x) * kProjectBlock;
   const int64_t nvalid = min(int64_t(kProjectBlock), a.n - base);
@@ -113,7 +113,6 @@ __global__ __launch_bounds__(kProjectBlock) void project_fwd_kernel(ProjectArgs 
   } else {
     cut = 2.0f * logf(alpha0 * 255.0f);
   }
-  const float* cf = coeff + threadIdx.x * S;
 
   for (int view = 0; view < a.views; ++view) {
     const FwdCamera& cam = a.cam[view];
@@ -175,12 +174,14 @@ __global__ __launch_bounds__(kProjectBlock) void project_fwd_kernel(ProjectArgs 
     const float en = fmaxf(sqrtf(ex * ex + ey * ey + ez * ez), 1e-12f);
     float basis[K];
     sh::basis<K>(ex / en, ey / en, ez / en, basis);
+    float coef[F];
+    sh::row_load<F>(coeff, threadIdx.x, coef);
     float rgb[3];
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
       float acc = 0.0f;
 #pragma unroll
-      for (int k = 0; k < K; ++k) acc += basis[k] * cf[k * 3 + c];
+      for (int k = 0; k < K; ++k) acc += basis[k] * coef[k * 3 + c];
       rgb[c] = fmaxf(acc + 0.5f, 0.0f);  // utils.py:75
     }
 

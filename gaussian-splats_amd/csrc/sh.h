@@ -150,19 +150,104 @@ __device__ __forceinline__ void store_coefficients(float* __restrict__ p, const 
   }
 }
 
+// LDS layout of a staged coefficient block: row g holds Gaussian g's F
+// floats.  When F is a multiple of 4 a row is C = F/4 16-byte chunks and the
+// block moves between memory and LDS with 16-byte accesses on both sides:
+//   - C odd: rows of C chunks, unpadded;
+//   - C a multiple of 4: rows of C chunks, chunk j of row g in slot
+//     j ^ chunk_swizzle(g) (the swizzle flips the two low bits, so it stays in
+//     the row's aligned group of four slots);
+//   - other even C: one chunk of padding (an odd row length).
+// A wave reading chunk j of 8 (16) consecutive rows then touches 8 (16)
+// distinct 16-byte bank groups of 32 (64) banks, and the stores of
+// consecutive chunks of the block land in distinct groups too.  Otherwise
+// (F % 4 != 0) rows of F + 1 floats (odd) for one-float accesses.
+template <int F>
+constexpr int row_stride() {
+  return F % 4 != 0 ? F + 1 : ((F / 4) % 2 == 1 || (F / 4) % 4 == 0) ? F : F + 4;
+}
+
+template <int F>
+__device__ __forceinline__ int chunk_swizzle(int g) {
+  if constexpr (F % 4 == 0 && (F / 4) % 4 == 0) {
+    return ((g >> 1) ^ (g >> 2)) & 3;
+  } else {
+    return 0;
+  }
+}
+
+// Row g of a staged block, into registers.
+template <int F>
+__device__ __forceinline__ void row_load(const float* lds, int g, float* out) {
+  const float* row = lds + g * row_stride<F>();
+  if constexpr (F % 4 == 0) {
+    const float4* r4 = reinterpret_cast<const float4*>(row);
+    const int sw = chunk_swizzle<F>(g);
+#pragma unroll
+    for (int i = 0; i < F / 4; ++i) {
+      const float4 v = r4[i ^ sw];
+      out[4 * i + 0] = v.x;
+      out[4 * i + 1] = v.y;
+      out[4 * i + 2] = v.z;
+      out[4 * i + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < F; ++i) out[i] = row[i];
+  }
+}
+
+// Registers into row g of a staged block.
+template <int F>
+__device__ __forceinline__ void row_store(float* lds, int g, const float* in) {
+  float* row = lds + g * row_stride<F>();
+  if constexpr (F % 4 == 0) {
+    float4* r4 = reinterpret_cast<float4*>(row);
+    const int sw = chunk_swizzle<F>(g);
+#pragma unroll
+    for (int i = 0; i < F / 4; ++i)
+      r4[i ^ sw] = make_float4(in[4 * i + 0], in[4 * i + 1], in[4 * i + 2], in[4 * i + 3]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < F; ++i) row[i] = in[i];
+  }
+}
+
 // Coefficient blocks staged through LDS: BLOCK Gaussians' F = 3K floats each
-// (contiguous in memory, 16-byte aligned block start) move between memory and
-// LDS rows of stride F + 1 (odd: a wave reading one row per lane hits
-// distinct banks) with coalesced 16-byte accesses.  In a full block every
-// thread issues all of its loads before the first LDS store, so they are in
-// flight together; a partial block (nvalid < BLOCK) takes a guarded loop.
-// Called by all BLOCK threads; the caller synchronises around them.
+// (contiguous in memory, 16-byte aligned block start; LDS 16-byte aligned)
+// move between memory and LDS rows (the layout above) with coalesced 16-byte
+// loads.  For F % 4 == 0 each 16-byte chunk lands whole in one row (one
+// 16-byte LDS store; lane i stores chunk i).  Otherwise a chunk can straddle two rows and is stored
+// float by float.  In a full block every thread issues all of its loads
+// before the first LDS store, so they are in flight together.  Called by all
+// BLOCK threads; the caller synchronises around them.
 template <int F, int BLOCK>
 __device__ __forceinline__ void stage_block(const float* __restrict__ src, int nvalid, float* lds) {
-  constexpr int S = F + 1;
+  constexpr int S = row_stride<F>();
+  const float4* src4 = reinterpret_cast<const float4*>(src);
+  if constexpr (F % 4 == 0) {
+    constexpr int C = F / 4;  // chunks per row; thread t's j-th chunk is t + j * BLOCK
+    if (nvalid == BLOCK) {
+      float4 v[C];
+#pragma unroll
+      for (int j = 0; j < C; ++j) v[j] = src4[threadIdx.x + j * BLOCK];
+#pragma unroll
+      for (int j = 0; j < C; ++j) {
+        const int i = threadIdx.x + j * BLOCK;
+        const int g = i / C;
+        reinterpret_cast<float4*>(lds + g * S)[(i - g * C) ^ chunk_swizzle<F>(g)] = v[j];
+      }
+      return;
+    }
+    const int chunks = nvalid * C;
+    for (int i = threadIdx.x; i < chunks; i += BLOCK) {
+      const int g = i / C;
+      reinterpret_cast<float4*>(lds + g * S)[(i - g * C) ^ chunk_swizzle<F>(g)] = src4[i];
+    }
+    return;
+  }
   constexpr int kVec4 = BLOCK * F / 4;  // F * BLOCK is a multiple of 4 for BLOCK % 4 == 0
   constexpr int kPerThread = (kVec4 + BLOCK - 1) / BLOCK;
-  const float4* src4 = reinterpret_cast<const float4*>(src);
   if (nvalid == BLOCK) {
     float4 v[kPerThread];
 #pragma unroll
@@ -213,8 +298,17 @@ __device__ __forceinline__ void stage_block(const float* __restrict__ src, int n
 // The reverse of stage_block: LDS rows to memory with coalesced stores.
 template <int F, int BLOCK>
 __device__ __forceinline__ void unstage_block(float* __restrict__ dst, int nvalid, const float* lds) {
-  constexpr int S = F + 1;
+  constexpr int S = row_stride<F>();
   float4* dst4 = reinterpret_cast<float4*>(dst);
+  if constexpr (F % 4 == 0) {
+    constexpr int C = F / 4;
+    const int chunks = nvalid * C;
+    for (int i = threadIdx.x; i < chunks; i += BLOCK) {
+      const int g = i / C;
+      dst4[i] = reinterpret_cast<const float4*>(lds + g * S)[(i - g * C) ^ chunk_swizzle<F>(g)];
+    }
+    return;
+  }
   const int total = nvalid * F;
   for (int i = threadIdx.x; i * 4 < total; i += BLOCK) {
     float vals[4];

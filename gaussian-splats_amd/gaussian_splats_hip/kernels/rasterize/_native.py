@@ -371,8 +371,13 @@ class LaunchTimer:
     the stream it runs on, while active (``with LaunchTimer("composite_bwd")``).
     Used by the benchmark to measure a kernel's per-launch duration in place."""
 
-    def __init__(self, name: str, capacity: int = 256):
+    def __init__(self, name: str, capacity: int = 256, hold_cycles: int = 0):
         self.name = name
+        # A launch that follows an idle stretch of the queue (the first of a
+        # step) would time the host's launch latency too: with hold_cycles,
+        # a spin kernel of that many clock cycles runs before the start event,
+        # so the launch is queued by the time the event fires.
+        self.hold_cycles = int(hold_cycles)
         self.events: list[tuple[torch.cuda.Event, torch.cuda.Event]] = []
         # Created up front, so a timed launch only records two events.
         self._pool = [
@@ -407,6 +412,8 @@ def launch(name: str, call):
     if timer is None:
         return call()
     start, end = timer.next_pair()
+    if timer.hold_cycles:
+        torch.cuda._sleep(timer.hold_cycles)
     start.record()
     status = call()
     end.record()

@@ -200,13 +200,30 @@ def _setup_context(ctx, inputs, output) -> None:
         ctx.view_project = nat.make_view(ctx.fx, ctx.fy, 0.0, 0.0, ctx.image_width, ctx.image_height)
         ctx.checkpoints = nat.checkpoints(output[8])
         num_tiles = output[8].shape[0]
-        ctx.tile_order = (
-            torch.empty(nat.library().gs_tile_order_items(ctx.view_composite, 1),
-                        dtype=torch.int32, device=mean.device),
-            nat.workspace(nat.library().gs_tile_order_workspace_bytes(num_tiles), mean.device),
-        )
+        lib = nat.library()
+        order = torch.empty(lib.gs_tile_order_items(ctx.view_composite, 1), dtype=torch.int32,
+                            device=mean.device)
+        order_ws = nat.workspace(lib.gs_tile_order_workspace_bytes(num_tiles), mean.device)
+        # The backward's dispatch plan depends only on the forward's lists and
+        # contributor counts, so it is computed now, behind the forward on the
+        # stream: the backward then starts with the compositing kernel.
+        _launch_backward_plan(output[8], output[2], ctx.view_composite, order, order_ws)
+        ctx.tile_order = order
     else:
         ctx.grad_projected = None
+
+
+@torch.compiler.disable
+def _launch_backward_plan(ranges, n_contributors, view, order, order_ws) -> None:
+    """gs_tile_order for the backward, run eagerly (also under torch.compile,
+    which cannot trace the C-ABI call)."""
+    nat.check(
+        nat.library().gs_tile_order(
+            nat.ptr(ranges), nat.ptr(n_contributors), view, nat.ptr(order), nat.ptr(order_ws),
+            order_ws.numel(), nat.stream(ranges.device),
+        ),
+        "tile_order",
+    )
 
 
 def _contiguous(t: torch.Tensor) -> torch.Tensor:
@@ -251,15 +268,8 @@ def _backward(ctx, *grad_outputs):
     lib = nat.library()
     stream = nat.stream(device)
     ptr = nat.ptr
-    order, order_ws = ctx.tile_order
+    order = ctx.tile_order
     checkpoints = ctx.checkpoints
-    nat.check(
-        lib.gs_tile_order(
-            ptr(ranges), ptr(n_contributors), ctx.view_composite, ptr(order), ptr(order_ws),
-            order_ws.numel(), stream,
-        ),
-        "tile_order",
-    )
     nat.check(
         nat.launch(
             "composite_bwd",

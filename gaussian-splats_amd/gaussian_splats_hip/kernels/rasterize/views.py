@@ -259,6 +259,14 @@ def _rasterize_views_fake(
     )
 
 
+@torch.compiler.disable
+def _backward_plan(view, ranges, n_contributors) -> torch.Tensor:
+    """The backward's dispatch plan, computed eagerly (also under
+    torch.compile, which cannot trace the C-ABI call)."""
+    return nat.dispatch_plan(view, ranges.shape[0], ranges.device, ranges=ranges,
+                             n_contributors=n_contributors)
+
+
 def _setup_context(ctx, inputs, output) -> None:
     ctx.set_materialize_grads(False)
     ctx.save_for_backward(*inputs[:5], *output[1:])
@@ -279,6 +287,17 @@ def _setup_context(ctx, inputs, output) -> None:
     ) = inputs[8:]
     ctx.active_tiles = nat.active_tiles(output[8])
     ctx.checkpoints = nat.checkpoints(output[8])
+    ctx.order = None
+    if inputs[0].is_cuda and ctx.rendering_mode == "gaussian":
+        # The backward's dispatch plan depends only on the forward's lists and
+        # contributor counts: computed now, behind the forward on the stream.
+        views = inputs[5].shape[0]
+        tw, th = nat.tiles(ctx.image_width, ctx.image_height, ctx.tile_size)
+        cols = mosaic_columns(views, tw, th)
+        view = _mosaic_view(ctx.image_width, ctx.image_height, ctx.tile_size, views, cols,
+                            opacity_threshold=ctx.opacity_threshold,
+                            active_tiles=ctx.active_tiles)
+        ctx.order = _backward_plan(view, output[8], output[2])
 
 
 def backward_views(
@@ -299,6 +318,7 @@ def backward_views(
     timer=None,
     active_tiles: int | None = None,
     checkpoints: torch.Tensor | None = None,
+    order: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, ...]:
     """composite_bwd over the mosaic -> project_bwd summed over the views.
 
@@ -306,7 +326,9 @@ def backward_views(
     returns the gradients of the five parameter tensors.  ``timer(name)``
     marks "composite_bwd" and "project_bwd".  ``active_tiles``: tiles with a
     non-empty list, and ``checkpoints``: the forward's checkpoint buffer
-    (defaults: those the forward recorded on the ranges)."""
+    (defaults: those the forward recorded on the ranges); ``order``: the
+    dispatch plan of these lists and contributor counts (default: computed
+    here)."""
     mark = timer or (lambda name: None)
     if active_tiles is None:
         active_tiles = nat.active_tiles(saved[7])
@@ -342,8 +364,9 @@ def backward_views(
     view = _mosaic_view(w, h, tile, views, cols, opacity_threshold=opacity_threshold,
                         active_tiles=active_tiles)
     grad_projected = torch.zeros((views * n, 9), dtype=torch.float32, device=device)
-    order = nat.dispatch_plan(view, ranges.shape[0], device, ranges=ranges,
-                              n_contributors=n_contributors)
+    if order is None:
+        order = nat.dispatch_plan(view, ranges.shape[0], device, ranges=ranges,
+                                  n_contributors=n_contributors)
     nat.check(
         nat.launch(
             "composite_bwd",
@@ -383,6 +406,7 @@ def _backward(ctx, *grad_outputs):
         *saved[:5], ctx.camera_rotations, ctx.camera_translations, ctx.intrinsics,
         ctx.image_width, ctx.image_height, ctx.tile_size, ctx.opacity_threshold, saved[5:],
         grad_outputs[0], active_tiles=ctx.active_tiles, checkpoints=ctx.checkpoints,
+        order=ctx.order,
     )
     return (*grads, *(None,) * 11)
 

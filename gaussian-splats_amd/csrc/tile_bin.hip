@@ -548,10 +548,11 @@ __device__ void find_owners(const int32_t* rel, int m, uint16_t* own, uint32_t* 
 // Ranks the workgroup's items by digit, finds each digit's offset among the
 // items of the earlier workgroups of its chain by look-back (a chain starts at
 // a workgroup with chain_start), and stores the NV values of every item at
-// base(d) + offset(d) + rank (below `capacity`).  Items at
-// i * 64 + lane < seg_valid of each wave's segment are valid; digits are
-// below 2^BITS.
-template <int BITS, int NV, typename Base>
+// base(d) + offset(d) + rank (below `capacity`).  Without LOOKBACK, base(d)
+// is already the digit's first output position for this workgroup (status,
+// b and chain_start are unused).  Items at i * 64 + lane < seg_valid of each
+// wave's segment are valid; digits are below 2^BITS.
+template <int BITS, int NV, bool LOOKBACK = true, typename Base>
 __device__ void place_items(BucketLds<BITS, NV>& sh, const uint32_t (&dig)[kItems],
                             const uint32_t (&val)[NV][kItems], int nvalid, int b,
                             bool chain_start, Base base, uint64_t* __restrict__ status,
@@ -584,13 +585,15 @@ __device__ void place_items(BucketLds<BITS, NV>& sh, const uint32_t (&dig)[kItem
     sh.cnt[1][d] = local_start + c0;
     sh.cnt[2][d] = local_start + c0 + c1;
     sh.cnt[3][d] = local_start + c0 + c1 + c2;
-    uint64_t* mine = status + int64_t(b) * D + d;
-    sweep::store_status(mine,
-                        (chain_start ? sweep::kFlagPrefix : sweep::kFlagAggregate) | uint64_t(tot));
     uint64_t excl = 0;
-    if (!chain_start) {
-      excl = sweep::look_back(status, D, b, d, err);
-      sweep::store_status(mine, sweep::kFlagPrefix | (excl + tot));
+    if constexpr (LOOKBACK) {
+      uint64_t* mine = status + int64_t(b) * D + d;
+      sweep::store_status(
+          mine, (chain_start ? sweep::kFlagPrefix : sweep::kFlagAggregate) | uint64_t(tot));
+      if (!chain_start) {
+        excl = sweep::look_back(status, D, b, d, err);
+        sweep::store_status(mine, sweep::kFlagPrefix | (excl + tot));
+      }
     }
     // Output position of reordered item j of digit d: gofs[d] + j (mod 2^32).
     sh.gofs[d] = base(d) + uint32_t(excl) - local_start;
@@ -722,18 +725,173 @@ __global__ __launch_bounds__(kBlock) void row_bucket_kernel(
       err, out, entries);
 }
 
-// Pass B: workgroup b covers intersections [c0, c0 + count) of one tile row
-// (metadata info[b] recorded by the width scan); row-list entry k of the row
-// owns positions [W[k], W[k] + width) and expands into its columns.  Each
-// intersection is bucketed by column inside its row and its Gaussian id
-// stored at ranges[tile].start + rank.
+// Pass B's workgroups: workgroup b covers intersections [c0, c0 + count) of
+// one tile row (metadata info[b] recorded by the width scan); row-list entry
+// k of the row owns positions [W[k], W[k] + width) and expands into its
+// columns.  Pass B buckets every intersection by column inside its row in
+// three launches instead of one chained pass: counts per (workgroup, column),
+// a scan of them along each row's workgroups, then the placement.  A row of
+// config 4 has ~1200 workgroups, and a look-back along that chain kept each
+// workgroup waiting ~14 of its 25 us.
+
+// The owner window [first, last] of workgroup b and its first position,
+// count and row.
+struct PassBWindow {
+  int64_t first, last;
+  uint32_t c0, nvalid, row;
+};
+__device__ __forceinline__ PassBWindow pass_b_window(const uint4* __restrict__ info, int64_t b,
+                                                     int64_t blocks) {
+  const uint4 me = info[b];
+  PassBWindow w;
+  w.row = me.z & 0xFFu;
+  w.first = me.x & 0x7FFFFFFFu;
+  w.last = me.w;  // last entry of the row, unless the next workgroup shares it
+  if (b + 1 < blocks) {
+    const uint4 next = info[b + 1];
+    if ((next.z & 0xFFu) == w.row && !(next.z >> 31))
+      w.last = int64_t(next.x & 0x7FFFFFFFu) - int64_t(next.x >> 31);
+  }
+  w.c0 = me.y;
+  w.nvalid = (me.z >> 8) & 0x1FFFu;
+  // Uniform over the workgroup: kept in scalar registers.
+  auto uni32 = [](uint32_t v) { return uint32_t(__builtin_amdgcn_readfirstlane(int(v))); };
+  auto uni64 = [&](int64_t v) {
+    return int64_t(uint64_t(uni32(uint32_t(v))) | (uint64_t(uni32(uint32_t(uint64_t(v) >> 32))) << 32));
+  };
+  w.first = uni64(w.first);
+  w.last = uni64(w.last);
+  w.c0 = uni32(w.c0);
+  w.nvalid = uni32(w.nvalid);
+  w.row = uni32(w.row);
+  return w;
+}
+
+// Pass-B workgroups are grouped in chunks of kChunk consecutive indices; the
+// part of tile row y inside chunk k has the sums slot k + y (unique: a later
+// row's workgroups all follow an earlier row's).
+constexpr int kChunk = 64;
+__host__ __device__ inline int64_t chunk_slots(int64_t blocks, int th) {
+  return (blocks + kChunk - 1) / kChunk + th + 1;
+}
+
+// Counts: every row-list entry of workgroup b's window adds +1 at the first
+// column of its intersections inside [c0, c0 + count) and -1 after the last
+// one, in an LDS difference array; its prefix over the columns is the
+// workgroup's count per column, stored at counts[b * tw + column] and added
+// to its chunk's sums (sums[(b / kChunk + row) * tw + column], zeroed
+// beforehand).  The window's entries are read contiguously (no item is
+// generated).
+template <int BITS>
+__global__ __launch_bounds__(kBlock) void column_count_kernel(
+    const uint32_t* __restrict__ rl_xw, const uint32_t* __restrict__ W,
+    const uint4* __restrict__ info, int tw, const int64_t* __restrict__ totals, int64_t total,
+    int64_t entries, int64_t blocks, uint32_t* __restrict__ counts, uint32_t* __restrict__ sums,
+    uint32_t* __restrict__ err) {
+  constexpr int D = 1 << BITS;
+  static_assert(D <= kBlock, "one column per thread");
+  __shared__ int32_t diff[D + 1];
+  __shared__ uint32_t scratch[4];
+  if (totals[0] != total || totals[1] != entries || totals[2] != blocks) {
+    if (threadIdx.x == 0) atomicOr(err, kDeviceFlagSizes);
+    return;
+  }
+  for (int d = threadIdx.x; d <= D; d += kBlock) diff[d] = 0;
+  const int64_t b = blockIdx.x;
+  const PassBWindow win = pass_b_window(info, b, blocks);
+  const int64_t span = win.last - win.first + 1;
+  if (span > kTile && threadIdx.x == 0) atomicOr(err, kDeviceFlagWindow);
+  const int m = int(min(max(span, int64_t(1)), int64_t(kTile)));
+  // All of the thread's loads are issued before the first LDS update.
+  constexpr int J = kTile / kBlock;
+  uint32_t xw[J], s0[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int64_t k = win.first + min(int(threadIdx.x) + j * kBlock, m - 1);
+    xw[j] = rl_xw[k];
+    s0[j] = W[k];
+  }
+  __syncthreads();
+  const uint32_t end = win.c0 + win.nvalid;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    if (int(threadIdx.x) + j * kBlock >= m) continue;
+    const uint32_t w = entry_width(xw[j]), x0 = entry_x0(xw[j]);
+    const uint32_t lo = max(s0[j], win.c0), hi = min(s0[j] + w, end);
+    if (lo < hi) {
+      atomicAdd(&diff[min(x0 + (lo - s0[j]), uint32_t(D))], 1);
+      atomicAdd(&diff[min(x0 + (hi - s0[j]), uint32_t(D))], -1);
+    }
+  }
+  __syncthreads();
+  const int d = threadIdx.x;
+  const uint32_t v = d < D ? uint32_t(diff[d]) : 0u;
+  uint32_t all;
+  const uint32_t cnt = block_exclusive_scan(v, scratch, all) + v;
+  if (d < tw) {
+    counts[b * tw + d] = cnt;
+    if (cnt) atomicAdd(&sums[(b / kChunk + win.row) * tw + d], cnt);
+  }
+}
+
+// Scan: the counts of chunk k's workgroups become each workgroup's first
+// output position per column, in place: ranges[tile].start, plus the sums of
+// the row's earlier chunks, plus the counts of the row's earlier workgroups
+// in the chunk.  One workgroup per chunk, one thread per column; a chunk
+// holds the ends of at most a few rows, walked in turn, and each thread's
+// loads of a run of sums or counts are issued together.
+__global__ __launch_bounds__(kBlock) void column_scan_kernel(
+    uint32_t* __restrict__ counts, const uint32_t* __restrict__ sums,
+    const uint4* __restrict__ info, const uint32_t* __restrict__ row_blk,
+    const int64_t* __restrict__ ranges, int tw, int th, const int64_t* __restrict__ totals,
+    int64_t total, int64_t entries, int64_t blocks) {
+  // Inconsistent sizes were flagged by the count pass; nothing is read then.
+  if (totals[0] != total || totals[1] != entries || totals[2] != blocks) return;
+  const int64_t k = blockIdx.x;
+  const int64_t lo = k * kChunk, hi = min(lo + kChunk, blocks);
+  int64_t b = lo;
+  while (b < hi) {
+    const uint32_t y = min(uint32_t(__builtin_amdgcn_readfirstlane(int(info[b].z & 0xFFu))),
+                           uint32_t(th - 1));
+    // At least one workgroup per round, so the walk ends whatever the tables hold.
+    const int64_t row_end = max(min(int64_t(row_blk[y + 1]), hi), b + 1);
+    const int64_t k0 = int64_t(row_blk[y]) / kChunk;  // the row's first chunk
+    for (int d = threadIdx.x; d < tw; d += kBlock) {
+      uint32_t acc = uint32_t(ranges[2 * (int64_t(y) * tw + d)]);
+      for (int64_t kk = k0; kk < k; kk += 8) {
+        uint32_t c[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) c[i] = kk + i < k ? sums[(kk + i + y) * tw + d] : 0u;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc += c[i];
+      }
+      for (int64_t bb = b; bb < row_end; bb += 16) {
+        uint32_t c[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) c[i] = bb + i < row_end ? counts[(bb + i) * tw + d] : 0u;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          if (bb + i < row_end) {
+            counts[(bb + i) * tw + d] = acc;
+            acc += c[i];
+          }
+        }
+      }
+    }
+    b = row_end;
+  }
+}
+
+// Placement: each intersection of workgroup b is generated in registers from
+// its owner, ranked by column within the workgroup and its Gaussian id
+// stored at offsets[b * tw + column] + rank.
 template <int BITS>
 __global__ __launch_bounds__(kBlock) void column_bucket_kernel(
     const uint32_t* __restrict__ rl_g, const uint32_t* __restrict__ rl_xw,
     const uint32_t* __restrict__ W, const uint4* __restrict__ info, int tw,
-    const int64_t* __restrict__ ranges, const int64_t* __restrict__ totals, int64_t total,
+    const uint32_t* __restrict__ offsets, const int64_t* __restrict__ totals, int64_t total,
     int64_t entries, int64_t blocks, int32_t* __restrict__ sorted_ids,
-    uint64_t* __restrict__ status, uint32_t* __restrict__ ticket, uint32_t* __restrict__ err) {
+    uint32_t* __restrict__ err) {
   __shared__ BucketLds<BITS, 1> sh;
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
@@ -741,32 +899,14 @@ __global__ __launch_bounds__(kBlock) void column_bucket_kernel(
     if (threadIdx.x == 0) atomicOr(err, kDeviceFlagSizes);
     return;
   }
-  if (threadIdx.x == 0) sh.block = int(atomicAdd(ticket, 1u));
   for (int d = threadIdx.x; d < 4 * (1 << BITS); d += kBlock) (&sh.cnt[0][0])[d] = 0;
-  __syncthreads();
-  const int b = sh.block;
-  if (threadIdx.x == 0) {
-    const uint4 me = info[b];
-    const uint32_t row = me.z & 0xFFu;
-    sh.window[0] = me.x & 0x7FFFFFFFu;
-    sh.window[1] = me.w;  // last entry of the row, unless the next workgroup shares it
-    if (b + 1 < blocks) {
-      const uint4 next = info[b + 1];
-      if ((next.z & 0xFFu) == row && !(next.z >> 31))
-        sh.window[1] = int64_t(next.x & 0x7FFFFFFFu) - int64_t(next.x >> 31);
-    }
-    sh.c0 = me.y;
-    sh.nvalid = (me.z >> 8) & 0x1FFFu;
-    sh.row = row;
-    sh.chain_start = me.z >> 31;
-  }
-  __syncthreads();
-  const uint32_t c0 = sh.c0;
-  const int nvalid = int(sh.nvalid);
-  const int ty = int(sh.row);
-  const int64_t k_first = sh.window[0];
+  const int b = blockIdx.x;
+  const PassBWindow win = pass_b_window(info, b, blocks);
+  const uint32_t c0 = win.c0;
+  const int nvalid = int(win.nvalid);
+  const int64_t k_first = win.first;
   int32_t* rel = reinterpret_cast<int32_t*>(sh.val);
-  const int m = load_window(W, k_first, sh.window[1], c0, rel, err);
+  const int m = load_window(W, k_first, win.last, c0, rel, err);
   find_owners(rel, m, sh.own, sh.scratch);
 
   uint32_t dig[kItems];
@@ -788,11 +928,10 @@ __global__ __launch_bounds__(kBlock) void column_bucket_kernel(
     dig[i] = e < nvalid ? d : 0u;
   }
   uint32_t* const out[1] = {reinterpret_cast<uint32_t*>(sorted_ids)};
-  const int64_t row_tiles = int64_t(ty) * tw;
-  place_items<BITS, 1>(
-      sh, dig, val, nvalid, b, sh.chain_start != 0,
-      [&](int d) { return d < tw ? uint32_t(ranges[2 * (row_tiles + d)]) : 0u; }, status, err,
-      out, uint32_t(total));
+  const uint32_t* mine = offsets + int64_t(b) * tw;
+  place_items<BITS, 1, false>(
+      sh, dig, val, nvalid, b, true, [&](int d) { return d < tw ? mine[d] : 0u; }, nullptr,
+      err, out, uint32_t(total));
 }
 
 template <int BITS>
@@ -807,14 +946,17 @@ void launch_row_bucket(unsigned blocks, const uint32_t* packed, const int32_t* o
 }
 
 template <int BITS>
-void launch_column_bucket(unsigned blocks, const uint32_t* rl_g, const uint32_t* rl_xw,
-                          const uint32_t* W, const uint4* info, int tw, const int64_t* ranges,
-                          const int64_t* totals, int64_t total, int64_t entries, int64_t blocks_b,
-                          int32_t* sorted_ids, uint64_t* status, uint32_t* ticket, uint32_t* err,
-                          hipStream_t s) {
-  column_bucket_kernel<BITS><<<blocks, kBlock, 0, s>>>(rl_g, rl_xw, W, info, tw, ranges, totals,
-                                                       total, entries, blocks_b, sorted_ids,
-                                                       status, ticket, err);
+void launch_pass_b(unsigned blocks, const uint32_t* rl_g, const uint32_t* rl_xw,
+                   const uint32_t* W, const uint4* info, int tw, int th, const uint32_t* row_blk,
+                   const int64_t* ranges, const int64_t* totals, int64_t total, int64_t entries,
+                   int64_t blocks_b, int32_t* sorted_ids, uint32_t* counts, uint32_t* sums,
+                   uint32_t* err, hipStream_t s) {
+  column_count_kernel<BITS><<<blocks, kBlock, 0, s>>>(rl_xw, W, info, tw, totals, total, entries,
+                                                      blocks_b, counts, sums, err);
+  column_scan_kernel<<<unsigned(ceil_div(blocks_b, kChunk)), kBlock, 0, s>>>(
+      counts, sums, info, row_blk, ranges, tw, th, totals, total, entries, blocks_b);
+  column_bucket_kernel<BITS><<<blocks, kBlock, 0, s>>>(rl_g, rl_xw, W, info, tw, counts, totals,
+                                                       total, entries, blocks_b, sorted_ids, err);
 }
 
 // Digit width of an axis of `tiles` tiles (at least 1 bit).
@@ -873,10 +1015,11 @@ struct EmitLayout {
   uint4* info = nullptr;        // [blocks B]
   uint64_t* zero = nullptr;     // statuses, then small words
   int64_t zero_words = 0;
+  uint32_t* col = nullptr;      // [blocks B x tiles_w] pass-B counts, then offsets
+  uint32_t* col_sums = nullptr;  // [chunk_slots x tiles_w] pass-B chunk sums (zeroed)
   uint64_t* status_a = nullptr;
-  uint64_t* status_b = nullptr;
   uint64_t* scan_status = nullptr;  // width scan
-  uint32_t* small = nullptr;  // tickets A, B, width scan; error flags
+  uint32_t* small = nullptr;  // tickets A, width scan
   size_t bytes = 0;
 };
 
@@ -894,16 +1037,17 @@ EmitLayout emit_layout(void* base, int64_t entries, int64_t blocks_b, int tw, in
   e.rl_xw = reinterpret_cast<uint32_t*>(take(size_t(entries) * 4));
   e.W = reinterpret_cast<uint32_t*>(take(size_t(entries) * 4));
   e.info = reinterpret_cast<uint4*>(take(size_t(blocks_b + 1) * 16));
+  e.col = reinterpret_cast<uint32_t*>(take(size_t(blocks_b) * size_t(tw) * 4));
   const int64_t words_a = blocks_a << axis_bits(th);
-  const int64_t words_b = blocks_b << axis_bits(tw);
   const int64_t words_w = blocks_a;
-  e.zero_words = words_a + words_b + words_w + 4;  // + 8 small 32-bit words
+  const int64_t words_s = (chunk_slots(blocks_b, th) * tw + 1) / 2;
+  e.zero_words = words_a + words_w + words_s + 4;  // + 8 small 32-bit words
   e.zero = reinterpret_cast<uint64_t*>(take(size_t(e.zero_words) * 8));
   if (e.zero) {
     e.status_a = e.zero;
-    e.status_b = e.status_a + words_a;
-    e.scan_status = e.status_b + words_b;
-    e.small = reinterpret_cast<uint32_t*>(e.scan_status + words_w);
+    e.scan_status = e.status_a + words_a;
+    e.col_sums = reinterpret_cast<uint32_t*>(e.scan_status + words_w);
+    e.small = reinterpret_cast<uint32_t*>(e.scan_status + words_w + words_s);
   }
   e.bytes = off;
   return e;
@@ -1056,7 +1200,6 @@ GS_API int gs_bin_tiles_emit(int64_t n,
   sweep::clear_kernel<<<unsigned(std::max<int64_t>(1, std::min<int64_t>(1024, ceil_div(e.zero_words, kBlock)))),
                         kBlock, 0, s>>>(e.zero, e.zero_words, nullptr, 0);
   uint32_t* ticket_a = e.small;
-  uint32_t* ticket_b = e.small + 1;
   uint32_t* ticket_w = e.small + 2;
   const unsigned blocks_a = unsigned(ceil_div(row_entries, kTile));
   switch (axis_bits(tiles_h)) {
@@ -1080,9 +1223,9 @@ GS_API int gs_bin_tiles_emit(int64_t n,
   switch (axis_bits(tiles_w)) {
 #define GS_COL_CASE(B)                                                                          \
   case B:                                                                                       \
-    launch_column_bucket<B>(unsigned(blocks), e.rl_g, e.rl_xw, e.W, e.info, tiles_w, ranges,    \
-                            totals, total, row_entries, blocks, sorted_ids, e.status_b,         \
-                            ticket_b, err, s);                                              \
+    launch_pass_b<B>(unsigned(blocks), e.rl_g, e.rl_xw, e.W, e.info, tiles_w, tiles_h,          \
+                     p.row_blk, ranges, totals, total, row_entries, blocks, sorted_ids, e.col,   \
+                     e.col_sums, err, s);                                                       \
     break;
     GS_COL_CASE(1) GS_COL_CASE(2) GS_COL_CASE(3) GS_COL_CASE(4)
     GS_COL_CASE(5) GS_COL_CASE(6) GS_COL_CASE(7) GS_COL_CASE(8)

@@ -362,33 +362,17 @@ __device__ __forceinline__ T from_lane63(T v) {
   }
 }
 
-// Exclusive scan of load(i) into out[0..n), and out[n] = total when
-// write_total; one kernel, kTile elements per workgroup.  Accesses are fully
-// coalesced: lane l of wave w handles the four-element groups
-// w * 256 + i * 64 + l (i < 4) of the tile, read and written with 16-byte
-// accesses when `vec` (load.load4 and out are 16-byte aligned); four wave
-// scans order the groups, one LDS exchange orders the waves, and a wave-wide
-// look-back gives the tile's offset.  sink.all sees every element with
-// out[i] and its value.
-template <typename Out, typename Load, typename Sink = NoSink>
-__global__ __launch_bounds__(kBlock) void scan_kernel(Load load, int64_t n, Out* __restrict__ out,
-                                                      bool write_total, bool vec,
-                                                      uint64_t* __restrict__ status,
-                                                      uint32_t* __restrict__ ticket,
-                                                      uint32_t* __restrict__ err,
-                                                      Sink sink = Sink{}) {
-  static_assert(kTile == 4 * 4 * kBlock, "16 elements per thread in groups of four");
-  __shared__ Out wave_total[4];
-  __shared__ Out s_excl;
-  __shared__ int s_block;
-  if (threadIdx.x == 0) s_block = int(atomicAdd(ticket, 1u));
-  __syncthreads();
-  const int b = s_block;
-  const int lane = threadIdx.x & 63;
-  const int wid = threadIdx.x >> 6;
-  const int64_t base = int64_t(b) * kTile;
-  Out v[4][4];
-  Out group_sum[4];
+// The row list's width scan runs as one look-back kernel up to this many
+// tiles (short chains, one launch) and as reduce-then-scan beyond (three
+// launches, no chain): config 3's 950 tiles 30 -> 23 us, config 4's 199 ->
+// 138 us.  The height scan keeps the look-back: its tile sums gather through
+// the depth order, which costs more than its chain (config 3 15 -> 24 us).
+constexpr int64_t kLookBackScanTiles = 16;
+
+// Loads the thread's 16 elements of tile b (the layout of scan_kernel).
+template <typename Out, typename Load>
+__device__ __forceinline__ void load_tile(const Load& load, int64_t n, bool vec, int64_t base,
+                                          int wid, int lane, Out (&v)[4][4]) {
   // A full tile (the workgroup-uniform case) loads its four groups without
   // per-lane branches, so all of a thread's loads are in flight together.
   const bool full = vec && base + kTile <= n;
@@ -407,6 +391,94 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(Load load, int64_t n, Out*
       }
     }
   }
+}
+
+// Reduce-then-scan, step 1: sums[b] = the sum of tile b's elements.
+template <typename Out, typename Load>
+__global__ __launch_bounds__(kBlock) void tile_sum_kernel(Load load, int64_t n, bool vec,
+                                                          Out* __restrict__ sums) {
+  __shared__ Out part[4];
+  const int lane = threadIdx.x & 63;
+  const int wid = threadIdx.x >> 6;
+  Out v[4][4];
+  load_tile<Out>(load, n, vec, int64_t(blockIdx.x) * kTile, wid, lane, v);
+  Out t = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) t += v[i][0] + v[i][1] + v[i][2] + v[i][3];
+  t = wave_sum(t);
+  if (lane == 0) part[wid] = t;
+  __syncthreads();
+  if (threadIdx.x == 0) sums[blockIdx.x] = part[0] + part[1] + part[2] + part[3];
+}
+
+// Reduce-then-scan, step 2 (one workgroup): the tile sums become the tiles'
+// exclusive offsets, in place; *total_out = the grand total when non-null.
+// Each thread owns a contiguous run of tiles and issues its loads eight at a
+// time.
+template <typename Out>
+__global__ __launch_bounds__(kBlock) void tile_offsets_kernel(Out* __restrict__ sums, int64_t nb,
+                                                              Out* __restrict__ total_out) {
+  __shared__ Out scratch[4];
+  const int64_t per = (nb + kBlock - 1) / kBlock;
+  const int64_t lo = int64_t(threadIdx.x) * per, hi = min(lo + per, nb);
+  Out acc = 0;
+  for (int64_t i = lo; i < hi; i += 8) {
+    Out c[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) c[j] = i + j < hi ? sums[i + j] : Out(0);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc += c[j];
+  }
+  Out total;
+  Out run = block_exclusive_scan(acc, scratch, total);
+  for (int64_t i = lo; i < hi; i += 8) {
+    Out c[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) c[j] = i + j < hi ? sums[i + j] : Out(0);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (i + j < hi) {
+        sums[i + j] = run;
+        run += c[j];
+      }
+    }
+  }
+  if (threadIdx.x == 0 && total_out) *total_out = total;
+}
+
+// Exclusive scan of load(i) into out[0..n), and out[n] = total when
+// write_total; kTile elements per workgroup.  With `offsets` (the tiles'
+// exclusive offsets from tile_sum_kernel + tile_offsets_kernel) the
+// workgroups need no ticket and no look-back; otherwise one kernel.  Accesses are fully
+// coalesced: lane l of wave w handles the four-element groups
+// w * 256 + i * 64 + l (i < 4) of the tile, read and written with 16-byte
+// accesses when `vec` (load.load4 and out are 16-byte aligned); four wave
+// scans order the groups, one LDS exchange orders the waves, and a wave-wide
+// look-back gives the tile's offset.  sink.all sees every element with
+// out[i] and its value.
+template <typename Out, typename Load, typename Sink = NoSink>
+__global__ __launch_bounds__(kBlock) void scan_kernel(Load load, int64_t n, Out* __restrict__ out,
+                                                      bool write_total, bool vec,
+                                                      uint64_t* __restrict__ status,
+                                                      uint32_t* __restrict__ ticket,
+                                                      uint32_t* __restrict__ err,
+                                                      Sink sink = Sink{},
+                                                      const Out* __restrict__ offsets = nullptr) {
+  static_assert(kTile == 4 * 4 * kBlock, "16 elements per thread in groups of four");
+  __shared__ Out wave_total[4];
+  __shared__ Out s_excl;
+  __shared__ int s_block;
+  if (!offsets) {
+    if (threadIdx.x == 0) s_block = int(atomicAdd(ticket, 1u));
+    __syncthreads();
+  }
+  const int b = offsets ? int(blockIdx.x) : s_block;
+  const int lane = threadIdx.x & 63;
+  const int wid = threadIdx.x >> 6;
+  const int64_t base = int64_t(b) * kTile;
+  Out v[4][4];
+  Out group_sum[4];
+  load_tile<Out>(load, n, vec, base, wid, lane, v);
 #pragma unroll
   for (int i = 0; i < 4; ++i) group_sum[i] = v[i][0] + v[i][1] + v[i][2] + v[i][3];
   // Exclusive prefix of each group inside the wave's 1024 elements.
@@ -427,7 +499,9 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(Load load, int64_t n, Out*
     if (w < wid) before += t;
     total += t;
   }
-  if (threadIdx.x < 64) {
+  if (offsets) {
+    if (threadIdx.x == 0) s_excl = offsets[b];
+  } else if (threadIdx.x < 64) {
     if (threadIdx.x == 0)
       store_status(status + b, (b == 0 ? kFlagPrefix : kFlagAggregate) | uint64_t(total));
     const uint64_t excl = b > 0 ? wave_look_back(status, b, err) : 0;

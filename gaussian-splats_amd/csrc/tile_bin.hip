@@ -1216,10 +1216,22 @@ GS_API int gs_bin_tiles_emit(int64_t n,
   }
   // Positions of the row-list entries in row-major intersection order,
   // recording each pass-B workgroup's metadata.
-  sweep::scan_kernel<uint32_t, WidthLoad, WidthSink><<<blocks_a, sweep::kBlock, 0, s>>>(
-      WidthLoad{e.rl_xw}, row_entries, e.W, false, true, e.scan_status, ticket_w, err,
-      WidthSink{e.rl_xw, p.row_e, p.row_a, p.row_blk, e.info, uint32_t(tiles_h),
-                uint32_t(blocks)});
+  const WidthSink width_sink{e.rl_xw, p.row_e, p.row_a, p.row_blk, e.info, uint32_t(tiles_h),
+                            uint32_t(blocks)};
+  if (blocks_a <= sweep::kLookBackScanTiles) {
+    sweep::scan_kernel<uint32_t, WidthLoad, WidthSink><<<blocks_a, sweep::kBlock, 0, s>>>(
+        WidthLoad{e.rl_xw}, row_entries, e.W, false, true, e.scan_status, ticket_w, err,
+        width_sink);
+  } else {
+    // Reduce-then-scan (see launch_scan); the tile sums reuse the status words.
+    uint32_t* sums = reinterpret_cast<uint32_t*>(e.scan_status);
+    sweep::tile_sum_kernel<uint32_t, WidthLoad><<<blocks_a, sweep::kBlock, 0, s>>>(
+        WidthLoad{e.rl_xw}, row_entries, true, sums);
+    sweep::tile_offsets_kernel<uint32_t><<<1, sweep::kBlock, 0, s>>>(sums, blocks_a, nullptr);
+    sweep::scan_kernel<uint32_t, WidthLoad, WidthSink><<<blocks_a, sweep::kBlock, 0, s>>>(
+        WidthLoad{e.rl_xw}, row_entries, e.W, false, true, nullptr, nullptr, err, width_sink,
+        sums);
+  }
   switch (axis_bits(tiles_w)) {
 #define GS_COL_CASE(B)                                                                          \
   case B:                                                                                       \

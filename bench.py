@@ -32,6 +32,8 @@ VALU_CLOCK_HZ = 2.4e9  # MI355X peak engine clock
 # so its per-launch time excludes the host's launch latency after the idle
 # gap at the start of a step.
 PROJECT_HOLD_CYCLES = 250_000
+# The same spin between the stages of the staged steps (stage_marker).
+STAGE_HOLD_CYCLES = 250_000
 
 
 def parse_args():
@@ -123,8 +125,9 @@ STAGE_KERNELS = {
     "project": ["project_fwd_kernel"],
     "bin": ["sweep::clear_kernel", "sweep::hist_kernel", "sweep::scatter_kernel x4 (depth sort)",
             "rect_diff_kernel", "tables_kernel", "sweep::scan_kernel<HeightLoad>"],
-    "emit": ["sweep::clear_kernel", "row_bucket_kernel", "sweep::scan_kernel<WidthLoad>",
-             "column_bucket_kernel"],
+    "emit": ["sweep::clear_kernel", "row_bucket_kernel", "sweep::tile_sum_kernel<WidthLoad>",
+             "sweep::tile_offsets_kernel", "sweep::scan_kernel<WidthLoad>", "column_count_kernel",
+             "column_scan_kernel", "column_bucket_kernel"],
     "sort": [],
     "composite": ["checkpoint_clear_kernel (lists above 8192 entries)", "composite_fwd_kernel"],
     "loss": ["l1_fwd_kernel", "l1_finish_kernel", "l1_bwd_kernel", "torch fill (gradient buffer)"],
@@ -164,18 +167,38 @@ def run_step(splats, cam, target, tile_size, near, far):
     return loss
 
 
+def stage_marker():
+    """Stage timing events: mark(name) ends the running stage and starts the
+    next one.  Between the two events the GPU spins (STAGE_HOLD_CYCLES), so the
+    next stage's first kernels are queued by the time its start event fires:
+    a stage's time then excludes the host's launch gap in front of it.
+    Returns (mark, times) where times() gives {stage: ms} once synchronised."""
+    starts, ends, order = {}, {}, []
+
+    def mark(name):
+        end = torch.cuda.Event(enable_timing=True)
+        end.record()
+        ends[name] = end
+        order.append(name)
+        torch.cuda._sleep(STAGE_HOLD_CYCLES)
+        start = torch.cuda.Event(enable_timing=True)
+        start.record()
+        starts[name] = start  # the start of the stage after `name`
+
+    def times():
+        return {b: starts[a].elapsed_time(ends[b]) for a, b in zip(order[:-1], order[1:])}
+
+    return mark, times
+
+
 def staged_step(params, cam, target, tile_size, near, far):
-    """One fwd+bwd through the stage functions with an event after each stage."""
+    """One fwd+bwd through the stage functions with timing events around each
+    stage (stage_marker)."""
     from gaussian_splats_hip.kernels.rasterize import composite_bwd, project_and_count, project_bwd
     from gaussian_splats_hip.kernels.rasterize.interface import forward_pipeline
     from gaussian_splats_hip.training import l1_loss_backward, l1_loss_forward
 
-    events = {}
-
-    def mark(name):
-        ev = torch.cuda.Event(enable_timing=True)
-        ev.record()
-        events[name] = ev
+    mark, stage_times = stage_marker()
 
     fx, fy = cam.focal_length
     cx, cy = cam.principal_point
@@ -195,8 +218,7 @@ def staged_step(params, cam, target, tile_size, near, far):
     project_bwd(*params, R, t, pinv, grad_proj, counts, fx, fy, w, h)
     mark("project_bwd")
     torch.cuda.synchronize()
-    order = ["start", "project", "bin", "emit", "sort", "composite", "loss", "composite_bwd", "project_bwd"]
-    ms = {b: events[a].elapsed_time(events[b]) for a, b in zip(order[:-1], order[1:])}
+    ms = stage_times()
     # Row-list entries: tile rows covered by the Gaussians with intersections.
     _, _, _, _, bounds, counts2 = project_and_count(*params, R, t, fx, fy, cx, cy, w, h, tile_size,
                                                     near, far, "gaussian", 0.95)
@@ -447,13 +469,7 @@ def bench_views(args, scene):
     rot, trans, intr, _, _ = camera_tensors(cams)
     runs = []
     for _ in range(3):
-        events = {}
-
-        def mark(name):
-            ev = torch.cuda.Event(enable_timing=True)
-            ev.record()
-            events[name] = ev
-
+        mark, stage_times = stage_marker()
         out = forward_views(*params, rot, trans, intr, w, h, tile, 0.999, scene.near, scene.far,
                             "gaussian", 0.95, timer=mark)
         _, code = l1_loss_forward(out[0], target)
@@ -462,9 +478,7 @@ def bench_views(args, scene):
         backward_views(*params, rot, trans, intr, w, h, tile, 0.999, out[1:], grad_image,
                        timer=mark)
         torch.cuda.synchronize()
-        order = ["start", "project", "bin", "emit", "sort", "composite", "loss", "composite_bwd",
-                 "project_bwd"]
-        runs.append({b: events[a].elapsed_time(events[b]) for a, b in zip(order[:-1], order[1:])})
+        runs.append(stage_times())
     stages_ms = {k: sum(r[k] for r in runs) / len(runs) for k in runs[0]}
 
     # Work figures: per-view processed pairs on the mosaic, row-list entries.

@@ -135,19 +135,35 @@ __global__ __launch_bounds__(kBlock) void hist_kernel(const K* __restrict__ keys
   __syncthreads();
   const int lane = __lane_id();
   const int64_t stride = int64_t(gridDim.x) * kBlock;
-  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
-    const K k = keys[i];
-    for (int p = 0; p < plan.passes; ++p) {
-      const uint32_t d = uint32_t(k >> plan.shift[p]) & ((1u << plan.bits[p]) - 1u);
-      // Active lanes with the same digit (digits have at most eight bits).
-      uint64_t peers = __ballot(1);
+  // Each round requests a thread's next kHistKeys keys together, then counts
+  // them (one dependent round trip per round, not per key).
+  constexpr int kHistKeys = 16;
+  for (int64_t i0 = int64_t(blockIdx.x) * kBlock + threadIdx.x; i0 - threadIdx.x < n;
+       i0 += stride * kHistKeys) {
+    K k[kHistKeys];
 #pragma unroll
-      for (int bit = 0; bit < 8; ++bit) {
-        const bool set = (d >> bit) & 1u;
-        const uint64_t ones = __ballot(set);
-        peers &= set ? ones : ~ones;
+    for (int u = 0; u < kHistKeys; ++u) {
+      const int64_t i = i0 + u * stride;
+      k[u] = i < n ? keys[i] : K(0);
+    }
+#pragma unroll
+    for (int u = 0; u < kHistKeys; ++u) {
+      const bool ok = i0 + u * stride < n;
+      const uint64_t active = __ballot(ok);
+      if (!active) continue;
+      for (int p = 0; p < plan.passes; ++p) {
+        const uint32_t d = uint32_t(k[u] >> plan.shift[p]) & ((1u << plan.bits[p]) - 1u);
+        // Active lanes with the same digit (digits have at most eight bits).
+        uint64_t peers = active;
+#pragma unroll
+        for (int bit = 0; bit < 8; ++bit) {
+          const bool set = (d >> bit) & 1u;
+          const uint64_t ones = __ballot(set);
+          peers &= set ? ones : ~ones;
+        }
+        if (ok && lane == __builtin_ctzll(peers))
+          atomicAdd(&h[p * 256 + d], uint32_t(__popcll(peers)));
       }
-      if (lane == __builtin_ctzll(peers)) atomicAdd(&h[p * 256 + d], uint32_t(__popcll(peers)));
     }
   }
   __syncthreads();

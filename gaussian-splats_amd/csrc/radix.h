@@ -117,7 +117,7 @@ int radix_sort(K* keys, const uint32_t* vals, int64_t n, int end_bit, uint32_t* 
   *keys_final = keys;
   if (n == 0) return GS_OK;
   const sweep::Plan plan = sweep::make_plan(end_bit);
-  const int hist_blocks = int(std::min<int64_t>(512, ceil_div(n, kBlock * 16)));
+  const int hist_blocks = int(std::min<int64_t>(1024, ceil_div(n, kBlock * 16)));
   sweep::hist_kernel<K><<<unsigned(hist_blocks), kBlock, 0, s>>>(keys, n, plan, ws.hist());
   K* kbuf[2] = {static_cast<K*>(ws.keys_alt), keys};
   const K* kin = keys;

@@ -225,6 +225,25 @@ __host__ __device__ inline int checkpoint_count(int64_t start, int max_n, int64_
   return int(m < kMaxCheckpoints ? m : kMaxCheckpoints);
 }
 
+// Hit masks (no counterpart in the reference): for every batch of 64 entries
+// of a tile's list that the forward walks, one 64-bit mask per 64-pixel band
+// of the tile (tile_bands), bit j set when entry j of the batch took a
+// nonzero alpha at a pixel of the band while the pixel was active.  The masks
+// of batch b of tile t, whose list starts at `start`, are at slot
+// start / 64 + t + b (unique for lists that follow each other in tile order,
+// as the binning writes them) times the tile's band count.  The backward
+// walks only the marked entries and bands.
+__host__ __device__ inline int64_t hit_mask_slot(int64_t start, int tile, int64_t batch) {
+  return (start >> 6) + tile + batch;
+}
+__host__ __device__ inline int tile_bands(int tile_size) {
+  return tile_size * tile_size >= 64 ? tile_size * tile_size / 64 : 1;
+}
+__host__ __device__ inline int64_t hit_mask_words(int64_t num_intersections, int num_tiles,
+                                                  int tile_size) {
+  return (num_intersections / 64 + num_tiles + 2) * tile_bands(tile_size);
+}
+
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 inline size_t align_up(size_t x, size_t a = 256) { return (x + a - 1) / a * a; }

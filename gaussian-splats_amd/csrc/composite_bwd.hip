@@ -51,6 +51,9 @@ struct CompositeBwdArgs {
   const int32_t* ckpt_table;
   const float4* ckpt_records;
   int64_t ckpt_capacity;
+  // The forward's hit masks (hit_mask_slot), read by the MASKS kernels.
+  const uint64_t* hit_masks;
+  int64_t hit_capacity;  // words
 };
 
 // One wave takes PIX pixels per lane of `tile`: the 64-pixel bands band0 ..
@@ -65,7 +68,11 @@ struct CompositeBwdArgs {
 // associative combine of back-to-front compositing, composite_bwd.py:24-36).
 // Segments past the last recorded checkpoint (a full pool) have no work; the
 // one at it runs to the end.
-template <int TILE, bool ABS, int PIX>
+// The walk takes the list in the forward's batches of 64 entries (lane j:
+// entry j of the batch), last batch first; each lane tests its entry's reach
+// of every band's active pixels.  MASKS: only the entries the forward's masks
+// mark (those that reached its active pixels) are gathered and tested.
+template <int TILE, bool ABS, int PIX, bool MASKS>
 __device__ __forceinline__ void composite_bwd_tile(const CompositeBwdArgs& a, float4 (*chunk)[3],
                                                    int lane, int tile, int band0, int seg) {
   constexpr int NPIX = TILE * TILE;
@@ -102,8 +109,26 @@ __device__ __forceinline__ void composite_bwd_tile(const CompositeBwdArgs& a, fl
     gs_[k] = 0.0f;
     max_n = max(max_n, ncon[k]);
   }
+  // MASKS: each band's largest contributor count.  The forward's wave of a
+  // band wrote the masks of every batch below it and may have stopped after
+  // it, so later words of the band are never read.  The wave-wide maxima are
+  // made scalar (readfirstlane), which keeps the walk's bounds in SGPRs.
+  int band_hi[PIX];
+  if constexpr (MASKS) {
+    max_n = 0;
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) max_n = max(max_n, __shfl_xor(max_n, o, 64));
+    for (int k = 0; k < PIX; ++k) {
+      int m = ncon[k];
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) m = max(m, __shfl_xor(m, o, 64));
+      band_hi[k] = __builtin_amdgcn_readfirstlane(m);
+      max_n = max(max_n, band_hi[k]);
+    }
+  } else {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) max_n = max(max_n, __shfl_xor(max_n, o, 64));
+    max_n = __builtin_amdgcn_readfirstlane(max_n);
+  }
   int lo = 0, hi = max_n;  // positions walked
   if (seg >= 0) {
     // Recorded checkpoints: a prefix of the tile's crossings (lane j reads
@@ -134,10 +159,6 @@ __device__ __forceinline__ void composite_bwd_tile(const CompositeBwdArgs& a, fl
     if (lo >= hi) return;
   }
 
-  // Pixel rectangle of this wave's bands clipped to the image.
-  const float rx0 = float(ox), ry0 = float(oy + band0 * kBandRows);
-  const float rx1 = float(min(ox + TILE, a.width) - 1);
-  const float ry1 = float(min(min(oy + (band0 + PIX) * kBandRows, oy + TILE), a.height) - 1);
   // Gradient fields written by this lane's two atomics: lane 16 r writes the
   // row-r fields of t0 and t1 of the nine-way sum, lane 1 the opacity total t2.
   const int field = sum9_field(lane >> 4);
@@ -147,20 +168,60 @@ __device__ __forceinline__ void composite_bwd_tile(const CompositeBwdArgs& a, fl
 
   // Each batch's ids are requested one batch ahead, once the current batch
   // is in LDS, so a batch waits on one dependent load (the gather), not two.
-  uint32_t next_id =
-      start + hi - 1 - lane >= start + lo ? uint32_t(a.ids[start + hi - 1 - lane]) : 0u;
-  for (int64_t top = start + hi; top > start + lo; top -= 64) {
-    const int64_t e = top - 1 - lane;
+  constexpr int kBands = NPIX >= 64 ? NPIX / 64 : 1;  // the tile's 64-pixel bands
+  const int64_t b_lo = lo >> 6;                   // lo is a multiple of 64
+  const int64_t b_end = (int64_t(hi) + 63) >> 6;  // batches [b_lo, b_end)
+  uint32_t next_id = b_end > b_lo && (b_end - 1) * 64 + lane < hi
+                         ? uint32_t(a.ids[start + (b_end - 1) * 64 + lane])
+                         : 0u;
+  // MASKS: the OR of batch bt's masks of the wave's bands (wave-uniform),
+  // requested one batch ahead.  The masks do not change during the launch:
+  // read through the constant address space, the uniform reads are scalar
+  // loads.
+  using ConstMasks = const __attribute__((address_space(4))) uint64_t*;
+  const ConstMasks masks = (ConstMasks)a.hit_masks;
+  uint64_t next_walk = ~uint64_t(0);
+  auto load_masks = [&](int64_t bt) {
+    const int64_t w0 = hit_mask_slot(start, tile, bt) * kBands + band0;
+    next_walk = 0;
+#pragma unroll
+    for (int k = 0; k < PIX; ++k)
+      next_walk |=
+          bt >= b_lo && bt * 64 < band_hi[k] && w0 + k < a.hit_capacity ? masks[w0 + k] : 0;
+  };
+  if constexpr (MASKS) load_masks(b_end - 1);
+  for (int64_t bt = b_end - 1; bt >= b_lo; --bt) {
+    const int pos0 = int(bt * 64);  // list position of lane 0's entry
+    const bool valid = pos0 + lane < hi;
+    const uint64_t walk = next_walk;  // MASKS: the entries to gather
+    // Each band's overlap test takes the rectangle of its pixels active at
+    // some position of the batch (ncon > pos0); a band with none is skipped.
+    float bx0[PIX], bx1[PIX], by0[PIX], by1[PIX];
+    uint32_t live_bands = 0;
+#pragma unroll
+    for (int k = 0; k < PIX; ++k) {
+      const uint64_t m = __ballot(pos0 < ncon[k]);
+      bx0[k] = bx1[k] = by0[k] = by1[k] = 0.0f;
+      if (m) {
+        uint32_t c;
+        int r0, r1;
+        band_span<TILE>(m, c, r0, r1);
+        bx0[k] = float(ox + __builtin_ctz(c));
+        bx1[k] = float(ox + 31 - __builtin_clz(c));
+        by0[k] = float(oy + (band0 + k) * kBandRows + r0);
+        by1[k] = float(oy + (band0 + k) * kBandRows + r1);
+        live_bands |= 1u << k;
+      }
+    }
     LaneSplat mine;
     int gid = 0;
-    uint32_t bands = 0;  // bit k: the Gaussian can reach a pixel of band k
-    if (e >= start + lo) {
+    uint32_t bands = 0;  // bit k: the Gaussian can reach an active pixel of band k
+    if (valid && live_bands && ((walk >> lane) & 1u)) {
       gid = int(min(next_id, a.max_id));
       const GsRecord rec = load_projected(a.pmean, a.pinv, a.pcolor, a.popacity, gid);
 #pragma unroll
       for (int k = 0; k < PIX; ++k) {
-        const float y0 = ry0 + float(k * kBandRows);
-        if (y0 <= ry1 && touches_rect(rec, rx0, rx1, y0, fminf(y0 + float(kBandRows - 1), ry1)))
+        if (((live_bands >> k) & 1u) && touches_rect(rec, bx0[k], bx1[k], by0[k], by1[k]))
           bands |= 1u << k;
       }
       mine = lane_splat(rec);
@@ -168,11 +229,12 @@ __device__ __forceinline__ void composite_bwd_tile(const CompositeBwdArgs& a, fl
     chunk[lane][0] = make_float4(mine.u, mine.v, mine.o, mine.pa);
     chunk[lane][1] = make_float4(mine.pb, mine.pc, mine.r, mine.g);
     chunk[lane][2] = make_float4(mine.b, mine.oa, mine.ob, mine.oc);
-    next_id = e - 64 >= start + lo ? uint32_t(a.ids[e - 64]) : 0u;
+    next_id = bt - 1 >= b_lo ? uint32_t(a.ids[start + (bt - 1) * 64 + lane]) : 0u;
+    if constexpr (MASKS) load_masks(bt - 1);
     uint64_t mask = __ballot(bands != 0);
     while (mask) {
-      const int j = __builtin_ctzll(mask);
-      mask &= mask - 1;
+      const int j = 63 - __builtin_clzll(mask);  // back to front
+      mask &= ~(uint64_t(1) << j);
       const uint32_t band_mask = uint32_t(__builtin_amdgcn_readlane(int(bands), j));
       const float4 f0 = chunk[j][0], f1 = chunk[j][1], f2 = chunk[j][2];
       Splat s;
@@ -186,7 +248,7 @@ __device__ __forceinline__ void composite_bwd_tile(const CompositeBwdArgs& a, fl
       s.r = f1.z;
       s.g = f1.w;
       s.bl = f2.x;
-      const int pos = int(top - 1 - start) - j;
+      const int pos = pos0 + j;
       const ColumnTerms c = column_terms(s, pxf);
       // Per-lane sums over the lane's pixels; -0 is the identity of +, so the
       // first term needs no add.
@@ -281,7 +343,7 @@ __device__ __forceinline__ void composite_bwd_tile(const CompositeBwdArgs& a, fl
 // composites the whole tile and the others have no work.  Each kernel thus
 // composites every pixel of any plan exactly once, with one instance of the
 // walk (two would share one register allocation).
-template <int TILE, bool ABS, bool QUARTERS>
+template <int TILE, bool ABS, bool QUARTERS, bool MASKS>
 __global__ __launch_bounds__(kCompositeWaves * 64) void composite_bwd_kernel(CompositeBwdArgs a) {
   constexpr int NPIX = TILE * TILE;
   constexpr int PIX_TILE = NPIX >= 64 ? NPIX / 64 : 1;
@@ -301,16 +363,24 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_bwd_kernel(Com
     static_assert(PIX_TILE >= kCompositeWaves, "quarters of 64-pixel bands");
     constexpr int QPIX = PIX_TILE / kCompositeWaves;
     if (kind == kItemQuarter) {
-      composite_bwd_tile<TILE, ABS, QPIX>(a, chunk[wid], lane, tile, index * QPIX, -1);
+      composite_bwd_tile<TILE, ABS, QPIX, MASKS>(a, chunk[wid], lane, tile, index * QPIX, -1);
     } else if (kind == kItemTile || index == 0) {  // a segmented tile whole, by its first item
       for (int q = 0; q < kCompositeWaves; ++q)
-        composite_bwd_tile<TILE, ABS, QPIX>(a, chunk[wid], lane, tile, q * QPIX, -1);
+        composite_bwd_tile<TILE, ABS, QPIX, MASKS>(a, chunk[wid], lane, tile, q * QPIX, -1);
     }
   } else {
     if (kind == kItemQuarter && index != 0) return;  // the tile whole, by its first quarter
-    composite_bwd_tile<TILE, ABS, PIX_TILE>(a, chunk[wid], lane, tile, 0,
-                                            kind == kItemSegment ? index : -1);
+    composite_bwd_tile<TILE, ABS, PIX_TILE, MASKS>(a, chunk[wid], lane, tile, 0,
+                                                   kind == kItemSegment ? index : -1);
   }
+}
+
+template <int TILE, bool QUARTERS, bool MASKS>
+void launch_masks(const CompositeBwdArgs& a, unsigned blocks, hipStream_t s) {
+  if (a.grad_abs)
+    composite_bwd_kernel<TILE, true, QUARTERS, MASKS><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
+  else
+    composite_bwd_kernel<TILE, false, QUARTERS, MASKS><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
 }
 
 template <int TILE, bool QUARTERS>
@@ -318,10 +388,10 @@ void launch_items(const CompositeBwdArgs& a, hipStream_t s) {
   const unsigned blocks = unsigned(
       a.items ? a.num_items / kCompositeWaves
               : (a.split_all ? a.num_tiles : ceil_div(a.num_tiles, kCompositeWaves)));
-  if (a.grad_abs)
-    composite_bwd_kernel<TILE, true, QUARTERS><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
+  if (a.hit_masks)
+    launch_masks<TILE, QUARTERS, true>(a, blocks, s);
   else
-    composite_bwd_kernel<TILE, false, QUARTERS><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
+    launch_masks<TILE, QUARTERS, false>(a, blocks, s);
 }
 
 template <int TILE>
@@ -346,7 +416,8 @@ extern "C" GS_API int gs_composite_bwd(const float* projected_mean,
                                        const int32_t* n_contributors, const int32_t* tile_order,
                                        gs_view view, float* grad_projected, float* grad_absolute,
                                        const void* checkpoints, size_t checkpoint_bytes,
-                                       int64_t num_intersections, void* stream) {
+                                       int64_t num_intersections, const uint64_t* hit_masks,
+                                       size_t hit_mask_bytes, void* stream) {
   clear_error();
   GS_TRY(check_view(view, true));
   GS_REQUIRE(view.rendering_mode == GS_MODE_GAUSSIAN, GS_ERR_UNSUPPORTED,
@@ -389,6 +460,18 @@ extern "C" GS_API int gs_composite_bwd(const float* projected_mean,
   a.ckpt_table = nullptr;
   a.ckpt_records = nullptr;
   a.ckpt_capacity = 0;
+  a.hit_masks = hit_masks;
+  a.hit_capacity = 0;
+  if (hit_masks) {
+    GS_REQUIRE(num_intersections >= 0, GS_ERR_INVALID_ARGUMENT, "negative intersection count");
+    const int64_t words = hit_mask_words(num_intersections, a.num_tiles, view.tile_size);
+    GS_REQUIRE(hit_mask_bytes >= size_t(words) * 8, GS_ERR_WORKSPACE,
+               "hit mask buffer too small (%zu bytes, need %zu)", hit_mask_bytes,
+               size_t(words) * 8);
+    GS_REQUIRE((reinterpret_cast<uintptr_t>(hit_masks) & 7u) == 0, GS_ERR_INVALID_ARGUMENT,
+               "hit masks must be 8-byte aligned");
+    a.hit_capacity = words;
+  }
   if (checkpoints && !plan.split_all) {
     GS_REQUIRE(num_intersections >= 0, GS_ERR_INVALID_ARGUMENT, "negative intersection count");
     const CheckpointLayout c = checkpoint_layout(const_cast<void*>(checkpoints), view.tile_size,

@@ -13,9 +13,12 @@
 // Integer pixel coordinates (no +0.5, torch.py:157-168), black background.
 //
 // Each lane gathers one Gaussian record of the next 64 list entries and tests
-// whether it can reach alpha >= 1/255 anywhere in the tile (touches_rect); the
-// wave then walks only the set bits of that ballot, reading each record as an
-// LDS broadcast.  The tile stops as soon as no pixel is active.
+// whether it can reach alpha >= 1/255 anywhere in the rectangle spanned by
+// the wave's pixels still active (touches_rect, band_span); the wave then
+// walks only the set bits of that ballot, reading each record as an LDS
+// broadcast.  The tile stops as soon as no pixel is active.  With hit masks,
+// each batch's ballot is stored for the backward, which then gathers only
+// the entries it marks.
 #include "common.h"
 #include "raster_math.h"
 
@@ -45,14 +48,18 @@ struct CompositeArgs {
   int32_t* ckpt_table;
   float4* ckpt_records;
   int64_t ckpt_capacity;
+  // The walked batches' hit masks (hit_mask_slot), or null: none.
+  uint64_t* hit_masks;
+  int64_t hit_capacity;  // words
 };
 
 // One wave composites PIX pixels per lane of `tile`: the 64-pixel bands
 // band0 .. band0 + PIX - 1 (all of the tile's bands for a whole-tile item, a
 // quarter of them for a quarter item; every wave walks the whole list).
 // With `checkpoints` (whole tiles only) the walk records the checkpoints
-// described at CheckpointLayout.
-template <int TILE, bool ELLIPSOID, int PIX>
+// described at CheckpointLayout; with HITS, every walked batch's overlap
+// ballot in the hit-mask words of each of the wave's bands.
+template <int TILE, bool ELLIPSOID, int PIX, bool HITS>
 __device__ __forceinline__ void composite_tile(const CompositeArgs& a, float4 (*chunk)[3],
                                                int* ck_slots, int lane, int tile, int band0,
                                                bool checkpoints) {
@@ -74,7 +81,11 @@ __device__ __forceinline__ void composite_tile(const CompositeArgs& a, float4 (*
   const float pxf = float(ox + lane % TILE);
   float pyf[PIX];
   float T[PIX], cr[PIX], cg[PIX], cb[PIX];
-  bool live[PIX];
+  // A pixel is active at list position pos while pos < ncon: ncon starts at
+  // the list length (0 for an inactive pixel) and becomes pos + 1 at the
+  // entry that deactivates it.  No per-pixel flag is carried through the
+  // walk: the comparison replaces the lane-mask merges that a loop-carried
+  // flag costs in scalar instructions per entry.
   int ncon[PIX];
   const bool start_active = (1.0f - 1.0f) < a.threshold;
 #pragma unroll
@@ -85,24 +96,18 @@ __device__ __forceinline__ void composite_tile(const CompositeArgs& a, float4 (*
     pyf[k] = float(py);
     T[k] = 1.0f;
     cr[k] = cg[k] = cb[k] = 0.0f;
-    live[k] = valid && start_active;
-    ncon[k] = live[k] ? list_len : 0;
+    ncon[k] = valid && start_active ? list_len : 0;
   }
-  // Pixel rectangle of this wave's bands clipped to the image, for the
-  // overlap test (64 / TILE rows per band).
-  constexpr int kBandRows = 64 / TILE > 0 ? 64 / TILE : 1;
-  const float rx0 = float(ox), ry0 = float(oy + band0 * kBandRows);
-  const float rx1 = float(min(ox + TILE, a.width) - 1);
-  const float ry1 = float(min(min(oy + (band0 + PIX) * kBandRows, oy + TILE), a.height) - 1);
+  constexpr int kBandRows = 64 / TILE > 0 ? 64 / TILE : 1;  // tile rows per band
 
-  auto any_live = [&]() {
+  bool running;
+  {
     bool l = false;
 #pragma unroll
-    for (int k = 0; k < PIX; ++k) l |= live[k];
-    return __ballot(l) != 0;
-  };
-
-  bool running = any_live();
+    for (int k = 0; k < PIX; ++k) l |= ncon[k] > 0;
+    running = __ballot(l) != 0;
+  }
+  constexpr int kBands = NPIX >= 64 ? NPIX / 64 : 1;  // the tile's 64-pixel bands
   // Checkpoint state (wave-uniform): crossings reached, records written (a
   // prefix of the crossings: once the pool is full every later allocation
   // fails), the walk position of the next crossing; the records' slots go to
@@ -139,6 +144,31 @@ __device__ __forceinline__ void composite_tile(const CompositeArgs& a, float4 (*
       ++ck_count;
       ck_next = ck_count < kMaxCheckpoints ? checkpoint_batch(start, ck_count + 1) : -1;
     }
+    // The overlap test's rectangle: the columns and rows of the pixels still
+    // active at the batch's first entry (a set that only shrinks within the
+    // batch; the walk is running, so it is not empty).
+    float rx0, rx1, ry0, ry1;
+    {
+      const int bpos = int(base - start);
+      uint32_t cols = 0;
+      int rlo = NPIX, rhi = -1;
+#pragma unroll
+      for (int k = 0; k < PIX; ++k) {
+        const uint64_t m = __ballot(bpos < ncon[k]);
+        if (m) {
+          uint32_t c;
+          int r0, r1;
+          band_span<TILE>(m, c, r0, r1);
+          cols |= c;
+          rlo = min(rlo, (band0 + k) * kBandRows + r0);
+          rhi = max(rhi, (band0 + k) * kBandRows + r1);
+        }
+      }
+      rx0 = float(ox + __builtin_ctz(cols));
+      rx1 = float(ox + 31 - __builtin_clz(cols));
+      ry0 = float(oy + rlo);
+      ry1 = float(oy + rhi);
+    }
     const int64_t e = base + lane;
     LaneSplat mine;
     bool keep = false;
@@ -152,8 +182,14 @@ __device__ __forceinline__ void composite_tile(const CompositeArgs& a, float4 (*
     chunk[lane][2] = make_float4(mine.b, mine.cut, 0.0f, 0.0f);
     id = e + 64 < end ? uint32_t(a.ids[e + 64]) : 0u;
     uint64_t mask = __ballot(keep);
+    if constexpr (HITS) {
+      // The batch's mask, the entries that can reach a pixel of the wave's
+      // bands still active, stored for each of the bands (vector stores).
+      const int64_t w0 = hit_mask_slot(start, tile, (base - start) >> 6) * kBands + band0;
+      if (lane < PIX && w0 + lane < a.hit_capacity) a.hit_masks[w0 + lane] = mask;
+    }
     // No break inside: the loop ends through its condition, which keeps the
-    // per-pixel active flags out of extra mask-merging control flow.
+    // walk's state out of extra mask-merging control flow.
     while (mask) {
       const int j = __builtin_ctzll(mask);
       mask &= mask - 1;
@@ -173,21 +209,25 @@ __device__ __forceinline__ void composite_tile(const CompositeArgs& a, float4 (*
       const ColumnTerms c = column_terms(s, pxf);
       // Branch-free: a finished pixel (or a cut alpha) blends with alpha = 0,
       // which leaves its colour and T unchanged.  T (1 - alpha) = T - w.
+      bool still = false;  // a pixel of the lane stays active after the entry
 #pragma unroll
       for (int k = 0; k < PIX; ++k) {
         float prob;
         const float raw = raw_alpha<ELLIPSOID>(s, c, pyf[k] - s.v, prob);
-        const float alpha = live[k] ? blend_alpha(raw) : 0.0f;
+        const float clamped = fminf(raw, kMaxAlpha);
+        const bool live = pos < ncon[k];
+        const bool take = live && clamped >= kMinAlpha;  // alpha = blend_alpha(raw) > 0
+        const float alpha = take ? clamped : 0.0f;
         const float w = T[k] * alpha;
         cr[k] += w * s.r;
         cg[k] += w * s.g;
         cb[k] += w * s.bl;
         T[k] = T[k] - w;
-        const bool done = live[k] && !(T[k] > a.t_active);
+        const bool done = live && !(T[k] > a.t_active);
         ncon[k] = done ? pos + 1 : ncon[k];
-        live[k] = live[k] && !done;
+        still |= live && !done;
       }
-      if (!any_live()) {
+      if (__ballot(still) == 0) {
         running = false;
         mask = 0;
       }
@@ -231,7 +271,7 @@ __device__ __forceinline__ void composite_tile(const CompositeArgs& a, float4 (*
 // first composites the whole tile and the others have no work.  Each kernel
 // thus composites every pixel of any plan exactly once, with one instance of
 // the walk (two would share one register allocation).
-template <int TILE, bool ELLIPSOID, bool QUARTERS, bool CKPT>
+template <int TILE, bool ELLIPSOID, bool QUARTERS, bool CKPT, bool HITS>
 __global__ __launch_bounds__(kCompositeWaves * 64) void composite_fwd_kernel(CompositeArgs a) {
   constexpr int NPIX = TILE * TILE;
   constexpr int PIX_TILE = NPIX >= 64 ? NPIX / 64 : 1;
@@ -255,15 +295,16 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_fwd_kernel(Com
     static_assert(PIX_TILE >= kCompositeWaves, "quarters of 64-pixel bands");
     constexpr int QPIX = PIX_TILE / kCompositeWaves;
     if (kind == kItemQuarter) {
-      composite_tile<TILE, ELLIPSOID, QPIX>(a, chunk[wid], ck_slots[wid], lane, tile, index * QPIX,
-                                            false);
+      composite_tile<TILE, ELLIPSOID, QPIX, HITS>(a, chunk[wid], ck_slots[wid], lane, tile,
+                                                  index * QPIX, false);
     } else {
       for (int q = 0; q < kCompositeWaves; ++q)
-        composite_tile<TILE, ELLIPSOID, QPIX>(a, chunk[wid], ck_slots[wid], lane, tile, q * QPIX,
-                                              false);
+        composite_tile<TILE, ELLIPSOID, QPIX, HITS>(a, chunk[wid], ck_slots[wid], lane, tile,
+                                                    q * QPIX, false);
     }
   } else {
-    composite_tile<TILE, ELLIPSOID, PIX_TILE>(a, chunk[wid], ck_slots[wid], lane, tile, 0, CKPT);
+    composite_tile<TILE, ELLIPSOID, PIX_TILE, HITS>(a, chunk[wid], ck_slots[wid], lane, tile, 0,
+                                                    CKPT);
   }
 }
 
@@ -273,13 +314,18 @@ void launch_items(const CompositeArgs& a, bool ellipsoid, hipStream_t s) {
       a.items ? a.num_items / kCompositeWaves
               : (a.split_all ? a.num_tiles : ceil_div(a.num_tiles, kCompositeWaves)));
   if (ellipsoid)
-    composite_fwd_kernel<TILE, true, QUARTERS, CKPT><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
+    composite_fwd_kernel<TILE, true, QUARTERS, CKPT, false>
+        <<<blocks, kCompositeWaves * 64, 0, s>>>(a);
+  else if (a.hit_masks)
+    composite_fwd_kernel<TILE, false, QUARTERS, CKPT, true>
+        <<<blocks, kCompositeWaves * 64, 0, s>>>(a);
   else
-    composite_fwd_kernel<TILE, false, QUARTERS, CKPT><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
+    composite_fwd_kernel<TILE, false, QUARTERS, CKPT, false>
+        <<<blocks, kCompositeWaves * 64, 0, s>>>(a);
 }
 
 // Checkpoint recording is a kernel of its own: the code for it costs the
-// walk registers (70 VGPRs instead of 64 at tile 16, 7 waves per SIMD
+// walk registers (73 VGPRs instead of 60 at tile 16, 6 waves per SIMD
 // instead of 8), which only long lists repay.
 template <int TILE>
 void launch(const CompositeArgs& a, bool ellipsoid, hipStream_t s) {
@@ -309,12 +355,19 @@ extern "C" GS_API size_t gs_composite_checkpoint_bytes(gs_view view, int64_t num
   return checkpoint_layout(nullptr, view.tile_size, num_intersections).bytes;
 }
 
+extern "C" GS_API size_t gs_composite_hit_mask_bytes(gs_view view, int64_t num_intersections) {
+  if (check_view(view, true) != GS_OK || num_intersections < 0) return 0;
+  const Mosaic m = mosaic_of(view);
+  return size_t(hit_mask_words(num_intersections, m.num_tiles(), view.tile_size)) * 8;
+}
+
 extern "C" GS_API int gs_composite(const void* records, int64_t num_records,
                                    const int32_t* gaussian_ids, int64_t num_intersections,
                                    const int64_t* ranges, const int32_t* tile_order, gs_view view,
                                    float* image, float* final_transmittance,
                                    int32_t* n_contributors, void* checkpoints,
-                                   size_t checkpoint_bytes, void* stream) {
+                                   size_t checkpoint_bytes, uint64_t* hit_masks,
+                                   size_t hit_mask_bytes, void* stream) {
   clear_error();
   GS_TRY(check_view(view, true));
   GS_REQUIRE(ranges && image && final_transmittance && n_contributors, GS_ERR_INVALID_ARGUMENT,
@@ -353,6 +406,19 @@ extern "C" GS_API int gs_composite(const void* records, int64_t num_records,
   a.ckpt_table = nullptr;
   a.ckpt_records = nullptr;
   a.ckpt_capacity = 0;
+  a.hit_masks = hit_masks;
+  a.hit_capacity = 0;
+  if (hit_masks) {
+    GS_REQUIRE(view.rendering_mode == GS_MODE_GAUSSIAN, GS_ERR_UNSUPPORTED,
+               "hit masks are recorded for Gaussian rendering only (its backward reads them)");
+    const int64_t words = hit_mask_words(num_intersections, a.num_tiles, view.tile_size);
+    GS_REQUIRE(hit_mask_bytes >= size_t(words) * 8, GS_ERR_WORKSPACE,
+               "hit mask buffer too small (%zu bytes, need %zu)", hit_mask_bytes,
+               size_t(words) * 8);
+    GS_REQUIRE((reinterpret_cast<uintptr_t>(hit_masks) & 7u) == 0, GS_ERR_INVALID_ARGUMENT,
+               "hit masks must be 8-byte aligned");
+    a.hit_capacity = words;
+  }
   hipStream_t s = as_stream(stream);
   if (checkpoints && !plan.split_all && view.tile_size <= 16) {
     const CheckpointLayout c = checkpoint_layout(checkpoints, view.tile_size, num_intersections);

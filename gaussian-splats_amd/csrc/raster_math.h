@@ -129,6 +129,21 @@ __device__ __forceinline__ bool touches_rect(const GsRecord& r, float x0, float 
   return m <= r.cut * (1.0f + 1e-3f) + 1e-3f;
 }
 
+// Columns and rows spanned by the set lanes of a 64-pixel band's ballot `m`
+// (m != 0), lane l holding the band's pixel in column l % TILE, row l / TILE:
+// `cols` gets bit c for every column with a set lane (the band's rows ORed
+// into the low TILE bits), r0 / r1 the first and last row.  Scalar work on a
+// wave-uniform mask.
+template <int TILE>
+__device__ __forceinline__ void band_span(uint64_t m, uint32_t& cols, int& r0, int& r1) {
+  uint64_t f = m;
+#pragma unroll
+  for (int s = 32; s >= TILE; s >>= 1) f |= f >> s;
+  cols = uint32_t(f) & uint32_t((uint64_t(1) << TILE) - 1);
+  r0 = __builtin_ctzll(m) / TILE;
+  r1 = (63 - __builtin_clzll(m)) / TILE;
+}
+
 __device__ __forceinline__ GsRecord load_record(const GsRecord* __restrict__ recs, int g) {
   const float4* p = reinterpret_cast<const float4*>(recs + g);
   const float4 a = p[0], b = p[1], c = p[2];

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parents[2] / "_lib" / "libgs_raster.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 GS_OK = 0
 GS_ERR_INVALID_ARGUMENT = 1
@@ -151,6 +151,32 @@ def checkpoint_buffer(view: GsView, num_intersections: int, longest: int,
     return buf[off:off + nbytes]
 
 
+_HIT_MASK_ATTR = "_gs_hit_masks"
+
+
+def set_hit_masks(ranges: torch.Tensor, buffer: torch.Tensor | None) -> None:
+    """Records on ``ranges`` the hit masks the forward wrote for its lists
+    (gs_composite), for the compositing backward of the same lists."""
+    setattr(ranges, _HIT_MASK_ATTR, buffer)
+
+
+def hit_masks(ranges: torch.Tensor | None) -> torch.Tensor | None:
+    """The buffer recorded by ``set_hit_masks``, or None."""
+    return getattr(ranges, _HIT_MASK_ATTR, None) if ranges is not None else None
+
+
+def hit_mask_buffer(view: GsView, num_intersections: int, device: torch.device) -> torch.Tensor:
+    """A hit-mask buffer for gs_composite (int64 words; the forward writes the
+    batches it walks, the backward reads the same ones)."""
+    nbytes = library().gs_composite_hit_mask_bytes(view, int(num_intersections))
+    return torch.empty(max(int(nbytes) // 8, 1), dtype=torch.int64, device=device)
+
+
+def buffer_bytes(t: torch.Tensor | None) -> int:
+    """Size in bytes of an optional buffer argument (0 for None)."""
+    return t.numel() * t.element_size() if t is not None else 0
+
+
 _SIGNATURES = {
     "gs_abi_version": (c_int, []),
     "gs_last_error": (ctypes.c_char_p, []),
@@ -205,15 +231,16 @@ _SIGNATURES = {
     ),
     "gs_tile_order_noalloc": (c_int, [c_void_p, c_void_p, GsView, c_void_p, c_void_p]),
     "gs_composite_checkpoint_bytes": (c_size_t, [GsView, c_int64, c_int64]),
+    "gs_composite_hit_mask_bytes": (c_size_t, [GsView, c_int64]),
     "gs_composite": (
         c_int,
         [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, GsView]
-        + [c_void_p] * 4 + [c_size_t, c_void_p],
+        + [c_void_p] * 4 + [c_size_t, c_void_p, c_size_t, c_void_p],
     ),
     "gs_composite_bwd": (
         c_int,
         [c_void_p] * 4 + [c_int64] + [c_void_p] * 6
-        + [GsView, c_void_p, c_void_p, c_void_p, c_size_t, c_int64, c_void_p],
+        + [GsView, c_void_p, c_void_p, c_void_p, c_size_t, c_int64, c_void_p, c_size_t, c_void_p],
     ),
     "gs_device_errors": (c_int, [c_void_p, c_int32, c_void_p]),
     "gs_project_bwd": (

@@ -22,10 +22,10 @@ def tile_order(
     active_tiles: int = 0,
 ) -> torch.Tensor:
     """Dispatch plan of the compositing kernels (gs_tile_order) for one view:
-    work items (``tile << 3`` for a whole tile, ``tile << 3 | 4 | q`` for
-    quarter ``q`` of its pixel bands, -1 unused) that keep each XCD's region
-    of tiles, start the longest expected work first and split the heaviest
-    tiles over four waves.  The estimate is the list length from ``ranges``
+    work items (``tile << 7`` for a whole tile, ``tile << 7 | 0x20 | q`` for
+    quarter ``q`` of its pixel bands, ``tile << 7 | 0x40 | s`` for segment
+    ``s`` of a backward walk, -1 unused) that keep each XCD's region of tiles
+    and start the longest expected work first.  The estimate is the list length from ``ranges``
     (the forward) or the largest contributor count per tile from
     ``n_contributors`` (the backward).  ``active_tiles`` must be the value the
     compositing call's view carries."""
@@ -56,10 +56,12 @@ def composite(
     *,
     records: torch.Tensor | None = None,
     order: torch.Tensor | None = None,
+    record_hits: bool = True,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Composites the sorted per-tile lists; returns ``(image[H,W,3],
     final_transmittance[H,W], n_contributors[H,W] int32)``.  The walk's
-    checkpoints (gs_composite) are recorded on ``ranges`` for the backward."""
+    checkpoints and (``record_hits``, Gaussian mode) hit masks (gs_composite)
+    are recorded on ``ranges`` for the backward."""
     _check_tile(tile_size)
     device = nat.require_gpu(mean, gaussian_ids, ranges)
     if records is None:
@@ -80,15 +82,19 @@ def composite(
     )
     checkpoints = nat.checkpoint_buffer(view, gaussian_ids.numel(), nat.longest_list(ranges_in),
                                         device)
+    hits = (nat.hit_mask_buffer(view, gaussian_ids.numel(), device)
+            if record_hits and rendering_mode == "gaussian" else None)
     nat.check(
         nat.library().gs_composite(
             nat.ptr(records), records.shape[0], nat.ptr(gaussian_ids), gaussian_ids.numel(),
             nat.ptr(ranges), nat.ptr(order), view, nat.ptr(image), nat.ptr(final_transmittance),
-            nat.ptr(n_contributors), nat.ptr(checkpoints),
-            checkpoints.numel() if checkpoints is not None else 0, nat.stream(device),
+            nat.ptr(n_contributors), nat.ptr(checkpoints), nat.buffer_bytes(checkpoints),
+            nat.ptr(hits), nat.buffer_bytes(hits), nat.stream(device),
         ),
         "composite",
     )
-    # The backward of these lists starts its segment walks at the checkpoints.
+    # The backward of these lists starts its segment walks at the checkpoints
+    # and walks the entries the hit masks mark.
     nat.set_checkpoints(ranges_in, checkpoints)
+    nat.set_hit_masks(ranges_in, hits)
     return image, final_transmittance, n_contributors

@@ -51,6 +51,7 @@ def composite_bwd(
     n_contributors = nat.prepare(n_contributors, torch.int32)
     active = nat.active_tiles(ranges)
     checkpoints = nat.checkpoints(ranges)
+    hits = nat.hit_masks(ranges)
     ranges = nat.prepare(ranges, torch.int64)
     gaussian_ids = nat.prepare(gaussian_ids, torch.int32)
     n = projected_mean.shape[0]
@@ -74,8 +75,8 @@ def composite_bwd(
                 nat.ptr(projected_opacity), n, nat.ptr(gaussian_ids), nat.ptr(ranges),
                 nat.ptr(grad_image), nat.ptr(final_transmittance), nat.ptr(n_contributors),
                 nat.ptr(order), view, nat.ptr(out), nat.ptr(absolute), nat.ptr(checkpoints),
-                checkpoints.numel() if checkpoints is not None else 0, gaussian_ids.numel(),
-                nat.stream(device),
+                nat.buffer_bytes(checkpoints), gaussian_ids.numel(), nat.ptr(hits),
+                nat.buffer_bytes(hits), nat.stream(device),
             ),
         ),
         "composite_bwd",

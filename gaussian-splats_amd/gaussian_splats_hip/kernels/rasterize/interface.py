@@ -45,11 +45,13 @@ def forward_pipeline(
     rendering_mode: str,
     confidence: float,
     timer=None,
+    record_hits: bool = True,
 ) -> tuple[torch.Tensor, ...]:
     """Runs project -> bin -> emit -> sort -> composite; ``timer(name)`` (optional)
     is called between stages for per-stage event timing (with row/column
     bucketing, "bin" ends after the plan, "emit" after the row pass and "sort"
-    after the column pass)."""
+    after the column pass).  ``record_hits``: the compositing forward records
+    the hit masks its backward walks (off when no gradient will follow)."""
     _check_tile(tile_size)
     device = nat.require_gpu(mean, rotation, scale, opacity, color)
     n = mean.shape[0]
@@ -83,7 +85,7 @@ def forward_pipeline(
     image, final_transmittance, n_contributors = composite(
         projected_mean, inverse_covariance, projected_color, projected_opacity, gaussian_ids,
         ranges, image_width, image_height, tile_size, opacity_threshold, rendering_mode,
-        confidence, records=records,
+        confidence, records=records, record_hits=record_hits,
     )
     mark("composite")
     return (
@@ -199,6 +201,7 @@ def _setup_context(ctx, inputs, output) -> None:
         )
         ctx.view_project = nat.make_view(ctx.fx, ctx.fy, 0.0, 0.0, ctx.image_width, ctx.image_height)
         ctx.checkpoints = nat.checkpoints(output[8])
+        ctx.hit_masks = nat.hit_masks(output[8])
         num_tiles = output[8].shape[0]
         lib = nat.library()
         order = torch.empty(lib.gs_tile_order_items(ctx.view_composite, 1), dtype=torch.int32,
@@ -270,6 +273,7 @@ def _backward(ctx, *grad_outputs):
     ptr = nat.ptr
     order = ctx.tile_order
     checkpoints = ctx.checkpoints
+    hits = ctx.hit_masks
     nat.check(
         nat.launch(
             "composite_bwd",
@@ -278,7 +282,8 @@ def _backward(ctx, *grad_outputs):
                 ptr(projected_opacity), projected_mean.shape[0], ptr(gaussian_ids), ptr(ranges),
                 ptr(grad_image), ptr(final_transmittance), ptr(n_contributors), ptr(order),
                 ctx.view_composite, ptr(grad_projected), None, ptr(checkpoints),
-                checkpoints.numel() if checkpoints is not None else 0, gaussian_ids.numel(), stream,
+                nat.buffer_bytes(checkpoints), gaussian_ids.numel(), ptr(hits),
+                nat.buffer_bytes(hits), stream,
             ),
         ),
         "composite_bwd",
@@ -329,7 +334,7 @@ def rasterize_outputs(*inputs) -> tuple[torch.Tensor, ...]:
         return _rasterize(*inputs)
     if torch.is_grad_enabled() and any(t.requires_grad for t in inputs[:5]):
         return _RasterizeFunction.apply(*inputs)
-    return forward_pipeline(*inputs, timer=stage_timer())
+    return forward_pipeline(*inputs, timer=stage_timer(), record_hits=False)
 
 
 def rasterize(

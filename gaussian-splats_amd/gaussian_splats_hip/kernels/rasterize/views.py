@@ -94,9 +94,11 @@ def forward_views(
     rendering_mode: str,
     confidence: float,
     timer=None,
+    record_hits: bool = True,
 ) -> tuple[torch.Tensor, ...]:
     """project (all views) -> bin (mosaic) -> composite (mosaic); ``timer(name)``
-    marks the stages as ``forward_pipeline`` does."""
+    marks the stages and ``record_hits`` selects the hit masks as
+    ``forward_pipeline`` does."""
     _check_tile(tile_size)
     if color.shape[1] > 16:
         raise NotImplementedError(
@@ -171,15 +173,19 @@ def forward_views(
     )
     checkpoints = nat.checkpoint_buffer(view, gaussian_ids.numel(), nat.longest_list(ranges),
                                         device)
+    hits = (nat.hit_mask_buffer(view, gaussian_ids.numel(), device)
+            if record_hits and rendering_mode == "gaussian" else None)
     nat.check(
         lib.gs_composite(
             ptr(records), records.shape[0], ptr(gaussian_ids), gaussian_ids.numel(), ptr(ranges),
             None, view, ptr(image), ptr(final_transmittance), ptr(n_contributors),
-            ptr(checkpoints), checkpoints.numel() if checkpoints is not None else 0, stream,
+            ptr(checkpoints), nat.buffer_bytes(checkpoints), ptr(hits), nat.buffer_bytes(hits),
+            stream,
         ),
         "composite",
     )
     nat.set_checkpoints(ranges, checkpoints)
+    nat.set_hit_masks(ranges, hits)
     mark("composite")
     return (
         image,
@@ -287,6 +293,7 @@ def _setup_context(ctx, inputs, output) -> None:
     ) = inputs[8:]
     ctx.active_tiles = nat.active_tiles(output[8])
     ctx.checkpoints = nat.checkpoints(output[8])
+    ctx.hit_masks = nat.hit_masks(output[8])
     ctx.order = None
     if inputs[0].is_cuda and ctx.rendering_mode == "gaussian":
         # The backward's dispatch plan depends only on the forward's lists and
@@ -319,21 +326,24 @@ def backward_views(
     active_tiles: int | None = None,
     checkpoints: torch.Tensor | None = None,
     order: torch.Tensor | None = None,
+    hit_masks: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, ...]:
     """composite_bwd over the mosaic -> project_bwd summed over the views.
 
     ``saved`` holds the forward's outputs 1..9 (transmittance through counts);
     returns the gradients of the five parameter tensors.  ``timer(name)``
     marks "composite_bwd" and "project_bwd".  ``active_tiles``: tiles with a
-    non-empty list, and ``checkpoints``: the forward's checkpoint buffer
-    (defaults: those the forward recorded on the ranges); ``order``: the
-    dispatch plan of these lists and contributor counts (default: computed
-    here)."""
+    non-empty list, ``checkpoints``: the forward's checkpoint buffer, and
+    ``hit_masks``: its hit masks (defaults: those the forward recorded on the
+    ranges); ``order``: the dispatch plan of these lists and contributor
+    counts (default: computed here)."""
     mark = timer or (lambda name: None)
     if active_tiles is None:
         active_tiles = nat.active_tiles(saved[7])
     if checkpoints is None:
         checkpoints = nat.checkpoints(saved[7])
+    if hit_masks is None:
+        hit_masks = nat.hit_masks(saved[7])
     mean, rotation, scale, opacity, color = (
         _contiguous(t) for t in (mean, rotation, scale, opacity, color)
     )
@@ -375,8 +385,8 @@ def backward_views(
                 ptr(projected_opacity), projected_mean.numel() // 3, ptr(gaussian_ids),
                 ptr(ranges), ptr(grad_image), ptr(final_transmittance), ptr(n_contributors),
                 ptr(order), view, ptr(grad_projected), None, ptr(checkpoints),
-                checkpoints.numel() if checkpoints is not None else 0, gaussian_ids.numel(),
-                stream,
+                nat.buffer_bytes(checkpoints), gaussian_ids.numel(), ptr(hit_masks),
+                nat.buffer_bytes(hit_masks), stream,
             ),
         ),
         "composite_bwd",
@@ -406,7 +416,7 @@ def _backward(ctx, *grad_outputs):
         *saved[:5], ctx.camera_rotations, ctx.camera_translations, ctx.intrinsics,
         ctx.image_width, ctx.image_height, ctx.tile_size, ctx.opacity_threshold, saved[5:],
         grad_outputs[0], active_tiles=ctx.active_tiles, checkpoints=ctx.checkpoints,
-        order=ctx.order,
+        order=ctx.order, hit_masks=ctx.hit_masks,
     )
     return (*grads, *(None,) * 11)
 
@@ -440,7 +450,7 @@ def rasterize_views_outputs(*inputs) -> tuple[torch.Tensor, ...]:
         return _rasterize_views(*inputs)
     if torch.is_grad_enabled() and any(t.requires_grad for t in inputs[:5]):
         return _RasterizeViewsFunction.apply(*inputs)
-    return forward_views(*inputs, timer=stage_timer())
+    return forward_views(*inputs, timer=stage_timer(), record_hits=False)
 
 
 def camera_tensors(cameras: Sequence[Camera]) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, int, int]:

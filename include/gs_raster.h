@@ -42,7 +42,7 @@ extern "C" {
 
 #define GS_API __attribute__((visibility("default")))
 
-#define GS_ABI_VERSION 10
+#define GS_ABI_VERSION 11
 
 typedef enum gs_status {
   GS_OK = 0,
@@ -307,11 +307,23 @@ GS_API int gs_tile_order_noalloc(
  * walk holds 16 pixels per lane, leaving no registers for the records). */
 GS_API size_t gs_composite_checkpoint_bytes(gs_view view, int64_t num_intersections,
                                             int64_t longest_list);
+/* hit_masks (optional, gs_composite_hit_mask_bytes(view, num_intersections)
+ * bytes, 8-byte aligned; no counterpart in the reference): for every batch of
+ * 64 entries of a tile's list that the walk processes, one 64-bit mask per
+ * 64-pixel band of the tile, bit j set when entry j passed the walk's overlap
+ * test, i.e. can reach alpha >= 1/255 inside the rectangle spanned by the
+ * pixels still active at the batch's first entry.  gs_composite_bwd, given
+ * the same buffer, gathers only the entries so marked (every entry that
+ * contributes to a pixel is), instead of every entry of its walk.  The slots
+ * assume the tiles' lists follow each other in tile order, as the binning
+ * writes them; batches the walk does not reach are not written.  Gaussian
+ * rendering only (GS_ERR_UNSUPPORTED otherwise). */
+GS_API size_t gs_composite_hit_mask_bytes(gs_view view, int64_t num_intersections);
 GS_API int gs_composite(
     const void* records, int64_t num_records, const int32_t* gaussian_ids,
     int64_t num_intersections, const int64_t* ranges, const int32_t* tile_order, gs_view view,
     float* image, float* final_transmittance, int32_t* n_contributors, void* checkpoints,
-    size_t checkpoint_bytes, void* stream);
+    size_t checkpoint_bytes, uint64_t* hit_masks, size_t hit_mask_bytes, void* stream);
 
 /* Back-to-front compositing gradient, accumulated with atomics into
  * grad_projected[N,9] (zeroed by the caller), from the op's projected outputs
@@ -326,7 +338,9 @@ GS_API int gs_composite(
  * a segment item starts its walk back at a checkpoint, with the
  * transmittance recorded there and g.S = g . (colour after it) / T, the
  * state the walk from the end would reach (the associative combine of
- * composite_bwd.py:24-36), so a long walk runs on many waves at once. */
+ * composite_bwd.py:24-36), so a long walk runs on many waves at once.
+ * hit_masks: the buffer gs_composite filled for the same lists and view (or
+ * NULL: every entry of the walk is gathered and tested). */
 GS_API int gs_composite_bwd(
     const float* projected_mean, const float* inverse_covariance,
     const float* projected_color, const float* projected_opacity, int64_t n,
@@ -334,7 +348,8 @@ GS_API int gs_composite_bwd(
     const float* grad_image, const float* final_transmittance,
     const int32_t* n_contributors, const int32_t* tile_order, gs_view view,
     float* grad_projected, float* grad_absolute, const void* checkpoints,
-    size_t checkpoint_bytes, int64_t num_intersections, void* stream);
+    size_t checkpoint_bytes, int64_t num_intersections, const uint64_t* hit_masks,
+    size_t hit_mask_bytes, void* stream);
 
 /* Chain rule from grad_projected to the parameters.  Replaces project_bwd
  * (src/gaussian_splats/kernels/rasterize/project_bwd.py:8-381); gradients are

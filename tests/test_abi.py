@@ -158,7 +158,7 @@ def test_invalid_tile_sizes(tile):
     lib = nat.library()
     fake = ctypes.c_void_p(16)
     status = lib.gs_composite(fake, 10, fake, 10, fake, None, _view(tile_size=tile), fake, fake,
-                              fake, None, 0, None)
+                              fake, None, 0, None, 0, None)
     assert status in (nat.GS_ERR_INVALID_ARGUMENT, nat.GS_ERR_UNSUPPORTED)
 
 
@@ -166,9 +166,30 @@ def test_backward_rejects_ellipsoid_mode():
     lib = nat.library()
     fake = ctypes.c_void_p(16)
     status = lib.gs_composite_bwd(*([fake] * 4), 10, *([fake] * 5), None,
-                                  _view(rendering_mode="ellipsoid"), fake, None, None, 0, 0, None)
+                                  _view(rendering_mode="ellipsoid"), fake, None, None, 0, 0,
+                                  None, 0, None)
     assert status == nat.GS_ERR_UNSUPPORTED
     assert b"Gaussian rendering" in lib.gs_last_error()
+
+
+def test_hit_masks_host_checks():
+    """Hit masks are recorded in Gaussian mode only, and their buffer must hold
+    gs_composite_hit_mask_bytes: both checked on the host, before any launch."""
+    lib = nat.library()
+    fake = ctypes.c_void_p(16)
+    view = _view(rendering_mode="ellipsoid")
+    status = lib.gs_composite(fake, 10, fake, 10, fake, None, view, fake, fake, fake, None, 0,
+                              fake, 1 << 20, None)
+    assert status == nat.GS_ERR_UNSUPPORTED
+    assert b"Gaussian rendering" in lib.gs_last_error()
+    need = lib.gs_composite_hit_mask_bytes(_view(), 10)
+    assert need > 0 and need % 8 == 0
+    status = lib.gs_composite(fake, 10, fake, 10, fake, None, _view(), fake, fake, fake, None, 0,
+                              fake, need - 8, None)
+    assert status == nat.GS_ERR_WORKSPACE
+    status = lib.gs_composite_bwd(*([fake] * 4), 10, *([fake] * 5), None, _view(), fake, None,
+                                  None, 0, 10, fake, need - 8, None)
+    assert status == nat.GS_ERR_WORKSPACE
 
 
 def test_misaligned_buffers_rejected():
@@ -185,7 +206,8 @@ def test_status_codes_map_to_python_exceptions():
     lib = nat.library()
     fake = ctypes.c_void_p(16)
     status = lib.gs_composite_bwd(*([fake] * 4), 10, *([fake] * 5), None,
-                                  _view(rendering_mode="ellipsoid"), fake, None, None, 0, 0, None)
+                                  _view(rendering_mode="ellipsoid"), fake, None, None, 0, 0,
+                                  None, 0, None)
     with pytest.raises(NotImplementedError):
         nat.check(status, "composite_bwd")
 
@@ -248,7 +270,7 @@ def test_multi_view_host_checks():
         )
         assert status == nat.GS_ERR_INVALID_ARGUMENT
         status = lib.gs_composite(fake, 10, fake, 10, fake, None, _view(**kw), fake, fake, fake,
-                                  None, 0, None)
+                                  None, 0, None, 0, None)
         assert status == nat.GS_ERR_INVALID_ARGUMENT
     # Virtual Gaussian indices (view * N + i) must fit int32.
     status = lib.gs_project_views(
@@ -265,7 +287,7 @@ def test_multi_view_host_checks():
     status = lib.gs_composite(
         fake, 10, fake, 10, fake, None, _view(image_width=1 << 16, image_height=1 << 16,
                                               tile_size=4, views=64, mosaic_cols=8),
-        fake, fake, fake, None, 0, None,
+        fake, fake, fake, None, 0, None, 0, None,
     )
     assert status == nat.GS_ERR_OVERFLOW
     # Zero Gaussians: nothing to do.

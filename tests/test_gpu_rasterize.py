@@ -254,7 +254,7 @@ def test_composite_backward_segmented_walks(device, entries):
     nat.check(nat.library().gs_composite_bwd(
         *(nat.ptr(t) for t in cols), entries, nat.ptr(gids), nat.ptr(granges), nat.ptr(g_dev),
         nat.ptr(final_t), nat.ptr(ncon), None, view, nat.ptr(whole), None, None, 0, 0,
-        nat.stream(device)), "composite_bwd")
+        None, 0, nat.stream(device)), "composite_bwd")
     torch.cuda.synchronize()
     scale = whole.abs().amax(dim=0, keepdim=True).clamp_min(1e-30).cpu()
     assert float(((grad - whole.cpu()).abs() / scale).max()) < 1e-5

@@ -407,7 +407,7 @@ def test_compositing_results_do_not_depend_on_tile_order(device, tile_size, imag
         nat.check(nat.library().gs_composite(
             nat.ptr(records), records.shape[0], nat.ptr(sid_d), sid_d.numel(), nat.ptr(ranges_d),
             nat.ptr(order), v, nat.ptr(img2), nat.ptr(ft2), nat.ptr(nc2), None, 0,
-            nat.stream(device)), "composite")
+            None, 0, nat.stream(device)), "composite")
         torch.cuda.synchronize()
         # The wrapper's walk records checkpoints, which sums each pixel's
         # colour in segments (rounding of the order of the sums).
@@ -438,12 +438,32 @@ def test_compositing_results_do_not_depend_on_tile_order(device, tile_size, imag
     nat.check(nat.library().gs_composite_bwd(
         *(nat.ptr(t) for t in args), args[0].shape[0], nat.ptr(sid_d), nat.ptr(ranges_d), nat.ptr(g),
         nat.ptr(final_t), nat.ptr(ncon), None, view, nat.ptr(grad2), None, None, 0, 0,
-        nat.stream(device)), "composite_bwd")
+        None, 0, nat.stream(device)), "composite_bwd")
     torch.cuda.synchronize()
     # Float atomics make both sums order-dependent: compare against the scale
     # of each gradient column (a skipped or repeated tile would be O(1) off).
     scale = grad2.abs().amax(dim=0, keepdim=True).clamp_min(1e-30)
     assert float(((grad - grad2).abs() / scale).max()) < 1e-4
+    # The wrapper's backward walked the forward's hit masks; here a forward
+    # whose tiles all ran as quarters (each band's wave stops at its own
+    # pixels) writes them over a buffer of ones, and a backward of whole
+    # tiles reads them: only the words each band's wave wrote may count.
+    lib = nat.library()
+    words = lib.gs_composite_hit_mask_bytes(few, sid_d.numel()) // 8
+    hits = torch.full((words,), -1, dtype=torch.int64, device=device)
+    img3, ft3, nc3 = torch.empty_like(image), torch.empty_like(final_t), torch.empty_like(ncon)
+    nat.check(lib.gs_composite(
+        nat.ptr(records), records.shape[0], nat.ptr(sid_d), sid_d.numel(), nat.ptr(ranges_d), None,
+        few, nat.ptr(img3), nat.ptr(ft3), nat.ptr(nc3), None, 0, nat.ptr(hits), words * 8,
+        nat.stream(device)), "composite")
+    grad3 = torch.zeros_like(grad)
+    nat.check(lib.gs_composite_bwd(
+        *(nat.ptr(t) for t in args), args[0].shape[0], nat.ptr(sid_d), nat.ptr(ranges_d), nat.ptr(g),
+        nat.ptr(ft3), nat.ptr(nc3), None, view, nat.ptr(grad3), None, None, 0, sid_d.numel(),
+        nat.ptr(hits), words * 8, nat.stream(device)), "composite_bwd")
+    torch.cuda.synchronize()
+    assert torch.equal(final_t, ft3) and torch.equal(ncon, nc3)
+    assert float(((grad3 - grad2).abs() / scale).max()) < 1e-4
 
 
 def test_device_check_failures_reach_the_host(device):

@@ -32,8 +32,10 @@ VALU_CLOCK_HZ = 2.4e9  # MI355X peak engine clock
 # so its per-launch time excludes the host's launch latency after the idle
 # gap at the start of a step.
 PROJECT_HOLD_CYCLES = 250_000
-# The same spin between the stages of the staged steps (stage_marker).
-STAGE_HOLD_CYCLES = 250_000
+# The spin between the stages of the staged steps (stage_marker), about 250 us:
+# longer than the host's wait for the binning totals and the launches after
+# it, so no stage's time includes a host gap.
+STAGE_HOLD_CYCLES = 600_000
 
 
 def parse_args():

@@ -270,7 +270,7 @@ GS_API int gs_bin_gaussians(uint32_t* depth_keys, const int32_t* counts, int64_t
   clear(ws, s);
   // depth_keys is used as a ping-pong buffer by the sort and is consumed.
   uint32_t* sorted_keys = nullptr;
-  GS_TRY(radix_sort<uint32_t>(depth_keys, nullptr, n, 32, reinterpret_cast<uint32_t*>(order),
+  GS_TRY((radix_sort<uint32_t, true>)(depth_keys, nullptr, n, 32, reinterpret_cast<uint32_t*>(order),
                               &sorted_keys, ws, s));
   launch_scan<int64_t>(sweep::GatherLoad<int32_t, int64_t>{counts, order}, n, offsets, true,
                        aligned_16(order), ws, s);

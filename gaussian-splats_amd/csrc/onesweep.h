@@ -126,8 +126,12 @@ __global__ __launch_bounds__(kBlock) inline void clear_kernel(uint64_t* big, int
 // wave that share a digit are found with eight ballots and counted by one LDS
 // atomic from the lowest of them: keys that agree in a digit (the exponent
 // byte of depths in one octave, the all-ones key of culled Gaussians) would
-// otherwise serialise 64 same-address atomics per wave.
-template <typename K>
+// otherwise serialise 64 same-address atomics per wave.  SPREAD (depth keys:
+// the bits of positive floats, ~0 for culled Gaussians): only the last pass,
+// the exponent byte, takes the ballots; the lower passes' digits are mantissa
+// bytes, spread over the bins, and each lane adds its own with one LDS
+// atomic, except the all-ones keys, counted once per wave.
+template <typename K, bool SPREAD = false>
 __global__ __launch_bounds__(kBlock) void hist_kernel(const K* __restrict__ keys, int64_t n,
                                                       Plan plan, uint32_t* __restrict__ hist) {
   __shared__ uint32_t h[kMaxPasses * 256];
@@ -151,7 +155,18 @@ __global__ __launch_bounds__(kBlock) void hist_kernel(const K* __restrict__ keys
       const bool ok = i0 + u * stride < n;
       const uint64_t active = __ballot(ok);
       if (!active) continue;
-      for (int p = 0; p < plan.passes; ++p) {
+      int first_ballot_pass = 0;
+      if constexpr (SPREAD) {
+        const bool ones = k[u] == ~K(0);
+        const uint32_t n_ones = uint32_t(__popcll(__ballot(ok && ones)));
+        for (int p = 0; p + 1 < plan.passes; ++p) {
+          const uint32_t d = uint32_t(k[u] >> plan.shift[p]) & ((1u << plan.bits[p]) - 1u);
+          if (ok && !ones) atomicAdd(&h[p * 256 + d], 1u);
+          if (lane == 0 && n_ones) atomicAdd(&h[p * 256 + (1u << plan.bits[p]) - 1u], n_ones);
+        }
+        first_ballot_pass = plan.passes - 1;
+      }
+      for (int p = first_ballot_pass; p < plan.passes; ++p) {
         const uint32_t d = uint32_t(k[u] >> plan.shift[p]) & ((1u << plan.bits[p]) - 1u);
         // Active lanes with the same digit (digits have at most eight bits).
         uint64_t peers = active;

@@ -109,7 +109,8 @@ void dispatch_scatter(int bits, const K* kin, const uint32_t* vin, K* kout, uint
 // Sorts (keys, vals) on bits [0, end_bit) after `clear` has zeroed the scratch.
 // vals == nullptr means vals[i] = i.  Sorted values land in vals_final;
 // *keys_final points at the sorted keys (keys or the scratch copy).
-template <typename K>
+// SPREAD: the keys are depth keys (see hist_kernel).
+template <typename K, bool SPREAD = false>
 int radix_sort(K* keys, const uint32_t* vals, int64_t n, int end_bit, uint32_t* vals_final,
                K** keys_final, const Scratch& ws, hipStream_t s) {
   GS_REQUIRE(n < (int64_t(1) << 32) - kTile, GS_ERR_OVERFLOW, "too many elements to sort (%lld)",
@@ -118,7 +119,7 @@ int radix_sort(K* keys, const uint32_t* vals, int64_t n, int end_bit, uint32_t* 
   if (n == 0) return GS_OK;
   const sweep::Plan plan = sweep::make_plan(end_bit);
   const int hist_blocks = int(std::min<int64_t>(1024, ceil_div(n, kBlock * 16)));
-  sweep::hist_kernel<K><<<unsigned(hist_blocks), kBlock, 0, s>>>(keys, n, plan, ws.hist());
+  sweep::hist_kernel<K, SPREAD><<<unsigned(hist_blocks), kBlock, 0, s>>>(keys, n, plan, ws.hist());
   K* kbuf[2] = {static_cast<K*>(ws.keys_alt), keys};
   const K* kin = keys;
   const uint32_t* vin = vals;

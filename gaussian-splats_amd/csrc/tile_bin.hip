@@ -1145,7 +1145,7 @@ GS_API int gs_bin_tiles_plan(uint32_t* depth_keys, const int32_t* bounds, const 
     clear(ws, s);
     // depth_keys is consumed (ping-pong buffer of the sort).
     uint32_t* sorted_keys = nullptr;
-    status = radix_sort<uint32_t>(depth_keys, nullptr, n, 32,
+    status = radix_sort<uint32_t, true>(depth_keys, nullptr, n, 32,
                                   reinterpret_cast<uint32_t*>(p.order), &sorted_keys, ws, s);
     // Row-list offsets in depth order, recording each pass-A workgroup's
     // first owner; they read the packed rectangles written on the side stream.

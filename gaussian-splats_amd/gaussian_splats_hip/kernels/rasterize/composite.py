@@ -82,6 +82,11 @@ def composite(
     )
     checkpoints = nat.checkpoint_buffer(view, gaussian_ids.numel(), nat.longest_list(ranges_in),
                                         device)
+    if order is None and checkpoints is not None:
+        # Long lists (above 8192 entries): more tiles than resident waves, and
+        # the kernel's span is the longest walk, so the longest lists start
+        # first (config 4: 0.90 -> 0.83 ms).
+        order = nat.dispatch_plan(view, tiles_w * tiles_h, device, ranges=ranges)
     hits = (nat.hit_mask_buffer(view, gaussian_ids.numel(), device)
             if record_hits and rendering_mode == "gaussian" else None)
     nat.check(

@@ -173,12 +173,15 @@ def forward_views(
     )
     checkpoints = nat.checkpoint_buffer(view, gaussian_ids.numel(), nat.longest_list(ranges),
                                         device)
+    # With long lists the longest walks start first (as composite does).
+    plan = (nat.dispatch_plan(view, ranges.shape[0], device, ranges=ranges)
+            if checkpoints is not None else None)
     hits = (nat.hit_mask_buffer(view, gaussian_ids.numel(), device)
             if record_hits and rendering_mode == "gaussian" else None)
     nat.check(
         lib.gs_composite(
             ptr(records), records.shape[0], ptr(gaussian_ids), gaussian_ids.numel(), ptr(ranges),
-            None, view, ptr(image), ptr(final_transmittance), ptr(n_contributors),
+            ptr(plan), view, ptr(image), ptr(final_transmittance), ptr(n_contributors),
             ptr(checkpoints), nat.buffer_bytes(checkpoints), ptr(hits), nat.buffer_bytes(hits),
             stream,
         ),

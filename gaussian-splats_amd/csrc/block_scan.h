@@ -65,10 +65,10 @@ __device__ __forceinline__ T wave_sum(T v) {
   return v;
 }
 
-// Exclusive prefix over a 256-thread block (4 waves); returns the block total
-// through `total`.  `scratch` must hold 4 values and is reused after return.
-template <typename T>
-__device__ __forceinline__ T block_exclusive_scan(T v, T* scratch, T& total) {
+// Exclusive prefix over a block of NW waves; returns the block total through
+// `total`.  `scratch` must hold NW values and is reused after return.
+template <int NW, typename T>
+__device__ __forceinline__ T block_exclusive_scan_waves(T v, T* scratch, T& total) {
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
   const T inc = wave_inclusive_scan(v);
@@ -77,7 +77,7 @@ __device__ __forceinline__ T block_exclusive_scan(T v, T* scratch, T& total) {
   T before = 0;
   T sum = 0;
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {
+  for (int w = 0; w < NW; ++w) {
     const T s = scratch[w];
     if (w < wid) before += s;
     sum += s;
@@ -85,6 +85,12 @@ __device__ __forceinline__ T block_exclusive_scan(T v, T* scratch, T& total) {
   total = sum;
   __syncthreads();
   return inc - v + before;
+}
+
+// Four-wave workgroups (256 threads).
+template <typename T>
+__device__ __forceinline__ T block_exclusive_scan(T v, T* scratch, T& total) {
+  return block_exclusive_scan_waves<4>(v, scratch, total);
 }
 
 }  // namespace gs

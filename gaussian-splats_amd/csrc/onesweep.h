@@ -239,7 +239,8 @@ template <typename K, int BITS>
 __global__ __launch_bounds__(kBlock) void scatter_kernel(
     const K* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, K* __restrict__ keys_out,
     uint32_t* __restrict__ vals_out, int64_t n, int shift, const uint32_t* __restrict__ hist,
-    uint64_t* __restrict__ status, uint32_t* __restrict__ ticket, uint32_t* __restrict__ err) {
+    uint64_t* __restrict__ status, uint32_t* __restrict__ ticket, uint32_t* __restrict__ err,
+    const uint32_t* __restrict__ gather_src, uint32_t* __restrict__ gather_out) {
   constexpr int D = 1 << BITS;
   constexpr int kSeg = kTile / 4;  // contiguous elements per wave
   __shared__ uint32_t cnt[4][D];
@@ -340,6 +341,9 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
     const uint32_t o = gofs[d] + uint32_t(j);
     keys_out[o] = k;
     vals_out[o] = svals[j];
+    // gather_out[o] = gather_src[value]: a payload of each element in the
+    // sorted order (the last pass only).
+    if (gather_out) gather_out[o] = gather_src[svals[j]];
   }
 }
 

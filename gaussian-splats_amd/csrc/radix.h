@@ -84,35 +84,41 @@ inline void clear(const Scratch& s, hipStream_t stream) {
 template <typename K, int BITS>
 void launch_scatter(const K* kin, const uint32_t* vin, K* kout, uint32_t* vout, int64_t n,
                     int shift, const uint32_t* hist, uint64_t* status, uint32_t* ticket,
-                    uint32_t* err, hipStream_t s) {
+                    uint32_t* err, const uint32_t* gsrc, uint32_t* gout, hipStream_t s) {
   const unsigned nblocks = unsigned(ceil_div(n, kTile));
-  sweep::scatter_kernel<K, BITS><<<nblocks, sweep::kBlock, 0, s>>>(kin, vin, kout, vout, n, shift,
-                                                                   hist, status, ticket, err);
+  sweep::scatter_kernel<K, BITS><<<nblocks, sweep::kBlock, 0, s>>>(
+      kin, vin, kout, vout, n, shift, hist, status, ticket, err, gsrc, gout);
 }
 
 template <typename K>
 void dispatch_scatter(int bits, const K* kin, const uint32_t* vin, K* kout, uint32_t* vout,
                       int64_t n, int shift, const uint32_t* hist, uint64_t* status,
-                      uint32_t* ticket, uint32_t* err, hipStream_t s) {
+                      uint32_t* ticket, uint32_t* err, const uint32_t* gsrc, uint32_t* gout,
+                      hipStream_t s) {
   switch (bits) {
-    case 1: launch_scatter<K, 1>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, s); break;
-    case 2: launch_scatter<K, 2>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, s); break;
-    case 3: launch_scatter<K, 3>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, s); break;
-    case 4: launch_scatter<K, 4>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, s); break;
-    case 5: launch_scatter<K, 5>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, s); break;
-    case 6: launch_scatter<K, 6>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, s); break;
-    case 7: launch_scatter<K, 7>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, s); break;
-    default: launch_scatter<K, 8>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, s); break;
+    case 1: launch_scatter<K, 1>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, gsrc, gout, s); break;
+    case 2: launch_scatter<K, 2>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, gsrc, gout, s); break;
+    case 3: launch_scatter<K, 3>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, gsrc, gout, s); break;
+    case 4: launch_scatter<K, 4>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, gsrc, gout, s); break;
+    case 5: launch_scatter<K, 5>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, gsrc, gout, s); break;
+    case 6: launch_scatter<K, 6>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, gsrc, gout, s); break;
+    case 7: launch_scatter<K, 7>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, gsrc, gout, s); break;
+    default: launch_scatter<K, 8>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, gsrc, gout, s); break;
   }
 }
 
 // Sorts (keys, vals) on bits [0, end_bit) after `clear` has zeroed the scratch.
 // vals == nullptr means vals[i] = i.  Sorted values land in vals_final;
 // *keys_final points at the sorted keys (keys or the scratch copy).
-// SPREAD: the keys are depth keys (see hist_kernel).
+// SPREAD: the keys are depth keys (see hist_kernel).  gather_out (optional):
+// the last pass also writes gather_out[i] = gather_src[vals_final[i]], after
+// `stream` has waited for `gather_ready` (an event that gather_src's producer
+// recorded before this call), so the earlier passes do not wait for it.
 template <typename K, bool SPREAD = false>
 int radix_sort(K* keys, const uint32_t* vals, int64_t n, int end_bit, uint32_t* vals_final,
-               K** keys_final, const Scratch& ws, hipStream_t s) {
+               K** keys_final, const Scratch& ws, hipStream_t s,
+               const uint32_t* gather_src = nullptr, uint32_t* gather_out = nullptr,
+               hipEvent_t gather_ready = nullptr) {
   GS_REQUIRE(n < (int64_t(1) << 32) - kTile, GS_ERR_OVERFLOW, "too many elements to sort (%lld)",
              (long long)n);
   *keys_final = keys;
@@ -128,8 +134,15 @@ int radix_sort(K* keys, const uint32_t* vals, int64_t n, int end_bit, uint32_t* 
   for (int pass = 0; pass < plan.passes; ++pass) {
     K* kout = kbuf[pass & 1];
     uint32_t* vout = (pass == plan.passes - 1) ? vals_final : ws.vbuf[pass & 1];
+    const bool last = pass == plan.passes - 1;
+    if (last && gather_out && gather_ready &&
+        hipStreamWaitEvent(s, gather_ready, 0) != hipSuccess) {
+      set_error("radix_sort: stream wait failed");
+      return GS_ERR_HIP;
+    }
     dispatch_scatter<K>(plan.bits[pass], kin, vin, kout, vout, n, plan.shift[pass],
-                        ws.hist() + pass * 256, status, ws.tickets() + pass, ws.flags, s);
+                        ws.hist() + pass * 256, status, ws.tickets() + pass, ws.flags,
+                        last ? gather_src : nullptr, last ? gather_out : nullptr, s);
     status += nblocks << plan.bits[pass];
     kin = kout;
     vin = vout;

@@ -363,18 +363,18 @@ __device__ __forceinline__ uint32_t entry_width(uint32_t xw) { return ((xw >> 8)
 __device__ __forceinline__ uint32_t entry_row(uint32_t xw) { return (xw >> 16) & 0xFFu; }
 
 // Row-list entries per Gaussian in depth order: its tile-row count, 0 if it
-// has no intersections.
+// has no intersections (from the rectangles the depth sort wrote in depth
+// order: contiguous reads).
 struct HeightLoad {
-  const uint32_t* packed;
-  const int32_t* order;
+  const uint32_t* packed_sorted;
   __device__ static uint32_t height(uint32_t r) { return r == kNoRect ? 0u : (r >> 24) + 1u; }
-  __device__ uint32_t operator()(int64_t i) const { return height(packed[order[i]]); }
+  __device__ uint32_t operator()(int64_t i) const { return height(packed_sorted[i]); }
   __device__ void load4(int64_t i, uint32_t (&v)[4]) const {
-    const int4 o = *reinterpret_cast<const int4*>(order + i);
-    v[0] = height(packed[o.x]);
-    v[1] = height(packed[o.y]);
-    v[2] = height(packed[o.z]);
-    v[3] = height(packed[o.w]);
+    const uint4 r = *reinterpret_cast<const uint4*>(packed_sorted + i);
+    v[0] = height(r.x);
+    v[1] = height(r.y);
+    v[2] = height(r.z);
+    v[3] = height(r.w);
   }
 };
 
@@ -653,11 +653,11 @@ __device__ int load_window(const uint32_t* __restrict__ offs, int64_t first, int
 // covered tile row), bucketed by tile row.  The first owner comes from
 // first_a (recorded by the height scan), the last one from the next
 // workgroup's first owner (a search for the final workgroup).  Reads the
-// packed rectangles; writes each entry's Gaussian id and packed first column /
-// width / row.
+// packed rectangles in depth order; writes each entry's Gaussian id and
+// packed first column / width / row.
 template <int BITS>
 __global__ __launch_bounds__(kBlock) void row_bucket_kernel(
-    const uint32_t* __restrict__ packed, const int32_t* __restrict__ order,
+    const uint32_t* __restrict__ packed_sorted, const int32_t* __restrict__ order,
     const uint32_t* __restrict__ offs, const uint32_t* __restrict__ first_a, int64_t n,
     uint32_t entries, int th, const uint32_t* __restrict__ row_a,
     const int64_t* __restrict__ totals, uint32_t* __restrict__ out_g,
@@ -699,9 +699,9 @@ __global__ __launch_bounds__(kBlock) void row_bucket_kernel(
   uint32_t dig[kItems];
   uint32_t val[2][kItems];
   // Every position has an owner in [0, m) (the running maximum starts at 0),
-  // so all gathers are in bounds: they are issued unconditionally, all
-  // kItems order reads first, then all rectangle reads, so each round of
-  // dependent loads is one round trip for the whole thread.
+  // so all gathers are in bounds: they are issued unconditionally and
+  // together (the ids and the rectangles are both in depth order: one round
+  // trip for the whole thread).
   int kk[kItems];
   int g[kItems];
   uint32_t r[kItems];
@@ -709,9 +709,8 @@ __global__ __launch_bounds__(kBlock) void row_bucket_kernel(
   for (int i = 0; i < kItems; ++i) {
     kk[i] = sh.own[wid * kSeg + i * 64 + lane];
     g[i] = order[p_first + kk[i]];
+    r[i] = packed_sorted[p_first + kk[i]];
   }
-#pragma unroll
-  for (int i = 0; i < kItems; ++i) r[i] = packed[g[i]];
 #pragma unroll
   for (int i = 0; i < kItems; ++i) {
     const int e = wid * kSeg + i * 64 + lane;
@@ -936,12 +935,12 @@ __global__ __launch_bounds__(kBlock) void column_bucket_kernel(
 }
 
 template <int BITS>
-void launch_row_bucket(unsigned blocks, const uint32_t* packed, const int32_t* order,
+void launch_row_bucket(unsigned blocks, const uint32_t* packed_sorted, const int32_t* order,
                        const uint32_t* offs, const uint32_t* first_a, int64_t n, uint32_t entries,
                        int th, const uint32_t* row_a, const int64_t* totals, uint32_t* out_g,
                        uint32_t* out_xw, uint64_t* status, uint32_t* ticket, uint32_t* err,
                        hipStream_t s) {
-  row_bucket_kernel<BITS><<<blocks, kBlock, 0, s>>>(packed, order, offs, first_a, n, entries, th,
+  row_bucket_kernel<BITS><<<blocks, kBlock, 0, s>>>(packed_sorted, order, offs, first_a, n, entries, th,
                                                     row_a, totals, out_g, out_xw, status, ticket,
                                                     err);
 }
@@ -967,6 +966,7 @@ int axis_bits(int tiles) { return std::max(1, bits_for(tiles)); }
 struct PlanLayout {
   int32_t* order = nullptr;    // [n] depth order
   uint32_t* packed = nullptr;  // [n] packed tile rectangles (pack_rect)
+  uint32_t* packed_sorted = nullptr;  // [n] the same in depth order (the sort's last pass)
   uint32_t* offs = nullptr;    // [n + 1] row-list offsets in depth order (written by emit)
   uint32_t* row_a = nullptr;   // [th + 1]
   uint32_t* row_e = nullptr;   // [th + 1]
@@ -990,6 +990,7 @@ PlanLayout plan_layout(void* base, int64_t n, int tw, int th) {
   };
   p.order = reinterpret_cast<int32_t*>(take(size_t(n) * 4));
   p.packed = reinterpret_cast<uint32_t*>(take(size_t(n) * 4));
+  p.packed_sorted = reinterpret_cast<uint32_t*>(take(size_t(n) * 4));
   p.offs = reinterpret_cast<uint32_t*>(take(size_t(n + 1) * 4));
   p.row_a = reinterpret_cast<uint32_t*>(take(size_t(th + 1) * 4));
   p.row_e = reinterpret_cast<uint32_t*>(take(size_t(th + 1) * 4));
@@ -1149,13 +1150,16 @@ GS_API int gs_bin_tiles_plan(uint32_t* depth_keys, const int32_t* bounds, const 
     clear(ws, s);
     // depth_keys is consumed (ping-pong buffer of the sort).
     uint32_t* sorted_keys = nullptr;
+    // Its last pass also writes the rectangles in depth order, once the side
+    // stream has written them (mark above).
     status = radix_sort<uint32_t, true>(depth_keys, nullptr, n, 32,
-                                  reinterpret_cast<uint32_t*>(p.order), &sorted_keys, ws, s);
+                                        reinterpret_cast<uint32_t*>(p.order), &sorted_keys, ws, s,
+                                        p.packed, p.packed_sorted, fork.mark);
     // Row-list offsets in depth order, recording each pass-A workgroup's
     // first owner; they read the packed rectangles written on the side stream.
     if (status == GS_OK) status = wait_side_mark(fork);
     if (status == GS_OK)
-      launch_scan<uint32_t>(HeightLoad{p.packed, p.order}, n, p.offs, true, true, ws, s,
+      launch_scan<uint32_t>(HeightLoad{p.packed_sorted}, n, p.offs, true, true, ws, s,
                             HeightSink{p.first_a, p.first_a_capacity});
   }
   // Always join, also after an error; with host_totals the host waits for
@@ -1209,7 +1213,7 @@ GS_API int gs_bin_tiles_emit(int64_t n,
   switch (axis_bits(tiles_h)) {
 #define GS_ROW_CASE(B)                                                                          \
   case B:                                                                                       \
-    launch_row_bucket<B>(blocks_a, p.packed, p.order, p.offs, p.first_a, n,                     \
+    launch_row_bucket<B>(blocks_a, p.packed_sorted, p.order, p.offs, p.first_a, n,              \
                          uint32_t(row_entries),                                                 \
                          tiles_h, p.row_a, totals, e.rl_g, e.rl_xw, e.status_a, ticket_a, err,  \
                          s);                                                                    \

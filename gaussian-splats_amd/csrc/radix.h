@@ -95,16 +95,20 @@ void dispatch_scatter(int bits, const K* kin, const uint32_t* vin, K* kout, uint
                       int64_t n, int shift, const uint32_t* hist, uint64_t* status,
                       uint32_t* ticket, uint32_t* err, const uint32_t* gsrc, uint32_t* gout,
                       hipStream_t s) {
+  // One launch per digit width (the kernel's template argument).
+#define GS_SCATTER(B)                                                                            \
+  launch_scatter<K, B>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, gsrc, gout, s)
   switch (bits) {
-    case 1: launch_scatter<K, 1>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, gsrc, gout, s); break;
-    case 2: launch_scatter<K, 2>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, gsrc, gout, s); break;
-    case 3: launch_scatter<K, 3>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, gsrc, gout, s); break;
-    case 4: launch_scatter<K, 4>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, gsrc, gout, s); break;
-    case 5: launch_scatter<K, 5>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, gsrc, gout, s); break;
-    case 6: launch_scatter<K, 6>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, gsrc, gout, s); break;
-    case 7: launch_scatter<K, 7>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, gsrc, gout, s); break;
-    default: launch_scatter<K, 8>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, gsrc, gout, s); break;
+    case 1: GS_SCATTER(1); break;
+    case 2: GS_SCATTER(2); break;
+    case 3: GS_SCATTER(3); break;
+    case 4: GS_SCATTER(4); break;
+    case 5: GS_SCATTER(5); break;
+    case 6: GS_SCATTER(6); break;
+    case 7: GS_SCATTER(7); break;
+    default: GS_SCATTER(8); break;
   }
+#undef GS_SCATTER
 }
 
 // Sorts (keys, vals) on bits [0, end_bit) after `clear` has zeroed the scratch.

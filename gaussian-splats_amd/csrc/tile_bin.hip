@@ -300,8 +300,10 @@ __global__ __launch_bounds__(NT) void tables_kernel(int32_t* __restrict__ diff2,
   int64_t tot_e, tot_c, tot_a, tot_b;
   const int64_t e_start = block_exclusive_scan_waves<NW>(row_entries, scratch, tot_e);
   const int64_t rd = y < th ? int64_t(rowdiff[y]) : 0;
-  const int64_t cover = block_exclusive_scan_waves<NW>(rd, scratch, tot_c) + rd;  // Gaussians on row y
-  const int64_t a_start = block_exclusive_scan_waves<NW>(y < th ? cover : int64_t(0), scratch, tot_a);
+  // Gaussians on row y.
+  const int64_t cover = block_exclusive_scan_waves<NW>(rd, scratch, tot_c) + rd;
+  const int64_t a_start =
+      block_exclusive_scan_waves<NW>(y < th ? cover : int64_t(0), scratch, tot_a);
   const int64_t blocks = (row_entries + kTile - 1) / kTile;
   const int64_t b_start = block_exclusive_scan_waves<NW>(blocks, scratch, tot_b);
   if (y < th) {
@@ -940,9 +942,9 @@ void launch_row_bucket(unsigned blocks, const uint32_t* packed_sorted, const int
                        int th, const uint32_t* row_a, const int64_t* totals, uint32_t* out_g,
                        uint32_t* out_xw, uint64_t* status, uint32_t* ticket, uint32_t* err,
                        hipStream_t s) {
-  row_bucket_kernel<BITS><<<blocks, kBlock, 0, s>>>(packed_sorted, order, offs, first_a, n, entries, th,
-                                                    row_a, totals, out_g, out_xw, status, ticket,
-                                                    err);
+  row_bucket_kernel<BITS><<<blocks, kBlock, 0, s>>>(packed_sorted, order, offs, first_a, n,
+                                                    entries, th, row_a, totals, out_g, out_xw,
+                                                    status, ticket, err);
 }
 
 template <int BITS>

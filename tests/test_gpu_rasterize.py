@@ -239,8 +239,26 @@ def test_composite_backward_segmented_walks(device, entries):
     # checkpoints (position 1024 of the list and its batch).
     f32 = lambda x: x.detach().float().contiguous().to(device)
     gids, granges = torch.as_tensor(sid).to(device), torch.as_tensor(ranges).to(device)
-    _, final_t, ncon = composite(f32(pmean), f32(pinv), f32(pcol), f32(pop), gids, granges,
-                                 w, h, ts, THRESHOLD, "gaussian", 0.95)
+    image, final_t, ncon = composite(f32(pmean), f32(pinv), f32(pcol), f32(pop), gids, granges,
+                                     w, h, ts, THRESHOLD, "gaussian", 0.95)
+    # That forward took the long-list kernel (plan by list length, checkpoints,
+    # records requested a batch ahead); the plain kernel in index order gives
+    # the same transmittance and contributor counts, and the image up to the
+    # order of the colour sums (the checkpoints sum each pixel's colour in
+    # segments).
+    from gaussian_splats_hip.kernels.rasterize.project import pack_records
+
+    records = pack_records(f32(pmean), f32(pinv), f32(pcol), f32(pop), "gaussian", 0.95)
+    img2, ft2, nc2 = torch.empty_like(image), torch.empty_like(final_t), torch.empty_like(ncon)
+    plain = nat.make_view(1.0, 1.0, 0.0, 0.0, w, h, ts, opacity_threshold=THRESHOLD)
+    ids32 = gids.to(torch.int32).contiguous()
+    nat.check(nat.library().gs_composite(
+        nat.ptr(records), records.shape[0], nat.ptr(ids32), ids32.numel(), nat.ptr(granges), None,
+        plain, nat.ptr(img2), nat.ptr(ft2), nat.ptr(nc2), None, 0, None, 0, nat.stream(device)),
+        "composite")
+    torch.cuda.synchronize()
+    assert torch.equal(final_t, ft2) and torch.equal(ncon, nc2)
+    assert float((image - img2).abs().max()) <= 1e-5
     plan = tile_order(granges, ncon, w, h, ts).cpu().numpy()
     segmented = set((plan[(plan >= 0) & ((plan & 0x40) != 0)] >> 7).tolist())
     assert {0, 8} <= segmented, segmented

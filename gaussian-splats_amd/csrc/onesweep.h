@@ -213,13 +213,23 @@ __device__ __forceinline__ void rank_items(const uint32_t* digits, int n_valid_f
 #pragma unroll
     for (int bit = 0; bit < BITS; ++bit) {
       m[bit] = uint32_t(int32_t(d << (31 - bit)) >> 31);  // v_bfe_i32: 0 or all ones
+      // Opaque, so that the ballot compares m itself (one instruction) rather
+      // than shifting the digit again for a sign test.
+      asm("" : "+v"(m[bit]));
       ones[bit] = __ballot(m[bit] != 0u);
     }
+    // Lanes whose digit differs from this lane's in some bit: the OR over the
+    // bits of (lanes with the bit set) ^ (this lane's bit), one v_bitop3_b32
+    // per bit and half (truth table 0xF6: src0 | (src1 ^ src2)).
+    uint32_t xlo = uint32_t(ones[0]) ^ m[0];
+    uint32_t xhi = uint32_t(ones[0] >> 32) ^ m[0];
 #pragma unroll
-    for (int bit = 0; bit < BITS; ++bit) {
-      plo &= ~(uint32_t(ones[bit]) ^ m[bit]);
-      phi &= ~(uint32_t(ones[bit] >> 32) ^ m[bit]);
+    for (int bit = 1; bit < BITS; ++bit) {
+      xlo = __builtin_amdgcn_bitop3_b32(xlo, uint32_t(ones[bit]), m[bit], 0xF6);
+      xhi = __builtin_amdgcn_bitop3_b32(xhi, uint32_t(ones[bit] >> 32), m[bit], 0xF6);
     }
+    plo &= ~xlo;
+    phi &= ~xhi;
     const uint32_t before = __builtin_amdgcn_mbcnt_hi(phi, __builtin_amdgcn_mbcnt_lo(plo, 0u));
     const uint32_t total = uint32_t(__popc(plo) + __popc(phi));
     uint32_t c = 0;

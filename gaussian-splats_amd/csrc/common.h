@@ -108,23 +108,35 @@ inline int checkpoint_pixels(int tile_size) {
   return tile_size * tile_size >= 64 ? tile_size * tile_size : 64;
 }
 
-// Layout of the checkpoint workspace: a counter, the table, the records.
+// Layout of the checkpoint workspace: a 256-byte header block (the pool
+// counter, then the stamp), the table, the records.  The records fill what
+// the caller's buffer holds beyond the header and table, up to one per table
+// slot and kCheckpointPoolBytes: a smaller buffer holds fewer records, and the
+// crossings beyond them are recorded as missing (-1).
 struct CheckpointLayout {
   uint32_t* counter = nullptr;
+  uint32_t* stamp = nullptr;  // kCheckpointStampWords words after the counter
   int32_t* table = nullptr;
   float4* records = nullptr;
   int64_t table_len = 0;
-  int64_t capacity = 0;  // records
-  size_t bytes = 0;
+  int64_t capacity = 0;     // records
+  size_t header_bytes = 0;  // header block + table: the least a buffer must hold
+  size_t bytes = 0;         // header + records
 };
-inline CheckpointLayout checkpoint_layout(void* base, int tile_size, int64_t total) {
+// The stamp says which walk wrote the table: the forward writes it with its
+// pool counter before the walk (or clears it when it records nothing into a
+// buffer it is given), and the backward trusts the table only when the stamp
+// matches its own view.  It cannot tell two walks of one geometry apart: the
+// buffer must come from the forward over the same lists.
+constexpr uint32_t kCheckpointMagic = 0x70636773u;  // "sgcp"
+constexpr int kCheckpointStampWords = 4;  // magic, tile size, tiles, table length
+inline CheckpointLayout checkpoint_layout(void* base, int tile_size, int64_t total,
+                                          size_t available = ~size_t(0)) {
   CheckpointLayout c;
   const size_t record = size_t(checkpoint_pixels(tile_size)) * 16;
   // A crossing's position lies below the list end + 64 (its batch starts
   // inside the list): table slots up to (total + 63) / kCheckpointEntries.
   c.table_len = total / kCheckpointEntries + 2;
-  const int64_t most = c.table_len;  // one record per table slot at most
-  c.capacity = std::min<int64_t>(most, int64_t(kCheckpointPoolBytes / record));
   char* p = static_cast<char*>(base);
   size_t off = 0;
   auto take = [&](size_t n) {
@@ -132,8 +144,14 @@ inline CheckpointLayout checkpoint_layout(void* base, int tile_size, int64_t tot
     off += (n + 255) / 256 * 256;
     return r;
   };
-  c.counter = reinterpret_cast<uint32_t*>(take(4));
+  c.counter = reinterpret_cast<uint32_t*>(take(4 * (1 + kCheckpointStampWords)));
+  c.stamp = c.counter ? c.counter + 1 : nullptr;
   c.table = reinterpret_cast<int32_t*>(take(size_t(c.table_len) * 4));
+  c.header_bytes = off;
+  const int64_t most = c.table_len;  // one record per table slot at most
+  const int64_t room = available > off ? int64_t((available - off) / record) : 0;
+  c.capacity = std::min<int64_t>(std::min<int64_t>(most, int64_t(kCheckpointPoolBytes / record)),
+                                 room);
   c.records = reinterpret_cast<float4*>(take(size_t(c.capacity) * record));
   c.bytes = off;
   return c;

@@ -47,10 +47,13 @@ struct CompositeBwdArgs {
   int view_tw, view_th, cols, views;  // tiles per view, mosaic layout (one view: cols = views = 1)
   float* grad;      // [N, 9]
   float* grad_abs;  // [N, 2]: sums of |per-pixel mean gradient| (ABS kernels only)
-  // The forward's checkpoints (CheckpointLayout), or null table: none.
+  // The forward's checkpoints (CheckpointLayout), or null table: none.  The
+  // table is used only when the forward's stamp matches this view.
   const int32_t* ckpt_table;
   const float4* ckpt_records;
   int64_t ckpt_capacity;
+  const uint32_t* ckpt_stamp;
+  uint32_t ckpt_table_len;
   // The forward's hit masks (hit_mask_slot), read by the MASKS kernels.
   const uint64_t* hit_masks;
   int64_t hit_capacity;  // words
@@ -133,8 +136,10 @@ __device__ __forceinline__ void composite_bwd_tile(const CompositeBwdArgs& a, fl
   if (seg >= 0) {
     // Recorded checkpoints: a prefix of the tile's crossings (lane j reads
     // the table slot of crossing j + 1).
-    const int m =
-        a.ckpt_table ? checkpoint_count(start, max_n, a.ranges[2 * tile + 1] - start) : 0;
+    const bool table =
+        a.ckpt_table && a.ckpt_stamp[0] == kCheckpointMagic && a.ckpt_stamp[1] == uint32_t(TILE) &&
+        a.ckpt_stamp[2] == uint32_t(a.num_tiles) && a.ckpt_stamp[3] == a.ckpt_table_len;
+    const int m = table ? checkpoint_count(start, max_n, a.ranges[2 * tile + 1] - start) : 0;
     const int64_t first = checkpoint_first(start);
     const int slot = lane < m ? a.ckpt_table[(first + int64_t(lane) * kCheckpointEntries) /
                                              kCheckpointEntries]
@@ -472,15 +477,24 @@ extern "C" GS_API int gs_composite_bwd(const float* projected_mean,
                "hit masks must be 8-byte aligned");
     a.hit_capacity = words;
   }
-  if (checkpoints && !plan.split_all) {
+  a.ckpt_stamp = nullptr;
+  a.ckpt_table_len = 0;
+  // The forward records checkpoints under these conditions only
+  // (composite_fwd.hip); its stamp is checked on the device as well.
+  if (checkpoints && !plan.split_all && view.tile_size <= 16 && n > 0) {
     GS_REQUIRE(num_intersections >= 0, GS_ERR_INVALID_ARGUMENT, "negative intersection count");
     const CheckpointLayout c = checkpoint_layout(const_cast<void*>(checkpoints), view.tile_size,
-                                                 num_intersections);
-    GS_REQUIRE(checkpoint_bytes >= c.bytes, GS_ERR_WORKSPACE,
-               "checkpoint buffer too small (%zu bytes, need %zu)", checkpoint_bytes, c.bytes);
+                                                 num_intersections, checkpoint_bytes);
+    GS_REQUIRE(checkpoint_bytes >= c.header_bytes, GS_ERR_WORKSPACE,
+               "checkpoint buffer too small (%zu bytes, need at least %zu)", checkpoint_bytes,
+               c.header_bytes);
+    GS_REQUIRE((reinterpret_cast<uintptr_t>(checkpoints) & 255u) == 0, GS_ERR_INVALID_ARGUMENT,
+               "checkpoint buffer must be 256-byte aligned");
     a.ckpt_table = c.table;
     a.ckpt_records = c.records;
     a.ckpt_capacity = c.capacity;
+    a.ckpt_stamp = c.stamp;
+    a.ckpt_table_len = uint32_t(c.table_len);
   }
   hipStream_t s = as_stream(stream);
   switch (view.tile_size) {

@@ -360,7 +360,16 @@ void launch(const CompositeArgs& a, bool ellipsoid, hipStream_t s) {
 
 using namespace gs;
 
-__global__ void checkpoint_clear_kernel(uint32_t* counter) { *counter = 0u; }
+// Resets the pool counter and stamps the table with the walk's geometry
+// (magic 0 when the walk records nothing into this buffer).
+__global__ void checkpoint_clear_kernel(uint32_t* counter, uint32_t magic, uint32_t tile_size,
+                                        uint32_t num_tiles, uint32_t table_len) {
+  counter[0] = 0u;
+  counter[1] = magic;
+  counter[2] = tile_size;
+  counter[3] = num_tiles;
+  counter[4] = table_len;
+}
 
 extern "C" GS_API size_t gs_composite_checkpoint_bytes(gs_view view, int64_t num_intersections,
                                                        int64_t longest_list) {
@@ -437,17 +446,27 @@ extern "C" GS_API int gs_composite(const void* records, int64_t num_records,
     a.hit_capacity = words;
   }
   hipStream_t s = as_stream(stream);
-  if (checkpoints && !plan.split_all && view.tile_size <= 16 && num_records > 0) {
-    const CheckpointLayout c = checkpoint_layout(checkpoints, view.tile_size, num_intersections);
-    GS_REQUIRE(checkpoint_bytes >= c.bytes, GS_ERR_WORKSPACE,
-               "checkpoint buffer too small (%zu bytes, need %zu)", checkpoint_bytes, c.bytes);
+  if (checkpoints) {
+    const CheckpointLayout c =
+        checkpoint_layout(checkpoints, view.tile_size, num_intersections, checkpoint_bytes);
+    GS_REQUIRE(checkpoint_bytes >= c.header_bytes, GS_ERR_WORKSPACE,
+               "checkpoint buffer too small (%zu bytes, need at least %zu)", checkpoint_bytes,
+               c.header_bytes);
     GS_REQUIRE((reinterpret_cast<uintptr_t>(checkpoints) & 255u) == 0, GS_ERR_INVALID_ARGUMENT,
                "checkpoint buffer must be 256-byte aligned");
-    a.ckpt_counter = c.counter;
-    a.ckpt_table = c.table;
-    a.ckpt_records = c.records;
-    a.ckpt_capacity = c.capacity;
-    checkpoint_clear_kernel<<<1, 1, 0, s>>>(c.counter);
+    // The walk records checkpoints only in whole-tile waves of at most 16
+    // pixels per lane; otherwise the stamp tells a backward that the table
+    // holds nothing.
+    const bool record = !plan.split_all && view.tile_size <= 16 && num_records > 0;
+    if (record) {
+      a.ckpt_counter = c.counter;
+      a.ckpt_table = c.table;
+      a.ckpt_records = c.records;
+      a.ckpt_capacity = c.capacity;
+    }
+    checkpoint_clear_kernel<<<1, 1, 0, s>>>(c.counter, record ? kCheckpointMagic : 0u,
+                                            uint32_t(view.tile_size), uint32_t(a.num_tiles),
+                                            uint32_t(c.table_len));
     GS_TRY(check_launch("composite checkpoints"));
   }
   const bool ellipsoid = view.rendering_mode == GS_MODE_ELLIPSOID;

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parents[2] / "_lib" / "libgs_raster.so"
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 GS_OK = 0
 GS_ERR_INVALID_ARGUMENT = 1
@@ -124,18 +124,47 @@ def longest_list(ranges: torch.Tensor) -> int:
     return int(value)
 
 
-_CHECKPOINT_ATTR = "_gs_checkpoints"
+_WALK_ATTR = "_gs_walk_state"
 
 
-def set_checkpoints(ranges: torch.Tensor, buffer: torch.Tensor | None) -> None:
-    """Records on ``ranges`` the forward's checkpoint buffer (gs_composite)
-    for the backward of the same lists."""
-    setattr(ranges, _CHECKPOINT_ATTR, buffer)
+def _stamp(t):
+    """A tensor's identity as a kernel read it: storage address, in-place
+    version counter, shape and dtype."""
+    if t is None:
+        return None
+    return (t.data_ptr(), t._version, tuple(t.shape), t.dtype)
 
 
-def checkpoints(ranges: torch.Tensor | None) -> torch.Tensor | None:
-    """The buffer recorded by ``set_checkpoints``, or None."""
-    return getattr(ranges, _CHECKPOINT_ATTR, None) if ranges is not None else None
+def walk_fingerprint(key: tuple, *tensors) -> tuple:
+    """Fingerprint of one compositing walk: the view parameters in ``key``
+    and the identity of every tensor the walk read or wrote.  gs_composite's
+    checkpoints and hit masks are valid for a backward only when its
+    arguments have the same fingerprint."""
+    return (tuple(key),) + tuple(_stamp(t) for t in tensors)
+
+
+def set_walk_state(n_contributors: torch.Tensor, fingerprint: tuple | None,
+                   checkpoints: torch.Tensor | None, hits: torch.Tensor | None) -> None:
+    """Records on the forward's own ``n_contributors`` output the checkpoint
+    and hit-mask buffers gs_composite wrote, with the fingerprint of that
+    call (``None`` for the op's outputs, which are consumed together)."""
+    setattr(n_contributors, _WALK_ATTR, (fingerprint, checkpoints, hits))
+
+
+def walk_buffers(n_contributors: torch.Tensor | None, fingerprint: tuple | None = None):
+    """``(checkpoints, hit_masks)`` recorded with ``n_contributors``, or
+    ``(None, None)``.  With a ``fingerprint``, only when it equals the one
+    recorded: a backward whose arguments are not exactly the forward's
+    (another projection, lists changed in place, another threshold) walks
+    every entry from the list's end.  That keeps it a pure function of its
+    arguments."""
+    state = getattr(n_contributors, _WALK_ATTR, None) if n_contributors is not None else None
+    if state is None:
+        return None, None
+    recorded, checkpoints, hits = state
+    if fingerprint is not None and recorded != fingerprint:
+        return None, None
+    return checkpoints, hits
 
 
 def checkpoint_buffer(view: GsView, num_intersections: int, longest: int,
@@ -149,20 +178,6 @@ def checkpoint_buffer(view: GsView, num_intersections: int, longest: int,
     buf = torch.empty(nbytes + 256, dtype=torch.uint8, device=device)
     off = (-buf.data_ptr()) % 256
     return buf[off:off + nbytes]
-
-
-_HIT_MASK_ATTR = "_gs_hit_masks"
-
-
-def set_hit_masks(ranges: torch.Tensor, buffer: torch.Tensor | None) -> None:
-    """Records on ``ranges`` the hit masks the forward wrote for its lists
-    (gs_composite), for the compositing backward of the same lists."""
-    setattr(ranges, _HIT_MASK_ATTR, buffer)
-
-
-def hit_masks(ranges: torch.Tensor | None) -> torch.Tensor | None:
-    """The buffer recorded by ``set_hit_masks``, or None."""
-    return getattr(ranges, _HIT_MASK_ATTR, None) if ranges is not None else None
 
 
 def hit_mask_buffer(view: GsView, num_intersections: int, device: torch.device) -> torch.Tensor:

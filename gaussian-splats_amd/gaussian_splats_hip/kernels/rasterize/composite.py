@@ -61,7 +61,9 @@ def composite(
     """Composites the sorted per-tile lists; returns ``(image[H,W,3],
     final_transmittance[H,W], n_contributors[H,W] int32)``.  The walk's
     checkpoints and (``record_hits``, Gaussian mode) hit masks (gs_composite)
-    are recorded on ``ranges`` for the backward."""
+    are recorded on the returned ``n_contributors`` with a fingerprint of
+    this call's arguments; ``composite_bwd`` uses them only when its own
+    arguments carry the same fingerprint."""
     _check_tile(tile_size)
     device = nat.require_gpu(mean, gaussian_ids, ranges)
     if records is None:
@@ -70,7 +72,7 @@ def composite(
     if ranges.shape != (tiles_w * tiles_h, 2):
         raise ValueError(f"ranges must be [{tiles_w * tiles_h}, 2], got {tuple(ranges.shape)}")
     active = nat.active_tiles(ranges)
-    ranges_in = ranges
+    ranges_in, gaussian_ids_in = ranges, gaussian_ids
     ranges = nat.prepare(ranges, torch.int64)
     gaussian_ids = nat.prepare(gaussian_ids, torch.int32)
     image = torch.empty((image_height, image_width, 3), dtype=torch.float32, device=device)
@@ -98,8 +100,25 @@ def composite(
         ),
         "composite",
     )
-    # The backward of these lists starts its segment walks at the checkpoints
+    # The backward of this walk starts its segment walks at the checkpoints
     # and walks the entries the hit masks mark.
-    nat.set_checkpoints(ranges_in, checkpoints)
-    nat.set_hit_masks(ranges_in, hits)
+    nat.set_walk_state(
+        n_contributors,
+        walk_key(image_width, image_height, tile_size, opacity_threshold, rendering_mode,
+                 mean, inverse_covariance, color, opacity, gaussian_ids_in, ranges_in,
+                 final_transmittance, n_contributors),
+        checkpoints, hits,
+    )
     return image, final_transmittance, n_contributors
+
+
+def walk_key(image_width, image_height, tile_size, opacity_threshold, rendering_mode, mean,
+             inverse_covariance, color, opacity, gaussian_ids, ranges, final_transmittance,
+             n_contributors) -> tuple:
+    """The fingerprint shared by ``composite`` and ``composite_bwd``."""
+    return nat.walk_fingerprint(
+        (int(image_width), int(image_height), int(tile_size), float(opacity_threshold),
+         str(rendering_mode)),
+        mean, inverse_covariance, color, opacity, gaussian_ids, ranges, final_transmittance,
+        n_contributors,
+    )

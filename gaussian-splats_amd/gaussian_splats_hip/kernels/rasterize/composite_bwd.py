@@ -14,6 +14,7 @@ from __future__ import annotations
 import torch
 
 from . import _native as nat
+from .composite import walk_key
 from .project import _check_tile
 
 
@@ -38,11 +39,21 @@ def composite_bwd(
     out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """``out`` (optional, zero-filled [N, 9] float32) receives the gradient;
-    returns ``(grad, absolute)`` when ``return_absolute``."""
+    returns ``(grad, absolute)`` when ``return_absolute``.
+
+    A pure function of its arguments, as the reference's is.  When they are
+    exactly those of an earlier ``composite`` call and its outputs (same
+    tensors, unmodified), the walk skips the entries that call's hit masks
+    leave out and starts long lists at its checkpoints.  Otherwise it walks
+    every entry from the end of each list."""
     if rendering_mode != "gaussian":
         raise AssertionError("Backward gradients are only supported for Gaussian rendering.")
     _check_tile(tile_size)
     device = nat.require_gpu(projected_mean, gaussian_ids, ranges, grad_image)
+    checkpoints, hits = nat.walk_buffers(n_contributors, walk_key(
+        image_width, image_height, tile_size, opacity_threshold, rendering_mode, projected_mean,
+        inverse_covariance, projected_color, projected_opacity, gaussian_ids, ranges,
+        final_transmittance, n_contributors))
     projected_mean, inverse_covariance, projected_color, projected_opacity = (
         nat.prepare(t) for t in (projected_mean, inverse_covariance, projected_color, projected_opacity)
     )
@@ -50,8 +61,6 @@ def composite_bwd(
     final_transmittance = nat.prepare(final_transmittance)
     n_contributors = nat.prepare(n_contributors, torch.int32)
     active = nat.active_tiles(ranges)
-    checkpoints = nat.checkpoints(ranges)
-    hits = nat.hit_masks(ranges)
     ranges = nat.prepare(ranges, torch.int64)
     gaussian_ids = nat.prepare(gaussian_ids, torch.int32)
     n = projected_mean.shape[0]

@@ -200,8 +200,7 @@ def _setup_context(ctx, inputs, output) -> None:
             opacity_threshold=ctx.opacity_threshold, active_tiles=nat.active_tiles(output[8]),
         )
         ctx.view_project = nat.make_view(ctx.fx, ctx.fy, 0.0, 0.0, ctx.image_width, ctx.image_height)
-        ctx.checkpoints = nat.checkpoints(output[8])
-        ctx.hit_masks = nat.hit_masks(output[8])
+        ctx.checkpoints, ctx.hit_masks = nat.walk_buffers(output[2])
         num_tiles = output[8].shape[0]
         lib = nat.library()
         order = torch.empty(lib.gs_tile_order_items(ctx.view_composite, 1), dtype=torch.int32,

@@ -187,8 +187,7 @@ def forward_views(
         ),
         "composite",
     )
-    nat.set_checkpoints(ranges, checkpoints)
-    nat.set_hit_masks(ranges, hits)
+    nat.set_walk_state(n_contributors, None, checkpoints, hits)
     mark("composite")
     return (
         image,
@@ -295,8 +294,7 @@ def _setup_context(ctx, inputs, output) -> None:
         ctx.confidence,
     ) = inputs[8:]
     ctx.active_tiles = nat.active_tiles(output[8])
-    ctx.checkpoints = nat.checkpoints(output[8])
-    ctx.hit_masks = nat.hit_masks(output[8])
+    ctx.checkpoints, ctx.hit_masks = nat.walk_buffers(output[2])
     ctx.order = None
     if inputs[0].is_cuda and ctx.rendering_mode == "gaussian":
         # The backward's dispatch plan depends only on the forward's lists and
@@ -337,16 +335,14 @@ def backward_views(
     returns the gradients of the five parameter tensors.  ``timer(name)``
     marks "composite_bwd" and "project_bwd".  ``active_tiles``: tiles with a
     non-empty list, ``checkpoints``: the forward's checkpoint buffer, and
-    ``hit_masks``: its hit masks (defaults: those the forward recorded on the
-    ranges); ``order``: the dispatch plan of these lists and contributor
+    ``hit_masks``: its hit masks (defaults: those the forward recorded on its
+    ``n_contributors`` output); ``order``: the dispatch plan of these lists and contributor
     counts (default: computed here)."""
     mark = timer or (lambda name: None)
     if active_tiles is None:
         active_tiles = nat.active_tiles(saved[7])
-    if checkpoints is None:
-        checkpoints = nat.checkpoints(saved[7])
-    if hit_masks is None:
-        hit_masks = nat.hit_masks(saved[7])
+    if checkpoints is None and hit_masks is None:
+        checkpoints, hit_masks = nat.walk_buffers(saved[1])
     mean, rotation, scale, opacity, color = (
         _contiguous(t) for t in (mean, rotation, scale, opacity, color)
     )

@@ -42,7 +42,7 @@ extern "C" {
 
 #define GS_API __attribute__((visibility("default")))
 
-#define GS_ABI_VERSION 11
+#define GS_ABI_VERSION 12
 
 typedef enum gs_status {
   GS_OK = 0,
@@ -301,7 +301,13 @@ GS_API int gs_tile_order_noalloc(
  * transmittance and the colour composited after that point (at most 63 per
  * tile, from a pool of at most 128 MiB), which gs_composite_bwd uses to walk
  * long lists back in segments at once.  The image is then the sum of the
- * colour before and after each record.  The query returns 0 (no buffer
+ * colour before and after each record.  A smaller buffer is accepted down to
+ * its header (counter, stamp and table): it holds as many records as fit,
+ * and the crossings past them are marked missing, which the backward walks
+ * without a record.  The forward stamps the buffer with its geometry (tile
+ * size, tiles, table length), or clears the stamp when its walk records
+ * nothing (tiles split into quarters, tile 32, no records); the backward
+ * uses the table only when the stamp matches its own view.  The query returns 0 (no buffer
  * needed) when longest_list, the longest list (totals[3] >> 32 of
  * gs_bin_tiles_plan), is not above 8192, and for tiles of 32 pixels (whose
  * walk holds 16 pixels per lane, leaving no registers for the records). */
@@ -338,7 +344,11 @@ GS_API int gs_composite(
  * a segment item starts its walk back at a checkpoint, with the
  * transmittance recorded there and g.S = g . (colour after it) / T, the
  * state the walk from the end would reach (the associative combine of
- * composite_bwd.py:24-36), so a long walk runs on many waves at once.
+ * composite_bwd.py:24-36), so a long walk runs on many waves at once.  It is
+ * read only where gs_composite records (whole tiles of at most 16 pixels, n
+ * > 0) and only when its stamp matches this view; the stamp cannot tell two
+ * walks of one geometry apart, so it must be the buffer of the forward over
+ * these same lists.
  * hit_masks: the buffer gs_composite filled for the same lists and view (or
  * NULL: every entry of the walk is gathered and tested). */
 GS_API int gs_composite_bwd(

@@ -58,6 +58,67 @@ def assert_close_flip_aware(actual, expected, margin, atol, rtol=0.0, loose=None
     return {"max_err": float(err[ok].max()) if bool(ok.any()) else 0.0, "flagged": flagged}
 
 
+def assert_forward_every_pixel(image, final_t, ncon, cols32, ids, ranges, width, height,
+                               tile_size, mask=None, threshold=0.999, atol=1e-5, t_rtol=1e-4,
+                               tile_chunk=64, max_near=0.01, what=""):
+    """Bounds every pixel of a GPU forward, those near a decision included.
+
+    The float64 oracle composites the GPU's own projected values ``cols32``
+    (u, v, inv00, inv01, inv11, rgb [N, 3], alpha0) along the GPU's lists with
+    the GPU's activity decisions (``ncon``) and the float32 oracle's cut and
+    clamp decisions.  The GPU image and transmittance must match that at
+    ``atol`` (transmittance: + ``t_rtol`` relative) on every pixel of
+    ``mask``, except where an entry's alpha-cut decision lies within
+    orc.CUT_NEAR of 1/255 (``cut_near`` entries at that pixel), where the GPU
+    may keep or drop it differently.  Keeping or dropping an entry of alpha
+    a changes the pixel by a * (T rgb + colour after it) <= 2 a max(rgb) and
+    the transmittance by a * T <= a.  So such a pixel is bounded by cut_near
+    times 2 max(rgb) / 255 (image) or 1 / 255 (transmittance) on top of the
+    tolerance, and at most ``max_near`` of the pixels may be such.  Returns
+    statistics."""
+    cols32 = [torch.as_tensor(c).detach().float().cpu() for c in cols32]
+    ids = np.asarray(ids)
+    ranges = np.asarray(ranges)
+    ncon = np.asarray(torch.as_tensor(ncon).cpu())
+    run32 = orc.composite(*cols32, ids, ranges, width, height, tile_size, threshold,
+                          tile_chunk=tile_chunk)
+    run64 = orc.composite(*(c.double() for c in cols32), ids, ranges, width, height, tile_size,
+                          threshold, tile_chunk=tile_chunk, decisions=run32.decisions,
+                          active_counts=ncon)
+    m = (torch.ones(height, width, dtype=torch.bool) if mask is None
+         else torch.as_tensor(mask).bool().cpu())
+    near = run64.cut_near.double()
+    max_rgb = float(cols32[5].abs().max()) if cols32[5].numel() else 0.0
+    img = torch.as_tensor(image).detach().double().cpu()
+    err = (img - run64.image.double()).abs().amax(-1)
+    bound = atol + near * (2 * max_rgb * (1 + 1e-5) / 255)
+    bad = m & (err > bound)
+    worst = float((err / bound)[m].max()) if bool(m.any()) else 0.0
+    assert not bool(bad.any()), (
+        f"{what}: {int(bad.sum())} of {int(m.sum())} pixels exceed their bound; worst "
+        f"{worst:.2f}x at {np.unravel_index(int(torch.where(m, err / bound, 0).argmax()), err.shape)}")
+    t = torch.as_tensor(final_t).detach().double().cpu()
+    t64 = run64.final_transmittance.double()
+    t_err = (t - t64).abs()
+    t_bound = atol + t_rtol * t64.abs() + near * ((1 + 1e-5) / 255)
+    t_bad = m & (t_err > t_bound)
+    assert not bool(t_bad.any()), (
+        f"{what}: {int(t_bad.sum())} transmittance values exceed their bound; worst "
+        f"{float((t_err / t_bound)[m].max()):.2f}x")
+    near_px = m & (near > 0)
+    frac = float(near_px.double().sum() / max(int(m.sum()), 1))
+    assert frac <= max_near, f"{what}: {frac:.3%} of pixels have a cut decision near 1/255"
+    stats = {
+        "pixels": int(m.sum()),
+        "near_cut_pixels": int(near_px.sum()),
+        "max_err": float(err[m & (near == 0)].max()) if bool((m & (near == 0)).any()) else 0.0,
+        "max_err_near_cut": float(err[near_px].max()) if bool(near_px.any()) else 0.0,
+        "worst_vs_bound": worst,
+    }
+    print(f"[{what}] every pixel: {stats}", flush=True)
+    return stats
+
+
 def rect_flip_tolerant_equal(actual_bounds, expected_bounds, projected, tile_size, extent):
     """Bounds must match exactly except where the oracle's (u -/+ r) / tile lies
     within 1e-5 (relative) of an integer, i.e. where an ulp decides the floor."""
@@ -409,6 +470,37 @@ def fixed_decision_rasterize_grads(params, cam, tile_size, near, far, lists, col
             for k in range(samples)]
     g32 = [list(per) for per in zip(*runs)]
     return g64, g32, run32.gaussian_cut_margin
+
+
+def segmented_scene(entries, width=64, height=64, tile_size=8):
+    """Projected splats whose lists cross the forward's checkpoints: every
+    entry is listed in tiles (0, 0) and (0, 1), an eighth of them also in
+    (1, 0) and (1, 1).  The first two lists are longer than the checkpoint
+    minimum (8192 entries) and walk ~1300 entries until T ~ 1e-3; the other
+    two walk their whole lists of 1125 or 1500.  The splats are wide (sigma >=
+    2000 px, alpha 0.0045-0.006), so no pixel sits near a discrete decision.
+    Returns (pmean, pinv, pcol, pop, sorted ids, ranges)."""
+    g = torch.Generator().manual_seed(entries + 1)
+    u = torch.rand(entries, generator=g) * 20 - 2
+    v = torch.rand(entries, generator=g) * 20 - 2
+    depth = torch.rand(entries, generator=g) * 5 + 1
+    pmean = torch.stack((u, v, depth), -1)
+    sigma = torch.rand(entries, generator=g) * 2000 + 2000
+    rho = (torch.rand(entries, generator=g) * 2 - 1) * 0.5
+    cov = torch.stack((sigma ** 2, rho * sigma ** 2, rho * sigma ** 2, sigma ** 2), -1).view(-1, 2, 2)
+    pinv = torch.linalg.inv(cov.double()).float()
+    pcol = torch.rand(entries, 3, generator=g)
+    pop = torch.rand(entries, 1, generator=g) * 0.0015 + 0.0045
+    tw = -(-width // tile_size)
+    th = -(-height // tile_size)
+    bounds = np.zeros((entries, 2, 2), dtype=np.int32)
+    bounds[:, 0, 1] = 1
+    bounds[: entries // 8, 0, 1] = 2
+    bounds[:, 1, 1] = 2
+    counts = ((bounds[:, 0, 1] - bounds[:, 0, 0]) * (bounds[:, 1, 1] - bounds[:, 1, 0])).astype(np.int32)
+    keys, ids = orc.emit_intersections(bounds, depth.numpy(), counts, tw)
+    sid, ranges, _ = orc.sort_intersections(keys, ids, tw * th)
+    return pmean, pinv, pcol, pop, sid, ranges
 
 
 # ---------------------------------------------------------------------------

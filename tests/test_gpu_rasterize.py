@@ -20,6 +20,7 @@ from parity import (
     fixed_decision_composite_grads,
     fixed_decision_rasterize_grads,
     oracle_camera,
+    segmented_scene,
 )
 
 pytestmark = pytest.mark.gpu
@@ -205,31 +206,10 @@ def test_composite_backward_segmented_walks(device, entries):
     unsegmented backward (no plan, no checkpoints) up to rounding."""
     from gaussian_splats_hip.kernels.rasterize.composite import tile_order
 
-    g = torch.Generator().manual_seed(entries + 1)
     w = h = 64
     ts = 8
-    u = torch.rand(entries, generator=g) * 20 - 2
-    v = torch.rand(entries, generator=g) * 20 - 2
-    depth = torch.rand(entries, generator=g) * 5 + 1
-    pmean = torch.stack((u, v, depth), -1)
-    sigma = torch.rand(entries, generator=g) * 2000 + 2000
-    rho = (torch.rand(entries, generator=g) * 2 - 1) * 0.5
-    cov = torch.stack((sigma ** 2, rho * sigma ** 2, rho * sigma ** 2, sigma ** 2), -1).view(-1, 2, 2)
-    pinv = torch.linalg.inv(cov.double()).float()
-    pcol = torch.rand(entries, 3, generator=g)
-    pop = torch.rand(entries, 1, generator=g) * 0.0015 + 0.0045
-    tw, th = nat.tiles(w, h, ts)
-    # Every entry is listed in tiles 0 and 8 (column 0, rows 0-1), an eighth
-    # of them also in tiles 1 and 9: tiles 0 and 8 hold lists longer than the
-    # checkpoint minimum (8192 entries) and walk ~1300 of them (until
-    # T ~ 1e-3), tiles 1 and 9 walk their whole lists of 1125 or 1500.
-    bounds = np.zeros((entries, 2, 2), dtype=np.int32)
-    bounds[:, 0, 1] = 1
-    bounds[: entries // 8, 0, 1] = 2
-    bounds[:, 1, 1] = 2
-    counts = ((bounds[:, 0, 1] - bounds[:, 0, 0]) * (bounds[:, 1, 1] - bounds[:, 1, 0])).astype(np.int32)
-    keys, ids = orc.emit_intersections(bounds, depth.numpy(), counts, tw)
-    sid, ranges, _ = orc.sort_intersections(keys, ids, tw * th)
+    pmean, pinv, pcol, pop, sid, ranges = segmented_scene(entries, w, h, ts)
+    g = torch.Generator().manual_seed(entries + 2)
     grad_image = torch.rand(h, w, 3, generator=g) * 2 - 1
     print(f"[segmented walks] {entries} entries", flush=True)
     grad, absolute, expected, expected32, _, explained = _composite_bwd_case(

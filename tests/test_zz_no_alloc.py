@@ -6,7 +6,9 @@ bit on consecutive calls of decreasing size -- the largest view the scratch
 holds, a 1080p view by contributor counts, then a smaller view by list
 lengths, so stale keys of the earlier calls remain in the scratch -- and on a
 mosaic of views; the 1080p and small orders also equal the order's numpy
-model.  Views beyond the scratch are rejected on the host before any launch.
+model.  The backward plan the op uses (ranges and contributor counts
+together, lists above 8192 entries whose walks cross checkpoints) writes the
+scratch's second half, the crossings, and holds segment items.  Views beyond the scratch are rejected on the host before any launch.
 """
 
 from __future__ import annotations
@@ -113,3 +115,23 @@ def test_noalloc_matches_workspace_order(device):
     expected, got = _both_orders(device, view, views * tw * th,
                                  ncon=torch.as_tensor(ncon).to(device))
     np.testing.assert_array_equal(got, expected)
+
+    # The op's backward plan: ranges and contributor counts together, with
+    # lists above 8192 entries whose walks cross checkpoints, so the crossings
+    # half of the scratch is written and the plan holds segment items (tile
+    # 8: tiles of 16 pixels or more are split into quarters, without
+    # segments, when fewer than 4096 of them have work).
+    w, h, tile = 256, 192, 8
+    tw, th = nat.tiles(w, h, tile)
+    lengths = rng.integers(0, 3000, size=tw * th)
+    long_tiles = rng.choice(tw * th, 24, replace=False)
+    lengths[long_tiles] = rng.integers(9000, 40000, size=long_tiles.size)
+    per_pixel = np.repeat(np.repeat(lengths.reshape(th, tw), tile, 0), tile, 1)[:h, :w]
+    ncon = (rng.random((h, w)) * np.minimum(per_pixel, 6000)).astype(np.int32)
+    view = nat.make_view(1.0, 1.0, 0.0, 0.0, w, h, tile)
+    print(f"[noalloc] backward plan with crossings, {tw * th} tiles", flush=True)
+    expected, got = _both_orders(device, view, tw * th,
+                                 ranges=torch.as_tensor(_ranges(lengths)).to(device),
+                                 ncon=torch.as_tensor(ncon).to(device))
+    np.testing.assert_array_equal(got, expected)
+    assert ((got >= 0) & ((got & 0x40) != 0)).any()

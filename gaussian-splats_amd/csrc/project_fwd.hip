@@ -85,23 +85,25 @@ __global__ __launch_bounds__(kProjectBlock) void project_fwd_kernel(ProjectArgs 
   __syncthreads();
   if (!have) return;
 
-  // View-independent terms, computed once per Gaussian.
+  // View-independent terms, computed once per Gaussian, in double precision
+  // like the covariance chain they feed (see below).
   // Normalised quaternion (w, x, y, z) -> rotation (utils.py:8-25).
-  const float qn = fmaxf(sqrtf(q.x * q.x + q.y * q.y + q.z * q.z + q.w * q.w), 1e-12f);
-  const float qw = q.x / qn, qx = q.y / qn, qy = q.z / qn, qz = q.w / qn;
-  const float q00 = 1.0f - 2.0f * (qy * qy + qz * qz);
-  const float q01 = 2.0f * (qx * qy - qw * qz);
-  const float q02 = 2.0f * (qx * qz + qw * qy);
-  const float q10 = 2.0f * (qx * qy + qw * qz);
-  const float q11 = 1.0f - 2.0f * (qx * qx + qz * qz);
-  const float q12 = 2.0f * (qy * qz - qw * qx);
-  const float q20 = 2.0f * (qx * qz - qw * qy);
-  const float q21 = 2.0f * (qy * qz + qw * qx);
-  const float q22 = 1.0f - 2.0f * (qx * qx + qy * qy);
+  const double dqx = q.x, dqy = q.y, dqz = q.z, dqw = q.w;
+  const double qn = fmax(sqrt(dqx * dqx + dqy * dqy + dqz * dqz + dqw * dqw), 1e-12);
+  const double qw = dqx / qn, qx = dqy / qn, qy = dqz / qn, qz = dqw / qn;
+  const double q00 = 1.0 - 2.0 * (qy * qy + qz * qz);
+  const double q01 = 2.0 * (qx * qy - qw * qz);
+  const double q02 = 2.0 * (qx * qz + qw * qy);
+  const double q10 = 2.0 * (qx * qy + qw * qz);
+  const double q11 = 1.0 - 2.0 * (qx * qx + qz * qz);
+  const double q12 = 2.0 * (qy * qz - qw * qx);
+  const double q20 = 2.0 * (qx * qz - qw * qy);
+  const double q21 = 2.0 * (qy * qz + qw * qx);
+  const double q22 = 1.0 - 2.0 * (qx * qx + qy * qy);
 
-  const float sx = expf(ls0);
-  const float sy = expf(ls1);
-  const float sz = expf(ls2);
+  const double sx = exp(double(ls0));
+  const double sy = exp(double(ls1));
+  const double sz = exp(double(ls2));
 
   const float alpha0 = 1.0f / (1.0f + expf(-lo));
   // Extent of the ellipse in standard deviations (torch.py:233-252) and the
@@ -136,35 +138,47 @@ __global__ __launch_bounds__(kProjectBlock) void project_fwd_kernel(ProjectArgs 
     const float u = cam.fx * px / d + cam.cx;
     const float v = -cam.fy * py / d + cam.cy;
 
-    // Perspective Jacobian with the 1.3 x half-FOV clamp (camera.py:106-119).
-    const float nx = fminf(fmaxf(px / dc, -cam.lim_x), cam.lim_x);
-    const float ny = fminf(fmaxf(py / dc, -cam.lim_y), cam.lim_y);
-    const float j00 = cam.fx / dc;
-    const float j02 = cam.fx * nx / dc;
-    const float j11 = -cam.fy / dc;
-    const float j12 = -cam.fy * ny / dc;
+    // The 2-D covariance and its inverse, in double precision from the
+    // float32 inputs.  For a nearly degenerate covariance (an edge-on flat
+    // splat, a needle) det = c00 c11 - c01^2 cancels, and float32 arithmetic
+    // loses the condition number's worth of digits in the inverse; computed
+    // in double, the stored inverse is the float32 rounding of the exact
+    // value.  The projection backward recomputes the same chain in double.
+    // Perspective Jacobian with the 1.3 x half-FOV clamp (camera.py:106-119),
+    // at the camera-space point p = R mu + t recomputed in double.
+    const double dpx = double(r00) * mx + double(r01) * my + double(r02) * mz + double(t0);
+    const double dpy = double(r10) * mx + double(r11) * my + double(r12) * mz + double(t1);
+    const double dpz = double(r20) * mx + double(r21) * my + double(r22) * mz + double(t2);
+    const double dd = -dpz;
+    const double ddc = fabs(dd) >= 1e-4 ? dd : copysign(1e-4, dd);
+    const double nx = fmin(fmax(dpx / ddc, -double(cam.lim_x)), double(cam.lim_x));
+    const double ny = fmin(fmax(dpy / ddc, -double(cam.lim_y)), double(cam.lim_y));
+    const double j00 = double(cam.fx) / ddc;
+    const double j02 = double(cam.fx) * nx / ddc;
+    const double j11 = -double(cam.fy) / ddc;
+    const double j12 = -double(cam.fy) * ny / ddc;
     // W = J Rc.
-    const float w00 = j00 * r00 + j02 * r20;
-    const float w01 = j00 * r01 + j02 * r21;
-    const float w02 = j00 * r02 + j02 * r22;
-    const float w10 = j11 * r10 + j12 * r20;
-    const float w11 = j11 * r11 + j12 * r21;
-    const float w12 = j11 * r12 + j12 * r22;
+    const double w00 = j00 * r00 + j02 * r20;
+    const double w01 = j00 * r01 + j02 * r21;
+    const double w02 = j00 * r02 + j02 * r22;
+    const double w10 = j11 * r10 + j12 * r20;
+    const double w11 = j11 * r11 + j12 * r21;
+    const double w12 = j11 * r12 + j12 * r22;
 
     // M = W Rq diag(s); Sigma = M M^T + eps I (camera.py:121-123).
-    const float m00 = (w00 * q00 + w01 * q10 + w02 * q20) * sx;
-    const float m01 = (w00 * q01 + w01 * q11 + w02 * q21) * sy;
-    const float m02 = (w00 * q02 + w01 * q12 + w02 * q22) * sz;
-    const float m10 = (w10 * q00 + w11 * q10 + w12 * q20) * sx;
-    const float m11 = (w10 * q01 + w11 * q11 + w12 * q21) * sy;
-    const float m12 = (w10 * q02 + w11 * q12 + w12 * q22) * sz;
-    const float c00 = m00 * m00 + m01 * m01 + m02 * m02 + a.eps;
-    const float c01 = m00 * m10 + m01 * m11 + m02 * m12;
-    const float c11 = m10 * m10 + m11 * m11 + m12 * m12 + a.eps;
-    const float det = c00 * c11 - c01 * c01;
-    const float i00 = c11 / det;
-    const float i01 = -c01 / det;
-    const float i11 = c00 / det;
+    const double m00 = (w00 * q00 + w01 * q10 + w02 * q20) * sx;
+    const double m01 = (w00 * q01 + w01 * q11 + w02 * q21) * sy;
+    const double m02 = (w00 * q02 + w01 * q12 + w02 * q22) * sz;
+    const double m10 = (w10 * q00 + w11 * q10 + w12 * q20) * sx;
+    const double m11 = (w10 * q01 + w11 * q11 + w12 * q21) * sy;
+    const double m12 = (w10 * q02 + w11 * q12 + w12 * q22) * sz;
+    const double c00 = m00 * m00 + m01 * m01 + m02 * m02 + double(a.eps);
+    const double c01 = m00 * m10 + m01 * m11 + m02 * m12;
+    const double c11 = m10 * m10 + m11 * m11 + m12 * m12 + double(a.eps);
+    const double rdet = 1.0 / (c00 * c11 - c01 * c01);
+    const float i00 = float(c11 * rdet);
+    const float i01 = float(-c01 * rdet);
+    const float i11 = float(c00 * rdet);
 
     // View direction from the Gaussian to the camera centre -R^T t
     // (torch.py:198, camera.py:37-39).
@@ -186,8 +200,8 @@ __global__ __launch_bounds__(kProjectBlock) void project_fwd_kernel(ProjectArgs 
     }
 
     // Rectangle of tiles touched by the extent ellipse (torch.py:233-252).
-    const float rx = extent * sqrtf(c00);
-    const float ry = extent * sqrtf(c11);
+    const float rx = extent * sqrtf(float(c00));
+    const float ry = extent * sqrtf(float(c11));
     // fmaxf/fminf map a NaN extent (alpha0 < 1/255) to the empty rectangle [0, 0).
     const float bx0 = fminf(fmaxf(floorf((u - rx) / a.tile), 0.0f), a.tiles_w);
     const float bx1 = fminf(fmaxf(floorf((u + rx) / a.tile) + 1.0f, 0.0f), a.tiles_w);

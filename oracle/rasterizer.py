@@ -37,6 +37,9 @@ import torch
 SH_C0 = 0.28209479177387814
 MIN_ALPHA = 1.0 / 255.0
 MAX_ALPHA = 0.99
+# Relative distance from the alpha cut, in units of alpha's float32 rounding
+# sensitivity, within which Composite.cut_near counts a decision.
+CUT_NEAR = 1e-5
 
 # Closed-form real SH constants (degree <= 3), band-major, m = -l..l.  These are
 # the normalisations the recurrence of utils.py:32-66 produces; the equality is
@@ -254,6 +257,15 @@ class Composite:
     # Per chunk start tile: (keep, clamped) booleans [entries, pixels] of the
     # alpha cut (alpha >= 1/255 after the clamp) and of the 0.99 clamp.
     decisions: dict
+    # [H, W]: the number of entries processed while active (or the first
+    # inactive one) whose alpha-cut decision lies within CUT_NEAR of 1/255, in
+    # units of alpha's rounding sensitivity (the relative distance divided by
+    # 1 + the quadratic form with absolute terms).  Two float32 evaluations of
+    # such an entry's alpha may keep or drop it differently.
+    cut_near: torch.Tensor
+    # Per chunk start tile: the [entries, pixels] pairs counted by cut_near,
+    # in the layout of ``decisions``.
+    near_pairs: dict
 
 
 def composite(
@@ -277,8 +289,12 @@ def composite(
     decisions: dict | None = None,
     active_counts: np.ndarray | None = None,
     transmittance: str = "log",
+    diagnostics: bool = True,
 ) -> Composite:
     """Dense per-(entry, pixel) compositing of each tile list (torch.py:172-225).
+
+    ``diagnostics=False`` computes the image only, as torch.py:172-225 does
+    (the CPU baseline's timing); the other fields keep their initial values.
 
     ``transmittance``: "log" (the reference's torch backend, torch.py:209-212:
     exp of a float64 cumulative sum of log1p(-alpha)) or "product" (the
@@ -294,7 +310,9 @@ def composite(
     result is then the exact-arithmetic value (in float64) of a compositor
     that took those discrete decisions, differentiable as before: with both,
     a float64 run's gradients are what a float32 implementation deciding like
-    that should produce up to its rounding.  Gaussian mode only.
+    that should produce up to its rounding.  In ellipsoid mode the kept
+    entries' indicator D <= cutoff is taken as decided (alpha = alpha0, or
+    0.99 where clamped).
 
     With ``probe`` (a list), every chunk appends ``(g, du, dv)``: zero leaves
     of shape [entries, pixels] added to the means inside the quadratic form, so
@@ -324,14 +342,14 @@ def composite(
     cutoff = -2 * math.log1p(-confidence)
     gmargin = torch.full((u.shape[0],), math.inf, dtype=torch.float64)
     gcmargin = torch.full((u.shape[0],), math.inf, dtype=torch.float64)
-    if (decisions is not None or active_counts is not None) and rendering_mode != "gaussian":
-        raise ValueError("fixed decisions apply to the gaussian rendering mode")
+    near_count = torch.zeros(num_tiles, P, dtype=torch.int64)
     if active_counts is not None:
         ac = np.zeros((tiles_h * tile_size, tiles_w * tile_size), dtype=np.int64)
         ac[:height, :width] = np.asarray(active_counts)
         ac = ac.reshape(tiles_h, tile_size, tiles_w, tile_size).transpose(0, 2, 1, 3)
         active_tiles = torch.as_tensor(ac.reshape(num_tiles, P))
     recorded = {}
+    near_pairs = {}
     parts = []
     for t0 in range(0, num_tiles, tile_chunk):
         t1 = min(num_tiles, t0 + tile_chunk)
@@ -365,13 +383,16 @@ def composite(
         raw = alpha0[g][:, None] * prob
         if decisions is not None:
             keep, clamped = decisions[t0]
-            alpha = torch.where(clamped, torch.full_like(raw, MAX_ALPHA), raw)
+            # Ellipsoid mode: a kept entry's indicator (D <= cutoff) was 1.
+            base = alpha0[g][:, None].expand_as(raw) if rendering_mode == "ellipsoid" else raw
+            alpha = torch.where(clamped, torch.full_like(raw, MAX_ALPHA), base)
             alpha = torch.where(keep, alpha, torch.zeros_like(alpha))
         else:
             alpha = raw.clamp_max(MAX_ALPHA)
             alpha = torch.where(alpha >= MIN_ALPHA, alpha, torch.zeros_like(alpha))
-            with torch.no_grad():
-                recorded[t0] = (alpha > 0, raw > MAX_ALPHA)
+            if diagnostics:
+                with torch.no_grad():
+                    recorded[t0] = (alpha > 0, raw > MAX_ALPHA)
         seg_start = torch.as_tensor(np.repeat(np.cumsum(counts) - counts, counts), dtype=torch.int64)
         if transmittance == "log":
             log_survival = torch.log1p(-alpha)
@@ -401,55 +422,60 @@ def composite(
         weights = T * alpha * active
         contrib = weights[..., None] * rgb[g][:, None, :]
         parts.append((t0, t1, torch.zeros(t1 - t0, P, 3, dtype=dt).index_add(0, rel, contrib)))
-        with torch.no_grad():
-            n_active = torch.zeros(t1 - t0, P, dtype=torch.int64).index_add(0, rel, active.long())
-            ncon[t0:t1] = n_active
-            # T after the last active entry: T_i * (1 - alpha_i) at position n - 1.
-            after = (T * (1 - alpha)).detach()
-            pos = torch.arange(hi - lo) - seg_start
-            last = active & (pos[:, None] == (n_active[rel] - 1))
-            ft = torch.ones(t1 - t0, P, dtype=dt)
-            sel = last.nonzero(as_tuple=True)
-            ft[rel[sel[0]], sel[1]] = after[sel]
-            final_t[t0:t1] = ft
-            # Decision margins over entries up to and including the first inactive one.
-            considered = pos[:, None] <= n_active[rel]
-            a64 = raw.detach().to(torch.float64).clamp_max(MAX_ALPHA)
-            m_cut = ((a64 - MIN_ALPHA).abs() / MIN_ALPHA)
-            if rendering_mode == "ellipsoid":
-                m_cut = torch.minimum(m_cut, (D.detach().to(torch.float64) - cutoff).abs() / cutoff)
-            T64 = T.detach().to(torch.float64)
-            m_thr = ((1 - T64) - opacity_threshold).abs() / T64.clamp_min(1e-30)
-            m = torch.minimum(m_cut, m_thr)
-            m = torch.where(considered, m, torch.full_like(m, math.inf))
-            mm = torch.full((t1 - t0, P), math.inf, dtype=torch.float64)
-            mm.index_reduce_(0, rel, m, "amin")
-            margin[t0:t1] = torch.minimum(margin[t0:t1], mm)
-            r64 = raw.detach().to(torch.float64)
-            m_cl = (r64 - MAX_ALPHA).abs() / MAX_ALPHA
-            m_cl = torch.where(considered & (alpha.detach() > 0), m_cl, torch.full_like(m_cl, math.inf))
-            cm = torch.full((t1 - t0, P), math.inf, dtype=torch.float64)
-            cm.index_reduce_(0, rel, m_cl, "amin")
-            cmargin[t0:t1] = torch.minimum(cmargin[t0:t1], cm)
-            # Per Gaussian: worst pixel margin among the pixels it reaches, and
-            # its own clamp margin there.
-            reach = considered & (alpha.detach() > 0)
-            per_entry = torch.where(reach, torch.minimum(mm[rel], m_cl), torch.full_like(m_cl, math.inf))
-            gmargin.index_reduce_(0, g, per_entry.amin(1), "amin")
-            # The same with the cut and clamp decisions only, in units of
-            # alpha's rounding sensitivity.
-            ddx, ddy = dx.detach().to(torch.float64), dy.detach().to(torch.float64)
-            d_abs = (inv00[g].detach().to(torch.float64).abs()[:, None] * ddx * ddx
-                     + 2 * (inv01[g].detach().to(torch.float64).abs()[:, None] * (ddx * ddy).abs())
-                     + inv11[g].detach().to(torch.float64).abs()[:, None] * ddy * ddy)
-            sens = 1 + d_abs
-            m_cc = torch.where(considered, torch.minimum(m_cut, m_cl) / sens,
-                               torch.full_like(m_cl, math.inf))
-            pc = torch.full((t1 - t0, P), math.inf, dtype=torch.float64)
-            pc.index_reduce_(0, rel, m_cc, "amin")
-            per_entry = torch.where(reach, torch.minimum(pc[rel], m_cl / sens),
-                                    torch.full_like(m_cl, math.inf))
-            gcmargin.index_reduce_(0, g, per_entry.amin(1), "amin")
+        if diagnostics:
+            with torch.no_grad():
+                n_active = torch.zeros(t1 - t0, P, dtype=torch.int64).index_add(0, rel, active.long())
+                ncon[t0:t1] = n_active
+                # T after the last active entry: T_i * (1 - alpha_i) at position n - 1.
+                after = (T * (1 - alpha)).detach()
+                pos = torch.arange(hi - lo) - seg_start
+                last = active & (pos[:, None] == (n_active[rel] - 1))
+                ft = torch.ones(t1 - t0, P, dtype=dt)
+                sel = last.nonzero(as_tuple=True)
+                ft[rel[sel[0]], sel[1]] = after[sel]
+                final_t[t0:t1] = ft
+                # Decision margins over entries up to and including the first inactive one.
+                considered = pos[:, None] <= n_active[rel]
+                a64 = raw.detach().to(torch.float64).clamp_max(MAX_ALPHA)
+                m_cut = ((a64 - MIN_ALPHA).abs() / MIN_ALPHA)
+                if rendering_mode == "ellipsoid":
+                    m_cut = torch.minimum(m_cut, (D.detach().to(torch.float64) - cutoff).abs() / cutoff)
+                T64 = T.detach().to(torch.float64)
+                m_thr = ((1 - T64) - opacity_threshold).abs() / T64.clamp_min(1e-30)
+                m = torch.minimum(m_cut, m_thr)
+                m = torch.where(considered, m, torch.full_like(m, math.inf))
+                mm = torch.full((t1 - t0, P), math.inf, dtype=torch.float64)
+                mm.index_reduce_(0, rel, m, "amin")
+                margin[t0:t1] = torch.minimum(margin[t0:t1], mm)
+                r64 = raw.detach().to(torch.float64)
+                m_cl = (r64 - MAX_ALPHA).abs() / MAX_ALPHA
+                m_cl = torch.where(considered & (alpha.detach() > 0), m_cl, torch.full_like(m_cl, math.inf))
+                cm = torch.full((t1 - t0, P), math.inf, dtype=torch.float64)
+                cm.index_reduce_(0, rel, m_cl, "amin")
+                cmargin[t0:t1] = torch.minimum(cmargin[t0:t1], cm)
+                # Per Gaussian: worst pixel margin among the pixels it reaches, and
+                # its own clamp margin there.
+                reach = considered & (alpha.detach() > 0)
+                per_entry = torch.where(reach, torch.minimum(mm[rel], m_cl), torch.full_like(m_cl, math.inf))
+                gmargin.index_reduce_(0, g, per_entry.amin(1), "amin")
+                # The same with the cut and clamp decisions only, in units of
+                # alpha's rounding sensitivity.
+                ddx, ddy = dx.detach().to(torch.float64), dy.detach().to(torch.float64)
+                d_abs = (inv00[g].detach().to(torch.float64).abs()[:, None] * ddx * ddx
+                         + 2 * (inv01[g].detach().to(torch.float64).abs()[:, None] * (ddx * ddy).abs())
+                         + inv11[g].detach().to(torch.float64).abs()[:, None] * ddy * ddy)
+                sens = 1 + d_abs
+                m_cc = torch.where(considered, torch.minimum(m_cut, m_cl) / sens,
+                                   torch.full_like(m_cl, math.inf))
+                pc = torch.full((t1 - t0, P), math.inf, dtype=torch.float64)
+                pc.index_reduce_(0, rel, m_cc, "amin")
+                near_cut = considered & (m_cut / sens < CUT_NEAR)
+                near_pairs[t0] = near_cut
+                near_count[t0:t1] += torch.zeros(t1 - t0, P, dtype=torch.int64).index_add(
+                    0, rel, near_cut.long())
+                per_entry = torch.where(reach, torch.minimum(pc[rel], m_cl / sens),
+                                        torch.full_like(m_cl, math.inf))
+                gcmargin.index_reduce_(0, g, per_entry.amin(1), "amin")
     for t0, t1, img in parts:
         image = image.index_add(0, torch.arange(t0, t1), img)
 
@@ -467,7 +493,133 @@ def composite(
         gmargin,
         gcmargin,
         decisions if decisions is not None else recorded,
+        to_image(near_count),
+        near_pairs,
     )
+
+
+def composite_backward_walk(
+    u: torch.Tensor,
+    v: torch.Tensor,
+    inv00: torch.Tensor,
+    inv01: torch.Tensor,
+    inv11: torch.Tensor,
+    rgb: torch.Tensor,
+    alpha0: torch.Tensor,
+    ids: np.ndarray,
+    ranges: np.ndarray,
+    width: int,
+    height: int,
+    tile_size: int,
+    grad_image: torch.Tensor,
+    decisions: dict,
+    active_counts: np.ndarray,
+    tile_chunk: int = 64,
+) -> torch.Tensor:
+    """Gradients [N, 9] (u, v, inv00, inv01 per matrix entry, inv11, r, g, b,
+    alpha0) of sum(composite * grad_image), by the algorithm of the
+    reference's Triton backward (kernels/rasterize/composite_bwd.py:100-160),
+    in the inputs' dtype.
+
+    Each tile's list is walked from its last active entry to its first.  The
+    suffix transmittance and suffix colour (the colour composited after an
+    entry, relative to the transmittance there) are accumulated from the back.
+    T_i = final_T / (suffix_T (1 - alpha_i)) and dL/dalpha_i = T_i g . (c_i -
+    S_i).  final_T is the forward's product of (1 - alpha) in the same dtype.
+    The Triton kernel floors the denominator at 1e-4, which makes its gradient
+    inexact for T_i below that; this restatement has no floor, so in float64
+    it equals autograd of :func:`composite`.  The discrete decisions are
+    fixed: ``decisions`` (the cut and clamp of a :func:`composite` call with
+    the same lists and ``tile_chunk``) and ``active_counts`` (entry k of a
+    pixel's list is active iff k < active_counts).  Gaussian mode.  Used as a
+    float32 evaluation of the reference's numerics along a back-to-front walk,
+    whose rounding grows with the walk's length."""
+    dt = u.dtype
+    tiles_w = -(-width // tile_size)
+    tiles_h = -(-height // tile_size)
+    num_tiles = tiles_w * tiles_h
+    P = tile_size * tile_size
+    ranges = np.asarray(ranges)
+    ids = np.asarray(ids)
+    ac = np.zeros((tiles_h * tile_size, tiles_w * tile_size), dtype=np.int64)
+    ac[:height, :width] = np.asarray(active_counts)
+    ac = torch.as_tensor(ac.reshape(tiles_h, tile_size, tiles_w, tile_size)
+                         .transpose(0, 2, 1, 3).reshape(num_tiles, P))
+    gi = torch.zeros(tiles_h * tile_size, tiles_w * tile_size, 3, dtype=dt)
+    gi[:height, :width] = torch.as_tensor(grad_image).to(dt)
+    gi = gi.reshape(tiles_h, tile_size, tiles_w, tile_size, 3).permute(0, 2, 1, 3, 4)
+    gi = gi.reshape(num_tiles, P, 3)
+    local_y, local_x = np.divmod(np.arange(P), tile_size)
+    lengths = ranges[:, 1] - ranges[:, 0]
+    # Decisions of (tile, k): each chunk holds its tiles' lists in tile order
+    # (composite's layout), so the chunks in order hold every list in tile
+    # order and (tile, k) is entry first[tile] + k.
+    chunks = [decisions[t0] for t0 in range(0, num_tiles, tile_chunk) if t0 in decisions]
+    keep_all = torch.cat([c[0] for c in chunks]) if chunks else torch.zeros(0, P, dtype=torch.bool)
+    clamp_all = torch.cat([c[1] for c in chunks]) if chunks else keep_all
+    first = np.cumsum(lengths) - lengths
+    walk = np.minimum(lengths, ac.amax(1).numpy())
+    tiles = np.nonzero(walk > 0)[0]
+    out = torch.zeros(u.shape[0], 9, dtype=dt)
+    if tiles.size == 0:
+        return out
+    tt = torch.as_tensor(tiles)
+    ox = torch.as_tensor((tiles % tiles_w) * tile_size, dtype=dt)[:, None]
+    oy = torch.as_tensor((tiles // tiles_w) * tile_size, dtype=dt)[:, None]
+    px = ox + torch.as_tensor(local_x, dtype=dt)[None]
+    py = oy + torch.as_tensor(local_y, dtype=dt)[None]
+    act = ac[tt]
+    g = gi[tt]
+    L = int(walk[tiles].max())
+
+    def entry(k):
+        """Per sampled tile: the Gaussian at position k (or -1) and its
+        alpha, raw alpha, probability and offsets at the tile's pixels."""
+        has = torch.as_tensor(k < walk[tiles])
+        pos = torch.as_tensor(np.where(k < walk[tiles], ranges[tiles, 0] + k, 0))
+        gid = torch.where(has, torch.as_tensor(ids)[pos].long(), torch.zeros_like(pos))
+        dx = px - u[gid][:, None]
+        dy = py - v[gid][:, None]
+        D = (inv00[gid][:, None] * dx * dx + 2 * inv01[gid][:, None] * dx * dy
+             + inv11[gid][:, None] * dy * dy)
+        prob = torch.exp(-0.5 * D)
+        raw = alpha0[gid][:, None] * prob
+        slot = torch.as_tensor(np.where(k < walk[tiles], first[tiles] + k, 0))
+        keep, clamped = keep_all[slot], clamp_all[slot]
+        on = has[:, None] & keep & (k < act)
+        alpha = torch.where(on, torch.where(clamped, torch.full_like(raw, MAX_ALPHA), raw),
+                            torch.zeros_like(raw))
+        return gid, has, dx, dy, prob, alpha, on & ~clamped
+
+    # The forward's final transmittance, in the working dtype.
+    final_t = torch.ones(len(tiles), P, dtype=dt)
+    for k in range(L):
+        final_t = final_t * (1 - entry(k)[5])
+    suffix_t = torch.ones(len(tiles), P, dtype=dt)
+    suffix_c = torch.zeros(len(tiles), P, 3, dtype=dt)
+    for k in range(L - 1, -1, -1):
+        gid, has, dx, dy, prob, alpha, free = entry(k)
+        c = rgb[gid][:, None, :]
+        t_i = final_t / (suffix_t * (1 - alpha))
+        grad_alpha = torch.where(free, t_i * (g * (c - suffix_c)).sum(-1), torch.zeros_like(alpha))
+        grad_d = grad_alpha * (-0.5 * alpha0[gid][:, None] * prob)
+        a, b, cc = inv00[gid][:, None], inv01[gid][:, None], inv11[gid][:, None]
+        rows = torch.stack((
+            (-2 * grad_d * (a * dx + b * dy)).sum(1),
+            (-2 * grad_d * (b * dx + cc * dy)).sum(1),
+            (grad_d * dx * dx).sum(1),
+            (grad_d * dx * dy).sum(1),
+            (grad_d * dy * dy).sum(1),
+            ((t_i * alpha)[..., None] * g).sum(1)[:, 0],
+            ((t_i * alpha)[..., None] * g).sum(1)[:, 1],
+            ((t_i * alpha)[..., None] * g).sum(1)[:, 2],
+            (grad_alpha * prob).sum(1),
+        ), -1)
+        rows = torch.where(has[:, None], rows, torch.zeros_like(rows))
+        out.index_add_(0, gid, rows)
+        suffix_c = alpha[..., None] * c + (1 - alpha)[..., None] * suffix_c
+        suffix_t = suffix_t * (1 - alpha)
+    return out
 
 
 @dataclass
@@ -501,12 +653,14 @@ def rasterize(
     decisions: dict | None = None,
     active_counts: np.ndarray | None = None,
     transmittance: str = "log",
+    diagnostics: bool = True,
 ) -> Render:
     """project -> cull/rect -> emit -> stable sort -> composite (torch.py:228-247).
 
     ``lists`` = (sorted ids, ranges) composites those lists instead of the
     ones binned here (sorted_keys is then None); ``decisions``,
-    ``active_counts`` and ``transmittance`` are passed to :func:`composite`."""
+    ``active_counts``, ``transmittance`` and ``diagnostics`` are passed to
+    :func:`composite`."""
     proj = project(mean, rotation, scale, opacity, color, cam, covariance_epsilon)
     tiles_w = -(-cam.width // tile_size)
     tiles_h = -(-cam.height // tile_size)
@@ -523,6 +677,7 @@ def rasterize(
         proj.inverse[:, 1, 1], proj.color, proj.opacity[:, 0], sorted_ids, ranges, cam.width,
         cam.height, tile_size, opacity_threshold, rendering_mode, confidence, tile_chunk,
         decisions=decisions, active_counts=active_counts, transmittance=transmittance,
+        diagnostics=diagnostics,
     )
     return Render(comp.image, proj, bounds, counts, sorted_ids, ranges, sorted_keys, comp)
 

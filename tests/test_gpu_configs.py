@@ -41,6 +41,7 @@ from parity import (
     FLOAT32_SAMPLES,
     assert_close_flip_aware,
     assert_close_to_truth,
+    assert_forward_every_pixel,
     assert_gradients_close,
     fixed_decision_composite_grads,
     fixed_decision_rasterize_grads,
@@ -206,6 +207,24 @@ def test_sampled_tiles_forward(device, name):
                             rtol=1e-4, what=f"{name} transmittance")
     ok = mask & (torch.as_tensor(comp.margin) >= 1e-4)
     assert torch.equal(ncon[ok], comp.n_contributors[ok]), f"{name}: contributor counts differ"
+    # Every pixel of those tiles, near a decision or not, against float64
+    # along the GPU's own lists and decisions.
+    out = r["out"]
+    ids, rng = restrict_lists(out[7].cpu().numpy(), out[8].cpu().numpy(), tiles,
+                              {t: m + TRUNCATE_SLACK for t, m in
+                               tile_max(ncon.numpy(), tiles, r["tw"], TILE).items()})
+    stats = assert_forward_every_pixel(image, final_t, ncon, _gpu_columns(out), ids, rng, r["w"],
+                                       r["h"], TILE, mask=mask, tile_chunk=CHUNK,
+                                       what=f"{name} image")
+    log(name, "every pixel", stats)
+
+
+def _gpu_columns(out, view=None):
+    """The GPU's projected values as the oracle's compositing columns (u, v,
+    inv00, inv01, inv11, rgb, alpha0), of one view for the multi-view op."""
+    pm, pinv, pcol, pop = (t.detach().cpu() if view is None else t[view].detach().cpu()
+                           for t in out[3:7])
+    return [pm[:, 0], pm[:, 1], pinv[:, 0, 0], pinv[:, 0, 1], pinv[:, 1, 1], pcol, pop[:, 0]]
 
 
 def _loss_weights(image, target, mask):
@@ -434,6 +453,16 @@ def test_config5_sampled_views_forward(device, config5):
                                 what=f"config5 view {v} transmittance")
         ok = mask & (margin >= 1e-4)
         assert torch.equal(ncon[v].cpu()[ok], comp.n_contributors[ok])
+        # Every pixel of the sampled tiles against float64 along the GPU's
+        # own lists (virtual ids v * n + i in the mosaic) and decisions.
+        gids_v, grng_v = _view_lists(gids.cpu().numpy(), ranges.cpu().numpy(), v, n, c["cols"],
+                                     c["tw"], c["th"])
+        ids_g, rng_g = restrict_lists(gids_v, grng_v, tiles, limits)
+        stats = assert_forward_every_pixel(img, final_t[v].cpu(), ncon[v].cpu(),
+                                           _gpu_columns(c["outs"], v), ids_g, rng_g, c["w"],
+                                           c["h"], TILE, mask=mask, tile_chunk=CHUNK,
+                                           what=f"config5 view {v} image")
+        log(f"config5 view {v} every pixel", stats)
 
 
 def test_config5_op_backward(device, config5):

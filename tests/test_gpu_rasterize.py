@@ -16,6 +16,7 @@ from oracle import rasterizer as orc
 from parity import (
     DECISION_WINDOW,
     assert_close_flip_aware,
+    assert_forward_every_pixel,
     assert_gradients_close,
     fixed_decision_composite_grads,
     fixed_decision_rasterize_grads,
@@ -61,6 +62,12 @@ def test_forward_matches_oracle(device, make, tile_size):
     stats = assert_close_flip_aware(image, ref.image, ref.composite.margin, atol=1e-5, what="image")
     print("image", stats)
     assert image.dtype == torch.float32
+    # Every pixel, near a decision or not, along the GPU's own lists.
+    w, h = scene.cameras[0].image_size
+    assert_forward_every_pixel(
+        image, final_t, ncon, [pmean[:, 0], pmean[:, 1], pinv[:, 0, 0], pinv[:, 0, 1],
+                               pinv[:, 1, 1], pcol, pop[:, 0]],
+        gids.numpy(), ranges.numpy(), w, h, tile_size, what="image")
 
     # Lists: the oracle's binning of the GPU's own projected values is bit-exact.
     w, h = scene.cameras[0].image_size

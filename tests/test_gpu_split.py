@@ -16,7 +16,14 @@ from gaussian_splats_hip.kernels.rasterize import _native as nat
 from gaussian_splats_hip.kernels.rasterize import composite, composite_bwd
 from gaussian_splats_hip.kernels.rasterize.interface import forward_pipeline
 from oracle import rasterizer as orc
-from parity import assert_close_flip_aware, oracle_camera
+from parity import (
+    DECISION_WINDOW,
+    assert_close_flip_aware,
+    assert_forward_every_pixel,
+    assert_gradients_close,
+    fixed_decision_composite_grads,
+    oracle_camera,
+)
 
 pytestmark = pytest.mark.gpu
 
@@ -68,27 +75,28 @@ def test_split_and_one_wave_shapes_agree(device, clustered):
     ref = orc.rasterize(*scene.params(), oracle_camera(cam), tile_size=16,
                         opacity_threshold=THRESHOLD, near=scene.near, far=scene.far)
     assert_close_flip_aware(a[0].cpu(), ref.image, ref.composite.margin, atol=1e-5, what="image")
+    cols32 = [pmean[:, 0], pmean[:, 1], pinv[:, 0, 0], pinv[:, 0, 1], pinv[:, 1, 1], pcol,
+              pop[:, 0]]
+    ids_np, ranges_np = gids.cpu().numpy(), ranges.cpu().numpy()
+    assert_forward_every_pixel(a[0].cpu(), a[1].cpu(), a[2].cpu(), [c.cpu() for c in cols32],
+                               ids_np, ranges_np, w, h, 16, what="image")
 
     g = torch.Generator().manual_seed(3)
     grad_image = torch.rand(h, w, 3, generator=g) * 2 - 1
-    ga = composite_bwd(*args, split_ranges, grad_image.to(device), final_t, ncon, w, h, 16,
-                       THRESHOLD, "gaussian").cpu().double()
-    gb = composite_bwd(*args, one_wave_ranges, grad_image.to(device), final_t, ncon, w, h, 16,
-                       THRESHOLD, "gaussian").cpu().double()
+    # Each shape's backward takes its own forward's outputs (bit-identical to
+    # the op's), so it walks with that forward's hit masks.
+    ga = composite_bwd(*args, split_ranges, grad_image.to(device), a[1], a[2], w, h, 16,
+                       THRESHOLD, "gaussian").cpu()
+    gb = composite_bwd(*args, one_wave_ranges, grad_image.to(device), b[1], b[2], w, h, 16,
+                       THRESHOLD, "gaussian").cpu()
 
     # float64 autograd of the oracle compositor on the GPU's own projected
-    # values and lists (as test_composite_backward_matches_autograd does).
-    leaves = [x.detach().cpu().double().clone().requires_grad_(True) for x in (
-        pmean[:, 0], pmean[:, 1], pinv[:, 0, 0], pinv[:, 0, 1], pinv[:, 1, 1], pcol, pop[:, 0])]
-    exp = orc.composite(*leaves, gids.cpu().numpy(), ranges.cpu().numpy(), w, h, 16, THRESHOLD)
-    (exp.image * grad_image.double()).sum().backward()
-    du, dv, da, db, dc, drgb, dop = (x.grad for x in leaves)
-    expected = torch.stack((du, dv, da, db / 2, dc, drgb[:, 0], drgb[:, 1], drgb[:, 2], dop), -1)
-    good = exp.gaussian_margin >= 1e-5
-    assert float(good.double().mean()) > 0.4
+    # values and lists with the GPU's activity decisions and the float32
+    # oracle's cut/clamp decisions, every Gaussian compared.
+    expected, expected32, margin, _ = fixed_decision_composite_grads(
+        [c.cpu() for c in cols32], ids_np, ranges_np, w, h, 16, ncon.cpu().numpy(), grad_image)
+    explained = margin < DECISION_WINDOW
     for name, got in (("split", ga), ("one wave", gb)):
-        for col in range(9):
-            scale = float(expected[:, col].abs().max())
-            err = (got[good, col] - expected[good, col]).abs()
-            bound = 1e-4 * expected[good, col].abs() + 1e-6 * scale
-            assert not bool((err > bound).any()), (name, col, float(err.max()), scale)
+        stats = assert_gradients_close(got, expected, f"{name} composite_bwd", explained=explained,
+                                       reference32=expected32)
+        print(f"[split] {name}: {stats}", flush=True)

@@ -235,6 +235,22 @@ def test_image_independent_of_tile_size():
         torch.testing.assert_close(im, imgs[0], atol=1e-12, rtol=0)
 
 
+def test_image_without_diagnostics_is_identical():
+    """diagnostics=False (the CPU baseline's timing) leaves the image and its
+    gradients bit for bit unchanged."""
+    params, cam = _scene(n=60, w=40, h=32)
+    leaves = [p.clone().requires_grad_(True) for p in params]
+    a = orc.rasterize(*leaves, cam, tile_size=8, near=0.1)
+    a.image.sum().backward()
+    ga = [p.grad.clone() for p in leaves]
+    for p in leaves:
+        p.grad = None
+    b = orc.rasterize(*leaves, cam, tile_size=8, near=0.1, diagnostics=False)
+    b.image.sum().backward()
+    assert torch.equal(a.image, b.image)
+    assert all(torch.equal(x, p.grad) for x, p in zip(ga, leaves))
+
+
 def test_weights_sum_to_one_minus_transmittance():
     params, cam = _scene(n=60, w=40, h=32)
     mean, rot, scale, op, col = params
@@ -386,8 +402,53 @@ def test_fixed_decisions_replay():
     fewer = np.maximum(c32.n_contributors.numpy() - 1, 0)
     bad, _ = run(torch.float64, decisions=c32.decisions, active_counts=fewer)
     assert float((bad.image - f64.image).detach().abs().max()) > 1e-3
-    with pytest.raises(ValueError):
-        orc.composite(*(x.detach() for x in (
-            proj.mean[:, 0], proj.mean[:, 1], proj.inverse[:, 0, 0], proj.inverse[:, 0, 1],
-            proj.inverse[:, 1, 1], proj.color, proj.opacity[:, 0])), sid, ranges, 48, 32, ts,
-            rendering_mode="ellipsoid", active_counts=fewer)
+
+    # Ellipsoid mode: replaying a float32 run's own decisions reproduces it;
+    # float64 with them equals float64 wherever the indicators agree.
+    cols = [x.detach() for x in (
+        proj.mean[:, 0], proj.mean[:, 1], proj.inverse[:, 0, 0], proj.inverse[:, 0, 1],
+        proj.inverse[:, 1, 1], proj.color, proj.opacity[:, 0])]
+    e32 = orc.composite(*(x.float() for x in cols), sid, ranges, 48, 32, ts,
+                        rendering_mode="ellipsoid", tile_chunk=3)
+    q32 = orc.composite(*(x.float() for x in cols), sid, ranges, 48, 32, ts,
+                        rendering_mode="ellipsoid", tile_chunk=3, decisions=e32.decisions,
+                        active_counts=e32.n_contributors.numpy())
+    assert torch.equal(e32.image, q32.image)
+    e64 = orc.composite(*cols, sid, ranges, 48, 32, ts, rendering_mode="ellipsoid", tile_chunk=3)
+    q64 = orc.composite(*cols, sid, ranges, 48, 32, ts, rendering_mode="ellipsoid", tile_chunk=3,
+                        decisions=e32.decisions, active_counts=e32.n_contributors.numpy())
+    pix = torch.as_tensor(e64.margin >= 1e-5)
+    assert float(pix.double().mean()) > 0.5
+    assert torch.allclose(e64.image[pix], q64.image[pix], rtol=0, atol=1e-12)
+
+
+@pytest.mark.parametrize("tile_size", (4, 16))
+def test_backward_walk_equals_autograd(tile_size):
+    """composite_backward_walk (the Triton backward's back-to-front algorithm,
+    without its 1e-4 floor) equals float64 autograd of composite with the same
+    fixed decisions, for every Gaussian and column; in float32 it stays
+    within float32 rounding of that."""
+    params, cam = _scene(n=120, w=40, h=28, log_scale=-1.7, spread=0.5)
+    proj = orc.project(*params, cam)
+    tw, th = -(-40 // tile_size), -(-28 // tile_size)
+    sid, ranges = _lists(proj, tile_size, tw, th)
+    cols = [proj.mean[:, 0], proj.mean[:, 1], proj.inverse[:, 0, 0], proj.inverse[:, 0, 1],
+            proj.inverse[:, 1, 1], proj.color, proj.opacity[:, 0]]
+    cols = [c.detach() for c in cols]
+    g = torch.rand(28, 40, 3, generator=torch.Generator().manual_seed(4), dtype=torch.float64) * 2 - 1
+    run32 = orc.composite(*(c.float() for c in cols), sid, ranges, 40, 28, tile_size, tile_chunk=5)
+    ncon = run32.n_contributors.numpy()
+    assert int(ncon.max()) > 5 and float(run32.final_transmittance.min()) < 0.2
+    leaves = [c.clone().requires_grad_(True) for c in cols]
+    ref = orc.composite(*leaves, sid, ranges, 40, 28, tile_size, tile_chunk=5,
+                        decisions=run32.decisions, active_counts=ncon)
+    (ref.image * g).sum().backward()
+    du, dv, da, db, dc, drgb, dop = (x.grad for x in leaves)
+    expected = torch.stack((du, dv, da, db / 2, dc, drgb[:, 0], drgb[:, 1], drgb[:, 2], dop), -1)
+    walk = orc.composite_backward_walk(*cols, sid, ranges, 40, 28, tile_size, g, run32.decisions,
+                                       ncon, tile_chunk=5)
+    scale = expected.abs().amax(0).clamp_min(1e-300)
+    assert float(((walk - expected).abs() / scale).max()) < 1e-10
+    walk32 = orc.composite_backward_walk(*(c.float() for c in cols), sid, ranges, 40, 28,
+                                         tile_size, g.float(), run32.decisions, ncon, tile_chunk=5)
+    assert float(((walk32.double() - expected).abs() / scale).max()) < 1e-4

@@ -50,6 +50,11 @@ def parse_args():
              "baked scene, or a .ply), viewed by a fitted 1920x1080 camera",
     )
     ap.add_argument("--tile-size", type=int, default=16)
+    ap.add_argument(
+        "--forward-only", action="store_true",
+        help="time the forward render alone (configs 1 and 2 are forward-only workloads); the "
+             "roofline line is then the forward compositing kernel's",
+    )
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-tiles", type=int, default=128, help="tiles in the CPU baseline sample")
     ap.add_argument("--out", default=None, help="also write the JSON line to this file")
@@ -130,6 +135,8 @@ STAGE_KERNELS = {
     "emit": ["sweep::clear_kernel", "row_bucket_kernel", "sweep::tile_sum_kernel<WidthLoad>",
              "sweep::tile_offsets_kernel", "sweep::scan_kernel<WidthLoad>", "column_count_kernel",
              "column_scan_kernel", "column_bucket_kernel"],
+    # With row/column bucketing the lists leave the emit stage sorted: the
+    # "sort" mark launches nothing and is not reported.
     "sort": [],
     "composite": ["checkpoint_clear_kernel (lists above 8192 entries)", "composite_fwd_kernel"],
     "loss": ["l1_fwd_kernel", "l1_finish_kernel", "l1_bwd_kernel", "torch fill (gradient buffer)"],
@@ -143,6 +150,8 @@ def stage_entries(stages_ms, bytes_model):
     the whole binning (bin + emit) against its own bytes."""
     stages = {}
     for name, ms in stages_ms.items():
+        if not STAGE_KERNELS.get(name, True):
+            continue  # a mark with no kernel of its own (its time joins "binning")
         entry = {"kernels": STAGE_KERNELS.get(name, []), "ms": round(ms, 4)}
         if name in bytes_model and ms > 0:
             gbs = bytes_model[name] / (ms * 1e-3) / 1e9
@@ -159,10 +168,13 @@ def stage_entries(stages_ms, bytes_model):
     return stages
 
 
-def run_step(splats, cam, target, tile_size, near, far):
+def run_step(splats, cam, target, tile_size, near, far, backward=True):
     from gaussian_splats_hip.splats import rasterize
     from gaussian_splats_hip.training import l1_loss
 
+    if not backward:
+        with torch.no_grad():
+            return rasterize(splats, cam, tile_size=tile_size, near=near, far=far)
     image = rasterize(splats, cam, tile_size=tile_size, near=near, far=far)
     loss = l1_loss(image, target)  # mean |image - target|, one fused kernel each way
     loss.backward()
@@ -193,9 +205,9 @@ def stage_marker():
     return mark, times
 
 
-def staged_step(params, cam, target, tile_size, near, far):
-    """One fwd+bwd through the stage functions with timing events around each
-    stage (stage_marker)."""
+def staged_step(params, cam, target, tile_size, near, far, backward=True):
+    """One fwd+bwd (with ``backward``) through the stage functions with timing
+    events around each stage (stage_marker)."""
     from gaussian_splats_hip.kernels.rasterize import composite_bwd, project_and_count, project_bwd
     from gaussian_splats_hip.kernels.rasterize.interface import forward_pipeline
     from gaussian_splats_hip.training import l1_loss_backward, l1_loss_forward
@@ -208,17 +220,18 @@ def staged_step(params, cam, target, tile_size, near, far):
     one = torch.ones((), dtype=torch.float32, device=params[0].device)
     R, t = host_extrinsics(cam)  # host memory: passed to the kernels by value
     out = forward_pipeline(*params, R, t, fx, fy, cx, cy, w, h, tile_size, 0.999, near, far,
-                           "gaussian", 0.95, timer=mark)
+                           "gaussian", 0.95, timer=mark, record_hits=backward)
     image, final_t, ncon, pmean, pinv, pcol, pop, gids, ranges, counts = out
-    _, code = l1_loss_forward(image, target)
-    grad_image = l1_loss_backward(code, one)
-    grad_proj = torch.zeros((pmean.shape[0], 9), dtype=torch.float32, device=pmean.device)
-    mark("loss")
-    composite_bwd(pmean, pinv, pcol, pop, gids, ranges, grad_image, final_t, ncon, w, h,
-                  tile_size, 0.999, "gaussian", out=grad_proj)
-    mark("composite_bwd")
-    project_bwd(*params, R, t, pinv, grad_proj, counts, fx, fy, w, h)
-    mark("project_bwd")
+    if backward:
+        _, code = l1_loss_forward(image, target)
+        grad_image = l1_loss_backward(code, one)
+        grad_proj = torch.zeros((pmean.shape[0], 9), dtype=torch.float32, device=pmean.device)
+        mark("loss")
+        composite_bwd(pmean, pinv, pcol, pop, gids, ranges, grad_image, final_t, ncon, w, h,
+                      tile_size, 0.999, "gaussian", out=grad_proj)
+        mark("composite_bwd")
+        project_bwd(*params, R, t, pinv, grad_proj, counts, fx, fy, w, h)
+        mark("project_bwd")
     torch.cuda.synchronize()
     ms = stage_times()
     # Row-list entries: tile rows covered by the Gaussians with intersections.
@@ -286,7 +299,8 @@ def cpu_config1_full(threads):
     with torch.no_grad():
         for i in range(4):
             t0 = time.perf_counter()
-            orc.rasterize(*scene.params(), ocam, tile_size=16, near=scene.near, far=scene.far)
+            orc.rasterize(*scene.params(), ocam, tile_size=16, near=scene.near, far=scene.far,
+                          diagnostics=False)
             if i > 0:
                 times.append(time.perf_counter() - t0)
     med = sorted(times)[1]
@@ -295,105 +309,201 @@ def cpu_config1_full(threads):
             f"{scene.num_points} Gaussians, SH0, tile 16"}
 
 
-def cpu_baseline(scene, tile_size, sample_tiles):
-    """The CPU oracle (torch-CPU restatement of the reference torch backend) on a
-    bounded sample: full projection + binning of all Gaussians, then dense
-    fwd+bwd compositing of ``sample_tiles`` non-empty tiles, stratified by list
-    length (equal numbers of tiles from each eighth of the non-empty tiles
-    sorted by length, seeded), each stratum timed on its own and its time per
-    tile scaled by the stratum's tile count.  Also: config 1 whole, and the
-    host's CPU and memory."""
+# The CPU baseline runs the whole algorithm up to these sizes and extrapolates
+# beyond them (labelled in its "sample" text).
+CPU_SORT_CAP = 40_000_000  # intersections emitted and sorted whole
+CPU_LIST_CAP = 20_000      # entries of one sampled tile composited whole
+CPU_VIEWS = 2              # views of a multi-view scene timed (the mean is scaled to all)
+
+
+def _cpu_tile_lists(bounds, counts, depth32, tiles, tiles_w):
+    """The (depth bits, index)-ordered lists of the given tiles, straight from
+    the rectangles: (ids, {tile: (start, end)})."""
+    import numpy as np
+
+    bits = np.ascontiguousarray(depth32, dtype=np.float32).view(np.uint32)
+    live = counts > 0
+    x0, x1, y0, y1 = bounds[:, 0, 0], bounds[:, 0, 1], bounds[:, 1, 0], bounds[:, 1, 1]
+    parts, where, pos = [], {}, 0
+    for t in tiles:
+        ty, tx = divmod(int(t), tiles_w)
+        cover = np.nonzero(live & (x0 <= tx) & (tx < x1) & (y0 <= ty) & (ty < y1))[0]
+        ordered = cover[np.lexsort((cover, bits[cover]))].astype(np.int32)
+        parts.append(ordered)
+        where[int(t)] = (pos, pos + ordered.size)
+        pos += ordered.size
+    return (np.concatenate(parts) if parts else np.zeros(0, np.int32)), where
+
+
+def cpu_baseline(scene, tile_size, sample_tiles, cam=None, target=None, backward=True,
+                 with_config1=True):
+    """The CPU oracle (torch-CPU restatement of the reference torch backend,
+    dense per (intersection, pixel), no early exit, without the oracle's
+    parity diagnostics) on a bounded sample of one
+    view's step, timed on all host threads:
+
+    * projection of all Gaussians, and their binning: emission and stable sort
+      of all intersections, or, above CPU_SORT_CAP of them, of a seeded subset
+      of Gaussians holding about CPU_SORT_CAP, its time scaled by I log I;
+    * forward (and, with ``backward``, backward) compositing of
+      ``sample_tiles`` non-empty tiles stratified by list length (equal
+      numbers from each eighth of the tiles sorted by length, seeded), each
+      eighth timed on its own, less the per-call cost that does not scale
+      with the tiles (counted once), and scaled by its tile count.  A list
+      above CPU_LIST_CAP entries is composited to that length and its time
+      scaled by the full length: the dense oracle's work is linear in it;
+    * the projection's backward, once, on the summed gradients.
+
+    Also: config 1 whole (``with_config1``), and the host's CPU and memory."""
     import numpy as np
 
     from oracle import rasterizer as orc
 
     threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
-    cam = scene.cameras[0]
+    cam = cam or scene.cameras[0]
     fx, fy = cam.focal_length
     cx, cy = cam.principal_point
     w, h = cam.image_size
     ocam = orc.Camera(*host_extrinsics(cam), fx, fy, cx, cy, w, h)
-    params = [p.detach().clone().requires_grad_(True) for p in scene.params()]
-    t0 = time.perf_counter()
-    proj = orc.project(*params, ocam)
-    tw, th = -(-w // tile_size), -(-h // tile_size)
-    bounds, counts = orc.tile_counts(proj, tile_size, tw, th, scene.near, scene.far)
-    keys, ids = orc.emit_intersections(bounds, proj.mean[:, 2].detach().numpy(), counts, tw)
-    sid, ranges, _ = orc.sort_intersections(keys, ids, tw * th)
-    t1 = time.perf_counter()
-    # Compositing runs on detached copies of the projected tensors, so each
-    # stratum back-propagates only through its own compositing; the
-    # projection's backward runs once at the end on the summed gradients.
-    leaves = [t.detach().requires_grad_(True)
-              for t in (proj.mean, proj.inverse, proj.color, proj.opacity)]
-    pm, pinv, pcol, pop = leaves
-    rng = np.random.default_rng(0)
-    nonempty = np.nonzero(ranges[:, 1] > ranges[:, 0])[0]
-    lengths = ranges[nonempty, 1] - ranges[nonempty, 0]
-    by_length = nonempty[np.argsort(lengths, kind="stable")]
-    strata = np.array_split(by_length, 8)
-    per = max(1, sample_tiles // len(strata))
+    if target is None:
+        if scene.target is None:  # forward-only scenes: a seeded target of the image's shape
+            target = torch.rand(h, w, 3, generator=torch.Generator().manual_seed(0))
+        else:
+            target = scene.target if scene.target.dim() == 3 else scene.target[0]
+    params = [p.detach().clone().requires_grad_(backward) for p in scene.params()]
+    grad_mode = torch.enable_grad() if backward else torch.no_grad()
+    notes = []
+    with grad_mode:
+        t0 = time.perf_counter()
+        proj = orc.project(*params, ocam)
+        tw, th = -(-w // tile_size), -(-h // tile_size)
+        bounds, counts = orc.tile_counts(proj, tile_size, tw, th, scene.near, scene.far)
+        depth32 = proj.mean[:, 2].detach().float().numpy()
+        t1 = time.perf_counter()
+        project_s = t1 - t0
+        total = int(counts.astype(np.int64).sum())
+        # Per-tile list lengths: a 2-D difference array of the rectangles.
+        diff = np.zeros((th + 1, tw + 1), dtype=np.int64)
+        live = counts > 0
+        b = bounds[live].astype(np.int64)
+        np.add.at(diff, (b[:, 1, 0], b[:, 0, 0]), 1)
+        np.add.at(diff, (b[:, 1, 0], b[:, 0, 1]), -1)
+        np.add.at(diff, (b[:, 1, 1], b[:, 0, 0]), -1)
+        np.add.at(diff, (b[:, 1, 1], b[:, 0, 1]), 1)
+        lengths_all = diff.cumsum(0).cumsum(1)[:th, :tw].reshape(-1)
+        rng = np.random.default_rng(0)
+        tb = time.perf_counter()
+        if total <= CPU_SORT_CAP:
+            keys, ids = orc.emit_intersections(bounds, depth32, counts, tw)
+            sid, ranges, _ = orc.sort_intersections(keys, ids, tw * th)
+            bin_s = time.perf_counter() - tb
+            notes.append(f"binning of all {total} intersections ({bin_s:.1f}s)")
+            lists = None
+        else:
+            subset = rng.random(counts.size) < CPU_SORT_CAP / total
+            sub_counts = np.where(subset, counts, 0)
+            sub_total = int(sub_counts.astype(np.int64).sum())
+            keys, ids = orc.emit_intersections(bounds, depth32, sub_counts, tw)
+            orc.sort_intersections(keys, ids, tw * th)
+            del keys, ids
+            sub_s = time.perf_counter() - tb
+            bin_s = sub_s * (total / sub_total) * (math.log(total) / math.log(sub_total))
+            notes.append(f"binning of a seeded subset of {sub_total} of the {total} "
+                         f"intersections ({sub_s:.1f}s), scaled by I log I to {bin_s:.1f}s")
+            lists = True
+        leaves = [t.detach().requires_grad_(backward)
+                  for t in (proj.mean, proj.inverse, proj.color, proj.opacity)]
+        pm, pinv, pcol, pop = leaves
+        nonempty = np.nonzero(lengths_all > 0)[0]
+        by_length = nonempty[np.argsort(lengths_all[nonempty], kind="stable")]
+        strata = np.array_split(by_length, 8)
+        per = max(1, sample_tiles // len(strata))
+        chosen_all = [rng.choice(st, size=min(per, len(st)), replace=False) if len(st) else st
+                      for st in strata]
+        if lists:
+            picked = np.concatenate([c for c in chosen_all if len(c)])
+            sid, where = _cpu_tile_lists(bounds, counts, depth32, picked, tw)
+        else:
+            where = {int(t): (int(ranges[t, 0]), int(ranges[t, 1])) for t in nonempty}
 
-    def mask_of(tiles):
-        mask = torch.zeros(th * tile_size, tw * tile_size)
-        for t in tiles:
-            ty, tx = divmod(int(t), tw)
-            mask[ty * tile_size:(ty + 1) * tile_size, tx * tile_size:(tx + 1) * tile_size] = 1
-        return mask[:h, :w, None]
+        def mask_of(tiles):
+            mask = torch.zeros(th * tile_size, tw * tile_size)
+            for t in tiles:
+                ty, tx = divmod(int(t), tw)
+                mask[ty * tile_size:(ty + 1) * tile_size, tx * tile_size:(tx + 1) * tile_size] = 1
+            return mask[:h, :w, None]
 
-    # The per-call cost that does not scale with the tiles (image-sized
-    # buffers, the chunk loop, the loss): one call with every list empty; it
-    # is taken off each stratum's time before scaling and counted once.
-    empty = ranges.copy()
-    empty[:, 1] = empty[:, 0]
-    te0 = time.perf_counter()
-    with torch.no_grad():
-        comp = orc.composite(pm[:, 0], pm[:, 1], pinv[:, 0, 0], pinv[:, 0, 1], pinv[:, 1, 1],
-                             pcol, pop[:, 0], sid, empty, w, h, tile_size, tile_chunk=8)
-        ((comp.image - scene.target).abs() * mask_of([])).sum()
-    fixed_s = time.perf_counter() - te0
-    composite_s = fixed_s
-    sampled_tiles = 0
-    for stratum in strata:
-        if len(stratum) == 0:
-            continue
-        chosen = rng.choice(stratum, size=min(per, len(stratum)), replace=False)
-        keep = np.zeros(tw * th, dtype=bool)
-        keep[chosen] = True
-        sampled = ranges.copy()
-        sampled[~keep] = sampled[~keep, :1]  # empty the other tiles
-        ts0 = time.perf_counter()
-        comp = orc.composite(pm[:, 0], pm[:, 1], pinv[:, 0, 0], pinv[:, 0, 1], pinv[:, 1, 1],
-                             pcol, pop[:, 0], sid, sampled, w, h, tile_size, tile_chunk=8)
-        loss = ((comp.image - scene.target).abs() * mask_of(chosen)).sum() / (w * h * 3)
-        loss.backward()
-        dt = max(time.perf_counter() - ts0 - fixed_s, 0.0)
-        composite_s += dt / len(chosen) * len(stratum)
-        sampled_tiles += len(chosen)
-    t2 = time.perf_counter()
-    outs = [(o, l.grad) for o, l in zip((proj.mean, proj.inverse, proj.color, proj.opacity), leaves)
-            if l.grad is not None and o.requires_grad]
-    torch.autograd.backward([o for o, _ in outs], [g for _, g in outs])
-    t3 = time.perf_counter()
-    full_s = (t1 - t0) + composite_s + (t3 - t2)
-    return {
+        def run(tiles, cap):
+            """Composites the tiles' lists (each cut at cap entries) and the
+            loss on their pixels; returns the scale full / composited."""
+            sub = np.zeros((tw * th, 2), dtype=np.int64)
+            pieces, pos, full, done = [], 0, 0, 0
+            for t in tiles:
+                s0, e0 = where[int(t)]
+                e = min(e0, s0 + cap)
+                pieces.append(sid[s0:e])
+                sub[int(t)] = (pos, pos + e - s0)
+                pos += e - s0
+                full += e0 - s0
+                done += e - s0
+            ids_sub = np.concatenate(pieces) if pieces else np.zeros(0, np.int32)
+            comp = orc.composite(pm[:, 0], pm[:, 1], pinv[:, 0, 0], pinv[:, 0, 1],
+                                 pinv[:, 1, 1], pcol, pop[:, 0], ids_sub, sub, w, h, tile_size,
+                                 tile_chunk=8, diagnostics=False)
+            loss = ((comp.image - target).abs() * mask_of(tiles)).sum() / (w * h * 3)
+            if backward:
+                loss.backward()
+            return full / max(done, 1)
+
+        # The per-call cost that does not scale with the tiles (image-sized
+        # buffers, the chunk loop, the loss): one call with every list empty.
+        tc0 = te0 = time.perf_counter()
+        with torch.no_grad():
+            run([], CPU_LIST_CAP)
+        fixed_s = time.perf_counter() - te0
+        composite_s = fixed_s
+        sampled, scaled = 0, 0
+        for stratum, chosen in zip(strata, chosen_all):
+            if len(stratum) == 0:
+                continue
+            ts0 = time.perf_counter()
+            factor = run(chosen, CPU_LIST_CAP)
+            dt = max(time.perf_counter() - ts0 - fixed_s, 0.0) * factor
+            composite_s += dt / len(chosen) * len(stratum)
+            sampled += len(chosen)
+            scaled += int(factor > 1.0)
+        t2 = time.perf_counter()
+        if backward:
+            outs = [(o, l.grad) for o, l in zip(
+                (proj.mean, proj.inverse, proj.color, proj.opacity), leaves)
+                if l.grad is not None and o.requires_grad]
+            torch.autograd.backward([o for o, _ in outs], [g for _, g in outs])
+        t3 = time.perf_counter()
+    full_s = project_s + bin_s + composite_s + (t3 - t2)
+    what = "fwd+bwd" if backward else "forward"
+    notes.append(
+        f"dense {what} compositing of {sampled} non-empty {tile_size}px tiles, {per} from each "
+        f"eighth of the tiles by list length ({t2 - tc0:.1f}s), each eighth's time per tile (less the {fixed_s:.2f}s per call that "
+        f"does not scale with the tiles, counted once) scaled to its {len(nonempty) // 8}-odd "
+        f"tiles" + (f"; {scaled} eighths held lists above {CPU_LIST_CAP} entries, composited to "
+                    f"that length and scaled linearly by their full length" if scaled else ""))
+    if backward:
+        notes.append(f"the projection backward ({t3 - t2:.1f}s)")
+    out = {
         "value": (w * h) / 1e6 / full_s,
         "unit": "Mpix/s",
         "cores": threads,
         "kind": "port",
-        "sample": (
-            f"torch-CPU oracle, float32: projection+binning of all {scene.num_points} Gaussians "
-            f"({t1 - t0:.1f}s) + dense fwd+bwd compositing of {sampled_tiles} non-empty "
-            f"{tile_size}px tiles, {per} from each eighth of the tiles by list length "
-            f"({t2 - t1:.1f}s), each eighth's time per tile (less the {fixed_s:.2f}s per call "
-            f"that does not scale with the tiles, counted once) scaled to its "
-            f"{len(nonempty) // 8}-odd tiles + the projection backward ({t3 - t2:.1f}s); "
-            f"estimate {full_s:.1f}s per step"
-        ),
+        "s_per_view": round(full_s, 2),
+        "sample": (f"torch-CPU oracle, float32, one view of {scene.num_points} Gaussians: "
+                   f"projection ({project_s:.1f}s) + " + " + ".join(notes)
+                   + f"; estimate {full_s:.1f}s per view"),
         "host": host_description(),
-        "config1_full": cpu_config1_full(threads),
     }
+    if with_config1:
+        out["config1_full"] = cpu_config1_full(threads)
+    return out
 
 
 def views_stage_bytes(n, k, views, total, rows, pixels, processed_fwd, processed_bwd):
@@ -545,6 +655,27 @@ def bench_views(args, scene):
         },
         "cpu_baseline": None,
     }
+    if not args.no_cpu_baseline:
+        # Views are independent on the CPU path (the reference renders one
+        # camera per call): time CPU_VIEWS of them, each on its own sample,
+        # and scale their mean time to all views.
+        print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
+        picked = list(range(0, views, max(1, views // CPU_VIEWS)))[:CPU_VIEWS]
+        per_view = [cpu_baseline(scene, tile, max(8, args.cpu_tiles // len(picked)), cam=cams[v],
+                                 target=scene.target[v], with_config1=(i == 0))
+                    for i, v in enumerate(picked)]
+        seconds = sum(p["s_per_view"] for p in per_view) / len(per_view) * views
+        cpu = dict(per_view[0])
+        cpu.update({
+            "value": views * w * h / 1e6 / seconds,
+            "s_per_step": round(seconds, 1),
+            "sample": (f"views {picked} of {views}, each: " + per_view[0]["sample"]
+                       + f"; the views' mean time scaled to all {views} views: "
+                       f"{seconds:.1f}s per step"),
+            "views_timed": [{"view": v, "s": p["s_per_view"]} for v, p in zip(picked, per_view)],
+        })
+        cpu.pop("s_per_view", None)
+        result["cpu_baseline"] = cpu
     line = json.dumps(result)
     print(line, flush=True)
     if args.out:
@@ -768,21 +899,26 @@ def main():
     params = [splats.mean.detach(), splats.rotation.detach(), splats.scale.detach(),
               splats.opacity.detach(), splats.color.detach()]
 
-    print(f"[bench] {scene.name}: N={scene.num_points} {w}x{h} tile={args.tile_size}", file=sys.stderr, flush=True)
+    backward = not args.forward_only
+    print(f"[bench] {scene.name}: N={scene.num_points} {w}x{h} tile={args.tile_size}"
+          f"{'' if backward else ' forward only'}", file=sys.stderr, flush=True)
     for _ in range(args.warmup):
         for p in splats.parameters():
             p.grad = None
-        run_step(splats, cam, target, args.tile_size, scene.near, scene.far)
+        run_step(splats, cam, target, args.tile_size, scene.near, scene.far, backward)
     torch.cuda.synchronize()
     print("[bench] warmup done", file=sys.stderr, flush=True)
 
     torch.cuda.synchronize()
-    with _native.LaunchTimer("composite_bwd", capacity=args.steps + 1) as timer:
+    # The dominant kernel, timed per launch with events on its stream: the
+    # compositing backward, or the forward compositing for a forward step.
+    dominant = "composite_bwd" if backward else "composite"
+    with _native.LaunchTimer(dominant, capacity=args.steps + 1) as timer:
         t0 = time.perf_counter()
         for _ in range(args.steps):
             for p in splats.parameters():
                 p.grad = None
-            run_step(splats, cam, target, args.tile_size, scene.near, scene.far)
+            run_step(splats, cam, target, args.tile_size, scene.near, scene.far, backward)
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
     ms_per_step = 1e3 * elapsed / args.steps
@@ -796,13 +932,14 @@ def main():
         for _ in range(args.steps):
             for p in splats.parameters():
                 p.grad = None
-            run_step(splats, cam, target, args.tile_size, scene.near, scene.far)
+            run_step(splats, cam, target, args.tile_size, scene.near, scene.far, backward)
         torch.cuda.synchronize()
 
     # Per-stage event timing (averaged over a few staged steps).
     stage_runs = []
     for _ in range(3):
-        ms, info = staged_step(params, cam, target, args.tile_size, scene.near, scene.far)
+        ms, info = staged_step(params, cam, target, args.tile_size, scene.near, scene.far,
+                               backward)
         stage_runs.append(ms)
     stages_ms = {k: sum(r[k] for r in stage_runs) / len(stage_runs) for k in stage_runs[0]}
     fwd_pairs, bwd_pairs = processed_pairs(info["ranges"], info["ncon"], args.tile_size, w, h)
@@ -810,14 +947,15 @@ def main():
                               w * h, fwd_pairs, bwd_pairs)
     stages = stage_entries(stages_ms, bytes_model)
 
-    # Dominant kernel: composite_bwd_kernel, timed per launch with HIP events
-    # on its stream during the timed steps.
+    # Dominant kernel, timed per launch with HIP events on its stream during
+    # the timed steps.
     dominant_ms = timer.mean_ms()
-    achieved = bytes_model["composite_bwd"] / (dominant_ms * 1e-3) / 1e9
+    achieved = bytes_model[dominant] / (dominant_ms * 1e-3) / 1e9
     traffic = None
     valu = None
     traffic_file = ROOT / "profiles" / "traffic_composite_bwd_config3.json"
-    if traffic_file.exists() and args.config == "config3" and args.tile_size == 16:
+    if (traffic_file.exists() and args.config == "config3" and args.tile_size == 16
+            and backward and not args.scene):
         measured = json.loads(traffic_file.read_text())
         traffic = measured["hbm_bytes_per_launch"]
         if "valu" in measured:
@@ -832,16 +970,20 @@ def main():
             valu = {"valu_busy_measured": m["valu_busy"], "formula": m["formula"],
                     "instructions": insts, "issue_ms_at_4_cycles": round(issue_ms, 4),
                     "issue_frac": round(issue_ms / dominant_ms, 4)}
+    # The bound is the resource the kernel saturates: VALU issue when its
+    # measured VALU busy exceeds 90%, else HBM; frac stays the HBM fraction.
+    bound = "valu" if valu is not None and valu["valu_busy_measured"] > 0.9 else "hbm"
+    kernel = "composite_bwd_kernel" if backward else "composite_fwd_kernel"
     roofline = {
-        "kernel": "composite_bwd_kernel<16>" if args.tile_size == 16 else "composite_bwd_kernel",
-        "bound": "hbm",
+        "kernel": f"{kernel}<{args.tile_size}>",
+        "bound": bound,
         "achieved": round(achieved, 1),
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
         "traffic": traffic,
         "launch_ms": round(dominant_ms, 4),
-        "algorithmic_bytes": bytes_model["composite_bwd"],
+        "algorithmic_bytes": bytes_model[dominant],
         "valu_issue": valu,
     }
 
@@ -860,10 +1002,12 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
-        cpu = cpu_baseline(scene, args.tile_size, args.cpu_tiles)
+        cpu = cpu_baseline(scene, args.tile_size, args.cpu_tiles, target=target.cpu(),
+                           backward=backward)
 
     result = {
-        "metric": "fwd+bwd Mpix/s at 1M Gaussians SH3 1080p",
+        "metric": ("fwd+bwd Mpix/s at 1M Gaussians SH3 1080p" if backward
+                   else "fwd Mpix/s (forward-only workload)"),
         "value": round(mpix / (ms_per_step * 1e-3), 3),
         "unit": "Mpix/s",
         "n_gpus": 1,
@@ -877,7 +1021,8 @@ def main():
         "data": "synthetic (seeded scenes.CONFIGS distributions)",
         "config": {
             "workload": (f"{scene.name}: {scene.num_points} Gaussians, "
-                         f"SH{math.isqrt(scene.color.shape[1]) - 1}, {w}x{h}, fwd+bwd, L1 loss"),
+                         f"SH{math.isqrt(scene.color.shape[1]) - 1}, {w}x{h}, "
+                         + ("fwd+bwd, L1 loss" if backward else "forward")),
             "tile_size": args.tile_size,
             "intersections": info["total"],
         },

@@ -92,12 +92,12 @@ def composite(
     hits = (nat.hit_mask_buffer(view, gaussian_ids.numel(), device)
             if record_hits and rendering_mode == "gaussian" else None)
     nat.check(
-        nat.library().gs_composite(
+        nat.launch("composite", lambda: nat.library().gs_composite(
             nat.ptr(records), records.shape[0], nat.ptr(gaussian_ids), gaussian_ids.numel(),
             nat.ptr(ranges), nat.ptr(order), view, nat.ptr(image), nat.ptr(final_transmittance),
             nat.ptr(n_contributors), nat.ptr(checkpoints), nat.buffer_bytes(checkpoints),
             nat.ptr(hits), nat.buffer_bytes(hits), nat.stream(device),
-        ),
+        )),
         "composite",
     )
     # The backward of this walk starts its segment walks at the checkpoints

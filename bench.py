@@ -434,9 +434,10 @@ def cpu_baseline(scene, tile_size, sample_tiles, cam=None, target=None, backward
                 mask[ty * tile_size:(ty + 1) * tile_size, tx * tile_size:(tx + 1) * tile_size] = 1
             return mask[:h, :w, None]
 
-        def run(tiles, cap):
+        def run(tiles, cap, grad=backward):
             """Composites the tiles' lists (each cut at cap entries) and the
-            loss on their pixels; returns the scale full / composited."""
+            loss on their pixels (back-propagated with ``grad``); returns the
+            scale full / composited."""
             sub = np.zeros((tw * th, 2), dtype=np.int64)
             pieces, pos, full, done = [], 0, 0, 0
             for t in tiles:
@@ -452,7 +453,7 @@ def cpu_baseline(scene, tile_size, sample_tiles, cam=None, target=None, backward
                                  pinv[:, 1, 1], pcol, pop[:, 0], ids_sub, sub, w, h, tile_size,
                                  tile_chunk=8, diagnostics=False)
             loss = ((comp.image - target).abs() * mask_of(tiles)).sum() / (w * h * 3)
-            if backward:
+            if grad:
                 loss.backward()
             return full / max(done, 1)
 
@@ -460,7 +461,7 @@ def cpu_baseline(scene, tile_size, sample_tiles, cam=None, target=None, backward
         # buffers, the chunk loop, the loss): one call with every list empty.
         tc0 = te0 = time.perf_counter()
         with torch.no_grad():
-            run([], CPU_LIST_CAP)
+            run([], CPU_LIST_CAP, grad=False)
         fixed_s = time.perf_counter() - te0
         composite_s = fixed_s
         sampled, scaled = 0, 0
@@ -486,7 +487,7 @@ def cpu_baseline(scene, tile_size, sample_tiles, cam=None, target=None, backward
         f"dense {what} compositing of {sampled} non-empty {tile_size}px tiles, {per} from each "
         f"eighth of the tiles by list length ({t2 - tc0:.1f}s), each eighth's time per tile (less the {fixed_s:.2f}s per call that "
         f"does not scale with the tiles, counted once) scaled to its {len(nonempty) // 8}-odd "
-        f"tiles" + (f"; {scaled} eighths held lists above {CPU_LIST_CAP} entries, composited to "
+        f"tiles" + (f"; {scaled} of the eighths held lists above {CPU_LIST_CAP} entries, composited to "
                     f"that length and scaled linearly by their full length" if scaled else ""))
     if backward:
         notes.append(f"the projection backward ({t3 - t2:.1f}s)")

@@ -262,12 +262,14 @@ def test_sampled_tiles_composite_backward(device, name):
     assert touched > 1000, touched
 
 
-def test_config3_op_backward(device):
+@pytest.mark.parametrize("name", ("config3", "config4"))
+def test_op_backward(device, name):
     """The op end to end (projection, binning, compositing, both backward
-    kernels) on config 3 with the mean-L1 loss restricted to the sampled
-    tiles, against float64 autograd of the oracle rasterizer along the GPU's
-    lists with fixed decisions."""
-    r = single_view("config3", device)
+    kernels; on config 4 with the long-list checkpoints and segment walks)
+    with the mean-L1 loss restricted to the sampled tiles, against float64
+    autograd of the oracle rasterizer along the GPU's lists with fixed
+    decisions (reference interface.py:176-239)."""
+    r = single_view(name, device)
     scene = r["scene"]
     cam = scene.cameras[0]
     fx, fy = cam.focal_length
@@ -285,16 +287,16 @@ def test_config3_op_backward(device):
     ncon_h = ncon.cpu().numpy()
     limits = {t: m + 1 for t, m in tile_max(ncon_h, tiles, r["tw"], TILE).items()}
     ids, rng = restrict_lists(gids.cpu().numpy(), granges.cpu().numpy(), tiles, limits)
-    log("config3 op: oracle projection of all Gaussians + compositing of", len(ids), "entries")
+    log(f"{name} op: oracle projection of all Gaussians + compositing of", len(ids), "entries")
     cols32 = (pm[:, 0], pm[:, 1], pinv[:, 0, 0], pinv[:, 0, 1], pinv[:, 1, 1], pcol, pop[:, 0])
     g64, g32, margin = fixed_decision_rasterize_grads(
         scene.params(), oracle_camera(cam), TILE, scene.near, scene.far, (ids, rng), cols32, ncon_h,
         weights.cpu(), tile_chunk=CHUNK)
     explained = margin < DECISION_WINDOW
-    for name, a, e, e32 in zip(("mean", "rotation", "scale", "opacity", "color"), actual, g64, g32):
-        stats = assert_gradients_close(a, e, f"config3 grad {name}", explained=explained,
+    for param, a, e, e32 in zip(("mean", "rotation", "scale", "opacity", "color"), actual, g64, g32):
+        stats = assert_gradients_close(a, e, f"{name} grad {param}", explained=explained,
                                        reference32=e32)
-        log("config3 op grad", name, stats)
+        log(f"{name} op grad", param, stats)
 
 
 def test_config3_project_bwd(device):

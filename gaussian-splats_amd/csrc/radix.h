@@ -117,19 +117,27 @@ void dispatch_scatter(int bits, const K* kin, const uint32_t* vin, K* kout, uint
 // SPREAD: the keys are depth keys (see hist_kernel).  gather_out (optional):
 // the last pass also writes gather_out[i] = gather_src[vals_final[i]], after
 // `stream` has waited for `gather_ready` (an event that gather_src's producer
-// recorded before this call), so the earlier passes do not wait for it.
-template <typename K, bool SPREAD = false>
+// recorded before the wait is enqueued), so the earlier passes do not wait
+// for it.  before_passes() is called on the host after the histogram is
+// enqueued and before the first pass (it may enqueue work on another stream
+// and record gather_ready there): the caller's stream has the histogram to
+// run while the host enqueues it.
+struct NoHook {
+  int operator()() const { return GS_OK; }
+};
+template <typename K, bool SPREAD = false, typename BeforePasses = NoHook>
 int radix_sort(K* keys, const uint32_t* vals, int64_t n, int end_bit, uint32_t* vals_final,
                K** keys_final, const Scratch& ws, hipStream_t s,
                const uint32_t* gather_src = nullptr, uint32_t* gather_out = nullptr,
-               hipEvent_t gather_ready = nullptr) {
+               hipEvent_t gather_ready = nullptr, BeforePasses before_passes = BeforePasses{}) {
   GS_REQUIRE(n < (int64_t(1) << 32) - kTile, GS_ERR_OVERFLOW, "too many elements to sort (%lld)",
              (long long)n);
   *keys_final = keys;
-  if (n == 0) return GS_OK;
+  if (n == 0) return before_passes();
   const sweep::Plan plan = sweep::make_plan(end_bit);
   const int hist_blocks = int(std::min<int64_t>(1024, ceil_div(n, kBlock * 16)));
   sweep::hist_kernel<K, SPREAD><<<unsigned(hist_blocks), kBlock, 0, s>>>(keys, n, plan, ws.hist());
+  GS_TRY(before_passes());
   K* kbuf[2] = {static_cast<K*>(ws.keys_alt), keys};
   const K* kin = keys;
   const uint32_t* vin = vals;

@@ -636,13 +636,16 @@ __device__ int load_window(const uint32_t* __restrict__ offs, int64_t first, int
   if (span > kTile && threadIdx.x == 0) atomicOr(err, kDeviceFlagWindow);
   const int m = int(min(max(span, int64_t(1)), int64_t(kTile)));
   // All of the thread's loads are issued before the first store (indices
-  // clamped into the window, so every load is in bounds).
+  // clamped into the window, so every load is in bounds), for the window's
+  // rounds of kBlock owners only.
+  const int rounds = (m + kBlock - 1) / kBlock;  // workgroup-uniform
   uint32_t v[kTile / kBlock];
 #pragma unroll
   for (int j = 0; j < kTile / kBlock; ++j)
-    v[j] = offs[first + min(int(threadIdx.x) + j * kBlock, m - 1)];
+    if (j < rounds) v[j] = offs[first + min(int(threadIdx.x) + j * kBlock, m - 1)];
 #pragma unroll
   for (int j = 0; j < kTile / kBlock; ++j) {
+    if (j >= rounds) break;
     const int k = int(threadIdx.x) + j * kBlock;
     if (k < m) rel[k] = int32_t(v[j] - c0);
   }
@@ -804,19 +807,25 @@ __global__ __launch_bounds__(kBlock) void column_count_kernel(
   const int64_t span = win.last - win.first + 1;
   if (span > kTile && threadIdx.x == 0) atomicOr(err, kDeviceFlagWindow);
   const int m = int(min(max(span, int64_t(1)), int64_t(kTile)));
-  // All of the thread's loads are issued before the first LDS update.
+  // All of the thread's loads are issued before the first LDS update, for
+  // the window's rounds of kBlock entries only (a window of wide entries
+  // holds a few hundred: config 4 ~360, config 3 ~730).
   constexpr int J = kTile / kBlock;
+  const int rounds = (m + kBlock - 1) / kBlock;  // workgroup-uniform
   uint32_t xw[J], s0[J];
 #pragma unroll
   for (int j = 0; j < J; ++j) {
-    const int64_t k = win.first + min(int(threadIdx.x) + j * kBlock, m - 1);
-    xw[j] = rl_xw[k];
-    s0[j] = W[k];
+    if (j < rounds) {
+      const int64_t k = win.first + min(int(threadIdx.x) + j * kBlock, m - 1);
+      xw[j] = rl_xw[k];
+      s0[j] = W[k];
+    }
   }
   __syncthreads();
   const uint32_t end = win.c0 + win.nvalid;
 #pragma unroll
   for (int j = 0; j < J; ++j) {
+    if (j >= rounds) break;
     if (int(threadIdx.x) + j * kBlock >= m) continue;
     const uint32_t w = entry_width(xw[j]), x0 = entry_x0(xw[j]);
     const uint32_t lo = max(s0[j], win.c0), hi = min(s0[j] + w, end);
@@ -1098,55 +1107,62 @@ GS_API int gs_bin_tiles_plan(uint32_t* depth_keys, const int32_t* bounds, const 
   GS_TRY(device_flags(s, &flags));
   // The tile tables need only the rectangles: they run on the side stream
   // while the depth sort and the row-list offset scan run on the caller's.
+  // The sort's clear and histogram are enqueued first, so the caller's
+  // stream has work while the host enqueues the side stream's.
   SideFork fork;
   GS_TRY(fork_side_stream(s, fork));
   const int words = (tiles_h + 1) * (tiles_w + 1);
-  sweep::clear_kernel<<<unsigned(std::max<int64_t>(1, std::min<int64_t>(256, ceil_div(p.table_words, kBlock)))),
-                        kBlock, 0, fork.side>>>(reinterpret_cast<uint64_t*>(p.table),
-                                                p.table_words, nullptr, 0);
-  if (n > 0) {
-    const unsigned blocks = unsigned(std::min<int64_t>(256, std::max<int64_t>(1, ceil_div(n, 4096))));
-    int32_t* diff2 = p.table;
-    int32_t* rowdiff = p.table + words;
-    if (words + tiles_h + 1 <= kPrivateTableWords) {
-      rect_diff_kernel<<<blocks, 256, size_t(words + tiles_h + 1) * 4, fork.side>>>(
-          reinterpret_cast<const int4*>(bounds), counts, n, tiles_w, tiles_h, diff2, rowdiff,
-          p.packed);
-    } else {
-      // Contiguous chunks with private corner windows (see the kernel).
-      const int64_t wblocks = std::min<int64_t>(512, std::max<int64_t>(1, ceil_div(n, 16384)));
-      const int64_t chunk = ceil_div(n, wblocks);
-      rect_diff_window_kernel<<<unsigned(ceil_div(n, chunk)), 256,
-                                size_t(kPrivateTableWords + tiles_h + 1) * 4, fork.side>>>(
-          reinterpret_cast<const int4*>(bounds), counts, n, chunk, tiles_w, tiles_h, diff2,
-          rowdiff, p.packed);
+  auto side_work = [&]() -> int {
+    sweep::clear_kernel<<<unsigned(std::max<int64_t>(1, std::min<int64_t>(256, ceil_div(p.table_words, kBlock)))),
+                          kBlock, 0, fork.side>>>(reinterpret_cast<uint64_t*>(p.table),
+                                                  p.table_words, nullptr, 0);
+    if (n > 0) {
+      const unsigned blocks = unsigned(std::min<int64_t>(256, std::max<int64_t>(1, ceil_div(n, 4096))));
+      int32_t* diff2 = p.table;
+      int32_t* rowdiff = p.table + words;
+      if (words + tiles_h + 1 <= kPrivateTableWords) {
+        rect_diff_kernel<<<blocks, 256, size_t(words + tiles_h + 1) * 4, fork.side>>>(
+            reinterpret_cast<const int4*>(bounds), counts, n, tiles_w, tiles_h, diff2, rowdiff,
+            p.packed);
+      } else {
+        // Contiguous chunks with private corner windows (see the kernel).
+        const int64_t wblocks = std::min<int64_t>(512, std::max<int64_t>(1, ceil_div(n, 16384)));
+        const int64_t chunk = ceil_div(n, wblocks);
+        rect_diff_window_kernel<<<unsigned(ceil_div(n, chunk)), 256,
+                                  size_t(kPrivateTableWords + tiles_h + 1) * 4, fork.side>>>(
+            reinterpret_cast<const int4*>(bounds), counts, n, chunk, tiles_w, tiles_h, diff2,
+            rowdiff, p.packed);
+      }
     }
-  }
-  // The row-list scan on the caller's stream reads the packed rectangles.
-  int status = n > 0 ? record_side_mark(fork) : GS_OK;
-  const int lds_words = tiles_h * (tiles_w + 1);
-  if (lds_words <= kPrivateTableWords) {
-    tables_kernel<true><<<1, 256, size_t(lds_words) * 4, fork.side>>>(
-        p.table, p.table + words, tiles_w, tiles_h, ranges, p.row_a, p.row_e, p.row_blk, totals);
-  } else {
-    // In global memory every step waits on memory: 16 waves instead of 4
-    // (config 5: 200 x 200 tiles, 330 -> 120 us).
-    tables_kernel<false, 1024><<<1, 1024, 0, fork.side>>>(p.table, p.table + words, tiles_w,
-                                                          tiles_h, ranges, p.row_a, p.row_e,
-                                                          p.row_blk, totals);
-  }
-  if (status == GS_OK) status = check_launch("bin_tiles_plan (tables)");
-  // The totals, then the sticky check-failure word beside them (its low
-  // half; the caller keeps the high half zero).
-  if (host_totals && status == GS_OK &&
-      (hipMemcpyAsync(host_totals, totals, 4 * sizeof(int64_t), hipMemcpyDeviceToHost,
-                      fork.side) != hipSuccess ||
-       hipMemcpyAsync(host_totals + 4, flags, sizeof(uint32_t), hipMemcpyDeviceToHost,
-                      fork.side) != hipSuccess)) {
-    set_error("bin_tiles_plan: copy of the totals failed");
-    status = GS_ERR_HIP;
-  }
-  if (n > 0 && status == GS_OK) {
+    // The depth sort's last pass and the row-list scan read the packed
+    // rectangles: they wait for this mark.
+    int st = n > 0 ? record_side_mark(fork) : GS_OK;
+    const int lds_words = tiles_h * (tiles_w + 1);
+    if (lds_words <= kPrivateTableWords) {
+      tables_kernel<true><<<1, 256, size_t(lds_words) * 4, fork.side>>>(
+          p.table, p.table + words, tiles_w, tiles_h, ranges, p.row_a, p.row_e, p.row_blk, totals);
+    } else {
+      // In global memory every step waits on memory: 16 waves instead of 4
+      // (config 5: 200 x 200 tiles, 330 -> 120 us).
+      tables_kernel<false, 1024><<<1, 1024, 0, fork.side>>>(p.table, p.table + words, tiles_w,
+                                                            tiles_h, ranges, p.row_a, p.row_e,
+                                                            p.row_blk, totals);
+    }
+    if (st == GS_OK) st = check_launch("bin_tiles_plan (tables)");
+    // The totals, then the sticky check-failure word beside them (its low
+    // half; the caller keeps the high half zero).
+    if (host_totals && st == GS_OK &&
+        (hipMemcpyAsync(host_totals, totals, 4 * sizeof(int64_t), hipMemcpyDeviceToHost,
+                        fork.side) != hipSuccess ||
+         hipMemcpyAsync(host_totals + 4, flags, sizeof(uint32_t), hipMemcpyDeviceToHost,
+                        fork.side) != hipSuccess)) {
+      set_error("bin_tiles_plan: copy of the totals failed");
+      st = GS_ERR_HIP;
+    }
+    return st;
+  };
+  int status = GS_OK;
+  if (n > 0) {
     Scratch ws = carve(p.sort_ws, n, 4, 32, n);
     ws.flags = flags;
     clear(ws, s);
@@ -1156,13 +1172,15 @@ GS_API int gs_bin_tiles_plan(uint32_t* depth_keys, const int32_t* bounds, const 
     // stream has written them (mark above).
     status = radix_sort<uint32_t, true>(depth_keys, nullptr, n, 32,
                                         reinterpret_cast<uint32_t*>(p.order), &sorted_keys, ws, s,
-                                        p.packed, p.packed_sorted, fork.mark);
+                                        p.packed, p.packed_sorted, fork.mark, side_work);
     // Row-list offsets in depth order, recording each pass-A workgroup's
     // first owner; they read the packed rectangles written on the side stream.
     if (status == GS_OK) status = wait_side_mark(fork);
     if (status == GS_OK)
       launch_scan<uint32_t>(HeightLoad{p.packed_sorted}, n, p.offs, true, true, ws, s,
                             HeightSink{p.first_a, p.first_a_capacity});
+  } else {
+    status = side_work();
   }
   // Always join, also after an error; with host_totals the host waits for
   // the tables only, while the sort keeps running on the caller's stream.

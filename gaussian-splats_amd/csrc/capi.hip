@@ -66,8 +66,10 @@ struct SideStream {
   hipEvent_t mark = nullptr;
   hipEvent_t join = nullptr;
 };
-SideStream g_side[kMaxDevices];
-std::mutex g_side_mutex;
+// Per thread: a thread's fork-to-join sequence uses its own stream and
+// events, so no lock is held across the host wait of a join (threads that
+// end leave their streams to the process's end).
+thread_local SideStream g_side[kMaxDevices];
 }  // namespace
 
 int stream_device(hipStream_t stream, int* device) {
@@ -84,7 +86,6 @@ int stream_device(hipStream_t stream, int* device) {
 int fork_side_stream(hipStream_t main, SideFork& f) {
   int device = 0;
   GS_TRY(stream_device(main, &device));
-  f.lock = std::unique_lock<std::mutex>(g_side_mutex);
   SideStream& s = g_side[device];
   if (!s.stream) {
     int current = 0;
@@ -125,7 +126,6 @@ int join_side_stream(SideFork& f, bool host_wait) {
   bool ok = hipEventRecord(f.join, f.side) == hipSuccess &&
             hipStreamWaitEvent(f.main, f.join, 0) == hipSuccess;
   if (ok && host_wait) ok = hipEventSynchronize(f.join) == hipSuccess;
-  f.lock = std::unique_lock<std::mutex>();
   GS_REQUIRE(ok, GS_ERR_HIP, "side stream join failed");
   return GS_OK;
 }

@@ -23,15 +23,16 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 int check_launch(const char* what);
 
 // Work forked from the caller's stream onto the library's side stream of the
-// same device (created once, default priority, non-blocking) and joined back
-// with an event, so two independent stages overlap.  The side stream is held
-// exclusively from fork to join.
+// same device and calling thread (created on the thread's first fork on that
+// device, default priority, non-blocking) and joined back with an event, so
+// two independent stages overlap.  Each thread has its own side stream and
+// events: calls from several threads on one GPU neither share nor wait for
+// them.
 struct SideFork {
   hipStream_t main = nullptr;
   hipStream_t side = nullptr;
   hipEvent_t mark = nullptr;
   hipEvent_t join = nullptr;
-  std::unique_lock<std::mutex> lock;
 };
 int fork_side_stream(hipStream_t main, SideFork& f);
 // One intermediate dependency: record_side_mark marks the side stream's work

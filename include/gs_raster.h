@@ -105,7 +105,11 @@ GS_API const char* gs_last_error(void);
 /* Reads the sticky word of the stream's GPU into *flags after the work
  * enqueued on `stream` so far has completed (this call synchronises the
  * stream), and clears it when `clear` != 0.  gs_bin_tiles_plan also copies
- * the word (as of its copy of the totals) to host_totals[4]. */
+ * the word (as of its copy of the totals) to host_totals[4].  That copy is
+ * the only read without a synchronisation of its own: it precedes the
+ * call's sort and the following gs_bin_tiles_emit, so a failure inside them
+ * is reported by the next gs_bin_tiles_plan (or by this call), one binning
+ * later.  The word is sticky, so no failure goes unreported. */
 GS_API int gs_device_errors(uint32_t* flags, int32_t clear, void* stream);
 
 /* Projection, SH colour, tile rectangle and culled count for N Gaussians.

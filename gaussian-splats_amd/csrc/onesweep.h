@@ -59,24 +59,38 @@ __device__ __forceinline__ uint64_t load_status(const uint64_t* p) {
 }
 
 // Sum of the values of workgroups [0, b) in column `col` of a [*, stride]
-// status array, walking back until an inclusive prefix is found.
+// status array, walking back until an inclusive prefix is found.  The
+// statuses of kLookBackBatch predecessors are requested together, so a walk
+// over workgroups that have published only their aggregates takes one
+// memory round trip per kLookBackBatch of them; they are consumed in order,
+// and the walk resumes at the first one not yet published.
+constexpr int kLookBackBatch = 4;
 __device__ inline uint64_t look_back(const uint64_t* status, int64_t stride, int b, int col,
                                      uint32_t* err) {
   uint64_t excl = 0;
-  for (int k = b - 1; k >= 0; --k) {
-    const uint64_t* p = status + int64_t(k) * stride + col;
-    uint64_t v = load_status(p);
-    int spins = 0;
-    while ((v >> 62) == 0) {
+  int spins = 0;
+  for (int k = b - 1; k >= 0;) {
+    uint64_t v[kLookBackBatch];
+#pragma unroll
+    for (int i = 0; i < kLookBackBatch; ++i)  // before workgroup 0: prefix 0
+      v[i] = k - i >= 0 ? load_status(status + int64_t(k - i) * stride + col) : kFlagPrefix;
+    int used = 0;
+#pragma unroll
+    for (int i = 0; i < kLookBackBatch; ++i) {
+      const uint64_t flag = v[i] >> 62;
+      if (flag == 0) break;
+      excl += v[i] & kValueMask;
+      if (flag == 2) return excl;
+      ++used;
+    }
+    if (used < kLookBackBatch) {  // predecessor k - used has not published yet
       if (++spins > kSpinLimit) {
         atomicOr(err, kDeviceFlagSpinLimit);
         return excl;
       }
       __builtin_amdgcn_s_sleep(2);
-      v = load_status(p);
     }
-    excl += v & kValueMask;
-    if ((v >> 62) == 2) break;
+    k -= used;
   }
   return excl;
 }

@@ -15,6 +15,7 @@ import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -578,10 +579,11 @@ def bench_views(args, scene):
     kind = kinds[0]
     ms_per_step, dominant_ms = timed[kind]
 
-    # Per-stage events over the batched path.
+    # Per-stage events over the batched path: the median of three staged steps
+    # after one untimed one.
     rot, trans, intr, _, _ = camera_tensors(cams)
     runs = []
-    for _ in range(3):
+    for i in range(4):
         mark, stage_times = stage_marker()
         out = forward_views(*params, rot, trans, intr, w, h, tile, 0.999, scene.near, scene.far,
                             "gaussian", 0.95, timer=mark)
@@ -591,8 +593,9 @@ def bench_views(args, scene):
         backward_views(*params, rot, trans, intr, w, h, tile, 0.999, out[1:], grad_image,
                        timer=mark)
         torch.cuda.synchronize()
-        runs.append(stage_times())
-    stages_ms = {k: sum(r[k] for r in runs) / len(runs) for k in runs[0]}
+        if i:
+            runs.append(stage_times())
+    stages_ms = {k: statistics.median(r[k] for r in runs) for k in runs[0]}
 
     # Work figures: per-view processed pairs on the mosaic, row-list entries.
     ncon, ranges, gids = out[2], out[8], out[7]
@@ -936,13 +939,20 @@ def main():
             run_step(splats, cam, target, args.tile_size, scene.near, scene.far, backward)
         torch.cuda.synchronize()
 
-    # Per-stage event timing (averaged over a few staged steps).
+    # Per-stage event timing: the median of five staged steps after one
+    # untimed one (the stage functions allocate their own buffers, and a first
+    # allocation of a size inside a stage would put its host wait in that
+    # stage's time).
     stage_runs = []
-    for _ in range(3):
+    for i in range(6):
         ms, info = staged_step(params, cam, target, args.tile_size, scene.near, scene.far,
                                backward)
-        stage_runs.append(ms)
-    stages_ms = {k: sum(r[k] for r in stage_runs) / len(stage_runs) for k in stage_runs[0]}
+        if i:
+            stage_runs.append(ms)
+    stages_ms = {k: statistics.median(r[k] for r in stage_runs) for k in stage_runs[0]}
+    print("[bench] staged runs (ms): " + "; ".join(
+        ", ".join(f"{k} {v:.3f}" for k, v in r.items()) for r in stage_runs),
+        file=sys.stderr, flush=True)
     fwd_pairs, bwd_pairs = processed_pairs(info["ranges"], info["ncon"], args.tile_size, w, h)
     bytes_model = stage_bytes(scene.num_points, scene.color.shape[1], info["total"], info["rows"],
                               w * h, fwd_pairs, bwd_pairs)

@@ -63,7 +63,6 @@ constexpr int kMaxDevices = 64;
 struct SideStream {
   hipStream_t stream = nullptr;
   hipEvent_t fork = nullptr;
-  hipEvent_t mark = nullptr;
   hipEvent_t join = nullptr;
 };
 // Per thread: a thread's fork-to-join sequence uses its own stream and
@@ -95,7 +94,6 @@ int fork_side_stream(hipStream_t main, SideFork& f) {
     // Default priority; the stream does not synchronise with the null stream.
     const bool ok = hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking) == hipSuccess &&
                     hipEventCreateWithFlags(&s.fork, hipEventDisableTiming) == hipSuccess &&
-                    hipEventCreateWithFlags(&s.mark, hipEventDisableTiming) == hipSuccess &&
                     hipEventCreateWithFlags(&s.join, hipEventDisableTiming) == hipSuccess;
     if (switch_device) (void)hipSetDevice(current);
     GS_REQUIRE(ok, GS_ERR_HIP, "could not create the side stream");
@@ -105,27 +103,17 @@ int fork_side_stream(hipStream_t main, SideFork& f) {
              GS_ERR_HIP, "side stream fork failed");
   f.main = main;
   f.side = s.stream;
-  f.mark = s.mark;
   f.join = s.join;
   return GS_OK;
 }
 
-int record_side_mark(SideFork& f) {
-  GS_REQUIRE(hipEventRecord(f.mark, f.side) == hipSuccess, GS_ERR_HIP,
-             "side stream mark failed");
-  return GS_OK;
-}
-
-int wait_side_mark(SideFork& f) {
-  GS_REQUIRE(hipStreamWaitEvent(f.main, f.mark, 0) == hipSuccess, GS_ERR_HIP,
-             "side stream wait failed");
-  return GS_OK;
-}
-
 int join_side_stream(SideFork& f, bool host_wait) {
-  bool ok = hipEventRecord(f.join, f.side) == hipSuccess &&
-            hipStreamWaitEvent(f.main, f.join, 0) == hipSuccess;
-  if (ok && host_wait) ok = hipEventSynchronize(f.join) == hipSuccess;
+  bool ok = hipEventRecord(f.join, f.side) == hipSuccess;
+  // With the host's wait, work the caller enqueues after this call follows
+  // the side stream's: the caller's stream is not given a wait packet (each
+  // one delays its next kernel by a few microseconds).
+  if (ok) ok = host_wait ? hipEventSynchronize(f.join) == hipSuccess
+                         : hipStreamWaitEvent(f.main, f.join, 0) == hipSuccess;
   GS_REQUIRE(ok, GS_ERR_HIP, "side stream join failed");
   return GS_OK;
 }

@@ -31,17 +31,13 @@ int check_launch(const char* what);
 struct SideFork {
   hipStream_t main = nullptr;
   hipStream_t side = nullptr;
-  hipEvent_t mark = nullptr;
   hipEvent_t join = nullptr;
 };
 int fork_side_stream(hipStream_t main, SideFork& f);
-// One intermediate dependency: record_side_mark marks the side stream's work
-// enqueued so far; work enqueued on the caller's stream after
-// wait_side_mark waits for it.
-int record_side_mark(SideFork& f);
-int wait_side_mark(SideFork& f);
-// Joins the side stream back into the caller's; with host_wait the host also
-// waits for the side stream's work (not the caller's) before returning.
+// Joins the side stream back into the caller's: the caller's stream waits
+// for the side stream's work, or, with host_wait, the host does (not for the
+// caller's stream) before returning, after which anything enqueued on the
+// caller's stream follows the side stream's work.
 int join_side_stream(SideFork& f, bool host_wait = false);
 
 // Device of a stream (the current device for the null stream).
@@ -292,6 +288,20 @@ inline Mosaic mosaic_of(const gs_view& v) {
   m.tw = tiles_along(v.image_width, v.tile_size);
   m.th = tiles_along(v.image_height, v.tile_size);
   return m;
+}
+
+// Per-Gaussian tile rectangle packed in 32 bits (grids of at most
+// kMaxAxisTiles x kMaxAxisTiles tiles): x0 | (width - 1) << 8 | y0 << 16 |
+// (height - 1) << 24, or kNoRect for a Gaussian without intersections.  The
+// projection writes them (gs_project_and_count's tile_rects) and the
+// row/column binning reads them: the 4 MB array for 1M Gaussians stays cache
+// resident, so the depth-ordered passes gather 4 B from it instead of 16 B
+// rectangles and 4 B counts from separate lines.
+constexpr int kMaxAxisTiles = 256;
+constexpr uint32_t kNoRect = 0xFFFFFFFFu;  // width 256 at x0 = 255 cannot occur
+
+__host__ __device__ __forceinline__ uint32_t pack_rect(int x0, int w, int y0, int h) {
+  return uint32_t(x0) | (uint32_t(w - 1) << 8) | (uint32_t(y0) << 16) | (uint32_t(h - 1) << 24);
 }
 
 // Maps a linear workgroup index onto a work index so that consecutive work

@@ -169,18 +169,29 @@ __global__ __launch_bounds__(kBlock) void hist_kernel(const K* __restrict__ keys
       const bool ok = i0 + u * stride < n;
       const uint64_t active = __ballot(ok);
       if (!active) continue;
+      // The pass loops run over the constant kKeyPasses (a key of B bytes
+      // has at most B passes of at most eight bits) with wave-uniform guards:
+      // constant indices keep the plan's shifts and masks in registers (a
+      // runtime index into the kernel argument reloaded them with a dependent
+      // scalar load per key and pass).
+      constexpr int kKeyPasses = int(sizeof(K)) < kMaxPasses ? int(sizeof(K)) : kMaxPasses;
       int first_ballot_pass = 0;
       if constexpr (SPREAD) {
         const bool ones = k[u] == ~K(0);
         const uint32_t n_ones = uint32_t(__popcll(__ballot(ok && ones)));
-        for (int p = 0; p + 1 < plan.passes; ++p) {
+#pragma unroll
+        for (int p = 0; p + 1 < kKeyPasses; ++p) {
+          if (p + 1 >= plan.passes) break;
           const uint32_t d = uint32_t(k[u] >> plan.shift[p]) & ((1u << plan.bits[p]) - 1u);
           if (ok && !ones) atomicAdd(&h[p * 256 + d], 1u);
           if (lane == 0 && n_ones) atomicAdd(&h[p * 256 + (1u << plan.bits[p]) - 1u], n_ones);
         }
         first_ballot_pass = plan.passes - 1;
       }
-      for (int p = first_ballot_pass; p < plan.passes; ++p) {
+#pragma unroll
+      for (int p = 0; p < kKeyPasses; ++p) {
+        if (p >= plan.passes) break;
+        if (p < first_ballot_pass) continue;
         const uint32_t d = uint32_t(k[u] >> plan.shift[p]) & ((1u << plan.bits[p]) - 1u);
         // Active lanes with the same digit (digits have at most eight bits).
         uint64_t peers = active;

@@ -50,10 +50,11 @@ struct ProjectArgs {
   float* pinv;
   float* pcolor;
   float* popacity;
-  int* bounds;
+  int* bounds;           // optional with tile_rects
   int* counts;
-  GsRecord* records;
-  uint32_t* depth_keys;
+  GsRecord* records;     // optional
+  uint32_t* depth_keys;  // optional
+  uint32_t* tile_rects;  // optional: packed rectangles (pack_rect) in mosaic tiles
 };
 
 // The colour block of kProjectBlock Gaussians is staged through LDS with
@@ -219,9 +220,13 @@ __global__ __launch_bounds__(kProjectBlock) void project_fwd_kernel(ProjectArgs 
     a.pcolor[vi * 3 + 1] = rgb[1];
     a.pcolor[vi * 3 + 2] = rgb[2];
     a.popacity[vi] = alpha0;
-    reinterpret_cast<int4*>(a.bounds)[vi] =
-        make_int4(x0 + cam.tile_x, x1 + cam.tile_x, y0 + cam.tile_y, y1 + cam.tile_y);
+    if (a.bounds)
+      reinterpret_cast<int4*>(a.bounds)[vi] =
+          make_int4(x0 + cam.tile_x, x1 + cam.tile_x, y0 + cam.tile_y, y1 + cam.tile_y);
     a.counts[vi] = count;
+    if (a.tile_rects)
+      a.tile_rects[vi] =
+          count > 0 ? pack_rect(x0 + cam.tile_x, x1 - x0, y0 + cam.tile_y, y1 - y0) : kNoRect;
 
     if (a.records) {
       float4* rec = reinterpret_cast<float4*>(a.records + vi);
@@ -264,15 +269,15 @@ namespace {
 
 // Projects for `views` cameras (host arrays: rotations [V, 9], translations
 // [V, 3], optional intrinsics [V, 4] = fx, fy, cx, cy, else the view's) in
-// launches of up to kMaxViews cameras.  With `mosaic`, bounds are shifted to
-// each view's tile origin in the mosaic of `view`.
+// launches of up to kMaxViews cameras.  With `mosaic`, bounds and tile
+// rectangles are shifted to each view's tile origin in the mosaic of `view`.
 int project_views(const float* mean, const float* rotation, const float* scale,
                   const float* opacity, const float* color, int64_t n, int32_t num_sh,
                   const float* camera_rotations, const float* camera_translations,
                   const float* intrinsics, int views, gs_view view, bool mosaic,
                   float* projected_mean, float* inverse_covariance, float* projected_color,
                   float* projected_opacity, int32_t* bounds, int32_t* counts, void* records,
-                  uint32_t* depth_keys, void* stream) {
+                  uint32_t* depth_keys, uint32_t* tile_rects, void* stream) {
   GS_REQUIRE(n >= 0, GS_ERR_INVALID_ARGUMENT, "negative Gaussian count");
   GS_TRY(check_view(view, true));
   GS_REQUIRE(num_sh == 1 || num_sh == 4 || num_sh == 9 || num_sh == 16, GS_ERR_UNSUPPORTED,
@@ -280,10 +285,10 @@ int project_views(const float* mean, const float* rotation, const float* scale,
   if (n == 0) return GS_OK;
   GS_REQUIRE(mean && rotation && scale && opacity && color && camera_rotations &&
                  camera_translations && projected_mean && inverse_covariance &&
-                 projected_color && projected_opacity && bounds && counts,
+                 projected_color && projected_opacity && (bounds || tile_rects) && counts,
              GS_ERR_INVALID_ARGUMENT, "null pointer argument");
   GS_REQUIRE(aligned16(rotation) && aligned16(color) && aligned16(inverse_covariance) &&
-                 aligned16(bounds) && (!records || aligned16(records)),
+                 (!bounds || aligned16(bounds)) && (!records || aligned16(records)),
              GS_ERR_INVALID_ARGUMENT,
              "rotation, color, inverse_covariance, bounds and records must be 16-byte aligned");
   GS_REQUIRE(int64_t(views) * n < (int64_t(1) << 31), GS_ERR_OVERFLOW,
@@ -307,6 +312,10 @@ int project_views(const float* mean, const float* rotation, const float* scale,
   a.ellipsoid_cutoff = float(cutoff);
   a.ellipsoid_extent = float(std::sqrt(cutoff));
   const Mosaic m = mosaic_of(view);
+  GS_REQUIRE(!tile_rects || ((mosaic ? m.tiles_w() : m.tw) <= kMaxAxisTiles &&
+                             (mosaic ? m.tiles_h() : m.th) <= kMaxAxisTiles),
+             GS_ERR_UNSUPPORTED, "packed tile rectangles need at most %d x %d tiles",
+             kMaxAxisTiles, kMaxAxisTiles);
   const dim3 grid(unsigned(ceil_div(n, kProjectBlock)));
   hipStream_t s = as_stream(stream);
   for (int first = 0; first < views; first += kMaxViews) {
@@ -333,8 +342,9 @@ int project_views(const float* mean, const float* rotation, const float* scale,
     a.pinv = inverse_covariance + off * 4;
     a.pcolor = projected_color + off * 3;
     a.popacity = projected_opacity + off;
-    a.bounds = bounds + off * 4;
+    a.bounds = bounds ? bounds + off * 4 : nullptr;
     a.counts = counts + off;
+    a.tile_rects = tile_rects ? tile_rects + off : nullptr;
     a.records = records ? static_cast<GsRecord*>(records) + off : nullptr;
     a.depth_keys = depth_keys ? depth_keys + off : nullptr;
     switch (num_sh) {
@@ -355,12 +365,13 @@ extern "C" GS_API int gs_project_and_count(
     const float* color, int64_t n, int32_t num_sh, const float* camera_rotation,
     const float* camera_translation, gs_view view, float* projected_mean,
     float* inverse_covariance, float* projected_color, float* projected_opacity,
-    int32_t* bounds, int32_t* counts, void* records, uint32_t* depth_keys, void* stream) {
+    int32_t* bounds, int32_t* counts, void* records, uint32_t* depth_keys, uint32_t* tile_rects,
+    void* stream) {
   clear_error();
   return project_views(mean, rotation, scale, opacity, color, n, num_sh, camera_rotation,
                        camera_translation, nullptr, 1, view, false, projected_mean,
                        inverse_covariance, projected_color, projected_opacity, bounds, counts,
-                       records, depth_keys, stream);
+                       records, depth_keys, tile_rects, stream);
 }
 
 extern "C" GS_API int gs_project_views(
@@ -369,12 +380,12 @@ extern "C" GS_API int gs_project_views(
     const float* camera_translations, const float* intrinsics, gs_view view,
     float* projected_mean, float* inverse_covariance, float* projected_color,
     float* projected_opacity, int32_t* bounds, int32_t* counts, void* records,
-    uint32_t* depth_keys, void* stream) {
+    uint32_t* depth_keys, uint32_t* tile_rects, void* stream) {
   clear_error();
   return project_views(mean, rotation, scale, opacity, color, n, num_sh, camera_rotations,
                        camera_translations, intrinsics, mosaic_of(view).views, view, true,
                        projected_mean, inverse_covariance, projected_color, projected_opacity,
-                       bounds, counts, records, depth_keys, stream);
+                       bounds, counts, records, depth_keys, tile_rects, stream);
 }
 
 extern "C" GS_API int gs_pack_records(const float* projected_mean,

@@ -115,13 +115,10 @@ void dispatch_scatter(int bits, const K* kin, const uint32_t* vin, K* kout, uint
 // vals == nullptr means vals[i] = i.  Sorted values land in vals_final;
 // *keys_final points at the sorted keys (keys or the scratch copy).
 // SPREAD: the keys are depth keys (see hist_kernel).  gather_out (optional):
-// the last pass also writes gather_out[i] = gather_src[vals_final[i]], after
-// `stream` has waited for `gather_ready` (an event that gather_src's producer
-// recorded before the wait is enqueued), so the earlier passes do not wait
-// for it.  before_passes() is called on the host after the histogram is
-// enqueued and before the first pass (it may enqueue work on another stream
-// and record gather_ready there): the caller's stream has the histogram to
-// run while the host enqueues it.
+// the last pass also writes gather_out[i] = gather_src[vals_final[i]].
+// before_passes() is called on the host after the histogram is enqueued and
+// before the first pass (it may enqueue work on another stream): the
+// caller's stream has the histogram to run while the host enqueues it.
 struct NoHook {
   int operator()() const { return GS_OK; }
 };
@@ -129,9 +126,11 @@ template <typename K, bool SPREAD = false, typename BeforePasses = NoHook>
 int radix_sort(K* keys, const uint32_t* vals, int64_t n, int end_bit, uint32_t* vals_final,
                K** keys_final, const Scratch& ws, hipStream_t s,
                const uint32_t* gather_src = nullptr, uint32_t* gather_out = nullptr,
-               hipEvent_t gather_ready = nullptr, BeforePasses before_passes = BeforePasses{}) {
+               BeforePasses before_passes = BeforePasses{}) {
   GS_REQUIRE(n < (int64_t(1) << 32) - kTile, GS_ERR_OVERFLOW, "too many elements to sort (%lld)",
              (long long)n);
+  GS_REQUIRE(end_bit <= int(8 * sizeof(K)), GS_ERR_INVALID_ARGUMENT,
+             "end bit %d beyond the %d-bit key", end_bit, int(8 * sizeof(K)));
   *keys_final = keys;
   if (n == 0) return before_passes();
   const sweep::Plan plan = sweep::make_plan(end_bit);
@@ -147,11 +146,6 @@ int radix_sort(K* keys, const uint32_t* vals, int64_t n, int end_bit, uint32_t* 
     K* kout = kbuf[pass & 1];
     uint32_t* vout = (pass == plan.passes - 1) ? vals_final : ws.vbuf[pass & 1];
     const bool last = pass == plan.passes - 1;
-    if (last && gather_out && gather_ready &&
-        hipStreamWaitEvent(s, gather_ready, 0) != hipSuccess) {
-      set_error("radix_sort: stream wait failed");
-      return GS_ERR_HIP;
-    }
     dispatch_scatter<K>(plan.bits[pass], kin, vin, kout, vout, n, plan.shift[pass],
                         ws.hist() + pass * 256, status, ws.tickets() + pass, ws.flags,
                         last ? gather_src : nullptr, last ? gather_out : nullptr, s);

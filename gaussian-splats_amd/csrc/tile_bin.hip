@@ -35,7 +35,6 @@ namespace gs {
 namespace {
 
 using sweep::kItems;
-constexpr int kMaxAxisTiles = 256;
 constexpr int kSeg = kTile / 4;  // items per wave
 // Rectangle tables at most this many words are accumulated in LDS first.
 constexpr int kPrivateTableWords = 12288;
@@ -44,28 +43,42 @@ constexpr int kPrivateTableWords = 12288;
 // Tables.
 // ---------------------------------------------------------------------------
 
-// Per-Gaussian tile rectangle packed in 32 bits (grids of at most 256 x 256
-// tiles): x0 | (width - 1) << 8 | y0 << 16 | (height - 1) << 24, or kNoRect
-// for a Gaussian without intersections.  The 4 MB array for 1M Gaussians
-// stays cache resident, so the depth-ordered passes gather 4 B from it
-// instead of 16 B rectangles and 4 B counts from separate lines.
-constexpr uint32_t kNoRect = 0xFFFFFFFFu;  // width 256 at x0 = 255 cannot occur
+// Rectangle [x0, x1) x [y0, y1) of a packed tile rectangle, clamped to the
+// grid (inside it when it comes from the projection; clamped so that no other
+// input indexes out of the tables); false for kNoRect or an empty one.
+__device__ __forceinline__ bool unpack_rect(uint32_t r, int tw, int th, int& x0, int& x1, int& y0,
+                                            int& y1) {
+  if (r == kNoRect) return false;
+  x0 = min(int(r & 0xFFu), tw);
+  x1 = min(x0 + int((r >> 8) & 0xFFu) + 1, tw);
+  y0 = min(int((r >> 16) & 0xFFu), th);
+  y1 = min(y0 + int(r >> 24) + 1, th);
+  return x1 > x0 && y1 > y0;
+}
 
-__device__ __forceinline__ uint32_t pack_rect(int x0, int w, int y0, int h) {
-  return uint32_t(x0) | (uint32_t(w - 1) << 8) | (uint32_t(y0) << 16) | (uint32_t(h - 1) << 24);
+// Packed rectangles from bounds [N, 2, 2] and counts (pack_rect; kNoRect for
+// Gaussians without intersections), for callers that have the projection's
+// bounds rather than its tile_rects output.
+__global__ __launch_bounds__(256) void pack_rects_kernel(const int4* __restrict__ bounds,
+                                                         const int32_t* __restrict__ counts,
+                                                         int64_t n, int tw, int th,
+                                                         uint32_t* __restrict__ rects) {
+  const int64_t g = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (g >= n) return;
+  const int4 b = bounds[g];
+  const int x0 = min(max(b.x, 0), tw), x1 = min(max(b.y, 0), tw);
+  const int y0 = min(max(b.z, 0), th), y1 = min(max(b.w, 0), th);
+  rects[g] = counts[g] > 0 && x1 > x0 && y1 > y0 ? pack_rect(x0, x1 - x0, y0, y1 - y0) : kNoRect;
 }
 
 // Corners of each counted Gaussian's rectangle [x0, x1) x [y0, y1) in the 2-D
 // difference array diff2 (th + 1 rows of pitch tw + 1) and ends of its rows in
-// the 1-D difference array rowdiff (th + 1); writes every Gaussian's packed
-// rectangle.  Grids whose tables fit LDS: each workgroup accumulates them
-// there and adds them to the global ones once.
-__global__ __launch_bounds__(256) void rect_diff_kernel(const int4* __restrict__ bounds,
-                                                        const int32_t* __restrict__ counts,
+// the 1-D difference array rowdiff (th + 1).  Grids whose tables fit LDS: each
+// workgroup accumulates them there and adds them to the global ones once.
+__global__ __launch_bounds__(256) void rect_diff_kernel(const uint32_t* __restrict__ rects,
                                                         int64_t n, int tw, int th,
                                                         int32_t* __restrict__ diff2,
-                                                        int32_t* __restrict__ rowdiff,
-                                                        uint32_t* __restrict__ packed) {
+                                                        int32_t* __restrict__ rowdiff) {
   extern __shared__ int32_t lds[];
   const int pitch = tw + 1;
   const int words = (th + 1) * pitch;
@@ -78,23 +91,16 @@ __global__ __launch_bounds__(256) void rect_diff_kernel(const int4* __restrict__
   constexpr int kBatch = 8;
   const int64_t stride = int64_t(gridDim.x) * 256;
   for (int64_t g0 = int64_t(blockIdx.x) * 256 + threadIdx.x; g0 < n; g0 += kBatch * stride) {
-    int cnt[kBatch];
-    int4 rect[kBatch];
+    uint32_t rect[kBatch];
 #pragma unroll
     for (int i = 0; i < kBatch; ++i) {
       const int64_t g = g0 + i * stride;
-      cnt[i] = g < n ? counts[g] : 0;
-      rect[i] = g < n ? bounds[g] : make_int4(0, 0, 0, 0);
+      rect[i] = g < n ? rects[g] : kNoRect;
     }
 #pragma unroll
     for (int i = 0; i < kBatch; ++i) {
-      // x0, x1, y0, y1 (inside the grid when they come from the projection;
-      // clamped so that no other input indexes out of the tables)
-      const int4 b = rect[i];
-      const int x0 = min(max(b.x, 0), tw), x1 = min(max(b.y, 0), tw);
-      const int y0 = min(max(b.z, 0), th), y1 = min(max(b.w, 0), th);
-      const bool counted = cnt[i] > 0 && x1 > x0 && y1 > y0;
-      if (counted) {
+      int x0, x1, y0, y1;
+      if (unpack_rect(rect[i], tw, th, x0, x1, y0, y1)) {
         atomicAdd(&t2[y0 * pitch + x0], 1);
         atomicAdd(&t2[y0 * pitch + x1], -1);
         atomicAdd(&t2[y1 * pitch + x0], -1);
@@ -102,8 +108,6 @@ __global__ __launch_bounds__(256) void rect_diff_kernel(const int4* __restrict__
         atomicAdd(&tr[y0], 1);
         atomicAdd(&tr[y1], -1);
       }
-      const int64_t g = g0 + i * stride;
-      if (g < n) packed[g] = counted ? pack_rect(x0, x1 - x0, y0, y1 - y0) : kNoRect;
     }
   }
   __syncthreads();
@@ -120,12 +124,10 @@ __global__ __launch_bounds__(256) void rect_diff_kernel(const int4* __restrict__
 // (second read); otherwise its corners go to diff2 directly.  Chunks of a
 // multi-view mosaic lie in one view (or two), whose window is that view's
 // block of tiles.
-__global__ __launch_bounds__(256) void rect_diff_window_kernel(const int4* __restrict__ bounds,
-                                                               const int32_t* __restrict__ counts,
+__global__ __launch_bounds__(256) void rect_diff_window_kernel(const uint32_t* __restrict__ rects,
                                                                int64_t n, int64_t chunk, int tw,
                                                                int th, int32_t* __restrict__ diff2,
-                                                               int32_t* __restrict__ rowdiff,
-                                                               uint32_t* __restrict__ packed) {
+                                                               int32_t* __restrict__ rowdiff) {
   extern __shared__ int32_t lds[];  // kPrivateTableWords window words, then th + 1 row words
   __shared__ int s_box[4];           // -x0, x1, -y0, y1 of the corner window (max-reduced)
   const int pitch = tw + 1;
@@ -137,16 +139,9 @@ __global__ __launch_bounds__(256) void rect_diff_window_kernel(const int4* __res
   if (threadIdx.x < 4) s_box[threadIdx.x] = INT_MIN;
   __syncthreads();
 
-  // Clamped rectangle of Gaussian g, or an empty one when it has no
-  // intersections (inside the grid when it comes from the projection; clamped
-  // so that no other input indexes out of the tables).
+  // Clamped rectangle of Gaussian g and whether it has intersections.
   auto rect = [&](int64_t g, int& x0, int& x1, int& y0, int& y1) {
-    const int4 b = bounds[g];
-    x0 = min(max(b.x, 0), tw);
-    x1 = min(max(b.y, 0), tw);
-    y0 = min(max(b.z, 0), th);
-    y1 = min(max(b.w, 0), th);
-    return counts[g] > 0 && x1 > x0 && y1 > y0;
+    return unpack_rect(rects[g], tw, th, x0, x1, y0, y1);
   };
 
   // 1. Corner window of the chunk.
@@ -188,15 +183,14 @@ __global__ __launch_bounds__(256) void rect_diff_window_kernel(const int4* __res
     for (int i = threadIdx.x; i < wpitch * wrows; i += 256) win[i] = 0;
   __syncthreads();
 
-  // 2. Corners and row ends; packed rectangles.
+  // 2. Corners and row ends.
   for (int64_t g0 = c0 + threadIdx.x; g0 < c1; g0 += kBatch * 256) {
 #pragma unroll
     for (int i = 0; i < kBatch; ++i) {
       const int64_t g = g0 + i * 256;
       if (g >= c1) continue;
       int x0, x1, y0, y1;
-      const bool counted = rect(g, x0, x1, y0, y1);
-      if (counted) {
+      if (rect(g, x0, x1, y0, y1)) {
         if (in_lds) {
           const int a0 = (y0 - wy0) * wpitch - wx0, a1 = (y1 - wy0) * wpitch - wx0;
           atomicAdd(&win[a0 + x0], 1);
@@ -212,7 +206,6 @@ __global__ __launch_bounds__(256) void rect_diff_window_kernel(const int4* __res
         atomicAdd(&tr[y0], 1);
         atomicAdd(&tr[y1], -1);
       }
-      packed[g] = counted ? pack_rect(x0, x1 - x0, y0, y1 - y0) : kNoRect;
     }
   }
   __syncthreads();
@@ -397,69 +390,6 @@ struct HeightSink {
       const uint32_t start = j * kTile;
       if (start < s[m] + h[m] && j < capacity)
         first_a[j] = uint32_t(p[m]) | (start == s[m] ? 0x80000000u : 0u);
-    }
-  }
-};
-
-// Width of a packed row-list entry.
-struct WidthLoad {
-  const uint32_t* xw;
-  __device__ uint32_t operator()(int64_t i) const { return entry_width(xw[i]); }
-  __device__ void load4(int64_t i, uint32_t (&v)[4]) const {
-    const uint4 q = *reinterpret_cast<const uint4*>(xw + i);
-    v[0] = entry_width(q.x);
-    v[1] = entry_width(q.y);
-    v[2] = entry_width(q.z);
-    v[3] = entry_width(q.w);
-  }
-};
-
-// Pass-B workgroup metadata: the rows' intersections [row_e[y], row_e[y+1])
-// are cut into workgroups of kTile starting at row_blk[y]; the row-list entry
-// k whose intersections [W[k], W[k] + width) contain a workgroup's first
-// position records
-//   info[b] = {k | (starts exactly there) << 31, first position,
-//              row | item count << 8 | (first of its row) << 31,
-//              last row-list entry of the row}.
-struct WidthSink {
-  const uint32_t* xw;
-  const uint32_t* row_e;
-  const uint32_t* row_a;
-  const uint32_t* row_blk;
-  uint4* info;
-  uint32_t rows;      // tile rows
-  uint32_t capacity;  // pass-B workgroups
-  // Reads for all M elements are issued together: the packed entries
-  // (clamped to the last real one), then the four row-table words of each
-  // entry's row (clamped to a real row).
-  template <int M>
-  __device__ void all(const int64_t (&k)[M], const uint32_t (&s)[M], const uint32_t (&w)[M],
-                      int64_t n) const {
-    uint32_t y[M];
-#pragma unroll
-    for (int m = 0; m < M; ++m) y[m] = entry_row(xw[min(k[m], n - 1)]);
-    uint32_t e0[M], e1[M], blk[M], a1[M];
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-      const uint32_t yy = min(y[m], rows - 1u);
-      e0[m] = row_e[yy];
-      e1[m] = row_e[yy + 1];
-      blk[m] = row_blk[yy];
-      a1[m] = row_a[yy + 1];
-    }
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-      if (k[m] >= n || y[m] >= rows) continue;
-      const uint32_t rel = s[m] - e0[m];
-      const uint32_t j = (rel + kTile - 1) / kTile;
-      const uint32_t start = j * kTile;
-      if (start < rel + w[m] && blk[m] + j < capacity) {
-        const uint32_t c0 = e0[m] + start;
-        const uint32_t count = min(uint32_t(kTile), e1[m] - c0);
-        info[blk[m] + j] = make_uint4(uint32_t(k[m]) | (start == rel ? 0x80000000u : 0u), c0,
-                                      y[m] | (count << 8) | (j == 0 ? 0x80000000u : 0u),
-                                      a1[m] - 1u);
-      }
     }
   }
 };
@@ -653,32 +583,76 @@ __device__ int load_window(const uint32_t* __restrict__ offs, int64_t first, int
   return m;
 }
 
+// Look-back value of the row pass for one (workgroup, tile row): its number
+// of row-list entries in the low kRowCountBits bits and their intersections
+// (the sum of their widths) above.  Sums along the chain stay exact while a
+// row holds fewer than 2^kRowCountBits entries (the host requires fewer
+// Gaussians) and fewer than 2^36 intersections (the intersection total is
+// below 2^32).
+constexpr int kRowCountBits = 26;
+constexpr uint64_t kRowCountMask = (uint64_t(1) << kRowCountBits) - 1;
+
+// Per-row state of a pass-A workgroup beside its bucketing arrays.
+template <int BITS>
+struct RowLds {
+  BucketLds<BITS, 2> b;
+  uint32_t wstart[1 << BITS];  // intersections of the workgroup's items before row d's first
+  uint32_t wend[1 << BITS];    // ... up to and including row d's last
+  uint32_t wofs[1 << BITS];    // W of reordered item j of row d = wofs[d] + its prefix
+  uint32_t e0[1 << BITS], e1[1 << BITS], blk[1 << BITS], a1[1 << BITS];  // row tables
+  uint32_t waves[kItems][4];   // per round of kBlock items: each wave's sum of widths
+};
+
 // Pass A: row-list entries [b kTile, b kTile + kTile) of the depth-ordered
 // expansion (Gaussian order[p] owns entries [offs[p], offs[p + 1]), one per
 // covered tile row), bucketed by tile row.  The first owner comes from
 // first_a (recorded by the height scan), the last one from the next
 // workgroup's first owner (a search for the final workgroup).  Reads the
-// packed rectangles in depth order; writes each entry's Gaussian id and
-// packed first column / width / row.
+// packed rectangles in depth order; writes each entry's Gaussian id, packed
+// first column / width / row, and W: the position of its first intersection
+// in row-major intersection order (row_e[row] + the widths of the row's
+// earlier entries).  The look-back carries each row's entry count and width
+// sum together, so W needs no scan of its own.  The entry whose
+// intersections hold a pass-B workgroup's first position records that
+// workgroup's metadata
+//   info[blk] = {entry | (starts exactly there) << 31, first position,
+//                row | item count << 8 | (first of its row) << 31,
+//                last row-list entry of the row}.
 template <int BITS>
 __global__ __launch_bounds__(kBlock) void row_bucket_kernel(
     const uint32_t* __restrict__ packed_sorted, const int32_t* __restrict__ order,
     const uint32_t* __restrict__ offs, const uint32_t* __restrict__ first_a, int64_t n,
     uint32_t entries, int th, const uint32_t* __restrict__ row_a,
-    const int64_t* __restrict__ totals, uint32_t* __restrict__ out_g,
-    uint32_t* __restrict__ out_xw, uint64_t* __restrict__ status, uint32_t* __restrict__ ticket,
-    uint32_t* __restrict__ err) {
-  __shared__ BucketLds<BITS, 2> sh;
+    const uint32_t* __restrict__ row_e, const uint32_t* __restrict__ row_blk,
+    const int64_t* __restrict__ totals, uint32_t blocks_b, uint32_t* __restrict__ out_g,
+    uint32_t* __restrict__ out_xw, uint32_t* __restrict__ out_w, uint4* __restrict__ info,
+    uint64_t* __restrict__ status, uint32_t* __restrict__ ticket, uint32_t* __restrict__ err) {
+  constexpr int D = 1 << BITS;
+  static_assert(D <= kBlock, "one row per thread");
+  __shared__ RowLds<BITS> L;
+  BucketLds<BITS, 2>& sh = L.b;
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
   // Sizes from the host must be the plan's; otherwise every workgroup leaves
   // (none waits on another) and the error flag is set.
-  if (totals[1] != int64_t(entries) || offs[n] != entries) {
+  if (totals[1] != int64_t(entries) || offs[n] != entries || totals[2] != int64_t(blocks_b)) {
     if (threadIdx.x == 0) atomicOr(err, kDeviceFlagSizes);
     return;
   }
   if (threadIdx.x == 0) sh.block = int(atomicAdd(ticket, 1u));
-  for (int d = threadIdx.x; d < 4 * (1 << BITS); d += kBlock) (&sh.cnt[0][0])[d] = 0;
+  for (int d = threadIdx.x; d < 4 * D; d += kBlock) (&sh.cnt[0][0])[d] = 0;
+  {
+    // Row tables (entry th of each holds the totals; rows at or past th
+    // hold no items).
+    const int d = threadIdx.x;
+    if (d < D) {
+      const bool row = d < th;
+      L.e0[d] = row ? row_e[d] : 0u;
+      L.e1[d] = row ? row_e[d + 1] : 0u;
+      L.blk[d] = row ? row_blk[d] : 0u;
+      L.a1[d] = row ? row_a[d + 1] : 0u;
+    }
+  }
   __syncthreads();
   const int b = sh.block;
   const int nblocks = int((int64_t(entries) + kTile - 1) / kTile);
@@ -702,7 +676,7 @@ __global__ __launch_bounds__(kBlock) void row_bucket_kernel(
   find_owners(rel, m, sh.own, sh.scratch);
 
   uint32_t dig[kItems];
-  uint32_t val[2][kItems];
+  uint32_t g_id[kItems], xw[kItems];
   // Every position has an owner in [0, m) (the running maximum starts at 0),
   // so all gathers are in bounds: they are issued unconditionally and
   // together (the ids and the rectangles are both in depth order: one round
@@ -719,19 +693,136 @@ __global__ __launch_bounds__(kBlock) void row_bucket_kernel(
 #pragma unroll
   for (int i = 0; i < kItems; ++i) {
     const int e = wid * kSeg + i * 64 + lane;
-    const uint32_t ty = (((r[i] >> 16) & 0xFFu) + uint32_t(e - rel[kk[i]])) & ((1u << BITS) - 1u);
+    const uint32_t ty = (((r[i] >> 16) & 0xFFu) + uint32_t(e - rel[kk[i]])) & (D - 1u);
     dig[i] = e < nvalid ? ty : 0u;
-    val[0][i] = uint32_t(g[i]);
-    val[1][i] = (r[i] & 0xFFFFu) | (ty << 16);  // first column, width - 1, row
+    g_id[i] = uint32_t(g[i]);
+    xw[i] = (r[i] & 0xFFFFu) | (ty << 16);  // first column, width - 1, row
   }
-  uint32_t* const out[2] = {out_g, out_xw};
-  place_items<BITS, 2>(
-      sh, dig, val, nvalid, b, b == 0, [&](int d) { return d <= th ? row_a[d] : 0u; }, status,
-      err, out, entries);
+
+  // 1. Stable rank by row within each wave; the rows' local starts.
+  const int seg_valid = nvalid - wid * kSeg;
+  uint32_t rank[kItems];
+  if (nvalid == kTile)
+    sweep::rank_items<BITS, true>(dig, seg_valid, sh.cnt[wid], rank);
+  else
+    sweep::rank_items<BITS, false>(dig, seg_valid, sh.cnt[wid], rank);
+  __syncthreads();
+  uint32_t tot = 0, n0 = 0, n1 = 0, n2 = 0;
+  if (threadIdx.x < D) {
+    n0 = sh.cnt[0][threadIdx.x];
+    n1 = sh.cnt[1][threadIdx.x];
+    n2 = sh.cnt[2][threadIdx.x];
+    tot = n0 + n1 + n2 + sh.cnt[3][threadIdx.x];
+  }
+  uint32_t all;
+  const uint32_t local_start = block_exclusive_scan(tot, sh.scratch, all);
+  if (threadIdx.x < D) {
+    const int d = threadIdx.x;
+    // Wave w's items of row d start at cnt[w][d] in the reordered tile.
+    sh.cnt[0][d] = local_start;
+    sh.cnt[1][d] = local_start + n0;
+    sh.cnt[2][d] = local_start + n0 + n1;
+    sh.cnt[3][d] = local_start + n0 + n1 + n2;
+  }
+  __syncthreads();
+
+  // 2. Reorder by row in LDS.
+#pragma unroll
+  for (int i = 0; i < kItems; ++i) {
+    if (i * 64 + lane < seg_valid) {
+      const uint32_t pos = sh.cnt[wid][dig[i]] + rank[i];
+      sh.dig[pos] = uint8_t(dig[i]);
+      sh.val[pos] = g_id[i];
+      sh.val[kTile + pos] = xw[i];
+    }
+  }
+  __syncthreads();
+
+  // 3. Widths of the reordered items: item j = threadIdx.x + i kBlock of this
+  // thread (the store layout below); wl[i] = the widths of the items before
+  // it.  One wave scan per round, then the earlier rounds' and waves' sums.
+  uint32_t wl[kItems], wv[kItems];
+#pragma unroll
+  for (int i = 0; i < kItems; ++i) {
+    const int j = int(threadIdx.x) + i * kBlock;
+    wv[i] = j < nvalid ? entry_width(sh.val[kTile + j]) : 0u;
+    const uint32_t inc = wave_inclusive_dpp(wv[i], AddOp{});
+    if (lane == 63) L.waves[i][wid] = inc;
+    wl[i] = inc - wv[i];
+  }
+  __syncthreads();
+  {
+    uint32_t before = 0;  // widths of the earlier rounds
+#pragma unroll
+    for (int i = 0; i < kItems; ++i) {
+      const uint32_t s0 = L.waves[i][0], s1 = L.waves[i][1], s2 = L.waves[i][2],
+                     s3 = L.waves[i][3];
+      wl[i] += before + (wid > 0 ? s0 : 0u) + (wid > 1 ? s1 : 0u) + (wid > 2 ? s2 : 0u);
+      before += s0 + s1 + s2 + s3;
+    }
+  }
+  // A row's items are contiguous: its first item records the widths before
+  // it, its last the widths up to its end.
+#pragma unroll
+  for (int i = 0; i < kItems; ++i) {
+    const int j = int(threadIdx.x) + i * kBlock;
+    if (j < nvalid) {
+      const uint32_t d = sh.dig[j];
+      if (j == 0 || sh.dig[j - 1] != d) L.wstart[d] = wl[i];
+      if (j == nvalid - 1 || sh.dig[j + 1] != d) L.wend[d] = wl[i] + wv[i];
+    }
+  }
+  __syncthreads();
+
+  // 4. Look-back along the rows' chains: (entries, intersections) of the
+  // earlier workgroups.
+  if (threadIdx.x < D) {
+    const int d = threadIdx.x;
+    const uint64_t wtot = tot ? uint64_t(L.wend[d] - L.wstart[d]) : 0u;
+    const uint64_t value = uint64_t(tot) | (wtot << kRowCountBits);
+    uint64_t* mine = status + int64_t(b) * D + d;
+    sweep::store_status(mine, (b == 0 ? sweep::kFlagPrefix : sweep::kFlagAggregate) | value);
+    uint64_t excl = 0;
+    if (b > 0) {
+      excl = sweep::look_back(status, D, b, d, err);
+      sweep::store_status(mine, sweep::kFlagPrefix | (excl + value));
+    }
+    // Output position of reordered item j of row d: gofs[d] + j (mod 2^32).
+    sh.gofs[d] = (d <= th ? row_a[d] : 0u) + uint32_t(excl & kRowCountMask) - local_start;
+    if (tot) L.wofs[d] = L.e0[d] + uint32_t(excl >> kRowCountBits) - L.wstart[d];
+  }
+  __syncthreads();
+
+  // 5. Stores, and the metadata of the pass-B workgroups whose first
+  // position an item's intersections hold (widths are below kTile, so at
+  // most one).
+#pragma unroll
+  for (int i = 0; i < kItems; ++i) {
+    const int j = int(threadIdx.x) + i * kBlock;
+    if (j >= nvalid) break;
+    const uint32_t d = sh.dig[j];
+    const uint32_t o = sh.gofs[d] + uint32_t(j);
+    if (o >= entries) continue;  // never for tables and lists built by this file
+    const uint32_t xwj = sh.val[kTile + j];
+    const uint32_t w = L.wofs[d] + wl[i];
+    out_g[o] = sh.val[j];
+    out_xw[o] = xwj;
+    out_w[o] = w;
+    const uint32_t rel_w = w - L.e0[d];
+    const uint32_t kb = (rel_w + kTile - 1) / kTile;
+    const uint32_t start = kb * kTile;
+    if (start < rel_w + wv[i] && L.blk[d] + kb < blocks_b) {
+      const uint32_t first = L.e0[d] + start;
+      const uint32_t count = min(uint32_t(kTile), L.e1[d] - first);
+      info[L.blk[d] + kb] = make_uint4(o | (start == rel_w ? 0x80000000u : 0u), first,
+                                       d | (count << 8) | (kb == 0 ? 0x80000000u : 0u),
+                                       L.a1[d] - 1u);
+    }
+  }
 }
 
 // Pass B's workgroups: workgroup b covers intersections [c0, c0 + count) of
-// one tile row (metadata info[b] recorded by the width scan); row-list entry
+// one tile row (metadata info[b] recorded by pass A); row-list entry
 // k of the row owns positions [W[k], W[k] + width) and expands into its
 // columns.  Pass B buckets every intersection by column inside its row in
 // three launches instead of one chained pass: counts per (workgroup, column),
@@ -948,12 +1039,14 @@ __global__ __launch_bounds__(kBlock) void column_bucket_kernel(
 template <int BITS>
 void launch_row_bucket(unsigned blocks, const uint32_t* packed_sorted, const int32_t* order,
                        const uint32_t* offs, const uint32_t* first_a, int64_t n, uint32_t entries,
-                       int th, const uint32_t* row_a, const int64_t* totals, uint32_t* out_g,
-                       uint32_t* out_xw, uint64_t* status, uint32_t* ticket, uint32_t* err,
-                       hipStream_t s) {
+                       int th, const uint32_t* row_a, const uint32_t* row_e,
+                       const uint32_t* row_blk, const int64_t* totals, uint32_t blocks_b,
+                       uint32_t* out_g, uint32_t* out_xw, uint32_t* out_w, uint4* info,
+                       uint64_t* status, uint32_t* ticket, uint32_t* err, hipStream_t s) {
   row_bucket_kernel<BITS><<<blocks, kBlock, 0, s>>>(packed_sorted, order, offs, first_a, n,
-                                                    entries, th, row_a, totals, out_g, out_xw,
-                                                    status, ticket, err);
+                                                    entries, th, row_a, row_e, row_blk, totals,
+                                                    blocks_b, out_g, out_xw, out_w, info, status,
+                                                    ticket, err);
 }
 
 template <int BITS>
@@ -976,7 +1069,6 @@ int axis_bits(int tiles) { return std::max(1, bits_for(tiles)); }
 // Persistent plan (written by gs_bin_tiles_plan, read by gs_bin_tiles_emit).
 struct PlanLayout {
   int32_t* order = nullptr;    // [n] depth order
-  uint32_t* packed = nullptr;  // [n] packed tile rectangles (pack_rect)
   uint32_t* packed_sorted = nullptr;  // [n] the same in depth order (the sort's last pass)
   uint32_t* offs = nullptr;    // [n + 1] row-list offsets in depth order (written by emit)
   uint32_t* row_a = nullptr;   // [th + 1]
@@ -1000,7 +1092,6 @@ PlanLayout plan_layout(void* base, int64_t n, int tw, int th) {
     return r;
   };
   p.order = reinterpret_cast<int32_t*>(take(size_t(n) * 4));
-  p.packed = reinterpret_cast<uint32_t*>(take(size_t(n) * 4));
   p.packed_sorted = reinterpret_cast<uint32_t*>(take(size_t(n) * 4));
   p.offs = reinterpret_cast<uint32_t*>(take(size_t(n + 1) * 4));
   p.row_a = reinterpret_cast<uint32_t*>(take(size_t(th + 1) * 4));
@@ -1031,8 +1122,7 @@ struct EmitLayout {
   uint32_t* col = nullptr;      // [blocks B x tiles_w] pass-B counts, then offsets
   uint32_t* col_sums = nullptr;  // [chunk_slots x tiles_w] pass-B chunk sums (zeroed)
   uint64_t* status_a = nullptr;
-  uint64_t* scan_status = nullptr;  // width scan
-  uint32_t* small = nullptr;  // tickets A, width scan
+  uint32_t* small = nullptr;  // ticket of pass A
   size_t bytes = 0;
 };
 
@@ -1052,15 +1142,13 @@ EmitLayout emit_layout(void* base, int64_t entries, int64_t blocks_b, int tw, in
   e.info = reinterpret_cast<uint4*>(take(size_t(blocks_b + 1) * 16));
   e.col = reinterpret_cast<uint32_t*>(take(size_t(blocks_b) * size_t(tw) * 4));
   const int64_t words_a = blocks_a << axis_bits(th);
-  const int64_t words_w = blocks_a;
   const int64_t words_s = (chunk_slots(blocks_b, th) * tw + 1) / 2;
-  e.zero_words = words_a + words_w + words_s + 4;  // + 8 small 32-bit words
+  e.zero_words = words_a + words_s + 4;  // + 8 small 32-bit words
   e.zero = reinterpret_cast<uint64_t*>(take(size_t(e.zero_words) * 8));
   if (e.zero) {
     e.status_a = e.zero;
-    e.scan_status = e.status_a + words_a;
-    e.col_sums = reinterpret_cast<uint32_t*>(e.scan_status + words_w);
-    e.small = reinterpret_cast<uint32_t*>(e.scan_status + words_w + words_s);
+    e.col_sums = reinterpret_cast<uint32_t*>(e.status_a + words_a);
+    e.small = reinterpret_cast<uint32_t*>(e.status_a + words_a + words_s);
   }
   e.bytes = off;
   return e;
@@ -1088,17 +1176,34 @@ GS_API size_t gs_bin_tiles_plan_bytes(int64_t n, int32_t tiles_w, int32_t tiles_
   return plan_layout(nullptr, n, tiles_w, tiles_h).bytes;
 }
 
-GS_API int gs_bin_tiles_plan(uint32_t* depth_keys, const int32_t* bounds, const int32_t* counts,
-                             int64_t n, int32_t tiles_w, int32_t tiles_h, int64_t* ranges,
+GS_API int gs_pack_tile_rects(const int32_t* bounds, const int32_t* counts, int64_t n,
+                              int32_t tiles_w, int32_t tiles_h, uint32_t* tile_rects,
+                              void* stream) {
+  clear_error();
+  GS_TRY(check_grid(tiles_w, tiles_h));
+  GS_REQUIRE(n >= 0, GS_ERR_INVALID_ARGUMENT, "invalid Gaussian count");
+  if (n == 0) return GS_OK;
+  GS_REQUIRE(bounds && counts && tile_rects && aligned16(bounds), GS_ERR_INVALID_ARGUMENT,
+             "null or misaligned pointer");
+  pack_rects_kernel<<<unsigned(ceil_div(n, 256)), 256, 0, as_stream(stream)>>>(
+      reinterpret_cast<const int4*>(bounds), counts, n, tiles_w, tiles_h, tile_rects);
+  return check_launch("pack_tile_rects");
+}
+
+GS_API int gs_bin_tiles_plan(uint32_t* depth_keys, const uint32_t* tile_rects, int64_t n,
+                             int32_t tiles_w, int32_t tiles_h, int64_t* ranges,
                              int64_t* totals, int64_t* host_totals, void* plan, size_t plan_bytes,
                              void* stream) {
   clear_error();
   GS_TRY(check_grid(tiles_w, tiles_h));
-  GS_REQUIRE(n >= 0 && n < (int64_t(1) << 31), GS_ERR_INVALID_ARGUMENT, "invalid Gaussian count");
+  GS_REQUIRE(n >= 0, GS_ERR_INVALID_ARGUMENT, "invalid Gaussian count");
+  GS_REQUIRE(n < (int64_t(1) << kRowCountBits), GS_ERR_OVERFLOW,
+             "row/column bucketing takes fewer than %lld Gaussians (got %lld)",
+             (long long)(int64_t(1) << kRowCountBits), (long long)n);
   GS_REQUIRE(ranges && totals && plan, GS_ERR_INVALID_ARGUMENT, "null pointer argument");
   GS_REQUIRE(aligned16(ranges), GS_ERR_INVALID_ARGUMENT, "ranges must be 16-byte aligned");
-  GS_REQUIRE(n == 0 || (depth_keys && bounds && counts && aligned16(bounds)),
-             GS_ERR_INVALID_ARGUMENT, "null or misaligned pointer");
+  GS_REQUIRE(n == 0 || (depth_keys && tile_rects), GS_ERR_INVALID_ARGUMENT,
+             "null pointer argument");
   const PlanLayout p = plan_layout(plan, n, tiles_w, tiles_h);
   GS_REQUIRE(plan_bytes >= p.bytes, GS_ERR_WORKSPACE, "plan workspace too small (%zu < %zu)",
              plan_bytes, p.bytes);
@@ -1122,21 +1227,18 @@ GS_API int gs_bin_tiles_plan(uint32_t* depth_keys, const int32_t* bounds, const 
       int32_t* rowdiff = p.table + words;
       if (words + tiles_h + 1 <= kPrivateTableWords) {
         rect_diff_kernel<<<blocks, 256, size_t(words + tiles_h + 1) * 4, fork.side>>>(
-            reinterpret_cast<const int4*>(bounds), counts, n, tiles_w, tiles_h, diff2, rowdiff,
-            p.packed);
+            tile_rects, n, tiles_w, tiles_h, diff2, rowdiff);
       } else {
         // Contiguous chunks with private corner windows (see the kernel).
         const int64_t wblocks = std::min<int64_t>(512, std::max<int64_t>(1, ceil_div(n, 16384)));
         const int64_t chunk = ceil_div(n, wblocks);
         rect_diff_window_kernel<<<unsigned(ceil_div(n, chunk)), 256,
                                   size_t(kPrivateTableWords + tiles_h + 1) * 4, fork.side>>>(
-            reinterpret_cast<const int4*>(bounds), counts, n, chunk, tiles_w, tiles_h, diff2,
-            rowdiff, p.packed);
+            tile_rects, n, chunk, tiles_w, tiles_h, diff2,
+            rowdiff);
       }
     }
-    // The depth sort's last pass and the row-list scan read the packed
-    // rectangles: they wait for this mark.
-    int st = n > 0 ? record_side_mark(fork) : GS_OK;
+    int st = GS_OK;
     const int lds_words = tiles_h * (tiles_w + 1);
     if (lds_words <= kPrivateTableWords) {
       tables_kernel<true><<<1, 256, size_t(lds_words) * 4, fork.side>>>(
@@ -1168,14 +1270,12 @@ GS_API int gs_bin_tiles_plan(uint32_t* depth_keys, const int32_t* bounds, const 
     clear(ws, s);
     // depth_keys is consumed (ping-pong buffer of the sort).
     uint32_t* sorted_keys = nullptr;
-    // Its last pass also writes the rectangles in depth order, once the side
-    // stream has written them (mark above).
+    // Its last pass also writes the rectangles in depth order.
     status = radix_sort<uint32_t, true>(depth_keys, nullptr, n, 32,
                                         reinterpret_cast<uint32_t*>(p.order), &sorted_keys, ws, s,
-                                        p.packed, p.packed_sorted, fork.mark, side_work);
+                                        tile_rects, p.packed_sorted, side_work);
     // Row-list offsets in depth order, recording each pass-A workgroup's
-    // first owner; they read the packed rectangles written on the side stream.
-    if (status == GS_OK) status = wait_side_mark(fork);
+    // first owner.
     if (status == GS_OK)
       launch_scan<uint32_t>(HeightLoad{p.packed_sorted}, n, p.offs, true, true, ws, s,
                             HeightSink{p.first_a, p.first_a_capacity});
@@ -1183,7 +1283,9 @@ GS_API int gs_bin_tiles_plan(uint32_t* depth_keys, const int32_t* bounds, const 
     status = side_work();
   }
   // Always join, also after an error; with host_totals the host waits for
-  // the tables only, while the sort keeps running on the caller's stream.
+  // the tables only, while the sort keeps running on the caller's stream
+  // (the caller's stream then needs no wait of its own: everything enqueued
+  // on it after this call follows the side stream's work).
   const int joined = join_side_stream(fork, host_totals != nullptr && status == GS_OK);
   GS_TRY(status);
   GS_TRY(joined);
@@ -1206,6 +1308,9 @@ GS_API int gs_bin_tiles_emit(int64_t n,
   GS_TRY(check_grid(tiles_w, tiles_h));
   GS_REQUIRE(n >= 0 && total >= 0 && row_entries >= 0 && blocks >= 0, GS_ERR_INVALID_ARGUMENT,
              "invalid emit arguments");
+  GS_REQUIRE(n < (int64_t(1) << kRowCountBits), GS_ERR_OVERFLOW,
+             "row/column bucketing takes fewer than %lld Gaussians (got %lld)",
+             (long long)(int64_t(1) << kRowCountBits), (long long)n);
   GS_REQUIRE(total < (int64_t(1) << 32) - kTile && row_entries < (int64_t(1) << 31),
              GS_ERR_OVERFLOW, "too many intersections (%lld)", (long long)total);
   GS_REQUIRE(blocks >= ceil_div(total, kTile) && blocks <= ceil_div(total, kTile) + tiles_h,
@@ -1228,37 +1333,20 @@ GS_API int gs_bin_tiles_emit(int64_t n,
   sweep::clear_kernel<<<unsigned(std::max<int64_t>(1, std::min<int64_t>(1024, ceil_div(e.zero_words, kBlock)))),
                         kBlock, 0, s>>>(e.zero, e.zero_words, nullptr, 0);
   uint32_t* ticket_a = e.small;
-  uint32_t* ticket_w = e.small + 2;
   const unsigned blocks_a = unsigned(ceil_div(row_entries, kTile));
+  // Pass A also writes every row-list entry's position in row-major
+  // intersection order and each pass-B workgroup's metadata.
   switch (axis_bits(tiles_h)) {
 #define GS_ROW_CASE(B)                                                                          \
   case B:                                                                                       \
     launch_row_bucket<B>(blocks_a, p.packed_sorted, p.order, p.offs, p.first_a, n,              \
-                         uint32_t(row_entries),                                                 \
-                         tiles_h, p.row_a, totals, e.rl_g, e.rl_xw, e.status_a, ticket_a, err,  \
-                         s);                                                                    \
+                         uint32_t(row_entries), tiles_h, p.row_a, p.row_e, p.row_blk, totals,   \
+                         uint32_t(blocks), e.rl_g, e.rl_xw, e.W, e.info, e.status_a, ticket_a,  \
+                         err, s);                                                               \
     break;
     GS_ROW_CASE(1) GS_ROW_CASE(2) GS_ROW_CASE(3) GS_ROW_CASE(4)
     GS_ROW_CASE(5) GS_ROW_CASE(6) GS_ROW_CASE(7) GS_ROW_CASE(8)
 #undef GS_ROW_CASE
-  }
-  // Positions of the row-list entries in row-major intersection order,
-  // recording each pass-B workgroup's metadata.
-  const WidthSink width_sink{e.rl_xw, p.row_e, p.row_a, p.row_blk, e.info, uint32_t(tiles_h),
-                            uint32_t(blocks)};
-  if (blocks_a <= sweep::kLookBackScanTiles) {
-    sweep::scan_kernel<uint32_t, WidthLoad, WidthSink><<<blocks_a, sweep::kBlock, 0, s>>>(
-        WidthLoad{e.rl_xw}, row_entries, e.W, false, true, e.scan_status, ticket_w, err,
-        width_sink);
-  } else {
-    // Reduce-then-scan (see launch_scan); the tile sums reuse the status words.
-    uint32_t* sums = reinterpret_cast<uint32_t*>(e.scan_status);
-    sweep::tile_sum_kernel<uint32_t, WidthLoad><<<blocks_a, sweep::kBlock, 0, s>>>(
-        WidthLoad{e.rl_xw}, row_entries, true, sums);
-    sweep::tile_offsets_kernel<uint32_t><<<1, sweep::kBlock, 0, s>>>(sums, blocks_a, nullptr);
-    sweep::scan_kernel<uint32_t, WidthLoad, WidthSink><<<blocks_a, sweep::kBlock, 0, s>>>(
-        WidthLoad{e.rl_xw}, row_entries, e.W, false, true, nullptr, nullptr, err, width_sink,
-        sums);
   }
   switch (axis_bits(tiles_w)) {
 #define GS_COL_CASE(B)                                                                          \

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parents[2] / "_lib" / "libgs_raster.so"
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 GS_OK = 0
 GS_ERR_INVALID_ARGUMENT = 1
@@ -197,11 +197,11 @@ _SIGNATURES = {
     "gs_last_error": (ctypes.c_char_p, []),
     "gs_project_and_count": (
         c_int,
-        [c_void_p] * 5 + [c_int64, c_int32, c_void_p, c_void_p, GsView] + [c_void_p] * 9,
+        [c_void_p] * 5 + [c_int64, c_int32, c_void_p, c_void_p, GsView] + [c_void_p] * 10,
     ),
     "gs_project_views": (
         c_int,
-        [c_void_p] * 5 + [c_int64, c_int32, c_void_p, c_void_p, c_void_p, GsView] + [c_void_p] * 9,
+        [c_void_p] * 5 + [c_int64, c_int32, c_void_p, c_void_p, c_void_p, GsView] + [c_void_p] * 10,
     ),
     "gs_pack_records": (c_int, [c_void_p] * 4 + [c_int64, GsView, c_void_p, c_void_p]),
     "gs_scan_workspace_bytes": (c_size_t, [c_int64]),
@@ -231,7 +231,10 @@ _SIGNATURES = {
     "gs_bin_tiles_plan_bytes": (c_size_t, [c_int64, c_int32, c_int32]),
     "gs_bin_tiles_plan": (
         c_int,
-        [c_void_p] * 3 + [c_int64, c_int32, c_int32] + [c_void_p] * 4 + [c_size_t, c_void_p],
+        [c_void_p] * 2 + [c_int64, c_int32, c_int32] + [c_void_p] * 4 + [c_size_t, c_void_p],
+    ),
+    "gs_pack_tile_rects": (
+        c_int, [c_void_p, c_void_p, c_int64, c_int32, c_int32, c_void_p, c_void_p]
     ),
     "gs_bin_tiles_emit_bytes": (c_size_t, [c_int64, c_int64, c_int64, c_int64, c_int32, c_int32]),
     "gs_bin_tiles_emit": (

@@ -16,7 +16,7 @@ import torch
 from ...timing import stage_timer
 from . import _native as nat
 from .composite import composite
-from .intersections import MAX_BUCKET_TILES, bin_gaussians, bin_tiles, emit_tiles, sort_tiles
+from .intersections import bin_gaussians, bin_tiles, bucketing_fits, emit_tiles, sort_tiles
 from .project import _check_tile, project_and_count
 
 if TYPE_CHECKING:  # the splat API imports this module, so only for annotations
@@ -60,17 +60,23 @@ def forward_pipeline(
 
     records = torch.empty((n, 12), dtype=torch.float32, device=device)
     depth_keys = torch.empty(n, dtype=torch.int32, device=device)
+    # Row/column bucketing reads the projection's packed tile rectangles (the
+    # int32 bounds are then not written); the other binning reads bounds.
+    bucketing = bucketing_fits(n, tiles_w, tiles_h)
+    tile_rects = torch.empty(n, dtype=torch.int32, device=device) if bucketing else None
     mark("start")
     projected_mean, inverse_covariance, projected_color, projected_opacity, bounds, counts = (
         project_and_count(
             mean, rotation, scale, opacity, color, camera_rotation, camera_translation,
             fx, fy, cx, cy, image_width, image_height, tile_size, near, far, rendering_mode,
-            confidence, records=records, depth_keys=depth_keys,
+            confidence, records=records, depth_keys=depth_keys, tile_rects=tile_rects,
+            bounds=not bucketing,
         )
     )
     mark("project")
-    if tiles_w <= MAX_BUCKET_TILES and tiles_h <= MAX_BUCKET_TILES:
-        gaussian_ids, ranges = bin_tiles(depth_keys, bounds, counts, tiles_w, tiles_h, timer=mark)
+    if bucketing:
+        gaussian_ids, ranges = bin_tiles(depth_keys, None, None, tiles_w, tiles_h, timer=mark,
+                                         tile_rects=tile_rects)
     else:
         order, offsets = bin_gaussians(depth_keys, counts)
         mark("bin")

@@ -144,27 +144,53 @@ def sort_tiles(
 
 
 MAX_BUCKET_TILES = 256
+# Row/column bucketing takes fewer Gaussians than this (the row pass's
+# look-back packs a row's entry count into 26 bits).
+MAX_BUCKET_GAUSSIANS = 1 << 26
+
+
+def bucketing_fits(n: int, tiles_w: int, tiles_h: int) -> bool:
+    """Whether bin_tiles takes n Gaussians on a tiles_w x tiles_h grid."""
+    return tiles_w <= MAX_BUCKET_TILES and tiles_h <= MAX_BUCKET_TILES and n < MAX_BUCKET_GAUSSIANS
 
 
 def bin_tiles(
     depth_keys: torch.Tensor,
-    bounds: torch.Tensor,
-    counts: torch.Tensor,
+    bounds: torch.Tensor | None,
+    counts: torch.Tensor | None,
     tiles_w: int,
     tiles_h: int,
     timer=None,
+    *,
+    tile_rects: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Sorted Gaussian ids and int64 ranges [T, 2] by row/column bucketing.
 
     Equivalent to ``bin_gaussians`` + ``emit_tiles`` + ``sort_tiles`` for grids of
-    at most ``MAX_BUCKET_TILES`` tiles per axis; ``depth_keys`` is consumed.
+    at most ``MAX_BUCKET_TILES`` tiles per axis and fewer than
+    ``MAX_BUCKET_GAUSSIANS`` Gaussians (``bucketing_fits``); ``depth_keys`` is
+    consumed.  The rectangles come from ``tile_rects`` (the projection's packed
+    rectangles, as the op passes them; ``bounds`` and ``counts`` are then
+    unused) or are packed here from ``bounds`` and ``counts``.
     ``timer(name)`` (optional) marks the end of the plan ("bin") and of the
     bucketing passes ("emit").
     """
     mark = timer or (lambda name: None)
-    device = nat.require_gpu(depth_keys, bounds, counts)
-    n = counts.shape[0]
     lib = nat.library()
+    if tile_rects is None:
+        device = nat.require_gpu(depth_keys, bounds, counts)
+        n = counts.shape[0]
+        bounds = nat.prepare(bounds, torch.int32)
+        counts = nat.prepare(counts, torch.int32)
+        tile_rects = torch.empty(n, dtype=torch.int32, device=device)
+        nat.check(
+            lib.gs_pack_tile_rects(nat.ptr(bounds), nat.ptr(counts), n, tiles_w, tiles_h,
+                                   nat.ptr(tile_rects), nat.stream(device)),
+            "pack_tile_rects",
+        )
+    else:
+        device = nat.require_gpu(depth_keys, tile_rects)
+        n = tile_rects.shape[0]
     s = nat.stream(device)
     plan = nat.workspace(lib.gs_bin_tiles_plan_bytes(n, tiles_w, tiles_h), device)
     ranges = torch.empty((tiles_w * tiles_h, 2), dtype=torch.int64, device=device)
@@ -176,7 +202,7 @@ def bin_tiles(
     host_totals = torch.zeros(5, dtype=torch.int64, pin_memory=True)
     nat.check(
         lib.gs_bin_tiles_plan(
-            nat.ptr(depth_keys), nat.ptr(bounds), nat.ptr(counts), n, tiles_w, tiles_h,
+            nat.ptr(depth_keys), nat.ptr(tile_rects), n, tiles_w, tiles_h,
             nat.ptr(ranges), nat.ptr(totals), c_void_p(host_totals.data_ptr()), nat.ptr(plan),
             plan.numel(), s,
         ),

@@ -41,14 +41,18 @@ def project_and_count(
     covariance_epsilon: float = 0.03,
     records: torch.Tensor | None = None,
     depth_keys: torch.Tensor | None = None,
-) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    tile_rects: torch.Tensor | None = None,
+    bounds: bool = True,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor | None, torch.Tensor]:
     """Projects Gaussians and counts their tiles without compacting.
 
     Returns ``(projected_mean[N,3], inverse_covariance[N,2,2], projected_color[N,3],
     projected_opacity[N,1], bounds[N,2,2] int32, counts[N] int32)`` in the original
     Gaussian order; culled Gaussians keep their slot with ``count == 0``.
-    ``records`` (N x 12 float32) and ``depth_keys`` (N int32) are optional extra
-    outputs used by the fused op.
+    ``records`` (N x 12 float32), ``depth_keys`` (N int32) and ``tile_rects``
+    (N int32, the packed rectangles ``bin_tiles`` reads) are optional extra
+    outputs used by the fused op, which also skips ``bounds`` (``bounds=False``
+    returns None in its place; it needs ``tile_rects``).
     """
     _check_tile(tile_size)
     if color.shape[1] > 16:
@@ -67,7 +71,15 @@ def project_and_count(
     inverse_covariance = mean.new_empty((n, 2, 2))
     projected_color = mean.new_empty((n, 3))
     projected_opacity = mean.new_empty((n, 1))
-    bounds = torch.empty((n, 2, 2), dtype=torch.int32, device=device)
+    if not bounds and tile_rects is None:
+        raise ValueError("bounds=False needs tile_rects")
+    if tile_rects is not None and (
+        tile_rects.device != device or tile_rects.dtype != torch.int32
+        or tile_rects.numel() != mean.shape[0] or not tile_rects.is_contiguous()
+    ):
+        raise ValueError("tile_rects must be a contiguous int32 tensor of N elements on the "
+                         "Gaussians' device")
+    bounds = torch.empty((n, 2, 2), dtype=torch.int32, device=device) if bounds else None
     counts = torch.empty(n, dtype=torch.int32, device=device)
     if n == 0:
         return projected_mean, inverse_covariance, projected_color, projected_opacity, bounds, counts
@@ -84,7 +96,7 @@ def project_and_count(
             c_void_p(camera_translation.data_ptr()), view,
             nat.ptr(projected_mean), nat.ptr(inverse_covariance), nat.ptr(projected_color),
             nat.ptr(projected_opacity), nat.ptr(bounds), nat.ptr(counts), nat.ptr(records),
-            nat.ptr(depth_keys), nat.stream(device),
+            nat.ptr(depth_keys), nat.ptr(tile_rects), nat.stream(device),
         )),
         "project_and_count",
     )

@@ -30,7 +30,14 @@ import torch
 
 from ...timing import stage_timer
 from . import _native as nat
-from .intersections import MAX_BUCKET_TILES, bin_gaussians, bin_tiles, emit_tiles, sort_tiles
+from .intersections import (
+    MAX_BUCKET_TILES,
+    bin_gaussians,
+    bin_tiles,
+    bucketing_fits,
+    emit_tiles,
+    sort_tiles,
+)
 from .interface import _contiguous
 from .project import _check_tile
 
@@ -123,7 +130,12 @@ def forward_views(
     inverse_covariance = mean.new_empty((views, n, 2, 2))
     projected_color = mean.new_empty((views, n, 3))
     projected_opacity = mean.new_empty((views, n, 1))
-    bounds = torch.empty((views, n, 2, 2), dtype=torch.int32, device=device)
+    # Row/column bucketing reads the projection's packed tile rectangles (the
+    # int32 bounds are then not written); the other binning reads bounds.
+    bucketing = bucketing_fits(vn, canvas_w, canvas_h)
+    bounds = (None if bucketing
+              else torch.empty((views, n, 2, 2), dtype=torch.int32, device=device))
+    tile_rects = torch.empty(vn, dtype=torch.int32, device=device) if bucketing else None
     counts = torch.empty((views, n), dtype=torch.int32, device=device)
     records = torch.empty((vn, 12), dtype=torch.float32, device=device)
     depth_keys = torch.empty(vn, dtype=torch.int32, device=device)
@@ -141,18 +153,18 @@ def forward_views(
             ptr(cam_r), ptr(cam_t), ptr(intr), project_view,
             ptr(projected_mean), ptr(inverse_covariance), ptr(projected_color),
             ptr(projected_opacity), ptr(bounds), ptr(counts), ptr(records), ptr(depth_keys),
-            stream,
+            ptr(tile_rects), stream,
         ),
         "project_views",
     )
     mark("project")
-    flat_bounds = bounds.view(vn, 2, 2)
     flat_counts = counts.view(vn)
-    if canvas_w <= MAX_BUCKET_TILES and canvas_h <= MAX_BUCKET_TILES:
+    if bucketing:
         gaussian_ids, ranges = bin_tiles(
-            depth_keys, flat_bounds, flat_counts, canvas_w, canvas_h, timer=mark
+            depth_keys, None, None, canvas_w, canvas_h, timer=mark, tile_rects=tile_rects
         )
     else:
+        flat_bounds = bounds.view(vn, 2, 2)
         order, offsets = bin_gaussians(depth_keys, flat_counts)
         mark("bin")
         total = int(offsets[vn].item()) if vn else 0

@@ -42,7 +42,7 @@ extern "C" {
 
 #define GS_API __attribute__((visibility("default")))
 
-#define GS_ABI_VERSION 12
+#define GS_ABI_VERSION 13
 
 typedef enum gs_status {
   GS_OK = 0,
@@ -117,7 +117,12 @@ GS_API int gs_device_errors(uint32_t* flags, int32_t clear, void* stream);
  * project.py:256-345) with the camera semantics of splats/camera.py:81-124
  * and splats/utils.py:8-75.  num_sh in {1, 4, 9, 16} (SH degree <= 3).
  * `records` (N x 48 B) and `depth_keys` (N x u32: depth bits for counted
- * Gaussians, 0xFFFFFFFF otherwise) are optional (NULL = not written). */
+ * Gaussians, 0xFFFFFFFF otherwise) are optional (NULL = not written), and so
+ * is `tile_rects` (N x u32, no counterpart in the reference: each counted
+ * Gaussian's tile rectangle packed as x0 | (x1 - x0 - 1) << 8 | y0 << 16 |
+ * (y1 - y0 - 1) << 24, 0xFFFFFFFF for the others; tile grids of at most
+ * 256 x 256, else GS_ERR_UNSUPPORTED), the input of gs_bin_tiles_plan.
+ * With tile_rects, `bounds` may be NULL (not written). */
 GS_API int gs_project_and_count(
     const float* mean, const float* rotation, const float* scale,
     const float* opacity, const float* color, int64_t n, int32_t num_sh,
@@ -125,7 +130,7 @@ GS_API int gs_project_and_count(
     gs_view view,
     float* projected_mean, float* inverse_covariance, float* projected_color,
     float* projected_opacity, int32_t* bounds, int32_t* counts,
-    void* records, uint32_t* depth_keys, void* stream);
+    void* records, uint32_t* depth_keys, uint32_t* tile_rects, void* stream);
 
 /* Multi-view projection (no counterpart in the reference, which renders one
  * camera per call): gs_project_and_count for the V = max(view.views, 1)
@@ -133,10 +138,10 @@ GS_API int gs_project_and_count(
  * `view`, each Gaussian's parameters read once per launch of up to 16
  * cameras.  Host arrays: camera_rotations [V, 9], camera_translations [V, 3],
  * intrinsics [V, 4] = (fx, fy, cx, cy) per camera, or NULL for view's.
- * Outputs are [V, N, ...] (view v's at Gaussian v * N).  bounds are in the
- * mosaic's tile grid (each view's rectangle shifted to its tile origin,
- * see gs_view.views), so binning V * N Gaussians over the mosaic's tiles
- * lists every view's tiles in one pass. */
+ * Outputs are [V, N, ...] (view v's at Gaussian v * N).  bounds and
+ * tile_rects are in the mosaic's tile grid (each view's rectangle shifted to
+ * its tile origin, see gs_view.views), so binning V * N Gaussians over the
+ * mosaic's tiles lists every view's tiles in one pass. */
 GS_API int gs_project_views(
     const float* mean, const float* rotation, const float* scale,
     const float* opacity, const float* color, int64_t n, int32_t num_sh,
@@ -144,7 +149,7 @@ GS_API int gs_project_views(
     const float* intrinsics, gs_view view,
     float* projected_mean, float* inverse_covariance, float* projected_color,
     float* projected_opacity, int32_t* bounds, int32_t* counts,
-    void* records, uint32_t* depth_keys, void* stream);
+    void* records, uint32_t* depth_keys, uint32_t* tile_rects, void* stream);
 
 /* Packs the per-Gaussian compositing record from the op's projected outputs
  * (used when compositing is called stage-wise, as composite.py:110 is).
@@ -216,7 +221,8 @@ GS_API int gs_sort_tiles(
     void* workspace, size_t workspace_bytes, void* stream);
 
 /* Row-bucketed binning, used by the op when the tile grid is at most
- * 256 x 256 (otherwise GS_ERR_UNSUPPORTED; use the three calls above).  Same
+ * 256 x 256 (otherwise GS_ERR_UNSUPPORTED) and n is below 2^26 (otherwise
+ * GS_ERR_OVERFLOW); use the three calls above beyond either.  Same
  * sorted ids and ranges as gs_bin_gaussians + gs_emit_tiles + gs_sort_tiles,
  * i.e. the stable (tile, depth bits, index) order of intersections.py:10-88,
  * with the tile-row and tile-column buckets filled directly from the tile
@@ -232,18 +238,26 @@ GS_API int gs_sort_tiles(
  * gs_device_errors) as of that copy: non-zero means an earlier binning or
  * sort call on this GPU left incomplete output.  The tables are built on a
  * side stream, so the host waits for them while the depth sort still runs on
- * `stream`.  `plan` (plan_bytes from
+ * `stream`; `stream` itself is then not made to wait for the side stream
+ * (work enqueued on it after the call follows the side stream's), without
+ * `host_totals` it is.  `plan` (plan_bytes from
  * gs_bin_tiles_plan_bytes) must stay alive until gs_bin_tiles_emit, which
  * takes the totals (device pointer and the values read from it) and writes
- * `sorted_ids` [totals[0]].  depth_keys (as
- * gs_project_and_count writes them: ~0u for Gaussians without
- * intersections) is consumed.  Together they replace intersections.py:44-88
+ * `sorted_ids` [totals[0]].  depth_keys and tile_rects are
+ * gs_project_and_count's (depth_keys: ~0u for Gaussians without
+ * intersections; consumed).  Together they replace intersections.py:44-88
  * for the op. */
 GS_API size_t gs_bin_tiles_plan_bytes(int64_t n, int32_t tiles_w, int32_t tiles_h);
 GS_API int gs_bin_tiles_plan(
-    uint32_t* depth_keys, const int32_t* bounds, const int32_t* counts, int64_t n,
+    uint32_t* depth_keys, const uint32_t* tile_rects, int64_t n,
     int32_t tiles_w, int32_t tiles_h, int64_t* ranges, int64_t* totals, int64_t* host_totals,
     void* plan, size_t plan_bytes, void* stream);
+/* tile_rects (the packing of gs_project_and_count) from bounds [N, 2, 2] and
+ * counts, for callers holding those instead; no counterpart in the
+ * reference. */
+GS_API int gs_pack_tile_rects(
+    const int32_t* bounds, const int32_t* counts, int64_t n, int32_t tiles_w, int32_t tiles_h,
+    uint32_t* tile_rects, void* stream);
 GS_API size_t gs_bin_tiles_emit_bytes(int64_t n, int64_t total, int64_t row_entries,
                                       int64_t blocks, int32_t tiles_w, int32_t tiles_h);
 GS_API int gs_bin_tiles_emit(

@@ -121,11 +121,18 @@ def test_bucketed_binning_host_checks():
     assert lib.gs_bin_tiles_plan_bytes(1000, 120, 68) > lib.gs_bin_tiles_plan_bytes(10, 120, 68)
     assert lib.gs_bin_tiles_plan_bytes(-1, 120, 68) == 0
     assert lib.gs_bin_tiles_emit_bytes(1000, 1 << 20, 1 << 18, 300, 120, 68) >= 3 * 4 * (1 << 18)
-    status = lib.gs_bin_tiles_plan(fake, fake, fake, 10, 257, 4, fake, fake, None, fake, 1 << 20, None)
+    status = lib.gs_bin_tiles_plan(fake, fake, 10, 257, 4, fake, fake, None, fake, 1 << 20, None)
     assert status == nat.GS_ERR_UNSUPPORTED
     assert b"at most 256" in lib.gs_last_error()
-    status = lib.gs_bin_tiles_plan(fake, fake, fake, 10, 120, 68, fake, fake, None, fake, 16, None)
+    status = lib.gs_bin_tiles_plan(fake, fake, 10, 120, 68, fake, fake, None, fake, 16, None)
     assert status == nat.GS_ERR_WORKSPACE
+    # the row pass's look-back packs a row's entry count into 26 bits
+    status = lib.gs_bin_tiles_plan(fake, fake, 1 << 26, 120, 68, fake, fake, None, fake, 1 << 40,
+                                   None)
+    assert status == nat.GS_ERR_OVERFLOW
+    assert b"fewer than 67108864 Gaussians" in lib.gs_last_error()
+    status = lib.gs_pack_tile_rects(fake, fake, 10, 257, 4, fake, None)
+    assert status == nat.GS_ERR_UNSUPPORTED
     # pass-B workgroups must match the intersection total (ceil(total / 4096) .. + rows)
     status = lib.gs_bin_tiles_emit(
         10, 120, 68, fake, 100000, 5000, 1, fake, 1 << 30, fake, fake, fake, 1 << 30, None
@@ -147,10 +154,24 @@ def test_project_rejects_unsupported_sh_before_launch():
     lib = nat.library()
     fake = ctypes.c_void_p(16)
     status = lib.gs_project_and_count(
-        fake, fake, fake, fake, fake, 10, 25, fake, fake, _view(), *([fake] * 6), None, None, None
+        fake, fake, fake, fake, fake, 10, 25, fake, fake, _view(), *([fake] * 6), None, None, None,
+        None,
     )
     assert status == nat.GS_ERR_UNSUPPORTED
     assert b"SH degrees above 3" in lib.gs_last_error()
+    # packed tile rectangles need a grid of at most 256 x 256 tiles
+    status = lib.gs_project_and_count(
+        fake, fake, fake, fake, fake, 10, 16, fake, fake, _view(image_width=257 * 16), *([fake] * 6),
+        None, None, fake, None,
+    )
+    assert status == nat.GS_ERR_UNSUPPORTED
+    assert b"at most 256" in lib.gs_last_error()
+    # without bounds the projection needs tile_rects
+    status = lib.gs_project_and_count(
+        fake, fake, fake, fake, fake, 10, 16, fake, fake, _view(), *([fake] * 4), None, fake,
+        None, None, None, None,
+    )
+    assert status == nat.GS_ERR_INVALID_ARGUMENT
 
 
 @pytest.mark.parametrize("tile", (0, 3, 12, 64))
@@ -197,7 +218,8 @@ def test_misaligned_buffers_rejected():
     fake = ctypes.c_void_p(16)
     bad = ctypes.c_void_p(20)
     status = lib.gs_project_and_count(
-        fake, bad, fake, fake, fake, 10, 16, fake, fake, _view(), *([fake] * 6), None, None, None
+        fake, bad, fake, fake, fake, 10, 16, fake, fake, _view(), *([fake] * 6), None, None, None,
+        None,
     )
     assert status == nat.GS_ERR_INVALID_ARGUMENT
 
@@ -266,7 +288,7 @@ def test_multi_view_host_checks():
     for kw in (dict(views=-1), dict(mosaic_cols=-2)):
         status = lib.gs_project_views(
             fake, fake, fake, fake, fake, 10, 16, fake, fake, None, _view(**kw), *([fake] * 6),
-            None, None, None,
+            None, None, None, None,
         )
         assert status == nat.GS_ERR_INVALID_ARGUMENT
         status = lib.gs_composite(fake, 10, fake, 10, fake, None, _view(**kw), fake, fake, fake,
@@ -275,7 +297,7 @@ def test_multi_view_host_checks():
     # Virtual Gaussian indices (view * N + i) must fit int32.
     status = lib.gs_project_views(
         fake, fake, fake, fake, fake, 1 << 28, 16, fake, fake, None, _view(views=16, mosaic_cols=4),
-        *([fake] * 6), None, None, None,
+        *([fake] * 6), None, None, None, None,
     )
     assert status == nat.GS_ERR_OVERFLOW
     status = lib.gs_project_bwd_views(
@@ -292,7 +314,7 @@ def test_multi_view_host_checks():
     assert status == nat.GS_ERR_OVERFLOW
     # Zero Gaussians: nothing to do.
     assert lib.gs_project_views(None, None, None, None, None, 0, 16, None, None, None,
-                                _view(views=3), *([None] * 8), None) == nat.GS_OK
+                                _view(views=3), *([None] * 9), None) == nat.GS_OK
 
 
 def test_multi_view_fake_implementation_shapes():

@@ -356,7 +356,7 @@ def _views_project_bounds(params, cams, scene, device):
     ptr = nat.ptr
     nat.check(nat.library().gs_project_views(
         *(ptr(p) for p in params), n, params[4].shape[1], ptr(rot), ptr(trans), ptr(intr), view, *(ptr(o) for o in outs), ptr(bounds),
-        ptr(counts), None, None, nat.stream(device)), "project_views")
+        ptr(counts), None, None, None, nat.stream(device)), "project_views")
     return bounds, cols, tw, th
 
 

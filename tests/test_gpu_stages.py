@@ -97,6 +97,92 @@ def test_project_ellipsoid_mode(device):
     rect_flip_tolerant_equal(gpu[4].cpu().numpy(), bounds, proj, 16, extent)
 
 
+def _decode_rects(rects):
+    """[x0, x1, y0, y1] of packed tile rectangles (numpy), decoded from the
+    packing the header documents: x0 | (x1 - x0 - 1) << 8 | y0 << 16 |
+    (y1 - y0 - 1) << 24."""
+    r = rects.cpu().numpy().view(np.uint32).astype(np.int64)
+    x0, y0 = r & 0xFF, (r >> 16) & 0xFF
+    return np.stack([x0, x0 + ((r >> 8) & 0xFF) + 1, y0, y0 + (r >> 24) + 1], -1)
+
+
+def _pack_from_bounds(bounds, counts, tw, th, device):
+    rects = torch.empty(counts.numel(), dtype=torch.int32, device=device)
+    nat.check(nat.library().gs_pack_tile_rects(
+        nat.ptr(bounds), nat.ptr(counts), counts.numel(), tw, th, nat.ptr(rects),
+        nat.stream(device)), "pack_tile_rects")
+    return rects
+
+
+@pytest.mark.parametrize("mode", ("gaussian", "ellipsoid"))
+def test_projection_packs_tile_rects(device, mode):
+    """The projection's packed rectangles decode to its bounds for every
+    Gaussian with intersections and are 0xFFFFFFFF for the others; they equal
+    gs_pack_tile_rects of the bounds and counts, and the projection writes the
+    same ones without bounds (as the op calls it)."""
+    scene = scenes.edge_case_scene(n=3000, sh_degree=1, image_size=(200, 120))
+    cam = scene.cameras[0]
+    fx, fy = cam.focal_length
+    cx, cy = cam.principal_point
+    w, h = cam.image_size
+    tw, th = nat.tiles(w, h, 16)
+    params = [t.to(device) for t in scene.params()]
+    args = (*params, cam.rotation_matrix, cam.translation, fx, fy, cx, cy, w, h, 16, scene.near,
+            scene.far, mode, CONFIDENCE)
+    rects = torch.empty(3000, dtype=torch.int32, device=device)
+    out = project_and_count(*args, tile_rects=rects)
+    bounds, counts = out[4], out[5]
+    counted = counts.cpu().numpy() > 0
+    assert 0 < counted.sum() < 3000
+    raw = rects.cpu().numpy().view(np.uint32)
+    assert (raw[~counted] == 0xFFFFFFFF).all()
+    np.testing.assert_array_equal(_decode_rects(rects)[counted],
+                                  bounds.cpu().numpy().reshape(-1, 4)[counted])
+    assert torch.equal(rects, _pack_from_bounds(bounds, counts, tw, th, device))
+    rects2 = torch.full_like(rects, 7)
+    out2 = project_and_count(*args, tile_rects=rects2, bounds=False)
+    assert out2[4] is None
+    assert torch.equal(rects2, rects) and torch.equal(out2[5], counts)
+
+
+def test_mosaic_projection_packs_shifted_tile_rects(device):
+    """gs_project_views' packed rectangles are in the mosaic's tile grid: each
+    view's bounds shifted to its tile origin, equal to gs_pack_tile_rects of
+    the mosaic bounds."""
+    from gaussian_splats_hip.kernels.rasterize.views import camera_tensors, mosaic_columns
+
+    scene = scenes.config5(seed=3, n=2000, views=5, size=96, focal=120.0)
+    rot, trans, intr, w, h = camera_tensors(scene.cameras)
+    v, n = 5, 2000
+    tw, th = nat.tiles(w, h, 16)
+    cols = mosaic_columns(v, tw, th)
+    rows = -(-v // cols)
+    params = [t.to(device) for t in scene.params()]
+    outs = [params[0].new_empty(s) for s in ((v, n, 3), (v, n, 2, 2), (v, n, 3), (v, n, 1))]
+    bounds = torch.empty((v, n, 2, 2), dtype=torch.int32, device=device)
+    counts = torch.empty((v, n), dtype=torch.int32, device=device)
+    rects = torch.empty(v * n, dtype=torch.int32, device=device)
+    view = nat.make_view(0.0, 0.0, 0.0, 0.0, w, h, 16, scene.near, scene.far, views=v,
+                         mosaic_cols=cols)
+    ptr = nat.ptr
+    print(f"[mosaic rects] {v} views, {cols} columns", flush=True)
+    nat.check(nat.library().gs_project_views(
+        *(ptr(p) for p in params), n, params[4].shape[1], ptr(rot), ptr(trans), ptr(intr), view,
+        *(ptr(o) for o in outs), ptr(bounds), ptr(counts), None, None, ptr(rects),
+        nat.stream(device)), "project_views")
+    flat_b = bounds.view(v * n, 2, 2)
+    flat_c = counts.view(v * n)
+    counted = flat_c.cpu().numpy() > 0
+    decoded = _decode_rects(rects)
+    np.testing.assert_array_equal(decoded[counted], flat_b.cpu().numpy().reshape(-1, 4)[counted])
+    for k in range(v):  # each view's rectangles lie in its block of the mosaic
+        d = decoded[k * n:(k + 1) * n][counted[k * n:(k + 1) * n]]
+        ox, oy = (k % cols) * tw, (k // cols) * th
+        assert len(d) and (d[:, 0] >= ox).all() and (d[:, 1] <= ox + tw).all()
+        assert (d[:, 2] >= oy).all() and (d[:, 3] <= oy + th).all()
+    assert torch.equal(rects, _pack_from_bounds(flat_b, flat_c, cols * tw, rows * th, device))
+
+
 def test_project_rejects_sh4(device):
     scene = scenes.edge_case_scene(n=64, sh_degree=3)
     color = torch.zeros(64, 25, 3)
@@ -506,8 +592,11 @@ def test_device_check_failures_reach_the_host(device):
     ranges = torch.empty((tw * th, 2), dtype=torch.int64, device=device)
     totals = torch.empty(4, dtype=torch.int64, device=device)
     host = torch.zeros(5, dtype=torch.int64, pin_memory=True)
+    rects = torch.empty(n, dtype=torch.int32, device=device)
+    nat.check(lib.gs_pack_tile_rects(nat.ptr(bounds), nat.ptr(counts), n, tw, th, nat.ptr(rects),
+                                     s), "pack")
     print("[device checks] plan", flush=True)
-    nat.check(lib.gs_bin_tiles_plan(nat.ptr(keys), nat.ptr(bounds), nat.ptr(counts), n, tw, th,
+    nat.check(lib.gs_bin_tiles_plan(nat.ptr(keys), nat.ptr(rects), n, tw, th,
                                     nat.ptr(ranges), nat.ptr(totals), c_void_p(host.data_ptr()),
                                     nat.ptr(plan), plan.numel(), s), "plan")
     total, rows, blocks, _, flags = host.tolist()

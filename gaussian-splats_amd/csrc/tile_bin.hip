@@ -596,8 +596,8 @@ constexpr uint64_t kRowCountMask = (uint64_t(1) << kRowCountBits) - 1;
 template <int BITS>
 struct RowLds {
   BucketLds<BITS, 2> b;
+  uint32_t wsum[1 << BITS];    // intersections of the workgroup's items of row d
   uint32_t wstart[1 << BITS];  // intersections of the workgroup's items before row d's first
-  uint32_t wend[1 << BITS];    // ... up to and including row d's last
   uint32_t wofs[1 << BITS];    // W of reordered item j of row d = wofs[d] + its prefix
   uint32_t e0[1 << BITS], e1[1 << BITS], blk[1 << BITS], a1[1 << BITS];  // row tables
   uint32_t waves[kItems][4];   // per round of kBlock items: each wave's sum of widths
@@ -646,6 +646,7 @@ __global__ __launch_bounds__(kBlock) void row_bucket_kernel(
     // hold no items).
     const int d = threadIdx.x;
     if (d < D) {
+      L.wsum[d] = 0;
       const bool row = d < th;
       L.e0[d] = row ? row_e[d] : 0u;
       L.e1[d] = row ? row_e[d + 1] : 0u;
@@ -698,6 +699,11 @@ __global__ __launch_bounds__(kBlock) void row_bucket_kernel(
     g_id[i] = uint32_t(g[i]);
     xw[i] = (r[i] & 0xFFFFu) | (ty << 16);  // first column, width - 1, row
   }
+  // Each row's intersections in this workgroup, for the look-back value
+  // (published right after the ranking; the per-item prefixes follow).
+#pragma unroll
+  for (int i = 0; i < kItems; ++i)
+    if (wid * kSeg + i * 64 + lane < nvalid) atomicAdd(&L.wsum[dig[i]], entry_width(xw[i]));
 
   // 1. Stable rank by row within each wave; the rows' local starts.
   const int seg_valid = nvalid - wid * kSeg;
@@ -716,6 +722,10 @@ __global__ __launch_bounds__(kBlock) void row_bucket_kernel(
   }
   uint32_t all;
   const uint32_t local_start = block_exclusive_scan(tot, sh.scratch, all);
+  // The look-back value: (entries, intersections) of row d in this workgroup,
+  // published at once so that later workgroups can walk past this one.
+  const uint64_t value =
+      threadIdx.x < D ? uint64_t(tot) | (uint64_t(L.wsum[threadIdx.x]) << kRowCountBits) : 0u;
   if (threadIdx.x < D) {
     const int d = threadIdx.x;
     // Wave w's items of row d start at cnt[w][d] in the reordered tile.
@@ -723,6 +733,8 @@ __global__ __launch_bounds__(kBlock) void row_bucket_kernel(
     sh.cnt[1][d] = local_start + n0;
     sh.cnt[2][d] = local_start + n0 + n1;
     sh.cnt[3][d] = local_start + n0 + n1 + n2;
+    sweep::store_status(status + int64_t(b) * D + d,
+                        (b == 0 ? sweep::kFlagPrefix : sweep::kFlagAggregate) | value);
   }
   __syncthreads();
 
@@ -762,14 +774,13 @@ __global__ __launch_bounds__(kBlock) void row_bucket_kernel(
     }
   }
   // A row's items are contiguous: its first item records the widths before
-  // it, its last the widths up to its end.
+  // it.
 #pragma unroll
   for (int i = 0; i < kItems; ++i) {
     const int j = int(threadIdx.x) + i * kBlock;
     if (j < nvalid) {
       const uint32_t d = sh.dig[j];
       if (j == 0 || sh.dig[j - 1] != d) L.wstart[d] = wl[i];
-      if (j == nvalid - 1 || sh.dig[j + 1] != d) L.wend[d] = wl[i] + wv[i];
     }
   }
   __syncthreads();
@@ -778,10 +789,7 @@ __global__ __launch_bounds__(kBlock) void row_bucket_kernel(
   // earlier workgroups.
   if (threadIdx.x < D) {
     const int d = threadIdx.x;
-    const uint64_t wtot = tot ? uint64_t(L.wend[d] - L.wstart[d]) : 0u;
-    const uint64_t value = uint64_t(tot) | (wtot << kRowCountBits);
     uint64_t* mine = status + int64_t(b) * D + d;
-    sweep::store_status(mine, (b == 0 ? sweep::kFlagPrefix : sweep::kFlagAggregate) | value);
     uint64_t excl = 0;
     if (b > 0) {
       excl = sweep::look_back(status, D, b, d, err);

@@ -111,15 +111,18 @@ def stage_bytes(n, k, total, rows, pixels, processed_fwd, processed_bwd):
     """Algorithmic HBM bytes per stage (n Gaussians with k SH coefficients,
     `total` intersections, `rows` row-list entries)."""
     return {
-        # params in (44 + 12k B) -> projected outputs, record, bounds, count, key (116 B)
-        "project": n * (44 + 12 * k) + 116 * n,
-        # depth sort: histogram + 4 passes of (key, id) in and out; rectangles
-        # for the tables; row-list offset scan (order, key, gathered rectangle)
-        "bin": 4 * n + 4 * 16 * n + 20 * n + 28 * n,
-        # pass A writes (id, packed columns) per row entry; the width scan
-        # reads and writes them; pass B reads its windows and writes one id
-        # per intersection
-        "emit": 8 * rows + 8 * rows + 8 * rows + 4 * total,
+        # params in (44 + 12k B) -> projected outputs (48 B), record (48 B),
+        # depth key and packed tile rectangle (4 + 4 B)
+        "project": n * (44 + 12 * k) + 104 * n,
+        # depth sort: histogram + 4 passes of (key, id) in and out, the last
+        # pass also gathering and writing the rectangles in depth order; the
+        # tables' rectangle reads; the row-list offset scan (rectangles in,
+        # offsets out)
+        "bin": 4 * n + 4 * 16 * n + 8 * n + 4 * n + 8 * n,
+        # pass A writes (id, packed columns, row-major position) per row
+        # entry; pass B reads its windows (packed columns, positions) and
+        # writes one id per intersection
+        "emit": 12 * rows + 8 * rows + 4 * total,
         "composite": 40 * processed_fwd + 20 * pixels,
         "composite_bwd": 76 * processed_bwd + 20 * pixels,
         # params in and gradients out; per Gaussian its 9 gradient inputs and
@@ -133,8 +136,7 @@ STAGE_KERNELS = {
     "project": ["project_fwd_kernel"],
     "bin": ["sweep::clear_kernel", "sweep::hist_kernel", "sweep::scatter_kernel x4 (depth sort)",
             "rect_diff_kernel", "tables_kernel", "sweep::scan_kernel<HeightLoad>"],
-    "emit": ["sweep::clear_kernel", "row_bucket_kernel", "sweep::tile_sum_kernel<WidthLoad>",
-             "sweep::tile_offsets_kernel", "sweep::scan_kernel<WidthLoad>", "column_count_kernel",
+    "emit": ["sweep::clear_kernel", "row_bucket_kernel", "column_count_kernel",
              "column_scan_kernel", "column_bucket_kernel"],
     # With row/column bucketing the lists leave the emit stage sorted: the
     # "sort" mark launches nothing and is not reported.
@@ -511,11 +513,11 @@ def cpu_baseline(scene, tile_size, sample_tiles, cam=None, target=None, backward
 def views_stage_bytes(n, k, views, total, rows, pixels, processed_fwd, processed_bwd):
     """Algorithmic HBM bytes per stage of the multi-view step: the projection
     reads the parameters once per launch of up to 16 cameras and writes the
-    116 B of outputs per (view, Gaussian); the backward reads the parameters
+    104 B of outputs per (view, Gaussian); the backward reads the parameters
     once, 40 B per (view, Gaussian) and writes the gradients once."""
     launches = -(-views // 16)
     single = stage_bytes(views * n, k, total, rows, pixels, processed_fwd, processed_bwd)
-    single["project"] = launches * n * (44 + 12 * k) + 116 * views * n
+    single["project"] = launches * n * (44 + 12 * k) + 104 * views * n
     single["project_bwd"] = (launches + 1) * n * (44 + 12 * k) + 40 * views * n
     return single
 
@@ -999,7 +1001,7 @@ def main():
     }
 
     # The HBM-bound kernels, timed per launch the same way: algorithmic bytes
-    # of the projection (parameters in, 116 B of outputs per Gaussian out)
+    # of the projection (parameters in, 104 B of outputs per Gaussian out)
     # and of its backward (parameters and dL/d projected in, gradients out).
     kernels = {}
     for name, t, nbytes in (("project_fwd_kernel", project_timer, bytes_model["project"]),

@@ -71,6 +71,17 @@ __global__ __launch_bounds__(256) void pack_rects_kernel(const int4* __restrict_
   rects[g] = counts[g] > 0 && x1 > x0 && y1 > y0 ? pack_rect(x0, x1 - x0, y0, y1 - y0) : kNoRect;
 }
 
+// Zeroes `words` 32-bit words at p (16-byte aligned): 16-byte stores over
+// grid-stride rounds, then the last words.
+__global__ __launch_bounds__(256) void zero_kernel(uint32_t* __restrict__ p, int64_t words) {
+  const int64_t quads = words >> 2;
+  const int64_t stride = int64_t(gridDim.x) * 256;
+  uint4* q = reinterpret_cast<uint4*>(p);
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < quads; i += stride)
+    q[i] = make_uint4(0u, 0u, 0u, 0u);
+  if (blockIdx.x == 0 && int64_t(threadIdx.x) < (words & 3)) p[(quads << 2) + threadIdx.x] = 0u;
+}
+
 // Corners of each counted Gaussian's rectangle [x0, x1) x [y0, y1) in the 2-D
 // difference array diff2 (th + 1 rows of pitch tw + 1) and ends of its rows in
 // the 1-D difference array rowdiff (th + 1).  Grids whose tables fit LDS: each
@@ -1201,7 +1212,7 @@ GS_API int gs_pack_tile_rects(const int32_t* bounds, const int32_t* counts, int6
 GS_API int gs_bin_tiles_plan(uint32_t* depth_keys, const uint32_t* tile_rects, int64_t n,
                              int32_t tiles_w, int32_t tiles_h, int64_t* ranges,
                              int64_t* totals, int64_t* host_totals, void* plan, size_t plan_bytes,
-                             void* stream) {
+                             void* clear_buf, size_t clear_bytes, void* stream) {
   clear_error();
   GS_TRY(check_grid(tiles_w, tiles_h));
   GS_REQUIRE(n >= 0, GS_ERR_INVALID_ARGUMENT, "invalid Gaussian count");
@@ -1212,6 +1223,8 @@ GS_API int gs_bin_tiles_plan(uint32_t* depth_keys, const uint32_t* tile_rects, i
   GS_REQUIRE(aligned16(ranges), GS_ERR_INVALID_ARGUMENT, "ranges must be 16-byte aligned");
   GS_REQUIRE(n == 0 || (depth_keys && tile_rects), GS_ERR_INVALID_ARGUMENT,
              "null pointer argument");
+  GS_REQUIRE(!clear_buf || (aligned16(clear_buf) && clear_bytes % 4 == 0), GS_ERR_INVALID_ARGUMENT,
+             "the buffer to clear must be 16-byte aligned and a multiple of 4 bytes");
   const PlanLayout p = plan_layout(plan, n, tiles_w, tiles_h);
   GS_REQUIRE(plan_bytes >= p.bytes, GS_ERR_WORKSPACE, "plan workspace too small (%zu < %zu)",
              plan_bytes, p.bytes);
@@ -1257,6 +1270,14 @@ GS_API int gs_bin_tiles_plan(uint32_t* depth_keys, const uint32_t* tile_rects, i
       tables_kernel<false, 1024><<<1, 1024, 0, fork.side>>>(p.table, p.table + words, tiles_w,
                                                             tiles_h, ranges, p.row_a, p.row_e,
                                                             p.row_blk, totals);
+    }
+    // The caller's buffer to clear (the op's gradient accumulator), beside
+    // the depth sort and before the totals: the host's wait for them, or the
+    // join, orders it before anything enqueued after this call.
+    if (clear_buf && clear_bytes >= 4) {
+      const int64_t words = int64_t(clear_bytes / 4);
+      zero_kernel<<<unsigned(std::max<int64_t>(1, std::min<int64_t>(2048, ceil_div(words, 1024)))),
+                    256, 0, fork.side>>>(static_cast<uint32_t*>(clear_buf), words);
     }
     if (st == GS_OK) st = check_launch("bin_tiles_plan (tables)");
     // The totals, then the sticky check-failure word beside them (its low

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parents[2] / "_lib" / "libgs_raster.so"
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 GS_OK = 0
 GS_ERR_INVALID_ARGUMENT = 1
@@ -167,6 +167,28 @@ def walk_buffers(n_contributors: torch.Tensor | None, fingerprint: tuple | None 
     return checkpoints, hits
 
 
+_ACCUMULATOR_ATTR = "_gs_grad_accumulator"
+
+
+def set_grad_accumulator(n_contributors: torch.Tensor, accumulator: torch.Tensor) -> None:
+    """Records on the forward's ``n_contributors`` the zeroed [N, 9] buffer
+    its backward accumulates the projected gradients into (zeroed by the
+    binning's side stream)."""
+    setattr(n_contributors, _ACCUMULATOR_ATTR, accumulator)
+
+
+def take_grad_accumulator(n_contributors: torch.Tensor | None) -> torch.Tensor | None:
+    """The zeroed gradient accumulator recorded with ``n_contributors``, once
+    (a later call gets None and must zero its own).  None while tracing
+    (torch.compile), where the outputs are fake tensors."""
+    if n_contributors is None or torch.compiler.is_compiling():
+        return None
+    acc = getattr(n_contributors, _ACCUMULATOR_ATTR, None)
+    if acc is not None:
+        delattr(n_contributors, _ACCUMULATOR_ATTR)
+    return acc
+
+
 def checkpoint_buffer(view: GsView, num_intersections: int, longest: int,
                       device: torch.device):
     """A checkpoint buffer for gs_composite (256-byte aligned), or None when
@@ -231,7 +253,8 @@ _SIGNATURES = {
     "gs_bin_tiles_plan_bytes": (c_size_t, [c_int64, c_int32, c_int32]),
     "gs_bin_tiles_plan": (
         c_int,
-        [c_void_p] * 2 + [c_int64, c_int32, c_int32] + [c_void_p] * 4 + [c_size_t, c_void_p],
+        [c_void_p] * 2 + [c_int64, c_int32, c_int32] + [c_void_p] * 4
+        + [c_size_t, c_void_p, c_size_t, c_void_p],
     ),
     "gs_pack_tile_rects": (
         c_int, [c_void_p, c_void_p, c_int64, c_int32, c_int32, c_void_p, c_void_p]

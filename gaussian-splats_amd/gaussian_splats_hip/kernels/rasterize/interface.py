@@ -74,9 +74,13 @@ def forward_pipeline(
         )
     )
     mark("project")
+    # The backward's [N, 9] gradient accumulator, zeroed beside the depth
+    # sort (on the binning's side stream) instead of on the stream later.
+    accumulator = (torch.empty((n, 9), dtype=torch.float32, device=device)
+                   if bucketing and record_hits and rendering_mode == "gaussian" else None)
     if bucketing:
         gaussian_ids, ranges = bin_tiles(depth_keys, None, None, tiles_w, tiles_h, timer=mark,
-                                         tile_rects=tile_rects)
+                                         tile_rects=tile_rects, clear=accumulator)
     else:
         order, offsets = bin_gaussians(depth_keys, counts)
         mark("bin")
@@ -94,6 +98,8 @@ def forward_pipeline(
         confidence, records=records, record_hits=record_hits,
     )
     mark("composite")
+    if accumulator is not None:
+        nat.set_grad_accumulator(n_contributors, accumulator)
     return (
         image,
         final_transmittance,
@@ -196,7 +202,10 @@ def _setup_context(ctx, inputs, output) -> None:
     # camera extrinsics in host memory and the two views.
     mean = inputs[0]
     if mean.is_cuda and ctx.rendering_mode == "gaussian":
-        ctx.grad_projected = torch.zeros((mean.shape[0], 9), dtype=torch.float32, device=mean.device)
+        ctx.grad_projected = nat.take_grad_accumulator(output[2])
+        if ctx.grad_projected is None:
+            ctx.grad_projected = torch.zeros((mean.shape[0], 9), dtype=torch.float32,
+                                             device=mean.device)
         ctx.camera_host = (
             nat.host_floats(inputs[5], 9, "camera_rotation"),
             nat.host_floats(inputs[6], 3, "camera_translation"),

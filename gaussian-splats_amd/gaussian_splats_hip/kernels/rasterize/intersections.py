@@ -163,6 +163,7 @@ def bin_tiles(
     timer=None,
     *,
     tile_rects: torch.Tensor | None = None,
+    clear: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Sorted Gaussian ids and int64 ranges [T, 2] by row/column bucketing.
 
@@ -171,7 +172,10 @@ def bin_tiles(
     ``MAX_BUCKET_GAUSSIANS`` Gaussians (``bucketing_fits``); ``depth_keys`` is
     consumed.  The rectangles come from ``tile_rects`` (the projection's packed
     rectangles, as the op passes them; ``bounds`` and ``counts`` are then
-    unused) or are packed here from ``bounds`` and ``counts``.
+    unused) or are packed here from ``bounds`` and ``counts``.  ``clear``
+    (optional, a contiguous float32 or int32 tensor on the device) is zeroed
+    beside the depth sort, on the side stream, before the call returns (the
+    op's gradient accumulator).
     ``timer(name)`` (optional) marks the end of the plan ("bin") and of the
     bucketing passes ("emit").
     """
@@ -204,7 +208,7 @@ def bin_tiles(
         lib.gs_bin_tiles_plan(
             nat.ptr(depth_keys), nat.ptr(tile_rects), n, tiles_w, tiles_h,
             nat.ptr(ranges), nat.ptr(totals), c_void_p(host_totals.data_ptr()), nat.ptr(plan),
-            plan.numel(), s,
+            plan.numel(), nat.ptr(clear), nat.buffer_bytes(clear), s,
         ),
         "bin_tiles_plan",
     )

@@ -159,9 +159,14 @@ def forward_views(
     )
     mark("project")
     flat_counts = counts.view(vn)
+    # The backward's [V N, 9] gradient accumulator, zeroed beside the depth
+    # sort (on the binning's side stream) instead of on the stream later.
+    accumulator = (torch.empty((vn, 9), dtype=torch.float32, device=device)
+                   if bucketing and record_hits and rendering_mode == "gaussian" else None)
     if bucketing:
         gaussian_ids, ranges = bin_tiles(
-            depth_keys, None, None, canvas_w, canvas_h, timer=mark, tile_rects=tile_rects
+            depth_keys, None, None, canvas_w, canvas_h, timer=mark, tile_rects=tile_rects,
+            clear=accumulator,
         )
     else:
         flat_bounds = bounds.view(vn, 2, 2)
@@ -200,6 +205,8 @@ def forward_views(
         "composite",
     )
     nat.set_walk_state(n_contributors, None, checkpoints, hits)
+    if accumulator is not None:
+        nat.set_grad_accumulator(n_contributors, accumulator)
     mark("composite")
     return (
         image,
@@ -384,7 +391,9 @@ def backward_views(
     ptr = nat.ptr
     view = _mosaic_view(w, h, tile, views, cols, opacity_threshold=opacity_threshold,
                         active_tiles=active_tiles)
-    grad_projected = torch.zeros((views * n, 9), dtype=torch.float32, device=device)
+    grad_projected = nat.take_grad_accumulator(saved[1])
+    if grad_projected is None:
+        grad_projected = torch.zeros((views * n, 9), dtype=torch.float32, device=device)
     if order is None:
         order = nat.dispatch_plan(view, ranges.shape[0], device, ranges=ranges,
                                   n_contributors=n_contributors)

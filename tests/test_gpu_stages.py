@@ -351,6 +351,23 @@ def test_bucketed_binning_empty_and_deterministic(device):
     assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
 
 
+@pytest.mark.parametrize("n, words", [(20000, 20000 * 9), (0, 4 * 9 + 1)])
+def test_bucketed_binning_clears_the_given_buffer(device, n, words):
+    """bin_tiles zeroes its `clear` buffer (the op's gradient accumulator) on
+    the side stream before it returns; the lists are those of a call without
+    it.  Word counts that are not a multiple of four take the tail path; with
+    no Gaussians only the side stream's work runs."""
+    b, d, c = _random_rects(n=max(n, 1), tiles_w=120, tiles_h=68, seed=5)
+    b, d, c = b[:n], d[:n], c[:n]
+    buf = torch.full((words,), 3.5, dtype=torch.float32, device=device)
+    print(f"[clear] n={n} words={words}", flush=True)
+    sid, rng = bin_tiles(_depth_keys(d, c).to(device), b.to(device), c.to(device), 120, 68,
+                         clear=buf)
+    assert not bool(buf.ne(0).any())
+    sid2, rng2 = bin_tiles(_depth_keys(d, c).to(device), b.to(device), c.to(device), 120, 68)
+    assert torch.equal(sid, sid2) and torch.equal(rng, rng2)
+
+
 def test_intersections_empty(device):
     bounds = torch.zeros(5, 2, 2, dtype=torch.int32, device=device)
     counts = torch.zeros(5, dtype=torch.int32, device=device)
@@ -598,7 +615,7 @@ def test_device_check_failures_reach_the_host(device):
     print("[device checks] plan", flush=True)
     nat.check(lib.gs_bin_tiles_plan(nat.ptr(keys), nat.ptr(rects), n, tw, th,
                                     nat.ptr(ranges), nat.ptr(totals), c_void_p(host.data_ptr()),
-                                    nat.ptr(plan), plan.numel(), s), "plan")
+                                    nat.ptr(plan), plan.numel(), None, 0, s), "plan")
     total, rows, blocks, _, flags = host.tolist()
     assert flags == 0 and total > 0
     wrong_rows = rows + 1

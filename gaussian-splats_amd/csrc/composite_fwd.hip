@@ -51,6 +51,11 @@ struct CompositeArgs {
   // The walked batches' hit masks (hit_mask_slot), or null: none.
   uint64_t* hit_masks;
   int64_t hit_capacity;  // words
+  // The backward's dispatch keys (gs_tile_order's workspace layout: per tile
+  // its largest contributor count, capped at 2^16 - 1, then per tile the
+  // checkpoints a backward walk crosses), written by whole-tile walks; or
+  // null: none.
+  uint32_t* tile_keys;
 };
 
 // One wave composites PIX pixels per lane of `tile`: the 64-pixel bands
@@ -59,10 +64,12 @@ struct CompositeArgs {
 // With `checkpoints` (whole tiles only) the walk records the checkpoints
 // described at CheckpointLayout; with HITS, every walked batch's overlap
 // ballot in the hit-mask words of each of the wave's bands.
+// With `write_key` (a whole-tile walk) and a.tile_keys, the tile's backward
+// dispatch key and checkpoint crossings are written once its walk ends.
 template <int TILE, bool ELLIPSOID, int PIX, bool HITS, bool PF = false>
 __device__ __forceinline__ void composite_tile(const CompositeArgs& a, float4 (*chunk)[3],
                                                int* ck_slots, int lane, int tile, int band0,
-                                               bool checkpoints) {
+                                               bool checkpoints, bool write_key) {
   constexpr int NPIX = TILE * TILE;
 
   // Mosaic tile -> view and the tile's pixel origin inside that view.
@@ -70,12 +77,19 @@ __device__ __forceinline__ void composite_tile(const CompositeArgs& a, float4 (*
   const int ty = tile / a.tiles_w;
   const int vx = tx / a.view_tw, vy = ty / a.view_th;
   const int view = vy * a.cols + vx;
-  if (view >= a.views) return;  // an empty slot of the mosaic's last row
-  const int ox = (tx - vx * a.view_tw) * TILE, oy = (ty - vy * a.view_th) * TILE;
-  const int64_t view_base = int64_t(view) * a.width * a.height;  // first pixel of the view
   const int64_t start = a.ranges[2 * tile];
   const int64_t end = a.ranges[2 * tile + 1];
   const int list_len = int(end - start);
+  write_key = write_key && a.tile_keys;
+  if (view >= a.views) {  // an empty slot of the mosaic's last row
+    if (write_key && lane == 0) {
+      a.tile_keys[tile] = 0u;
+      a.tile_keys[a.num_tiles + tile] = uint32_t(checkpoint_count(start, 0, list_len));
+    }
+    return;
+  }
+  const int ox = (tx - vx * a.view_tw) * TILE, oy = (ty - vy * a.view_th) * TILE;
+  const int64_t view_base = int64_t(view) * a.width * a.height;  // first pixel of the view
 
   // The lane's pixels share one column (see column_terms).
   const float pxf = float(ox + lane % TILE);
@@ -278,6 +292,18 @@ __device__ __forceinline__ void composite_tile(const CompositeArgs& a, float4 (*
       a.n_contrib[pix] = ncon[k];
     }
   }
+  if (write_key) {
+    // The tile's largest contributor count (pixels outside the image hold 0).
+    int m = 0;
+#pragma unroll
+    for (int k = 0; k < PIX; ++k) m = max(m, ncon[k]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = max(m, __shfl_xor(m, o, 64));
+    if (lane == 0) {
+      a.tile_keys[tile] = uint32_t(min(m, 0xFFFF));
+      a.tile_keys[a.num_tiles + tile] = uint32_t(checkpoint_count(start, m, list_len));
+    }
+  }
 }
 
 // kCompositeWaves waves per workgroup, one work item each (composite_item);
@@ -313,15 +339,15 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_fwd_kernel(Com
     constexpr int QPIX = PIX_TILE / kCompositeWaves;
     if (kind == kItemQuarter) {
       composite_tile<TILE, ELLIPSOID, QPIX, HITS>(a, chunk[wid], ck_slots[wid], lane, tile,
-                                                  index * QPIX, false);
+                                                  index * QPIX, false, false);
     } else {
       for (int q = 0; q < kCompositeWaves; ++q)
         composite_tile<TILE, ELLIPSOID, QPIX, HITS>(a, chunk[wid], ck_slots[wid], lane, tile,
-                                                    q * QPIX, false);
+                                                    q * QPIX, false, false);
     }
   } else {
     composite_tile<TILE, ELLIPSOID, PIX_TILE, HITS, CKPT>(a, chunk[wid], ck_slots[wid], lane, tile,
-                                                          0, CKPT);
+                                                          0, CKPT, true);
   }
 }
 
@@ -393,7 +419,8 @@ extern "C" GS_API int gs_composite(const void* records, int64_t num_records,
                                    float* image, float* final_transmittance,
                                    int32_t* n_contributors, void* checkpoints,
                                    size_t checkpoint_bytes, uint64_t* hit_masks,
-                                   size_t hit_mask_bytes, void* stream) {
+                                   size_t hit_mask_bytes, uint32_t* tile_keys,
+                                   size_t tile_keys_bytes, void* stream) {
   clear_error();
   GS_TRY(check_view(view, true));
   GS_REQUIRE(ranges && image && final_transmittance && n_contributors, GS_ERR_INVALID_ARGUMENT,
@@ -434,6 +461,12 @@ extern "C" GS_API int gs_composite(const void* records, int64_t num_records,
   a.ckpt_capacity = 0;
   a.hit_masks = hit_masks;
   a.hit_capacity = 0;
+  GS_REQUIRE(!tile_keys || tile_keys_bytes >= size_t(a.num_tiles) * 2 * sizeof(uint32_t),
+             GS_ERR_WORKSPACE, "tile key buffer too small (%zu bytes, need %zu)",
+             tile_keys_bytes, size_t(a.num_tiles) * 2 * sizeof(uint32_t));
+  // Keys come from whole-tile walks; with every tile split into quarters the
+  // backward's plan computes them itself.
+  a.tile_keys = plan.split_all ? nullptr : tile_keys;
   if (hit_masks) {
     GS_REQUIRE(view.rendering_mode == GS_MODE_GAUSSIAN, GS_ERR_UNSUPPORTED,
                "hit masks are recorded for Gaussian rendering only (its backward reads them)");

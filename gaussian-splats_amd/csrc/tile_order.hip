@@ -288,18 +288,27 @@ int scratch_keys(hipStream_t stream, uint32_t** keys) {
 
 // Both kernels on `s`: keys for every tile, then the per-region plans.
 // Every key the plan kernel reads is written by the key kernel of the same
-// call, so `key` needs no clearing.
+// call, or, with keys_ready, by the forward compositing that produced
+// n_contributors (gs_composite's tile_keys: whole-tile walks write every
+// tile's key), so `key` needs no clearing.
 int tile_order_launch(const int64_t* ranges, const int32_t* n_contributors, const gs_view& view,
-                      const Mosaic& m, int32_t* items, uint32_t* key, hipStream_t s) {
+                      const Mosaic& m, int32_t* items, uint32_t* key, bool keys_ready,
+                      hipStream_t s) {
   const int num_tiles = m.num_tiles();
   GS_REQUIRE(num_tiles < (1 << 24), GS_ERR_OVERFLOW, "too many tiles (%d)", num_tiles);
   const DispatchPlan plan =
       dispatch_plan(num_tiles, view.tile_size, view.active_tiles, n_contributors != nullptr);
   uint32_t* crossings = key + num_tiles;
-  tile_key_kernel<<<unsigned(ceil_div(num_tiles, 4)), 256, 0, s>>>(
-      ranges, n_contributors, m.tiles_w(), num_tiles, view.tile_size, view.image_width,
-      view.image_height, m.tw, m.th, m.cols, m.views, key, crossings);
-  GS_TRY(check_launch("tile_order keys"));
+  // The forward writes keys only when it walked whole tiles.
+  const bool forward_keys = keys_ready && n_contributors &&
+                            !dispatch_plan(num_tiles, view.tile_size, view.active_tiles, false)
+                                 .split_all;
+  if (!forward_keys) {
+    tile_key_kernel<<<unsigned(ceil_div(num_tiles, 4)), 256, 0, s>>>(
+        ranges, n_contributors, m.tiles_w(), num_tiles, view.tile_size, view.image_width,
+        view.image_height, m.tw, m.th, m.cols, m.views, key, crossings);
+    GS_TRY(check_launch("tile_order keys"));
+  }
   tile_plan_kernel<<<8, kOrderThreads, 0, s>>>(key, crossings, num_tiles,
                                                 plan.segments ? 1 : 0, plan.split_all ? 1 : 0,
                                                 plan.items() / 8, items);
@@ -324,7 +333,7 @@ GS_API int64_t gs_tile_order_items(gs_view view, int32_t by_contributors) {
 
 GS_API int gs_tile_order(const int64_t* ranges, const int32_t* n_contributors, gs_view view,
                          int32_t* order, void* workspace, size_t workspace_bytes,
-                         void* stream) {
+                         int32_t keys_ready, void* stream) {
   clear_error();
   GS_TRY(check_view(view, true));
   const Mosaic m = mosaic_of(view);
@@ -335,7 +344,8 @@ GS_API int gs_tile_order(const int64_t* ranges, const int32_t* n_contributors, g
              GS_ERR_WORKSPACE, "workspace too small (%zu bytes, need %zu)", workspace_bytes,
              gs_tile_order_workspace_bytes(num_tiles));
   return tile_order_launch(ranges, n_contributors, view, m, order,
-                           static_cast<uint32_t*>(workspace), as_stream(stream));
+                           static_cast<uint32_t*>(workspace), keys_ready != 0,
+                           as_stream(stream));
 }
 
 GS_API int gs_tile_order_noalloc(const int64_t* ranges, const int32_t* n_contributors,
@@ -353,7 +363,7 @@ GS_API int gs_tile_order_noalloc(const int64_t* ranges, const int32_t* n_contrib
   const hipStream_t s = as_stream(stream);
   uint32_t* keys = nullptr;
   GS_TRY(scratch_keys(s, &keys));
-  return tile_order_launch(ranges, n_contributors, view, m, order, keys, s);
+  return tile_order_launch(ranges, n_contributors, view, m, order, keys, false, s);
 }
 
 }  // extern "C"

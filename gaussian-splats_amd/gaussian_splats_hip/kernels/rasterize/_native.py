@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parents[2] / "_lib" / "libgs_raster.so"
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 GS_OK = 0
 GS_ERR_INVALID_ARGUMENT = 1
@@ -167,26 +167,30 @@ def walk_buffers(n_contributors: torch.Tensor | None, fingerprint: tuple | None 
     return checkpoints, hits
 
 
-_ACCUMULATOR_ATTR = "_gs_grad_accumulator"
+_FORWARD_BUFFERS_ATTR = "_gs_forward_buffers"
 
 
-def set_grad_accumulator(n_contributors: torch.Tensor, accumulator: torch.Tensor) -> None:
-    """Records on the forward's ``n_contributors`` the zeroed [N, 9] buffer
-    its backward accumulates the projected gradients into (zeroed by the
-    binning's side stream)."""
-    setattr(n_contributors, _ACCUMULATOR_ATTR, accumulator)
+def set_forward_buffer(n_contributors: torch.Tensor, name: str, buffer: torch.Tensor) -> None:
+    """Records on the forward's ``n_contributors`` a buffer the forward
+    prepared for its backward: "grad_accumulator", the [N, 9] buffer the
+    compositing backward accumulates into (zeroed by the binning's side
+    stream), or "tile_keys", the backward's dispatch keys (gs_composite's
+    tile_keys)."""
+    buffers = getattr(n_contributors, _FORWARD_BUFFERS_ATTR, None)
+    if buffers is None:
+        buffers = {}
+        setattr(n_contributors, _FORWARD_BUFFERS_ATTR, buffers)
+    buffers[name] = buffer
 
 
-def take_grad_accumulator(n_contributors: torch.Tensor | None) -> torch.Tensor | None:
-    """The zeroed gradient accumulator recorded with ``n_contributors``, once
-    (a later call gets None and must zero its own).  None while tracing
+def take_forward_buffer(n_contributors: torch.Tensor | None, name: str) -> torch.Tensor | None:
+    """The buffer recorded under ``name`` with ``n_contributors``, once (a
+    later call gets None and must make its own).  None while tracing
     (torch.compile), where the outputs are fake tensors."""
     if n_contributors is None or torch.compiler.is_compiling():
         return None
-    acc = getattr(n_contributors, _ACCUMULATOR_ATTR, None)
-    if acc is not None:
-        delattr(n_contributors, _ACCUMULATOR_ATTR)
-    return acc
+    buffers = getattr(n_contributors, _FORWARD_BUFFERS_ATTR, None)
+    return buffers.pop(name, None) if buffers else None
 
 
 def checkpoint_buffer(view: GsView, num_intersections: int, longest: int,
@@ -268,7 +272,7 @@ _SIGNATURES = {
     "gs_tile_order_workspace_bytes": (c_size_t, [c_int32]),
     "gs_tile_order_items": (c_int64, [GsView, c_int32]),
     "gs_tile_order": (
-        c_int, [c_void_p, c_void_p, GsView, c_void_p, c_void_p, c_size_t, c_void_p]
+        c_int, [c_void_p, c_void_p, GsView, c_void_p, c_void_p, c_size_t, c_int32, c_void_p]
     ),
     "gs_tile_order_noalloc": (c_int, [c_void_p, c_void_p, GsView, c_void_p, c_void_p]),
     "gs_composite_checkpoint_bytes": (c_size_t, [GsView, c_int64, c_int64]),
@@ -276,7 +280,7 @@ _SIGNATURES = {
     "gs_composite": (
         c_int,
         [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, GsView]
-        + [c_void_p] * 4 + [c_size_t, c_void_p, c_size_t, c_void_p],
+        + [c_void_p] * 4 + [c_size_t, c_void_p, c_size_t, c_void_p, c_size_t, c_void_p],
     ),
     "gs_composite_bwd": (
         c_int,
@@ -526,7 +530,7 @@ def dispatch_plan(
     ws = workspace(lib.gs_tile_order_workspace_bytes(num_tiles), device)
     check(
         lib.gs_tile_order(
-            ptr(ranges), ptr(n_contributors), view, ptr(items), ptr(ws), ws.numel(),
+            ptr(ranges), ptr(n_contributors), view, ptr(items), ptr(ws), ws.numel(), 0,
             stream(device),
         ),
         "tile_order",

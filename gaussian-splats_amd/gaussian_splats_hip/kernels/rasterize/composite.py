@@ -57,13 +57,16 @@ def composite(
     records: torch.Tensor | None = None,
     order: torch.Tensor | None = None,
     record_hits: bool = True,
+    tile_keys: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Composites the sorted per-tile lists; returns ``(image[H,W,3],
     final_transmittance[H,W], n_contributors[H,W] int32)``.  The walk's
     checkpoints and (``record_hits``, Gaussian mode) hit masks (gs_composite)
     are recorded on the returned ``n_contributors`` with a fingerprint of
     this call's arguments; ``composite_bwd`` uses them only when its own
-    arguments carry the same fingerprint."""
+    arguments carry the same fingerprint.  ``tile_keys`` (optional, a
+    gs_tile_order workspace) receives the backward plan's keys as the walks
+    end (gs_composite's tile_keys)."""
     _check_tile(tile_size)
     device = nat.require_gpu(mean, gaussian_ids, ranges)
     if records is None:
@@ -96,7 +99,8 @@ def composite(
             nat.ptr(records), records.shape[0], nat.ptr(gaussian_ids), gaussian_ids.numel(),
             nat.ptr(ranges), nat.ptr(order), view, nat.ptr(image), nat.ptr(final_transmittance),
             nat.ptr(n_contributors), nat.ptr(checkpoints), nat.buffer_bytes(checkpoints),
-            nat.ptr(hits), nat.buffer_bytes(hits), nat.stream(device),
+            nat.ptr(hits), nat.buffer_bytes(hits), nat.ptr(tile_keys),
+            nat.buffer_bytes(tile_keys), nat.stream(device),
         )),
         "composite",
     )

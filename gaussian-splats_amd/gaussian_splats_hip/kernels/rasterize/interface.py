@@ -92,14 +92,21 @@ def forward_pipeline(
         mark("emit")
         gaussian_ids, ranges = sort_tiles(tile_keys, ids, tiles_w * tiles_h)
     mark("sort")
+    # With a backward to follow, the compositing walks write its dispatch
+    # plan's keys (the backward's gs_tile_order then skips its key kernel).
+    tile_keys = (nat.workspace(nat.library().gs_tile_order_workspace_bytes(ranges.shape[0]),
+                               device)
+                 if record_hits and rendering_mode == "gaussian" else None)
     image, final_transmittance, n_contributors = composite(
         projected_mean, inverse_covariance, projected_color, projected_opacity, gaussian_ids,
         ranges, image_width, image_height, tile_size, opacity_threshold, rendering_mode,
-        confidence, records=records, record_hits=record_hits,
+        confidence, records=records, record_hits=record_hits, tile_keys=tile_keys,
     )
     mark("composite")
     if accumulator is not None:
-        nat.set_grad_accumulator(n_contributors, accumulator)
+        nat.set_forward_buffer(n_contributors, "grad_accumulator", accumulator)
+    if tile_keys is not None:
+        nat.set_forward_buffer(n_contributors, "tile_keys", tile_keys)
     return (
         image,
         final_transmittance,
@@ -202,7 +209,7 @@ def _setup_context(ctx, inputs, output) -> None:
     # camera extrinsics in host memory and the two views.
     mean = inputs[0]
     if mean.is_cuda and ctx.rendering_mode == "gaussian":
-        ctx.grad_projected = nat.take_grad_accumulator(output[2])
+        ctx.grad_projected = nat.take_forward_buffer(output[2], "grad_accumulator")
         if ctx.grad_projected is None:
             ctx.grad_projected = torch.zeros((mean.shape[0], 9), dtype=torch.float32,
                                              device=mean.device)
@@ -220,24 +227,30 @@ def _setup_context(ctx, inputs, output) -> None:
         lib = nat.library()
         order = torch.empty(lib.gs_tile_order_items(ctx.view_composite, 1), dtype=torch.int32,
                             device=mean.device)
-        order_ws = nat.workspace(lib.gs_tile_order_workspace_bytes(num_tiles), mean.device)
+        # The forward's walks wrote the plan's keys into this workspace, when
+        # they ran as whole tiles (gs_tile_order checks).
+        order_ws = nat.take_forward_buffer(output[2], "tile_keys")
+        keys_ready = order_ws is not None
+        if order_ws is None:
+            order_ws = nat.workspace(lib.gs_tile_order_workspace_bytes(num_tiles), mean.device)
         # The backward's dispatch plan depends only on the forward's lists and
         # contributor counts, so it is computed now, behind the forward on the
         # stream: the backward then starts with the compositing kernel.
-        _launch_backward_plan(output[8], output[2], ctx.view_composite, order, order_ws)
+        _launch_backward_plan(output[8], output[2], ctx.view_composite, order, order_ws,
+                              keys_ready)
         ctx.tile_order = order
     else:
         ctx.grad_projected = None
 
 
 @torch.compiler.disable
-def _launch_backward_plan(ranges, n_contributors, view, order, order_ws) -> None:
+def _launch_backward_plan(ranges, n_contributors, view, order, order_ws, keys_ready) -> None:
     """gs_tile_order for the backward, run eagerly (also under torch.compile,
     which cannot trace the C-ABI call)."""
     nat.check(
         nat.library().gs_tile_order(
             nat.ptr(ranges), nat.ptr(n_contributors), view, nat.ptr(order), nat.ptr(order_ws),
-            order_ws.numel(), nat.stream(ranges.device),
+            order_ws.numel(), 1 if keys_ready else 0, nat.stream(ranges.device),
         ),
         "tile_order",
     )

@@ -200,13 +200,13 @@ def forward_views(
             ptr(records), records.shape[0], ptr(gaussian_ids), gaussian_ids.numel(), ptr(ranges),
             ptr(plan), view, ptr(image), ptr(final_transmittance), ptr(n_contributors),
             ptr(checkpoints), nat.buffer_bytes(checkpoints), ptr(hits), nat.buffer_bytes(hits),
-            stream,
+            None, 0, stream,
         ),
         "composite",
     )
     nat.set_walk_state(n_contributors, None, checkpoints, hits)
     if accumulator is not None:
-        nat.set_grad_accumulator(n_contributors, accumulator)
+        nat.set_forward_buffer(n_contributors, "grad_accumulator", accumulator)
     mark("composite")
     return (
         image,
@@ -391,7 +391,7 @@ def backward_views(
     ptr = nat.ptr
     view = _mosaic_view(w, h, tile, views, cols, opacity_threshold=opacity_threshold,
                         active_tiles=active_tiles)
-    grad_projected = nat.take_grad_accumulator(saved[1])
+    grad_projected = nat.take_forward_buffer(saved[1], "grad_accumulator")
     if grad_projected is None:
         grad_projected = torch.zeros((views * n, 9), dtype=torch.float32, device=device)
     if order is None:

@@ -42,7 +42,7 @@ extern "C" {
 
 #define GS_API __attribute__((visibility("default")))
 
-#define GS_ABI_VERSION 14
+#define GS_ABI_VERSION 15
 
 typedef enum gs_status {
   GS_OK = 0,
@@ -285,12 +285,17 @@ GS_API int gs_bin_tiles_emit(
  * tile's pixels (a plan for gs_composite_bwd).  The compositing call takes
  * the plan made for it with the same view (tile size, mosaic and
  * active_tiles); its results do not depend on it.  The workspace holds two
- * words per tile. */
+ * words per tile: each tile's key, then its checkpoint crossings.  With
+ * keys_ready (a backward plan), the workspace was passed as gs_composite's
+ * tile_keys for the forward that produced n_contributors with this view, and
+ * the keys it wrote are used instead of being recomputed (when that forward
+ * split every tile into quarters it wrote none, and they are recomputed). */
 GS_API size_t gs_tile_order_workspace_bytes(int32_t num_tiles);
 GS_API int64_t gs_tile_order_items(gs_view view, int32_t by_contributors); /* -1: bad view */
 GS_API int gs_tile_order(
     const int64_t* ranges, const int32_t* n_contributors, gs_view view,
-    int32_t* tile_order, void* workspace, size_t workspace_bytes, void* stream);
+    int32_t* tile_order, void* workspace, size_t workspace_bytes, int32_t keys_ready,
+    void* stream);
 
 /* gs_tile_order without a workspace argument (no counterpart in the
  * reference): for callers that cannot allocate device memory (code under HIP
@@ -344,13 +349,20 @@ GS_API size_t gs_composite_checkpoint_bytes(gs_view view, int64_t num_intersecti
  * contributes to a pixel is), instead of every entry of its walk.  The slots
  * assume the tiles' lists follow each other in tile order, as the binning
  * writes them; batches the walk does not reach are not written.  Gaussian
- * rendering only (GS_ERR_UNSUPPORTED otherwise). */
+ * rendering only (GS_ERR_UNSUPPORTED otherwise).
+ * tile_keys (optional, gs_tile_order_workspace_bytes(tiles) bytes; no
+ * counterpart in the reference): a workspace for the backward's
+ * gs_tile_order, filled as each tile's walk ends with its key (the largest
+ * contributor count of its pixels, capped at 2^16 - 1) and its checkpoint
+ * crossings, so that plan (keys_ready) does not read n_contributors again.
+ * Not written when every tile is split into quarters. */
 GS_API size_t gs_composite_hit_mask_bytes(gs_view view, int64_t num_intersections);
 GS_API int gs_composite(
     const void* records, int64_t num_records, const int32_t* gaussian_ids,
     int64_t num_intersections, const int64_t* ranges, const int32_t* tile_order, gs_view view,
     float* image, float* final_transmittance, int32_t* n_contributors, void* checkpoints,
-    size_t checkpoint_bytes, uint64_t* hit_masks, size_t hit_mask_bytes, void* stream);
+    size_t checkpoint_bytes, uint64_t* hit_masks, size_t hit_mask_bytes, uint32_t* tile_keys,
+    size_t tile_keys_bytes, void* stream);
 
 /* Back-to-front compositing gradient, accumulated with atomics into
  * grad_projected[N,9] (zeroed by the caller), from the op's projected outputs

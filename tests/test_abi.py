@@ -45,10 +45,10 @@ def test_tile_order_host_checks():
     assert lib.gs_tile_order_workspace_bytes(8160) >= 8160 * 4
     ws = lib.gs_tile_order_workspace_bytes(8160)
     view = _view(tile_size=16)
-    assert lib.gs_tile_order(null, null, view, fake, fake, ws, null) == nat.GS_ERR_INVALID_ARGUMENT
-    assert lib.gs_tile_order(fake, null, view, null, fake, ws, null) == nat.GS_ERR_INVALID_ARGUMENT
-    assert lib.gs_tile_order(fake, null, view, fake, fake, 0, null) == nat.GS_ERR_WORKSPACE
-    assert lib.gs_tile_order(fake, null, _view(tile_size=3), fake, fake, ws, null) in (
+    assert lib.gs_tile_order(null, null, view, fake, fake, ws, 0, null) == nat.GS_ERR_INVALID_ARGUMENT
+    assert lib.gs_tile_order(fake, null, view, null, fake, ws, 0, null) == nat.GS_ERR_INVALID_ARGUMENT
+    assert lib.gs_tile_order(fake, null, view, fake, fake, 0, 0, null) == nat.GS_ERR_WORKSPACE
+    assert lib.gs_tile_order(fake, null, _view(tile_size=3), fake, fake, ws, 0, null) in (
         nat.GS_ERR_INVALID_ARGUMENT, nat.GS_ERR_UNSUPPORTED)
 
 
@@ -185,7 +185,7 @@ def test_invalid_tile_sizes(tile):
     lib = nat.library()
     fake = ctypes.c_void_p(16)
     status = lib.gs_composite(fake, 10, fake, 10, fake, None, _view(tile_size=tile), fake, fake,
-                              fake, None, 0, None, 0, None)
+                              fake, None, 0, None, 0, None, 0, None)
     assert status in (nat.GS_ERR_INVALID_ARGUMENT, nat.GS_ERR_UNSUPPORTED)
 
 
@@ -206,14 +206,20 @@ def test_hit_masks_host_checks():
     fake = ctypes.c_void_p(16)
     view = _view(rendering_mode="ellipsoid")
     status = lib.gs_composite(fake, 10, fake, 10, fake, None, view, fake, fake, fake, None, 0,
-                              fake, 1 << 20, None)
+                              fake, 1 << 20, None, 0, None)
     assert status == nat.GS_ERR_UNSUPPORTED
     assert b"Gaussian rendering" in lib.gs_last_error()
     need = lib.gs_composite_hit_mask_bytes(_view(), 10)
     assert need > 0 and need % 8 == 0
     status = lib.gs_composite(fake, 10, fake, 10, fake, None, _view(), fake, fake, fake, None, 0,
-                              fake, need - 8, None)
+                              fake, need - 8, None, 0, None)
     assert status == nat.GS_ERR_WORKSPACE
+    # the backward plan's key buffer holds two words per tile
+    tiles = nat.tiles(100, 100, 16)
+    status = lib.gs_composite(fake, 10, fake, 10, fake, None, _view(), fake, fake, fake, None, 0,
+                              None, 0, fake, 8 * tiles[0] * tiles[1] - 4, None)
+    assert status == nat.GS_ERR_WORKSPACE
+    assert b"tile key buffer too small" in lib.gs_last_error()
     status = lib.gs_composite_bwd(*([fake] * 4), 10, *([fake] * 5), None, _view(), fake, None,
                                   None, 0, 10, fake, need - 8, None)
     assert status == nat.GS_ERR_WORKSPACE
@@ -298,7 +304,7 @@ def test_multi_view_host_checks():
         )
         assert status == nat.GS_ERR_INVALID_ARGUMENT
         status = lib.gs_composite(fake, 10, fake, 10, fake, None, _view(**kw), fake, fake, fake,
-                                  None, 0, None, 0, None)
+                                  None, 0, None, 0, None, 0, None)
         assert status == nat.GS_ERR_INVALID_ARGUMENT
     # Virtual Gaussian indices (view * N + i) must fit int32.
     status = lib.gs_project_views(
@@ -315,7 +321,7 @@ def test_multi_view_host_checks():
     status = lib.gs_composite(
         fake, 10, fake, 10, fake, None, _view(image_width=1 << 16, image_height=1 << 16,
                                               tile_size=4, views=64, mosaic_cols=8),
-        fake, fake, fake, None, 0, None, 0, None,
+        fake, fake, fake, None, 0, None, 0, None, 0, None,
     )
     assert status == nat.GS_ERR_OVERFLOW
     # Zero Gaussians: nothing to do.

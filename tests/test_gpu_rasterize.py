@@ -241,7 +241,8 @@ def test_composite_backward_segmented_walks(device, entries):
     ids32 = gids.to(torch.int32).contiguous()
     nat.check(nat.library().gs_composite(
         nat.ptr(records), records.shape[0], nat.ptr(ids32), ids32.numel(), nat.ptr(granges), None,
-        plain, nat.ptr(img2), nat.ptr(ft2), nat.ptr(nc2), None, 0, None, 0, nat.stream(device)),
+        plain, nat.ptr(img2), nat.ptr(ft2), nat.ptr(nc2), None, 0, None, 0, None, 0,
+        nat.stream(device)),
         "composite")
     torch.cuda.synchronize()
     assert torch.equal(final_t, ft2) and torch.equal(ncon, nc2)

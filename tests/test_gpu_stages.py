@@ -440,6 +440,71 @@ def test_composite_empty_tiles(device):
     assert torch.all(final_t == 1) and torch.count_nonzero(ncon) == 0
 
 
+@pytest.mark.parametrize("scene_kind, tile", [("edge96x64", 8), ("config2", 16), ("edge1040", 16),
+                                              ("edge160x96", 32)])
+def test_forward_writes_backward_plan_keys(device, scene_kind, tile):
+    """The keys the forward's whole-tile walks write (gs_composite's
+    tile_keys) equal the key kernel's, from the same n_contributors and
+    ranges, and the backward plan made from them (keys_ready) equals the one
+    made without.  When every tile ran as quarters (fewer than 4096 tiles
+    with work, tiles of 16 and 32) the forward writes none and the plan
+    recomputes them."""
+    if scene_kind == "config2":
+        scene = scenes.config2(n=40_000)
+    else:
+        size = {"edge96x64": (96, 64), "edge1040": (1040, 1040), "edge160x96": (160, 96)}[scene_kind]
+        scene = scenes.edge_case_scene(n=3000, sh_degree=1, image_size=size)
+    cam = scene.cameras[0]
+    fx, fy = cam.focal_length
+    cx, cy = cam.principal_point
+    w, h = cam.image_size
+    params = [t.to(device) for t in scene.params()]
+    pmean, pinv, pcol, pop, _, _ = project_and_count(
+        *params, cam.rotation_matrix, cam.translation, fx, fy, cx, cy, w, h, tile, scene.near,
+        scene.far, "gaussian", CONFIDENCE)
+    tw, th = nat.tiles(w, h, tile)
+    lib = nat.library()
+    keys_fwd = nat.workspace(lib.gs_tile_order_workspace_bytes(tw * th), device)
+    keys_fwd.fill_(0x5A)
+    out = forward_lists(params, cam, scene, tile, device)
+    sid, ranges = out
+    active = nat.active_tiles(ranges)
+    whole_tiles = tile not in (16, 32) or active >= 4096
+    print(f"[plan keys] {scene_kind} tile {tile}: {active} active tiles, forward keys "
+          f"{whole_tiles}", flush=True)
+    if scene_kind == "config2":
+        assert whole_tiles  # the case the forward's keys serve
+    _, _, ncon = composite(pmean, pinv, pcol, pop, sid, ranges, w, h, tile, THRESHOLD, "gaussian",
+                           CONFIDENCE, tile_keys=keys_fwd)
+    view = nat.make_view(1.0, 1.0, 0.0, 0.0, w, h, tile, opacity_threshold=THRESHOLD,
+                         active_tiles=nat.active_tiles(ranges))
+    count = lib.gs_tile_order_items(view, 1)
+    items = [torch.full((count,), -9, dtype=torch.int32, device=device) for _ in range(2)]
+    keys_kernel = nat.workspace(lib.gs_tile_order_workspace_bytes(tw * th), device)
+    s = nat.stream(device)
+    nat.check(lib.gs_tile_order(nat.ptr(ranges), nat.ptr(ncon), view, nat.ptr(items[0]),
+                                nat.ptr(keys_kernel), keys_kernel.numel(), 0, s), "tile_order")
+    nat.check(lib.gs_tile_order(nat.ptr(ranges), nat.ptr(ncon), view, nat.ptr(items[1]),
+                                nat.ptr(keys_fwd), keys_fwd.numel(), 1, s), "tile_order")
+    torch.cuda.synchronize(device)
+    assert torch.equal(items[0], items[1])
+    nbytes = 2 * tw * th * 4  # both words of every tile
+    assert torch.equal(keys_fwd[:nbytes], keys_kernel[:nbytes])
+
+
+def forward_lists(params, cam, scene, tile, device):
+    """Sorted ids and ranges of the op's binning for one camera."""
+    from gaussian_splats_hip.kernels.rasterize.interface import forward_pipeline
+
+    fx, fy = cam.focal_length
+    cx, cy = cam.principal_point
+    w, h = cam.image_size
+    out = forward_pipeline(*params, cam.rotation_matrix, cam.translation, fx, fy, cx, cy, w, h,
+                           tile, THRESHOLD, scene.near, scene.far, "gaussian", CONFIDENCE,
+                           record_hits=False)
+    return out[7], out[8]
+
+
 @pytest.mark.parametrize(
     "shape", [(120, 68, 16, 0), (120, 68, 16, 3000), (7, 5, 8, 0), (1, 1, 16, 0), (33, 2, 4, 0),
               (100, 100, 16, 0), (60, 40, 32, 0)])
@@ -528,7 +593,7 @@ def test_compositing_results_do_not_depend_on_tile_order(device, tile_size, imag
         nat.check(nat.library().gs_composite(
             nat.ptr(records), records.shape[0], nat.ptr(sid_d), sid_d.numel(), nat.ptr(ranges_d),
             nat.ptr(order), v, nat.ptr(img2), nat.ptr(ft2), nat.ptr(nc2), None, 0,
-            None, 0, nat.stream(device)), "composite")
+            None, 0, None, 0, nat.stream(device)), "composite")
         torch.cuda.synchronize()
         # The wrapper's walk records checkpoints, which sums each pixel's
         # colour in segments (rounding of the order of the sums).
@@ -576,7 +641,7 @@ def test_compositing_results_do_not_depend_on_tile_order(device, tile_size, imag
     nat.check(lib.gs_composite(
         nat.ptr(records), records.shape[0], nat.ptr(sid_d), sid_d.numel(), nat.ptr(ranges_d), None,
         few, nat.ptr(img3), nat.ptr(ft3), nat.ptr(nc3), None, 0, nat.ptr(hits), words * 8,
-        nat.stream(device)), "composite")
+        None, 0, nat.stream(device)), "composite")
     grad3 = torch.zeros_like(grad)
     nat.check(lib.gs_composite_bwd(
         *(nat.ptr(t) for t in args), args[0].shape[0], nat.ptr(sid_d), nat.ptr(ranges_d), nat.ptr(g),

@@ -135,7 +135,7 @@ def test_backward_with_a_full_checkpoint_pool(device, records):
     nat.check(nat.library().gs_composite(
         nat.ptr(records_buf), records_buf.shape[0], nat.ptr(ids32), ids32.numel(),
         nat.ptr(granges), None, view, nat.ptr(image), nat.ptr(final_t), nat.ptr(ncon),
-        nat.ptr(ckpt), nbytes, None, 0, nat.stream(device)), "composite")
+        nat.ptr(ckpt), nbytes, None, 0, None, 0, nat.stream(device)), "composite")
     order = tile_order(granges, ncon, w, h, ts)
     plan = order.cpu().numpy()
     assert ((plan >= 0) & ((plan & 0x40) != 0)).any()  # the plan has segment items

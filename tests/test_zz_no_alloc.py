@@ -38,7 +38,7 @@ def _both_orders(device, view, num_tiles, ranges=None, ncon=None):
     count = lib.gs_tile_order_items(view, int(ncon is not None))
     expected = torch.full((count,), -7, dtype=torch.int32, device=device)
     nat.check(lib.gs_tile_order(nat.ptr(ranges), nat.ptr(ncon), view, nat.ptr(expected),
-                                nat.ptr(ws), ws.numel(), s), "tile_order")
+                                nat.ptr(ws), ws.numel(), 0, s), "tile_order")
     got = torch.full((count,), -7, dtype=torch.int32, device=device)
     nat.check(lib.gs_tile_order_noalloc(nat.ptr(ranges), nat.ptr(ncon), view, nat.ptr(got), s),
               "tile_order_noalloc")

@@ -29,10 +29,6 @@ import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 VALU_CLOCK_HZ = 2.4e9  # MI355X peak engine clock
-# Spin before the projection's start event (about 100 us at the engine clock),
-# so its per-launch time excludes the host's launch latency after the idle
-# gap at the start of a step.
-PROJECT_HOLD_CYCLES = 250_000
 # The spin between the stages of the staged steps (stage_marker), about 250 us:
 # longer than the host's wait for the binning totals and the launches after
 # it, so no stage's time includes a host gap.
@@ -916,8 +912,10 @@ def main():
     print("[bench] warmup done", file=sys.stderr, flush=True)
 
     torch.cuda.synchronize()
-    # The dominant kernel, timed per launch with events on its stream: the
-    # compositing backward, or the forward compositing for a forward step.
+    # The dominant kernel, timed per launch with HIP events that its launch
+    # carries (the kernel's own start and end timestamps, no marker packets
+    # on the stream): the compositing backward, or the forward compositing
+    # for a forward step.
     dominant = "composite_bwd" if backward else "composite"
     with _native.LaunchTimer(dominant, capacity=args.steps + 1) as timer:
         t0 = time.perf_counter()
@@ -930,10 +928,9 @@ def main():
     ms_per_step = 1e3 * elapsed / args.steps
     mpix = (w * h) / 1e6
     print(f"[bench] timed {args.steps} steps: {ms_per_step:.3f} ms/step", file=sys.stderr, flush=True)
-    # The other kernels' per-launch times, from as many further steps outside
-    # the timed region (their timing events would add to the step time).
-    with _native.LaunchTimer("project", capacity=args.steps + 1,
-                             hold_cycles=PROJECT_HOLD_CYCLES) as project_timer, \
+    # The other kernels' per-launch times, the same way, from as many further
+    # steps outside the timed region.
+    with _native.LaunchTimer("project", capacity=args.steps + 1) as project_timer, \
             _native.LaunchTimer("project_bwd", capacity=args.steps + 1) as project_bwd_timer:
         for _ in range(args.steps):
             for p in splats.parameters():
@@ -960,8 +957,8 @@ def main():
                               w * h, fwd_pairs, bwd_pairs)
     stages = stage_entries(stages_ms, bytes_model)
 
-    # Dominant kernel, timed per launch with HIP events on its stream during
-    # the timed steps.
+    # Dominant kernel, timed per launch with the HIP events its launches
+    # carried during the timed steps.
     dominant_ms = timer.mean_ms()
     achieved = bytes_model[dominant] / (dominant_ms * 1e-3) / 1e9
     traffic = None

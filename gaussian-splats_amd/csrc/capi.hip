@@ -24,6 +24,18 @@ void set_error(const char* fmt, ...) {
 
 void clear_error() { g_error[0] = 0; }
 
+namespace {
+thread_local LaunchEvents g_launch_events;
+thread_local bool g_launch_events_taken = false;
+}  // namespace
+
+LaunchEvents take_launch_events() {
+  const LaunchEvents e = g_launch_events;
+  if (e.start || e.stop) g_launch_events_taken = true;
+  g_launch_events = LaunchEvents{};
+  return e;
+}
+
 int check_launch(const char* what) {
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
@@ -176,6 +188,20 @@ GS_API int gs_device_errors(uint32_t* flags, int32_t clear, void* stream) {
 }
 
 GS_API int gs_abi_version(void) { return GS_ABI_VERSION; }
+
+GS_API int gs_arm_launch_events(void* start, void* stop) {
+  gs::clear_error();
+  gs::g_launch_events = gs::LaunchEvents{static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)};
+  gs::g_launch_events_taken = false;
+  return GS_OK;
+}
+
+GS_API int gs_disarm_launch_events(void) {
+  const int taken = gs::g_launch_events_taken ? 1 : 0;
+  gs::g_launch_events = gs::LaunchEvents{};
+  gs::g_launch_events_taken = false;
+  return taken;
+}
 
 GS_API const char* gs_last_error(void) { return gs::g_error; }
 

@@ -383,9 +383,9 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_bwd_kernel(Com
 template <int TILE, bool QUARTERS, bool MASKS>
 void launch_masks(const CompositeBwdArgs& a, unsigned blocks, hipStream_t s) {
   if (a.grad_abs)
-    composite_bwd_kernel<TILE, true, QUARTERS, MASKS><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
+    launch_timed(composite_bwd_kernel<TILE, true, QUARTERS, MASKS>, blocks, kCompositeWaves * 64, 0, s, a);
   else
-    composite_bwd_kernel<TILE, false, QUARTERS, MASKS><<<blocks, kCompositeWaves * 64, 0, s>>>(a);
+    launch_timed(composite_bwd_kernel<TILE, false, QUARTERS, MASKS>, blocks, kCompositeWaves * 64, 0, s, a);
 }
 
 template <int TILE, bool QUARTERS>

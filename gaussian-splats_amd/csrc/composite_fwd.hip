@@ -357,14 +357,14 @@ void launch_items(const CompositeArgs& a, bool ellipsoid, hipStream_t s) {
       a.items ? a.num_items / kCompositeWaves
               : (a.split_all ? a.num_tiles : ceil_div(a.num_tiles, kCompositeWaves)));
   if (ellipsoid)
-    composite_fwd_kernel<TILE, true, QUARTERS, CKPT, false>
-        <<<blocks, kCompositeWaves * 64, 0, s>>>(a);
+    launch_timed(composite_fwd_kernel<TILE, true, QUARTERS, CKPT, false>, blocks, kCompositeWaves * 64, 0,
+                 s, a);
   else if (a.hit_masks)
-    composite_fwd_kernel<TILE, false, QUARTERS, CKPT, true>
-        <<<blocks, kCompositeWaves * 64, 0, s>>>(a);
+    launch_timed(composite_fwd_kernel<TILE, false, QUARTERS, CKPT, true>, blocks, kCompositeWaves * 64, 0,
+                 s, a);
   else
-    composite_fwd_kernel<TILE, false, QUARTERS, CKPT, false>
-        <<<blocks, kCompositeWaves * 64, 0, s>>>(a);
+    launch_timed(composite_fwd_kernel<TILE, false, QUARTERS, CKPT, false>, blocks, kCompositeWaves * 64, 0,
+                 s, a);
 }
 
 // Checkpoint recording is a kernel of its own: the code for it costs the

@@ -62,7 +62,7 @@ __global__ __launch_bounds__(kLossBlock) void l1_fwd_kernel(const float* __restr
     const float4* tg4 = reinterpret_cast<const float4*>(target);
     char4* c4 = reinterpret_cast<char4*>(code);
     for (int64_t i = t0; i < n4; i += stride) {
-      const float4 x = im4[i], t = tg4[i];
+      const float4 x = load_nt(im4 + i), t = load_nt(tg4 + i);  // read once
       int c0, c1, c2, c3;
       acc += loss_term(x.x, t.x, clamp, c0);
       acc += loss_term(x.y, t.y, clamp, c1);

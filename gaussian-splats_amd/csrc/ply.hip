@@ -192,7 +192,7 @@ GS_API int gs_ply_unpack(const void* records, int64_t n, int32_t record_bytes,
   const int64_t blocks = ceil_div(n, a.group);
   GS_REQUIRE(blocks <= INT32_MAX, GS_ERR_OVERFLOW, "too many Gaussians");
   const size_t lds = align_up(size_t(a.group) * record_bytes + 32, 16);
-  ply_unpack_kernel<<<int(blocks), kPlyBlock, lds, as_stream(stream)>>>(a);
+  launch_timed(ply_unpack_kernel, int(blocks), kPlyBlock, uint32_t(lds), as_stream(stream), a);
   return check_launch("ply_unpack");
 }
 
@@ -221,7 +221,7 @@ GS_API int gs_ply_pack(const float* mean, const float* normals, const float* rot
   const int64_t blocks = ceil_div(n, a.group);
   GS_REQUIRE(blocks <= INT32_MAX, GS_ERR_OVERFLOW, "too many Gaussians");
   const size_t lds = size_t(a.group) * a.record_floats * sizeof(float);
-  ply_pack_kernel<<<int(blocks), kPlyBlock, lds, as_stream(stream)>>>(a);
+  launch_timed(ply_pack_kernel, int(blocks), kPlyBlock, uint32_t(lds), as_stream(stream), a);
   return check_launch("ply_pack");
 }
 

@@ -264,16 +264,18 @@ __global__ __launch_bounds__(kBlock) void project_bwd_kernel(ProjectBwdArgs a) {
   // coefficients, so all of these loads are in flight together (threads past
   // the end read the last Gaussian and write nothing).
   const int64_t gl = have ? gi : a.n - 1;
-  const float mx = a.mean[gl * 3 + 0], myy = a.mean[gl * 3 + 1], mz = a.mean[gl * 3 + 2];
-  const float lop = a.opacity[gl];
-  const float4 qr = reinterpret_cast<const float4*>(a.rotation)[gl];
-  const float ls0 = a.scale[gl * 3 + 0], ls1 = a.scale[gl * 3 + 1], ls2 = a.scale[gl * 3 + 2];
-  const int32_t count0 = a.counts[gl];
+  const float mx = load_nt(a.mean + gl * 3 + 0), myy = load_nt(a.mean + gl * 3 + 1),
+              mz = load_nt(a.mean + gl * 3 + 2);
+  const float lop = load_nt(a.opacity + gl);
+  const float4 qr = load_nt(reinterpret_cast<const float4*>(a.rotation) + gl);
+  const float ls0 = load_nt(a.scale + gl * 3 + 0), ls1 = load_nt(a.scale + gl * 3 + 1),
+              ls2 = load_nt(a.scale + gl * 3 + 2);
+  const int32_t count0 = load_nt(a.counts + gl);
   // One view: its gradient inputs too.
   float gin0[9];
   if (!MULTI) {
 #pragma unroll
-    for (int i = 0; i < 9; ++i) gin0[i] = a.grad_in[gl * 9 + i];
+    for (int i = 0; i < 9; ++i) gin0[i] = load_nt(a.grad_in + gl * 9 + i);
   }
   sh::stage_block<F, kBlock>(a.color + base * F, nvalid, coeff);
   __syncthreads();
@@ -433,17 +435,17 @@ int project_bwd_views(const float* mean, const float* rotation, const float* sca
     a.accumulate = first > 0;
     if (views == 1) {
       switch (num_sh) {
-        case 1: project_bwd_kernel<1, false><<<grid, kBlock, 0, s>>>(a); break;
-        case 4: project_bwd_kernel<4, false><<<grid, kBlock, 0, s>>>(a); break;
-        case 9: project_bwd_kernel<9, false><<<grid, kBlock, 0, s>>>(a); break;
-        default: project_bwd_kernel<16, false><<<grid, kBlock, 0, s>>>(a); break;
+        case 1: launch_timed(project_bwd_kernel<1, false>, grid, kBlock, 0, s, a); break;
+        case 4: launch_timed(project_bwd_kernel<4, false>, grid, kBlock, 0, s, a); break;
+        case 9: launch_timed(project_bwd_kernel<9, false>, grid, kBlock, 0, s, a); break;
+        default: launch_timed(project_bwd_kernel<16, false>, grid, kBlock, 0, s, a); break;
       }
     } else {
       switch (num_sh) {
-        case 1: project_bwd_kernel<1, true><<<grid, kBlock, 0, s>>>(a); break;
-        case 4: project_bwd_kernel<4, true><<<grid, kBlock, 0, s>>>(a); break;
-        case 9: project_bwd_kernel<9, true><<<grid, kBlock, 0, s>>>(a); break;
-        default: project_bwd_kernel<16, true><<<grid, kBlock, 0, s>>>(a); break;
+        case 1: launch_timed(project_bwd_kernel<1, true>, grid, kBlock, 0, s, a); break;
+        case 4: launch_timed(project_bwd_kernel<4, true>, grid, kBlock, 0, s, a); break;
+        case 9: launch_timed(project_bwd_kernel<9, true>, grid, kBlock, 0, s, a); break;
+        default: launch_timed(project_bwd_kernel<16, true>, grid, kBlock, 0, s, a); break;
       }
     }
     GS_TRY(check_launch("project_bwd"));

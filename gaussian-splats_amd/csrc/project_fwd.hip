@@ -74,14 +74,14 @@ __global__ __launch_bounds__(kProjectBlock) void project_fwd_kernel(ProjectArgs 
   // their loads are in flight together with it (threads past the end read
   // the last Gaussian, branch-free, and return after the barrier).
   const int64_t gl = have ? gi : a.n - 1;
-  const float mx = a.mean[gl * 3 + 0];
-  const float my = a.mean[gl * 3 + 1];
-  const float mz = a.mean[gl * 3 + 2];
-  const float4 q = reinterpret_cast<const float4*>(a.rotation)[gl];
-  const float ls0 = a.scale[gl * 3 + 0];
-  const float ls1 = a.scale[gl * 3 + 1];
-  const float ls2 = a.scale[gl * 3 + 2];
-  const float lo = a.opacity[gl];
+  const float mx = load_nt(a.mean + gl * 3 + 0);
+  const float my = load_nt(a.mean + gl * 3 + 1);
+  const float mz = load_nt(a.mean + gl * 3 + 2);
+  const float4 q = load_nt(reinterpret_cast<const float4*>(a.rotation) + gl);
+  const float ls0 = load_nt(a.scale + gl * 3 + 0);
+  const float ls1 = load_nt(a.scale + gl * 3 + 1);
+  const float ls2 = load_nt(a.scale + gl * 3 + 2);
+  const float lo = load_nt(a.opacity + gl);
   sh::stage_block<F, kProjectBlock>(a.color + base * F, int(nvalid), coeff);
   __syncthreads();
   if (!have) return;
@@ -348,10 +348,10 @@ int project_views(const float* mean, const float* rotation, const float* scale,
     a.records = records ? static_cast<GsRecord*>(records) + off : nullptr;
     a.depth_keys = depth_keys ? depth_keys + off : nullptr;
     switch (num_sh) {
-      case 1: project_fwd_kernel<1><<<grid, kProjectBlock, 0, s>>>(a); break;
-      case 4: project_fwd_kernel<4><<<grid, kProjectBlock, 0, s>>>(a); break;
-      case 9: project_fwd_kernel<9><<<grid, kProjectBlock, 0, s>>>(a); break;
-      default: project_fwd_kernel<16><<<grid, kProjectBlock, 0, s>>>(a); break;
+      case 1: launch_timed(project_fwd_kernel<1>, grid, kProjectBlock, 0, s, a); break;
+      case 4: launch_timed(project_fwd_kernel<4>, grid, kProjectBlock, 0, s, a); break;
+      case 9: launch_timed(project_fwd_kernel<9>, grid, kProjectBlock, 0, s, a); break;
+      default: launch_timed(project_fwd_kernel<16>, grid, kProjectBlock, 0, s, a); break;
     }
     GS_TRY(check_launch("project_fwd"));
   }

@@ -11,6 +11,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include "common.h"
+
 namespace gs {
 namespace sh {
 
@@ -230,7 +232,7 @@ __device__ __forceinline__ void stage_block(const float* __restrict__ src, int n
     if (nvalid == BLOCK) {
       float4 v[C];
 #pragma unroll
-      for (int j = 0; j < C; ++j) v[j] = src4[threadIdx.x + j * BLOCK];
+      for (int j = 0; j < C; ++j) v[j] = load_nt(src4 + threadIdx.x + j * BLOCK);
 #pragma unroll
       for (int j = 0; j < C; ++j) {
         const int i = threadIdx.x + j * BLOCK;
@@ -242,7 +244,7 @@ __device__ __forceinline__ void stage_block(const float* __restrict__ src, int n
     const int chunks = nvalid * C;
     for (int i = threadIdx.x; i < chunks; i += BLOCK) {
       const int g = i / C;
-      reinterpret_cast<float4*>(lds + g * S)[(i - g * C) ^ chunk_swizzle<F>(g)] = src4[i];
+      reinterpret_cast<float4*>(lds + g * S)[(i - g * C) ^ chunk_swizzle<F>(g)] = load_nt(src4 + i);
     }
     return;
   }

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parents[2] / "_lib" / "libgs_raster.so"
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 GS_OK = 0
 GS_ERR_INVALID_ARGUMENT = 1
@@ -221,6 +221,8 @@ def buffer_bytes(t: torch.Tensor | None) -> int:
 _SIGNATURES = {
     "gs_abi_version": (c_int, []),
     "gs_last_error": (ctypes.c_char_p, []),
+    "gs_arm_launch_events": (c_int, [c_void_p, c_void_p]),
+    "gs_disarm_launch_events": (c_int, []),
     "gs_project_and_count": (
         c_int,
         [c_void_p] * 5 + [c_int64, c_int32, c_void_p, c_void_p, GsView] + [c_void_p] * 10,
@@ -439,28 +441,34 @@ def prepare(t: torch.Tensor, dtype: torch.dtype = torch.float32) -> torch.Tensor
 
 
 class LaunchTimer:
-    """Brackets every C-ABI launch of one entry point with timing events on
-    the stream it runs on, while active (``with LaunchTimer("composite_bwd")``).
-    Used by the benchmark to measure a kernel's per-launch duration in place."""
+    """Times every launch of one entry point's main kernel while active
+    (``with LaunchTimer("composite_bwd")``).  The launch carries the timing
+    events (gs_arm_launch_events), so each pair holds the kernel's own start
+    and end timestamps: no marker packet is queued on the stream, and the
+    host's launch latency is not counted.  Used by the benchmark to measure a
+    kernel's per-launch duration in place."""
 
-    def __init__(self, name: str, capacity: int = 256, hold_cycles: int = 0):
+    def __init__(self, name: str, capacity: int = 256):
         self.name = name
-        # A launch that follows an idle stretch of the queue (the first of a
-        # step) would time the host's launch latency too: with hold_cycles,
-        # a spin kernel of that many clock cycles runs before the start event,
-        # so the launch is queued by the time the event fires.
-        self.hold_cycles = int(hold_cycles)
         self.events: list[tuple[torch.cuda.Event, torch.cuda.Event]] = []
-        # Created up front, so a timed launch only records two events.
-        self._pool = [
-            (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-            for _ in range(capacity)
-        ]
+        self._pool = [self._pair() for _ in range(capacity)]
+        torch.cuda.synchronize()
+
+    @staticmethod
+    def _pair() -> tuple[torch.cuda.Event, torch.cuda.Event]:
+        # torch creates the HIP event at its first record; the launch then
+        # re-records it with the kernel's timestamps.
+        pair = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        for e in pair:
+            e.record()
+        return pair
 
     def next_pair(self) -> tuple[torch.cuda.Event, torch.cuda.Event]:
         if self._pool:
             return self._pool.pop()
-        return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        pair = self._pair()
+        pair[1].synchronize()
+        return pair
 
     def __enter__(self) -> "LaunchTimer":
         _TIMERS[self.name] = self
@@ -478,18 +486,21 @@ _TIMERS: dict[str, LaunchTimer] = {}
 
 
 def launch(name: str, call):
-    """Runs ``call()`` (one C-ABI entry point), timed when a LaunchTimer for
-    ``name`` is active."""
+    """Runs ``call()`` (one C-ABI entry point); while a LaunchTimer for
+    ``name`` is active its main kernel's launch carries a pair of timing
+    events, kept when a launch took them."""
     timer = _TIMERS.get(name)
     if timer is None:
         return call()
     start, end = timer.next_pair()
-    if timer.hold_cycles:
-        torch.cuda._sleep(timer.hold_cycles)
-    start.record()
-    status = call()
-    end.record()
-    timer.events.append((start, end))
+    lib = library()
+    check(lib.gs_arm_launch_events(start.cuda_event, end.cuda_event), "arm_launch_events")
+    try:
+        status = call()
+    finally:
+        taken = lib.gs_disarm_launch_events()
+    if taken:
+        timer.events.append((start, end))
     return status
 
 

@@ -42,7 +42,7 @@ extern "C" {
 
 #define GS_API __attribute__((visibility("default")))
 
-#define GS_ABI_VERSION 15
+#define GS_ABI_VERSION 16
 
 typedef enum gs_status {
   GS_OK = 0,
@@ -91,6 +91,22 @@ GS_API int gs_abi_version(void);
 
 /* Message describing the last failure on the calling thread ("" if none). */
 GS_API const char* gs_last_error(void);
+
+/* Kernel timing for benchmarks.  No counterpart in the reference (its
+ * benchmark times whole calls on the host); for callers that measure one
+ * kernel's duration per launch.  gs_arm_launch_events arms two hipEvent_t
+ * (created beforehand; either may be null) for the calling thread's next
+ * timed kernel: the main kernel of gs_project_and_count, gs_project_views,
+ * gs_project_bwd, gs_project_bwd_views, gs_composite, gs_composite_bwd,
+ * gs_ply_pack or gs_ply_unpack (the first one launched, for calls that
+ * launch several).
+ * That launch carries the events (hipExtLaunchKernel), so they take the
+ * kernel's own start and end timestamps; hipEventElapsedTime of the pair is
+ * its duration.  gs_disarm_launch_events disarms them and returns 1 if a
+ * launch took them since they were armed, 0 if none did (the call failed
+ * before its kernel, or had nothing to launch). */
+GS_API int gs_arm_launch_events(void* start_event, void* stop_event);
+GS_API int gs_disarm_launch_events(void);
 
 /* Device-side check failures.  The binning and sort kernels validate what
  * they cannot check on the host (sizes passed between calls against the

@@ -97,6 +97,32 @@ def test_project_ellipsoid_mode(device):
     rect_flip_tolerant_equal(gpu[4].cpu().numpy(), bounds, proj, 16, extent)
 
 
+def test_launch_events_time_one_kernel(device):
+    """A LaunchTimer's events ride on the projection kernel's launch: each
+    pair is taken by exactly one launch, spans a positive time, and the
+    outputs equal an untimed launch's; a call that launches no kernel (no
+    Gaussians) takes none."""
+    scene = scenes.edge_case_scene(n=2000, sh_degree=3)
+    plain, _, _, _ = _project_both(scene, device, 16)
+    with nat.LaunchTimer("project", capacity=4) as timer:
+        timed = [_project_both(scene, device, 16)[0] for _ in range(3)]
+        empty = [torch.empty((0,) + t.shape[1:], dtype=t.dtype, device=device)
+                 for t in scene.params()]
+        cam = scene.cameras[0]
+        project_and_count(*empty, cam.rotation_matrix.to(device), cam.translation.to(device),
+                          *cam.focal_length, *cam.principal_point, *cam.image_size, 16,
+                          scene.near, scene.far, "gaussian", CONFIDENCE)
+    assert len(timer.events) == 3
+    times = [s.elapsed_time(e) for s, e in timer.events]
+    print("[launch events] project ms", times, flush=True)
+    assert all(0.0 < t < 100.0 for t in times)
+    for out in timed:
+        for a, b in zip(out, plain):
+            assert torch.equal(a, b)
+    lib = nat.library()
+    assert lib.gs_disarm_launch_events() == 0
+
+
 def _decode_rects(rects):
     """[x0, x1, y0, y1] of packed tile rectangles (numpy), decoded from the
     packing the header documents: x0 | (x1 - x0 - 1) << 8 | y0 << 16 |

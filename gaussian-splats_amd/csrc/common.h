@@ -228,13 +228,26 @@ struct DispatchPlan {
   int region_blocks = 1;   // workgroups (of kCompositeWaves items) per region
   int items() const { return 8 * kCompositeWaves * region_blocks; }
 };
+// The plan deals the tiles to the 8 XCD regions in chunks of
+// region_chunk(num_tiles) consecutive tiles (a multiple of kCompositeWaves,
+// about eight chunks per region, at most 64 tiles), chunk c to region c % 8:
+// a dense band of the image is spread over every XCD, while the tiles of a
+// chunk (neighbours that share Gaussians) stay in one XCD's L2.
+__host__ __device__ inline int region_chunk(int num_tiles) {
+  const int k = (num_tiles + 63) / 64;
+  return k < kCompositeWaves ? kCompositeWaves : k > 64 ? 64 : (k + kCompositeWaves - 1) & ~(kCompositeWaves - 1);
+}
+// Tiles of the largest region (region 0).
+__host__ __device__ inline int region_max_tiles(int num_tiles) {
+  const int k = region_chunk(num_tiles);
+  const int chunks = (num_tiles + k - 1) / k;
+  return (chunks + 7) / 8 * k;
+}
 inline DispatchPlan dispatch_plan(int num_tiles, int tile_size, int active, bool backward) {
   DispatchPlan p;
   p.split_all = tile_size >= 16 && composite_split(num_tiles, active);
   p.segments = backward && !p.split_all;
-  // Tiles of the largest region (tile_order.hip's region split).
-  const int nb = (num_tiles + kCompositeWaves - 1) / kCompositeWaves;
-  const int t_max = (nb + 7) / 8 * kCompositeWaves;
+  const int t_max = region_max_tiles(num_tiles);
   const int cap = p.split_all ? 4 * t_max : p.segments ? (1 + kSegmentSpare) * t_max : t_max;
   p.region_blocks = cap > kCompositeWaves ? (cap + kCompositeWaves - 1) / kCompositeWaves : 1;
   return p;

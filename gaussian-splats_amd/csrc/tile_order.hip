@@ -2,8 +2,13 @@
 //
 // The compositing kernels run one wave per work item, four items per
 // workgroup, and map workgroups onto XCDs so that each XCD composites one
-// contiguous region of tiles (xcd_swizzle: neighbouring tiles share Gaussians,
-// which then stay in that XCD's L2).  Two things stretch a launch beyond its
+// region of the plan (xcd_swizzle).  A region is every eighth chunk of
+// consecutive tiles (region_chunk): neighbouring tiles share Gaussians, which
+// then stay in that XCD's L2, and a dense band of the image is spread over
+// all eight XCDs (config 4, 4M Gaussians at 1600 x 1600, concentrates its
+// work in the middle rows: with contiguous regions four XCDs idled while the
+// other four walked it, 0.67 / 0.64 ms forward / backward; dealt, 0.61 /
+// 0.47 ms).  Two things stretch a launch beyond its
 // average wave: workgroups dispatched last (when not every wave fits on the
 // GPU at once) that hold long tiles, and single tiles whose walk alone is
 // longer than the rest of the launch (long lists in dense regions).  The plan
@@ -93,13 +98,19 @@ __device__ __forceinline__ uint32_t block_exclusive(uint32_t v, uint32_t* scratc
   return before + incl - v;
 }
 
-// Region r of the order: the tiles of the workgroups xcd_swizzle gives XCD r.
-__device__ __forceinline__ void region(int r, int num_tiles, int& lo, int& hi) {
-  const int nb = (num_tiles + kCompositeWaves - 1) / kCompositeWaves;
-  const int q = nb >> 3, rem = nb & 7;
-  const int b0 = r * q + min(r, rem), b1 = (r + 1) * q + min(r + 1, rem);
-  lo = min(b0 * kCompositeWaves, num_tiles);
-  hi = min(b1 * kCompositeWaves, num_tiles);
+// Region r of the order (the slots xcd_swizzle gives XCD r): chunks r, r + 8,
+// r + 16, ... of region_chunk(num_tiles) tiles.  Its number of tiles, and its
+// tile e.
+__device__ __forceinline__ int region_size(int r, int num_tiles) {
+  const int k = region_chunk(num_tiles);
+  const int chunks = (num_tiles + k - 1) / k;
+  const int mine = chunks > r ? (chunks - r + 7) / 8 : 0;
+  if (mine == 0) return 0;
+  const int last = r + 8 * (mine - 1);
+  return (mine - 1) * k + min(k, num_tiles - last * k);
+}
+__device__ __forceinline__ int region_tile(int r, int e, int k) {
+  return ((e / k) * 8 + r) * k + e % k;
 }
 
 // One workgroup per region: a stable counting sort of the region's tiles by
@@ -122,14 +133,15 @@ __global__ __launch_bounds__(kOrderThreads) void tile_plan_kernel(
   __shared__ int32_t sorted_tile[kOrderMax];
   __shared__ uint8_t sorted_extra[kOrderMax];
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  int lo, hi;
-  region(blockIdx.x, num_tiles, lo, hi);
-  const int n = hi - lo;
+  const int r = blockIdx.x;
+  const int n = region_size(r, num_tiles);
+  const int rk = region_chunk(num_tiles);
   int32_t* out = items + int64_t(blockIdx.x) * region_slots;
   if (n > kOrderMax) {  // too large to sort here: index order, no segments
     const int per = split_all ? 4 : 1;
     for (int i = threadIdx.x; i < n * per; i += kOrderThreads)
-      out[i] = split_all ? ((lo + i / 4) << 7 | 0x20 | (i & 3)) : (lo + i) << 7;
+      out[i] = split_all ? (region_tile(r, i / 4, rk) << 7 | 0x20 | (i & 3))
+                         : region_tile(r, i, rk) << 7;
     for (int i = n * per + threadIdx.x; i < region_slots; i += kOrderThreads) out[i] = -1;
     return;
   }
@@ -143,7 +155,7 @@ __global__ __launch_bounds__(kOrderThreads) void tile_plan_kernel(
 #pragma unroll
   for (int i = 0; i < kPerLane; ++i) {
     const int e = s0 + i * 64 + lane;
-    k[i] = e < s1 ? key[lo + e] : 0u;
+    k[i] = e < s1 ? key[region_tile(r, e, rk)] : 0u;
     m = max(m, k[i]);
   }
 #pragma unroll
@@ -202,8 +214,9 @@ __global__ __launch_bounds__(kOrderThreads) void tile_plan_kernel(
     const int e = s0 + i * 64 + lane;
     if (e < s1) {
       const int p = int(start[dig[i]] + cnt[wid][dig[i]] + rank[i]);  // sorted position
-      sorted_tile[p] = lo + e;
-      sorted_extra[p] = uint8_t(split_all ? 3u : segments ? min(crossings[lo + e], 63u) : 0u);
+      const int t = region_tile(r, e, rk);
+      sorted_tile[p] = t;
+      sorted_extra[p] = uint8_t(split_all ? 3u : segments ? min(crossings[t], 63u) : 0u);
     }
   }
   __syncthreads();

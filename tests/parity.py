@@ -567,15 +567,20 @@ CHECKPOINT_MAX = 63        # per tile
 CHECKPOINT_MIN_LIST = 8192  # lists of at most this many entries record none
 
 
+def plan_chunk(num_tiles, waves=PLAN_WAVES):
+    """Tiles per chunk dealt to the regions: about num_tiles / 64, a multiple
+    of the workgroup's waves, between one workgroup's tiles and 64."""
+    k = -(-num_tiles // 64)
+    return waves if k < waves else 64 if k > 64 else -(-k // waves) * waves
+
+
 def plan_regions(num_tiles, waves=PLAN_WAVES):
-    """Tile ranges of the eight XCD regions (the compositing workgroup split)."""
-    nb = -(-num_tiles // waves)
-    q, r = nb >> 3, nb & 7
-    out = []
-    for x in range(8):
-        b0, b1 = x * q + min(x, r), (x + 1) * q + min(x + 1, r)
-        out.append((min(b0 * waves, num_tiles), min(b1 * waves, num_tiles)))
-    return out
+    """Tiles of the eight XCD regions, in region order: chunk c of
+    plan_chunk(num_tiles) consecutive tiles belongs to region c % 8."""
+    k = plan_chunk(num_tiles, waves)
+    tiles = np.arange(num_tiles)
+    chunk = tiles // k
+    return [tiles[chunk % 8 == r] for r in range(8)]
 
 
 def plan_slots(num_tiles, tile_size, active=0, backward=False):
@@ -583,8 +588,8 @@ def plan_slots(num_tiles, tile_size, active=0, backward=False):
     live = active if 0 < active < num_tiles else num_tiles
     split_all = tile_size >= 16 and live < PLAN_SPLIT_TILES
     segments = backward and not split_all
-    nb = -(-num_tiles // PLAN_WAVES)
-    t_max = -(-nb // 8) * PLAN_WAVES
+    k = plan_chunk(num_tiles)
+    t_max = -(-(-(-num_tiles // k)) // 8) * k  # tiles of the largest region (region 0)
     cap = 4 * t_max if split_all else (1 + PLAN_SEGMENT_SPARE) * t_max if segments else t_max
     blocks = -(-cap // PLAN_WAVES) if cap > PLAN_WAVES else 1
     return PLAN_WAVES * blocks, segments, split_all
@@ -613,7 +618,8 @@ def checkpoint_crossings(start, max_n, list_len):
 
 def expected_plan(keys, tile_size, active=0, backward=False, crossings=None):
     """The work items gs_tile_order writes for per-tile work keys (list
-    lengths, or largest contributor counts for a backward plan): per region, a
+    lengths, or largest contributor counts for a backward plan): per region
+    (plan_regions, tiles in ascending index), a
     stable sort by the key's eight most significant bits (relative to the
     region's largest key, keys capped at 2^16 - 1), largest first; each tile
     as its four quarters (tile << 7 | 0x20 | q) when every tile is split, as
@@ -627,22 +633,22 @@ def expected_plan(keys, tile_size, active=0, backward=False, crossings=None):
         crossings = np.zeros(num_tiles, dtype=np.int64)
     slots, segments, split_all = plan_slots(num_tiles, tile_size, active, backward)
     items = np.full(8 * slots, -1, dtype=np.int64)
-    for r, (lo, hi) in enumerate(plan_regions(num_tiles)):
-        n = hi - lo
+    for r, region in enumerate(plan_regions(num_tiles)):
+        n = region.size
         out = items[r * slots:(r + 1) * slots]
         if n == 0:
             continue
         if n > PLAN_SORT_MAX:
             if split_all:
-                t = lo + np.arange(4 * n) // 4
+                t = region[np.arange(4 * n) // 4]
                 out[:4 * n] = t << 7 | 0x20 | (np.arange(4 * n) & 3)
             else:
-                out[:n] = (lo + np.arange(n)) << 7
+                out[:n] = region << 7
             continue
-        k = keys[lo:hi]
+        k = keys[region]
         shift = max(0, int(k.max() | 1).bit_length() - 8)
         order = np.lexsort((np.arange(n), -(k >> shift)))
-        extra = np.array([3 if split_all else (min(int(crossings[lo + e]), CHECKPOINT_MAX)
+        extra = np.array([3 if split_all else (min(int(crossings[region[e]]), CHECKPOINT_MAX)
                                                 if segments else 0) for e in order],
                          dtype=np.int64)
         # Thread-blocked greedy of the library: blocks of 8 sorted tiles; a
@@ -658,7 +664,7 @@ def expected_plan(keys, tile_size, active=0, backward=False, crossings=None):
                 before += kept[i]
         pos = 0
         for p, e in enumerate(order):
-            t = lo + int(e)
+            t = int(region[e])
             x = int(kept[p])
             if x == 0:
                 out[pos] = t << 7

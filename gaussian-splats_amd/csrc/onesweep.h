@@ -145,18 +145,19 @@ __global__ __launch_bounds__(kBlock) inline void clear_kernel(uint64_t* big, int
 // the exponent byte, takes the ballots; the lower passes' digits are mantissa
 // bytes, spread over the bins, and each lane adds its own with one LDS
 // atomic, except the all-ones keys, counted once per wave.
+constexpr int kHistBlock = 1024;
+constexpr int kHistKeys = 4;
 template <typename K, bool SPREAD = false>
-__global__ __launch_bounds__(kBlock) void hist_kernel(const K* __restrict__ keys, int64_t n,
+__global__ __launch_bounds__(kHistBlock) void hist_kernel(const K* __restrict__ keys, int64_t n,
                                                       Plan plan, uint32_t* __restrict__ hist) {
   __shared__ uint32_t h[kMaxPasses * 256];
-  for (int i = threadIdx.x; i < plan.passes * 256; i += kBlock) h[i] = 0;
+  for (int i = threadIdx.x; i < plan.passes * 256; i += kHistBlock) h[i] = 0;
   __syncthreads();
   const int lane = __lane_id();
-  const int64_t stride = int64_t(gridDim.x) * kBlock;
+  const int64_t stride = int64_t(gridDim.x) * kHistBlock;
   // Each round requests a thread's next kHistKeys keys together, then counts
   // them (one dependent round trip per round, not per key).
-  constexpr int kHistKeys = 16;
-  for (int64_t i0 = int64_t(blockIdx.x) * kBlock + threadIdx.x; i0 - threadIdx.x < n;
+  for (int64_t i0 = int64_t(blockIdx.x) * kHistBlock + threadIdx.x; i0 - threadIdx.x < n;
        i0 += stride * kHistKeys) {
     K k[kHistKeys];
 #pragma unroll
@@ -207,7 +208,7 @@ __global__ __launch_bounds__(kBlock) void hist_kernel(const K* __restrict__ keys
     }
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < plan.passes * 256; i += kBlock)
+  for (int i = threadIdx.x; i < plan.passes * 256; i += kHistBlock)
     if (h[i]) atomicAdd(&hist[i], h[i]);
 }
 

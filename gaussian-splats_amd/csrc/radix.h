@@ -134,8 +134,10 @@ int radix_sort(K* keys, const uint32_t* vals, int64_t n, int end_bit, uint32_t* 
   *keys_final = keys;
   if (n == 0) return before_passes();
   const sweep::Plan plan = sweep::make_plan(end_bit);
-  const int hist_blocks = int(std::min<int64_t>(1024, ceil_div(n, kBlock * 16)));
-  sweep::hist_kernel<K, SPREAD><<<unsigned(hist_blocks), kBlock, 0, s>>>(keys, n, plan, ws.hist());
+  const int hist_blocks =
+      int(std::min<int64_t>(1024, ceil_div(n, sweep::kHistBlock * sweep::kHistKeys)));
+  sweep::hist_kernel<K, SPREAD>
+      <<<unsigned(hist_blocks), sweep::kHistBlock, 0, s>>>(keys, n, plan, ws.hist());
   GS_TRY(before_passes());
   K* kbuf[2] = {static_cast<K*>(ws.keys_alt), keys};
   const K* kin = keys;

@@ -882,27 +882,37 @@ __device__ __forceinline__ PassBWindow pass_b_window(const uint4* __restrict__ i
   return w;
 }
 
-// Pass-B workgroups are grouped in chunks of kChunk consecutive indices; the
-// part of tile row y inside chunk k has the sums slot k + y (unique: a later
-// row's workgroups all follow an earlier row's).
-constexpr int kChunk = 64;
+// Pass-B workgroups are grouped in chunks of 2^chunk_shift consecutive
+// indices; the part of tile row y inside chunk k has the sums slot k + y
+// (unique: a later row's workgroups all follow an earlier row's).  A chunk
+// is about 1/32 of a tile row's workgroups, 16 to 64: the scan walks a
+// chunk's workgroups in turn and, per row, the sums of the row's earlier
+// chunks (config 3, ~80 workgroups per row: scan 16.2 -> 8.7 us with chunks
+// of 16 instead of 64; config 4, ~1200: 64.8 -> 61.3 us with 32).
+__host__ __device__ inline int chunk_shift(int64_t blocks, int th) {
+  const int64_t per_row = (blocks + th - 1) / (th > 0 ? th : 1) / 32;
+  int sh = 4;
+  while (sh < 6 && (int64_t(1) << (sh + 1)) <= per_row) ++sh;
+  return sh;
+}
 __host__ __device__ inline int64_t chunk_slots(int64_t blocks, int th) {
-  return (blocks + kChunk - 1) / kChunk + th + 1;
+  const int sh = chunk_shift(blocks, th);
+  return ((blocks + (int64_t(1) << sh) - 1) >> sh) + th + 1;
 }
 
 // Counts: every row-list entry of workgroup b's window adds +1 at the first
 // column of its intersections inside [c0, c0 + count) and -1 after the last
 // one, in an LDS difference array; its prefix over the columns is the
 // workgroup's count per column, stored at counts[b * tw + column] and added
-// to its chunk's sums (sums[(b / kChunk + row) * tw + column], zeroed
+// to its chunk's sums (sums[((b >> cs) + row) * tw + column], zeroed
 // beforehand).  The window's entries are read contiguously (no item is
 // generated).
 template <int BITS>
 __global__ __launch_bounds__(kBlock) void column_count_kernel(
     const uint32_t* __restrict__ rl_xw, const uint32_t* __restrict__ W,
     const uint4* __restrict__ info, int tw, const int64_t* __restrict__ totals, int64_t total,
-    int64_t entries, int64_t blocks, uint32_t* __restrict__ counts, uint32_t* __restrict__ sums,
-    uint32_t* __restrict__ err) {
+    int64_t entries, int64_t blocks, int cs, uint32_t* __restrict__ counts,
+    uint32_t* __restrict__ sums, uint32_t* __restrict__ err) {
   constexpr int D = 1 << BITS;
   static_assert(D <= kBlock, "one column per thread");
   __shared__ int32_t diff[D + 1];
@@ -951,7 +961,7 @@ __global__ __launch_bounds__(kBlock) void column_count_kernel(
   const uint32_t cnt = block_exclusive_scan(v, scratch, all) + v;
   if (d < tw) {
     counts[b * tw + d] = cnt;
-    if (cnt) atomicAdd(&sums[(b / kChunk + win.row) * tw + d], cnt);
+    if (cnt) atomicAdd(&sums[((b >> cs) + win.row) * tw + d], cnt);
   }
 }
 
@@ -965,18 +975,18 @@ __global__ __launch_bounds__(kBlock) void column_scan_kernel(
     uint32_t* __restrict__ counts, const uint32_t* __restrict__ sums,
     const uint4* __restrict__ info, const uint32_t* __restrict__ row_blk,
     const int64_t* __restrict__ ranges, int tw, int th, const int64_t* __restrict__ totals,
-    int64_t total, int64_t entries, int64_t blocks) {
+    int64_t total, int64_t entries, int64_t blocks, int cs) {
   // Inconsistent sizes were flagged by the count pass; nothing is read then.
   if (totals[0] != total || totals[1] != entries || totals[2] != blocks) return;
   const int64_t k = blockIdx.x;
-  const int64_t lo = k * kChunk, hi = min(lo + kChunk, blocks);
+  const int64_t lo = k << cs, hi = min(lo + (int64_t(1) << cs), blocks);
   int64_t b = lo;
   while (b < hi) {
     const uint32_t y = min(uint32_t(__builtin_amdgcn_readfirstlane(int(info[b].z & 0xFFu))),
                            uint32_t(th - 1));
     // At least one workgroup per round, so the walk ends whatever the tables hold.
     const int64_t row_end = max(min(int64_t(row_blk[y + 1]), hi), b + 1);
-    const int64_t k0 = int64_t(row_blk[y]) / kChunk;  // the row's first chunk
+    const int64_t k0 = int64_t(row_blk[y]) >> cs;  // the row's first chunk
     for (int d = threadIdx.x; d < tw; d += kBlock) {
       uint32_t acc = uint32_t(ranges[2 * (int64_t(y) * tw + d)]);
       for (int64_t kk = k0; kk < k; kk += 8) {
@@ -1078,10 +1088,11 @@ void launch_pass_b(unsigned blocks, const uint32_t* rl_g, const uint32_t* rl_xw,
                    const int64_t* ranges, const int64_t* totals, int64_t total, int64_t entries,
                    int64_t blocks_b, int32_t* sorted_ids, uint32_t* counts, uint32_t* sums,
                    uint32_t* err, hipStream_t s) {
+  const int cs = chunk_shift(blocks_b, th);
   column_count_kernel<BITS><<<blocks, kBlock, 0, s>>>(rl_xw, W, info, tw, totals, total, entries,
-                                                      blocks_b, counts, sums, err);
-  column_scan_kernel<<<unsigned(ceil_div(blocks_b, kChunk)), kBlock, 0, s>>>(
-      counts, sums, info, row_blk, ranges, tw, th, totals, total, entries, blocks_b);
+                                                      blocks_b, cs, counts, sums, err);
+  column_scan_kernel<<<unsigned(ceil_div(blocks_b, int64_t(1) << cs)), kBlock, 0, s>>>(
+      counts, sums, info, row_blk, ranges, tw, th, totals, total, entries, blocks_b, cs);
   column_bucket_kernel<BITS><<<blocks, kBlock, 0, s>>>(rl_g, rl_xw, W, info, tw, counts, totals,
                                                        total, entries, blocks_b, sorted_ids, err);
 }

@@ -116,29 +116,29 @@ void dispatch_scatter(int bits, const K* kin, const uint32_t* vin, K* kout, uint
 // *keys_final points at the sorted keys (keys or the scratch copy).
 // SPREAD: the keys are depth keys (see hist_kernel).  gather_out (optional):
 // the last pass also writes gather_out[i] = gather_src[vals_final[i]].
-// before_passes() is called on the host after the histogram is enqueued and
-// before the first pass (it may enqueue work on another stream): the
-// caller's stream has the histogram to run while the host enqueues it.
+// hook() is called on the host once the histogram and the first pass are
+// enqueued, before the other passes (it may enqueue work on another stream):
+// the caller's stream has those two kernels to run while the host enqueues
+// it.
 struct NoHook {
   int operator()() const { return GS_OK; }
 };
-template <typename K, bool SPREAD = false, typename BeforePasses = NoHook>
+template <typename K, bool SPREAD = false, typename Hook = NoHook>
 int radix_sort(K* keys, const uint32_t* vals, int64_t n, int end_bit, uint32_t* vals_final,
                K** keys_final, const Scratch& ws, hipStream_t s,
                const uint32_t* gather_src = nullptr, uint32_t* gather_out = nullptr,
-               BeforePasses before_passes = BeforePasses{}) {
+               Hook hook = Hook{}) {
   GS_REQUIRE(n < (int64_t(1) << 32) - kTile, GS_ERR_OVERFLOW, "too many elements to sort (%lld)",
              (long long)n);
   GS_REQUIRE(end_bit <= int(8 * sizeof(K)), GS_ERR_INVALID_ARGUMENT,
              "end bit %d beyond the %d-bit key", end_bit, int(8 * sizeof(K)));
   *keys_final = keys;
-  if (n == 0) return before_passes();
+  if (n == 0) return hook();
   const sweep::Plan plan = sweep::make_plan(end_bit);
   const int hist_blocks =
       int(std::min<int64_t>(1024, ceil_div(n, sweep::kHistBlock * sweep::kHistKeys)));
   sweep::hist_kernel<K, SPREAD>
       <<<unsigned(hist_blocks), sweep::kHistBlock, 0, s>>>(keys, n, plan, ws.hist());
-  GS_TRY(before_passes());
   K* kbuf[2] = {static_cast<K*>(ws.keys_alt), keys};
   const K* kin = keys;
   const uint32_t* vin = vals;
@@ -154,6 +154,7 @@ int radix_sort(K* keys, const uint32_t* vals, int64_t n, int end_bit, uint32_t* 
     status += nblocks << plan.bits[pass];
     kin = kout;
     vin = vout;
+    if (pass == 0) GS_TRY(hook());
   }
   *keys_final = const_cast<K*>(kin);
   return check_launch("radix_sort");

@@ -1248,8 +1248,13 @@ GS_API int gs_bin_tiles_plan(uint32_t* depth_keys, const uint32_t* tile_rects, i
   GS_TRY(device_flags(s, &flags));
   // The tile tables need only the rectangles: they run on the side stream
   // while the depth sort and the row-list offset scan run on the caller's.
-  // The sort's clear and histogram are enqueued first, so the caller's
-  // stream has work while the host enqueues the side stream's.
+  // The sort's clear, histogram and first pass are enqueued first, so the
+  // caller's stream has work while the host enqueues the side stream's
+  // kernels; the copies of the totals (slow host calls) are enqueued last,
+  // once every kernel of both streams is.  (Under the kernel trace, whose
+  // launches are slower, copies enqueued before the other passes held them
+  // back 30-50 us on config 3; unprofiled steps measured the same either
+  // way.)
   SideFork fork;
   GS_TRY(fork_side_stream(s, fork));
   const int words = (tiles_h + 1) * (tiles_w + 1);
@@ -1295,9 +1300,13 @@ GS_API int gs_bin_tiles_plan(uint32_t* depth_keys, const uint32_t* tile_rects, i
                     256, 0, fork.side>>>(static_cast<uint32_t*>(clear_buf), words);
     }
     if (st == GS_OK) st = check_launch("bin_tiles_plan (tables)");
+    return st;
+  };
+  auto copy_totals = [&]() -> int {
+    int st = GS_OK;
     // The totals, then the sticky check-failure word beside them (its low
     // half; the caller keeps the high half zero).
-    if (host_totals && st == GS_OK &&
+    if (host_totals &&
         (hipMemcpyAsync(host_totals, totals, 4 * sizeof(int64_t), hipMemcpyDeviceToHost,
                         fork.side) != hipSuccess ||
          hipMemcpyAsync(host_totals + 4, flags, sizeof(uint32_t), hipMemcpyDeviceToHost,
@@ -1326,6 +1335,7 @@ GS_API int gs_bin_tiles_plan(uint32_t* depth_keys, const uint32_t* tile_rects, i
   } else {
     status = side_work();
   }
+  if (status == GS_OK) status = copy_totals();
   // Always join, also after an error; with host_totals the host waits for
   // the tables only, while the sort keeps running on the caller's stream
   // (the caller's stream then needs no wait of its own: everything enqueued

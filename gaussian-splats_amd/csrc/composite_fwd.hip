@@ -68,8 +68,9 @@ struct CompositeArgs {
 // dispatch key and checkpoint crossings are written once its walk ends.
 template <int TILE, bool ELLIPSOID, int PIX, bool HITS, bool PF = false>
 __device__ __forceinline__ void composite_tile(const CompositeArgs& a, float4 (*chunk)[3],
-                                               int* ck_slots, int lane, int tile, int band0,
-                                               bool checkpoints, bool write_key) {
+                                               float4 (*chunk2)[3], int* ck_slots, int lane,
+                                               int tile, int band0, bool checkpoints,
+                                               bool write_key) {
   constexpr int NPIX = TILE * TILE;
 
   // Mosaic tile -> view and the tile's pixel origin inside that view.
@@ -131,100 +132,73 @@ __device__ __forceinline__ void composite_tile(const CompositeArgs& a, float4 (*
   int ck_next =
       checkpoints && checkpoint_count(start, list_len, list_len) > 0 ? checkpoint_batch(start, 1)
                                                                      : -1;
-  // The ids of each batch are requested one batch ahead, once the current
-  // batch's records are in LDS, so they arrive while the current batch is
-  // walked and each batch waits on one dependent load (the record gather).
-  uint32_t id = start + lane < end ? uint32_t(a.ids[start + lane]) : 0u;
-  // PF: the records are requested one batch ahead as well (their ids two
-  // ahead), so a long walk does not wait on each batch's gather (config 4:
-  // 0.83 -> 0.67 ms; the checkpoint kernel's registers hold them at no cost
-  // in occupancy, the plain kernel's would lose a wave per SIMD).
-  GsRecord next;
-  if constexpr (PF) {
-    // Unconditional (a conditional load here costs the prefetch its gain):
-    // lanes past the list read record 0, and this kernel runs only with
-    // records (the host's condition for checkpoints).
-    next = load_record(a.records, min(id, a.max_id));
-    id = start + 64 + lane < end ? uint32_t(a.ids[start + 64 + lane]) : 0u;
-  }
-  for (int64_t base = start; running && base < end; base += 64) {
-    if (checkpoints && int(base - start) == ck_next) {
-      // Crossing ck_count + 1: record T and the colour since the previous
-      // record, then restart the colour sums.
-      uint32_t slot = 0xFFFFFFFFu;
-      if (lane == 0 && ck_written == ck_count) slot = atomicAdd(a.ckpt_counter, 1u);
-      slot = uint32_t(__builtin_amdgcn_readfirstlane(int(slot)));
-      const bool ok = ck_written == ck_count && int64_t(slot) < a.ckpt_capacity;
-      const int64_t pos = checkpoint_first(start) + int64_t(ck_count) * kCheckpointEntries;
-      if (lane == 0) a.ckpt_table[pos / kCheckpointEntries] = ok ? int32_t(slot) : -1;
-      if (ok) {
-        float4* rec = a.ckpt_records + int64_t(slot) * kRecord;
-#pragma unroll
-        for (int k = 0; k < PIX; ++k) {
-          rec[lane + 64 * k] = make_float4(T[k], cr[k], cg[k], cb[k]);
-          cr[k] = cg[k] = cb[k] = 0.0f;
-        }
-        if (lane == 0) ck_slots[ck_written] = int(slot);
-        ++ck_written;
-      }
-      ++ck_count;
-      ck_next = ck_count < kMaxCheckpoints ? checkpoint_batch(start, ck_count + 1) : -1;
-    }
-    // The overlap test's rectangle: the columns and rows of the pixels still
-    // active at the batch's first entry (a set that only shrinks within the
-    // batch; the walk is running, so it is not empty).
-    float rx0, rx1, ry0, ry1;
-    {
-      const int bpos = int(base - start);
-      uint32_t cols = 0;
-      int rlo = NPIX, rhi = -1;
+  // Crossing ck_count + 1 at list offset bpos (a batch start): record T and
+  // the colour since the previous record, then restart the colour sums.
+  auto checkpoint_at = [&](int bpos) {
+    if (!(checkpoints && bpos == ck_next)) return;
+    uint32_t slot = 0xFFFFFFFFu;
+    if (lane == 0 && ck_written == ck_count) slot = atomicAdd(a.ckpt_counter, 1u);
+    slot = uint32_t(__builtin_amdgcn_readfirstlane(int(slot)));
+    const bool ok = ck_written == ck_count && int64_t(slot) < a.ckpt_capacity;
+    const int64_t pos = checkpoint_first(start) + int64_t(ck_count) * kCheckpointEntries;
+    if (lane == 0) a.ckpt_table[pos / kCheckpointEntries] = ok ? int32_t(slot) : -1;
+    if (ok) {
+      float4* rec = a.ckpt_records + int64_t(slot) * kRecord;
 #pragma unroll
       for (int k = 0; k < PIX; ++k) {
-        const uint64_t m = __ballot(bpos < ncon[k]);
-        if (m) {
-          uint32_t c;
-          int r0, r1;
-          band_span<TILE>(m, c, r0, r1);
-          cols |= c;
-          rlo = min(rlo, (band0 + k) * kBandRows + r0);
-          rhi = max(rhi, (band0 + k) * kBandRows + r1);
-        }
+        rec[lane + 64 * k] = make_float4(T[k], cr[k], cg[k], cb[k]);
+        cr[k] = cg[k] = cb[k] = 0.0f;
       }
-      rx0 = float(ox + __builtin_ctz(cols));
-      rx1 = float(ox + 31 - __builtin_clz(cols));
-      ry0 = float(oy + rlo);
-      ry1 = float(oy + rhi);
+      if (lane == 0) ck_slots[ck_written] = int(slot);
+      ++ck_written;
     }
-    const int64_t e = base + lane;
-    LaneSplat mine;
-    bool keep = false;
-    if (e < end) {
-      const GsRecord rec = PF ? next : load_record(a.records, min(id, a.max_id));
-      keep = touches_rect(rec, rx0, rx1, ry0, ry1);
-      mine = lane_splat(rec);
+    ++ck_count;
+    ck_next = ck_count < kMaxCheckpoints ? checkpoint_batch(start, ck_count + 1) : -1;
+  };
+  // The overlap test's rectangle: the columns and rows of the pixels still
+  // active at list offset bpos (a set that only shrinks along the walk; the
+  // walk is running, so it is not empty).
+  auto active_rect = [&](int bpos, float& rx0, float& rx1, float& ry0, float& ry1) {
+    uint32_t cols = 0;
+    int rlo = NPIX, rhi = -1;
+#pragma unroll
+    for (int k = 0; k < PIX; ++k) {
+      const uint64_t m = __ballot(bpos < ncon[k]);
+      if (m) {
+        uint32_t c;
+        int r0, r1;
+        band_span<TILE>(m, c, r0, r1);
+        cols |= c;
+        rlo = min(rlo, (band0 + k) * kBandRows + r0);
+        rhi = max(rhi, (band0 + k) * kBandRows + r1);
+      }
     }
-    chunk[lane][0] = make_float4(mine.u, mine.v, mine.o, mine.pa);
-    chunk[lane][1] = make_float4(mine.pb, mine.pc, mine.r, mine.g);
-    chunk[lane][2] = make_float4(mine.b, mine.cut, 0.0f, 0.0f);
-    if constexpr (PF) {
-      next = load_record(a.records, min(id, a.max_id));
-      id = e + 128 < end ? uint32_t(a.ids[e + 128]) : 0u;
-    } else {
-      id = e + 64 < end ? uint32_t(a.ids[e + 64]) : 0u;
-    }
-    uint64_t mask = __ballot(keep);
+    rx0 = float(ox + __builtin_ctz(cols));
+    rx1 = float(ox + 31 - __builtin_clz(cols));
+    ry0 = float(oy + rlo);
+    ry1 = float(oy + rhi);
+  };
+  auto stage = [&](float4 (*rows)[3], const LaneSplat& mine) {
+    rows[lane][0] = make_float4(mine.u, mine.v, mine.o, mine.pa);
+    rows[lane][1] = make_float4(mine.pb, mine.pc, mine.r, mine.g);
+    rows[lane][2] = make_float4(mine.b, mine.cut, 0.0f, 0.0f);
+  };
+  // The batch's mask, the entries that can reach a pixel of the wave's bands
+  // still active, stored for each of the bands (vector stores).
+  auto store_hits = [&](uint64_t mask, int64_t base) {
     if constexpr (HITS) {
-      // The batch's mask, the entries that can reach a pixel of the wave's
-      // bands still active, stored for each of the bands (vector stores).
       const int64_t w0 = hit_mask_slot(start, tile, (base - start) >> 6) * kBands + band0;
       if (lane < PIX && w0 + lane < a.hit_capacity) a.hit_masks[w0 + lane] = mask;
     }
-    // No break inside: the loop ends through its condition, which keeps the
-    // walk's state out of extra mask-merging control flow.
+  };
+  // Blends the kept entries of the batch at `base` (staged in `rows`) in list
+  // order.  No break inside: the loop ends through its condition, which keeps
+  // the walk's state out of extra mask-merging control flow.
+  auto composite_batch = [&](uint64_t mask, float4 (*rows)[3], int64_t base) {
     while (mask) {
       const int j = __builtin_ctzll(mask);
       mask &= mask - 1;
-      const float4 f0 = chunk[j][0], f1 = chunk[j][1], f2 = chunk[j][2];
+      const float4 f0 = rows[j][0], f1 = rows[j][1], f2 = rows[j][2];
       Splat s;
       s.u = f0.x;
       s.v = f0.y;
@@ -262,6 +236,76 @@ __device__ __forceinline__ void composite_tile(const CompositeArgs& a, float4 (*
         running = false;
         mask = 0;
       }
+    }
+  };
+
+  uint32_t id = start + lane < end ? uint32_t(a.ids[start + lane]) : 0u;
+  if constexpr (PF) {
+    // Long lists (the checkpoint kernel), whose walks are latency bound: two
+    // batches per step.  Both are tested against the rectangle of the pixels
+    // active at the first one's start (for the second, a superset of its own
+    // rectangle: an entry kept only by it reaches alpha >= 1/255 at no active
+    // pixel and blends nothing), so the two tests' dependent chains overlap,
+    // and both batches' records are requested a step ahead (ids two ahead).
+    // Unconditional loads: lanes past the list read record 0, and this
+    // kernel runs only with records (the host's condition for checkpoints).
+    GsRecord next0 = load_record(a.records, min(id, a.max_id));
+    id = start + 64 + lane < end ? uint32_t(a.ids[start + 64 + lane]) : 0u;
+    GsRecord next1 = load_record(a.records, min(id, a.max_id));
+    uint32_t id0 = start + 128 + lane < end ? uint32_t(a.ids[start + 128 + lane]) : 0u;
+    uint32_t id1 = start + 192 + lane < end ? uint32_t(a.ids[start + 192 + lane]) : 0u;
+    for (int64_t base = start; running && base < end; base += 128) {
+      checkpoint_at(int(base - start));
+      float rx0, rx1, ry0, ry1;
+      active_rect(int(base - start), rx0, rx1, ry0, ry1);
+      const int64_t e = base + lane;
+      const bool second = base + 64 < end;  // wave-uniform
+      LaneSplat mine0, mine1;
+      bool keep0 = false, keep1 = false;
+      if (e < end) {
+        keep0 = touches_rect(next0, rx0, rx1, ry0, ry1);
+        mine0 = lane_splat(next0);
+      }
+      if (e + 64 < end) {
+        keep1 = touches_rect(next1, rx0, rx1, ry0, ry1);
+        mine1 = lane_splat(next1);
+      }
+      stage(chunk, mine0);
+      stage(chunk2, mine1);
+      next0 = load_record(a.records, min(id0, a.max_id));
+      next1 = load_record(a.records, min(id1, a.max_id));
+      id0 = e + 256 < end ? uint32_t(a.ids[e + 256]) : 0u;
+      id1 = e + 320 < end ? uint32_t(a.ids[e + 320]) : 0u;
+      const uint64_t mask0 = __ballot(keep0), mask1 = __ballot(keep1);
+      store_hits(mask0, base);
+      if (second) store_hits(mask1, base + 64);
+      composite_batch(mask0, chunk, base);
+      if (running && second) {
+        checkpoint_at(int(base + 64 - start));
+        composite_batch(mask1, chunk2, base + 64);
+      }
+    }
+  } else {
+    // The ids of each batch are requested one batch ahead, once the current
+    // batch's records are in LDS, so they arrive while the current batch is
+    // walked and each batch waits on one dependent load (the record gather).
+    for (int64_t base = start; running && base < end; base += 64) {
+      checkpoint_at(int(base - start));
+      float rx0, rx1, ry0, ry1;
+      active_rect(int(base - start), rx0, rx1, ry0, ry1);
+      const int64_t e = base + lane;
+      LaneSplat mine;
+      bool keep = false;
+      if (e < end) {
+        const GsRecord rec = load_record(a.records, min(id, a.max_id));
+        keep = touches_rect(rec, rx0, rx1, ry0, ry1);
+        mine = lane_splat(rec);
+      }
+      stage(chunk, mine);
+      id = e + 64 < end ? uint32_t(a.ids[e + 64]) : 0u;
+      const uint64_t mask = __ballot(keep);
+      store_hits(mask, base);
+      composite_batch(mask, chunk, base);
     }
   }
   // The records' colours become the colour composited after each record (a
@@ -326,6 +370,8 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_fwd_kernel(Com
   // (pb, pc, r, g), (b, cut, -, -): written once per lane, then read as LDS
   // broadcasts per entry instead of ten v_readlane.
   __shared__ float4 chunk[kCompositeWaves][64][3];
+  // The second batch of a two-batch step (checkpoint kernel only).
+  __shared__ float4 chunk2[kCompositeWaves][CKPT ? 64 : 1][3];
   __shared__ int ck_slots[kCompositeWaves][CKPT ? kMaxCheckpoints : 1];  // a wave's records
   const int slot = xcd_swizzle(blockIdx.x, gridDim.x) * kCompositeWaves + wid;
   int tile, kind, index;
@@ -338,16 +384,16 @@ __global__ __launch_bounds__(kCompositeWaves * 64) void composite_fwd_kernel(Com
     static_assert(PIX_TILE >= kCompositeWaves, "quarters of 64-pixel bands");
     constexpr int QPIX = PIX_TILE / kCompositeWaves;
     if (kind == kItemQuarter) {
-      composite_tile<TILE, ELLIPSOID, QPIX, HITS>(a, chunk[wid], ck_slots[wid], lane, tile,
-                                                  index * QPIX, false, false);
+      composite_tile<TILE, ELLIPSOID, QPIX, HITS>(a, chunk[wid], chunk2[wid], ck_slots[wid], lane,
+                                                  tile, index * QPIX, false, false);
     } else {
       for (int q = 0; q < kCompositeWaves; ++q)
-        composite_tile<TILE, ELLIPSOID, QPIX, HITS>(a, chunk[wid], ck_slots[wid], lane, tile,
-                                                    q * QPIX, false, false);
+        composite_tile<TILE, ELLIPSOID, QPIX, HITS>(a, chunk[wid], chunk2[wid], ck_slots[wid],
+                                                    lane, tile, q * QPIX, false, false);
     }
   } else {
-    composite_tile<TILE, ELLIPSOID, PIX_TILE, HITS, CKPT>(a, chunk[wid], ck_slots[wid], lane, tile,
-                                                          0, CKPT, true);
+    composite_tile<TILE, ELLIPSOID, PIX_TILE, HITS, CKPT>(a, chunk[wid], chunk2[wid],
+                                                          ck_slots[wid], lane, tile, 0, CKPT, true);
   }
 }
 

@@ -166,9 +166,16 @@ __global__ __launch_bounds__(kOrderThreads) void tile_plan_kernel(
   uint32_t dig[kPerLane], rank[kPerLane];
 #pragma unroll
   for (int i = 0; i < kPerLane; ++i) {
+    dig[i] = 255u - (k[i] >> shift);
+    rank[i] = 0;
+  }
+#pragma unroll
+  for (int i = 0; i < kPerLane; ++i) {
+    // Rounds past the wave's segment hold no tile (a region of n tiles fills
+    // ceil(n / 1024) of the eight): skipped, wave-uniformly.
+    if (s0 + i * 64 >= s1) break;
     const int e = s0 + i * 64 + lane;
     const bool valid = e < s1;
-    dig[i] = 255u - (k[i] >> shift);
     uint32_t plo = uint32_t(__ballot(valid)), phi = uint32_t(__ballot(valid) >> 32);
 #pragma unroll
     for (int bit = 0; bit < 8; ++bit) {

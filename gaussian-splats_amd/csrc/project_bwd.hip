@@ -351,14 +351,14 @@ __global__ __launch_bounds__(kBlock) void project_bwd_kernel(ProjectBwdArgs a) {
     for (int i = 0; i < F; ++i) gcoef[i] += prev[i];
   }
   if (have) {
-    a.g_mean[gi * 3 + 0] = gmx;
-    a.g_mean[gi * 3 + 1] = gmy;
-    a.g_mean[gi * 3 + 2] = gmz;
-    reinterpret_cast<float4*>(a.g_rot)[gi] = make_float4(gq[0], gq[1], gq[2], gq[3]);
-    a.g_scale[gi * 3 + 0] = gs3[0];
-    a.g_scale[gi * 3 + 1] = gs3[1];
-    a.g_scale[gi * 3 + 2] = gs3[2];
-    a.g_opacity[gi] = gop;
+    store_nt(gmx, a.g_mean + gi * 3 + 0);
+    store_nt(gmy, a.g_mean + gi * 3 + 1);
+    store_nt(gmz, a.g_mean + gi * 3 + 2);
+    store_nt(make_float4(gq[0], gq[1], gq[2], gq[3]), reinterpret_cast<float4*>(a.g_rot) + gi);
+    store_nt(gs3[0], a.g_scale + gi * 3 + 0);
+    store_nt(gs3[1], a.g_scale + gi * 3 + 1);
+    store_nt(gs3[2], a.g_scale + gi * 3 + 2);
+    store_nt(gop, a.g_opacity + gi);
     // Each thread overwrites only its own row, which only it has read.
     sh::row_store<F>(coeff, threadIdx.x, gcoef);
   }

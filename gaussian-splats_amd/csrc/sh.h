@@ -307,7 +307,8 @@ __device__ __forceinline__ void unstage_block(float* __restrict__ dst, int nvali
     const int chunks = nvalid * C;
     for (int i = threadIdx.x; i < chunks; i += BLOCK) {
       const int g = i / C;
-      dst4[i] = reinterpret_cast<const float4*>(lds + g * S)[(i - g * C) ^ chunk_swizzle<F>(g)];
+      store_nt(reinterpret_cast<const float4*>(lds + g * S)[(i - g * C) ^ chunk_swizzle<F>(g)],
+               dst4 + i);
     }
     return;
   }

@@ -23,6 +23,8 @@ constexpr int kBlock = 256;
 constexpr int kItems = 16;  // per thread: 4096 keys per tile keeps the look-back chain short
 constexpr int kTile = kBlock * kItems;  // elements per workgroup
 constexpr int kMaxPasses = 8;
+constexpr int kMaxDigitBits = 8;  // digits of up to 8 bits (256 buckets)
+constexpr int kHistStride = 1 << kMaxDigitBits;  // histogram words per pass
 constexpr uint64_t kFlagAggregate = 1ull << 62;
 constexpr uint64_t kFlagPrefix = 2ull << 62;
 constexpr uint64_t kValueMask = (1ull << 62) - 1;
@@ -32,13 +34,20 @@ struct Plan {
   int passes;
   int shift[kMaxPasses];
   int bits[kMaxPasses];
+  // With `remap`, the histogram and the first pass sort key' = min(key -
+  // base, cap) (keys below `base` wrap to large values and clamp to `cap`),
+  // and the first pass writes key' for the later ones.
+  bool remap;
+  uint64_t base;
+  uint64_t cap;
 };
 
-// Splits [0, end_bit) into ceil(end_bit / 8) passes of near-equal width.
-inline Plan make_plan(int end_bit) {
+// Splits [0, end_bit) into ceil(end_bit / max_bits) passes of near-equal
+// width (max_bits <= kMaxDigitBits).
+inline Plan make_plan(int end_bit, int max_bits = 8) {
   Plan p{};
   const int total = end_bit <= 0 ? 1 : end_bit;
-  p.passes = (total + 7) / 8;
+  p.passes = (total + max_bits - 1) / max_bits;
   int shift = 0;
   for (int i = 0; i < p.passes; ++i) {
     const int left = p.passes - i;
@@ -150,8 +159,8 @@ constexpr int kHistKeys = 4;
 template <typename K, bool SPREAD = false>
 __global__ __launch_bounds__(kHistBlock) void hist_kernel(const K* __restrict__ keys, int64_t n,
                                                       Plan plan, uint32_t* __restrict__ hist) {
-  __shared__ uint32_t h[kMaxPasses * 256];
-  for (int i = threadIdx.x; i < plan.passes * 256; i += kHistBlock) h[i] = 0;
+  __shared__ uint32_t h[kMaxPasses * kHistStride];
+  for (int i = threadIdx.x; i < plan.passes * kHistStride; i += kHistBlock) h[i] = 0;
   __syncthreads();
   const int lane = __lane_id();
   const int64_t stride = int64_t(gridDim.x) * kHistBlock;
@@ -164,6 +173,7 @@ __global__ __launch_bounds__(kHistBlock) void hist_kernel(const K* __restrict__ 
     for (int u = 0; u < kHistKeys; ++u) {
       const int64_t i = i0 + u * stride;
       k[u] = i < n ? keys[i] : K(0);
+      if (plan.remap) k[u] = min(K(k[u] - K(plan.base)), K(plan.cap));
     }
 #pragma unroll
     for (int u = 0; u < kHistKeys; ++u) {
@@ -178,14 +188,15 @@ __global__ __launch_bounds__(kHistBlock) void hist_kernel(const K* __restrict__ 
       constexpr int kKeyPasses = int(sizeof(K)) < kMaxPasses ? int(sizeof(K)) : kMaxPasses;
       int first_ballot_pass = 0;
       if constexpr (SPREAD) {
-        const bool ones = k[u] == ~K(0);
+        const bool ones = k[u] == (plan.remap ? K(plan.cap) : ~K(0));
         const uint32_t n_ones = uint32_t(__popcll(__ballot(ok && ones)));
 #pragma unroll
         for (int p = 0; p + 1 < kKeyPasses; ++p) {
           if (p + 1 >= plan.passes) break;
           const uint32_t d = uint32_t(k[u] >> plan.shift[p]) & ((1u << plan.bits[p]) - 1u);
-          if (ok && !ones) atomicAdd(&h[p * 256 + d], 1u);
-          if (lane == 0 && n_ones) atomicAdd(&h[p * 256 + (1u << plan.bits[p]) - 1u], n_ones);
+          if (ok && !ones) atomicAdd(&h[p * kHistStride + d], 1u);
+          if (lane == 0 && n_ones)
+            atomicAdd(&h[p * kHistStride + (1u << plan.bits[p]) - 1u], n_ones);
         }
         first_ballot_pass = plan.passes - 1;
       }
@@ -197,18 +208,18 @@ __global__ __launch_bounds__(kHistBlock) void hist_kernel(const K* __restrict__ 
         // Active lanes with the same digit (digits have at most eight bits).
         uint64_t peers = active;
 #pragma unroll
-        for (int bit = 0; bit < 8; ++bit) {
+        for (int bit = 0; bit < kMaxDigitBits; ++bit) {
           const bool set = (d >> bit) & 1u;
           const uint64_t ones = __ballot(set);
           peers &= set ? ones : ~ones;
         }
         if (ok && lane == __builtin_ctzll(peers))
-          atomicAdd(&h[p * 256 + d], uint32_t(__popcll(peers)));
+          atomicAdd(&h[p * kHistStride + d], uint32_t(__popcll(peers)));
       }
     }
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < plan.passes * 256; i += kHistBlock)
+  for (int i = threadIdx.x; i < plan.passes * kHistStride; i += kHistBlock)
     if (h[i]) atomicAdd(&hist[i], h[i]);
 }
 
@@ -271,13 +282,20 @@ __device__ __forceinline__ void rank_items(const uint32_t* digits, int n_valid_f
 // thread -> rank within each wave -> per-digit workgroup counts -> look-back for
 // the global offsets -> reorder the tile in LDS by digit -> coalesced stores.
 // vals_in == nullptr means vals[i] = i.
+// With `remap` (the first pass of a remapped plan), the keys are mapped to
+// min(key - base, cap) as they are loaded, and written so.
 template <typename K, int BITS>
 __global__ __launch_bounds__(kBlock) void scatter_kernel(
     const K* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, K* __restrict__ keys_out,
     uint32_t* __restrict__ vals_out, int64_t n, int shift, const uint32_t* __restrict__ hist,
     uint64_t* __restrict__ status, uint32_t* __restrict__ ticket, uint32_t* __restrict__ err,
-    const uint32_t* __restrict__ gather_src, uint32_t* __restrict__ gather_out) {
+    const uint32_t* __restrict__ gather_src, uint32_t* __restrict__ gather_out, bool remap,
+    uint64_t remap_base, uint64_t remap_cap) {
   constexpr int D = 1 << BITS;
+  static_assert(D <= kBlock || D % kBlock == 0, "digits per thread");
+  // Per-digit work: DPT consecutive digits per thread (d = DPT t + q), so one
+  // block scan orders them all.
+  constexpr int DPT = D > kBlock ? D / kBlock : 1;
   constexpr int kSeg = kTile / 4;  // contiguous elements per wave
   __shared__ uint32_t cnt[4][D];
   __shared__ uint32_t gofs[D];
@@ -322,6 +340,10 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
                      : 0u;
     }
   }
+  if (remap) {
+#pragma unroll
+    for (int i = 0; i < kItems; ++i) key[i] = min(K(key[i] - K(remap_base)), K(remap_cap));
+  }
 #pragma unroll
   for (int i = 0; i < kItems; ++i) dig[i] = uint32_t(key[i] >> shift) & (D - 1);
 
@@ -332,32 +354,52 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
     rank_items<BITS, false>(dig, seg_valid, cnt[wid], rank);
   __syncthreads();
 
-  uint32_t tot = 0, c0 = 0, c1 = 0, c2 = 0;
-  if (threadIdx.x < D) {
-    c0 = cnt[0][threadIdx.x];
-    c1 = cnt[1][threadIdx.x];
-    c2 = cnt[2][threadIdx.x];
-    tot = c0 + c1 + c2 + cnt[3][threadIdx.x];
+  uint32_t tot[DPT], c0[DPT], c1[DPT], c2[DPT], hv[DPT];
+  uint32_t tsum = 0, hsum = 0;
+#pragma unroll
+  for (int q = 0; q < DPT; ++q) {
+    const int d = DPT * int(threadIdx.x) + q;
+    tot[q] = c0[q] = c1[q] = c2[q] = hv[q] = 0;
+    if (d < D) {
+      c0[q] = cnt[0][d];
+      c1[q] = cnt[1][d];
+      c2[q] = cnt[2][d];
+      tot[q] = c0[q] + c1[q] + c2[q] + cnt[3][d];
+      hv[q] = hist[d];
+    }
+    tsum += tot[q];
+    hsum += hv[q];
   }
   uint32_t all;
-  const uint32_t local_start = block_exclusive_scan(tot, scratch, all);
-  const uint32_t hv = threadIdx.x < D ? hist[threadIdx.x] : 0u;
-  const uint32_t digit_base = block_exclusive_scan(hv, scratch, all);
-  if (threadIdx.x < D) {
-    // Wave w's items of digit d start at cnt[w][d] in the reordered tile.
-    cnt[0][threadIdx.x] = local_start;
-    cnt[1][threadIdx.x] = local_start + c0;
-    cnt[2][threadIdx.x] = local_start + c0 + c1;
-    cnt[3][threadIdx.x] = local_start + c0 + c1 + c2;
-    uint64_t* mine = status + int64_t(b) * D + threadIdx.x;
-    store_status(mine, (b == 0 ? kFlagPrefix : kFlagAggregate) | uint64_t(tot));
-    uint64_t excl = 0;
-    if (b > 0) {
-      excl = look_back(status, D, b, threadIdx.x, err);
-      store_status(mine, kFlagPrefix | (excl + tot));
+  uint32_t local_start = block_exclusive_scan(tsum, scratch, all);
+  uint32_t digit_base = block_exclusive_scan(hsum, scratch, all);
+  uint64_t excl[DPT];
+#pragma unroll
+  for (int q = 0; q < DPT; ++q) {
+    const int d = DPT * int(threadIdx.x) + q;
+    excl[q] = 0;
+    if (d < D)
+      store_status(status + int64_t(b) * D + d,
+                   (b == 0 ? kFlagPrefix : kFlagAggregate) | uint64_t(tot[q]));
+  }
+#pragma unroll
+  for (int q = 0; q < DPT; ++q) {
+    const int d = DPT * int(threadIdx.x) + q;
+    if (d < D) {
+      // Wave w's items of digit d start at cnt[w][d] in the reordered tile.
+      cnt[0][d] = local_start;
+      cnt[1][d] = local_start + c0[q];
+      cnt[2][d] = local_start + c0[q] + c1[q];
+      cnt[3][d] = local_start + c0[q] + c1[q] + c2[q];
+      if (b > 0) {
+        excl[q] = look_back(status, D, b, d, err);
+        store_status(status + int64_t(b) * D + d, kFlagPrefix | (excl[q] + tot[q]));
+      }
+      // Output position of reordered item j of digit d: gofs[d] + j (mod 2^32).
+      gofs[d] = digit_base + uint32_t(excl[q]) - local_start;
     }
-    // Output position of reordered item j of digit d: gofs[d] + j (mod 2^32).
-    gofs[threadIdx.x] = digit_base + uint32_t(excl) - local_start;
+    local_start += tot[q];
+    digit_base += hv[q];
   }
   __syncthreads();
 

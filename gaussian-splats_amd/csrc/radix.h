@@ -29,13 +29,13 @@ struct Scratch {
   uint64_t* scan_status = nullptr;
   uint64_t* zero_begin = nullptr;
   int64_t zero_words = 0;  // 64-bit words of status
-  uint32_t* small = nullptr;  // hist[kMaxPasses*256], tickets[kMaxPasses], scan ticket
+  uint32_t* small = nullptr;  // hist[kMaxPasses*kHistStride], tickets[kMaxPasses], scan ticket
   int small_words = 0;
   size_t bytes = 0;
   uint32_t* flags = nullptr;  // the device's sticky check-failure word
 
   uint32_t* hist() const { return small; }
-  uint32_t* tickets() const { return small + sweep::kMaxPasses * 256; }
+  uint32_t* tickets() const { return small + sweep::kMaxPasses * sweep::kHistStride; }
   uint32_t* scan_ticket() const { return tickets() + sweep::kMaxPasses; }
 };
 
@@ -46,9 +46,12 @@ inline int64_t sort_status_words(int64_t n, const sweep::Plan& p) {
   return words;
 }
 
-// Lays out scratch for a sort of n keys of key_bytes over end_bit bits
-// (end_bit < 0: no sort) and a scan of scan_n elements (0: no scan).
-inline Scratch carve(void* ws, int64_t n, int key_bytes, int end_bit, int64_t scan_n) {
+// Lays out scratch for a sort of n keys of key_bytes over at most end_bit
+// bits in digits of at most max_bits (end_bit < 0: no sort) and a scan of
+// scan_n elements (0: no scan).  The look-back statuses are sized for the
+// largest plan of any end bit up to end_bit.
+inline Scratch carve(void* ws, int64_t n, int key_bytes, int end_bit, int64_t scan_n,
+                     int max_bits = 8) {
   Scratch s;
   char* p = static_cast<char*>(ws);
   size_t off = 0;
@@ -60,7 +63,8 @@ inline Scratch carve(void* ws, int64_t n, int key_bytes, int end_bit, int64_t sc
       s.vbuf[i] = p ? reinterpret_cast<uint32_t*>(p + off) : nullptr;
       off += align_up(size_t(n) * 4);
     }
-    sort_words = sort_status_words(n, sweep::make_plan(end_bit));
+    for (int e = 1; e <= end_bit; ++e)
+      sort_words = std::max(sort_words, sort_status_words(n, sweep::make_plan(e, max_bits)));
   }
   const int64_t scan_words = scan_n > 0 ? ceil_div(scan_n, kTile) : 0;
   s.zero_begin = p ? reinterpret_cast<uint64_t*>(p + off) : nullptr;
@@ -68,7 +72,7 @@ inline Scratch carve(void* ws, int64_t n, int key_bytes, int end_bit, int64_t sc
   s.scan_status = p ? s.zero_begin + sort_words : nullptr;
   s.zero_words = sort_words + scan_words;
   off += align_up(size_t(s.zero_words) * 8);
-  s.small_words = sweep::kMaxPasses * 256 + sweep::kMaxPasses + 1;
+  s.small_words = sweep::kMaxPasses * sweep::kHistStride + sweep::kMaxPasses + 1;
   s.small = p ? reinterpret_cast<uint32_t*>(p + off) : nullptr;
   off += align_up(size_t(s.small_words) * 4);
   s.bytes = off;
@@ -84,20 +88,22 @@ inline void clear(const Scratch& s, hipStream_t stream) {
 template <typename K, int BITS>
 void launch_scatter(const K* kin, const uint32_t* vin, K* kout, uint32_t* vout, int64_t n,
                     int shift, const uint32_t* hist, uint64_t* status, uint32_t* ticket,
-                    uint32_t* err, const uint32_t* gsrc, uint32_t* gout, hipStream_t s) {
+                    uint32_t* err, const uint32_t* gsrc, uint32_t* gout, bool remap,
+                    uint64_t base, uint64_t cap, hipStream_t s) {
   const unsigned nblocks = unsigned(ceil_div(n, kTile));
   sweep::scatter_kernel<K, BITS><<<nblocks, sweep::kBlock, 0, s>>>(
-      kin, vin, kout, vout, n, shift, hist, status, ticket, err, gsrc, gout);
+      kin, vin, kout, vout, n, shift, hist, status, ticket, err, gsrc, gout, remap, base, cap);
 }
 
 template <typename K>
 void dispatch_scatter(int bits, const K* kin, const uint32_t* vin, K* kout, uint32_t* vout,
                       int64_t n, int shift, const uint32_t* hist, uint64_t* status,
                       uint32_t* ticket, uint32_t* err, const uint32_t* gsrc, uint32_t* gout,
-                      hipStream_t s) {
+                      bool remap, uint64_t base, uint64_t cap, hipStream_t s) {
   // One launch per digit width (the kernel's template argument).
-#define GS_SCATTER(B)                                                                            \
-  launch_scatter<K, B>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, gsrc, gout, s)
+#define GS_SCATTER(B)                                                                  \
+  launch_scatter<K, B>(kin, vin, kout, vout, n, shift, hist, status, ticket, err, gsrc, gout, \
+                       remap, base, cap, s)
   switch (bits) {
     case 1: GS_SCATTER(1); break;
     case 2: GS_SCATTER(2); break;
@@ -123,18 +129,34 @@ void dispatch_scatter(int bits, const K* kin, const uint32_t* vin, K* kout, uint
 struct NoHook {
   int operator()() const { return GS_OK; }
 };
+// KeyRemap: sort min(key - base, 2^end_bit - 1) (the scratch was carved for
+// `max_bits`); keys below base or at least base + 2^end_bit - 1 sort last,
+// in index order.  Off: the keys' bits [0, end_bit) in digits of at most 8
+// bits.
+struct KeyRemap {
+  bool on = false;
+  uint64_t base = 0;
+  int max_bits = 8;
+};
 template <typename K, bool SPREAD = false, typename Hook = NoHook>
 int radix_sort(K* keys, const uint32_t* vals, int64_t n, int end_bit, uint32_t* vals_final,
                K** keys_final, const Scratch& ws, hipStream_t s,
                const uint32_t* gather_src = nullptr, uint32_t* gather_out = nullptr,
-               Hook hook = Hook{}) {
+               Hook hook = Hook{}, KeyRemap remap = KeyRemap{}) {
   GS_REQUIRE(n < (int64_t(1) << 32) - kTile, GS_ERR_OVERFLOW, "too many elements to sort (%lld)",
              (long long)n);
   GS_REQUIRE(end_bit <= int(8 * sizeof(K)), GS_ERR_INVALID_ARGUMENT,
              "end bit %d beyond the %d-bit key", end_bit, int(8 * sizeof(K)));
   *keys_final = keys;
   if (n == 0) return hook();
-  const sweep::Plan plan = sweep::make_plan(end_bit);
+  GS_REQUIRE(remap.max_bits >= 1 && remap.max_bits <= sweep::kMaxDigitBits &&
+                 (!remap.on || end_bit < int(8 * sizeof(K))),
+             GS_ERR_INVALID_ARGUMENT, "bad key remap (%d-bit digits, end bit %d)", remap.max_bits,
+             end_bit);
+  sweep::Plan plan = sweep::make_plan(end_bit, remap.max_bits);
+  plan.remap = remap.on;
+  plan.base = remap.base;
+  plan.cap = remap.on ? (uint64_t(1) << end_bit) - 1 : ~uint64_t(0);
   const int hist_blocks =
       int(std::min<int64_t>(1024, ceil_div(n, sweep::kHistBlock * sweep::kHistKeys)));
   sweep::hist_kernel<K, SPREAD>
@@ -149,8 +171,9 @@ int radix_sort(K* keys, const uint32_t* vals, int64_t n, int end_bit, uint32_t* 
     uint32_t* vout = (pass == plan.passes - 1) ? vals_final : ws.vbuf[pass & 1];
     const bool last = pass == plan.passes - 1;
     dispatch_scatter<K>(plan.bits[pass], kin, vin, kout, vout, n, plan.shift[pass],
-                        ws.hist() + pass * 256, status, ws.tickets() + pass, ws.flags,
-                        last ? gather_src : nullptr, last ? gather_out : nullptr, s);
+                        ws.hist() + pass * sweep::kHistStride, status, ws.tickets() + pass,
+                        ws.flags, last ? gather_src : nullptr, last ? gather_out : nullptr,
+                        pass == 0 && plan.remap, plan.base, plan.cap, s);
     status += nblocks << plan.bits[pass];
     kin = kout;
     vin = vout;

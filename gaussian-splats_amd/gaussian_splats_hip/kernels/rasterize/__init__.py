@@ -6,6 +6,7 @@ from .interface import rasterize
 from .intersections import (
     bin_gaussians,
     bin_tiles,
+    depth_key_range,
     emit_intersections,
     emit_tiles,
     sort_intersections,
@@ -20,6 +21,7 @@ __all__ = [
     "bin_tiles",
     "composite",
     "composite_bwd",
+    "depth_key_range",
     "emit_intersections",
     "emit_tiles",
     "pack_records",

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parents[2] / "_lib" / "libgs_raster.so"
-ABI_VERSION = 16
+ABI_VERSION = 17
 
 GS_OK = 0
 GS_ERR_INVALID_ARGUMENT = 1
@@ -259,7 +259,7 @@ _SIGNATURES = {
     "gs_bin_tiles_plan_bytes": (c_size_t, [c_int64, c_int32, c_int32]),
     "gs_bin_tiles_plan": (
         c_int,
-        [c_void_p] * 2 + [c_int64, c_int32, c_int32] + [c_void_p] * 4
+        [c_void_p] * 2 + [c_int64, ctypes.c_uint32, c_int32, c_int32, c_int32] + [c_void_p] * 4
         + [c_size_t, c_void_p, c_size_t, c_void_p],
     ),
     "gs_pack_tile_rects": (

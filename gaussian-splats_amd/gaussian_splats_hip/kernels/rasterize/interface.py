@@ -16,7 +16,14 @@ import torch
 from ...timing import stage_timer
 from . import _native as nat
 from .composite import composite
-from .intersections import bin_gaussians, bin_tiles, bucketing_fits, emit_tiles, sort_tiles
+from .intersections import (
+    bin_gaussians,
+    bin_tiles,
+    bucketing_fits,
+    depth_key_range,
+    emit_tiles,
+    sort_tiles,
+)
 from .project import _check_tile, project_and_count
 
 if TYPE_CHECKING:  # the splat API imports this module, so only for annotations
@@ -80,7 +87,8 @@ def forward_pipeline(
                    if bucketing and record_hits and rendering_mode == "gaussian" else None)
     if bucketing:
         gaussian_ids, ranges = bin_tiles(depth_keys, None, None, tiles_w, tiles_h, timer=mark,
-                                         tile_rects=tile_rects, clear=accumulator)
+                                         tile_rects=tile_rects, clear=accumulator,
+                                         key_range=depth_key_range(near, far))
     else:
         order, offsets = bin_gaussians(depth_keys, counts)
         mark("bin")

@@ -16,6 +16,7 @@ from __future__ import annotations
 
 from ctypes import c_void_p
 
+import numpy as np
 import torch
 
 from . import _native as nat
@@ -154,6 +155,22 @@ def bucketing_fits(n: int, tiles_w: int, tiles_h: int) -> bool:
     return tiles_w <= MAX_BUCKET_TILES and tiles_h <= MAX_BUCKET_TILES and n < MAX_BUCKET_GAUSSIANS
 
 
+def depth_key_range(near: float, far: float) -> tuple[int, int]:
+    """(key_base, key_bits) of gs_bin_tiles_plan for depth keys of the
+    projection with these clipping planes: every counted Gaussian's depth d
+    satisfies near < d < far (float32), so its key (the bits of d) minus the
+    bits of near lies in [1, bits(far) - bits(near)), below 2^key_bits - 1,
+    the value culled keys map to.  (0, 32) (the keys' own 32 bits) unless
+    0 < near < far < inf."""
+    n32, f32 = np.float32(near), np.float32(far)
+    if not (0.0 < n32 < f32 < np.inf):
+        return 0, 32
+    base = int(n32.view(np.uint32))
+    span = int(f32.view(np.uint32)) - base
+    bits = span.bit_length()
+    return (base, bits) if bits < 32 else (0, 32)
+
+
 def bin_tiles(
     depth_keys: torch.Tensor,
     bounds: torch.Tensor | None,
@@ -164,6 +181,7 @@ def bin_tiles(
     *,
     tile_rects: torch.Tensor | None = None,
     clear: torch.Tensor | None = None,
+    key_range: tuple[int, int] = (0, 32),
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Sorted Gaussian ids and int64 ranges [T, 2] by row/column bucketing.
 
@@ -175,7 +193,8 @@ def bin_tiles(
     unused) or are packed here from ``bounds`` and ``counts``.  ``clear``
     (optional, a contiguous float32 or int32 tensor on the device) is zeroed
     beside the depth sort, on the side stream, before the call returns (the
-    op's gradient accumulator).
+    op's gradient accumulator).  ``key_range`` = (key_base, key_bits) of the
+    depth sort (``depth_key_range``; the default sorts the keys' 32 bits).
     ``timer(name)`` (optional) marks the end of the plan ("bin") and of the
     bucketing passes ("emit").
     """
@@ -206,7 +225,8 @@ def bin_tiles(
     host_totals = torch.zeros(5, dtype=torch.int64, pin_memory=True)
     nat.check(
         lib.gs_bin_tiles_plan(
-            nat.ptr(depth_keys), nat.ptr(tile_rects), n, tiles_w, tiles_h,
+            nat.ptr(depth_keys), nat.ptr(tile_rects), n, int(key_range[0]), int(key_range[1]),
+            tiles_w, tiles_h,
             nat.ptr(ranges), nat.ptr(totals), c_void_p(host_totals.data_ptr()), nat.ptr(plan),
             plan.numel(), nat.ptr(clear), nat.buffer_bytes(clear), s,
         ),

@@ -35,6 +35,7 @@ from .intersections import (
     bin_gaussians,
     bin_tiles,
     bucketing_fits,
+    depth_key_range,
     emit_tiles,
     sort_tiles,
 )
@@ -166,7 +167,7 @@ def forward_views(
     if bucketing:
         gaussian_ids, ranges = bin_tiles(
             depth_keys, None, None, canvas_w, canvas_h, timer=mark, tile_rects=tile_rects,
-            clear=accumulator,
+            clear=accumulator, key_range=depth_key_range(near, far),
         )
     else:
         flat_bounds = bounds.view(vn, 2, 2)

@@ -42,7 +42,7 @@ extern "C" {
 
 #define GS_API __attribute__((visibility("default")))
 
-#define GS_ABI_VERSION 16
+#define GS_ABI_VERSION 17
 
 typedef enum gs_status {
   GS_OK = 0,
@@ -262,15 +262,23 @@ GS_API int gs_sort_tiles(
  * `sorted_ids` [totals[0]].  depth_keys and tile_rects are
  * gs_project_and_count's (depth_keys: ~0u for Gaussians without
  * intersections; consumed).  Together they replace intersections.py:44-88
- * for the op.  `clear` (optional, 16-byte aligned, clear_bytes a multiple
+ * for the op.  key_bits in [1, 32]: with 32 the depth order is that of the
+ * keys' 32 bits (four sort passes); below 32 it is that of min(key -
+ * key_base, 2^key_bits - 1) (keys below key_base or at least key_base +
+ * 2^key_bits - 1 sort last, in index order), in ceil(key_bits / 8) passes
+ * of near-equal width.  The op passes key_base = the bits of its float near
+ * plane and key_bits = the bit length of bits(far) - bits(near): every
+ * counted Gaussian's depth lies strictly between the planes, so the order is
+ * the same (near 0.2, far 100: 27 bits, passes of 7, 7, 7 and 6 bits).  `clear` (optional, 16-byte aligned, clear_bytes a multiple
  * of 4; no counterpart in the reference) is zeroed on the side stream beside
  * the depth sort, before the totals are copied: the op passes the backward's
  * [N, 9] gradient accumulator, so no fill runs on `stream`. */
 GS_API size_t gs_bin_tiles_plan_bytes(int64_t n, int32_t tiles_w, int32_t tiles_h);
 GS_API int gs_bin_tiles_plan(
-    uint32_t* depth_keys, const uint32_t* tile_rects, int64_t n,
-    int32_t tiles_w, int32_t tiles_h, int64_t* ranges, int64_t* totals, int64_t* host_totals,
-    void* plan, size_t plan_bytes, void* clear, size_t clear_bytes, void* stream);
+    uint32_t* depth_keys, const uint32_t* tile_rects, int64_t n, uint32_t key_base,
+    int32_t key_bits, int32_t tiles_w, int32_t tiles_h, int64_t* ranges, int64_t* totals,
+    int64_t* host_totals, void* plan, size_t plan_bytes, void* clear, size_t clear_bytes,
+    void* stream);
 /* tile_rects (the packing of gs_project_and_count) from bounds [N, 2, 2] and
  * counts, for callers holding those instead; no counterpart in the
  * reference. */

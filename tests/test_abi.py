@@ -121,22 +121,28 @@ def test_bucketed_binning_host_checks():
     assert lib.gs_bin_tiles_plan_bytes(1000, 120, 68) > lib.gs_bin_tiles_plan_bytes(10, 120, 68)
     assert lib.gs_bin_tiles_plan_bytes(-1, 120, 68) == 0
     assert lib.gs_bin_tiles_emit_bytes(1000, 1 << 20, 1 << 18, 300, 120, 68) >= 3 * 4 * (1 << 18)
-    status = lib.gs_bin_tiles_plan(fake, fake, 10, 257, 4, fake, fake, None, fake, 1 << 20, None,
-                                   0, None)
+    status = lib.gs_bin_tiles_plan(fake, fake, 10, 0, 32, 257, 4, fake, fake, None, fake, 1 << 20,
+                                   None, 0, None)
     assert status == nat.GS_ERR_UNSUPPORTED
     assert b"at most 256" in lib.gs_last_error()
-    status = lib.gs_bin_tiles_plan(fake, fake, 10, 120, 68, fake, fake, None, fake, 16, None, 0,
-                                   None)
+    status = lib.gs_bin_tiles_plan(fake, fake, 10, 0, 32, 120, 68, fake, fake, None, fake, 16, None,
+                                   0, None)
     assert status == nat.GS_ERR_WORKSPACE
     # the buffer to clear must be 16-byte aligned, a multiple of 4 bytes
-    status = lib.gs_bin_tiles_plan(fake, fake, 10, 120, 68, fake, fake, None, fake, 1 << 30,
+    status = lib.gs_bin_tiles_plan(fake, fake, 10, 0, 32, 120, 68, fake, fake, None, fake, 1 << 30,
                                    fake, 6, None)
     assert status == nat.GS_ERR_INVALID_ARGUMENT
     # the row pass's look-back packs a row's entry count into 26 bits
-    status = lib.gs_bin_tiles_plan(fake, fake, 1 << 26, 120, 68, fake, fake, None, fake, 1 << 40,
-                                   None, 0, None)
+    status = lib.gs_bin_tiles_plan(fake, fake, 1 << 26, 0, 32, 120, 68, fake, fake, None, fake,
+                                   1 << 40, None, 0, None)
     assert status == nat.GS_ERR_OVERFLOW
     assert b"fewer than 67108864 Gaussians" in lib.gs_last_error()
+    # the depth sort's key range: 1 to 32 bits
+    for bits in (0, 33):
+        status = lib.gs_bin_tiles_plan(fake, fake, 10, 0, bits, 120, 68, fake, fake, None, fake,
+                                       1 << 30, None, 0, None)
+        assert status == nat.GS_ERR_INVALID_ARGUMENT
+        assert b"key_bits" in lib.gs_last_error()
     status = lib.gs_pack_tile_rects(fake, fake, 10, 257, 4, fake, None)
     assert status == nat.GS_ERR_UNSUPPORTED
     # pass-B workgroups must match the intersection total (ceil(total / 4096) .. + rows)

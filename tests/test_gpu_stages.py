@@ -306,6 +306,44 @@ def test_bucketed_binning_bit_exact(device, shape, n):
     assert np.array_equal(sid.cpu().numpy(), sid_o)
 
 
+@pytest.mark.parametrize(
+    "near, far, n, shape",
+    ((0.2, 100.0, 20000, (120, 68)), (0.01, 10.0, 4096, (24, 17)), (1.0, 1.5, 4096, (37, 1)),
+     (0.2, 100.0, 0, (24, 17))),
+    ids=("near0.2-far100", "near0.01-far10", "near1-far1.5", "empty"),
+)
+def test_bucketed_binning_remapped_depth_keys(device, near, far, n, shape):
+    """The op's depth sort over min(key - bits(near), 2^k - 1) (near 0.2,
+    far 100: k = 27, passes of 7, 7, 7 and 6 bits): the lists equal the
+    oracle's stable (depth bits, index) sort, depths drawn between the planes
+    with ties, culled Gaussians (key ~0) and depths just inside both
+    planes."""
+    from gaussian_splats_hip.kernels.rasterize import depth_key_range
+
+    tiles_w, tiles_h = shape
+    key_range = depth_key_range(near, far)
+    assert key_range[1] < 32
+    bounds, _, counts = _random_rects(n=max(n, 1), tiles_w=tiles_w, tiles_h=tiles_h, seed=n + 3)
+    bounds, counts = bounds[:n], counts[:n]
+    g = torch.Generator().manual_seed(n)
+    lo, hi = np.float32(near), np.float32(far)
+    depths = torch.exp(torch.rand(n, generator=g, dtype=torch.float64) * (math.log(hi) - math.log(lo))
+                       + math.log(lo)).float()
+    depths = torch.clamp(depths, float(np.nextafter(lo, hi)), float(np.nextafter(hi, lo)))
+    if n >= 8:
+        depths[: n // 8] = depths[n // 8 : n // 4]  # ties
+        depths[n // 4] = float(np.nextafter(lo, hi))  # just inside the near plane
+        depths[n // 4 + 1] = float(np.nextafter(hi, lo))  # just inside the far plane
+    keys_o, ids_o = orc.emit_intersections(bounds.numpy(), depths.numpy(), counts.numpy(), tiles_w)
+    sid_o, ranges_o, _ = orc.sort_intersections(keys_o, ids_o, tiles_w * tiles_h)
+    print(f"remapped depth keys near={near} far={far} bits={key_range[1]} n={n} "
+          f"intersections={len(sid_o)}", flush=True)
+    sid, ranges = bin_tiles(_depth_keys(depths, counts).to(device), bounds.to(device),
+                            counts.to(device), tiles_w, tiles_h, key_range=key_range)
+    assert np.array_equal(ranges.cpu().numpy(), ranges_o)
+    assert np.array_equal(sid.cpu().numpy(), sid_o)
+
+
 def test_bucketed_binning_long_rows(device):
     """Rows holding many workgroups of intersections (full-width rectangles)
     and Gaussians spanning many rows, so both passes chain look-backs across
@@ -704,7 +742,7 @@ def test_device_check_failures_reach_the_host(device):
     nat.check(lib.gs_pack_tile_rects(nat.ptr(bounds), nat.ptr(counts), n, tw, th, nat.ptr(rects),
                                      s), "pack")
     print("[device checks] plan", flush=True)
-    nat.check(lib.gs_bin_tiles_plan(nat.ptr(keys), nat.ptr(rects), n, tw, th,
+    nat.check(lib.gs_bin_tiles_plan(nat.ptr(keys), nat.ptr(rects), n, 0, 32, tw, th,
                                     nat.ptr(ranges), nat.ptr(totals), c_void_p(host.data_ptr()),
                                     nat.ptr(plan), plan.numel(), None, 0, s), "plan")
     total, rows, blocks, _, flags = host.tolist()

@@ -283,13 +283,15 @@ __device__ __forceinline__ void rank_items(const uint32_t* digits, int n_valid_f
 // the global offsets -> reorder the tile in LDS by digit -> coalesced stores.
 // vals_in == nullptr means vals[i] = i.
 // With `remap` (the first pass of a remapped plan), the keys are mapped to
-// min(key - base, cap) as they are loaded, and written so.
-template <typename K, int BITS>
+// min(key - base, cap) as they are loaded, and written so.  PAY: a second
+// 32-bit value per element (pay_in, in the input order) moves with the keys
+// to pay_out.
+template <typename K, int BITS, bool PAY>
 __global__ __launch_bounds__(kBlock) void scatter_kernel(
     const K* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, K* __restrict__ keys_out,
     uint32_t* __restrict__ vals_out, int64_t n, int shift, const uint32_t* __restrict__ hist,
     uint64_t* __restrict__ status, uint32_t* __restrict__ ticket, uint32_t* __restrict__ err,
-    const uint32_t* __restrict__ gather_src, uint32_t* __restrict__ gather_out, bool remap,
+    const uint32_t* __restrict__ pay_in, uint32_t* __restrict__ pay_out, bool remap,
     uint64_t remap_base, uint64_t remap_cap) {
   constexpr int D = 1 << BITS;
   static_assert(D <= kBlock || D % kBlock == 0, "digits per thread");
@@ -303,6 +305,7 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
   __shared__ int s_block;
   __shared__ K skeys[kTile];
   __shared__ uint32_t svals[kTile];
+  __shared__ uint32_t spay[PAY ? kTile : 1];
 
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
@@ -318,10 +321,16 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
 
   K key[kItems];
   uint32_t val[kItems];
+  uint32_t pay[PAY ? kItems : 1];
   uint32_t dig[kItems];
   if (full) {
 #pragma unroll
     for (int i = 0; i < kItems; ++i) key[i] = kin[i * 64 + lane];
+    if constexpr (PAY) {
+      const uint32_t* pin = pay_in + base + wid * kSeg;
+#pragma unroll
+      for (int i = 0; i < kItems; ++i) pay[i] = pin[i * 64 + lane];
+    }
     if (vals_in) {
       const uint32_t* vin = vals_in + base + wid * kSeg;
 #pragma unroll
@@ -338,6 +347,7 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
       key[i] = valid ? kin[o] : K(0);
       val[i] = valid ? (vals_in ? vals_in[base + wid * kSeg + o] : uint32_t(base + wid * kSeg + o))
                      : 0u;
+      if constexpr (PAY) pay[i] = valid ? pay_in[base + wid * kSeg + o] : 0u;
     }
   }
   if (remap) {
@@ -409,6 +419,7 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
       const uint32_t pos = cnt[wid][dig[i]] + rank[i];
       skeys[pos] = key[i];
       svals[pos] = val[i];
+      if constexpr (PAY) spay[pos] = pay[i];
     }
   }
   __syncthreads();
@@ -419,9 +430,7 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
     const uint32_t o = gofs[d] + uint32_t(j);
     keys_out[o] = k;
     vals_out[o] = svals[j];
-    // gather_out[o] = gather_src[value]: a payload of each element in the
-    // sorted order (the last pass only).
-    if (gather_out) gather_out[o] = gather_src[svals[j]];
+    if constexpr (PAY) pay_out[o] = spay[j];
   }
 }
 

@@ -25,6 +25,7 @@ inline int bits_for(int64_t count) {  // ceil(log2(count)), 0 for count <= 1
 struct Scratch {
   void* keys_alt = nullptr;
   uint32_t* vbuf[2] = {nullptr, nullptr};
+  uint32_t* pbuf[2] = {nullptr, nullptr};  // payload ping-pong (carved with `payload`)
   uint64_t* sort_status = nullptr;
   uint64_t* scan_status = nullptr;
   uint64_t* zero_begin = nullptr;
@@ -51,7 +52,7 @@ inline int64_t sort_status_words(int64_t n, const sweep::Plan& p) {
 // scan_n elements (0: no scan).  The look-back statuses are sized for the
 // largest plan of any end bit up to end_bit.
 inline Scratch carve(void* ws, int64_t n, int key_bytes, int end_bit, int64_t scan_n,
-                     int max_bits = 8) {
+                     int max_bits = 8, bool payload = false) {
   Scratch s;
   char* p = static_cast<char*>(ws);
   size_t off = 0;
@@ -61,6 +62,10 @@ inline Scratch carve(void* ws, int64_t n, int key_bytes, int end_bit, int64_t sc
     off += align_up(size_t(n) * key_bytes);
     for (int i = 0; i < 2; ++i) {
       s.vbuf[i] = p ? reinterpret_cast<uint32_t*>(p + off) : nullptr;
+      off += align_up(size_t(n) * 4);
+    }
+    for (int i = 0; payload && i < 2; ++i) {
+      s.pbuf[i] = p ? reinterpret_cast<uint32_t*>(p + off) : nullptr;
       off += align_up(size_t(n) * 4);
     }
     for (int e = 1; e <= end_bit; ++e)
@@ -88,11 +93,16 @@ inline void clear(const Scratch& s, hipStream_t stream) {
 template <typename K, int BITS>
 void launch_scatter(const K* kin, const uint32_t* vin, K* kout, uint32_t* vout, int64_t n,
                     int shift, const uint32_t* hist, uint64_t* status, uint32_t* ticket,
-                    uint32_t* err, const uint32_t* gsrc, uint32_t* gout, bool remap,
+                    uint32_t* err, const uint32_t* pin, uint32_t* pout, bool remap,
                     uint64_t base, uint64_t cap, hipStream_t s) {
   const unsigned nblocks = unsigned(ceil_div(n, kTile));
-  sweep::scatter_kernel<K, BITS><<<nblocks, sweep::kBlock, 0, s>>>(
-      kin, vin, kout, vout, n, shift, hist, status, ticket, err, gsrc, gout, remap, base, cap);
+  if (pin)
+    sweep::scatter_kernel<K, BITS, true><<<nblocks, sweep::kBlock, 0, s>>>(
+        kin, vin, kout, vout, n, shift, hist, status, ticket, err, pin, pout, remap, base, cap);
+  else
+    sweep::scatter_kernel<K, BITS, false><<<nblocks, sweep::kBlock, 0, s>>>(
+        kin, vin, kout, vout, n, shift, hist, status, ticket, err, nullptr, nullptr, remap, base,
+        cap);
 }
 
 template <typename K>
@@ -120,8 +130,9 @@ void dispatch_scatter(int bits, const K* kin, const uint32_t* vin, K* kout, uint
 // Sorts (keys, vals) on bits [0, end_bit) after `clear` has zeroed the scratch.
 // vals == nullptr means vals[i] = i.  Sorted values land in vals_final;
 // *keys_final points at the sorted keys (keys or the scratch copy).
-// SPREAD: the keys are depth keys (see hist_kernel).  gather_out (optional):
-// the last pass also writes gather_out[i] = gather_src[vals_final[i]].
+// SPREAD: the keys are depth keys (see hist_kernel).  payload_src (optional,
+// with scratch carved with `payload`): a second value per element, in the
+// input order, that moves with the keys to payload_final.
 // hook() is called on the host once the histogram and the first pass are
 // enqueued, before the other passes (it may enqueue work on another stream):
 // the caller's stream has those two kernels to run while the host enqueues
@@ -141,7 +152,7 @@ struct KeyRemap {
 template <typename K, bool SPREAD = false, typename Hook = NoHook>
 int radix_sort(K* keys, const uint32_t* vals, int64_t n, int end_bit, uint32_t* vals_final,
                K** keys_final, const Scratch& ws, hipStream_t s,
-               const uint32_t* gather_src = nullptr, uint32_t* gather_out = nullptr,
+               const uint32_t* payload_src = nullptr, uint32_t* payload_final = nullptr,
                Hook hook = Hook{}, KeyRemap remap = KeyRemap{}) {
   GS_REQUIRE(n < (int64_t(1) << 32) - kTile, GS_ERR_OVERFLOW, "too many elements to sort (%lld)",
              (long long)n);
@@ -161,22 +172,26 @@ int radix_sort(K* keys, const uint32_t* vals, int64_t n, int end_bit, uint32_t* 
       int(std::min<int64_t>(1024, ceil_div(n, sweep::kHistBlock * sweep::kHistKeys)));
   sweep::hist_kernel<K, SPREAD>
       <<<unsigned(hist_blocks), sweep::kHistBlock, 0, s>>>(keys, n, plan, ws.hist());
+  GS_REQUIRE(!payload_src || (payload_final && ws.pbuf[0] && ws.pbuf[1]),
+             GS_ERR_INVALID_ARGUMENT, "payload without its buffers");
   K* kbuf[2] = {static_cast<K*>(ws.keys_alt), keys};
   const K* kin = keys;
   const uint32_t* vin = vals;
+  const uint32_t* pin = payload_src;
   uint64_t* status = ws.sort_status;
   const int64_t nblocks = ceil_div(n, kTile);
   for (int pass = 0; pass < plan.passes; ++pass) {
     K* kout = kbuf[pass & 1];
-    uint32_t* vout = (pass == plan.passes - 1) ? vals_final : ws.vbuf[pass & 1];
     const bool last = pass == plan.passes - 1;
+    uint32_t* vout = last ? vals_final : ws.vbuf[pass & 1];
+    uint32_t* pout = pin ? (last ? payload_final : ws.pbuf[pass & 1]) : nullptr;
     dispatch_scatter<K>(plan.bits[pass], kin, vin, kout, vout, n, plan.shift[pass],
                         ws.hist() + pass * sweep::kHistStride, status, ws.tickets() + pass,
-                        ws.flags, last ? gather_src : nullptr, last ? gather_out : nullptr,
-                        pass == 0 && plan.remap, plan.base, plan.cap, s);
+                        ws.flags, pin, pout, pass == 0 && plan.remap, plan.base, plan.cap, s);
     status += nblocks << plan.bits[pass];
     kin = kout;
     vin = vout;
+    pin = pout;
     if (pass == 0) GS_TRY(hook());
   }
   *keys_final = const_cast<K*>(kin);

@@ -1145,7 +1145,7 @@ PlanLayout plan_layout(void* base, int64_t n, int tw, int th) {
   p.first_a_capacity =
       uint32_t(ceil_div(std::min(int64_t(n) * th, int64_t(1) << 31), kTile) + 1);
   p.first_a = reinterpret_cast<uint32_t*>(take(size_t(p.first_a_capacity) * 4));
-  const size_t sort_bytes = carve(nullptr, n, 4, 32, n, kDepthDigitBits).bytes;
+  const size_t sort_bytes = carve(nullptr, n, 4, 32, n, kDepthDigitBits, true).bytes;
   p.sort_ws = take(sort_bytes);
   p.bytes = off;
   return p;
@@ -1327,12 +1327,13 @@ GS_API int gs_bin_tiles_plan(uint32_t* depth_keys, const uint32_t* tile_rects, i
   };
   int status = GS_OK;
   if (n > 0) {
-    Scratch ws = carve(p.sort_ws, n, 4, 32, n, kDepthDigitBits);
+    Scratch ws = carve(p.sort_ws, n, 4, 32, n, kDepthDigitBits, true);
     ws.flags = flags;
     clear(ws, s);
     // depth_keys is consumed (ping-pong buffer of the sort).
     uint32_t* sorted_keys = nullptr;
-    // Its last pass also writes the rectangles in depth order.
+    // The packed rectangles move with the keys through every pass (a payload
+    // in index order), so the last pass writes them in depth order.
     // With key_bits < 32 the sort orders min(key - key_base, 2^key_bits - 1)
     // in digits of up to kDepthDigitBits bits.
     KeyRemap remap;

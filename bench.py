@@ -110,11 +110,11 @@ def stage_bytes(n, k, total, rows, pixels, processed_fwd, processed_bwd):
         # params in (44 + 12k B) -> projected outputs (48 B), record (48 B),
         # depth key and packed tile rectangle (4 + 4 B)
         "project": n * (44 + 12 * k) + 104 * n,
-        # depth sort: histogram + 4 passes of (key, id) in and out, the last
-        # pass also gathering and writing the rectangles in depth order; the
-        # tables' rectangle reads; the row-list offset scan (rectangles in,
-        # offsets out)
-        "bin": 4 * n + 4 * 16 * n + 8 * n + 4 * n + 8 * n,
+        # depth sort: histogram, then 4 passes moving (key, id, packed
+        # rectangle), the first reading only keys and rectangles (its ids are
+        # the positions); the tables' rectangle reads; the row-list offset
+        # scan (rectangles in, offsets out)
+        "bin": 4 * n + 20 * n + 3 * 24 * n + 4 * n + 8 * n,
         # pass A writes (id, packed columns, row-major position) per row
         # entry; pass B reads its windows (packed columns, positions) and
         # writes one id per intersection

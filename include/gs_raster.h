@@ -269,8 +269,9 @@ GS_API int gs_sort_tiles(
  * of near-equal width.  The op passes key_base = the bits of its float near
  * plane and key_bits = the bit length of bits(far) - bits(near): every
  * counted Gaussian's depth lies strictly between the planes, so the order is
- * the same (near 0.2, far 100: 27 bits, passes of 7, 7, 7 and 6 bits).  `clear` (optional, 16-byte aligned, clear_bytes a multiple
- * of 4; no counterpart in the reference) is zeroed on the side stream beside
+ * the same (near 0.2, far 100: 27 bits, passes of 7, 7, 7 and 6 bits).
+ * `clear` (optional, 16-byte aligned, clear_bytes a multiple of 4; no
+ * counterpart in the reference) is zeroed on the side stream beside
  * the depth sort, before the totals are copied: the op passes the backward's
  * [N, 9] gradient accumulator, so no fill runs on `stream`. */
 GS_API size_t gs_bin_tiles_plan_bytes(int64_t n, int32_t tiles_w, int32_t tiles_h);

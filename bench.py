@@ -622,6 +622,20 @@ def bench_views(args, scene):
     achieved = model["composite_bwd"] / (views if kind == "loop" else 1) / (dominant_ms * 1e-3) / 1e9
     other = "loop" if kind == "batched" else "batched"
     compared = {f"{other}_ms_per_step": round(timed[other][0], 4)} if other in timed else {}
+    # The batched backward's measured counters (config 5 only): HBM traffic
+    # per launch and VALU busy; the bound is VALU issue above 90% busy.
+    traffic, valu = None, None
+    counters = ROOT / "profiles" / "traffic_composite_bwd_config5.json"
+    if counters.exists() and scene.name == "config5" and kind == "batched" and tile == 16:
+        measured = json.loads(counters.read_text())
+        traffic = measured["hbm_bytes_per_launch"]
+        m = measured["valu"]
+        insts = m["sq_insts_valu_per_launch"]
+        issue_ms = insts * 4 / (1024 * VALU_CLOCK_HZ) * 1e3
+        valu = {"valu_busy_measured": m["valu_busy"], "formula": m["formula"],
+                "instructions": insts, "issue_ms_at_4_cycles": round(issue_ms, 4),
+                "issue_frac": round(issue_ms / dominant_ms, 4)}
+    bound = "valu" if valu is not None and valu["valu_busy_measured"] > 0.9 else "hbm"
     result = {
         "metric": "fwd+bwd Mpix/s, multi-view batch",
         "value": round(views * w * h / 1e6 / (ms_per_step * 1e-3), 3),
@@ -647,13 +661,14 @@ def bench_views(args, scene):
         "stages": stages,
         "roofline": {
             "kernel": "composite_bwd_kernel",
-            "bound": "hbm",
+            "bound": bound,
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
             "launch_ms": round(dominant_ms, 4),
+            "valu_issue": valu,
         },
         "cpu_baseline": None,
     }

@@ -230,12 +230,12 @@ __global__ __launch_bounds__(kHistBlock) void hist_kernel(const K* __restrict__ 
 // the digit in this wave's segment lives in LDS.  All peers write the same new
 // count, so no leader election is needed; a wave's LDS accesses execute in
 // program order, so item i+1 sees item i's counts.
-template <int BITS, bool FULL>
+template <int BITS, bool FULL, int ITEMS = kItems>
 __device__ __forceinline__ void rank_items(const uint32_t* digits, int n_valid_from_seg,
                                            uint32_t* wcnt, uint32_t* rank) {
   const int lane = __lane_id();
 #pragma unroll
-  for (int i = 0; i < kItems; ++i) {
+  for (int i = 0; i < ITEMS; ++i) {
     const uint32_t d = digits[i];
     bool valid = true;
     uint32_t plo = ~0u, phi = ~0u;
@@ -278,30 +278,34 @@ __device__ __forceinline__ void rank_items(const uint32_t* digits, int n_valid_f
   }
 }
 
-// One stable LSD pass over BITS bits at `shift`: ticket -> load 16 elements per
-// thread -> rank within each wave -> per-digit workgroup counts -> look-back for
-// the global offsets -> reorder the tile in LDS by digit -> coalesced stores.
+// One stable LSD pass over BITS bits at `shift`: ticket -> load kTile / (64
+// WAVES) elements per thread -> rank within each wave -> per-digit workgroup
+// counts -> look-back for the global offsets -> reorder the tile in LDS by
+// digit -> coalesced stores.
 // vals_in == nullptr means vals[i] = i.
 // With `remap` (the first pass of a remapped plan), the keys are mapped to
 // min(key - base, cap) as they are loaded, and written so.  PAY: a second
 // 32-bit value per element (pay_in, in the input order) moves with the keys
 // to pay_out.
-template <typename K, int BITS, bool PAY>
-__global__ __launch_bounds__(kBlock) void scatter_kernel(
+template <typename K, int BITS, bool PAY, int WAVES = 4>
+__global__ __launch_bounds__(WAVES * 64) void scatter_kernel(
     const K* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, K* __restrict__ keys_out,
     uint32_t* __restrict__ vals_out, int64_t n, int shift, const uint32_t* __restrict__ hist,
     uint64_t* __restrict__ status, uint32_t* __restrict__ ticket, uint32_t* __restrict__ err,
     const uint32_t* __restrict__ pay_in, uint32_t* __restrict__ pay_out, bool remap,
     uint64_t remap_base, uint64_t remap_cap) {
   constexpr int D = 1 << BITS;
-  static_assert(D <= kBlock || D % kBlock == 0, "digits per thread");
+  constexpr int kThreads = WAVES * 64;
+  constexpr int ITEMS = kTile / kThreads;  // per thread
+  static_assert(ITEMS * kThreads == kTile, "whole items per thread");
+  static_assert(D <= kThreads || D % kThreads == 0, "digits per thread");
   // Per-digit work: DPT consecutive digits per thread (d = DPT t + q), so one
   // block scan orders them all.
-  constexpr int DPT = D > kBlock ? D / kBlock : 1;
-  constexpr int kSeg = kTile / 4;  // contiguous elements per wave
-  __shared__ uint32_t cnt[4][D];
+  constexpr int DPT = D > kThreads ? D / kThreads : 1;
+  constexpr int kSeg = kTile / WAVES;  // contiguous elements per wave
+  __shared__ uint32_t cnt[WAVES][D];
   __shared__ uint32_t gofs[D];
-  __shared__ uint32_t scratch[4];
+  __shared__ uint32_t scratch[WAVES];
   __shared__ int s_block;
   __shared__ K skeys[kTile];
   __shared__ uint32_t svals[kTile];
@@ -310,7 +314,7 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
   if (threadIdx.x == 0) s_block = int(atomicAdd(ticket, 1u));
-  for (int d = threadIdx.x; d < 4 * D; d += kBlock) (&cnt[0][0])[d] = 0;
+  for (int d = threadIdx.x; d < WAVES * D; d += kThreads) (&cnt[0][0])[d] = 0;
   __syncthreads();
   const int b = s_block;
   const int64_t base = int64_t(b) * kTile;
@@ -319,29 +323,29 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
   const int seg_valid = nvalid - wid * kSeg;  // valid elements from this wave's segment start
   const K* kin = keys_in + base + wid * kSeg;
 
-  K key[kItems];
-  uint32_t val[kItems];
-  uint32_t pay[PAY ? kItems : 1];
-  uint32_t dig[kItems];
+  K key[ITEMS];
+  uint32_t val[ITEMS];
+  uint32_t pay[PAY ? ITEMS : 1];
+  uint32_t dig[ITEMS];
   if (full) {
 #pragma unroll
-    for (int i = 0; i < kItems; ++i) key[i] = kin[i * 64 + lane];
+    for (int i = 0; i < ITEMS; ++i) key[i] = kin[i * 64 + lane];
     if constexpr (PAY) {
       const uint32_t* pin = pay_in + base + wid * kSeg;
 #pragma unroll
-      for (int i = 0; i < kItems; ++i) pay[i] = pin[i * 64 + lane];
+      for (int i = 0; i < ITEMS; ++i) pay[i] = pin[i * 64 + lane];
     }
     if (vals_in) {
       const uint32_t* vin = vals_in + base + wid * kSeg;
 #pragma unroll
-      for (int i = 0; i < kItems; ++i) val[i] = vin[i * 64 + lane];
+      for (int i = 0; i < ITEMS; ++i) val[i] = vin[i * 64 + lane];
     } else {
 #pragma unroll
-      for (int i = 0; i < kItems; ++i) val[i] = uint32_t(base) + uint32_t(wid * kSeg + i * 64 + lane);
+      for (int i = 0; i < ITEMS; ++i) val[i] = uint32_t(base) + uint32_t(wid * kSeg + i * 64 + lane);
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < kItems; ++i) {
+    for (int i = 0; i < ITEMS; ++i) {
       const int o = i * 64 + lane;
       const bool valid = o < seg_valid;
       key[i] = valid ? kin[o] : K(0);
@@ -352,37 +356,37 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
   }
   if (remap) {
 #pragma unroll
-    for (int i = 0; i < kItems; ++i) key[i] = min(K(key[i] - K(remap_base)), K(remap_cap));
+    for (int i = 0; i < ITEMS; ++i) key[i] = min(K(key[i] - K(remap_base)), K(remap_cap));
   }
 #pragma unroll
-  for (int i = 0; i < kItems; ++i) dig[i] = uint32_t(key[i] >> shift) & (D - 1);
+  for (int i = 0; i < ITEMS; ++i) dig[i] = uint32_t(key[i] >> shift) & (D - 1);
 
-  uint32_t rank[kItems];
+  uint32_t rank[ITEMS];
   if (full)
-    rank_items<BITS, true>(dig, seg_valid, cnt[wid], rank);
+    rank_items<BITS, true, ITEMS>(dig, seg_valid, cnt[wid], rank);
   else
-    rank_items<BITS, false>(dig, seg_valid, cnt[wid], rank);
+    rank_items<BITS, false, ITEMS>(dig, seg_valid, cnt[wid], rank);
   __syncthreads();
 
-  uint32_t tot[DPT], c0[DPT], c1[DPT], c2[DPT], hv[DPT];
+  // cw[q][w]: wave w's count of the thread's digit q.
+  uint32_t tot[DPT], cw[DPT][WAVES], hv[DPT];
   uint32_t tsum = 0, hsum = 0;
 #pragma unroll
   for (int q = 0; q < DPT; ++q) {
     const int d = DPT * int(threadIdx.x) + q;
-    tot[q] = c0[q] = c1[q] = c2[q] = hv[q] = 0;
-    if (d < D) {
-      c0[q] = cnt[0][d];
-      c1[q] = cnt[1][d];
-      c2[q] = cnt[2][d];
-      tot[q] = c0[q] + c1[q] + c2[q] + cnt[3][d];
-      hv[q] = hist[d];
+    tot[q] = hv[q] = 0;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) {
+      cw[q][w] = d < D ? cnt[w][d] : 0u;
+      tot[q] += cw[q][w];
     }
+    if (d < D) hv[q] = hist[d];
     tsum += tot[q];
     hsum += hv[q];
   }
   uint32_t all;
-  uint32_t local_start = block_exclusive_scan(tsum, scratch, all);
-  uint32_t digit_base = block_exclusive_scan(hsum, scratch, all);
+  uint32_t local_start = block_exclusive_scan_waves<WAVES>(tsum, scratch, all);
+  uint32_t digit_base = block_exclusive_scan_waves<WAVES>(hsum, scratch, all);
   uint64_t excl[DPT];
 #pragma unroll
   for (int q = 0; q < DPT; ++q) {
@@ -397,10 +401,12 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
     const int d = DPT * int(threadIdx.x) + q;
     if (d < D) {
       // Wave w's items of digit d start at cnt[w][d] in the reordered tile.
-      cnt[0][d] = local_start;
-      cnt[1][d] = local_start + c0[q];
-      cnt[2][d] = local_start + c0[q] + c1[q];
-      cnt[3][d] = local_start + c0[q] + c1[q] + c2[q];
+      uint32_t start = local_start;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) {
+        cnt[w][d] = start;
+        start += cw[q][w];
+      }
       if (b > 0) {
         excl[q] = look_back(status, D, b, d, err);
         store_status(status + int64_t(b) * D + d, kFlagPrefix | (excl[q] + tot[q]));
@@ -414,7 +420,7 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
   __syncthreads();
 
 #pragma unroll
-  for (int i = 0; i < kItems; ++i) {
+  for (int i = 0; i < ITEMS; ++i) {
     if (full || i * 64 + lane < seg_valid) {
       const uint32_t pos = cnt[wid][dig[i]] + rank[i];
       skeys[pos] = key[i];
@@ -424,7 +430,7 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(
   }
   __syncthreads();
 
-  for (int j = threadIdx.x; j < nvalid; j += kBlock) {
+  for (int j = threadIdx.x; j < nvalid; j += kThreads) {
     const K k = skeys[j];
     const uint32_t d = uint32_t(k >> shift) & (D - 1);
     const uint32_t o = gofs[d] + uint32_t(j);

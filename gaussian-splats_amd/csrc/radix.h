@@ -90,17 +90,26 @@ inline void clear(const Scratch& s, hipStream_t stream) {
                                                                s.small_words);
 }
 
+// Waves per workgroup of the scatter passes (kTile / (64 kScatterWaves) keys
+// per thread).  Eight waves of 8 keys, two per SIMD, hide more of a pass's
+// dependent steps than four waves of 16 (82 VGPRs instead of 145): depth sort
+// passes on 1M keys 19.4 -> 18.2 us (7-bit digits), 17.6 -> 16.1 (6-bit), on
+// 4M keys 50.8 -> 49.7 and 41.6 -> 37.9; on 8M keys the 7-bit passes are
+// slower (75 -> 80 us) and the 6-bit one faster (108 -> 98).
+constexpr int kScatterWaves = 8;
+
 template <typename K, int BITS>
 void launch_scatter(const K* kin, const uint32_t* vin, K* kout, uint32_t* vout, int64_t n,
                     int shift, const uint32_t* hist, uint64_t* status, uint32_t* ticket,
                     uint32_t* err, const uint32_t* pin, uint32_t* pout, bool remap,
                     uint64_t base, uint64_t cap, hipStream_t s) {
   const unsigned nblocks = unsigned(ceil_div(n, kTile));
+  constexpr int W = kScatterWaves;
   if (pin)
-    sweep::scatter_kernel<K, BITS, true><<<nblocks, sweep::kBlock, 0, s>>>(
+    sweep::scatter_kernel<K, BITS, true, W><<<nblocks, W * 64, 0, s>>>(
         kin, vin, kout, vout, n, shift, hist, status, ticket, err, pin, pout, remap, base, cap);
   else
-    sweep::scatter_kernel<K, BITS, false><<<nblocks, sweep::kBlock, 0, s>>>(
+    sweep::scatter_kernel<K, BITS, false, W><<<nblocks, W * 64, 0, s>>>(
         kin, vin, kout, vout, n, shift, hist, status, ticket, err, nullptr, nullptr, remap, base,
         cap);
 }

@@ -906,15 +906,90 @@ __host__ __device__ inline int64_t chunk_slots(int64_t blocks, int th) {
   return ((blocks + (int64_t(1) << sh) - 1) >> sh) + th + 1;
 }
 
-// Counts: every row-list entry of workgroup b's window adds +1 at the first
-// column of its intersections inside [c0, c0 + count) and -1 after the last
-// one, in an LDS difference array; its prefix over the columns is the
+// Counts: every row-list entry of pass-B workgroup b's window adds +1 at the
+// first column of its intersections inside [c0, c0 + count) and -1 after the
+// last one, in an LDS difference array; its prefix over the columns is the
 // workgroup's count per column, stored at counts[b * tw + column] and added
 // to its chunk's sums (sums[((b >> cs) + row) * tw + column], zeroed
 // beforehand).  The window's entries are read contiguously (no item is
-// generated).
+// generated).  Two forms: one wave per window, kBlock / 64 windows per
+// workgroup, for windows of a few hundred entries (config 4 ~360, config 3
+// ~730: too few to keep a whole workgroup and its barriers busy; config 4
+// 152 -> 97 us), and one workgroup per window for windows of thousands of
+// entries (narrow entries, config 5: 63 us against 76 per wave).
 template <int BITS>
-__global__ __launch_bounds__(kBlock) void column_count_kernel(
+__global__ __launch_bounds__(kBlock) void column_count_wave_kernel(
+    const uint32_t* __restrict__ rl_xw, const uint32_t* __restrict__ W,
+    const uint4* __restrict__ info, int tw, const int64_t* __restrict__ totals, int64_t total,
+    int64_t entries, int64_t blocks, int cs, uint32_t* __restrict__ counts,
+    uint32_t* __restrict__ sums, uint32_t* __restrict__ err) {
+  constexpr int D = 1 << BITS;
+  constexpr int kWaves = kBlock / 64;
+  constexpr int kCols = (D + 63) / 64;  // columns per lane, consecutive
+  constexpr int kBatch = 8;             // rounds of 64 entries whose loads are issued together
+  __shared__ int32_t diff[kWaves][D + 1];
+  if (totals[0] != total || totals[1] != entries || totals[2] != blocks) {
+    if (threadIdx.x == 0) atomicOr(err, kDeviceFlagSizes);
+    return;
+  }
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  const int64_t b = int64_t(blockIdx.x) * kWaves + wid;
+  if (b >= blocks) return;  // wave-uniform; the kernel has no workgroup barrier
+  int32_t* const dw = diff[wid];
+  for (int d = lane; d <= D; d += 64) dw[d] = 0;
+  const PassBWindow win = pass_b_window(info, b, blocks);
+  const int64_t span = win.last - win.first + 1;
+  if (span > kTile && lane == 0) atomicOr(err, kDeviceFlagWindow);
+  const int m = int(min(max(span, int64_t(1)), int64_t(kTile)));
+  const uint32_t end = win.c0 + win.nvalid;
+  // The zeros above are ordered before the marks: one wave's LDS accesses
+  // complete in program order, and the fence keeps the compiler's order.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  for (int r0 = 0; r0 < m; r0 += 64 * kBatch) {  // wave-uniform
+    uint32_t xw[kBatch], s0[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int e = min(r0 + j * 64 + lane, m - 1);
+      xw[j] = rl_xw[win.first + e];
+      s0[j] = W[win.first + e];
+    }
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      if (r0 + j * 64 + lane >= m) continue;
+      const uint32_t w = entry_width(xw[j]), x0 = entry_x0(xw[j]);
+      const uint32_t lo = max(s0[j], win.c0), hi = min(s0[j] + w, end);
+      if (lo < hi) {
+        atomicAdd(&dw[min(x0 + (lo - s0[j]), uint32_t(D))], 1);
+        atomicAdd(&dw[min(x0 + (hi - s0[j]), uint32_t(D))], -1);
+      }
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+  // Inclusive prefix over the columns: kCols consecutive ones per lane, then
+  // the lanes' totals scanned across the wave.
+  uint32_t c[kCols];
+  uint32_t run = 0;
+#pragma unroll
+  for (int k = 0; k < kCols; ++k) {
+    const int d = lane * kCols + k;
+    run += d < D ? uint32_t(dw[d]) : 0u;
+    c[k] = run;
+  }
+  const uint32_t before = wave_inclusive_scan(run) - run;
+#pragma unroll
+  for (int k = 0; k < kCols; ++k) {
+    const int d = lane * kCols + k;
+    const uint32_t cnt = before + c[k];
+    if (d < tw) {
+      counts[b * tw + d] = cnt;
+      if (cnt) atomicAdd(&sums[((b >> cs) + win.row) * tw + d], cnt);
+    }
+  }
+}
+
+template <int BITS>
+__global__ __launch_bounds__(kBlock) void column_count_block_kernel(
     const uint32_t* __restrict__ rl_xw, const uint32_t* __restrict__ W,
     const uint4* __restrict__ info, int tw, const int64_t* __restrict__ totals, int64_t total,
     int64_t entries, int64_t blocks, int cs, uint32_t* __restrict__ counts,
@@ -1088,6 +1163,10 @@ void launch_row_bucket(unsigned blocks, const uint32_t* packed_sorted, const int
                                                     ticket, err);
 }
 
+// Mean row-list entries per pass-B window up to which column counting takes
+// one wave per window (above: one workgroup per window).
+constexpr int64_t kCountWaveEntries = 1024;
+
 template <int BITS>
 void launch_pass_b(unsigned blocks, const uint32_t* rl_g, const uint32_t* rl_xw,
                    const uint32_t* W, const uint4* info, int tw, int th, const uint32_t* row_blk,
@@ -1095,8 +1174,13 @@ void launch_pass_b(unsigned blocks, const uint32_t* rl_g, const uint32_t* rl_xw,
                    int64_t blocks_b, int32_t* sorted_ids, uint32_t* counts, uint32_t* sums,
                    uint32_t* err, hipStream_t s) {
   const int cs = chunk_shift(blocks_b, th);
-  column_count_kernel<BITS><<<blocks, kBlock, 0, s>>>(rl_xw, W, info, tw, totals, total, entries,
-                                                      blocks_b, cs, counts, sums, err);
+  if (entries <= kCountWaveEntries * blocks_b)  // windows of kCountWaveEntries entries or fewer
+    column_count_wave_kernel<BITS><<<unsigned(ceil_div(blocks_b, int64_t(kBlock / 64))), kBlock,
+                                     0, s>>>(rl_xw, W, info, tw, totals, total, entries, blocks_b,
+                                             cs, counts, sums, err);
+  else
+    column_count_block_kernel<BITS><<<blocks, kBlock, 0, s>>>(
+        rl_xw, W, info, tw, totals, total, entries, blocks_b, cs, counts, sums, err);
   column_scan_kernel<<<unsigned(ceil_div(blocks_b, int64_t(1) << cs)), kBlock, 0, s>>>(
       counts, sums, info, row_blk, ranges, tw, th, totals, total, entries, blocks_b, cs);
   column_bucket_kernel<BITS><<<blocks, kBlock, 0, s>>>(rl_g, rl_xw, W, info, tw, counts, totals,

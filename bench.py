@@ -132,8 +132,9 @@ STAGE_KERNELS = {
     "project": ["project_fwd_kernel"],
     "bin": ["sweep::clear_kernel", "sweep::hist_kernel", "sweep::scatter_kernel x4 (depth sort)",
             "rect_diff_kernel", "tables_kernel", "sweep::scan_kernel<HeightLoad>"],
-    "emit": ["sweep::clear_kernel", "row_bucket_kernel", "column_count_kernel",
-             "column_scan_kernel", "column_bucket_kernel"],
+    "emit": ["sweep::clear_kernel", "row_bucket_kernel",
+             "column_count_wave_kernel (or column_count_block_kernel)", "column_scan_kernel",
+             "column_bucket_kernel"],
     # With row/column bucketing the lists leave the emit stage sorted: the
     # "sort" mark launches nothing and is not reported.
     "sort": [],

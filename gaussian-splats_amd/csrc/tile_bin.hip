@@ -1046,6 +1046,14 @@ __global__ __launch_bounds__(kBlock) void column_count_block_kernel(
   }
 }
 
+// Threads per chunk of the column scan: the columns rounded up to whole
+// waves (at most the workgroup), so a 256-thread workgroup scans two chunks
+// of up to 128 columns, four of up to 64.
+__host__ __device__ inline int column_scan_group(int tw) {
+  const int g = ((tw + 63) / 64) * 64;
+  return g < kBlock ? g : kBlock;
+}
+
 // Scan: the counts of chunk k's workgroups become each workgroup's first
 // output position per column, in place: ranges[tile].start, plus the sums of
 // the row's earlier chunks, plus the counts of the row's earlier workgroups
@@ -1059,7 +1067,14 @@ __global__ __launch_bounds__(kBlock) void column_scan_kernel(
     int64_t total, int64_t entries, int64_t blocks, int cs) {
   // Inconsistent sizes were flagged by the count pass; nothing is read then.
   if (totals[0] != total || totals[1] != entries || totals[2] != blocks) return;
-  const int64_t k = blockIdx.x;
+  // Groups of whole waves, one column per thread, one chunk per group: a
+  // workgroup scans kBlock / column_scan_group(tw) chunks.
+  const int group = column_scan_group(tw);
+  const int sub = int(threadIdx.x) / group;
+  const int64_t k = int64_t(blockIdx.x) * (kBlock / group) + sub;
+  const int64_t nchunks = (blocks + (int64_t(1) << cs) - 1) >> cs;
+  if (sub >= kBlock / group || k >= nchunks) return;  // wave-uniform: groups are whole waves
+  const int first_d = int(threadIdx.x) - sub * group;
   const int64_t lo = k << cs, hi = min(lo + (int64_t(1) << cs), blocks);
   int64_t b = lo;
   while (b < hi) {
@@ -1068,7 +1083,7 @@ __global__ __launch_bounds__(kBlock) void column_scan_kernel(
     // At least one workgroup per round, so the walk ends whatever the tables hold.
     const int64_t row_end = max(min(int64_t(row_blk[y + 1]), hi), b + 1);
     const int64_t k0 = int64_t(row_blk[y]) >> cs;  // the row's first chunk
-    for (int d = threadIdx.x; d < tw; d += kBlock) {
+    for (int d = first_d; d < tw; d += group) {
       uint32_t acc = uint32_t(ranges[2 * (int64_t(y) * tw + d)]);
       for (int64_t kk = k0; kk < k; kk += 8) {
         uint32_t c[8];
@@ -1181,8 +1196,10 @@ void launch_pass_b(unsigned blocks, const uint32_t* rl_g, const uint32_t* rl_xw,
   else
     column_count_block_kernel<BITS><<<blocks, kBlock, 0, s>>>(
         rl_xw, W, info, tw, totals, total, entries, blocks_b, cs, counts, sums, err);
-  column_scan_kernel<<<unsigned(ceil_div(blocks_b, int64_t(1) << cs)), kBlock, 0, s>>>(
-      counts, sums, info, row_blk, ranges, tw, th, totals, total, entries, blocks_b, cs);
+  const int64_t chunks = ceil_div(blocks_b, int64_t(1) << cs);
+  column_scan_kernel<<<unsigned(ceil_div(chunks, int64_t(kBlock / column_scan_group(tw)))), kBlock,
+                       0, s>>>(counts, sums, info, row_blk, ranges, tw, th, totals, total, entries,
+                               blocks_b, cs);
   column_bucket_kernel<BITS><<<blocks, kBlock, 0, s>>>(rl_g, rl_xw, W, info, tw, counts, totals,
                                                        total, entries, blocks_b, sorted_ids, err);
 }
